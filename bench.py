@@ -1,0 +1,281 @@
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+Headline: one step = the block-Hadamard rotation (128) + per-token int8
+quantization of X [4096, 3072] and the W8A8 int8 GEMM against W [12288, 3072] with the bias and
+tanh-GELU epilogue, bf16 out. `value` is TOPS over the whole step (2·M·N·K ops), inputs resident
+in HBM. `roofline` is the GEMM kernel's achieved int8 TOPS (timed alone with HIP events on the
+launch stream) against the 5.0 POPS dense int8 MFMA peak. `decode` is BASELINE's second target:
+the fp8 rowwise linear at M=1, K=4096, N=14336 (quantize + GEMV fused in one launch), in HBM GB/s
+against 8 TB/s, rotating 8 weight copies (470 MB) so the 256 MB MALL cannot hold them.
+`configs` reports the other BASELINE configs. `cpu_baseline` times the reference's CPU law
+(the oracle's restatement of internal/int8_linear.py:415-448, its literal int32 matmul) on a
+bounded sample of the same workload on this host's cores.
+
+Prints one JSON line. Only one GPU is used; `--gpus` above 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "cozy-runtime_amd"))
+
+METRIC = "quantized-linear TOPS & % MFMA peak (M=4096,K=3072,N=12288); M=1 HBM GB/s"
+#: MI355X datasheet peaks (dense): int8 5.0 POPS, fp8 5.0 PFLOPS, bf16 2.5 PFLOPS, HBM 8 TB/s.
+PEAK_INT8_TOPS = 5000.0
+PEAK_FP8_TFLOPS = 5000.0
+PEAK_HBM_GBS = 8000.0
+
+
+def _seeded(torch, seed: int):
+    return torch.Generator(device="cuda").manual_seed(seed)
+
+
+def _activations(torch, m: int, k: int, seed: int):
+    """bf16 ~N(0,1) with 1% of the K channels scaled x20, generated on the device."""
+    gen = _seeded(torch, seed)
+    x = torch.randn(m, k, generator=gen, device="cuda")
+    chans = torch.randperm(k, generator=gen, device="cuda")[: max(1, k // 100)]
+    x[:, chans] *= 20
+    return x.to(torch.bfloat16)
+
+
+def _weights(torch, n: int, k: int, seed: int):
+    return (torch.randn(n, k, generator=_seeded(torch, seed), device="cuda") * 0.02).to(torch.bfloat16)
+
+
+class Timer:
+    """HIP events on the launch stream (torch's current stream, which every launch here uses)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, fn, iters: int, warmup: int) -> float:
+        """Average ms per call of `fn` over `iters` back-to-back calls after `warmup`."""
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / iters
+
+
+def _check(code: int) -> None:
+    if code != 0:
+        from cozyq import _lib
+
+        raise RuntimeError(f"kernel launch failed: {_lib.error_name(code)}")
+
+
+def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
+    m, k, n = 4096, 3072, 12288
+    x = _activations(torch, m, k, 20261202)
+    data, scale = ops.int8_quantize_rot(_weights(torch, n, k, 20261203), 128)
+    bias = (torch.randn(n, generator=_seeded(torch, 5), device="cuda") * 0.1).to(torch.bfloat16)
+    q = torch.empty(m, k, dtype=torch.int8, device="cuda")
+    s = torch.empty(m, dtype=torch.float32, device="cuda")
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    xp, qp, sp, dp, wp, bp, op = (t.data_ptr() for t in (x, q, s, data, scale, bias, out))
+
+    def quantize():
+        _check(lib.cozyq_quantize_rot(0, xp, 0, qp, sp, m, k, 128, stream))
+
+    def gemm():
+        _check(lib.cozyq_gemm_ex(0, 0, qp, sp, dp, wp, bp, op, n, 0, m, n, k, 1, stream))
+
+    def step():
+        quantize()
+        gemm()
+
+    timer = Timer(torch)
+    ms_step = timer.run(step, steps, warmup)
+    ms_gemm = timer.run(gemm, steps, 2)
+    ms_quant = timer.run(quantize, steps, 2)
+    ops_count = 2.0 * m * n * k
+    gemm_tops = ops_count / (ms_gemm * 1e-3) / 1e12
+    traffic_alg = m * k + n * k + m * n * 2 + n * 2 + (m + n) * 4
+    return {
+        "ms_per_step": ms_step,
+        "tops": ops_count / (ms_step * 1e-3) / 1e12,
+        "gemm_ms": ms_gemm,
+        "quantize_ms": ms_quant,
+        "quantize_gbs": (m * k * 2 + m * k + m * 4) / (ms_quant * 1e-3) / 1e9,
+        "roofline": {
+            "bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
+            "frac": gemm_tops / PEAK_INT8_TOPS, "traffic": None,
+            "kernel": "gemm_kernel<int8> 256x256 (bias+GELU epilogue)",
+            "algorithmic_ops": ops_count, "algorithmic_bytes": traffic_alg,
+        },
+    }
+
+
+def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -> dict:
+    k, n, copies = 4096, 14336, 8
+    x = _activations(torch, m, k, 31)
+    weights = [ops.fp8_quantize(_weights(torch, n, k, 40 + c)) for c in range(copies)]
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    ptrs = [(w.data_ptr(), s.data_ptr()) for w, s in weights]
+    xp, op = x.data_ptr(), out.data_ptr()
+    turn = [0]
+
+    def launch():
+        wp, sp = ptrs[turn[0] % copies]
+        turn[0] += 1
+        _check(lib.cozyq_fp8_linear(0, xp, 0, wp, sp, None, op, 0, m, n, k, stream))
+
+    ms = Timer(torch).run(launch, max(steps, 64), max(warmup, 8))
+    nbytes = n * k + n * 4 + m * k * 2 + m * n * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"M": m, "K": k, "N": n, "us": ms * 1e3, "bytes": nbytes, "gbs": gbs,
+            "frac": gbs / PEAK_HBM_GBS, "weight_copies": copies,
+            "kernel": "fp8_small_kernel (fused quantize + GEMV)"}
+
+
+def bench_fp8(torch, ops, lib, stream, m: int, steps: int) -> dict:
+    k, n = 4096, 14336
+    x = _activations(torch, m, k, 33)
+    data, scale = ops.fp8_quantize(_weights(torch, n, k, 34))
+    q, s = ops.fp8_quantize(x)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    args = (q.data_ptr(), s.data_ptr(), data.data_ptr(), scale.data_ptr())
+
+    def gemm():
+        _check(lib.cozyq_gemm(0, 0, 1, *args, None, out.data_ptr(), n, 0, m, n, k, -1, None, None,
+                              stream))  # fmt: skip
+
+    ms = Timer(torch).run(gemm, steps, 2)
+    tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"M": m, "us": ms * 1e3, "tflops": tflops, "frac_mfma": tflops / PEAK_FP8_TFLOPS}
+
+
+def bench_mx(torch, ops, lib, stream, steps: int) -> dict:
+    m = 4096
+    shapes = {"qkv": (3072, 9216), "attn_out": (3072, 3072), "ffn_up": (3072, 12288),
+              "ffn_down": (12288, 3072)}
+    result, total_ops, total_ms = {}, 0.0, 0.0
+    for name, (k, n) in shapes.items():
+        x = _activations(torch, m, k, 71)
+        data, wbyte = ops.mx_quantize(_weights(torch, n, k, 72))
+        q = torch.empty(m, k, dtype=torch.float8_e4m3fn, device="cuda")
+        qs = torch.empty(m, k // 32, dtype=torch.uint8, device="cuda")
+        out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+
+        def step():
+            _check(lib.cozyq_mx_quantize(0, x.data_ptr(), 0, q.data_ptr(), qs.data_ptr(), m, k,
+                                         stream))  # fmt: skip
+            _check(lib.cozyq_mx_gemm(0, q.data_ptr(), qs.data_ptr(), data.data_ptr(),
+                                     wbyte.data_ptr(), None, out.data_ptr(), n, 0, m, n, k,
+                                     stream))  # fmt: skip
+
+        ms = Timer(torch).run(step, steps, 2)
+        ops_count = 2.0 * m * n * k
+        total_ops += ops_count
+        total_ms += ms
+        result[name] = {"K": k, "N": n, "us": ms * 1e3, "tflops": ops_count / (ms * 1e-3) / 1e12}
+    result["block_tflops"] = total_ops / (total_ms * 1e-3) / 1e12
+    result["frac_mfma"] = result["block_tflops"] / PEAK_FP8_TFLOPS
+    return result
+
+
+def cpu_baseline(torch, rows: int = 1024) -> dict:
+    """The reference's CPU law for config 2 on rows 0..rows-1 of the batch: rotation + per-token
+    int8 (`quantize_rows`), the literal int32 matmul, both scales, bias and GELU."""
+    from oracle import laws
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    k, n = 3072, 12288
+    gen = torch.Generator().manual_seed(20261202)
+    x = torch.randn(rows, k, generator=gen)
+    chans = torch.randperm(k, generator=gen)[: k // 100]
+    x[:, chans] *= 20
+    x = x.to(torch.bfloat16)
+    w = torch.randn(n, k, generator=gen) * 0.02
+    data, scale = laws.int8_weight_rotated(w, 128)
+    bias = (torch.randn(n, generator=gen) * 0.1).to(torch.bfloat16)
+    start = time.perf_counter()
+    laws.int8_linear(x, data, scale, bias, torch.bfloat16, rotation=128, gelu=True, literal=True)
+    seconds = time.perf_counter() - start
+    return {
+        "value": 2.0 * rows * n * k / seconds / 1e12, "unit": "TOPS", "cores": threads,
+        "kind": "port", "seconds": seconds,
+        "sample": f"config 2 rows 0..{rows - 1}: X[{rows},{k}] bf16 -> rotate(128)+int8, "
+                  f"int32 matmul with W[{n},{k}], scales, bias, GELU (torch CPU)",
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the linear shards "
+              "along M with no exchange); run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from cozyq import _lib, prebuilt
+
+    ops = prebuilt.library(0)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    c2 = bench_c2(torch, ops, lib, stream, args.steps, args.warmup)
+    print(f"[bench] c2 {c2['ms_per_step']:.4f} ms/step, gemm {c2['gemm_ms']:.4f} ms", file=sys.stderr, flush=True)
+    decode = bench_decode(torch, ops, lib, stream, args.steps, args.warmup)
+    print(f"[bench] decode M=1 {decode['us']:.2f} us {decode['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    configs = {}
+    if not args.no_extra:
+        configs["c3_fp8"] = [bench_fp8(torch, ops, lib, stream, m, max(10, args.steps // 2))
+                             for m in (256, 4096)]  # fmt: skip
+        configs["c3_fp8_small"] = [bench_decode(torch, ops, lib, stream, args.steps, args.warmup, m=16)]
+        configs["c5_mxfp8"] = bench_mx(torch, ops, lib, stream, max(10, args.steps // 2))
+        print("[bench] extra configs done", file=sys.stderr, flush=True)
+    baseline = None if args.no_cpu else cpu_baseline(torch)
+    line = {
+        "metric": METRIC,
+        "value": c2["tops"],
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": c2["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "config 2: rotate(128)+per-token int8 + W8A8 int8 GEMM + bias + "
+                               "tanh-GELU, bf16 out", "M": 4096, "K": 3072, "N": 12288,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": c2["roofline"],
+        "decode": decode,
+        "phases": {"quantize_ms": c2["quantize_ms"], "quantize_gbs": c2["quantize_gbs"],
+                   "gemm_ms": c2["gemm_ms"]},
+        "configs": configs,
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

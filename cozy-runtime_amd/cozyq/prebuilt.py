@@ -1,0 +1,461 @@
+"""`Prebuilt`: the op library over the HIP kernels, one per card — cozyq's stand-in for
+cozy-runtime's `internal/prebuilt.py:80-434` (`Prebuilt`), with the same method names, argument
+meaning, validation and errors, plus the MXFP8 and int4-g64 SVDQuant ops the reference serves
+through cuBLASLt and nvfp4 kernels respectively.
+
+It allocates outputs with torch and launches on torch's current stream by raw pointer through
+the C ABI (`_lib`). There is no fallback: a shape no kernel takes raises, and a missing library
+raises `KernelsAbsent` when the op is opened (`library`). `torch` is imported lazily so the
+module imports without it.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any
+
+from cozyq import _lib
+
+Tensor = Any
+Dtype = Any
+
+#: The one tensor-core family this library carries (the reference's `FAMILIES`,
+#: `_kernels/__init__.py`): CDNA4's MFMA on gfx950.
+FAMILIES = ("mfma.cdna4",)
+#: How many checked weights `Prebuilt` remembers (`internal/prebuilt.py:75`).
+CHECKED = 4096
+#: Rows the fused fp8 linear takes in one launch (`cozyq_fp8_linear`).
+FP8_SMALL_ROWS = 16
+#: The svdq low-rank ranks the kernels take.
+RANKS = (16, 32, 64)
+#: int4 SVDQuant K-group.
+INT4_GROUP = 64
+MX_BLOCK = 32
+
+
+@dataclass(frozen=True, slots=True)
+class _Format:
+    name: str
+    fp8: bool
+    #: the activation width each row must be a multiple of
+    multiple: int
+
+
+#: `internal/prebuilt.py:68`: int8 rows rotate in 256-groups; fp8 rows are 16-byte multiples.
+INT8, FP8 = _Format("int8", False, 256), _Format("fp8", True, 16)
+MX = _Format("mxfp8", True, 128)
+SVDQ = _Format("svdq-int4", False, INT4_GROUP)
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else int(t.data_ptr())
+
+
+@dataclass(slots=True)
+class Prebuilt:
+    """The ops on one card (`internal/prebuilt.py:80-434`)."""
+
+    torch: Any
+    index: int
+    family: str = FAMILIES[0]
+    _lib: Any = field(init=False)
+    _checked: set[tuple[object, ...]] = field(init=False, default_factory=set)
+
+    def __post_init__(self) -> None:
+        self._lib = _lib.load()
+
+    # ------------------------------------------------------------------ reference surface
+
+    def int8_linear(
+        self, x: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None, out_dtype: Dtype
+    ) -> Tensor:
+        """`x @ W.T + bias` for an int8.convrot weight (`internal/prebuilt.py:99-117`): the GEMV
+        for up to `GEMV_ROWS` rows where it serves, else quantize + GEMM."""
+        flat = self._rows(INT8, x)
+        rows, width = flat.shape
+        bias = self._weight(INT8, data, scale, bias, width, out_dtype)
+        shape = (*x.shape[:-1], data.shape[0])
+        if rows <= self._lib.cozyq_gemv_rows():
+            out = self.torch.empty(shape, dtype=out_dtype, device=x.device)
+            code = 0 if rows == 0 else self._lib.cozyq_gemv(
+                self.index, flat.data_ptr(), self._half(flat.dtype), data.data_ptr(),
+                scale.data_ptr(), _ptr(bias), out.data_ptr(), self._half(out_dtype), rows,
+                data.shape[0], width, self._stream(),
+            )  # fmt: skip
+            if code != self._lib.cozyq_not_supported():
+                self._check(code, "the GEMV")
+                return out
+        q, scales = self.int8_quantize(flat)
+        return self.int8_gemm(q, scales, data, scale, bias, out_dtype).view(shape)
+
+    def fp8_linear(
+        self, x: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None, out_dtype: Dtype
+    ) -> Tensor:
+        """`x @ W.T + bias` for an fp8.rowwise weight (`internal/prebuilt.py:119-124`). Up to
+        `FP8_SMALL_ROWS` rows run as one fused launch (quantize + GEMV), more as two."""
+        flat = self._rows(FP8, x)
+        rows, width = flat.shape
+        shape = (*x.shape[:-1], data.shape[0])
+        if 0 < rows <= FP8_SMALL_ROWS:
+            bias = self._weight(FP8, data, scale, bias, width, out_dtype)
+            out = self.torch.empty(shape, dtype=out_dtype, device=x.device)
+            code = self._lib.cozyq_fp8_linear(
+                self.index, flat.data_ptr(), self._half(flat.dtype), data.data_ptr(),
+                scale.data_ptr(), _ptr(bias), out.data_ptr(), self._half(out_dtype), rows,
+                data.shape[0], width, self._stream(),
+            )  # fmt: skip
+            if code != self._lib.cozyq_not_supported():
+                self._check(code, "the fp8 linear")
+                return out
+        q, scales = self.fp8_quantize(flat)
+        return self.fp8_gemm(q, scales, data, scale, bias, out_dtype).view(shape)
+
+    def int8_quantize(
+        self, x: Tensor, scale: Tensor | None = None, shift: Tensor | None = None, norm: int = 0,
+        eps: float = 0.0, activation: int = 0, up: Tensor | None = None,
+    ) -> tuple[Tensor, Tensor]:
+        return self._quantize(INT8, x, scale, shift, norm, eps, activation, up)
+
+    def fp8_quantize(
+        self, x: Tensor, scale: Tensor | None = None, shift: Tensor | None = None, norm: int = 0,
+        eps: float = 0.0, activation: int = 0, up: Tensor | None = None,
+    ) -> tuple[Tensor, Tensor]:
+        return self._quantize(FP8, x, scale, shift, norm, eps, activation, up)
+
+    def int8_gemm(
+        self, q: Tensor, scales: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None,
+        out_dtype: Dtype, config: int = -1, out: Tensor | None = None,
+    ) -> Tensor:
+        return self._gemm(INT8, q, scales, data, scale, bias, out_dtype, config, out)
+
+    def fp8_gemm(
+        self, q: Tensor, scales: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None,
+        out_dtype: Dtype, config: int = -1, out: Tensor | None = None,
+    ) -> Tensor:
+        return self._gemm(FP8, q, scales, data, scale, bias, out_dtype, config, out)
+
+    # ---------------------------------------------------------------- build extensions
+
+    def int8_quantize_rot(self, x: Tensor, rotation: int) -> tuple[Tensor, Tensor]:
+        """Per-token int8 with rotation 256 (the reference's), 128 (H2⊗H4⊗H4⊗H4, 1/√128 folded
+        into the scale) or 0 (none): `cozyq_quantize_rot`."""
+        torch = self.torch
+        multiple = 16 if rotation == 0 else rotation
+        flat = self._rows(_Format("int8", False, multiple), x)
+        rows, width = flat.shape
+        q = torch.empty(rows, width, dtype=torch.int8, device=x.device)
+        scales = torch.empty(rows, dtype=torch.float32, device=x.device)
+        code = self._lib.cozyq_quantize_rot(
+            self.index, flat.data_ptr(), self._half(flat.dtype), q.data_ptr(), scales.data_ptr(),
+            rows, width, rotation, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the quantization")
+        return q, scales
+
+    def int8_gemm_ex(
+        self, q: Tensor, scales: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None,
+        out_dtype: Dtype, epilogue: int = 0, out: Tensor | None = None,
+    ) -> Tensor:
+        """`int8_gemm` for any rotation lane (K % 16), with an epilogue activation
+        (0 none, 1 tanh-GELU)."""
+        return self._gemm(_Format("int8", False, 16), q, scales, data, scale, bias, out_dtype,
+                          -1, out, epilogue)  # fmt: skip
+
+    def int8_acc(self, q: Tensor, data: Tensor) -> Tensor:
+        """The raw int32 `q @ dataᵀ` of the int8 MFMA mainloop (test entry)."""
+        torch = self.torch
+        rows, width = q.shape
+        acc = torch.empty(rows, data.shape[0], dtype=torch.int32, device=q.device)
+        code = self._lib.cozyq_gemm_i32(
+            self.index, q.data_ptr(), data.data_ptr(), acc.data_ptr(), rows, data.shape[0], width,
+            self._stream(),
+        )  # fmt: skip
+        self._check(code, "the int32 GEMM")
+        return acc
+
+    def mx_quantize(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        """`leaves.quantize_activation_mx`'s law (`internal/encoding/leaves.py:1411-1424`):
+        e4m3 `[M, K]` and row-major E8M0 bytes `[M, K/32]`."""
+        torch = self.torch
+        flat = self._rows(_Format("mxfp8", True, MX_BLOCK), x)
+        rows, width = flat.shape
+        q = torch.empty(rows, width, dtype=torch.float8_e4m3fn, device=x.device)
+        scales = torch.empty(rows, width // MX_BLOCK, dtype=torch.uint8, device=x.device)
+        code = self._lib.cozyq_mx_quantize(
+            self.index, flat.data_ptr(), self._half(flat.dtype), q.data_ptr(), scales.data_ptr(),
+            rows, width, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the MX quantization")
+        return q, scales
+
+    def mx_gemm(
+        self, q: Tensor, qscales: Tensor, data: Tensor, wscales: Tensor, bias: Tensor | None,
+        out_dtype: Dtype, out: Tensor | None = None,
+    ) -> Tensor:
+        """`_scaled_mm` with 1x32 E8M0 block scales (`internal/encoding/leaves.py:1509-1519`) on
+        the scaled MFMA; scale grids row-major `[rows, K/32]`."""
+        torch = self.torch
+        if q.dtype != torch.float8_e4m3fn or q.dim() != 2 or not q.is_contiguous():
+            raise ValueError("mx_gemm: q must be a contiguous e4m3 [M, K]")
+        rows, width = q.shape
+        if width % MX.multiple:
+            raise ValueError(f"mx_gemm: K must be a multiple of {MX.multiple}, not {width}")
+        n = data.shape[0]
+        grid = (width // MX_BLOCK,)
+        if qscales.dtype not in (torch.uint8, torch.float8_e8m0fnu) or tuple(qscales.shape) != (rows, *grid):
+            raise ValueError(f"mx_gemm: q scales must be E8M0 bytes [{rows}, {grid[0]}]")
+        if data.dtype != torch.float8_e4m3fn or tuple(data.shape) != (n, width) or not data.is_contiguous():
+            raise ValueError(f"mx_gemm: data must be a contiguous e4m3 [N, {width}]")
+        if wscales.dtype not in (torch.uint8, torch.float8_e8m0fnu) or tuple(wscales.shape) != (n, *grid):
+            raise ValueError(f"mx_gemm: weight scales must be E8M0 bytes [{n}, {grid[0]}]")
+        if n % 8:
+            raise ValueError("mx_gemm: N must be a multiple of 8")
+        self._half(out_dtype)
+        bias = None if bias is None else bias.to(out_dtype).contiguous()
+        direct = out is not None and _writable(out, rows, n, out_dtype, q.device)
+        result = out if direct else torch.empty(rows, n, dtype=out_dtype, device=q.device)
+        if rows == 0:
+            return _landed(result, out)
+        code = self._lib.cozyq_mx_gemm(
+            self.index, q.data_ptr(), qscales.contiguous().data_ptr(), data.data_ptr(),
+            wscales.contiguous().data_ptr(), _ptr(bias), result.data_ptr(), result.stride(0),
+            self._half(out_dtype), rows, n, width, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the MX GEMM")
+        return _landed(result, out)
+
+    def mx_linear(
+        self, x: Tensor, data: Tensor, wscales: Tensor, bias: Tensor | None, out_dtype: Dtype
+    ) -> Tensor:
+        q, qs = self.mx_quantize(x)
+        out = self.mx_gemm(q, qs, data, wscales, bias, out_dtype)
+        return out.view(*x.shape[:-1], data.shape[0])
+
+    def svdq_quantize(
+        self, x: Tensor, p: Tensor, down: Tensor
+    ) -> tuple[Tensor, Tensor, Tensor]:
+        """The int4-g64 activation side (`cozyq_svdq_int4_quantize`): packed codes `[M, K/2]`,
+        fp16 group scales `[M, K/64]` and the low-rank input `bf16(x·downᵀ)` `[M, R]`."""
+        torch = self.torch
+        flat = self._rows(SVDQ, x)
+        rows, width = flat.shape
+        r = int(down.shape[0])
+        if r not in RANKS or tuple(down.shape) != (r, width) or down.dtype != torch.bfloat16:
+            raise ValueError(f"svdq: down must be bf16 [R, {width}], R in {RANKS}")
+        if p.dtype != torch.float32 or p.numel() != width:
+            raise ValueError(f"svdq: p must be float32 with {width} values")
+        act = torch.empty(rows, width // 2, dtype=torch.uint8, device=x.device)
+        ascales = torch.empty(rows, width // INT4_GROUP, dtype=torch.float16, device=x.device)
+        la = torch.empty(rows, r, dtype=torch.bfloat16, device=x.device)
+        code = self._lib.cozyq_svdq_int4_quantize(
+            self.index, flat.data_ptr(), self._half(flat.dtype), p.contiguous().data_ptr(),
+            down.contiguous().data_ptr(), act.data_ptr(), ascales.data_ptr(), la.data_ptr(), rows,
+            width, r, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the svdq quantization")
+        return act, ascales, la
+
+    def svdq_gemm(
+        self, act: Tensor, ascales: Tensor, la: Tensor, w: Tensor, wscales: Tensor, up: Tensor,
+        bias: Tensor | None, out_dtype: Dtype,
+    ) -> Tensor:
+        torch = self.torch
+        rows, width = int(act.shape[0]), 2 * int(act.shape[1])
+        n, r = int(w.shape[0]), int(up.shape[1])
+        if tuple(w.shape) != (n, width // 2) or tuple(wscales.shape) != (n, width // INT4_GROUP):
+            raise ValueError(f"svdq: weight codes [N, {width // 2}] and scales [N, {width // INT4_GROUP}]")
+        if tuple(up.shape) != (n, r) or up.dtype != torch.bfloat16 or tuple(la.shape) != (rows, r):
+            raise ValueError("svdq: up must be bf16 [N, R] and la [M, R]")
+        if n % 8:
+            raise ValueError("svdq: N must be a multiple of 8")
+        self._half(out_dtype)
+        bias = None if bias is None else bias.to(out_dtype).contiguous()
+        out = torch.empty(rows, n, dtype=out_dtype, device=act.device)
+        if rows == 0:
+            return out
+        code = self._lib.cozyq_svdq_int4_gemm(
+            self.index, act.data_ptr(), ascales.data_ptr(), w.data_ptr(), wscales.data_ptr(),
+            la.data_ptr(), up.contiguous().data_ptr(), _ptr(bias), out.data_ptr(),
+            self._half(out_dtype), rows, n, width, r, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the svdq GEMM")
+        return out
+
+    def svdq_linear(
+        self, x: Tensor, p: Tensor, down: Tensor, w: Tensor, wscales: Tensor, up: Tensor,
+        bias: Tensor | None, out_dtype: Dtype,
+    ) -> Tensor:
+        act, ascales, la = self.svdq_quantize(x, p, down)
+        out = self.svdq_gemm(act, ascales, la, w, wscales, up, bias, out_dtype)
+        return out.view(*x.shape[:-1], w.shape[0])
+
+    # ---------------------------------------------------------------------- internals
+
+    def _quantize(
+        self, f: _Format, x: Tensor, scale: Tensor | None, shift: Tensor | None, norm: int,
+        eps: float, activation: int, up: Tensor | None,
+    ) -> tuple[Tensor, Tensor]:
+        """`internal/prebuilt.py:252-291`. The producer prologue (`scale`, `shift`, `norm`,
+        `activation`, `up`) is not served: the C ABI answers NOT_SUPPORTED and this raises."""
+        torch = self.torch
+        if any(v is not None for v in (scale, shift, up)) or norm or activation:
+            raise NotImplementedError(f"{f.name}_quantize: the producer prologue is not served")
+        flat = self._rows(f, x)
+        rows, width = flat.shape
+        q = torch.empty(rows, width, dtype=torch.float8_e4m3fn if f.fp8 else torch.int8,
+                        device=x.device)  # fmt: skip
+        scales = torch.empty(rows, dtype=torch.float32, device=x.device)
+        code = self._lib.cozyq_quantize(
+            self.index, f.fp8, flat.data_ptr(), self._half(flat.dtype), q.data_ptr(),
+            scales.data_ptr(), rows, width, None, None, 0, 0, 1, 0, 0.0, 0, None, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the quantization")
+        return q, scales
+
+    def _gemm(
+        self, f: _Format, q: Tensor, scales: Tensor, data: Tensor, scale: Tensor,
+        bias: Tensor | None, out_dtype: Dtype, config: int, out: Tensor | None = None,
+        epilogue: int = 0,
+    ) -> Tensor:
+        """`internal/prebuilt.py:293-358`: `[M, N]` into `out` where given, written in place when
+        its rows sit 16-byte multiples apart, else copied into it."""
+        torch = self.torch
+        want = torch.float8_e4m3fn if f.fp8 else torch.int8
+        if q.dtype != want or q.dim() != 2 or not q.is_contiguous() or q.data_ptr() % 16:
+            raise ValueError(f"{f.name}_gemm: q must be a contiguous, aligned {want} [M, K]")
+        rows, width = q.shape
+        if scales.dtype != torch.float32 or scales.numel() != rows or not scales.is_contiguous():
+            raise ValueError(f"{f.name}_gemm: scales must be contiguous float32 with {rows} values")
+        if width % f.multiple:
+            raise ValueError(f"{f.name}_gemm: K must be a multiple of {f.multiple}, not {width}")
+        bias = self._weight(f, data, scale, bias, width, out_dtype)
+        n = data.shape[0]
+        direct = out is not None and _writable(out, rows, n, out_dtype, q.device)
+        result = out if direct and out is not None else torch.empty(
+            rows, n, dtype=out_dtype, device=q.device)
+        if rows == 0:
+            return _landed(result, out)
+        if epilogue == 0 and f in (INT8, FP8):
+            code = self._lib.cozyq_gemm(
+                self.index, FAMILIES.index(self.family), f.fp8, q.data_ptr(), scales.data_ptr(),
+                data.data_ptr(), scale.data_ptr(), _ptr(bias), result.data_ptr(),
+                result.stride(0), self._half(out_dtype), rows, n, width, config, None, None,
+                self._stream(),
+            )  # fmt: skip
+        else:
+            code = self._lib.cozyq_gemm_ex(
+                self.index, f.fp8, q.data_ptr(), scales.data_ptr(), data.data_ptr(),
+                scale.data_ptr(), _ptr(bias), result.data_ptr(), result.stride(0),
+                self._half(out_dtype), rows, n, width, epilogue, self._stream(),
+            )  # fmt: skip
+        if code == self._lib.cozyq_not_supported() and config >= 0:
+            raise ValueError(f"{f.name}_gemm: config {config} cannot take {rows}x{width}")
+        self._check(code, "the GEMM")
+        return _landed(result, out)
+
+    def _rows(self, f: _Format, x: Tensor, width: int | None = None) -> Tensor:
+        """`internal/prebuilt.py:360-370`: contiguous, 16-byte aligned rows on this card."""
+        width = x.shape[-1] if width is None else width
+        if not x.is_cuda or x.get_device() != self.index:
+            raise ValueError(f"{f.name}: x must be on cuda:{self.index}")
+        if width % f.multiple or width > self._lib.cozyq_max_k():
+            raise ValueError(f"{f.name}: K must be a multiple of {f.multiple} up to "
+                             f"{self._lib.cozyq_max_k()}, not {width}")  # fmt: skip
+        flat = x.reshape(-1, x.shape[-1]).contiguous()
+        return flat if flat.data_ptr() % 16 == 0 else flat.clone()
+
+    def _weight(
+        self, f: _Format, data: Tensor, scale: Tensor, bias: Tensor | None, width: int,
+        out_dtype: Dtype,
+    ) -> Tensor | None:
+        """`internal/prebuilt.py:372-406`."""
+        key = (data.dtype, scale.dtype, data.data_ptr(), scale.data_ptr(), *data.shape, width,
+               out_dtype)  # fmt: skip
+        if bias is None and key in self._checked and data.is_contiguous():
+            return None
+        torch = self.torch
+        want = torch.float8_e4m3fn if f.fp8 else torch.int8
+        if data.dtype != want or data.dim() != 2 or data.shape[1] != width:
+            raise ValueError(f"{f.name}: data must be {want} [N, {width}]")
+        if not data.is_contiguous() or data.data_ptr() % 16 or data.shape[0] % 8:
+            raise ValueError(f"{f.name}: data must be contiguous, aligned, N a multiple of 8")
+        if scale.dtype != torch.float32 or scale.numel() != data.shape[0]:
+            raise ValueError(f"{f.name}: scale must be float32 with {data.shape[0]} values")
+        if not scale.is_contiguous():
+            raise ValueError(f"{f.name}: scale must be contiguous")
+        on = (data, scale) if bias is None else (data, scale, bias)
+        if any(t.get_device() != self.index for t in on):
+            raise ValueError(f"{f.name}: the weight's tensors must be on cuda:{self.index}")
+        self._half(out_dtype)
+        if bias is None:
+            if len(self._checked) >= CHECKED:
+                self._checked.clear()
+            self._checked.add(key)
+            return None
+        if bias.numel() != data.shape[0]:
+            raise ValueError(f"{f.name}: bias must have {data.shape[0]} values")
+        return bias.to(out_dtype).contiguous()
+
+    def _half(self, dtype: Dtype) -> bool:
+        if dtype not in (self.torch.bfloat16, self.torch.float16):
+            raise ValueError(f"8-bit linear: activations and outputs are bf16 or fp16, not {dtype}")
+        return bool(dtype == self.torch.float16)
+
+    def _stream(self) -> int:
+        return int(self.torch._C._cuda_getCurrentRawStream(self.index))
+
+    def _check(self, code: int, what: str) -> None:
+        """`internal/prebuilt.py:428-434`."""
+        if code == 0:
+            return
+        detail = f"8-bit linear: {what}: {_lib.error_name(code)}"
+        if code == self._lib.cozyq_out_of_memory():
+            raise self.torch.cuda.OutOfMemoryError(detail)
+        raise RuntimeError(detail)
+
+
+def _writable(out: Tensor, rows: int, n: int, dtype: Dtype, device: Any) -> bool:
+    """`internal/prebuilt.py:449-460`."""
+    return (
+        out.dtype == dtype
+        and out.device == device
+        and tuple(out.shape) == (rows, n)
+        and out.stride(1) == 1
+        and out.stride(0) >= n
+        and out.stride(0) * out.element_size() % 16 == 0
+        and out.data_ptr() % 16 == 0
+    )
+
+
+def _landed(result: Tensor, out: Tensor | None) -> Tensor:
+    if out is None or result is out:
+        return result
+    out.copy_(result)
+    return out
+
+
+_LIBRARIES: dict[int, Prebuilt] = {}
+
+
+def library(index: int = 0) -> Prebuilt:
+    """The op library on cuda:`index`, opened once (`internal/prebuilt.py:568-598`). Raises
+    `_lib.KernelsAbsent` where the HIP library is not built or loadable, and RuntimeError where
+    the device is not the gfx950 the library carries."""
+    found = _LIBRARIES.get(index)
+    if found is not None:
+        return found
+    torch = _torch()
+    if not torch.cuda.is_available():
+        raise RuntimeError("cozyq: no GPU visible")
+    arch = torch.cuda.get_device_properties(index).gcnArchName.split(":")[0]
+    carried = _lib.load().cozyq_arch().decode()
+    if arch != carried:
+        raise RuntimeError(f"cozyq carries {carried} device code; cuda:{index} is {arch}")
+    ops = _LIBRARIES[index] = Prebuilt(torch, index)
+    return ops

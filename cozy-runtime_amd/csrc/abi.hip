@@ -1,0 +1,200 @@
+// The C ABI of include/cozyq.h: argument checks, the device guard and the kernel dispatch.
+// Shapes and modes are checked here (hipErrorInvalidValue, as kernels/csrc/gemm.cpp:81-97,
+// 130-133 does); dtypes, contiguity and alignment are the Python caller's, as in the reference.
+#include <hip/hip_runtime.h>
+
+#include "../../include/cozyq.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+// `device` current for one call and the caller's restored after (kernels/csrc/gemm.cpp:22-39).
+class OnDevice {
+  public:
+    explicit OnDevice(int device) {
+        error_ = hipGetDevice(&previous_);
+        if (error_ == hipSuccess && previous_ != device) error_ = hipSetDevice(device);
+    }
+    ~OnDevice() {
+        int now = -1;
+        if (error_ == hipSuccess && hipGetDevice(&now) == hipSuccess && now != previous_)
+            (void)hipSetDevice(previous_);
+    }
+    hipError_t error() const { return error_; }
+
+  private:
+    int previous_ = -1;
+    hipError_t error_ = hipSuccess;
+};
+
+hipStream_t on(void* stream) { return static_cast<hipStream_t>(stream); }
+
+bool fits(int K, int multiple) { return K > 0 && K <= cozyq::kMaxK && K % multiple == 0; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int cozyq_not_supported(void) { return hipErrorNotSupported; }
+int cozyq_out_of_memory(void) { return hipErrorOutOfMemory; }
+int cozyq_gemv_rows(void) { return 4; }
+int cozyq_max_k(void) { return cozyq::kMaxK; }
+const char* cozyq_arch(void) { return "gfx950"; }
+const char* cozyq_error_name(int code) { return hipGetErrorName(static_cast<hipError_t>(code)); }
+
+int cozyq_quantize(int device, int fp8, const void* x, int x_half, void* q, float* scales, int M,
+                   int K, const void* scale, const void* shift, int64_t scale_stride,
+                   int64_t shift_stride, int rows_per_entry, int norm, float eps, int activation,
+                   const void* up, void* stream) {
+    (void)scale_stride; (void)shift_stride; (void)eps;
+    if (!fits(K, fp8 ? 16 : 256) || M < 0 || norm < 0 || norm > 2 || activation < 0 ||
+        activation > 4 || rows_per_entry < 1)
+        return hipErrorInvalidValue;
+    const bool gated = activation == 3 || activation == 4;
+    if (gated && (norm != 0 || scale || shift)) return hipErrorInvalidValue;
+    if (up != nullptr && activation != 4) return hipErrorInvalidValue;
+    if (scale || shift || norm || activation || up) return hipErrorNotSupported;
+    if (M == 0) return hipSuccess;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    if (fp8)
+        return cozyq::fp8_quantize(x, x_half, static_cast<uint8_t*>(q), scales, M, K, on(stream));
+    return cozyq::rotate_quantize(x, x_half, static_cast<int8_t*>(q), scales, M, K, 256,
+                                  on(stream));
+}
+
+int cozyq_quantize_rot(int device, const void* x, int x_half, int8_t* q, float* scales, int M,
+                       int K, int rotation, void* stream) {
+    const int multiple = rotation == 0 ? 16 : rotation;
+    if ((rotation != 0 && rotation != 128 && rotation != 256) || !fits(K, multiple) || M < 0)
+        return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::rotate_quantize(x, x_half, q, scales, M, K, rotation, on(stream));
+}
+
+int cozyq_gemv(int device, const void* x, int x_half, const int8_t* w, const float* w_scale,
+               const void* bias, void* out, int out_half, int M, int N, int K, void* stream) {
+    (void)device; (void)x; (void)x_half; (void)w; (void)w_scale; (void)bias; (void)out;
+    (void)out_half; (void)stream;
+    if (!fits(K, 256) || N < 1 || M < 0) return hipErrorInvalidValue;
+    return hipErrorNotSupported;
+}
+
+static int gemm_checked(int device, int fp8, const void* q, const float* scales, const void* w,
+                        const float* w_scale, const void* bias, void* out, int64_t ldo,
+                        int out_half, int M, int N, int K, int epilogue, int multiple,
+                        void* stream) {
+    if (M < 1 || N < 1 || N % 8 || !fits(K, multiple) || epilogue < 0 || epilogue > 1)
+        return hipErrorInvalidValue;
+    if (ldo < N || ldo % 8 || !aligned16(out)) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    if (fp8)
+        return cozyq::gemm_fp8(static_cast<const uint8_t*>(q), scales,
+                               static_cast<const uint8_t*>(w), w_scale, bias, out, ldo, out_half,
+                               M, N, K, epilogue, on(stream));
+    return cozyq::gemm_int8(static_cast<const int8_t*>(q), scales, static_cast<const int8_t*>(w),
+                            w_scale, bias, out, ldo, out_half, M, N, K, epilogue, on(stream));
+}
+
+int cozyq_gemm(int device, int family, int fp8, const void* q, const float* scales,
+               const void* w, const float* w_scale, const void* bias, void* out, int64_t ldo,
+               int out_half, int M, int N, int K, int config, cozyq_allocate_fn allocate,
+               void* allocate_context, void* stream) {
+    (void)allocate; (void)allocate_context;
+    if (family != 0) return hipErrorInvalidValue;
+    if (config > 0) return hipErrorNotSupported;
+    return gemm_checked(device, fp8, q, scales, w, w_scale, bias, out, ldo, out_half, M, N, K, 0,
+                        fp8 ? 16 : 256, stream);
+}
+
+int cozyq_gemm_ex(int device, int fp8, const void* q, const float* scales, const void* w,
+                  const float* w_scale, const void* bias, void* out, int64_t ldo, int out_half,
+                  int M, int N, int K, int epilogue, void* stream) {
+    return gemm_checked(device, fp8, q, scales, w, w_scale, bias, out, ldo, out_half, M, N, K,
+                        epilogue, 16, stream);
+}
+
+int cozyq_gemm_i32(int device, const int8_t* q, const int8_t* w, int32_t* acc, int M, int N,
+                   int K, void* stream) {
+    if (M < 1 || N < 1 || N % 8 || !fits(K, 16)) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::gemm_int8_acc(q, w, acc, M, N, K, on(stream));
+}
+
+int cozyq_fp8_linear(int device, const void* x, int x_half, const uint8_t* w,
+                     const float* w_scale, const void* bias, void* out, int out_half, int M,
+                     int N, int K, void* stream) {
+    if (M < 0 || N < 1 || N % 8 || !fits(K, 16)) return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::fp8_linear_small(x, x_half, w, w_scale, bias, out, out_half, M, N, K,
+                                   on(stream));
+}
+
+int cozyq_mx_quantize(int device, const void* x, int x_half, uint8_t* q, uint8_t* scales, int M,
+                      int K, void* stream) {
+    if (M < 0 || !fits(K, 32)) return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::mx_quantize(x, x_half, q, scales, M, K, on(stream));
+}
+
+int cozyq_mx_gemm(int device, const uint8_t* q, const uint8_t* q_scales, const uint8_t* w,
+                  const uint8_t* w_scales, const void* bias, void* out, int64_t ldo, int out_half,
+                  int M, int N, int K, void* stream) {
+    if (M < 1 || N < 1 || N % 8 || !fits(K, 128)) return hipErrorInvalidValue;
+    if (ldo < N || ldo % 8 || !aligned16(out)) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::gemm_mx(q, q_scales, w, w_scales, bias, out, ldo, out_half, M, N, K,
+                          on(stream));
+}
+
+int cozyq_svdq_int4_quantize(int device, const void* x, int x_half, const float* p,
+                             const void* down, uint8_t* act, uint16_t* ascales, void* la, int M,
+                             int K, int R, void* stream) {
+    if (M < 0 || !fits(K, 64) || (R != 16 && R != 32 && R != 64)) return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::svdq_int4_quantize(x, x_half, p, down, act, ascales, la, M, K, R, on(stream));
+}
+
+int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales,
+                         const uint8_t* w, const uint16_t* wscales, const void* la,
+                         const void* up, const void* bias, void* out, int out_half, int M, int N,
+                         int K, int R, void* stream) {
+    if (M < 1 || N < 1 || N % 8 || !fits(K, 64) || (R != 16 && R != 32 && R != 64))
+        return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::svdq_int4_gemm(act, ascales, w, wscales, la, up, bias, out, out_half, M, N, K,
+                                 R, on(stream));
+}
+
+void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = cozyq::e4m3_rn(in[i]);
+}
+
+void cozyq_host_mx_byte(const float* amax, uint8_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = cozyq::mx_byte(amax[i]);
+}
+
+int cozyq_probe_mfma(int device, int kind, const void* a, const void* b, const void* sa,
+                     const void* sb, void* d, void* stream) {
+    if (kind < 0 || kind > 3) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::mfma_probe(kind, a, b, sa, sb, d, on(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,125 @@
+// Shared device helpers for the gfx950 kernels: vector types, 16-bit float conversions, the
+// OCP E4M3 and E8M0 encoders, and the MFMA wrappers. Every conversion here rounds exactly as
+// torch's CPU casts do, so kernel outputs can be compared bit for bit with the CPU law.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cozyq {
+
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kMaxK = 32768;
+constexpr float kE4m3Max = 448.0f;
+constexpr float kScaleFloor = 1e-12f;
+
+__host__ __device__ __forceinline__ uint32_t bits_of(float f) { return __builtin_bit_cast(uint32_t, f); }
+__host__ __device__ __forceinline__ float float_of(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// 16-bit activations: bf16 widens by a shift, fp16 by the hardware conversion (exact).
+template <bool kHalf>
+__device__ __forceinline__ float widen(uint16_t h) {
+    if constexpr (kHalf) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, h));
+    } else {
+        return float_of(static_cast<uint32_t>(h) << 16);
+    }
+}
+
+// float32 -> bf16, round to nearest even; NaN -> 0x7FC0 (c10::BFloat16's rule).
+__host__ __device__ __forceinline__ uint16_t bf16_rn(float f) {
+    uint32_t u = bits_of(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+template <bool kHalf>
+__device__ __forceinline__ uint16_t narrow(float f) {
+    if constexpr (kHalf) {
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));  // v_cvt_f16_f32: RNE
+    } else {
+        return bf16_rn(f);
+    }
+}
+
+// float32 -> OCP E4M3FN byte, round to nearest even, subnormals in 2^-9 steps, |v| >= 480 and
+// NaN -> 0x7F with the sign kept: torch's `.to(float8_e4m3fn)` (callers clamp to ±448 first).
+__host__ __device__ __forceinline__ uint8_t e4m3_rn(float v) {
+    const uint32_t u = bits_of(v);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t mag = u & 0x7fffffffu;
+    if (mag >= 0x43f00000u) return static_cast<uint8_t>(sign | 0x7fu);  // >= 480, inf, NaN
+    if (mag < 0x3c800000u) {                                                // < 2^-6: subnormal
+        // |v|·2^9 is exact (a power-of-two scale of a value below 8); rint rounds half to even.
+        const float units = __builtin_rintf(float_of(mag) * 512.0f);
+        return static_cast<uint8_t>(sign | static_cast<uint32_t>(units));
+    }
+    // Normal: keep 3 mantissa bits, round to nearest even at bit 20; a carry bumps the exponent.
+    const uint32_t kept = (mag + 0x7ffffu + ((mag >> 20) & 1u)) >> 20;
+    return static_cast<uint8_t>(sign | (kept - (120u << 3)));
+}
+
+// E4M3FN byte -> float32 (exact).
+__device__ __forceinline__ float e4m3_value(uint32_t b) {
+    const uint32_t sign = (b & 0x80u) << 24;
+    const uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
+    if (e == 0) return float_of(sign | bits_of(static_cast<float>(m) * 0.001953125f));  // m·2^-9
+    return float_of(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+// The MX block exponent byte of a block maximum: clamp(ceil(log2(amax / 448)) + 127, 0, 254),
+// 0 for amax == 0 (internal/encoding/leaves.py:1417-1421), with the ceiling of the log taken
+// exactly from the quotient's bits rather than from a log2 routine.
+__host__ __device__ __forceinline__ uint8_t mx_byte(float amax) {
+    if (!(amax > 0.0f)) return 0;  // exponent -127 -> byte 0
+    const float v = amax / kE4m3Max;
+    const uint32_t u = bits_of(v);
+    const int biased = static_cast<int>((u >> 23) & 0xffu);
+    const uint32_t man = u & 0x7fffffu;
+    int e;
+    if (biased == 0) {  // subnormal quotient: v = man · 2^-149
+        const int msb = 31 - __builtin_clz(man);
+        e = (man & (man - 1)) ? msb - 148 : msb - 149;
+    } else {
+        e = (man == 0) ? biased - 127 : biased - 126;
+    }
+    int b = e + 127;
+    b = b < 0 ? 0 : (b > 254 ? 254 : b);
+    return static_cast<uint8_t>(b);
+}
+
+// 2^(byte - 127) as float32 by construction; byte 0 is 2^-127 (formats.py:577-585).
+__device__ __forceinline__ float e8m0_value(uint32_t b) {
+    return b == 0 ? float_of(1u << 22) : float_of(b << 23);
+}
+
+// ---------------------------------------------------------------------------------- MFMA
+// D(16x16) += A(16xK)·B(Kx16). Lane l supplies row l%16 of A and column l%16 of B, its K
+// slice chosen by l/16; both operands loaded with the same pattern pair every k correctly.
+// The result's lane l holds rows 4·(l/16)+r (r = 0..3) of column l%16.
+
+__device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// e4m3 x e4m3, K = 128 per call (format code 0 for both operands), float32 accumulate.
+__device__ __forceinline__ f32x4 mfma_f8(i32x8 a, i32x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// The same with an E8M0 scale per lane for each operand (its 32-element K block).
+__device__ __forceinline__ f32x4 mfma_f8_scaled(i32x8 a, i32x8 b, f32x4 c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace cozyq

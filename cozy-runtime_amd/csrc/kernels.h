@@ -1,0 +1,46 @@
+// Launchers of the gfx950 kernels, called by the C ABI (abi.hip) after it has checked the
+// arguments. Each enqueues on `s` and returns the launch's error code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cozyq {
+
+hipError_t rotate_quantize(const void* x, bool x_half, int8_t* q, float* scales, int M, int K,
+                           int rotation, hipStream_t s);
+hipError_t fp8_quantize(const void* x, bool x_half, uint8_t* q, float* scales, int M, int K,
+                        hipStream_t s);
+hipError_t mx_quantize(const void* x, bool x_half, uint8_t* q, uint8_t* scales, int M, int K,
+                       hipStream_t s);
+
+hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
+                     const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
+                     int epilogue, hipStream_t s);
+hipError_t gemm_fp8(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
+                    const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
+                    int epilogue, hipStream_t s);
+hipError_t gemm_mx(const uint8_t* q, const uint8_t* qe, const uint8_t* w, const uint8_t* we,
+                   const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
+                   hipStream_t s);
+hipError_t gemm_int8_acc(const int8_t* q, const int8_t* w, int32_t* acc, int M, int N, int K,
+                         hipStream_t s);
+
+hipError_t fp8_linear_small(const void* x, bool x_half, const uint8_t* w, const float* ws,
+                            const void* bias, void* out, bool out_half, int M, int N, int K,
+                            hipStream_t s);
+
+hipError_t svdq_int4_quantize(const void* x, bool x_half, const float* p, const void* down,
+                              uint8_t* act, uint16_t* ascales, void* la, int M, int K, int R,
+                              hipStream_t s);
+hipError_t svdq_int4_gemm(const uint8_t* act, const uint16_t* ascales, const uint8_t* w,
+                          const uint16_t* wscales, const void* la, const void* up,
+                          const void* bias, void* out, bool out_half, int M, int N, int K, int R,
+                          hipStream_t s);
+
+}  // namespace cozyq
+
+namespace cozyq {
+hipError_t mfma_probe(int kind, const void* a, const void* b, const void* sa, const void* sb,
+                      void* d, hipStream_t s);
+}  // namespace cozyq

@@ -1,0 +1,49 @@
+// Test entry: one MFMA of each kind the kernels use, on operands given per lane, so a GPU test
+// can confirm the lane layouts the GEMMs assume (which row/column/K slice a lane supplies, which
+// outputs it receives, and which K block an E8M0 scale applies to) against a CPU product.
+#include "common.h"
+#include "kernels.h"
+
+namespace cozyq {
+namespace {
+
+// a, b: 64 lanes x 32 bytes (i8 and bf16 kinds use the first 16); sa, sb: 64 bytes;
+// d: 64 lanes x 4 words (int32 or float32).
+__global__ void mfma_probe_kernel(int kind, const uint8_t* a, const uint8_t* b, const uint8_t* sa,
+                                  const uint8_t* sb, uint32_t* d) {
+    const int l = threadIdx.x;
+    const i32x8 a8 = *reinterpret_cast<const i32x8*>(a + 32 * l);
+    const i32x8 b8 = *reinterpret_cast<const i32x8*>(b + 32 * l);
+    const i32x4 a4 = {a8[0], a8[1], a8[2], a8[3]};
+    const i32x4 b4 = {b8[0], b8[1], b8[2], b8[3]};
+    uint32_t r[4];
+    if (kind == 0) {
+        const i32x4 c = mfma_i8(a4, b4, i32x4{0, 0, 0, 0});
+        for (int i = 0; i < 4; ++i) r[i] = static_cast<uint32_t>(c[i]);
+    } else if (kind == 1) {
+        const f32x4 c = mfma_f8(a8, b8, f32x4{0, 0, 0, 0});
+        for (int i = 0; i < 4; ++i) r[i] = bits_of(c[i]);
+    } else if (kind == 2) {
+        const f32x4 c = mfma_f8_scaled(a8, b8, f32x4{0, 0, 0, 0}, sa[l], sb[l]);
+        for (int i = 0; i < 4; ++i) r[i] = bits_of(c[i]);
+    } else {
+        const bf16x8 ab = __builtin_bit_cast(bf16x8, a4);
+        const bf16x8 bb = __builtin_bit_cast(bf16x8, b4);
+        const f32x4 c = mfma_bf16(ab, bb, f32x4{0, 0, 0, 0});
+        for (int i = 0; i < 4; ++i) r[i] = bits_of(c[i]);
+    }
+    for (int i = 0; i < 4; ++i) d[4 * l + i] = r[i];
+}
+
+}  // namespace
+
+hipError_t mfma_probe(int kind, const void* a, const void* b, const void* sa, const void* sb,
+                      void* d, hipStream_t s) {
+    mfma_probe_kernel<<<1, 64, 0, s>>>(kind, static_cast<const uint8_t*>(a),
+                                       static_cast<const uint8_t*>(b),
+                                       static_cast<const uint8_t*>(sa),
+                                       static_cast<const uint8_t*>(sb), static_cast<uint32_t*>(d));
+    return hipGetLastError();
+}
+
+}  // namespace cozyq

@@ -1,0 +1,306 @@
+// Per-token activation quantization for gfx950: the block-Hadamard rotation with int8
+// quantization, the rowwise E4M3 quantization and the MX (E8M0 per 32) quantization.
+//
+// Each kernel reproduces the reference's CPU torch law bit for bit: the rotation's float32
+// additions in the law's stage order and association (internal/encoding/formats.py:667-671),
+// correctly rounded float32 division (internal/int8_linear.py:427, internal/fp8_linear.py:
+// 62-63), round-half-even and the casts of `common.h`. All three are HBM-bound: one read of the
+// 16-bit rows, one write of the codes.
+#include "common.h"
+#include "kernels.h"
+
+namespace cozyq {
+namespace {
+
+constexpr int kThreads = 256;
+// The rotated kernel stages 4096 elements of a row through LDS at a time: 16 groups of 256 or
+// 32 of 128, one phase-3 task (16 contiguous outputs) per thread per chunk.
+constexpr int kChunk = 4096;
+
+// LDS position of element `lo` (0..15) of 16-run `hi` of group `g`: runs padded to 20 floats and
+// groups by 16 more, so both the strided (phase 2) and the contiguous (phase 3) reads of a wave
+// fall on distinct banks.
+template <int kRot>
+struct Layout {
+    static constexpr int kRuns = kRot / 16;             // 16-runs per group
+    static constexpr int kGroupStride = kRuns * 20 + 16;
+    static constexpr int kGroups = kChunk / kRot;       // groups per chunk
+    static constexpr int kFloats = kGroups * kGroupStride;
+    __device__ static int at(int g, int hi, int lo) { return g * kGroupStride + hi * 20 + lo; }
+};
+
+__device__ __forceinline__ void h4(float& a, float& b, float& c, float& d) {
+    // formats.py:670: (a+b+c-d, a+b-c+d, a-b+c+d, b+c+d-a), each left to right.
+    const float o0 = a + b + c - d;
+    const float o1 = a + b - c + d;
+    const float o2 = a - b + c + d;
+    const float o3 = b + c + d - a;
+    a = o0; b = o1; c = o2; d = o3;
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) m = fmaxf(m, red[w]);
+    __syncthreads();
+    return m;
+}
+
+// Loads 8 consecutive 16-bit values as floats.
+template <bool kHalf>
+__device__ __forceinline__ void load8(const uint16_t* p, float* v) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = widen<kHalf>(static_cast<uint16_t>(w[i] & 0xffffu));
+        v[2 * i + 1] = widen<kHalf>(static_cast<uint16_t>(w[i] >> 16));
+    }
+}
+
+__device__ __forceinline__ int8_t q8(float v, float scale) {
+    // torch.round(r / s).clamp_(-127, 127): IEEE division, half to even, clamp.
+    float r = __builtin_rintf(v / scale);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return static_cast<int8_t>(static_cast<int>(r));
+}
+
+// Rotation by H_kRot (256: H4^⊗4 then ·1/16; 128: H2⊗H4^⊗3 unnormalized) and per-row int8.
+// One block per row; kMaxChunks bounds the row's 4096-element chunks held in registers.
+template <bool kHalf, int kRot, int kMaxChunks>
+__global__ __launch_bounds__(kThreads) void rotate_quantize_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales, int K) {
+    using L = Layout<kRot>;
+    __shared__ __attribute__((aligned(16))) float lds[L::kFloats];
+    __shared__ float red[kThreads / 64];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const uint16_t* xr = x + static_cast<int64_t>(row) * K;
+    const int chunks = (K + kChunk - 1) / kChunk;
+    float out[kMaxChunks][16];
+    float amax = 0.0f;
+
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+        if (c >= chunks) break;
+        const int base = c * kChunk;
+        const int width = min(kChunk, K - base);
+        // Phase 1: the chunk into LDS, 16 bytes a load.
+        for (int e = tid * 8; e < width; e += kThreads * 8) {
+            float v[8];
+            load8<kHalf>(xr + base + e, v);
+            const int g = e / kRot, within = e % kRot;
+            float* dst = lds + L::at(g, within / 16, within % 16);
+            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<float4*>(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        __syncthreads();
+        // Phase 2: the outer two stages; thread holds one column `t` of a group's runs.
+        const int groups = width / kRot;
+        for (int task = tid; task < groups * 16; task += kThreads) {
+            const int g = task / 16, t = task % 16;
+            float v[L::kRuns];
+#pragma unroll
+            for (int hi = 0; hi < L::kRuns; ++hi) v[hi] = lds[L::at(g, hi, t)];
+            if constexpr (kRot == 256) {
+#pragma unroll
+                for (int d2 = 0; d2 < 4; ++d2) h4(v[d2], v[4 + d2], v[8 + d2], v[12 + d2]);
+#pragma unroll
+                for (int d1 = 0; d1 < 4; ++d1) h4(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
+            } else {
+#pragma unroll
+                for (int d2 = 0; d2 < 4; ++d2) {
+                    const float a = v[d2], b = v[4 + d2];
+                    v[d2] = a + b;
+                    v[4 + d2] = a - b;
+                }
+#pragma unroll
+                for (int d1 = 0; d1 < 2; ++d1) h4(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
+            }
+#pragma unroll
+            for (int hi = 0; hi < L::kRuns; ++hi) lds[L::at(g, hi, t)] = v[hi];
+        }
+        __syncthreads();
+        // Phase 3: the inner two stages on one contiguous 16-run per thread.
+        {
+            const int g = tid / L::kRuns, hi = tid % L::kRuns;
+            float* w = out[c];
+            if (g < groups) {
+                const float* src = lds + L::at(g, hi, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 f = *reinterpret_cast<const float4*>(src + 4 * i);
+                    w[4 * i] = f.x; w[4 * i + 1] = f.y; w[4 * i + 2] = f.z; w[4 * i + 3] = f.w;
+                }
+#pragma unroll
+                for (int d4 = 0; d4 < 4; ++d4) h4(w[d4], w[4 + d4], w[8 + d4], w[12 + d4]);
+#pragma unroll
+                for (int d3 = 0; d3 < 4; ++d3) h4(w[4 * d3], w[4 * d3 + 1], w[4 * d3 + 2], w[4 * d3 + 3]);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    if constexpr (kRot == 256) w[i] = w[i] * 0.0625f;  // .mul_(1.0 / 16), exact
+                    amax = fmaxf(amax, fabsf(w[i]));
+                }
+            }
+        }
+        __syncthreads();
+    }
+    amax = block_max(amax, red);
+    const float scale = fmaxf(amax / 127.0f, kScaleFloor);
+    if (tid == 0) scales[row] = kRot == 128 ? scale * 0.08838834764831845f : scale;
+    int8_t* qr = q + static_cast<int64_t>(row) * K;
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+        if (c >= chunks) break;
+        const int base = c * kChunk;
+        const int groups = min(kChunk, K - base) / kRot;
+        const int g = tid / L::kRuns, hi = tid % L::kRuns;
+        if (g >= groups) continue;
+        uint32_t packed[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                word |= (static_cast<uint32_t>(static_cast<uint8_t>(q8(out[c][4 * i + j], scale)))) << (8 * j);
+            packed[i] = word;
+        }
+        *reinterpret_cast<uint4*>(qr + base + g * kRot + hi * 16) =
+            make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    }
+}
+
+// Per-row int8 without rotation (build lane): s = max(amax/127, 1e-12), q = clamp(rne(x/s)).
+// Per-row E4M3 (fp8 = true): s = max(amax/448, 1e-12), q = e4m3(clamp(x/s, ±448)).
+// One block per row; two passes over the row (the second from cache).
+template <bool kHalf, bool kFp8>
+__global__ __launch_bounds__(kThreads) void rowwise_quantize_kernel(
+    const uint16_t* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scales, int K) {
+    __shared__ float red[kThreads / 64];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const uint16_t* xr = x + static_cast<int64_t>(row) * K;
+    float amax = 0.0f;
+    for (int e = tid * 8; e < K; e += kThreads * 8) {
+        float v[8];
+        load8<kHalf>(xr + e, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    }
+    amax = block_max(amax, red);
+    const float scale = fmaxf(amax / (kFp8 ? kE4m3Max : 127.0f), kScaleFloor);
+    if (tid == 0) scales[row] = scale;
+    uint8_t* qr = q + static_cast<int64_t>(row) * K;
+    for (int e = tid * 8; e < K; e += kThreads * 8) {
+        float v[8];
+        load8<kHalf>(xr + e, v);
+        uint32_t word[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t b;
+            if constexpr (kFp8) {
+                const float r = fminf(fmaxf(v[i] / scale, -kE4m3Max), kE4m3Max);
+                b = e4m3_rn(r);
+            } else {
+                b = static_cast<uint8_t>(q8(v[i], scale));
+            }
+            word[i / 4] |= b << (8 * (i % 4));
+        }
+        *reinterpret_cast<uint2*>(qr + e) = make_uint2(word[0], word[1]);
+    }
+}
+
+// MX quantization: 4 threads per 32-element block, 8 elements each.
+template <bool kHalf>
+__global__ __launch_bounds__(kThreads) void mx_quantize_kernel(
+    const uint16_t* __restrict__ x, uint8_t* __restrict__ q, uint8_t* __restrict__ scales,
+    int64_t total8) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    // Every lane takes part in the shuffles; lanes past the end work on a clamped copy.
+    const int64_t at = i < total8 ? i : total8 - 1;
+    float v[8];
+    load8<kHalf>(x + at * 8, v);
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const uint32_t byte = mx_byte(amax);
+    // x / 2^(byte-127) as x · 2^(127-byte): the same real number, rounded once either way.
+    const float inv = byte >= 254 ? float_of(1u << 22) : float_of((254u - byte) << 23);
+    if (i >= total8) return;
+    uint32_t word[2] = {0, 0};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float r = fminf(fmaxf(v[k] * inv, -kE4m3Max), kE4m3Max);
+        word[k / 4] |= static_cast<uint32_t>(e4m3_rn(r)) << (8 * (k % 4));
+    }
+    *reinterpret_cast<uint2*>(q + i * 8) = make_uint2(word[0], word[1]);
+    if ((i & 3) == 0) scales[i >> 2] = static_cast<uint8_t>(byte);
+}
+
+template <bool kHalf, int kRot>
+hipError_t launch_rotated(const void* x, int8_t* q, float* scales, int M, int K, hipStream_t s) {
+    const int chunks = (K + kChunk - 1) / kChunk;
+    const dim3 grid(M), block(kThreads);
+    auto xp = static_cast<const uint16_t*>(x);
+    if (chunks <= 1)
+        rotate_quantize_kernel<kHalf, kRot, 1><<<grid, block, 0, s>>>(xp, q, scales, K);
+    else if (chunks <= 2)
+        rotate_quantize_kernel<kHalf, kRot, 2><<<grid, block, 0, s>>>(xp, q, scales, K);
+    else if (chunks <= 4)
+        rotate_quantize_kernel<kHalf, kRot, 4><<<grid, block, 0, s>>>(xp, q, scales, K);
+    else
+        rotate_quantize_kernel<kHalf, kRot, 8><<<grid, block, 0, s>>>(xp, q, scales, K);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t rotate_quantize(const void* x, bool x_half, int8_t* q, float* scales, int M, int K,
+                           int rotation, hipStream_t s) {
+    if (M == 0) return hipSuccess;
+    if (rotation == 0) {
+        auto xp = static_cast<const uint16_t*>(x);
+        auto qp = reinterpret_cast<uint8_t*>(q);
+        if (x_half)
+            rowwise_quantize_kernel<true, false><<<M, kThreads, 0, s>>>(xp, qp, scales, K);
+        else
+            rowwise_quantize_kernel<false, false><<<M, kThreads, 0, s>>>(xp, qp, scales, K);
+        return hipGetLastError();
+    }
+    if (rotation == 256)
+        return x_half ? launch_rotated<true, 256>(x, q, scales, M, K, s)
+                      : launch_rotated<false, 256>(x, q, scales, M, K, s);
+    if (rotation == 128)
+        return x_half ? launch_rotated<true, 128>(x, q, scales, M, K, s)
+                      : launch_rotated<false, 128>(x, q, scales, M, K, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t fp8_quantize(const void* x, bool x_half, uint8_t* q, float* scales, int M, int K,
+                        hipStream_t s) {
+    if (M == 0) return hipSuccess;
+    auto xp = static_cast<const uint16_t*>(x);
+    if (x_half)
+        rowwise_quantize_kernel<true, true><<<M, kThreads, 0, s>>>(xp, q, scales, K);
+    else
+        rowwise_quantize_kernel<false, true><<<M, kThreads, 0, s>>>(xp, q, scales, K);
+    return hipGetLastError();
+}
+
+hipError_t mx_quantize(const void* x, bool x_half, uint8_t* q, uint8_t* scales, int M, int K,
+                       hipStream_t s) {
+    const int64_t total8 = static_cast<int64_t>(M) * K / 8;
+    if (total8 == 0) return hipSuccess;
+    const int64_t blocks = (total8 + kThreads - 1) / kThreads;
+    auto xp = static_cast<const uint16_t*>(x);
+    if (x_half)
+        mx_quantize_kernel<true><<<blocks, kThreads, 0, s>>>(xp, q, scales, total8);
+    else
+        mx_quantize_kernel<false><<<blocks, kThreads, 0, s>>>(xp, q, scales, total8);
+    return hipGetLastError();
+}
+
+}  // namespace cozyq

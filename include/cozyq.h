@@ -1,0 +1,152 @@
+/* cozyq — MI355X (gfx950) quantized-linear kernels behind a C ABI.
+ *
+ * The drop-in replacement for cozy-runtime's native `_kernels._gemm` module
+ * (reference: kernels/csrc/gemm.cpp:194-222, stubs src/cozy_runtime/_kernels/_gemm.pyi:1-116).
+ * Arguments are raw device pointers, sizes and a HIP stream: neither torch nor Python is a
+ * build input, and the caller allocates every operand and output. Every call returns a
+ * hipError_t code: 0 ran; hipErrorNotSupported (cozyq_not_supported()) means no kernel takes
+ * this shape and the caller decides; hipErrorInvalidValue rejects arguments; hipErrorOutOfMemory
+ * (cozyq_out_of_memory()) is the device's. Launches go on `stream` with `device` current for the
+ * call and the caller's device restored afterwards. No entry point allocates or synchronizes,
+ * so each may be recorded into a HIP graph.
+ *
+ * Layouts: activations and outputs are row-major with the reduction axis K last; weights are
+ * [N, K] row-major (the nn.Linear layout); per-row scales are float32. `x_half` / `out_half`
+ * select fp16 (1) or bf16 (0) for 16-bit tensors.
+ */
+#ifndef COZYQ_H
+#define COZYQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Constants (reference: gemm.cpp:194-203 `NOT_SUPPORTED`, `OUT_OF_MEMORY`, `GEMV_ROWS`, `MAX_K`). */
+int cozyq_not_supported(void);
+int cozyq_out_of_memory(void);
+int cozyq_gemv_rows(void);
+int cozyq_max_k(void);
+/* The device-code target this library carries, e.g. "gfx950". */
+const char* cozyq_arch(void);
+
+/* hipGetErrorName of a returned code (reference: gemm.cpp:204 `error_name`). */
+const char* cozyq_error_name(int code);
+
+/* Per-token activation quantization (reference: gemm.cpp:83-115 `quantize`, law
+ * internal/int8_linear.py:422-428 for int8 and internal/fp8_linear.py:56-63 for fp8).
+ * fp8 = 0: each row rotated by H256/16 (regular H4⊗H4⊗H4⊗H4) and quantized to int8 with
+ *          scales[m] = max(amax/127, 1e-12); K % 256 == 0.
+ * fp8 = 1: each row quantized to OCP E4M3 with scales[m] = max(amax/448, 1e-12); K % 16 == 0.
+ * q: [M, K] (int8 or e4m3 bytes); scales: [M] float32. K <= cozyq_max_k().
+ * scale/shift/norm/activation/up describe the reference's producer prologue; this build
+ * serves none yet: any of them set returns hipErrorNotSupported. */
+int cozyq_quantize(int device, int fp8, const void* x, int x_half, void* q, float* scales, int M,
+                   int K, const void* scale, const void* shift, int64_t scale_stride,
+                   int64_t shift_stride, int rows_per_entry, int norm, float eps, int activation,
+                   const void* up, void* stream);
+
+/* int8 quantization with an explicit rotation (no reference counterpart: the reference's int8
+ * lane always rotates by 256). rotation 256 is cozyq_quantize's law; 0 is plain per-token int8
+ * (K % 16 == 0); 128 is H2⊗H4⊗H4⊗H4 with the unnormalized sums quantized and the 1/sqrt(128)
+ * folded into scales[m] (K % 128 == 0). */
+int cozyq_quantize_rot(int device, const void* x, int x_half, int8_t* q, float* scales, int M,
+                       int K, int rotation, void* stream);
+
+/* The fused few-row int8 linear (reference: gemm.cpp:117-125 `gemv`, rotate.cu:351-407).
+ * Not served by this build yet: returns hipErrorNotSupported, and callers quantize + GEMM. */
+int cozyq_gemv(int device, const void* x, int x_half, const int8_t* w, const float* w_scale,
+               const void* bias, void* out, int out_half, int M, int N, int K, void* stream);
+
+/* A caller-provided scratch allocator (reference: gemm.cpp:55-67 `allocate`); may be NULL.
+ * This build's GEMMs need no scratch and never call it. */
+typedef void* (*cozyq_allocate_fn)(size_t bytes, void* context);
+
+/* The quantized GEMM with the dequantizing epilogue (reference: gemm.cpp:127-145 `gemm`,
+ * epilogue contract int8.h:65-71):
+ *   out[m, n] = (acc[m, n] · scales[m]) · w_scale[n] (+ bias[n]),
+ * acc the exact int32 (fp8 = 0, int8 q and w) or float32 (fp8 = 1, e4m3 q and w) sum over K.
+ * int8: rounded as internal/int8_linear.py:445-448 + :276 (two float32 products, one cast,
+ * then the bias added in the output dtype), bit-for-bit. fp8: float32 accumulation, one cast.
+ * out rows are `ldo` elements apart (ldo >= N, ldo % 8 == 0, out 16-byte aligned). family must
+ * be 0 (the one CDNA4 MFMA family); config -1 chooses by shape, 0 names the 256x256 tile,
+ * other values return hipErrorNotSupported. N % 8 == 0; K % 256 (int8) or K % 16 (fp8). */
+int cozyq_gemm(int device, int family, int fp8, const void* q, const float* scales,
+               const void* w, const float* w_scale, const void* bias, void* out, int64_t ldo,
+               int out_half, int M, int N, int K, int config, cozyq_allocate_fn allocate,
+               void* allocate_context, void* stream);
+
+/* cozyq_gemm with an epilogue activation (no reference counterpart: the reference's epilogue
+ * is scales + bias only). epilogue 0: none; 1: tanh-GELU applied in float32 to the result of
+ * cozyq_gemm's arithmetic, then cast. int8 K % 16 == 0 (any rotation lane). */
+int cozyq_gemm_ex(int device, int fp8, const void* q, const float* scales, const void* w,
+                  const float* w_scale, const void* bias, void* out, int64_t ldo, int out_half,
+                  int M, int N, int K, int epilogue, void* stream);
+
+/* Test entry (no reference counterpart): the raw int32 accumulators acc = q·wᵀ of the int8
+ * GEMM, [M, N] row-major, for bit-exact checks of the MFMA mainloop. */
+int cozyq_gemm_i32(int device, const int8_t* q, const int8_t* w, int32_t* acc, int M, int N,
+                   int K, void* stream);
+
+/* The fp8 linear for few rows in one launch (no reference counterpart: the reference has no
+ * fp8 GEMV, internal/fp8_linear.py:114-129 quantizes then multiplies): each row of x quantized
+ * by cozyq_quantize's fp8 law inside the kernel, then out = acc·s_x·w_scale (+ bias).
+ * M <= 16, K % 16 == 0. */
+int cozyq_fp8_linear(int device, const void* x, int x_half, const uint8_t* w,
+                     const float* w_scale, const void* bias, void* out, int out_half, int M,
+                     int N, int K, void* stream);
+
+/* MXFP8 activation quantization (law: internal/encoding/leaves.py:1411-1424): per 32-block
+ * of each row, byte = clamp(ceil(log2(amax/448)) + 127, 0, 254) (0 blocks: 0), elements
+ * e4m3(clamp(x / 2^(byte-127), ±448)). q: [M, K] e4m3; scales: [M, K/32] E8M0, row-major.
+ * K % 32 == 0. */
+int cozyq_mx_quantize(int device, const void* x, int x_half, uint8_t* q, uint8_t* scales, int M,
+                      int K, void* stream);
+
+/* MXFP8 GEMM on the E8M0-scaled MFMA (reference: internal/encoding/leaves.py:1509-1519, which
+ * calls cuBLASLt's `_scaled_mm` with 1x32 block scales):
+ *   out[m, n] = Σ_k (q[m,k]·2^(qs[m,k/32]-127))·(w[n,k]·2^(ws[n,k/32]-127)) (+ bias[n]),
+ * float32 accumulation, one cast. Scale grids are row-major [rows, K/32] (not cuBLAS's 128x4).
+ * K % 128 == 0, N % 8 == 0, ldo as cozyq_gemm. */
+int cozyq_mx_gemm(int device, const uint8_t* q, const uint8_t* q_scales, const uint8_t* w,
+                  const uint8_t* w_scales, const void* bias, void* out, int64_t ldo, int out_half,
+                  int M, int N, int K, void* stream);
+
+/* SVDQuant W4A4 activation side, int4-g64 variant (reference: gemm.cpp:169-178
+ * `svdq_quantize`, whose law is nvfp4): xs = bf16(x·p); per 64-group of each row
+ * s = fp16(amax/7), code = clamp(rne(xs/s), -8, 7) (0 where s == 0), packed two a byte,
+ * element 2k low: act [M, K/2], ascales [M, K/64] fp16. Also the low-rank input
+ * la = bf16(x · downᵀ), down [R, K] bf16, la [M, R] bf16. K % 64 == 0, R in {16, 32, 64}. */
+int cozyq_svdq_int4_quantize(int device, const void* x, int x_half, const float* p,
+                             const void* down, uint8_t* act, uint16_t* ascales, void* la, int M,
+                             int K, int R, void* stream);
+
+/* SVDQuant W4A4 GEMM, int4-g64 variant (reference: gemm.cpp:180-190 `svdq_gemm`, svdq.cu:
+ * 446-485): out = Σ_g (Σ_{k∈g} act·w)·ascales[m,g]·wscales[n,g] + la·upᵀ + bias, float32
+ * accumulation, one cast. w [N, K/2] packed like act; wscales [N, K/64] fp16; up [N, R] bf16.
+ * K % 64 == 0, N % 8 == 0. */
+int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales,
+                         const uint8_t* w, const uint16_t* wscales, const void* la,
+                         const void* up, const void* bias, void* out, int out_half, int M, int N,
+                         int K, int R, void* stream);
+
+/* Test entries (no reference counterpart): the kernels' scalar conversions run on the host,
+ * so CPU tests can hold the device code's arithmetic against torch without a GPU. */
+void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n);
+void cozyq_host_mx_byte(const float* amax, uint8_t* out, int64_t n);
+
+/* Test entry (no reference counterpart): one 16x16 MFMA on per-lane operands, to confirm the
+ * lane layouts the GEMMs rely on. kind 0: i32_16x16x64_i8 (a, b: 64 lanes x 16 bytes);
+ * 1: f32_16x16x128_f8f6f4 e4m3 (64 lanes x 32 bytes); 2: the same with E8M0 scales sa, sb
+ * (one byte a lane); 3: f32_16x16x32_bf16 (64 lanes x 16 bytes). a and b are read as 64 lanes
+ * x 32 bytes; d receives 64 lanes x 4 int32/float32 words. */
+int cozyq_probe_mfma(int device, int kind, const void* a, const void* b, const void* sa,
+                     const void* sb, void* d, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* COZYQ_H */

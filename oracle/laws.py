@@ -1,0 +1,460 @@
+"""CPU restatement of the quantized-linear laws — TEST INFRASTRUCTURE ONLY (see `oracle/__init__`).
+
+Every function restates one law of cozy-runtime (`/root/reference`, cited `path:line`, paths
+relative to `src/cozy_runtime/`) in torch CPU ops, operation for operation, so that the float32
+rounding sequence is the reference's. Where this build adds a law the reference lacks (the
+128-channel rotation, the rotation-off int8 lane, the tanh-GELU epilogue, the int4-g64 SVDQuant
+variant), the docstring says "build law" and names what pins it.
+
+Pins, exercised in `tests/test_oracle.py`:
+- `hadamard` (256): the reference's int8.convrot decode vectors (signs and index order) and the
+  closed form H·H = n·I; float32 association order: the expression text at
+  `internal/encoding/formats.py:667-671`, which the code below evaluates left to right.
+- `e4m3`, `e8m0_multipliers`, `to_blocked`/`from_blocked`: the reference's fp8 and mxfp8 decode
+  vectors, plus an independent bit-level e4m3 encoder checked over every bf16/fp16 input.
+- `mx_quantize`: brute force over every positive bf16 and fp16 block maximum (exact integer ceil
+  of log2) and the round trip through the mxfp8 decode law.
+- `int8_*` products: int32 GEMM against numpy int64 matmul.
+- `int4_quantize` (build law): round trip bound |x − q·s| ≤ s/2 and brute force on small cases.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+#: E4M3's largest finite magnitude (`internal/encoding/formats.py:497`).
+E4M3_MAX = 448.0
+#: A derived scale's floor (`internal/fp8_linear.py:24`, `internal/int8_linear.py:426`).
+SCALE_FLOOR = 1e-12
+#: MX block along K (`internal/encoding/formats.py:118`).
+MX_BLOCK = 32
+#: The reference's rotation sizes `4**k` (`internal/encoding/formats.py:661`); 128 is this
+#: build's extension (H2 ⊗ H4 ⊗ H4 ⊗ H4).
+ROTATION_SIZES = tuple(4**k for k in range(1, 9))
+#: int4 SVDQuant variant: K-group and code range (build law).
+INT4_GROUP = 64
+INT4_MAX = 7.0
+
+
+# ----------------------------------------------------------------------------- rotation
+
+
+def _digits(size: int) -> list[int]:
+    """The radices of the rotation's stages, outer digit first."""
+    if size in ROTATION_SIZES:
+        return [4] * ROTATION_SIZES.index(size) + [4]
+    if size == 128:
+        return [2, 4, 4, 4]
+    raise ValueError(f"rotation size {size} is neither 4**k nor 128")
+
+
+def hadamard(x: torch.Tensor, size: int) -> torch.Tensor:
+    """Each `size`-group of the last axis times the unnormalized Hadamard, one stage per digit,
+    outer digit first (`internal/encoding/formats.py:657-671`; numpy twin
+    `derive/microscale.py:272-282`). A 4-point stage maps (a, b, c, d) to
+    (a+b+c-d, a+b-c+d, a-b+c+d, b+c+d-a), each evaluated left to right in x's dtype. Size 128
+    (build law) puts the Sylvester 2-point stage (a+b, a-b) first, then three 4-point stages."""
+    shape = x.shape
+    digits = _digits(size)
+    work = x.reshape(-1, *digits)
+    for axis in range(1, len(digits) + 1):
+        parts = work.unbind(axis)
+        if len(parts) == 4:
+            a, b, c, d = parts
+            out = (a + b + c - d, a + b - c + d, a - b + c + d, b + c + d - a)
+        else:
+            a, b = parts
+            out = (a + b, a - b)
+        work = torch.stack(out, axis)
+    return work.reshape(shape)
+
+
+# ------------------------------------------------------------------------- int8 lanes
+
+
+def quantize_rows_int8(x: torch.Tensor, rotation: int = 256) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-token int8 of the rotated rows: `int8_linear.quantize_rows`
+    (`internal/int8_linear.py:422-428`) for `rotation=256`:
+    r = H256(x.float()) · (1/16); s = max(amax|r| / 127, 1e-12); q = clamp(rne(r / s), ±127).
+
+    Build laws: `rotation=0` is the rotation-off lane (r = x.float()); `rotation=128` keeps the
+    unnormalized H128 sums r, quantizes them with s as above, then returns the row scale
+    s · fp32(1/√128), so codes never depend on the irrational constant.
+    Returns int8 `[M, K]` and float32 `[M, 1]`."""
+    flat = x.reshape(-1, x.shape[-1]).float()
+    if rotation == 0:
+        rotated = flat.clone()
+    elif rotation == 128:
+        rotated = hadamard(flat, 128)
+    else:
+        rotated = hadamard(flat, rotation).mul_(1.0 / math.isqrt(rotation))
+    row_scale = (rotated.abs().amax(-1, keepdim=True) / 127.0).clamp_(min=SCALE_FLOOR)
+    quantized = torch.round(rotated / row_scale).clamp_(-127, 127).to(torch.int8)
+    if rotation == 128:
+        row_scale = row_scale * torch.tensor(1.0 / math.sqrt(128.0), dtype=torch.float32)
+    return quantized, row_scale
+
+
+def int8_weight_rowwise(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-row int8 weight: `s = max(amax/127, 1e-12)`, `q = clamp(rne(w/s), ±127)`
+    (`internal/probe.py:764-767`). Returns int8 `[N, K]`, float32 `[N]`."""
+    w = w.float()
+    scale = (w.abs().amax(dim=-1) / 127.0).clamp(min=SCALE_FLOOR)
+    payload = torch.round(w / scale.unsqueeze(-1)).clamp(-127, 127)
+    return payload.to(torch.int8), scale
+
+
+def int8_weight_rotated(w: torch.Tensor, rotation: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The weight side of a rotated int8 lane: each row rotated by the same orthonormal block
+    Hadamard as the activations, then per-row int8 (`quantize_rows_int8`'s law on W's rows), so
+    (H x)·(H w)ᵀ / n = x·wᵀ. The reference produces these bytes in tensorfs
+    (`derive/microscale.py:117-138`, parity unpinned there); this is the build's producer."""
+    q, s = quantize_rows_int8(w, rotation)
+    return q, s.reshape(-1)
+
+
+def int32_gemm(q: torch.Tensor, data: torch.Tensor, literal: bool = False) -> torch.Tensor:
+    """`q.int32 @ data.int32ᵀ` (`internal/int8_linear.py:446`), exact. Evaluated as a float64
+    matmul, which is exact while K·127² < 2**53, and checked against numpy int64 in the tests;
+    `literal=True` runs the reference's own int32 matmul (the timed CPU baseline)."""
+    if literal:
+        return q.to(torch.int32) @ data.to(torch.int32).t()
+    k = int(q.shape[-1])
+    assert k * 127 * 127 < 2**53
+    return (q.double() @ data.double().t()).to(torch.int32)
+
+
+def int8_product(
+    q: torch.Tensor, row_scale: torch.Tensor, data: torch.Tensor, scale: torch.Tensor,
+    out_dtype: torch.dtype, literal: bool = False,
+) -> torch.Tensor:
+    """`_product`'s CPU branch (`internal/int8_linear.py:431-448`): int32 accumulate, then
+    `(acc.float() · row_scale) · w_scale` in float32 (two roundings), then one cast."""
+    acc = int32_gemm(q, data, literal)
+    out = acc.float().mul_(row_scale.reshape(-1, 1)).mul_(scale.float().reshape(1, -1))
+    return out.to(out_dtype)
+
+
+def gelu_tanh(y: torch.Tensor) -> torch.Tensor:
+    """tanh-GELU in float32 with the reference's constants (`internal/prebuilt.py:775`):
+    0.5·y·(1 + tanh(0.79788456·(y + 0.044715·y³)))."""
+    y = y.float()
+    return 0.5 * y * (1.0 + torch.tanh(0.79788456 * (y + 0.044715 * y * y * y)))
+
+
+def int8_linear(
+    x: torch.Tensor, data: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
+    out_dtype: torch.dtype, rotation: int = 256, gelu: bool = False, literal: bool = False,
+) -> torch.Tensor:
+    """The eager int8 linear (`internal/int8_linear.py:275-276,415-419`): quantize, product,
+    then `+ bias` in the output dtype. `gelu=True` (build law for the DiT FFN-up epilogue)
+    applies `gelu_tanh` to that result in float32 and casts once more. `literal=True` runs the
+    reference's int32 matmul (the CPU path timed as the baseline)."""
+    q, row_scale = quantize_rows_int8(x, rotation)
+    out = int8_product(q, row_scale, data, scale, out_dtype, literal)
+    if bias is not None:
+        out = out + bias.to(out.dtype)
+    if gelu:
+        out = gelu_tanh(out).to(out_dtype)
+    return out.reshape(*x.shape[:-1], -1)
+
+
+def int8_exact(
+    x: torch.Tensor, data: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
+    rotation: int = 256, gelu: bool = False,
+) -> torch.Tensor:
+    """The same product in float64 after quantization (`internal/prebuilt.py:751-763`'s role):
+    what a kernel computes before its output rounding."""
+    q, row_scale = quantize_rows_int8(x, rotation)
+    out = int32_gemm(q, data).double() * row_scale.double() * scale.double().reshape(1, -1)
+    if bias is not None:
+        out = out + bias.double()
+    if gelu:
+        out = gelu_tanh(out.float()).double()
+    return out
+
+
+# ------------------------------------------------------------------------- fp8 rowwise
+
+
+def fp8_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """`fp8_linear.eager_quantize` (`internal/fp8_linear.py:56-63`): per row
+    s = max(float(amax|x|) / 448, 1e-12); q = e4m3(clamp(x.float() / s, ±448)), round to
+    nearest even, e4m3 subnormals kept. Returns e4m3 `[M, K]` and float32 `[M, 1]`."""
+    flat = x.reshape(-1, x.shape[-1])
+    scale = (flat.abs().amax(dim=-1, keepdim=True).float() / E4M3_MAX).clamp(min=SCALE_FLOOR)
+    q = (flat.float() / scale).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    return q, scale
+
+
+def fp8_weight(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-row E4M3 weight (`internal/probe.py:706-709`)."""
+    w = w.float()
+    scale = (w.abs().amax(dim=-1) / E4M3_MAX).clamp(min=SCALE_FLOOR)
+    payload = (w / scale.unsqueeze(-1)).clamp(-E4M3_MAX, E4M3_MAX)
+    return payload.to(torch.float8_e4m3fn), scale
+
+
+def fp8_exact(
+    x: torch.Tensor, data: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None
+) -> torch.Tensor:
+    """`(q·Wᵀ)·s_x·s_w + bias` (`internal/fp8_linear.py:97-111`, `_scaled_mm` semantics) in
+    float64 from the law's codes: e4m3 products and their sums are exact in float64 here."""
+    q, sx = fp8_quantize(x)
+    out = (q.double() @ data.double().t()) * sx.double() * scale.double().reshape(1, -1)
+    return out if bias is None else out + bias.double()
+
+
+def fp8_linear(
+    x: torch.Tensor, data: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
+    out_dtype: torch.dtype,
+) -> torch.Tensor:
+    """The CPU path timed as the fp8 baseline: `eager_quantize`, then dequantize and a float32
+    matmul, both scales, one cast, then `+ bias` in the output dtype. The reference's own CPU
+    call (`torch._scaled_mm` with row-wise scales) does not run on CPU torch 2.10, so this
+    dequantize form stands in for it."""
+    q, sx = fp8_quantize(x)
+    out = (q.float() @ data.float().t()).mul_(sx).mul_(scale.float().reshape(1, -1))
+    out = out.to(out_dtype)
+    return out if bias is None else out + bias.to(out_dtype)
+
+
+# ----------------------------------------------------------------------------- MXFP8
+
+
+def e8m0_multipliers(byte: torch.Tensor) -> torch.Tensor:
+    """E8M0 bytes → float32 by bit construction (`internal/encoding/formats.py:577-585`):
+    b ↦ bits b<<23; 0 ↦ 2**-127 (bits 1<<22); 255 ↦ NaN."""
+    raw = byte.view(torch.uint8)
+    bits = raw.to(torch.int32) << 23
+    bits = torch.where(raw == 0, torch.full_like(bits, 1 << 22), bits)
+    mult = bits.view(torch.float32)
+    return torch.where(raw == 255, torch.full_like(mult, float("nan")), mult)
+
+
+def mx_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """`leaves.quantize_activation_mx` (`internal/encoding/leaves.py:1411-1424`): per 32-block,
+    e = ceil(log2(amax/448)) (−127 for an all-zero block); byte = clamp(e+127, 0, 254);
+    payload = e4m3(clamp(x / 2**(byte−127), ±448)). K % 32 == 0. Returns e4m3 `[M, K]` and
+    uint8 `[M, K/32]`."""
+    flat = x.reshape(-1, x.shape[-1])
+    rows, cols = int(flat.shape[0]), int(flat.shape[1])
+    work = flat.float().view(rows, cols // MX_BLOCK, MX_BLOCK)
+    amax = work.abs().amax(dim=-1)
+    exponent = torch.where(
+        amax > 0, torch.ceil(torch.log2(amax / E4M3_MAX)), torch.full_like(amax, -127.0)
+    )
+    byte = (exponent + 127).clamp(0.0, 254.0).to(torch.uint8)
+    payload = (work / e8m0_multipliers(byte).unsqueeze(-1)).view(rows, cols)
+    return payload.clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn), byte
+
+
+def mx_dequantize(payload: torch.Tensor, byte: torch.Tensor) -> torch.Tensor:
+    """`MicroScaledDequant.decode`'s value (`internal/encoding/formats.py:638-650`) in float32,
+    for a row-major grid `[rows, ceil(K/32)]`: exact."""
+    rows, cols = int(payload.shape[0]), int(payload.shape[1])
+    mult = e8m0_multipliers(byte.contiguous())
+    return payload.float() * mult.repeat_interleave(MX_BLOCK, dim=1)[:, :cols]
+
+
+def mx_exact(
+    x: torch.Tensor, data: torch.Tensor, wbyte: torch.Tensor, bias: torch.Tensor | None
+) -> torch.Tensor:
+    """`_scaled_mm` with 1×32 E8M0 block scales (`internal/encoding/leaves.py:1509-1519`) in
+    float64 from the law's codes: Σ_k (p_x·2^e_x)(p_w·2^e_w) + bias."""
+    p, b = mx_quantize(x)
+    out = mx_dequantize(p, b).double() @ mx_dequantize(data, wbyte).double().t()
+    return out if bias is None else out + bias.double()
+
+
+def mx_linear(
+    x: torch.Tensor, data: torch.Tensor, wbyte: torch.Tensor, bias: torch.Tensor | None,
+    out_dtype: torch.dtype,
+) -> torch.Tensor:
+    """The CPU path timed as the MXFP8 baseline: `quantize_activation_mx`, exact E8M0 dequant
+    of both operands, a float32 matmul, one cast, then `+ bias` in the output dtype."""
+    p, b = mx_quantize(x)
+    out = (mx_dequantize(p, b) @ mx_dequantize(data, wbyte).t()).to(out_dtype)
+    return out if bias is None else out + bias.to(out_dtype)
+
+
+def _blocked_shape(rows: int, cols: int) -> tuple[int, int]:
+    return -(-rows // 128) * 128, -(-cols // 4) * 4
+
+
+def to_blocked(scales: torch.Tensor) -> torch.Tensor:
+    """Row-major `[rows, cols]` scale bytes → cuBLAS's 128×4 tiled layout
+    (`internal/encoding/formats.py:158-170`)."""
+    rows, cols = int(scales.shape[0]), int(scales.shape[1])
+    prow, pcol = _blocked_shape(rows, cols)
+    padded = torch.zeros(prow, pcol, dtype=scales.dtype)
+    padded[:rows, :cols] = scales
+    tiles = padded.view(prow // 128, 128, pcol // 4, 4).permute(0, 2, 1, 3)
+    return tiles.reshape(-1, 4, 32, 4).transpose(1, 2).reshape(-1).contiguous()
+
+
+def from_blocked(blocked: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    """`to_blocked`'s inverse (`internal/encoding/formats.py:173-178`)."""
+    prow, pcol = _blocked_shape(rows, cols)
+    tiles = blocked.reshape(-1, 32, 4, 4).transpose(1, 2).reshape(prow // 128, pcol // 4, 128, 4)
+    return tiles.permute(0, 2, 1, 3).reshape(prow, pcol)[:rows, :cols]
+
+
+# ------------------------------------------------------------- W4A4 int4-g64 SVDQuant
+
+
+def int4_quantize(v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Build law (no reference counterpart; the reference's W4A4 is nvfp4,
+    `internal/svdq_linear.py:605-618`): per row and per 64-group of float32 values v,
+    s = fp16(amax|v| / 7); q = 0 where s == 0, else clamp(rne(v / float(s)), −8, 7).
+    Returns int8 codes `[M, K]` (values −8..7) and float16 scales `[M, K/64]`."""
+    rows, cols = int(v.shape[0]), int(v.shape[1])
+    work = v.float().reshape(rows, cols // INT4_GROUP, INT4_GROUP)
+    s16 = (work.abs().amax(dim=-1) / INT4_MAX).to(torch.float16)
+    s32 = s16.float().unsqueeze(-1)
+    q = torch.round(work / s32).clamp(-8, 7)
+    q = torch.where(s32 == 0, torch.zeros_like(q), q)
+    return q.to(torch.int8).reshape(rows, cols), s16
+
+
+def pack_int4(q: torch.Tensor) -> torch.Tensor:
+    """Codes −8..7 `[R, C]` → bytes `[R, C/2]`, element 2k in the low nibble (the reference's
+    nibble order, `internal/svdq_linear.py:482-484`)."""
+    u = (q.to(torch.int16) & 0xF).to(torch.uint8)
+    return (u[:, 0::2] | (u[:, 1::2] << 4)).contiguous()
+
+
+def unpack_int4(packed: torch.Tensor) -> torch.Tensor:
+    """`pack_int4`'s inverse: signed codes as int8."""
+    lo = (packed & 0xF).to(torch.int16)
+    hi = (packed >> 4).to(torch.int16)
+    both = torch.stack((lo, hi), dim=-1).reshape(packed.shape[0], -1)
+    return torch.where(both >= 8, both - 16, both).to(torch.int8)
+
+
+def svdq_smooth(x: torch.Tensor, p: torch.Tensor) -> torch.Tensor:
+    """`bf16(x · p)` as float32 (`internal/svdq_linear.py:592-595`)."""
+    flat = x.reshape(-1, int(p.numel()))
+    return (flat.float() * p.float()).to(torch.bfloat16).float()
+
+
+def svdq_down(x: torch.Tensor, l1: torch.Tensor) -> torch.Tensor:
+    """The low-rank branch's input `bf16(x · L1)` with L1 `[K, R]` (`internal/svdq_linear.py:
+    598-602`, whose `down` is L1ᵀ), accumulated in float32 (here float64, then one rounding)."""
+    flat = x.reshape(-1, int(l1.shape[0]))
+    return (flat.double() @ l1.double()).to(torch.bfloat16)
+
+
+def svdq_weight(
+    w: torch.Tensor, p: torch.Tensor, l1: torch.Tensor, l2: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Build weight producer: the residual W − (L1·L2)ᵀ moved into the smoothed basis (÷ p per
+    input channel, so (x·p)·Rᵀ = x·(W − (L1L2)ᵀ)ᵀ), then `int4_quantize` per 64-group.
+    Returns packed codes `[N, K/2]` and float16 scales `[N, K/64]`."""
+    residual = w.double() - (l1.double() @ l2.double()).t()
+    smoothed = (residual / p.double().reshape(1, -1)).float()
+    q, s = int4_quantize(smoothed)
+    return pack_int4(q), s
+
+
+def svdq_exact(
+    x: torch.Tensor, p: torch.Tensor, wcodes: torch.Tensor, wscale: torch.Tensor,
+    l1: torch.Tensor, l2: torch.Tensor, bias: torch.Tensor | None,
+) -> torch.Tensor:
+    """The W4A4 product in float64 (`internal/svdq_linear.py:639-659`'s structure with the
+    int4-g64 law): Σ_g (Σ_{k∈g} qx·qw)·sx[m,g]·sw[n,g] + bf16(x·L1)·L2 + bias."""
+    qx, sx = int4_quantize(svdq_smooth(x, p))
+    qw = unpack_int4(wcodes)
+    rows, cols = int(qx.shape[0]), int(qx.shape[1])
+    groups = cols // INT4_GROUP
+    ax = qx.double().reshape(rows, groups, INT4_GROUP) * sx.double().unsqueeze(-1)
+    aw = qw.double().reshape(-1, groups, INT4_GROUP) * wscale.double().unsqueeze(-1)
+    out = ax.reshape(rows, cols) @ aw.reshape(-1, cols).t()
+    out = out + svdq_down(x, l1).double() @ l2.double()
+    return out if bias is None else out + bias.double()
+
+
+def svdq_linear(
+    x: torch.Tensor, p: torch.Tensor, wcodes: torch.Tensor, wscale: torch.Tensor,
+    l1: torch.Tensor, l2: torch.Tensor, bias: torch.Tensor | None, out_dtype: torch.dtype,
+) -> torch.Tensor:
+    """The CPU path timed as the W4A4 baseline: the int4 law, dequantized float32 matmul, the
+    bf16 low-rank branch and the bias, one cast."""
+    qx, sx = int4_quantize(svdq_smooth(x, p))
+    rows, cols = int(qx.shape[0]), int(qx.shape[1])
+    groups = cols // INT4_GROUP
+    ax = (qx.float().reshape(rows, groups, INT4_GROUP) * sx.float().unsqueeze(-1)).reshape(rows, cols)
+    qw = unpack_int4(wcodes)
+    aw = (qw.float().reshape(-1, groups, INT4_GROUP) * wscale.float().unsqueeze(-1)).reshape(-1, cols)
+    out = ax @ aw.t() + svdq_down(x, l1).float() @ l2.float()
+    if bias is not None:
+        out = out + bias.float()
+    return out.to(out_dtype)
+
+
+# ------------------------------------------------------------------------ decode laws
+
+
+def decode_int8_convrot(payload: torch.Tensor, scale: torch.Tensor, size: int,
+                        dtype: torch.dtype) -> torch.Tensor:
+    """`Int8ConvRotDequant.decode` (`internal/encoding/formats.py:733-752`):
+    hadamard(int32 data)·scale·(1/√size) in float32, one cast."""
+    block = hadamard(payload.to(torch.int32), size).to(torch.float32)
+    block.mul_(scale.to(torch.float32).reshape(-1, 1)).mul_(1.0 / math.isqrt(size))
+    return block.to(dtype)
+
+
+def decode_rowwise(payload: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """`RowwiseDequant.decode` (`internal/encoding/formats.py:557-569`): data·scale[row] in
+    float32, one cast."""
+    rows = int(payload.shape[0])
+    return (payload.to(torch.float32) * scale.to(torch.float32).reshape(rows, 1)).to(dtype)
+
+
+def decode_mxfp8(payload: torch.Tensor, scale: torch.Tensor, layout: str,
+                 dtype: torch.dtype) -> torch.Tensor:
+    """`MicroScaledDequant.decode` (`internal/encoding/formats.py:638-650`) for one matrix."""
+    rows, cols = int(payload.shape[0]), int(payload.shape[1])
+    blocks = -(-cols // MX_BLOCK)
+    grid = from_blocked(scale.reshape(-1), rows, blocks) if layout == "cublas_128x4" \
+        else scale.reshape(rows, blocks)
+    return mx_dequantize(payload, grid).to(dtype)
+
+
+# ------------------------------------------------------------- independent bit laws
+
+
+def e4m3_bits_numpy(v: np.ndarray) -> np.ndarray:
+    """float32 → OCP E4M3FN byte by integer arithmetic only (round to nearest even, subnormals
+    at 2**-9 steps, |v| > 448 → NaN 0x7F like an unsaturated cast). An independent encoder the
+    tests hold torch's cast (`.to(torch.float8_e4m3fn)`) and the kernels' against."""
+    bits = np.ascontiguousarray(v, dtype=np.float32).view(np.uint32).astype(np.int64)
+    sign = (bits >> 31) << 7
+    mag = bits & 0x7FFFFFFF
+    exp = mag >> 23
+    man = mag & 0x7FFFFF
+    out = np.zeros_like(mag)
+    # normal e4m3: f32 exponent 121..135 (2**-6 .. 2**8); keep 3 mantissa bits
+    e8 = exp - 127 + 7
+    normal = e8 >= 1
+    shift = np.where(normal, 20, 20 + (1 - e8))  # subnormal: fewer kept bits
+    full = np.where(normal, man | 0x800000, man | 0x800000)
+    shift = np.minimum(shift, 40)
+    kept = full >> shift
+    rem = full & ((np.int64(1) << shift) - 1)
+    half = np.int64(1) << (shift - 1)
+    up = (rem > half) | ((rem == half) & ((kept & 1) == 1))
+    kept = kept + up
+    # normal: kept holds 1.mmm (4 bits, maybe 5 after carry); value = kept·2**(e8-7-3)
+    n_code = np.where(kept >= 16, ((e8 + 1) << 3) | ((kept >> 1) & 7), (e8 << 3) | (kept & 7))
+    s_code = kept  # subnormal: kept counts 2**-9 units (carry into 8 gives the first normal)
+    code = np.where(normal, n_code, s_code)
+    zero = (mag == 0) | (exp < 127 - 7 - 3 - 1)  # below half the smallest subnormal
+    code = np.where(zero, 0, code)
+    nan = (exp == 255) | (code > 0x7E)
+    code = np.where(nan, 0x7F, code)
+    out = (sign | code).astype(np.uint8)
+    return out

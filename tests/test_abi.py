@@ -1,0 +1,84 @@
+"""The C-ABI library on the CPU: it loads, exports every entry point `include/cozyq.h` declares
+(and ctypes binds each), and the kernels' scalar conversions — compiled for the host from the
+same source — agree with torch's casts and the oracle's exponent law. No GPU call is made."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from cozyq import _lib
+from oracle import laws
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "cozyq.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"\b(cozyq_[a-z0-9_]+)\s*\(", text)) - {"cozyq_allocate_fn"}
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+
+
+def test_constants():
+    lib = _lib.load()
+    assert lib.cozyq_not_supported() == 801  # hipErrorNotSupported
+    assert lib.cozyq_out_of_memory() == 2  # hipErrorOutOfMemory
+    assert lib.cozyq_gemv_rows() == 4
+    assert lib.cozyq_max_k() == 32768
+    assert lib.cozyq_arch() == b"gfx950"
+    assert _lib.error_name(801) == "hipErrorNotSupported"
+
+
+def _host(fn: str, values: np.ndarray) -> np.ndarray:
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.zeros(values.shape, dtype=np.uint8)
+    getattr(_lib.load(), fn)(values.ctypes.data_as(ctypes.c_void_p),
+                             out.ctypes.data_as(ctypes.c_void_p), values.size)  # fmt: skip
+    return out
+
+
+def _every(dtype: torch.dtype) -> np.ndarray:
+    raw = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(dtype).float()
+    return raw[torch.isfinite(raw)].numpy()
+
+
+def test_device_e4m3_encoder_matches_torch_cast():
+    """The kernels' `e4m3_rn` against `.to(float8_e4m3fn)` on every bf16 and fp16 value in
+    range, on float32 values at and beside every E4M3 rounding midpoint, and on random float32."""
+    gen = np.random.default_rng(0)
+    v = np.concatenate([_every(torch.bfloat16), _every(torch.float16),
+                        gen.standard_normal(200000).astype(np.float32) * 100])  # fmt: skip
+    codes = np.arange(0, 0x7F, dtype=np.uint8)
+    vals = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy().astype(np.float64)
+    mids = ((vals[:-1] + vals[1:]) / 2).astype(np.float32)
+    bits = mids.view(np.uint32)
+    v = np.concatenate([v, mids, (bits + 1).view(np.float32), (bits - 1).view(np.float32)])
+    v = np.concatenate([v, -v])
+    v = v[np.abs(v) <= 448]
+    got = _host("cozyq_host_e4m3", v)
+    want = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, want)
+
+
+def test_device_mx_byte_matches_the_law():
+    """The kernels' `mx_byte` against the law's torch log2/ceil for every positive bf16/fp16
+    block maximum, zero and the extremes."""
+    for dtype in (torch.bfloat16, torch.float16):
+        v = _every(dtype)
+        v = np.concatenate([v[v > 0], [0.0]]).astype(np.float32)
+        block = torch.zeros(v.size, 32)
+        block[:, 0] = torch.from_numpy(v)
+        _, want = laws.mx_quantize(block.to(dtype))
+        assert np.array_equal(_host("cozyq_host_mx_byte", v), want.reshape(-1).numpy())

@@ -1,0 +1,330 @@
+"""GPU parity of the HIP kernels against the CPU oracle (`oracle/laws.py`), through the C ABI.
+
+Bar: codes, scales and int32 accumulators bit-exact; int8 outputs bit-exact to the CPU law
+(`internal/int8_linear.py:431-448` + `:276`); fp8, MXFP8 and GELU outputs within
+|got − exact| ≤ ATOL·rms(exact) + RTOL·|exact| of the float64 product of the law's codes.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import laws
+
+pytestmark = pytest.mark.gpu
+
+#: Output tolerance for float-accumulated products: atol relative to the output RMS, and rtol.
+ATOL, RTOL = 1e-2, 2e-2
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from cozyq import prebuilt
+
+    return prebuilt.library(0)
+
+
+def activations(m: int, k: int, seed: int, dtype=torch.bfloat16) -> torch.Tensor:
+    """~N(0,1) with 1% of the channels scaled x20 (the BASELINE outlier distribution)."""
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=gen)
+    chans = torch.randperm(k, generator=gen)[: max(1, k // 100)]
+    x[:, chans] *= 20
+    return x.to(dtype)
+
+
+def weights(n: int, k: int, seed: int) -> torch.Tensor:
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randn(n, k, generator=gen) * 0.02
+
+
+def assert_close(got: torch.Tensor, exact: torch.Tensor) -> None:
+    got, exact = got.double().cpu(), exact.double().cpu()
+    rms = exact.pow(2).mean().sqrt().item()
+    bound = ATOL * rms + RTOL * exact.abs()
+    err = (got - exact).abs()
+    worst = (err - bound).max().item()
+    assert worst <= 0, f"max excess {worst:.3g} (rms {rms:.3g}, max err {err.max().item():.3g})"
+
+
+# ---------------------------------------------------------------------- MFMA layouts
+
+
+def _probe(kind: int, a: np.ndarray, b: np.ndarray, sa=None, sb=None) -> np.ndarray:
+    from cozyq import _lib
+
+    lib = _lib.load()
+    ta = torch.from_numpy(a.view(np.uint8).reshape(64, 32)).to(DEV)
+    tb = torch.from_numpy(b.view(np.uint8).reshape(64, 32)).to(DEV)
+    tsa = torch.from_numpy(np.zeros(64, np.uint8) if sa is None else sa).to(DEV)
+    tsb = torch.from_numpy(np.zeros(64, np.uint8) if sb is None else sb).to(DEV)
+    d = torch.zeros(64, 4, dtype=torch.int32, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    code = lib.cozyq_probe_mfma(0, kind, ta.data_ptr(), tb.data_ptr(), tsa.data_ptr(),
+                                tsb.data_ptr(), d.data_ptr(), stream)  # fmt: skip
+    assert code == 0
+    torch.cuda.synchronize()
+    return d.cpu().numpy()
+
+
+def _expand(lanes: np.ndarray, per_lane: int) -> np.ndarray:
+    """Per-lane slices -> the 16 x (4·per_lane) matrix they stand for: lane l supplies row l%16,
+    K slice l//16."""
+    mat = np.zeros((16, 4 * per_lane), dtype=lanes.dtype)
+    for lane in range(64):
+        mat[lane % 16, (lane // 16) * per_lane:(lane // 16 + 1) * per_lane] = lanes[lane]
+    return mat
+
+
+def _check_layout(d: np.ndarray, want: np.ndarray, exact: bool) -> None:
+    for lane in range(64):
+        for r in range(4):
+            got, ref = d[lane, r], want[4 * (lane // 16) + r, lane % 16]
+            if exact:
+                assert got == ref, (lane, r)
+            else:
+                assert abs(got - ref) <= 1e-5 * (1 + abs(ref)), (lane, r, got, ref)
+
+
+def test_mfma_i8_layout():
+    rng = np.random.default_rng(0)
+    a = rng.integers(-128, 128, (64, 32), dtype=np.int8)
+    b = rng.integers(-128, 128, (64, 32), dtype=np.int8)
+    d = _probe(0, a, b).astype(np.int64)
+    want = _expand(a[:, :16], 16).astype(np.int64) @ _expand(b[:, :16], 16).astype(np.int64).T
+    _check_layout(d, want, exact=True)
+
+
+def _e4m3_lanes(rng) -> np.ndarray:
+    codes = rng.integers(0, 256, (64, 32), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x38  # no NaN codes
+    return codes
+
+
+def _e4m3_values(codes: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).double().numpy()
+
+
+def test_mfma_f8_layout():
+    rng = np.random.default_rng(1)
+    a, b = _e4m3_lanes(rng), _e4m3_lanes(rng)
+    d = _probe(1, a, b).view(np.float32).astype(np.float64)
+    want = _expand(_e4m3_values(a), 32) @ _expand(_e4m3_values(b), 32).T
+    _check_layout(d, want, exact=False)
+
+
+def test_mfma_f8_scaled_layout():
+    """Each lane's E8M0 byte scales the 32 K elements that lane supplies."""
+    rng = np.random.default_rng(2)
+    a, b = _e4m3_lanes(rng), _e4m3_lanes(rng)
+    sa = rng.integers(118, 136, 64, dtype=np.uint8)
+    sb = rng.integers(118, 136, 64, dtype=np.uint8)
+    d = _probe(2, a, b, sa, sb).view(np.float32).astype(np.float64)
+    av = _e4m3_values(a) * np.exp2(sa.astype(np.float64) - 127)[:, None]
+    bv = _e4m3_values(b) * np.exp2(sb.astype(np.float64) - 127)[:, None]
+    want = _expand(av, 32) @ _expand(bv, 32).T
+    _check_layout(d, want, exact=False)
+
+
+def test_mfma_bf16_layout():
+    rng = np.random.default_rng(3)
+    a = torch.randn(64, 16, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    b = torch.randn(64, 16, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    d = _probe(3, a.view(torch.uint8).numpy(), b.view(torch.uint8).numpy()).view(np.float32)
+    want = _expand(a[:, :8].double().numpy(), 8) @ _expand(b[:, :8].double().numpy(), 8).T
+    _check_layout(d.astype(np.float64), want, exact=False)
+    del rng
+
+
+# ------------------------------------------------------------------------ int8 lane
+
+QUANT_SHAPES = [(1, 256), (3, 1024), (300, 3072), (64, 4352), (5, 32768), (257, 12288)]
+
+
+@pytest.mark.parametrize("rotation", [256, 128, 0])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", QUANT_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_int8_quantize_bit_exact(ops, rotation, dtype, shape):
+    m, k = shape
+    x = activations(m, k, seed=m * 7 + k, dtype=dtype)
+    x[m // 2] = 0  # an all-zero row takes the scale floor
+    if m > 2:
+        x[1] *= 1e-6  # a tiny row
+    if rotation == 256:
+        q, s = ops.int8_quantize(x.to(DEV))
+    else:
+        q, s = ops.int8_quantize_rot(x.to(DEV), rotation)
+    wq, ws = laws.quantize_rows_int8(x, rotation)
+    assert torch.equal(q.cpu(), wq)
+    assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
+
+
+GEMM_SHAPES = [(1, 8, 256), (300, 512, 1024), (257, 264, 384), (64, 1032, 3072), (513, 256, 4096)]
+
+
+@pytest.mark.parametrize("shape", GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_int8_accumulators_bit_exact(ops, shape):
+    m, n, k = shape
+    gen = torch.Generator().manual_seed(m + n + k)
+    q = torch.randint(-127, 128, (m, k), generator=gen, dtype=torch.int8)
+    w = torch.randint(-127, 128, (n, k), generator=gen, dtype=torch.int8)
+    acc = ops.int8_acc(q.to(DEV), w.to(DEV))
+    assert torch.equal(acc.cpu(), laws.int32_gemm(q, w))
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(3, 512, 1024), (300, 512, 1024), (257, 264, 768)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_int8_linear_bit_exact(ops, shape, dtype, bias):
+    """The whole int8.convrot linear (quantize + GEMM + epilogue) equals the CPU law bit for bit,
+    with the probe's recipe (`internal/prebuilt.py:616-623`): random int8 data, scales ~1e-3."""
+    m, n, k = shape
+    gen = torch.Generator().manual_seed(20261017 + m)
+    data = torch.randint(-127, 128, (n, k), generator=gen, dtype=torch.int8)
+    scale = (torch.randn(n, generator=gen).abs() + 0.5) * 1e-3
+    b = torch.randn(n, generator=gen).to(dtype) if bias else None
+    x = torch.randn(m, k, generator=gen).to(dtype)
+    got = ops.int8_linear(x.to(DEV), data.to(DEV), scale.to(DEV),
+                          None if b is None else b.to(DEV), dtype)  # fmt: skip
+    want = laws.int8_linear(x, data, scale, b, dtype)
+    assert torch.equal(got.cpu(), want)
+
+
+@pytest.mark.parametrize("rotation", [0, 128, 256])
+def test_int8_gemm_rotation_lanes_and_gelu(ops, rotation):
+    m, n, k = 200, 264, 1024
+    x = activations(m, k, seed=11)
+    w = weights(n, k, seed=12)
+    data, scale = laws.int8_weight_rotated(w, rotation) if rotation else laws.int8_weight_rowwise(w)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(13)) * 0.1).to(torch.bfloat16)
+    q, s = ops.int8_quantize_rot(x.to(DEV), rotation)
+    plain = ops.int8_gemm_ex(q, s, data.to(DEV), scale.to(DEV), bias.to(DEV), torch.bfloat16, 0)
+    assert torch.equal(plain.cpu(), laws.int8_linear(x, data, scale, bias, torch.bfloat16, rotation))
+    gelu = ops.int8_gemm_ex(q, s, data.to(DEV), scale.to(DEV), bias.to(DEV), torch.bfloat16, 1)
+    assert_close(gelu, laws.int8_exact(x, data, scale, bias, rotation, gelu=True))
+    # and the rotated product approximates the unquantized linear
+    ref = x.double() @ w.double().t() + bias.double()
+    rel = (plain.cpu().double() - ref).norm() / ref.norm()
+    assert rel < 0.05
+
+
+def test_int8_output_into_wider_rows(ops):
+    """`out` with rows `ldo` apart (a sibling's column range of a packed output) is written in
+    place (`internal/prebuilt.py:449-460`)."""
+    m, n, k = 100, 256, 512
+    x = activations(m, k, seed=21)
+    data, scale = laws.int8_weight_rotated(weights(n, k, 22), 256)
+    packed = torch.zeros(m, 3 * n, dtype=torch.bfloat16, device=DEV)
+    view = packed[:, n:2 * n]
+    q, s = ops.int8_quantize(x.to(DEV))
+    got = ops.int8_gemm(q, s, data.to(DEV), scale.to(DEV), None, torch.bfloat16, out=view)
+    assert got.data_ptr() == view.data_ptr()
+    want = laws.int8_linear(x, data, scale, None, torch.bfloat16)
+    assert torch.equal(packed[:, n:2 * n].cpu(), want)
+    assert (packed[:, :n] == 0).all() and (packed[:, 2 * n:] == 0).all()
+
+
+# ------------------------------------------------------------------------- fp8 lane
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(1, 16), (3, 1024), (300, 4096), (17, 4112), (4, 32768)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_fp8_quantize_bit_exact(ops, shape, dtype):
+    m, k = shape
+    x = activations(m, k, seed=m + k, dtype=dtype)
+    x[0, :3] = torch.tensor([1e-7, -3e-5, 0.0]).to(dtype)  # subnormal e4m3 codes
+    if m > 2:
+        x[m - 1] = 0
+    q, s = ops.fp8_quantize(x.to(DEV))
+    wq, ws = laws.fp8_quantize(x)
+    assert torch.equal(q.cpu().view(torch.uint8), wq.view(torch.uint8))
+    assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("shape", [(300, 512, 1024), (257, 264, 4096), (64, 1024, 2064)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_fp8_gemm_within_tolerance(ops, shape, bias):
+    m, n, k = shape
+    x = activations(m, k, seed=31 + m)
+    data, scale = laws.fp8_weight(weights(n, k, seed=32))
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(33)) * 0.1).to(torch.bfloat16) \
+        if bias else None
+    q, s = ops.fp8_quantize(x.to(DEV))
+    got = ops.fp8_gemm(q, s, data.to(DEV), scale.to(DEV), None if b is None else b.to(DEV),
+                       torch.bfloat16)  # fmt: skip
+    assert_close(got, laws.fp8_exact(x, data, scale, b))
+
+
+@pytest.mark.parametrize("m", [1, 2, 5, 16])
+@pytest.mark.parametrize("k", [4096, 1040])
+def test_fp8_small_linear_within_tolerance(ops, m, k):
+    n = 1032
+    x = activations(m, k, seed=41 + m)
+    data, scale = laws.fp8_weight(weights(n, k, seed=42))
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(43)) * 0.1).to(torch.bfloat16)
+    got = ops.fp8_linear(x.to(DEV), data.to(DEV), scale.to(DEV), b.to(DEV), torch.bfloat16)
+    assert got.shape == (m, n)
+    assert_close(got, laws.fp8_exact(x, data, scale, b))
+
+
+# ------------------------------------------------------------------------ MXFP8 lane
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(1, 32), (3, 1024), (300, 3072), (64, 12288)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_mx_quantize_bit_exact(ops, shape, dtype):
+    m, k = shape
+    x = activations(m, k, seed=51 + k, dtype=dtype)
+    x = x * torch.logspace(-8, 8, m).reshape(-1, 1).to(dtype)
+    x[0, :32] = 0  # a zero block
+    q, s = ops.mx_quantize(x.to(DEV))
+    wq, ws = laws.mx_quantize(x)
+    assert torch.equal(q.cpu().view(torch.uint8), wq.view(torch.uint8))
+    assert torch.equal(s.cpu(), ws)
+
+
+@pytest.mark.parametrize("shape", [(300, 512, 1024), (257, 264, 3072), (1, 8, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_mx_gemm_within_tolerance(ops, shape):
+    m, n, k = shape
+    x = activations(m, k, seed=61 + m)
+    data, wbyte = laws.mx_quantize(weights(n, k, seed=62))
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(63)) * 0.1).to(torch.bfloat16)
+    q, qs = ops.mx_quantize(x.to(DEV))
+    got = ops.mx_gemm(q, qs, data.to(DEV), wbyte.to(DEV), b.to(DEV), torch.bfloat16)
+    assert_close(got, laws.mx_exact(x, data, wbyte, b))
+
+
+# ------------------------------------------------------------------ full-size property
+
+
+def test_c2_full_size_codes_and_sampled_rows(ops):
+    """BASELINE config 2 at its real shape: every code and scale bit-exact, the int32
+    accumulators of 48 sampled rows exact, and the bias + GELU outputs of those rows within
+    tolerance."""
+    m, k, n = 4096, 3072, 12288
+    x = activations(m, k, seed=20261202)
+    w = weights(n, k, seed=20261203)
+    data, scale = laws.int8_weight_rotated(w, 128)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(5)) * 0.1).to(torch.bfloat16)
+    q, s = ops.int8_quantize_rot(x.to(DEV), 128)
+    wq, ws = laws.quantize_rows_int8(x, 128)
+    assert torch.equal(q.cpu(), wq)
+    assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
+    out = ops.int8_gemm_ex(q, s, data.to(DEV), scale.to(DEV), bias.to(DEV), torch.bfloat16, 1)
+    acc = ops.int8_acc(q, data.to(DEV))
+    rows = torch.randperm(m, generator=torch.Generator().manual_seed(6))[:48]
+    assert torch.equal(acc.cpu()[rows], laws.int32_gemm(wq[rows], data))
+    exact = laws.int32_gemm(wq[rows], data).double() * ws[rows].double() * scale.double()
+    exact = laws.gelu_tanh((exact + bias.double()).float()).double()
+    assert_close(out.cpu()[rows], exact)
+    assert math.isfinite(out.float().abs().max().item())

@@ -1,0 +1,304 @@
+"""Pins the CPU oracle (`oracle/laws.py`) to things other than itself: the reference's own decode
+vectors (`tests/golden/ref_*_vectors.json`, copied from cozy-runtime's
+`internal/encoding/vectors/cases/`), closed forms, brute force over every bf16/fp16 input, and an
+independent bit-level E4M3 encoder."""
+
+from __future__ import annotations
+
+import base64
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import laws
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+DTYPES = {"F32": torch.float32, "BF16": torch.bfloat16, "F16": torch.float16, "I8": torch.int8,
+          "F8_E4M3": torch.float8_e4m3fn, "F8_E5M2": torch.float8_e5m2, "F8_E8M0": torch.uint8}
+
+
+def _tensor(bits: str, dtype: str, shape: list[int]) -> torch.Tensor:
+    raw = bytearray(base64.b64decode(bits))
+    return torch.frombuffer(raw, dtype=DTYPES[dtype]).reshape(shape) if raw else \
+        torch.empty(shape, dtype=DTYPES[dtype])
+
+
+def _cases(name: str, component: str) -> list[dict]:
+    data = json.loads((GOLDEN / f"ref_{name}_vectors.json").read_text())
+    return [c for c in data["cases"] if c["component"] == component]
+
+
+def _parts(case: dict) -> dict[str, torch.Tensor]:
+    return {p["role"]: _tensor(p["bits"], p["dtype"], p["shape"]) for p in case["parts"]}
+
+
+def _expect_bytes(case: dict) -> bytes:
+    return base64.b64decode(case["expect"])
+
+
+def _same(got: torch.Tensor, case: dict) -> bool:
+    """Bit-for-bit equality with the vector's expected output, except that a NaN matches any
+    NaN (NaN payload bits are not part of any law here)."""
+    want = torch.frombuffer(bytearray(_expect_bytes(case)), dtype=got.dtype).reshape(got.shape)
+    nan = torch.isnan(got.float())
+    if not torch.equal(nan, torch.isnan(want.float())):
+        return False
+    bits = torch.int32 if got.element_size() == 4 else torch.int16
+    return torch.equal(got[~nan].contiguous().view(bits), want[~nan].contiguous().view(bits))
+
+
+# ----------------------------------------------------------------- reference vectors
+
+
+@pytest.mark.parametrize("case", _cases("int8", "int8.convrot"), ids=lambda c: c["key"])
+def test_int8_convrot_decode_vectors(case):
+    """The reference's int8.convrot decode vectors pin the rotation's signs and index order."""
+    parts = _parts(case)
+    size = case["encoding"]["params"]["rotation_size"]
+    rows, cols = case["shape"]
+    got = laws.decode_int8_convrot(parts["weight"].reshape(rows, cols), parts["scale"], size,
+                                   DTYPES[case["dtype"]])  # fmt: skip
+    assert _same(got, case)
+
+
+@pytest.mark.parametrize("case", _cases("int8", "int8.rowwise"), ids=lambda c: c["key"])
+def test_int8_rowwise_decode_vectors(case):
+    parts = _parts(case)
+    got = laws.decode_rowwise(parts["weight"], parts["scale"], DTYPES[case["dtype"]])
+    assert _same(got, case)
+
+
+@pytest.mark.parametrize(
+    "case",
+    [c for c in _cases("fp8", "fp8.rowwise") if c["parts"][0]["dtype"] == "F8_E4M3"],
+    ids=lambda c: c["key"],
+)
+def test_fp8_rowwise_decode_vectors(case):
+    """Pins the E4M3 element values the fp8 lane's codes stand for (the E5M2 cases are another
+    element type, off this path)."""
+    parts = _parts(case)
+    shape = case["shape"]
+    rows = int(np.prod(shape[:-1]))
+    got = laws.decode_rowwise(parts["weight"].reshape(rows, shape[-1]), parts["scale"].reshape(-1),
+                              DTYPES[case["dtype"]])  # fmt: skip
+    assert _same(got, case)
+
+
+@pytest.mark.parametrize("case", _cases("mxfp8", "mxfp8"), ids=lambda c: c["key"])
+def test_mxfp8_decode_vectors(case):
+    """Pins the E8M0 multipliers, ragged last blocks and the cuBLAS 128x4 layout."""
+    parts = _parts(case)
+    shape = case["shape"]
+    layout = case["encoding"]["params"]["scale_layout"]
+    dtype = DTYPES[case["dtype"]]
+    weight, scale = parts["weight"], parts["scale"]
+    if len(shape) == 3:  # an expert stack decodes one matrix at a time
+        got = torch.stack([laws.decode_mxfp8(weight[e], scale[e], layout, dtype)
+                           for e in range(shape[0])])  # fmt: skip
+    else:
+        got = laws.decode_mxfp8(weight, scale, layout, dtype)
+    assert _same(got, case)
+
+
+def test_blocked_layout_round_trip():
+    grid = torch.randint(0, 255, (300, 7), dtype=torch.uint8)
+    blocked = laws.to_blocked(grid)
+    assert blocked.numel() == 384 * 8
+    assert torch.equal(laws.from_blocked(blocked, 300, 7), grid)
+
+
+# -------------------------------------------------------------------- closed forms
+
+
+def _kron_h(size: int) -> np.ndarray:
+    h4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=np.int64)
+    h2 = np.array([[1, 1], [1, -1]], dtype=np.int64)
+    factors = [h2, h4, h4, h4] if size == 128 else [h4] * int(round(math.log(size, 4)))
+    out = np.ones((1, 1), dtype=np.int64)
+    for f in factors:
+        out = np.kron(out, f)
+    return out
+
+
+@pytest.mark.parametrize("size", [4, 16, 64, 256, 1024, 128])
+def test_hadamard_is_the_kronecker_matrix(size):
+    """The staged rotation equals x·H for H the Kronecker product, outer factor first; H is
+    symmetric and H·H = n·I."""
+    h = _kron_h(size)
+    assert np.array_equal(h, h.T)
+    assert np.array_equal(h @ h, size * np.eye(size, dtype=np.int64))
+    x = torch.randint(-1000, 1000, (3, 2 * size), dtype=torch.int64)
+    got = laws.hadamard(x, size).numpy()
+    want = np.concatenate([x[:, :size].numpy() @ h, x[:, size:].numpy() @ h], axis=1)
+    assert np.array_equal(got, want)
+
+
+def test_hadamard_float_stage_order_is_associated_left_to_right():
+    """The float32 rotation differs from other evaluation orders on some inputs and equals the
+    stated one: ((a+b)+c)-d per output, outer stage first (formats.py:667-671). A plausible
+    mistake, (a+b)+(c-d), changes bits here."""
+    gen = torch.Generator().manual_seed(7)
+    x = (torch.randn(64, 256, generator=gen) * torch.logspace(-4, 4, 256)).float()
+    ref = laws.hadamard(x, 256)
+    work = x.reshape(-1, 4, 4, 4, 4)
+    for axis in range(1, 5):
+        a, b, c, d = work.unbind(axis)
+        work = torch.stack(((a + b) + (c - d), (a + b) - (c - d), (a - b) + (c + d),
+                            (b + c) + (d - a)), axis)  # fmt: skip
+    other = work.reshape(x.shape)
+    assert not torch.equal(ref, other)
+    exact = laws.hadamard(x.double(), 256)
+    assert torch.allclose(ref.double(), exact, rtol=0, atol=1e-3 * exact.abs().max().item())
+
+
+def test_int32_gemm_matches_numpy_int64():
+    gen = torch.Generator().manual_seed(1)
+    q = torch.randint(-127, 128, (37, 512), generator=gen, dtype=torch.int8)
+    w = torch.randint(-127, 128, (24, 512), generator=gen, dtype=torch.int8)
+    got = laws.int32_gemm(q, w)
+    want = q.numpy().astype(np.int64) @ w.numpy().astype(np.int64).T
+    assert np.array_equal(got.numpy().astype(np.int64), want)
+
+
+@pytest.mark.parametrize("rotation", [0, 128, 256])
+def test_int8_quantize_round_trip(rotation):
+    """Codes reach ±127 at each row's maximum, every element dequantizes within half a step of
+    the rotated (normalized) row, and all-zero rows give zero codes."""
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(9, 1024, generator=gen).to(torch.bfloat16)
+    x[3] = 0
+    q, s = laws.quantize_rows_int8(x, rotation)
+    assert q.dtype == torch.int8 and s.shape == (9, 1)
+    xf = x.float().double()
+    if rotation:
+        rotated = laws.hadamard(xf, rotation) / math.sqrt(rotation)
+    else:
+        rotated = xf
+    err = (q.double() * s.double() - rotated).abs()
+    assert (err <= s.double() * 0.5 * (1 + 1e-5) + 1e-30).all()
+    live = [r for r in range(9) if r != 3]
+    assert (q[live].abs().amax(-1) == 127).all()
+    assert (q[3] == 0).all()
+
+
+# --------------------------------------------------------------------- E4M3 / E8M0
+
+
+def _all_half_values(dtype: torch.dtype) -> torch.Tensor:
+    raw = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(dtype)
+    return raw[torch.isfinite(raw.float())].float()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_e4m3_cast_matches_bit_encoder_on_every_input(dtype):
+    """torch's cast (the law's) and the independent integer encoder agree on every bf16/fp16
+    value in [-448, 448]."""
+    v = _all_half_values(dtype)
+    v = v[v.abs() <= 448]
+    got = v.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    want = laws.e4m3_bits_numpy(v.numpy())
+    assert np.array_equal(got, want)
+
+
+def _e4m3_midpoints() -> np.ndarray:
+    codes = np.arange(0, 0x7F, dtype=np.uint8)
+    vals = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy().astype(np.float64)
+    mids = (vals[:-1] + vals[1:]) / 2
+    f32 = mids.astype(np.float32)
+    bits = f32.view(np.uint32)
+    near = np.concatenate([f32, (bits + 1).view(np.float32), (bits - 1).view(np.float32)])
+    near = np.concatenate([near, -near, vals.astype(np.float32), -vals.astype(np.float32)])
+    return near[np.abs(near) <= 448]
+
+
+def test_e4m3_cast_at_round_to_nearest_even_midpoints():
+    v = _e4m3_midpoints()
+    got = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, laws.e4m3_bits_numpy(v))
+
+
+def _exact_mx_byte(amax: np.ndarray) -> np.ndarray:
+    """clamp(ceil(log2(amax/448)) + 127, 0, 254) with the ceiling taken exactly."""
+    q = (amax.astype(np.float32) / np.float32(448.0)).astype(np.float64)
+    mant, exp = np.frexp(q)  # q = mant·2^exp, mant in [0.5, 1)
+    e = np.where(mant == 0.5, exp - 1, exp)
+    b = np.clip(e + 127, 0, 254)
+    return np.where(amax > 0, b, 0).astype(np.uint8)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mx_exponent_every_block_max(dtype):
+    """`mx_quantize`'s byte (torch log2 + ceil, the law) equals the exact integer ceiling for
+    every positive bf16/fp16 block maximum."""
+    v = _all_half_values(dtype)
+    v = v[v > 0]
+    block = torch.zeros(v.numel(), 32)
+    block[:, 5] = v
+    _, byte = laws.mx_quantize(block.to(dtype))
+    assert np.array_equal(byte.reshape(-1).numpy(), _exact_mx_byte(v.numpy()))
+
+
+def test_mx_round_trip_and_zero_blocks():
+    gen = torch.Generator().manual_seed(3)
+    x = (torch.randn(8, 256, generator=gen) * torch.logspace(-6, 6, 8).reshape(-1, 1)).to(torch.bfloat16)
+    x[2, 32:64] = 0
+    p, b = laws.mx_quantize(x)
+    assert b[2, 1] == 0 and (p[2, 32:64].float() == 0).all()
+    got = laws.mx_dequantize(p, b)
+    blocks = x.float().reshape(8, 8, 32)
+    mult = laws.e8m0_multipliers(b).unsqueeze(-1)
+    # scaled block maxima land in (224, 448]; half an e4m3 ulp there is at most 16
+    top = (blocks.abs().amax(-1, keepdim=True) / mult)
+    assert ((top > 224) | (top == 0)).all() and (top <= 448).all()
+    err = (got.reshape(8, 8, 32) - blocks).abs()
+    assert (err <= 16 * mult).all()
+    assert p.float().abs().max() <= 448
+
+
+def test_e8m0_multipliers_by_construction():
+    byte = torch.arange(0, 256, dtype=torch.int32).to(torch.uint8)
+    got = laws.e8m0_multipliers(byte)
+    assert got[0].item() == 2.0 ** -127
+    assert all(got[b].item() == 2.0 ** (b - 127) for b in range(1, 255))
+    assert math.isnan(got[255].item())
+
+
+# ------------------------------------------------------------------ int4-g64 (build law)
+
+
+def test_int4_quantize_round_trip_and_edges():
+    gen = torch.Generator().manual_seed(4)
+    v = torch.randn(6, 256, generator=gen) * torch.logspace(-3, 3, 6).reshape(-1, 1)
+    v[1, 64:128] = 0
+    q, s = laws.int4_quantize(v)
+    assert q.dtype == torch.int8 and s.dtype == torch.float16 and s.shape == (6, 4)
+    assert int(q.min()) >= -8 and int(q.max()) <= 7
+    assert (q[1, 64:128] == 0).all() and s[1, 1] == 0
+    deq = (q.float().reshape(6, 4, 64) * s.float().unsqueeze(-1)).reshape(6, 256)
+    assert ((deq - v).abs() <= s.float().repeat_interleave(64, 1) * 0.5 + 1e-30).all()
+
+
+def test_int4_quantize_brute_force_small():
+    """Every code is the nearest of −8..7 steps to v/s (ties to even), s = fp16(amax/7)."""
+    gen = torch.Generator().manual_seed(5)
+    v = torch.randn(4, 64, generator=gen)
+    q, s = laws.int4_quantize(v)
+    for r in range(4):
+        scale = float(s[r, 0])
+        assert scale == float(np.float16(np.float32(v[r].abs().max()) / np.float32(7.0)))
+        for k in range(64):
+            t = float(np.float32(v[r, k]) / np.float32(scale))
+            best = min(range(-8, 8), key=lambda c: (abs(c - t), c % 2))
+            assert int(q[r, k]) == best
+
+
+def test_int4_pack_round_trip():
+    q = torch.randint(-8, 8, (5, 128), dtype=torch.int8)
+    packed = laws.pack_int4(q)
+    assert packed.shape == (5, 64)
+    assert int(packed[0, 0]) & 0xF == int(q[0, 0]) & 0xF
+    assert torch.equal(laws.unpack_int4(packed), q)
