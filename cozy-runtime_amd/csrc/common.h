@@ -42,6 +42,10 @@ __host__ __device__ __forceinline__ uint16_t bf16_rn(float f) {
 template <bool kHalf>
 __device__ __forceinline__ uint16_t narrow(float f) {
     if constexpr (kHalf) {
+        // The float32 value is materialized first: otherwise the backend folds the producing
+        // multiply into v_fma_mix*_f16, rounding once where the CPU law rounds to float32 and
+        // then to fp16.
+        asm volatile("" : "+v"(f));
         return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));  // v_cvt_f16_f32: RNE
     } else {
         return bf16_rn(f);
@@ -103,6 +107,10 @@ __device__ __forceinline__ float e8m0_value(uint32_t b) {
 // D(16x16) += A(16xK)·B(Kx16). Lane l supplies row l%16 of A and column l%16 of B, its K
 // slice chosen by l/16; both operands loaded with the same pattern pair every k correctly.
 // The result's lane l holds rows 4·(l/16)+r (r = 0..3) of column l%16.
+// f8f6f4 (K = 128, 32 bytes a lane): lane group g = l/16 holds k in [16g, 16g+16) in bytes
+// 0..15 and k in [64+16g, 64+16g+16) in bytes 16..31, and the E8M0 scale of K block κ
+// (k in [32κ, 32κ+32)) of row (column) i is lane i + 16κ's (measured on gfx950 by the probe
+// tests). A lane group therefore loads 16-byte chunks g and g+4 of a 128-byte K step.
 
 __device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);

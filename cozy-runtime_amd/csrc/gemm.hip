@@ -24,20 +24,18 @@ constexpr int kOperand = kTile * kStep;  // bytes of one operand's stage
 
 enum Kind { kInt8 = 0, kFp8 = 1, kMx = 2 };
 
-// Physical 16-byte chunk of logical chunk `c` (0..7) in LDS row `r`.
+// Physical 16-byte chunk of logical chunk `c` (0..7) in LDS row `r`: the 16 rows a fragment
+// read touches at one chunk land on 16 distinct 4-bank groups.
 template <int kKind>
 __device__ __forceinline__ int swz(int r, int c) {
-    if constexpr (kKind == kInt8) {
-        return c ^ ((r >> 1) & 7);
-    } else {
-        return c ^ (((r >> 1) & 3) << 1);  // keeps each lane's 32-byte pair adjacent
-    }
+    return c ^ ((r >> 1) & 7);
 }
 
 __device__ __forceinline__ float gelu_tanh(float y) {
     return 0.5f * y * (1.0f + tanhf(0.79788456f * (y + 0.044715f * y * y * y)));
 }
 
+// kEpi: 0 plain, 1 tanh-GELU, 2 raw int32 accumulators to `acc_out` (test entry; no scales read).
 template <int kKind, bool kOutHalf, bool kBias, int kEpi>
 __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     const uint8_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ xs,
@@ -131,21 +129,23 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
         } else {
             i32x8 a[8], b[8];
             int sa[8], sb[8];
+            // Lane group fq takes chunks fq and fq+4 (the f8f6f4 K layout, `common.h`), so MX
+            // block fq of this step is the one its E8M0 byte scales.
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int r = wn * 128 + i * 16 + fr;
-                const uint8_t* p = la + r * kStep + swz<kKind>(r, 2 * fq) * 16;
-                const i32x4 lo = *reinterpret_cast<const i32x4*>(p);
-                const i32x4 hi = *reinterpret_cast<const i32x4*>(p + 16);
+                const uint8_t* row = la + r * kStep;
+                const i32x4 lo = *reinterpret_cast<const i32x4*>(row + swz<kKind>(r, fq) * 16);
+                const i32x4 hi = *reinterpret_cast<const i32x4*>(row + swz<kKind>(r, fq + 4) * 16);
                 a[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 if constexpr (kKind == kMx) sa[i] = sc[cur][1][r * 4 + fq];
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int r = wm * 128 + j * 16 + fr;
-                const uint8_t* p = lb + r * kStep + swz<kKind>(r, 2 * fq) * 16;
-                const i32x4 lo = *reinterpret_cast<const i32x4*>(p);
-                const i32x4 hi = *reinterpret_cast<const i32x4*>(p + 16);
+                const uint8_t* row = lb + r * kStep;
+                const i32x4 lo = *reinterpret_cast<const i32x4*>(row + swz<kKind>(r, fq) * 16);
+                const i32x4 hi = *reinterpret_cast<const i32x4*>(row + swz<kKind>(r, fq + 4) * 16);
                 b[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 if constexpr (kKind == kMx) sb[j] = sc[cur][0][r * 4 + fq];
             }
@@ -171,16 +171,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     for (int j = 0; j < 8; ++j) {
         const int m = m0 + wm * 128 + j * 16 + fr;
         if (m >= M) continue;
+        if constexpr (kEpi == 2) {
+            static_assert(kKind == kInt8, "raw accumulators are the int8 GEMM's");
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int n = n0 + wn * 128 + i * 16 + 4 * fq;
+                if (n < N) *reinterpret_cast<i32x4*>(acc_out + static_cast<int64_t>(m) * N + n) = acc[i][j];
+            }
+            continue;
+        }
         const float xsm = (kKind == kMx) ? 1.0f : xs[m];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int n = n0 + wn * 128 + i * 16 + 4 * fq;
             if (n >= N) continue;
-            if (acc_out != nullptr) {
-                if constexpr (kKind == kInt8)
-                    *reinterpret_cast<i32x4*>(acc_out + static_cast<int64_t>(m) * N + n) = acc[i][j];
-                continue;
-            }
             float wsv[4] = {1.0f, 1.0f, 1.0f, 1.0f};
             uint16_t bv[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -267,7 +271,7 @@ hipError_t gemm_mx(const uint8_t* q, const uint8_t* qe, const uint8_t* w, const 
 
 hipError_t gemm_int8_acc(const int8_t* q, const int8_t* w, int32_t* acc, int M, int N, int K,
                          hipStream_t s) {
-    return launch<kInt8, false, false, 0>(q, nullptr, w, nullptr, nullptr, nullptr, nullptr,
+    return launch<kInt8, false, false, 2>(q, nullptr, w, nullptr, nullptr, nullptr, nullptr,
                                           nullptr, acc, N, M, N, K, s);
 }
 

@@ -110,25 +110,52 @@ def _e4m3_values(codes: np.ndarray) -> np.ndarray:
     return torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).double().numpy()
 
 
+def _f8_matrix(lanes: np.ndarray, scales: np.ndarray | None = None) -> np.ndarray:
+    """The 16 x 128 operand the f8f6f4 MFMA reads from 64 lanes x 32 bytes: lane group g holds
+    k in [16g, 16g+16) in bytes 0..15 and k in [64+16g, 80+16g) in bytes 16..31; the E8M0 byte
+    of row i's K block κ (k in [32κ, 32κ+32)) is lane i + 16κ's."""
+    mat = np.zeros((16, 128))
+    for lane in range(64):
+        i, g = lane % 16, lane // 16
+        mat[i, 16 * g:16 * g + 16] = lanes[lane, :16]
+        mat[i, 64 + 16 * g:80 + 16 * g] = lanes[lane, 16:]
+    if scales is not None:
+        for i in range(16):
+            for kb in range(4):
+                mat[i, 32 * kb:32 * kb + 32] *= 2.0 ** (float(scales[i + 16 * kb]) - 127)
+    return mat
+
+
+#: The f8f6f4 matrix core's sum of 128 exact e4m3 products is not a sequential float32 sum:
+#: measured on gfx950 within 2^-14.6 of the sum of the products' magnitudes; held to 2^-13.
+F8_SUM_BOUND = 2.0 ** -13
+
+
+def _check_f8(d: np.ndarray, a: np.ndarray, b: np.ndarray) -> None:
+    want = a @ b.T
+    size = np.abs(a) @ np.abs(b).T
+    for lane in range(64):
+        for r in range(4):
+            i, j = 4 * (lane // 16) + r, lane % 16
+            err = abs(d[lane, r] - want[i, j])
+            assert err <= F8_SUM_BOUND * size[i, j] + 1e-30, (lane, r, err / size[i, j])
+
+
 def test_mfma_f8_layout():
     rng = np.random.default_rng(1)
     a, b = _e4m3_lanes(rng), _e4m3_lanes(rng)
     d = _probe(1, a, b).view(np.float32).astype(np.float64)
-    want = _expand(_e4m3_values(a), 32) @ _expand(_e4m3_values(b), 32).T
-    _check_layout(d, want, exact=False)
+    _check_f8(d, _f8_matrix(_e4m3_values(a)), _f8_matrix(_e4m3_values(b)))
 
 
 def test_mfma_f8_scaled_layout():
-    """Each lane's E8M0 byte scales the 32 K elements that lane supplies."""
+    """Each lane's E8M0 byte scales one 32-element K block of one row (column)."""
     rng = np.random.default_rng(2)
     a, b = _e4m3_lanes(rng), _e4m3_lanes(rng)
     sa = rng.integers(118, 136, 64, dtype=np.uint8)
     sb = rng.integers(118, 136, 64, dtype=np.uint8)
     d = _probe(2, a, b, sa, sb).view(np.float32).astype(np.float64)
-    av = _e4m3_values(a) * np.exp2(sa.astype(np.float64) - 127)[:, None]
-    bv = _e4m3_values(b) * np.exp2(sb.astype(np.float64) - 127)[:, None]
-    want = _expand(av, 32) @ _expand(bv, 32).T
-    _check_layout(d, want, exact=False)
+    _check_f8(d, _f8_matrix(_e4m3_values(a), sa), _f8_matrix(_e4m3_values(b), sb))
 
 
 def test_mfma_bf16_layout():
