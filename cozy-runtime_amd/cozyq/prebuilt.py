@@ -57,6 +57,13 @@ def _ptr(t: Tensor | None) -> int | None:
     return None if t is None else int(t.data_ptr())
 
 
+def _aligned(t: Tensor) -> Tensor:
+    """`t` contiguous at a 16-byte address: the epilogues read scales and biases 16 bytes at a
+    time."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 @dataclass(slots=True)
 class Prebuilt:
     """The ops on one card (`internal/prebuilt.py:80-434`)."""
@@ -80,6 +87,7 @@ class Prebuilt:
         flat = self._rows(INT8, x)
         rows, width = flat.shape
         bias = self._weight(INT8, data, scale, bias, width, out_dtype)
+        scale = _aligned(scale)
         shape = (*x.shape[:-1], data.shape[0])
         if rows <= self._lib.cozyq_gemv_rows():
             out = self.torch.empty(shape, dtype=out_dtype, device=x.device)
@@ -335,6 +343,7 @@ class Prebuilt:
         if width % f.multiple:
             raise ValueError(f"{f.name}_gemm: K must be a multiple of {f.multiple}, not {width}")
         bias = self._weight(f, data, scale, bias, width, out_dtype)
+        scale = _aligned(scale)
         n = data.shape[0]
         direct = out is not None and _writable(out, rows, n, out_dtype, q.device)
         result = out if direct and out is not None else torch.empty(
@@ -400,7 +409,7 @@ class Prebuilt:
             return None
         if bias.numel() != data.shape[0]:
             raise ValueError(f"{f.name}: bias must have {data.shape[0]} values")
-        return bias.to(out_dtype).contiguous()
+        return _aligned(bias.to(out_dtype))
 
     def _half(self, dtype: Dtype) -> bool:
         if dtype not in (self.torch.bfloat16, self.torch.float16):

@@ -1,6 +1,6 @@
-// The quantized GEMMs on gfx950 MFMA: int8 (v_mfma_i32_16x16x64_i8, exact int32 sums), e4m3
-// rowwise (v_mfma_f32_16x16x128_f8f6f4) and MXFP8 (v_mfma_scale_f32_16x16x128_f8f6f4 with the
-// E8M0 block scales fed to the matrix core), with the dequantizing epilogue fused.
+// The fp8 GEMMs on gfx950 MFMA: e4m3 rowwise (v_mfma_f32_16x16x128_f8f6f4) and MXFP8
+// (v_mfma_scale_f32_16x16x128_f8f6f4 with the E8M0 block scales fed to the matrix core), with
+// the dequantizing epilogue fused. (The int8 GEMM is gemm_i8.hip.)
 //
 // One workgroup of 4 waves computes a 256x256 output tile; each wave owns a 128x128 quadrant as
 // 8x8 MFMA blocks of 16x16 (256 accumulator registers a lane). K advances 128 bytes a step
@@ -249,13 +249,6 @@ hipError_t dispatch(const void* q, const float* xs, const void* w, const float* 
 
 }  // namespace
 
-hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
-                     const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
-                     int epilogue, hipStream_t s) {
-    return dispatch<kInt8>(q, xs, w, ws, nullptr, nullptr, bias, out, ldo, out_half, M, N, K,
-                           epilogue, s);
-}
-
 hipError_t gemm_fp8(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                     const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
                     int epilogue, hipStream_t s) {
@@ -267,12 +260,6 @@ hipError_t gemm_mx(const uint8_t* q, const uint8_t* qe, const uint8_t* w, const 
                    const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
                    hipStream_t s) {
     return dispatch<kMx>(q, nullptr, w, nullptr, qe, we, bias, out, ldo, out_half, M, N, K, 0, s);
-}
-
-hipError_t gemm_int8_acc(const int8_t* q, const int8_t* w, int32_t* acc, int M, int N, int K,
-                         hipStream_t s) {
-    return launch<kInt8, false, false, 2>(q, nullptr, w, nullptr, nullptr, nullptr, nullptr,
-                                          nullptr, acc, N, M, N, K, s);
 }
 
 }  // namespace cozyq

@@ -8,7 +8,7 @@ namespace cozyq {
 namespace {
 
 // a, b: 64 lanes x 32 bytes (i8 and bf16 kinds use the first 16); sa, sb: 64 bytes;
-// d: 64 lanes x 4 words (int32 or float32).
+// d: 64 lanes x 16 words (int32 or float32; the 16x16 kinds fill the first 4).
 __global__ void mfma_probe_kernel(int kind, const uint8_t* a, const uint8_t* b, const uint8_t* sa,
                                   const uint8_t* sb, uint32_t* d) {
     const int l = threadIdx.x;
@@ -16,8 +16,14 @@ __global__ void mfma_probe_kernel(int kind, const uint8_t* a, const uint8_t* b, 
     const i32x8 b8 = *reinterpret_cast<const i32x8*>(b + 32 * l);
     const i32x4 a4 = {a8[0], a8[1], a8[2], a8[3]};
     const i32x4 b4 = {b8[0], b8[1], b8[2], b8[3]};
-    uint32_t r[4];
-    if (kind == 0) {
+    uint32_t r[16] = {};
+    if (kind == 4) {
+        typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+        i32x16 z;
+        for (int i = 0; i < 16; ++i) z[i] = 0;
+        const i32x16 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, b4, z, 0, 0, 0);
+        for (int i = 0; i < 16; ++i) r[i] = static_cast<uint32_t>(c[i]);
+    } else if (kind == 0) {
         const i32x4 c = mfma_i8(a4, b4, i32x4{0, 0, 0, 0});
         for (int i = 0; i < 4; ++i) r[i] = static_cast<uint32_t>(c[i]);
     } else if (kind == 1) {
@@ -32,7 +38,7 @@ __global__ void mfma_probe_kernel(int kind, const uint8_t* a, const uint8_t* b, 
         const f32x4 c = mfma_bf16(ab, bb, f32x4{0, 0, 0, 0});
         for (int i = 0; i < 4; ++i) r[i] = bits_of(c[i]);
     }
-    for (int i = 0; i < 4; ++i) d[4 * l + i] = r[i];
+    for (int i = 0; i < 16; ++i) d[16 * l + i] = r[i];
 }
 
 }  // namespace

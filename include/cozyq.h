@@ -70,7 +70,8 @@ typedef void* (*cozyq_allocate_fn)(size_t bytes, void* context);
  * acc the exact int32 (fp8 = 0, int8 q and w) or float32 (fp8 = 1, e4m3 q and w) sum over K.
  * int8: rounded as internal/int8_linear.py:445-448 + :276 (two float32 products, one cast,
  * then the bias added in the output dtype), bit-for-bit. fp8: float32 accumulation, one cast.
- * out rows are `ldo` elements apart (ldo >= N, ldo % 8 == 0, out 16-byte aligned). family must
+ * out rows are `ldo` elements apart (ldo >= N, ldo % 8 == 0, out 16-byte aligned); w_scale and
+ * bias are 16-byte aligned. family must
  * be 0 (the one CDNA4 MFMA family); config -1 chooses by shape, 0 names the 256x256 tile,
  * other values return hipErrorNotSupported. N % 8 == 0; K % 256 (int8) or K % 16 (fp8). */
 int cozyq_gemm(int device, int family, int fp8, const void* q, const float* scales,
@@ -140,8 +141,9 @@ void cozyq_host_mx_byte(const float* amax, uint8_t* out, int64_t n);
 /* Test entry (no reference counterpart): one 16x16 MFMA on per-lane operands, to confirm the
  * lane layouts the GEMMs rely on. kind 0: i32_16x16x64_i8 (a, b: 64 lanes x 16 bytes);
  * 1: f32_16x16x128_f8f6f4 e4m3 (64 lanes x 32 bytes); 2: the same with E8M0 scales sa, sb
- * (one byte a lane); 3: f32_16x16x32_bf16 (64 lanes x 16 bytes). a and b are read as 64 lanes
- * x 32 bytes; d receives 64 lanes x 4 int32/float32 words. */
+ * (one byte a lane); 3: f32_16x16x32_bf16 (64 lanes x 16 bytes); 4: i32_32x32x32_i8 (64 lanes
+ * x 16 bytes). a and b are read as 64 lanes x 32 bytes; d receives 64 lanes x 16 int32/float32
+ * words (the 16x16 kinds fill the first 4). */
 int cozyq_probe_mfma(int device, int kind, const void* a, const void* b, const void* sa,
                      const void* sb, void* d, void* stream);
 
