@@ -190,6 +190,52 @@ def bench_mx(torch, ops, lib, stream, steps: int) -> dict:
     return result
 
 
+def bench_svdq(torch, ops, lib, stream, steps: int) -> dict:
+    """Config 4: SVDQuant W4A4 int4-g64, M=4096, K=N=3072, rank 32: the activation kernel
+    (smoothing, int4 codes, la = bf16(x·downᵀ)) then the GEMM with the low-rank add and bias."""
+    from oracle import laws
+
+    m, k, n, r = 4096, 3072, 3072, 32
+    gen = torch.Generator().manual_seed(20261204)
+    x = _activations(torch, m, k, 81)
+    p = (torch.rand(k, generator=gen) * 1.5 + 0.5).cuda()
+    down = (torch.randn(r, k, generator=gen) * 0.02).to(torch.bfloat16)
+    up = (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16)
+    codes, scales = laws.svdq_weight(torch.randn(n, k, generator=gen) * 0.02, p.cpu(), down, up)
+    down, up, codes, scales = down.cuda(), up.cuda(), codes.cuda(), scales.cuda()
+    bias = (torch.randn(n, generator=gen) * 0.5).to(torch.bfloat16).cuda()
+    act = torch.empty(m, k // 2, dtype=torch.uint8, device="cuda")
+    ascales = torch.empty(m, k // 64, dtype=torch.float16, device="cuda")
+    la = torch.empty(m, r, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+
+    def quantize():
+        _check(lib.cozyq_svdq_int4_quantize(0, x.data_ptr(), 0, p.data_ptr(), down.data_ptr(),
+                                            act.data_ptr(), ascales.data_ptr(), la.data_ptr(), m,
+                                            k, r, stream))  # fmt: skip
+
+    def gemm():
+        _check(lib.cozyq_svdq_int4_gemm(0, act.data_ptr(), ascales.data_ptr(), codes.data_ptr(),
+                                        scales.data_ptr(), la.data_ptr(), up.data_ptr(),
+                                        bias.data_ptr(), out.data_ptr(), 0, m, n, k, r, stream))  # fmt: skip
+
+    def step():
+        quantize()
+        gemm()
+
+    timer = Timer(torch)
+    q_ms = timer.run(quantize, steps, 2)
+    g_ms = timer.run(gemm, steps, 2)
+    ms = timer.run(step, steps, 2)
+    int4_ops = 2.0 * m * n * k
+    lowrank_flops = 2.0 * m * r * (k + n)
+    return {"M": m, "K": k, "N": n, "R": r, "us": ms * 1e3, "quantize_us": q_ms * 1e3,
+            "gemm_us": g_ms * 1e3, "tops": (int4_ops + lowrank_flops) / (ms * 1e-3) / 1e12,
+            "gemm_tops": int4_ops / (g_ms * 1e-3) / 1e12,
+            "frac_int8_mfma": int4_ops / (g_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
+            "kernel": "svdq_gemm_kernel (int4 unpacked to int8, 32x32x32 MFMA, per-group rescale)"}
+
+
 def cpu_baseline(torch, rows: int = 1024) -> dict:
     """The reference's CPU law for config 2 on rows 0..rows-1 of the batch: rotation + per-token
     int8 (`quantize_rows`), the literal int32 matmul, both scales, bias and GELU."""
@@ -247,6 +293,7 @@ def main() -> int:
         configs["c3_fp8"] = [bench_fp8(torch, ops, lib, stream, m, max(10, args.steps // 2))
                              for m in (256, 4096)]  # fmt: skip
         configs["c3_fp8_small"] = [bench_decode(torch, ops, lib, stream, args.steps, args.warmup, m=16)]
+        configs["c4_svdq_w4a4"] = bench_svdq(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["c5_mxfp8"] = bench_mx(torch, ops, lib, stream, max(10, args.steps // 2))
         print("[bench] extra configs done", file=sys.stderr, flush=True)
     baseline = None if args.no_cpu else cpu_baseline(torch)

@@ -261,9 +261,11 @@ class Prebuilt:
         act = torch.empty(rows, width // 2, dtype=torch.uint8, device=x.device)
         ascales = torch.empty(rows, width // INT4_GROUP, dtype=torch.float16, device=x.device)
         la = torch.empty(rows, r, dtype=torch.bfloat16, device=x.device)
+        if rows == 0:
+            return act, ascales, la
         code = self._lib.cozyq_svdq_int4_quantize(
-            self.index, flat.data_ptr(), self._half(flat.dtype), p.contiguous().data_ptr(),
-            down.contiguous().data_ptr(), act.data_ptr(), ascales.data_ptr(), la.data_ptr(), rows,
+            self.index, flat.data_ptr(), self._half(flat.dtype), _aligned(p).data_ptr(),
+            _aligned(down).data_ptr(), act.data_ptr(), ascales.data_ptr(), la.data_ptr(), rows,
             width, r, self._stream(),
         )  # fmt: skip
         self._check(code, "the svdq quantization")
@@ -282,14 +284,22 @@ class Prebuilt:
             raise ValueError("svdq: up must be bf16 [N, R] and la [M, R]")
         if n % 8:
             raise ValueError("svdq: N must be a multiple of 8")
+        if act.dtype != torch.uint8 or w.dtype != torch.uint8 or la.dtype != torch.bfloat16:
+            raise ValueError("svdq: codes must be uint8 (two int4 a byte) and la bf16")
+        if ascales.dtype != torch.float16 or wscales.dtype != torch.float16:
+            raise ValueError("svdq: group scales must be float16")
+        if tuple(ascales.shape) != (rows, width // INT4_GROUP):
+            raise ValueError(f"svdq: activation scales must be [{rows}, {width // INT4_GROUP}]")
         self._half(out_dtype)
-        bias = None if bias is None else bias.to(out_dtype).contiguous()
+        bias = None if bias is None else _aligned(bias.to(out_dtype))
         out = torch.empty(rows, n, dtype=out_dtype, device=act.device)
         if rows == 0:
             return out
+        act, ascales, w, wscales, la, up = (
+            _aligned(t) for t in (act, ascales, w, wscales, la, up))
         code = self._lib.cozyq_svdq_int4_gemm(
             self.index, act.data_ptr(), ascales.data_ptr(), w.data_ptr(), wscales.data_ptr(),
-            la.data_ptr(), up.contiguous().data_ptr(), _ptr(bias), out.data_ptr(),
+            la.data_ptr(), up.data_ptr(), _ptr(bias), out.data_ptr(),
             self._half(out_dtype), rows, n, width, r, self._stream(),
         )  # fmt: skip
         self._check(code, "the svdq GEMM")

@@ -164,6 +164,8 @@ int cozyq_svdq_int4_quantize(int device, const void* x, int x_half, const float*
                              int K, int R, void* stream) {
     if (M < 0 || !fits(K, 64) || (R != 16 && R != 32 && R != 64)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
+    if (!aligned16(x) || !aligned16(p) || !aligned16(down) || !aligned16(act))
+        return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
     return cozyq::svdq_int4_quantize(x, x_half, p, down, act, ascales, la, M, K, R, on(stream));
@@ -174,6 +176,8 @@ int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales
                          const void* up, const void* bias, void* out, int out_half, int M, int N,
                          int K, int R, void* stream) {
     if (M < 1 || N < 1 || N % 8 || !fits(K, 64) || (R != 16 && R != 32 && R != 64))
+        return hipErrorInvalidValue;
+    if (!aligned16(act) || !aligned16(w) || !aligned16(la) || !aligned16(up))
         return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();

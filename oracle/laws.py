@@ -16,6 +16,10 @@ Pins, exercised in `tests/test_oracle.py`:
   of log2) and the round trip through the mxfp8 decode law.
 - `int8_*` products: int32 GEMM against numpy int64 matmul.
 - `int4_quantize` (build law): round trip bound |x − q·s| ≤ s/2 and brute force on small cases.
+- `svdq_smooth`, `svdq_down`, `svdq_exact` (the W4A4 structure): closed forms — unit and
+  power-of-two smoothing, one-hot and integer-valued down projections (against numpy int64),
+  the fp16 cast of `down` for fp16 x, and activations/weights placed on the int4 grid so that
+  the product equals numpy's matmul of the dequantized operands, group by group.
 """
 
 from __future__ import annotations
@@ -341,20 +345,24 @@ def svdq_smooth(x: torch.Tensor, p: torch.Tensor) -> torch.Tensor:
     return (flat.float() * p.float()).to(torch.bfloat16).float()
 
 
-def svdq_down(x: torch.Tensor, l1: torch.Tensor) -> torch.Tensor:
-    """The low-rank branch's input `bf16(x · L1)` with L1 `[K, R]` (`internal/svdq_linear.py:
-    598-602`, whose `down` is L1ᵀ), accumulated in float32 (here float64, then one rounding)."""
-    flat = x.reshape(-1, int(l1.shape[0]))
-    return (flat.double() @ l1.double()).to(torch.bfloat16)
+def svdq_down(x: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
+    """The low-rank branch's input `bf16(x · downᵀ)`, down `[R, K]` (`internal/svdq_linear.py:
+    598-602`): x in its half dtype (bf16 for float32 x) and down cast to that dtype, the
+    products summed exactly (float64 here; the reference accumulates in float32), one
+    rounding to bf16."""
+    flat = x.reshape(-1, int(down.shape[1]))
+    half = flat.dtype if flat.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
+    return (flat.to(half).double() @ down.to(half).double().t()).to(torch.bfloat16)
 
 
 def svdq_weight(
-    w: torch.Tensor, p: torch.Tensor, l1: torch.Tensor, l2: torch.Tensor
+    w: torch.Tensor, p: torch.Tensor, down: torch.Tensor, up: torch.Tensor
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Build weight producer: the residual W − (L1·L2)ᵀ moved into the smoothed basis (÷ p per
-    input channel, so (x·p)·Rᵀ = x·(W − (L1L2)ᵀ)ᵀ), then `int4_quantize` per 64-group.
+    """Build weight producer (the reference's is tensorfs's SVDQ writer, not in the repository):
+    the residual W − up·down moved into the smoothed basis (÷ p per input channel, so
+    (x·p)·Rᵀ = x·(W − up·down)ᵀ), then `int4_quantize` per 64-group. down `[R, K]`, up `[N, R]`.
     Returns packed codes `[N, K/2]` and float16 scales `[N, K/64]`."""
-    residual = w.double() - (l1.double() @ l2.double()).t()
+    residual = w.double() - up.double() @ down.double()
     smoothed = (residual / p.double().reshape(1, -1)).float()
     q, s = int4_quantize(smoothed)
     return pack_int4(q), s
@@ -362,10 +370,10 @@ def svdq_weight(
 
 def svdq_exact(
     x: torch.Tensor, p: torch.Tensor, wcodes: torch.Tensor, wscale: torch.Tensor,
-    l1: torch.Tensor, l2: torch.Tensor, bias: torch.Tensor | None,
+    down: torch.Tensor, up: torch.Tensor, bias: torch.Tensor | None,
 ) -> torch.Tensor:
     """The W4A4 product in float64 (`internal/svdq_linear.py:639-659`'s structure with the
-    int4-g64 law): Σ_g (Σ_{k∈g} qx·qw)·sx[m,g]·sw[n,g] + bf16(x·L1)·L2 + bias."""
+    int4-g64 law): Σ_g (Σ_{k∈g} qx·qw)·sx[m,g]·sw[n,g] + bf16(x·downᵀ)·upᵀ + bias."""
     qx, sx = int4_quantize(svdq_smooth(x, p))
     qw = unpack_int4(wcodes)
     rows, cols = int(qx.shape[0]), int(qx.shape[1])
@@ -373,23 +381,24 @@ def svdq_exact(
     ax = qx.double().reshape(rows, groups, INT4_GROUP) * sx.double().unsqueeze(-1)
     aw = qw.double().reshape(-1, groups, INT4_GROUP) * wscale.double().unsqueeze(-1)
     out = ax.reshape(rows, cols) @ aw.reshape(-1, cols).t()
-    out = out + svdq_down(x, l1).double() @ l2.double()
+    out = out + svdq_down(x, down).double() @ up.double().t()
     return out if bias is None else out + bias.double()
 
 
 def svdq_linear(
     x: torch.Tensor, p: torch.Tensor, wcodes: torch.Tensor, wscale: torch.Tensor,
-    l1: torch.Tensor, l2: torch.Tensor, bias: torch.Tensor | None, out_dtype: torch.dtype,
+    down: torch.Tensor, up: torch.Tensor, bias: torch.Tensor | None, out_dtype: torch.dtype,
 ) -> torch.Tensor:
-    """The CPU path timed as the W4A4 baseline: the int4 law, dequantized float32 matmul, the
-    bf16 low-rank branch and the bias, one cast."""
+    """The CPU path timed as the W4A4 baseline (`internal/svdq_linear.py:639-659` with the
+    int4-g64 law): activations quantized, both operands dequantized to float32, one float32
+    matmul, plus the bf16 low-rank branch and the bias in float32, one cast."""
     qx, sx = int4_quantize(svdq_smooth(x, p))
     rows, cols = int(qx.shape[0]), int(qx.shape[1])
     groups = cols // INT4_GROUP
     ax = (qx.float().reshape(rows, groups, INT4_GROUP) * sx.float().unsqueeze(-1)).reshape(rows, cols)
     qw = unpack_int4(wcodes)
     aw = (qw.float().reshape(-1, groups, INT4_GROUP) * wscale.float().unsqueeze(-1)).reshape(-1, cols)
-    out = ax @ aw.t() + svdq_down(x, l1).float() @ l2.float()
+    out = ax @ aw.t() + svdq_down(x, down).float() @ up.float().t()
     if bias is not None:
         out = out + bias.float()
     return out.to(out_dtype)

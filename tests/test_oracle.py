@@ -302,3 +302,98 @@ def test_int4_pack_round_trip():
     assert packed.shape == (5, 64)
     assert int(packed[0, 0]) & 0xF == int(q[0, 0]) & 0xF
     assert torch.equal(laws.unpack_int4(packed), q)
+
+
+# --------------------------------------------------------------- SVDQuant W4A4 structure
+
+
+def test_svdq_smooth_closed_forms():
+    """Unit smoothing returns x itself; a power-of-two p scales exactly; a general p lands every
+    value on the bf16 grid (the rounding is taken) within half a bf16 step of the product."""
+    gen = torch.Generator().manual_seed(6)
+    x = torch.randn(3, 128, generator=gen).to(torch.bfloat16)
+    assert torch.equal(laws.svdq_smooth(x, torch.ones(128)), x.float())
+    assert torch.equal(laws.svdq_smooth(x, torch.full((128,), 0.25)), x.float() * 0.25)
+    p = torch.rand(128, generator=gen) * 1.5 + 0.5
+    got = laws.svdq_smooth(x, p)
+    assert (got.view(torch.int32) & 0xFFFF).eq(0).all()
+    exact = x.double() * p.double()
+    assert ((got.double() - exact).abs() <= exact.abs() * 2.0 ** -8).all()
+    assert not torch.equal(got, (x.float() * p))  # the bf16 rounding is taken
+
+
+def test_svdq_down_one_hot_and_integer():
+    """A one-hot down row picks one input column; integer-valued operands sum exactly (numpy
+    int64); an fp16 x casts down to fp16 first, so a bf16 value below fp16's range vanishes."""
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(5, 192, generator=gen).to(torch.bfloat16)
+    down = torch.zeros(16, 192, dtype=torch.bfloat16)
+    cols = torch.randperm(192, generator=gen)[:16]
+    down[torch.arange(16), cols] = 1
+    assert torch.equal(laws.svdq_down(x, down), x[:, cols])
+    xi = torch.randint(-20, 21, (6, 256), generator=gen)
+    di = torch.randint(-20, 21, (32, 256), generator=gen)
+    want = xi.numpy().astype(np.int64) @ di.numpy().astype(np.int64).T
+    got = laws.svdq_down(xi.to(torch.bfloat16), di.to(torch.bfloat16))
+    assert torch.equal(got, torch.from_numpy(want).to(torch.bfloat16))
+    xh = torch.ones(1, 64, dtype=torch.float16)
+    tiny = torch.full((16, 64), 1e-9, dtype=torch.bfloat16)  # below fp16's least subnormal / 2
+    assert laws.svdq_down(xh, tiny).eq(0).all()
+    assert laws.svdq_down(xh.to(torch.bfloat16), tiny).ne(0).all()
+
+
+def _on_grid(gen: torch.Generator, rows: int, cols: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Values exactly on the int4 grid: per 64-group codes with ±7 present and a power-of-two
+    step, so that int4_quantize gives back these codes and step."""
+    q = torch.randint(-7, 8, (rows, cols), generator=gen)
+    q[:, ::64] = 7
+    step = 2.0 ** torch.randint(-6, 2, (rows, cols // 64), generator=gen).float()
+    v = (q.float().reshape(rows, -1, 64) * step.unsqueeze(-1)).reshape(rows, cols)
+    return v, q.to(torch.int8), step.to(torch.float16)
+
+
+def test_svdq_exact_on_the_grid_equals_matmul():
+    """With x and the residual on the int4 grid, unit smoothing and a zero low-rank branch, the
+    W4A4 product is numpy's matmul of the two matrices: a transposed, shifted or mis-scaled
+    group fails it."""
+    gen = torch.Generator().manual_seed(8)
+    x, qx, sx = _on_grid(gen, 9, 320)
+    w, qw, sw = _on_grid(gen, 24, 320)
+    assert torch.equal(laws.int4_quantize(x)[0], qx) and torch.equal(laws.int4_quantize(x)[1], sx)
+    codes, scales = laws.pack_int4(qw), sw
+    down = torch.zeros(16, 320, dtype=torch.bfloat16)
+    up = torch.zeros(24, 16, dtype=torch.bfloat16)
+    got = laws.svdq_exact(x.to(torch.bfloat16), torch.ones(320), codes, scales, down, up, None)
+    want = x.double().numpy() @ w.double().numpy().T
+    assert np.array_equal(got.numpy(), want)
+    bias = torch.randn(24, generator=gen).to(torch.bfloat16)
+    got_b = laws.svdq_exact(x.to(torch.bfloat16), torch.ones(320), codes, scales, down, up, bias)
+    assert np.array_equal(got_b.numpy(), want + bias.double().numpy())
+
+
+def test_svdq_exact_low_rank_branch_only():
+    """Zero residual codes: the product is the low-rank branch alone, bf16(x·downᵀ)·upᵀ."""
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randint(-4, 5, (7, 128), generator=gen).to(torch.bfloat16)
+    down = torch.randint(-3, 4, (32, 128), generator=gen).to(torch.bfloat16)
+    up = torch.randint(-3, 4, (40, 32), generator=gen).to(torch.bfloat16)
+    codes = torch.zeros(40, 64, dtype=torch.uint8)
+    scales = torch.ones(40, 2, dtype=torch.float16)
+    got = laws.svdq_exact(x, torch.ones(128), codes, scales, down, up, None)
+    la = x.double().numpy() @ down.double().numpy().T  # small integers: exact in bf16
+    assert np.array_equal(got.numpy(), la @ up.double().numpy().T)
+
+
+def test_svdq_weight_reconstructs_effective_weight():
+    """The producer's residual, dequantized and re-smoothed, plus up·down is W to within half a
+    quantization step per element (the int4 round trip), and exactly W on the grid."""
+    gen = torch.Generator().manual_seed(10)
+    r, n, k = 16, 24, 192
+    down = (torch.randn(r, k, generator=gen) * 0.02).to(torch.bfloat16)
+    up = (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16)
+    grid, _, _ = _on_grid(gen, n, k)
+    p = 2.0 ** torch.randint(-1, 2, (k,), generator=gen).float()
+    w = grid.double() * p.double() + up.double() @ down.double()
+    codes, scales = laws.svdq_weight(w, p, down, up)
+    deq = (laws.unpack_int4(codes).double().reshape(n, -1, 64) * scales.double().unsqueeze(-1)).reshape(n, k)
+    assert np.allclose((deq * p.double() + up.double() @ down.double()).numpy(), w.numpy(), rtol=0, atol=1e-12)
