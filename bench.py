@@ -33,6 +33,12 @@ METRIC = "quantized-linear TOPS & % MFMA peak (M=4096,K=3072,N=12288); M=1 HBM G
 PEAK_INT8_TOPS = 5000.0
 PEAK_FP8_TFLOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
+#: HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (one counter a
+#: pass, each scaled by the same counter's reading for a 256 MiB device copy: x2.0 and x1.0),
+#: summarized in profiles/hbm_traffic_pmc.txt. The config-2 GEMM reads X and W ~4.5x: each of
+#: the 8 XCDs' L2s fetches the K-slices its own tiles use.
+TRAFFIC_C2_GEMM = {"read": 227.43e6, "write": 100.66e6}
+TRAFFIC_DECODE = {"read": 59.15e6, "write": 0.03e6}
 
 
 def _seeded(torch, seed: int):
@@ -115,7 +121,8 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
         "quantize_gbs": (m * k * 2 + m * k + m * 4) / (ms_quant * 1e-3) / 1e9,
         "roofline": {
             "bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
-            "frac": gemm_tops / PEAK_INT8_TOPS, "traffic": None,
+            "frac": gemm_tops / PEAK_INT8_TOPS,
+            "traffic": TRAFFIC_C2_GEMM["read"] + TRAFFIC_C2_GEMM["write"],
             "kernel": "gemm_kernel<int8> 256x256 (bias+GELU epilogue)",
             "algorithmic_ops": ops_count, "algorithmic_bytes": traffic_alg,
         },
@@ -140,7 +147,8 @@ def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -
     nbytes = n * k + n * 4 + m * k * 2 + m * n * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"M": m, "K": k, "N": n, "us": ms * 1e3, "bytes": nbytes, "gbs": gbs,
-            "frac": gbs / PEAK_HBM_GBS, "weight_copies": copies,
+            "frac": gbs / PEAK_HBM_GBS, "traffic": TRAFFIC_DECODE["read"] + TRAFFIC_DECODE["write"],
+            "weight_copies": copies,
             "kernel": "fp8_small_kernel (fused quantize + GEMV)"}
 
 
@@ -263,6 +271,24 @@ def cpu_baseline(torch, rows: int = 1024) -> dict:
     }
 
 
+def only(torch, ops, lib, stream, args) -> int:
+    """One leg alone, for `rocprofv3` runs (kernel traces and counters per dispatch)."""
+    if args.only == "copy":
+        nbytes = 256 << 20
+        src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        ms = Timer(torch).run(lambda: dst.copy_(src), args.steps, args.warmup)
+        figures = {"copy_bytes": nbytes, "us": ms * 1e3, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
+    elif args.only == "c2":
+        figures = bench_c2(torch, ops, lib, stream, args.steps, args.warmup)
+    elif args.only == "decode":
+        figures = bench_decode(torch, ops, lib, stream, args.steps, args.warmup)
+    else:
+        figures = bench_svdq(torch, ops, lib, stream, args.steps)
+    print(json.dumps({"only": args.only, **figures}))
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -270,6 +296,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
+    parser.add_argument("--only", choices=("c2", "decode", "svdq", "copy"),
+                        help="profiling aid: run one leg (or a plain 256 MiB device copy, the "
+                             "counter calibration) --steps times and print its figures only")  # fmt: skip
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the linear shards "
@@ -284,6 +313,8 @@ def main() -> int:
     lib = _lib.load()
     stream = torch.cuda.current_stream().cuda_stream
 
+    if args.only:
+        return only(torch, ops, lib, stream, args)
     c2 = bench_c2(torch, ops, lib, stream, args.steps, args.warmup)
     print(f"[bench] c2 {c2['ms_per_step']:.4f} ms/step, gemm {c2['gemm_ms']:.4f} ms", file=sys.stderr, flush=True)
     decode = bench_decode(torch, ops, lib, stream, args.steps, args.warmup)
