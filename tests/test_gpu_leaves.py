@@ -1,0 +1,147 @@
+"""The encoded leaves end to end on the GPU (`cozyq.leaves`): each provider's leaf against the
+CPU oracle, and the reference's call-graph behaviours — shared operands (`quantize_once`),
+producer operands (`int8_rows`), writing into a sibling group's column range (`out=`), the
+decode-row path and autocast. int8 outputs bit-exact; the others within ATOL·rms + RTOL·|x|."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from cozyq import int8_linear, leaves, operands
+from oracle import laws
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-2, 2e-2
+DEV = "cuda:0"
+
+
+class _Linear(torch.nn.Module):
+    def __init__(self, bias: torch.Tensor | None) -> None:
+        super().__init__()
+        self.bias = bias
+
+
+def _gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def activations(m: int, k: int, seed: int, dtype=torch.bfloat16) -> torch.Tensor:
+    gen = _gen(seed)
+    x = torch.randn(m, k, generator=gen)
+    x[:, torch.randperm(k, generator=gen)[: max(1, k // 100)]] *= 20
+    return x.to(dtype)
+
+
+def assert_close(got: torch.Tensor, exact: torch.Tensor) -> None:
+    got, exact = got.double().cpu(), exact.double().cpu()
+    rms = exact.pow(2).mean().sqrt().item()
+    worst = ((got - exact).abs() - (ATOL * rms + RTOL * exact.abs())).max().item()
+    assert worst <= 0, f"max excess {worst:.3g} (rms {rms:.3g})"
+
+
+def int8_leaf(n: int, k: int, seed: int, bias: bool = True):
+    data, scale = laws.int8_weight_rotated(torch.randn(n, k, generator=_gen(seed)) * 0.02, 256)
+    b = (torch.randn(n, generator=_gen(seed + 1)) * 0.1).to(torch.bfloat16) if bias else None
+    leaf = leaves.Int8ConvRotNativeLeaf().leaf(
+        torch, {"weight": data.to(DEV), "scale": scale.to(DEV)},
+        _Linear(None if b is None else b.to(DEV)), torch.bfloat16)  # fmt: skip
+    return leaf, data, scale, b
+
+
+@pytest.mark.parametrize("m", [3, 300])
+def test_int8_leaf_bit_exact(m):
+    leaf, data, scale, b = int8_leaf(520, 1024, 71)
+    x = activations(m, 1024, 72 + m)
+    got = leaf(x.to(DEV))
+    assert got.dtype == torch.bfloat16 and got.shape == (m, 520)
+    assert torch.equal(got.cpu(), laws.int8_linear(x, data, scale, b, torch.bfloat16, rotation=256))
+
+
+def test_int8_leaves_share_one_quantization(monkeypatch):
+    """q, k and v of one input quantize it once inside `quantize_once`, and each output is what
+    the leaf computes alone."""
+    x = activations(200, 512, 81).to(DEV)
+    trio = [int8_leaf(256, 512, 82 + 7 * i)[0] for i in range(3)]
+    alone = [leaf(x) for leaf in trio]
+    lib = int8_linear.library(0)
+    calls = []
+    original = type(lib).int8_quantize
+
+    def counting(self, *args, **kwargs):
+        calls.append(1)
+        return original(self, *args, **kwargs)
+
+    monkeypatch.setattr(type(lib), "int8_quantize", counting)
+    with operands.quantize_once(x):
+        shared = [leaf(x) for leaf in trio]
+    assert len(calls) == 1
+    for a, s in zip(alone, shared):
+        assert torch.equal(a, s)
+
+
+def test_int8_rows_operand_and_out_into_a_column_range():
+    leaf, data, scale, b = int8_leaf(264, 768, 91)
+    x = activations(130, 768, 92)
+    xd = x.to(DEV)
+    pre = operands.int8_rows(xd, (leaf,))
+    assert isinstance(pre, operands.PreQuantized) and pre.provider == operands.INT8_CONVROT
+    want = laws.int8_linear(x, data, scale, b, torch.bfloat16, rotation=256)
+    assert torch.equal(leaf(xd, prequantized=pre).cpu(), want)
+    packed = torch.zeros(130, 3 * 264, dtype=torch.bfloat16, device=DEV)
+    got = leaf(xd, out=packed[:, 264:528])
+    assert got.data_ptr() == packed[:, 264:528].data_ptr()
+    assert torch.equal(packed[:, 264:528].cpu(), want)
+    assert packed[:, :264].eq(0).all() and packed[:, 528:].eq(0).all()
+    assert leaf(xd, prequantized=pre, out=packed[:, :264]).data_ptr() == packed.data_ptr()
+
+
+def test_int8_leaf_autocast_dtype():
+    leaf, data, scale, _ = int8_leaf(256, 512, 95, bias=False)
+    x = activations(40, 512, 96)
+    with torch.autocast("cuda", dtype=torch.float16):
+        got = leaf(x.to(DEV))
+    assert got.dtype == torch.float16
+    want = laws.int8_linear(x.to(torch.float16), data, scale, None, torch.float16, rotation=256)
+    assert torch.equal(got.cpu(), want)
+
+
+@pytest.mark.parametrize("m", [1, 16, 300])
+def test_fp8_leaf_within_tolerance(m):
+    n, k = 1032, 2048
+    data, scale = laws.fp8_weight(torch.randn(n, k, generator=_gen(101)) * 0.02)
+    b = (torch.randn(n, generator=_gen(102)) * 0.1).to(torch.bfloat16)
+    leaf = leaves.RowwiseNativeLeaf().leaf(torch, {"weight": data.to(DEV), "scale": scale.to(DEV)},
+                                           _Linear(b.to(DEV)), torch.bfloat16)  # fmt: skip
+    x = activations(m, k, 103 + m)
+    got = leaf(x.to(DEV))
+    assert got.shape == (m, n) and leaf.operand == operands.ROWWISE_FP8
+    assert_close(got, laws.fp8_exact(x, data, scale, b))
+
+
+def test_mx_leaf_within_tolerance():
+    n, k, m = 264, 1024, 300
+    data, wbyte = laws.mx_quantize(torch.randn(n, k, generator=_gen(111)) * 0.02)
+    b = (torch.randn(n, generator=_gen(112)) * 0.1).to(torch.bfloat16)
+    provider = leaves.MicroScaledNativeLeaf(params=(("scale_layout", "cublas_128x4"),))
+    leaf = provider.leaf(torch, {"weight": data.to(DEV), "scale": laws.to_blocked(wbyte).to(DEV)},
+                         _Linear(b.to(DEV)), torch.bfloat16)  # fmt: skip
+    x = activations(m, k, 113)
+    assert_close(leaf(x.to(DEV)), laws.mx_exact(x, data, wbyte, b))
+
+
+def test_svdq_leaf_within_tolerance():
+    n, k, r, m = 520, 1024, 32, 260
+    gen = _gen(121)
+    p = torch.rand(k, generator=gen) * 1.5 + 0.5
+    down = (torch.randn(r, k, generator=gen) * 0.02).to(torch.bfloat16)
+    up = (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16)
+    codes, scales = laws.svdq_weight(torch.randn(n, k, generator=gen) * 0.02, p, down, up)
+    b = (torch.randn(n, generator=gen) * 0.1).to(torch.bfloat16)
+    parts = {"weight": codes, "scale": scales, "pre_quant_scale": p, "lowrank_down": down,
+             "lowrank_up": up}  # fmt: skip
+    leaf = leaves.SvdqInt4NativeLeaf().leaf(torch, {key: v.to(DEV) for key, v in parts.items()},
+                                            _Linear(b.to(DEV)), torch.bfloat16)  # fmt: skip
+    x = activations(m, k, 122)
+    assert_close(leaf(x.to(DEV)), laws.svdq_exact(x, p, codes, scales, down, up, b))

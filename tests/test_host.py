@@ -1,0 +1,158 @@
+"""The host layer on the CPU (no kernels run): the leaf providers' surface, leaf construction
+and buffers, operand sharing (`quantize_once`, `shared_operand`, `int8_rows`), the 128x4 scale
+layout against the oracle's, and that a leaf refuses to compute off the GPU instead of falling
+back."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from cozyq import layout, leaves, operands
+from oracle import laws
+
+
+class _Linear(torch.nn.Module):
+    def __init__(self, n: int, k: int, bias: bool) -> None:
+        super().__init__()
+        self.weight = torch.nn.Parameter(torch.zeros(n, k))
+        self.bias = torch.nn.Parameter(torch.ones(n)) if bias else None
+
+
+def test_providers_surface_and_launch_table():
+    table = leaves.launch_providers()
+    assert set(table) == {"fp8.rowwise", "int8.convrot", "svdq.int4g64", "mxfp8"}
+    names = {p.name for ps in table.values() for p in ps}
+    assert names == {operands.ROWWISE_FP8, operands.INT8_CONVROT, leaves.MXFP8, leaves.SVDQ_INT4}
+    for scheme, (provider,) in table.items():
+        assert provider.encoding == scheme
+        assert provider.route == "encoded_gemm"
+        assert provider.device_predicate == "rocm.gfx950"
+        assert provider.output_dtype_rule == "contract"
+        assert {"weight", "scale"} <= provider.required
+        assert leaves.serves(provider, "gfx950") and not leaves.serves(provider, "gfx942")
+        with pytest.raises(AssertionError):
+            provider.decode(torch, {}, torch.empty(0))
+
+
+def test_supports_messages():
+    fp8 = leaves.RowwiseNativeLeaf()
+    assert fp8.supports((64, 128), {}) == ""
+    assert "K divisible by 16" in fp8.supports((64, 120), {})
+    assert "rank-2" in fp8.supports((4, 4, 4), {})
+    i8 = leaves.Int8ConvRotNativeLeaf()
+    assert i8.supports((64, 512), {"rotation_size": 256}) == ""
+    assert "256-groups" in i8.supports((64, 512), {"rotation_size": 128})
+    assert "divisible by 8" in i8.supports((60, 512), {"rotation_size": 256})
+    mx = leaves.MicroScaledNativeLeaf()
+    assert mx.supports((64, 256), {}) == "" and "128-element" in mx.supports((64, 96), {})
+    sv = leaves.SvdqInt4NativeLeaf()
+    assert sv.supports((64, 96), {"rank": 32}) == ""
+    assert "ranks" in sv.supports((64, 96), {"rank": 8})
+    assert "K % 64" in sv.supports((64, 40), {})
+
+
+def test_native_leaf_buffers_roles_and_refusal_off_gpu():
+    provider = leaves.Int8ConvRotNativeLeaf()
+    data = torch.randint(-127, 128, (16, 256), dtype=torch.int8)
+    scale = torch.rand(16, dtype=torch.float64)
+    leaf = provider.leaf(torch, {"weight": data, "scale": scale}, _Linear(16, 256, True), torch.bfloat16)
+    assert isinstance(leaf, torch.nn.Module)
+    assert leaf.data is data and leaf.scale.dtype == torch.float32  # the kernels read f32
+    assert not hasattr(leaf, "weight")  # no `.weight`: BUFFERS maps it to `data`
+    assert set(leaf.roles()) == {"weight", "scale"}
+    assert leaf.in_features == 256 and leaf.out_features == 16
+    assert leaf.operand == operands.INT8_CONVROT and leaf.WRITES_INTO
+    assert "provider='cozy.int8-convrot256.native-leaf/1'" in repr(leaf)
+    assert leaf.bias is not None and "_logical_dtype" not in leaf.state_dict()
+    x = torch.randn(8, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="gfx950"):
+        leaf(x)  # no CPU fallback: the kernels are the only implementation
+
+
+def test_fp8_and_svdq_leaves_refuse_off_gpu():
+    fp8 = leaves.RowwiseNativeLeaf().leaf(
+        torch, {"weight": torch.zeros(8, 64, dtype=torch.float8_e4m3fn), "scale": torch.ones(8)},
+        _Linear(8, 64, False), torch.bfloat16)  # fmt: skip
+    with pytest.raises(ValueError, match="gfx950"):
+        fp8(torch.randn(2, 64, dtype=torch.bfloat16))
+    parts = {"weight": torch.zeros(8, 32, dtype=torch.uint8), "scale": torch.ones(8, 1),
+             "pre_quant_scale": torch.ones(64), "lowrank_down": torch.zeros(16, 64),
+             "lowrank_up": torch.zeros(8, 16)}  # fmt: skip
+    sv = leaves.SvdqInt4NativeLeaf().leaf(torch, parts, _Linear(8, 64, False), torch.bfloat16)
+    assert sv.in_features == 64 and sv.scale.dtype == torch.float16
+    with pytest.raises(ValueError, match="gfx950"):
+        sv(torch.randn(2, 64, dtype=torch.bfloat16))
+
+
+def test_mx_leaf_untiles_cublas_scales():
+    gen = torch.Generator().manual_seed(3)
+    n, k = 136, 256
+    grid = torch.randint(0, 255, (n, k // 32), generator=gen, dtype=torch.uint8)
+    weight = torch.zeros(n, k, dtype=torch.float8_e4m3fn)
+    tiled = laws.to_blocked(grid)
+    provider = leaves.MicroScaledNativeLeaf(params=(("scale_layout", "cublas_128x4"),))
+    leaf = provider.leaf(torch, {"weight": weight, "scale": tiled}, _Linear(n, k, False), torch.bfloat16)
+    assert torch.equal(leaf.scale, grid)
+    plain = leaves.MicroScaledNativeLeaf().leaf(torch, {"weight": weight, "scale": grid},
+                                                _Linear(n, k, False), torch.bfloat16)  # fmt: skip
+    assert torch.equal(plain.scale, grid)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (128, 4), (130, 7), (300, 96), (17, 384)])
+def test_layout_matches_oracle(rows, cols):
+    grid = torch.randint(0, 256, (rows, cols), dtype=torch.uint8)
+    assert torch.equal(layout.to_blocked(torch, grid), laws.to_blocked(grid))
+    assert torch.equal(layout.from_blocked(torch, laws.to_blocked(grid), rows, cols), grid)
+    with pytest.raises(ValueError):
+        layout.from_blocked(torch, grid.reshape(-1)[:-1], rows, cols) if rows * cols > 1 else \
+            layout.from_blocked(torch, torch.zeros(3, dtype=torch.uint8), rows, cols)
+
+
+def _op(counter: list[int], x: torch.Tensor, provider: str):
+    def make():
+        counter.append(1)
+        return operands.PreQuantized(x, torch.ones(1), tuple(x.shape), provider)
+
+    return make
+
+
+def test_quantize_once_scope_shares_per_provider():
+    x, y = torch.randn(4, 8), torch.randn(4, 8)
+    made: list[int] = []
+    with operands.quantize_once(x, None):
+        a = operands.shared_operand(x, operands.INT8_CONVROT, _op(made, x, operands.INT8_CONVROT))
+        b = operands.shared_operand(x, operands.INT8_CONVROT, _op(made, x, operands.INT8_CONVROT))
+        c = operands.shared_operand(x, operands.ROWWISE_FP8, _op(made, x, operands.ROWWISE_FP8))
+        assert operands.shared_operand(y, operands.INT8_CONVROT, _op(made, y, "p")) is None  # no consumer
+    assert a is b and c is not a and len(made) == 2  # one per provider; y (no consumer) none
+
+
+def test_siblings_share_then_learn_their_group():
+    class Leaf:
+        pass
+
+    q, k, v = Leaf(), Leaf(), Leaf()
+    x = torch.randn(4, 8)
+    made: list[int] = []
+    p = operands.INT8_CONVROT
+    first = [operands.shared_operand(x, p, _op(made, x, p), leaf) for leaf in (q, k, v)]
+    assert first[0] is first[1] is first[2] and len(made) == 1
+    x2 = torch.randn(4, 8)  # a new input retires the held operand; q learns its group of 3
+    operands.shared_operand(x2, p, _op(made, x2, p), q)
+    assert q._cozy_siblings == 3 and len(made) == 2
+    x.add_(1)  # an in-place change is never served stale
+    operands.shared_operand(x, p, _op(made, x, p), q)
+    assert len(made) == 3
+
+
+def test_int8_rows_declines_foreign_consumers():
+    x = torch.randn(4, 256, dtype=torch.bfloat16)
+    assert operands.int8_rows(x, ()) is None
+    assert operands.int8_rows(x, (torch.nn.Linear(256, 8),)) is None
+    leaf = leaves.Int8ConvRotNativeLeaf().leaf(
+        torch, {"weight": torch.zeros(8, 256, dtype=torch.int8), "scale": torch.ones(8)},
+        _Linear(8, 256, False), torch.bfloat16)  # fmt: skip
+    assert operands.int8_rows(x, (leaf,)) is None  # a CPU tensor: the caller runs its own ops
+    with pytest.raises(ValueError, match="gate"):
+        operands.int8_rows(x, (leaf,), activation="situ", norm="rms")
