@@ -130,6 +130,12 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
 
 
 def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -> dict:
+    """Config 3 at decode size: the fused fp8 linear (quantize + GEMV, one launch), 8 rotating
+    weight copies (470 MB, beyond the 256 MB MALL). A decode step is a few microseconds of GPU
+    work, less than a Python-issued launch costs on the host, so the launches are captured
+    once into a HIP graph (64 of them, 8 per copy) and the graph is replayed: `us` is GPU time
+    per linear. `us_eager` is the same launches issued one by one from Python. The graph's
+    output is checked bit for bit against an eager launch."""
     k, n, copies = 4096, 14336, 8
     x = _activations(torch, m, k, 31)
     weights = [ops.fp8_quantize(_weights(torch, n, k, 40 + c)) for c in range(copies)]
@@ -138,18 +144,44 @@ def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -
     xp, op = x.data_ptr(), out.data_ptr()
     turn = [0]
 
-    def launch():
+    def launch(raw_stream):
         wp, sp = ptrs[turn[0] % copies]
         turn[0] += 1
-        _check(lib.cozyq_fp8_linear(0, xp, 0, wp, sp, None, op, 0, m, n, k, stream))
+        _check(lib.cozyq_fp8_linear(0, xp, 0, wp, sp, None, op, 0, m, n, k, raw_stream))
 
-    ms = Timer(torch).run(launch, max(steps, 64), max(warmup, 8))
+    eager_ms = Timer(torch).run(lambda: launch(stream), max(steps, 64), max(warmup, 8))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    per_graph = 8 * copies
+    turn[0] = 0
+    with torch.cuda.stream(side):
+        launch(side.cuda_stream)  # warm the side stream
+        torch.cuda.synchronize()
+        turn[0] = 0
+        with torch.cuda.graph(graph, stream=side):
+            raw = torch.cuda.current_stream().cuda_stream
+            for _ in range(per_graph):
+                launch(raw)
+    torch.cuda.synchronize()
+    replays = max(4, steps // 8)
+    ms = Timer(torch).run(graph.replay, replays, 2) / per_graph
+    graph.replay()
+    torch.cuda.synchronize()
+    replayed = out.clone()
+    turn[0] = copies - 1  # the graph's last launch used the last copy
+    launch(stream)
+    torch.cuda.synchronize()
+    if not torch.equal(replayed, out):
+        raise RuntimeError("decode: the graph replay differs from the eager launch")
     nbytes = n * k + n * 4 + m * k * 2 + m * n * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"M": m, "K": k, "N": n, "us": ms * 1e3, "bytes": nbytes, "gbs": gbs,
-            "frac": gbs / PEAK_HBM_GBS, "traffic": TRAFFIC_DECODE["read"] + TRAFFIC_DECODE["write"],
-            "weight_copies": copies,
-            "kernel": "fp8_small_kernel (fused quantize + GEMV)"}
+    return {"M": m, "K": k, "N": n, "us": ms * 1e3, "us_eager": eager_ms * 1e3, "bytes": nbytes,
+            "gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
+            "traffic": TRAFFIC_DECODE["read"] + TRAFFIC_DECODE["write"], "weight_copies": copies,
+            "timing": "HIP graph of 64 launches, replayed", "kernel": "fp8_decode_kernel (M<=4) / "
+            "fp8_small_kernel (M<=16): quantize fused with the GEMV"}
 
 
 def bench_fp8(torch, ops, lib, stream, m: int, steps: int) -> dict:

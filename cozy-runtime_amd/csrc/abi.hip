@@ -133,6 +133,8 @@ int cozyq_fp8_linear(int device, const void* x, int x_half, const uint8_t* w,
                      int N, int K, void* stream) {
     if (M < 0 || N < 1 || N % 8 || !fits(K, 16)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
+    if (!aligned16(x) || !aligned16(w) || (reinterpret_cast<uintptr_t>(out) & 7))
+        return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
     return cozyq::fp8_linear_small(x, x_half, w, w_scale, bias, out, out_half, M, N, K,
@@ -187,6 +189,21 @@ int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales
 
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = cozyq::e4m3_rn(in[i]);
+}
+
+int cozyq_probe_e4m3(int device, const float* in, uint8_t* out, int64_t n, void* stream) {
+    if (n < 0 || n % 2) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::e4m3_probe(in, out, n, on(stream));
+}
+
+int cozyq_probe_div(int device, const float* x, const float* s, float* out, int64_t n,
+                    void* stream) {
+    if (n < 0) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::div_probe(x, s, out, n, on(stream));
 }
 
 void cozyq_host_mx_byte(const float* amax, uint8_t* out, int64_t n) {

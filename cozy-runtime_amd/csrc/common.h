@@ -69,6 +69,25 @@ __host__ __device__ __forceinline__ uint8_t e4m3_rn(float v) {
     return static_cast<uint8_t>(sign | (kept - (120u << 3)));
 }
 
+// x / s for s > 0, rounded to nearest even, given r = RN(1/s): q = RN(x·r) is within an ulp of
+// x / s, the remainder x − q·s is exact on the FMA, and one correction q + rem·r rounds to
+// RN(x / s) (Markstein's theorem; quotients that underflow excepted, which every caller here maps
+// to code 0 anyway). The sign is x's, as a true division's is (the correction turns −0 into +0).
+// Held against IEEE division by the GPU tests.
+__device__ __forceinline__ float div_rn(float x, float s, float r) {
+    const float q = x * r;
+    const float rem = __builtin_fmaf(-q, s, x);
+    return __builtin_copysignf(__builtin_fmaf(rem, r, q), x);
+}
+
+// Four float32 values (each within ±448) -> four OCP E4M3 bytes, first in the low byte, on
+// gfx950's v_cvt_pk_fp8_f32 (round to nearest even: bit-identical to `e4m3_rn` there, checked
+// exhaustively near every rounding boundary by the GPU tests).
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
+}
+
 // E4M3FN byte -> float32 (exact).
 __device__ __forceinline__ float e4m3_value(uint32_t b) {
     const uint32_t sign = (b & 0x80u) << 24;

@@ -41,6 +41,8 @@ hipError_t svdq_int4_gemm(const uint8_t* act, const uint16_t* ascales, const uin
 }  // namespace cozyq
 
 namespace cozyq {
+hipError_t div_probe(const float* x, const float* s, float* out, int64_t n, hipStream_t st);
+hipError_t e4m3_probe(const float* in, uint8_t* out, int64_t n, hipStream_t s);
 hipError_t mfma_probe(int kind, const void* a, const void* b, const void* sa, const void* sb,
                       void* d, hipStream_t s);
 }  // namespace cozyq

@@ -41,7 +41,37 @@ __global__ void mfma_probe_kernel(int kind, const uint8_t* a, const uint8_t* b, 
     for (int i = 0; i < 16; ++i) d[16 * l + i] = r[i];
 }
 
+// Two floats a thread through gfx950's v_cvt_pk_fp8_f32 (OCP E4M3, round to nearest even): the
+// conversion the quantizers may use in place of the software encoder once it agrees bit for bit.
+__global__ void e4m3_probe_kernel(const float* in, uint8_t* out, int64_t pairs) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= pairs) return;
+    const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(in[2 * i], in[2 * i + 1], 0, false);
+    out[2 * i] = static_cast<uint8_t>(packed & 0xff);
+    out[2 * i + 1] = static_cast<uint8_t>((packed >> 8) & 0xff);
+}
+
+// div_rn against the hardware's correctly rounded division, one pair a thread.
+__global__ void div_probe_kernel(const float* x, const float* s, float* out, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    out[i] = div_rn(x[i], s[i], 1.0f / s[i]);
+}
+
 }  // namespace
+
+hipError_t div_probe(const float* x, const float* s, float* out, int64_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    div_probe_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(x, s, out, n);
+    return hipGetLastError();
+}
+
+hipError_t e4m3_probe(const float* in, uint8_t* out, int64_t n, hipStream_t s) {
+    const int64_t pairs = n / 2;
+    if (pairs == 0) return hipSuccess;
+    e4m3_probe_kernel<<<static_cast<unsigned>((pairs + 255) / 256), 256, 0, s>>>(in, out, pairs);
+    return hipGetLastError();
+}
 
 hipError_t mfma_probe(int kind, const void* a, const void* b, const void* sa, const void* sb,
                       void* d, hipStream_t s) {

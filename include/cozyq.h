@@ -138,6 +138,15 @@ int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n);
 void cozyq_host_mx_byte(const float* amax, uint8_t* out, int64_t n);
 
+/* Test entry (no reference counterpart): float32 -> E4M3 bytes through gfx950's hardware
+ * conversion (v_cvt_pk_fp8_f32), n even, to hold it against the software encoder. */
+int cozyq_probe_e4m3(int device, const float* in, uint8_t* out, int64_t n, void* stream);
+
+/* Test entry (no reference counterpart): x / s through the quantizers' reciprocal-and-correction
+ * division, to hold it against IEEE division. */
+int cozyq_probe_div(int device, const float* x, const float* s, float* out, int64_t n,
+                    void* stream);
+
 /* Test entry (no reference counterpart): one 16x16 MFMA on per-lane operands, to confirm the
  * lane layouts the GEMMs rely on. kind 0: i32_16x16x64_i8 (a, b: 64 lanes x 16 bytes);
  * 1: f32_16x16x128_f8f6f4 e4m3 (64 lanes x 32 bytes); 2: the same with E8M0 scales sa, sb

@@ -52,6 +52,69 @@ def assert_close(got: torch.Tensor, exact: torch.Tensor) -> None:
     assert worst <= 0, f"max excess {worst:.3g} (rms {rms:.3g}, max err {err.max().item():.3g})"
 
 
+# --------------------------------------------------------- hardware E4M3 conversion
+
+
+def test_hardware_e4m3_conversion_matches_torch_cast():
+    """gfx950's v_cvt_pk_fp8_f32 against torch's `.to(float8_e4m3fn)` (via the software encoder,
+    itself held to torch's cast in test_abi) on every float32 within ±448 at a stride of 61
+    patterns, every float32 in [2^-11, 2^-5] (the subnormal boundary), and every E4M3 rounding
+    midpoint ±2 ulp, both signs: the quantizers use it only if all agree."""
+    from cozyq import _lib
+
+    lib = _lib.load()
+    top = int(np.float32(448.0).view(np.uint32))
+    sweep = np.arange(0, top + 1, 61, dtype=np.uint32)
+    low = np.arange(np.float32(2.0**-11).view(np.uint32), np.float32(2.0**-5).view(np.uint32),
+                    dtype=np.uint32)  # fmt: skip
+    codes = np.arange(0, 0x7F, dtype=np.uint8)
+    vals = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy().astype(np.float64)
+    mids = ((vals[:-1] + vals[1:]) / 2).astype(np.float32).view(np.uint32).astype(np.int64)
+    near = np.clip(np.concatenate([mids + d for d in (-2, -1, 0, 1, 2)]), 0, None).astype(np.uint32)
+    bits = np.concatenate([sweep, low, near, np.array([top], np.uint32)])
+    v = bits.view(np.float32)
+    v = np.concatenate([v, -v])
+    if v.size % 2:
+        v = v[:-1]
+    want = np.zeros(v.shape, dtype=np.uint8)
+    lib.cozyq_host_e4m3(v.ctypes.data, want.ctypes.data, v.size)
+    tin = torch.from_numpy(v).to(DEV)
+    tout = torch.empty(v.size, dtype=torch.uint8, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.cozyq_probe_e4m3(0, tin.data_ptr(), tout.data_ptr(), v.size, stream) == 0
+    got = tout.cpu().numpy()
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} differ, e.g. {v[bad[:4]]} -> {got[bad[:4]]} vs {want[bad[:4]]}"
+
+
+def test_reciprocal_division_matches_ieee_division():
+    """div_rn (q = x·RN(1/s), one FMA correction) against correctly rounded float32 division on
+    100M pairs with random significands and exponents spanning ±60 binades: bit-identical
+    wherever the quotient is a normal float (an underflowing quotient only has to stay tiny:
+    every caller maps it to code 0)."""
+    from cozyq import _lib
+
+    lib = _lib.load()
+    gen = torch.Generator(device=DEV).manual_seed(17)
+    n = 100_000_000
+    mant = torch.rand(n, generator=gen, device=DEV) + 1.0
+    x = mant * torch.exp2(torch.randint(-60, 61, (n,), generator=gen, device=DEV).float())
+    x = torch.where(torch.rand(n, generator=gen, device=DEV) < 0.5, -x, x)
+    x[:1000] = 0.0
+    x[1000:2000] = -0.0  # a signed zero keeps its sign: e4m3 codes it 0x80
+    s = (torch.rand(n, generator=gen, device=DEV) + 1.0) * torch.exp2(
+        torch.randint(-60, 61, (n,), generator=gen, device=DEV).float())
+    out = torch.empty_like(x)
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.cozyq_probe_div(0, x.data_ptr(), s.data_ptr(), out.data_ptr(), n, stream) == 0
+    want = x.cpu() / s.cpu()  # IEEE float32 division on the host
+    got = out.cpu()
+    normal = want.abs() >= 2.0**-126
+    assert torch.equal(got[normal], want[normal])
+    assert (got[~normal].abs() < 2.0**-100).all()
+    assert torch.equal(torch.signbit(got), torch.signbit(want))
+
+
 # ---------------------------------------------------------------------- MFMA layouts
 
 
@@ -312,8 +375,8 @@ def test_fp8_gemm_within_tolerance(ops, shape, bias):
     assert_close(got, laws.fp8_exact(x, data, scale, b))
 
 
-@pytest.mark.parametrize("m", [1, 2, 5, 16])
-@pytest.mark.parametrize("k", [4096, 1040])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 16])
+@pytest.mark.parametrize("k", [4096, 1040, 16384, 8208])
 def test_fp8_small_linear_within_tolerance(ops, m, k):
     n = 1032
     x = activations(m, k, seed=41 + m)
