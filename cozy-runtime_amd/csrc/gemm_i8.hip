@@ -186,14 +186,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca[h][i], cb[h][j], acc[i][j], 0, 0, 0);
-        // Issue order: the 8 slot loads and 16 fragment reads spread between the 32 MFMAs, so
-        // an LDS or load queue that is full stalls one memory instruction, not the matrix core.
+        // Issue order: the step's 8 slot loads first, then one fragment read per two MFMAs.
+        // Loads spread between the MFMAs stall the wave (and its matrix core) whenever the
+        // memory queue is full; issued up front they queue while the MFMAs run (measured on
+        // MI355X: 218 -> 187 us at config 2 against the spread order).
+        __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);      // 8 buffer loads (to LDS)
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 buffer load (to LDS)
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // 2 LDS reads
+        for (int g = 0; g < 16; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
             __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
         }
     };
