@@ -6,6 +6,8 @@
 // correctly rounded float32 division (internal/int8_linear.py:427, internal/fp8_linear.py:
 // 62-63), round-half-even and the casts of `common.h`. All three are HBM-bound: one read of the
 // 16-bit rows, one write of the codes.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -61,9 +63,12 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
     }
 }
 
-__device__ __forceinline__ int8_t q8(float v, float scale) {
-    // torch.round(r / s).clamp_(-127, 127): IEEE division, half to even, clamp.
-    float r = __builtin_rintf(v / scale);
+// torch.round(v / s).clamp_(-127, 127): the correctly rounded quotient, half to even, clamp.
+// `rs` = RN(1/s) for a finite s takes the quotient on div_rn; an infinite s (a row holding an
+// infinity) divides.
+template <bool kFast>
+__device__ __forceinline__ int8_t q8(float v, float scale, float rs) {
+    float r = __builtin_rintf(kFast ? div_rn(v, scale, rs) : v / scale);
     r = fminf(fmaxf(r, -127.0f), 127.0f);
     return static_cast<int8_t>(static_cast<int>(r));
 }
@@ -151,25 +156,30 @@ __global__ __launch_bounds__(kThreads) void rotate_quantize_kernel(
     const float scale = fmaxf(amax / 127.0f, kScaleFloor);
     if (tid == 0) scales[row] = kRot == 128 ? scale * 0.08838834764831845f : scale;
     int8_t* qr = q + static_cast<int64_t>(row) * K;
+    const float rs = 1.0f / scale;
+    auto emit = [&](auto fast) {
 #pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) {
-        if (c >= chunks) break;
-        const int base = c * kChunk;
-        const int groups = min(kChunk, K - base) / kRot;
-        const int g = tid / L::kRuns, hi = tid % L::kRuns;
-        if (g >= groups) continue;
-        uint32_t packed[4];
+        for (int c = 0; c < kMaxChunks; ++c) {
+            if (c >= chunks) break;
+            const int base = c * kChunk;
+            const int groups = min(kChunk, K - base) / kRot;
+            const int g = tid / L::kRuns, hi = tid % L::kRuns;
+            if (g >= groups) continue;
+            uint32_t packed[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            uint32_t word = 0;
+            for (int i = 0; i < 4; ++i) {
+                uint32_t word = 0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                word |= (static_cast<uint32_t>(static_cast<uint8_t>(q8(out[c][4 * i + j], scale)))) << (8 * j);
-            packed[i] = word;
+                for (int j = 0; j < 4; ++j)
+                    word |= static_cast<uint32_t>(static_cast<uint8_t>(
+                                q8<decltype(fast)::value>(out[c][4 * i + j], scale, rs))) << (8 * j);
+                packed[i] = word;
+            }
+            *reinterpret_cast<uint4*>(qr + base + g * kRot + hi * 16) =
+                make_uint4(packed[0], packed[1], packed[2], packed[3]);
         }
-        *reinterpret_cast<uint4*>(qr + base + g * kRot + hi * 16) =
-            make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    }
+    };
+    if (scale < __builtin_huge_valf()) emit(std::true_type{}); else emit(std::false_type{});
 }
 
 // Per-row int8 without rotation (build lane): s = max(amax/127, 1e-12), q = clamp(rne(x/s)).
@@ -192,23 +202,29 @@ __global__ __launch_bounds__(kThreads) void rowwise_quantize_kernel(
     const float scale = fmaxf(amax / (kFp8 ? kE4m3Max : 127.0f), kScaleFloor);
     if (tid == 0) scales[row] = scale;
     uint8_t* qr = q + static_cast<int64_t>(row) * K;
-    for (int e = tid * 8; e < K; e += kThreads * 8) {
-        float v[8];
-        load8<kHalf>(xr + e, v);
-        uint32_t word[2] = {0, 0};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            uint32_t b;
+    const float rs = 1.0f / scale;
+    auto emit = [&](auto fast) {
+        constexpr bool kFast = decltype(fast)::value;
+        for (int e = tid * 8; e < K; e += kThreads * 8) {
+            float v[8];
+            load8<kHalf>(xr + e, v);
+            uint32_t word[2] = {0, 0};
             if constexpr (kFp8) {
-                const float r = fminf(fmaxf(v[i] / scale, -kE4m3Max), kE4m3Max);
-                b = e4m3_rn(r);
+                float r[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    r[i] = fminf(fmaxf(kFast ? div_rn(v[i], scale, rs) : v[i] / scale, -kE4m3Max), kE4m3Max);
+                word[0] = e4m3x4(r[0], r[1], r[2], r[3]);
+                word[1] = e4m3x4(r[4], r[5], r[6], r[7]);
             } else {
-                b = static_cast<uint8_t>(q8(v[i], scale));
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    word[i / 4] |= static_cast<uint32_t>(static_cast<uint8_t>(q8<kFast>(v[i], scale, rs))) << (8 * (i % 4));
             }
-            word[i / 4] |= b << (8 * (i % 4));
+            *reinterpret_cast<uint2*>(qr + e) = make_uint2(word[0], word[1]);
         }
-        *reinterpret_cast<uint2*>(qr + e) = make_uint2(word[0], word[1]);
-    }
+    };
+    if (scale < __builtin_huge_valf()) emit(std::true_type{}); else emit(std::false_type{});
 }
 
 // MX quantization: 4 threads per 32-element block, 8 elements each.
@@ -230,13 +246,11 @@ __global__ __launch_bounds__(kThreads) void mx_quantize_kernel(
     // x / 2^(byte-127) as x · 2^(127-byte): the same real number, rounded once either way.
     const float inv = byte >= 254 ? float_of(1u << 22) : float_of((254u - byte) << 23);
     if (i >= total8) return;
-    uint32_t word[2] = {0, 0};
+    float r[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float r = fminf(fmaxf(v[k] * inv, -kE4m3Max), kE4m3Max);
-        word[k / 4] |= static_cast<uint32_t>(e4m3_rn(r)) << (8 * (k % 4));
-    }
-    *reinterpret_cast<uint2*>(q + i * 8) = make_uint2(word[0], word[1]);
+    for (int k = 0; k < 8; ++k) r[k] = fminf(fmaxf(v[k] * inv, -kE4m3Max), kE4m3Max);
+    *reinterpret_cast<uint2*>(q + i * 8) =
+        make_uint2(e4m3x4(r[0], r[1], r[2], r[3]), e4m3x4(r[4], r[5], r[6], r[7]));
     if ((i & 3) == 0) scales[i >> 2] = static_cast<uint8_t>(byte);
 }
 

@@ -110,11 +110,14 @@ __global__ __launch_bounds__(kQWaves * 64) void svdq_quantize_kernel(
         amax = fmaxf(amax, __shfl_xor(amax, 32));
         const _Float16 s16 = static_cast<_Float16>(amax / kLevels);
         const float s = static_cast<float>(s16);
+        // A zero scale gives code 0 (the law's `where`), and so does an infinite one (v / inf).
+        const bool coded = s != 0.0f && s < __builtin_huge_valf();
+        const float rs = 1.0f / s;
         uint32_t packed[2] = {0u, 0u};
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             float c = 0.0f;
-            if (s != 0.0f) c = fminf(fmaxf(__builtin_rintf(v[i] / s), -8.0f), 7.0f);
+            if (coded) c = fminf(fmaxf(__builtin_rintf(div_rn(v[i], s, rs)), -8.0f), 7.0f);
             const uint32_t nib = static_cast<uint32_t>(static_cast<int>(c)) & 0xfu;
             packed[i >> 3] |= nib << (4 * (i & 7));
         }
