@@ -144,10 +144,21 @@ def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -
     xp, op = x.data_ptr(), out.data_ptr()
     turn = [0]
 
+    # Up to 4 rows: one fused launch. More: quantize once, then the (narrow-tile) GEMM, the path
+    # `Prebuilt.fp8_linear` takes.
+    q = torch.empty(m, k, dtype=torch.uint8, device="cuda")
+    qs = torch.empty(m, dtype=torch.float32, device="cuda")
+
     def launch(raw_stream):
         wp, sp = ptrs[turn[0] % copies]
         turn[0] += 1
-        _check(lib.cozyq_fp8_linear(0, xp, 0, wp, sp, None, op, 0, m, n, k, raw_stream))
+        if m <= 4:
+            _check(lib.cozyq_fp8_linear(0, xp, 0, wp, sp, None, op, 0, m, n, k, raw_stream))
+            return
+        _check(lib.cozyq_quantize(0, 1, xp, 0, q.data_ptr(), qs.data_ptr(), m, k, None, None, 0,
+                                  0, 1, 0, 0.0, 0, None, raw_stream))  # fmt: skip
+        _check(lib.cozyq_gemm(0, 0, 1, q.data_ptr(), qs.data_ptr(), wp, sp, None, op, n, 0, m, n,
+                              k, -1, None, None, raw_stream))  # fmt: skip
 
     eager_ms = Timer(torch).run(lambda: launch(stream), max(steps, 64), max(warmup, 8))
 
@@ -180,8 +191,9 @@ def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -
     return {"M": m, "K": k, "N": n, "us": ms * 1e3, "us_eager": eager_ms * 1e3, "bytes": nbytes,
             "gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
             "traffic": TRAFFIC_DECODE["read"] + TRAFFIC_DECODE["write"], "weight_copies": copies,
-            "timing": "HIP graph of 64 launches, replayed", "kernel": "fp8_decode_kernel (M<=4) / "
-            "fp8_small_kernel (M<=16): quantize fused with the GEMV"}
+            "timing": "HIP graph of 64 launches, replayed",
+            "kernel": "fp8_decode_kernel (quantize fused with the GEMV)" if m <= 4 else
+                      "rowwise_quantize_kernel<fp8> + fp8_narrow_kernel"}
 
 
 def bench_fp8(torch, ops, lib, stream, m: int, steps: int) -> dict:

@@ -32,7 +32,7 @@ OPERANDS = {INT8_CONVROT: INT8_CONVROT, ROWWISE_FP8: ROWWISE_FP8}
 _NATIVE_OPS: dict[str, Any] = {INT8_CONVROT: int8_linear, ROWWISE_FP8: fp8_linear}
 #: Rows a leaf sends to its op's one-launch linear instead of a shared operand: the int8 GEMV
 #: rows (the reference's `few`), and for fp8 the fused quantize + GEMV kernel's.
-_FEW_ROWS = {INT8_CONVROT: int8_linear.GEMV_ROWS, ROWWISE_FP8: 16}
+_FEW_ROWS = {INT8_CONVROT: int8_linear.GEMV_ROWS, ROWWISE_FP8: 4}
 #: The card rows (the reference keys them by CUDA capability, `arch.py:51-64`): the
 #: tensor-core formats each multiplies in.
 ARCH_ROWS = {"gfx950": frozenset({"int8", "fp8", "mxfp8", "int4"})}

@@ -24,8 +24,9 @@ Dtype = Any
 FAMILIES = ("mfma.cdna4",)
 #: How many checked weights `Prebuilt` remembers (`internal/prebuilt.py:75`).
 CHECKED = 4096
-#: Rows the fused fp8 linear takes in one launch (`cozyq_fp8_linear`).
-FP8_SMALL_ROWS = 16
+#: Rows the fused fp8 linear takes in one launch (`cozyq_fp8_linear`); more rows quantize once
+#: and run the GEMM.
+FP8_SMALL_ROWS = 4
 #: The svdq low-rank ranks the kernels take.
 RANKS = (16, 32, 64)
 #: int4 SVDQuant K-group.

@@ -252,6 +252,8 @@ hipError_t dispatch(const void* q, const float* xs, const void* w, const float* 
 hipError_t gemm_fp8(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                     const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
                     int epilogue, hipStream_t s) {
+    if (M <= 256)  // few rows: narrow tiles keep ~224 workgroups on the weight stream
+        return gemm_fp8_narrow(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
     return dispatch<kFp8>(q, xs, w, ws, nullptr, nullptr, bias, out, ldo, out_half, M, N, K,
                           epilogue, s);
 }

@@ -26,6 +26,10 @@ hipError_t gemm_mx(const uint8_t* q, const uint8_t* qe, const uint8_t* w, const 
 hipError_t gemm_int8_acc(const int8_t* q, const int8_t* w, int32_t* acc, int M, int N, int K,
                          hipStream_t s);
 
+hipError_t gemm_fp8_narrow(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
+                           const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
+                           int K, int epilogue, hipStream_t s);
+
 hipError_t fp8_linear_small(const void* x, bool x_half, const uint8_t* w, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
                             hipStream_t s);

@@ -361,8 +361,10 @@ def test_fp8_quantize_bit_exact(ops, shape, dtype):
 
 
 @pytest.mark.parametrize("bias", [False, True])
-@pytest.mark.parametrize("shape", [(300, 512, 1024), (257, 264, 4096), (64, 1024, 2064)],
-                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("shape", [(300, 512, 1024), (257, 264, 4096), (64, 1024, 2064),
+                                   (1, 8, 128), (16, 136, 4096), (33, 200, 1040), (100, 520, 1040),
+                                   (129, 264, 4096), (256, 2048, 4096)],
+                         ids=lambda s: "x".join(map(str, s)))  # fmt: skip
 def test_fp8_gemm_within_tolerance(ops, shape, bias):
     m, n, k = shape
     x = activations(m, k, seed=31 + m)
