@@ -306,6 +306,8 @@ hipError_t launch(const int8_t* q, const float* xs, const int8_t* w, const float
 hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                      const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
                      int epilogue, hipStream_t s) {
+    if (M <= 256)  // few rows: narrow tiles keep ~224 workgroups on the weight stream
+        return gemm_int8_narrow(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
     const bool b = bias != nullptr;
 #define COZYQ_CASE(H, B, E) \
     if (out_half == H && b == B && epilogue == E) return launch<H, B, E>(q, xs, w, ws, bias, out, nullptr, ldo, M, N, K, s);

@@ -1,14 +1,17 @@
-// The fp8 rowwise GEMM for few rows (M <= 256) on gfx950: the same product and epilogue as
-// gemm.hip's (out = (acc·xs[m])·ws[n] (+ bias), float32 accumulation on
-// v_mfma_f32_16x16x128_f8f6f4), tiled kTM x kTN so that a few rows still spread over ~224
-// workgroups: the weight stream, not the matrix core, bounds these shapes (at M = 256 the
-// 58.7 MB weight is 7.3 us of HBM against 6 us of MFMA).
+// The int8 and fp8 rowwise GEMMs for few rows (M <= 256) on gfx950, with the epilogues of the
+// big kernels: int8 on v_mfma_i32_16x16x64_i8 (exact int32; the CPU law's (acc·xs)·ws, cast,
+// then + bias in the output dtype, internal/int8_linear.py:445-448 and :276), fp8 on
+// v_mfma_f32_16x16x128_f8f6f4 ((acc·xs)·ws + bias in float32, one cast). Tiles of kTM x kTN
+// keep a few rows spread over ~224 workgroups: the weight stream, not the matrix core, bounds
+// these shapes (at M = 256 the 58.7 MB fp8 weight is 7.3 us of HBM against 6 us of MFMA).
 //
 // A workgroup of 4 waves (2 x 2) owns a kTM x kTN tile; K advances 128 bytes a step through a
 // double-buffered LDS stage filled from registers. Every global read is a buffer load bounded by
 // the matrix (rows past M or N and bytes past K read as zeros), so no launch shape can read
 // outside the operands. MFMA A is the W tile, B the X tile: each lane's four results are four
 // consecutive output columns of one row.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -35,8 +38,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_from(const uint8_t* base,
                                              0, bytes, 0x00020000);
 }
 
-template <int kTM, int kTN, bool kOutHalf, bool kBias, int kEpi>
-__global__ __launch_bounds__(kThreads) void fp8_narrow_kernel(
+template <bool kInt8, int kTM, int kTN, bool kOutHalf, bool kBias, int kEpi>
+__global__ __launch_bounds__(kThreads) void narrow_kernel(
     const uint8_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ xs,
     const float* __restrict__ ws, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
     int64_t ldo, int M, int N, int K, int tiles_m) {
@@ -88,11 +91,12 @@ __global__ __launch_bounds__(kThreads) void fp8_narrow_kernel(
         }
     };
 
-    f32x4 acc[kBI][kBJ];
+    typedef std::conditional_t<kInt8, i32x4, f32x4> Acc;
+    Acc acc[kBI][kBJ];
 #pragma unroll
     for (int i = 0; i < kBI; ++i)
 #pragma unroll
-        for (int j = 0; j < kBJ; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < kBJ; ++j) acc[i][j] = Acc{0, 0, 0, 0};
 
     load(0);
     store(0);
@@ -102,6 +106,27 @@ __global__ __launch_bounds__(kThreads) void fp8_narrow_kernel(
     const int fr = lane & 15, fq = lane >> 4;
     for (int ks = 0; ks < nk; ++ks) {
         const int cur = ks & 1;
+        if constexpr (kInt8) {
+            // 16x16x64: lane group fq supplies 16-byte chunk fq of each 64-byte K half h.
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                i32x4 a[kBI], b[kBJ];
+#pragma unroll
+                for (int i = 0; i < kBI; ++i) {
+                    const int r = wn * (kTN / 2) + i * 16 + fr;
+                    a[i] = *reinterpret_cast<const i32x4*>(&lw[cur][r * kStep + swz(r, 4 * h + fq) * 16]);
+                }
+#pragma unroll
+                for (int j = 0; j < kBJ; ++j) {
+                    const int r = wm * (kTM / 2) + j * 16 + fr;
+                    b[j] = *reinterpret_cast<const i32x4*>(&lx[cur][r * kStep + swz(r, 4 * h + fq) * 16]);
+                }
+#pragma unroll
+                for (int i = 0; i < kBI; ++i)
+#pragma unroll
+                    for (int j = 0; j < kBJ; ++j) acc[i][j] = mfma_i8(a[i], b[j], acc[i][j]);
+            }
+        } else {
         // Lane group fq reads chunks fq and fq + 4 (the f8f6f4 K layout, `common.h`).
         i32x8 a[kBI], b[kBJ];
 #pragma unroll
@@ -124,6 +149,7 @@ __global__ __launch_bounds__(kThreads) void fp8_narrow_kernel(
         for (int i = 0; i < kBI; ++i)
 #pragma unroll
             for (int j = 0; j < kBJ; ++j) acc[i][j] = mfma_f8(a[i], b[j], acc[i][j]);
+        }
         if (ks + 1 < nk) {
             store(cur ^ 1);
             if (ks + 2 < nk) load(ks + 2);
@@ -131,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void fp8_narrow_kernel(
         __syncthreads();
     }
 
-    // Epilogue (internal/fp8_linear.py:97-111's scaling, the bias in float32, one cast).
+    // Epilogue: the lane's four consecutive columns of one row, an 8-byte store.
 #pragma unroll
     for (int j = 0; j < kBJ; ++j) {
         const int m = m0 + wm * (kTM / 2) + j * 16 + fr;
@@ -144,9 +170,16 @@ __global__ __launch_bounds__(kThreads) void fp8_narrow_kernel(
             uint16_t o[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float v = __fmul_rn(__fmul_rn(acc[i][j][r], xsm), ws[n + r]);
-                if constexpr (kBias) v = __fadd_rn(v, widen<kOutHalf>(bias[n + r]));
-                o[r] = narrow<kOutHalf>(v);
+                if constexpr (kInt8) {
+                    // Each step rounded on its own, no fused multiply-add.
+                    const float v = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][r]), xsm), ws[n + r]);
+                    o[r] = narrow<kOutHalf>(v);
+                    if constexpr (kBias) o[r] = narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(o[r]), widen<kOutHalf>(bias[n + r])));
+                } else {
+                    float v = __fmul_rn(__fmul_rn(acc[i][j][r], xsm), ws[n + r]);
+                    if constexpr (kBias) v = __fadd_rn(v, widen<kOutHalf>(bias[n + r]));
+                    o[r] = narrow<kOutHalf>(v);
+                }
                 if constexpr (kEpi == 1) o[r] = narrow<kOutHalf>(gelu_tanh(widen<kOutHalf>(o[r])));
             }
             *reinterpret_cast<uint2*>(out + static_cast<int64_t>(m) * ldo + n) =
@@ -155,23 +188,23 @@ __global__ __launch_bounds__(kThreads) void fp8_narrow_kernel(
     }
 }
 
-template <int kTM, int kTN, bool kOutHalf, bool kBias, int kEpi>
+template <bool kInt8, int kTM, int kTN, bool kOutHalf, bool kBias, int kEpi>
 hipError_t launch(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                   const void* bias, void* out, int64_t ldo, int M, int N, int K, hipStream_t s) {
     const int tiles_m = (M + kTM - 1) / kTM, tiles_n = (N + kTN - 1) / kTN;
-    fp8_narrow_kernel<kTM, kTN, kOutHalf, kBias, kEpi><<<tiles_m * tiles_n, kThreads, 0, s>>>(
+    narrow_kernel<kInt8, kTM, kTN, kOutHalf, kBias, kEpi><<<tiles_m * tiles_n, kThreads, 0, s>>>(
         q, w, xs, ws, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, M, N,
         K, tiles_m);
     return hipGetLastError();
 }
 
-template <int kTM, int kTN>
+template <bool kInt8, int kTM, int kTN>
 hipError_t shaped(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                   const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
                   int epilogue, hipStream_t s) {
     const bool b = bias != nullptr;
 #define COZYQ_CASE(H, B, E) \
-    if (out_half == H && b == B && epilogue == E) return launch<kTM, kTN, H, B, E>(q, xs, w, ws, bias, out, ldo, M, N, K, s);
+    if (out_half == H && b == B && epilogue == E) return launch<kInt8, kTM, kTN, H, B, E>(q, xs, w, ws, bias, out, ldo, M, N, K, s);
     COZYQ_CASE(false, false, 0)
     COZYQ_CASE(false, true, 0)
     COZYQ_CASE(true, false, 0)
@@ -184,16 +217,30 @@ hipError_t shaped(const uint8_t* q, const float* xs, const uint8_t* w, const flo
     return hipErrorInvalidValue;
 }
 
+template <bool kInt8>
+hipError_t narrow(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
+                  const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
+                  int epilogue, hipStream_t s) {
+    if (M <= 32) return shaped<kInt8, 32, 64>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
+    if (M <= 64) return shaped<kInt8, 64, 64>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
+    if (M <= 128) return shaped<kInt8, 128, 64>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
+    if (M <= 256) return shaped<kInt8, 128, 128>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
+    return hipErrorNotSupported;
+}
+
 }  // namespace
 
 hipError_t gemm_fp8_narrow(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                            const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
                            int K, int epilogue, hipStream_t s) {
-    if (M <= 32) return shaped<32, 64>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
-    if (M <= 64) return shaped<64, 64>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
-    if (M <= 128) return shaped<128, 64>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
-    if (M <= 256) return shaped<128, 128>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
-    return hipErrorNotSupported;
+    return narrow<false>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
+}
+
+hipError_t gemm_int8_narrow(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
+                            const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
+                            int K, int epilogue, hipStream_t s) {
+    return narrow<true>(reinterpret_cast<const uint8_t*>(q), xs, reinterpret_cast<const uint8_t*>(w),
+                        ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
 }
 
 }  // namespace cozyq

@@ -30,6 +30,10 @@ hipError_t gemm_fp8_narrow(const uint8_t* q, const float* xs, const uint8_t* w, 
                            const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
                            int K, int epilogue, hipStream_t s);
 
+hipError_t gemm_int8_narrow(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
+                            const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
+                            int K, int epilogue, hipStream_t s);
+
 hipError_t fp8_linear_small(const void* x, bool x_half, const uint8_t* w, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
                             hipStream_t s);

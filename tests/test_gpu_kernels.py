@@ -291,8 +291,10 @@ def test_int8_accumulators_bit_exact(ops, shape):
 
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shape", [(3, 512, 1024), (300, 512, 1024), (257, 264, 768)],
-                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("shape", [(3, 512, 1024), (300, 512, 1024), (257, 264, 768),
+                                   (1, 1032, 4096), (16, 136, 256), (64, 520, 1024),
+                                   (129, 264, 768), (256, 2048, 512)],
+                         ids=lambda s: "x".join(map(str, s)))  # fmt: skip
 def test_int8_linear_bit_exact(ops, shape, dtype, bias):
     """The whole int8.convrot linear (quantize + GEMM + epilogue) equals the CPU law bit for bit,
     with the probe's recipe (`internal/prebuilt.py:616-623`): random int8 data, scales ~1e-3."""
@@ -324,6 +326,19 @@ def test_int8_gemm_rotation_lanes_and_gelu(ops, rotation):
     ref = x.double() @ w.double().t() + bias.double()
     rel = (plain.cpu().double() - ref).norm() / ref.norm()
     assert rel < 0.05
+
+
+@pytest.mark.parametrize("m", [5, 40, 100])
+def test_int8_narrow_ragged_k_bit_exact(ops, m):
+    """Few rows (the narrow tiles) with K = 1040, a last 128-byte step only partly inside the
+    rows: the rotation-free lane, bit-exact to the CPU law."""
+    n, k = 264, 1040
+    x = activations(m, k, seed=71 + m)
+    data, scale = laws.int8_weight_rowwise(weights(n, k, seed=72))
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(73)) * 0.1).to(torch.bfloat16)
+    q, s = ops.int8_quantize_rot(x.to(DEV), 0)
+    got = ops.int8_gemm_ex(q, s, data.to(DEV), scale.to(DEV), bias.to(DEV), torch.bfloat16, 0)
+    assert torch.equal(got.cpu(), laws.int8_linear(x, data, scale, bias, torch.bfloat16, 0))
 
 
 def test_int8_output_into_wider_rows(ops):
