@@ -38,7 +38,7 @@ PEAK_HBM_GBS = 8000.0
 #: summarized in profiles/hbm_traffic_pmc.txt. The config-2 GEMM reads X and W ~4.5x: each of
 #: the 8 XCDs' L2s fetches the K-slices its own tiles use.
 TRAFFIC_C2_GEMM = {"read": 227.43e6, "write": 100.66e6}
-TRAFFIC_DECODE = {"read": 59.15e6, "write": 0.03e6}
+TRAFFIC_DECODE = {"read": 59.07e6, "write": 0.06e6}
 
 
 def _seeded(torch, seed: int):
@@ -327,6 +327,11 @@ def only(torch, ops, lib, stream, args) -> int:
         figures = bench_c2(torch, ops, lib, stream, args.steps, args.warmup)
     elif args.only == "decode":
         figures = bench_decode(torch, ops, lib, stream, args.steps, args.warmup)
+    elif args.only == "fp8":
+        figures = {"c3_fp8": [bench_fp8(torch, ops, lib, stream, m, args.steps) for m in (256, 4096)],
+                   "c3_fp8_small": bench_decode(torch, ops, lib, stream, args.steps, args.warmup, m=16)}
+    elif args.only == "mx":
+        figures = bench_mx(torch, ops, lib, stream, args.steps)
     else:
         figures = bench_svdq(torch, ops, lib, stream, args.steps)
     print(json.dumps({"only": args.only, **figures}))
@@ -340,7 +345,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
-    parser.add_argument("--only", choices=("c2", "decode", "svdq", "copy"),
+    parser.add_argument("--only", choices=("c2", "decode", "fp8", "svdq", "mx", "copy"),
                         help="profiling aid: run one leg (or a plain 256 MiB device copy, the "
                              "counter calibration) --steps times and print its figures only")  # fmt: skip
     args = parser.parse_args()

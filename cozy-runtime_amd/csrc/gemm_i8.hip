@@ -1,16 +1,18 @@
 // The W8A8 int8 GEMM on gfx950: out = epilogue(q · wᵀ), q [M, K] and w [N, K] int8, exact int32
 // accumulation on v_mfma_i32_32x32x32_i8 (from one wave per SIMD it sustains 82% of the int8
-// peak where the 16x16x64 form sustains 53%, measured on MI355X).
+// peak on low-entropy operands and 66% on random ones, where the 16x16x64 form sustains 53%,
+// measured on MI355X).
 //
 // A workgroup of 4 waves owns a 256x256 output tile; each wave a 128x128 quadrant as 4x4 MFMA
-// blocks of 32x32 (256 accumulator registers a lane, held in AGPRs). K advances 64 bytes a step through a
-// ring of 4 LDS slots (32 KB each: the X and W tiles' 256 rows x 64 bytes), filled by
-// buffer_load_dwordx4 ... lds straight from HBM/L2 — no staging registers, and rows past M or N
-// and columns past K read as zeros through the buffer's bounds. A slot is refilled three steps
-// before it is read, one barrier a step; each step's MFMAs run on fragments read from LDS during
-// the previous step. Tiles are ordered so that each XCD (workgroups b ≡ x mod 8) works through a
-// contiguous run of tiles, 4 M-tiles by 8 N-tiles at a time, which share their X and W K-slices
-// in that XCD's L2.
+// blocks of 32x32 (256 accumulator registers a lane, held in AGPRs). A step's MFMAs consume 64
+// bytes of K; the LDS holds two buffers of 128 bytes of K (64 KB each: the X and W tiles' 256 rows
+// x 128 bytes), so every load moves whole 128-byte cache lines (half-line loads measured 36%
+// slower through L2 on MI355X). Buffers are filled by buffer_load_dwordx4 ... lds straight from
+// HBM/L2 — no staging registers, and rows past M or N and columns past K read as zeros through
+// the buffer's bounds. A buffer is refilled two steps before it is read, one barrier every two
+// steps; each step's MFMAs run on fragments read from LDS during the previous step. Tiles are
+// ordered so that each XCD (workgroups b ≡ x mod 8) works through a contiguous run of tiles, 4
+// M-tiles by 8 N-tiles at a time, which share their X and W K-slices in that XCD's L2.
 #include "common.h"
 #include "kernels.h"
 
@@ -18,18 +20,17 @@ namespace cozyq {
 namespace {
 
 constexpr int kTile = 256;
-constexpr int kSlotK = 64;                     // K bytes per slot
-constexpr int kSlots = 4;
+constexpr int kPairK = 128;                    // K bytes a buffer holds: two steps, whole lines
 constexpr int kThreads = 256;
-constexpr int kOpBytes = kTile * kSlotK;       // one operand's slot: 16 KB
-constexpr int kSlotBytes = 2 * kOpBytes;       // X then W
-constexpr int kLoadsPerSlot = 8;               // buffer loads a lane issues per slot
+constexpr int kOpBytes = kTile * kPairK;       // one operand's buffer: 32 KB
+constexpr int kPairBytes = 2 * kOpBytes;       // X then W
+constexpr int kLoadsPerPair = 16;              // buffer loads a lane issues per buffer
 constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer offset past num_records reads zeros
 constexpr int kGroupM = 4;                     // M-tiles a tile group spans
 
 constexpr int kStageRow = 128 * 2 + 16;         // one staged output row: 128 bf16 + pad
 constexpr int kStageBytes = 128 * kStageRow;    // one wave's staged quadrant
-constexpr int kLdsBytes = 4 * kStageBytes > kSlots * kSlotBytes ? 4 * kStageBytes : kSlots * kSlotBytes;
+constexpr int kLdsBytes = 4 * kStageBytes > 2 * kPairBytes ? 4 * kStageBytes : 2 * kPairBytes;
 
 typedef __attribute__((address_space(3))) void LdsPtr;
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
@@ -48,24 +49,55 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
     __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));
 }
 
-// 16-byte chunk `c` (0..3) of LDS row `r` sits at chunk c ^ ((r/2) % 4): any 8 consecutive rows
-// read at one chunk land on 8 distinct 16-byte bank groups of a 128-byte LDS cycle (measured
-// conflict-free on gfx950 with SQ_LDS_BANK_CONFLICT).
-__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 3); }
+// 16-byte chunk `c` (0..7) of a 128-byte LDS row `r` sits at chunk c ^ ((r/2) % 8): the 16 rows
+// a ds_read_b128 serves together, read at one logical chunk, land on 16 distinct 16-byte bank
+// groups of 256 bytes.
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
 
+// tanh-GELU, 0.5·y·(1 + tanh(u)) with u = 0.79788456·(y + 0.044715·y³), as y / (1 + e^(-2u)):
+// e^(-2u) = 2^(y·(c1 + c2·y²)) with c1 = -2·log2(e)·0.79788456 and c2 = 0.044715·c1.
 __device__ __forceinline__ float gelu_tanh(float y) {
-    // 0.5·y·(1 + tanh(u)) = y / (1 + e^(-2u)), u = 0.79788456·(y + 0.044715·y³); e^t as 2^(t·log2 e)
-    const float u = 0.79788456f * (y + 0.044715f * y * y * y);
-    return y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * u));
+    const float t = __builtin_fmaf(-0.10294324f, y * y, -2.3022082f);
+    return y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y * t));
+}
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two float32 values rounded to the output dtype (round to nearest even), packed low then high:
+// bf16 pairs in one v_cvt_pk_bf16_f32, fp16 one by one through the fenced conversion.
+template <bool kOutHalf>
+__device__ __forceinline__ uint32_t round2(float a, float b) {
+    if constexpr (kOutHalf) {
+        return narrow<true>(a) | (static_cast<uint32_t>(narrow<true>(b)) << 16);
+    } else {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+    }
 }
 
 template <bool kOutHalf>
-__device__ __forceinline__ uint16_t round_out(float v) {
-    if constexpr (kOutHalf) {
-        return narrow<true>(v);
-    } else {
-        return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));  // v_cvt_pk_bf16_f32: RNE
-    }
+__device__ __forceinline__ float low_of(uint32_t p) {
+    if constexpr (kOutHalf) return widen<true>(static_cast<uint16_t>(p & 0xffff));
+    return float_of(p << 16);
+}
+
+template <bool kOutHalf>
+__device__ __forceinline__ float high_of(uint32_t p) {
+    if constexpr (kOutHalf) return widen<true>(static_cast<uint16_t>(p >> 16));
+    return float_of(p & 0xffff0000u);
+}
+
+// Two dequantized float32 values through the rest of the law: one rounding to the output
+// dtype, + bias in that dtype (internal/int8_linear.py:276), then optionally tanh-GELU.
+template <bool kOutHalf, bool kBias, int kEpi>
+__device__ __forceinline__ uint32_t finish2(float a, float b, uint32_t bias2) {
+    uint32_t p = round2<kOutHalf>(a, b);
+    if constexpr (kBias)
+        p = round2<kOutHalf>(__fadd_rn(low_of<kOutHalf>(p), low_of<kOutHalf>(bias2)),
+                             __fadd_rn(high_of<kOutHalf>(p), high_of<kOutHalf>(bias2)));
+    if constexpr (kEpi == 1)
+        p = round2<kOutHalf>(gelu_tanh(low_of<kOutHalf>(p)), gelu_tanh(high_of<kOutHalf>(p)));
+    return p;
 }
 
 // kEpi: 0 the CPU law's dequantization (+ bias in the output dtype), 1 that then tanh-GELU,
@@ -105,47 +137,53 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int8_t*>(W + static_cast<int64_t>(n0) * K), 0, wbytes, 0x00020000);
 
-    // Load j (0..3) of a wave fills LDS rows [(4j + wave)·16, +16) of an operand's slot: lane l
-    // writes row +l/4, physical chunk l%4, so it reads that row's logical chunk (l%4) ^ swz.
-    int rowoff[4], chunk[4];
+    // Load j (0..7) of a wave fills LDS rows [(4j + wave)·8, +8) of an operand's buffer: lane l
+    // writes row +l/8, physical chunk l%8 (whole 128-byte lines, 8 lanes a row), so it reads that
+    // row's logical chunk (l%8) ^ swz.
+    int rowoff[8], chunk[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = (4 * j + wave) * 16 + (lane >> 2);
-        chunk[j] = 16 * swz(r, lane & 3);
+    for (int j = 0; j < 8; ++j) {
+        const int r = (4 * j + wave) * 8 + (lane >> 3);
+        chunk[j] = 16 * swz(r, lane & 7);
         rowoff[j] = r * K + chunk[j];
     }
-#define COZYQ_ISSUE(step)                                                                            \
+#define COZYQ_ISSUE(pair)                                                                            \
     do {                                                                                             \
-        uint8_t* slot_ = lds + ((step) & (kSlots - 1)) * kSlotBytes;                                                \
-        const int k0_ = (step) * kSlotK;                                                             \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                              \
+        uint8_t* buf_ = lds + ((pair) & 1) * kPairBytes;                                             \
+        const int k0_ = (pair) * kPairK;                                                             \
+        _Pragma("unroll") for (int j = 0; j < 8; ++j) {                                              \
             const uint32_t off_ = (k0_ + chunk[j] < K) ? static_cast<uint32_t>(rowoff[j] + k0_) : kOutOfRange; \
             const int base_ = (4 * j + wave) * 1024;                                                 \
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (LdsPtr*)(slot_ + base_), 16, off_, 0, 0, 0); \
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LdsPtr*)(slot_ + kOpBytes + base_), 16, off_, 0, 0, 0); \
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (LdsPtr*)(buf_ + base_), 16, off_, 0, 0, 0); \
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LdsPtr*)(buf_ + kOpBytes + base_), 16, off_, 0, 0, 0); \
         }                                                                                            \
     } while (0)
 
     // Fragment reads (32x32x32: lane l supplies row l%32, 16-byte chunk l/32 of a 32-byte K
-    // half): A = W rows (wn half), B = X rows (wm half); two K halves a slot.
+    // half): A = W rows (wn half), B = X rows (wm half); step e (0, 1) of a buffer reads its
+    // logical chunks 4e + 2h + l/32.
     const int fr = lane & 31, fq = lane >> 5;
-    int aoff[2][4], boff[2][4];
+    int aoff[2][2][4], boff[2][2][4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int rw = wn * 128 + i * 32 + fr, rx = wm * 128 + i * 32 + fr;
-            aoff[h][i] = kOpBytes + rw * kSlotK + 16 * swz(rw, 2 * h + fq);
-            boff[h][i] = rx * kSlotK + 16 * swz(rx, 2 * h + fq);
-        }
-    auto fetch = [&](int step, i32x4 (*a)[4], i32x4 (*b)[4]) {
-        const uint8_t* slot = lds + (step & (kSlots - 1)) * kSlotBytes;
+    for (int e = 0; e < 2; ++e)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                a[h][i] = *reinterpret_cast<const i32x4*>(slot + aoff[h][i]);
-                b[h][i] = *reinterpret_cast<const i32x4*>(slot + boff[h][i]);
+                const int rw = wn * 128 + i * 32 + fr, rx = wm * 128 + i * 32 + fr;
+                aoff[e][h][i] = kOpBytes + rw * kPairK + 16 * swz(rw, 4 * e + 2 * h + fq);
+                boff[e][h][i] = rx * kPairK + 16 * swz(rx, 4 * e + 2 * h + fq);
+            }
+    // Step s reads buffer (s/2) % 2, half s % 2.
+    auto fetch = [&](int step, i32x4 (*a)[4], i32x4 (*b)[4]) {
+        const uint8_t* buf = lds + ((step >> 1) & 1) * kPairBytes;
+        const int e = step & 1;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[h][i] = *reinterpret_cast<const i32x4*>(buf + aoff[e][h][i]);
+                b[h][i] = *reinterpret_cast<const i32x4*>(buf + boff[e][h][i]);
             }
     };
 
@@ -157,28 +195,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-    const int nk = (K + kSlotK - 1) / kSlotK;
-    // Every step issues one slot's loads, also past the last step (their offsets fall outside
-    // the buffer: no traffic, zeros into a slot nothing reads), so each step is one block the
-    // scheduler can interleave and the pending-load count at a step's top is always two slots.
-#pragma unroll
-    for (int s = 0; s < kSlots; ++s) COZYQ_ISSUE(s);
+    const int np = (K + kPairK - 1) / kPairK;
+    // Buffers 0 and 1 take pairs 0 and 1; pair p + 2 is issued at the top of step 2p + 1, once
+    // every wave's reads of pair p are in registers, and must land by the top of step 2p + 3.
+    // Past the last pair the offsets fall outside the buffer: zeros into a buffer nothing reads.
+    COZYQ_ISSUE(0);
+    COZYQ_ISSUE(1);
     fence();
-    wait_vmcnt<3 * kLoadsPerSlot>();  // slot 0 complete
+    wait_vmcnt<kLoadsPerPair>();  // pair 0 complete
     __builtin_amdgcn_s_barrier();
     fence();
 
     i32x4 fa[2][2][4], fb[2][2][4];
     fetch(0, fa[0], fb[0]);
 
-    auto step_body = [&](int s, i32x4 (*ca)[4], i32x4 (*cb)[4], i32x4 (*na)[4], i32x4 (*nb)[4]) {
-        fence();
-        wait_vmcnt<2 * kLoadsPerSlot>();  // slot s+1 complete (s+2 and s+3 may be in flight)
-        wait_lgkmcnt0();                  // this wave's reads of slot s are in registers
-        __builtin_amdgcn_s_barrier();     // every wave's are: slot s may be refilled
-        fence();
-        COZYQ_ISSUE(s + kSlots);
-        fetch(s + 1, na, nb);  // past the last step: unused registers
+    auto mfmas = [&](i32x4 (*ca)[4], i32x4 (*cb)[4]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -186,23 +217,39 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca[h][i], cb[h][j], acc[i][j], 0, 0, 0);
-        // Issue order: the step's 8 slot loads first, then one fragment read per two MFMAs.
-        // Loads spread between the MFMAs stall the wave (and its matrix core) whenever the
-        // memory queue is full; issued up front they queue while the MFMAs run (measured on
-        // MI355X: 218 -> 187 us at config 2 against the spread order).
-        __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);      // 8 buffer loads (to LDS)
+    };
+    // Step 2p: the next step's fragments come from the same buffer, which has landed.
+    auto even_step = [&](int s, i32x4 (*ca)[4], i32x4 (*cb)[4], i32x4 (*na)[4], i32x4 (*nb)[4]) {
+        fetch(s + 1, na, nb);
+        mfmas(ca, cb);
 #pragma unroll
         for (int g = 0; g < 16; ++g) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
             __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
         }
     };
-    int s = 0;
-    for (; s + 1 < nk; s += 2) {
-        step_body(s, fa[0], fb[0], fa[1], fb[1]);
-        step_body(s + 1, fa[1], fb[1], fa[0], fb[0]);
+    // Step 2p + 1: pair p + 1 must have landed (the only loads in flight), every wave's reads of
+    // pair p are done, and its buffer takes pair p + 2.
+    auto odd_step = [&](int s, i32x4 (*ca)[4], i32x4 (*cb)[4], i32x4 (*na)[4], i32x4 (*nb)[4]) {
+        fence();
+        wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier();
+        fence();
+        COZYQ_ISSUE((s >> 1) + 2);
+        fetch(s + 1, na, nb);  // past the last step: unused registers
+        mfmas(ca, cb);
+        __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);     // 16 buffer loads (to LDS)
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
+        }
+    };
+    for (int s = 0; s < 2 * np; s += 2) {
+        even_step(s, fa[0], fb[0], fa[1], fb[1]);
+        odd_step(s + 1, fa[1], fb[1], fa[0], fb[0]);
     }
-    if (s < nk) step_body(s, fa[0], fb[0], fa[1], fb[1]);
 
     // Epilogue. Block (i, j): lane holds out[m][n] for m = j-block row l%32 and, per register
     // r, n = i-block column 8·(r/4) + 4·(l/32) + r%4 (MFMA rows are W rows): four runs of four
@@ -210,6 +257,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     // loaded once, ahead of the arithmetic.
     const int nl = n0 + wn * 128 + 4 * fq;  // the lane's first column
     if constexpr (kEpi == 2) {
+        wait_vmcnt<0>();  // the zero-filling loads past the last step land before the LDS is released
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int m = m0 + wm * 128 + j * 32 + fr;
@@ -236,6 +284,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
             wsv[i][g] = *reinterpret_cast<const float4*>(ws + n);
             if constexpr (kBias) bv[i][g] = *reinterpret_cast<const uint2*>(bias + n);
         }
+    float xsv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xsv[j] = xs[min(m0 + wm * 128 + j * 32 + fr, M - 1)];
     // All loads have landed and all waves are done with the ring before it becomes the staging
     // area.
     fence();
@@ -247,32 +298,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int ml = j * 32 + fr;  // row within the quadrant
-        const int m = m0 + wm * 128 + ml;
-        const float xsm = xs[min(m, M - 1)];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
+                // internal/int8_linear.py:445-448: (acc·xs)·ws, each product rounded to float32.
+                float v[4];
                 const float w4[4] = {wsv[i][g].x, wsv[i][g].y, wsv[i][g].z, wsv[i][g].w};
-                uint16_t b4[4] = {0, 0, 0, 0};
-                if constexpr (kBias) {
-                    b4[0] = bv[i][g].x & 0xffff; b4[1] = bv[i][g].x >> 16;
-                    b4[2] = bv[i][g].y & 0xffff; b4[3] = bv[i][g].y >> 16;
-                }
-                uint16_t o[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    // internal/int8_linear.py:445-448 then :276: (acc·xs)·ws rounded to float32
-                    // at each product, one cast, then + bias in the output dtype.
-                    const float v = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][4 * g + r]), xsm), w4[r]);
-                    o[r] = round_out<kOutHalf>(v);
-                    if constexpr (kBias)
-                        o[r] = round_out<kOutHalf>(__fadd_rn(widen<kOutHalf>(o[r]), widen<kOutHalf>(b4[r])));
-                    if constexpr (kEpi == 1) o[r] = round_out<kOutHalf>(gelu_tanh(widen<kOutHalf>(o[r])));
-                }
+                for (int r = 0; r < 4; ++r)
+                    v[r] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][4 * g + r]), xsv[j]), w4[r]);
+                const uint2 b2 = kBias ? bv[i][g] : make_uint2(0, 0);
                 const int col = i * 32 + 8 * g + 4 * fq;  // column within the quadrant
                 *reinterpret_cast<uint2*>(stage + ml * kStageRow + 2 * col) =
-                    make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16), o[2] | (static_cast<uint32_t>(o[3]) << 16));
+                    make_uint2(finish2<kOutHalf, kBias, kEpi>(v[0], v[1], b2.x),
+                               finish2<kOutHalf, kBias, kEpi>(v[2], v[3], b2.y));
             }
     }
     wait_lgkmcnt0();  // a wave reads back only its own quadrant
