@@ -12,6 +12,7 @@ typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kMaxK = 32768;
@@ -143,6 +144,19 @@ __device__ __forceinline__ f32x4 mfma_f8(i32x8 a, i32x8 b, f32x4 c) {
 // The same with an E8M0 scale per lane for each operand (its 32-element K block).
 __device__ __forceinline__ f32x4 mfma_f8_scaled(i32x8 a, i32x8 b, f32x4 c, int sa, int sb) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
+}
+
+// The 32x32 form, K = 64 per call: lane l supplies row (column) l%32, lane group g = l/32
+// holds k in [16g, 16g+16) in bytes 0..15 and k in [32+16g, 32+16g+16) in bytes 16..31, and
+// the E8M0 scale of K block κ of row i is lane i + 32κ's; result register r of lane l is row
+// 8·(r/4) + 4·(l/32) + r%4 of column l%32 (measured on gfx950 by the probe tests).
+__device__ __forceinline__ f32x16 mfma_f8_32(i32x8 a, i32x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+template <int kSelA = 0, int kSelB = 0>
+__device__ __forceinline__ f32x16 mfma_f8_32_scaled(i32x8 a, i32x8 b, f32x16 c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, kSelA, sa, kSelB, sb);
 }
 
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {

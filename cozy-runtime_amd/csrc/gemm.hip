@@ -1,14 +1,25 @@
-// The fp8 GEMMs on gfx950 MFMA: e4m3 rowwise (v_mfma_f32_16x16x128_f8f6f4) and MXFP8
-// (v_mfma_scale_f32_16x16x128_f8f6f4 with the E8M0 block scales fed to the matrix core), with
-// the dequantizing epilogue fused. (The int8 GEMM is gemm_i8.hip.)
+// The 256x256-tile GEMMs on gfx950: int8 W8A8 (exact int32 accumulation on
+// v_mfma_i32_32x32x32_i8), fp8 e4m3 row-wise (v_mfma_scale_f32_32x32x64_f8f6f4, float32
+// accumulation) and MXFP8 (the same MFMA with each operand's E8M0 block scales fed to the
+// matrix core), with the dequantizing epilogue fused: out = epilogue(q · wᵀ), q [M, K] and
+// w [N, K] with K contiguous, one byte an element. (Few-row GEMMs are gemm_narrow.hip.)
 //
-// One workgroup of 4 waves computes a 256x256 output tile; each wave owns a 128x128 quadrant as
-// 8x8 MFMA blocks of 16x16 (256 accumulator registers a lane). K advances 128 bytes a step
-// through a double-buffered LDS stage (2 x 64 KB): both operands are K-contiguous rows (X is
-// [M, K], W is [N, K]), loaded 16 bytes a lane with whole 128-byte lines per row, and stored
-// with a 16-byte-chunk XOR swizzle so each MFMA fragment read is bank-conflict free.
-// The MFMA's A operand is the W tile and its B operand the X tile, so each lane's four results
-// are four consecutive output columns of one row: an 8-byte store.
+// A workgroup of 4 waves owns a 256x256 output tile; each wave a 128x128 quadrant as 4x4 MFMA
+// blocks of 32x32 (256 accumulator registers a lane, held in AGPRs). A step's MFMAs consume 64
+// bytes of K; the LDS holds two buffers of 128 bytes of K (the X and W tiles' 256 rows x 128
+// bytes, and for MX their rows' four E8M0 bytes), so every load moves whole 128-byte cache lines
+// (half-line loads measured 36% slower through L2 on MI355X). Buffers are filled by
+// buffer_load ... lds straight from HBM/L2 — no staging registers, and rows past M or N and
+// columns past K read as zeros through the buffer's bounds. A buffer is refilled two steps
+// before it is read, one barrier every two steps; each step's MFMAs run on fragments read from
+// LDS during the previous step. Tiles are ordered so that each XCD (workgroups b ≡ x mod 8)
+// works through a contiguous run of tiles, 4 M-tiles by 8 N-tiles at a time, which share their
+// X and W K-slices in that XCD's L2.
+//
+// MFMA rates from one wave per SIMD on MI355X: i8 32x32x32 82% of the int8 peak on low-entropy
+// operands and 66% on random ones (power), f8 32x32x64 87%. The MFMA's A operand is the W tile
+// and its B operand the X tile, so each lane's results are runs of four consecutive output
+// columns of one row.
 #include <type_traits>
 
 #include "common.h"
@@ -17,213 +28,433 @@
 namespace cozyq {
 namespace {
 
-constexpr int kTile = 256;        // output rows and columns per workgroup
-constexpr int kStep = 128;        // K bytes per LDS stage
-constexpr int kThreads = 256;
-constexpr int kOperand = kTile * kStep;  // bytes of one operand's stage
-
 enum Kind { kInt8 = 0, kFp8 = 1, kMx = 2 };
 
-// Physical 16-byte chunk of logical chunk `c` (0..7) in LDS row `r`: the 16 rows a fragment
-// read touches at one chunk land on 16 distinct 4-bank groups.
+constexpr int kTile = 256;
+constexpr int kPairK = 128;                    // K bytes a buffer holds: two steps, whole lines
+constexpr int kThreads = 256;
+constexpr int kOpBytes = kTile * kPairK;       // one operand's buffer: 32 KB
+constexpr int kScaleBytes = kTile * 4;         // MX: one operand's E8M0 bytes for a buffer
+constexpr int kPairBytes = 2 * kOpBytes + 2 * kScaleBytes;  // X, W, X scales, W scales
+constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer offset past num_records reads zeros
+constexpr int kGroupM = 4;                     // M-tiles a tile group spans
+
+constexpr int kStageRow = 128 * 2 + 16;         // one staged output row: 128 bf16 + pad
+constexpr int kStageBytes = 128 * kStageRow;    // one wave's staged quadrant
+constexpr int kLdsBytes = 4 * kStageBytes > 2 * kPairBytes ? 4 * kStageBytes : 2 * kPairBytes;
+
+// Buffer loads a lane issues per buffer: 8 of 16 bytes for each operand, and for MX one of 4
+// bytes for each operand's scales.
 template <int kKind>
-__device__ __forceinline__ int swz(int r, int c) {
-    return c ^ ((r >> 1) & 7);
+constexpr int kLoads = kKind == kMx ? 18 : 16;
+
+typedef __attribute__((address_space(3))) void LdsPtr;
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+
+// s_waitcnt with only vmcnt <= N (expcnt and lgkmcnt left unconstrained): gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Keeps the compiler from moving memory operations across the waits and barriers below.
+__device__ __forceinline__ void fence() { asm volatile("" ::: "memory"); }
+
+__device__ __forceinline__ void wait_lgkmcnt0() {
+    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));
+}
+
+// 16-byte chunk `c` (0..7) of a 128-byte LDS row `r` sits at chunk c ^ ((r/2) % 8): the 16 rows
+// a ds_read_b128 serves together, read at one logical chunk, land on 16 distinct 16-byte bank
+// groups of 256 bytes.
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+
+// tanh-GELU, 0.5·y·(1 + tanh(u)) with u = 0.79788456·(y + 0.044715·y³), as y / (1 + e^(-2u)):
+// e^(-2u) = 2^(y·(c1 + c2·y²)) with c1 = -2·log2(e)·0.79788456 and c2 = 0.044715·c1.
 __device__ __forceinline__ float gelu_tanh(float y) {
-    return 0.5f * y * (1.0f + tanhf(0.79788456f * (y + 0.044715f * y * y * y)));
+    const float t = __builtin_fmaf(-0.10294324f, y * y, -2.3022082f);
+    return y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y * t));
 }
 
-// kEpi: 0 plain, 1 tanh-GELU, 2 raw int32 accumulators to `acc_out` (test entry; no scales read).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two float32 values rounded to the output dtype (round to nearest even), packed low then high:
+// bf16 pairs in one v_cvt_pk_bf16_f32, fp16 one by one through the fenced conversion.
+template <bool kOutHalf>
+__device__ __forceinline__ uint32_t round2(float a, float b) {
+    if constexpr (kOutHalf) {
+        return narrow<true>(a) | (static_cast<uint32_t>(narrow<true>(b)) << 16);
+    } else {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+    }
+}
+
+template <bool kOutHalf>
+__device__ __forceinline__ float low_of(uint32_t p) {
+    if constexpr (kOutHalf) return widen<true>(static_cast<uint16_t>(p & 0xffff));
+    return float_of(p << 16);
+}
+
+template <bool kOutHalf>
+__device__ __forceinline__ float high_of(uint32_t p) {
+    if constexpr (kOutHalf) return widen<true>(static_cast<uint16_t>(p >> 16));
+    return float_of(p & 0xffff0000u);
+}
+
+// Two dequantized float32 values through the rest of the law: one rounding to the output
+// dtype, + bias in that dtype (internal/int8_linear.py:276), then optionally tanh-GELU.
+template <bool kOutHalf, bool kBias, int kEpi>
+__device__ __forceinline__ uint32_t finish2(float a, float b, uint32_t bias2) {
+    uint32_t p = round2<kOutHalf>(a, b);
+    if constexpr (kBias)
+        p = round2<kOutHalf>(__fadd_rn(low_of<kOutHalf>(p), low_of<kOutHalf>(bias2)),
+                             __fadd_rn(high_of<kOutHalf>(p), high_of<kOutHalf>(bias2)));
+    if constexpr (kEpi == 1)
+        p = round2<kOutHalf>(gelu_tanh(low_of<kOutHalf>(p)), gelu_tanh(high_of<kOutHalf>(p)));
+    return p;
+}
+
+// Two float32 values of the fp8 / MX laws (bias already added in float32) through the rest of
+// the epilogue: one rounding to the output dtype, then optionally tanh-GELU.
+template <bool kOutHalf, int kEpi>
+__device__ __forceinline__ uint32_t finish2_float(float a, float b) {
+    uint32_t p = round2<kOutHalf>(a, b);
+    if constexpr (kEpi == 1)
+        p = round2<kOutHalf>(gelu_tanh(low_of<kOutHalf>(p)), gelu_tanh(high_of<kOutHalf>(p)));
+    return p;
+}
+
+// One step's operands a lane holds: 4 W-row and 4 X-row fragments of 32 bytes (16-byte chunks
+// g and g+2 of the step's 64 bytes for lane group g = l/32: the int8 MFMA takes them as two K
+// halves, the f8f6f4 MFMA as one K = 64 operand), and for MX the E8M0 byte of each fragment's
+// K block g.
+struct Frags {
+    i32x8 a[4], b[4];
+    int sa[4], sb[4];
+};
+
+__device__ __forceinline__ i32x4 half_of(const i32x8& v, int h) {
+    return h == 0 ? __builtin_shufflevector(v, v, 0, 1, 2, 3) : __builtin_shufflevector(v, v, 4, 5, 6, 7);
+}
+
+// kEpi: 0 the law's dequantization (+ bias), 1 that then tanh-GELU, 2 the raw int32
+// accumulators (int8 test entry).
 template <int kKind, bool kOutHalf, bool kBias, int kEpi>
 __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     const uint8_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ xs,
     const float* __restrict__ ws, const uint8_t* __restrict__ xe, const uint8_t* __restrict__ we,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int32_t* __restrict__ acc_out,
-    int64_t ldo, int M, int N, int K, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][kOperand];
-    __shared__ __attribute__((aligned(16))) uint8_t sc[2][2][kTile * 4];  // MX: [row][block]
+    int64_t ldo, int M, int N, int K, int tiles_m, int tiles_n) {
+    static_assert(kEpi != 2 || kKind == kInt8, "raw accumulators are the int8 GEMM's");
+    typedef std::conditional_t<kKind == kInt8, i32x16, f32x16> Acc;
+    // The two buffers during the K loop; afterwards each wave's 128x128 output quadrant, staged
+    // for whole-row stores (rows padded to kStageRow bytes).
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA bases go in M0
     const int wm = wave >> 1, wn = wave & 1;
-    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
-    const int m0 = tm * kTile, n0 = tn * kTile;
-    const int nk = (K + kStep - 1) / kStep;
-    const int kblocks = K / 32;
 
-    // Global -> register staging: chunk tid + 256·i is row tid/8 + 32·i, 16-byte column tid%8.
-    const int col = tid & 7;
-    uint4 stage[2][8];
-    uint32_t sstage[2] = {0, 0};
-    auto load = [&](int ks) {
-        const int kb = ks * kStep + col * 16;
-        const bool live = kb < K;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = (tid >> 3) + 32 * i;
-            const int xr = min(m0 + r, M - 1), wr = min(n0 + r, N - 1);
-            stage[0][i] = live ? *reinterpret_cast<const uint4*>(X + static_cast<int64_t>(xr) * K + kb)
-                               : make_uint4(0, 0, 0, 0);
-            stage[1][i] = live ? *reinterpret_cast<const uint4*>(W + static_cast<int64_t>(wr) * K + kb)
-                               : make_uint4(0, 0, 0, 0);
-        }
-        if constexpr (kKind == kMx) {
-            // Each thread: one row's four E8M0 bytes (K blocks 4ks..4ks+3) of X and of W.
-            const int r = tid;
-            const int xr = min(m0 + r, M - 1), wr = min(n0 + r, N - 1);
-            sstage[0] = *reinterpret_cast<const uint32_t*>(xe + static_cast<int64_t>(xr) * kblocks + 4 * ks);
-            sstage[1] = *reinterpret_cast<const uint32_t*>(we + static_cast<int64_t>(wr) * kblocks + 4 * ks);
-        }
+    // Tile order: XCD-contiguous runs, then groups of kGroupM M-tiles with N fastest inside.
+    const int tiles = tiles_m * tiles_n;
+    int t = blockIdx.x;
+    if ((tiles & 7) == 0) t = (t & 7) * (tiles >> 3) + (t >> 3);
+    const int group = t / (kGroupM * tiles_n);
+    const int gm = min(kGroupM, tiles_m - group * kGroupM);
+    const int within = t - group * kGroupM * tiles_n;
+    const int tm = group * kGroupM + within % gm, tn = within / gm;
+    // The tile arithmetic divides on the vector unit; the origin is uniform, and buffer
+    // descriptors must sit in scalar registers.
+    const int m0 = __builtin_amdgcn_readfirstlane(tm * kTile);
+    const int n0 = __builtin_amdgcn_readfirstlane(tn * kTile);
+
+    // Buffer views of this tile's rows: reads past the last row return zeros.
+    auto rows_view = [&](const uint8_t* base, int rows_left, int row_bytes) {
+        const int64_t span = static_cast<int64_t>(rows_left) * row_bytes;
+        const uint32_t bytes = span > 0x7fffffff ? 0x7fffffffu : static_cast<uint32_t>(span);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, bytes, 0x00020000);
     };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = (tid >> 3) + 32 * i;
-            const int off = r * kStep + swz<kKind>(r, col) * 16;
-            *reinterpret_cast<uint4*>(&lds[buf][0][off]) = stage[0][i];
-            *reinterpret_cast<uint4*>(&lds[buf][1][off]) = stage[1][i];
-        }
-        if constexpr (kKind == kMx) {
-            *reinterpret_cast<uint32_t*>(&sc[buf][0][tid * 4]) = sstage[0];
-            *reinterpret_cast<uint32_t*>(&sc[buf][1][tid * 4]) = sstage[1];
-        }
-    };
-
-    typedef std::conditional_t<kKind == kInt8, i32x4, f32x4> Acc;
-    Acc acc[8][8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = Acc{0, 0, 0, 0};
-
-    load(0);
-    store(0);
-    if (nk > 1) load(1);
-    __syncthreads();
-
-    const int fr = lane & 15, fq = lane >> 4;
-    for (int ks = 0; ks < nk; ++ks) {
-        const int cur = ks & 1;
-        const uint8_t* la = lds[cur][1];  // W tile: MFMA A
-        const uint8_t* lb = lds[cur][0];  // X tile: MFMA B
-        if constexpr (kKind == kInt8) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                i32x4 a[8], b[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int r = wn * 128 + i * 16 + fr;
-                    a[i] = *reinterpret_cast<const i32x4*>(la + r * kStep + swz<kKind>(r, h * 4 + fq) * 16);
-                }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int r = wm * 128 + j * 16 + fr;
-                    b[j] = *reinterpret_cast<const i32x4*>(lb + r * kStep + swz<kKind>(r, h * 4 + fq) * 16);
-                }
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) acc[i][j] = mfma_i8(a[i], b[j], acc[i][j]);
-            }
-        } else {
-            i32x8 a[8], b[8];
-            int sa[8], sb[8];
-            // Lane group fq takes chunks fq and fq+4 (the f8f6f4 K layout, `common.h`), so MX
-            // block fq of this step is the one its E8M0 byte scales.
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int r = wn * 128 + i * 16 + fr;
-                const uint8_t* row = la + r * kStep;
-                const i32x4 lo = *reinterpret_cast<const i32x4*>(row + swz<kKind>(r, fq) * 16);
-                const i32x4 hi = *reinterpret_cast<const i32x4*>(row + swz<kKind>(r, fq + 4) * 16);
-                a[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                if constexpr (kKind == kMx) sa[i] = sc[cur][1][r * 4 + fq];
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int r = wm * 128 + j * 16 + fr;
-                const uint8_t* row = lb + r * kStep;
-                const i32x4 lo = *reinterpret_cast<const i32x4*>(row + swz<kKind>(r, fq) * 16);
-                const i32x4 hi = *reinterpret_cast<const i32x4*>(row + swz<kKind>(r, fq + 4) * 16);
-                b[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                if constexpr (kKind == kMx) sb[j] = sc[cur][0][r * 4 + fq];
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    if constexpr (kKind == kMx)
-                        acc[i][j] = mfma_f8_scaled(a[i], b[j], acc[i][j], sa[i], sb[j]);
-                    else
-                        acc[i][j] = mfma_f8(a[i], b[j], acc[i][j]);
-                }
-        }
-        if (ks + 1 < nk) {
-            store(cur ^ 1);
-            if (ks + 2 < nk) load(ks + 2);
-        }
-        __syncthreads();
+    const __amdgpu_buffer_rsrc_t xr = rows_view(X + static_cast<int64_t>(m0) * K, M - m0, K);
+    const __amdgpu_buffer_rsrc_t wr = rows_view(W + static_cast<int64_t>(n0) * K, N - n0, K);
+    const int kb = K / 32;  // MX: E8M0 bytes a row (K % 128 == 0)
+    __amdgpu_buffer_rsrc_t xer = xr, wer = wr;
+    if constexpr (kKind == kMx) {
+        xer = rows_view(xe + static_cast<int64_t>(m0) * kb, M - m0, kb);
+        wer = rows_view(we + static_cast<int64_t>(n0) * kb, N - n0, kb);
     }
+    const int soff = (64 * wave + lane) * kb;  // MX: the lane's scale row in the tile
 
-    // Epilogue: lane holds out[m][n..n+3] of each block.
+    // Load j (0..7) of a wave fills LDS rows [(4j + wave)·8, +8) of an operand's buffer: lane l
+    // writes row +l/8, physical chunk l%8 (whole 128-byte lines, 8 lanes a row), so it reads that
+    // row's logical chunk (l%8) ^ swz. MX scales: wave w's lane l loads the four E8M0 bytes of
+    // row 64w + l.
+    int rowoff[8], chunk[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int m = m0 + wm * 128 + j * 16 + fr;
-        if (m >= M) continue;
-        if constexpr (kEpi == 2) {
-            static_assert(kKind == kInt8, "raw accumulators are the int8 GEMM's");
+        const int r = (4 * j + wave) * 8 + (lane >> 3);
+        chunk[j] = 16 * swz(r, lane & 7);
+        rowoff[j] = r * K + chunk[j];
+    }
+#define COZYQ_ISSUE(pair)                                                                            \
+    do {                                                                                             \
+        uint8_t* buf_ = lds + ((pair) & 1) * kPairBytes;                                             \
+        const int k0_ = (pair) * kPairK;                                                             \
+        _Pragma("unroll") for (int j = 0; j < 8; ++j) {                                              \
+            const uint32_t off_ = (k0_ + chunk[j] < K) ? static_cast<uint32_t>(rowoff[j] + k0_) : kOutOfRange; \
+            const int base_ = (4 * j + wave) * 1024;                                                 \
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (LdsPtr*)(buf_ + base_), 16, off_, 0, 0, 0); \
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LdsPtr*)(buf_ + kOpBytes + base_), 16, off_, 0, 0, 0); \
+        }                                                                                            \
+        if constexpr (kKind == kMx) {                                                                \
+            const uint32_t so_ = (4 * (pair) < kb) ? static_cast<uint32_t>(soff + 4 * (pair)) : kOutOfRange; \
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xer, (LdsPtr*)(buf_ + 2 * kOpBytes + 256 * wave), 4, so_, 0, 0, 0); \
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wer, (LdsPtr*)(buf_ + 2 * kOpBytes + kScaleBytes + 256 * wave), 4, so_, 0, 0, 0); \
+        }                                                                                            \
+    } while (0)
+
+    // Fragment reads (lane l supplies row l%32; lane group l/32 its K chunks): A = W rows (wn
+    // half), B = X rows (wm half); step e (0, 1) of a buffer reads its logical chunks 4e + 2h +
+    // l/32, h = 0, 1, and (MX) byte 2e + l/32 of the row's four scale bytes.
+    const int fr = lane & 31, fq = lane >> 5;
+    int aoff[2][2][4], boff[2][2][4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int n = n0 + wn * 128 + i * 16 + 4 * fq;
-                if (n < N) *reinterpret_cast<i32x4*>(acc_out + static_cast<int64_t>(m) * N + n) = acc[i][j];
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rw = wn * 128 + i * 32 + fr, rx = wm * 128 + i * 32 + fr;
+                aoff[e][h][i] = kOpBytes + rw * kPairK + 16 * swz(rw, 4 * e + 2 * h + fq);
+                boff[e][h][i] = rx * kPairK + 16 * swz(rx, 4 * e + 2 * h + fq);
             }
-            continue;
+    // Step s reads buffer (s/2) % 2, half s % 2.
+    auto fetch = [&](int step, Frags& f) {
+        const uint8_t* buf = lds + ((step >> 1) & 1) * kPairBytes;
+        const int e = step & 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const i32x4 alo = *reinterpret_cast<const i32x4*>(buf + aoff[e][0][i]);
+            const i32x4 ahi = *reinterpret_cast<const i32x4*>(buf + aoff[e][1][i]);
+            const i32x4 blo = *reinterpret_cast<const i32x4*>(buf + boff[e][0][i]);
+            const i32x4 bhi = *reinterpret_cast<const i32x4*>(buf + boff[e][1][i]);
+            f.a[i] = __builtin_shufflevector(alo, ahi, 0, 1, 2, 3, 4, 5, 6, 7);
+            f.b[i] = __builtin_shufflevector(blo, bhi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
-        const float xsm = (kKind == kMx) ? 1.0f : xs[m];
+        if constexpr (kKind == kMx) {
+            const int shift = 8 * (2 * e + fq);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int n = n0 + wn * 128 + i * 16 + 4 * fq;
-            if (n >= N) continue;
-            float wsv[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-            uint16_t bv[4] = {0, 0, 0, 0};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {  // scalar loads: scale and bias may be any views
-                if constexpr (kKind != kMx) wsv[r] = ws[n + r];
-                if constexpr (kBias) bv[r] = bias[n + r];
+            for (int i = 0; i < 4; ++i) {
+                const int rw = wn * 128 + i * 32 + fr, rx = wm * 128 + i * 32 + fr;
+                const uint32_t sw = *reinterpret_cast<const uint32_t*>(buf + 2 * kOpBytes + kScaleBytes + 4 * rw);
+                const uint32_t sx = *reinterpret_cast<const uint32_t*>(buf + 2 * kOpBytes + 4 * rx);
+                f.sa[i] = static_cast<int>((sw >> shift) & 0xff);
+                f.sb[i] = static_cast<int>((sx >> shift) & 0xff);
             }
-            uint16_t o[4];
+        }
+    };
+
+    Acc acc[4][4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if constexpr (kKind == kInt8) {
-                    // internal/int8_linear.py:445-448 then :276: (acc·xs)·ws, cast, + bias in
-                    // the output dtype: each step rounded on its own, no fused multiply-add.
-                    const float v = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][r]), xsm), wsv[r]);
-                    o[r] = narrow<kOutHalf>(v);
-                    if constexpr (kBias) o[r] = narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(o[r]), widen<kOutHalf>(bv[r])));
-                } else {
-                    float v = __fmul_rn(__fmul_rn(acc[i][j][r], xsm), wsv[r]);
-                    if constexpr (kBias) v = __fadd_rn(v, widen<kOutHalf>(bv[r]));
-                    o[r] = narrow<kOutHalf>(v);
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    const int np = (K + kPairK - 1) / kPairK;
+    // Buffers 0 and 1 take pairs 0 and 1; pair p + 2 is issued at the top of step 2p + 1, once
+    // every wave's reads of pair p are in registers, and must land by the top of step 2p + 3.
+    // Past the last pair the offsets fall outside the buffer: zeros into a buffer nothing reads.
+    COZYQ_ISSUE(0);
+    COZYQ_ISSUE(1);
+    fence();
+    wait_vmcnt<kLoads<kKind>>();  // pair 0 complete
+    __builtin_amdgcn_s_barrier();
+    fence();
+
+    Frags f0, f1;
+    fetch(0, f0);
+
+    auto mfmas = [&](const Frags& c) {
+        if constexpr (kKind == kInt8) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(half_of(c.a[i], h), half_of(c.b[j], h), acc[i][j], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if constexpr (kKind == kMx)
+                        acc[i][j] = mfma_f8_32_scaled(c.a[i], c.b[j], acc[i][j], c.sa[i], c.sb[j]);
+                    else
+                        acc[i][j] = mfma_f8_32(c.a[i], c.b[j], acc[i][j]);
                 }
-                if constexpr (kEpi == 1) o[r] = narrow<kOutHalf>(gelu_tanh(widen<kOutHalf>(o[r])));
-            }
-            const uint2 packed = make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16),
-                                            o[2] | (static_cast<uint32_t>(o[3]) << 16));
-            *reinterpret_cast<uint2*>(out + static_cast<int64_t>(m) * ldo + n) = packed;
         }
+    };
+    // Issue order within a step: LDS reads spread one (MX: one to two) per MFMA group.
+    auto schedule = [&]() {
+        if constexpr (kKind == kInt8) {
+#pragma unroll
+            for (int g = 0; g < 16; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
+            }
+        } else if constexpr (kKind == kFp8) {
+#pragma unroll
+            for (int g = 0; g < 16; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+        }
+    };
+    // Step 2p: the next step's fragments come from the same buffer, which has landed.
+    auto even_step = [&](int s, const Frags& cur, Frags& next) {
+        fetch(s + 1, next);
+        mfmas(cur);
+        schedule();
+    };
+    // Step 2p + 1: pair p + 1 must have landed (the only loads in flight), every wave's reads of
+    // pair p are done, and its buffer takes pair p + 2.
+    auto odd_step = [&](int s, const Frags& cur, Frags& next) {
+        fence();
+        wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier();
+        fence();
+        COZYQ_ISSUE((s >> 1) + 2);
+        fetch(s + 1, next);  // past the last step: unused registers
+        mfmas(cur);
+        __builtin_amdgcn_sched_group_barrier(0x020, kLoads<kKind>, 0);  // the buffer loads first
+        schedule();
+    };
+    for (int s = 0; s < 2 * np; s += 2) {
+        even_step(s, f0, f1);
+        odd_step(s + 1, f1, f0);
+    }
+
+    // Epilogue. Block (i, j): lane holds out[m][n] for m = j-block row l%32 and, per register
+    // r, n = i-block column 8·(r/4) + 4·(l/32) + r%4 (MFMA rows are W rows): four runs of four
+    // consecutive columns, each an 8-byte store. The lane's 64 weight scales and biases are
+    // loaded once, ahead of the arithmetic.
+    const int nl = n0 + wn * 128 + 4 * fq;  // the lane's first column
+    if constexpr (kEpi == 2) {
+        wait_vmcnt<0>();  // the zero-filling loads past the last step land before the LDS is released
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = m0 + wm * 128 + j * 32 + fr;
+            if (m >= M) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int n = nl + i * 32 + 8 * g;
+                    if (n < N)
+                        *reinterpret_cast<i32x4*>(acc_out + static_cast<int64_t>(m) * N + n) =
+                            i32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                }
+        }
+        return;
+    }
+    float4 wsv[4][4];
+    uint2 bv[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int n = min(nl + i * 32 + 8 * g, N - 4);  // N % 8 == 0: a clamped run stays in bounds
+            wsv[i][g] = kKind == kMx ? make_float4(1.0f, 1.0f, 1.0f, 1.0f) : *reinterpret_cast<const float4*>(ws + n);
+            if constexpr (kBias) bv[i][g] = *reinterpret_cast<const uint2*>(bias + n);
+        }
+    float xsv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xsv[j] = kKind == kMx ? 1.0f : xs[min(m0 + wm * 128 + j * 32 + fr, M - 1)];
+    // All loads have landed and all waves are done with the buffers before they become the
+    // staging area.
+    fence();
+    wait_vmcnt<0>();
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    fence();
+    uint8_t* stage = lds + wave * kStageBytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ml = j * 32 + fr;  // row within the quadrant
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float w4[4] = {wsv[i][g].x, wsv[i][g].y, wsv[i][g].z, wsv[i][g].w};
+                const uint2 b2 = kBias ? bv[i][g] : make_uint2(0, 0);
+                uint2 packed;
+                if constexpr (kKind == kInt8) {
+                    // internal/int8_linear.py:445-448: (acc·xs)·ws, each product rounded to float32.
+                    float v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        v[r] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][4 * g + r]), xsv[j]), w4[r]);
+                    packed = make_uint2(finish2<kOutHalf, kBias, kEpi>(v[0], v[1], b2.x),
+                                        finish2<kOutHalf, kBias, kEpi>(v[2], v[3], b2.y));
+                } else {
+                    // internal/fp8_linear.py:92-111 (`_scaled_mm` with row and column scales):
+                    // (acc·xs)·ws (MX: acc, its block scales applied in the MFMA), + bias in float32.
+                    float v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        v[r] = acc[i][j][4 * g + r];
+                        if constexpr (kKind == kFp8) v[r] = __fmul_rn(__fmul_rn(v[r], xsv[j]), w4[r]);
+                    }
+                    if constexpr (kBias) {
+                        v[0] = __fadd_rn(v[0], low_of<kOutHalf>(b2.x));
+                        v[1] = __fadd_rn(v[1], high_of<kOutHalf>(b2.x));
+                        v[2] = __fadd_rn(v[2], low_of<kOutHalf>(b2.y));
+                        v[3] = __fadd_rn(v[3], high_of<kOutHalf>(b2.y));
+                    }
+                    packed = make_uint2(finish2_float<kOutHalf, kEpi>(v[0], v[1]),
+                                        finish2_float<kOutHalf, kEpi>(v[2], v[3]));
+                }
+                const int col = i * 32 + 8 * g + 4 * fq;  // column within the quadrant
+                *reinterpret_cast<uint2*>(stage + ml * kStageRow + 2 * col) = packed;
+            }
+    }
+    wait_lgkmcnt0();  // a wave reads back only its own quadrant
+    // Whole rows: 16 lanes cover one quadrant row's 256 bytes; 4 rows an instruction.
+    const int cl = (lane & 15) * 8;  // first of the lane's 8 columns
+    const int n = n0 + wn * 128 + cl;
+#pragma unroll 4
+    for (int r0 = 0; r0 < 128; r0 += 4) {
+        const int ml = r0 + (lane >> 4);
+        const int m = m0 + wm * 128 + ml;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + ml * kStageRow + 2 * cl);
+        if (m < M && n < N) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * ldo + n) = v;
     }
 }
+
+#undef COZYQ_ISSUE
 
 template <int kKind, bool kOutHalf, bool kBias, int kEpi>
 hipError_t launch(const void* q, const float* xs, const void* w, const float* ws,
                   const uint8_t* xe, const uint8_t* we, const void* bias, void* out,
-                  int32_t* acc_out, int64_t ldo, int M, int N, int K, hipStream_t s) {
+                  int32_t* acc, int64_t ldo, int M, int N, int K, hipStream_t s) {
     const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTile - 1) / kTile;
     gemm_kernel<kKind, kOutHalf, kBias, kEpi><<<tiles_m * tiles_n, kThreads, 0, s>>>(
         static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(w), xs, ws, xe, we,
-        static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), acc_out, ldo, M, N, K,
-        tiles_n);
+        static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), acc, ldo, M, N, K,
+        tiles_m, tiles_n);
     return hipGetLastError();
 }
 
@@ -239,15 +470,32 @@ hipError_t dispatch(const void* q, const float* xs, const void* w, const float* 
     COZYQ_CASE(false, true, 0)
     COZYQ_CASE(true, false, 0)
     COZYQ_CASE(true, true, 0)
-    COZYQ_CASE(false, false, 1)
-    COZYQ_CASE(false, true, 1)
-    COZYQ_CASE(true, false, 1)
-    COZYQ_CASE(true, true, 1)
+    if constexpr (kKind != kMx) {
+        COZYQ_CASE(false, false, 1)
+        COZYQ_CASE(false, true, 1)
+        COZYQ_CASE(true, false, 1)
+        COZYQ_CASE(true, true, 1)
+    }
 #undef COZYQ_CASE
     return hipErrorInvalidValue;
 }
 
 }  // namespace
+
+hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
+                     const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
+                     int epilogue, hipStream_t s) {
+    if (M <= 256)  // few rows: narrow tiles keep ~224 workgroups on the weight stream
+        return gemm_int8_narrow(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
+    return dispatch<kInt8>(q, xs, w, ws, nullptr, nullptr, bias, out, ldo, out_half, M, N, K,
+                           epilogue, s);
+}
+
+hipError_t gemm_int8_acc(const int8_t* q, const int8_t* w, int32_t* acc, int M, int N, int K,
+                         hipStream_t s) {
+    return launch<kInt8, false, false, 2>(q, nullptr, w, nullptr, nullptr, nullptr, nullptr,
+                                          nullptr, acc, N, M, N, K, s);
+}
 
 hipError_t gemm_fp8(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                     const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,

@@ -23,6 +23,11 @@ __global__ void mfma_probe_kernel(int kind, const uint8_t* a, const uint8_t* b, 
         for (int i = 0; i < 16; ++i) z[i] = 0;
         const i32x16 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, b4, z, 0, 0, 0);
         for (int i = 0; i < 16; ++i) r[i] = static_cast<uint32_t>(c[i]);
+    } else if (kind == 5 || kind == 6) {
+        f32x16 z;
+        for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+        const f32x16 c = kind == 5 ? mfma_f8_32(a8, b8, z) : mfma_f8_32_scaled(a8, b8, z, sa[l], sb[l]);
+        for (int i = 0; i < 16; ++i) r[i] = bits_of(c[i]);
     } else if (kind == 0) {
         const i32x4 c = mfma_i8(a4, b4, i32x4{0, 0, 0, 0});
         for (int i = 0; i < 4; ++i) r[i] = static_cast<uint32_t>(c[i]);

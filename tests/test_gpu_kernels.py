@@ -133,7 +133,7 @@ def _probe(kind: int, a: np.ndarray, b: np.ndarray, sa=None, sb=None) -> np.ndar
     assert code == 0
     torch.cuda.synchronize()
     out = d.cpu().numpy()
-    return out if kind == 4 else out[:, :4].copy()
+    return out if kind in (4, 5, 6) else out[:, :4].copy()
 
 
 def _expand(lanes: np.ndarray, per_lane: int) -> np.ndarray:
@@ -241,6 +241,62 @@ def test_mfma_f8_scaled_layout():
     sb = rng.integers(118, 136, 64, dtype=np.uint8)
     d = _probe(2, a, b, sa, sb).view(np.float32).astype(np.float64)
     _check_f8(d, _f8_matrix(_e4m3_values(a), sa), _f8_matrix(_e4m3_values(b), sb), 2.0 ** -11)
+
+
+def _f8_matrix32(lanes: np.ndarray, scales: np.ndarray | None = None, layout: str = "halves") -> np.ndarray:
+    """The 32 x 64 operand the 32x32x64 f8f6f4 MFMA reads from 64 lanes x 32 bytes. "halves":
+    lane group g = l/32 holds k in [16g, 16g+16) in bytes 0..15 and k in [32+16g, 48+16g) in bytes
+    16..31; "runs": lane group g holds k in [32g, 32g+32). The E8M0 byte of row i's K block κ is
+    lane i + 32κ's."""
+    mat = np.zeros((32, 64))
+    for lane in range(64):
+        i, g = lane % 32, lane // 32
+        if layout == "halves":
+            mat[i, 16 * g:16 * g + 16] = lanes[lane, :16]
+            mat[i, 32 + 16 * g:48 + 16 * g] = lanes[lane, 16:]
+        else:
+            mat[i, 32 * g:32 * g + 32] = lanes[lane]
+    if scales is not None:
+        for i in range(32):
+            for kb in range(2):
+                mat[i, 32 * kb:32 * kb + 32] *= 2.0 ** (float(scales[i + 32 * kb]) - 127)
+    return mat
+
+
+def _f8_32_error(d: np.ndarray, a: np.ndarray, b: np.ndarray) -> float:
+    """Largest error of a 32x32 result (lane l, register r = row 8·(r/4) + 4·(l/32) + r%4 of
+    column l%32) against the CPU product, relative to the sum of the products' magnitudes."""
+    want, size = a @ b.T, np.abs(a) @ np.abs(b).T
+    worst = 0.0
+    for lane in range(64):
+        for r in range(16):
+            i, j = 8 * (r // 4) + 4 * (lane // 32) + r % 4, lane % 32
+            worst = max(worst, abs(d[lane, r] - want[i, j]) / (size[i, j] + 1e-30))
+    return worst
+
+
+def test_mfma_f8_32x32_layout():
+    """32x32x64 e4m3: the 32x32 output layout of the int8 32x32x32 form. (Unscaled, any K order
+    common to both operands gives the same product; the scaled test below fixes the K order.)"""
+    rng = np.random.default_rng(11)
+    a, b = _e4m3_lanes(rng), _e4m3_lanes(rng)
+    d = _probe(5, a, b).view(np.float32).astype(np.float64)
+    err = _f8_32_error(d, _f8_matrix32(_e4m3_values(a)), _f8_matrix32(_e4m3_values(b)))
+    assert err <= 2.0 ** -11, err
+
+
+def test_mfma_f8_32x32_scaled_layout():
+    """The K order ("halves": lane group g holds 16-byte chunks g and g+2 of a 64-byte K step)
+    and the scale lanes (row (column) i, K block κ from lane i + 32κ) of the 32x32x64 form."""
+    rng = np.random.default_rng(12)
+    a, b = _e4m3_lanes(rng), _e4m3_lanes(rng)
+    sa = rng.integers(118, 136, 64, dtype=np.uint8)
+    sb = rng.integers(118, 136, 64, dtype=np.uint8)
+    d = _probe(6, a, b, sa, sb).view(np.float32).astype(np.float64)
+    va, vb = _e4m3_values(a), _e4m3_values(b)
+    errs = {lay: _f8_32_error(d, _f8_matrix32(va, sa, lay), _f8_matrix32(vb, sb, lay))
+            for lay in ("halves", "runs")}
+    assert errs["halves"] <= 2.0 ** -11, errs
 
 
 def test_mfma_bf16_layout():
@@ -378,7 +434,8 @@ def test_fp8_quantize_bit_exact(ops, shape, dtype):
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("shape", [(300, 512, 1024), (257, 264, 4096), (64, 1024, 2064),
                                    (1, 8, 128), (16, 136, 4096), (33, 200, 1040), (100, 520, 1040),
-                                   (129, 264, 4096), (256, 2048, 4096)],
+                                   (129, 264, 4096), (256, 2048, 4096), (512, 1024, 4096),
+                                   (1000, 776, 2064), (4096, 520, 4096)],
                          ids=lambda s: "x".join(map(str, s)))  # fmt: skip
 def test_fp8_gemm_within_tolerance(ops, shape, bias):
     m, n, k = shape
@@ -390,6 +447,31 @@ def test_fp8_gemm_within_tolerance(ops, shape, bias):
     got = ops.fp8_gemm(q, s, data.to(DEV), scale.to(DEV), None if b is None else b.to(DEV),
                        torch.bfloat16)  # fmt: skip
     assert_close(got, laws.fp8_exact(x, data, scale, b))
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(300, 512, 1024), (520, 264, 2064), (40, 136, 4096)],
+                         ids=lambda s: "x".join(map(str, s)))  # fmt: skip
+def test_fp8_gemm_gelu_and_fp16_within_tolerance(ops, shape, out_dtype):
+    """The fp8 GEMM's tanh-GELU epilogue through the C ABI (cozyq_gemm_ex, fp8 = 1): the law's
+    rounded output (bias in float32), then GELU in float32 and one more rounding."""
+    from cozyq import _lib
+
+    m, n, k = shape
+    x = activations(m, k, seed=35 + m)
+    data, scale = laws.fp8_weight(weights(n, k, seed=36))
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(37)) * 0.1).to(torch.bfloat16)
+    q, s = ops.fp8_quantize(x.to(DEV))
+    out = torch.empty(m, n, dtype=out_dtype, device=DEV)
+    bias = b.to(out_dtype).to(DEV)
+    wd, ws = data.to(DEV), scale.to(DEV)
+    code = _lib.load().cozyq_gemm_ex(0, 1, q.data_ptr(), s.data_ptr(), wd.data_ptr(), ws.data_ptr(),
+                                     bias.data_ptr(), out.data_ptr(), n,
+                                     int(out_dtype == torch.float16), m, n, k, 1,
+                                     torch.cuda.current_stream().cuda_stream)  # fmt: skip
+    assert code == 0
+    rounded = laws.fp8_exact(x, data, scale, b.to(out_dtype)).to(out_dtype)
+    assert_close(out, laws.gelu_tanh(rounded.float()).double())
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 16])
@@ -421,15 +503,19 @@ def test_mx_quantize_bit_exact(ops, shape, dtype):
     assert torch.equal(s.cpu(), ws)
 
 
-@pytest.mark.parametrize("shape", [(300, 512, 1024), (257, 264, 3072), (1, 8, 128)],
-                         ids=lambda s: "x".join(map(str, s)))
-def test_mx_gemm_within_tolerance(ops, shape):
+@pytest.mark.parametrize("bias", [True, False])
+@pytest.mark.parametrize("shape", [(300, 512, 1024), (257, 264, 3072), (1, 8, 128),
+                                   (512, 1024, 4096), (260, 264, 12288)],
+                         ids=lambda s: "x".join(map(str, s)))  # fmt: skip
+def test_mx_gemm_within_tolerance(ops, shape, bias):
     m, n, k = shape
     x = activations(m, k, seed=61 + m)
     data, wbyte = laws.mx_quantize(weights(n, k, seed=62))
-    b = (torch.randn(n, generator=torch.Generator().manual_seed(63)) * 0.1).to(torch.bfloat16)
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(63)) * 0.1).to(torch.bfloat16) \
+        if bias else None
     q, qs = ops.mx_quantize(x.to(DEV))
-    got = ops.mx_gemm(q, qs, data.to(DEV), wbyte.to(DEV), b.to(DEV), torch.bfloat16)
+    got = ops.mx_gemm(q, qs, data.to(DEV), wbyte.to(DEV), None if b is None else b.to(DEV),
+                      torch.bfloat16)  # fmt: skip
     assert_close(got, laws.mx_exact(x, data, wbyte, b))
 
 
