@@ -108,8 +108,8 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
 
     timer = Timer(torch)
     ms_step = timer.run(step, steps, warmup)
-    ms_gemm = timer.run(gemm, steps, 2)
-    ms_quant = timer.run(quantize, steps, 2)
+    ms_gemm = timer.run(gemm, steps, warmup)
+    ms_quant = timer.run(quantize, steps, warmup)
     ops_count = 2.0 * m * n * k
     gemm_tops = ops_count / (ms_gemm * 1e-3) / 1e12
     traffic_alg = m * k + n * k + m * n * 2 + n * 2 + (m + n) * 4
@@ -342,7 +342,10 @@ def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
-    parser.add_argument("--warmup", type=int, default=5)
+    # The chip's clocks settle over the first ~20 ms of sustained MFMA load (measured: the first
+    # 20-launch round of the C2 GEMM runs ~12% slower than later ones), so the default warmup
+    # covers that.
+    parser.add_argument("--warmup", type=int, default=100)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
     parser.add_argument("--only", choices=("c2", "decode", "fp8", "svdq", "mx", "copy"),
