@@ -41,7 +41,11 @@ constexpr int kGroupM = 4;                     // M-tiles a tile group spans
 
 constexpr int kStageRow = 128 * 2 + 16;         // one staged output row: 128 bf16 + pad
 constexpr int kStageBytes = 128 * kStageRow;    // one wave's staged quadrant
-constexpr int kLdsBytes = 4 * kStageBytes > 2 * kPairBytes ? 4 * kStageBytes : 2 * kPairBytes;
+constexpr int kEpiBase = 4 * kStageBytes > 2 * kPairBytes ? 4 * kStageBytes : 2 * kPairBytes;
+// The tile's epilogue operands, loaded into LDS with the first buffer: 256 weight scales, 256
+// biases and 256 row scales, past the buffers and the staging area.
+constexpr int kWsOff = kEpiBase, kBiasOff = kEpiBase + 1024, kXsOff = kEpiBase + 1536;
+constexpr int kLdsBytes = kEpiBase + 2560;
 
 // Buffer loads a lane issues per buffer: 8 of 16 bytes for each operand, and for MX one of 4
 // bytes for each operand's scales.
@@ -267,6 +271,25 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     // Buffers 0 and 1 take pairs 0 and 1; pair p + 2 is issued at the top of step 2p + 1, once
     // every wave's reads of pair p are in registers, and must land by the top of step 2p + 3.
     // Past the last pair the offsets fall outside the buffer: zeros into a buffer nothing reads.
+    // The epilogue's operands first (they land before pair 0 is seen complete): wave w loads
+    // columns (rows) 64w..64w+63 of the tile; past N (M) they read as zeros.
+    if constexpr (kEpi != 2) {
+        const int c = 64 * wave + lane;
+        if constexpr (kKind != kMx) {
+            const auto wsr = rows_view(reinterpret_cast<const uint8_t*>(ws + n0), N - n0, 4);
+            const auto xsr = rows_view(reinterpret_cast<const uint8_t*>(xs + m0), M - m0, 4);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, (LdsPtr*)(lds + kWsOff + 256 * wave), 4, 4 * c, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xsr, (LdsPtr*)(lds + kXsOff + 256 * wave), 4, 4 * c, 0, 0, 0);
+        }
+        // Biases two a lane (LDS-DMA writes each lane's data at a 4-byte stride whatever the
+        // load size): waves 0 and 1 cover the tile's 256.
+        if constexpr (kBias) {
+            if (wave < 2) {
+                const auto br = rows_view(reinterpret_cast<const uint8_t*>(bias + n0), N - n0, 2);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (LdsPtr*)(lds + kBiasOff + 256 * wave), 4, 4 * c, 0, 0, 0);
+            }
+        }
+    }
     COZYQ_ISSUE(0);
     COZYQ_ISSUE(1);
     fence();
@@ -349,8 +372,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
 
     // Epilogue. Block (i, j): lane holds out[m][n] for m = j-block row l%32 and, per register
     // r, n = i-block column 8·(r/4) + 4·(l/32) + r%4 (MFMA rows are W rows): four runs of four
-    // consecutive columns, each an 8-byte store. The lane's 64 weight scales and biases are
-    // loaded once, ahead of the arithmetic.
+    // consecutive columns, each an 8-byte store. The lane's 64 weight scales and biases and 4
+    // row scales are read from LDS once, ahead of the arithmetic.
     const int nl = n0 + wn * 128 + 4 * fq;  // the lane's first column
     if constexpr (kEpi == 2) {
         wait_vmcnt<0>();  // the zero-filling loads past the last step land before the LDS is released
@@ -370,19 +393,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
         }
         return;
     }
-    float4 wsv[4][4];
-    uint2 bv[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int n = min(nl + i * 32 + 8 * g, N - 4);  // N % 8 == 0: a clamped run stays in bounds
-            wsv[i][g] = kKind == kMx ? make_float4(1.0f, 1.0f, 1.0f, 1.0f) : *reinterpret_cast<const float4*>(ws + n);
-            if constexpr (kBias) bv[i][g] = *reinterpret_cast<const uint2*>(bias + n);
-        }
-    float xsv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) xsv[j] = kKind == kMx ? 1.0f : xs[min(m0 + wm * 128 + j * 32 + fr, M - 1)];
     // All loads have landed and all waves are done with the buffers before they become the
     // staging area.
     fence();
@@ -390,7 +400,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
     fence();
+    float4 wsv[4][4];
+    uint2 bv[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int c = nl - n0 + i * 32 + 8 * g;  // column within the tile
+            wsv[i][g] = kKind == kMx ? make_float4(1.0f, 1.0f, 1.0f, 1.0f)
+                                     : *reinterpret_cast<const float4*>(lds + kWsOff + 4 * c);
+            if constexpr (kBias) bv[i][g] = *reinterpret_cast<const uint2*>(lds + kBiasOff + 2 * c);
+        }
+    float xsv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        xsv[j] = kKind == kMx ? 1.0f : *reinterpret_cast<const float*>(lds + kXsOff + 4 * (wm * 128 + j * 32 + fr));
+    // Block row j at a time: its 32 rows are computed and staged, then stored as whole rows while
+    // the next block row's arithmetic runs (the stores are not waited on).
     uint8_t* stage = lds + wave * kStageBytes;
+    const int cl = (lane & 15) * 8;  // first of the lane's 8 columns in a stored row
+    const int n = n0 + wn * 128 + cl;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int ml = j * 32 + fr;  // row within the quadrant
@@ -430,17 +459,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
                 const int col = i * 32 + 8 * g + 4 * fq;  // column within the quadrant
                 *reinterpret_cast<uint2*>(stage + ml * kStageRow + 2 * col) = packed;
             }
-    }
-    wait_lgkmcnt0();  // a wave reads back only its own quadrant
-    // Whole rows: 16 lanes cover one quadrant row's 256 bytes; 4 rows an instruction.
-    const int cl = (lane & 15) * 8;  // first of the lane's 8 columns
-    const int n = n0 + wn * 128 + cl;
-#pragma unroll 4
-    for (int r0 = 0; r0 < 128; r0 += 4) {
-        const int ml = r0 + (lane >> 4);
-        const int m = m0 + wm * 128 + ml;
-        const uint4 v = *reinterpret_cast<const uint4*>(stage + ml * kStageRow + 2 * cl);
-        if (m < M && n < N) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * ldo + n) = v;
+        wait_lgkmcnt0();  // a wave reads back only its own rows
+        // Whole rows: 16 lanes cover one quadrant row's 256 bytes; 4 rows an instruction.
+#pragma unroll
+        for (int r0 = 0; r0 < 32; r0 += 4) {
+            const int rl = j * 32 + r0 + (lane >> 4);
+            const int m = m0 + wm * 128 + rl;
+            const uint4 v = *reinterpret_cast<const uint4*>(stage + rl * kStageRow + 2 * cl);
+            if (m < M && n < N) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * ldo + n) = v;
+        }
     }
 }
 
