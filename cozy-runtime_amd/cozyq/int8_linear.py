@@ -96,11 +96,10 @@ def prologue(
     up: Tensor | None = None,
 ) -> PreQuantized | None:
     """`activation(norm(x)·(1 + scale) + shift)` rotated and quantized in one pass
-    (`internal/int8_linear.py:308-357`), with the reference's argument rules (a gated
-    activation stands alone; `up` only with swiglu). The producer prologue is not fused into
-    the gfx950 quantize kernel yet (`cozyq_quantize` answers NOT_SUPPORTED for it), so every
-    call that names one returns None and the caller runs its own ops — the reference's answer
-    when its op does not serve; a plain call (no prologue) quantizes."""
+    (`internal/int8_linear.py:308-357`) when each of `consumers` is an un-hooked leaf of the
+    rows' width taking int8.convrot's operand; else None and the caller runs its own ops. The
+    reference's argument rules hold: a gated activation (`GATED`, or swiglu without `up`) reads
+    x's [hidden | gate] halves alone; `up` only with swiglu, of x's shape."""
     gated = activation in GATED or (activation == "swiglu" and up is None)
     if gated and (norm is not None or scale is not None or shift is not None or x.shape[-1] % 2):
         raise ValueError(f"int8_rows: {activation} takes [hidden | gate] rows, no norm or tables")
@@ -110,17 +109,24 @@ def prologue(
         raise ValueError("int8_rows: swiglu takes gate and up rows, no norm or tables")
     if norm not in NORMS or activation not in ACTIVATIONS:
         raise ValueError(f"int8_rows: norm {norm!r} / activation {activation!r} unknown")
+    if up is not None and (up.shape != x.shape or up.dtype != x.dtype or not up.is_cuda):
+        return None
     width = x.shape[-1] // 2 if gated else x.shape[-1]
     if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16):
+        return None
+    if any(t is not None and t.dtype != x.dtype for t in (scale, shift)):
+        return None  # eager promotes the rows to the table's dtype
+    hooks = torch.nn.modules.module
+    if hooks._global_forward_hooks or hooks._global_forward_pre_hooks:
         return None
     for module in consumers:
         if getattr(module, "operand", None) != INT8_CONVROT or getattr(module, "in_features", None) != width:
             return None
         if not _inert(module):
             return None
-    if any(v is not None for v in (scale, shift, up)) or norm is not None or activation is not None:
-        return None
-    payload, row_scale = library(x.get_device()).int8_quantize(x)
+    payload, row_scale = library(x.get_device()).int8_quantize(
+        x, scale, shift, NORMS[norm], eps, ACTIVATIONS[activation], up
+    )
     return PreQuantized(payload, row_scale, (*x.shape[:-1], width), INT8_CONVROT)
 
 

@@ -43,6 +43,10 @@ class _Format:
 
 
 #: `internal/prebuilt.py:68`: int8 rows rotate in 256-groups; fp8 rows are 16-byte multiples.
+#: The prologue's gated activation codes (`internal/prebuilt.py` SITU / SWIGLU): x holds
+#: [hidden | gate] (or, for SwiGLU without `up`, [up | gate]) halves.
+SITU, SWIGLU = 3, 4
+
 INT8, FP8 = _Format("int8", False, 256), _Format("fp8", True, 16)
 MX = _Format("mxfp8", True, 128)
 SVDQ = _Format("svdq-int4", False, INT4_GROUP)
@@ -56,6 +60,10 @@ def _torch():
 
 def _ptr(t: Tensor | None) -> int | None:
     return None if t is None else int(t.data_ptr())
+
+
+def _stride(t: Tensor | None) -> int:
+    return 0 if t is None else int(t.stride(0))
 
 
 def _aligned(t: Tensor) -> Tensor:
@@ -320,22 +328,48 @@ class Prebuilt:
         self, f: _Format, x: Tensor, scale: Tensor | None, shift: Tensor | None, norm: int,
         eps: float, activation: int, up: Tensor | None,
     ) -> tuple[Tensor, Tensor]:
-        """`internal/prebuilt.py:252-291`. The producer prologue (`scale`, `shift`, `norm`,
-        `activation`, `up`) is not served: the C ABI answers NOT_SUPPORTED and this raises."""
+        """`internal/prebuilt.py:252-291`: per-row quantization with the producer prologue
+        `activation(norm(x)·(1 + scale) + shift)` folded in. A gated row (SiTU, or SwiGLU
+        without `up`) quantizes to half its width."""
         torch = self.torch
-        if any(v is not None for v in (scale, shift, up)) or norm or activation:
-            raise NotImplementedError(f"{f.name}_quantize: the producer prologue is not served")
-        flat = self._rows(f, x)
-        rows, width = flat.shape
+        gated = activation == SITU or (activation == SWIGLU and up is None)
+        flat = self._rows(f, x, x.shape[-1] // 2 if gated else x.shape[-1])
+        rows, width = flat.shape[0], flat.shape[1] // 2 if gated else flat.shape[1]
+        if gated and (x.shape[-1] % 2 or norm or scale is not None or shift is not None):
+            raise ValueError(f"{f.name}_quantize: a gated activation takes [hidden | gate] rows alone")
+        if up is not None and (
+            activation != SWIGLU or up.shape != x.shape or up.dtype != x.dtype or norm
+            or scale is not None or shift is not None
+        ):
+            raise ValueError(f"{f.name}_quantize: SwiGLU takes gate and up rows of one shape alone")
+        other = None if up is None else self._rows(f, up)
         q = torch.empty(rows, width, dtype=torch.float8_e4m3fn if f.fp8 else torch.int8,
                         device=x.device)  # fmt: skip
         scales = torch.empty(rows, dtype=torch.float32, device=x.device)
+        tables = [self._table(t, flat) for t in (scale, shift)]
+        entries = next((t.shape[0] for t in tables if t is not None), rows) or 1
+        if any(t is not None and t.shape[0] != entries for t in tables) or rows % entries:
+            raise ValueError(f"{f.name}_quantize: modulation rows do not divide {rows} rows")
         code = self._lib.cozyq_quantize(
             self.index, f.fp8, flat.data_ptr(), self._half(flat.dtype), q.data_ptr(),
-            scales.data_ptr(), rows, width, None, None, 0, 0, 1, 0, 0.0, 0, None, self._stream(),
+            scales.data_ptr(), rows, width, _ptr(tables[0]), _ptr(tables[1]),
+            _stride(tables[0]), _stride(tables[1]), max(rows // entries, 1), norm, eps,
+            activation, _ptr(other), self._stream(),
         )  # fmt: skip
         self._check(code, "the quantization")
         return q, scales
+
+    def _table(self, table: Tensor | None, flat: Tensor) -> Tensor | None:
+        """`internal/prebuilt.py:408-417`: a modulation table as `[E, K]` rows read 16 bytes at
+        a time."""
+        if table is None:
+            return None
+        if table.device != flat.device or table.dtype != flat.dtype:
+            raise ValueError("a modulation table must match the activation's device and dtype")
+        found = table.reshape(-1, flat.shape[1])
+        if found.stride(1) != 1 or found.stride(0) % 8 or found.data_ptr() % 16:
+            found = found.contiguous()
+        return found if found.data_ptr() % 16 == 0 else found.clone()
 
     def _gemm(
         self, f: _Format, q: Tensor, scales: Tensor, data: Tensor, scale: Tensor,

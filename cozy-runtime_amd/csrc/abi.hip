@@ -49,21 +49,29 @@ int cozyq_quantize(int device, int fp8, const void* x, int x_half, void* q, floa
                    int K, const void* scale, const void* shift, int64_t scale_stride,
                    int64_t shift_stride, int rows_per_entry, int norm, float eps, int activation,
                    const void* up, void* stream) {
-    (void)scale_stride; (void)shift_stride; (void)eps;
     if (!fits(K, fp8 ? 16 : 256) || M < 0 || norm < 0 || norm > 2 || activation < 0 ||
         activation > 4 || rows_per_entry < 1)
         return hipErrorInvalidValue;
     const bool gated = activation == 3 || activation == 4;
     if (gated && (norm != 0 || scale || shift)) return hipErrorInvalidValue;
     if (up != nullptr && activation != 4) return hipErrorInvalidValue;
-    if (scale || shift || norm || activation || up) return hipErrorNotSupported;
+    // The tables and `up` are read 16 bytes at a time, as x is.
+    if ((scale && (!aligned16(scale) || scale_stride < 0 || scale_stride % 8)) ||
+        (shift && (!aligned16(shift) || shift_stride < 0 || shift_stride % 8)) ||
+        (up && !aligned16(up)) || !aligned16(x))
+        return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
+    const cozyq::Prologue pro{static_cast<const uint16_t*>(scale), static_cast<const uint16_t*>(shift),
+                              scale_stride, shift_stride, rows_per_entry, norm, eps, activation,
+                              static_cast<const uint16_t*>(up)};
+    const bool any = scale || shift || norm || activation;
     if (fp8)
-        return cozyq::fp8_quantize(x, x_half, static_cast<uint8_t*>(q), scales, M, K, on(stream));
+        return cozyq::fp8_quantize(x, x_half, static_cast<uint8_t*>(q), scales, M, K,
+                                   any ? &pro : nullptr, on(stream));
     return cozyq::rotate_quantize(x, x_half, static_cast<int8_t*>(q), scales, M, K, 256,
-                                  on(stream));
+                                  any ? &pro : nullptr, on(stream));
 }
 
 int cozyq_quantize_rot(int device, const void* x, int x_half, int8_t* q, float* scales, int M,
@@ -74,7 +82,7 @@ int cozyq_quantize_rot(int device, const void* x, int x_half, int8_t* q, float* 
     if (M == 0) return hipSuccess;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
-    return cozyq::rotate_quantize(x, x_half, q, scales, M, K, rotation, on(stream));
+    return cozyq::rotate_quantize(x, x_half, q, scales, M, K, rotation, nullptr, on(stream));
 }
 
 int cozyq_gemv(int device, const void* x, int x_half, const int8_t* w, const float* w_scale,

@@ -7,10 +7,26 @@
 
 namespace cozyq {
 
+// The producer's prologue folded into the quantize pass (reference: kernels/csrc/gemm/int8.h:
+// 25-47): activation(norm(x) · (1 + scale) + shift). Tables are in x's dtype, rows
+// `*_stride` elements apart; row r of x reads table row r / rows_per_entry. norm 0 none, 1
+// layer, 2 RMS (no affine); act 0 none, 1 GELU (erf), 2 tanh-GELU, 3 SiTU on [hidden | gate]
+// rows of 2K, 4 SwiGLU (gate rows in x and up rows in `up`; without `up`, [up | gate] rows).
+struct Prologue {
+    const uint16_t* scale;
+    const uint16_t* shift;
+    int64_t scale_stride, shift_stride;
+    int rows_per_entry, norm;
+    float eps;
+    int act;
+    const uint16_t* up;
+};
+
+// `pro` may be null (no prologue); with one, rotation must be 256.
 hipError_t rotate_quantize(const void* x, bool x_half, int8_t* q, float* scales, int M, int K,
-                           int rotation, hipStream_t s);
+                           int rotation, const Prologue* pro, hipStream_t s);
 hipError_t fp8_quantize(const void* x, bool x_half, uint8_t* q, float* scales, int M, int K,
-                        hipStream_t s);
+                        const Prologue* pro, hipStream_t s);
 hipError_t mx_quantize(const void* x, bool x_half, uint8_t* q, uint8_t* scales, int M, int K,
                        hipStream_t s);
 

@@ -63,6 +63,128 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
     }
 }
 
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) m += red[w];
+    __syncthreads();
+    return m;
+}
+
+// A float32 value rounded to the rows' dtype and widened back (an eager op's output).
+template <bool kHalf>
+__device__ __forceinline__ float in_dtype(float v) {
+    return widen<kHalf>(narrow<kHalf>(v));
+}
+
+// The producer's prologue (`Prologue`, kernels.h; reference rotate.cu:195-282) is computed in
+// float32 before the rotation, in the reference kernel's order of operations.
+constexpr int kNormLayer = 1;
+constexpr int kActGelu = 1, kActGeluTanh = 2, kActSitu = 3, kActSwiglu = 4;
+
+__device__ __forceinline__ bool halves(const Prologue& p) {
+    return p.act == kActSitu || (p.act == kActSwiglu && p.up == nullptr);
+}
+
+// Elements e..e+7 of row `row` after the prologue; `mean` and `rstd` are the row's norm
+// statistics (mean 0 for the RMS norm).
+template <bool kHalf>
+__device__ __forceinline__ void load8_prologue(const Prologue& p, const uint16_t* x, int row,
+                                               int K, int e, float mean, float rstd, float* v) {
+    if (halves(p)) {
+        const uint16_t* xr = x + static_cast<int64_t>(row) * (2 * K);
+        float h[8], g[8];
+        load8<kHalf>(xr + e, h);
+        load8<kHalf>(xr + K + e, g);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (p.act == kActSitu) {
+                // rotate.cu:252: (4 tanh(g/4) / (1 + e^-g)) · (25 tanh(h/25))
+                v[i] = (4.0f * tanhf(g[i] * 0.25f) / (1.0f + expf(-g[i]))) * (25.0f * tanhf(h[i] / 25.0f));
+            } else {
+                // rotate.cu:271-282: silu(gate) in the row dtype (IEEE divide), times up, rounded again
+                const float silu = in_dtype<kHalf>(g[i] / (1.0f + expf(-g[i])));
+                v[i] = in_dtype<kHalf>(silu * h[i]);
+            }
+        }
+        return;
+    }
+    const int64_t at = static_cast<int64_t>(row) * K + e;
+    load8<kHalf>(x + at, v);
+    if (p.act == kActSwiglu) {  // gate rows in x, up rows in `up` (rotate.cu:260-268)
+        float u[8];
+        load8<kHalf>(p.up + at, u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float silu = in_dtype<kHalf>(v[i] / (1.0f + expf(-v[i])));
+            v[i] = in_dtype<kHalf>(silu * u[i]);
+        }
+        return;
+    }
+    if (p.norm != 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (v[i] - mean) * rstd;
+    }
+    const int64_t entry = row / p.rows_per_entry;
+    if (p.scale != nullptr) {
+        float m[8];
+        load8<kHalf>(p.scale + entry * p.scale_stride + e, m);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] *= 1.0f + m[i];
+    }
+    if (p.shift != nullptr) {
+        float m[8];
+        load8<kHalf>(p.shift + entry * p.shift_stride + e, m);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] += m[i];
+    }
+    if (p.act == kActGelu) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.5f * v[i] * (1.0f + erff(v[i] * 0.70710678f));
+    } else if (p.act == kActGeluTanh) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float y = v[i];
+            v[i] = 0.5f * y * (1.0f + tanhf(0.79788456f * (y + 0.044715f * y * y * y)));
+        }
+    }
+}
+
+// The row's norm statistics (rotate.cu:204-221): the mean (layer norm; 0 for RMS) and
+// rsqrt(Σ(x - mean)² / K + eps) over x's K elements, every thread of the block taking part.
+template <bool kHalf>
+__device__ __forceinline__ float2 norm_stats(const Prologue& p, const uint16_t* x, int row, int K,
+                                             float* red) {
+    if (p.norm == 0) return make_float2(0.0f, 1.0f);
+    const uint16_t* xr = x + static_cast<int64_t>(row) * K;
+    float mean = 0.0f;
+    if (p.norm == kNormLayer) {
+        float sum = 0.0f;
+        for (int e = threadIdx.x * 8; e < K; e += blockDim.x * 8) {
+            float v[8];
+            load8<kHalf>(xr + e, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sum += v[i];
+        }
+        mean = block_sum(sum, red) / static_cast<float>(K);
+    }
+    float squares = 0.0f;
+    for (int e = threadIdx.x * 8; e < K; e += blockDim.x * 8) {
+        float v[8];
+        load8<kHalf>(xr + e, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float d = v[i] - mean;
+            squares += d * d;
+        }
+    }
+    const float total = block_sum(squares, red);
+    return make_float2(mean, rsqrtf(total / static_cast<float>(K) + p.eps));
+}
+
 // torch.round(v / s).clamp_(-127, 127): the correctly rounded quotient, half to even, clamp.
 // `rs` = RN(1/s) for a finite s takes the quotient on div_rn; an infinite s (a row holding an
 // infinity) divides.
@@ -75,14 +197,17 @@ __device__ __forceinline__ int8_t q8(float v, float scale, float rs) {
 
 // Rotation by H_kRot (256: H4^⊗4 then ·1/16; 128: H2⊗H4^⊗3 unnormalized) and per-row int8.
 // One block per row; kMaxChunks bounds the row's 4096-element chunks held in registers.
-template <bool kHalf, int kRot, int kMaxChunks>
+template <bool kHalf, int kRot, int kMaxChunks, bool kPro = false>
 __global__ __launch_bounds__(kThreads) void rotate_quantize_kernel(
-    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales, int K) {
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales, int K,
+    Prologue pro) {
     using L = Layout<kRot>;
     __shared__ __attribute__((aligned(16))) float lds[L::kFloats];
     __shared__ float red[kThreads / 64];
     const int row = blockIdx.x, tid = threadIdx.x;
     const uint16_t* xr = x + static_cast<int64_t>(row) * K;
+    float2 stats = make_float2(0.0f, 1.0f);
+    if constexpr (kPro) stats = norm_stats<kHalf>(pro, x, row, K, red);
     const int chunks = (K + kChunk - 1) / kChunk;
     float out[kMaxChunks][16];
     float amax = 0.0f;
@@ -95,7 +220,10 @@ __global__ __launch_bounds__(kThreads) void rotate_quantize_kernel(
         // Phase 1: the chunk into LDS, 16 bytes a load.
         for (int e = tid * 8; e < width; e += kThreads * 8) {
             float v[8];
-            load8<kHalf>(xr + base + e, v);
+            if constexpr (kPro)
+                load8_prologue<kHalf>(pro, x, row, K, base + e, stats.x, stats.y, v);
+            else
+                load8<kHalf>(xr + base + e, v);
             const int g = e / kRot, within = e % kRot;
             float* dst = lds + L::at(g, within / 16, within % 16);
             *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
@@ -185,16 +313,25 @@ __global__ __launch_bounds__(kThreads) void rotate_quantize_kernel(
 // Per-row int8 without rotation (build lane): s = max(amax/127, 1e-12), q = clamp(rne(x/s)).
 // Per-row E4M3 (fp8 = true): s = max(amax/448, 1e-12), q = e4m3(clamp(x/s, ±448)).
 // One block per row; two passes over the row (the second from cache).
-template <bool kHalf, bool kFp8>
+template <bool kHalf, bool kFp8, bool kPro = false>
 __global__ __launch_bounds__(kThreads) void rowwise_quantize_kernel(
-    const uint16_t* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scales, int K) {
+    const uint16_t* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scales, int K,
+    Prologue pro) {
     __shared__ float red[kThreads / 64];
     const int row = blockIdx.x, tid = threadIdx.x;
     const uint16_t* xr = x + static_cast<int64_t>(row) * K;
+    float2 stats = make_float2(0.0f, 1.0f);
+    if constexpr (kPro) stats = norm_stats<kHalf>(pro, x, row, K, red);
+    auto load = [&](int e, float* v) {
+        if constexpr (kPro)
+            load8_prologue<kHalf>(pro, x, row, K, e, stats.x, stats.y, v);
+        else
+            load8<kHalf>(xr + e, v);
+    };
     float amax = 0.0f;
     for (int e = tid * 8; e < K; e += kThreads * 8) {
         float v[8];
-        load8<kHalf>(xr + e, v);
+        load(e, v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
     }
@@ -207,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void rowwise_quantize_kernel(
         constexpr bool kFast = decltype(fast)::value;
         for (int e = tid * 8; e < K; e += kThreads * 8) {
             float v[8];
-            load8<kHalf>(xr + e, v);
+            load(e, v);
             uint32_t word[2] = {0, 0};
             if constexpr (kFp8) {
                 float r[8];
@@ -254,54 +391,64 @@ __global__ __launch_bounds__(kThreads) void mx_quantize_kernel(
     if ((i & 3) == 0) scales[i >> 2] = static_cast<uint8_t>(byte);
 }
 
-template <bool kHalf, int kRot>
-hipError_t launch_rotated(const void* x, int8_t* q, float* scales, int M, int K, hipStream_t s) {
+template <bool kHalf, int kRot, bool kPro>
+hipError_t launch_rotated(const void* x, int8_t* q, float* scales, int M, int K,
+                          const Prologue& pro, hipStream_t s) {
     const int chunks = (K + kChunk - 1) / kChunk;
     const dim3 grid(M), block(kThreads);
     auto xp = static_cast<const uint16_t*>(x);
     if (chunks <= 1)
-        rotate_quantize_kernel<kHalf, kRot, 1><<<grid, block, 0, s>>>(xp, q, scales, K);
+        rotate_quantize_kernel<kHalf, kRot, 1, kPro><<<grid, block, 0, s>>>(xp, q, scales, K, pro);
     else if (chunks <= 2)
-        rotate_quantize_kernel<kHalf, kRot, 2><<<grid, block, 0, s>>>(xp, q, scales, K);
+        rotate_quantize_kernel<kHalf, kRot, 2, kPro><<<grid, block, 0, s>>>(xp, q, scales, K, pro);
     else if (chunks <= 4)
-        rotate_quantize_kernel<kHalf, kRot, 4><<<grid, block, 0, s>>>(xp, q, scales, K);
+        rotate_quantize_kernel<kHalf, kRot, 4, kPro><<<grid, block, 0, s>>>(xp, q, scales, K, pro);
     else
-        rotate_quantize_kernel<kHalf, kRot, 8><<<grid, block, 0, s>>>(xp, q, scales, K);
+        rotate_quantize_kernel<kHalf, kRot, 8, kPro><<<grid, block, 0, s>>>(xp, q, scales, K, pro);
+    return hipGetLastError();
+}
+
+template <bool kHalf, bool kFp8>
+hipError_t launch_rowwise(const void* x, uint8_t* q, float* scales, int M, int K,
+                          const Prologue* pro, hipStream_t s) {
+    auto xp = static_cast<const uint16_t*>(x);
+    if (pro != nullptr)
+        rowwise_quantize_kernel<kHalf, kFp8, true><<<M, kThreads, 0, s>>>(xp, q, scales, K, *pro);
+    else
+        rowwise_quantize_kernel<kHalf, kFp8, false><<<M, kThreads, 0, s>>>(xp, q, scales, K, Prologue{});
     return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t rotate_quantize(const void* x, bool x_half, int8_t* q, float* scales, int M, int K,
-                           int rotation, hipStream_t s) {
+                           int rotation, const Prologue* pro, hipStream_t s) {
     if (M == 0) return hipSuccess;
+    if (pro != nullptr) {
+        if (rotation != 256) return hipErrorInvalidValue;
+        return x_half ? launch_rotated<true, 256, true>(x, q, scales, M, K, *pro, s)
+                      : launch_rotated<false, 256, true>(x, q, scales, M, K, *pro, s);
+    }
+    const Prologue none{};
     if (rotation == 0) {
-        auto xp = static_cast<const uint16_t*>(x);
         auto qp = reinterpret_cast<uint8_t*>(q);
-        if (x_half)
-            rowwise_quantize_kernel<true, false><<<M, kThreads, 0, s>>>(xp, qp, scales, K);
-        else
-            rowwise_quantize_kernel<false, false><<<M, kThreads, 0, s>>>(xp, qp, scales, K);
-        return hipGetLastError();
+        return x_half ? launch_rowwise<true, false>(x, qp, scales, M, K, nullptr, s)
+                      : launch_rowwise<false, false>(x, qp, scales, M, K, nullptr, s);
     }
     if (rotation == 256)
-        return x_half ? launch_rotated<true, 256>(x, q, scales, M, K, s)
-                      : launch_rotated<false, 256>(x, q, scales, M, K, s);
+        return x_half ? launch_rotated<true, 256, false>(x, q, scales, M, K, none, s)
+                      : launch_rotated<false, 256, false>(x, q, scales, M, K, none, s);
     if (rotation == 128)
-        return x_half ? launch_rotated<true, 128>(x, q, scales, M, K, s)
-                      : launch_rotated<false, 128>(x, q, scales, M, K, s);
+        return x_half ? launch_rotated<true, 128, false>(x, q, scales, M, K, none, s)
+                      : launch_rotated<false, 128, false>(x, q, scales, M, K, none, s);
     return hipErrorInvalidValue;
 }
 
 hipError_t fp8_quantize(const void* x, bool x_half, uint8_t* q, float* scales, int M, int K,
-                        hipStream_t s) {
+                        const Prologue* pro, hipStream_t s) {
     if (M == 0) return hipSuccess;
-    auto xp = static_cast<const uint16_t*>(x);
-    if (x_half)
-        rowwise_quantize_kernel<true, true><<<M, kThreads, 0, s>>>(xp, q, scales, K);
-    else
-        rowwise_quantize_kernel<false, true><<<M, kThreads, 0, s>>>(xp, q, scales, K);
-    return hipGetLastError();
+    return x_half ? launch_rowwise<true, true>(x, q, scales, M, K, pro, s)
+                  : launch_rowwise<false, true>(x, q, scales, M, K, pro, s);
 }
 
 hipError_t mx_quantize(const void* x, bool x_half, uint8_t* q, uint8_t* scales, int M, int K,

@@ -41,8 +41,15 @@ const char* cozyq_error_name(int code);
  *          scales[m] = max(amax/127, 1e-12); K % 256 == 0.
  * fp8 = 1: each row quantized to OCP E4M3 with scales[m] = max(amax/448, 1e-12); K % 16 == 0.
  * q: [M, K] (int8 or e4m3 bytes); scales: [M] float32. K <= cozyq_max_k().
- * scale/shift/norm/activation/up describe the reference's producer prologue; this build
- * serves none yet: any of them set returns hipErrorNotSupported. */
+ * The producer's prologue (reference: int8.h:25-47, rotate.cu:195-282) is applied in float32
+ * before the rotation / quantization: activation(norm(x) · (1 + scale[e]) + shift[e]) with
+ * e = m / rows_per_entry. norm 0 none, 1 layer, 2 RMS (no affine; eps inside the rsqrt);
+ * scale/shift: tables in x's dtype, rows scale_stride/shift_stride elements apart (multiples of
+ * 8, 16-byte aligned), or NULL; activation 0 none, 1 GELU (erf), 2 tanh-GELU, 3 SiTU (x rows
+ * are [hidden | gate], 2K wide: 4 tanh(g/4) sigmoid(g) · 25 tanh(h/25)), 4 SwiGLU (x holds the
+ * gate rows and `up` the up rows, [M, K] each, silu(gate) · up with each product rounded to
+ * x's dtype; without `up`, x rows are [up | gate], 2K wide). The gated activations (3, 4) take
+ * no norm or tables; `up` only with 4. Violations return hipErrorInvalidValue. */
 int cozyq_quantize(int device, int fp8, const void* x, int x_half, void* q, float* scales, int M,
                    int K, const void* scale, const void* shift, int64_t scale_stride,
                    int64_t shift_stride, int rows_per_entry, int norm, float eps, int activation,

@@ -16,6 +16,10 @@ Pins, exercised in `tests/test_oracle.py`:
   of log2) and the round trip through the mxfp8 decode law.
 - `int8_*` products: int32 GEMM against numpy int64 matmul.
 - `int4_quantize` (build law): round trip bound |x − q·s| ≤ s/2 and brute force on small cases.
+- `prologue` (the producer prologue, compared with tolerance on the GPU since its
+  transcendentals are the platform's): closed forms (constant and alternating rows through
+  each norm, unit / zero modulation, table-row selection) and the library routines `math.erf`,
+  `math.tanh`, `math.exp` and `torch.nn.functional.silu` on scalars.
 - `svdq_smooth`, `svdq_down`, `svdq_exact` (the W4A4 structure): closed forms — unit and
   power-of-two smoothing, one-hot and integer-valued down projections (against numpy int64),
   the fp16 cast of `down` for fp16 x, and activations/weights placed on the int4 grid so that
@@ -192,6 +196,57 @@ def fp8_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     scale = (flat.abs().amax(dim=-1, keepdim=True).float() / E4M3_MAX).clamp(min=SCALE_FLOOR)
     q = (flat.float() / scale).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
     return q, scale
+
+
+#: The producer prologue's codes (`internal/int8_linear.py:302-305`, `kernels/csrc/gemm/int8.h:25-26`).
+NORM_LAYER, NORM_RMS = 1, 2
+ACT_GELU, ACT_GELU_TANH, ACT_SITU, ACT_SWIGLU = 1, 2, 3, 4
+
+
+def prologue(
+    x: torch.Tensor, *, scale: torch.Tensor | None = None, shift: torch.Tensor | None = None,
+    norm: int = 0, eps: float = 0.0, activation: int = 0, up: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The producer's prologue folded into the quantize pass, in float32 and in the reference
+    kernel's order of operations (`kernels/csrc/gemm/rotate.cu:195-282`, contract
+    `int8.h:25-47`): activation(norm(x)·(1 + scale[e]) + shift[e]), e = row // (rows // entries).
+    - norm: mean = Σx/K (layer; 0 for RMS), rstd = rsqrt(Σ(x − mean)²/K + eps), (x − mean)·rstd.
+    - activation 1: 0.5·y·(1 + erf(y·0.70710678)); 2: 0.5·y·(1 + tanh(0.79788456·(y + 0.044715·y³))).
+    - 3 (SiTU, x = [hidden | gate]): (4·tanh(g/4) / (1 + e^-g))·(25·tanh(h/25)).
+    - 4 (SwiGLU): silu(g) = g / (1 + e^-g) rounded to x's dtype, times up, rounded again; gate
+      rows in x and up rows in `up`, or x = [up | gate] without `up`.
+    Returns the float32 rows the rotation / quantization takes."""
+    dtype = x.dtype
+    flat = x.reshape(-1, x.shape[-1]).float()
+    if activation == ACT_SITU:
+        h, g = flat.chunk(2, -1)
+        return (4.0 * torch.tanh(g * 0.25) / (1.0 + torch.exp(-g))) * (25.0 * torch.tanh(h / 25.0))
+    if activation == ACT_SWIGLU:
+        if up is None:
+            u, g = flat.chunk(2, -1)
+        else:
+            g, u = flat, up.reshape(-1, up.shape[-1]).float()
+        silu = (g / (1.0 + torch.exp(-g))).to(dtype).float()
+        return (silu * u).to(dtype).float()
+    v = flat
+    if norm:
+        k = float(v.shape[-1])
+        mean = v.sum(-1, keepdim=True) / k if norm == NORM_LAYER else torch.zeros_like(v[:, :1])
+        d = v - mean
+        rstd = torch.rsqrt((d * d).sum(-1, keepdim=True) / k + eps)
+        v = (v - mean) * rstd
+    rows = v.shape[0]
+    for table, kind in ((scale, "scale"), (shift, "shift")):
+        if table is None:
+            continue
+        t = table.reshape(-1, v.shape[-1]).float()
+        entry = torch.arange(rows) // (rows // t.shape[0])
+        v = v * (1.0 + t[entry]) if kind == "scale" else v + t[entry]
+    if activation == ACT_GELU:
+        v = 0.5 * v * (1.0 + torch.erf(v * 0.70710678))
+    elif activation == ACT_GELU_TANH:
+        v = 0.5 * v * (1.0 + torch.tanh(0.79788456 * (v + 0.044715 * v * v * v)))
+    return v
 
 
 def fp8_weight(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

@@ -486,6 +486,60 @@ def test_fp8_small_linear_within_tolerance(ops, m, k):
     assert_close(got, laws.fp8_exact(x, data, scale, b))
 
 
+# ------------------------------------------------------------------ producer prologue
+
+#: (name, norm, eps, tables, activation, up): the prologue shapes `int8_rows` forwards.
+PROLOGUES = [
+    ("rms", laws.NORM_RMS, 1e-6, False, 0, False),
+    ("layer+gelu_tanh", laws.NORM_LAYER, 1e-5, False, laws.ACT_GELU_TANH, False),
+    ("rms+tables+gelu", laws.NORM_RMS, 1e-6, True, laws.ACT_GELU, False),
+    ("tables", 0, 0.0, True, 0, False),
+    ("situ", 0, 0.0, False, laws.ACT_SITU, False),
+    ("swiglu_up", 0, 0.0, False, laws.ACT_SWIGLU, True),
+    ("swiglu_halves", 0, 0.0, False, laws.ACT_SWIGLU, False),
+]
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["int8", "fp8"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("case", PROLOGUES, ids=[c[0] for c in PROLOGUES])
+def test_quantize_prologue_within_one_step(ops, fp8, dtype, case):
+    """The producer prologue folded into the quantize pass, against the CPU law on the same
+    rows. Its norm sums and transcendentals are the platform's, not torch CPU's, so the check is
+    a bound: scales within 1e-5 relative, every dequantized value within one quantization step
+    (int8) or one e4m3 step (fp8), and at most 1% of codes different. SwiGLU rounds silu to the
+    rows' dtype, where a one-ulp float32 difference can move a bf16 value by a whole step (and
+    with the row maximum, the scale): its bounds are 2^-7, two steps and 5%."""
+    name, norm, eps, tables, act, with_up = case
+    m, k = (48, 4112) if fp8 else (48, 3072)
+    gated = act == laws.ACT_SITU or (act == laws.ACT_SWIGLU and not with_up)
+    x = activations(m, 2 * k if gated else k, seed=500 + PROLOGUES.index(case), dtype=dtype)
+    gen = torch.Generator().manual_seed(71)
+    scale = shift = up = None
+    if tables:  # two table rows over the 48 rows: rows_per_entry 24
+        scale = (torch.randn(2, k, generator=gen) * 0.2).to(dtype)
+        shift = (torch.randn(2, k, generator=gen) * 0.2).to(dtype)
+    if with_up:
+        up = activations(m, k, seed=72, dtype=dtype)
+    dev = lambda t: None if t is None else t.to(DEV)  # noqa: E731
+    quantize = ops.fp8_quantize if fp8 else ops.int8_quantize
+    q, s = quantize(x.to(DEV), dev(scale), dev(shift), norm, eps, act, dev(up))
+    rows = laws.prologue(x, scale=scale, shift=shift, norm=norm, eps=eps, activation=act, up=up)
+    if fp8:
+        wq, ws = laws.fp8_quantize(rows)
+        got, want = q.cpu().float(), wq.float()
+        step = (want.abs() * 2.0**-3).clamp(min=2.0**-9)  # one e4m3 step at the value
+    else:
+        wq, ws = laws.quantize_rows_int8(rows, 256)
+        got, want = q.cpu().float(), wq.float()
+        step = torch.ones_like(want)
+    s, ws = s.cpu().reshape(-1, 1), ws.reshape(-1, 1)
+    swiglu = act == laws.ACT_SWIGLU
+    assert ((s - ws).abs() <= (2.0**-7 if swiglu else 1e-5) * ws).all()
+    assert ((got * s - want * ws).abs() <= (2.01 if swiglu else 1.01) * step * ws + 1e-30).all()
+    assert (got != want).float().mean() <= (0.05 if swiglu else 0.01)
+
+
 # ------------------------------------------------------------------------ MXFP8 lane
 
 

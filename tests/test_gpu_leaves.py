@@ -97,6 +97,28 @@ def test_int8_rows_operand_and_out_into_a_column_range():
     assert leaf(xd, prequantized=pre, out=packed[:, :264]).data_ptr() == packed.data_ptr()
 
 
+def test_int8_rows_with_a_prologue():
+    """`int8_rows` with the producer prologue (RMS norm, a two-row modulation table, tanh-GELU)
+    hands the leaf rows quantized in one pass; the linear matches the law on the prologue's
+    rows within tolerance (the prologue's transcendentals are the platform's)."""
+    leaf, data, scale, b = int8_leaf(264, 768, 93)
+    x = activations(130, 768, 94)
+    mod = (torch.randn(2, 768, generator=_gen(95)) * 0.2).to(torch.bfloat16)
+    pre = operands.int8_rows(x.to(DEV), (leaf,), norm="rms", eps=1e-6, scale=mod.to(DEV),
+                             activation="gelu_tanh")  # fmt: skip
+    assert isinstance(pre, operands.PreQuantized) and pre.shape == (130, 768)
+    got = leaf(x.to(DEV), prequantized=pre)
+    rows = laws.prologue(x, scale=mod, norm=laws.NORM_RMS, eps=1e-6,
+                         activation=laws.ACT_GELU_TANH)  # fmt: skip
+    assert_close(got, laws.int8_exact(rows, data, scale, b, 256))
+    gated = activations(130, 2 * 768, 96)
+    pre = operands.int8_rows(gated.to(DEV), (leaf,), activation="situ")
+    assert isinstance(pre, operands.PreQuantized) and pre.shape == (130, 768)
+    got = leaf(gated[:, :768].to(DEV), prequantized=pre)
+    assert_close(got, laws.int8_exact(laws.prologue(gated, activation=laws.ACT_SITU), data,
+                                      scale, b, 256))  # fmt: skip
+
+
 def test_int8_leaf_autocast_dtype():
     leaf, data, scale, _ = int8_leaf(256, 512, 95, bias=False)
     x = activations(40, 512, 96)

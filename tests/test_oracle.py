@@ -397,3 +397,62 @@ def test_svdq_weight_reconstructs_effective_weight():
     codes, scales = laws.svdq_weight(w, p, down, up)
     deq = (laws.unpack_int4(codes).double().reshape(n, -1, 64) * scales.double().unsqueeze(-1)).reshape(n, k)
     assert np.allclose((deq * p.double() + up.double() @ down.double()).numpy(), w.numpy(), rtol=0, atol=1e-12)
+
+
+# ------------------------------------------------------------------- producer prologue
+
+
+def test_prologue_norms_on_closed_forms():
+    """A constant row c: RMS → c/√(c² + eps), layer → 0. An alternating row ±a: layer and RMS
+    both → ±a/√(a² + eps). An identity prologue returns the rows widened."""
+    c, a, eps = 3.0, 0.5, 1e-3
+    const = torch.full((2, 256), c, dtype=torch.bfloat16)
+    rms = laws.prologue(const, norm=laws.NORM_RMS, eps=eps)
+    assert torch.allclose(rms, torch.full_like(rms, c / math.sqrt(c * c + eps)), rtol=2e-7)
+    assert laws.prologue(const, norm=laws.NORM_LAYER, eps=eps).abs().max() == 0
+    alt = torch.tensor([a, -a] * 128, dtype=torch.float16).repeat(3, 1)
+    want = alt.double() / math.sqrt(a * a + eps)
+    for norm in (laws.NORM_LAYER, laws.NORM_RMS):
+        assert torch.allclose(laws.prologue(alt, norm=norm, eps=eps).double(), want, rtol=2e-7)
+    x = torch.randn(5, 64, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    assert torch.equal(laws.prologue(x), x.float())
+
+
+def test_prologue_modulation_tables_and_rows_per_entry():
+    """scale −1 zeroes a row, scale 0 and shift 0 leave it; with zero rows and two table rows
+    over four x rows, rows 0–1 read shift row 0 and rows 2–3 shift row 1."""
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(4, 128, generator=gen).to(torch.bfloat16)
+    assert laws.prologue(x, scale=torch.full((1, 128), -1.0, dtype=torch.bfloat16)).abs().max() == 0
+    zeros = torch.zeros(2, 128, dtype=torch.bfloat16)
+    assert torch.equal(laws.prologue(x, scale=zeros, shift=zeros), x.float())
+    shift = torch.randn(2, 128, generator=gen).to(torch.bfloat16)
+    got = laws.prologue(torch.zeros(4, 128, dtype=torch.bfloat16), shift=shift)
+    assert torch.equal(got[:2], shift[:1].float().expand(2, -1))
+    assert torch.equal(got[2:], shift[1:].float().expand(2, -1))
+
+
+def test_prologue_activations_against_library_routines():
+    """GELU (erf), tanh-GELU, SiTU and SwiGLU against Python's `math` routines in float64 (and
+    torch's `silu`, the reference's eager SwiGLU), value by value."""
+    vals = [-6.0, -2.5, -1.0, -0.25, 0.0, 0.125, 0.75, 1.5, 3.0, 8.0]
+    x = torch.tensor([vals * 2], dtype=torch.float32).to(torch.bfloat16)
+    xs = [float(v) for v in x.float().reshape(-1)]
+    gelu = laws.prologue(x, activation=laws.ACT_GELU).reshape(-1)
+    tanh_gelu = laws.prologue(x, activation=laws.ACT_GELU_TANH).reshape(-1)
+    for got, v in zip(gelu.tolist(), xs):
+        assert abs(got - 0.5 * v * (1 + math.erf(v / math.sqrt(2)))) <= 1e-6 * (1 + abs(v))
+    for got, v in zip(tanh_gelu.tolist(), xs):
+        want = 0.5 * v * (1 + math.tanh(0.79788456 * (v + 0.044715 * v**3)))
+        assert abs(got - want) <= 1e-6 * (1 + abs(v))
+    situ = laws.prologue(x, activation=laws.ACT_SITU).reshape(-1)  # h = first half, g = second
+    half = len(xs) // 2
+    for i, got in enumerate(situ.tolist()):
+        h, g = xs[i], xs[half + i]
+        want = 4 * math.tanh(g / 4) / (1 + math.exp(-g)) * 25 * math.tanh(h / 25)
+        assert abs(got - want) <= 1e-5 * (1 + abs(want))
+    ones = torch.ones_like(x)
+    swiglu = laws.prologue(x, activation=laws.ACT_SWIGLU, up=ones)
+    assert torch.equal(swiglu.to(torch.bfloat16), torch.nn.functional.silu(x.float()).to(torch.bfloat16))
+    halves = laws.prologue(torch.cat([ones, x], -1), activation=laws.ACT_SWIGLU)
+    assert torch.equal(halves, swiglu)
