@@ -196,6 +196,59 @@ def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -
                       "rowwise_quantize_kernel<fp8> + fp8_narrow_kernel"}
 
 
+def _graph_us(torch, launch, per_graph: int, replays: int) -> float:
+    """GPU µs per launch of `launch(raw_stream)`, captured `per_graph` times into a HIP graph on a
+    side stream and replayed."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        launch(side.cuda_stream)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            raw = torch.cuda.current_stream().cuda_stream
+            for _ in range(per_graph):
+                launch(raw)
+    torch.cuda.synchronize()
+    return Timer(torch).run(graph.replay, replays, 2) / per_graph * 1e3
+
+
+def bench_int8_decode(torch, ops, lib, stream, steps: int) -> dict:
+    """The int8.convrot linear at decode size on config 2's weight (M=1, K=3072, N=12288): the
+    fused GEMV (`cozyq_gemv`: rotation, quantization and GEMV in one launch) against the
+    two-launch path (quantize, then the narrow-tile GEMM), each over 8 rotating weight copies
+    (302 MB, beyond the MALL), graph-replayed."""
+    m, k, n, copies = 1, 3072, 12288, 8
+    x = _activations(torch, m, k, 61)
+    weights = [ops.int8_quantize_rot(_weights(torch, n, k, 62 + c), 256) for c in range(copies)]
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    q = torch.empty(m, k, dtype=torch.int8, device="cuda")
+    qs = torch.empty(m, dtype=torch.float32, device="cuda")
+    turn = [0]
+
+    def fused(raw):
+        w, ws = weights[turn[0] % copies]
+        turn[0] += 1
+        _check(lib.cozyq_gemv(0, x.data_ptr(), 0, w.data_ptr(), ws.data_ptr(), None, out.data_ptr(),
+                              0, m, n, k, raw))  # fmt: skip
+
+    def two_launch(raw):
+        w, ws = weights[turn[0] % copies]
+        turn[0] += 1
+        _check(lib.cozyq_quantize(0, 0, x.data_ptr(), 0, q.data_ptr(), qs.data_ptr(), m, k, None,
+                                  None, 0, 0, 1, 0, 0.0, 0, None, raw))  # fmt: skip
+        _check(lib.cozyq_gemm(0, 0, 0, q.data_ptr(), qs.data_ptr(), w.data_ptr(), ws.data_ptr(),
+                              None, out.data_ptr(), n, 0, m, n, k, -1, None, None, raw))  # fmt: skip
+
+    replays = max(4, steps // 8)
+    us = _graph_us(torch, fused, 8 * copies, replays)
+    us_two = _graph_us(torch, two_launch, 8 * copies, replays)
+    nbytes = n * k + n * 4 + m * k * 2 + m * n * 2
+    return {"M": m, "K": k, "N": n, "us": us, "gbs": nbytes / (us * 1e-6) / 1e9,
+            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, "us_quantize_then_gemm": us_two,
+            "kernel": "int8_decode_kernel (rotation + quantize fused with the GEMV)"}
+
+
 def bench_fp8(torch, ops, lib, stream, m: int, steps: int) -> dict:
     k, n = 4096, 14336
     x = _activations(torch, m, k, 33)
@@ -332,6 +385,8 @@ def only(torch, ops, lib, stream, args) -> int:
                    "c3_fp8_small": bench_decode(torch, ops, lib, stream, args.steps, args.warmup, m=16)}
     elif args.only == "mx":
         figures = bench_mx(torch, ops, lib, stream, args.steps)
+    elif args.only == "int8_decode":
+        figures = bench_int8_decode(torch, ops, lib, stream, args.steps)
     else:
         figures = bench_svdq(torch, ops, lib, stream, args.steps)
     print(json.dumps({"only": args.only, **figures}))
@@ -348,7 +403,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=100)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
-    parser.add_argument("--only", choices=("c2", "decode", "fp8", "svdq", "mx", "copy"),
+    parser.add_argument("--only", choices=("c2", "decode", "int8_decode", "fp8", "svdq", "mx", "copy"),
                         help="profiling aid: run one leg (or a plain 256 MiB device copy, the "
                              "counter calibration) --steps times and print its figures only")  # fmt: skip
     args = parser.parse_args()
@@ -376,6 +431,7 @@ def main() -> int:
         configs["c3_fp8"] = [bench_fp8(torch, ops, lib, stream, m, max(10, args.steps // 2))
                              for m in (256, 4096)]  # fmt: skip
         configs["c3_fp8_small"] = [bench_decode(torch, ops, lib, stream, args.steps, args.warmup, m=16)]
+        configs["int8_decode"] = bench_int8_decode(torch, ops, lib, stream, args.steps)
         configs["c4_svdq_w4a4"] = bench_svdq(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["c5_mxfp8"] = bench_mx(torch, ops, lib, stream, max(10, args.steps // 2))
         print("[bench] extra configs done", file=sys.stderr, flush=True)

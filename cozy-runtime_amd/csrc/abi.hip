@@ -87,10 +87,15 @@ int cozyq_quantize_rot(int device, const void* x, int x_half, int8_t* q, float* 
 
 int cozyq_gemv(int device, const void* x, int x_half, const int8_t* w, const float* w_scale,
                const void* bias, void* out, int out_half, int M, int N, int K, void* stream) {
-    (void)device; (void)x; (void)x_half; (void)w; (void)w_scale; (void)bias; (void)out;
-    (void)out_half; (void)stream;
     if (!fits(K, 256) || N < 1 || M < 0) return hipErrorInvalidValue;
-    return hipErrorNotSupported;
+    // The kernel writes two outputs a wave and reads 16 bytes a lane.
+    if (N % 8 || !aligned16(x) || !aligned16(w) || (reinterpret_cast<uintptr_t>(out) & 3))
+        return hipErrorNotSupported;
+    if (M == 0) return hipSuccess;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::int8_linear_small(x, x_half, w, w_scale, bias, out, out_half, M, N, K,
+                                    on(stream));
 }
 
 static int gemm_checked(int device, int fp8, const void* q, const float* scales, const void* w,

@@ -4,6 +4,7 @@
 // caller quantizes once and runs the narrow GEMM (gemm_narrow.hip).
 #include "common.h"
 #include "kernels.h"
+#include "rotate.h"
 
 namespace cozyq {
 namespace {
@@ -209,6 +210,218 @@ __global__ __launch_bounds__(kDThreads) void fp8_decode_kernel(
     }
 }
 
+// The int8 linear for 1..4 rows in one launch (reference: rotate.cu:351-407 `gemv_kernel`):
+// each workgroup rotates (H256/16) and quantizes the activation rows into LDS bit for bit as the
+// CPU law does (internal/int8_linear.py:422-428; the rotation's phases are rotate.h's) while its
+// weight rows stream in, then takes the exact int32 dot products on the int8 MFMA and applies
+// the law's epilogue ((acc·xs)·ws, one cast, + bias in the output dtype). Same structure as the
+// fp8 decode above: activation loads first, the weight stream in 1 KB contiguous loads, and the
+// dot product as the trace of a 16x16x64 MFMA over 16 64-byte pieces of one 1 KB span.
+constexpr int kISpanBatch = 4;  // 1 KB spans of each row a wave has in flight
+
+template <bool kXHalf, bool kOutHalf, bool kBias, int kM, int kChunks>
+__global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ W, const float* __restrict__ ws,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int N, int K) {
+    static_assert(kM * kChunks <= kXLoads, "activation registers");
+    using L = Layout<256>;
+    constexpr int kChunks4 = (kChunks + 1) / 2;  // 4096-element rotation chunks of a row
+    // The rotation's workspace; once every row is rotated, the rows' codes (`stride` bytes each,
+    // zero past K) in the same bytes.
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    float* work = reinterpret_cast<float*>(smem);
+    int8_t* xq = reinterpret_cast<int8_t*>(smem);
+    __shared__ float red[kDWaves][kM];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int spans = (K + 1023) / 1024;
+    const int stride = spans * 1024;
+    const int nw = blockIdx.x * (kDWaves * kRowsPerWave) + wave * kRowsPerWave;  // the wave's first row
+
+    // 1. The activation: this thread's 8-element runs of every row (branch-free buffer loads,
+    // zeros past K), issued before the weight stream so the rotation does not wait for it.
+    uint4 xv[kM][kChunks];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(x + static_cast<int64_t>(m) * K), 0, 2 * K, 0x00020000);
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) {
+            const int e = c * (kDThreads * 8) + tid * 8;
+            xv[m][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, 2 * e, 0, 0));
+        }
+    }
+    asm volatile("" ::: "memory");  // the weight loads stay behind the activation's
+
+    // 2. The weight stream: kISpanBatch 1 KB spans of each of the wave's rows.
+    __amdgpu_buffer_rsrc_t wr[kRowsPerWave];
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave; ++i)
+        wr[i] = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t*>(W + static_cast<int64_t>(min(nw + i, N - 1)) * K), 0, K, 0x00020000);
+    uint4 wv[kRowsPerWave][kISpanBatch];
+    auto issue = [&](int first) {
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave; ++i)
+#pragma unroll
+            for (int b = 0; b < kISpanBatch; ++b) {
+                const int k = (first + b) * 1024 + 16 * lane;  // >= K reads zeros
+                wv[i][b] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr[i], k, 0, kStreamPolicy));
+            }
+    };
+    issue(0);
+
+    // 3. Each row rotated chunk by chunk through the workspace (phase 1 from the registers:
+    // the thread's runs at tid·8 and 2048 + tid·8 of the chunk), its amax, then the codes.
+    float rot[kM][kChunks4][16];
+    float amax[kM];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        amax[m] = 0.0f;
+#pragma unroll
+        for (int c4 = 0; c4 < kChunks4; ++c4) {
+            const int base = c4 * kChunk;
+            if (base >= K) break;
+            const int width = min(kChunk, K - base);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int c = 2 * c4 + h;
+                const int e = h * (kDThreads * 8) + tid * 8;  // within the chunk
+                if (c >= kChunks || e >= width) continue;
+                const uint32_t w4[4] = {xv[m][c].x, xv[m][c].y, xv[m][c].z, xv[m][c].w};
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[2 * i] = widen<kXHalf>(static_cast<uint16_t>(w4[i] & 0xffffu));
+                    v[2 * i + 1] = widen<kXHalf>(static_cast<uint16_t>(w4[i] >> 16));
+                }
+                const int g = e / 256, within = e % 256;
+                float* dst = work + L::at(g, within / 16, within % 16);
+                *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<float4*>(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
+            rotate_lds_chunk<256, kDThreads>(work, width, tid, rot[m][c4], amax[m]);
+            __syncthreads();
+        }
+        for (int off = 32; off > 0; off >>= 1) amax[m] = fmaxf(amax[m], __shfl_xor(amax[m], off));
+        if (lane == 0) red[wave][m] = amax[m];
+    }
+    __syncthreads();
+    float scale[kM];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        float v = red[0][m];
+#pragma unroll
+        for (int w = 1; w < kDWaves; ++w) v = fmaxf(v, red[w][m]);
+        scale[m] = fmaxf(v / 127.0f, kScaleFloor);
+    }
+    // The codes: the thread's 16-run (group tid / 16, run tid % 16) of each chunk; zeros past K.
+    const int g = tid / 16, hi = tid % 16;
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        const float s = scale[m];
+        const float rs = 1.0f / s;
+        const bool fast = s < __builtin_huge_valf();  // an infinite scale divides
+#pragma unroll
+        for (int c4 = 0; c4 < kChunks4; ++c4) {
+            const int at = c4 * kChunk + g * 256 + hi * 16;
+            if (at >= stride) continue;
+            uint32_t packed[4] = {0, 0, 0, 0};
+            if (at < K) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int8_t c = fast ? q8<true>(rot[m][c4][i], s, rs) : q8<false>(rot[m][c4][i], s, rs);
+                    packed[i / 4] |= static_cast<uint32_t>(static_cast<uint8_t>(c)) << (8 * (i % 4));
+                }
+            }
+            *reinterpret_cast<uint4*>(xq + m * stride + at) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        }
+    }
+    __syncthreads();
+
+    // 4. Products: per weight row, per activation row, the trace accumulates over the spans.
+    i32x4 acc[kRowsPerWave][kM];
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave; ++i)
+#pragma unroll
+        for (int m = 0; m < kM; ++m) acc[i][m] = i32x4{0, 0, 0, 0};
+    for (int first = 0; first < spans; first += kISpanBatch) {
+        if (first != 0) issue(first);
+#pragma unroll
+        for (int b = 0; b < kISpanBatch; ++b) {
+            if (first + b >= spans) break;
+            i32x4 xb[kM];
+#pragma unroll
+            for (int m = 0; m < kM; ++m)
+                xb[m] = *reinterpret_cast<const i32x4*>(xq + m * stride + (first + b) * 1024 + 16 * lane);
+#pragma unroll
+            for (int i = 0; i < kRowsPerWave; ++i) {
+                const i32x4 a = __builtin_bit_cast(i32x4, wv[i][b]);
+#pragma unroll
+                for (int m = 0; m < kM; ++m) acc[i][m] = mfma_i8(a, xb[m], acc[i][m]);
+            }
+        }
+    }
+
+    // 5. The trace: D[a][a] sits in lane a + 16·(a/4), register a % 4; sum those 16 lanes.
+    const int a = lane & 15;
+    const bool diagonal = (lane >> 4) == (a >> 2);
+    int dot[kRowsPerWave][kM];
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave; ++i)
+#pragma unroll
+        for (int m = 0; m < kM; ++m) {
+            const i32x4 d = acc[i][m];
+            const int r = a & 3;
+            int v = r == 0 ? d[0] : (r == 1 ? d[1] : (r == 2 ? d[2] : d[3]));
+            v = diagonal ? v : 0;
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            dot[i][m] = v;
+        }
+    if (lane != 0 || nw >= N) return;  // N % 8 == 0: a wave's rows are all in or all out
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        uint32_t o[(kRowsPerWave + 1) / 2];
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave; ++i) {
+            // internal/int8_linear.py:445-448 then :276: (acc·xs)·ws, cast, + bias in the output dtype.
+            const float v = __fmul_rn(__fmul_rn(static_cast<float>(dot[i][m]), scale[m]), ws[nw + i]);
+            uint32_t h = narrow<kOutHalf>(v);
+            if constexpr (kBias)
+                h = narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(bias[nw + i])));
+            o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
+        }
+        uint16_t* dst = out + static_cast<int64_t>(m) * N + nw;
+        static_assert(kRowsPerWave == 2, "the stores below write two outputs");
+        *reinterpret_cast<uint32_t*>(dst) = o[0];
+    }
+}
+
+template <bool kXHalf, bool kOutHalf, bool kBias>
+hipError_t launch_int8_decode(const uint16_t* x, const int8_t* w, const float* ws,
+                              const uint16_t* bias, uint16_t* out, int M, int N, int K,
+                              hipStream_t s) {
+    const int blocks = (N + kDWaves * kRowsPerWave - 1) / (kDWaves * kRowsPerWave);
+    const int64_t codes = static_cast<int64_t>(M) * ((K + 1023) / 1024) * 1024;
+    const int64_t work = static_cast<int64_t>(Layout<256>::kFloats) * 4;
+    const int64_t lds = codes > work ? codes : work;
+    const int chunks = (K + kDThreads * 8 - 1) / (kDThreads * 8);
+#define COZYQ_ROWS(R, C)                                                                           \
+    if (M == R && chunks <= C) {                                                                   \
+        int8_decode_kernel<kXHalf, kOutHalf, kBias, R, C><<<blocks, kDThreads, lds, s>>>(x, w, ws, bias, out, N, K); \
+        return hipGetLastError();                                                                  \
+    }
+    COZYQ_ROWS(1, 2)
+    COZYQ_ROWS(1, 8)
+    COZYQ_ROWS(2, 2)
+    COZYQ_ROWS(2, 4)
+    COZYQ_ROWS(3, 2)
+    COZYQ_ROWS(4, 2)
+#undef COZYQ_ROWS
+    return hipErrorNotSupported;
+}
+
 template <bool kXHalf, bool kOutHalf, bool kBias>
 hipError_t launch_decode(const uint16_t* x, const uint8_t* w, const float* ws,
                          const uint16_t* bias, uint16_t* out, int M, int N, int K, hipStream_t s) {
@@ -243,6 +456,29 @@ hipError_t fp8_linear_small(const void* x, bool x_half, const uint8_t* w, const 
 #define COZYQ_CASE(XH, OH, B)                                                                      \
     if (x_half == XH && out_half == OH && (bias != nullptr) == B)                                  \
         return launch_decode<XH, OH, B>(xp, w, ws, bp, op, M, N, K, s);
+    COZYQ_CASE(false, false, false)
+    COZYQ_CASE(false, false, true)
+    COZYQ_CASE(false, true, false)
+    COZYQ_CASE(false, true, true)
+    COZYQ_CASE(true, false, false)
+    COZYQ_CASE(true, false, true)
+    COZYQ_CASE(true, true, false)
+    COZYQ_CASE(true, true, true)
+#undef COZYQ_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t int8_linear_small(const void* x, bool x_half, const int8_t* w, const float* ws,
+                             const void* bias, void* out, bool out_half, int M, int N, int K,
+                             hipStream_t s) {
+    // 1..4 rows whose activation fits the registers (M·K <= 16384); the rest is quantize + GEMM.
+    if (M < 1 || M > 4 || static_cast<int64_t>(M) * K > kXLoads * kDThreads * 8) return hipErrorNotSupported;
+    auto xp = static_cast<const uint16_t*>(x);
+    auto bp = static_cast<const uint16_t*>(bias);
+    auto op = static_cast<uint16_t*>(out);
+#define COZYQ_CASE(XH, OH, B)                                                                      \
+    if (x_half == XH && out_half == OH && (bias != nullptr) == B)                                  \
+        return launch_int8_decode<XH, OH, B>(xp, w, ws, bp, op, M, N, K, s);
     COZYQ_CASE(false, false, false)
     COZYQ_CASE(false, false, true)
     COZYQ_CASE(false, true, false)

@@ -50,6 +50,11 @@ hipError_t gemm_int8_narrow(const int8_t* q, const float* xs, const int8_t* w, c
                             const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
                             int K, int epilogue, hipStream_t s);
 
+// The fused int8 linear for 1..4 rows (rotate H256 + quantize + GEMV in one launch);
+// hipErrorNotSupported past M·K = 16384.
+hipError_t int8_linear_small(const void* x, bool x_half, const int8_t* w, const float* ws,
+                             const void* bias, void* out, bool out_half, int M, int N, int K,
+                             hipStream_t s);
 hipError_t fp8_linear_small(const void* x, bool x_half, const uint8_t* w, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
                             hipStream_t s);

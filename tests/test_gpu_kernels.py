@@ -366,6 +366,61 @@ def test_int8_linear_bit_exact(ops, shape, dtype, bias):
     assert torch.equal(got.cpu(), want)
 
 
+GEMV_SHAPES = [(1, 256), (1, 768), (1, 3072), (1, 4096), (1, 8192), (1, 12288), (1, 16384),
+               (2, 3072), (2, 8192), (3, 1024), (3, 4096), (4, 2304), (4, 4096)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("shape", GEMV_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_int8_gemv_bit_exact(ops, shape, dtype):
+    """The fused few-row int8 linear (`cozyq_gemv`: rotation, per-row int8 and the GEMV in one
+    launch) is served for M <= 4, M·K <= 16384, and equals the CPU law bit for bit: codes from
+    the rotation, exact int32 products, the epilogue's roundings. Rows include an all-zero row
+    (the scale floor) and an outlier channel; N = 1032 leaves a ragged last workgroup."""
+    from cozyq import _lib
+
+    m, k = shape
+    n = 1032
+    gen = torch.Generator().manual_seed(20261210 + 7 * m + k)
+    data = torch.randint(-127, 128, (n, k), generator=gen, dtype=torch.int8)
+    scale = (torch.randn(n, generator=gen).abs() + 0.5) * 1e-3
+    x = torch.randn(m, k, generator=gen)
+    x[:, k // 3] *= 40
+    if m > 1:
+        x[1] = 0
+    x = x.to(dtype)
+    for b in (None, torch.randn(n, generator=gen).to(dtype)):
+        out = torch.empty(m, n, dtype=dtype, device=DEV)
+        xd, wd, sd = x.to(DEV), data.to(DEV), scale.to(DEV)
+        bd = None if b is None else b.to(DEV)
+        code = _lib.load().cozyq_gemv(0, xd.data_ptr(), int(dtype == torch.float16), wd.data_ptr(),
+                                      sd.data_ptr(), None if bd is None else bd.data_ptr(),
+                                      out.data_ptr(), int(dtype == torch.float16), m, n, k,
+                                      torch.cuda.current_stream().cuda_stream)  # fmt: skip
+        assert code == 0, _lib.error_name(code)
+        assert torch.equal(out.cpu(), laws.int8_linear(x, data, scale, b, dtype))
+
+
+def test_int8_gemv_declines_wide_rows(ops):
+    """Past M·K = 16384 the GEMV answers NOT_SUPPORTED and `int8_linear` quantizes + GEMMs, as
+    the reference's caller does (`internal/prebuilt.py:99-118`): still bit-exact."""
+    from cozyq import _lib
+
+    lib = _lib.load()
+    m, n, k = 2, 264, 12288
+    gen = torch.Generator().manual_seed(5)
+    data = torch.randint(-127, 128, (n, k), generator=gen, dtype=torch.int8)
+    scale = (torch.randn(n, generator=gen).abs() + 0.5) * 1e-3
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    xd, wd, sd = x.to(DEV), data.to(DEV), scale.to(DEV)
+    code = lib.cozyq_gemv(0, xd.data_ptr(), 0, wd.data_ptr(), sd.data_ptr(), None, out.data_ptr(),
+                          0, m, n, k, torch.cuda.current_stream().cuda_stream)  # fmt: skip
+    assert code == lib.cozyq_not_supported()
+    got = ops.int8_linear(xd, wd, sd, None, torch.bfloat16)
+    assert torch.equal(got.cpu(), laws.int8_linear(x, data, scale, None, torch.bfloat16))
+
+
 @pytest.mark.parametrize("rotation", [0, 128, 256])
 def test_int8_gemm_rotation_lanes_and_gelu(ops, rotation):
     m, n, k = 200, 264, 1024
