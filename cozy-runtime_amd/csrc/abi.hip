@@ -88,8 +88,8 @@ int cozyq_quantize_rot(int device, const void* x, int x_half, int8_t* q, float* 
 int cozyq_gemv(int device, const void* x, int x_half, const int8_t* w, const float* w_scale,
                const void* bias, void* out, int out_half, int M, int N, int K, void* stream) {
     if (!fits(K, 256) || N < 1 || M < 0) return hipErrorInvalidValue;
-    // The kernel writes two outputs a wave and reads 16 bytes a lane.
-    if (N % 8 || !aligned16(x) || !aligned16(w) || (reinterpret_cast<uintptr_t>(out) & 3))
+    // The kernel writes four outputs (8 bytes) a wave and reads 16 bytes a lane.
+    if (N % 8 || !aligned16(x) || !aligned16(w) || (reinterpret_cast<uintptr_t>(out) & 7))
         return hipErrorNotSupported;
     if (M == 0) return hipSuccess;
     const OnDevice guard(device);

@@ -218,6 +218,9 @@ __global__ __launch_bounds__(kDThreads) void fp8_decode_kernel(
 // fp8 decode above: activation loads first, the weight stream in 1 KB contiguous loads, and the
 // dot product as the trace of a 16x16x64 MFMA over 16 64-byte pieces of one 1 KB span.
 constexpr int kISpanBatch = 4;  // 1 KB spans of each row a wave has in flight
+// Weight rows a wave owns: 4 measured 5% faster than 2 at M=1, K=3072, N=12288 on MI355X (the
+// workgroup's rotation is shared by twice the rows), 8 slower.
+constexpr int kIRows = 4;
 
 template <bool kXHalf, bool kOutHalf, bool kBias, int kM, int kChunks>
 __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
@@ -237,7 +240,7 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int spans = (K + 1023) / 1024;
     const int stride = spans * 1024;
-    const int nw = blockIdx.x * (kDWaves * kRowsPerWave) + wave * kRowsPerWave;  // the wave's first row
+    const int nw = blockIdx.x * (kDWaves * kIRows) + wave * kIRows;  // the wave's first row
 
     // 1. The activation: this thread's 8-element runs of every row (branch-free buffer loads,
     // zeros past K), issued before the weight stream so the rotation does not wait for it.
@@ -255,15 +258,15 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
     asm volatile("" ::: "memory");  // the weight loads stay behind the activation's
 
     // 2. The weight stream: kISpanBatch 1 KB spans of each of the wave's rows.
-    __amdgpu_buffer_rsrc_t wr[kRowsPerWave];
+    __amdgpu_buffer_rsrc_t wr[kIRows];
 #pragma unroll
-    for (int i = 0; i < kRowsPerWave; ++i)
+    for (int i = 0; i < kIRows; ++i)
         wr[i] = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<int8_t*>(W + static_cast<int64_t>(min(nw + i, N - 1)) * K), 0, K, 0x00020000);
-    uint4 wv[kRowsPerWave][kISpanBatch];
+    uint4 wv[kIRows][kISpanBatch];
     auto issue = [&](int first) {
 #pragma unroll
-        for (int i = 0; i < kRowsPerWave; ++i)
+        for (int i = 0; i < kIRows; ++i)
 #pragma unroll
             for (int b = 0; b < kISpanBatch; ++b) {
                 const int k = (first + b) * 1024 + 16 * lane;  // >= K reads zeros
@@ -341,9 +344,9 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
     __syncthreads();
 
     // 4. Products: per weight row, per activation row, the trace accumulates over the spans.
-    i32x4 acc[kRowsPerWave][kM];
+    i32x4 acc[kIRows][kM];
 #pragma unroll
-    for (int i = 0; i < kRowsPerWave; ++i)
+    for (int i = 0; i < kIRows; ++i)
 #pragma unroll
         for (int m = 0; m < kM; ++m) acc[i][m] = i32x4{0, 0, 0, 0};
     for (int first = 0; first < spans; first += kISpanBatch) {
@@ -356,7 +359,7 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
             for (int m = 0; m < kM; ++m)
                 xb[m] = *reinterpret_cast<const i32x4*>(xq + m * stride + (first + b) * 1024 + 16 * lane);
 #pragma unroll
-            for (int i = 0; i < kRowsPerWave; ++i) {
+            for (int i = 0; i < kIRows; ++i) {
                 const i32x4 a = __builtin_bit_cast(i32x4, wv[i][b]);
 #pragma unroll
                 for (int m = 0; m < kM; ++m) acc[i][m] = mfma_i8(a, xb[m], acc[i][m]);
@@ -367,9 +370,9 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
     // 5. The trace: D[a][a] sits in lane a + 16·(a/4), register a % 4; sum those 16 lanes.
     const int a = lane & 15;
     const bool diagonal = (lane >> 4) == (a >> 2);
-    int dot[kRowsPerWave][kM];
+    int dot[kIRows][kM];
 #pragma unroll
-    for (int i = 0; i < kRowsPerWave; ++i)
+    for (int i = 0; i < kIRows; ++i)
 #pragma unroll
         for (int m = 0; m < kM; ++m) {
             const i32x4 d = acc[i][m];
@@ -379,12 +382,12 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
             for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
             dot[i][m] = v;
         }
-    if (lane != 0 || nw >= N) return;  // N % 8 == 0: a wave's rows are all in or all out
+    if (lane != 0 || nw >= N) return;  // N % 4 == 0: a wave's rows are all in or all out
 #pragma unroll
     for (int m = 0; m < kM; ++m) {
-        uint32_t o[(kRowsPerWave + 1) / 2];
+        uint32_t o[(kIRows + 1) / 2];
 #pragma unroll
-        for (int i = 0; i < kRowsPerWave; ++i) {
+        for (int i = 0; i < kIRows; ++i) {
             // internal/int8_linear.py:445-448 then :276: (acc·xs)·ws, cast, + bias in the output dtype.
             const float v = __fmul_rn(__fmul_rn(static_cast<float>(dot[i][m]), scale[m]), ws[nw + i]);
             uint32_t h = narrow<kOutHalf>(v);
@@ -393,8 +396,8 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
             o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
         }
         uint16_t* dst = out + static_cast<int64_t>(m) * N + nw;
-        static_assert(kRowsPerWave == 2, "the stores below write two outputs");
-        *reinterpret_cast<uint32_t*>(dst) = o[0];
+        static_assert(kIRows == 4, "the store below writes four outputs");
+        *reinterpret_cast<uint2*>(dst) = make_uint2(o[0], o[1]);
     }
 }
 
@@ -402,7 +405,7 @@ template <bool kXHalf, bool kOutHalf, bool kBias>
 hipError_t launch_int8_decode(const uint16_t* x, const int8_t* w, const float* ws,
                               const uint16_t* bias, uint16_t* out, int M, int N, int K,
                               hipStream_t s) {
-    const int blocks = (N + kDWaves * kRowsPerWave - 1) / (kDWaves * kRowsPerWave);
+    const int blocks = (N + kDWaves * kIRows - 1) / (kDWaves * kIRows);
     const int64_t codes = static_cast<int64_t>(M) * ((K + 1023) / 1024) * 1024;
     const int64_t work = static_cast<int64_t>(Layout<256>::kFloats) * 4;
     const int64_t lds = codes > work ? codes : work;
