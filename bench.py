@@ -249,6 +249,47 @@ def bench_int8_decode(torch, ops, lib, stream, steps: int) -> dict:
             "kernel": "int8_decode_kernel (rotation + quantize fused with the GEMV)"}
 
 
+def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
+    """The w4a8.convrot GEMM on config 2's weight shape (K=3072, N=12288; 4-bit codes + E4M3
+    group scales, 21.2 MB against int8's 37.7 MB) at M = 1, 16, 256 (the fused GEMM, codes
+    unpacked in registers) and 4096 (unpack once + the 256x256 int8 GEMM), int8.convrot's
+    operand precomputed; bias + bf16 out."""
+    from cozyq import prebuilt
+
+    k, n = 3072, 12288
+    gen = torch.Generator(device="cuda").manual_seed(91)
+    codes = torch.randint(0, 256, (n, k // 2), generator=gen, device="cuda", dtype=torch.uint8)
+    gs = (torch.randn(n, k // 16, generator=gen, device="cuda").abs() * 40 + 16).clamp(max=440)
+    w = prebuilt.W4a8(codes, gs.to(torch.float8_e4m3fn),
+                      (torch.rand(n, generator=gen, device="cuda") + 0.5) * 1e-3, None)  # fmt: skip
+    bias = torch.randn(n, generator=gen, device="cuda").to(torch.bfloat16)
+    levels = torch.empty(n, k, dtype=torch.int8, device="cuda")
+    rows = []
+    for m in (1, 16, 256, 4096):
+        q, s = ops.int8_quantize(_activations(torch, m, k, 92))
+        out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        args = (q.data_ptr(), s.data_ptr())
+
+        def fused():
+            _check(lib.cozyq_w4a8_gemm(0, *args, codes.data_ptr(), w.group_scale.data_ptr(), None,
+                                       w.scale.data_ptr(), bias.data_ptr(), out.data_ptr(), 0, m, n,
+                                       k, -1, stream))  # fmt: skip
+
+        def unpacked():
+            _check(lib.cozyq_w4a8_unpack(0, codes.data_ptr(), w.group_scale.data_ptr(), None,
+                                         levels.data_ptr(), n, k, stream))  # fmt: skip
+            _check(lib.cozyq_gemm(0, 0, 0, *args, levels.data_ptr(), w.scale.data_ptr(),
+                                  bias.data_ptr(), out.data_ptr(), n, 0, m, n, k, -1, None, None,
+                                  stream))  # fmt: skip
+
+        ms = Timer(torch).run(fused if m < prebuilt.UNPACK_ROWS else unpacked, steps, 5)
+        weight_bytes = n * k // 2 + n * k // 16 + n * 4
+        rows.append({"M": m, "us": ms * 1e3, "tops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
+                     "weight_gbs": weight_bytes / (ms * 1e-3) / 1e9,
+                     "path": "fused narrow GEMM" if m < prebuilt.UNPACK_ROWS else "unpack + int8 GEMM"})
+    return {"K": k, "N": n, "rows": rows}
+
+
 def bench_fp8(torch, ops, lib, stream, m: int, steps: int) -> dict:
     k, n = 4096, 14336
     x = _activations(torch, m, k, 33)
@@ -387,6 +428,8 @@ def only(torch, ops, lib, stream, args) -> int:
         figures = bench_mx(torch, ops, lib, stream, args.steps)
     elif args.only == "int8_decode":
         figures = bench_int8_decode(torch, ops, lib, stream, args.steps)
+    elif args.only == "w4a8":
+        figures = bench_w4a8(torch, ops, lib, stream, args.steps)
     else:
         figures = bench_svdq(torch, ops, lib, stream, args.steps)
     print(json.dumps({"only": args.only, **figures}))
@@ -403,7 +446,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=100)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
-    parser.add_argument("--only", choices=("c2", "decode", "int8_decode", "fp8", "svdq", "mx", "copy"),
+    parser.add_argument("--only", choices=("c2", "decode", "int8_decode", "w4a8", "fp8", "svdq", "mx", "copy"),
                         help="profiling aid: run one leg (or a plain 256 MiB device copy, the "
                              "counter calibration) --steps times and print its figures only")  # fmt: skip
     args = parser.parse_args()
@@ -432,6 +475,7 @@ def main() -> int:
                              for m in (256, 4096)]  # fmt: skip
         configs["c3_fp8_small"] = [bench_decode(torch, ops, lib, stream, args.steps, args.warmup, m=16)]
         configs["int8_decode"] = bench_int8_decode(torch, ops, lib, stream, args.steps)
+        configs["w4a8"] = bench_w4a8(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["c4_svdq_w4a4"] = bench_svdq(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["c5_mxfp8"] = bench_mx(torch, ops, lib, stream, max(10, args.steps // 2))
         print("[bench] extra configs done", file=sys.stderr, flush=True)

@@ -33,6 +33,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_float, c_int, _P, _P],
     ),
     "cozyq_quantize_rot": (c_int, [c_int, _P, c_int, _P, _P, c_int, c_int, c_int, _P]),
+    "cozyq_w4a8_gemm": (c_int, [c_int, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int,
+                                c_int, _P]),
+    "cozyq_w4a8_unpack": (c_int, [c_int, _P, _P, _P, _P, c_int, c_int, _P]),
     "cozyq_gemv": (c_int, [c_int, _P, c_int, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P]),
     "cozyq_gemm": (
         c_int,

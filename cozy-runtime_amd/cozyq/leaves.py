@@ -17,7 +17,7 @@ from collections.abc import Mapping, Sequence
 from dataclasses import dataclass
 from typing import Any, ClassVar
 
-from cozyq import fp8_linear, int8_linear, layout
+from cozyq import fp8_linear, int8_linear, layout, prebuilt, w4a8_linear
 from cozyq.operands import INT8_CONVROT, ROWWISE_FP8, PreQuantized, read, shared_operand
 
 Tensor = Any
@@ -25,9 +25,10 @@ Dtype = Any
 Params = tuple[tuple[str, object], ...]
 
 MXFP8 = "cozy.mxfp8.native-leaf/2"
+W4A8 = "cozy.w4a8-convrot256.native-leaf/1"
 SVDQ_INT4 = "cozyq.svdq-int4g64.native-leaf/1"
 #: The operand geometry each 8-bit leaf's GEMM reads (`internal/encoding/leaves.py:207`).
-OPERANDS = {INT8_CONVROT: INT8_CONVROT, ROWWISE_FP8: ROWWISE_FP8}
+OPERANDS = {INT8_CONVROT: INT8_CONVROT, ROWWISE_FP8: ROWWISE_FP8, W4A8: INT8_CONVROT}
 #: The 8-bit leaves' ops by provider (`internal/encoding/leaves.py:355`).
 _NATIVE_OPS: dict[str, Any] = {INT8_CONVROT: int8_linear, ROWWISE_FP8: fp8_linear}
 #: Rows a leaf sends to its op's one-launch linear instead of a shared operand: the int8 GEMV
@@ -176,6 +177,43 @@ def _native_leaf_class(torch: Any) -> Any:
     return NativeLinear
 
 
+def _w4a8_leaf_class(torch: Any) -> Any:
+    """`NativeLinear` over w4a8's roles (`internal/encoding/leaves.py:900-942`): its GEMM
+    (`w4a8_linear`) on int8.convrot's operand, shared with the int8 leaves."""
+    cached = getattr(_w4a8_leaf_class, "_cached", None)
+    if cached is not None:
+        return cached
+
+    class W4a8Linear(_native_leaf_class(torch)):
+        def weights(self) -> prebuilt.W4a8:
+            return prebuilt.W4a8(read(self.data), read(self.group_scale), read(self.scale),
+                                 read(self._buffers.get("codebook")))  # fmt: skip
+
+        def linear(self, x, prequantized, out=None):
+            out_dtype = self.out_dtype
+            if isinstance(x, PreQuantized):
+                if torch.is_autocast_enabled(x.payload.device.type):
+                    out_dtype = torch.get_autocast_dtype(x.payload.device.type)
+                return w4a8_linear.gemm(torch, x, self.weights(), read(self.bias), out_dtype, out)
+            cast = x
+            if torch.is_autocast_enabled(x.device.type):
+                out_dtype = torch.get_autocast_dtype(x.device.type)
+                cast = x.to(out_dtype)
+            if prequantized is None or prequantized.provider != INT8_CONVROT:
+                capturing = x.is_cuda and torch.cuda.is_current_stream_capturing()
+                sibling = None if capturing else self
+                prequantized = shared_operand(x, INT8_CONVROT,
+                                              lambda: int8_linear.quantize(torch, cast), sibling)  # fmt: skip
+            if prequantized is not None:
+                return w4a8_linear.gemm(torch, prequantized, self.weights(), read(self.bias),
+                                        out_dtype, out)  # fmt: skip
+            return int8_linear.landed(
+                w4a8_linear.linear(torch, cast, self.weights(), read(self.bias), out_dtype), out)
+
+    _w4a8_leaf_class._cached = W4a8Linear
+    return W4a8Linear
+
+
 def _svdq_leaf_class(torch: Any) -> Any:
     """The W4A4 leaf: smoothing, int4 activations and the low-rank input in one launch, then
     the GEMM with the low-rank add and the bias in its epilogue (one rounding)."""
@@ -316,6 +354,46 @@ class Int8ConvRotNativeLeaf(_Provider):
 
 
 @dataclass(frozen=True, slots=True)
+class W4a8NativeLeaf(_Provider):
+    """`w4a8.convrot` encoded GEMM (`internal/encoding/leaves.py:945-1045`): 4-bit codes in
+    int8.convrot's rotated basis with E4M3 group scales per 16 and a row scale (4.5 bits a
+    weight), unpacked to int8 levels in registers and multiplied with int8.convrot's operand
+    on the int8 MFMA: W4A8 with int8.convrot's epilogue. It takes group 16, rotation 256, and a
+    codebook or the uniform grid."""
+
+    encoding: str = "w4a8.convrot"
+    params: Params = ()
+
+    name = property(lambda self: W4A8)
+    schemes = property(lambda self: frozenset({"w4a8.convrot"}))
+    code_revision = property(lambda self: "1")
+    suite = property(lambda self: "w4a8-native")
+    formats = property(lambda self: frozenset({"int8"}))
+    required = property(lambda self: frozenset({"weight", "group_scale", "scale"}))
+    optional = property(lambda self: frozenset({"codebook"}))
+
+    def supports(self, shape: Sequence[int], params: Mapping[str, object]) -> str:
+        """Rank 2; group 16 and int8.convrot's 256-blocks; N divisible by 8."""
+        why = _rank2(shape)
+        wanted = {"group_size": 16, "rotation": "kron_regular_h4", "rotation_size": INT8_ROTATION}
+        if not why and dict(params) != wanted:
+            why = f"the w4a8 GEMM reads {wanted}; this weight's are {dict(params)}"
+        if not why and (int(shape[1]) % INT8_ROTATION or int(shape[0]) % 8):
+            why = f"the w4a8 GEMM needs K % {INT8_ROTATION} and N % 8 == 0; this is {list(shape)}"
+        return why
+
+    def leaf(self, torch: Any, parts: Mapping[str, Tensor], replaced: object, out_dtype: Dtype) -> Any:
+        codes = parts["weight"]
+        roles = {"weight": codes, "group_scale": parts["group_scale"],
+                 "scale": parts["scale"].to(torch.float32)}  # fmt: skip
+        if "codebook" in parts:
+            roles["codebook"] = parts["codebook"].to(torch.float32)
+        return _w4a8_leaf_class(torch)(None, roles, getattr(replaced, "bias", None), out_dtype,
+                                       self.name, self.encoding, 2 * int(codes.shape[1]),
+                                       int(codes.shape[0]))  # fmt: skip
+
+
+@dataclass(frozen=True, slots=True)
 class MicroScaledNativeLeaf(_Provider):
     """mxfp8 encoded GEMM (`internal/encoding/leaves.py:1427-1546`) on gfx950's E8M0-scaled
     MFMA: the e4m3 payload and its E8M0 grid stay resident; activations are quantized per
@@ -414,7 +492,8 @@ def launch_providers() -> dict[str, tuple[Any, ...]]:
     """Scheme -> its encoded-GEMM providers on gfx950, in the reference's preference order
     (`internal/encoding/selection.py:248-274`, the encoded_gemm entries)."""
     out: dict[str, list[Any]] = {}
-    for build in (RowwiseNativeLeaf, Int8ConvRotNativeLeaf, SvdqInt4NativeLeaf, MicroScaledNativeLeaf):
+    for build in (RowwiseNativeLeaf, Int8ConvRotNativeLeaf, W4a8NativeLeaf, SvdqInt4NativeLeaf,
+                  MicroScaledNativeLeaf):
         for scheme in sorted(build().schemes):
             out.setdefault(scheme, []).append(build(scheme))
     return {scheme: tuple(candidates) for scheme, candidates in out.items()}

@@ -47,6 +47,12 @@ class _Format:
 #: [hidden | gate] (or, for SwiGLU without `up`, [up | gate]) halves.
 SITU, SWIGLU = 3, 4
 
+#: `w4a8_gemm`'s config that unpacks the codes once and multiplies on the int8 GEMM, and the
+#: rows from which it is chosen (`internal/prebuilt.py:48-49`): past 256 rows the 256x256 int8
+#: GEMM outruns the fused narrow-tile one, and the unpack is one pass over the weight.
+UNPACK = 3
+UNPACK_ROWS = 257
+
 INT8, FP8 = _Format("int8", False, 256), _Format("fp8", True, 16)
 MX = _Format("mxfp8", True, 128)
 SVDQ = _Format("svdq-int4", False, INT4_GROUP)
@@ -56,6 +62,18 @@ def _torch():
     import torch
 
     return torch
+
+
+@dataclass(frozen=True)
+class W4a8:
+    """One `w4a8.convrot` weight as the GEMM reads it (`internal/prebuilt.py:437-446`): `codes`
+    bytes [N, K/2] (even k in the low nibble), E4M3 `group_scale` [N, K/16], float32 row
+    `scale` [N] and `codebook` [16] (None: the uniform grid `q - 8`)."""
+
+    codes: Tensor
+    group_scale: Tensor
+    scale: Tensor
+    codebook: Tensor | None
 
 
 def _ptr(t: Tensor | None) -> int | None:
@@ -144,6 +162,86 @@ class Prebuilt:
         eps: float = 0.0, activation: int = 0, up: Tensor | None = None,
     ) -> tuple[Tensor, Tensor]:
         return self._quantize(FP8, x, scale, shift, norm, eps, activation, up)
+
+    def w4a8_linear(self, x: Tensor, w: W4a8, bias: Tensor | None, out_dtype: Dtype) -> Tensor:
+        """`internal/prebuilt.py:176-178`: int8.convrot's operand, then `w4a8_gemm`."""
+        q, scales = self.int8_quantize(x)
+        return self.w4a8_gemm(q, scales, w, bias, out_dtype).view(*x.shape[:-1], w.codes.shape[0])
+
+    def w4a8_gemm(
+        self, q: Tensor, scales: Tensor, w: W4a8, bias: Tensor | None, out_dtype: Dtype,
+        config: int = -1,
+    ) -> Tensor:
+        """`internal/prebuilt.py:180-222`: `q @ unpack(w).T`, both scales and the bias. From
+        `UNPACK_ROWS` rows the codes unpack once to int8 and the int8 GEMM multiplies them
+        (config `UNPACK`); fewer rows take the fused GEMM. Every config is the same law, bit for
+        bit."""
+        torch = self.torch
+        if q.dtype != torch.int8 or q.dim() != 2 or not q.is_contiguous() or q.data_ptr() % 16:
+            raise ValueError("w4a8_gemm: q must be a contiguous, aligned int8 [M, K]")
+        rows, width = q.shape
+        if scales.dtype != torch.float32 or scales.numel() != rows or not scales.is_contiguous():
+            raise ValueError(f"w4a8_gemm: scales must be contiguous float32 with {rows} values")
+        bias = self._w4a8_weight(w, bias, width, out_dtype)
+        n = w.codes.shape[0]
+        if config == UNPACK or (config < 0 and rows >= UNPACK_ROWS):
+            levels = torch.empty(n, width, dtype=torch.int8, device=q.device)
+            code = self._lib.cozyq_w4a8_unpack(
+                self.index, w.codes.data_ptr(), w.group_scale.data_ptr(), _ptr(w.codebook),
+                levels.data_ptr(), n, width, self._stream(),
+            )  # fmt: skip
+            self._check(code, "the w4a8 unpack")
+            return self.int8_gemm(q, scales, levels, w.scale, bias, out_dtype)
+        out = torch.empty(rows, n, dtype=out_dtype, device=q.device)
+        if rows == 0:
+            return out
+        code = self._lib.cozyq_w4a8_gemm(
+            self.index, q.data_ptr(), scales.data_ptr(), w.codes.data_ptr(),
+            w.group_scale.data_ptr(), _ptr(w.codebook), w.scale.data_ptr(), _ptr(bias),
+            out.data_ptr(), self._half(out_dtype), rows, n, width, config, self._stream(),
+        )  # fmt: skip
+        if code == self._lib.cozyq_not_supported() and config >= 0:
+            raise ValueError(f"w4a8_gemm: config {config} cannot take {rows}x{width}")
+        self._check(code, "the w4a8 GEMM")
+        return out
+
+    def w4a8_unpack(self, w: W4a8) -> Tensor:
+        """The int8 levels [N, K] of `w`'s codes (`cozyq_w4a8_unpack`)."""
+        n, width = w.codes.shape[0], 2 * w.codes.shape[1]
+        self._w4a8_weight(w, None, width, self.torch.bfloat16)
+        levels = self.torch.empty(n, width, dtype=self.torch.int8, device=w.codes.device)
+        code = self._lib.cozyq_w4a8_unpack(
+            self.index, w.codes.data_ptr(), w.group_scale.data_ptr(), _ptr(w.codebook),
+            levels.data_ptr(), n, width, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the w4a8 unpack")
+        return levels
+
+    def _w4a8_weight(self, w: W4a8, bias: Tensor | None, width: int, out_dtype: Dtype) -> Tensor | None:
+        """`internal/prebuilt.py:224-251`."""
+        torch = self.torch
+        n = w.codes.shape[0]
+        shapes = ((w.codes, (n, width // 2)), (w.group_scale, (n, width // 16)), (w.scale, (n,)))
+        if any(tuple(t.shape) != shape or not t.is_contiguous() for t, shape in shapes):
+            raise ValueError(f"w4a8: codes, group scales and scale must be [{n}, {width // 2}], "
+                             f"[{n}, {width // 16}] and [{n}], contiguous")  # fmt: skip
+        if w.codes.element_size() != 1 or w.group_scale.dtype != torch.float8_e4m3fn:
+            raise ValueError("w4a8: codes are bytes and group scales E4M3")
+        if w.scale.dtype != torch.float32 or n % 8 or w.codes.data_ptr() % 16:
+            raise ValueError("w4a8: scale is float32, N a multiple of 8, codes 16-byte aligned")
+        if w.group_scale.data_ptr() % 4:
+            raise ValueError("w4a8: group scales must be 4-byte aligned")
+        if w.codebook is not None and (w.codebook.dtype != torch.float32 or w.codebook.numel() != 16):
+            raise ValueError("w4a8: the codebook is 16 float32 levels")
+        on = [t for t in (w.codes, w.group_scale, w.scale, w.codebook, bias) if t is not None]
+        if any(not t.is_cuda or t.get_device() != self.index for t in on):
+            raise ValueError(f"w4a8: the weight's tensors must be on cuda:{self.index}")
+        self._half(out_dtype)
+        if bias is None:
+            return None
+        if bias.numel() != n:
+            raise ValueError(f"w4a8: bias must have {n} values")
+        return bias.to(out_dtype).contiguous()
 
     def int8_gemm(
         self, q: Tensor, scales: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None,

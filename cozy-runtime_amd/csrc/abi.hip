@@ -141,6 +141,28 @@ int cozyq_gemm_i32(int device, const int8_t* q, const int8_t* w, int32_t* acc, i
     return cozyq::gemm_int8_acc(q, w, acc, M, N, K, on(stream));
 }
 
+int cozyq_w4a8_gemm(int device, const int8_t* q, const float* scales, const uint8_t* w,
+                    const uint8_t* s, const float* codebook, const float* w_scale, const void* bias,
+                    void* out, int out_half, int M, int N, int K, int config, void* stream) {
+    if (M < 1 || N < 8 || N % 8 || !fits(K, 256)) return hipErrorInvalidValue;
+    if (config > 0) return hipErrorNotSupported;  // config 0: the one (narrow-tile) GEMM
+    if (!aligned16(q) || !aligned16(w) || (reinterpret_cast<uintptr_t>(out) & 7))
+        return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::gemm_w4a8_narrow(q, scales, w, s, codebook, w_scale, bias, out, out_half, M, N,
+                                   K, on(stream));
+}
+
+int cozyq_w4a8_unpack(int device, const uint8_t* w, const uint8_t* s, const float* codebook,
+                      int8_t* out, int N, int K, void* stream) {
+    if (N < 1 || !fits(K, 256)) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(w) & 7) || !aligned16(out)) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::w4a8_unpack(w, s, codebook, out, N, K, on(stream));
+}
+
 int cozyq_fp8_linear(int device, const void* x, int x_half, const uint8_t* w,
                      const float* w_scale, const void* bias, void* out, int out_half, int M,
                      int N, int K, void* stream) {

@@ -89,8 +89,9 @@ __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
     return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
 }
 
-// E4M3FN byte -> float32 (exact).
+// E4M3FN byte -> float32 (exact); S.1111.111 is NaN (E4M3FN has no infinities).
 __device__ __forceinline__ float e4m3_value(uint32_t b) {
+    if ((b & 0x7fu) == 0x7fu) return __builtin_nanf("");
     const uint32_t sign = (b & 0x80u) << 24;
     const uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
     if (e == 0) return float_of(sign | bits_of(static_cast<float>(m) * 0.001953125f));  // m·2^-9

@@ -38,12 +38,63 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_from(const uint8_t* base,
                                              0, bytes, 0x00020000);
 }
 
-template <bool kInt8, int kTM, int kTN, bool kOutHalf, bool kBias, int kEpi>
+// w4a8.convrot weights (internal/prebuilt.py:437-492): 4-bit codes [N, K/2] (even k in the low
+// nibble), one E4M3 group scale per 16 codes [N, K/16], and a codebook of 16 float32 levels (or
+// the uniform grid q − 8). A code's int8 level is clamp(rne(level · group scale), ±127), a NaN
+// product 0 — one float32 multiply, so a 256 x 16 table T[scale byte][code] holds every level.
+struct W4 {
+    const uint8_t* group_scale;
+    const float* codebook;  // null: the uniform grid
+};
+
+// T[b][c] for b = the calling thread's index (256 threads), as 16 bytes at table + 16·b.
+__device__ __forceinline__ void w4_table_row(const float* codebook, uint32_t* table, int b) {
+    const float e = e4m3_value(static_cast<uint32_t>(b));
+    uint32_t words[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        const float level = codebook != nullptr ? codebook[c] : static_cast<float>(c - 8);
+        float r = __builtin_rintf(level * e);  // torch.round: half to even
+        r = __builtin_isnan(r) ? 0.0f : fminf(fmaxf(r, -127.0f), 127.0f);
+        words[c / 4] |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int>(r))) << (8 * (c % 4));
+    }
+    *reinterpret_cast<uint4*>(table + 4 * b) = make_uint4(words[0], words[1], words[2], words[3]);
+}
+
+// 16 codes (8 bytes, k order) of one group with scale byte b -> their 16 int8 levels (k order),
+// by byte selects from the group's table row: codes 0..7 from its low 8 bytes, 8..15 from its
+// high 8, chosen per byte by the code's bit 3.
+__device__ __forceinline__ uint4 w4_unpack16(uint32_t c01, uint32_t c23, const uint32_t* table,
+                                             uint32_t b) {
+    const uint4 t = *reinterpret_cast<const uint4*>(table + 4 * b);
+    auto four = [&](uint32_t spread) {  // four codes, one a byte
+        const uint32_t sel = spread & 0x07070707u;
+        const uint32_t lo = __builtin_amdgcn_perm(t.y, t.x, sel);  // levels of codes 0..7
+        const uint32_t hi = __builtin_amdgcn_perm(t.w, t.z, sel);  // levels of codes 8..15
+        const uint32_t m = ((spread >> 3) & 0x01010101u) * 0xffu;
+        return (hi & m) | (lo & ~m);
+    };
+    uint32_t out[4];
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        const uint32_t x = d ? c23 : c01;
+        const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
+        // byte i holds k = 2i (low nibble) and 2i + 1 (high): interleave into k order.
+        out[2 * d] = four(__builtin_amdgcn_perm(hi, lo, 0x05010400u));
+        out[2 * d + 1] = four(__builtin_amdgcn_perm(hi, lo, 0x07030602u));
+    }
+    return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// kW4: W is w4a8.convrot codes (with `w4`), unpacked to int8 levels in registers on the way
+// into LDS; the rest is the int8 path (kInt8 must be true).
+template <bool kInt8, int kTM, int kTN, bool kOutHalf, bool kBias, int kEpi, bool kW4 = false>
 __global__ __launch_bounds__(kThreads) void narrow_kernel(
     const uint8_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ xs,
     const float* __restrict__ ws, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
-    int64_t ldo, int M, int N, int K, int tiles_m) {
+    int64_t ldo, int M, int N, int K, int tiles_m, W4 w4) {
     static_assert(kTM % 32 == 0 && kTN % 32 == 0 && kTM <= 128 && kTN <= 128, "tile");
+    static_assert(!kW4 || kInt8, "w4a8 runs the int8 path");
     constexpr int kXLoads = kTM * 8 / kThreads;   // 16-byte chunks a thread stages a step
     constexpr int kWLoads = kTN * 8 / kThreads;
     constexpr int kBI = kTN / 32, kBJ = kTM / 32;  // 16x16 blocks of a wave: n by m
@@ -57,12 +108,20 @@ __global__ __launch_bounds__(kThreads) void narrow_kernel(
     const int m0 = __builtin_amdgcn_readfirstlane(tm * kTM);
     const int n0 = __builtin_amdgcn_readfirstlane(tn * kTN);
     const __amdgpu_buffer_rsrc_t xr = rows_from(X, m0, M, K);
-    const __amdgpu_buffer_rsrc_t wr = rows_from(W, n0, N, K);
+    // kW4: W rows are K/2 code bytes, and the group scales K/16 bytes a row.
+    const __amdgpu_buffer_rsrc_t wr = rows_from(W, n0, N, kW4 ? K / 2 : K);
+    const __amdgpu_buffer_rsrc_t gr = rows_from(kW4 ? w4.group_scale : W, n0, N, kW4 ? K / 16 : K);
     const int nk = (K + kStep - 1) / kStep;
+    __shared__ __attribute__((aligned(16))) uint32_t table[kW4 ? 256 * 4 : 4];
+    if constexpr (kW4) {
+        w4_table_row(w4.codebook, table, threadIdx.x);
+        __syncthreads();
+    }
 
     // Chunk tid + 256·i: row (tid + 256·i) / 8 of the tile, 16-byte column tid % 8.
     const int col = tid & 7;
     uint4 sx[kXLoads], sw[kWLoads];
+    uint32_t sg[kWLoads];  // kW4: the chunk's group scale byte (its 16 codes in sw[i].x, .y)
     auto load = [&](int ks) {
         const int kb = ks * kStep + col * 16;
 #pragma unroll
@@ -74,8 +133,17 @@ __global__ __launch_bounds__(kThreads) void narrow_kernel(
 #pragma unroll
         for (int i = 0; i < kWLoads; ++i) {
             const int r = (tid >> 3) + 32 * i;
-            const uint32_t off = kb < K ? static_cast<uint32_t>(r * K + kb) : kOutOfRange;
-            sw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+            if constexpr (kW4) {
+                // The chunk's 16 codes (8 bytes) and its group scale: zeros past K level to 0.
+                const uint32_t off = kb < K ? static_cast<uint32_t>(r * (K / 2) + kb / 2) : kOutOfRange;
+                const uint32_t goff = kb < K ? static_cast<uint32_t>(r * (K / 16) + kb / 16) : kOutOfRange;
+                const auto c = __builtin_amdgcn_raw_buffer_load_b64(wr, off, 0, 0);
+                sw[i] = make_uint4(c[0], c[1], 0, 0);
+                sg[i] = __builtin_amdgcn_raw_buffer_load_b8(gr, goff, 0, 0);
+            } else {
+                const uint32_t off = kb < K ? static_cast<uint32_t>(r * K + kb) : kOutOfRange;
+                sw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+            }
         }
     };
     auto store = [&](int buf) {
@@ -87,7 +155,9 @@ __global__ __launch_bounds__(kThreads) void narrow_kernel(
 #pragma unroll
         for (int i = 0; i < kWLoads; ++i) {
             const int r = (tid >> 3) + 32 * i;
-            *reinterpret_cast<uint4*>(&lw[buf][r * kStep + swz(r, col) * 16]) = sw[i];
+            uint4 v = sw[i];
+            if constexpr (kW4) v = w4_unpack16(sw[i].x, sw[i].y, table, sg[i] & 0xffu);
+            *reinterpret_cast<uint4*>(&lw[buf][r * kStep + swz(r, col) * 16]) = v;
         }
     };
 
@@ -188,23 +258,24 @@ __global__ __launch_bounds__(kThreads) void narrow_kernel(
     }
 }
 
-template <bool kInt8, int kTM, int kTN, bool kOutHalf, bool kBias, int kEpi>
+template <bool kInt8, int kTM, int kTN, bool kOutHalf, bool kBias, int kEpi, bool kW4>
 hipError_t launch(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
-                  const void* bias, void* out, int64_t ldo, int M, int N, int K, hipStream_t s) {
+                  const void* bias, void* out, int64_t ldo, int M, int N, int K, W4 w4,
+                  hipStream_t s) {
     const int tiles_m = (M + kTM - 1) / kTM, tiles_n = (N + kTN - 1) / kTN;
-    narrow_kernel<kInt8, kTM, kTN, kOutHalf, kBias, kEpi><<<tiles_m * tiles_n, kThreads, 0, s>>>(
+    narrow_kernel<kInt8, kTM, kTN, kOutHalf, kBias, kEpi, kW4><<<tiles_m * tiles_n, kThreads, 0, s>>>(
         q, w, xs, ws, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, M, N,
-        K, tiles_m);
+        K, tiles_m, w4);
     return hipGetLastError();
 }
 
-template <bool kInt8, int kTM, int kTN>
+template <bool kInt8, int kTM, int kTN, bool kW4 = false>
 hipError_t shaped(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                   const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
-                  int epilogue, hipStream_t s) {
+                  int epilogue, hipStream_t s, W4 w4 = W4{nullptr, nullptr}) {
     const bool b = bias != nullptr;
 #define COZYQ_CASE(H, B, E) \
-    if (out_half == H && b == B && epilogue == E) return launch<kInt8, kTM, kTN, H, B, E>(q, xs, w, ws, bias, out, ldo, M, N, K, s);
+    if (out_half == H && b == B && epilogue == E) return launch<kInt8, kTM, kTN, H, B, E, kW4>(q, xs, w, ws, bias, out, ldo, M, N, K, w4, s);
     COZYQ_CASE(false, false, 0)
     COZYQ_CASE(false, true, 0)
     COZYQ_CASE(true, false, 0)
@@ -228,7 +299,46 @@ hipError_t narrow(const uint8_t* q, const float* xs, const uint8_t* w, const flo
     return hipErrorNotSupported;
 }
 
+// The unpack law over a whole weight (internal/prebuilt.py:471-492): one thread a group of 16.
+__global__ __launch_bounds__(kThreads) void w4a8_unpack_kernel(const uint8_t* __restrict__ codes,
+                                                               const uint8_t* __restrict__ gs,
+                                                               const float* __restrict__ codebook,
+                                                               int8_t* __restrict__ out, int64_t groups,
+                                                               int K) {
+    __shared__ __attribute__((aligned(16))) uint32_t table[256 * 4];
+    w4_table_row(codebook, table, threadIdx.x);
+    __syncthreads();
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (g >= groups) return;
+    const int64_t per_row = K / 16;
+    const int64_t row = g / per_row, grp = g % per_row;
+    const uint2 c = *reinterpret_cast<const uint2*>(codes + row * (K / 2) + grp * 8);
+    const uint4 v = w4_unpack16(c.x, c.y, table, gs[row * per_row + grp]);
+    *reinterpret_cast<uint4*>(out + row * K + grp * 16) = v;
+}
+
 }  // namespace
+
+hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* codes,
+                            const uint8_t* group_scale, const float* codebook, const float* ws,
+                            const void* bias, void* out, bool out_half, int M, int N, int K,
+                            hipStream_t s) {
+    const W4 w4{group_scale, codebook};
+    auto qp = reinterpret_cast<const uint8_t*>(q);
+    if (M <= 32) return shaped<true, 32, 64, true>(qp, xs, codes, ws, bias, out, N, out_half, M, N, K, 0, s, w4);
+    if (M <= 64) return shaped<true, 64, 64, true>(qp, xs, codes, ws, bias, out, N, out_half, M, N, K, 0, s, w4);
+    if (M <= 128) return shaped<true, 128, 64, true>(qp, xs, codes, ws, bias, out, N, out_half, M, N, K, 0, s, w4);
+    return shaped<true, 128, 128, true>(qp, xs, codes, ws, bias, out, N, out_half, M, N, K, 0, s, w4);
+}
+
+hipError_t w4a8_unpack(const uint8_t* codes, const uint8_t* group_scale, const float* codebook,
+                       int8_t* out, int N, int K, hipStream_t s) {
+    const int64_t groups = static_cast<int64_t>(N) * (K / 16);
+    if (groups == 0) return hipSuccess;
+    w4a8_unpack_kernel<<<static_cast<unsigned>((groups + kThreads - 1) / kThreads), kThreads, 0, s>>>(
+        codes, group_scale, codebook, out, groups, K);
+    return hipGetLastError();
+}
 
 hipError_t gemm_fp8_narrow(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                            const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,

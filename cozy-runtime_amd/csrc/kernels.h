@@ -46,6 +46,15 @@ hipError_t gemm_fp8_narrow(const uint8_t* q, const float* xs, const uint8_t* w, 
                            const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
                            int K, int epilogue, hipStream_t s);
 
+// w4a8.convrot: codes [N, K/2], E4M3 group scales [N, K/16], codebook (16 float32 levels or
+// null for q − 8); the fused narrow-tile GEMM (int8 q [M, K], the int8 epilogue, out [M, N]) and
+// the unpack to int8 levels [N, K].
+hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* codes,
+                            const uint8_t* group_scale, const float* codebook, const float* ws,
+                            const void* bias, void* out, bool out_half, int M, int N, int K,
+                            hipStream_t s);
+hipError_t w4a8_unpack(const uint8_t* codes, const uint8_t* group_scale, const float* codebook,
+                       int8_t* out, int N, int K, hipStream_t s);
 hipError_t gemm_int8_narrow(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                             const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
                             int K, int epilogue, hipStream_t s);

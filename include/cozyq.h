@@ -102,6 +102,24 @@ int cozyq_gemm_ex(int device, int fp8, const void* q, const float* scales, const
 int cozyq_gemm_i32(int device, const int8_t* q, const int8_t* w, int32_t* acc, int M, int N,
                    int K, void* stream);
 
+/* The w4a8.convrot GEMM (reference: gemm.cpp:147-157 `w4a8_gemm`, w4a8.cu): int8 q [M, K]
+ * (int8.convrot's operand) times the int8 levels of 4-bit codes w [N, K/2] (even k in the low
+ * nibble) with E4M3 group scales s [N, K/16] and a codebook of 16 float32 levels (NULL: the
+ * uniform grid q - 8): level = clamp(rne(codebook[code] · e4m3(s)), ±127), a NaN product 0
+ * (internal/prebuilt.py:471-492). The codes are unpacked in registers on the way to the int8
+ * MFMA; the epilogue is cozyq_gemm's int8 law with w_scale [N], bit for bit. out [M, N].
+ * N % 8 == 0, K % 256 == 0; q and w 16-byte aligned, out 8-byte aligned. config -1 or 0;
+ * others return hipErrorNotSupported. */
+int cozyq_w4a8_gemm(int device, const int8_t* q, const float* scales, const uint8_t* w,
+                    const uint8_t* s, const float* codebook, const float* w_scale, const void* bias,
+                    void* out, int out_half, int M, int N, int K, int config, void* stream);
+
+/* The same codes unpacked to their int8 levels, out [N, K] (reference: gemm.cpp:159-166
+ * `w4a8_unpack`): the many-row path multiplies these on the int8 GEMM. w 8-byte aligned, out
+ * 16-byte aligned. */
+int cozyq_w4a8_unpack(int device, const uint8_t* w, const uint8_t* s, const float* codebook,
+                      int8_t* out, int N, int K, void* stream);
+
 /* The fp8 linear for few rows in one launch (no reference counterpart: the reference has no
  * fp8 GEMV, internal/fp8_linear.py:114-129 quantizes then multiplies): each row of x quantized
  * by cozyq_quantize's fp8 law inside the kernel, then out = acc·s_x·w_scale (+ bias).

@@ -16,6 +16,9 @@ Pins, exercised in `tests/test_oracle.py`:
   of log2) and the round trip through the mxfp8 decode law.
 - `int8_*` products: int32 GEMM against numpy int64 matmul.
 - `int4_quantize` (build law): round trip bound |x − q·s| ≤ s/2 and brute force on small cases.
+- `w4a8_unpack`: closed forms (unit group scale on the uniform grid gives q − 8, the nibble
+  order, NaN scales, the ±127 clamp) and numpy's float32 multiply and `rint` over every
+  (scale byte, code) pair.
 - `prologue` (the producer prologue, compared with tolerance on the GPU since its
   transcendentals are the platform's): closed forms (constant and alternating rows through
   each norm, unit / zero modulation, table-row selection) and the library routines `math.erf`,
@@ -247,6 +250,29 @@ def prologue(
     elif activation == ACT_GELU_TANH:
         v = 0.5 * v * (1.0 + torch.tanh(0.79788456 * (v + 0.044715 * v * v * v)))
     return v
+
+
+#: comfy-kitchen's frozen 16-level Lloyd-Max codebook, the one the reference's w4a8 producer
+#: writes (`internal/prebuilt.py:679-682`).
+W4A8_CODEBOOK = (
+    -0.980602, -0.794529, -0.638165, -0.500986, -0.377321, -0.263187, -0.155210, -0.050720,
+    0.052541, 0.156985, 0.265284, 0.379533, 0.502636, 0.638953, 0.794876, 0.980671,
+)  # fmt: skip
+
+
+def w4a8_unpack(codes: torch.Tensor, group_scale: torch.Tensor,
+                codebook: torch.Tensor | None) -> torch.Tensor:  # fmt: skip
+    """The int8 levels [N, K] of `w4a8.convrot` codes (`internal/prebuilt.py:471-492`):
+    `codes` bytes [N, K/2], even k in the low nibble; `group_scale` E4M3 [N, K/16];
+    level = clamp(round_half_even(codebook[q] · e4m3(group_scale)), ±127), one float32 multiply,
+    a NaN product 0; `codebook` None is the uniform grid q − 8."""
+    codes = codes.view(torch.uint8)
+    rows, half = codes.shape
+    levels = (torch.arange(-8, 8, dtype=torch.float32) if codebook is None
+              else codebook.reshape(16).float())  # fmt: skip
+    q = torch.stack((codes & 15, codes >> 4), dim=-1).reshape(rows, -1).long()
+    grouped = levels[q].view(rows, -1, 16) * group_scale.float().unsqueeze(-1)
+    return torch.round(grouped).nan_to_num_(0.0).clamp_(-127, 127).view(rows, -1).to(torch.int8)
 
 
 def fp8_weight(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

@@ -595,6 +595,63 @@ def test_quantize_prologue_within_one_step(ops, fp8, dtype, case):
     assert (got != want).float().mean() <= (0.05 if swiglu else 0.01)
 
 
+# ------------------------------------------------------------------------- w4a8 lane
+
+
+def _w4a8(n: int, k: int, seed: int, codebook: bool):
+    """A w4a8.convrot weight with the probe's recipe (`internal/prebuilt.py:695-706`): random
+    code bytes, E4M3 group scales |N(0,1)|·40 + 16 clamped to 440, row scales ~1e-3."""
+    from cozyq import prebuilt
+
+    gen = torch.Generator().manual_seed(seed)
+    codes = torch.randint(0, 256, (n, k // 2), generator=gen, dtype=torch.uint8)
+    gs = (torch.randn(n, k // 16, generator=gen).abs() * 40 + 16).clamp(max=440).to(torch.float8_e4m3fn)
+    scale = (torch.randn(n, generator=gen).abs() + 0.5) * 1e-3
+    book = torch.tensor(laws.W4A8_CODEBOOK) if codebook else None
+    dev = prebuilt.W4a8(codes.to(DEV), gs.to(DEV), scale.to(DEV), None if book is None else book.to(DEV))
+    return dev, laws.w4a8_unpack(codes, gs, book), scale
+
+
+@pytest.mark.parametrize("codebook", [True, False], ids=["codebook", "uniform"])
+def test_w4a8_unpack_every_scale_byte_bit_exact(ops, codebook):
+    """`cozyq_w4a8_unpack` over a weight whose 256 rows carry the 256 E4M3 scale bytes (NaN
+    included) and random codes: every level equals the CPU law."""
+    from cozyq import prebuilt
+
+    gen = torch.Generator().manual_seed(9)
+    codes = torch.randint(0, 256, (256, 512), generator=gen, dtype=torch.uint8)
+    gs = torch.arange(256, dtype=torch.uint8).reshape(256, 1).expand(256, 64).contiguous()
+    gs = gs.view(torch.float8_e4m3fn)
+    book = torch.tensor(laws.W4A8_CODEBOOK) if codebook else None
+    w = prebuilt.W4a8(codes.to(DEV), gs.to(DEV), torch.ones(256, device=DEV),
+                      None if book is None else book.to(DEV))  # fmt: skip
+    assert torch.equal(ops.w4a8_unpack(w).cpu(), laws.w4a8_unpack(codes, gs, book))
+
+
+@pytest.mark.parametrize("codebook", [True, False], ids=["codebook", "uniform"])
+@pytest.mark.parametrize("shape", [(1, 264, 1024), (3, 520, 1024), (16, 136, 256), (100, 256, 3072),
+                                   (256, 512, 768), (300, 520, 1024)],
+                         ids=lambda s: "x".join(map(str, s)))  # fmt: skip
+def test_w4a8_linear_bit_exact(ops, shape, codebook):
+    """The w4a8 linear (int8.convrot's operand, the fused unpack-in-registers GEMM up to 256
+    rows, unpack + the int8 GEMM beyond) equals the int8 CPU law on the unpacked levels, bit for
+    bit, with and without bias; the fused and unpack configs agree bit for bit."""
+    from cozyq import prebuilt
+
+    m, n, k = shape
+    w, levels, scale = _w4a8(n, k, 20261022 + m, codebook)
+    gen = torch.Generator().manual_seed(m + k)
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16)
+    b = torch.randn(n, generator=gen).to(torch.bfloat16)
+    for bias in (None, b):
+        got = ops.w4a8_linear(x.to(DEV), w, None if bias is None else bias.to(DEV), torch.bfloat16)
+        assert torch.equal(got.cpu(), laws.int8_linear(x, levels, scale, bias, torch.bfloat16))
+    q, s = ops.int8_quantize(x.to(DEV))
+    fused = ops.w4a8_gemm(q, s, w, b.to(DEV), torch.bfloat16, 0)
+    unpacked = ops.w4a8_gemm(q, s, w, b.to(DEV), torch.bfloat16, prebuilt.UNPACK)
+    assert torch.equal(fused, unpacked)
+
+
 # ------------------------------------------------------------------------ MXFP8 lane
 
 

@@ -119,6 +119,50 @@ def test_int8_rows_with_a_prologue():
                                       scale, b, 256))  # fmt: skip
 
 
+def test_w4a8_leaf_shares_the_int8_operand(monkeypatch):
+    """The w4a8 leaf (`W4a8NativeLeaf`) takes int8.convrot's operand: its forward equals the int8
+    law on the unpacked levels, bit for bit, and an int8 leaf beside it reads the same shared
+    operand."""
+    from cozyq import prebuilt
+
+    n, k = 264, 1024
+    gen = _gen(97)
+    codes = torch.randint(0, 256, (n, k // 2), generator=gen, dtype=torch.uint8)
+    gs = (torch.randn(n, k // 16, generator=gen).abs() * 40 + 16).clamp(max=440).to(torch.float8_e4m3fn)
+    scale = (torch.randn(n, generator=gen).abs() + 0.5) * 1e-3
+    book = torch.tensor(laws.W4A8_CODEBOOK)
+    b = (torch.randn(n, generator=gen) * 0.1).to(torch.bfloat16)
+    provider = leaves.W4a8NativeLeaf()
+    assert provider.supports((n, k), {"group_size": 16, "rotation": "kron_regular_h4",
+                                      "rotation_size": 256}) == ""  # fmt: skip
+    leaf = provider.leaf(torch, {"weight": codes.to(DEV), "group_scale": gs.to(DEV),
+                                 "scale": scale.to(DEV), "codebook": book.to(DEV)},
+                         _Linear(b.to(DEV)), torch.bfloat16)  # fmt: skip
+    assert leaf.operand == operands.INT8_CONVROT
+    levels = laws.w4a8_unpack(codes, gs, book)
+    for m in (3, 130):
+        x = activations(m, k, 98 + m)
+        want = laws.int8_linear(x, levels, scale, b, torch.bfloat16, rotation=256)
+        assert torch.equal(leaf(x.to(DEV)).cpu(), want)
+    int8, _, _, _ = int8_leaf(264, k, 99)
+    x = activations(130, k, 100).to(DEV)
+    alone = (leaf(x), int8(x))
+    lib = int8_linear.library(0)
+    calls = []
+    original = type(lib).int8_quantize
+
+    def counting(self, *args, **kwargs):
+        calls.append(1)
+        return original(self, *args, **kwargs)
+
+    monkeypatch.setattr(type(lib), "int8_quantize", counting)
+    with operands.quantize_once(x):
+        shared = (leaf(x), int8(x))
+    assert len(calls) == 1
+    assert all(torch.equal(a, s) for a, s in zip(alone, shared))
+    assert isinstance(leaf.weights(), prebuilt.W4a8)
+
+
 def test_int8_leaf_autocast_dtype():
     leaf, data, scale, _ = int8_leaf(256, 512, 95, bias=False)
     x = activations(40, 512, 96)

@@ -21,9 +21,11 @@ class _Linear(torch.nn.Module):
 
 def test_providers_surface_and_launch_table():
     table = leaves.launch_providers()
-    assert set(table) == {"fp8.rowwise", "int8.convrot", "svdq.int4g64", "mxfp8"}
+    assert set(table) == {"fp8.rowwise", "int8.convrot", "w4a8.convrot", "svdq.int4g64", "mxfp8"}
     names = {p.name for ps in table.values() for p in ps}
-    assert names == {operands.ROWWISE_FP8, operands.INT8_CONVROT, leaves.MXFP8, leaves.SVDQ_INT4}
+    assert names == {operands.ROWWISE_FP8, operands.INT8_CONVROT, leaves.W4A8, leaves.MXFP8,
+                     leaves.SVDQ_INT4}  # fmt: skip
+    assert leaves.OPERANDS[leaves.W4A8] == operands.INT8_CONVROT
     for scheme, (provider,) in table.items():
         assert provider.encoding == scheme
         assert provider.route == "encoded_gemm"
@@ -33,6 +35,17 @@ def test_providers_surface_and_launch_table():
         assert leaves.serves(provider, "gfx950") and not leaves.serves(provider, "gfx942")
         with pytest.raises(AssertionError):
             provider.decode(torch, {}, torch.empty(0))
+
+
+def test_w4a8_supports_messages():
+    """`internal/encoding/leaves.py:1004-1013`: group 16, the 256 rotation, K % 256, N % 8."""
+    w4 = leaves.W4a8NativeLeaf()
+    ok = {"group_size": 16, "rotation": "kron_regular_h4", "rotation_size": 256}
+    assert w4.supports((64, 512), ok) == ""
+    assert "reads" in w4.supports((64, 512), {**ok, "group_size": 32})
+    assert "K % 256" in w4.supports((64, 640), ok)
+    assert "N % 8" in w4.supports((60, 512), ok)
+    assert w4.optional == frozenset({"codebook"})
 
 
 def test_supports_messages():

@@ -456,3 +456,39 @@ def test_prologue_activations_against_library_routines():
     assert torch.equal(swiglu.to(torch.bfloat16), torch.nn.functional.silu(x.float()).to(torch.bfloat16))
     halves = laws.prologue(torch.cat([ones, x], -1), activation=laws.ACT_SWIGLU)
     assert torch.equal(halves, swiglu)
+
+
+# ------------------------------------------------------------------------------ w4a8
+
+
+def _e4m3_bytes(values: list[int]) -> torch.Tensor:
+    return torch.tensor(values, dtype=torch.uint8).view(torch.float8_e4m3fn)
+
+
+def test_w4a8_unpack_closed_forms():
+    """Scale byte 0x38 (1.0) on the uniform grid gives q − 8; byte i holds k = 2i in its low
+    nibble; NaN scales (0x7F, 0xFF) level to 0; 448 (0x7E) times the codebook's ±0.98 clamps to
+    ±127."""
+    codes = torch.tensor([[0x10 * (2 * i + 1 & 15) + (2 * i & 15) for i in range(8)]], dtype=torch.uint8)
+    one = _e4m3_bytes([0x38]).reshape(1, 1)
+    got = laws.w4a8_unpack(codes, one, None)
+    assert got.tolist() == [[k - 8 for k in range(16)]]
+    nan = _e4m3_bytes([0x7F]).reshape(1, 1)
+    assert laws.w4a8_unpack(codes, nan, None).abs().max() == 0
+    book = torch.tensor(laws.W4A8_CODEBOOK)
+    big = laws.w4a8_unpack(codes, _e4m3_bytes([0x7E]).reshape(1, 1), book)
+    assert big[0, 0] == -127 and big[0, 15] == 127
+
+
+def test_w4a8_unpack_every_scale_and_code_against_numpy():
+    """Every (E4M3 scale byte, code) pair, codebook and uniform grid: the float32 product
+    rounded half to even (numpy's float32 multiply and `rint`), NaN to 0, clamped to ±127."""
+    codes = torch.tensor([[0x10 * (2 * i + 1) + 2 * i for i in range(8)]] * 256, dtype=torch.uint8)
+    scales = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).reshape(256, 1)
+    scale_f = np.array([[float(v)] for v in scales.float().reshape(-1)], dtype=np.float32)
+    for book in (torch.tensor(laws.W4A8_CODEBOOK), None):
+        levels = np.arange(-8, 8, dtype=np.float32) if book is None else book.numpy().astype(np.float32)
+        with np.errstate(invalid="ignore"):
+            want = np.rint(scale_f * levels[None, :])
+        want = np.clip(np.nan_to_num(want, nan=0.0), -127, 127).astype(np.int8)
+        assert np.array_equal(laws.w4a8_unpack(codes, scales, book).numpy(), want)
