@@ -29,7 +29,7 @@ constexpr float kLevels = 7.0f;
 // ------------------------------------------------------------------- activation quantize
 
 constexpr int kQRows = 16;  // rows a block (the MFMA's M)
-constexpr int kQWaves = 4;  // waves take a row block's 64-groups round-robin
+constexpr int kQWaves = 16;  // waves take a row block's 64-groups round-robin
 
 // Eight 16-bit values (one uint4) as float32.
 template <bool kHalf>
