@@ -688,6 +688,46 @@ def test_mx_gemm_within_tolerance(ops, shape, bias):
 # ------------------------------------------------------------------ full-size property
 
 
+def test_c3_full_size_fp8_codes_and_sampled_rows(ops):
+    """BASELINE config 3 at M=4096 (K=4096, N=14336): every e4m3 code and scale of the
+    activation bit-exact, and 48 sampled output rows within tolerance of the float64 product;
+    the whole output finite."""
+    m, k, n = 4096, 4096, 14336
+    x = activations(m, k, seed=20261203)
+    data, scale = laws.fp8_weight(weights(n, k, seed=20261204))
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(7)) * 0.1).to(torch.bfloat16)
+    q, s = ops.fp8_quantize(x.to(DEV))
+    wq, ws = laws.fp8_quantize(x)
+    assert torch.equal(q.cpu().view(torch.uint8), wq.view(torch.uint8))
+    assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
+    out = ops.fp8_gemm(q, s, data.to(DEV), scale.to(DEV), bias.to(DEV), torch.bfloat16)
+    rows = torch.randperm(m, generator=torch.Generator().manual_seed(8))[:48]
+    exact = (wq[rows].double() @ data.double().t()) * ws[rows].double() * scale.double().reshape(1, -1)
+    assert_close(out.cpu()[rows], exact + bias.double())
+    assert math.isfinite(out.float().abs().max().item())
+
+
+@pytest.mark.parametrize("shape", [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072)],
+                         ids=["qkv", "attn_out", "ffn_up", "ffn_down"])
+def test_c5_full_size_mx_codes_and_sampled_rows(ops, shape):
+    """BASELINE config 5 at M=4096 over the DiT block's four shapes: every e4m3 code and E8M0
+    byte of the activation bit-exact, and 32 sampled output rows within tolerance of the float64
+    product of the dequantized operands."""
+    k, n = shape
+    m = 4096
+    x = activations(m, k, seed=20261205 + k)
+    data, wbyte = laws.mx_quantize(weights(n, k, seed=20261206 + n))
+    q, qs = ops.mx_quantize(x.to(DEV))
+    wq, wqs = laws.mx_quantize(x)
+    assert torch.equal(q.cpu().view(torch.uint8), wq.view(torch.uint8))
+    assert torch.equal(qs.cpu(), wqs)
+    out = ops.mx_gemm(q, qs, data.to(DEV), wbyte.to(DEV), None, torch.bfloat16)
+    rows = torch.randperm(m, generator=torch.Generator().manual_seed(9))[:32]
+    exact = laws.mx_dequantize(wq[rows], wqs[rows]).double() @ laws.mx_dequantize(data, wbyte).double().t()
+    assert_close(out.cpu()[rows], exact)
+    assert math.isfinite(out.float().abs().max().item())
+
+
 def test_c2_full_size_codes_and_sampled_rows(ops):
     """BASELINE config 2 at its real shape: every code and scale bit-exact, the int32
     accumulators of 48 sampled rows exact, and the bias + GELU outputs of those rows within
