@@ -61,6 +61,19 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_int, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P],
     ),
+    "cozyq_decode": (
+        c_int,
+        [c_int, c_int, _P, _P, c_int, c_int, c_int, c_int, _P, c_int, c_int, _P, c_int, c_int,
+         c_int, _P, c_int, c_int64, c_int64, c_int, _P],
+    ),
+    "cozyq_decode_convrot": (
+        c_int, [c_int, _P, _P, c_int, c_int, _P, c_int, c_int64, c_int64, _P]
+    ),
+    "cozyq_decode_svdq": (
+        c_int,
+        [c_int, _P, _P, c_int, c_int, _P, c_int, _P, c_int, _P, c_int, _P, c_int, _P, c_int,
+         c_int, _P, c_int, c_int64, c_int64, _P],
+    ),
     "cozyq_host_e4m3": (None, [_P, _P, c_int64]),
     "cozyq_host_mx_byte": (None, [_P, _P, c_int64]),
     "cozyq_probe_div": (c_int, [c_int, _P, _P, _P, c_int64, _P]),

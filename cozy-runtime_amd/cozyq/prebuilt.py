@@ -420,6 +420,54 @@ class Prebuilt:
         out = self.svdq_gemm(act, ascales, la, w, wscales, up, bias, out_dtype)
         return out.view(*x.shape[:-1], w.shape[0])
 
+    # -------------------------------------------------------------- stored-format decode
+
+    def decode_table(
+        self, code: int, weight: Tensor, scale: Tensor, scale_type: int, out: Tensor, rows: int,
+        cols: int, *, grid: int, block: int = 1, tiled: bool = False,
+        scale_2: Tensor | None = None, per_matrix: bool = False, divide: bool = False,
+        post: Tensor | None = None, post_type: int = 0, high_first: bool = False,
+        matrices: int = 1,
+    ) -> None:
+        """`cozyq_decode` into `out`: `matrices` stacked `[rows, cols]` matrices, the element
+        law of `internal/encoding/formats.py:438-868` and `internal/decode_cores.py:196-230`.
+        Parts are contiguous on `out`'s device; `post` is one factor or one per column."""
+        post_mode = 0 if post is None else (2 if post.numel() == cols and cols != 1 else 1)
+        second = 0 if scale_2 is None else (2 if divide else 1)
+        code = self._lib.cozyq_decode(
+            self.index, code, weight.data_ptr(), scale.data_ptr(), scale_type, grid, block,
+            int(tiled), _ptr(scale_2), int(per_matrix), second, _ptr(post), post_type, post_mode,
+            int(high_first), out.data_ptr(), _out_type(self.torch, out.dtype), rows, cols,
+            matrices, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the decode")
+
+    def decode_convrot(
+        self, weight: Tensor, scale: Tensor, scale_type: int, size: int, out: Tensor, rows: int,
+        cols: int,
+    ) -> None:
+        """`cozyq_decode_convrot` into `out` (`internal/encoding/formats.py:733-752`)."""
+        code = self._lib.cozyq_decode_convrot(
+            self.index, weight.data_ptr(), scale.data_ptr(), scale_type, size, out.data_ptr(),
+            _out_type(self.torch, out.dtype), rows, cols, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the int8.convrot decode")
+
+    def decode_svdq(
+        self, weight: Tensor, scale: Tensor, tiled: bool, high_first: bool, scale_2: Tensor,
+        divide: bool, channel: Tensor | None, channel_type: int, smooth: Tensor,
+        smooth_type: int, down: Tensor, down_type: int, up: Tensor, up_type: int, out: Tensor,
+        rows: int, cols: int,
+    ) -> None:
+        """`cozyq_decode_svdq` into `out` (`internal/decode_schemes.py:464-489`)."""
+        code = self._lib.cozyq_decode_svdq(
+            self.index, weight.data_ptr(), scale.data_ptr(), int(tiled), int(high_first),
+            scale_2.data_ptr(), int(divide), _ptr(channel), channel_type, smooth.data_ptr(),
+            smooth_type, down.data_ptr(), down_type, up.data_ptr(), up_type, int(down.shape[0]),
+            out.data_ptr(), _out_type(self.torch, out.dtype), rows, cols, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the svdq.nvfp4 decode")
+
     # ---------------------------------------------------------------------- internals
 
     def _quantize(
@@ -570,6 +618,11 @@ class Prebuilt:
         if code == self._lib.cozyq_out_of_memory():
             raise self.torch.cuda.OutOfMemoryError(detail)
         raise RuntimeError(detail)
+
+
+def _out_type(torch: Any, dtype: Dtype) -> int:
+    """The decode kernels' destination code: 0 f32, 1 bf16, 2 f16."""
+    return {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[dtype]
 
 
 def _writable(out: Tensor, rows: int, n: int, dtype: Dtype, device: Any) -> bool:

@@ -222,6 +222,113 @@ int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales
                                  R, on(stream));
 }
 
+int cozyq_decode(int device, int code, const void* w, const void* scale, int scale_type, int grid,
+                 int block, int tiled, const float* scale_2, int scale_2_step, int second,
+                 const void* post, int post_type, int post_mode, int high_first, void* out,
+                 int out_type, int64_t rows, int64_t cols, int matrices, void* stream) {
+    using namespace cozyq;
+    if (code < kCodeI8 || code > kCodeE2m1 || scale_type < kNumF32 || scale_type > kNumE4m3 ||
+        out_type < kNumF32 || out_type > kNumF16 || grid < kGridTensor || grid > kGridBlocks ||
+        second < kSecondNone || second > kSecondDivide || post_mode < kPostNone ||
+        post_mode > kPostColumn || rows < 0 || cols < 1 || matrices < 1 || matrices > 65535)
+        return hipErrorInvalidValue;
+    if (grid == kGridBlocks && block < 1) return hipErrorInvalidValue;
+    if (tiled && grid != kGridBlocks) return hipErrorInvalidValue;
+    if (code == kCodeE2m1 && cols % 2) return hipErrorInvalidValue;
+    if ((second && !scale_2) || (post_mode && (!post || post_type > kNumE4m3 || post_type < 0)) ||
+        !w || !scale || !out)
+        return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    TableDecode a{};
+    a.weight = static_cast<const uint8_t*>(w);
+    a.weight_stride = code == kCodeE2m1 ? rows * cols / 2 : rows * cols;
+    a.scale = scale;
+    a.scale_type = scale_type;
+    a.scale_size = scale_type <= kNumF16 ? (scale_type == kNumF32 ? 4 : 2) : 1;
+    a.grid = grid;
+    a.block = block;
+    a.tiled = tiled;
+    if (grid == kGridRow) {
+        a.scale_stride = rows;
+    } else if (grid == kGridBlocks) {
+        const int64_t width = (cols + block - 1) / block;
+        a.scale_stride = tiled ? ((rows + 127) / 128 * 128) * ((width + 3) / 4 * 4) : rows * width;
+    }
+    a.scale_2 = scale_2;
+    a.scale_2_step = scale_2_step ? 1 : 0;
+    a.second = second;
+    a.post = post;
+    a.post_type = post_type;
+    a.post_mode = post_mode;
+    a.high_first = high_first ? 1 : 0;
+    a.out = out;
+    a.out_stride = rows * cols;
+    a.rows = rows;
+    a.cols = cols;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return decode_table(a, code, out_type, matrices, on(stream));
+}
+
+int cozyq_decode_convrot(int device, const int8_t* w, const void* scale, int scale_type,
+                         int rotation_size, void* out, int out_type, int64_t rows, int64_t cols,
+                         void* stream) {
+    using namespace cozyq;
+    int digits = 0;
+    for (int size = 4; size <= 65536; size *= 4) {
+        ++digits;
+        if (size == rotation_size) break;
+    }
+    if (rotation_size < 4 || rotation_size > 65536 || (1 << (2 * digits)) != rotation_size)
+        return hipErrorInvalidValue;
+    if (scale_type < kNumF32 || scale_type > kNumF16 || out_type < kNumF32 ||
+        out_type > kNumF16 || rows < 0 || cols < 1 || cols % rotation_size || !w || !scale || !out)
+        return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    // Groups of 64 and more are read and written 64 elements a lane, 16 bytes at a time.
+    if (rotation_size >= 64 && (!aligned16(w) || !aligned16(out))) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return decode_convrot(w, scale, scale_type, out, out_type, rows, cols, digits, on(stream));
+}
+
+int cozyq_decode_svdq(int device, const uint8_t* w, const uint8_t* scale, int tiled,
+                      int high_first, const float* scale_2, int divide, const void* channel_scale,
+                      int channel_type, const void* smooth, int smooth_type, const void* down,
+                      int down_type, const void* up, int up_type, int rank, void* out,
+                      int out_type, int64_t rows, int64_t cols, void* stream) {
+    using namespace cozyq;
+    const auto plain = [](int t) { return t >= kNumF32 && t <= kNumF16; };
+    if (rows < 0 || cols < 16 || cols % 16 || rank < 1 || !plain(smooth_type) ||
+        !plain(down_type) || !plain(up_type) || !plain(out_type) ||
+        (channel_scale && channel_type != kNumF32 && channel_type != kNumE4m3) || !w || !scale ||
+        !scale_2 || !smooth || !down || !up || !out)
+        return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    SvdqDecode a{};
+    a.weight = w;
+    a.scale = scale;
+    a.tiled = tiled ? 1 : 0;
+    a.high_first = high_first ? 1 : 0;
+    a.divide = divide ? 1 : 0;
+    a.scale_2 = scale_2;
+    a.channel = channel_scale;
+    a.channel_type = channel_type;
+    a.smooth = smooth;
+    a.smooth_type = smooth_type;
+    a.down = down;
+    a.down_type = down_type;
+    a.up = up;
+    a.up_type = up_type;
+    a.rank = rank;
+    a.out = out;
+    a.rows = rows;
+    a.cols = cols;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return decode_svdq(a, out_type, on(stream));
+}
+
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = cozyq::e4m3_rn(in[i]);
 }

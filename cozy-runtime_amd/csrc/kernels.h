@@ -76,6 +76,59 @@ hipError_t svdq_int4_gemm(const uint8_t* act, const uint16_t* ascales, const uin
                           const void* bias, void* out, bool out_half, int M, int N, int K, int R,
                           hipStream_t s);
 
+// ------------------------------------------------------------------ stored-format decode
+// Element codes, numeric part dtypes, scale grids and second-level modes of the decode kernels
+// (internal/encoding/formats.py:438-868; internal/decode_cores.py:196-230).
+enum DecodeCode : int { kCodeI8 = 0, kCodeE4m3 = 1, kCodeE5m2 = 2, kCodeE2m1 = 3 };
+enum DecodeNum : int { kNumF32 = 0, kNumBf16 = 1, kNumF16 = 2, kNumE8m0 = 3, kNumE4m3 = 4 };
+enum DecodeGrid : int { kGridTensor = 0, kGridRow = 1, kGridCol = 2, kGridBlocks = 3 };
+enum DecodeSecond : int { kSecondNone = 0, kSecondMultiply = 1, kSecondDivide = 2 };
+enum DecodePost : int { kPostNone = 0, kPostOne = 1, kPostColumn = 2 };
+
+// One matrix [rows, cols] (or a stack of them, `weight_stride` bytes, `scale_stride` scale
+// elements and `out_stride` outputs apart; `scale_2_step` 1 for a factor per matrix).
+struct TableDecode {
+    const uint8_t* weight;
+    int64_t weight_stride;
+    const void* scale;
+    int64_t scale_stride;
+    int scale_type, scale_size, grid, block, tiled;
+    const float* scale_2;
+    int scale_2_step, second;
+    const void* post;
+    int post_type, post_mode, high_first;
+    void* out;
+    int64_t out_stride;
+    int64_t rows, cols;
+};
+
+// svdq.nvfp4: codes [rows, cols/2], E4M3 scales per 16 (row-major or 128x4 tiles), scale_2,
+// optional channel scale [rows], smoothing [cols], lowrank_down [rank, cols], lowrank_up
+// [rows, rank].
+struct SvdqDecode {
+    const uint8_t* weight;
+    const uint8_t* scale;
+    int tiled, high_first, divide;
+    const float* scale_2;
+    const void* channel;
+    int channel_type;
+    const void* smooth;
+    int smooth_type;
+    const void* down;
+    int down_type;
+    const void* up;
+    int up_type, rank;
+    void* out;
+    int64_t rows, cols;
+};
+
+hipError_t decode_table(const TableDecode& a, int code, int out_type, int matrices, hipStream_t s);
+// `digits` = k of the 4^k group; groups of 64 and more need total % 64 == 0 and 16-byte
+// aligned parts (hipErrorInvalidValue otherwise).
+hipError_t decode_convrot(const int8_t* w, const void* scale, int scale_type, void* out, int out_type,
+                          int64_t rows, int64_t cols, int digits, hipStream_t s);
+hipError_t decode_svdq(const SvdqDecode& a, int out_type, hipStream_t s);
+
 }  // namespace cozyq
 
 namespace cozyq {

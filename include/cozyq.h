@@ -163,6 +163,45 @@ int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales
                          const void* up, const void* bias, void* out, int out_half, int M, int N,
                          int K, int R, void* stream);
 
+/* Stored-format decode into a float destination (reference: the `decoded_float` providers of
+ * internal/encoding/formats.py — TensorwiseDequant :438-488, RowwiseDequant :507-569,
+ * MicroScaledDequant :588-650, Nvfp4Dequant :762-868 — and the nvfp4 decode core with its
+ * per-column factor, internal/decode_schemes.py:362-431 and internal/decode_cores.py:196-230):
+ *   out[e, i, j] = round(v · s · g)  (second 1),  round(v · (s / g))  (second 2),
+ *   then · post (one factor or post[j]) before the rounding; each step a float32 rounding,
+ *   one rounding (nearest even) into out.
+ * v = value(w[e, i, j]) by `code`: 0 int8, 1 E4M3, 2 E5M2, 3 E2M1 packed two a byte (element 2k
+ * in the low nibble, the high one with high_first). s = scale[grid(i, j)] by `grid`: 0 one
+ * scale, 1 one per row, 2 one per column, 3 row blocks of `block` columns stored row-major
+ * [rows, ceil(cols/block)] or, with `tiled`, in cuBLAS's 128x4 tiles (formats.py:154-178).
+ * g = scale_2[e · scale_2_step]. Part dtypes (scale_type, post_type, out_type): 0 f32, 1 bf16,
+ * 2 f16, 3 E8M0 (255 is NaN), 4 E4M3; out is f32, bf16 or f16. `matrices` stacked matrices of
+ * [rows, cols] each, with a scale grid (row, block) and an optional scale_2 of their own. */
+int cozyq_decode(int device, int code, const void* w, const void* scale, int scale_type, int grid,
+                 int block, int tiled, const float* scale_2, int scale_2_step, int second,
+                 const void* post, int post_type, int post_mode, int high_first, void* out,
+                 int out_type, int64_t rows, int64_t cols, int matrices, void* stream);
+
+/* int8.convrot decode (reference: Int8ConvRotDequant.decode, internal/encoding/formats.py:
+ * 733-752): out[i, :] = round((H·w[i, g])·scale[i]·2^-k) for each rotation_size = 4^k group g,
+ * H the regular H4⊗…⊗H4 (formats.py:657-671) summed exactly in int32. rotation_size in
+ * 4 .. 65536, cols % rotation_size == 0; from 64 up, w and out 16-byte aligned. scale_type and
+ * out_type as cozyq_decode (0-2). */
+int cozyq_decode_convrot(int device, const int8_t* w, const void* scale, int scale_type,
+                         int rotation_size, void* out, int out_type, int64_t rows, int64_t cols,
+                         void* stream);
+
+/* svdq.nvfp4 decode (reference: internal/decode_schemes.py:464-489): the nvfp4 value of
+ * cozyq_decode (code 3, blocks of 16, E4M3 scales, second 1 or 2 by `divide`), · channel_scale[i]
+ * (f32 or E4M3, optional), · smooth[j], then + up[i, r]·down[r, j] for r = 0 .. rank−1, each
+ * product and sum rounded to float32, one rounding into out. w [rows, cols/2], scale
+ * [rows, cols/16] (or tiled), smooth [cols], down [rank, cols], up [rows, rank]; cols % 16 == 0. */
+int cozyq_decode_svdq(int device, const uint8_t* w, const uint8_t* scale, int tiled,
+                      int high_first, const float* scale_2, int divide, const void* channel_scale,
+                      int channel_type, const void* smooth, int smooth_type, const void* down,
+                      int down_type, const void* up, int up_type, int rank, void* out,
+                      int out_type, int64_t rows, int64_t cols, void* stream);
+
 /* Test entries (no reference counterpart): the kernels' scalar conversions run on the host,
  * so CPU tests can hold the device code's arithmetic against torch without a GPU. */
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n);

@@ -504,6 +504,82 @@ def decode_rowwise(payload: torch.Tensor, scale: torch.Tensor, dtype: torch.dtyp
     return (payload.to(torch.float32) * scale.to(torch.float32).reshape(rows, 1)).to(dtype)
 
 
+def decode_columnwise(payload: torch.Tensor, scale: torch.Tensor,
+                      dtype: torch.dtype) -> torch.Tensor:
+    """`RowwiseDequant.decode` for a `.columnwise` scheme (`internal/encoding/formats.py:
+    557-569`): data·scale[column] in float32, one cast."""
+    cols = int(payload.shape[-1])
+    return (payload.to(torch.float32) * scale.to(torch.float32).reshape(1, cols)).to(dtype)
+
+
+def decode_tensorwise(payload: torch.Tensor, scale: torch.Tensor,
+                      dtype: torch.dtype) -> torch.Tensor:
+    """`TensorwiseDequant.decode` (`internal/encoding/formats.py:485-492`): data·scale in
+    float32, one cast."""
+    return (payload.to(torch.float32) * scale.to(torch.float32).reshape(())).to(dtype)
+
+
+#: E2M1 by nibble, bit 3 the sign (`internal/encoding/formats.py:755-759`).
+E2M1_VALUES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+               -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0)  # fmt: skip
+NVFP4_BLOCK = 16
+
+
+def nvfp4_values(weight: torch.Tensor, scale: torch.Tensor, scale_2: torch.Tensor,
+                 high_first: bool = False, divide: bool = False) -> torch.Tensor:
+    """`formats.nvfp4_values` (`internal/encoding/formats.py:762-783`) for one matrix: bytes
+    `[R, C/2]` (element 2k in the low nibble, or the high one with `high_first`), a row-major
+    E4M3 grid `[R, C/16]`, a float32 `scale_2` → float32 `[R, C]`: `(e2m1·s)·g`, or
+    `e2m1·(s/g)` with `divide`."""
+    rows, cols = int(weight.shape[0]), int(weight.shape[1]) * 2
+    w = weight.view(torch.uint8)
+    pair = (w >> 4, w & 0x0F) if high_first else (w & 0x0F, w >> 4)
+    codes = torch.stack(pair, dim=-1).reshape(rows, cols)
+    lut = torch.tensor(E2M1_VALUES, dtype=torch.float32)
+    blocks = lut[codes.long()].view(rows, cols // NVFP4_BLOCK, NVFP4_BLOCK)
+    second = scale_2.to(torch.float32).reshape(())
+    block_scale = scale.to(torch.float32).reshape(rows, cols // NVFP4_BLOCK, 1)
+    if divide:
+        return blocks.mul_(block_scale / second).view(rows, cols)
+    blocks.mul_(block_scale)
+    return blocks.view(rows, cols).mul_(second)
+
+
+def decode_nvfp4(weight: torch.Tensor, scale: torch.Tensor, scale_2: torch.Tensor, layout: str,
+                 high_first: bool, divide: bool, post: torch.Tensor | None,
+                 dtype: torch.dtype) -> torch.Tensor:
+    """The nvfp4 decode of one matrix (`internal/decode_schemes.py:362-402`,
+    `internal/decode_cores.py:196-230`): `nvfp4_values`, then `· post[j]` (AWQ's
+    `pre_quant_scale`) when given, one cast. `scale` row-major or in cuBLAS's 128x4 tiles."""
+    rows, cols = int(weight.shape[0]), int(weight.shape[1]) * 2
+    grid = from_blocked(scale.reshape(-1), rows, cols // NVFP4_BLOCK) \
+        if layout == "cublas_128x4" else scale.reshape(rows, cols // NVFP4_BLOCK)
+    value = nvfp4_values(weight, grid, scale_2, high_first, divide)
+    if post is not None:
+        factor = post.reshape(-1).to(torch.float32)
+        value = value * (factor if factor.numel() == cols else factor[0])
+    return value.to(dtype)
+
+
+def decode_svdq_nvfp4(weight: torch.Tensor, scale: torch.Tensor, scale_2: torch.Tensor,
+                      layout: str, high_first: bool, divide: bool,
+                      channel: torch.Tensor | None, smooth: torch.Tensor, down: torch.Tensor,
+                      up: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """The svdq.nvfp4 decode (`internal/decode_schemes.py:464-489`): the nvfp4 value,
+    `· channel[i]`, `· smooth[j]`, then `+ up[i, r]·down[r, j]` for r in order, each product
+    rounded to float32 before its add; one cast."""
+    rows, cols = int(weight.shape[0]), int(weight.shape[1]) * 2
+    value = decode_nvfp4(weight, scale, scale_2, layout, high_first, divide, None, torch.float32)
+    if channel is not None:
+        value = value * channel.to(torch.float32).reshape(rows, 1)
+    value = value * smooth.to(torch.float32).reshape(1, cols)
+    u = up.to(torch.float32).reshape(rows, -1)
+    d = down.to(torch.float32).reshape(u.shape[1], cols)
+    for r in range(u.shape[1]):
+        value.add_(torch.mul(u[:, r : r + 1], d[r : r + 1, :]))
+    return value.to(dtype)
+
+
 def decode_mxfp8(payload: torch.Tensor, scale: torch.Tensor, layout: str,
                  dtype: torch.dtype) -> torch.Tensor:
     """`MicroScaledDequant.decode` (`internal/encoding/formats.py:638-650`) for one matrix."""

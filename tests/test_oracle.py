@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 import torch
 
+import vectors
 from oracle import laws
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -72,14 +73,9 @@ def test_int8_rowwise_decode_vectors(case):
     assert _same(got, case)
 
 
-@pytest.mark.parametrize(
-    "case",
-    [c for c in _cases("fp8", "fp8.rowwise") if c["parts"][0]["dtype"] == "F8_E4M3"],
-    ids=lambda c: c["key"],
-)
+@pytest.mark.parametrize("case", _cases("fp8", "fp8.rowwise"), ids=lambda c: c["key"])
 def test_fp8_rowwise_decode_vectors(case):
-    """Pins the E4M3 element values the fp8 lane's codes stand for (the E5M2 cases are another
-    element type, off this path)."""
+    """Pins the E4M3 and E5M2 element values and the float32-then-one-cast rounding."""
     parts = _parts(case)
     shape = case["shape"]
     rows = int(np.prod(shape[:-1]))
@@ -102,6 +98,78 @@ def test_mxfp8_decode_vectors(case):
     else:
         got = laws.decode_mxfp8(weight, scale, layout, dtype)
     assert _same(got, case)
+
+
+@pytest.mark.parametrize(
+    "case", vectors.cases("fp8", "fp8.tensorwise") + vectors.cases("int8", "int8.tensorwise"),
+    ids=lambda c: c["key"])
+def test_tensorwise_decode_vectors(case):
+    parts = vectors.parts(case)
+    got = laws.decode_tensorwise(parts["weight"], parts["scale"], DTYPES[case["dtype"]])
+    assert vectors.same(got, case)
+
+
+@pytest.mark.parametrize(
+    "case", vectors.cases("fp8", "fp8.columnwise") + vectors.cases("int8", "int8.columnwise"),
+    ids=lambda c: c["key"])
+def test_columnwise_decode_vectors(case):
+    parts = vectors.parts(case)
+    got = laws.decode_columnwise(parts["weight"], parts["scale"], DTYPES[case["dtype"]])
+    assert vectors.same(got, case)
+
+
+def _nvfp4_oracle(case: dict) -> torch.Tensor:
+    """The nvfp4 law over a case's parts: one matrix at a time for a stack (each with its own
+    scale_2 and, under cuBLAS tiles, its own grid)."""
+    parts, params = vectors.parts(case), case["encoding"]["params"]
+    shape = case["shape"]
+    rows, cols = shape[-2], shape[-1]
+    stack = int(np.prod(shape[:-2])) if len(shape) > 2 else 1
+    weight = parts["weight"].reshape(stack, rows, cols // 2)
+    scale = parts["scale"].reshape(stack, -1)
+    second = parts["scale_2"].reshape(-1)
+    out = [laws.decode_nvfp4(weight[e], scale[e], second[e if second.numel() > 1 else 0],
+                             params["scale_layout"], params["nibble_order"] == "high_first",
+                             params["global_scale"] == "divide", parts.get("pre_quant_scale"),
+                             DTYPES[case["dtype"]]) for e in range(stack)]  # fmt: skip
+    return torch.stack(out).reshape(shape)
+
+
+@pytest.mark.parametrize("case", vectors.cases("nvfp4", "nvfp4"), ids=lambda c: c["key"])
+def test_nvfp4_decode_vectors(case):
+    """Pins E2M1's values, both nibble orders, multiply/divide second-level scales, the E4M3
+    block scales in both layouts, per-matrix scale_2 and AWQ's per-column pre_quant_scale."""
+    assert vectors.same(_nvfp4_oracle(case), case)
+
+
+@pytest.mark.parametrize("case", vectors.cases("svdq", "svdq"), ids=lambda c: c["key"])
+def test_svdq_nvfp4_decode_vectors(case):
+    """Pins the svdq.nvfp4 decode: channel scale (f32 or E4M3), smoothing, and the low-rank
+    term added product by product in rank order."""
+    parts, params = vectors.parts(case), case["encoding"]["params"]
+    got = laws.decode_svdq_nvfp4(
+        parts["weight"], parts["scale"], parts["scale_2"], params["scale_layout"],
+        params["nibble_order"] == "high_first", params["global_scale"] == "divide",
+        parts.get("channel_scale"), parts["pre_quant_scale"], parts["lowrank_down"],
+        parts["lowrank_up"], DTYPES[case["dtype"]])  # fmt: skip
+    assert vectors.same(got, case)
+
+
+def test_svdq_decode_rank_order_is_pinned():
+    """A plausible slip — one fused sum of the low-rank products instead of adding each rounded
+    product in turn — changes the result on values chosen to expose it, so the vectors above
+    hold the order, not just the sum."""
+    torch.manual_seed(3)
+    rows, cols, rank = 4, 16, 8
+    weight = torch.zeros(rows, cols // 2, dtype=torch.uint8)
+    scale = torch.ones(rows, 1).to(torch.float8_e4m3fn)
+    up = torch.randn(rows, rank) * 1e3
+    down = torch.randn(rank, cols) * 1e-3
+    smooth = torch.ones(cols)
+    law = laws.decode_svdq_nvfp4(weight, scale, torch.tensor(1.0), "row_major", False, False,
+                                 None, smooth, down, up, torch.float32)  # fmt: skip
+    fused = (up.double() @ down.double()).float()
+    assert not torch.equal(law, fused)
 
 
 def test_blocked_layout_round_trip():
