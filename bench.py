@@ -382,6 +382,86 @@ def bench_svdq(torch, ops, lib, stream, steps: int) -> dict:
             "kernel": "svdq_gemm_kernel (int4 unpacked to int8, 32x32x32 MFMA, per-group rescale)"}
 
 
+def bench_weights(torch, ops, lib, stream, steps: int) -> dict:
+    """The stored-format decode kernels (checkpoint weight -> bf16) on the configs' weight
+    shapes: int8.convrot (256) and mxfp8 (cuBLAS 128x4 scales) on config 2's [12288, 3072],
+    fp8.rowwise on config 3's [14336, 4096], nvfp4 (high-first nibbles, 128x4 E4M3 scales,
+    divide) on [12288, 3072] and svdq.nvfp4 (rank 32) on config 4's [3072, 3072]. Each runs over
+    3 rotating (weight, destination) pairs (beyond the 256 MB MALL), graph-replayed through the
+    C ABI. Bytes are the parts read once and the destination written once."""
+    gen = torch.Generator(device="cuda").manual_seed(95)
+    copies, replays = 3, max(4, steps // 8)
+
+    def rnd(shape, dtype=torch.uint8):
+        return torch.randint(0, 256, shape, generator=gen, device="cuda", dtype=torch.int32).to(torch.uint8).view(dtype)
+
+    def measure(name, make, launch, nbytes):
+        sets = [make() for _ in range(copies)]
+        turn = [0]
+
+        def go(raw):
+            launch(sets[turn[0] % copies], raw)
+            turn[0] += 1
+
+        us = _graph_us(torch, go, 4 * copies, replays)
+        return {"format": name, "us": us, "gbs": nbytes / (us * 1e-6) / 1e9,
+                "frac_hbm": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, "bytes": nbytes}
+
+    out = []
+    n, k = 12288, 3072
+
+    def convrot():
+        return (rnd((n, k), torch.int8), torch.rand(n, device="cuda"), torch.empty(n, k, dtype=torch.bfloat16, device="cuda"))
+
+    out.append(measure("int8.convrot256 [12288,3072]", convrot, lambda t, raw: _check(lib.cozyq_decode_convrot(
+        0, t[0].data_ptr(), t[1].data_ptr(), 0, 256, t[2].data_ptr(), 1, n, k, raw)), n * k * 3 + n * 4))
+
+    n3, k3 = 14336, 4096
+
+    def rowwise():
+        return (rnd((n3, k3)), torch.rand(n3, device="cuda"), torch.empty(n3, k3, dtype=torch.bfloat16, device="cuda"))
+
+    out.append(measure("fp8.rowwise [14336,4096]", rowwise, lambda t, raw: _check(lib.cozyq_decode(
+        0, 1, t[0].data_ptr(), t[1].data_ptr(), 0, 1, 1, 0, None, 0, 0, None, 0, 0, 0, t[2].data_ptr(), 1,
+        n3, k3, 1, raw)), n3 * k3 * 3 + n3 * 4))
+
+    blocks = k // 32
+    tiled = (-(-n // 128) * 128) * (-(-blocks // 4) * 4)
+
+    def mx():
+        return (rnd((n, k)) & 0x77, torch.randint(110, 130, (tiled,), device="cuda", dtype=torch.int32).to(torch.uint8),
+                torch.empty(n, k, dtype=torch.bfloat16, device="cuda"))
+
+    out.append(measure("mxfp8 128x4 [12288,3072]", mx, lambda t, raw: _check(lib.cozyq_decode(
+        0, 1, t[0].data_ptr(), t[1].data_ptr(), 3, 3, 32, 1, None, 0, 0, None, 0, 0, 0, t[2].data_ptr(), 1,
+        n, k, 1, raw)), n * k * 3 + tiled))
+
+    tiled16 = (-(-n // 128) * 128) * (-(-(k // 16) // 4) * 4)
+    second = torch.tensor([0.5], device="cuda")
+
+    def nvfp4():
+        return (rnd((n, k // 2)), rnd((tiled16,)) & 0x3F, torch.empty(n, k, dtype=torch.bfloat16, device="cuda"))
+
+    out.append(measure("nvfp4 128x4 [12288,3072]", nvfp4, lambda t, raw: _check(lib.cozyq_decode(
+        0, 3, t[0].data_ptr(), t[1].data_ptr(), 4, 3, 16, 1, second.data_ptr(), 0, 2, None, 0, 0, 1,
+        t[2].data_ptr(), 1, n, k, 1, raw)), n * k // 2 + tiled16 + n * k * 2))
+
+    n4, k4, rank = 3072, 3072, 32
+    smooth = torch.rand(k4, device="cuda") + 0.5
+
+    def svdq():
+        return (rnd((n4, k4 // 2)), rnd((n4, k4 // 16)) & 0x3F,
+                (torch.randn(rank, k4, device="cuda") * 0.05).to(torch.bfloat16),
+                (torch.randn(n4, rank, device="cuda") * 0.05).to(torch.bfloat16),
+                torch.empty(n4, k4, dtype=torch.bfloat16, device="cuda"))
+
+    out.append(measure("svdq.nvfp4 r32 [3072,3072]", svdq, lambda t, raw: _check(lib.cozyq_decode_svdq(
+        0, t[0].data_ptr(), t[1].data_ptr(), 0, 0, second.data_ptr(), 0, None, 0, smooth.data_ptr(), 0,
+        t[2].data_ptr(), 1, t[3].data_ptr(), 1, rank, t[4].data_ptr(), 1, n4, k4, raw)),
+        n4 * k4 // 2 + n4 * k4 // 16 + n4 * k4 * 2 + (n4 + k4) * rank * 2 + k4 * 4))
+    return {"decode_formats": out}
+
+
 def cpu_baseline(torch, rows: int = 1024) -> dict:
     """The reference's CPU law for config 2 on rows 0..rows-1 of the batch: rotation + per-token
     int8 (`quantize_rows`), the literal int32 matmul, both scales, bias and GELU."""
@@ -430,6 +510,8 @@ def only(torch, ops, lib, stream, args) -> int:
         figures = bench_int8_decode(torch, ops, lib, stream, args.steps)
     elif args.only == "w4a8":
         figures = bench_w4a8(torch, ops, lib, stream, args.steps)
+    elif args.only == "weights":
+        figures = bench_weights(torch, ops, lib, stream, args.steps)
     else:
         figures = bench_svdq(torch, ops, lib, stream, args.steps)
     print(json.dumps({"only": args.only, **figures}))
@@ -446,7 +528,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=100)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
-    parser.add_argument("--only", choices=("c2", "decode", "int8_decode", "w4a8", "fp8", "svdq", "mx", "copy"),
+    parser.add_argument("--only", choices=("c2", "decode", "int8_decode", "w4a8", "fp8", "svdq", "mx", "weights",
+                                                    "copy"),
                         help="profiling aid: run one leg (or a plain 256 MiB device copy, the "
                              "counter calibration) --steps times and print its figures only")  # fmt: skip
     args = parser.parse_args()
@@ -478,6 +561,7 @@ def main() -> int:
         configs["w4a8"] = bench_w4a8(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["c4_svdq_w4a4"] = bench_svdq(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["c5_mxfp8"] = bench_mx(torch, ops, lib, stream, max(10, args.steps // 2))
+        configs["weight_decode"] = bench_weights(torch, ops, lib, stream, args.steps)["decode_formats"]
         print("[bench] extra configs done", file=sys.stderr, flush=True)
     baseline = None if args.no_cpu else cpu_baseline(torch)
     line = {

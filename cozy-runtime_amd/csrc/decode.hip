@@ -71,20 +71,70 @@ __device__ __forceinline__ void store_one(void* out, int64_t idx, float v) {
     else static_cast<uint16_t*>(out)[idx] = narrow<kOut == kNumF16>(v);
 }
 
-template <int kOut>
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Two floats → two bf16 in one word, first in the low half: v_cvt_pk_bf16_f32, round to
+// nearest even (NaN stays NaN).
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
+template <bool kStream>
+__device__ __forceinline__ void put16(u32x4* dst, u32x4 v) {
+    if constexpr (kStream) __builtin_nontemporal_store(v, dst);
+    else *dst = v;
+}
+
+// 16 outputs from element `idx` on, as 16-byte stores; `kStream` marks them non-temporal (a
+// decoded weight is written once), which pays where a wave's stores fill whole lines together
+// and costs where each lane writes a line of its own.
+template <int kOut, bool kStream = true>
 __device__ __forceinline__ void store16(void* out, int64_t idx, const float (&v)[16]) {
     if constexpr (kOut == kNumF32) {
-        float4* dst = reinterpret_cast<float4*>(static_cast<float*>(out) + idx);
+        u32x4* dst = reinterpret_cast<u32x4*>(static_cast<float*>(out) + idx);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) dst[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        for (int k = 0; k < 4; ++k)
+            put16<kStream>(dst + k, u32x4{bits_of(v[4 * k]), bits_of(v[4 * k + 1]), bits_of(v[4 * k + 2]),
+                                          bits_of(v[4 * k + 3])});
     } else {
         uint32_t w[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            w[k] = narrow<kOut == kNumF16>(v[2 * k]) | (static_cast<uint32_t>(narrow<kOut == kNumF16>(v[2 * k + 1])) << 16);
-        uint4* dst = reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + idx);
-        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        for (int k = 0; k < 8; ++k) {
+            if constexpr (kOut == kNumBf16) w[k] = bf16_pair(v[2 * k], v[2 * k + 1]);
+            else w[k] = narrow<true>(v[2 * k]) | (static_cast<uint32_t>(narrow<true>(v[2 * k + 1])) << 16);
+        }
+        u32x4* dst = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + idx);
+        put16<kStream>(dst, u32x4{w[0], w[1], w[2], w[3]});
+        put16<kStream>(dst + 1, u32x4{w[4], w[5], w[6], w[7]});
+    }
+}
+
+// The values of 16 one-byte codes held in four words, first code in the low byte: E4M3 and E5M2
+// through gfx950's v_cvt_pk_f32_fp8 / v_cvt_pk_f32_bf8 (OCP formats, exact, NaN and infinity
+// kept), int8 by sign extension.
+template <int kCode>
+__device__ __forceinline__ void values16(const uint32_t (&w)[4], float (&v)[16]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if constexpr (kCode == kCodeI8) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) v[4 * q + b] = static_cast<float>(static_cast<int8_t>(w[q] >> (8 * b)));
+        } else {
+            f32x2 lo, hi;
+            if constexpr (kCode == kCodeE4m3) {
+                lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[q]), false);
+                hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[q]), true);
+            } else {
+                lo = __builtin_amdgcn_cvt_pk_f32_bf8(static_cast<int>(w[q]), false);
+                hi = __builtin_amdgcn_cvt_pk_f32_bf8(static_cast<int>(w[q]), true);
+            }
+            v[4 * q] = lo.x;
+            v[4 * q + 1] = lo.y;
+            v[4 * q + 2] = hi.x;
+            v[4 * q + 3] = hi.y;
+        }
     }
 }
 
@@ -113,6 +163,40 @@ __device__ __forceinline__ float table_law(int second, float v, float s, float g
     return v;
 }
 
+// A wave's 64 runs of 16 outputs leave through LDS: each lane writes its run (2 or 4 16-byte
+// chunks), then store k of the wave writes chunks [64k, 64k + 64) — 1 KB of whole lines — as
+// non-temporal stores. Chunks of runs at or past `runs` are not stored.
+template <int kOut>
+__device__ __forceinline__ void store_runs(void* out, int64_t wave_run, int64_t runs, const float (&v)[16],
+                                           u32x4* lds, int lane) {
+    constexpr int kChunks = kOut == kNumF32 ? 4 : 2;
+    u32x4 c[kChunks];
+    if constexpr (kOut == kNumF32) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            c[q] = u32x4{bits_of(v[4 * q]), bits_of(v[4 * q + 1]), bits_of(v[4 * q + 2]), bits_of(v[4 * q + 3])};
+    } else {
+        uint32_t w[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if constexpr (kOut == kNumBf16) w[k] = bf16_pair(v[2 * k], v[2 * k + 1]);
+            else w[k] = narrow<true>(v[2 * k]) | (static_cast<uint32_t>(narrow<true>(v[2 * k + 1])) << 16);
+        }
+        c[0] = u32x4{w[0], w[1], w[2], w[3]};
+        c[1] = u32x4{w[4], w[5], w[6], w[7]};
+    }
+#pragma unroll
+    for (int q = 0; q < kChunks; ++q) lds[lane * kChunks + (q ^ (lane & (kChunks - 1)))] = c[q];
+    __builtin_amdgcn_wave_barrier();
+    u32x4* base = reinterpret_cast<u32x4*>(static_cast<uint8_t*>(out) + wave_run * 16 * (kOut == kNumF32 ? 4 : 2));
+#pragma unroll
+    for (int k = 0; k < kChunks; ++k) {
+        const int chunk = 64 * k + lane, owner = chunk / kChunks, q = chunk % kChunks;
+        const u32x4 word = lds[owner * kChunks + (q ^ (owner & (kChunks - 1)))];
+        if (wave_run + owner < runs) __builtin_nontemporal_store(word, base + chunk);
+    }
+}
+
 // Runs of 16 elements: rows are whole runs (cols % 16 == 0), the parts 16-byte aligned (8 for
 // packed E2M1) and the block size, if any, a multiple of 16, so a run has one block scale.
 template <int kCode, int kOut>
@@ -120,36 +204,46 @@ __global__ __launch_bounds__(256) void table_run_kernel(TableDecode a) {
     const int64_t e = blockIdx.y;
     const int64_t runs = a.rows * a.cols / 16;
     const int64_t run = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (run >= runs) return;
-    const int64_t i = run / (a.cols / 16), j0 = (run % (a.cols / 16)) * 16;
+    __shared__ u32x4 stage[4 * 64 * (kOut == kNumF32 ? 4 : 2)];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t wave_run = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave;
+    if (wave_run >= runs) return;  // whole waves only: the stores below exchange within a wave
+    const bool live = run < runs;
+    const int64_t at = live ? run : wave_run;  // idle lanes decode the wave's first run, unstored
+    const int64_t i = at / (a.cols / 16), j0 = (at % (a.cols / 16)) * 16;
     const uint8_t* weight = a.weight + e * a.weight_stride;
     const void* scale = static_cast<const uint8_t*>(a.scale) + e * a.scale_stride * a.scale_size;
     const float g = a.second ? a.scale_2[e * a.scale_2_step] : 1.0f;
-    uint32_t c[16];
+    float v[16];
     if constexpr (kCode == kCodeE2m1) {
-        const uint2 raw = *reinterpret_cast<const uint2*>(weight + run * 8);
-        const uint32_t lo_first = a.high_first ? 0u : 1u;
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(weight + at * 8));
+        // v_cvt_scalef32_pk_f32_fp4 at scale 1: a byte's low nibble to .x, its high one to .y.
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const uint32_t byte = ((k < 4 ? raw.x : raw.y) >> (8 * (k & 3))) & 0xffu;
-            c[2 * k] = lo_first ? (byte & 15u) : (byte >> 4);
-            c[2 * k + 1] = lo_first ? (byte >> 4) : (byte & 15u);
+            const int word = static_cast<int>(k < 4 ? raw.x : raw.y);
+            f32x2 pair;
+            switch (k & 3) {
+                case 0: pair = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 0); break;
+                case 1: pair = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 1); break;
+                case 2: pair = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 2); break;
+                default: pair = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 3);
+            }
+            v[2 * k] = a.high_first ? pair.y : pair.x;
+            v[2 * k + 1] = a.high_first ? pair.x : pair.y;
         }
     } else {
-        const uint4 raw = *reinterpret_cast<const uint4*>(weight + run * 16);
+        const u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(weight + at * 16));
         const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-        for (int k = 0; k < 16; ++k) c[k] = (w4[k >> 2] >> (8 * (k & 3))) & 0xffu;
+        values16<kCode>(w4, v);
     }
-    float v[16];
     if (a.grid == kGridCol) {
 #pragma unroll
-        for (int k = 0; k < 16; ++k)
-            v[k] = table_law(a.second, code_value<kCode>(c[k]), num_at(scale, a.scale_type, j0 + k), g);
+        for (int k = 0; k < 16; ++k) v[k] = table_law(a.second, v[k], num_at(scale, a.scale_type, j0 + k), g);
     } else {
         const float s = num_at(scale, a.scale_type, grid_index(a, i, j0));
 #pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = table_law(a.second, code_value<kCode>(c[k]), s, g);
+        for (int k = 0; k < 16; ++k) v[k] = table_law(a.second, v[k], s, g);
     }
     if (a.post_mode == kPostOne) {
         const float p = num_at(a.post, a.post_type, 0);
@@ -159,7 +253,8 @@ __global__ __launch_bounds__(256) void table_run_kernel(TableDecode a) {
 #pragma unroll
         for (int k = 0; k < 16; ++k) v[k] = v[k] * num_at(a.post, a.post_type, j0 + k);
     }
-    store16<kOut>(a.out, e * a.out_stride + run * 16, v);
+    void* out = static_cast<uint8_t*>(a.out) + e * a.out_stride * (kOut == kNumF32 ? 4 : 2);
+    store_runs<kOut>(out, wave_run, runs, v, stage + wave * 64 * (kOut == kNumF32 ? 4 : 2), lane);
 }
 
 // Any shape and alignment: one element per thread, grid-stride.
@@ -220,6 +315,9 @@ hipError_t table_out(const TableDecode& a, int out_type, int matrices, hipStream
 
 // ---------------------------------------------------------------------- int8.convrot
 
+// A plain DPP move. (Asked with bound_ctrl set, the backend folds the move into the consuming
+// v_add_u32_dpp / v_subrev_u32_dpp; that form produced wrong sums on gfx950 in this kernel, so
+// the moves stay separate.)
 template <int kCtrl>
 __device__ __forceinline__ int dpp(int v) {
     return __builtin_amdgcn_mov_dpp(v, kCtrl, 0xf, 0xf, false);
@@ -354,22 +452,53 @@ void convrot_kernel(
         }
     }
 
-    if (!active) return;
     constexpr float kInv = 1.0f / static_cast<float>(1 << kDigits);  // 1/√(4^k), exact
     constexpr int kGroup = 1 << (2 * kDigits);
-    float s = num_at(scale, scale_type, base / cols);
+    float s = active ? num_at(scale, scale_type, base / cols) : 0.0f;
+    float f[64];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        float run[16];
-#pragma unroll
-        for (int b = 0; b < 16; ++b) {
-            const int r = 16 * k + b;
-            if constexpr (kGroup < 64) {  // groups of 4 or 16 may start a new row inside the lane
-                if (r % kGroup == 0 && r > 0) s = num_at(scale, scale_type, (base + r) / cols);
-            }
-            run[b] = (static_cast<float>(v[r]) * s) * kInv;
+    for (int r = 0; r < 64; ++r) {
+        if constexpr (kGroup < 64) {  // groups of 4 or 16 may start a new row inside the lane
+            if (active && r % kGroup == 0 && r > 0) s = num_at(scale, scale_type, (base + r) / cols);
         }
-        store16<kOut>(out, base + 16 * k, run);
+        f[r] = (static_cast<float>(v[r]) * s) * kInv;
+    }
+    if constexpr (kOut == kNumF32 || kDigits > 6) {
+        if (!active) return;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float run[16];
+#pragma unroll
+            for (int b = 0; b < 16; ++b) run[b] = f[16 * k + b];
+            store16<kOut, false>(out, base + 16 * k, run);
+        }
+    } else {
+        // 16-bit outputs leave through LDS: each lane writes its 128 bytes, then store k of the
+        // wave writes bytes [1024k, 1024k + 1024) of the wave's 8 KB, whole lines at once, so the
+        // stores can stream. 16-byte chunks are XOR-swizzled by lane to spread LDS banks.
+        __shared__ u32x4 stage[4 * 64 * 8];
+        u32x4* mine = stage + wave * 512;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            uint32_t w[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const float lo = f[8 * c + 2 * b], hi = f[8 * c + 2 * b + 1];
+                if constexpr (kOut == kNumBf16) w[b] = bf16_pair(lo, hi);
+                else w[b] = narrow<true>(lo) | (static_cast<uint32_t>(narrow<true>(hi)) << 16);
+            }
+            mine[lane * 8 + (c ^ (lane & 7))] = u32x4{w[0], w[1], w[2], w[3]};
+        }
+        __builtin_amdgcn_wave_barrier();
+        const int64_t wave_base = block_base + 4096 * wave;  // first element of the wave
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int owner = 8 * k + lane / 8, chunk = lane % 8;  // lane `owner`'s chunk
+            const u32x4 word = mine[owner * 8 + (chunk ^ (owner & 7))];
+            const int64_t first = wave_base + 512 * k + 8 * lane;
+            if (first < total)
+                __builtin_nontemporal_store(word, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + first));
+        }
     }
 }
 
@@ -439,48 +568,139 @@ hipError_t convrot_digits(const int8_t* w, const void* scale, int scale_type, vo
 
 // ---------------------------------------------------------------------- svdq.nvfp4
 
-// One run of 16 columns of row i a thread (cols % 16 == 0): the nvfp4 value, · c_i, · p_j,
-// then `+ up[i, r] · down[r, j]` for r = 0 .. R−1, each product rounded before its add
-// (internal/decode_schemes.py:464-489).
+// A workgroup takes 32 rows × 256 columns, a thread 2 rows × 16 columns (cols % 16 == 0): the
+// nvfp4 value, · c_i, · p_j, then `+ up[i, r] · down[r, j]` for r = 0 .. R−1, each product
+// rounded before its add (internal/decode_schemes.py:464-489). The factors pass through LDS as
+// float32, 16 ranks at a time: down [16][256] (a run's four 16-byte pieces 256 bytes apart, so
+// the 16 runs of a row read distinct banks) and up transposed [16][32]. Every global read is a
+// bounded buffer load (past the end reads 0) issued without a branch; what rows or columns past
+// the matrix read is never stored.
+constexpr int kSvdqRows = 32, kSvdqCols = 256, kSvdqRanks = 16, kSvdqRowsPer = 2;
+
+// N elements of a float32 / bf16 / f16 part at element offsets `off`, each clamped into the
+// part's `n` elements, issued back to back.
+template <int N>
+__device__ __forceinline__ void load_nums(const void* base, int type, int64_t n, const int64_t (&off)[N],
+                                          float (&out)[N]) {
+    if (type == kNumF32) {
+        const float* f = static_cast<const float*>(base);
+#pragma unroll
+        for (int k = 0; k < N; ++k) out[k] = f[off[k] < n ? off[k] : n - 1];
+    } else {
+        const uint16_t* h = static_cast<const uint16_t*>(base);
+        uint16_t x[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) x[k] = h[off[k] < n ? off[k] : n - 1];
+#pragma unroll
+        for (int k = 0; k < N; ++k) out[k] = type == kNumBf16 ? widen<false>(x[k]) : widen<true>(x[k]);
+    }
+}
+
+
 template <int kOut>
 __global__ __launch_bounds__(256) void svdq_decode_kernel(SvdqDecode a) {
-    const int64_t runs = a.rows * a.cols / 16;
-    const int64_t run = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (run >= runs) return;
-    const int64_t i = run / (a.cols / 16), j0 = (run % (a.cols / 16)) * 16;
-    const uint8_t* packed = a.weight + run * 8;
+    __shared__ float down_lds[kSvdqRanks][kSvdqCols];
+    __shared__ float up_lds[kSvdqRanks][kSvdqRows];
+    const int t = threadIdx.x, run = t % 16, group = t / 16;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.y) * kSvdqRows;
+    const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kSvdqCols;
+    const int64_t j0 = col0 + 16 * run;
     const float g = a.scale_2[0];
+    const int second = a.divide ? kSecondDivide : kSecondMultiply;
     TableDecode grid{};
     grid.grid = kGridBlocks;
     grid.block = 16;
     grid.tiled = a.tiled;
     grid.cols = a.cols;
-    const float s = e4m3_value(a.scale[grid_index(grid, i, j0)]);
-    const float c = a.channel ? num_at(a.channel, a.channel_type, i) : 1.0f;
-    float v[16];
+    // Rows and columns past the matrix read the last row's and column's parts: never stored.
+    const int64_t jc = j0 < a.cols ? j0 : a.cols - 16;
+    float p[16];
+    {
+        int64_t off[16];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t byte = packed[k];
-        const uint32_t first = a.high_first ? byte >> 4 : byte & 15u;
-        const uint32_t second = a.high_first ? byte & 15u : byte >> 4;
-        v[2 * k] = table_law(a.divide ? kSecondDivide : kSecondMultiply, e2m1_value(first), s, g);
-        v[2 * k + 1] = table_law(a.divide ? kSecondDivide : kSecondMultiply, e2m1_value(second), s, g);
+        for (int k = 0; k < 16; ++k) off[k] = jc + k;
+        load_nums<16>(a.smooth, a.smooth_type, a.cols, off, p);
     }
+    float v[kSvdqRowsPer][16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        if (a.channel) v[k] = v[k] * c;
-        v[k] = v[k] * num_at(a.smooth, a.smooth_type, j0 + k);
-    }
-    for (int r = 0; r < a.rank; ++r) {
-        const float u = num_at(a.up, a.up_type, i * a.rank + r);
+    for (int m = 0; m < kSvdqRowsPer; ++m) {
+        const int64_t r = row0 + kSvdqRowsPer * group + m;
+        const int64_t i = r < a.rows ? r : a.rows - 1;
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 raw = *reinterpret_cast<const u32x2*>(a.weight + (i * a.cols + jc) / 2);
+        const float s = e4m3_value(a.scale[grid_index(grid, i, jc)]);
+        const float c = a.channel ? num_at(a.channel, a.channel_type, i) : 1.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t byte = ((k < 4 ? raw.x : raw.y) >> (8 * (k & 3))) & 0xffu;
+            const uint32_t first = a.high_first ? byte >> 4 : byte & 15u;
+            const uint32_t next = a.high_first ? byte & 15u : byte >> 4;
+            v[m][2 * k] = table_law(second, e2m1_value(first), s, g);
+            v[m][2 * k + 1] = table_law(second, e2m1_value(next), s, g);
+        }
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const float prod = u * num_at(a.down, a.down_type, static_cast<int64_t>(r) * a.cols + j0 + k);
-            v[k] = v[k] + prod;
+            if (a.channel) v[m][k] = v[m][k] * c;
+            v[m][k] = v[m][k] * p[k];
         }
     }
+
+    const int pos = 64 * ((t % 16) / 4) + 4 * (t / 16) + t % 4;  // column t's slot in down_lds
+    constexpr int kUpPer = kSvdqRanks * kSvdqRows / 256;  // up entries a thread stages
+    for (int r0 = 0; r0 < a.rank; r0 += kSvdqRanks) {
+        const int chunk = a.rank - r0 < kSvdqRanks ? a.rank - r0 : kSvdqRanks;
+        float x[kSvdqRanks], y[kUpPer];
+        {
+            int64_t off[kSvdqRanks];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) store_one<kOut>(a.out, run * 16 + k, v[k]);
+            for (int rr = 0; rr < kSvdqRanks; ++rr) off[rr] = (r0 + rr) * a.cols + col0 + t;
+            load_nums<kSvdqRanks>(a.down, a.down_type, a.rank * a.cols, off, x);
+            int64_t uoff[kUpPer];
+#pragma unroll
+            for (int q = 0; q < kUpPer; ++q) {
+                const int e = t + 256 * q;
+                uoff[q] = (row0 + e / kSvdqRanks) * a.rank + r0 + e % kSvdqRanks;
+            }
+            load_nums<kUpPer>(a.up, a.up_type, a.rows * a.rank, uoff, y);
+        }
+        __syncthreads();  // the previous chunk's reads are done
+#pragma unroll
+        for (int rr = 0; rr < kSvdqRanks; ++rr) down_lds[rr][pos] = x[rr];
+#pragma unroll
+        for (int q = 0; q < kUpPer; ++q) {
+            const int e = t + 256 * q;
+            up_lds[e % kSvdqRanks][e / kSvdqRanks] = y[q];
+        }
+        __syncthreads();
+        for (int rr = 0; rr < chunk; ++rr) {
+            const float2 u = *reinterpret_cast<const float2*>(&up_lds[rr][kSvdqRowsPer * group]);
+            float d[16];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 z = *reinterpret_cast<const float4*>(&down_lds[rr][64 * k + 4 * run]);
+                d[4 * k] = z.x;
+                d[4 * k + 1] = z.y;
+                d[4 * k + 2] = z.z;
+                d[4 * k + 3] = z.w;
+            }
+            const float um[kSvdqRowsPer] = {u.x, u.y};
+#pragma unroll
+            for (int m = 0; m < kSvdqRowsPer; ++m) {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const float prod = um[m] * d[k];
+                    v[m][k] = v[m][k] + prod;
+                }
+            }
+        }
+    }
+
+    const bool cols_in = j0 < a.cols;
+#pragma unroll
+    for (int m = 0; m < kSvdqRowsPer; ++m) {
+        const int64_t i = row0 + kSvdqRowsPer * group + m;
+        if (cols_in && i < a.rows) store16<kOut, false>(a.out, i * a.cols + j0, v[m]);
+    }
 }
 
 }  // namespace
@@ -504,16 +724,13 @@ hipError_t decode_convrot(const int8_t* w, const void* scale, int scale_type, vo
 }
 
 hipError_t decode_svdq(const SvdqDecode& a, int out_type, hipStream_t s) {
-    const int64_t blocks = (a.rows * a.cols / 16 + 255) / 256;
+    const dim3 grid(static_cast<uint32_t>((a.cols + kSvdqCols - 1) / kSvdqCols),
+                    static_cast<uint32_t>((a.rows + kSvdqRows - 1) / kSvdqRows));
+    if (grid.y > 65535) return hipErrorInvalidValue;
     switch (out_type) {
-        case kNumF32:
-            hipLaunchKernelGGL(svdq_decode_kernel<kNumF32>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, s, a);
-            break;
-        case kNumBf16:
-            hipLaunchKernelGGL(svdq_decode_kernel<kNumBf16>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, s, a);
-            break;
-        default:
-            hipLaunchKernelGGL(svdq_decode_kernel<kNumF16>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, s, a);
+        case kNumF32: hipLaunchKernelGGL(svdq_decode_kernel<kNumF32>, grid, dim3(256), 0, s, a); break;
+        case kNumBf16: hipLaunchKernelGGL(svdq_decode_kernel<kNumBf16>, grid, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL(svdq_decode_kernel<kNumF16>, grid, dim3(256), 0, s, a);
     }
     return hipGetLastError();
 }
