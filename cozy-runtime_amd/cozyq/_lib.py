@@ -74,6 +74,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_int, _P, _P, c_int, c_int, _P, c_int, _P, c_int, _P, c_int, _P, c_int, _P, c_int,
          c_int, _P, c_int, c_int64, c_int64, _P],
     ),
+    "cozyq_encode_int8_convrot": (c_int, [c_int, _P, c_int, _P, _P, c_int64, c_int, _P]),
+    "cozyq_encode_w4a8": (c_int, [c_int, _P, c_int, _P, _P, _P, _P, c_int64, c_int, _P]),
+    "cozyq_encode_fp8_rowwise": (c_int, [c_int, _P, c_int, _P, _P, c_int64, c_int, _P]),
+    "cozyq_encode_mxfp8": (c_int, [c_int, _P, c_int, _P, _P, c_int, c_int64, c_int, _P]),
+    "cozyq_encode_nvfp4": (
+        c_int, [c_int, _P, c_int, _P, _P, _P, _P, _P, c_int64, c_int, _P]
+    ),
+    "cozyq_measure": (c_int, [c_int, _P, c_int, _P, c_int64, _P, c_int, _P, _P]),
     "cozyq_host_e4m3": (None, [_P, _P, c_int64]),
     "cozyq_host_mx_byte": (None, [_P, _P, c_int64]),
     "cozyq_probe_div": (c_int, [c_int, _P, _P, _P, c_int64, _P]),

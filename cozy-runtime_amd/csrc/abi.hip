@@ -329,6 +329,69 @@ int cozyq_decode_svdq(int device, const uint8_t* w, const uint8_t* scale, int ti
     return decode_svdq(a, out_type, on(stream));
 }
 
+int cozyq_encode_int8_convrot(int device, const void* w, int w_type, int8_t* q, float* scale,
+                               int64_t rows, int K, void* stream) {
+    if (w_type < 0 || w_type > 2 || rows < 0 || rows > 0x7fffffff || !fits(K, 256)) return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    if (!aligned16(w) || !aligned16(q)) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::encode_rotated(w, w_type, rows, K, q, scale, nullptr, nullptr, nullptr, false, on(stream));
+}
+
+int cozyq_encode_w4a8(int device, const void* w, int w_type, const float* codebook, uint8_t* codes,
+                      uint8_t* group_scale, float* scale, int64_t rows, int K, void* stream) {
+    if (w_type < 0 || w_type > 2 || rows < 0 || rows > 0x7fffffff || !fits(K, 256) || !codebook)
+        return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    if (!aligned16(w) || (reinterpret_cast<uintptr_t>(codes) & 7)) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::encode_rotated(w, w_type, rows, K, nullptr, scale, codes, group_scale, codebook, true,
+                                 on(stream));
+}
+
+int cozyq_encode_fp8_rowwise(int device, const void* w, int w_type, uint8_t* q, float* scale,
+                             int64_t rows, int K, void* stream) {
+    if (w_type < 0 || w_type > 2 || rows < 0 || rows > 0x7fffffff || !fits(K, 8)) return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    if (!aligned16(w) || (reinterpret_cast<uintptr_t>(q) & 7)) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::encode_fp8_rowwise(w, w_type, rows, K, q, scale, on(stream));
+}
+
+int cozyq_encode_mxfp8(int device, const void* w, int w_type, uint8_t* q, uint8_t* scale, int tiled,
+                       int64_t rows, int K, void* stream) {
+    if (w_type < 0 || w_type > 2 || rows < 0 || !fits(K, 32)) return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    if (!aligned16(w) || (reinterpret_cast<uintptr_t>(q) & 7)) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::encode_mx(w, w_type, rows, K, q, scale, tiled ? 1 : 0, on(stream));
+}
+
+int cozyq_encode_nvfp4(int device, const void* w, int w_type, uint8_t* codes, uint8_t* scale,
+                       float* scale_2, uint32_t* amax, unsigned long long* saturated, int64_t rows,
+                       int K, void* stream) {
+    if (w_type < 0 || w_type > 2 || rows < 0 || !fits(K, 16) || !amax || !saturated || !scale_2)
+        return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    if (!aligned16(w) || (reinterpret_cast<uintptr_t>(codes) & 7)) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::encode_nvfp4(w, w_type, rows, K, amax, codes, scale, scale_2, saturated, on(stream));
+}
+
+int cozyq_measure(int device, const void* w, int w_type, const float* decoded, int64_t total,
+                  double* partial, int parts, double* out, void* stream) {
+    if (w_type < 0 || w_type > 2 || total < 0 || parts < 1 || !w || !decoded || !partial || !out)
+        return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::measure(w, w_type, decoded, total, partial, parts, out, on(stream));
+}
+
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = cozyq::e4m3_rn(in[i]);
 }

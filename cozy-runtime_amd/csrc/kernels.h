@@ -129,6 +129,22 @@ hipError_t decode_convrot(const int8_t* w, const void* scale, int scale_type, vo
                           int64_t rows, int64_t cols, int digits, hipStream_t s);
 hipError_t decode_svdq(const SvdqDecode& a, int out_type, hipStream_t s);
 
+// Weight encoders (encode.hip), input float32 / bf16 / fp16 by `in_type` (kNumF32 .. kNumF16),
+// row-major [rows, K]. encode_rotated: int8.convrot (q, scale) or, with w4, w4a8.convrot (codes
+// [rows, K/2], group_scale [rows, K/16], scale) against a 16-entry codebook; K % 256 == 0.
+// encode_nvfp4 needs a zeroed `amax` word and `saturated` counter.
+hipError_t encode_rotated(const void* w, int in_type, int64_t rows, int K, int8_t* q, float* scale, uint8_t* codes,
+                          uint8_t* group_scale, const float* codebook, bool w4, hipStream_t s);
+hipError_t encode_fp8_rowwise(const void* w, int in_type, int64_t rows, int K, uint8_t* q, float* scale,
+                              hipStream_t s);
+hipError_t encode_mx(const void* w, int in_type, int64_t rows, int K, uint8_t* q, uint8_t* scale, int tiled,
+                     hipStream_t s);
+hipError_t encode_nvfp4(const void* w, int in_type, int64_t rows, int K, uint32_t* amax, uint8_t* codes,
+                        uint8_t* scale, float* scale_2, unsigned long long* saturated, hipStream_t s);
+// [Σ(w − d)², Σ w², max |w − d|] in float64 into `out`, through `parts` float64 triples.
+hipError_t measure(const void* w, int in_type, const float* d, int64_t total, double* partial, int parts,
+                   double* out, hipStream_t s);
+
 }  // namespace cozyq
 
 namespace cozyq {

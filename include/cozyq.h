@@ -202,6 +202,41 @@ int cozyq_decode_svdq(int device, const uint8_t* w, const uint8_t* scale, int ti
                       int down_type, const void* up, int up_type, int rank, void* out,
                       int out_type, int64_t rows, int64_t cols, void* stream);
 
+/* Weight encoders (reference: the tensorfs producers behind derive/microscale.py —
+ * encode_int8_convrot256 :295-334, encode_fp8_rowwise :223-262, encode_w4a8 :349-408,
+ * encode_nvfp4 :146-217 — whose arithmetic tensorfs holds; the laws here are this build's).
+ * w is row-major [rows, K] of w_type 0 f32, 1 bf16, 2 f16, 16-byte aligned.
+ * int8.convrot: r = H256(w)/16 (the reference's stage order), scale = max(amax/127, 1e-12),
+ *   q = clamp(rne(r/scale), ±127); K % 256 == 0.
+ * w4a8.convrot: int8.convrot's r and scale, t = r/scale; per 16-group group_scale =
+ *   e4m3(max|t| / max|codebook|); each 4-bit code the nearest of clamp(rne(codebook[c]·σ), ±127)
+ *   (first on a tie), even k in the low nibble: codes [rows, K/2], group_scale [rows, K/16].
+ * fp8.rowwise: scale = max(amax/448, 1e-12), q = e4m3(clamp(w/scale, ±448)); K % 8 == 0.
+ * mxfp8: per 32-block the MX law of cozyq_mx_quantize; E8M0 grid row-major [rows, K/32] or,
+ *   with tiled, cuBLAS's 128x4 tiles (padding left as the caller filled it); K % 32 == 0.
+ * nvfp4: scale_2 = amax(|w|)/2688 (1 for an all-zero matrix); per 16-block the E4M3 scale of
+ *   e4m3(amax_b/(6·scale_2)) and its two neighbours with the least squared error, codes e2m1 of
+ *   w/(scale·scale_2) to nearest even, saturated at ±6 and counted into `saturated`; low nibble
+ *   first, row-major scales; `amax` and `saturated` zeroed by the caller; K % 16 == 0. */
+int cozyq_encode_int8_convrot(int device, const void* w, int w_type, int8_t* q, float* scale,
+                              int64_t rows, int K, void* stream);
+int cozyq_encode_w4a8(int device, const void* w, int w_type, const float* codebook, uint8_t* codes,
+                      uint8_t* group_scale, float* scale, int64_t rows, int K, void* stream);
+int cozyq_encode_fp8_rowwise(int device, const void* w, int w_type, uint8_t* q, float* scale,
+                             int64_t rows, int K, void* stream);
+int cozyq_encode_mxfp8(int device, const void* w, int w_type, uint8_t* q, uint8_t* scale, int tiled,
+                       int64_t rows, int K, void* stream);
+int cozyq_encode_nvfp4(int device, const void* w, int w_type, uint8_t* codes, uint8_t* scale,
+                       float* scale_2, uint32_t* amax, unsigned long long* saturated, int64_t rows,
+                       int K, void* stream);
+
+/* What an encoding lost (reference: the measured acceptance facts of derive/microscale.py:64-110,
+ * `sse`, `energy`, `max_abs_err`): out = [Σ(w − d)², Σ w², max |w − d|] in float64 over `total`
+ * elements of w (w_type as above) against its float32 decode d, folded through `parts`
+ * float64 triples in `partial`. */
+int cozyq_measure(int device, const void* w, int w_type, const float* decoded, int64_t total,
+                  double* partial, int parts, double* out, void* stream);
+
 /* Test entries (no reference counterpart): the kernels' scalar conversions run on the host,
  * so CPU tests can hold the device code's arithmetic against torch without a GPU. */
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n);

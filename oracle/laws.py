@@ -590,6 +590,91 @@ def decode_mxfp8(payload: torch.Tensor, scale: torch.Tensor, layout: str,
     return mx_dequantize(payload, grid).to(dtype)
 
 
+# -------------------------------------------------------------------- weight encoders
+# Build laws: the reference's producers live in tensorfs (derive/microscale.py:117-408), whose
+# arithmetic is not in the reference, so these encoders are this build's own. int8.convrot and
+# fp8.rowwise weights use `int8_weight_rotated` and `fp8_weight` above; mxfp8 uses `mx_quantize`.
+
+
+def e2m1_code(r: torch.Tensor) -> torch.Tensor:
+    """float32 → E2M1 nibble, nearest even on ties, |r| > 6 saturating to 6; bit 3 set where
+    r < 0 (build law)."""
+    a = r.abs()
+    m = torch.full_like(a, 7, dtype=torch.int32)
+    for bound, code, inclusive in ((5.0, 6, True), (3.5, 5, False), (2.5, 4, True), (1.75, 3, False),
+                                   (1.25, 2, True), (0.75, 1, False), (0.25, 0, True)):  # fmt: skip
+        m = torch.where(a <= bound if inclusive else a < bound, torch.full_like(m, code), m)
+    return m | torch.where(r < 0, 8, 0).to(torch.int32)
+
+
+def encode_nvfp4(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, int]:
+    """nvfp4 producer (build law; the reference's is tensorfs's `nvfp4-min-sse/1`,
+    `derive/microscale.py:146-217`): g = amax|w| / (448·6) (1 for an all-zero matrix); per
+    16-block the E4M3 scale among c0 = e4m3(amax_b / (6g)), c0 − 1 and c0 + 1 (positive codes,
+    first of equals in that order) whose decode `(e2m1·s)·g` has the least float32 squared error
+    summed in k order; codes e2m1 of w / (s·g). Returns bytes [R, K/2] (low nibble first), E4M3
+    bytes [R, K/16], g (float32 scalar) and the count of |w/(s·g)| > 6."""
+    x = w.float()
+    rows, cols = x.shape
+    blocks = x.reshape(rows, cols // 16, 16)
+    amax_t = x.abs().max() if x.numel() else torch.tensor(0.0)
+    g = (amax_t / torch.tensor(E4M3_MAX * 6.0)) if amax_t > 0 else torch.tensor(1.0)
+    amax_b = blocks.abs().amax(dim=-1)
+    six_g = torch.tensor(6.0) * g
+    c0 = (amax_b / six_g).clamp(max=E4M3_MAX).to(torch.float8_e4m3fn).view(torch.uint8).to(torch.int32)
+    cands = (c0, torch.where(c0 > 1, c0 - 1, c0), torch.where(c0 < 0x7E, c0 + 1, c0))
+    lut = torch.tensor(E2M1_VALUES, dtype=torch.float32)
+
+    def trial(code: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        s = code.to(torch.uint8).view(torch.float8_e4m3fn).float().unsqueeze(-1)
+        d = s * g
+        r = torch.where(d > 0, blocks / torch.where(d > 0, d, torch.ones_like(d)), torch.zeros_like(blocks))
+        q = e2m1_code(r)
+        value = torch.where(d > 0, (lut[q.long()] * s) * g, torch.zeros_like(blocks))
+        diff = blocks - value
+        err = torch.zeros_like(amax_b)
+        for k in range(16):
+            err = err + diff[..., k] * diff[..., k]
+        return err, q, r
+
+    best = c0.clone()
+    best_err = torch.full_like(amax_b, float("inf"))
+    for code in cands:
+        err, _, _ = trial(code)
+        take = err < best_err
+        best = torch.where(take, code, best)
+        best_err = torch.where(take, err, best_err)
+    _, q, r = trial(best)
+    saturated = int((r.abs() > 6.0).sum())
+    q = q.reshape(rows, cols).to(torch.uint8)
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).contiguous()
+    return packed, best.to(torch.uint8), g.reshape(()).float(), saturated
+
+
+def encode_w4a8(w: torch.Tensor, codebook: torch.Tensor | None = None,
+                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """w4a8.convrot producer (build law; the reference's is tensorfs's
+    `w4a8-convrot256-fixed/1`, `derive/microscale.py:349-408`): int8.convrot's rotated rows r
+    and row scale s (`quantize_rows_int8`), t = r / s; per 16-group σ = e4m3(max|t| / max|c|)
+    and each code the nearest of the levels clamp(rne(c[q]·σ), ±127) — the unpack law
+    (`w4a8_unpack`) — first on a tie. Returns codes [N, K/2] (even k low), E4M3 [N, K/16] and
+    the float32 row scale [N]."""
+    cb = torch.tensor(W4A8_CODEBOOK, dtype=torch.float32) if codebook is None else codebook.float()
+    x = w.float()
+    rows, cols = x.shape
+    r = hadamard(x, 256).mul_(1.0 / 16)
+    s = (r.abs().amax(dim=-1) / 127.0).clamp(min=SCALE_FLOOR)
+    t = (r / s.unsqueeze(-1)).view(rows, cols // 16, 16)
+    ga = t.abs().amax(dim=-1)
+    sb = (ga / cb.abs().max()).clamp(max=E4M3_MAX).to(torch.float8_e4m3fn)
+    sigma = sb.float().unsqueeze(-1)
+    levels = torch.round(cb.view(1, 1, 16) * sigma).nan_to_num_(0.0).clamp_(-127, 127)
+    dist = (levels.unsqueeze(-2) - t.unsqueeze(-1)).abs()
+    code = dist.argmin(dim=-1).to(torch.uint8).view(rows, cols)
+    packed = (code[:, 0::2] | (code[:, 1::2] << 4)).contiguous()
+    return packed, sb.view(torch.uint8), s
+
+
 # ------------------------------------------------------------- independent bit laws
 
 
