@@ -17,7 +17,8 @@ from collections.abc import Mapping, Sequence
 from dataclasses import dataclass
 from typing import Any, ClassVar
 
-from cozyq import fp8_linear, int8_linear, layout, prebuilt, w4a8_linear
+from cozyq import decode as dec
+from cozyq import fp8_linear, int8_linear, layout, nvfp4_linear, prebuilt, w4a8_linear
 from cozyq.operands import INT8_CONVROT, ROWWISE_FP8, PreQuantized, read, shared_operand
 
 Tensor = Any
@@ -27,6 +28,7 @@ Params = tuple[tuple[str, object], ...]
 MXFP8 = "cozy.mxfp8.native-leaf/2"
 W4A8 = "cozy.w4a8-convrot256.native-leaf/1"
 SVDQ_INT4 = "cozyq.svdq-int4g64.native-leaf/1"
+NVFP4 = "cozy.nvfp4.native-leaf/1"
 #: The operand geometry each 8-bit leaf's GEMM reads (`internal/encoding/leaves.py:207`).
 OPERANDS = {INT8_CONVROT: INT8_CONVROT, ROWWISE_FP8: ROWWISE_FP8, W4A8: INT8_CONVROT}
 #: The 8-bit leaves' ops by provider (`internal/encoding/leaves.py:355`).
@@ -36,7 +38,7 @@ _NATIVE_OPS: dict[str, Any] = {INT8_CONVROT: int8_linear, ROWWISE_FP8: fp8_linea
 _FEW_ROWS = {INT8_CONVROT: int8_linear.GEMV_ROWS, ROWWISE_FP8: 4}
 #: The card rows (the reference keys them by CUDA capability, `arch.py:51-64`): the
 #: tensor-core formats each multiplies in.
-ARCH_ROWS = {"gfx950": frozenset({"int8", "fp8", "mxfp8", "int4"})}
+ARCH_ROWS = {"gfx950": frozenset({"int8", "fp8", "mxfp8", "int4", "bf16"})}
 DEVICE_PREDICATE = "rocm.gfx950"
 INT8_ROTATION = 256
 MX_BLOCK = 32
@@ -488,12 +490,92 @@ class SvdqInt4NativeLeaf(_Provider):
                                        self.name, self.encoding, in_features, out_features)  # fmt: skip
 
 
+def _nvfp4_leaf_class(torch: Any) -> Any:
+    """`EncodedLinear` keyed by nvfp4's stored roles (`internal/encoding/leaves.py:1056-1065`)."""
+    cached = getattr(_nvfp4_leaf_class, "_cached", None)
+    if cached is not None:
+        return cached
+
+    class Nvfp4Linear(_leaf_class(torch)):  # type: ignore[misc]
+        BUFFERS: ClassVar[dict[str, str]] = {"scale": "weight_scale", "scale_2": "weight_scale_2"}
+
+    _nvfp4_leaf_class._cached = Nvfp4Linear
+    return Nvfp4Linear
+
+
+def _nvfp4_forward(torch: Any, leaf: Any, x: Tensor, out_dtype: Dtype) -> Tensor:
+    """`Nvfp4NativeLeaf._forward` (`internal/encoding/leaves.py:1158-1170`)."""
+    return nvfp4_linear.matmul(torch, x, leaf.weight, leaf.weight_scale, None, leaf.weight_scale_2,
+                               out_dtype)  # fmt: skip
+
+
+@dataclass(frozen=True, slots=True)
+class Nvfp4NativeLeaf(_Provider):
+    """`nvfp4` encoded GEMM (`internal/encoding/leaves.py:1069-1203`): the E2M1 payload and E4M3
+    block scales stay resident (0.56 bytes a weight). Up to 16 rows take the W4A16 GEMV on the
+    bf16/fp16 MFMA; more rows decode the weight per 128-row chunk and take the library GEMM. The
+    scales are held in cuBLAS's 128x4 tiles and the nibbles low first, as the reference's leaf
+    holds them; a `divide` second level is held as its float32 reciprocal, as there."""
+
+    encoding: str = "nvfp4"
+    params: Params = ()
+
+    name = property(lambda self: NVFP4)
+    schemes = property(lambda self: frozenset({"nvfp4"}))
+    code_revision = property(lambda self: "1")
+    suite = property(lambda self: "nvfp4-native")
+    # The reference's leaf names none (W4A16 runs on every MMA card); here the kernels multiply on
+    # gfx950's bf16/fp16 MFMA.
+    formats = property(lambda self: frozenset({"bf16"}))
+    out_dtypes = property(lambda self: frozenset({"bfloat16", "float16", "float32"}))
+    required = property(lambda self: frozenset({"weight", "scale", "scale_2"}))
+    optional = property(lambda self: frozenset({"input_scale"}))
+
+    def supports(self, shape: Sequence[int], params: Mapping[str, object]) -> str:
+        """The decode's block law, and K % 32, N % 8 (`internal/encoding/leaves.py:1127-1134`)."""
+        why = _rank2(shape) or dec.Nvfp4Dequant().supports(shape, params)
+        if why:
+            return why
+        if int(shape[1]) % 32 or int(shape[0]) % 8:
+            return f"the FP4 GEMM needs K % 32 == 0 and N % 8 == 0; this tensor is {list(shape)}"
+        return ""
+
+    def resident_bytes(self, parts: Mapping[str, Any]) -> int:
+        rows, cols = dec.blocked_shape(int(parts["scale"].shape[0]), int(parts["scale"].shape[1]))
+        return int(parts["weight"].nbytes) + rows * cols + 4
+
+    def fill_scratch_bytes(self, parts: Mapping[str, Any]) -> int:
+        rows, cols = dec.blocked_shape(int(parts["scale"].shape[0]), int(parts["scale"].shape[1]))
+        return 3 * rows * cols
+
+    def leaf(self, torch: Any, parts: Mapping[str, Tensor], replaced: object, out_dtype: Dtype) -> Any:
+        params = dict(self.params)
+        weight = parts["weight"].view(torch.uint8)
+        if params.get("nibble_order") == "high_first":
+            weight = (weight << 4) | (weight >> 4)  # the kernels read element 2k low
+        out_features, in_features = int(weight.shape[0]), 2 * int(weight.shape[1])
+        rows, cols = dec.blocked_shape(out_features, in_features // 16)
+        if params.get("scale_layout") == "cublas_128x4":
+            blocked = parts["scale"].view(torch.uint8).reshape(rows, cols)
+        else:
+            blocked = layout.to_blocked(torch, parts["scale"].view(torch.uint8).reshape(
+                out_features, in_features // 16)).view(rows, cols)  # fmt: skip
+        second = parts["scale_2"].to(torch.float32).reshape(1)
+        if params.get("global_scale") == "divide":
+            second = 1.0 / second
+        return _nvfp4_leaf_class(torch)(
+            functools.partial(_nvfp4_forward, torch),
+            {"weight": weight, "scale": blocked.view(torch.float8_e4m3fn), "scale_2": second},
+            getattr(replaced, "bias", None), out_dtype, self.name, self.encoding, in_features,
+            out_features)  # fmt: skip
+
+
 def launch_providers() -> dict[str, tuple[Any, ...]]:
     """Scheme -> its encoded-GEMM providers on gfx950, in the reference's preference order
     (`internal/encoding/selection.py:248-274`, the encoded_gemm entries)."""
     out: dict[str, list[Any]] = {}
     for build in (RowwiseNativeLeaf, Int8ConvRotNativeLeaf, W4a8NativeLeaf, SvdqInt4NativeLeaf,
-                  MicroScaledNativeLeaf):
+                  MicroScaledNativeLeaf, Nvfp4NativeLeaf):
         for scheme in sorted(build().schemes):
             out.setdefault(scheme, []).append(build(scheme))
     return {scheme: tuple(candidates) for scheme, candidates in out.items()}

@@ -420,6 +420,30 @@ class Prebuilt:
         out = self.svdq_gemm(act, ascales, la, w, wscales, up, bias, out_dtype)
         return out.view(*x.shape[:-1], w.shape[0])
 
+    # ------------------------------------------------------------------- nvfp4 W4A16
+
+    def nvfp4_gemv(self, x: Tensor, weight: Tensor, blocked_scale: Tensor, scale_2: Tensor,
+                   out_dtype: Dtype) -> Tensor:
+        """`cozyq_nvfp4_gemv` (the `_gemv` path of `internal/nvfp4_linear.py:126-201`): up to 16
+        bf16/fp16 rows against packed E2M1 codes [N, K/2] (low nibble first), E4M3 scales in
+        cuBLAS's 128x4 tiles and a float32 second level; out [M, N] in `out_dtype` (bf16/fp16)."""
+        torch = self.torch
+        flat = x.reshape(-1, x.shape[-1])
+        rows, cols = int(flat.shape[0]), int(flat.shape[1])
+        n = int(weight.shape[0])
+        if rows > 16 or cols % 32 or 2 * int(weight.shape[1]) != cols:
+            raise ValueError(f"nvfp4 GEMV: up to 16 rows and K % 32 == 0 matching the weight's "
+                             f"{2 * int(weight.shape[1])} columns; got [{rows}, {cols}]")  # fmt: skip
+        flat = flat if flat.is_contiguous() and flat.data_ptr() % 16 == 0 else flat.contiguous().clone()
+        out = torch.empty(rows, n, dtype=out_dtype, device=x.device)
+        code = self._lib.cozyq_nvfp4_gemv(
+            self.index, flat.data_ptr(), self._half(flat.dtype), weight.data_ptr(),
+            blocked_scale.data_ptr(), scale_2.data_ptr(), out.data_ptr(), self._half(out_dtype),
+            rows, n, cols, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the nvfp4 GEMV")
+        return out
+
     # -------------------------------------------------------------- stored-format decode
 
     def decode_table(

@@ -329,6 +329,22 @@ int cozyq_decode_svdq(int device, const uint8_t* w, const uint8_t* scale, int ti
     return decode_svdq(a, out_type, on(stream));
 }
 
+int cozyq_nvfp4_gemv(int device, const void* x, int x_half, const uint8_t* w, const uint8_t* scale,
+                     const float* scale_2, void* out, int out_half, int M, int N, int K, void* stream) {
+    if (M < 0 || M > 16 || N < 1 || K < 32 || K % 32 || K > cozyq::kMaxK || !x || !w || !scale ||
+        !scale_2 || !out)
+        return hipErrorInvalidValue;
+    if (static_cast<int64_t>(N) * (K / 2) >= 0x7fffffff ||
+        static_cast<int64_t>((N + 127) / 128 * 128) * ((K / 16 + 3) / 4 * 4) >= 0x7fffffff)
+        return hipErrorNotSupported;
+    if (M == 0) return hipSuccess;
+    if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & 3) || (reinterpret_cast<uintptr_t>(out) & 1))
+        return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::nvfp4_gemv(x, x_half != 0, w, scale, scale_2, out, out_half != 0, M, N, K, on(stream));
+}
+
 int cozyq_encode_int8_convrot(int device, const void* w, int w_type, int8_t* q, float* scale,
                                int64_t rows, int K, void* stream) {
     if (w_type < 0 || w_type > 2 || rows < 0 || rows > 0x7fffffff || !fits(K, 256)) return hipErrorInvalidValue;

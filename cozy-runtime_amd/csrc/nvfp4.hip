@@ -1,0 +1,145 @@
+// The nvfp4 W4A16 GEMV on gfx950 (reference: the `_gemv` path of internal/nvfp4_linear.py:
+// 126-201, served at most DECODE_ROWS = 16 rows, :338-377): out[m, n] = round((Σ_k x[m, k] ·
+// bf16(e2m1[n, k] · s[n, k/16])) · g), float32 accumulation. The stored weight stays packed
+// (0.56 bytes a weight): codes [N, K/2] (element 2k in the low nibble), E4M3 block scales in
+// cuBLAS's 128x4 tiles (the leaf's resident layout), g the float32 second level.
+//
+// A workgroup of 8 waves takes 16 output rows; wave w takes the 32-wide K steps w, w + 8, ....
+// Per step a lane decodes 8 weights of its row (one code dword, one scale byte): E2M1 by
+// v_cvt_scalef32_pk_f32_fp4, times the E4M3 scale — exact in float32 and again in bf16 or fp16 —
+// and one v_mfma_f32_16x16x32 multiplies them against the activation rows (zero past M).
+// The eight waves' partial sums meet in LDS and are added in wave order, so a row's result does
+// not depend on M or on the rows beside it. Every global read is a bounded buffer load: rows past
+// N or M read zeros.
+#include "common.h"
+#include "kernels.h"
+
+namespace cozyq {
+namespace {
+
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2n __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2n __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2n __attribute__((ext_vector_type(2)));
+
+constexpr int kGemvWaves = 8;
+constexpr int kStepsAhead = 4;  // K steps a wave keeps in flight
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded_rsrc(const void* p, int64_t bytes) {
+    const int64_t cap = bytes < 0x7fffffff ? bytes : 0x7fffffff;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(cap), 0x00020000);
+}
+
+// The eight weights of one code dword times the block scale, as the MFMA's packed operand. The
+// conversion runs at scale 1 and the E4M3 scale multiplies after (exact in float32): the
+// instruction's own scale operand is an MX exponent and keeps only a power of two.
+template <bool kHalf>
+__device__ __forceinline__ i32x4 weights8(uint32_t word, float s) {
+    const int w = static_cast<int>(word);
+    const f32x2n p0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0) * s;
+    const f32x2n p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1) * s;
+    const f32x2n p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2) * s;
+    const f32x2n p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3) * s;
+    if constexpr (kHalf) {
+        return i32x4{__builtin_bit_cast(int, __builtin_convertvector(p0, f16x2n)),
+                     __builtin_bit_cast(int, __builtin_convertvector(p1, f16x2n)),
+                     __builtin_bit_cast(int, __builtin_convertvector(p2, f16x2n)),
+                     __builtin_bit_cast(int, __builtin_convertvector(p3, f16x2n))};
+    } else {
+        return i32x4{__builtin_bit_cast(int, __builtin_convertvector(p0, bf16x2n)),
+                     __builtin_bit_cast(int, __builtin_convertvector(p1, bf16x2n)),
+                     __builtin_bit_cast(int, __builtin_convertvector(p2, bf16x2n)),
+                     __builtin_bit_cast(int, __builtin_convertvector(p3, bf16x2n))};
+    }
+}
+
+template <bool kHalf>
+__device__ __forceinline__ f32x4 mfma16(i32x4 a, i32x4 b, f32x4 c) {
+    if constexpr (kHalf)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c, 0, 0, 0);
+}
+
+// kXHalf: activations (and the weights fed beside them) fp16, else bf16; kOutHalf likewise.
+template <bool kXHalf, bool kOutHalf>
+__global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint16_t* __restrict__ x,
+                                                                     const uint8_t* __restrict__ w,
+                                                                     const uint8_t* __restrict__ scale,
+                                                                     const float* __restrict__ scale_2,
+                                                                     uint16_t* __restrict__ out, int M, int N, int K) {
+    __shared__ f32x4 partial[kGemvWaves][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * 16;
+    const int row = n0 + (lane & 15);  // the weight row this lane decodes
+    const int sub = lane >> 4;          // its 8-element slice of a 32-wide step
+    const int width = K / 16, col_tiles = (width + 3) / 4;
+    const __amdgpu_buffer_rsrc_t wr = bounded_rsrc(w, static_cast<int64_t>(N) * (K / 2));
+    const __amdgpu_buffer_rsrc_t sr = bounded_rsrc(scale, static_cast<int64_t>((N + 127) / 128 * 128) * col_tiles * 4);
+    const __amdgpu_buffer_rsrc_t xr = bounded_rsrc(x, static_cast<int64_t>(M) * K * 2);
+    // Rows past N read past the codes' end (zeros); rows past M read past x's end (zeros).
+    const int code_row = row < N ? row : N;
+    const int x_row = (lane & 15) < M ? (lane & 15) : M;
+    const int64_t code_base = static_cast<int64_t>(code_row) * (K / 2);
+    const int tile_row = (row >> 7) * col_tiles, in_tile = (row & 31) * 16 + ((row & 127) >> 5) * 4;
+
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int steps = K / 32;
+    for (int s0 = wave; s0 < steps; s0 += kGemvWaves * kStepsAhead) {
+        uint32_t code[kStepsAhead];
+        uint32_t sbyte[kStepsAhead];
+        i32x4 xv[kStepsAhead];
+#pragma unroll
+        for (int j = 0; j < kStepsAhead; ++j) {
+            const int step = s0 + j * kGemvWaves;
+            const bool live = step < steps;  // steps past K read zeros from every buffer
+            const int k = 32 * step + 8 * sub;
+            const int b = k / 16;
+            code[j] = __builtin_amdgcn_raw_buffer_load_b32(wr, live ? static_cast<int>(code_base + k / 2) : 0x7fffffff, 0, 0);
+            const int sidx = row < N && live ? ((tile_row + (b >> 2)) * 512 + in_tile + (b & 3)) : 0x7fffffff;
+            sbyte[j] = __builtin_amdgcn_raw_buffer_load_b8(sr, sidx, 0, 0);
+            xv[j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                xr, live ? static_cast<int>((static_cast<int64_t>(x_row) * K + k) * 2) : 0x7fffffff, 0, 0));
+        }
+#pragma unroll
+        for (int j = 0; j < kStepsAhead; ++j) acc = mfma16<kXHalf>(weights8<kXHalf>(code[j], e4m3_value(sbyte[j])), xv[j], acc);
+    }
+    partial[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    f32x4 sum = partial[0][lane];
+#pragma unroll
+    for (int v = 1; v < kGemvWaves; ++v) {
+        const f32x4 p = partial[v][lane];
+        sum = f32x4{sum[0] + p[0], sum[1] + p[1], sum[2] + p[2], sum[3] + p[3]};
+    }
+    // D[n][m]: lane holds rows n0 + 4·(lane/16) + r of column m = lane % 16.
+    const float g = scale_2[0];
+    const int m = lane & 15;
+    if (m >= M) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int n = n0 + 4 * (lane >> 4) + r;
+        if (n < N) out[static_cast<int64_t>(m) * N + n] = narrow<kOutHalf>(sum[r] * g);
+    }
+}
+
+}  // namespace
+
+hipError_t nvfp4_gemv(const void* x, bool x_half, const uint8_t* w, const uint8_t* scale, const float* scale_2,
+                      void* out, bool out_half, int M, int N, int K, hipStream_t s) {
+    const dim3 grid((N + 15) / 16), block(64 * kGemvWaves);
+    const auto* xp = static_cast<const uint16_t*>(x);
+    auto* op = static_cast<uint16_t*>(out);
+    if (x_half) {
+        if (out_half) hipLaunchKernelGGL((nvfp4_gemv_kernel<true, true>), grid, block, 0, s, xp, w, scale, scale_2, op, M, N, K);
+        else hipLaunchKernelGGL((nvfp4_gemv_kernel<true, false>), grid, block, 0, s, xp, w, scale, scale_2, op, M, N, K);
+    } else {
+        if (out_half) hipLaunchKernelGGL((nvfp4_gemv_kernel<false, true>), grid, block, 0, s, xp, w, scale, scale_2, op, M, N, K);
+        else hipLaunchKernelGGL((nvfp4_gemv_kernel<false, false>), grid, block, 0, s, xp, w, scale, scale_2, op, M, N, K);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace cozyq

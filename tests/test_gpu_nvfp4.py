@@ -1,0 +1,114 @@
+"""The nvfp4 encoded linear on the GPU (`cozyq.nvfp4_linear`, `csrc/nvfp4.hip`).
+
+The W4A16 GEMV (up to 16 rows) and the decode + library GEMM path are held to the float64
+product of the activations and the exact decoded weight (the oracle's `decode_nvfp4`, pinned by
+the reference's nvfp4 vectors), within rtol 2e-2 / atol 1e-2·rms like every floating output
+here. The GEMV's rows are bit-identical whatever M is, and repeat bit for bit.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import laws
+
+pytestmark = pytest.mark.gpu
+
+CUDA = "cuda:0"
+RTOL, ATOL = 2e-2, 1e-2
+
+
+def _weight(n: int, k: int, seed: int):
+    g = torch.Generator().manual_seed(seed)
+    codes = torch.randint(0, 256, (n, k // 2), generator=g, dtype=torch.int32).to(torch.uint8)
+    grid = (torch.rand(n, k // 16, generator=g) * 4 + 0.25).to(torch.float8_e4m3fn)
+    second = torch.tensor([0.02])
+    exact = laws.decode_nvfp4(codes, grid, second, "row_major", False, False, None, torch.float32)
+    blocked = laws.to_blocked(grid.view(torch.uint8)).view(*laws._blocked_shape(n, k // 16))
+    return codes, grid, blocked, second, exact
+
+
+def _close(got: torch.Tensor, want: torch.Tensor) -> None:
+    got = got.double().cpu()
+    rms = float(want.pow(2).mean().sqrt())
+    bad = ((got - want).abs() > ATOL * rms + RTOL * want.abs()).sum()
+    assert int(bad) == 0, f"{int(bad)} of {want.numel()} outside tolerance"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (3, 200, 1024), (16, 264, 96), (16, 4096, 3072)])
+def test_nvfp4_gemv_against_the_exact_product(dtype, m, n, k):
+    from cozyq import prebuilt
+
+    codes, _, blocked, second, exact = _weight(n, k, m + n)
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(k)) * 0.5).to(dtype)
+    ops = prebuilt.library(0)
+    got = ops.nvfp4_gemv(x.to(CUDA), codes.to(CUDA), blocked.to(CUDA), second.to(CUDA), dtype)
+    torch.cuda.synchronize()
+    assert got.shape == (m, n) and got.dtype == dtype
+    _close(got, x.double() @ exact.double().t())
+
+
+def test_nvfp4_gemv_rows_do_not_depend_on_m():
+    from cozyq import prebuilt
+
+    codes, _, blocked, second, _ = _weight(4096, 2048, 9)
+    x = torch.randn(16, 2048, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    ops = prebuilt.library(0)
+    w, s, g = codes.to(CUDA), blocked.to(CUDA), second.to(CUDA)
+    full = ops.nvfp4_gemv(x.to(CUDA), w, s, g, torch.bfloat16).cpu()
+    again = ops.nvfp4_gemv(x.to(CUDA), w, s, g, torch.bfloat16).cpu()
+    assert torch.equal(full.view(torch.int16), again.view(torch.int16))
+    for m in (1, 5):
+        part = ops.nvfp4_gemv(x[:m].to(CUDA), w, s, g, torch.bfloat16).cpu()
+        assert torch.equal(part.view(torch.int16), full[:m].view(torch.int16))
+
+
+@pytest.mark.parametrize("rows", [17, 64])
+def test_nvfp4_matmul_more_rows_decodes_per_chunk(rows, monkeypatch):
+    """Past 16 rows: the weight decoded per 128-row chunk (here forced small, so the last chunk
+    is partial) and the library GEMM."""
+    from cozyq import nvfp4_linear
+
+    n, k = 300, 1024
+    codes, grid, blocked, second, exact = _weight(n, k, 3)
+    monkeypatch.setattr(nvfp4_linear, "_DECODE_CHUNK", 2 * k * 128)
+    x = torch.randn(2, rows, k, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    got = nvfp4_linear.matmul(torch, x.to(CUDA), codes.to(CUDA), blocked.to(CUDA), None,
+                              second.to(CUDA), torch.float32)  # fmt: skip
+    torch.cuda.synchronize()
+    assert got.shape == (2, rows, n) and got.dtype == torch.float32
+    want = x.double().reshape(-1, k) @ exact.double().t()
+    _close(got.reshape(-1, n), want)
+
+
+@pytest.mark.parametrize("layout,order,mode", [("row_major", "low_first", "multiply"),
+                                               ("cublas_128x4", "high_first", "divide")])
+@pytest.mark.parametrize("rows", [1, 40])
+def test_nvfp4_leaf_forward(layout, order, mode, rows):
+    """The provider's leaf from stored parts of either convention, with a bias."""
+    from cozyq import leaves
+
+    n, k = 256, 512
+    g = torch.Generator().manual_seed(5)
+    codes = torch.randint(0, 256, (n, k // 2), generator=g, dtype=torch.int32).to(torch.uint8)
+    grid = (torch.rand(n, k // 16, generator=g) * 4 + 0.25).to(torch.float8_e4m3fn)
+    second = torch.tensor(0.05 if mode == "multiply" else 20.0)
+    exact = laws.decode_nvfp4(codes, grid, second, "row_major", order == "high_first",
+                              mode == "divide", None, torch.float32)  # fmt: skip
+    scale = grid if layout == "row_major" else laws.to_blocked(grid.view(torch.uint8)).view(
+        *laws._blocked_shape(n, k // 16)).view(torch.float8_e4m3fn)  # fmt: skip
+    params = (("block_size", 16), ("global_scale", mode), ("nibble_order", order),
+              ("scale_layout", layout))  # fmt: skip
+    lin = torch.nn.Linear(k, n, bias=True)
+    lin.bias.data = (torch.randn(n, generator=g) * 0.1)
+    lin = lin.to(CUDA).to(torch.bfloat16)
+    leaf = leaves.Nvfp4NativeLeaf("nvfp4", params).leaf(
+        torch, {"weight": codes.to(CUDA), "scale": scale.to(CUDA), "scale_2": second.to(CUDA)},
+        lin, torch.bfloat16)  # fmt: skip
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    got = leaf(x.to(CUDA))
+    torch.cuda.synchronize()
+    want = x.double() @ exact.double().t() + lin.bias.detach().double().cpu()
+    _close(got, want)

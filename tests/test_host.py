@@ -21,10 +21,11 @@ class _Linear(torch.nn.Module):
 
 def test_providers_surface_and_launch_table():
     table = leaves.launch_providers()
-    assert set(table) == {"fp8.rowwise", "int8.convrot", "w4a8.convrot", "svdq.int4g64", "mxfp8"}
+    assert set(table) == {"fp8.rowwise", "int8.convrot", "w4a8.convrot", "svdq.int4g64", "mxfp8",
+                          "nvfp4"}  # fmt: skip
     names = {p.name for ps in table.values() for p in ps}
     assert names == {operands.ROWWISE_FP8, operands.INT8_CONVROT, leaves.W4A8, leaves.MXFP8,
-                     leaves.SVDQ_INT4}  # fmt: skip
+                     leaves.SVDQ_INT4, leaves.NVFP4}  # fmt: skip
     assert leaves.OPERANDS[leaves.W4A8] == operands.INT8_CONVROT
     for scheme, (provider,) in table.items():
         assert provider.encoding == scheme
@@ -35,6 +36,40 @@ def test_providers_surface_and_launch_table():
         assert leaves.serves(provider, "gfx950") and not leaves.serves(provider, "gfx942")
         with pytest.raises(AssertionError):
             provider.decode(torch, {}, torch.empty(0))
+
+
+def test_nvfp4_leaf_surface_and_supports():
+    """`internal/encoding/leaves.py:1069-1134`: roles, out dtypes, the decode's block law, K % 32
+    and N % 8."""
+    nv = leaves.Nvfp4NativeLeaf()
+    ok = {"block_size": 16, "global_scale": "multiply", "nibble_order": "low_first",
+          "scale_layout": "row_major"}  # fmt: skip
+    assert nv.name == "cozy.nvfp4.native-leaf/1" and nv.suite == "nvfp4-native"
+    assert nv.required == {"weight", "scale", "scale_2"} and nv.optional == {"input_scale"}
+    assert nv.supports((64, 256), ok) == ""
+    assert "K % 32" in nv.supports((64, 48), ok)
+    assert "N % 8" in nv.supports((60, 256), ok)
+    assert "expected one of" in nv.supports((64, 256), {**ok, "global_scale": "add"})
+    assert "rank-2" in nv.supports((2, 64, 256), ok)
+
+
+def test_nvfp4_leaf_holds_the_kernels_layout():
+    """Fill: a high-first weight is held low first, row-major scales in 128x4 tiles, a divide
+    second level as its reciprocal (`internal/encoding/leaves.py:1172-1203`)."""
+    torch.manual_seed(0)
+    codes = torch.randint(0, 256, (8, 32), dtype=torch.uint8)
+    grid = torch.randint(1, 120, (8, 4), dtype=torch.uint8)
+    nv = leaves.Nvfp4NativeLeaf("nvfp4", (("block_size", 16), ("global_scale", "divide"),
+                                          ("nibble_order", "high_first"),
+                                          ("scale_layout", "row_major")))  # fmt: skip
+    leaf = nv.leaf(torch, {"weight": codes, "scale": grid.view(torch.float8_e4m3fn),
+                           "scale_2": torch.tensor(4.0)}, _Linear(8, 64, False), torch.bfloat16)  # fmt: skip
+    assert torch.equal(leaf.weight, (codes << 4) | (codes >> 4))
+    assert torch.equal(leaf.weight_scale.view(torch.uint8).reshape(-1), laws.to_blocked(grid))
+    assert float(leaf.weight_scale_2) == 0.25
+    assert (leaf.in_features, leaf.out_features) == (64, 8)
+    with pytest.raises(ValueError, match="on the GPU"):
+        leaf(torch.zeros(2, 64, dtype=torch.bfloat16))
 
 
 def test_w4a8_supports_messages():
