@@ -462,6 +462,36 @@ def bench_weights(torch, ops, lib, stream, steps: int) -> dict:
     return {"decode_formats": out}
 
 
+def bench_nvfp4(torch, ops, lib, stream, steps: int) -> dict:
+    """The nvfp4 W4A16 GEMV (`cozyq_nvfp4_gemv`) on config 3's weight shape (K=4096, N=14336:
+    29.4 MB of E2M1 codes + 3.7 MB of tiled E4M3 scales, 0.56 bytes a weight) at M = 1 and 16,
+    over 8 rotating weight copies (265 MB, beyond the MALL), graph-replayed; bf16 in and out."""
+    k, n, copies = 4096, 14336, 8
+    gen = torch.Generator(device="cuda").manual_seed(97)
+    tiled = (-(-n // 128) * 128) * (-(-(k // 16) // 4) * 4)
+    weights = [(torch.randint(0, 256, (n, k // 2), generator=gen, device="cuda", dtype=torch.int32).to(torch.uint8),
+                (torch.randint(0x30, 0x48, (tiled,), generator=gen, device="cuda", dtype=torch.int32)).to(torch.uint8))
+               for _ in range(copies)]
+    second = torch.tensor([0.02], device="cuda")
+    out = []
+    for m in (1, 16):
+        x = _activations(torch, m, k, 98)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        turn = [0]
+
+        def go(raw):
+            w, s = weights[turn[0] % copies]
+            turn[0] += 1
+            _check(lib.cozyq_nvfp4_gemv(0, x.data_ptr(), 0, w.data_ptr(), s.data_ptr(), second.data_ptr(),
+                                        y.data_ptr(), 0, m, n, k, raw))  # fmt: skip
+
+        us = _graph_us(torch, go, 8 * copies, max(4, steps // 8))
+        nbytes = n * k // 2 + tiled + m * k * 2 + m * n * 2
+        out.append({"M": m, "K": k, "N": n, "us": us, "gbs": nbytes / (us * 1e-6) / 1e9,
+                    "frac_hbm": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, "bytes": nbytes})
+    return {"nvfp4_w4a16_gemv": out}
+
+
 def cpu_baseline(torch, rows: int = 1024) -> dict:
     """The reference's CPU law for config 2 on rows 0..rows-1 of the batch: rotation + per-token
     int8 (`quantize_rows`), the literal int32 matmul, both scales, bias and GELU."""
@@ -512,6 +542,8 @@ def only(torch, ops, lib, stream, args) -> int:
         figures = bench_w4a8(torch, ops, lib, stream, args.steps)
     elif args.only == "weights":
         figures = bench_weights(torch, ops, lib, stream, args.steps)
+    elif args.only == "nvfp4":
+        figures = bench_nvfp4(torch, ops, lib, stream, args.steps)
     else:
         figures = bench_svdq(torch, ops, lib, stream, args.steps)
     print(json.dumps({"only": args.only, **figures}))
@@ -529,7 +561,7 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
     parser.add_argument("--only", choices=("c2", "decode", "int8_decode", "w4a8", "fp8", "svdq", "mx", "weights",
-                                                    "copy"),
+                                                    "nvfp4", "copy"),
                         help="profiling aid: run one leg (or a plain 256 MiB device copy, the "
                              "counter calibration) --steps times and print its figures only")  # fmt: skip
     args = parser.parse_args()
@@ -562,6 +594,7 @@ def main() -> int:
         configs["c4_svdq_w4a4"] = bench_svdq(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["c5_mxfp8"] = bench_mx(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["weight_decode"] = bench_weights(torch, ops, lib, stream, args.steps)["decode_formats"]
+        configs["nvfp4_w4a16"] = bench_nvfp4(torch, ops, lib, stream, args.steps)["nvfp4_w4a16_gemv"]
         print("[bench] extra configs done", file=sys.stderr, flush=True)
     baseline = None if args.no_cpu else cpu_baseline(torch)
     line = {

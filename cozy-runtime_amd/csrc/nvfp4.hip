@@ -4,8 +4,8 @@
 // (0.56 bytes a weight): codes [N, K/2] (element 2k in the low nibble), E4M3 block scales in
 // cuBLAS's 128x4 tiles (the leaf's resident layout), g the float32 second level.
 //
-// A workgroup of 8 waves takes 16 output rows; wave w takes the 32-wide K steps w, w + 8, ....
-// Per step a lane decodes 8 weights of its row (one code dword, one scale byte): E2M1 by
+// A workgroup of 8 waves takes 16 output rows; wave w takes the 128-column macro steps w, w + 8,
+// .... Per 32 columns a lane decodes 8 weights of its row: E2M1 by
 // v_cvt_scalef32_pk_f32_fp4, times the E4M3 scale — exact in float32 and again in bf16 or fp16 —
 // and one v_mfma_f32_16x16x32 multiplies them against the activation rows (zero past M).
 // The eight waves' partial sums meet in LDS and are added in wave order, so a row's result does
@@ -24,7 +24,7 @@ typedef __bf16 bf16x2n __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2n __attribute__((ext_vector_type(2)));
 
 constexpr int kGemvWaves = 8;
-constexpr int kStepsAhead = 4;  // K steps a wave keeps in flight
+constexpr int kStepsAhead = 2;  // macro steps a wave keeps in flight
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded_rsrc(const void* p, int64_t bytes) {
     const int64_t cap = bytes < 0x7fffffff ? bytes : 0x7fffffff;
@@ -63,6 +63,11 @@ __device__ __forceinline__ f32x4 mfma16(i32x4 a, i32x4 b, f32x4 c) {
 }
 
 // kXHalf: activations (and the weights fed beside them) fp16, else bf16; kOutHalf likewise.
+// A macro step is 128 columns: a lane loads 16 bytes of its row's codes (32 weights, columns
+// 128t + 32·sub ..), the two E4M3 scales that cover them (adjacent bytes of a 128x4 tile, as
+// the first block is even) and its activation row's 32 matching columns, and feeds 4 MFMAs,
+// MFMA j taking columns 128t + 32·sub + 8j .. + 8 on both sides: every lane group pairs the
+// same columns of A and B, so the four products add up to the 128-column dot product.
 template <bool kXHalf, bool kOutHalf>
 __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint16_t* __restrict__ x,
                                                                      const uint8_t* __restrict__ w,
@@ -73,7 +78,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n0 = blockIdx.x * 16;
     const int row = n0 + (lane & 15);  // the weight row this lane decodes
-    const int sub = lane >> 4;          // its 8-element slice of a 32-wide step
+    const int sub = lane >> 4;          // its 32-column quarter of a macro step
     const int width = K / 16, col_tiles = (width + 3) / 4;
     const __amdgpu_buffer_rsrc_t wr = bounded_rsrc(w, static_cast<int64_t>(N) * (K / 2));
     const __amdgpu_buffer_rsrc_t sr = bounded_rsrc(scale, static_cast<int64_t>((N + 127) / 128 * 128) * col_tiles * 4);
@@ -85,25 +90,45 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
     const int tile_row = (row >> 7) * col_tiles, in_tile = (row & 31) * 16 + ((row & 127) >> 5) * 4;
 
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int steps = K / 32;
-    for (int s0 = wave; s0 < steps; s0 += kGemvWaves * kStepsAhead) {
-        uint32_t code[kStepsAhead];
+    const int macro = K / 128;  // whole macro steps; a 32..96-column tail is handled below
+    for (int t0 = wave; t0 < macro; t0 += kGemvWaves * kStepsAhead) {
+        i32x4 code[kStepsAhead], xv[kStepsAhead][4];
         uint32_t sbyte[kStepsAhead];
-        i32x4 xv[kStepsAhead];
 #pragma unroll
         for (int j = 0; j < kStepsAhead; ++j) {
-            const int step = s0 + j * kGemvWaves;
-            const bool live = step < steps;  // steps past K read zeros from every buffer
-            const int k = 32 * step + 8 * sub;
-            const int b = k / 16;
-            code[j] = __builtin_amdgcn_raw_buffer_load_b32(wr, live ? static_cast<int>(code_base + k / 2) : 0x7fffffff, 0, 0);
-            const int sidx = row < N && live ? ((tile_row + (b >> 2)) * 512 + in_tile + (b & 3)) : 0x7fffffff;
-            sbyte[j] = __builtin_amdgcn_raw_buffer_load_b8(sr, sidx, 0, 0);
-            xv[j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                xr, live ? static_cast<int>((static_cast<int64_t>(x_row) * K + k) * 2) : 0x7fffffff, 0, 0));
+            const int t = t0 + j * kGemvWaves;
+            const bool live = t < macro;
+            const int k = 128 * t + 32 * sub;
+            const int b = k / 16;  // even
+            code[j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                wr, live ? static_cast<int>(code_base + k / 2) : 0x7ffffff0, 0, 0));
+            const int sidx = row < N && live ? ((tile_row + (b >> 2)) * 512 + in_tile + (b & 3)) : 0x7ffffff0;
+            sbyte[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, sidx, 0, 0);
+            const int xo = live ? static_cast<int>((static_cast<int64_t>(x_row) * K + k) * 2) : 0x7fffff00;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                xv[j][q] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                    xr, xo + 16 * q, 0, 0));
         }
 #pragma unroll
-        for (int j = 0; j < kStepsAhead; ++j) acc = mfma16<kXHalf>(weights8<kXHalf>(code[j], e4m3_value(sbyte[j])), xv[j], acc);
+        for (int j = 0; j < kStepsAhead; ++j) {
+            const float s0 = e4m3_value(sbyte[j] & 0xffu), s1 = e4m3_value((sbyte[j] >> 8) & 0xffu);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                acc = mfma16<kXHalf>(weights8<kXHalf>(static_cast<uint32_t>(code[j][q]), q < 2 ? s0 : s1), xv[j][q], acc);
+        }
+    }
+    // A tail of 1..3 32-column steps past the last whole macro step, one per wave.
+    const int tail = (K % 128) / 32;
+    if (wave < tail) {
+        const int k = 128 * macro + 32 * wave + 8 * sub;
+        const int b = k / 16;
+        const uint32_t c = __builtin_amdgcn_raw_buffer_load_b32(wr, static_cast<int>(code_base + k / 2), 0, 0);
+        const int sidx = row < N ? ((tile_row + (b >> 2)) * 512 + in_tile + (b & 3)) : 0x7fffffff;
+        const uint32_t sb = __builtin_amdgcn_raw_buffer_load_b8(sr, sidx, 0, 0);
+        const i32x4 xt = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+            xr, static_cast<int>((static_cast<int64_t>(x_row) * K + k) * 2), 0, 0));
+        acc = mfma16<kXHalf>(weights8<kXHalf>(c, e4m3_value(sb)), xt, acc);
     }
     partial[wave][lane] = acc;
     __syncthreads();
