@@ -4,7 +4,8 @@
 // (0.56 bytes a weight): codes [N, K/2] (element 2k in the low nibble), E4M3 block scales in
 // cuBLAS's 128x4 tiles (the leaf's resident layout), g the float32 second level.
 //
-// A workgroup of 8 waves takes 16 output rows; wave w takes the 128-column macro steps w, w + 8,
+// A workgroup of 8 waves takes 16 output rows (four rows from each 32-row quarter of a
+// 128-row scale tile); wave w takes the 128-column macro steps w, w + 8,
 // .... Per 32 columns a lane decodes 8 weights of its row: E2M1 by
 // v_cvt_scalef32_pk_f32_fp4, times the E4M3 scale — exact in float32 and again in bf16 or fp16 —
 // and one v_mfma_f32_16x16x32 multiplies them against the activation rows (zero past M).
@@ -76,8 +77,12 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
                                                                      uint16_t* __restrict__ out, int M, int N, int K) {
     __shared__ f32x4 partial[kGemvWaves][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n0 = blockIdx.x * 16;
-    const int row = n0 + (lane & 15);  // the weight row this lane decodes
+    // A workgroup's 16 rows are 32q + 4j + p (q, p = 0..3) of a 128-row tile block: the four
+    // 16-byte scale chunks of rows 4j .. 4j + 3 hold those 16 rows' scales, so a tile's bytes are
+    // fetched once. MFMA row i is tile row 32·(i/4) + 4j + i%4.
+    const int tile_block = blockIdx.x >> 3, j4 = 4 * (blockIdx.x & 7);
+    const auto row_of = [&](int i) { return 128 * tile_block + 32 * (i >> 2) + j4 + (i & 3); };
+    const int row = row_of(lane & 15);  // the weight row this lane decodes
     const int sub = lane >> 4;          // its 32-column quarter of a macro step
     const int width = K / 16, col_tiles = (width + 3) / 4;
     const __amdgpu_buffer_rsrc_t wr = bounded_rsrc(w, static_cast<int64_t>(N) * (K / 2));
@@ -139,13 +144,13 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
         const f32x4 p = partial[v][lane];
         sum = f32x4{sum[0] + p[0], sum[1] + p[1], sum[2] + p[2], sum[3] + p[3]};
     }
-    // D[n][m]: lane holds rows n0 + 4·(lane/16) + r of column m = lane % 16.
+    // D[i][m]: lane holds MFMA rows 4·(lane/16) + r of column m = lane % 16.
     const float g = scale_2[0];
     const int m = lane & 15;
     if (m >= M) return;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const int n = n0 + 4 * (lane >> 4) + r;
+        const int n = row_of(4 * (lane >> 4) + r);
         if (n < N) out[static_cast<int64_t>(m) * N + n] = narrow<kOutHalf>(sum[r] * g);
     }
 }
@@ -154,7 +159,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
 
 hipError_t nvfp4_gemv(const void* x, bool x_half, const uint8_t* w, const uint8_t* scale, const float* scale_2,
                       void* out, bool out_half, int M, int N, int K, hipStream_t s) {
-    const dim3 grid((N + 15) / 16), block(64 * kGemvWaves);
+    const dim3 grid((N + 127) / 128 * 8), block(64 * kGemvWaves);
     const auto* xp = static_cast<const uint16_t*>(x);
     auto* op = static_cast<uint16_t*>(out);
     if (x_half) {
