@@ -492,6 +492,60 @@ def bench_nvfp4(torch, ops, lib, stream, steps: int) -> dict:
     return {"nvfp4_w4a16_gemv": out}
 
 
+def bench_bake(torch, ops, lib, stream, steps: int) -> dict:
+    """The LoRA bake (`cozyq_bake`, `cozyq_bake_nvfp4`) of a rank-32 update into config 2's
+    weight shape ([12288, 3072]) in each stored form, in place, over 4 rotating weight copies,
+    graph-replayed. Algorithmic bytes: the stored weight read and written, its scales, and the
+    factors read once; the kernel's bound is the VALU (rank FMAs plus one Philox4x32-10 draw an
+    element), which `gelems` (elements baked per second) reports."""
+    from cozyq import bake as cb
+
+    rows, cols, rank, copies = 12288, 3072, 32, 4
+    gen = torch.Generator(device="cuda").manual_seed(131)
+    up = torch.randn(rows, rank, generator=gen, device="cuda") * 1e-4
+    down = torch.randn(rank, cols, generator=gen, device="cuda")
+    rotated = cb.rotate_factor(torch, down)
+    scale = torch.full((rows,), 0.01, device="cuda")
+    second = torch.tensor([0.01], device="cuda")
+    factors = 4 * rank * (rows + cols)
+    forms = {
+        "bf16": (cb.BF16, torch.bfloat16, 2 * rows * cols),
+        "fp8.rowwise": (cb.ROWWISE, torch.uint8, rows * cols + 4 * rows),
+        "int8.convrot": (cb.INT8, torch.int8, rows * cols + 4 * rows),
+        "nvfp4": (cb.NVFP4, torch.uint8, rows * cols // 2 + rows * cols // 16),
+    }
+    out = []
+    for name, (form, dtype, stored) in forms.items():
+        if form == cb.NVFP4:
+            weights = [(torch.randint(0, 256, (rows, cols // 2), generator=gen, device="cuda", dtype=torch.int32).to(torch.uint8),
+                        torch.randint(0x30, 0x48, (rows, cols // 16), generator=gen, device="cuda", dtype=torch.int32).to(torch.uint8))
+                       for _ in range(copies)]  # fmt: skip
+        elif dtype == torch.bfloat16:
+            weights = [(torch.randn(rows, cols, generator=gen, device="cuda") * 0.02).to(dtype) for _ in range(copies)]
+        else:
+            weights = [torch.randint(-100, 100, (rows, cols), generator=gen, device="cuda", dtype=torch.int32).to(dtype)
+                       for _ in range(copies)]  # fmt: skip
+        turn = [0]
+        sides = rotated if form == cb.INT8 else down
+
+        def go(raw, form=form, weights=weights, sides=sides):
+            w = weights[turn[0] % copies]
+            turn[0] += 1
+            if form == cb.NVFP4:
+                _check(lib.cozyq_bake_nvfp4(0, w[0].data_ptr(), w[1].data_ptr(), second.data_ptr(), up.data_ptr(),
+                                            sides.data_ptr(), rows, cols, rank, 77, raw))  # fmt: skip
+            else:
+                _check(lib.cozyq_bake(0, form, w.data_ptr(), scale.data_ptr(), up.data_ptr(), sides.data_ptr(),
+                                      rows, cols, rank, 77, raw))  # fmt: skip
+
+        us = _graph_us(torch, go, 4 * copies, max(4, steps // 8))
+        nbytes = 2 * stored + factors
+        out.append({"form": name, "rows": rows, "cols": cols, "rank": rank, "us": us,
+                    "gelems": rows * cols / (us * 1e-6) / 1e9, "gbs": nbytes / (us * 1e-6) / 1e9,
+                    "frac_hbm": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, "bytes": nbytes})
+    return {"lora_bake": out}
+
+
 def cpu_baseline(torch, rows: int = 1024) -> dict:
     """The reference's CPU law for config 2 on rows 0..rows-1 of the batch: rotation + per-token
     int8 (`quantize_rows`), the literal int32 matmul, both scales, bias and GELU."""
@@ -544,6 +598,8 @@ def only(torch, ops, lib, stream, args) -> int:
         figures = bench_weights(torch, ops, lib, stream, args.steps)
     elif args.only == "nvfp4":
         figures = bench_nvfp4(torch, ops, lib, stream, args.steps)
+    elif args.only == "bake":
+        figures = bench_bake(torch, ops, lib, stream, args.steps)
     else:
         figures = bench_svdq(torch, ops, lib, stream, args.steps)
     print(json.dumps({"only": args.only, **figures}))
@@ -561,7 +617,7 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
     parser.add_argument("--only", choices=("c2", "decode", "int8_decode", "w4a8", "fp8", "svdq", "mx", "weights",
-                                                    "nvfp4", "copy"),
+                                                    "nvfp4", "bake", "copy"),
                         help="profiling aid: run one leg (or a plain 256 MiB device copy, the "
                              "counter calibration) --steps times and print its figures only")  # fmt: skip
     args = parser.parse_args()
@@ -595,6 +651,7 @@ def main() -> int:
         configs["c5_mxfp8"] = bench_mx(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["weight_decode"] = bench_weights(torch, ops, lib, stream, args.steps)["decode_formats"]
         configs["nvfp4_w4a16"] = bench_nvfp4(torch, ops, lib, stream, args.steps)["nvfp4_w4a16_gemv"]
+        configs["lora_bake"] = bench_bake(torch, ops, lib, stream, args.steps)["lora_bake"]
         print("[bench] extra configs done", file=sys.stderr, flush=True)
     baseline = None if args.no_cpu else cpu_baseline(torch)
     line = {

@@ -8,7 +8,7 @@ falls back to anything: a missing or unloadable library raises `KernelsAbsent` w
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_float, c_int, c_int64, c_void_p
+from ctypes import c_float, c_int, c_int64, c_uint32, c_void_p
 from pathlib import Path
 
 PATH = Path(__file__).resolve().parent / "libcozyq.so"
@@ -83,6 +83,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int, [c_int, _P, c_int, _P, _P, _P, _P, _P, c_int64, c_int, _P]
     ),
     "cozyq_measure": (c_int, [c_int, _P, c_int, _P, c_int64, _P, c_int, _P, _P]),
+    "cozyq_bake": (c_int, [c_int, c_int, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_uint32, _P]),
+    "cozyq_bake_nvfp4": (c_int, [c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_uint32, _P]),
+    "cozyq_bake_rotate_factor": (c_int, [c_int, _P, _P, c_int64, c_int64, _P]),
     "cozyq_host_e4m3": (None, [_P, _P, c_int64]),
     "cozyq_host_mx_byte": (None, [_P, _P, c_int64]),
     "cozyq_probe_div": (c_int, [c_int, _P, _P, _P, c_int64, _P]),

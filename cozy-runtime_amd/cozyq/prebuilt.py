@@ -626,6 +626,66 @@ class Prebuilt:
             raise ValueError(f"{f.name}: bias must have {data.shape[0]} values")
         return _aligned(bias.to(out_dtype))
 
+    # -------------------------------------------------------------- LoRA bake
+
+    def bake(self, form: int, data: Tensor, scale: Tensor | None, up: Tensor, down: Tensor,
+             seed: int) -> None:  # fmt: skip
+        """`cozyq_bake` in place (`_bake_kernel`, `internal/lora_bake.py:1013-1053`): `data`
+        contiguous [rows, cols] of the form, `scale` float32 [rows] (row-scaled forms), `up`
+        float32 [rows, rank], `down` float32 [rank, cols] (int8.convrot: rotated)."""
+        rows, cols = (int(v) for v in data.shape)
+        rank = self._factors(up, down, rows, cols, (data,) if scale is None else (data, scale))
+        code = self._lib.cozyq_bake(
+            self.index, form, data.data_ptr(), None if scale is None else scale.data_ptr(),
+            up.data_ptr(), down.data_ptr(), rows, cols, rank, seed & 0xFFFFFFFF, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the LoRA bake")
+
+    def bake_nvfp4(self, data: Tensor, blocks: Tensor, second: Tensor, up: Tensor, down: Tensor,
+                   seed: int) -> None:  # fmt: skip
+        """`cozyq_bake_nvfp4` in place (`_bake_nvfp4_kernel`, `internal/lora_bake.py:955-1011`):
+        codes uint8 [rows, cols/2], E4M3 block bytes uint8 [rows, cols/16], float32 `second`."""
+        rows, cols = int(data.shape[0]), 2 * int(data.shape[1])
+        if tuple(blocks.shape) != (rows, cols // 16) or not blocks.is_contiguous():
+            raise ValueError(f"nvfp4 bake: block scales must be contiguous [{rows}, {cols // 16}]")
+        rank = self._factors(up, down, rows, cols, (data, blocks, second))
+        code = self._lib.cozyq_bake_nvfp4(
+            self.index, data.data_ptr(), blocks.data_ptr(), second.data_ptr(), up.data_ptr(),
+            down.data_ptr(), rows, cols, rank, seed & 0xFFFFFFFF, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the nvfp4 LoRA bake")
+
+    def rotate_factor(self, down: Tensor) -> Tensor:
+        """`cozyq_bake_rotate_factor` (`rotate_factor`, `internal/lora_bake.py:366-369`): float32
+        [rank, cols] times H256/16 per 256 columns, into a new tensor."""
+        if down.dtype != self.torch.float32 or down.dim() != 2 or not down.is_contiguous():
+            raise ValueError("rotate_factor: down must be contiguous float32 [rank, cols]")
+        if down.get_device() != self.index:
+            raise ValueError(f"rotate_factor: down must be on cuda:{self.index}")
+        out = self.torch.empty_like(down)
+        code = self._lib.cozyq_bake_rotate_factor(
+            self.index, down.data_ptr(), out.data_ptr(), int(down.shape[0]), int(down.shape[1]),
+            self._stream(),
+        )  # fmt: skip
+        self._check(code, "the factor rotation")
+        return out
+
+    def _factors(self, up: Tensor, down: Tensor, rows: int, cols: int, stored: tuple) -> int:
+        torch = self.torch
+        for t in (up, down):
+            if t.dtype != torch.float32 or t.dim() != 2 or not t.is_contiguous():
+                raise ValueError("LoRA bake: factors must be contiguous float32 matrices")
+        rank = int(up.shape[1])
+        if int(up.shape[0]) != rows or tuple(down.shape) != (rank, cols):
+            raise ValueError(f"LoRA bake: up must be [{rows}, rank] and down [rank, {cols}]; got "
+                             f"{tuple(up.shape)} and {tuple(down.shape)}")  # fmt: skip
+        for t in (*stored, up, down):
+            if not t.is_cuda or t.get_device() != self.index:
+                raise ValueError(f"LoRA bake: every tensor must be on cuda:{self.index}")
+        if not stored[0].is_contiguous():
+            raise ValueError("a fused bake writes a contiguous [out, in] weight")
+        return rank
+
     def _half(self, dtype: Dtype) -> bool:
         if dtype not in (self.torch.bfloat16, self.torch.float16):
             raise ValueError(f"8-bit linear: activations and outputs are bf16 or fp16, not {dtype}")

@@ -408,6 +408,48 @@ int cozyq_measure(int device, const void* w, int w_type, const float* decoded, i
     return cozyq::measure(w, w_type, decoded, total, partial, parts, out, on(stream));
 }
 
+int cozyq_bake_rotate_factor(int device, const float* down, float* out, int64_t rank, int64_t cols,
+                             void* stream) {
+    if (rank < 0 || cols < 0 || cols % 256 || rank * cols > (int64_t{1} << 40)) return hipErrorInvalidValue;
+    if (rank == 0 || cols == 0) return hipSuccess;
+    if (!down || !out) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::rotate_factor(down, out, rank * cols / 256, on(stream));
+}
+
+// Tiles are 64 rows × 128 columns: the grid's y extent bounds the rows.
+static bool bake_shape(int64_t rows, int64_t cols, int64_t rank) {
+    return rows >= 0 && cols >= 0 && rank >= 0 && rows <= 65535LL * 64 && cols <= 0x7fffffff &&
+           rank <= 0x7fffffff && rows * cols <= (int64_t{1} << 40);
+}
+
+int cozyq_bake(int device, int form, void* data, const float* scale, const float* up, const float* down,
+               int64_t rows, int64_t cols, int64_t rank, uint32_t seed, void* stream) {
+    if (form < cozyq::kBakeBf16 || form > cozyq::kBakeInt8 || !bake_shape(rows, cols, rank))
+        return hipErrorInvalidValue;
+    if (rows == 0 || cols == 0) return hipSuccess;
+    const bool scaled = form == cozyq::kBakeRowwise || form == cozyq::kBakeInt8;
+    if (!data || (scaled && !scale) || (rank > 0 && (!up || !down))) return hipErrorInvalidValue;
+    const size_t size = form == cozyq::kBakeF32 ? 4 : (form <= cozyq::kBakeF16 ? 2 : 1);
+    if (reinterpret_cast<uintptr_t>(data) % size) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::bake(form, data, scale, up, down, static_cast<int>(rows), static_cast<int>(cols),
+                       static_cast<int>(rank), seed, on(stream));
+}
+
+int cozyq_bake_nvfp4(int device, uint8_t* data, uint8_t* blocks, const float* second, const float* up,
+                     const float* down, int64_t rows, int64_t cols, int64_t rank, uint32_t seed, void* stream) {
+    if (!bake_shape(rows, cols, rank) || cols % 16) return hipErrorInvalidValue;
+    if (rows == 0 || cols == 0) return hipSuccess;
+    if (!data || !blocks || !second || (rank > 0 && (!up || !down))) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::bake_nvfp4(data, blocks, second, up, down, static_cast<int>(rows), static_cast<int>(cols),
+                             static_cast<int>(rank), seed, on(stream));
+}
+
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = cozyq::e4m3_rn(in[i]);
 }

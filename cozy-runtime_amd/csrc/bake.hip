@@ -1,0 +1,350 @@
+// The LoRA bake on gfx950 (reference: `fused`, internal/lora_bake.py:775-815, and its Triton
+// kernels :901-1053): a stored weight takes `up @ down` in place and is rounded back onto its
+// own form — bf16 stochastically (16 noise bits added under the kept ones), f16 / f32 to
+// nearest, fp8.rowwise E4M3 stochastically on the kept row scale, int8.convrot by a stochastic
+// floor on the kept row scale (`down` rotated first, `rotate_factor_kernel`), canonical nvfp4 by
+// stochastic E2M1 on its block grid (a block's E4M3 scale refitted only when its baked maximum
+// outgrows 7/6 of it).
+//
+// Element (row, col)'s noise is Triton's Philox4x32-10 draw at counter row·cols + col (mod 2^32)
+// under the seed, so a bake writes the bytes the reference's fused bake does for the same delta.
+// The delta is one float32 FMA chain per element over ranks 0, 1, ... from +0.
+//
+// A workgroup of 256 lanes takes a 64-row × 128-column tile: lane (rg = tid/16, cg = tid%16)
+// owns rows 4rg .. 4rg+3 and columns 4cg .. 4cg+3 and 64+4cg .. 64+4cg+3 (each 16-lane row of
+// a wave reads 256 contiguous bytes of LDS per rank). `up` (transposed) and `down` are staged
+// through LDS 32 ranks at a time. The hot part is the VALU: rank FMAs plus one Philox (ten
+// rounds, two 32x32→64-bit multiplies each) per element, against a few bytes of HBM.
+#include "common.h"
+#include "kernels.h"
+
+namespace cozyq {
+namespace {
+
+constexpr int kTileRows = 64, kTileCols = 128, kRankChunk = 32, kBakeThreads = 256;
+
+// Philox4x32-10 (Salmon et al., SC'11) at counter (offset, 0, 0, 0) under key (k0, k1): the
+// first output word, Triton's `tl.randint`.
+__device__ __forceinline__ uint32_t philox_word(uint32_t offset, uint32_t k0, uint32_t k1) {
+    uint32_t c0 = offset, c1 = 0, c2 = 0, c3 = 0;
+#pragma unroll
+    for (int round = 0; round < 10; ++round) {
+        const uint64_t pb = static_cast<uint64_t>(0xCD9E8D57u) * c2;
+        const uint64_t pa = static_cast<uint64_t>(0xD2511F53u) * c0;
+        c0 = static_cast<uint32_t>(pb >> 32) ^ c1 ^ k0;
+        c2 = static_cast<uint32_t>(pa >> 32) ^ c3 ^ k1;
+        c1 = static_cast<uint32_t>(pb);
+        c3 = static_cast<uint32_t>(pa);
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    return c0;
+}
+
+// Triton's `tl.rand` from a draw: the int32 view folded to non-negative (x < 0 → −x − 1),
+// converted and scaled by the largest float32 that keeps (2^31 − 1)·scale under 1.
+__device__ __forceinline__ float uniform(uint32_t word) {
+    const int32_t x = static_cast<int32_t>(word);
+    return static_cast<float>(x < 0 ? ~x : x) * 0x1.fffffep-32f;
+}
+
+// E4M3 byte → float32 with the reserved codes saturating to ±448.
+__device__ __forceinline__ float e4m3_sat(uint32_t code) {
+    const uint32_t field = (code >> 3) & 15u, mantissa = code & 7u;
+    float magnitude = field == 0 ? static_cast<float>(mantissa) * 0.001953125f
+                                 : static_cast<float>(mantissa + 8u) * float_of((field + 117u) << 23);
+    if ((code & 127u) == 127u) magnitude = 448.0f;
+    return code > 127u ? -magnitude : magnitude;
+}
+
+// float32 payload → E4M3 byte, saturating at 448: twenty noise bits added under the three kept
+// mantissa bits and the rest truncated; below 2^-6 the value is lifted by 2^-6 into the binade
+// whose step (2^-9) is the subnormal one, and lowered back by the code offset.
+__device__ __forceinline__ uint32_t e4m3_stochastic(float payload, uint32_t noise) {
+    const float magnitude = __builtin_fminf(__builtin_fabsf(payload), 448.0f);
+    const bool small = magnitude < 0.015625f;
+    const float lifted = small ? magnitude + 0.015625f : magnitude;
+    const int kept = static_cast<int>((bits_of(lifted) + (noise >> 12)) >> 20);
+    const int code = kept - (small ? 968 : 960);
+    return static_cast<uint32_t>(payload < 0.0f ? (code | 128) : code);
+}
+
+// The least E4M3 code (0..126) whose value holds need ≥ 0: the float32 bits rounded up to three
+// mantissa bits, or below 2^-6 a count of 2^-9 steps.
+__device__ __forceinline__ uint32_t e4m3_at_least(float need) {
+    const uint32_t bits = (bits_of(need) + 0xFFFFFu) & 0xFFF00000u;
+    const int normal = ((static_cast<int>(bits >> 23) - 120) << 3) | static_cast<int>((bits >> 20) & 7u);
+    const int code = need < 0.015625f ? static_cast<int>(__builtin_ceilf(__builtin_fmaxf(need * 512.0f, 0.0f)))
+                                      : normal;
+    return static_cast<uint32_t>(code < 0 ? 0 : (code > 126 ? 126 : code));
+}
+
+__device__ __forceinline__ float e2m1_of(uint32_t code) {
+    const float index = static_cast<float>(code & 7u);
+    const float magnitude = index < 4.0f ? index * 0.5f : (index < 6.0f ? index - 2.0f : (index < 7.0f ? 4.0f : 6.0f));
+    return code >= 8u ? -magnitude : magnitude;
+}
+
+// |payload| (block units, saturating at 6) → E2M1 magnitude code, the upper neighbour when the
+// draw is under the fraction of the step covered.
+__device__ __forceinline__ uint32_t e2m1_stochastic(float payload, float draw) {
+    const float magnitude = __builtin_fminf(__builtin_fabsf(payload), 6.0f);
+    const float step = magnitude < 2.0f ? 0.5f : (magnitude < 4.0f ? 1.0f : 2.0f);
+    const float low = __builtin_fminf(__builtin_floorf(magnitude / step) * step, 6.0f);
+    const float index = low < 2.0f ? low * 2.0f : (low < 4.0f ? low + 2.0f : (low < 6.0f ? 6.0f : 7.0f));
+    return static_cast<uint32_t>(index + (draw < (magnitude - low) / step ? 1.0f : 0.0f));
+}
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return float_of(static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(bits_of(v)), kCtrl, 0xf, 0xf, false)));
+}
+
+// The column of a lane's element j (0..7) within its tile.
+__device__ __forceinline__ int tile_col(int cg, int j) { return (j < 4 ? 4 * cg : 64 + 4 * cg) + (j & 3); }
+
+// acc[i][j] = Σ_r up[row_i, r] · down[r, col_j], one FMA chain in rank order from +0. Rows past
+// `rows` and columns past `cols` stage zeros. Every lane of the workgroup calls it.
+__device__ __forceinline__ void tile_delta(float (&acc)[4][8], const float* __restrict__ up,
+                                           const float* __restrict__ down, int rows, int cols, int rank,
+                                           int row0, int col0, float (*up_lds)[kTileRows],
+                                           float (*down_lds)[kTileCols]) {
+    const int tid = threadIdx.x, rg = tid >> 4, cg = tid & 15;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+    for (int r0 = 0; r0 < rank; r0 += kRankChunk) {
+        __syncthreads();  // the previous chunk is consumed
+        for (int e = tid; e < kRankChunk * kTileRows; e += kBakeThreads) {
+            const int k = e % kRankChunk, r = e / kRankChunk;
+            const int row = row0 + r, rk = r0 + k;
+            up_lds[k][r] = row < rows && rk < rank ? up[static_cast<int64_t>(row) * rank + rk] : 0.0f;
+        }
+        for (int e = tid; e < kRankChunk * kTileCols; e += kBakeThreads) {
+            const int c = e % kTileCols, k = e / kTileCols;
+            const int col = col0 + c, rk = r0 + k;
+            down_lds[k][c] = col < cols && rk < rank ? down[static_cast<int64_t>(rk) * cols + col] : 0.0f;
+        }
+        __syncthreads();
+        const int n = rank - r0 < kRankChunk ? rank - r0 : kRankChunk;
+        for (int k = 0; k < n; ++k) {
+            const f32x4 u = *reinterpret_cast<const f32x4*>(&up_lds[k][4 * rg]);
+            const f32x4 d0 = *reinterpret_cast<const f32x4*>(&down_lds[k][4 * cg]);
+            const f32x4 d1 = *reinterpret_cast<const f32x4*>(&down_lds[k][64 + 4 * cg]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] = __builtin_fmaf(u[i], d0[j], acc[i][j]);
+                    acc[i][4 + j] = __builtin_fmaf(u[i], d1[j], acc[i][4 + j]);
+                }
+        }
+    }
+}
+
+// Stored element types by form.
+template <int kForm> struct Stored;
+template <> struct Stored<kBakeBf16> { using T = uint16_t; };
+template <> struct Stored<kBakeF16> { using T = uint16_t; };
+template <> struct Stored<kBakeF32> { using T = float; };
+template <> struct Stored<kBakeRowwise> { using T = uint8_t; };
+template <> struct Stored<kBakeInt8> { using T = int8_t; };
+
+// One element of a `_bake_kernel` form: the stored value (its bits), the delta, the row's unit
+// (ROWWISE, INT8) and the element's Philox counter → the new stored value.
+template <int kForm>
+__device__ __forceinline__ typename Stored<kForm>::T bake_one(typename Stored<kForm>::T v, float d, float unit,
+                                                               uint32_t at, uint32_t k0, uint32_t k1) {
+    if constexpr (kForm == kBakeBf16) {
+        const float value = float_of(static_cast<uint32_t>(v) << 16) + d;
+        const uint32_t noise = philox_word(at, k0, k1);
+        return static_cast<uint16_t>((bits_of(value) + (noise >> 16)) >> 16);
+    } else if constexpr (kForm == kBakeF16) {
+        return narrow<true>(widen<true>(v) + d);
+    } else if constexpr (kForm == kBakeF32) {
+        return v + d;
+    } else if constexpr (kForm == kBakeRowwise) {
+        const float payload = e4m3_sat(v) + d / unit;
+        return static_cast<uint8_t>(e4m3_stochastic(payload, philox_word(at, k0, k1)));
+    } else {
+        const float draw = uniform(philox_word(at, k0, k1));
+        const float stored = __builtin_floorf((static_cast<float>(v) + d / unit) + draw);
+        return static_cast<int8_t>(__builtin_fminf(__builtin_fmaxf(stored, -127.0f), 127.0f));
+    }
+}
+
+// kVec: cols % 4 == 0 and `data` aligned to four elements, so each lane's four-column group
+// moves as one load and one store.
+template <int kForm, bool kVec>
+__global__ __launch_bounds__(kBakeThreads) void bake_kernel(typename Stored<kForm>::T* __restrict__ data,
+                                                            const float* __restrict__ scale,
+                                                            const float* __restrict__ up,
+                                                            const float* __restrict__ down, int rows, int cols,
+                                                            int rank, uint32_t seed) {
+    using T = typename Stored<kForm>::T;
+    __shared__ float up_lds[kRankChunk][kTileRows];
+    __shared__ float down_lds[kRankChunk][kTileCols];
+    const int row0 = blockIdx.y * kTileRows, col0 = blockIdx.x * kTileCols;
+    float acc[4][8];
+    tile_delta(acc, up, down, rows, cols, rank, row0, col0, up_lds, down_lds);
+    const int rg = threadIdx.x >> 4, cg = threadIdx.x & 15;
+    const uint32_t k1 = (seed >> 31) ? 0xFFFFFFFFu : 0u;  // the int32 seed sign-extended
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = row0 + 4 * rg + i;
+        if (row >= rows) break;
+        const float unit = (kForm == kBakeRowwise || kForm == kBakeInt8) ? scale[row] : 1.0f;
+        T* line = data + static_cast<int64_t>(row) * cols;
+        const uint32_t line_at = static_cast<uint32_t>(static_cast<uint64_t>(row) * static_cast<uint64_t>(cols));
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int col = col0 + tile_col(cg, 4 * h);
+            if (col >= cols) continue;
+            if constexpr (kVec) {
+                struct alignas(4 * sizeof(T)) Four { T v[4]; };
+                Four four = *reinterpret_cast<const Four*>(line + col);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    four.v[e] = bake_one<kForm>(four.v[e], acc[i][4 * h + e], unit, line_at + col + e, seed, k1);
+                *reinterpret_cast<Four*>(line + col) = four;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < cols)
+                        line[col + e] = bake_one<kForm>(line[col + e], acc[i][4 * h + e], unit, line_at + col + e, seed, k1);
+            }
+        }
+    }
+}
+
+// `_bake_nvfp4_kernel`: codes [rows, cols/2] (element 2k in the low nibble), E4M3 block bytes
+// [rows, cols/16], the float32 second level at `second`; cols % 16 == 0. A 16-column block is
+// the four lanes cg = 4q .. 4q+3 of one half-row, so its maximum is a DPP quad reduction; every
+// lane reaches it (rows or blocks past the end bake zeros and store nothing).
+__global__ __launch_bounds__(kBakeThreads) void bake_nvfp4_kernel(uint8_t* __restrict__ data, uint8_t* __restrict__ blocks,
+                                                                  const float* __restrict__ second,
+                                                                  const float* __restrict__ up,
+                                                                  const float* __restrict__ down, int rows, int cols,
+                                                                  int rank, uint32_t seed) {
+    __shared__ float up_lds[kRankChunk][kTileRows];
+    __shared__ float down_lds[kRankChunk][kTileCols];
+    const int row0 = blockIdx.y * kTileRows, col0 = blockIdx.x * kTileCols;
+    float acc[4][8];
+    tile_delta(acc, up, down, rows, cols, rank, row0, col0, up_lds, down_lds);
+    const int rg = threadIdx.x >> 4, cg = threadIdx.x & 15;
+    const uint32_t k1 = (seed >> 31) ? 0xFFFFFFFFu : 0u;
+    const float level = second[0];
+    const int width = cols / 2, count = cols / 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = row0 + 4 * rg + i;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int col = col0 + tile_col(cg, 4 * h);
+            const bool live = row < rows && col < cols;
+            const int64_t pair = static_cast<int64_t>(row) * width + col / 2;
+            const int64_t which = static_cast<int64_t>(row) * count + col / 16;
+            const uint32_t codes = live ? (static_cast<uint32_t>(data[pair]) | (static_cast<uint32_t>(data[pair + 1]) << 8)) : 0u;
+            const uint32_t kept = live ? static_cast<uint32_t>(blocks[which]) : 0u;
+            const float scaled = e4m3_sat(kept) * level;
+            float target[4];
+            float peak = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                target[e] = __builtin_fmaf(e2m1_of((codes >> (4 * e)) & 15u), scaled, acc[i][4 * h + e]);
+                peak = __builtin_fmaxf(peak, __builtin_fabsf(target[e]));
+            }
+            peak = __builtin_fmaxf(peak, dpp_f32<0xB1>(peak));  // quad_perm [1,0,3,2]
+            peak = __builtin_fmaxf(peak, dpp_f32<0x4E>(peak));  // quad_perm [2,3,0,1]
+            const float need = peak / (6.0f * level);
+            const bool grown = need * 6.0f > e4m3_sat(kept) * 7.0f;
+            const uint32_t block = grown ? e4m3_at_least(need) : kept;
+            const float unit = e4m3_sat(block) * level;
+            const float den = unit > 0.0f ? unit : 1.0f;
+            const uint32_t at = static_cast<uint32_t>(static_cast<uint64_t>(row) * static_cast<uint64_t>(cols) + col);
+            uint32_t out = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t stored = (codes >> (4 * e)) & 15u;
+                uint32_t nibble = e2m1_stochastic(target[e] / den, uniform(philox_word(at + e, seed, k1)));
+                const bool negative = target[e] == 0.0f ? stored >= 8u : target[e] < 0.0f;
+                out |= (nibble | (negative ? 8u : 0u)) << (4 * e);
+            }
+            if (live) {
+                data[pair] = static_cast<uint8_t>(out);
+                data[pair + 1] = static_cast<uint8_t>(out >> 8);
+                if ((cg & 3) == 0) blocks[which] = static_cast<uint8_t>(block);
+            }
+        }
+    }
+}
+
+// `rotate_factor`: each 256 columns of `down` times the regular Hadamard H4⊗H4⊗H4⊗H4, one
+// 4-point stage per digit, outer digit (stride 64) first, each output evaluated left to right as
+// (a+b+c−d, a+b−c+d, a−b+c+d, b+c+d−a), then 1/16. Four 256-groups per workgroup.
+__global__ __launch_bounds__(256) void rotate_factor_kernel(const float* __restrict__ down, float* __restrict__ out,
+                                                            int64_t groups) {
+    __shared__ float lds[4][256];
+    const int q = threadIdx.x >> 6, t = threadIdx.x & 63;
+    const int64_t group = static_cast<int64_t>(blockIdx.x) * 4 + q;
+    const bool live = group < groups;
+    float* x = lds[q];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[t + 64 * k] = live ? down[group * 256 + t + 64 * k] : 0.0f;
+    __syncthreads();
+#pragma unroll
+    for (int stride = 64; stride >= 1; stride /= 4) {
+        const int base = (t / stride) * 4 * stride + t % stride;
+        const float a = x[base], b = x[base + stride], c = x[base + 2 * stride], d = x[base + 3 * stride];
+        x[base] = ((a + b) + c) - d;
+        x[base + stride] = ((a + b) - c) + d;
+        x[base + 2 * stride] = ((a - b) + c) + d;
+        x[base + 3 * stride] = ((b + c) + d) - a;
+        __syncthreads();
+    }
+    if (live)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) out[group * 256 + t + 64 * k] = x[t + 64 * k] * 0.0625f;
+}
+
+template <int kForm>
+hipError_t launch_bake(void* data, const float* scale, const float* up, const float* down, int rows, int cols,
+                       int rank, uint32_t seed, hipStream_t s) {
+    using T = typename Stored<kForm>::T;
+    const dim3 grid((cols + kTileCols - 1) / kTileCols, (rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
+    T* d = static_cast<T*>(data);
+    const bool vec = cols % 4 == 0 && reinterpret_cast<uintptr_t>(data) % (4 * sizeof(T)) == 0;
+    if (vec) hipLaunchKernelGGL((bake_kernel<kForm, true>), grid, block, 0, s, d, scale, up, down, rows, cols, rank, seed);
+    else hipLaunchKernelGGL((bake_kernel<kForm, false>), grid, block, 0, s, d, scale, up, down, rows, cols, rank, seed);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t bake(int form, void* data, const float* scale, const float* up, const float* down, int rows, int cols,
+                int rank, uint32_t seed, hipStream_t s) {
+    switch (form) {
+        case kBakeBf16: return launch_bake<kBakeBf16>(data, scale, up, down, rows, cols, rank, seed, s);
+        case kBakeF16: return launch_bake<kBakeF16>(data, scale, up, down, rows, cols, rank, seed, s);
+        case kBakeF32: return launch_bake<kBakeF32>(data, scale, up, down, rows, cols, rank, seed, s);
+        case kBakeRowwise: return launch_bake<kBakeRowwise>(data, scale, up, down, rows, cols, rank, seed, s);
+        case kBakeInt8: return launch_bake<kBakeInt8>(data, scale, up, down, rows, cols, rank, seed, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const float* up, const float* down,
+                      int rows, int cols, int rank, uint32_t seed, hipStream_t s) {
+    const dim3 grid((cols + kTileCols - 1) / kTileCols, (rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
+    hipLaunchKernelGGL(bake_nvfp4_kernel, grid, block, 0, s, data, blocks, second, up, down, rows, cols, rank, seed);
+    return hipGetLastError();
+}
+
+hipError_t rotate_factor(const float* down, float* out, int64_t groups, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>((groups + 3) / 4)), block(256);
+    hipLaunchKernelGGL(rotate_factor_kernel, grid, block, 0, s, down, out, groups);
+    return hipGetLastError();
+}
+
+}  // namespace cozyq

@@ -247,6 +247,38 @@ int cozyq_encode_nvfp4(int device, const void* w, int w_type, uint8_t* codes, ui
 int cozyq_measure(int device, const void* w, int w_type, const float* decoded, int64_t total,
                   double* partial, int parts, double* out, void* stream);
 
+/* LoRA bake, in place (reference: `fused`, internal/lora_bake.py:775-815, and its Triton kernel
+ * `_bake_kernel`, :1013-1053, one entry for its five forms): data [rows, cols] takes
+ * up [rows, rank] @ down [rank, cols] (float32, one FMA chain per element in rank order) and is
+ * rounded back onto its form. form 0: bf16 (stochastic: 16 noise bits added under the kept
+ * ones), 1: fp16, 2: float32 (nearest), 3: fp8.rowwise E4M3 bytes on the kept float32 row scale
+ * `scale` [rows] (stochastic, saturating at 448), 4: int8.convrot (`down` already
+ * `cozyq_bake_rotate_factor`ed; floor(code + delta/scale + u), clamped to ±127). Element (r, c)'s
+ * noise is Philox4x32-10 at counter (r·cols + c mod 2^32, 0, 0, 0) under the key (seed, seed's
+ * sign), Triton's `tl.randint` / `tl.rand`; the reference passes seed & 0x7FFFFFFF. data aligned
+ * to its element; rows ≤ 65535·64. Errors: hipErrorInvalidValue for a bad form, shape or
+ * pointer. */
+int cozyq_bake(int device, int form, void* data, const float* scale, const float* up,
+               const float* down, int64_t rows, int64_t cols, int64_t rank, uint32_t seed,
+               void* stream);
+
+/* LoRA bake into canonical nvfp4 (reference: `_bake_nvfp4_kernel`, internal/lora_bake.py:
+ * 955-1011, `bake_nvfp4` with `keep`): codes [rows, cols/2] (element 2k in the low nibble), E4M3
+ * block bytes [rows, cols/16] row-major, float32 second level at `second` (kept). A block keeps
+ * its scale unless its baked maximum passes 7/6 of it, then takes the least E4M3 code that holds
+ * it; elements round stochastically on the block's E2M1 grid (saturating at 6) with the noise of
+ * `cozyq_bake`'s `tl.rand`; a zero keeps its stored sign. cols % 16 == 0. */
+int cozyq_bake_nvfp4(int device, uint8_t* data, uint8_t* blocks, const float* second,
+                     const float* up, const float* down, int64_t rows, int64_t cols, int64_t rank,
+                     uint32_t seed, void* stream);
+
+/* `down` [rank, cols] in an int8-convrot256/1 weight's basis (reference: `rotate_factor`,
+ * internal/lora_bake.py:366-369): each 256 columns times the regular Hadamard H4⊗H4⊗H4⊗H4 in
+ * the expression order of internal/encoding/formats.py:664-671, then 1/16; out [rank, cols]
+ * float32. cols % 256 == 0. */
+int cozyq_bake_rotate_factor(int device, const float* down, float* out, int64_t rank,
+                             int64_t cols, void* stream);
+
 /* Test entries (no reference counterpart): the kernels' scalar conversions run on the host,
  * so CPU tests can hold the device code's arithmetic against torch without a GPU. */
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n);

@@ -1,0 +1,259 @@
+"""CPU restatement of the LoRA bake's fused law — TEST INFRASTRUCTURE ONLY (see `oracle/__init__`).
+
+The reference bakes `up @ down` into a stored weight in place on the GPU with one Triton kernel
+per stored form (`internal/lora_bake.py:775-815` `fused`, kernels `:955-1053`): bf16 (stochastic
+by adding 16 noise bits), f16 and f32 (nearest), `fp8.rowwise` (E4M3 data, stochastic, row
+scale kept), `int8-convrot256/1` (int8 of the rotated rows, stochastic floor, row scale kept,
+`down` rotated by `rotate_factor`) and canonical `nvfp4` (E2M1 codes, E4M3 block scales kept
+unless a block outgrows 7/6 of its scale, the f32 second level kept). The noise of element
+(row, col) is Triton's Philox draw at counter `row * cols + col` (taken mod 2^32) under the
+31-bit seed. Everything here is numpy float32 / uint32 arithmetic, operation for operation:
+
+- `delta`: `up @ down` as one float32 FMA chain per element in rank order from +0 — the order an
+  IEEE f32 `tl.dot`'s FMA lowering takes over `:1023-1033`. The FMA is exact (`fma32`).
+- nvfp4's target is `fma(e2m1, scale·level, delta)`: the product-plus-delta at `:990` under
+  Triton's default floating-point contraction. Every other mul/add of the kernels is separate.
+
+Pins, exercised in `tests/test_bake.py`:
+- `philox` (Philox4x32-10, Salmon et al., SC'11): the three published Random123 known-answer
+  vectors (zero, all-ones and pi counters/keys).
+- `randint`, `rand` (seed/offset mapping and the uint → [0, 1) map of Triton's `tl.randint` /
+  `tl.rand`): `tests/golden/philox_vectors.json`, written by `tests/golden/make_philox_vectors.py`
+  from Triton's own interpreter (the installed library, not the reference).
+- `fma32`: exact rational arithmetic (`fractions.Fraction`) rounded to float32 by an
+  independent integer rounding, over random and constructed near-tie triples.
+- `e4m3_value`, `e4m3_stochastic`, `e4m3_at_least`, `e2m1_value`, `e2m1_stochastic`: brute force
+  over every code and every neighbouring pair — exact grid values round to themselves under any
+  noise, the result is always one of the two grid neighbours, rounding up happens exactly when
+  the draw is under the covered fraction; `e4m3_at_least` is the least code whose value holds
+  the need (against a sorted search of the 127 magnitudes).
+- `bake`, `bake_nvfp4`: the reference's own self-check cases (`probe`, `:852-898`, exact
+  results for every form over partial tiles and two inner steps); rank 0 writes back every byte
+  (but the reserved E4M3 codes and signed zeros, as the law says); the mean over seeds of a
+  stochastic bake is the exact target (statistical bound); nearest rounding for f16 against
+  numpy's own cast.
+- `rotate_factor`: the reference's Hadamard expression order (`internal/encoding/formats.py:
+  664-671`, evaluated left to right, as `laws.hadamard`) and the closed form H·H = 256·I.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import laws
+
+#: Stored forms (`internal/lora_bake.py:768`).
+BF16, F16, F32, ROWWISE, INT8, NVFP4 = range(6)
+#: A seed is 31 bits (`internal/lora_bake.py:770`).
+SEED_MASK = 0x7FFFFFFF
+
+# Philox4x32 constants: the Weyl key increments and the round multipliers.
+_KEY_A, _KEY_B = np.uint32(0x9E3779B9), np.uint32(0xBB67AE85)
+_ROUND_A, _ROUND_B = np.uint64(0xD2511F53), np.uint64(0xCD9E8D57)
+#: Triton's uint32 → [0, 1) scale, the largest float32 with (2^31 − 1)·scale < 1.
+UNIFORM_SCALE = np.float32(4.6566127342e-10)
+
+_F32 = np.float32
+_U32 = np.uint32
+
+
+# ----------------------------------------------------------------------------- noise
+
+
+def philox(key: int, c0, c1=0, c2=0, c3=0, rounds: int = 10):
+    """Philox4x32-`rounds` of counters (c0, c1, c2, c3) under the 64-bit key (lo, hi), uint32
+    arrays. Each round: c0' = hi(B·c2) ^ c1 ^ k0, c2' = hi(A·c0) ^ c3 ^ k1, c1' = lo(B·c2),
+    c3' = lo(A·c0), then the key adds its Weyl constants."""
+    shape = np.broadcast(np.asarray(c0), np.asarray(c1), np.asarray(c2), np.asarray(c3)).shape
+    c = [np.broadcast_to(np.asarray(v, dtype=np.uint64) & 0xFFFFFFFF, shape).astype(np.uint64)
+         for v in (c0, c1, c2, c3)]  # fmt: skip
+    k0, k1 = np.uint64(key & 0xFFFFFFFF), np.uint64((key >> 32) & 0xFFFFFFFF)
+    mask = np.uint64(0xFFFFFFFF)
+    for _ in range(rounds):
+        pb, pa = _ROUND_B * c[2], _ROUND_A * c[0]
+        c = [((pb >> np.uint64(32)) ^ c[1] ^ k0) & mask, pb & mask,
+             ((pa >> np.uint64(32)) ^ c[3] ^ k1) & mask, pa & mask]  # fmt: skip
+        k0 = (k0 + np.uint64(_KEY_A)) & mask
+        k1 = (k1 + np.uint64(_KEY_B)) & mask
+    return tuple(v.astype(np.uint32) for v in c)
+
+
+def _key(seed: int) -> int:
+    """Triton's key from an int32 seed argument: sign-extended to 64 bits (`tl.philox`)."""
+    seed = int(seed) & 0xFFFFFFFF
+    return seed | (0xFFFFFFFF << 32) if seed >= 1 << 31 else seed
+
+
+def randint(seed: int, offset) -> np.ndarray:
+    """`tl.randint(seed, offset)` for uint32 offsets: the first Philox output at counter
+    (offset, 0, 0, 0)."""
+    return philox(_key(seed), np.asarray(offset, dtype=np.uint64) & 0xFFFFFFFF)[0]
+
+
+def rand(seed: int, offset) -> np.ndarray:
+    """`tl.rand`: the int32 view of `randint` folded to non-negative (x < 0 → −x − 1), converted
+    to float32 and times `UNIFORM_SCALE`; in [0, 1)."""
+    x = randint(seed, offset).view(np.int32)
+    folded = np.where(x < 0, ~x, x)
+    return folded.astype(np.float32) * UNIFORM_SCALE
+
+
+# ----------------------------------------------------------------------------- exact float32 FMA
+
+
+def fma32(a, b, c) -> np.ndarray:
+    """float32 fused multiply-add, correctly rounded: the float32 product is exact in float64,
+    the float64 sum is made round-to-odd (TwoSum error, then the odd neighbour), and rounding a
+    round-to-odd float64 to float32 is the correct rounding (Boldo & Melquiond, 2008)."""
+    a64, b64, c64 = (np.asarray(v, dtype=np.float32).astype(np.float64) for v in (a, b, c))
+    p = a64 * b64
+    s = p + c64
+    bb = s - p
+    err = (p - (s - bb)) + (c64 - bb)
+    bits = np.asarray(s).view(np.int64)
+    even = (bits & 1) == 0
+    away = (err > 0) == (s > 0)
+    fix = (err != 0) & even & np.isfinite(s)
+    bits = np.where(fix, bits + np.where(away, 1, -1), bits)
+    return bits.view(np.float64).astype(np.float32)
+
+
+def delta(up: np.ndarray, down: np.ndarray) -> np.ndarray:
+    """`up @ down` (float32 `[rows, rank]` × `[rank, cols]`) as a float32 FMA chain per element
+    over ranks 0, 1, ... from +0."""
+    rows, rank = up.shape
+    acc = np.zeros((rows, down.shape[1]), dtype=np.float32)
+    for r in range(rank):
+        acc = fma32(up[:, r : r + 1], down[r : r + 1, :], acc)
+    return acc
+
+
+# ----------------------------------------------------------------------------- grids
+
+
+def e4m3_value(code) -> np.ndarray:
+    """E4M3 bytes → float32, the two reserved codes saturating to ±448
+    (`internal/lora_bake.py:901-909`)."""
+    code = np.asarray(code).astype(np.int64)
+    field, mantissa = (code >> 3) & 15, (code & 7).astype(np.float32)
+    normal = (mantissa + _F32(8)) * ((field + 117) << 23).astype(np.uint32).view(np.float32)
+    magnitude = np.where(field == 0, mantissa * _F32(0.001953125), normal).astype(np.float32)
+    magnitude = np.where((code & 127) == 127, _F32(448), magnitude)
+    return np.where(code > 127, -magnitude, magnitude).astype(np.float32)
+
+
+def e4m3_stochastic(payload, noise) -> np.ndarray:
+    """float32 payload → E4M3 byte, saturating at 448: twenty noise bits added under the three
+    kept mantissa bits, the rest truncated; below 2^-6 the value is lifted by 2^-6 into the
+    grid of step 2^-9 (`internal/lora_bake.py:911-922`). A NaN payload takes 448's code."""
+    payload = np.asarray(payload, dtype=np.float32)
+    magnitude = np.fmin(np.abs(payload), _F32(448))
+    small = magnitude < _F32(0.015625)
+    lifted = np.where(small, magnitude + _F32(0.015625), magnitude).astype(np.float32)
+    kept = ((lifted.view(np.uint32) + (np.asarray(noise, dtype=np.uint32) >> 12)) >> 20).astype(np.int64)
+    code = kept - np.where(small, 968, 960)
+    return np.where(payload < 0, code | 128, code).astype(np.uint8)
+
+
+def e4m3_at_least(need) -> np.ndarray:
+    """The least E4M3 code (0..126) whose value holds `need` ≥ 0: its float32 bits rounded up
+    to three mantissa bits, or below 2^-6 a count of 2^-9 (`internal/lora_bake.py:924-931`)."""
+    need = np.asarray(need, dtype=np.float32)
+    bits = ((need.view(np.uint32).astype(np.uint64) + 0xFFFFF) & 0xFFF00000).astype(np.int64)
+    normal = (((bits >> 23) - 120) << 3) | ((bits >> 20) & 7)
+    tiny = np.ceil(np.fmax(need * _F32(512), _F32(0))).astype(np.int64)
+    code = np.where(need < _F32(0.015625), tiny, normal)
+    return np.clip(code, 0, 126)
+
+
+def e2m1_value(code) -> np.ndarray:
+    """E2M1 codes (sign in bit 3) → float32 (`internal/lora_bake.py:933-940`)."""
+    code = np.asarray(code).astype(np.int64)
+    magnitude = np.asarray(laws.E2M1_VALUES[:8], dtype=np.float32)[code & 7]
+    return np.where(code >= 8, -magnitude, magnitude).astype(np.float32)
+
+
+def e2m1_stochastic(payload, draw) -> np.ndarray:
+    """|payload| (block units, saturating at 6) → its E2M1 magnitude code, the upper neighbour
+    when the draw is under the fraction of the step covered (`internal/lora_bake.py:942-953`)."""
+    payload, draw = np.asarray(payload, dtype=np.float32), np.asarray(draw, dtype=np.float32)
+    magnitude = np.fmin(np.abs(payload), _F32(6))
+    step = np.where(magnitude < 2, _F32(0.5), np.where(magnitude < 4, _F32(1), _F32(2))).astype(np.float32)
+    low = np.fmin(np.floor(magnitude / step) * step, _F32(6)).astype(np.float32)
+    index = np.where(low < 2, low * 2, np.where(low < 4, low + 2, np.where(low < 6, 6, 7)))
+    up = draw < ((magnitude - low) / step).astype(np.float32)
+    return (index.astype(np.int64) + up).astype(np.int64)
+
+
+# ----------------------------------------------------------------------------- bakes
+
+
+def rotate_factor(down: np.ndarray) -> np.ndarray:
+    """`down` `[rank, in]` in an `int8-convrot256/1` weight's basis: each 256 input channels
+    times the unnormalized regular Hadamard in the reference's expression order, then 1/16
+    (`internal/lora_bake.py:366-369`)."""
+    rotated = laws.hadamard(torch.from_numpy(np.ascontiguousarray(down, dtype=np.float32)), 256)
+    return rotated.numpy().astype(np.float32) * _F32(1.0 / 16)
+
+
+def _offsets(rows: int, cols: int) -> np.ndarray:
+    return (np.arange(rows, dtype=np.uint64)[:, None] * np.uint64(cols)
+            + np.arange(cols, dtype=np.uint64)[None, :]) & np.uint64(0xFFFFFFFF)  # fmt: skip
+
+
+def bake(form: int, data: np.ndarray, scale: np.ndarray | None, up: np.ndarray, down: np.ndarray,
+         seed: int) -> np.ndarray:  # fmt: skip
+    """The new stored data of one `_bake_kernel` form (`internal/lora_bake.py:1013-1053`):
+    `data` `[rows, cols]` as stored (bf16 / f16 as uint16 bits, f32, E4M3 or int8 bytes),
+    `scale` the float32 row scale of ROWWISE and INT8, `up` float32 `[rows, rank]`, `down`
+    float32 `[rank, cols]` (INT8: already `rotate_factor`ed)."""
+    rows, cols = data.shape
+    d = delta(up.astype(np.float32), down.astype(np.float32))
+    at = _offsets(rows, cols)
+    if form == INT8:
+        unit = scale.astype(np.float32).reshape(-1, 1)
+        draw = rand(seed, at)
+        payload = (data.astype(np.float32) + (d / unit).astype(np.float32)).astype(np.float32)
+        stored = np.floor((payload + draw).astype(np.float32))
+        return np.clip(stored, -127, 127).astype(np.int8)
+    if form == ROWWISE:
+        unit = scale.astype(np.float32).reshape(-1, 1)
+        payload = (e4m3_value(data) + (d / unit).astype(np.float32)).astype(np.float32)
+        return e4m3_stochastic(payload, randint(seed, at))
+    if form == BF16:
+        value = (data.astype(np.uint32) << 16).view(np.float32) + d
+        kept = (value.astype(np.float32).view(np.uint32) + (randint(seed, at) >> 16)) >> 16
+        return kept.astype(np.uint16)
+    if form == F16:
+        value = data.view(np.float16).astype(np.float32) + d
+        return value.astype(np.float16).view(np.uint16)
+    if form == F32:
+        return (data.astype(np.float32) + d).astype(np.float32)
+    raise ValueError(f"no bake form {form}")
+
+
+def bake_nvfp4(data: np.ndarray, blocks: np.ndarray, second: float, up: np.ndarray,
+               down: np.ndarray, seed: int) -> tuple[np.ndarray, np.ndarray]:  # fmt: skip
+    """`_bake_nvfp4_kernel` (`internal/lora_bake.py:955-1011`): canonical nvfp4 codes `[rows,
+    cols/2]` (element 2k in the low nibble) and E4M3 block bytes `[rows, cols/16]`, second level
+    kept. A block's scale is kept unless its baked maximum needs more than 7/6 of it, then the
+    least code that holds it; each element rounds stochastically on its block's grid and a zero
+    keeps its stored sign. Returns the new (codes, blocks)."""
+    rows, cols = data.shape[0], 2 * data.shape[1]
+    level = _F32(second)
+    codes = np.stack((data & 15, data >> 4), axis=-1).reshape(rows, cols).astype(np.int64)
+    scaled = np.repeat(blocks.astype(np.int64), 16, axis=1)
+    d = delta(up.astype(np.float32), down.astype(np.float32))
+    target = fma32(e2m1_value(codes), e4m3_value(scaled) * level, d)
+    need = (np.abs(target).reshape(rows, -1, 16).max(axis=2) / (_F32(6) * level)).astype(np.float32)
+    kept = blocks.astype(np.int64)
+    grown = (need * _F32(6)).astype(np.float32) > (e4m3_value(kept) * _F32(7)).astype(np.float32)
+    block = np.where(grown, e4m3_at_least(need), kept)
+    unit = np.repeat((e4m3_value(block) * level).astype(np.float32), 16, axis=1)
+    payload = (target / np.where(unit > 0, unit, _F32(1))).astype(np.float32)
+    nibble = e2m1_stochastic(payload, rand(seed, _offsets(rows, cols)))
+    negative = np.where(target == 0, codes >= 8, target < 0)
+    nibble = nibble | np.where(negative, 8, 0)
+    packed = (nibble[:, 0::2] | (nibble[:, 1::2] << 4)).astype(np.uint8)
+    return packed, block.astype(np.uint8)

@@ -1,0 +1,547 @@
+"""The LoRA bake (`oracle/bake.py` on the CPU, `csrc/bake.hip` + `cozyq.bake` on the GPU).
+
+CPU: the oracle pinned to things other than itself — Philox's published known-answer vectors,
+Triton's own draws (`tests/golden/philox_vectors.json`), exact rational FMA, brute force over
+the E4M3 / E2M1 grids, the reference's self-check cases (`internal/lora_bake.py:852-898`),
+rank-0 identity and the expectation of stochastic rounding. GPU: every form bit-exact against
+the oracle over ragged shapes, ranks and seeds, through the C ABI and the host mirror.
+"""
+
+from __future__ import annotations
+
+import json
+import random
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bake as ob
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+CUDA = "cuda:0"
+
+
+# ----------------------------------------------------------------------------- noise pins
+
+
+@pytest.mark.parametrize("key,counter,want", [
+    (0, (0, 0, 0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((1 << 64) - 1, (0xFFFFFFFF,) * 4, (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    (0x299F31D0A4093822, (0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+])  # fmt: skip
+def test_philox_known_answers(key, counter, want):
+    """Random123's published philox4x32-10 known-answer vectors."""
+    got = ob.philox(key, *(np.array([c], dtype=np.uint64) for c in counter))
+    assert tuple(int(v[0]) for v in got) == want
+
+
+def test_noise_matches_tritons_draws():
+    data = json.loads((GOLDEN / "philox_vectors.json").read_text())
+    for case in data["cases"]:
+        offsets = np.array(case["offsets"], dtype=np.uint64)
+        assert ob.randint(case["seed"], offsets).tolist() == case["randint"], case["seed"]
+        bits = ob.rand(case["seed"], offsets).view(np.uint32).tolist()
+        assert bits == case["rand_bits"], case["seed"]
+        assert (ob.rand(case["seed"], offsets) < 1).all()
+
+
+# ----------------------------------------------------------------------------- exact FMA
+
+
+def _round_f32(x: Fraction) -> float:
+    """Exact rational → nearest float32 (ties to even), by integer arithmetic."""
+    if x == 0:
+        return 0.0
+    sign, x = (-1.0 if x < 0 else 1.0), abs(x)
+    e = x.numerator.bit_length() - x.denominator.bit_length()
+    while Fraction(2) ** e > x:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= x:
+        e += 1
+    quantum = Fraction(2) ** (max(e, -126) - 23)
+    q, r = divmod(x, quantum)
+    q = int(q)
+    if r * 2 > quantum or (r * 2 == quantum and q % 2 == 1):
+        q += 1
+    return sign * float(np.float32(float(q * quantum)))
+
+
+def test_fma32_is_correctly_rounded():
+    rng = random.Random(11)
+    a, b, c = [], [], []
+    for _ in range(3000):
+        x = np.float32(rng.uniform(-4, 4) * 2.0 ** rng.randint(-30, 30))
+        y = np.float32(rng.uniform(-4, 4) * 2.0 ** rng.randint(-30, 30))
+        a.append(x)
+        b.append(y)
+        # Constructed near-ties: c cancels the product's top, so its low bits decide.
+        p = float(x) * float(y)
+        choice = rng.randrange(4)
+        if choice == 0:
+            c.append(np.float32(-p))
+        elif choice == 1:
+            c.append(np.float32(-p * (1 + 2.0**-24)))
+        elif choice == 2:
+            c.append(np.float32(p * 2.0**-25))
+        else:
+            c.append(np.float32(rng.uniform(-4, 4) * 2.0 ** rng.randint(-40, 40)))
+    # (1 + 2^-12)^2 - 1: the unfused form loses the 2^-24 term.
+    a.append(np.float32(1 + 2.0**-12))
+    b.append(np.float32(1 + 2.0**-12))
+    c.append(np.float32(-1))
+    a, b, c = (np.array(v, dtype=np.float32) for v in (a, b, c))
+    got = ob.fma32(a, b, c)
+    for i in range(len(a)):
+        want = _round_f32(Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i])))
+        assert float(got[i]) == want, (a[i], b[i], c[i])
+    assert float(got[-1]) == 2.0**-11 + 2.0**-24
+
+
+# ----------------------------------------------------------------------------- grids
+
+
+def _e4m3_magnitudes() -> np.ndarray:
+    return ob.e4m3_value(np.arange(127))
+
+
+def test_e4m3_value_against_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = ob.e4m3_value(codes)
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite], want[finite])
+    assert got[127] == 448 and got[255] == -448
+
+
+def test_e4m3_stochastic_neighbours():
+    """Every grid value rounds to itself under any noise; between two neighbours the result is
+    one of them, the upper exactly when the noise's top twenty bits exceed the covered part."""
+    mags = _e4m3_magnitudes()
+    noise = np.array([0, 1 << 12, 0x7FFFFFFF, 0xFFFFFFFF, 0x12345678], dtype=np.uint32)
+    for code in range(127):
+        for sign in (1, -1):
+            got = ob.e4m3_stochastic(np.full(noise.shape, sign * mags[code], np.float32), noise)
+            want = code | (128 if sign < 0 and mags[code] != 0 else 0)
+            assert (got == want).all(), (code, sign)
+    rng = np.random.default_rng(3)
+    for low in range(126):
+        frac = rng.random(64).astype(np.float32)
+        x = (mags[low] + frac * (mags[low + 1] - mags[low])).astype(np.float32)
+        draws = rng.integers(0, 1 << 32, 64, dtype=np.uint64).astype(np.uint32)
+        got = ob.e4m3_stochastic(x, draws).astype(np.int64)
+        assert set(got.tolist()) <= {low, low + 1}
+        # The covered part in units of 2^-20 of a step, against the noise's top 20 bits.
+        step = np.float64(mags[low + 1]) - np.float64(mags[low])
+        covered = np.floor((x.astype(np.float64) - mags[low]) / step * (1 << 20) + 1e-9)
+        up = (draws >> 12).astype(np.float64) + covered >= (1 << 20)
+        assert np.array_equal(got == low + 1, up), low
+    assert ob.e4m3_stochastic(np.float32([1e6, -1e6, 448.5]), np.uint32([0xFFFFFFFF] * 3)).tolist() == [126, 254, 126]
+
+
+def test_e4m3_at_least_is_the_least_holding_code():
+    mags = _e4m3_magnitudes()
+    rng = np.random.default_rng(5)
+    need = np.concatenate([mags, mags * np.float32(1 + 2**-20), rng.random(4000).astype(np.float32) * 500,
+                           rng.random(1000).astype(np.float32) * 0.02, [0.0]]).astype(np.float32)  # fmt: skip
+    got = ob.e4m3_at_least(need)
+    want = np.minimum(np.searchsorted(mags, need, side="left"), 126)
+    assert np.array_equal(got, want)
+
+
+def test_e2m1_value_and_stochastic():
+    assert ob.e2m1_value(np.arange(16)).tolist() == [0, .5, 1, 1.5, 2, 3, 4, 6, -0.0, -.5, -1, -1.5, -2, -3, -4, -6]
+    grid = ob.e2m1_value(np.arange(8))
+    for code in range(8):
+        for draw in (0.0, 0.5, 0.999):
+            assert int(ob.e2m1_stochastic(np.float32([grid[code]]), np.float32([draw]))[0]) == code
+    rng = np.random.default_rng(6)
+    for low in range(7):
+        x = (grid[low] + rng.random(200) * (grid[low + 1] - grid[low])).astype(np.float32)
+        draw = rng.random(200).astype(np.float32)
+        got = ob.e2m1_stochastic(x, draw)
+        frac = (x - grid[low]) / (grid[low + 1] - grid[low])
+        assert np.array_equal(got, low + (draw < frac)), low
+    assert ob.e2m1_stochastic(np.float32([7.0, -100.0]), np.float32([0.0, 0.9])).tolist() == [7, 7]
+
+
+# ----------------------------------------------------------------------------- bakes
+
+
+def _probe_factors(rows: int = 70, rank: int = 24, cols: int = 96):
+    up = np.full((rows, rank), 1 / 32, dtype=np.float32)
+    up[1::2] = -1 / 32
+    return up, np.ones((rank, cols), dtype=np.float32)
+
+
+def _want(rows: int, cols: int) -> np.ndarray:
+    return np.tile(np.float32([[1.0], [-0.5]]), (rows // 2, cols))
+
+
+def _bf16_bits(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def _decode(form: int, data: np.ndarray, scale=None) -> np.ndarray:
+    if form == ob.BF16:
+        return (data.astype(np.uint32) << 16).view(np.float32)
+    if form == ob.F16:
+        return data.view(np.float16).astype(np.float32)
+    if form == ob.ROWWISE:
+        return ob.e4m3_value(data) * scale.reshape(-1, 1)
+    if form == ob.INT8:
+        return data.astype(np.float32) * scale.reshape(-1, 1)
+    return data.astype(np.float32)
+
+
+@pytest.mark.parametrize("form", [ob.BF16, ob.F16, ob.F32, ob.ROWWISE])
+def test_reference_self_check_cases(form):
+    """`probe`: 0.25 + 24·(±1/32) is 1.0 or −0.5 on every grid, over partial tiles."""
+    rows, cols = 70, 96
+    up, down = _probe_factors()
+    if form == ob.ROWWISE:
+        data = np.full((rows, cols), 0x30, dtype=np.uint8)  # E4M3 0.5
+        scale = np.full(rows, 0.5, dtype=np.float32)
+    else:
+        quarter = np.full((rows, cols), 0.25, dtype=np.float32)
+        data = {ob.BF16: _bf16_bits(quarter), ob.F16: quarter.astype(np.float16).view(np.uint16),
+                ob.F32: quarter}[form]  # fmt: skip
+        scale = None
+    out = ob.bake(form, data, scale, up, down, form)
+    assert np.array_equal(_decode(form, out, scale), _want(rows, cols))
+
+
+def test_reference_self_check_nvfp4_and_int8():
+    rows, cols = 70, 96
+    up, down = _probe_factors()
+    codes, blocks = ob.bake_nvfp4(np.full((rows, cols // 2), 0x11, np.uint8),
+                                  np.full((rows, cols // 16), 0x30, np.uint8), 1.0, up, down, 5)  # fmt: skip
+    assert (blocks == 0x30).all()
+    nib = np.stack((codes & 15, codes >> 4), -1).reshape(rows, cols)
+    assert np.array_equal(ob.e2m1_value(nib) * 0.5, _want(rows, cols))
+    # int8 of rotated rows: 2 + 24·(±1/48)/0.5 is 3 or 1; H keeps a constant row.
+    ones = np.ones((24, 256), dtype=np.float32)
+    assert np.array_equal(ob.rotate_factor(ones), ones)
+    out = ob.bake(ob.INT8, np.full((rows, 256), 2, np.int8), np.full(rows, 0.5, np.float32),
+                  up * np.float32(32 / 48), ob.rotate_factor(ones), 4)  # fmt: skip
+    assert np.array_equal(out, np.tile(np.int8([[3], [1]]), (rows // 2, 256)))
+
+
+def test_rotate_factor_is_orthonormal():
+    rng = np.random.default_rng(8)
+    x = rng.integers(-50, 50, (3, 512)).astype(np.float32)
+    assert np.array_equal(ob.rotate_factor(ob.rotate_factor(x)), x)
+    y = rng.standard_normal((4, 768)).astype(np.float32)
+    r = ob.rotate_factor(y)
+    np.testing.assert_allclose(np.linalg.norm(r, axis=1), np.linalg.norm(y, axis=1), rtol=1e-5)
+
+
+def _random_stored(form: int, rows: int, cols: int, rng):
+    w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+    if form == ob.BF16:
+        return _bf16_bits(w), None
+    if form == ob.F16:
+        return w.astype(np.float16).view(np.uint16), None
+    if form == ob.F32:
+        return w, None
+    # Headroom under the grid's top (448, 127) so that a small delta never saturates.
+    scale = (np.abs(w).max(axis=1) / (400.0 if form == ob.ROWWISE else 110.0)).astype(np.float32)
+    if form == ob.ROWWISE:
+        data = torch.from_numpy(w / scale[:, None]).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        return data, scale
+    return np.clip(np.rint(w / scale[:, None]), -127, 127).astype(np.int8), scale
+
+
+@pytest.mark.parametrize("form", [ob.BF16, ob.F16, ob.F32, ob.ROWWISE, ob.INT8])
+def test_rank_zero_writes_every_byte_back(form):
+    rng = np.random.default_rng(form)
+    data, scale = _random_stored(form, 9, 40, rng)
+    if form == ob.ROWWISE:
+        data[0, :4] = [0x7F, 0xFF, 0x80, 0x00]  # reserved codes saturate; −0 becomes +0
+    out = ob.bake(form, data, scale, np.zeros((9, 0), np.float32), np.zeros((0, 40), np.float32), 3)
+    want = data.copy()
+    if form == ob.ROWWISE:
+        want[0, :4] = [0x7E, 0xFE, 0x00, 0x00]
+    assert np.array_equal(out.view(np.uint8), want.view(np.uint8))
+    codes = rng.integers(0, 256, (9, 16), dtype=np.uint8)
+    blocks = rng.integers(1, 100, (9, 2), dtype=np.uint8)
+    got = ob.bake_nvfp4(codes, blocks, 0.01, np.zeros((9, 0), np.float32), np.zeros((0, 32), np.float32), 1)
+    assert np.array_equal(got[0], codes) and np.array_equal(got[1], blocks)
+
+
+@pytest.mark.parametrize("form", [ob.BF16, ob.ROWWISE, ob.INT8])
+def test_stochastic_bake_is_unbiased(form):
+    """The mean over seeds of the stored value is the exact target, within the sampling bound."""
+    rng = np.random.default_rng(20 + form)
+    rows, cols, rank = 4, 64, 3
+    data, scale = _random_stored(form, rows, cols, rng)
+    up = (rng.standard_normal((rows, rank)) * 0.01).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    used = ob.rotate_factor(np.pad(down, ((0, 0), (0, 256 - cols)))) if form == ob.INT8 else down
+    if form == ob.INT8:
+        data = np.pad(data, ((0, 0), (0, 256 - cols)))
+    base = _decode(form, data, scale).astype(np.float64)
+    target = base + up.astype(np.float64) @ used.astype(np.float64)
+    seeds = 400
+    total = sum(_decode(form, ob.bake(form, data, scale, up, used, s), scale).astype(np.float64)
+                for s in range(seeds))  # fmt: skip
+    mean = total / seeds
+    # One step of the grid bounds a single draw's error; the mean's spread is ≤ step/(2√seeds).
+    if form == ob.BF16:
+        step = np.abs(target) * 2.0**-7
+    elif form == ob.ROWWISE:
+        step = np.maximum(np.abs(target) * 2.0**-3, 2.0**-9 * scale[:, None])
+    else:
+        step = np.broadcast_to(scale[:, None].astype(np.float64), target.shape)
+    assert (np.abs(mean - target) <= 5 * step / (2 * np.sqrt(seeds)) + 1e-12).all()
+
+
+def test_nvfp4_block_grows_past_seven_sixths():
+    """A block whose baked maximum passes 7/6 of its scale takes the least code that holds it;
+    one under that keeps its scale and saturates."""
+    rows, cols = 2, 16
+    codes = np.full((rows, 8), 0x77, np.uint8)  # every element 6
+    blocks = np.full((rows, 1), 0x38, np.uint8)  # E4M3 1.0
+    up = np.float32([[0.9], [1.5]])  # 6 + 0.9 < 7 (kept); 6 + 1.5 > 7 (grows)
+    down = np.ones((1, cols), np.float32)
+    new_codes, new_blocks = ob.bake_nvfp4(codes, blocks, 1.0, up, down, 9)
+    assert new_blocks[0, 0] == 0x38 and (new_codes[0] == 0x77).all()
+    need = np.float32(7.5) / np.float32(6)
+    grown = int(new_blocks[1, 0])
+    assert grown == int(ob.e4m3_at_least(np.float32([need]))[0])
+    assert ob.e4m3_value(grown) >= need > ob.e4m3_value(grown - 1)
+
+
+def test_f16_rounds_to_nearest():
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((5, 24)) * 0.1).astype(np.float16)
+    up = np.float32(rng.integers(-8, 8, (5, 1))) * np.float32(2.0**-12)
+    down = np.ones((1, 24), np.float32)
+    out = ob.bake(ob.F16, w.view(np.uint16), None, up, down, 0)
+    want = (w.astype(np.float64) + up.astype(np.float64)).astype(np.float16)
+    assert np.array_equal(out.view(np.float16), want)
+
+
+# ----------------------------------------------------------------------------- host surface (CPU)
+
+
+def test_bakeable_mirrors_the_reference_roles():
+    from cozyq import bake as cb
+
+    assert cb.bakeable("plain", {}, {"value": "bf16"})
+    assert not cb.bakeable("plain", {}, {"value": "f8_e4m3fn"})
+    assert cb.bakeable("fp8.rowwise", {}, {"weight": "f8_e4m3fn", "scale": "f32"})
+    assert not cb.bakeable("fp8.rowwise", {}, {"weight": "f8_e4m3fn", "scale": "bf16"})
+    roles = {"weight": "u8", "scale": "f8_e4m3fn", "scale_2": "f32", "input_scale": "f32"}
+    assert cb.bakeable("nvfp4", dict(cb.NVFP4_PARAMS), roles)
+    assert not cb.bakeable("nvfp4", {**cb.NVFP4_PARAMS, "scale_layout": "cublas_128x4"}, roles)
+    assert not cb.bakeable("nvfp4", {"nibble_order": "high_first"}, roles)
+    assert cb.bakeable("int8.convrot", {}, {"weight": "i8", "scale": "f32"})
+    assert cb.bakeable("int8.convrot", {"rotation_size": 256}, {"weight": "i8", "scale": "f32"})
+    assert not cb.bakeable("int8.convrot", {"rotation_size": 64}, {"weight": "i8", "scale": "f32"})
+    assert not cb.bakeable("int8.rowwise", {}, {"weight": "i8", "scale": "f32"})
+
+
+def test_bake_refuses_what_it_does_not_build():
+    from cozyq import bake as cb
+
+    value = torch.zeros(4, 8, dtype=torch.bfloat16)
+    down, up = torch.zeros(2, 8), torch.zeros(4, 2)
+    for kwargs in ({"stats": object()}, {"more": lambda a, b: None}, {"how": "eager"},
+                   {"gain": torch.ones(4)}):  # fmt: skip
+        with pytest.raises(NotImplementedError):
+            cb.bake(torch, {"value": value}, down, up, seed=1, **kwargs)
+    with pytest.raises(ValueError, match="GPU"):
+        cb.bake(torch, {"value": value}, down, up, seed=1)
+    with pytest.raises(NotImplementedError):
+        cb.recipe(False)
+    assert cb.recipe().startswith(cb.VARIANT)
+
+
+# ----------------------------------------------------------------------------- GPU parity
+
+
+def _stored_for(form: int, rows: int, cols: int, seed: int):
+    rng = np.random.default_rng(seed)
+    data, scale = _random_stored(form, rows, cols, rng)
+    if form == ob.INT8:
+        data = np.ascontiguousarray(data)
+    return data, scale, rng
+
+
+def _torch_data(form: int, data: np.ndarray) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(data))
+    return {ob.BF16: lambda: t.view(torch.bfloat16), ob.F16: lambda: t.view(torch.float16),
+            ob.F32: lambda: t, ob.ROWWISE: lambda: t, ob.INT8: lambda: t}[form]()  # fmt: skip
+
+
+def _bytes(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().contiguous().view(torch.uint8).numpy()
+
+
+SHAPES = [(70, 96, 24), (1, 1, 1), (129, 257, 33), (64, 128, 0), (300, 1000, 64), (3, 4, 40)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("form", [ob.BF16, ob.F16, ob.F32, ob.ROWWISE])
+@pytest.mark.parametrize("rows,cols,rank", SHAPES)
+def test_gpu_bake_bit_exact(form, rows, cols, rank):
+    from cozyq import prebuilt
+
+    print(f"bake form={form} rows={rows} cols={cols} rank={rank}", flush=True)
+    data, scale, rng = _stored_for(form, rows, cols, 100 * form + rows)
+    up = (rng.standard_normal((rows, rank)) * 0.02).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    seed = int(rng.integers(0, 1 << 31))
+    want = ob.bake(form, data, scale, up, down, seed)
+    ops = prebuilt.library(0)
+    t = _torch_data(form, data).to(CUDA)
+    s = None if scale is None else torch.from_numpy(scale).to(CUDA)
+    ops.bake(form, t, s, torch.from_numpy(up).to(CUDA), torch.from_numpy(down).to(CUDA), seed)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bytes(t), want.view(np.uint8).reshape(rows, -1))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("form", [ob.BF16, ob.ROWWISE])
+def test_gpu_bake_unaligned_rows_and_high_seed(form):
+    """A data pointer off its four-element alignment takes the element path; a seed with bit 31
+    set keys Philox with the sign-extended word, as an int32 Triton argument does."""
+    from cozyq import prebuilt
+
+    rows, cols, rank = 33, 64, 5
+    data, scale, rng = _stored_for(form, rows, cols + 1, 7 + form)
+    up = (rng.standard_normal((rows, rank)) * 0.02).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    seed = 0x80000123
+    backing = _torch_data(form, data).to(CUDA)
+    view = backing.view(-1)[1 : 1 + rows * cols].view(rows, cols)  # offset by one element
+    host = _bytes(view).view(data.dtype).reshape(rows, cols)
+    want = ob.bake(form, host, scale, up, down, seed)
+    prebuilt.library(0).bake(form, view, None if scale is None else torch.from_numpy(scale).to(CUDA),
+                             torch.from_numpy(up).to(CUDA), torch.from_numpy(down).to(CUDA), seed)  # fmt: skip
+    torch.cuda.synchronize()
+    assert np.array_equal(_bytes(view), want.view(np.uint8).reshape(rows, -1))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols,rank", [(70, 256, 24), (129, 512, 33), (5, 1024, 7), (64, 256, 0)])
+def test_gpu_bake_int8_convrot_bit_exact(rows, cols, rank):
+    from cozyq import bake as cb
+
+    print(f"bake int8 rows={rows} cols={cols} rank={rank}", flush=True)
+    data, scale, rng = _stored_for(ob.INT8, rows, cols, rows + rank)
+    up = (rng.standard_normal((rows, rank)) * 0.02).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    seed = int(rng.integers(0, 1 << 31))
+    rotated = cb.rotate_factor(torch, torch.from_numpy(down).to(CUDA))
+    assert np.array_equal(rotated.cpu().numpy().view(np.uint32), ob.rotate_factor(down).view(np.uint32))
+    want = ob.bake(ob.INT8, data, scale, up, ob.rotate_factor(down), seed)
+    stored = {"weight": torch.from_numpy(data).to(CUDA), "scale": torch.from_numpy(scale).to(CUDA)}
+    cb.bake(torch, stored, torch.from_numpy(down).to(CUDA), torch.from_numpy(up).to(CUDA), seed=seed)
+    torch.cuda.synchronize()
+    assert np.array_equal(stored["weight"].cpu().numpy(), want)
+
+
+def _nvfp4_stored(rows: int, cols: int, rng):
+    codes = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+    blocks = rng.integers(0x20, 0x48, (rows, cols // 16), dtype=np.uint8)  # E4M3 0.125 .. 2.0
+    return codes, blocks
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols,rank,gain", [(70, 96, 24, 0.3), (129, 272, 33, 3.0),
+                                                 (300, 1024, 64, 1.0), (16, 16, 0, 1.0),
+                                                 (65, 144, 1, 20.0)])  # fmt: skip
+def test_gpu_bake_nvfp4_bit_exact(rows, cols, rank, gain):
+    """Codes and block bytes bit-exact against the oracle; `gain` sizes the delta so that some
+    blocks keep their scale and others grow."""
+    from cozyq import bake as cb
+
+    print(f"bake nvfp4 rows={rows} cols={cols} rank={rank}", flush=True)
+    rng = np.random.default_rng(rows * cols + rank)
+    codes, blocks = _nvfp4_stored(rows, cols, rng)
+    second = np.float32(0.03)
+    up = (rng.standard_normal((rows, rank)) * 0.02 * gain).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    seed = int(rng.integers(0, 1 << 31))
+    want_codes, want_blocks = ob.bake_nvfp4(codes, blocks, second, up, down, seed)
+    stored = {"weight": torch.from_numpy(codes).to(CUDA),
+              "scale": torch.from_numpy(blocks).view(torch.float8_e4m3fn).to(CUDA),
+              "scale_2": torch.tensor([second], device=CUDA)}  # fmt: skip
+    cb.bake(torch, stored, torch.from_numpy(down).to(CUDA), torch.from_numpy(up).to(CUDA), seed=seed)
+    torch.cuda.synchronize()
+    assert np.array_equal(stored["scale"].view(torch.uint8).cpu().numpy(), want_blocks)
+    assert np.array_equal(stored["weight"].cpu().numpy(), want_codes)
+    if gain >= 3.0:
+        assert (want_blocks != blocks).any()
+
+
+@pytest.mark.gpu
+def test_gpu_probe_and_conv_flattening():
+    from cozyq import bake as cb
+
+    verdict = cb.probe(torch, torch.device(CUDA))
+    assert verdict.ok, verdict.detail
+    # A 3x3 convolution bakes as a matrix with 9 columns per input channel.
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal((8, 4, 3, 3)) * 0.1).astype(np.float32)
+    down = rng.standard_normal((2, 4, 3, 3)).astype(np.float32)
+    up = (rng.standard_normal((8, 2, 1, 1)) * 0.1).astype(np.float32)
+    want = ob.bake(ob.F32, w.reshape(8, -1), None, up.reshape(8, 2), down.reshape(2, -1), 17)
+    stored = {"value": torch.from_numpy(w).to(CUDA)}
+    cb.bake(torch, stored, torch.from_numpy(down).to(CUDA), torch.from_numpy(up).to(CUDA), seed=17)
+    assert np.array_equal(stored["value"].cpu().numpy().reshape(8, -1), want)
+
+
+@pytest.mark.gpu
+def test_gpu_dora_gain_folds_into_a_row_scale():
+    from cozyq import bake as cb
+
+    rows, cols = 16, 64
+    data, scale, rng = _stored_for(ob.ROWWISE, rows, cols, 3)
+    gain = (rng.random(rows) + 0.5).astype(np.float32)
+    stored = {"weight": torch.from_numpy(data).view(torch.float8_e4m3fn).to(CUDA),
+              "scale": torch.from_numpy(scale).to(CUDA)}  # fmt: skip
+    zero_down, zero_up = torch.zeros(0, cols, device=CUDA), torch.zeros(rows, 0, device=CUDA)
+    cb.bake(torch, stored, zero_down, zero_up, seed=1, gain=torch.from_numpy(gain).to(CUDA))
+    assert np.array_equal(stored["scale"].cpu().numpy(), scale * gain)
+    assert np.array_equal(stored["weight"].view(torch.uint8).cpu().numpy(), data)
+
+
+@pytest.mark.gpu
+def test_gpu_bake_full_size_bf16_properties():
+    """At a 4096 x 4096 weight: each baked value is one of the two bf16 neighbours of its exact
+    target (within one float32 rounding of the delta) and the mean error over 16M elements is
+    centred; a rank-0 bake writes every byte back."""
+    from cozyq import prebuilt
+
+    rows = cols = 4096
+    rank = 32
+    g = torch.Generator(device=CUDA).manual_seed(5)
+    base = (torch.randn(rows, cols, device=CUDA, generator=g) * 0.02).to(torch.bfloat16)
+    up = torch.randn(rows, rank, device=CUDA, generator=g) * 1e-3
+    down = torch.randn(rank, cols, device=CUDA, generator=g)
+    ops = prebuilt.library(0)
+    data = base.clone()
+    ops.bake(ob.BF16, data, None, up, down, 99)
+    delta = up.double() @ down.double()
+    target = base.double() + delta
+    err = data.double() - target
+    # The float32 sum the kernel rounds is within `slack` of the exact target: the FMA chain's
+    # error is relative to Σ|up·down| (rank roundings), the add's to |base|. A bf16 neighbour of
+    # that sum is under one ulp, at most 2^-7 of its magnitude, away.
+    slack = (base.double().abs() + up.double().abs() @ down.double().abs()) * 2.0**-17
+    ulp = (target.abs() + slack) * 2.0**-7
+    excess = err.abs() / (ulp + slack)
+    worst = int(excess.argmax())
+    assert float(excess.max()) <= 1.0, (
+        f"element {worst}: stored {float(data.view(-1)[worst])}, target {float(target.view(-1)[worst])}, "
+        f"base {float(base.view(-1)[worst])}, excess {float(excess.max())}")
+    assert abs(float(err.mean())) < 4 * float(ulp.mean()) / (rows * cols) ** 0.5
+    same = base.clone()
+    ops.bake(ob.BF16, same, None, up[:, :0].contiguous(), down[:0].contiguous(), 99)
+    assert torch.equal(same.view(torch.int16), base.view(torch.int16))
