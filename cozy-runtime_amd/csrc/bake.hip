@@ -86,13 +86,16 @@ __device__ __forceinline__ float e2m1_of(uint32_t code) {
 }
 
 // |payload| (block units, saturating at 6) → E2M1 magnitude code, the upper neighbour when the
-// draw is under the fraction of the step covered.
+// draw is under the fraction of the step covered. The step is 0.5, 1 or 2, so dividing by it is
+// multiplying by 2, 1 or 0.5: exact, and the same float32 results as the division.
 __device__ __forceinline__ uint32_t e2m1_stochastic(float payload, float draw) {
     const float magnitude = __builtin_fminf(__builtin_fabsf(payload), 6.0f);
-    const float step = magnitude < 2.0f ? 0.5f : (magnitude < 4.0f ? 1.0f : 2.0f);
-    const float low = __builtin_fminf(__builtin_floorf(magnitude / step) * step, 6.0f);
+    const bool fine = magnitude < 2.0f, mid = magnitude < 4.0f;
+    const float step = fine ? 0.5f : (mid ? 1.0f : 2.0f);
+    const float per_step = fine ? 2.0f : (mid ? 1.0f : 0.5f);
+    const float low = __builtin_fminf(__builtin_floorf(magnitude * per_step) * step, 6.0f);
     const float index = low < 2.0f ? low * 2.0f : (low < 4.0f ? low + 2.0f : (low < 6.0f ? 6.0f : 7.0f));
-    return static_cast<uint32_t>(index + (draw < (magnitude - low) / step ? 1.0f : 0.0f));
+    return static_cast<uint32_t>(index + (draw < (magnitude - low) * per_step ? 1.0f : 0.0f));
 }
 
 template <int kCtrl>
