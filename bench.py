@@ -110,6 +110,17 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
     ms_step = timer.run(step, steps, warmup)
     ms_gemm = timer.run(gemm, steps, warmup)
     ms_quant = timer.run(quantize, steps, warmup)
+
+    # The same step at the reference's own rotation (256, regular H4^4, the parity-pinned one):
+    # its weight rotated and quantized alike, the same GEMM and epilogue.
+    data256, scale256 = ops.int8_quantize_rot(_weights(torch, n, k, 20261203), 256)
+    dp256, wp256 = data256.data_ptr(), scale256.data_ptr()
+
+    def step256():
+        _check(lib.cozyq_quantize_rot(0, xp, 0, qp, sp, m, k, 256, stream))
+        _check(lib.cozyq_gemm_ex(0, 0, qp, sp, dp256, wp256, bp, op, n, 0, m, n, k, 1, stream))
+
+    ms_step256 = timer.run(step256, steps, warmup // 4)
     ops_count = 2.0 * m * n * k
     gemm_tops = ops_count / (ms_gemm * 1e-3) / 1e12
     traffic_alg = m * k + n * k + m * n * 2 + n * 2 + (m + n) * 4
@@ -119,6 +130,7 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
         "gemm_ms": ms_gemm,
         "quantize_ms": ms_quant,
         "quantize_gbs": (m * k * 2 + m * k + m * 4) / (ms_quant * 1e-3) / 1e9,
+        "rotation256": {"ms_per_step": ms_step256, "tops": ops_count / (ms_step256 * 1e-3) / 1e12},
         "roofline": {
             "bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
             "frac": gemm_tops / PEAK_INT8_TOPS,
@@ -533,10 +545,10 @@ def bench_bake(torch, ops, lib, stream, steps: int) -> dict:
             turn[0] += 1
             if form == cb.NVFP4:
                 _check(lib.cozyq_bake_nvfp4(0, w[0].data_ptr(), w[1].data_ptr(), second.data_ptr(), up.data_ptr(),
-                                            sides.data_ptr(), rows, cols, rank, 77, raw))  # fmt: skip
+                                            sides.data_ptr(), None, None, rows, cols, rank, 77, 0, raw))  # fmt: skip
             else:
                 _check(lib.cozyq_bake(0, form, w.data_ptr(), scale.data_ptr(), up.data_ptr(), sides.data_ptr(),
-                                      rows, cols, rank, 77, raw))  # fmt: skip
+                                      None, None, rows, cols, rank, 77, 0, raw))  # fmt: skip
 
         us = _graph_us(torch, go, 4 * copies, max(4, steps // 8))
         nbytes = 2 * stored + factors
@@ -674,7 +686,7 @@ def main() -> int:
         "decode": decode,
         "phases": {"quantize_ms": c2["quantize_ms"], "quantize_gbs": c2["quantize_gbs"],
                    "gemm_ms": c2["gemm_ms"]},
-        "configs": configs,
+        "configs": {"c2_rotation256": [c2["rotation256"]], **configs},
         "cpu_baseline": baseline,
     }
     print(json.dumps(line))

@@ -18,16 +18,20 @@ Element (row, col)'s noise is Triton's Philox draw at counter `row * cols + col`
 weight's 31-bit seed, and the delta is one float32 FMA chain in rank order, so a bake writes the
 bytes the reference's fused bake writes for the same factors.
 
-Not built: the reference's eager bake (`bake_plain`, `bake_rowwise`, `bake_int8_convrot`,
-`bake_nvfp4` over torch's generator), which serves `Stats`, `refit` / `regrid` grids, nearest and
-feedback rounding, a DoRA gain on plain or nvfp4 rows and LoKr rows (`more`); asking for any of
-them raises NotImplementedError. A DoRA gain on a row-scaled weight folds into its scale, as the
-reference does. Tensors off the GPU raise.
+What the reference bakes eagerly runs on the same kernels: a DoRA gain on plain or nvfp4 rows
+(plain rows times the gain, nvfp4 decoded values times it, then the delta — the eager law's
+roundings), a LoKr's dense rows (`more`, added to the delta; rotated for int8.convrot), `gain_rows`
+(nearest rounding, no delta) and DoRA's row `norms`. Their stochastic bytes are drawn from the
+Philox stream above, where the reference's eager bake draws from torch's generator: the same law
+in distribution, not the same bytes. Not built: `Stats`, the `refit` / `regrid` grids and
+error-feedback rounding (eager-only diagnostics and options `bake` never selects); asking for
+them raises NotImplementedError. Tensors off the GPU raise.
 """
 
 from __future__ import annotations
 
-from collections.abc import Mapping
+from collections.abc import Callable, Mapping, Sequence
+from dataclasses import dataclass
 from typing import Any, NamedTuple
 
 Tensor = Any
@@ -47,6 +51,12 @@ NVFP4_PARAMS = {
 }
 #: The rotation a baked int8.convrot weight carries (`int8-convrot256/1`).
 CONVROT_GROUP = 256
+#: `cozyq_bake`'s flags: round to nearest instead of stochastically; the rows times their gain
+#: alone.
+NEAREST, NO_DELTA = 1, 2
+#: A dense delta's rows `[start, stop)`, float32 `[rows, in]`, added beside `up @ down`
+#: (`internal/lora_bake.py:207`).
+Dense = Callable[[int, int], Tensor]
 
 
 class Verdict(NamedTuple):
@@ -91,17 +101,64 @@ def rotate_factor(torch: Any, down: Tensor) -> Tensor:
     return _ops(down).rotate_factor(down.to(torch.float32).contiguous())
 
 
-def fused(torch: Any, stored: dict[str, Tensor], down: Tensor, up: Tensor, seed: int) -> None:
+@dataclass(frozen=True, slots=True)
+class Kron:
+    """A LoKr term (`internal/lora_bake.py:210-224`): `scale * kron(w1, w2)` (`w1` `[a, b]`,
+    `w2` `[c, d]`), the product's rows `index` (int64 `[out]`, in order). Its rows are expanded
+    with torch on the GPU and added to a bake's delta."""
+
+    w1: Tensor
+    w2: Tensor
+    scale: float
+    index: Tensor
+
+    def __call__(self, start: int, stop: int) -> Tensor:
+        # Row p * c + q of kron(w1, w2) is w1[p] (x) w2[q].
+        at = self.index[start:stop]
+        c = self.w2.shape[0]
+        w1, w2 = self.w1[at // c].float(), self.w2[at % c].float()
+        return (w1[:, :, None] * w2[:, None, :]).flatten(1).mul_(self.scale)
+
+
+def dense(terms: Sequence[Kron]) -> Dense | None:
+    """The sum of `terms`' rows, None for none (`internal/lora_bake.py:227-239`)."""
+    if not terms:
+        return None
+    first, *rest = terms
+
+    def rows(start: int, stop: int) -> Tensor:
+        out = first(start, stop)
+        for term in rest:
+            out.add_(term(start, stop))
+        return out
+
+    return rows
+
+
+def _more_rows(torch: Any, more: Dense | None, rows: int, rotated: bool) -> Tensor | None:
+    if more is None:
+        return None
+    block = more(0, rows).to(torch.float32).contiguous()
+    return rotate_factor(torch, block) if rotated else block
+
+
+def fused(torch: Any, stored: dict[str, Tensor], down: Tensor, up: Tensor, seed: int, *,
+          gain: Tensor | None = None, more: Dense | None = None, flags: int = 0) -> None:  # fmt: skip
     """`bake`, one kernel launch (`internal/lora_bake.py:775-815`): each tile adds its
-    `up @ down` (float32) to the decoded stored values and rounds them back in place."""
+    `up @ down` (float32) to the decoded stored values and rounds them back in place. `gain`
+    (plain and nvfp4 rows), `more` and `flags` are the eager bake's additions."""
     up32 = up.to(torch.float32).contiguous()
     down32 = down.to(torch.float32).contiguous()
+    gain32 = None if gain is None else gain.to(torch.float32).reshape(-1).contiguous()
     if "scale_2" in stored:
         raw = stored["weight"].view(torch.uint8)
         second = stored["scale_2"].to(torch.float32).reshape(1)
+        rows = raw.shape[0]
         _ops(raw).bake_nvfp4(raw, stored["scale"].view(torch.uint8), second, up32, down32,
-                             seed & SEED_MASK)  # fmt: skip
+                             seed & SEED_MASK, gain=gain32, more=_more_rows(torch, more, rows, False),
+                             flags=flags)  # fmt: skip
         return
+    rotated = False
     if "value" in stored:
         data = stored["value"]
         kinds = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}
@@ -110,12 +167,15 @@ def fused(torch: Any, stored: dict[str, Tensor], down: Tensor, up: Tensor, seed:
         kind, scale = kinds[data.dtype], None
     elif stored["weight"].dtype == torch.int8:
         data, scale, kind = stored["weight"], stored["scale"].reshape(-1), INT8
-        down32 = rotate_factor(torch, down32)
+        down32, rotated = rotate_factor(torch, down32), True
     else:
         data, scale, kind = stored["weight"].view(torch.uint8), stored["scale"].reshape(-1), ROWWISE
     if scale is not None and (scale.dtype != torch.float32 or not scale.is_contiguous()):
         raise ValueError("a row-scaled bake keeps a contiguous float32 row scale")
-    _ops(data).bake(kind, data, scale, up32, down32, seed & SEED_MASK)
+    if scale is not None and gain32 is not None:
+        raise ValueError("a row-scaled weight takes its gain in its scale")
+    _ops(data).bake(kind, data, scale, up32, down32, seed & SEED_MASK, gain=gain32,
+                    more=_more_rows(torch, more, data.shape[0], rotated), flags=flags)  # fmt: skip
 
 
 def bake(
@@ -128,25 +188,110 @@ def bake(
     stats: Any = None,
     how: str | None = "fused",
     gain: Tensor | None = None,
-    more: Any = None,
+    more: Dense | None = None,
 ) -> None:
     """Bake `up @ down` into one stored weight by its roles (`internal/lora_bake.py:554-645`):
-    plain floats, `fp8.rowwise`, `int8-convrot256/1` or canonical `nvfp4`. A convolution's weight
-    and factors bake as matrices, each kernel tap one more input column. `gain` (float32 per
-    output row, a DoRA's) on a row-scaled weight multiplies its scale exactly; `seed` names the
-    weight's noise. `down` and `up` may have rank 0."""
+    plain floats, `fp8.rowwise`, `int8-convrot256/1` or canonical `nvfp4`. bf16, E4M3, int8 and
+    E2M1 round stochastically, scales kept; `seed` names the weight's noise. A convolution's
+    weight and factors bake as matrices, each kernel tap one more input column. `gain` (float32
+    per output row, a DoRA's) scales the stored rows first: a row-scaled weight's scale exactly, a
+    plain or nvfp4 one's values, rounded once with the delta. `more` (a LoKr's dense rows,
+    `dense`) adds beside `up @ down`. `how` is accepted for the reference's callers: every bake
+    runs on the HIP kernels. `down` and `up` may have rank 0."""
     if down.dim() > 2:
         stored = {role: t.view(t.shape[0], -1) if t.dim() > 2 else t for role, t in stored.items()}
         down, up = down.flatten(1), up.flatten(1)
     if gain is not None and "value" not in stored and "scale_2" not in stored:
         stored["scale"].view(-1).mul_(gain)
         gain = None
-    if stats is not None or gain is not None or more is not None or how not in ("fused", None):
-        raise NotImplementedError(
-            "cozyq bakes by the fused law only: Stats, a DoRA gain on plain or nvfp4 rows, LoKr "
-            "rows and the eager reference bake are not built"
-        )
-    fused(torch, stored, down, up, seed)
+    if stats is not None:
+        raise NotImplementedError("cozyq's bake keeps no Stats (the reference's eager measurement)")
+    if how not in ("fused", "eager", None):
+        raise ValueError(f"no bake path {how!r}")
+    fused(torch, stored, down, up, seed, gain=gain, more=more)
+
+
+def rotate_rows(torch: Any, rows: Dense) -> Dense:
+    """`rows` in an `int8-convrot256/1` weight's basis, as `rotate_factor` rotates `down`
+    (`internal/lora_bake.py:648-650`)."""
+    return lambda start, stop: rotate_factor(torch, rows(start, stop))
+
+
+def norms(torch: Any, stored: Mapping[str, Tensor], down: Tensor, up: Tensor) -> Tensor:
+    """Each output row's L2 norm of a linear's stored weight plus `up @ down`, float32 `[out]`
+    (`internal/lora_bake.py:653-689`). An `int8-convrot256/1` weight's rows are rotated, and so is
+    the delta: the rotation is orthonormal, so the norm is the unrotated weight's."""
+    up32 = up.to(torch.float32).contiguous()
+    down32 = down.to(torch.float32).contiguous()
+    if "scale_2" in stored:
+        raw = stored["weight"].view(torch.uint8)
+        second = stored["scale_2"].to(torch.float32).reshape(1)
+        return _ops(raw).bake_norms(NVFP4, raw, None, up32, down32, cols=2 * raw.shape[1],
+                                    blocks=stored["scale"].view(torch.uint8), second=second)  # fmt: skip
+    if "value" in stored:
+        value = stored["value"]
+        kind = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}[value.dtype]
+        return _ops(value).bake_norms(kind, value, None, up32, down32, cols=value.shape[1])
+    data, scale = stored["weight"], stored["scale"].reshape(-1).to(torch.float32).contiguous()
+    if data.dtype == torch.int8:
+        return _ops(data).bake_norms(INT8, data, scale, up32, rotate_factor(torch, down32),
+                                     cols=data.shape[1])  # fmt: skip
+    raw = data.view(torch.uint8)
+    return _ops(raw).bake_norms(ROWWISE, raw, scale, up32, down32, cols=raw.shape[1])
+
+
+def dora_ratio(torch: Any, magnitude: Tensor, norm: Tensor) -> Tensor:
+    """`m / ||V||` per output row, float32; 0 where `V`'s row is 0
+    (`internal/lora_bake.py:692-695`)."""
+    tiny = torch.finfo(torch.float32).tiny
+    return torch.where(norm > 0, magnitude.float() / norm.clamp_min(tiny), 0.0)
+
+
+def dora_weight(torch: Any, weight: Tensor, down: Tensor, up: Tensor, magnitude: Tensor,
+                s: float, t: float) -> Tensor:  # fmt: skip
+    """PEFT's DoRA weight at strength `t`, float32 `[out, in]`: `W + t * (m * V / ||V|| - W)`
+    per output row, `V = W + s * B @ A` (`internal/lora_bake.py:698-712`)."""
+    v = weight + (up.float() @ down.float()) * s
+    ratio = dora_ratio(torch, magnitude, torch.linalg.vector_norm(v, dim=1))
+    return weight + (v * ratio[:, None] - weight) * t
+
+
+def dora(torch: Any, stored: Mapping[str, Tensor],
+         terms: list[tuple[Tensor, Tensor, Tensor, float, float]]) -> tuple[Tensor, list[Tensor]]:  # fmt: skip
+    """A stored linear's DoRA terms, each `(A, B, m, s, t)`, as its row gain and each term's B
+    scale (float32 `[out]`, `internal/lora_bake.py:715-730`): `g = 1 + t * (r - 1)` and
+    `c = t * s * r` with `r = m / ||V||`, the norms taken from the stored rows (`norms`)."""
+    gain = torch.ones_like(terms[0][2], dtype=torch.float32)
+    scales = []
+    for down, up, magnitude, s, t in terms:
+        ratio = dora_ratio(torch, magnitude, norms(torch, stored, down, up.float() * s))
+        gain.add_(ratio - 1, alpha=t)
+        scales.append(ratio.mul_(t * s))
+    return gain, scales
+
+
+def gain_rows(torch: Any, stored: dict[str, Tensor], gain: Tensor) -> None:
+    """Each output row of a stored weight times `gain` (float32 `[out]`), in place
+    (`internal/lora_bake.py:733-749`): a row-scaled weight's scale exactly, a plain one's values
+    rounded once to nearest, an nvfp4 one's re-encoded (`bake_nvfp4` with no delta, nearest)."""
+    gain32 = gain.to(torch.float32).reshape(-1).contiguous()
+    if "scale_2" not in stored and "value" not in stored:
+        stored["scale"].view(-1).mul_(gain32)
+        return
+    probe = stored["weight"] if "scale_2" in stored else stored["value"]
+    cols = 2 * probe.shape[1] if "scale_2" in stored else probe.shape[1]
+    down = torch.zeros((0, cols), dtype=torch.float32, device=probe.device)
+    up = torch.zeros((probe.shape[0], 0), dtype=torch.float32, device=probe.device)
+    fused(torch, stored, down, up, 0, gain=gain32, flags=NEAREST | NO_DELTA)
+
+
+def accumulate(torch: Any, x: Tensor, out: Tensor, down: Tensor, up: Tensor, alpha: float) -> None:
+    """`out += alpha * (x @ down.T) @ up.T` in two library GEMMs (`internal/lora_bake.py:
+    752-761`): the up projection adds into the base output, so no `[rows, out]` update is ever
+    allocated."""
+    flat, rows = out.view(-1, out.shape[-1]), x.reshape(-1, x.shape[-1])
+    low = torch.nn.functional.linear(rows, down.to(rows.dtype))
+    flat.addmm_(low.to(flat.dtype), up.to(flat.dtype).t(), alpha=alpha)
 
 
 def recipe(fused: bool = True) -> str:

@@ -629,31 +629,55 @@ class Prebuilt:
     # -------------------------------------------------------------- LoRA bake
 
     def bake(self, form: int, data: Tensor, scale: Tensor | None, up: Tensor, down: Tensor,
-             seed: int) -> None:  # fmt: skip
+             seed: int, *, gain: Tensor | None = None, more: Tensor | None = None,
+             flags: int = 0) -> None:  # fmt: skip
         """`cozyq_bake` in place (`_bake_kernel`, `internal/lora_bake.py:1013-1053`): `data`
         contiguous [rows, cols] of the form, `scale` float32 [rows] (row-scaled forms), `up`
-        float32 [rows, rank], `down` float32 [rank, cols] (int8.convrot: rotated)."""
+        float32 [rows, rank], `down` float32 [rank, cols] (int8.convrot: rotated). `gain`
+        (float32 [rows], plain forms), `more` (float32 [rows, cols]) and `flags` (1 nearest,
+        2 no delta) are the eager bake's additions."""
         rows, cols = (int(v) for v in data.shape)
-        rank = self._factors(up, down, rows, cols, (data,) if scale is None else (data, scale))
+        stored = (data,) if scale is None else (data, scale)
+        rank = self._factors(up, down, rows, cols, stored, gain, more)
         code = self._lib.cozyq_bake(
-            self.index, form, data.data_ptr(), None if scale is None else scale.data_ptr(),
-            up.data_ptr(), down.data_ptr(), rows, cols, rank, seed & 0xFFFFFFFF, self._stream(),
+            self.index, form, data.data_ptr(), _ptr(scale), up.data_ptr(), down.data_ptr(),
+            _ptr(gain), _ptr(more), rows, cols, rank, seed & 0xFFFFFFFF, flags, self._stream(),
         )  # fmt: skip
         self._check(code, "the LoRA bake")
 
     def bake_nvfp4(self, data: Tensor, blocks: Tensor, second: Tensor, up: Tensor, down: Tensor,
-                   seed: int) -> None:  # fmt: skip
+                   seed: int, *, gain: Tensor | None = None, more: Tensor | None = None,
+                   flags: int = 0) -> None:  # fmt: skip
         """`cozyq_bake_nvfp4` in place (`_bake_nvfp4_kernel`, `internal/lora_bake.py:955-1011`):
-        codes uint8 [rows, cols/2], E4M3 block bytes uint8 [rows, cols/16], float32 `second`."""
+        codes uint8 [rows, cols/2], E4M3 block bytes uint8 [rows, cols/16], float32 `second`;
+        `gain`, `more` and `flags` as `bake`'s (the eager `bake_nvfp4`, `:458-525`)."""
         rows, cols = int(data.shape[0]), 2 * int(data.shape[1])
         if tuple(blocks.shape) != (rows, cols // 16) or not blocks.is_contiguous():
             raise ValueError(f"nvfp4 bake: block scales must be contiguous [{rows}, {cols // 16}]")
-        rank = self._factors(up, down, rows, cols, (data, blocks, second))
+        rank = self._factors(up, down, rows, cols, (data, blocks, second), gain, more)
         code = self._lib.cozyq_bake_nvfp4(
             self.index, data.data_ptr(), blocks.data_ptr(), second.data_ptr(), up.data_ptr(),
-            down.data_ptr(), rows, cols, rank, seed & 0xFFFFFFFF, self._stream(),
+            down.data_ptr(), _ptr(gain), _ptr(more), rows, cols, rank, seed & 0xFFFFFFFF, flags,
+            self._stream(),
         )  # fmt: skip
         self._check(code, "the nvfp4 LoRA bake")
+
+    def bake_norms(self, form: int, data: Tensor, scale: Tensor | None, up: Tensor, down: Tensor,
+                   *, cols: int, blocks: Tensor | None = None,
+                   second: Tensor | None = None) -> Tensor:  # fmt: skip
+        """`cozyq_bake_norms` (`norms`, `internal/lora_bake.py:653-689`): each row's L2 norm of
+        the decoded weight plus `up @ down`, float32 [rows]. form 5 is nvfp4 (codes `data`,
+        `blocks`, `second`)."""
+        rows = int(data.shape[0])
+        stored = tuple(t for t in (data, scale, blocks, second) if t is not None)
+        rank = self._factors(up, down, rows, cols, stored)
+        out = self.torch.empty(rows, dtype=self.torch.float32, device=data.device)
+        code = self._lib.cozyq_bake_norms(
+            self.index, form, data.data_ptr(), _ptr(scale), _ptr(blocks), _ptr(second),
+            up.data_ptr(), down.data_ptr(), rows, cols, rank, out.data_ptr(), self._stream(),
+        )  # fmt: skip
+        self._check(code, "the row norms")
+        return out
 
     def rotate_factor(self, down: Tensor) -> Tensor:
         """`cozyq_bake_rotate_factor` (`rotate_factor`, `internal/lora_bake.py:366-369`): float32
@@ -670,11 +694,19 @@ class Prebuilt:
         self._check(code, "the factor rotation")
         return out
 
-    def _factors(self, up: Tensor, down: Tensor, rows: int, cols: int, stored: tuple) -> int:
+    def _factors(self, up: Tensor, down: Tensor, rows: int, cols: int, stored: tuple,
+                 gain: Tensor | None = None, more: Tensor | None = None) -> int:  # fmt: skip
         torch = self.torch
         for t in (up, down):
             if t.dtype != torch.float32 or t.dim() != 2 or not t.is_contiguous():
                 raise ValueError("LoRA bake: factors must be contiguous float32 matrices")
+        if gain is not None and (gain.dtype != torch.float32 or gain.numel() != rows
+                                 or not gain.is_contiguous()):  # fmt: skip
+            raise ValueError(f"LoRA bake: gain must be contiguous float32 with {rows} values")
+        if more is not None and (more.dtype != torch.float32 or tuple(more.shape) != (rows, cols)
+                                 or not more.is_contiguous()):  # fmt: skip
+            raise ValueError(f"LoRA bake: dense rows must be contiguous float32 [{rows}, {cols}]")
+        stored = stored + tuple(t for t in (gain, more) if t is not None)
         rank = int(up.shape[1])
         if int(up.shape[0]) != rows or tuple(down.shape) != (rank, cols):
             raise ValueError(f"LoRA bake: up must be [{rows}, rank] and down [rank, {cols}]; got "

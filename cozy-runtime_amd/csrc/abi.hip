@@ -424,9 +424,18 @@ static bool bake_shape(int64_t rows, int64_t cols, int64_t rank) {
            rank <= 0x7fffffff && rows * cols <= (int64_t{1} << 40);
 }
 
+// A bake's options: gain only for plain and nvfp4 rows (a row-scaled weight takes it in its
+// scale), known flags only.
+static bool bake_options(int form, const float* gain, int flags) {
+    if (flags & ~(cozyq::kBakeNearest | cozyq::kBakeNoDelta)) return false;
+    return !gain || form <= cozyq::kBakeF32 || form == cozyq::kBakeNvfp4;
+}
+
 int cozyq_bake(int device, int form, void* data, const float* scale, const float* up, const float* down,
-               int64_t rows, int64_t cols, int64_t rank, uint32_t seed, void* stream) {
-    if (form < cozyq::kBakeBf16 || form > cozyq::kBakeInt8 || !bake_shape(rows, cols, rank))
+               const float* gain, const float* more, int64_t rows, int64_t cols, int64_t rank, uint32_t seed,
+               int flags, void* stream) {
+    if (form < cozyq::kBakeBf16 || form > cozyq::kBakeInt8 || !bake_shape(rows, cols, rank) ||
+        !bake_options(form, gain, flags))
         return hipErrorInvalidValue;
     if (rows == 0 || cols == 0) return hipSuccess;
     const bool scaled = form == cozyq::kBakeRowwise || form == cozyq::kBakeInt8;
@@ -435,19 +444,38 @@ int cozyq_bake(int device, int form, void* data, const float* scale, const float
     if (reinterpret_cast<uintptr_t>(data) % size) return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
-    return cozyq::bake(form, data, scale, up, down, static_cast<int>(rows), static_cast<int>(cols),
-                       static_cast<int>(rank), seed, on(stream));
+    return cozyq::bake(form, data, scale, up, down, cozyq::BakeOptions{gain, more, flags}, static_cast<int>(rows),
+                       static_cast<int>(cols), static_cast<int>(rank), seed, on(stream));
 }
 
 int cozyq_bake_nvfp4(int device, uint8_t* data, uint8_t* blocks, const float* second, const float* up,
-                     const float* down, int64_t rows, int64_t cols, int64_t rank, uint32_t seed, void* stream) {
-    if (!bake_shape(rows, cols, rank) || cols % 16) return hipErrorInvalidValue;
+                     const float* down, const float* gain, const float* more, int64_t rows, int64_t cols,
+                     int64_t rank, uint32_t seed, int flags, void* stream) {
+    if (!bake_shape(rows, cols, rank) || cols % 16 || !bake_options(cozyq::kBakeNvfp4, gain, flags))
+        return hipErrorInvalidValue;
     if (rows == 0 || cols == 0) return hipSuccess;
     if (!data || !blocks || !second || (rank > 0 && (!up || !down))) return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
-    return cozyq::bake_nvfp4(data, blocks, second, up, down, static_cast<int>(rows), static_cast<int>(cols),
-                             static_cast<int>(rank), seed, on(stream));
+    return cozyq::bake_nvfp4(data, blocks, second, up, down, cozyq::BakeOptions{gain, more, flags},
+                             static_cast<int>(rows), static_cast<int>(cols), static_cast<int>(rank), seed, on(stream));
+}
+
+int cozyq_bake_norms(int device, int form, const void* data, const float* scale, const uint8_t* blocks,
+                     const float* second, const float* up, const float* down, int64_t rows, int64_t cols,
+                     int64_t rank, float* out, void* stream) {
+    if (form < cozyq::kBakeBf16 || form > cozyq::kBakeNvfp4 || !bake_shape(rows, cols, rank) ||
+        (form == cozyq::kBakeNvfp4 && cols % 16))
+        return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    const bool scaled = form == cozyq::kBakeRowwise || form == cozyq::kBakeInt8;
+    if (!out || (cols > 0 && !data) || (scaled && !scale) || (form == cozyq::kBakeNvfp4 && (!blocks || !second)) ||
+        (rank > 0 && cols > 0 && (!up || !down)))
+        return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::bake_norms(form, data, scale, blocks, second, up, down, static_cast<int>(rows),
+                             static_cast<int>(cols), static_cast<int>(rank), out, on(stream));
 }
 
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n) {

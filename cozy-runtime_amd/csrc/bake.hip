@@ -154,37 +154,93 @@ template <> struct Stored<kBakeF32> { using T = float; };
 template <> struct Stored<kBakeRowwise> { using T = uint8_t; };
 template <> struct Stored<kBakeInt8> { using T = int8_t; };
 
+// The nearest E4M3 byte of a payload, saturating at 448, ties to the even code; the sign bit is
+// set for a negative payload only (so −0 stores +0), as the reference's nearest encoder does.
+__device__ __forceinline__ uint32_t e4m3_nearest(float payload) {
+    const uint32_t code = e4m3_rn(__builtin_fminf(__builtin_fabsf(payload), 448.0f));
+    return payload < 0.0f ? (code | 128u) : code;
+}
+
+// |payload| (block units, saturating at 6) → the nearest E2M1 magnitude code, ties to the even
+// code.
+__device__ __forceinline__ uint32_t e2m1_nearest(float payload) {
+    const float magnitude = __builtin_fminf(__builtin_fabsf(payload), 6.0f);
+    const bool fine = magnitude < 2.0f, mid = magnitude < 4.0f;
+    const float step = fine ? 0.5f : (mid ? 1.0f : 2.0f);
+    const float per_step = fine ? 2.0f : (mid ? 1.0f : 0.5f);
+    const float low = __builtin_fminf(__builtin_floorf(magnitude * per_step) * step, 6.0f);
+    const float index = low < 2.0f ? low * 2.0f : (low < 4.0f ? low + 2.0f : (low < 6.0f ? 6.0f : 7.0f));
+    const float fraction = (magnitude - low) * per_step;
+    const uint32_t base = static_cast<uint32_t>(index);
+    return base + ((fraction > 0.5f || (fraction == 0.5f && (base & 1u))) ? 1u : 0u);
+}
+
+// What a bake takes beyond the fused law (the reference's eager bake and `gain_rows`): a float32
+// gain per row for plain and nvfp4 rows, dense float32 rows added to the delta (a LoKr's), and
+// the flags kBakeNearest (round to nearest instead of stochastically) and kBakeNoDelta (the
+// rows times their gain alone, no delta added).
+struct Extra {
+    const float* gain;
+    const float* more;
+    bool nearest, no_delta;
+};
+
 // One element of a `_bake_kernel` form: the stored value (its bits), the delta, the row's unit
-// (ROWWISE, INT8) and the element's Philox counter → the new stored value.
-template <int kForm>
+// (ROWWISE, INT8) or gain (plain, with kExtra), and the element's Philox counter → the new stored
+// value. Without kExtra this is the fused law exactly; with it, plain rows are
+// round(round(v·gain) + delta) and every form can round to nearest.
+template <int kForm, bool kExtra>
 __device__ __forceinline__ typename Stored<kForm>::T bake_one(typename Stored<kForm>::T v, float d, float unit,
-                                                               uint32_t at, uint32_t k0, uint32_t k1) {
-    if constexpr (kForm == kBakeBf16) {
-        const float value = float_of(static_cast<uint32_t>(v) << 16) + d;
-        const uint32_t noise = philox_word(at, k0, k1);
-        return static_cast<uint16_t>((bits_of(value) + (noise >> 16)) >> 16);
-    } else if constexpr (kForm == kBakeF16) {
-        return narrow<true>(widen<true>(v) + d);
-    } else if constexpr (kForm == kBakeF32) {
-        return v + d;
+                                                               const Extra& x, uint32_t at, uint32_t k0, uint32_t k1) {
+    if constexpr (kForm == kBakeBf16 || kForm == kBakeF16 || kForm == kBakeF32) {
+        float value;
+        if constexpr (kForm == kBakeBf16) value = float_of(static_cast<uint32_t>(v) << 16);
+        else if constexpr (kForm == kBakeF16) value = widen<true>(v);
+        else value = v;
+        if constexpr (kExtra) {
+            value = value * unit;  // the row's gain (1 without one: exact)
+            if (!x.no_delta) value = value + d;
+        } else {
+            value = value + d;
+        }
+        if constexpr (kForm == kBakeBf16) {
+            if (kExtra && x.nearest) return bf16_rn(value);
+            const uint32_t noise = philox_word(at, k0, k1);
+            return static_cast<uint16_t>((bits_of(value) + (noise >> 16)) >> 16);
+        } else if constexpr (kForm == kBakeF16) {
+            return narrow<true>(value);
+        } else {
+            return value;
+        }
     } else if constexpr (kForm == kBakeRowwise) {
-        const float payload = e4m3_sat(v) + d / unit;
+        const float payload = kExtra && x.no_delta ? e4m3_sat(v) : e4m3_sat(v) + d / unit;
+        if (kExtra && x.nearest) return static_cast<uint8_t>(e4m3_nearest(payload));
         return static_cast<uint8_t>(e4m3_stochastic(payload, philox_word(at, k0, k1)));
     } else {
-        const float draw = uniform(philox_word(at, k0, k1));
-        const float stored = __builtin_floorf((static_cast<float>(v) + d / unit) + draw);
+        const float payload = kExtra && x.no_delta ? static_cast<float>(v) : static_cast<float>(v) + d / unit;
+        const float stored = kExtra && x.nearest ? __builtin_rintf(payload)
+                                                 : __builtin_floorf(payload + uniform(philox_word(at, k0, k1)));
         return static_cast<int8_t>(__builtin_fminf(__builtin_fmaxf(stored, -127.0f), 127.0f));
     }
 }
 
+// The delta of element (row, col) with the dense extra rows added (kExtra and `more` set).
+template <bool kExtra>
+__device__ __forceinline__ float with_more(float d, const Extra& x, int64_t at) {
+    if constexpr (kExtra) {
+        if (x.more) return d + x.more[at];
+    }
+    return d;
+}
+
 // kVec: cols % 4 == 0 and `data` aligned to four elements, so each lane's four-column group
 // moves as one load and one store.
-template <int kForm, bool kVec>
+template <int kForm, bool kVec, bool kExtra>
 __global__ __launch_bounds__(kBakeThreads) void bake_kernel(typename Stored<kForm>::T* __restrict__ data,
                                                             const float* __restrict__ scale,
                                                             const float* __restrict__ up,
-                                                            const float* __restrict__ down, int rows, int cols,
-                                                            int rank, uint32_t seed) {
+                                                            const float* __restrict__ down, Extra x, int rows,
+                                                            int cols, int rank, uint32_t seed) {
     using T = typename Stored<kForm>::T;
     __shared__ float up_lds[kRankChunk][kTileRows];
     __shared__ float down_lds[kRankChunk][kTileCols];
@@ -197,8 +253,11 @@ __global__ __launch_bounds__(kBakeThreads) void bake_kernel(typename Stored<kFor
     for (int i = 0; i < 4; ++i) {
         const int row = row0 + 4 * rg + i;
         if (row >= rows) break;
-        const float unit = (kForm == kBakeRowwise || kForm == kBakeInt8) ? scale[row] : 1.0f;
-        T* line = data + static_cast<int64_t>(row) * cols;
+        float unit = 1.0f;
+        if constexpr (kForm == kBakeRowwise || kForm == kBakeInt8) unit = scale[row];
+        else if (kExtra && x.gain) unit = x.gain[row];
+        const int64_t line0 = static_cast<int64_t>(row) * cols;
+        T* line = data + line0;
         const uint32_t line_at = static_cast<uint32_t>(static_cast<uint64_t>(row) * static_cast<uint64_t>(cols));
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -209,13 +268,16 @@ __global__ __launch_bounds__(kBakeThreads) void bake_kernel(typename Stored<kFor
                 Four four = *reinterpret_cast<const Four*>(line + col);
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    four.v[e] = bake_one<kForm>(four.v[e], acc[i][4 * h + e], unit, line_at + col + e, seed, k1);
+                    four.v[e] = bake_one<kForm, kExtra>(four.v[e], with_more<kExtra>(acc[i][4 * h + e], x, line0 + col + e),
+                                                        unit, x, line_at + col + e, seed, k1);
                 *reinterpret_cast<Four*>(line + col) = four;
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     if (col + e < cols)
-                        line[col + e] = bake_one<kForm>(line[col + e], acc[i][4 * h + e], unit, line_at + col + e, seed, k1);
+                        line[col + e] = bake_one<kForm, kExtra>(
+                            line[col + e], with_more<kExtra>(acc[i][4 * h + e], x, line0 + col + e), unit, x,
+                            line_at + col + e, seed, k1);
             }
         }
     }
@@ -224,12 +286,16 @@ __global__ __launch_bounds__(kBakeThreads) void bake_kernel(typename Stored<kFor
 // `_bake_nvfp4_kernel`: codes [rows, cols/2] (element 2k in the low nibble), E4M3 block bytes
 // [rows, cols/16], the float32 second level at `second`; cols % 16 == 0. A 16-column block is
 // the four lanes cg = 4q .. 4q+3 of one half-row, so its maximum is a DPP quad reduction; every
-// lane reaches it (rows or blocks past the end bake zeros and store nothing).
+// lane reaches it (rows or blocks past the end bake zeros and store nothing). Without kExtra the
+// target is fma(e2m1, scale·level, delta), the fused law; with it, the eager law's separate
+// roundings round(round(round(e2m1·(scale·level))·gain) + delta) (`bake_nvfp4`,
+// internal/lora_bake.py:458-525), no delta under kBakeNoDelta, and nearest E2M1 on request.
+template <bool kExtra>
 __global__ __launch_bounds__(kBakeThreads) void bake_nvfp4_kernel(uint8_t* __restrict__ data, uint8_t* __restrict__ blocks,
                                                                   const float* __restrict__ second,
                                                                   const float* __restrict__ up,
-                                                                  const float* __restrict__ down, int rows, int cols,
-                                                                  int rank, uint32_t seed) {
+                                                                  const float* __restrict__ down, Extra x, int rows,
+                                                                  int cols, int rank, uint32_t seed) {
     __shared__ float up_lds[kRankChunk][kTileRows];
     __shared__ float down_lds[kRankChunk][kTileCols];
     const int row0 = blockIdx.y * kTileRows, col0 = blockIdx.x * kTileCols;
@@ -242,6 +308,7 @@ __global__ __launch_bounds__(kBakeThreads) void bake_nvfp4_kernel(uint8_t* __res
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = row0 + 4 * rg + i;
+        const float gain = kExtra && x.gain && row < rows ? x.gain[row] : 1.0f;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int col = col0 + tile_col(cg, 4 * h);
@@ -255,7 +322,15 @@ __global__ __launch_bounds__(kBakeThreads) void bake_nvfp4_kernel(uint8_t* __res
             float peak = 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                target[e] = __builtin_fmaf(e2m1_of((codes >> (4 * e)) & 15u), scaled, acc[i][4 * h + e]);
+                const float value = e2m1_of((codes >> (4 * e)) & 15u);
+                if constexpr (kExtra) {
+                    const float base = (value * scaled) * gain;
+                    const float d = live ? with_more<true>(acc[i][4 * h + e], x, static_cast<int64_t>(row) * cols + col + e)
+                                         : acc[i][4 * h + e];
+                    target[e] = x.no_delta ? base : base + d;
+                } else {
+                    target[e] = __builtin_fmaf(value, scaled, acc[i][4 * h + e]);
+                }
                 peak = __builtin_fmaxf(peak, __builtin_fabsf(target[e]));
             }
             peak = __builtin_fmaxf(peak, dpp_f32<0xB1>(peak));  // quad_perm [1,0,3,2]
@@ -270,7 +345,10 @@ __global__ __launch_bounds__(kBakeThreads) void bake_nvfp4_kernel(uint8_t* __res
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t stored = (codes >> (4 * e)) & 15u;
-                uint32_t nibble = e2m1_stochastic(target[e] / den, uniform(philox_word(at + e, seed, k1)));
+                const float payload = target[e] / den;
+                uint32_t nibble;
+                if (kExtra && x.nearest) nibble = e2m1_nearest(payload);
+                else nibble = e2m1_stochastic(payload, uniform(philox_word(at + e, seed, k1)));
                 const bool negative = target[e] == 0.0f ? stored >= 8u : target[e] < 0.0f;
                 out |= (nibble | (negative ? 8u : 0u)) << (4 * e);
             }
@@ -280,6 +358,65 @@ __global__ __launch_bounds__(kBakeThreads) void bake_nvfp4_kernel(uint8_t* __res
                 if ((cg & 3) == 0) blocks[which] = static_cast<uint8_t>(block);
             }
         }
+    }
+}
+
+// `norms` (internal/lora_bake.py:653-689): each row's L2 norm of the decoded stored weight plus
+// `up @ down`, float32 out [rows]. One workgroup per 64 rows walks every 128-column tile in
+// order, so a row's float64 sum of squares is the same on every call. kForm: a `_bake_kernel`
+// form, or kBakeNvfp4 (codes at `data`, block bytes at `blocks`, level at `second`).
+
+template <int kForm>
+__global__ __launch_bounds__(kBakeThreads) void bake_norms_kernel(const void* __restrict__ data,
+                                                                  const float* __restrict__ scale,
+                                                                  const uint8_t* __restrict__ blocks,
+                                                                  const float* __restrict__ second,
+                                                                  const float* __restrict__ up,
+                                                                  const float* __restrict__ down, int rows, int cols,
+                                                                  int rank, float* __restrict__ out) {
+    __shared__ float up_lds[kRankChunk][kTileRows];
+    __shared__ float down_lds[kRankChunk][kTileCols];
+    const int row0 = blockIdx.x * kTileRows;
+    const int rg = threadIdx.x >> 4, cg = threadIdx.x & 15;
+    double sums[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int col0 = 0; col0 < cols; col0 += kTileCols) {
+        float acc[4][8];
+        tile_delta(acc, up, down, rows, cols, rank, row0, col0, up_lds, down_lds);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = row0 + 4 * rg + i;
+            if (row >= rows) continue;
+            float unit = 1.0f;
+            if constexpr (kForm == kBakeRowwise || kForm == kBakeInt8) unit = scale[row];
+            const int64_t line0 = static_cast<int64_t>(row) * cols;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int col = col0 + tile_col(cg, j);
+                if (col >= cols) continue;
+                const int64_t at = line0 + col;
+                float value;
+                if constexpr (kForm == kBakeBf16) value = widen<false>(static_cast<const uint16_t*>(data)[at]);
+                else if constexpr (kForm == kBakeF16) value = widen<true>(static_cast<const uint16_t*>(data)[at]);
+                else if constexpr (kForm == kBakeF32) value = static_cast<const float*>(data)[at];
+                else if constexpr (kForm == kBakeRowwise) value = e4m3_sat(static_cast<const uint8_t*>(data)[at]) * unit;
+                else if constexpr (kForm == kBakeInt8) value = static_cast<float>(static_cast<const int8_t*>(data)[at]) * unit;
+                else {
+                    const uint32_t byte = static_cast<const uint8_t*>(data)[at >> 1];
+                    const uint32_t code = (col & 1) ? (byte >> 4) : (byte & 15u);
+                    value = e2m1_of(code) * (e4m3_sat(blocks[static_cast<int64_t>(row) * (cols / 16) + col / 16]) * second[0]);
+                }
+                const double t = static_cast<double>(value + acc[i][j]);
+                sums[i] += t * t;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        double v = sums[i];
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off);  // the 16 lanes of a row group
+        const int row = row0 + 4 * rg + i;
+        if (cg == 0 && row < rows) out[row] = static_cast<float>(__builtin_sqrt(v));
     }
 }
 
@@ -312,36 +449,69 @@ __global__ __launch_bounds__(256) void rotate_factor_kernel(const float* __restr
 }
 
 template <int kForm>
-hipError_t launch_bake(void* data, const float* scale, const float* up, const float* down, int rows, int cols,
-                       int rank, uint32_t seed, hipStream_t s) {
+hipError_t launch_bake(void* data, const float* scale, const float* up, const float* down, const BakeOptions& o,
+                       int rows, int cols, int rank, uint32_t seed, hipStream_t s) {
     using T = typename Stored<kForm>::T;
     const dim3 grid((cols + kTileCols - 1) / kTileCols, (rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
     T* d = static_cast<T*>(data);
     const bool vec = cols % 4 == 0 && reinterpret_cast<uintptr_t>(data) % (4 * sizeof(T)) == 0;
-    if (vec) hipLaunchKernelGGL((bake_kernel<kForm, true>), grid, block, 0, s, d, scale, up, down, rows, cols, rank, seed);
-    else hipLaunchKernelGGL((bake_kernel<kForm, false>), grid, block, 0, s, d, scale, up, down, rows, cols, rank, seed);
+    const Extra x{o.gain, o.more, (o.flags & kBakeNearest) != 0, (o.flags & kBakeNoDelta) != 0};
+    const bool extra = o.gain || o.more || o.flags;
+#define COZYQ_BAKE(V, E) hipLaunchKernelGGL((bake_kernel<kForm, V, E>), grid, block, 0, s, d, scale, up, down, x, rows, cols, rank, seed)
+    if (vec) {
+        if (extra) COZYQ_BAKE(true, true); else COZYQ_BAKE(true, false);
+    } else {
+        if (extra) COZYQ_BAKE(false, true); else COZYQ_BAKE(false, false);
+    }
+#undef COZYQ_BAKE
+    return hipGetLastError();
+}
+
+template <int kForm>
+hipError_t launch_norms(const void* data, const float* scale, const uint8_t* blocks, const float* second,
+                        const float* up, const float* down, int rows, int cols, int rank, float* out, hipStream_t s) {
+    const dim3 grid((rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
+    hipLaunchKernelGGL((bake_norms_kernel<kForm>), grid, block, 0, s, data, scale, blocks, second, up, down, rows,
+                       cols, rank, out);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t bake(int form, void* data, const float* scale, const float* up, const float* down, int rows, int cols,
-                int rank, uint32_t seed, hipStream_t s) {
+hipError_t bake(int form, void* data, const float* scale, const float* up, const float* down, const BakeOptions& o,
+                int rows, int cols, int rank, uint32_t seed, hipStream_t s) {
     switch (form) {
-        case kBakeBf16: return launch_bake<kBakeBf16>(data, scale, up, down, rows, cols, rank, seed, s);
-        case kBakeF16: return launch_bake<kBakeF16>(data, scale, up, down, rows, cols, rank, seed, s);
-        case kBakeF32: return launch_bake<kBakeF32>(data, scale, up, down, rows, cols, rank, seed, s);
-        case kBakeRowwise: return launch_bake<kBakeRowwise>(data, scale, up, down, rows, cols, rank, seed, s);
-        case kBakeInt8: return launch_bake<kBakeInt8>(data, scale, up, down, rows, cols, rank, seed, s);
+        case kBakeBf16: return launch_bake<kBakeBf16>(data, scale, up, down, o, rows, cols, rank, seed, s);
+        case kBakeF16: return launch_bake<kBakeF16>(data, scale, up, down, o, rows, cols, rank, seed, s);
+        case kBakeF32: return launch_bake<kBakeF32>(data, scale, up, down, o, rows, cols, rank, seed, s);
+        case kBakeRowwise: return launch_bake<kBakeRowwise>(data, scale, up, down, o, rows, cols, rank, seed, s);
+        case kBakeInt8: return launch_bake<kBakeInt8>(data, scale, up, down, o, rows, cols, rank, seed, s);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const float* up, const float* down,
-                      int rows, int cols, int rank, uint32_t seed, hipStream_t s) {
+                      const BakeOptions& o, int rows, int cols, int rank, uint32_t seed, hipStream_t s) {
     const dim3 grid((cols + kTileCols - 1) / kTileCols, (rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
-    hipLaunchKernelGGL(bake_nvfp4_kernel, grid, block, 0, s, data, blocks, second, up, down, rows, cols, rank, seed);
+    const Extra x{o.gain, o.more, (o.flags & kBakeNearest) != 0, (o.flags & kBakeNoDelta) != 0};
+    if (o.gain || o.more || o.flags)
+        hipLaunchKernelGGL((bake_nvfp4_kernel<true>), grid, block, 0, s, data, blocks, second, up, down, x, rows, cols, rank, seed);
+    else
+        hipLaunchKernelGGL((bake_nvfp4_kernel<false>), grid, block, 0, s, data, blocks, second, up, down, x, rows, cols, rank, seed);
     return hipGetLastError();
+}
+
+hipError_t bake_norms(int form, const void* data, const float* scale, const uint8_t* blocks, const float* second,
+                      const float* up, const float* down, int rows, int cols, int rank, float* out, hipStream_t s) {
+    switch (form) {
+        case kBakeBf16: return launch_norms<kBakeBf16>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
+        case kBakeF16: return launch_norms<kBakeF16>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
+        case kBakeF32: return launch_norms<kBakeF32>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
+        case kBakeRowwise: return launch_norms<kBakeRowwise>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
+        case kBakeInt8: return launch_norms<kBakeInt8>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
+        case kBakeNvfp4: return launch_norms<kBakeNvfp4>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t rotate_factor(const float* down, float* out, int64_t groups, hipStream_t s) {

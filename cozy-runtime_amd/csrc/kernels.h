@@ -151,15 +151,29 @@ hipError_t measure(const void* w, int in_type, const float* d, int64_t total, do
                    double* out, hipStream_t s);
 
 // LoRA bake (bake.hip), in place: the stored forms of the reference's fused bake
-// (internal/lora_bake.py:768) but nvfp4, which has its own entry.
-enum BakeForm { kBakeBf16 = 0, kBakeF16 = 1, kBakeF32 = 2, kBakeRowwise = 3, kBakeInt8 = 4 };
+// (internal/lora_bake.py:768); nvfp4 has its own entry.
+enum BakeForm { kBakeBf16 = 0, kBakeF16 = 1, kBakeF32 = 2, kBakeRowwise = 3, kBakeInt8 = 4, kBakeNvfp4 = 5 };
+// kBakeNearest: round to nearest (ties to even) instead of stochastically; kBakeNoDelta: the
+// rows times their gain alone (`gain_rows`).
+enum BakeFlags { kBakeNearest = 1, kBakeNoDelta = 2 };
+// Beyond the fused law: a float32 gain per row (plain and nvfp4 rows), dense float32 rows
+// [rows, cols] added to the delta, flags. All null / 0: the fused law exactly.
+struct BakeOptions {
+    const float* gain;
+    const float* more;
+    int flags;
+};
 // data [rows, cols] of the form, scale float32 [rows] (kBakeRowwise, kBakeInt8), up float32
 // [rows, rank], down float32 [rank, cols] (kBakeInt8: already rotated), the 32-bit seed.
-hipError_t bake(int form, void* data, const float* scale, const float* up, const float* down, int rows, int cols,
-                int rank, uint32_t seed, hipStream_t s);
+hipError_t bake(int form, void* data, const float* scale, const float* up, const float* down, const BakeOptions& o,
+                int rows, int cols, int rank, uint32_t seed, hipStream_t s);
 // codes [rows, cols/2], E4M3 block bytes [rows, cols/16], second level at `second`; cols % 16 == 0.
 hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const float* up, const float* down,
-                      int rows, int cols, int rank, uint32_t seed, hipStream_t s);
+                      const BakeOptions& o, int rows, int cols, int rank, uint32_t seed, hipStream_t s);
+// Row L2 norms of the decoded weight plus up @ down into out [rows] (float32); form as above,
+// kBakeNvfp4 with `blocks` and `second`.
+hipError_t bake_norms(int form, const void* data, const float* scale, const uint8_t* blocks, const float* second,
+                      const float* up, const float* down, int rows, int cols, int rank, float* out, hipStream_t s);
 // out = each 256-group of down times H256 / 16; `groups` = rank · cols / 256.
 hipError_t rotate_factor(const float* down, float* out, int64_t groups, hipStream_t s);
 

@@ -255,22 +255,39 @@ int cozyq_measure(int device, const void* w, int w_type, const float* decoded, i
  * `scale` [rows] (stochastic, saturating at 448), 4: int8.convrot (`down` already
  * `cozyq_bake_rotate_factor`ed; floor(code + delta/scale + u), clamped to ±127). Element (r, c)'s
  * noise is Philox4x32-10 at counter (r·cols + c mod 2^32, 0, 0, 0) under the key (seed, seed's
- * sign), Triton's `tl.randint` / `tl.rand`; the reference passes seed & 0x7FFFFFFF. data aligned
- * to its element; rows ≤ 65535·64. Errors: hipErrorInvalidValue for a bad form, shape or
- * pointer. */
+ * sign), Triton's `tl.randint` / `tl.rand`; the reference passes seed & 0x7FFFFFFF.
+ * With gain, more and flags null / 0 this is the fused law exactly. The reference's eager bake
+ * (`bake_plain` / `bake_rowwise` / `bake_int8_convrot`, :271-423) and `gain_rows` (:733-749) add:
+ * `gain` float32 [rows] multiplying plain rows first (forms 0-2 only; a row-scaled weight takes
+ * it in its scale), `more` float32 [rows, cols] added to the delta (a LoKr's dense rows; form 4:
+ * rotated like `down`), flags 1 = round to nearest (ties to even) instead of stochastically,
+ * 2 = no delta (the rows times their gain alone). data aligned to its element; rows ≤ 65535·64.
+ * Errors: hipErrorInvalidValue for a bad form, shape, pointer, flag or a gain on forms 3-4. */
 int cozyq_bake(int device, int form, void* data, const float* scale, const float* up,
-               const float* down, int64_t rows, int64_t cols, int64_t rank, uint32_t seed,
-               void* stream);
+               const float* down, const float* gain, const float* more, int64_t rows,
+               int64_t cols, int64_t rank, uint32_t seed, int flags, void* stream);
 
 /* LoRA bake into canonical nvfp4 (reference: `_bake_nvfp4_kernel`, internal/lora_bake.py:
  * 955-1011, `bake_nvfp4` with `keep`): codes [rows, cols/2] (element 2k in the low nibble), E4M3
  * block bytes [rows, cols/16] row-major, float32 second level at `second` (kept). A block keeps
  * its scale unless its baked maximum passes 7/6 of it, then takes the least E4M3 code that holds
  * it; elements round stochastically on the block's E2M1 grid (saturating at 6) with the noise of
- * `cozyq_bake`'s `tl.rand`; a zero keeps its stored sign. cols % 16 == 0. */
+ * `cozyq_bake`'s `tl.rand`; a zero keeps its stored sign. cols % 16 == 0. With gain, more or
+ * flags (as `cozyq_bake`'s) the target follows the eager `bake_nvfp4` (:458-525): the decoded
+ * value times the row's gain, plus the delta, each rounded. */
 int cozyq_bake_nvfp4(int device, uint8_t* data, uint8_t* blocks, const float* second,
-                     const float* up, const float* down, int64_t rows, int64_t cols, int64_t rank,
-                     uint32_t seed, void* stream);
+                     const float* up, const float* down, const float* gain, const float* more,
+                     int64_t rows, int64_t cols, int64_t rank, uint32_t seed, int flags,
+                     void* stream);
+
+/* Each row's L2 norm of a stored weight plus up @ down (reference: `norms`, internal/lora_bake.py:
+ * 653-689, DoRA's ||V||): out float32 [rows]. form as `cozyq_bake`'s, or 5 for nvfp4 (codes at
+ * data, block bytes at `blocks`, level at `second`); form 4 takes `down` rotated. The sum of
+ * squares is float64, in a fixed order. */
+int cozyq_bake_norms(int device, int form, const void* data, const float* scale,
+                     const uint8_t* blocks, const float* second, const float* up,
+                     const float* down, int64_t rows, int64_t cols, int64_t rank, float* out,
+                     void* stream);
 
 /* `down` [rank, cols] in an int8-convrot256/1 weight's basis (reference: `rotate_factor`,
  * internal/lora_bake.py:366-369): each 256 columns times the regular Hadamard H4⊗H4⊗H4⊗H4 in

@@ -202,58 +202,156 @@ def _offsets(rows: int, cols: int) -> np.ndarray:
             + np.arange(cols, dtype=np.uint64)[None, :]) & np.uint64(0xFFFFFFFF)  # fmt: skip
 
 
+def e4m3_nearest(payload) -> np.ndarray:
+    """float32 payload → the nearest E4M3 byte, saturating at 448, ties to the even code, the
+    sign bit for a negative payload only (`_nearest`, `internal/lora_bake.py:156-160`); the
+    magnitude's code by torch's own round-to-nearest-even cast."""
+    payload = np.asarray(payload, dtype=np.float32)
+    magnitude = np.fmin(np.abs(payload), _F32(448))
+    code = torch.from_numpy(np.ascontiguousarray(magnitude)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    return np.where(payload < 0, code | 128, code).astype(np.uint8)
+
+
+def e2m1_nearest(payload) -> np.ndarray:
+    """|payload| → the nearest E2M1 magnitude code, ties to the even code, saturating at 6
+    (`_e2m1` with `nearest`, `internal/lora_bake.py:435-455`), by a search of the eight
+    magnitudes."""
+    magnitude = np.fmin(np.abs(np.asarray(payload, dtype=np.float32)), _F32(6))
+    grid = np.asarray(laws.E2M1_VALUES[:8], dtype=np.float32)
+    low = np.clip(np.searchsorted(grid, magnitude, side="right") - 1, 0, 7)
+    high = np.minimum(low + 1, 7)
+    gap = grid[high] - grid[low]
+    fraction = np.where(gap > 0, (magnitude - grid[low]) / np.where(gap > 0, gap, 1), 0).astype(np.float32)
+    up = (fraction > 0.5) | ((fraction == 0.5) & (low % 2 == 1))
+    return (low + up).astype(np.int64)
+
+
+def _bf16_nearest(value: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(value, dtype=np.float32)).to(torch.bfloat16).view(
+        torch.int16).numpy().view(np.uint16)  # fmt: skip
+
+
 def bake(form: int, data: np.ndarray, scale: np.ndarray | None, up: np.ndarray, down: np.ndarray,
-         seed: int) -> np.ndarray:  # fmt: skip
+         seed: int, *, gain: np.ndarray | None = None, more: np.ndarray | None = None,
+         nearest: bool = False, no_delta: bool = False) -> np.ndarray:  # fmt: skip
     """The new stored data of one `_bake_kernel` form (`internal/lora_bake.py:1013-1053`):
     `data` `[rows, cols]` as stored (bf16 / f16 as uint16 bits, f32, E4M3 or int8 bytes),
     `scale` the float32 row scale of ROWWISE and INT8, `up` float32 `[rows, rank]`, `down`
-    float32 `[rank, cols]` (INT8: already `rotate_factor`ed)."""
+    float32 `[rank, cols]` (INT8: already `rotate_factor`ed).
+
+    The eager bake's additions (`bake_plain`, `bake_rowwise`, `bake_int8_convrot`,
+    `gain_rows`, `:271-423,733-749`): `gain` float32 `[rows]` multiplies plain rows first,
+    `more` float32 `[rows, cols]` adds to the delta, `nearest` rounds to nearest (ties to even)
+    instead of stochastically, `no_delta` leaves the rows times their gain alone. Build law:
+    the row-scaled forms keep the fused order `decode + delta / scale` under them too."""
     rows, cols = data.shape
     d = delta(up.astype(np.float32), down.astype(np.float32))
+    if more is not None:
+        d = (d + more.astype(np.float32)).astype(np.float32)
     at = _offsets(rows, cols)
     if form == INT8:
         unit = scale.astype(np.float32).reshape(-1, 1)
-        draw = rand(seed, at)
-        payload = (data.astype(np.float32) + (d / unit).astype(np.float32)).astype(np.float32)
-        stored = np.floor((payload + draw).astype(np.float32))
+        payload = data.astype(np.float32)
+        if not no_delta:
+            payload = (payload + (d / unit).astype(np.float32)).astype(np.float32)
+        if nearest:
+            stored = np.rint(payload)
+        else:
+            stored = np.floor((payload + rand(seed, at)).astype(np.float32))
         return np.clip(stored, -127, 127).astype(np.int8)
     if form == ROWWISE:
         unit = scale.astype(np.float32).reshape(-1, 1)
-        payload = (e4m3_value(data) + (d / unit).astype(np.float32)).astype(np.float32)
-        return e4m3_stochastic(payload, randint(seed, at))
+        payload = e4m3_value(data)
+        if not no_delta:
+            payload = (payload + (d / unit).astype(np.float32)).astype(np.float32)
+        return e4m3_nearest(payload) if nearest else e4m3_stochastic(payload, randint(seed, at))
     if form == BF16:
-        value = (data.astype(np.uint32) << 16).view(np.float32) + d
-        kept = (value.astype(np.float32).view(np.uint32) + (randint(seed, at) >> 16)) >> 16
+        value = (data.astype(np.uint32) << 16).view(np.float32)
+    elif form == F16:
+        value = data.view(np.float16).astype(np.float32)
+    elif form == F32:
+        value = data.astype(np.float32)
+    else:
+        raise ValueError(f"no bake form {form}")
+    if gain is not None:
+        value = (value * gain.astype(np.float32).reshape(-1, 1)).astype(np.float32)
+    if not no_delta:
+        value = (value + d).astype(np.float32)
+    if form == BF16:
+        if nearest:
+            return _bf16_nearest(value)
+        kept = (value.view(np.uint32) + (randint(seed, at) >> 16)) >> 16
         return kept.astype(np.uint16)
     if form == F16:
-        value = data.view(np.float16).astype(np.float32) + d
         return value.astype(np.float16).view(np.uint16)
-    if form == F32:
-        return (data.astype(np.float32) + d).astype(np.float32)
-    raise ValueError(f"no bake form {form}")
+    return value
 
 
 def bake_nvfp4(data: np.ndarray, blocks: np.ndarray, second: float, up: np.ndarray,
-               down: np.ndarray, seed: int) -> tuple[np.ndarray, np.ndarray]:  # fmt: skip
+               down: np.ndarray, seed: int, *, gain: np.ndarray | None = None,
+               more: np.ndarray | None = None, nearest: bool = False,
+               no_delta: bool = False) -> tuple[np.ndarray, np.ndarray]:  # fmt: skip
     """`_bake_nvfp4_kernel` (`internal/lora_bake.py:955-1011`): canonical nvfp4 codes `[rows,
     cols/2]` (element 2k in the low nibble) and E4M3 block bytes `[rows, cols/16]`, second level
     kept. A block's scale is kept unless its baked maximum needs more than 7/6 of it, then the
     least code that holds it; each element rounds stochastically on its block's grid and a zero
-    keeps its stored sign. Returns the new (codes, blocks)."""
+    keeps its stored sign. Returns the new (codes, blocks).
+
+    With `gain`, `more`, `nearest` or `no_delta` (the eager `bake_nvfp4`, `:458-525`, and
+    `gain_rows`): the target is `round(round(round(e2m1·(scale·level))·gain) + delta)`, each
+    product and sum rounded, and `nearest` rounds E2M1 to nearest (ties to even)."""
     rows, cols = data.shape[0], 2 * data.shape[1]
     level = _F32(second)
     codes = np.stack((data & 15, data >> 4), axis=-1).reshape(rows, cols).astype(np.int64)
     scaled = np.repeat(blocks.astype(np.int64), 16, axis=1)
     d = delta(up.astype(np.float32), down.astype(np.float32))
-    target = fma32(e2m1_value(codes), e4m3_value(scaled) * level, d)
+    if more is not None:
+        d = (d + more.astype(np.float32)).astype(np.float32)
+    scale_level = (e4m3_value(scaled) * level).astype(np.float32)
+    if gain is None and more is None and not nearest and not no_delta:
+        target = fma32(e2m1_value(codes), scale_level, d)
+    else:
+        g = np.ones(rows, np.float32) if gain is None else gain.astype(np.float32)
+        base = ((e2m1_value(codes) * scale_level).astype(np.float32) * g.reshape(-1, 1)).astype(np.float32)
+        target = base if no_delta else (base + d).astype(np.float32)
     need = (np.abs(target).reshape(rows, -1, 16).max(axis=2) / (_F32(6) * level)).astype(np.float32)
     kept = blocks.astype(np.int64)
     grown = (need * _F32(6)).astype(np.float32) > (e4m3_value(kept) * _F32(7)).astype(np.float32)
     block = np.where(grown, e4m3_at_least(need), kept)
     unit = np.repeat((e4m3_value(block) * level).astype(np.float32), 16, axis=1)
     payload = (target / np.where(unit > 0, unit, _F32(1))).astype(np.float32)
-    nibble = e2m1_stochastic(payload, rand(seed, _offsets(rows, cols)))
+    if nearest:
+        nibble = e2m1_nearest(payload)
+    else:
+        nibble = e2m1_stochastic(payload, rand(seed, _offsets(rows, cols)))
     negative = np.where(target == 0, codes >= 8, target < 0)
     nibble = nibble | np.where(negative, 8, 0)
     packed = (nibble[:, 0::2] | (nibble[:, 1::2] << 4)).astype(np.uint8)
     return packed, block.astype(np.uint8)
+
+
+def norms(form: int, data: np.ndarray, scale: np.ndarray | None, up: np.ndarray,
+          down: np.ndarray, *, blocks: np.ndarray | None = None,
+          second: float | None = None) -> np.ndarray:  # fmt: skip
+    """`norms` (`internal/lora_bake.py:653-689`): each row's L2 norm of the decoded stored
+    weight plus `up @ down` — decoded as the eager reference decodes (`value.float()`,
+    `decode_e4m3(code)·scale`, `code·scale`, `e2m1·(e4m3(block)·level)`), the delta added in
+    float32, the squares summed in float64. `form` NVFP4 takes codes `data` and `blocks`."""
+    rows = data.shape[0]
+    if form == NVFP4:
+        cols = 2 * data.shape[1]
+        codes = np.stack((data & 15, data >> 4), axis=-1).reshape(rows, cols)
+        scaled = (e4m3_value(np.repeat(blocks.astype(np.int64), 16, axis=1)) * _F32(second)).astype(np.float32)
+        value = (e2m1_value(codes) * scaled).astype(np.float32)
+    elif form == BF16:
+        value = (data.astype(np.uint32) << 16).view(np.float32)
+    elif form == F16:
+        value = data.view(np.float16).astype(np.float32)
+    elif form == F32:
+        value = data.astype(np.float32)
+    elif form == ROWWISE:
+        value = (e4m3_value(data) * scale.astype(np.float32).reshape(-1, 1)).astype(np.float32)
+    else:
+        value = (data.astype(np.float32) * scale.astype(np.float32).reshape(-1, 1)).astype(np.float32)
+    target = (value + delta(up.astype(np.float32), down.astype(np.float32))).astype(np.float64)
+    return np.sqrt((target * target).sum(axis=1)).astype(np.float32)

@@ -350,15 +350,97 @@ def test_bake_refuses_what_it_does_not_build():
 
     value = torch.zeros(4, 8, dtype=torch.bfloat16)
     down, up = torch.zeros(2, 8), torch.zeros(4, 2)
-    for kwargs in ({"stats": object()}, {"more": lambda a, b: None}, {"how": "eager"},
-                   {"gain": torch.ones(4)}):  # fmt: skip
-        with pytest.raises(NotImplementedError):
+    with pytest.raises(NotImplementedError):
+        cb.bake(torch, {"value": value}, down, up, seed=1, stats=object())
+    with pytest.raises(ValueError, match="no bake path"):
+        cb.bake(torch, {"value": value}, down, up, seed=1, how="triton")
+    for kwargs in ({}, {"how": "eager"}, {"gain": torch.ones(4)}, {"more": lambda a, b: None}):
+        with pytest.raises(ValueError, match="GPU"):
             cb.bake(torch, {"value": value}, down, up, seed=1, **kwargs)
-    with pytest.raises(ValueError, match="GPU"):
-        cb.bake(torch, {"value": value}, down, up, seed=1)
     with pytest.raises(NotImplementedError):
         cb.recipe(False)
     assert cb.recipe().startswith(cb.VARIANT)
+
+
+def test_abi_refuses_bad_bake_options():
+    """Argument checks answer before any device work: a gain on a row-scaled form, unknown
+    flags, nvfp4 columns off the 16-block, an unknown form."""
+    from cozyq import _lib
+
+    lib = _lib.load()
+    bad = lib.cozyq_bake(0, 3, 16, 16, 16, 16, 16, None, 4, 8, 2, 1, 0, None)
+    assert bad != 0
+    assert lib.cozyq_bake(0, 0, 16, None, 16, 16, None, None, 4, 8, 2, 1, 4, None) != 0
+    assert lib.cozyq_bake(0, 6, 16, None, 16, 16, None, None, 4, 8, 2, 1, 0, None) != 0
+    assert lib.cozyq_bake_nvfp4(0, 16, 16, 16, 16, 16, None, None, 4, 24, 2, 1, 0, None) != 0
+    assert lib.cozyq_bake_norms(0, 6, 16, None, None, None, 16, 16, 4, 8, 2, 16, None) != 0
+    assert lib.cozyq_bake_rotate_factor(0, 16, 16, 2, 100, None) != 0
+    # Empty shapes succeed without touching a device.
+    assert lib.cozyq_bake(0, 0, None, None, None, None, None, None, 0, 8, 2, 1, 0, None) == 0
+
+
+def test_nearest_grids_tie_to_even():
+    mags = _e4m3_magnitudes()
+    mids = ((mags[:-1].astype(np.float64) + mags[1:]) / 2).astype(np.float32)
+    got = ob.e4m3_nearest(mids).astype(np.int64)
+    low = np.arange(126)
+    assert np.array_equal(got, np.where(low % 2 == 0, low, low + 1))
+    rng = np.random.default_rng(12)
+    x = (rng.random(5000) * 460).astype(np.float32)
+    near = np.argmin(np.abs(mags[None, :].astype(np.float64) - x[:, None]), axis=1)
+    got = ob.e4m3_nearest(x).astype(np.int64)
+    assert (np.abs(mags[got] - x) <= np.abs(mags[near] - x)).all()
+    assert ob.e4m3_nearest(np.float32([-0.0, -1.0, -500.0])).tolist() == [0, 0xB8, 0xFE]
+    grid = ob.e2m1_value(np.arange(8))
+    mid2 = ((grid[:-1] + grid[1:]) / 2).astype(np.float32)
+    assert ob.e2m1_nearest(mid2).tolist() == [0, 2, 2, 4, 4, 6, 6]
+    assert ob.e2m1_nearest(np.float32([0.2, 0.3, 5.1, 9.0])).tolist() == [0, 1, 7, 7]
+
+
+def test_gain_rows_laws():
+    """`gain_rows` on plain rows is the reference's own line, `value.float() * gain` cast to
+    nearest; on nvfp4 rows a unit gain writes every byte back."""
+    rng = np.random.default_rng(13)
+    w = (rng.standard_normal((6, 40)) * 0.1).astype(np.float32)
+    gain = (rng.random(6) + 0.5).astype(np.float32)
+    bits = _bf16_bits(w)
+    got = ob.bake(ob.BF16, bits, None, np.zeros((6, 0), np.float32), np.zeros((0, 40), np.float32), 0,
+                  gain=gain, nearest=True, no_delta=True)  # fmt: skip
+    want = (torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float() * torch.from_numpy(gain)[:, None]
+            ).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)  # fmt: skip
+    assert np.array_equal(got, want)
+    codes = rng.integers(0, 256, (6, 16), dtype=np.uint8)
+    blocks = rng.integers(0x28, 0x48, (6, 2), dtype=np.uint8)
+    none_r, none_c = np.zeros((6, 0), np.float32), np.zeros((0, 32), np.float32)
+    same = ob.bake_nvfp4(codes, blocks, 0.05, none_r, none_c, 0, gain=np.ones(6, np.float32),
+                         nearest=True, no_delta=True)  # fmt: skip
+    assert np.array_equal(same[0], codes) and np.array_equal(same[1], blocks)
+
+
+@pytest.mark.parametrize("form", [ob.BF16, ob.F16, ob.F32, ob.ROWWISE, ob.INT8, ob.NVFP4])
+def test_norms_against_float64(form):
+    rng = np.random.default_rng(40 + form)
+    rows, cols, rank = 7, 256, 3
+    up = (rng.standard_normal((rows, rank)) * 0.05).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    if form == ob.NVFP4:
+        codes = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+        blocks = rng.integers(0x28, 0x48, (rows, cols // 16), dtype=np.uint8)
+        got = ob.norms(form, codes, None, up, down, blocks=blocks, second=0.02)
+        nib = np.stack((codes & 15, codes >> 4), -1).reshape(rows, cols)
+        s = torch.from_numpy(np.repeat(blocks, 16, axis=1)).view(torch.float8_e4m3fn).double().numpy()
+        base = np.asarray(laws_values(nib), np.float64) * s * 0.02
+    else:
+        data, scale = _random_stored(form, rows, cols, rng)
+        got = ob.norms(form, data, scale, up, down)
+        base = _decode(form, data, scale).astype(np.float64)
+    want = np.linalg.norm(base + up.astype(np.float64) @ down.astype(np.float64), axis=1)
+    np.testing.assert_allclose(got, want, rtol=2e-6)
+
+
+def laws_values(nib: np.ndarray) -> np.ndarray:
+    table = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0.0, -.5, -1, -1.5, -2, -3, -4, -6])
+    return table[nib.astype(np.int64)]
 
 
 # ----------------------------------------------------------------------------- GPU parity
@@ -545,3 +627,179 @@ def test_gpu_bake_full_size_bf16_properties():
     same = base.clone()
     ops.bake(ob.BF16, same, None, up[:, :0].contiguous(), down[:0].contiguous(), 99)
     assert torch.equal(same.view(torch.int16), base.view(torch.int16))
+
+
+# ----------------------------------------------------------------------------- GPU: eager additions
+
+EXTRA = [  # (gain, more, nearest, no_delta)
+    (True, False, False, False), (False, True, False, False), (True, True, True, False),
+    (True, False, True, True), (False, False, True, False),
+]
+
+
+def _extras(rng, rows: int, cols: int, gain: bool, more: bool):
+    g = (rng.random(rows) + 0.5).astype(np.float32) if gain else None
+    m = (rng.standard_normal((rows, cols)) * 0.01).astype(np.float32) if more else None
+    return g, m
+
+
+def _flags(nearest: bool, no_delta: bool) -> int:
+    return (1 if nearest else 0) | (2 if no_delta else 0)
+
+
+def _cuda(a):
+    return None if a is None else torch.from_numpy(a).to(CUDA)
+
+
+# A row-scaled weight takes its gain in its scale: the kernel's gain is for plain rows only.
+OPTION_CASES = [(form, *extra) for form in (ob.BF16, ob.F16, ob.F32, ob.ROWWISE, ob.INT8) for extra in EXTRA
+                if not (extra[0] and form in (ob.ROWWISE, ob.INT8))]  # fmt: skip
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("form,gain,more,nearest,no_delta", OPTION_CASES)
+def test_gpu_bake_options_bit_exact(form, gain, more, nearest, no_delta):
+    """gain (plain rows), dense extra rows, nearest rounding and no-delta through the C ABI,
+    bit-exact against the oracle, on a ragged shape."""
+    from cozyq import prebuilt
+
+    rows, cols, rank = 67, 256 if form == ob.INT8 else 131, 9
+    data, scale, rng = _stored_for(form, rows, cols, 500 + form)
+    up = (rng.standard_normal((rows, rank)) * 0.02).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    g, m = _extras(rng, rows, cols, gain, more)
+    seed = int(rng.integers(0, 1 << 31))
+    want = ob.bake(form, data, scale, up, down, seed, gain=g, more=m, nearest=nearest, no_delta=no_delta)
+    t = _torch_data(form, data).to(CUDA)
+    prebuilt.library(0).bake(form, t, _cuda(scale), _cuda(up), _cuda(down), seed, gain=_cuda(g), more=_cuda(m),
+                             flags=_flags(nearest, no_delta))  # fmt: skip
+    torch.cuda.synchronize()
+    assert np.array_equal(_bytes(t), want.view(np.uint8).reshape(rows, -1))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("gain,more,nearest,no_delta", EXTRA)
+def test_gpu_bake_nvfp4_options_bit_exact(gain, more, nearest, no_delta):
+    from cozyq import prebuilt
+
+    rows, cols, rank = 70, 272, 5
+    rng = np.random.default_rng(71 + 2 * gain + more)
+    codes, blocks = _nvfp4_stored(rows, cols, rng)
+    up = (rng.standard_normal((rows, rank)) * 0.05).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    g, m = _extras(rng, rows, cols, gain, more)
+    if g is not None:
+        g = g * 1.5  # some blocks outgrow their scale
+    seed = int(rng.integers(0, 1 << 31))
+    want = ob.bake_nvfp4(codes, blocks, 0.03, up, down, seed, gain=g, more=m, nearest=nearest, no_delta=no_delta)
+    c, b = torch.from_numpy(codes).to(CUDA), torch.from_numpy(blocks).to(CUDA)
+    prebuilt.library(0).bake_nvfp4(c, b, torch.tensor([0.03], device=CUDA), _cuda(up), _cuda(down), seed,
+                                   gain=_cuda(g), more=_cuda(m), flags=_flags(nearest, no_delta))  # fmt: skip
+    torch.cuda.synchronize()
+    assert np.array_equal(b.cpu().numpy(), want[1])
+    assert np.array_equal(c.cpu().numpy(), want[0])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("form", [ob.BF16, ob.F16, ob.F32, ob.ROWWISE, ob.INT8, ob.NVFP4])
+def test_gpu_norms_against_the_oracle(form):
+    """`norms` through the host mirror: float64 sums in a fixed order, so equal to the oracle's
+    within float64 reassociation, and the same bits on every call."""
+    from cozyq import bake as cb
+
+    rng = np.random.default_rng(90 + form)
+    rows, cols, rank = 131, 512, 7
+    up = (rng.standard_normal((rows, rank)) * 0.05).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    if form == ob.NVFP4:
+        codes, blocks = _nvfp4_stored(rows, cols, rng)
+        want = ob.norms(form, codes, None, up, down, blocks=blocks, second=0.02)
+        stored = {"weight": torch.from_numpy(codes).to(CUDA),
+                  "scale": torch.from_numpy(blocks).view(torch.float8_e4m3fn).to(CUDA),
+                  "scale_2": torch.tensor([0.02], device=CUDA)}  # fmt: skip
+    else:
+        data, scale, _ = _stored_for(form, rows, cols, 91 + form)
+        used = ob.rotate_factor(down) if form == ob.INT8 else down
+        want = ob.norms(form, data, scale, up, used)
+        t = _torch_data(form, data).to(CUDA)
+        if form in (ob.BF16, ob.F16, ob.F32):
+            stored = {"value": t}
+        else:
+            weight = t.view(torch.float8_e4m3fn) if form == ob.ROWWISE else t
+            stored = {"weight": weight, "scale": torch.from_numpy(scale).to(CUDA)}
+    got = cb.norms(torch, stored, _cuda(down), _cuda(up))
+    again = cb.norms(torch, stored, _cuda(down), _cuda(up))
+    assert torch.equal(got, again)
+    np.testing.assert_allclose(got.cpu().numpy(), want, rtol=1e-6)
+
+
+@pytest.mark.gpu
+def test_gpu_dora_and_gain_rows_through_the_mirror():
+    """`dora` as PEFT's merged weight: with t = 1, baking `c·B @ A` after `gain_rows(g)` lands
+    within bf16 rounding of `dora_weight` (float64 reference), for a plain bf16 weight."""
+    from cozyq import bake as cb
+
+    rows, cols, rank = 96, 256, 4
+    g = torch.Generator().manual_seed(3)
+    w = (torch.randn(rows, cols, generator=g) * 0.05).to(torch.bfloat16)
+    down = torch.randn(rank, cols, generator=g) * 0.1
+    up = torch.randn(rows, rank, generator=g) * 0.1
+    magnitude = torch.rand(rows, generator=g) + 0.5
+    s, t = 0.8, 1.0
+    stored = {"value": w.to(CUDA)}
+    gain, scales = cb.dora(torch, stored, [(down.to(CUDA), up.to(CUDA), magnitude.to(CUDA), s, t)])
+    cb.gain_rows(torch, stored, gain)
+    cb.bake(torch, stored, down.to(CUDA), (up.to(CUDA) * scales[0][:, None]), seed=5)
+    want = cb.dora_weight(torch, w.double(), down.double(), up.double(), magnitude.double(), s, t)
+    got = stored["value"].double().cpu()
+    # Two bf16 roundings: `gain_rows` rounds g·W to nearest (half an ulp of |g·W|), the bake
+    # rounds the sum stochastically (under one ulp of it); an ulp is at most 2^-7 of a magnitude.
+    scaled = (gain.double().cpu()[:, None] * w.double()).abs()
+    bound = (0.5 * scaled + want.abs() + scaled * 2.0**-7) * 2.0**-7 * 1.01 + 1e-6
+    assert bool(((got - want).abs() <= bound).all())
+    # The row gain on a row-scaled weight is its scale's, exactly.
+    data, scale, _ = _stored_for(ob.ROWWISE, rows, cols, 6)
+    fp8 = {"weight": torch.from_numpy(data).view(torch.float8_e4m3fn).to(CUDA),
+           "scale": torch.from_numpy(scale).to(CUDA)}  # fmt: skip
+    cb.gain_rows(torch, fp8, gain)
+    assert torch.equal(fp8["scale"].cpu(), torch.from_numpy(scale) * gain.cpu())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("form", [ob.BF16, ob.INT8, ob.NVFP4])
+def test_gpu_lokr_rows_bake_bit_exact(form):
+    """A LoKr term's dense rows (`Kron`, `dense`) add to the delta; int8.convrot rotates them."""
+    from cozyq import bake as cb
+
+    rng = np.random.default_rng(33 + form)
+    rows, cols, rank = 64, 256, 3
+    w1 = rng.standard_normal((8, 16)).astype(np.float32)
+    w2 = rng.standard_normal((8, 16)).astype(np.float32)
+    kron = cb.Kron(torch.from_numpy(w1).to(CUDA), torch.from_numpy(w2).to(CUDA), 0.01,
+                   torch.arange(rows, device=CUDA))  # fmt: skip
+    more = (np.kron(w1, w2) * np.float32(0.01)).astype(np.float32)
+    up = (rng.standard_normal((rows, rank)) * 0.02).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    seed = 1234
+    if form == ob.NVFP4:
+        codes, blocks = _nvfp4_stored(rows, cols, rng)
+        want = ob.bake_nvfp4(codes, blocks, 0.03, up, down, seed, more=more)
+        stored = {"weight": torch.from_numpy(codes).to(CUDA),
+                  "scale": torch.from_numpy(blocks).view(torch.float8_e4m3fn).to(CUDA),
+                  "scale_2": torch.tensor([0.03], device=CUDA)}  # fmt: skip
+        cb.bake(torch, stored, _cuda(down), _cuda(up), seed=seed, more=cb.dense([kron]))
+        assert np.array_equal(stored["scale"].view(torch.uint8).cpu().numpy(), want[1])
+        assert np.array_equal(stored["weight"].cpu().numpy(), want[0])
+        return
+    data, scale, _ = _stored_for(form, rows, cols, 34)
+    if form == ob.INT8:
+        want = ob.bake(form, data, scale, up, ob.rotate_factor(down), seed, more=ob.rotate_factor(more))
+        stored = {"weight": torch.from_numpy(data).to(CUDA), "scale": torch.from_numpy(scale).to(CUDA)}
+        key = "weight"
+    else:
+        want = ob.bake(form, data, scale, up, down, seed, more=more)
+        stored = {"value": _torch_data(form, data).to(CUDA)}
+        key = "value"
+    cb.bake(torch, stored, _cuda(down), _cuda(up), seed=seed, more=cb.dense([kron]))
+    torch.cuda.synchronize()
+    assert np.array_equal(_bytes(stored[key]), want.view(np.uint8).reshape(rows, -1))
