@@ -211,6 +211,104 @@ def bake(
     fused(torch, stored, down, up, seed, gain=gain, more=more)
 
 
+ROUNDINGS = ("nearest", "stochastic", "feedback")
+GRIDS = ("keep", "refit", "regrid")
+
+
+def _rounding_flags(rounding: str, stats: Any, allowed: tuple[str, ...] = ("nearest", "stochastic")) -> int:
+    if rounding not in ROUNDINGS:
+        raise ValueError(f"no rounding {rounding!r}")
+    if rounding not in allowed:
+        raise NotImplementedError(f"cozyq bakes by nearest or stochastic rounding, not {rounding!r}")
+    if stats is not None:
+        raise NotImplementedError("cozyq's bake keeps no Stats (the reference's eager measurement)")
+    return NEAREST if rounding == "nearest" else 0
+
+
+def _scaled_up(torch: Any, up: Tensor, alpha: float) -> Tensor:
+    """`up` times `alpha` before the product: the reference scales the product instead
+    (`_delta`, `internal/lora_bake.py:242-246`), the same for a power of two and within a float32
+    rounding otherwise. `bake` itself always passes 1."""
+    up32 = up.to(torch.float32)
+    return up32 if alpha == 1.0 else up32 * alpha
+
+
+def bake_plain(torch: Any, weight: Tensor, down: Tensor, up: Tensor, alpha: float, *,
+               rounding: str = "nearest", generator: Any = None, stats: Any = None,
+               more: Dense | None = None, gain: Tensor | None = None, seed: int = 0) -> None:  # fmt: skip
+    """`weight = gain * weight + alpha * up @ down`, float32, rounded once to its dtype
+    (`internal/lora_bake.py:271-305`); bf16 rounds stochastically on request, other dtypes to
+    nearest. The noise is the Philox stream under `seed` (the reference's eager draws come from
+    `generator`, which is not used here)."""
+    flags = _rounding_flags(rounding, stats)
+    if weight.dtype != torch.bfloat16:
+        flags = NEAREST
+    fused(torch, {"value": weight}, down, _scaled_up(torch, up, alpha), seed, gain=gain, more=more,
+          flags=flags)  # fmt: skip
+
+
+def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tensor, alpha: float, *,
+                 rounding: str = "nearest", grid: str = "refit", generator: Any = None,
+                 stats: Any = None, more: Dense | None = None, seed: int = 0) -> None:  # fmt: skip
+    """Bake into `fp8.rowwise` (`internal/lora_bake.py:319-363`) with the row scales kept
+    (`grid="keep"`); `refit` and `regrid` rescale rows from their baked maximum and are not
+    built."""
+    if grid not in GRIDS:
+        raise ValueError(f"no grid {grid!r}")
+    if grid != "keep":
+        raise NotImplementedError("cozyq keeps a rowwise weight's scales (grid='keep')")
+    flags = _rounding_flags(rounding, stats)
+    fused(torch, {"weight": data, "scale": scale}, down, _scaled_up(torch, up, alpha), seed, more=more,
+          flags=flags)  # fmt: skip
+
+
+def bake_int8_convrot(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tensor, alpha: float, *,
+                      rounding: str = "nearest", generator: Any = None, stats: Any = None,
+                      more: Dense | None = None, seed: int = 0) -> None:  # fmt: skip
+    """Bake into `int8-convrot256/1` (`internal/lora_bake.py:372-423`): `down` and the dense
+    rows rotated into the weight's basis, the row scale kept, nearest or stochastic floor,
+    clamped to ±127."""
+    flags = _rounding_flags(rounding, stats)
+    fused(torch, {"weight": data, "scale": scale}, down, _scaled_up(torch, up, alpha), seed, more=more,
+          flags=flags)  # fmt: skip
+
+
+def bake_nvfp4(torch: Any, weight: Tensor, scale: Tensor, scale_2: Tensor, down: Tensor, up: Tensor,
+               alpha: float, *, rounding: str = "stochastic", grid: str = "keep", generator: Any = None,
+               stats: Any = None, more: Dense | None = None, gain: Tensor | None = None,
+               seed: int = 0) -> None:  # fmt: skip
+    """Bake into canonical `nvfp4` (`internal/lora_bake.py:458-525`) with `keep`: the second level
+    kept and a block's scale refitted only past 7/6 of it. `refit` is not built."""
+    if grid not in GRIDS:
+        raise ValueError(f"no grid {grid!r}")
+    if grid != "keep":
+        raise NotImplementedError("cozyq keeps nvfp4's levels (grid='keep')")
+    flags = _rounding_flags(rounding, stats)
+    extra = gain is not None or more is not None or flags
+    stored = {"weight": weight, "scale": scale, "scale_2": scale_2}
+    if extra or rounding != "stochastic":
+        fused(torch, stored, down, _scaled_up(torch, up, alpha), seed, gain=gain, more=more, flags=flags)
+    else:
+        # Without additions the eager law's separate roundings still apply (`base + delta`).
+        ones = torch.ones(weight.shape[0], dtype=torch.float32, device=weight.device)
+        fused(torch, stored, down, _scaled_up(torch, up, alpha), seed, gain=ones)
+
+
+def warm(torch: Any, device: int) -> None:
+    """The bake kernels are part of `libcozyq.so` and serve from the first call
+    (`internal/lora_bake.py:817-821` builds Triton kernels here): opening the library is all."""
+    serving(torch, device)
+
+
+def serving(torch: Any, device: int) -> str:
+    """How a bake on GPU `device` runs (`internal/lora_bake.py:824-835`): always `fused`, the
+    HIP kernels; the library opens (or raises) here."""
+    from cozyq import prebuilt
+
+    prebuilt.library(device)
+    return "fused"
+
+
 def rotate_rows(torch: Any, rows: Dense) -> Dense:
     """`rows` in an `int8-convrot256/1` weight's basis, as `rotate_factor` rotates `down`
     (`internal/lora_bake.py:648-650`)."""

@@ -803,3 +803,60 @@ def test_gpu_lokr_rows_bake_bit_exact(form):
     cb.bake(torch, stored, _cuda(down), _cuda(up), seed=seed, more=cb.dense([kron]))
     torch.cuda.synchronize()
     assert np.array_equal(_bytes(stored[key]), want.view(np.uint8).reshape(rows, -1))
+
+
+def test_eager_entry_points_refuse_unbuilt_options():
+    from cozyq import bake as cb
+
+    t = torch.zeros(4, 16)
+    down, up = torch.zeros(1, 16), torch.zeros(4, 1)
+    with pytest.raises(NotImplementedError):
+        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0)  # default grid "refit"
+    with pytest.raises(NotImplementedError):
+        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, grid="keep", rounding="feedback")
+    with pytest.raises(NotImplementedError):
+        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit")
+    with pytest.raises(NotImplementedError):
+        cb.bake_plain(torch, t, down, up, 1.0, stats=object())
+    with pytest.raises(ValueError):
+        cb.bake_int8_convrot(torch, t, t, down, up, 1.0, rounding="up")
+
+
+@pytest.mark.gpu
+def test_gpu_eager_entry_points():
+    """`bake_plain` / `bake_rowwise` / `bake_int8_convrot` / `bake_nvfp4` called directly, with
+    alpha, as the reference's eager functions are: bit-exact against the oracle's laws."""
+    from cozyq import bake as cb
+
+    rng = np.random.default_rng(77)
+    rows, cols, rank, alpha, seed = 40, 256, 4, 0.5, 99
+    up = (rng.standard_normal((rows, rank)) * 0.04).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    up_a = (up * np.float32(alpha)).astype(np.float32)
+    assert cb.serving(torch, 0) == "fused"
+    # bf16 nearest with a gain
+    data, _, _ = _stored_for(ob.BF16, rows, cols, 1)
+    gain = (rng.random(rows) + 0.5).astype(np.float32)
+    t = _torch_data(ob.BF16, data).to(CUDA)
+    cb.bake_plain(torch, t, _cuda(down), _cuda(up), alpha, gain=_cuda(gain), seed=seed)
+    assert np.array_equal(_bytes(t), ob.bake(ob.BF16, data, None, up_a, down, seed, gain=gain,
+                                            nearest=True).view(np.uint8))  # fmt: skip
+    # fp8.rowwise, keep, stochastic
+    data, scale, _ = _stored_for(ob.ROWWISE, rows, cols, 2)
+    w = torch.from_numpy(data).view(torch.float8_e4m3fn).to(CUDA)
+    cb.bake_rowwise(torch, w, _cuda(scale), _cuda(down), _cuda(up), alpha, grid="keep", rounding="stochastic",
+                    seed=seed)  # fmt: skip
+    assert np.array_equal(w.view(torch.uint8).cpu().numpy(), ob.bake(ob.ROWWISE, data, scale, up_a, down, seed))
+    # int8.convrot, nearest
+    data, scale, _ = _stored_for(ob.INT8, rows, cols, 3)
+    w = torch.from_numpy(data).to(CUDA)
+    cb.bake_int8_convrot(torch, w, _cuda(scale), _cuda(down), _cuda(up), alpha, seed=seed)
+    want = ob.bake(ob.INT8, data, scale, up_a, ob.rotate_factor(down), seed, nearest=True)
+    assert np.array_equal(w.cpu().numpy(), want)
+    # nvfp4, the eager law's roundings, stochastic
+    codes, blocks = _nvfp4_stored(rows, cols, rng)
+    c, b = torch.from_numpy(codes).to(CUDA), torch.from_numpy(blocks).view(torch.float8_e4m3fn).to(CUDA)
+    cb.bake_nvfp4(torch, c, b, torch.tensor([0.03], device=CUDA), _cuda(down), _cuda(up), alpha, seed=seed)
+    want = ob.bake_nvfp4(codes, blocks, 0.03, up_a, down, seed, gain=np.ones(rows, np.float32))
+    assert np.array_equal(b.view(torch.uint8).cpu().numpy(), want[1])
+    assert np.array_equal(c.cpu().numpy(), want[0])
