@@ -548,7 +548,7 @@ def bench_bake(torch, ops, lib, stream, steps: int) -> dict:
                                             sides.data_ptr(), None, None, rows, cols, rank, 77, 0, raw))  # fmt: skip
             else:
                 _check(lib.cozyq_bake(0, form, w.data_ptr(), scale.data_ptr(), up.data_ptr(), sides.data_ptr(),
-                                      None, None, rows, cols, rank, 77, 0, raw))  # fmt: skip
+                                      None, None, None, rows, cols, rank, 77, 0, raw))  # fmt: skip
 
         us = _graph_us(torch, go, 4 * copies, max(4, steps // 8))
         nbytes = 2 * stored + factors

@@ -84,12 +84,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "cozyq_measure": (c_int, [c_int, _P, c_int, _P, c_int64, _P, c_int, _P, _P]),
     "cozyq_bake": (
-        c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_uint32, c_int, _P]
+        c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_uint32, c_int, _P]
     ),
     "cozyq_bake_nvfp4": (
         c_int, [c_int, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_uint32, c_int, _P]
     ),
     "cozyq_bake_norms": (
+        c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]
+    ),
+    "cozyq_bake_row_amax": (
         c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]
     ),
     "cozyq_bake_rotate_factor": (c_int, [c_int, _P, _P, c_int64, c_int64, _P]),

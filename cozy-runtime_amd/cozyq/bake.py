@@ -23,7 +23,8 @@ What the reference bakes eagerly runs on the same kernels: a DoRA gain on plain 
 roundings), a LoKr's dense rows (`more`, added to the delta; rotated for int8.convrot), `gain_rows`
 (nearest rounding, no delta) and DoRA's row `norms`. Their stochastic bytes are drawn from the
 Philox stream above, where the reference's eager bake draws from torch's generator: the same law
-in distribution, not the same bytes. Not built: `Stats`, the `refit` / `regrid` grids and
+in distribution, not the same bytes. `bake_rowwise`'s `refit` / `regrid` grids run on a row-amax
+kernel and the bake kernel's new-scale mode. Not built: `Stats`, nvfp4's `refit` grid and
 error-feedback rounding (eager-only diagnostics and options `bake` never selects); asking for
 them raises NotImplementedError. Tensors off the GPU raise.
 """
@@ -247,19 +248,46 @@ def bake_plain(torch: Any, weight: Tensor, down: Tensor, up: Tensor, alpha: floa
           flags=flags)  # fmt: skip
 
 
+#: `bake_rowwise`'s floor of a refitted row scale and E4M3's largest value
+#: (`internal/lora_bake.py:72`, `internal/encoding/formats.py:497`).
+ROW_SCALE_FLOOR, E4M3_MAX = 1e-12, 448.0
+
+
 def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tensor, alpha: float, *,
                  rounding: str = "nearest", grid: str = "refit", generator: Any = None,
                  stats: Any = None, more: Dense | None = None, seed: int = 0) -> None:  # fmt: skip
-    """Bake into `fp8.rowwise` (`internal/lora_bake.py:319-363`) with the row scales kept
-    (`grid="keep"`); `refit` and `regrid` rescale rows from their baked maximum and are not
-    built."""
+    """Bake into `fp8.rowwise` (`internal/lora_bake.py:319-363`): `data` `[out, in]` E4M3,
+    `scale` one float32 per output row. `keep` rounds on the stored grid (the fused law's
+    order, `decode + delta / scale`); `refit` sets each row's scale from its baked maximum,
+    `max(amax / 448, 1e-12)`, and `regrid` raises that by 1/32 to 3/32 by the row's golden-ratio
+    fraction, so every element rounds afresh: codes are `(decode · scale + delta) / new`, the
+    eager law's order, and `scale` takes the new values."""
     if grid not in GRIDS:
         raise ValueError(f"no grid {grid!r}")
-    if grid != "keep":
-        raise NotImplementedError("cozyq keeps a rowwise weight's scales (grid='keep')")
     flags = _rounding_flags(rounding, stats)
-    fused(torch, {"weight": data, "scale": scale}, down, _scaled_up(torch, up, alpha), seed, more=more,
-          flags=flags)  # fmt: skip
+    up_a = _scaled_up(torch, up, alpha)
+    stored = {"weight": data, "scale": scale}
+    if grid == "keep":
+        fused(torch, stored, down, up_a, seed, more=more, flags=flags)
+        return
+    raw, scales = data.view(torch.uint8), scale.view(-1)
+    if scales.dtype != torch.float32 or not scales.is_contiguous():
+        raise ValueError("a row-scaled bake keeps a contiguous float32 row scale")
+    up32, down32 = up_a.to(torch.float32).contiguous(), down.to(torch.float32).contiguous()
+    more_rows = _more_rows(torch, more, raw.shape[0], False)
+    if more_rows is not None:
+        raise NotImplementedError("cozyq refits rowwise scales from up @ down alone (no LoKr rows)")
+    ops = _ops(raw)
+    amax = ops.bake_norms(ROWWISE, raw, scales, up32, down32, cols=raw.shape[1], amax=True)
+    # amax / 448 as torch runs it on a GPU (the reference's eager bake included): times the float32
+    # reciprocal, written out so that it does not depend on that detail.
+    new = (amax * (1.0 / E4M3_MAX)).clamp(min=ROW_SCALE_FLOOR)
+    if grid == "regrid":
+        row = torch.arange(raw.shape[0], device=raw.device, dtype=torch.float32)
+        new = new * (1 + (1 + 2 * torch.frac(row * 0.6180339887)) / 32)
+    new = new.contiguous()
+    ops.bake(ROWWISE, raw, scales, up32, down32, seed & SEED_MASK, flags=flags, rescale=new)
+    scales.copy_(new)
 
 
 def bake_int8_convrot(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tensor, alpha: float, *,

@@ -630,18 +630,23 @@ class Prebuilt:
 
     def bake(self, form: int, data: Tensor, scale: Tensor | None, up: Tensor, down: Tensor,
              seed: int, *, gain: Tensor | None = None, more: Tensor | None = None,
-             flags: int = 0) -> None:  # fmt: skip
+             flags: int = 0, rescale: Tensor | None = None) -> None:  # fmt: skip
         """`cozyq_bake` in place (`_bake_kernel`, `internal/lora_bake.py:1013-1053`): `data`
         contiguous [rows, cols] of the form, `scale` float32 [rows] (row-scaled forms), `up`
         float32 [rows, rank], `down` float32 [rank, cols] (int8.convrot: rotated). `gain`
         (float32 [rows], plain forms), `more` (float32 [rows, cols]) and `flags` (1 nearest,
-        2 no delta) are the eager bake's additions."""
+        2 no delta) are the eager bake's additions; `rescale` (float32 [rows], fp8.rowwise) bakes
+        onto new row scales, which the caller then stores."""
         rows, cols = (int(v) for v in data.shape)
         stored = (data,) if scale is None else (data, scale)
         rank = self._factors(up, down, rows, cols, stored, gain, more)
+        if rescale is not None and (rescale.dtype != self.torch.float32 or rescale.numel() != rows
+                                    or not rescale.is_contiguous()):  # fmt: skip
+            raise ValueError(f"LoRA bake: new row scales must be contiguous float32 with {rows} values")
         code = self._lib.cozyq_bake(
             self.index, form, data.data_ptr(), _ptr(scale), up.data_ptr(), down.data_ptr(),
-            _ptr(gain), _ptr(more), rows, cols, rank, seed & 0xFFFFFFFF, flags, self._stream(),
+            _ptr(gain), _ptr(more), _ptr(rescale), rows, cols, rank, seed & 0xFFFFFFFF, flags,
+            self._stream(),
         )  # fmt: skip
         self._check(code, "the LoRA bake")
 
@@ -663,20 +668,21 @@ class Prebuilt:
         self._check(code, "the nvfp4 LoRA bake")
 
     def bake_norms(self, form: int, data: Tensor, scale: Tensor | None, up: Tensor, down: Tensor,
-                   *, cols: int, blocks: Tensor | None = None,
-                   second: Tensor | None = None) -> Tensor:  # fmt: skip
+                   *, cols: int, blocks: Tensor | None = None, second: Tensor | None = None,
+                   amax: bool = False) -> Tensor:  # fmt: skip
         """`cozyq_bake_norms` (`norms`, `internal/lora_bake.py:653-689`): each row's L2 norm of
-        the decoded weight plus `up @ down`, float32 [rows]. form 5 is nvfp4 (codes `data`,
-        `blocks`, `second`)."""
+        the decoded weight plus `up @ down`, float32 [rows]; with `amax`, `cozyq_bake_row_amax`
+        (each row's max |·|). form 5 is nvfp4 (codes `data`, `blocks`, `second`)."""
         rows = int(data.shape[0])
         stored = tuple(t for t in (data, scale, blocks, second) if t is not None)
         rank = self._factors(up, down, rows, cols, stored)
         out = self.torch.empty(rows, dtype=self.torch.float32, device=data.device)
-        code = self._lib.cozyq_bake_norms(
+        entry = self._lib.cozyq_bake_row_amax if amax else self._lib.cozyq_bake_norms
+        code = entry(
             self.index, form, data.data_ptr(), _ptr(scale), _ptr(blocks), _ptr(second),
             up.data_ptr(), down.data_ptr(), rows, cols, rank, out.data_ptr(), self._stream(),
         )  # fmt: skip
-        self._check(code, "the row norms")
+        self._check(code, "the row reduction")
         return out
 
     def rotate_factor(self, down: Tensor) -> Tensor:

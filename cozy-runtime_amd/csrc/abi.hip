@@ -432,10 +432,10 @@ static bool bake_options(int form, const float* gain, int flags) {
 }
 
 int cozyq_bake(int device, int form, void* data, const float* scale, const float* up, const float* down,
-               const float* gain, const float* more, int64_t rows, int64_t cols, int64_t rank, uint32_t seed,
-               int flags, void* stream) {
+               const float* gain, const float* more, const float* rescale, int64_t rows, int64_t cols,
+               int64_t rank, uint32_t seed, int flags, void* stream) {
     if (form < cozyq::kBakeBf16 || form > cozyq::kBakeInt8 || !bake_shape(rows, cols, rank) ||
-        !bake_options(form, gain, flags))
+        !bake_options(form, gain, flags) || (rescale && (form != cozyq::kBakeRowwise || (flags & cozyq::kBakeNoDelta))))
         return hipErrorInvalidValue;
     if (rows == 0 || cols == 0) return hipSuccess;
     const bool scaled = form == cozyq::kBakeRowwise || form == cozyq::kBakeInt8;
@@ -444,7 +444,7 @@ int cozyq_bake(int device, int form, void* data, const float* scale, const float
     if (reinterpret_cast<uintptr_t>(data) % size) return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
-    return cozyq::bake(form, data, scale, up, down, cozyq::BakeOptions{gain, more, flags}, static_cast<int>(rows),
+    return cozyq::bake(form, data, scale, up, down, cozyq::BakeOptions{gain, more, flags, rescale}, static_cast<int>(rows),
                        static_cast<int>(cols), static_cast<int>(rank), seed, on(stream));
 }
 
@@ -457,13 +457,13 @@ int cozyq_bake_nvfp4(int device, uint8_t* data, uint8_t* blocks, const float* se
     if (!data || !blocks || !second || (rank > 0 && (!up || !down))) return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
-    return cozyq::bake_nvfp4(data, blocks, second, up, down, cozyq::BakeOptions{gain, more, flags},
+    return cozyq::bake_nvfp4(data, blocks, second, up, down, cozyq::BakeOptions{gain, more, flags, nullptr},
                              static_cast<int>(rows), static_cast<int>(cols), static_cast<int>(rank), seed, on(stream));
 }
 
-int cozyq_bake_norms(int device, int form, const void* data, const float* scale, const uint8_t* blocks,
+static int bake_rows(int device, int form, const void* data, const float* scale, const uint8_t* blocks,
                      const float* second, const float* up, const float* down, int64_t rows, int64_t cols,
-                     int64_t rank, float* out, void* stream) {
+                     int64_t rank, float* out, bool amax, void* stream) {
     if (form < cozyq::kBakeBf16 || form > cozyq::kBakeNvfp4 || !bake_shape(rows, cols, rank) ||
         (form == cozyq::kBakeNvfp4 && cols % 16))
         return hipErrorInvalidValue;
@@ -475,7 +475,19 @@ int cozyq_bake_norms(int device, int form, const void* data, const float* scale,
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
     return cozyq::bake_norms(form, data, scale, blocks, second, up, down, static_cast<int>(rows),
-                             static_cast<int>(cols), static_cast<int>(rank), out, on(stream));
+                             static_cast<int>(cols), static_cast<int>(rank), out, amax, on(stream));
+}
+
+int cozyq_bake_norms(int device, int form, const void* data, const float* scale, const uint8_t* blocks,
+                     const float* second, const float* up, const float* down, int64_t rows, int64_t cols,
+                     int64_t rank, float* out, void* stream) {
+    return bake_rows(device, form, data, scale, blocks, second, up, down, rows, cols, rank, out, false, stream);
+}
+
+int cozyq_bake_row_amax(int device, int form, const void* data, const float* scale, const uint8_t* blocks,
+                        const float* second, const float* up, const float* down, int64_t rows, int64_t cols,
+                        int64_t rank, float* out, void* stream) {
+    return bake_rows(device, form, data, scale, blocks, second, up, down, rows, cols, rank, out, true, stream);
 }
 
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n) {

@@ -183,6 +183,7 @@ struct Extra {
     const float* gain;
     const float* more;
     bool nearest, no_delta;
+    const float* rescale;  // ROWWISE: each row's new scale (`refit` / `regrid`), or null to keep
 };
 
 // One element of a `_bake_kernel` form: the stored value (its bits), the delta, the row's unit
@@ -191,7 +192,8 @@ struct Extra {
 // round(round(v·gain) + delta) and every form can round to nearest.
 template <int kForm, bool kExtra>
 __device__ __forceinline__ typename Stored<kForm>::T bake_one(typename Stored<kForm>::T v, float d, float unit,
-                                                               const Extra& x, uint32_t at, uint32_t k0, uint32_t k1) {
+                                                               float fresh, const Extra& x, uint32_t at, uint32_t k0,
+                                                               uint32_t k1) {
     if constexpr (kForm == kBakeBf16 || kForm == kBakeF16 || kForm == kBakeF32) {
         float value;
         if constexpr (kForm == kBakeBf16) value = float_of(static_cast<uint32_t>(v) << 16);
@@ -213,7 +215,14 @@ __device__ __forceinline__ typename Stored<kForm>::T bake_one(typename Stored<kF
             return value;
         }
     } else if constexpr (kForm == kBakeRowwise) {
-        const float payload = kExtra && x.no_delta ? e4m3_sat(v) : e4m3_sat(v) + d / unit;
+        float payload;
+        if (kExtra && x.rescale) {
+            // `bake_rowwise` on a new grid (internal/lora_bake.py:340-352): the decoded row plus
+            // the delta, over the row's new scale.
+            payload = (e4m3_sat(v) * unit + d) / fresh;
+        } else {
+            payload = kExtra && x.no_delta ? e4m3_sat(v) : e4m3_sat(v) + d / unit;
+        }
         if (kExtra && x.nearest) return static_cast<uint8_t>(e4m3_nearest(payload));
         return static_cast<uint8_t>(e4m3_stochastic(payload, philox_word(at, k0, k1)));
     } else {
@@ -253,9 +262,12 @@ __global__ __launch_bounds__(kBakeThreads) void bake_kernel(typename Stored<kFor
     for (int i = 0; i < 4; ++i) {
         const int row = row0 + 4 * rg + i;
         if (row >= rows) break;
-        float unit = 1.0f;
+        float unit = 1.0f, fresh = 1.0f;
         if constexpr (kForm == kBakeRowwise || kForm == kBakeInt8) unit = scale[row];
         else if (kExtra && x.gain) unit = x.gain[row];
+        if constexpr (kForm == kBakeRowwise) {
+            if (kExtra && x.rescale) fresh = x.rescale[row];
+        }
         const int64_t line0 = static_cast<int64_t>(row) * cols;
         T* line = data + line0;
         const uint32_t line_at = static_cast<uint32_t>(static_cast<uint64_t>(row) * static_cast<uint64_t>(cols));
@@ -269,15 +281,15 @@ __global__ __launch_bounds__(kBakeThreads) void bake_kernel(typename Stored<kFor
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     four.v[e] = bake_one<kForm, kExtra>(four.v[e], with_more<kExtra>(acc[i][4 * h + e], x, line0 + col + e),
-                                                        unit, x, line_at + col + e, seed, k1);
+                                                        unit, fresh, x, line_at + col + e, seed, k1);
                 *reinterpret_cast<Four*>(line + col) = four;
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     if (col + e < cols)
                         line[col + e] = bake_one<kForm, kExtra>(
-                            line[col + e], with_more<kExtra>(acc[i][4 * h + e], x, line0 + col + e), unit, x,
-                            line_at + col + e, seed, k1);
+                            line[col + e], with_more<kExtra>(acc[i][4 * h + e], x, line0 + col + e), unit, fresh,
+                            x, line_at + col + e, seed, k1);
             }
         }
     }
@@ -366,7 +378,7 @@ __global__ __launch_bounds__(kBakeThreads) void bake_nvfp4_kernel(uint8_t* __res
 // order, so a row's float64 sum of squares is the same on every call. kForm: a `_bake_kernel`
 // form, or kBakeNvfp4 (codes at `data`, block bytes at `blocks`, level at `second`).
 
-template <int kForm>
+template <int kForm, bool kMax>
 __global__ __launch_bounds__(kBakeThreads) void bake_norms_kernel(const void* __restrict__ data,
                                                                   const float* __restrict__ scale,
                                                                   const uint8_t* __restrict__ blocks,
@@ -406,7 +418,8 @@ __global__ __launch_bounds__(kBakeThreads) void bake_norms_kernel(const void* __
                     value = e2m1_of(code) * (e4m3_sat(blocks[static_cast<int64_t>(row) * (cols / 16) + col / 16]) * second[0]);
                 }
                 const double t = static_cast<double>(value + acc[i][j]);
-                sums[i] += t * t;
+                if constexpr (kMax) sums[i] = __builtin_fmax(sums[i], __builtin_fabs(t));
+                else sums[i] += t * t;
             }
         }
     }
@@ -414,9 +427,12 @@ __global__ __launch_bounds__(kBakeThreads) void bake_norms_kernel(const void* __
     for (int i = 0; i < 4; ++i) {
         double v = sums[i];
 #pragma unroll
-        for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off);  // the 16 lanes of a row group
+        for (int off = 1; off < 16; off <<= 1) {  // the 16 lanes of a row group
+            const double other = __shfl_xor(v, off);
+            v = kMax ? __builtin_fmax(v, other) : v + other;
+        }
         const int row = row0 + 4 * rg + i;
-        if (cg == 0 && row < rows) out[row] = static_cast<float>(__builtin_sqrt(v));
+        if (cg == 0 && row < rows) out[row] = static_cast<float>(kMax ? v : __builtin_sqrt(v));
     }
 }
 
@@ -455,8 +471,8 @@ hipError_t launch_bake(void* data, const float* scale, const float* up, const fl
     const dim3 grid((cols + kTileCols - 1) / kTileCols, (rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
     T* d = static_cast<T*>(data);
     const bool vec = cols % 4 == 0 && reinterpret_cast<uintptr_t>(data) % (4 * sizeof(T)) == 0;
-    const Extra x{o.gain, o.more, (o.flags & kBakeNearest) != 0, (o.flags & kBakeNoDelta) != 0};
-    const bool extra = o.gain || o.more || o.flags;
+    const Extra x{o.gain, o.more, (o.flags & kBakeNearest) != 0, (o.flags & kBakeNoDelta) != 0, o.rescale};
+    const bool extra = o.gain || o.more || o.flags || o.rescale;
 #define COZYQ_BAKE(V, E) hipLaunchKernelGGL((bake_kernel<kForm, V, E>), grid, block, 0, s, d, scale, up, down, x, rows, cols, rank, seed)
     if (vec) {
         if (extra) COZYQ_BAKE(true, true); else COZYQ_BAKE(true, false);
@@ -469,10 +485,15 @@ hipError_t launch_bake(void* data, const float* scale, const float* up, const fl
 
 template <int kForm>
 hipError_t launch_norms(const void* data, const float* scale, const uint8_t* blocks, const float* second,
-                        const float* up, const float* down, int rows, int cols, int rank, float* out, hipStream_t s) {
+                        const float* up, const float* down, int rows, int cols, int rank, float* out, bool amax,
+                        hipStream_t s) {
     const dim3 grid((rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
-    hipLaunchKernelGGL((bake_norms_kernel<kForm>), grid, block, 0, s, data, scale, blocks, second, up, down, rows,
-                       cols, rank, out);
+    if (amax)
+        hipLaunchKernelGGL((bake_norms_kernel<kForm, true>), grid, block, 0, s, data, scale, blocks, second, up, down,
+                           rows, cols, rank, out);
+    else
+        hipLaunchKernelGGL((bake_norms_kernel<kForm, false>), grid, block, 0, s, data, scale, blocks, second, up, down,
+                           rows, cols, rank, out);
     return hipGetLastError();
 }
 
@@ -493,7 +514,7 @@ hipError_t bake(int form, void* data, const float* scale, const float* up, const
 hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const float* up, const float* down,
                       const BakeOptions& o, int rows, int cols, int rank, uint32_t seed, hipStream_t s) {
     const dim3 grid((cols + kTileCols - 1) / kTileCols, (rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
-    const Extra x{o.gain, o.more, (o.flags & kBakeNearest) != 0, (o.flags & kBakeNoDelta) != 0};
+    const Extra x{o.gain, o.more, (o.flags & kBakeNearest) != 0, (o.flags & kBakeNoDelta) != 0, nullptr};
     if (o.gain || o.more || o.flags)
         hipLaunchKernelGGL((bake_nvfp4_kernel<true>), grid, block, 0, s, data, blocks, second, up, down, x, rows, cols, rank, seed);
     else
@@ -502,14 +523,15 @@ hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const
 }
 
 hipError_t bake_norms(int form, const void* data, const float* scale, const uint8_t* blocks, const float* second,
-                      const float* up, const float* down, int rows, int cols, int rank, float* out, hipStream_t s) {
+                      const float* up, const float* down, int rows, int cols, int rank, float* out, bool amax,
+                      hipStream_t s) {
     switch (form) {
-        case kBakeBf16: return launch_norms<kBakeBf16>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
-        case kBakeF16: return launch_norms<kBakeF16>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
-        case kBakeF32: return launch_norms<kBakeF32>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
-        case kBakeRowwise: return launch_norms<kBakeRowwise>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
-        case kBakeInt8: return launch_norms<kBakeInt8>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
-        case kBakeNvfp4: return launch_norms<kBakeNvfp4>(data, scale, blocks, second, up, down, rows, cols, rank, out, s);
+        case kBakeBf16: return launch_norms<kBakeBf16>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
+        case kBakeF16: return launch_norms<kBakeF16>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
+        case kBakeF32: return launch_norms<kBakeF32>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
+        case kBakeRowwise: return launch_norms<kBakeRowwise>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
+        case kBakeInt8: return launch_norms<kBakeInt8>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
+        case kBakeNvfp4: return launch_norms<kBakeNvfp4>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -162,6 +162,7 @@ struct BakeOptions {
     const float* gain;
     const float* more;
     int flags;
+    const float* rescale;  // kBakeRowwise: each row's new scale [rows] (`refit`, `regrid`); null keeps
 };
 // data [rows, cols] of the form, scale float32 [rows] (kBakeRowwise, kBakeInt8), up float32
 // [rows, rank], down float32 [rank, cols] (kBakeInt8: already rotated), the 32-bit seed.
@@ -170,10 +171,11 @@ hipError_t bake(int form, void* data, const float* scale, const float* up, const
 // codes [rows, cols/2], E4M3 block bytes [rows, cols/16], second level at `second`; cols % 16 == 0.
 hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const float* up, const float* down,
                       const BakeOptions& o, int rows, int cols, int rank, uint32_t seed, hipStream_t s);
-// Row L2 norms of the decoded weight plus up @ down into out [rows] (float32); form as above,
-// kBakeNvfp4 with `blocks` and `second`.
+// Row L2 norms (or, with `amax`, row maxima of |·|) of the decoded weight plus up @ down into out
+// [rows] (float32); form as above, kBakeNvfp4 with `blocks` and `second`.
 hipError_t bake_norms(int form, const void* data, const float* scale, const uint8_t* blocks, const float* second,
-                      const float* up, const float* down, int rows, int cols, int rank, float* out, hipStream_t s);
+                      const float* up, const float* down, int rows, int cols, int rank, float* out, bool amax,
+                      hipStream_t s);
 // out = each 256-group of down times H256 / 16; `groups` = rank · cols / 256.
 hipError_t rotate_factor(const float* down, float* out, int64_t groups, hipStream_t s);
 

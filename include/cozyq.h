@@ -261,11 +261,15 @@ int cozyq_measure(int device, const void* w, int w_type, const float* decoded, i
  * `gain` float32 [rows] multiplying plain rows first (forms 0-2 only; a row-scaled weight takes
  * it in its scale), `more` float32 [rows, cols] added to the delta (a LoKr's dense rows; form 4:
  * rotated like `down`), flags 1 = round to nearest (ties to even) instead of stochastically,
- * 2 = no delta (the rows times their gain alone). data aligned to its element; rows ≤ 65535·64.
- * Errors: hipErrorInvalidValue for a bad form, shape, pointer, flag or a gain on forms 3-4. */
+ * 2 = no delta (the rows times their gain alone). `rescale` float32 [rows] (form 3 only) bakes
+ * onto new row scales (`bake_rowwise`'s `refit` / `regrid` grids, :319-363): each code is the
+ * rounding of (e4m3·scale + delta) / rescale, in the eager law's order; the caller stores
+ * `rescale` as the new scale. data aligned to its element; rows ≤ 65535·64. Errors:
+ * hipErrorInvalidValue for a bad form, shape, pointer, flag, a gain on forms 3-4 or a rescale
+ * off form 3. */
 int cozyq_bake(int device, int form, void* data, const float* scale, const float* up,
-               const float* down, const float* gain, const float* more, int64_t rows,
-               int64_t cols, int64_t rank, uint32_t seed, int flags, void* stream);
+               const float* down, const float* gain, const float* more, const float* rescale,
+               int64_t rows, int64_t cols, int64_t rank, uint32_t seed, int flags, void* stream);
 
 /* LoRA bake into canonical nvfp4 (reference: `_bake_nvfp4_kernel`, internal/lora_bake.py:
  * 955-1011, `bake_nvfp4` with `keep`): codes [rows, cols/2] (element 2k in the low nibble), E4M3
@@ -288,6 +292,14 @@ int cozyq_bake_norms(int device, int form, const void* data, const float* scale,
                      const uint8_t* blocks, const float* second, const float* up,
                      const float* down, int64_t rows, int64_t cols, int64_t rank, float* out,
                      void* stream);
+
+/* Each row's max |decoded stored weight + up @ down| (reference: the row amax `bake_rowwise`'s
+ * `refit` takes, internal/lora_bake.py:344-346), out float32 [rows]; arguments as
+ * `cozyq_bake_norms`'s. A maximum, so the same on every call. */
+int cozyq_bake_row_amax(int device, int form, const void* data, const float* scale,
+                        const uint8_t* blocks, const float* second, const float* up,
+                        const float* down, int64_t rows, int64_t cols, int64_t rank, float* out,
+                        void* stream);
 
 /* `down` [rank, cols] in an int8-convrot256/1 weight's basis (reference: `rotate_factor`,
  * internal/lora_bake.py:366-369): each 256 columns times the regular Hadamard H4⊗H4⊗H4⊗H4 in

@@ -233,7 +233,8 @@ def _bf16_nearest(value: np.ndarray) -> np.ndarray:
 
 def bake(form: int, data: np.ndarray, scale: np.ndarray | None, up: np.ndarray, down: np.ndarray,
          seed: int, *, gain: np.ndarray | None = None, more: np.ndarray | None = None,
-         nearest: bool = False, no_delta: bool = False) -> np.ndarray:  # fmt: skip
+         nearest: bool = False, no_delta: bool = False,
+         rescale: np.ndarray | None = None) -> np.ndarray:  # fmt: skip
     """The new stored data of one `_bake_kernel` form (`internal/lora_bake.py:1013-1053`):
     `data` `[rows, cols]` as stored (bf16 / f16 as uint16 bits, f32, E4M3 or int8 bytes),
     `scale` the float32 row scale of ROWWISE and INT8, `up` float32 `[rows, rank]`, `down`
@@ -243,7 +244,9 @@ def bake(form: int, data: np.ndarray, scale: np.ndarray | None, up: np.ndarray, 
     `gain_rows`, `:271-423,733-749`): `gain` float32 `[rows]` multiplies plain rows first,
     `more` float32 `[rows, cols]` adds to the delta, `nearest` rounds to nearest (ties to even)
     instead of stochastically, `no_delta` leaves the rows times their gain alone. Build law:
-    the row-scaled forms keep the fused order `decode + delta / scale` under them too."""
+    the row-scaled forms keep the fused order `decode + delta / scale` under them too.
+    `rescale` (ROWWISE, `bake_rowwise`'s `refit` / `regrid`, `:340-352`): each row's new scale;
+    the payload is then the eager order `(decode · scale + delta) / new`."""
     rows, cols = data.shape
     d = delta(up.astype(np.float32), down.astype(np.float32))
     if more is not None:
@@ -262,7 +265,10 @@ def bake(form: int, data: np.ndarray, scale: np.ndarray | None, up: np.ndarray, 
     if form == ROWWISE:
         unit = scale.astype(np.float32).reshape(-1, 1)
         payload = e4m3_value(data)
-        if not no_delta:
+        if rescale is not None:
+            target = ((payload * unit).astype(np.float32) + d).astype(np.float32)
+            payload = (target / rescale.astype(np.float32).reshape(-1, 1)).astype(np.float32)
+        elif not no_delta:
             payload = (payload + (d / unit).astype(np.float32)).astype(np.float32)
         return e4m3_nearest(payload) if nearest else e4m3_stochastic(payload, randint(seed, at))
     if form == BF16:
@@ -328,6 +334,30 @@ def bake_nvfp4(data: np.ndarray, blocks: np.ndarray, second: float, up: np.ndarr
     nibble = nibble | np.where(negative, 8, 0)
     packed = (nibble[:, 0::2] | (nibble[:, 1::2] << 4)).astype(np.uint8)
     return packed, block.astype(np.uint8)
+
+
+def row_amax(data: np.ndarray, scale: np.ndarray, up: np.ndarray, down: np.ndarray) -> np.ndarray:
+    """An fp8.rowwise weight's row maxima of |decode · scale + up @ down|, float32 — the amax
+    `bake_rowwise`'s `refit` takes (`internal/lora_bake.py:344-346`)."""
+    base = (e4m3_value(data) * scale.astype(np.float32).reshape(-1, 1)).astype(np.float32)
+    target = (base + delta(up.astype(np.float32), down.astype(np.float32))).astype(np.float32)
+    return np.abs(target).max(axis=1).astype(np.float32)
+
+
+def refit_scales(amax: np.ndarray, regrid: bool) -> np.ndarray:
+    """`bake_rowwise`'s new row scales (`internal/lora_bake.py:344-349`), float32 operation for
+    operation: `max(amax / 448, 1e-12)`, and for `regrid` times
+    `1 + (1 + 2·frac(row · 0.6180339887)) / 32`. The reference runs these as torch ops on its GPU,
+    where a tensor divided by a Python scalar is multiplied by the scalar's float32 reciprocal:
+    `amax · RN(1/448)` (the /32 is exact either way)."""
+    new = np.maximum((amax.astype(np.float32) * _F32(1.0 / 448.0)).astype(np.float32), _F32(1e-12))
+    if regrid:
+        row = np.arange(amax.shape[0], dtype=np.float32)
+        x = (row * _F32(0.6180339887)).astype(np.float32)
+        frac = (x - np.trunc(x)).astype(np.float32)
+        factor = (_F32(1) + ((_F32(1) + (_F32(2) * frac).astype(np.float32)).astype(np.float32) / _F32(32))).astype(np.float32)
+        new = (new * factor).astype(np.float32)
+    return new.astype(np.float32)
 
 
 def norms(form: int, data: np.ndarray, scale: np.ndarray | None, up: np.ndarray,

@@ -368,15 +368,19 @@ def test_abi_refuses_bad_bake_options():
     from cozyq import _lib
 
     lib = _lib.load()
-    bad = lib.cozyq_bake(0, 3, 16, 16, 16, 16, 16, None, 4, 8, 2, 1, 0, None)
+    bad = lib.cozyq_bake(0, 3, 16, 16, 16, 16, 16, None, None, 4, 8, 2, 1, 0, None)
     assert bad != 0
-    assert lib.cozyq_bake(0, 0, 16, None, 16, 16, None, None, 4, 8, 2, 1, 4, None) != 0
-    assert lib.cozyq_bake(0, 6, 16, None, 16, 16, None, None, 4, 8, 2, 1, 0, None) != 0
+    assert lib.cozyq_bake(0, 0, 16, None, 16, 16, None, None, None, 4, 8, 2, 1, 4, None) != 0
+    assert lib.cozyq_bake(0, 6, 16, None, 16, 16, None, None, None, 4, 8, 2, 1, 0, None) != 0
+    # A new row scale is for fp8.rowwise only, and not with "no delta".
+    assert lib.cozyq_bake(0, 4, 16, 16, 16, 16, None, None, 16, 4, 256, 2, 1, 0, None) != 0
+    assert lib.cozyq_bake(0, 3, 16, 16, 16, 16, None, None, 16, 4, 8, 2, 1, 2, None) != 0
+    assert lib.cozyq_bake_row_amax(0, 7, 16, None, None, None, 16, 16, 4, 8, 2, 16, None) != 0
     assert lib.cozyq_bake_nvfp4(0, 16, 16, 16, 16, 16, None, None, 4, 24, 2, 1, 0, None) != 0
     assert lib.cozyq_bake_norms(0, 6, 16, None, None, None, 16, 16, 4, 8, 2, 16, None) != 0
     assert lib.cozyq_bake_rotate_factor(0, 16, 16, 2, 100, None) != 0
     # Empty shapes succeed without touching a device.
-    assert lib.cozyq_bake(0, 0, None, None, None, None, None, None, 0, 8, 2, 1, 0, None) == 0
+    assert lib.cozyq_bake(0, 0, None, None, None, None, None, None, None, 0, 8, 2, 1, 0, None) == 0
 
 
 def test_nearest_grids_tie_to_even():
@@ -810,8 +814,10 @@ def test_eager_entry_points_refuse_unbuilt_options():
 
     t = torch.zeros(4, 16)
     down, up = torch.zeros(1, 16), torch.zeros(4, 1)
-    with pytest.raises(NotImplementedError):
-        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0)  # default grid "refit"
+    with pytest.raises(ValueError, match="GPU"):
+        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0)  # default grid "refit": built
+    with pytest.raises(ValueError, match="no grid"):
+        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, grid="wide")
     with pytest.raises(NotImplementedError):
         cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, grid="keep", rounding="feedback")
     with pytest.raises(NotImplementedError):
@@ -860,3 +866,45 @@ def test_gpu_eager_entry_points():
     want = ob.bake_nvfp4(codes, blocks, 0.03, up_a, down, seed, gain=np.ones(rows, np.float32))
     assert np.array_equal(b.view(torch.uint8).cpu().numpy(), want[1])
     assert np.array_equal(c.cpu().numpy(), want[0])
+
+
+def test_refit_scales_law():
+    """`refit` puts each row's baked maximum at 448 exactly in payload units (before rounding);
+    `regrid` lifts the scale by 1/32 to 3/32."""
+    amax = np.float32([448.0, 0.0, 1.0, 1e-20, 3.5])
+    refit = ob.refit_scales(amax, False)
+    inv = np.float32(1 / 448)
+    assert refit.tolist() == [np.float32(448) * inv, np.float32(1e-12), inv, np.float32(1e-12), np.float32(3.5) * inv]
+    assert abs(float(refit[0]) - 1.0) <= 2**-23
+    regrid = ob.refit_scales(amax, True)
+    ratio = regrid.astype(np.float64) / refit
+    assert ((ratio >= 1 + 1 / 32 - 1e-6) & (ratio <= 1 + 3 / 32 + 1e-6)).all()
+    assert regrid[0] == np.float32(1.0) * np.float32(1 + 1 / 32)  # row 0: frac(0) = 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("grid", ["refit", "regrid"])
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+def test_gpu_bake_rowwise_new_grids(grid, rounding):
+    """`bake_rowwise(grid=refit|regrid)`: the row maxima, the new scales and every code
+    bit-exact against the oracle."""
+    from cozyq import bake as cb
+
+    rows, cols, rank, seed = 70, 300, 6, 321
+    data, scale, rng = _stored_for(ob.ROWWISE, rows, cols, 60)
+    up = (rng.standard_normal((rows, rank)) * 0.05).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    amax = ob.row_amax(data, scale, up, down)
+    new = ob.refit_scales(amax, grid == "regrid")
+    want = ob.bake(ob.ROWWISE, data, scale, up, down, seed, nearest=rounding == "nearest", rescale=new)
+    w = torch.from_numpy(data).view(torch.float8_e4m3fn).to(CUDA)
+    s = _cuda(scale)
+    from cozyq import prebuilt
+
+    got_amax = prebuilt.library(0).bake_norms(ob.ROWWISE, w.view(torch.uint8), s, _cuda(up), _cuda(down),
+                                             cols=cols, amax=True)  # fmt: skip
+    assert np.array_equal(got_amax.cpu().numpy(), amax)
+    cb.bake_rowwise(torch, w, s, _cuda(down), _cuda(up), 1.0, rounding=rounding, grid=grid, seed=seed)
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), new.view(np.uint32))
+    assert np.array_equal(w.view(torch.uint8).cpu().numpy(), want)
