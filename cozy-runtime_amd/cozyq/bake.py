@@ -24,13 +24,16 @@ roundings), a LoKr's dense rows (`more`, added to the delta; rotated for int8.co
 (nearest rounding, no delta) and DoRA's row `norms`. Their stochastic bytes are drawn from the
 Philox stream above, where the reference's eager bake draws from torch's generator: the same law
 in distribution, not the same bytes. `bake_rowwise`'s `refit` / `regrid` grids run on a row-amax
-kernel and the bake kernel's new-scale mode. Not built: `Stats`, nvfp4's `refit` grid and
-error-feedback rounding (eager-only diagnostics and options `bake` never selects); asking for
-them raises NotImplementedError. Tensors off the GPU raise.
+kernel and the bake kernel's new-scale mode, and `Stats` on an accounting kernel that reads a
+copy of the weight taken before the bake. Not built: nvfp4's `refit` grid and error-feedback
+rounding (options `bake` never selects); asking for them raises NotImplementedError. Tensors off
+the GPU raise.
 """
 
 from __future__ import annotations
 
+import math
+import time
 from collections.abc import Callable, Mapping, Sequence
 from dataclasses import dataclass
 from typing import Any, NamedTuple
@@ -63,6 +66,83 @@ Dense = Callable[[int, int], Tensor]
 class Verdict(NamedTuple):
     ok: bool
     detail: str
+
+
+@dataclass(slots=True)
+class Stats:
+    """Sums over every baked element, in the weights' own units (`internal/lora_bake.py:78-123`),
+    taken on the GPU by `cozyq_bake_stats` from the weight before and after each bake."""
+
+    layers: int = 0
+    elements: int = 0
+    #: |W + delta|^2, |delta|^2, |stored - (W + delta)|^2 and <stored - W, delta>
+    weight_energy: float = 0.0
+    delta_energy: float = 0.0
+    error_energy: float = 0.0
+    kept: float = 0.0
+    #: the delta's action on its own inputs, |delta @ down.T|^2, and the rounding error's there
+    effect_energy: float = 0.0
+    effect_error: float = 0.0
+    saturated: int = 0
+    seconds: float = 0.0
+
+    @property
+    def retention(self) -> float:
+        """The delta's own direction in what was stored: 1.0 keeps all of it, 0.0 none."""
+        return self.kept / self.delta_energy if self.delta_energy else 1.0
+
+    @property
+    def sqnr_db(self) -> float:
+        """Baked weight against the rounding error the bake added."""
+        return _db(self.weight_energy, self.error_energy)
+
+    @property
+    def effect_snr_db(self) -> float:
+        """What the LoRA does to the inputs it reads, against what rounding did to them."""
+        return _db(self.effect_energy, self.effect_error)
+
+    def add(self, other: Stats) -> None:
+        for name in self.__slots__:
+            setattr(self, name, getattr(self, name) + getattr(other, name))
+
+    def document(self) -> dict[str, float | int]:
+        return {
+            "layers": self.layers,
+            "elements": self.elements,
+            "retention": self.retention,
+            "sqnr_db": self.sqnr_db,
+            "effect_snr_db": self.effect_snr_db,
+            "delta_to_weight_db": _db(self.delta_energy, self.weight_energy),
+            "saturated": self.saturated,
+            "seconds": self.seconds,
+        }
+
+
+def _db(signal: float, noise: float) -> float:
+    if noise <= 0:
+        return math.inf
+    return 10 * math.log10(signal / noise) if signal > 0 else -math.inf
+
+
+def _account(torch: Any, stats: Stats, form: int, before: dict[str, Tensor], after: dict[str, Tensor],
+             up: Tensor, down: Tensor, cols: int, gain: Tensor | None, more: Tensor | None,
+             began: float) -> None:  # fmt: skip
+    """One bake's sums into `stats` (`_account` and `_finish`, `internal/lora_bake.py:249-268,
+    528-534`): `cozyq_bake_stats`' per-group partials, added in group order on the host."""
+    data = after["data"]
+    partial = _ops(data).bake_stats(form, before, after, up, down, cols=cols, gain=gain, more=more)
+    sums = partial.cpu().sum(0).tolist()
+    stats.weight_energy += sums[0]
+    stats.delta_energy += sums[1]
+    stats.error_energy += sums[2]
+    stats.kept += sums[3]
+    stats.saturated += int(round(sums[4]))
+    stats.effect_energy += sums[5]
+    stats.effect_error += sums[6]
+    stats.elements += int(data.shape[0]) * cols
+    torch.cuda.synchronize(data.device)
+    stats.layers += 1
+    stats.seconds += time.perf_counter() - began
 
 
 def bakeable(scheme: str, params: Mapping[str, object], roles: Mapping[str, str]) -> bool:
@@ -144,20 +224,28 @@ def _more_rows(torch: Any, more: Dense | None, rows: int, rotated: bool) -> Tens
 
 
 def fused(torch: Any, stored: dict[str, Tensor], down: Tensor, up: Tensor, seed: int, *,
-          gain: Tensor | None = None, more: Dense | None = None, flags: int = 0) -> None:  # fmt: skip
+          gain: Tensor | None = None, more: Dense | None = None, flags: int = 0,
+          stats: Stats | None = None) -> None:  # fmt: skip
     """`bake`, one kernel launch (`internal/lora_bake.py:775-815`): each tile adds its
     `up @ down` (float32) to the decoded stored values and rounds them back in place. `gain`
-    (plain and nvfp4 rows), `more` and `flags` are the eager bake's additions."""
+    (plain and nvfp4 rows), `more` and `flags` are the eager bake's additions; `stats` takes the
+    bake's accounting from a copy of the weight before it."""
+    began = time.perf_counter()
     up32 = up.to(torch.float32).contiguous()
     down32 = down.to(torch.float32).contiguous()
     gain32 = None if gain is None else gain.to(torch.float32).reshape(-1).contiguous()
     if "scale_2" in stored:
         raw = stored["weight"].view(torch.uint8)
+        blocks = stored["scale"].view(torch.uint8)
         second = stored["scale_2"].to(torch.float32).reshape(1)
         rows = raw.shape[0]
-        _ops(raw).bake_nvfp4(raw, stored["scale"].view(torch.uint8), second, up32, down32,
-                             seed & SEED_MASK, gain=gain32, more=_more_rows(torch, more, rows, False),
-                             flags=flags)  # fmt: skip
+        more_rows = _more_rows(torch, more, rows, False)
+        before = None if stats is None else {"data": raw.clone(), "blocks": blocks.clone(), "second": second}
+        _ops(raw).bake_nvfp4(raw, blocks, second, up32, down32, seed & SEED_MASK, gain=gain32,
+                             more=more_rows, flags=flags)  # fmt: skip
+        if stats is not None:
+            after = {"data": raw, "blocks": blocks, "second": second}
+            _account(torch, stats, NVFP4, before, after, up32, down32, 2 * raw.shape[1], gain32, more_rows, began)
         return
     rotated = False
     if "value" in stored:
@@ -175,8 +263,15 @@ def fused(torch: Any, stored: dict[str, Tensor], down: Tensor, up: Tensor, seed:
         raise ValueError("a row-scaled bake keeps a contiguous float32 row scale")
     if scale is not None and gain32 is not None:
         raise ValueError("a row-scaled weight takes its gain in its scale")
-    _ops(data).bake(kind, data, scale, up32, down32, seed & SEED_MASK, gain=gain32,
-                    more=_more_rows(torch, more, data.shape[0], rotated), flags=flags)  # fmt: skip
+    more_rows = _more_rows(torch, more, data.shape[0], rotated)
+    before = None
+    if stats is not None:
+        before = {"data": data.clone()} if scale is None else {"data": data.clone(), "scale": scale}
+    _ops(data).bake(kind, data, scale, up32, down32, seed & SEED_MASK, gain=gain32, more=more_rows,
+                    flags=flags)  # fmt: skip
+    if stats is not None:
+        after = {"data": data} if scale is None else {"data": data, "scale": scale}
+        _account(torch, stats, kind, before, after, up32, down32, data.shape[1], gain32, more_rows, began)
 
 
 def bake(
@@ -205,24 +300,20 @@ def bake(
     if gain is not None and "value" not in stored and "scale_2" not in stored:
         stored["scale"].view(-1).mul_(gain)
         gain = None
-    if stats is not None:
-        raise NotImplementedError("cozyq's bake keeps no Stats (the reference's eager measurement)")
     if how not in ("fused", "eager", None):
         raise ValueError(f"no bake path {how!r}")
-    fused(torch, stored, down, up, seed, gain=gain, more=more)
+    fused(torch, stored, down, up, seed, gain=gain, more=more, stats=stats)
 
 
 ROUNDINGS = ("nearest", "stochastic", "feedback")
 GRIDS = ("keep", "refit", "regrid")
 
 
-def _rounding_flags(rounding: str, stats: Any, allowed: tuple[str, ...] = ("nearest", "stochastic")) -> int:
+def _rounding_flags(rounding: str, allowed: tuple[str, ...] = ("nearest", "stochastic")) -> int:
     if rounding not in ROUNDINGS:
         raise ValueError(f"no rounding {rounding!r}")
     if rounding not in allowed:
         raise NotImplementedError(f"cozyq bakes by nearest or stochastic rounding, not {rounding!r}")
-    if stats is not None:
-        raise NotImplementedError("cozyq's bake keeps no Stats (the reference's eager measurement)")
     return NEAREST if rounding == "nearest" else 0
 
 
@@ -241,11 +332,11 @@ def bake_plain(torch: Any, weight: Tensor, down: Tensor, up: Tensor, alpha: floa
     (`internal/lora_bake.py:271-305`); bf16 rounds stochastically on request, other dtypes to
     nearest. The noise is the Philox stream under `seed` (the reference's eager draws come from
     `generator`, which is not used here)."""
-    flags = _rounding_flags(rounding, stats)
+    flags = _rounding_flags(rounding)
     if weight.dtype != torch.bfloat16:
         flags = NEAREST
     fused(torch, {"value": weight}, down, _scaled_up(torch, up, alpha), seed, gain=gain, more=more,
-          flags=flags)  # fmt: skip
+          flags=flags, stats=stats)  # fmt: skip
 
 
 #: `bake_rowwise`'s floor of a refitted row scale and E4M3's largest value
@@ -264,11 +355,11 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
     eager law's order, and `scale` takes the new values."""
     if grid not in GRIDS:
         raise ValueError(f"no grid {grid!r}")
-    flags = _rounding_flags(rounding, stats)
+    flags = _rounding_flags(rounding)
     up_a = _scaled_up(torch, up, alpha)
     stored = {"weight": data, "scale": scale}
     if grid == "keep":
-        fused(torch, stored, down, up_a, seed, more=more, flags=flags)
+        fused(torch, stored, down, up_a, seed, more=more, flags=flags, stats=stats)
         return
     raw, scales = data.view(torch.uint8), scale.view(-1)
     if scales.dtype != torch.float32 or not scales.is_contiguous():
@@ -278,6 +369,8 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
     if more_rows is not None:
         raise NotImplementedError("cozyq refits rowwise scales from up @ down alone (no LoKr rows)")
     ops = _ops(raw)
+    began = time.perf_counter()
+    before = None if stats is None else {"data": raw.clone(), "scale": scales.clone()}
     amax = ops.bake_norms(ROWWISE, raw, scales, up32, down32, cols=raw.shape[1], amax=True)
     # amax / 448 as torch runs it on a GPU (the reference's eager bake included): times the float32
     # reciprocal, written out so that it does not depend on that detail.
@@ -288,6 +381,9 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
     new = new.contiguous()
     ops.bake(ROWWISE, raw, scales, up32, down32, seed & SEED_MASK, flags=flags, rescale=new)
     scales.copy_(new)
+    if stats is not None:
+        _account(torch, stats, ROWWISE, before, {"data": raw, "scale": scales}, up32, down32, raw.shape[1],
+                 None, None, began)  # fmt: skip
 
 
 def bake_int8_convrot(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tensor, alpha: float, *,
@@ -296,9 +392,9 @@ def bake_int8_convrot(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up:
     """Bake into `int8-convrot256/1` (`internal/lora_bake.py:372-423`): `down` and the dense
     rows rotated into the weight's basis, the row scale kept, nearest or stochastic floor,
     clamped to ±127."""
-    flags = _rounding_flags(rounding, stats)
+    flags = _rounding_flags(rounding)
     fused(torch, {"weight": data, "scale": scale}, down, _scaled_up(torch, up, alpha), seed, more=more,
-          flags=flags)  # fmt: skip
+          flags=flags, stats=stats)  # fmt: skip
 
 
 def bake_nvfp4(torch: Any, weight: Tensor, scale: Tensor, scale_2: Tensor, down: Tensor, up: Tensor,
@@ -311,15 +407,16 @@ def bake_nvfp4(torch: Any, weight: Tensor, scale: Tensor, scale_2: Tensor, down:
         raise ValueError(f"no grid {grid!r}")
     if grid != "keep":
         raise NotImplementedError("cozyq keeps nvfp4's levels (grid='keep')")
-    flags = _rounding_flags(rounding, stats)
+    flags = _rounding_flags(rounding)
     extra = gain is not None or more is not None or flags
     stored = {"weight": weight, "scale": scale, "scale_2": scale_2}
     if extra or rounding != "stochastic":
-        fused(torch, stored, down, _scaled_up(torch, up, alpha), seed, gain=gain, more=more, flags=flags)
+        fused(torch, stored, down, _scaled_up(torch, up, alpha), seed, gain=gain, more=more, flags=flags,
+              stats=stats)  # fmt: skip
     else:
         # Without additions the eager law's separate roundings still apply (`base + delta`).
         ones = torch.ones(weight.shape[0], dtype=torch.float32, device=weight.device)
-        fused(torch, stored, down, _scaled_up(torch, up, alpha), seed, gain=ones)
+        fused(torch, stored, down, _scaled_up(torch, up, alpha), seed, gain=ones, stats=stats)
 
 
 def warm(torch: Any, device: int) -> None:

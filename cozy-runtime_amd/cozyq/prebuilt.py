@@ -685,6 +685,27 @@ class Prebuilt:
         self._check(code, "the row reduction")
         return out
 
+    def bake_stats(self, form: int, before: dict[str, Tensor], after: dict[str, Tensor], up: Tensor,
+                   down: Tensor, *, cols: int, gain: Tensor | None = None,
+                   more: Tensor | None = None) -> Tensor:  # fmt: skip
+        """`cozyq_bake_stats` (`_account`, `internal/lora_bake.py:249-268`): the accounting of one
+        bake from its parts before and after (`data`, and `scale` or `blocks` + `second`), float64
+        [groups, 7] partial sums."""
+        data = after["data"]
+        rows = int(data.shape[0])
+        rank = self._factors(up, down, rows, cols, tuple(after.values()) + tuple(before.values()), gain, more)
+        if rank > 128:
+            raise ValueError("LoRA bake accounting: rank above 128")
+        partial = self.torch.empty((rows + 63) // 64, 7, dtype=self.torch.float64, device=data.device)
+        code = self._lib.cozyq_bake_stats(
+            self.index, form, before["data"].data_ptr(), data.data_ptr(), _ptr(before.get("scale")),
+            _ptr(after.get("scale")), _ptr(before.get("blocks")), _ptr(after.get("blocks")),
+            _ptr(after.get("second")), _ptr(gain), _ptr(more), up.data_ptr(), down.data_ptr(), rows,
+            cols, rank, partial.data_ptr(), self._stream(),
+        )  # fmt: skip
+        self._check(code, "the bake accounting")
+        return partial
+
     def rotate_factor(self, down: Tensor) -> Tensor:
         """`cozyq_bake_rotate_factor` (`rotate_factor`, `internal/lora_bake.py:366-369`): float32
         [rank, cols] times H256/16 per 256 columns, into a new tensor."""

@@ -490,6 +490,26 @@ int cozyq_bake_row_amax(int device, int form, const void* data, const float* sca
     return bake_rows(device, form, data, scale, blocks, second, up, down, rows, cols, rank, out, true, stream);
 }
 
+int cozyq_bake_stats(int device, int form, const void* before, const void* after, const float* scale_before,
+                     const float* scale_after, const uint8_t* blocks_before, const uint8_t* blocks_after,
+                     const float* second, const float* gain, const float* more, const float* up,
+                     const float* down, int64_t rows, int64_t cols, int64_t rank, double* partial, void* stream) {
+    if (form < cozyq::kBakeBf16 || form > cozyq::kBakeNvfp4 || !bake_shape(rows, cols, rank) || rank > 128 ||
+        (form == cozyq::kBakeNvfp4 && cols % 16))
+        return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    const bool scaled = form == cozyq::kBakeRowwise || form == cozyq::kBakeInt8;
+    if (!partial || (cols > 0 && (!before || !after)) || (scaled && (!scale_before || !scale_after)) ||
+        (form == cozyq::kBakeNvfp4 && (!blocks_before || !blocks_after || !second)) ||
+        (rank > 0 && cols > 0 && (!up || !down)))
+        return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    const cozyq::BakeStats st{before, after, scale_before, scale_after, blocks_before, blocks_after, second, gain, more};
+    return cozyq::bake_stats(form, st, up, down, static_cast<int>(rows), static_cast<int>(cols),
+                             static_cast<int>(rank), partial, on(stream));
+}
+
 void cozyq_host_e4m3(const float* in, uint8_t* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = cozyq::e4m3_rn(in[i]);
 }

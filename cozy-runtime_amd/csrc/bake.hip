@@ -436,6 +436,143 @@ __global__ __launch_bounds__(kBakeThreads) void bake_norms_kernel(const void* __
     }
 }
 
+// A bake's accounting (`Stats`, `_account`, internal/lora_bake.py:249-268): from the weight before
+// and after the bake and the same delta, per workgroup of 64 rows over every column tile in
+// order, float64 sums of |target|², |delta|², |stored − target|², (stored − base)·delta, the
+// saturated count, and the rank-space energies |delta @ downᵀ|², |(stored − target) @ downᵀ|²
+// (the projections accumulated per row and rank in LDS in tile order). target = base + delta,
+// both decoded as the eager reference decodes; `partial` receives kStatTerms doubles a workgroup.
+constexpr int kStatTerms = 7, kStatRanks = 128;
+
+struct StatsArgs {
+    const void* before;
+    const void* after;
+    const float* scale_before;
+    const float* scale_after;
+    const uint8_t* blocks_before;
+    const uint8_t* blocks_after;
+    const float* second;
+    const float* gain;
+    const float* more;
+};
+
+template <int kForm>
+__device__ __forceinline__ float stat_value(const void* data, const float* scale, const uint8_t* blocks, float level,
+                                            int64_t at, int row, int col, int cols) {
+    if constexpr (kForm == kBakeBf16) return widen<false>(static_cast<const uint16_t*>(data)[at]);
+    else if constexpr (kForm == kBakeF16) return widen<true>(static_cast<const uint16_t*>(data)[at]);
+    else if constexpr (kForm == kBakeF32) return static_cast<const float*>(data)[at];
+    else if constexpr (kForm == kBakeRowwise) return e4m3_sat(static_cast<const uint8_t*>(data)[at]) * scale[row];
+    else if constexpr (kForm == kBakeInt8) return static_cast<float>(static_cast<const int8_t*>(data)[at]) * scale[row];
+    else {
+        const uint32_t byte = static_cast<const uint8_t*>(data)[at >> 1];
+        const uint32_t code = (col & 1) ? (byte >> 4) : (byte & 15u);
+        return e2m1_of(code) * (e4m3_sat(blocks[static_cast<int64_t>(row) * (cols / 16) + col / 16]) * level);
+    }
+}
+
+template <int kForm>
+__global__ __launch_bounds__(kBakeThreads) void bake_stats_kernel(StatsArgs a, const float* __restrict__ up,
+                                                                  const float* __restrict__ down, int rows, int cols,
+                                                                  int rank, double* __restrict__ partial) {
+    __shared__ float up_lds[kRankChunk][kTileRows];
+    __shared__ float down_lds[kRankChunk][kTileCols];
+    __shared__ float proj[2][kTileRows][kStatRanks];  // delta and error projections, per row and rank
+    __shared__ double red[kBakeThreads / 64][kStatTerms];
+    const int row0 = blockIdx.x * kTileRows;
+    const int tid = threadIdx.x, rg = tid >> 4, cg = tid & 15;
+    for (int e = tid; e < 2 * kTileRows * kStatRanks; e += kBakeThreads) (&proj[0][0][0])[e] = 0.0f;
+    const float level = kForm == kBakeNvfp4 ? a.second[0] : 1.0f;
+    double sum[5] = {0.0, 0.0, 0.0, 0.0, 0.0};  // target², delta², error², kept, saturated
+    for (int col0 = 0; col0 < cols; col0 += kTileCols) {
+        float acc[4][8];
+        tile_delta(acc, up, down, rows, cols, rank, row0, col0, up_lds, down_lds);  // syncs before reuse
+        float dv[4][8], ev[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = row0 + 4 * rg + i;
+            const float gain = (kForm <= kBakeF32 || kForm == kBakeNvfp4) && a.gain && row < rows ? a.gain[row] : 1.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int col = col0 + tile_col(cg, j);
+                dv[i][j] = 0.0f;
+                ev[i][j] = 0.0f;
+                if (row >= rows || col >= cols) continue;
+                const int64_t at = static_cast<int64_t>(row) * cols + col;
+                float base = stat_value<kForm>(a.before, a.scale_before, a.blocks_before, level, at, row, col, cols);
+                if constexpr (kForm <= kBakeF32 || kForm == kBakeNvfp4) base = base * gain;
+                const float d = a.more ? acc[i][j] + a.more[at] : acc[i][j];
+                const float target = base + d;
+                const float stored = stat_value<kForm>(a.after, a.scale_after, a.blocks_after, level, at, row, col, cols);
+                const float err = stored - target;
+                sum[0] += static_cast<double>(target) * target;
+                sum[1] += static_cast<double>(d) * d;
+                sum[2] += static_cast<double>(err) * err;
+                sum[3] += static_cast<double>(stored - base) * static_cast<double>(d);
+                if constexpr (kForm == kBakeRowwise) {
+                    sum[4] += __builtin_fabsf(target / a.scale_after[row]) > 464.0f ? 1.0 : 0.0;
+                } else if constexpr (kForm == kBakeInt8) {
+                    const float code = static_cast<float>(static_cast<const int8_t*>(a.before)[at]);
+                    sum[4] += __builtin_fabsf(code + d / a.scale_before[row]) > 127.5f ? 1.0 : 0.0;
+                } else if constexpr (kForm == kBakeNvfp4) {
+                    const float unit = e4m3_sat(a.blocks_after[static_cast<int64_t>(row) * (cols / 16) + col / 16]) * level;
+                    sum[4] += unit > 0.0f && __builtin_fabsf(target / unit) > 6.0f ? 1.0 : 0.0;
+                }
+                dv[i][j] = d;
+                ev[i][j] = err;
+            }
+        }
+        // The projections onto down's rows: each lane's 8 columns, then the 16 lanes of a row group.
+        for (int r = 0; r < rank; ++r) {
+            float dcol[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int col = col0 + tile_col(cg, j);
+                dcol[j] = col < cols ? down[static_cast<int64_t>(r) * cols + col] : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float pd = 0.0f, pe = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    pd = __builtin_fmaf(dv[i][j], dcol[j], pd);
+                    pe = __builtin_fmaf(ev[i][j], dcol[j], pe);
+                }
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) {
+                    pd += __shfl_xor(pd, off);
+                    pe += __shfl_xor(pe, off);
+                }
+                if (cg == 0) {
+                    proj[0][4 * rg + i][r] += pd;
+                    proj[1][4 * rg + i][r] += pe;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    double effect = 0.0, effect_error = 0.0;
+    for (int e = tid; e < kTileRows * kStatRanks; e += kBakeThreads) {
+        const double pd = (&proj[0][0][0])[e], pe = (&proj[1][0][0])[e];
+        effect += pd * pd;
+        effect_error += pe * pe;
+    }
+    double terms[kStatTerms] = {sum[0], sum[1], sum[2], sum[3], sum[4], effect, effect_error};
+    const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+    for (int t = 0; t < kStatTerms; ++t) {
+        double v = terms[t];
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+        if (lane == 0) red[wave][t] = v;
+    }
+    __syncthreads();
+    if (tid < kStatTerms) {
+        double v = 0.0;
+        for (int w = 0; w < kBakeThreads / 64; ++w) v += red[w][tid];
+        partial[static_cast<int64_t>(blockIdx.x) * kStatTerms + tid] = v;
+    }
+}
+
 // `rotate_factor`: each 256 columns of `down` times the regular Hadamard H4⊗H4⊗H4⊗H4, one
 // 4-point stage per digit, outer digit (stride 64) first, each output evaluated left to right as
 // (a+b+c−d, a+b−c+d, a−b+c+d, b+c+d−a), then 1/16. Four 256-groups per workgroup.
@@ -534,6 +671,26 @@ hipError_t bake_norms(int form, const void* data, const float* scale, const uint
         case kBakeNvfp4: return launch_norms<kBakeNvfp4>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t bake_stats(int form, const BakeStats& st, const float* up, const float* down, int rows, int cols, int rank,
+                      double* partial, hipStream_t s) {
+    const StatsArgs a{st.before, st.after, st.scale_before, st.scale_after, st.blocks_before, st.blocks_after,
+                      st.second, st.gain, st.more};
+    const dim3 grid((rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
+#define COZYQ_STATS(F) \
+    case F: hipLaunchKernelGGL((bake_stats_kernel<F>), grid, block, 0, s, a, up, down, rows, cols, rank, partial); break;
+    switch (form) {
+        COZYQ_STATS(kBakeBf16)
+        COZYQ_STATS(kBakeF16)
+        COZYQ_STATS(kBakeF32)
+        COZYQ_STATS(kBakeRowwise)
+        COZYQ_STATS(kBakeInt8)
+        COZYQ_STATS(kBakeNvfp4)
+        default: return hipErrorInvalidValue;
+    }
+#undef COZYQ_STATS
+    return hipGetLastError();
 }
 
 hipError_t rotate_factor(const float* down, float* out, int64_t groups, hipStream_t s) {

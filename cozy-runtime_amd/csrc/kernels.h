@@ -176,6 +176,22 @@ hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const
 hipError_t bake_norms(int form, const void* data, const float* scale, const uint8_t* blocks, const float* second,
                       const float* up, const float* down, int rows, int cols, int rank, float* out, bool amax,
                       hipStream_t s);
+// A bake's accounting: the weight before and after (each form's parts), the same gain and dense
+// rows the bake took; partial receives 7 doubles per 64-row workgroup ([target², delta², error²,
+// kept, saturated, effect, effect error]). rank ≤ 128.
+struct BakeStats {
+    const void* before;
+    const void* after;
+    const float* scale_before;
+    const float* scale_after;
+    const uint8_t* blocks_before;
+    const uint8_t* blocks_after;
+    const float* second;
+    const float* gain;
+    const float* more;
+};
+hipError_t bake_stats(int form, const BakeStats& st, const float* up, const float* down, int rows, int cols, int rank,
+                      double* partial, hipStream_t s);
 // out = each 256-group of down times H256 / 16; `groups` = rank · cols / 256.
 hipError_t rotate_factor(const float* down, float* out, int64_t groups, hipStream_t s);
 

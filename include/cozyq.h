@@ -301,6 +301,19 @@ int cozyq_bake_row_amax(int device, int form, const void* data, const float* sca
                         const float* down, int64_t rows, int64_t cols, int64_t rank, float* out,
                         void* stream);
 
+/* A bake's accounting (reference: `Stats` and `_account`, internal/lora_bake.py:78-123,249-268):
+ * the weight's parts before and after a bake (`before` / `after`, and for form 3-4 the row
+ * scales, for form 5 the block bytes and `second`), with the gain, dense rows and factors the bake
+ * took (form 4: `down` and `more` rotated). target = base + delta, decoded as the eager reference
+ * decodes; partial receives 7 doubles per 64-row group, ceil(rows / 64) · 7 in all: Σ target²,
+ * Σ delta², Σ (stored − target)², Σ (stored − base)·delta, the saturated count, Σ (delta @ downᵀ)²
+ * and Σ ((stored − target) @ downᵀ)², each in a fixed order. rank ≤ 128. */
+int cozyq_bake_stats(int device, int form, const void* before, const void* after,
+                     const float* scale_before, const float* scale_after,
+                     const uint8_t* blocks_before, const uint8_t* blocks_after, const float* second,
+                     const float* gain, const float* more, const float* up, const float* down,
+                     int64_t rows, int64_t cols, int64_t rank, double* partial, void* stream);
+
 /* `down` [rank, cols] in an int8-convrot256/1 weight's basis (reference: `rotate_factor`,
  * internal/lora_bake.py:366-369): each 256 columns times the regular Hadamard H4⊗H4⊗H4⊗H4 in
  * the expression order of internal/encoding/formats.py:664-671, then 1/16; out [rank, cols]

@@ -385,3 +385,62 @@ def norms(form: int, data: np.ndarray, scale: np.ndarray | None, up: np.ndarray,
         value = (data.astype(np.float32) * scale.astype(np.float32).reshape(-1, 1)).astype(np.float32)
     target = (value + delta(up.astype(np.float32), down.astype(np.float32))).astype(np.float64)
     return np.sqrt((target * target).sum(axis=1)).astype(np.float32)
+
+
+def account(form: int, before: np.ndarray, after: np.ndarray, up: np.ndarray, down: np.ndarray, *,
+            scale_before: np.ndarray | None = None, scale_after: np.ndarray | None = None,
+            blocks_before: np.ndarray | None = None, blocks_after: np.ndarray | None = None,
+            second: float = 1.0, gain: np.ndarray | None = None,
+            more: np.ndarray | None = None) -> dict[str, float]:  # fmt: skip
+    """`_account` (`internal/lora_bake.py:249-268`) of one bake from the weight before and after:
+    base and stored decoded as the eager reference decodes, delta the FMA chain (plus `more`),
+    target = base + delta in float32, the sums in float64; saturation by each form's payload
+    (`|target / scale| > 464`, `|code + delta / scale| > 127.5`, `|target / unit| > 6`)."""
+    def decoded(data, scale, blocks):
+        if form == NVFP4:
+            rows, cols = data.shape[0], 2 * data.shape[1]
+            codes = np.stack((data & 15, data >> 4), axis=-1).reshape(rows, cols)
+            s = (e4m3_value(np.repeat(blocks.astype(np.int64), 16, axis=1)) * _F32(second)).astype(np.float32)
+            return (e2m1_value(codes) * s).astype(np.float32)
+        if form == BF16:
+            return (data.astype(np.uint32) << 16).view(np.float32)
+        if form == F16:
+            return data.view(np.float16).astype(np.float32)
+        if form == F32:
+            return data.astype(np.float32)
+        if form == ROWWISE:
+            return (e4m3_value(data) * scale.astype(np.float32).reshape(-1, 1)).astype(np.float32)
+        return (data.astype(np.float32) * scale.astype(np.float32).reshape(-1, 1)).astype(np.float32)
+
+    base = decoded(before, scale_before, blocks_before)
+    if gain is not None and form in (BF16, F16, F32, NVFP4):
+        base = (base * gain.astype(np.float32).reshape(-1, 1)).astype(np.float32)
+    d = delta(up.astype(np.float32), down.astype(np.float32))
+    if more is not None:
+        d = (d + more.astype(np.float32)).astype(np.float32)
+    target = (base + d).astype(np.float32)
+    stored = decoded(after, scale_after, blocks_after)
+    err = (stored - target).astype(np.float32)
+    if form == ROWWISE:
+        saturated = int((np.abs((target / scale_after.astype(np.float32).reshape(-1, 1)).astype(np.float32)) > 464).sum())
+    elif form == INT8:
+        payload = (before.astype(np.float32) + (d / scale_before.astype(np.float32).reshape(-1, 1)).astype(np.float32))
+        saturated = int((np.abs(payload.astype(np.float32)) > 127.5).sum())
+    elif form == NVFP4:
+        unit = np.repeat((e4m3_value(blocks_after.astype(np.int64)) * _F32(second)).astype(np.float32), 16, axis=1)
+        ratio = (target / np.where(unit > 0, unit, _F32(1))).astype(np.float32)
+        saturated = int(((unit > 0) & (np.abs(ratio) > 6)).sum())
+    else:
+        saturated = 0
+    basis = down.astype(np.float64).T
+    d64, e64 = d.astype(np.float64), err.astype(np.float64)
+    return {
+        "weight_energy": float((target.astype(np.float64) ** 2).sum()),
+        "delta_energy": float((d64 ** 2).sum()),
+        "error_energy": float((e64 ** 2).sum()),
+        "kept": float(((stored.astype(np.float64) - base.astype(np.float64)) * d64).sum()),
+        "saturated": saturated,
+        "effect_energy": float(((d64 @ basis) ** 2).sum()),
+        "effect_error": float(((e64 @ basis) ** 2).sum()),
+        "elements": int(target.size),
+    }

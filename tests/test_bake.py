@@ -350,11 +350,11 @@ def test_bake_refuses_what_it_does_not_build():
 
     value = torch.zeros(4, 8, dtype=torch.bfloat16)
     down, up = torch.zeros(2, 8), torch.zeros(4, 2)
-    with pytest.raises(NotImplementedError):
-        cb.bake(torch, {"value": value}, down, up, seed=1, stats=object())
+    with pytest.raises(ValueError, match="GPU"):
+        cb.bake(torch, {"value": value}, down, up, seed=1, stats=cb.Stats())
     with pytest.raises(ValueError, match="no bake path"):
         cb.bake(torch, {"value": value}, down, up, seed=1, how="triton")
-    for kwargs in ({}, {"how": "eager"}, {"gain": torch.ones(4)}, {"more": lambda a, b: None}):
+    for kwargs in ({}, {"how": "eager"}, {"gain": torch.ones(4)}, {"more": lambda a, b: torch.zeros(b - a, 8)}):
         with pytest.raises(ValueError, match="GPU"):
             cb.bake(torch, {"value": value}, down, up, seed=1, **kwargs)
     with pytest.raises(NotImplementedError):
@@ -822,8 +822,8 @@ def test_eager_entry_points_refuse_unbuilt_options():
         cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, grid="keep", rounding="feedback")
     with pytest.raises(NotImplementedError):
         cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit")
-    with pytest.raises(NotImplementedError):
-        cb.bake_plain(torch, t, down, up, 1.0, stats=object())
+    with pytest.raises(ValueError, match="GPU"):
+        cb.bake_plain(torch, t, down, up, 1.0, stats=cb.Stats())  # Stats: built
     with pytest.raises(ValueError):
         cb.bake_int8_convrot(torch, t, t, down, up, 1.0, rounding="up")
 
@@ -908,3 +908,61 @@ def test_gpu_bake_rowwise_new_grids(grid, rounding):
     torch.cuda.synchronize()
     assert np.array_equal(s.cpu().numpy().view(np.uint32), new.view(np.uint32))
     assert np.array_equal(w.view(torch.uint8).cpu().numpy(), want)
+
+
+def test_stats_properties():
+    from cozyq import bake as cb
+
+    st = cb.Stats(layers=1, elements=10, weight_energy=100.0, delta_energy=4.0, error_energy=1.0, kept=3.0,
+                  effect_energy=10.0, effect_error=0.1)  # fmt: skip
+    assert st.retention == 0.75 and st.sqnr_db == 20.0 and abs(st.effect_snr_db - 20.0) < 1e-12
+    other = cb.Stats(layers=2, elements=5, saturated=3)
+    st.add(other)
+    assert st.layers == 3 and st.elements == 15 and st.saturated == 3
+    assert cb.Stats().retention == 1.0 and cb.Stats().sqnr_db == float("inf")
+    assert set(st.document()) == {"layers", "elements", "retention", "sqnr_db", "effect_snr_db",
+                                  "delta_to_weight_db", "saturated", "seconds"}  # fmt: skip
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("form", [ob.BF16, ob.F16, ob.F32, ob.ROWWISE, ob.INT8, ob.NVFP4])
+def test_gpu_bake_stats_against_the_oracle(form):
+    """`bake(..., stats=Stats())`: the accounting kernel's sums against the oracle's `account`
+    over the same weight before and after (float64 sums: to 1e-9; the rank-space energies, whose
+    projections the kernel sums in float32, to 1e-4; the saturated count exactly)."""
+    from cozyq import bake as cb
+
+    rng = np.random.default_rng(700 + form)
+    rows, cols, rank, seed = 70, 256, 5, 41
+    up = (rng.standard_normal((rows, rank)) * (0.5 if form in (ob.ROWWISE, ob.INT8, ob.NVFP4) else 0.02)).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    stats = cb.Stats()
+    if form == ob.NVFP4:
+        codes, blocks = _nvfp4_stored(rows, cols, rng)
+        stored = {"weight": torch.from_numpy(codes).to(CUDA),
+                  "scale": torch.from_numpy(blocks).view(torch.float8_e4m3fn).to(CUDA),
+                  "scale_2": torch.tensor([0.03], device=CUDA)}  # fmt: skip
+        cb.bake(torch, stored, _cuda(down), _cuda(up), seed=seed, stats=stats)
+        want = ob.account(form, codes, stored["weight"].cpu().numpy(), up, down, blocks_before=blocks,
+                          blocks_after=stored["scale"].view(torch.uint8).cpu().numpy(), second=0.03)  # fmt: skip
+    else:
+        data, scale, _ = _stored_for(form, rows, cols, 701)
+        if form in (ob.BF16, ob.F16, ob.F32):
+            stored = {"value": _torch_data(form, data).to(CUDA)}
+            key = "value"
+        else:
+            w = torch.from_numpy(data).to(CUDA)
+            stored = {"weight": w.view(torch.float8_e4m3fn) if form == ob.ROWWISE else w, "scale": _cuda(scale)}
+            key = "weight"
+        cb.bake(torch, stored, _cuda(down), _cuda(up), seed=seed, stats=stats)
+        after = _bytes(stored[key]).view(data.dtype).reshape(data.shape)
+        used = ob.rotate_factor(down) if form == ob.INT8 else down
+        want = ob.account(form, data, after, up, used, scale_before=scale, scale_after=scale)
+    assert stats.layers == 1 and stats.elements == want["elements"] == rows * cols
+    assert stats.saturated == want["saturated"]
+    for name in ("weight_energy", "delta_energy", "error_energy", "kept"):
+        assert abs(getattr(stats, name) - want[name]) <= 1e-9 * max(abs(want[name]), 1e-30) + 1e-30, name
+    for name in ("effect_energy", "effect_error"):
+        assert abs(getattr(stats, name) - want[name]) <= 1e-4 * abs(want[name]) + 1e-12, name
+    if form in (ob.ROWWISE, ob.INT8):
+        assert stats.saturated > 0  # the large delta drives kept-scale payloads past the grid
