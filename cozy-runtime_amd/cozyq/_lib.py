@@ -92,6 +92,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cozyq_bake_norms": (
         c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]
     ),
+    "cozyq_bake_feedback": (c_int, [c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P]),
     "cozyq_bake_stats": (
         c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]
     ),

@@ -352,13 +352,16 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
     order, `decode + delta / scale`); `refit` sets each row's scale from its baked maximum,
     `max(amax / 448, 1e-12)`, and `regrid` raises that by 1/32 to 3/32 by the row's golden-ratio
     fraction, so every element rounds afresh: codes are `(decode · scale + delta) / new`, the
-    eager law's order, and `scale` takes the new values."""
+    eager law's order, and `scale` takes the new values. `feedback` rounding (any grid) rounds
+    those payloads to nearest with each 32-column run carrying its error (`encode_e4m3`,
+    `:163-197`), the same bytes on every bake."""
     if grid not in GRIDS:
         raise ValueError(f"no grid {grid!r}")
-    flags = _rounding_flags(rounding)
+    feedback = rounding == "feedback"
+    flags = 0 if feedback else _rounding_flags(rounding)
     up_a = _scaled_up(torch, up, alpha)
     stored = {"weight": data, "scale": scale}
-    if grid == "keep":
+    if grid == "keep" and not feedback:
         fused(torch, stored, down, up_a, seed, more=more, flags=flags, stats=stats)
         return
     raw, scales = data.view(torch.uint8), scale.view(-1)
@@ -367,19 +370,27 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
     up32, down32 = up_a.to(torch.float32).contiguous(), down.to(torch.float32).contiguous()
     more_rows = _more_rows(torch, more, raw.shape[0], False)
     if more_rows is not None:
-        raise NotImplementedError("cozyq refits rowwise scales from up @ down alone (no LoKr rows)")
+        raise NotImplementedError("cozyq refits or feeds back rowwise scales from up @ down alone (no LoKr rows)")
     ops = _ops(raw)
     began = time.perf_counter()
     before = None if stats is None else {"data": raw.clone(), "scale": scales.clone()}
-    amax = ops.bake_norms(ROWWISE, raw, scales, up32, down32, cols=raw.shape[1], amax=True)
-    # amax / 448 as torch runs it on a GPU (the reference's eager bake included): times the float32
-    # reciprocal, written out so that it does not depend on that detail.
-    new = (amax * (1.0 / E4M3_MAX)).clamp(min=ROW_SCALE_FLOOR)
+    if grid == "keep":
+        new = scales.clone()
+    else:
+        amax = ops.bake_norms(ROWWISE, raw, scales, up32, down32, cols=raw.shape[1], amax=True)
+        # amax / 448 as torch runs it on a GPU (the reference's eager bake included): times the
+        # float32 reciprocal, written out so that it does not depend on that detail.
+        new = (amax * (1.0 / E4M3_MAX)).clamp(min=ROW_SCALE_FLOOR)
     if grid == "regrid":
         row = torch.arange(raw.shape[0], device=raw.device, dtype=torch.float32)
         new = new * (1 + (1 + 2 * torch.frac(row * 0.6180339887)) / 32)
     new = new.contiguous()
-    ops.bake(ROWWISE, raw, scales, up32, down32, seed & SEED_MASK, flags=flags, rescale=new)
+    if feedback:
+        # Each element's nearest-rounding error carried into the next of its 32-column run, the
+        # eager law's order `(decode · scale + delta) / new` on every grid, `keep`'s included.
+        ops.bake_feedback(raw, scales, up32, down32, new)
+    else:
+        ops.bake(ROWWISE, raw, scales, up32, down32, seed & SEED_MASK, flags=flags, rescale=new)
     scales.copy_(new)
     if stats is not None:
         _account(torch, stats, ROWWISE, before, {"data": raw, "scale": scales}, up32, down32, raw.shape[1],

@@ -650,6 +650,21 @@ class Prebuilt:
         )  # fmt: skip
         self._check(code, "the LoRA bake")
 
+    def bake_feedback(self, data: Tensor, scale: Tensor, up: Tensor, down: Tensor, fresh: Tensor) -> None:
+        """`cozyq_bake_feedback` in place (`encode_e4m3` with `feedback` under `bake_rowwise`,
+        `internal/lora_bake.py:163-197`, `:319-363`): `data` contiguous E4M3 [rows, cols],
+        `scale` its float32 row scales, `fresh` float32 [rows] the scales after the bake (the
+        same values for `keep`); every 32-column run carries its nearest-rounding error."""
+        rows, cols = (int(v) for v in data.shape)
+        rank = self._factors(up, down, rows, cols, (data, scale))
+        if fresh.dtype != self.torch.float32 or fresh.numel() != rows or not fresh.is_contiguous():
+            raise ValueError(f"LoRA bake: new row scales must be contiguous float32 with {rows} values")
+        code = self._lib.cozyq_bake_feedback(
+            self.index, data.data_ptr(), scale.data_ptr(), fresh.data_ptr(), up.data_ptr(),
+            down.data_ptr(), rows, cols, rank, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the error-feedback LoRA bake")
+
     def bake_nvfp4(self, data: Tensor, blocks: Tensor, second: Tensor, up: Tensor, down: Tensor,
                    seed: int, *, gain: Tensor | None = None, more: Tensor | None = None,
                    flags: int = 0) -> None:  # fmt: skip

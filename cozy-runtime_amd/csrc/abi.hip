@@ -490,6 +490,17 @@ int cozyq_bake_row_amax(int device, int form, const void* data, const float* sca
     return bake_rows(device, form, data, scale, blocks, second, up, down, rows, cols, rank, out, true, stream);
 }
 
+int cozyq_bake_feedback(int device, uint8_t* data, const float* scale, const float* fresh, const float* up,
+                        const float* down, int64_t rows, int64_t cols, int64_t rank, void* stream) {
+    if (!bake_shape(rows, cols, rank)) return hipErrorInvalidValue;
+    if (rows == 0 || cols == 0) return hipSuccess;
+    if (!data || !scale || !fresh || (rank > 0 && (!up || !down))) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::bake_feedback(data, scale, fresh, up, down, static_cast<int>(rows), static_cast<int>(cols),
+                                static_cast<int>(rank), on(stream));
+}
+
 int cozyq_bake_stats(int device, int form, const void* before, const void* after, const float* scale_before,
                      const float* scale_after, const uint8_t* blocks_before, const uint8_t* blocks_after,
                      const float* second, const float* gain, const float* more, const float* up,

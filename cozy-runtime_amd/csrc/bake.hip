@@ -295,6 +295,66 @@ __global__ __launch_bounds__(kBakeThreads) void bake_kernel(typename Stored<kFor
     }
 }
 
+// `bake_rowwise` with error feedback (internal/lora_bake.py:163-197 `encode_e4m3`, `feedback`):
+// each row's payloads `(e4m3·scale + delta) / new` round to nearest, each element's rounding
+// error carried into the next element of its 32-column run (a run's sum kept without a draw).
+// The tile's payloads go through LDS, one lane walks each (row, run) in column order, and the
+// codes come back through LDS to the lanes that own them. `fresh` is each row's scale after the
+// bake (the kept one, or `refit` / `regrid`'s).
+constexpr int kFeedbackRun = 32;
+
+__global__ __launch_bounds__(kBakeThreads) void bake_feedback_kernel(uint8_t* __restrict__ data,
+                                                                     const float* __restrict__ scale,
+                                                                     const float* __restrict__ fresh,
+                                                                     const float* __restrict__ up,
+                                                                     const float* __restrict__ down, int rows,
+                                                                     int cols, int rank) {
+    __shared__ float up_lds[kRankChunk][kTileRows];
+    __shared__ float down_lds[kRankChunk][kTileCols];
+    __shared__ float stage[kTileRows][kTileCols + 1];
+    const int row0 = blockIdx.y * kTileRows, col0 = blockIdx.x * kTileCols;
+    float acc[4][8];
+    tile_delta(acc, up, down, rows, cols, rank, row0, col0, up_lds, down_lds);
+    const int rg = threadIdx.x >> 4, cg = threadIdx.x & 15;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int rl = 4 * rg + i, row = row0 + rl;
+        const float unit = row < rows ? scale[row] : 1.0f, now = row < rows ? fresh[row] : 1.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int cl = tile_col(cg, j), col = col0 + cl;
+            float payload = 0.0f;  // columns past the end pad the run with zeros
+            if (row < rows && col < cols)
+                payload = (e4m3_sat(data[static_cast<int64_t>(row) * cols + col]) * unit + acc[i][j]) / now;
+            stage[rl][cl] = payload;
+        }
+    }
+    __syncthreads();
+    {
+        const int rl = threadIdx.x >> 2, run = threadIdx.x & 3;  // 64 rows x 4 runs
+        float carry = 0.0f;
+        for (int k = 0; k < kFeedbackRun; ++k) {
+            const int cl = run * kFeedbackRun + k;
+            const float want = stage[rl][cl] + carry;
+            const uint32_t code = e4m3_nearest(want);
+            const float kept = e4m3_sat(code & 127u);
+            carry = want - (code >= 128u ? -kept : kept);
+            stage[rl][cl] = float_of(code);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int rl = 4 * rg + i, row = row0 + rl;
+        if (row >= rows) continue;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int cl = tile_col(cg, j), col = col0 + cl;
+            if (col < cols) data[static_cast<int64_t>(row) * cols + col] = static_cast<uint8_t>(bits_of(stage[rl][cl]));
+        }
+    }
+}
+
 // `_bake_nvfp4_kernel`: codes [rows, cols/2] (element 2k in the low nibble), E4M3 block bytes
 // [rows, cols/16], the float32 second level at `second`; cols % 16 == 0. A 16-column block is
 // the four lanes cg = 4q .. 4q+3 of one half-row, so its maximum is a DPP quad reduction; every
@@ -671,6 +731,13 @@ hipError_t bake_norms(int form, const void* data, const float* scale, const uint
         case kBakeNvfp4: return launch_norms<kBakeNvfp4>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t bake_feedback(uint8_t* data, const float* scale, const float* fresh, const float* up, const float* down,
+                         int rows, int cols, int rank, hipStream_t s) {
+    const dim3 grid((cols + kTileCols - 1) / kTileCols, (rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
+    hipLaunchKernelGGL(bake_feedback_kernel, grid, block, 0, s, data, scale, fresh, up, down, rows, cols, rank);
+    return hipGetLastError();
 }
 
 hipError_t bake_stats(int form, const BakeStats& st, const float* up, const float* down, int rows, int cols, int rank,

@@ -176,6 +176,10 @@ hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const
 hipError_t bake_norms(int form, const void* data, const float* scale, const uint8_t* blocks, const float* second,
                       const float* up, const float* down, int rows, int cols, int rank, float* out, bool amax,
                       hipStream_t s);
+// fp8.rowwise with error feedback: codes from (e4m3·scale + delta) / fresh rounded to nearest
+// with each run of 32 columns carrying its rounding error; fresh = the rows' scales after.
+hipError_t bake_feedback(uint8_t* data, const float* scale, const float* fresh, const float* up, const float* down,
+                         int rows, int cols, int rank, hipStream_t s);
 // A bake's accounting: the weight before and after (each form's parts), the same gain and dense
 // rows the bake took; partial receives 7 doubles per 64-row workgroup ([target², delta², error²,
 // kept, saturated, effect, effect error]). rank ≤ 128.

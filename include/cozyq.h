@@ -301,6 +301,16 @@ int cozyq_bake_row_amax(int device, int form, const void* data, const float* sca
                         const float* down, int64_t rows, int64_t cols, int64_t rank, float* out,
                         void* stream);
 
+/* An fp8.rowwise bake with error feedback (reference: `encode_e4m3(..., "feedback")`,
+ * internal/lora_bake.py:163-197, under `bake_rowwise`): payload (e4m3·scale + delta) / fresh
+ * (fresh = each row's scale after the bake: the kept one or a refitted one), each element
+ * rounded to nearest E4M3 (saturating at 448) with the rounding error of the element before it
+ * in its run of 32 columns added first; runs start at column multiples of 32. No noise. data
+ * [rows, cols] E4M3 bytes in place; the caller stores `fresh` as the new scale. */
+int cozyq_bake_feedback(int device, uint8_t* data, const float* scale, const float* fresh,
+                        const float* up, const float* down, int64_t rows, int64_t cols,
+                        int64_t rank, void* stream);
+
 /* A bake's accounting (reference: `Stats` and `_account`, internal/lora_bake.py:78-123,249-268):
  * the weight's parts before and after a bake (`before` / `after`, and for form 3-4 the row
  * scales, for form 5 the block bytes and `second`), with the gain, dense rows and factors the bake

@@ -336,6 +336,40 @@ def bake_nvfp4(data: np.ndarray, blocks: np.ndarray, second: float, up: np.ndarr
     return packed, block.astype(np.uint8)
 
 
+FEEDBACK_RUN = 32
+
+
+def e4m3_feedback(payload: np.ndarray) -> np.ndarray:
+    """`encode_e4m3` with `feedback` (`internal/lora_bake.py:163-197`): `[rows, cols]` float32
+    payloads → E4M3 bytes, the columns padded with zeros to runs of 32; along each run the
+    carried error (from +0) is added before `e4m3_nearest`, and the new carry is that sum minus
+    the stored signed magnitude, all in float32."""
+    payload = np.asarray(payload, dtype=np.float32)
+    rows, cols = payload.shape
+    pad = -cols % FEEDBACK_RUN
+    runs = np.pad(payload, ((0, 0), (0, pad))).reshape(rows, -1, FEEDBACK_RUN)
+    out = np.empty(runs.shape, dtype=np.uint8)
+    carry = np.zeros(runs.shape[:2], dtype=np.float32)
+    for k in range(FEEDBACK_RUN):
+        want = (runs[..., k] + carry).astype(np.float32)
+        code = e4m3_nearest(want)
+        out[..., k] = code
+        stored = e4m3_value(code & 0x7F)
+        carry = (want - np.where(code >= 0x80, -stored, stored)).astype(np.float32)
+    return out.reshape(rows, -1)[:, :cols]
+
+
+def bake_feedback(data: np.ndarray, scale: np.ndarray, up: np.ndarray, down: np.ndarray,
+                  fresh: np.ndarray) -> np.ndarray:
+    """`bake_rowwise` with `feedback` rounding (`internal/lora_bake.py:319-363`): payloads
+    `(decode · scale + delta) / fresh` (`fresh` the row scales after the bake, `scale` itself for
+    `keep`) through `e4m3_feedback`."""
+    d = delta(up.astype(np.float32), down.astype(np.float32))
+    unit = scale.astype(np.float32).reshape(-1, 1)
+    target = ((e4m3_value(data) * unit).astype(np.float32) + d).astype(np.float32)
+    return e4m3_feedback((target / fresh.astype(np.float32).reshape(-1, 1)).astype(np.float32))
+
+
 def row_amax(data: np.ndarray, scale: np.ndarray, up: np.ndarray, down: np.ndarray) -> np.ndarray:
     """An fp8.rowwise weight's row maxima of |decode · scale + up @ down|, float32 — the amax
     `bake_rowwise`'s `refit` takes (`internal/lora_bake.py:344-346`)."""

@@ -818,8 +818,11 @@ def test_eager_entry_points_refuse_unbuilt_options():
         cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0)  # default grid "refit": built
     with pytest.raises(ValueError, match="no grid"):
         cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, grid="wide")
+    with pytest.raises(ValueError, match="GPU"):
+        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, grid="keep", rounding="feedback")  # built
     with pytest.raises(NotImplementedError):
-        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, grid="keep", rounding="feedback")
+        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, rounding="feedback",
+                        more=lambda a, b: torch.zeros(b - a, 16))  # fmt: skip
     with pytest.raises(NotImplementedError):
         cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit")
     with pytest.raises(ValueError, match="GPU"):
@@ -910,6 +913,39 @@ def test_gpu_bake_rowwise_new_grids(grid, rounding):
     assert np.array_equal(w.view(torch.uint8).cpu().numpy(), want)
 
 
+def test_feedback_known_run():
+    """A run of 10.4s where E4M3's step is 1 (8..16): the carry cycles 0.4, -0.2, 0.2, -0.4, 0,
+    so the codes repeat 10, 11, 10, 11, 10 and every five of them sum to 52 = 5 · 10.4; the
+    34th column starts a new run (carry from zero)."""
+    got = ob.e4m3_value(ob.e4m3_feedback(np.full((1, 34), 10.4, np.float32)))[0]
+    assert got[:30].tolist() == [10, 11, 10, 11, 10] * 6
+    assert got[32:].tolist() == [10, 11]
+    neg = ob.e4m3_value(ob.e4m3_feedback(np.full((1, 5), -10.4, np.float32)))[0]
+    assert neg.tolist() == [-10, -11, -10, -11, -10]
+
+
+def test_feedback_keeps_run_sums():
+    """Payloads already on the grid come back unchanged; off the grid, each run's stored sum
+    stays within half a step (of the last element) of the payloads' sum, where rounding each
+    element alone drifts by many steps on a biased run; ragged columns pad the last run."""
+    grid = _e4m3_magnitudes()
+    rng = np.random.default_rng(5)
+    on = np.where(rng.random((9, 70)) < 0.5, -1, 1) * grid[rng.integers(0, 127, (9, 70))]
+    on = on.astype(np.float32)
+    assert np.array_equal(ob.e4m3_value(ob.e4m3_feedback(on)), on)
+    payload = (rng.random((40, 200)) * 0.4 + 20.3).astype(np.float32)  # step 2 between 16 and 32
+    fb = ob.e4m3_value(ob.e4m3_feedback(payload)).astype(np.float64)
+    near = ob.e4m3_value(ob.e4m3_nearest(payload)).astype(np.float64)
+    for start in range(0, 200, 32):
+        stop = min(start + 32, 200)
+        want = payload[:, start:stop].astype(np.float64).sum(1)
+        assert (np.abs(fb[:, start:stop].sum(1) - want) <= 1.0 + 1e-3).all()
+        if stop - start == 32:
+            assert (np.abs(near[:, start:stop].sum(1) - want) > 8).all()
+    sat = ob.e4m3_value(ob.e4m3_feedback(np.full((1, 3), 500.0, np.float32)))[0]
+    assert sat.tolist() == [448, 448, 448]
+
+
 def test_stats_properties():
     from cozyq import bake as cb
 
@@ -966,3 +1002,30 @@ def test_gpu_bake_stats_against_the_oracle(form):
         assert abs(getattr(stats, name) - want[name]) <= 1e-4 * abs(want[name]) + 1e-12, name
     if form in (ob.ROWWISE, ob.INT8):
         assert stats.saturated > 0  # the large delta drives kept-scale payloads past the grid
+
+
+
+FEEDBACK_SHAPES = [(70, 300, 6), (129, 257, 33), (1, 1, 1), (64, 128, 0), (3, 40, 128)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("grid", ["keep", "refit", "regrid"])
+@pytest.mark.parametrize("rows,cols,rank", FEEDBACK_SHAPES)
+def test_gpu_bake_rowwise_feedback(grid, rows, cols, rank):
+    """`bake_rowwise(rounding="feedback")`: every code and new scale bit-exact against the oracle
+    (`keep` with a delta large enough to saturate rows)."""
+    from cozyq import bake as cb
+
+    data, scale, rng = _stored_for(ob.ROWWISE, rows, cols, 61 + rank)
+    up = (rng.standard_normal((rows, rank)) * (3.0 if grid == "keep" else 0.05)).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    new = scale if grid == "keep" else ob.refit_scales(ob.row_amax(data, scale, up, down), grid == "regrid")
+    want = ob.bake_feedback(data, scale, up, down, new)
+    w = torch.from_numpy(data).view(torch.float8_e4m3fn).to(CUDA)
+    s = _cuda(scale)
+    cb.bake_rowwise(torch, w, s, _cuda(down), _cuda(up), 1.0, rounding="feedback", grid=grid)
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), new.view(np.uint32))
+    got = w.view(torch.uint8).cpu().numpy()
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} codes differ, first at {bad[0].tolist()}"
