@@ -8,7 +8,7 @@ falls back to anything: a missing or unloadable library raises `KernelsAbsent` w
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_float, c_int, c_int64, c_uint32, c_void_p
+from ctypes import c_double, c_float, c_int, c_int64, c_uint32, c_void_p
 from pathlib import Path
 
 PATH = Path(__file__).resolve().parent / "libcozyq.so"
@@ -92,6 +92,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cozyq_bake_norms": (
         c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]
     ),
+    "cozyq_bake_nvfp4_refit": (c_int, [c_int, _P, _P, _P, c_double, _P, _P, c_int64, c_int64, c_int64, c_uint32, c_int, _P]),
     "cozyq_bake_feedback": (c_int, [c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P]),
     "cozyq_bake_stats": (
         c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]

@@ -412,13 +412,18 @@ def bake_nvfp4(torch: Any, weight: Tensor, scale: Tensor, scale_2: Tensor, down:
                alpha: float, *, rounding: str = "stochastic", grid: str = "keep", generator: Any = None,
                stats: Any = None, more: Dense | None = None, gain: Tensor | None = None,
                seed: int = 0) -> None:  # fmt: skip
-    """Bake into canonical `nvfp4` (`internal/lora_bake.py:458-525`) with `keep`: the second level
-    kept and a block's scale refitted only past 7/6 of it. `refit` is not built."""
+    """Bake into canonical `nvfp4` (`internal/lora_bake.py:458-525`). `keep`: the second level
+    kept and a block's scale refitted only past 7/6 of it. `refit`: the second level set from
+    the baked tensor's amax and every block's scale from its own, saturation-free."""
     if grid not in GRIDS:
         raise ValueError(f"no grid {grid!r}")
-    if grid != "keep":
-        raise NotImplementedError("cozyq keeps nvfp4's levels (grid='keep')")
+    if grid == "regrid":
+        raise NotImplementedError("cozyq bakes nvfp4 on grid 'keep' or 'refit'")
     flags = _rounding_flags(rounding)
+    if grid == "refit":
+        _bake_nvfp4_refit(torch, weight, scale, scale_2, down, up, alpha, flags=flags, seed=seed, stats=stats,
+                          more=more, gain=gain)  # fmt: skip
+        return
     extra = gain is not None or more is not None or flags
     stored = {"weight": weight, "scale": scale, "scale_2": scale_2}
     if extra or rounding != "stochastic":
@@ -428,6 +433,31 @@ def bake_nvfp4(torch: Any, weight: Tensor, scale: Tensor, scale_2: Tensor, down:
         # Without additions the eager law's separate roundings still apply (`base + delta`).
         ones = torch.ones(weight.shape[0], dtype=torch.float32, device=weight.device)
         fused(torch, stored, down, _scaled_up(torch, up, alpha), seed, gain=ones, stats=stats)
+
+
+def _bake_nvfp4_refit(torch: Any, weight: Tensor, scale: Tensor, scale_2: Tensor, down: Tensor, up: Tensor,
+                      alpha: float, *, flags: int, seed: int, stats: Any, more: Dense | None,
+                      gain: Tensor | None) -> None:  # fmt: skip
+    """`bake_nvfp4(grid="refit")` (`internal/lora_bake.py:495-525`): the baked tensor's amax (the
+    row maxima of `cozyq_bake_row_amax`, then their maximum) sets the new second level
+    `amax / 2688` in float64 (1 for all zeros), and one launch refits every block on it."""
+    if gain is not None or more is not None or stats is not None:
+        raise NotImplementedError("cozyq refits nvfp4 from up @ down alone (no gain, LoKr rows or Stats)")
+    raw, blocks = weight.view(torch.uint8), scale.view(torch.uint8)
+    rows, cols = int(raw.shape[0]), 2 * int(raw.shape[1])
+    up32 = _scaled_up(torch, up, alpha).to(torch.float32).contiguous()
+    down32 = down.to(torch.float32).contiguous()
+    second = scale_2.to(torch.float32).reshape(-1)[:1].contiguous()
+    ops = _ops(raw)
+    stored_second = float(second[0])
+    amax = 0.0
+    if rows and cols:
+        amax = float(ops.bake_norms(NVFP4, raw, None, up32, down32, cols=cols, blocks=blocks, second=second,
+                                    amax=True).max())  # fmt: skip
+    level = amax / (E4M3_MAX * 6.0) if amax > 0 else 1.0
+    ops.bake_nvfp4_refit(raw, blocks, second, up32, down32, seed & SEED_MASK, level, flags=flags)
+    if level != stored_second:
+        scale_2.copy_(torch.full_like(scale_2, level))
 
 
 def warm(torch: Any, device: int) -> None:

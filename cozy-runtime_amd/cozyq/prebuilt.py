@@ -650,6 +650,21 @@ class Prebuilt:
         )  # fmt: skip
         self._check(code, "the LoRA bake")
 
+    def bake_nvfp4_refit(self, data: Tensor, blocks: Tensor, second: Tensor, up: Tensor, down: Tensor,
+                         seed: int, level: float, *, flags: int = 0) -> None:  # fmt: skip
+        """`cozyq_bake_nvfp4_refit` in place (`bake_nvfp4` with `grid="refit"`,
+        `internal/lora_bake.py:458-525`): decodes at `second`, refits every block on the new
+        second level `level` (a float64 the caller then stores), `flags` 1 for nearest."""
+        rows, cols = int(data.shape[0]), 2 * int(data.shape[1])
+        if tuple(blocks.shape) != (rows, cols // 16) or not blocks.is_contiguous():
+            raise ValueError(f"nvfp4 bake: block scales must be contiguous [{rows}, {cols // 16}]")
+        rank = self._factors(up, down, rows, cols, (data, blocks, second))
+        code = self._lib.cozyq_bake_nvfp4_refit(
+            self.index, data.data_ptr(), blocks.data_ptr(), second.data_ptr(), float(level), up.data_ptr(),
+            down.data_ptr(), rows, cols, rank, seed & 0xFFFFFFFF, flags, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the nvfp4 refit LoRA bake")
+
     def bake_feedback(self, data: Tensor, scale: Tensor, up: Tensor, down: Tensor, fresh: Tensor) -> None:
         """`cozyq_bake_feedback` in place (`encode_e4m3` with `feedback` under `bake_rowwise`,
         `internal/lora_bake.py:163-197`, `:319-363`): `data` contiguous E4M3 [rows, cols],

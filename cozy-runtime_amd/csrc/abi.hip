@@ -461,6 +461,23 @@ int cozyq_bake_nvfp4(int device, uint8_t* data, uint8_t* blocks, const float* se
                              static_cast<int>(rows), static_cast<int>(cols), static_cast<int>(rank), seed, on(stream));
 }
 
+int cozyq_bake_nvfp4_refit(int device, uint8_t* data, uint8_t* blocks, const float* second, double level,
+                           const float* up, const float* down, int64_t rows, int64_t cols, int64_t rank,
+                           uint32_t seed, int flags, void* stream) {
+    if (!bake_shape(rows, cols, rank) || cols % 16 || (flags & ~cozyq::kBakeNearest) || !(level > 0.0) ||
+        !(level < 3.4e38))
+        return hipErrorInvalidValue;
+    if (rows == 0 || cols == 0) return hipSuccess;
+    if (!data || !blocks || !second || (rank > 0 && (!up || !down))) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    cozyq::BakeOptions o{nullptr, nullptr, flags, nullptr};
+    o.refit = true;
+    o.level = level;
+    return cozyq::bake_nvfp4(data, blocks, second, up, down, o, static_cast<int>(rows), static_cast<int>(cols),
+                             static_cast<int>(rank), seed, on(stream));
+}
+
 static int bake_rows(int device, int form, const void* data, const float* scale, const uint8_t* blocks,
                      const float* second, const float* up, const float* down, int64_t rows, int64_t cols,
                      int64_t rank, float* out, bool amax, void* stream) {

@@ -184,6 +184,9 @@ struct Extra {
     const float* more;
     bool nearest, no_delta;
     const float* rescale;  // ROWWISE: each row's new scale (`refit` / `regrid`), or null to keep
+    // nvfp4 `refit`: every block's scale refitted to peak·need_inv on the new second level
+    bool refit;
+    float level, need_inv;
 };
 
 // One element of a `_bake_kernel` form: the stored value (its bits), the delta, the row's unit
@@ -407,17 +410,24 @@ __global__ __launch_bounds__(kBakeThreads) void bake_nvfp4_kernel(uint8_t* __res
             }
             peak = __builtin_fmaxf(peak, dpp_f32<0xB1>(peak));  // quad_perm [1,0,3,2]
             peak = __builtin_fmaxf(peak, dpp_f32<0x4E>(peak));  // quad_perm [2,3,0,1]
-            const float need = peak / (6.0f * level);
-            const bool grown = need * 6.0f > e4m3_sat(kept) * 7.0f;
-            const uint32_t block = grown ? e4m3_at_least(need) : kept;
-            const float unit = e4m3_sat(block) * level;
+            uint32_t block;
+            float unit;
+            if (kExtra && x.refit) {
+                block = e4m3_at_least(peak * x.need_inv);
+                unit = e4m3_sat(block) * x.level;
+            } else {
+                const float need = peak / (6.0f * level);
+                const bool grown = need * 6.0f > e4m3_sat(kept) * 7.0f;
+                block = grown ? e4m3_at_least(need) : kept;
+                unit = e4m3_sat(block) * level;
+            }
             const float den = unit > 0.0f ? unit : 1.0f;
             const uint32_t at = static_cast<uint32_t>(static_cast<uint64_t>(row) * static_cast<uint64_t>(cols) + col);
             uint32_t out = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t stored = (codes >> (4 * e)) & 15u;
-                const float payload = target[e] / den;
+                const float payload = kExtra && x.refit && unit == 0.0f ? 0.0f : target[e] / den;
                 uint32_t nibble;
                 if (kExtra && x.nearest) nibble = e2m1_nearest(payload);
                 else nibble = e2m1_stochastic(payload, uniform(philox_word(at + e, seed, k1)));
@@ -711,8 +721,15 @@ hipError_t bake(int form, void* data, const float* scale, const float* up, const
 hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const float* up, const float* down,
                       const BakeOptions& o, int rows, int cols, int rank, uint32_t seed, hipStream_t s) {
     const dim3 grid((cols + kTileCols - 1) / kTileCols, (rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
-    const Extra x{o.gain, o.more, (o.flags & kBakeNearest) != 0, (o.flags & kBakeNoDelta) != 0, nullptr};
-    if (o.gain || o.more || o.flags)
+    Extra x{o.gain, o.more, (o.flags & kBakeNearest) != 0, (o.flags & kBakeNoDelta) != 0, nullptr, false, 0.0f, 0.0f};
+    if (o.refit) {
+        // The reference's float64 second level, stored as float32; a block's need is its peak
+        // over 6·second as torch divides by a Python scalar: times the float32 reciprocal.
+        x.refit = true;
+        x.level = static_cast<float>(o.level);
+        x.need_inv = 1.0f / static_cast<float>(6.0 * o.level);
+    }
+    if (o.gain || o.more || o.flags || o.refit)
         hipLaunchKernelGGL((bake_nvfp4_kernel<true>), grid, block, 0, s, data, blocks, second, up, down, x, rows, cols, rank, seed);
     else
         hipLaunchKernelGGL((bake_nvfp4_kernel<false>), grid, block, 0, s, data, blocks, second, up, down, x, rows, cols, rank, seed);

@@ -163,6 +163,8 @@ struct BakeOptions {
     const float* more;
     int flags;
     const float* rescale;  // kBakeRowwise: each row's new scale [rows] (`refit`, `regrid`); null keeps
+    bool refit = false;    // kBakeNvfp4: every block refitted on the new second level `level`
+    double level = 0.0;
 };
 // data [rows, cols] of the form, scale float32 [rows] (kBakeRowwise, kBakeInt8), up float32
 // [rows, rank], down float32 [rank, cols] (kBakeInt8: already rotated), the 32-bit seed.

@@ -301,6 +301,17 @@ int cozyq_bake_row_amax(int device, int form, const void* data, const float* sca
                         const float* down, int64_t rows, int64_t cols, int64_t rank, float* out,
                         void* stream);
 
+/* An nvfp4 bake with `grid="refit"` (reference: `bake_nvfp4`, internal/lora_bake.py:458-525):
+ * the target decodes at the stored `second` level (e2m1·(e4m3(block)·second), plus delta); every
+ * block's scale becomes the least E4M3 code at or above peak·(1/float(6·level)) and its elements
+ * round on e4m3(block)·float(level). `level` is the new second level the caller takes from the
+ * baked tensor's amax (amax / 2688 in double, 1 for all zeros) and then stores; flags 0
+ * (stochastic, Philox counter row·cols + col) or 1 (nearest). data [rows, cols/2], blocks
+ * [rows, cols/16] in place. */
+int cozyq_bake_nvfp4_refit(int device, uint8_t* data, uint8_t* blocks, const float* second,
+                           double level, const float* up, const float* down, int64_t rows,
+                           int64_t cols, int64_t rank, uint32_t seed, int flags, void* stream);
+
 /* An fp8.rowwise bake with error feedback (reference: `encode_e4m3(..., "feedback")`,
  * internal/lora_bake.py:163-197, under `bake_rowwise`): payload (e4m3·scale + delta) / fresh
  * (fresh = each row's scale after the bake: the kept one or a refitted one), each element

@@ -336,6 +336,39 @@ def bake_nvfp4(data: np.ndarray, blocks: np.ndarray, second: float, up: np.ndarr
     return packed, block.astype(np.uint8)
 
 
+def bake_nvfp4_refit(data: np.ndarray, blocks: np.ndarray, second: float, up: np.ndarray,
+                     down: np.ndarray, seed: int, *, nearest: bool = False,
+                     ) -> tuple[np.ndarray, np.ndarray, np.float32]:  # fmt: skip
+    """`bake_nvfp4` with `grid="refit"` (`internal/lora_bake.py:495-525`): the eager target
+    `round(e2m1·(scale·level)) + delta`; the new second level `amax / (6·448)` in float64 (a
+    Python float there), 1 for an all-zero tensor; every block's scale the least E4M3 code at or
+    above `peak / (6·second)` as torch divides by a Python scalar on its GPU (times the float32
+    reciprocal of the float32 divisor); the unit `e4m3(block) · float32(second)`, a payload of 0
+    where it is 0. Returns the new (codes, blocks, float32 second level)."""
+    rows, cols = data.shape[0], 2 * data.shape[1]
+    level = _F32(second)
+    codes = np.stack((data & 15, data >> 4), axis=-1).reshape(rows, cols).astype(np.int64)
+    scale_level = (e4m3_value(np.repeat(blocks.astype(np.int64), 16, axis=1)) * level).astype(np.float32)
+    d = delta(up.astype(np.float32), down.astype(np.float32))
+    target = ((e2m1_value(codes) * scale_level).astype(np.float32) + d).astype(np.float32)
+    amax = float(np.abs(target).max()) if target.size else 0.0
+    new = amax / (448.0 * 6.0) if amax > 0 else 1.0
+    new32 = _F32(new)
+    inv = (_F32(1) / _F32(6.0 * new)).astype(np.float32)
+    need = (np.abs(target).reshape(rows, -1, 16).max(axis=2) * inv).astype(np.float32)
+    block = e4m3_at_least(need)
+    unit = np.repeat((e4m3_value(block) * new32).astype(np.float32), 16, axis=1)
+    payload = np.where(unit > 0, (target / np.where(unit > 0, unit, _F32(1))).astype(np.float32), _F32(0))
+    if nearest:
+        nibble = e2m1_nearest(payload)
+    else:
+        nibble = e2m1_stochastic(payload, rand(seed, _offsets(rows, cols)))
+    negative = np.where(target == 0, codes >= 8, target < 0)
+    nibble = nibble | np.where(negative, 8, 0)
+    packed = (nibble[:, 0::2] | (nibble[:, 1::2] << 4)).astype(np.uint8)
+    return packed, block.astype(np.uint8), new32
+
+
 FEEDBACK_RUN = 32
 
 

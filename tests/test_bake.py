@@ -379,6 +379,11 @@ def test_abi_refuses_bad_bake_options():
     assert lib.cozyq_bake_nvfp4(0, 16, 16, 16, 16, 16, None, None, 4, 24, 2, 1, 0, None) != 0
     assert lib.cozyq_bake_norms(0, 6, 16, None, None, None, 16, 16, 4, 8, 2, 16, None) != 0
     assert lib.cozyq_bake_rotate_factor(0, 16, 16, 2, 100, None) != 0
+    # nvfp4 refit: a positive finite level, nearest or stochastic only, 16-column blocks.
+    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, 0.0, 16, 16, 4, 32, 2, 1, 0, None) != 0
+    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, float("inf"), 16, 16, 4, 32, 2, 1, 0, None) != 0
+    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, 1.0, 16, 16, 4, 32, 2, 1, 2, None) != 0
+    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, 1.0, 16, 16, 4, 24, 2, 1, 0, None) != 0
     # Empty shapes succeed without touching a device.
     assert lib.cozyq_bake(0, 0, None, None, None, None, None, None, None, 0, 8, 2, 1, 0, None) == 0
 
@@ -823,8 +828,12 @@ def test_eager_entry_points_refuse_unbuilt_options():
     with pytest.raises(NotImplementedError):
         cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, rounding="feedback",
                         more=lambda a, b: torch.zeros(b - a, 16))  # fmt: skip
+    with pytest.raises(ValueError, match="GPU"):
+        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit")  # built
     with pytest.raises(NotImplementedError):
-        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit")
+        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="regrid")
+    with pytest.raises(NotImplementedError):
+        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit", gain=torch.ones(4))
     with pytest.raises(ValueError, match="GPU"):
         cb.bake_plain(torch, t, down, up, 1.0, stats=cb.Stats())  # Stats: built
     with pytest.raises(ValueError):
@@ -946,6 +955,30 @@ def test_feedback_keeps_run_sums():
     assert sat.tolist() == [448, 448, 448]
 
 
+def test_nvfp4_refit_is_saturation_free():
+    """`refit`: the tensor's peak lands on 6 · 448 · level exactly as the reference sets it, no
+    element's payload passes 6, and nearest rounding leaves each element within half a step
+    (at most one unit) of its target; an all-zero tensor takes level 1 and stays zero."""
+    rng = np.random.default_rng(8)
+    rows, cols, rank = 24, 96, 5
+    codes, blocks = _nvfp4_stored(rows, cols, rng)
+    up = (rng.standard_normal((rows, rank)) * 0.3).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    new_codes, new_blocks, level = ob.bake_nvfp4_refit(codes, blocks, 0.05, up, down, 3, nearest=True)
+    nib = np.stack((codes & 15, codes >> 4), axis=-1).reshape(rows, cols)
+    scaled = (ob.e4m3_value(np.repeat(blocks, 16, axis=1)) * np.float32(0.05)).astype(np.float32)
+    target = ((ob.e2m1_value(nib) * scaled).astype(np.float32) + ob.delta(up, down)).astype(np.float64)
+    assert float(level) == np.float32(np.abs(target).max() / 2688.0)
+    unit = np.repeat(ob.e4m3_value(new_blocks).astype(np.float64) * float(level), 16, axis=1)
+    out = ob.e2m1_value(np.stack((new_codes & 15, new_codes >> 4), axis=-1).reshape(rows, cols)) * unit
+    assert (np.abs(target) <= 6 * unit * (1 + 1e-6)).all()
+    assert (np.abs(out - target) <= unit * (1 + 1e-6)).all()
+    zero_codes, zero_blocks, one = ob.bake_nvfp4_refit(np.zeros_like(codes), blocks, 0.05,
+                                                        np.zeros((rows, 0), np.float32),
+                                                        np.zeros((0, cols), np.float32), 3)  # fmt: skip
+    assert float(one) == 1.0 and not zero_blocks.any() and not (zero_codes & 0x77).any()
+
+
 def test_stats_properties():
     from cozyq import bake as cb
 
@@ -1029,3 +1062,44 @@ def test_gpu_bake_rowwise_feedback(grid, rows, cols, rank):
     got = w.view(torch.uint8).cpu().numpy()
     bad = np.argwhere(got != want)
     assert bad.size == 0, f"{len(bad)} codes differ, first at {bad[0].tolist()}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nearest", [True, False])
+@pytest.mark.parametrize("rows,cols,rank", [(40, 256, 4), (129, 272, 33), (1, 16, 1), (64, 128, 0)])
+def test_gpu_bake_nvfp4_refit(nearest, rows, cols, rank):
+    """`bake_nvfp4(grid="refit")`: the new second level, every block byte and every code
+    bit-exact against the oracle (stochastic on the Philox stream)."""
+    from cozyq import bake as cb
+
+    rng = np.random.default_rng(rows + rank)
+    codes, blocks = _nvfp4_stored(rows, cols, rng)
+    up = (rng.standard_normal((rows, rank)) * 0.2).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    seed = 1234
+    want_codes, want_blocks, level = ob.bake_nvfp4_refit(codes, blocks, 0.04, up, down, seed, nearest=nearest)
+    c, b = torch.from_numpy(codes).to(CUDA), torch.from_numpy(blocks).view(torch.float8_e4m3fn).to(CUDA)
+    second = torch.tensor([0.04], device=CUDA)
+    cb.bake_nvfp4(torch, c, b, second, _cuda(down), _cuda(up), 1.0, grid="refit",
+                  rounding="nearest" if nearest else "stochastic", seed=seed)  # fmt: skip
+    torch.cuda.synchronize()
+    assert second.cpu().numpy().view(np.uint32)[0] == np.float32(level).view(np.uint32)
+    assert np.array_equal(b.view(torch.uint8).cpu().numpy(), want_blocks)
+    assert np.array_equal(c.cpu().numpy(), want_codes)
+
+
+@pytest.mark.gpu
+def test_gpu_bake_nvfp4_refit_all_zero():
+    """An all-zero nvfp4 weight with no delta refits to level 1 and zero blocks, as the
+    reference's `amax > 0` test sets it."""
+    from cozyq import bake as cb
+
+    rows, cols = 8, 64
+    c = torch.zeros(rows, cols // 2, dtype=torch.uint8, device=CUDA)
+    b = torch.full((rows, cols // 16), 0x30, dtype=torch.uint8, device=CUDA).view(torch.float8_e4m3fn)
+    second = torch.tensor([0.5], device=CUDA)
+    cb.bake_nvfp4(torch, c, b, second, torch.zeros(0, cols, device=CUDA), torch.zeros(rows, 0, device=CUDA),
+                  1.0, grid="refit", rounding="nearest")  # fmt: skip
+    torch.cuda.synchronize()
+    assert float(second) == 1.0
+    assert not b.view(torch.uint8).any() and not c.any()
