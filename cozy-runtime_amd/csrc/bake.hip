@@ -416,7 +416,9 @@ __global__ __launch_bounds__(kBakeThreads) void bake_nvfp4_kernel(uint8_t* __res
                 block = e4m3_at_least(peak * x.need_inv);
                 unit = e4m3_sat(block) * x.level;
             } else {
-                const float need = peak / (6.0f * level);
+                // The fused kernel divides by 6·level; the eager bake divides by a Python float,
+                // which torch runs on the GPU as a multiply by the float32 reciprocal.
+                const float need = kExtra ? peak * (1.0f / (6.0f * level)) : peak / (6.0f * level);
                 const bool grown = need * 6.0f > e4m3_sat(kept) * 7.0f;
                 block = grown ? e4m3_at_least(need) : kept;
                 unit = e4m3_sat(block) * level;

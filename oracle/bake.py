@@ -305,7 +305,9 @@ def bake_nvfp4(data: np.ndarray, blocks: np.ndarray, second: float, up: np.ndarr
 
     With `gain`, `more`, `nearest` or `no_delta` (the eager `bake_nvfp4`, `:458-525`, and
     `gain_rows`): the target is `round(round(round(e2m1·(scale·level))·gain) + delta)`, each
-    product and sum rounded, and `nearest` rounds E2M1 to nearest (ties to even)."""
+    product and sum rounded, a block's need is its peak times the float32 reciprocal of
+    `6·level` (torch's division by a Python scalar on the GPU), and `nearest` rounds E2M1 to
+    nearest (ties to even)."""
     rows, cols = data.shape[0], 2 * data.shape[1]
     level = _F32(second)
     codes = np.stack((data & 15, data >> 4), axis=-1).reshape(rows, cols).astype(np.int64)
@@ -320,7 +322,13 @@ def bake_nvfp4(data: np.ndarray, blocks: np.ndarray, second: float, up: np.ndarr
         g = np.ones(rows, np.float32) if gain is None else gain.astype(np.float32)
         base = ((e2m1_value(codes) * scale_level).astype(np.float32) * g.reshape(-1, 1)).astype(np.float32)
         target = base if no_delta else (base + d).astype(np.float32)
-    need = (np.abs(target).reshape(rows, -1, 16).max(axis=2) / (_F32(6) * level)).astype(np.float32)
+    peak = np.abs(target).reshape(rows, -1, 16).max(axis=2)
+    if gain is None and more is None and not nearest and not no_delta:
+        need = (peak / (_F32(6) * level)).astype(np.float32)  # the Triton kernel: a division
+    else:
+        # The eager bake's `amax / (6.0 * second)` divides by a Python float: on the GPU, torch
+        # multiplies by the float32 reciprocal of the float32 divisor.
+        need = (peak * (_F32(1) / (_F32(6) * level)).astype(np.float32)).astype(np.float32)
     kept = blocks.astype(np.int64)
     grown = (need * _F32(6)).astype(np.float32) > (e4m3_value(kept) * _F32(7)).astype(np.float32)
     block = np.where(grown, e4m3_at_least(need), kept)

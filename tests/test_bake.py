@@ -1103,3 +1103,17 @@ def test_gpu_bake_nvfp4_refit_all_zero():
     torch.cuda.synchronize()
     assert float(second) == 1.0
     assert not b.view(torch.uint8).any() and not c.any()
+
+
+@pytest.mark.gpu
+def test_gpu_torch_divides_by_a_python_float_as_a_reciprocal_multiply():
+    """The eager bake's premise (`amax / (6.0 * second)`, `amax / 448`): torch on the GPU
+    computes `tensor / python_float` as `tensor · float32(1 / float32(divisor))`, which differs
+    from the IEEE quotient in the last bit for some inputs; the oracle's eager laws follow it."""
+    rng = np.random.default_rng(3)
+    a = (rng.random(1 << 16) * 100 + 1).astype(np.float32)
+    for b in (448.0, 6.0 * 0.3, 6.0 * float(np.float32(0.07)), 2688.0):
+        got = (torch.from_numpy(a).to(CUDA) / b).cpu().numpy()
+        recip = (a * (np.float32(1) / np.float32(b))).astype(np.float32)
+        assert np.array_equal(got.view(np.uint32), recip.view(np.uint32)), b
+    assert not np.array_equal((a / np.float32(448.0)).astype(np.float32), (a * (np.float32(1) / np.float32(448.0))).astype(np.float32))
