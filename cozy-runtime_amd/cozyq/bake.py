@@ -348,11 +348,11 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
                  rounding: str = "nearest", grid: str = "refit", generator: Any = None,
                  stats: Any = None, more: Dense | None = None, seed: int = 0) -> None:  # fmt: skip
     """Bake into `fp8.rowwise` (`internal/lora_bake.py:319-363`): `data` `[out, in]` E4M3,
-    `scale` one float32 per output row. `keep` rounds on the stored grid (the fused law's
-    order, `decode + delta / scale`); `refit` sets each row's scale from its baked maximum,
+    `scale` one float32 per output row. `keep` rounds on the stored grid; `refit` sets each row's scale from its baked maximum,
     `max(amax / 448, 1e-12)`, and `regrid` raises that by 1/32 to 3/32 by the row's golden-ratio
-    fraction, so every element rounds afresh: codes are `(decode · scale + delta) / new`, the
-    eager law's order, and `scale` takes the new values. `feedback` rounding (any grid) rounds
+    fraction, so every element rounds afresh. On every grid the codes are
+    `(decode · scale + delta) / new` (`new` the kept scale for `keep`), the eager law's order,
+    and `scale` takes the new values. `feedback` rounding (any grid) rounds
     those payloads to nearest with each 32-column run carrying its error (`encode_e4m3`,
     `:163-197`), the same bytes on every bake."""
     if grid not in GRIDS:
@@ -360,16 +360,12 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
     feedback = rounding == "feedback"
     flags = 0 if feedback else _rounding_flags(rounding)
     up_a = _scaled_up(torch, up, alpha)
-    stored = {"weight": data, "scale": scale}
-    if grid == "keep" and not feedback:
-        fused(torch, stored, down, up_a, seed, more=more, flags=flags, stats=stats)
-        return
     raw, scales = data.view(torch.uint8), scale.view(-1)
     if scales.dtype != torch.float32 or not scales.is_contiguous():
         raise ValueError("a row-scaled bake keeps a contiguous float32 row scale")
     up32, down32 = up_a.to(torch.float32).contiguous(), down.to(torch.float32).contiguous()
     more_rows = _more_rows(torch, more, raw.shape[0], False)
-    if more_rows is not None:
+    if more_rows is not None and (grid != "keep" or feedback):
         raise NotImplementedError("cozyq refits or feeds back rowwise scales from up @ down alone (no LoKr rows)")
     ops = _ops(raw)
     began = time.perf_counter()
@@ -390,11 +386,12 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
         # eager law's order `(decode · scale + delta) / new` on every grid, `keep`'s included.
         ops.bake_feedback(raw, scales, up32, down32, new)
     else:
-        ops.bake(ROWWISE, raw, scales, up32, down32, seed & SEED_MASK, flags=flags, rescale=new)
+        # `keep` too bakes onto a row scale (the kept one), for the eager order above.
+        ops.bake(ROWWISE, raw, scales, up32, down32, seed & SEED_MASK, more=more_rows, flags=flags, rescale=new)
     scales.copy_(new)
     if stats is not None:
         _account(torch, stats, ROWWISE, before, {"data": raw, "scale": scales}, up32, down32, raw.shape[1],
-                 None, None, began)  # fmt: skip
+                 None, more_rows, began)  # fmt: skip
 
 
 def bake_int8_convrot(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tensor, alpha: float, *,

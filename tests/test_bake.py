@@ -864,7 +864,8 @@ def test_gpu_eager_entry_points():
     w = torch.from_numpy(data).view(torch.float8_e4m3fn).to(CUDA)
     cb.bake_rowwise(torch, w, _cuda(scale), _cuda(down), _cuda(up), alpha, grid="keep", rounding="stochastic",
                     seed=seed)  # fmt: skip
-    assert np.array_equal(w.view(torch.uint8).cpu().numpy(), ob.bake(ob.ROWWISE, data, scale, up_a, down, seed))
+    assert np.array_equal(w.view(torch.uint8).cpu().numpy(),
+                          ob.bake(ob.ROWWISE, data, scale, up_a, down, seed, rescale=scale))  # the eager order
     # int8.convrot, nearest
     data, scale, _ = _stored_for(ob.INT8, rows, cols, 3)
     w = torch.from_numpy(data).to(CUDA)
@@ -1117,3 +1118,28 @@ def test_gpu_torch_divides_by_a_python_float_as_a_reciprocal_multiply():
         recip = (a * (np.float32(1) / np.float32(b))).astype(np.float32)
         assert np.array_equal(got.view(np.uint32), recip.view(np.uint32)), b
     assert not np.array_equal((a / np.float32(448.0)).astype(np.float32), (a * (np.float32(1) / np.float32(448.0))).astype(np.float32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+def test_gpu_bake_rowwise_keep_eager_order(rounding):
+    """`bake_rowwise(grid="keep")` with LoKr rows and `Stats`: codes `(decode · scale + delta) /
+    scale` as the reference's eager bake orders them, the scale kept, bit-exact."""
+    from cozyq import bake as cb
+
+    rows, cols, rank, seed = 50, 200, 5, 77
+    data, scale, rng = _stored_for(ob.ROWWISE, rows, cols, 62)
+    up = (rng.standard_normal((rows, rank)) * 0.05).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    extra = (rng.standard_normal((rows, cols)) * 0.01).astype(np.float32)
+    want = ob.bake(ob.ROWWISE, data, scale, up, down, seed, more=extra, nearest=rounding == "nearest",
+                   rescale=scale)  # fmt: skip
+    w = torch.from_numpy(data).view(torch.float8_e4m3fn).to(CUDA)
+    s, dense = _cuda(scale), _cuda(extra)
+    stats = cb.Stats()
+    cb.bake_rowwise(torch, w, s, _cuda(down), _cuda(up), 1.0, rounding=rounding, grid="keep", seed=seed,
+                    more=lambda a, b: dense[a:b], stats=stats)  # fmt: skip
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), scale.view(np.uint32))
+    assert np.array_equal(w.view(torch.uint8).cpu().numpy(), want)
+    assert stats.elements == rows * cols
