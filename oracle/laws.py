@@ -14,7 +14,13 @@ Pins, exercised in `tests/test_oracle.py`:
   vectors, plus an independent bit-level e4m3 encoder checked over every bf16/fp16 input.
 - `mx_quantize`: brute force over every positive bf16 and fp16 block maximum (exact integer ceil
   of log2) and the round trip through the mxfp8 decode law.
-- `int8_*` products: int32 GEMM against numpy int64 matmul.
+- `int8_*` products: int32 GEMM against numpy int64 matmul; `int8_epilogue`'s float sequence
+  (accumulator to float32, `· xs`, `· ws`, the cast, the bias in the output dtype) against
+  exact rational arithmetic with an independent round-to-nearest-even, on cases where each
+  plausible reordering gives other bits.
+- `gelu_tanh` (build law for the C2 epilogue): torch's tanh-approximate GELU in float64 over
+  every bf16 value in [-12, 12], bounded by the formula's own cancellation; zero and the
+  odd-part identity.
 - `int4_quantize` (build law): round trip bound |x − q·s| ≤ s/2 and brute force on small cases.
 - `w4a8_unpack`: closed forms (unit group scale on the uniform grid gives q − 8, the nibble
   order, NaN scales, the ±127 clamp) and numpy's float32 multiply and `rint` over every
@@ -138,15 +144,25 @@ def int32_gemm(q: torch.Tensor, data: torch.Tensor, literal: bool = False) -> to
     return (q.double() @ data.double().t()).to(torch.int32)
 
 
+def int8_epilogue(
+    acc: torch.Tensor, row_scale: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
+    out_dtype: torch.dtype,
+) -> torch.Tensor:
+    """The int8 lane's float sequence after the exact int32 product: `acc.float()` (rounds
+    past 2**24), `· row_scale` then `· w_scale` in float32, one cast to the output dtype
+    (`internal/int8_linear.py:447-448`), then `+ bias` in that dtype (`:276`)."""
+    out = acc.float().mul_(row_scale.reshape(-1, 1)).mul_(scale.float().reshape(1, -1))
+    out = out.to(out_dtype)
+    return out if bias is None else out + bias.to(out.dtype)
+
+
 def int8_product(
     q: torch.Tensor, row_scale: torch.Tensor, data: torch.Tensor, scale: torch.Tensor,
     out_dtype: torch.dtype, literal: bool = False,
 ) -> torch.Tensor:
     """`_product`'s CPU branch (`internal/int8_linear.py:431-448`): int32 accumulate, then
     `(acc.float() · row_scale) · w_scale` in float32 (two roundings), then one cast."""
-    acc = int32_gemm(q, data, literal)
-    out = acc.float().mul_(row_scale.reshape(-1, 1)).mul_(scale.float().reshape(1, -1))
-    return out.to(out_dtype)
+    return int8_epilogue(int32_gemm(q, data, literal), row_scale, scale, None, out_dtype)
 
 
 def gelu_tanh(y: torch.Tensor) -> torch.Tensor:
@@ -165,9 +181,7 @@ def int8_linear(
     applies `gelu_tanh` to that result in float32 and casts once more. `literal=True` runs the
     reference's int32 matmul (the CPU path timed as the baseline)."""
     q, row_scale = quantize_rows_int8(x, rotation)
-    out = int8_product(q, row_scale, data, scale, out_dtype, literal)
-    if bias is not None:
-        out = out + bias.to(out.dtype)
+    out = int8_epilogue(int32_gemm(q, data, literal), row_scale, scale, bias, out_dtype)
     if gelu:
         out = gelu_tanh(out).to(out_dtype)
     return out.reshape(*x.shape[:-1], -1)

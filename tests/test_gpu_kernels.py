@@ -688,6 +688,55 @@ def test_mx_gemm_within_tolerance(ops, shape, bias):
 # ------------------------------------------------------------------ full-size property
 
 
+def test_c1_full_size_rowwise_int8_bit_exact(ops):
+    """BASELINE config 1 at its real shape (M=128, K=N=3072): no rotation, per-token int8
+    activations and the per-output-channel int8 weight law (`internal/probe.py:764-767`).
+    Codes, scales, int32 accumulators and the bf16 output, without and with a bias, all equal
+    the CPU law bit for bit."""
+    m, k, n = 128, 3072, 3072
+    x = activations(m, k, seed=20261201)
+    data, scale = laws.int8_weight_rowwise(weights(n, k, seed=20261211))
+    q, s = ops.int8_quantize_rot(x.to(DEV), 0)
+    wq, ws = laws.quantize_rows_int8(x, 0)
+    assert torch.equal(q.cpu(), wq)
+    assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
+    wd, sd = data.to(DEV), scale.to(DEV)
+    assert torch.equal(ops.int8_acc(q, wd).cpu(), laws.int32_gemm(wq, data))
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(12)) * 0.1).to(torch.bfloat16)
+    for b in (None, bias):
+        got = ops.int8_gemm_ex(q, s, wd, sd, None if b is None else b.to(DEV), torch.bfloat16, 0)
+        assert torch.equal(got.cpu(), laws.int8_linear(x, data, scale, b, torch.bfloat16, rotation=0))
+
+
+@pytest.fixture(scope="module")
+def c3_weight():
+    """Config 3's fp8 weight (N=14336, K=4096) by the per-row E4M3 law, shared by the M sweep."""
+    data, scale = laws.fp8_weight(weights(14336, 4096, seed=20261204))
+    return data, scale
+
+
+@pytest.mark.parametrize("m", [1, 16, 256])
+def test_c3_decode_shapes_within_tolerance(ops, c3_weight, m):
+    """BASELINE config 3 at M = 1, 16 and 256 on its real weight (K=4096, N=14336), through the
+    leaf's own route (`fp8_linear`: the fused quantize + GEMV for M <= 4, quantize + the narrow
+    GEMM above): every output row within tolerance of the float64 product of the law's codes,
+    and for M > 4 the activation's codes and scales bit-exact."""
+    data, scale = c3_weight
+    k, n = 4096, 14336
+    x = activations(m, k, seed=20261203 + m)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(7)) * 0.1).to(torch.bfloat16)
+    wd, sd, bd = data.to(DEV), scale.to(DEV), bias.to(DEV)
+    got = ops.fp8_linear(x.to(DEV), wd, sd, bd, torch.bfloat16)
+    assert got.shape == (m, n)
+    assert_close(got, laws.fp8_exact(x, data, scale, bias))
+    if m > 4:
+        q, s = ops.fp8_quantize(x.to(DEV))
+        wq, ws = laws.fp8_quantize(x)
+        assert torch.equal(q.cpu().view(torch.uint8), wq.view(torch.uint8))
+        assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
+
+
+
 def test_c3_full_size_fp8_codes_and_sampled_rows(ops):
     """BASELINE config 3 at M=4096 (K=4096, N=14336): every e4m3 code and scale of the
     activation bit-exact, and 48 sampled output rows within tolerance of the float64 product;

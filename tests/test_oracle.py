@@ -8,6 +8,7 @@ from __future__ import annotations
 import base64
 import json
 import math
+from fractions import Fraction
 from pathlib import Path
 
 import numpy as np
@@ -230,6 +231,128 @@ def test_int32_gemm_matches_numpy_int64():
     got = laws.int32_gemm(q, w)
     want = q.numpy().astype(np.int64) @ w.numpy().astype(np.int64).T
     assert np.array_equal(got.numpy().astype(np.int64), want)
+
+
+# Exact rational arithmetic with an independent round-to-nearest-even onto a binary grid: the
+# int8 epilogue's rounding sequence is checked against it, not against torch.
+_FORMATS = {torch.float32: (24, -126), torch.bfloat16: (8, -126), torch.float16: (11, -14)}
+
+
+def _rne(v: Fraction, dtype: torch.dtype) -> Fraction:
+    """`v` rounded to nearest (ties to even) in `dtype` (significand bits, least normal
+    exponent; subnormals kept; the cases here stay far from overflow)."""
+    if v == 0:
+        return Fraction(0)
+    bits, emin = _FORMATS[dtype]
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    ulp = Fraction(2) ** (max(e, emin) - bits + 1)
+    units = a / ulp
+    whole = units.numerator // units.denominator
+    rest = units - whole
+    if rest > Fraction(1, 2) or (rest == Fraction(1, 2) and whole % 2 == 1):
+        whole += 1
+    return (whole * ulp) if v > 0 else -(whole * ulp)
+
+
+def _frac(t: torch.Tensor) -> list[Fraction]:
+    return [Fraction(v) for v in t.double().reshape(-1).tolist()]
+
+
+def _epilogue_cases(dtype: torch.dtype):
+    """int32 accumulators (a third of them past 2**24, where `acc.float()` rounds), row and
+    column scales that are not powers of two, and biases of the output dtype."""
+    gen = torch.Generator().manual_seed(20261202)
+    rows, cols = 48, 64
+    acc = torch.randint(-(1 << 20), 1 << 20, (rows, cols), generator=gen, dtype=torch.int64)
+    big = torch.randint(1 << 24, 49_000_000, (rows, cols), generator=gen, dtype=torch.int64)
+    acc = torch.where(torch.rand(rows, cols, generator=gen) < 0.33, big * acc.sign(), acc)
+    acc = acc.to(torch.int32)
+    xs = ((torch.rand(rows, 1, generator=gen) + 0.3) * 1e-2).float()
+    ws = ((torch.rand(cols, generator=gen) + 0.3) * 1e-3).float()
+    bias = (torch.randn(cols, generator=gen) * 4).to(dtype)
+    return acc, xs, ws, bias
+
+
+def test_int8_epilogue_rounding_sequence():
+    """`laws.int8_epilogue` against the reference's sequence evaluated in exact rationals
+    (`internal/int8_linear.py:447-448` + `:276`): rne32(acc), rne32(· xs), rne32(· ws), one
+    rounding to the output dtype, then the bias added in that dtype (a float32 sum rounded
+    once more). A float32 output shows the products' order bit for bit; bf16 and fp16 outputs
+    show the cast and the bias step. Each plausible variant — xs·ws first, ws first, no
+    rounding of the accumulator, one fused multiply-add with the bias, the bias added before the
+    cast — changes some of these bits, so this pins the order and not only the values."""
+    f32 = torch.float32
+    differs: dict[str, int] = {}
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
+        acc, xs, ws, bias = _epilogue_cases(dtype)
+        got = laws.int8_epilogue(acc, xs, ws, bias, dtype)
+        a_, x_, w_, b_ = _frac(acc), _frac(xs), _frac(ws), _frac(bias)
+        cols = acc.shape[1]
+
+        def out(p, b):  # the cast, then the bias in the output dtype
+            return _rne(_rne(_rne(p, dtype) + b, f32), dtype)
+
+        def law(a, x, w, b):
+            return out(_rne(_rne(_rne(a, f32) * x, f32) * w, f32), b)
+
+        variants = {
+            "xs*ws first": lambda a, x, w, b: out(_rne(_rne(a, f32) * _rne(x * w, f32), f32), b),
+            "ws first": lambda a, x, w, b: out(_rne(_rne(_rne(a, f32) * w, f32) * x, f32), b),
+            "exact accumulator": lambda a, x, w, b: out(_rne(_rne(a * x, f32) * w, f32), b),
+            "fma with bias": lambda a, x, w, b: _rne(_rne(_rne(_rne(a, f32) * x, f32) * w + b, f32), dtype),
+            "bias before cast": lambda a, x, w, b: _rne(_rne(_rne(_rne(_rne(a, f32) * x, f32) * w, f32) + b, f32), dtype),
+        }
+        want = []
+        for i, a in enumerate(a_):
+            r, c = divmod(i, cols)
+            args = (a, x_[r], w_[c], b_[c])
+            expect = law(*args)
+            want.append(expect)
+            for name, fn in variants.items():
+                differs[name] = differs.get(name, 0) + (fn(*args) != expect)
+        assert _frac(got) == want, dtype
+    assert all(n > 0 for n in differs.values()), differs
+
+
+def test_int8_linear_uses_the_pinned_epilogue():
+    """`int8_linear` is quantize → exact int32 product → the epilogue pinned above."""
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(5, 512, generator=gen).to(torch.bfloat16)
+    data = torch.randint(-127, 128, (24, 512), generator=gen, dtype=torch.int8)
+    scale = (torch.rand(24, generator=gen) + 0.5) * 1e-3
+    bias = torch.randn(24, generator=gen).to(torch.bfloat16)
+    q, s = laws.quantize_rows_int8(x, 256)
+    want = laws.int8_epilogue(laws.int32_gemm(q, data), s, scale, bias, torch.bfloat16)
+    assert torch.equal(laws.int8_linear(x, data, scale, bias, torch.bfloat16), want)
+
+
+def test_gelu_tanh_against_library_routine():
+    """`laws.gelu_tanh` (float32) against torch's tanh-approximate GELU evaluated in float64, on
+    every bf16 value in [-12, 12]: within 4 float32 ulps of the result, plus |y|·2**-23 for the
+    cancellation in 1 + tanh(u) as the reference writes it (`internal/prebuilt.py:775`: f32
+    tanh(u) near −1 carries 2**-25 of absolute error), plus 2**-126 (the reference's constant
+    0.79788456 and √(2/π) agree to 1e-9 relative); exactly 0 at 0, and the odd-part identity
+    gelu(y) − gelu(−y) = y. A wrong constant, a dropped ½ or the erf form miss these bounds."""
+    raw = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+    y = raw[torch.isfinite(raw) & (raw.abs() <= 12)]
+    got = laws.gelu_tanh(y).double()
+    want = torch.nn.functional.gelu(y.double(), approximate="tanh")
+    eps = torch.finfo(torch.float32).eps
+    bound = 4 * eps * want.abs() + y.double().abs() * 2.0**-23 + 2.0**-126
+    assert ((got - want).abs() <= bound).all()
+    wrong = 0.5 * y.double() * (1 + torch.tanh(0.79788456 * (y.double() + 0.0447 * y.double() ** 3)))
+    assert ((wrong - want).abs() > bound).any()
+    erf = torch.nn.functional.gelu(y.double())
+    assert ((erf - want).abs() > bound).sum() > 1000
+    assert laws.gelu_tanh(torch.zeros(1)).item() == 0.0
+    pos = y[y > 0]
+    odd = (laws.gelu_tanh(pos).double() - laws.gelu_tanh(-pos).double() - pos.double()).abs()
+    assert (odd <= 4 * torch.finfo(torch.float32).eps * pos.double()).all()
 
 
 @pytest.mark.parametrize("rotation", [0, 128, 256])
