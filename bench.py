@@ -11,7 +11,12 @@ the fp8 rowwise linear at M=1, K=4096, N=14336 (quantize + GEMV fused in one lau
 against 8 TB/s, rotating 8 weight copies (470 MB) so the 256 MB MALL cannot hold them.
 `configs` reports the other BASELINE configs. `cpu_baseline` times the reference's CPU law
 (the oracle's restatement of internal/int8_linear.py:415-448, its literal int32 matmul) on a
-bounded sample of the same workload on this host's cores.
+bounded sample of the same workload on this host's cores; `cpu_baselines` does so for every
+config.
+
+Timing: a fixed clock pre-roll (PREROLL_MS of the C2 step, whatever --warmup says), then the
+driver's contract for `value` (W warm-up steps, K steps between two synchronizations); every
+other figure is the median of SAMPLES interleaved samples (HIP events on the launch stream).
 
 Prints one JSON line. Only one GPU is used; `--gpus` above 1 exits with a message.
 """
@@ -33,12 +38,32 @@ METRIC = "quantized-linear TOPS & % MFMA peak (M=4096,K=3072,N=12288); M=1 HBM G
 PEAK_INT8_TOPS = 5000.0
 PEAK_FP8_TFLOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
-#: HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (one counter a
-#: pass, each scaled by the same counter's reading for a 256 MiB device copy: x2.0 and x1.0),
-#: summarized in profiles/hbm_traffic_pmc.txt. The config-2 GEMM reads X and W ~4.5x: each of
-#: the 8 XCDs' L2s fetches the K-slices its own tiles use.
-TRAFFIC_C2_GEMM = {"read": 227.43e6, "write": 100.66e6}
-TRAFFIC_DECODE = {"read": 59.07e6, "write": 0.06e6}
+#: HBM bytes per launch come from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs (one counter a
+#: pass, each scaled by the same counter's reading for a 256 MiB device copy), whose summary
+#: table is committed here; `roofline.traffic` is read from it by kernel name (null if absent).
+PMC_SUMMARY = ROOT / "profiles" / "hbm_traffic_pmc.txt"
+#: Timed samples per figure (medians are reported) and the clock pre-roll before any timing.
+SAMPLES = 15
+PREROLL_MS = 60.0
+
+
+def pmc_traffic(leg: str, kernel: str) -> dict | None:
+    """HBM bytes per dispatch of `kernel` (its demangled name's prefix) in leg `leg` of the
+    committed PMC summary: {"read", "write", "total"} in bytes, or None."""
+    try:
+        lines = PMC_SUMMARY.read_text().splitlines()
+    except OSError:
+        return None
+    for line in lines:
+        cols = line.split()
+        if len(cols) < 7 or cols[0] != leg:
+            continue
+        name = " ".join(cols[1:-5])
+        if name.startswith(kernel):
+            read, write = float(cols[-3]) * 1e6, float(cols[-1]) * 1e6
+            return {"read": read, "write": write, "total": read + write,
+                    "source": f"{PMC_SUMMARY.relative_to(ROOT)}: {name}"}
+    return None
 
 
 def _seeded(torch, seed: int):
@@ -78,6 +103,40 @@ class Timer:
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / iters
 
+    def interleaved(self, fns: dict, samples: int = SAMPLES, batch: int = 8) -> dict:
+        """Per-call ms of each of `fns`: `samples` rounds, each timing `batch` back-to-back calls
+        of every function in turn (candidates interleaved, as `internal/bench/gemm.py:370-392`
+        does), so clock drift falls on all of them alike. Returns the median per function, with
+        the fastest and slowest sample."""
+        torch = self.torch
+        events = {name: [] for name in fns}
+        for _ in range(samples):
+            for name, fn in fns.items():
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                for _ in range(batch):
+                    fn()
+                b.record()
+                events[name].append((a, b))
+        torch.cuda.synchronize()
+        out = {}
+        for name, pairs in events.items():
+            ms = sorted(a.elapsed_time(b) / batch for a, b in pairs)
+            out[name] = {"ms": ms[len(ms) // 2], "min_ms": ms[0], "max_ms": ms[-1], "samples": len(ms)}
+        return out
+
+
+def preroll(torch, fn, ms: float = PREROLL_MS) -> float:
+    """Runs `fn` back to back for at least `ms` of wall time before anything is timed: the
+    chip's clocks rise over the first ~20 ms of sustained MFMA load (the first 20-launch round
+    of the C2 GEMM measured ~12% slower than later ones). Returns the wall ms spent."""
+    start = time.perf_counter()
+    while (time.perf_counter() - start) * 1e3 < ms:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+    return (time.perf_counter() - start) * 1e3
+
 
 def _check(code: int) -> None:
     if code != 0:
@@ -107,9 +166,9 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
         gemm()
 
     timer = Timer(torch)
+    preroll_ms = preroll(torch, step)
+    # The driver's contract: W untimed steps, then exactly K steps between two synchronizations.
     ms_step = timer.run(step, steps, warmup)
-    ms_gemm = timer.run(gemm, steps, warmup)
-    ms_quant = timer.run(quantize, steps, warmup)
 
     # The same step at the reference's own rotation (256, regular H4^4, the parity-pinned one):
     # its weight rotated and quantized alike, the same GEMM and epilogue.
@@ -120,13 +179,18 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
         _check(lib.cozyq_quantize_rot(0, xp, 0, qp, sp, m, k, 256, stream))
         _check(lib.cozyq_gemm_ex(0, 0, qp, sp, dp256, wp256, bp, op, n, 0, m, n, k, 1, stream))
 
-    ms_step256 = timer.run(step256, steps, warmup // 4)
+    med = timer.interleaved({"step": step, "gemm": gemm, "quantize": quantize, "step256": step256})
+    ms_gemm, ms_quant, ms_step256 = med["gemm"]["ms"], med["quantize"]["ms"], med["step256"]["ms"]
     ops_count = 2.0 * m * n * k
     gemm_tops = ops_count / (ms_gemm * 1e-3) / 1e12
     traffic_alg = m * k + n * k + m * n * 2 + n * 2 + (m + n) * 4
+    c2_traffic = pmc_traffic("c2", "void gemm_kernel<0, false, true, 1>")
     return {
         "ms_per_step": ms_step,
         "tops": ops_count / (ms_step * 1e-3) / 1e12,
+        "preroll_ms": preroll_ms,
+        "step_median_ms": med["step"]["ms"],
+        "samples": med,
         "gemm_ms": ms_gemm,
         "quantize_ms": ms_quant,
         "quantize_gbs": (m * k * 2 + m * k + m * 4) / (ms_quant * 1e-3) / 1e9,
@@ -134,11 +198,42 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
         "roofline": {
             "bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
             "frac": gemm_tops / PEAK_INT8_TOPS,
-            "traffic": TRAFFIC_C2_GEMM["read"] + TRAFFIC_C2_GEMM["write"],
+            "traffic": None if c2_traffic is None else c2_traffic["total"],
+            "traffic_read_write": c2_traffic,
             "kernel": "gemm_kernel<int8> 256x256 (bias+GELU epilogue)",
             "algorithmic_ops": ops_count, "algorithmic_bytes": traffic_alg,
         },
     }
+
+
+def bench_c1(torch, ops, lib, stream) -> dict:
+    """Config 1 on the GPU: M=128, K=N=3072, no rotation, per-token int8 (`cozyq_quantize_rot`
+    with rotation 0) and the per-output-channel int8 weight, then the int8 GEMM (the narrow
+    tiles at this M), bf16 out. 2.4 GOP: launch- and latency-bound, reported in µs and TOPS."""
+    m, k, n = 128, 3072, 3072
+    x = _activations(torch, m, k, 20261201)
+    data, scale = ops.int8_quantize_rot(_weights(torch, n, k, 20261211), 0)
+    q = torch.empty(m, k, dtype=torch.int8, device="cuda")
+    s = torch.empty(m, dtype=torch.float32, device="cuda")
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    xp, qp, sp, dp, wp, op = (t.data_ptr() for t in (x, q, s, data, scale, out))
+
+    def quantize():
+        _check(lib.cozyq_quantize_rot(0, xp, 0, qp, sp, m, k, 0, stream))
+
+    def gemm():
+        _check(lib.cozyq_gemm_ex(0, 0, qp, sp, dp, wp, None, op, n, 0, m, n, k, 0, stream))
+
+    def step():
+        quantize()
+        gemm()
+
+    med = Timer(torch).interleaved({"step": step, "gemm": gemm, "quantize": quantize}, batch=16)
+    ops_count = 2.0 * m * n * k
+    return {"M": m, "K": k, "N": n, "us": med["step"]["ms"] * 1e3,
+            "gemm_us": med["gemm"]["ms"] * 1e3, "quantize_us": med["quantize"]["ms"] * 1e3,
+            "tops": ops_count / (med["step"]["ms"] * 1e-3) / 1e12,
+            "kernel": "rotate_quantize_kernel (rotation 0) + narrow_kernel<int8>"}
 
 
 def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -> dict:
@@ -188,8 +283,8 @@ def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -
             for _ in range(per_graph):
                 launch(raw)
     torch.cuda.synchronize()
-    replays = max(4, steps // 8)
-    ms = Timer(torch).run(graph.replay, replays, 2) / per_graph
+    graph.replay()
+    ms = Timer(torch).interleaved({"graph": graph.replay}, batch=2)["graph"]["ms"] / per_graph
     graph.replay()
     torch.cuda.synchronize()
     replayed = out.clone()
@@ -202,8 +297,9 @@ def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"M": m, "K": k, "N": n, "us": ms * 1e3, "us_eager": eager_ms * 1e3, "bytes": nbytes,
             "gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
-            "traffic": TRAFFIC_DECODE["read"] + TRAFFIC_DECODE["write"], "weight_copies": copies,
-            "timing": "HIP graph of 64 launches, replayed",
+            "traffic": (pmc_traffic("decode", "void fp8_decode_kernel") or {}).get("total"),
+            "weight_copies": copies,
+            "timing": "HIP graph of 64 launches, replayed; median of 15 samples of 2 replays",
             "kernel": "fp8_decode_kernel (quantize fused with the GEMV)" if m <= 4 else
                       "rowwise_quantize_kernel<fp8> + fp8_narrow_kernel"}
 
@@ -222,7 +318,9 @@ def _graph_us(torch, launch, per_graph: int, replays: int) -> float:
             for _ in range(per_graph):
                 launch(raw)
     torch.cuda.synchronize()
-    return Timer(torch).run(graph.replay, replays, 2) / per_graph * 1e3
+    graph.replay()
+    batch = max(1, min(4, replays // 4))
+    return Timer(torch).interleaved({"graph": graph.replay}, batch=batch)["graph"]["ms"] / per_graph * 1e3
 
 
 def bench_int8_decode(torch, ops, lib, stream, steps: int) -> dict:
@@ -314,16 +412,23 @@ def bench_fp8(torch, ops, lib, stream, m: int, steps: int) -> dict:
         _check(lib.cozyq_gemm(0, 0, 1, *args, None, out.data_ptr(), n, 0, m, n, k, -1, None, None,
                               stream))  # fmt: skip
 
-    ms = Timer(torch).run(gemm, steps, 2)
+    def step():
+        _check(lib.cozyq_quantize(0, 1, x.data_ptr(), 0, q.data_ptr(), s.data_ptr(), m, k, None,
+                                  None, 0, 0, 1, 0, 0.0, 0, None, stream))  # fmt: skip
+        gemm()
+
+    med = Timer(torch).interleaved({"gemm": gemm, "step": step}, batch=max(2, min(8, steps // 4)))
+    ms = med["gemm"]["ms"]
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-    return {"M": m, "us": ms * 1e3, "tflops": tflops, "frac_mfma": tflops / PEAK_FP8_TFLOPS}
+    return {"M": m, "us": ms * 1e3, "step_us": med["step"]["ms"] * 1e3, "tflops": tflops,
+            "frac_mfma": tflops / PEAK_FP8_TFLOPS}
 
 
 def bench_mx(torch, ops, lib, stream, steps: int) -> dict:
     m = 4096
     shapes = {"qkv": (3072, 9216), "attn_out": (3072, 3072), "ffn_up": (3072, 12288),
               "ffn_down": (12288, 3072)}
-    result, total_ops, total_ms = {}, 0.0, 0.0
+    fns, sizes = {}, {}
     for name, (k, n) in shapes.items():
         x = _activations(torch, m, k, 71)
         data, wbyte = ops.mx_quantize(_weights(torch, n, k, 72))
@@ -331,14 +436,18 @@ def bench_mx(torch, ops, lib, stream, steps: int) -> dict:
         qs = torch.empty(m, k // 32, dtype=torch.uint8, device="cuda")
         out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
 
-        def step():
+        def step(x=x, data=data, wbyte=wbyte, q=q, qs=qs, out=out, k=k, n=n):
             _check(lib.cozyq_mx_quantize(0, x.data_ptr(), 0, q.data_ptr(), qs.data_ptr(), m, k,
                                          stream))  # fmt: skip
             _check(lib.cozyq_mx_gemm(0, q.data_ptr(), qs.data_ptr(), data.data_ptr(),
                                      wbyte.data_ptr(), None, out.data_ptr(), n, 0, m, n, k,
                                      stream))  # fmt: skip
 
-        ms = Timer(torch).run(step, steps, 2)
+        fns[name], sizes[name] = step, (k, n)
+    med = Timer(torch).interleaved(fns, batch=max(2, min(8, steps // 4)))
+    result, total_ops, total_ms = {}, 0.0, 0.0
+    for name, (k, n) in sizes.items():
+        ms = med[name]["ms"]
         ops_count = 2.0 * m * n * k
         total_ops += ops_count
         total_ms += ms
@@ -381,10 +490,9 @@ def bench_svdq(torch, ops, lib, stream, steps: int) -> dict:
         quantize()
         gemm()
 
-    timer = Timer(torch)
-    q_ms = timer.run(quantize, steps, 2)
-    g_ms = timer.run(gemm, steps, 2)
-    ms = timer.run(step, steps, 2)
+    med = Timer(torch).interleaved({"quantize": quantize, "gemm": gemm, "step": step},
+                                   batch=max(2, min(8, steps // 4)))  # fmt: skip
+    q_ms, g_ms, ms = med["quantize"]["ms"], med["gemm"]["ms"], med["step"]["ms"]
     int4_ops = 2.0 * m * n * k
     lowrank_flops = 2.0 * m * r * (k + n)
     return {"M": m, "K": k, "N": n, "R": r, "us": ms * 1e3, "quantize_us": q_ms * 1e3,
@@ -558,31 +666,113 @@ def bench_bake(torch, ops, lib, stream, steps: int) -> dict:
     return {"lora_bake": out}
 
 
-def cpu_baseline(torch, rows: int = 1024) -> dict:
-    """The reference's CPU law for config 2 on rows 0..rows-1 of the batch: rotation + per-token
-    int8 (`quantize_rows`), the literal int32 matmul, both scales, bias and GELU."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as info:
+            for line in info:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_threads() -> int:
+    """The host threads the baseline uses: this process's CPU set, capped by OMP_NUM_THREADS
+    where the job sets it (the GPU box gives one GPU's job a 16-thread share)."""
+    cores = len(os.sched_getaffinity(0))
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return min(cores, cap) if cap > 0 else cores
+
+
+def _cpu_seconds(fn, runs: int = 3) -> tuple[float, list[float]]:
+    """One untimed warm-up call, then the median wall time of `runs` calls."""
+    fn()
+    times = []
+    for _ in range(runs):
+        start = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - start)
+    return sorted(times)[len(times) // 2], times
+
+
+def cpu_baselines(torch) -> dict:
+    """The reference's CPU laws, restated in the oracle (`kind: "port"`), timed on this host's
+    cores on a bounded sample of each config (one warm-up call, then the median of 3): C1 whole
+    (rowwise int8, the literal int32 matmul), C2 on 1024 of its rows (rotation 128 + int8, int32
+    matmul, scales, bias, GELU), C3 at M=1024 (e4m3 quantize, dequantize, float32 matmul: CPU
+    torch's `_scaled_mm` rejects row-wise scales), C4 at M=1024 (int4-g64 quantize, dequantized
+    float32 matmul + the bf16 low-rank branch), C5 on 512 rows of each DiT shape (MX quantize,
+    E8M0 dequant, float32 matmul). `value` is the sample's ops per second."""
     from oracle import laws
 
-    threads = len(os.sched_getaffinity(0))
+    threads = _cpu_threads()
     torch.set_num_threads(threads)
-    k, n = 3072, 12288
     gen = torch.Generator().manual_seed(20261202)
-    x = torch.randn(rows, k, generator=gen)
-    chans = torch.randperm(k, generator=gen)[: k // 100]
-    x[:, chans] *= 20
-    x = x.to(torch.bfloat16)
-    w = torch.randn(n, k, generator=gen) * 0.02
-    data, scale = laws.int8_weight_rotated(w, 128)
-    bias = (torch.randn(n, generator=gen) * 0.1).to(torch.bfloat16)
-    start = time.perf_counter()
-    laws.int8_linear(x, data, scale, bias, torch.bfloat16, rotation=128, gelu=True, literal=True)
-    seconds = time.perf_counter() - start
-    return {
-        "value": 2.0 * rows * n * k / seconds / 1e12, "unit": "TOPS", "cores": threads,
-        "kind": "port", "seconds": seconds,
-        "sample": f"config 2 rows 0..{rows - 1}: X[{rows},{k}] bf16 -> rotate(128)+int8, "
-                  f"int32 matmul with W[{n},{k}], scales, bias, GELU (torch CPU)",
-    }
+
+    def acts(m, k):
+        x = torch.randn(m, k, generator=gen)
+        x[:, torch.randperm(k, generator=gen)[: k // 100]] *= 20
+        return x.to(torch.bfloat16)
+
+    def wts(n, k):
+        return torch.randn(n, k, generator=gen) * 0.02
+
+    bf16 = torch.bfloat16
+    out = {}
+
+    def record(name, fn, ops_count, unit, sample):
+        seconds, times = _cpu_seconds(fn)
+        out[name] = {"value": ops_count / seconds / 1e12, "unit": unit, "cores": threads,
+                     "kind": "port", "seconds": seconds, "runs_s": times, "sample": sample}
+
+    k1 = n1 = 3072
+    x1 = acts(128, k1)
+    d1, s1 = laws.int8_weight_rowwise(wts(n1, k1))
+    record("c1", lambda: laws.int8_linear(x1, d1, s1, None, bf16, rotation=0, literal=True),
+           2.0 * 128 * n1 * k1, "TOPS", "config 1 whole: X[128,3072] -> per-token int8, int32 "
+           "matmul with W[3072,3072] rowwise int8, both scales, bf16")  # fmt: skip
+    k2, n2, m2 = 3072, 12288, 1024
+    x2 = acts(m2, k2)
+    d2, s2 = laws.int8_weight_rotated(wts(n2, k2), 128)
+    b2 = (torch.randn(n2, generator=gen) * 0.1).to(bf16)
+    record("c2", lambda: laws.int8_linear(x2, d2, s2, b2, bf16, rotation=128, gelu=True, literal=True),
+           2.0 * m2 * n2 * k2, "TOPS", f"config 2 rows 0..{m2 - 1}: X[{m2},{k2}] -> rotate(128)+int8, "
+           f"int32 matmul with W[{n2},{k2}], scales, bias, tanh-GELU")  # fmt: skip
+    k3, n3, m3 = 4096, 14336, 1024
+    x3 = acts(m3, k3)
+    d3, s3 = laws.fp8_weight(wts(n3, k3))
+    record("c3", lambda: laws.fp8_linear(x3, d3, s3, None, bf16), 2.0 * m3 * n3 * k3, "TFLOPS",
+           f"config 3 at M={m3}: e4m3 rowwise quantize, dequantize, float32 matmul with "
+           f"W[{n3},{k3}] e4m3, bf16")  # fmt: skip
+    k4 = n4 = 3072
+    m4, r4 = 1024, 32
+    x4 = acts(m4, k4)
+    p4 = torch.rand(k4, generator=gen) * 1.5 + 0.5
+    down4 = (torch.randn(r4, k4, generator=gen) * 0.02).to(bf16)
+    up4 = (torch.randn(n4, r4, generator=gen) * 0.02).to(bf16)
+    c4, sc4 = laws.svdq_weight(wts(n4, k4), p4, down4, up4)
+    record("c4", lambda: laws.svdq_linear(x4, p4, c4, sc4, down4, up4, None, bf16),
+           2.0 * m4 * n4 * k4 + 2.0 * m4 * r4 * (k4 + n4), "TOPS",
+           f"config 4 at M={m4}: smoothing, int4-g64 quantize, dequantized float32 matmul with "
+           f"W[{n4},{k4}] int4-g64, rank-32 bf16 low-rank branch")  # fmt: skip
+    m5 = 512
+    mx_total_ops, mx_seconds = 0.0, 0.0
+    for name, (k5, n5) in {"qkv": (3072, 9216), "attn_out": (3072, 3072), "ffn_up": (3072, 12288),
+                           "ffn_down": (12288, 3072)}.items():  # fmt: skip
+        x5 = acts(m5, k5)
+        d5, e5 = laws.mx_quantize(wts(n5, k5))
+        seconds, _ = _cpu_seconds(lambda: laws.mx_linear(x5, d5, e5, None, bf16))
+        mx_total_ops += 2.0 * m5 * n5 * k5
+        mx_seconds += seconds
+    out["c5"] = {"value": mx_total_ops / mx_seconds / 1e12, "unit": "TFLOPS", "cores": threads,
+                 "kind": "port", "seconds": mx_seconds,
+                 "sample": f"config 5, {m5} rows through each of the four DiT shapes: MX quantize, "
+                           "E8M0 dequant, float32 matmul"}
+    cpu = _cpu_model()
+    for entry in out.values():
+        entry["cpu"] = cpu
+    return out
 
 
 def only(torch, ops, lib, stream, args) -> int:
@@ -595,6 +785,8 @@ def only(torch, ops, lib, stream, args) -> int:
         figures = {"copy_bytes": nbytes, "us": ms * 1e3, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
     elif args.only == "c2":
         figures = bench_c2(torch, ops, lib, stream, args.steps, args.warmup)
+    elif args.only == "c1":
+        figures = bench_c1(torch, ops, lib, stream)
     elif args.only == "decode":
         figures = bench_decode(torch, ops, lib, stream, args.steps, args.warmup)
     elif args.only == "fp8":
@@ -628,7 +820,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=100)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
-    parser.add_argument("--only", choices=("c2", "decode", "int8_decode", "w4a8", "fp8", "svdq", "mx", "weights",
+    parser.add_argument("--only", choices=("c1", "c2", "decode", "int8_decode", "w4a8", "fp8", "svdq", "mx", "weights",
                                                     "nvfp4", "bake", "copy"),
                         help="profiling aid: run one leg (or a plain 256 MiB device copy, the "
                              "counter calibration) --steps times and print its figures only")  # fmt: skip
@@ -654,6 +846,7 @@ def main() -> int:
     print(f"[bench] decode M=1 {decode['us']:.2f} us {decode['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     configs = {}
     if not args.no_extra:
+        configs["c1_int8_rowwise"] = [bench_c1(torch, ops, lib, stream)]
         configs["c3_fp8"] = [bench_fp8(torch, ops, lib, stream, m, max(10, args.steps // 2))
                              for m in (256, 4096)]  # fmt: skip
         configs["c3_fp8_small"] = [bench_decode(torch, ops, lib, stream, args.steps, args.warmup, m=16)]
@@ -665,7 +858,7 @@ def main() -> int:
         configs["nvfp4_w4a16"] = bench_nvfp4(torch, ops, lib, stream, args.steps)["nvfp4_w4a16_gemv"]
         configs["lora_bake"] = bench_bake(torch, ops, lib, stream, args.steps)["lora_bake"]
         print("[bench] extra configs done", file=sys.stderr, flush=True)
-    baseline = None if args.no_cpu else cpu_baseline(torch)
+    baselines = None if args.no_cpu else cpu_baselines(torch)
     line = {
         "metric": METRIC,
         "value": c2["tops"],
@@ -684,10 +877,16 @@ def main() -> int:
                    "parallelism": "none (1 GPU)"},
         "roofline": c2["roofline"],
         "decode": decode,
+        "preroll_ms": c2["preroll_ms"],
+        "timing": f"value: {args.steps} steps between two synchronizations after {args.warmup} "
+                  f"warm-up steps and a {PREROLL_MS:.0f} ms clock pre-roll; phase and config "
+                  f"figures: medians of {SAMPLES} interleaved samples (HIP events)",
         "phases": {"quantize_ms": c2["quantize_ms"], "quantize_gbs": c2["quantize_gbs"],
-                   "gemm_ms": c2["gemm_ms"]},
+                   "gemm_ms": c2["gemm_ms"], "step_median_ms": c2["step_median_ms"],
+                   "samples": c2["samples"]},
         "configs": {"c2_rotation256": [c2["rotation256"]], **configs},
-        "cpu_baseline": baseline,
+        "cpu_baseline": None if baselines is None else baselines["c2"],
+        "cpu_baselines": baselines,
     }
     print(json.dumps(line))
     return 0
