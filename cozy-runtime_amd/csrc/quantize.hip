@@ -11,6 +11,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "rotate.h"
+#include "rows.h"
 
 namespace cozyq {
 namespace {
@@ -229,6 +230,36 @@ __global__ __launch_bounds__(kThreads) void rotate_quantize_kernel(
     if (scale < __builtin_huge_valf()) emit(std::true_type{}); else emit(std::false_type{});
 }
 
+// Rows of at most kRowMaxK elements with no prologue: one wave per row (rows.h), no workgroup
+// barrier, and each wave's next row loaded while it rotates and quantizes the current one, so a
+// CU keeps ~12 rows (72 KB at K = 3072) of loads in flight.
+constexpr int kRowWaves = 4;
+
+template <bool kHalf, int kRot>
+__global__ __launch_bounds__(64 * kRowWaves) void row_quantize_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales, int M, int K) {
+    __shared__ __attribute__((aligned(16))) float lds[kRowWaves][kRowLdsFloats<kRot> > 0 ? kRowLdsFloats<kRot> : 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int stride = gridDim.x * kRowWaves;
+    int row = blockIdx.x * kRowWaves + wave;
+    if (row >= M) return;
+    uint4 a[kRowLoads], b[kRowLoads];
+    auto view = [&](int r) { return row_view(x + static_cast<int64_t>(min(r, M - 1)) * K, K); };
+    row_loads(view(row), lane, a);
+    // Two rows a trip with the buffers' roles swapped: the next row's loads (clamped to the last
+    // row, so the loads stay branch-free) are issued before the current row is worked on.
+    while (true) {
+        row_loads(view(row + stride), lane, b);
+        quantize_row_wave<kHalf, kRot>(a, K, lane, lds[wave], q + static_cast<int64_t>(row) * K, scales + row);
+        row += stride;
+        if (row >= M) break;
+        row_loads(view(row + stride), lane, a);
+        quantize_row_wave<kHalf, kRot>(b, K, lane, lds[wave], q + static_cast<int64_t>(row) * K, scales + row);
+        row += stride;
+        if (row >= M) break;
+    }
+}
+
 // Per-row int8 without rotation (build lane): s = max(amax/127, 1e-12), q = clamp(rne(x/s)).
 // Per-row E4M3 (fp8 = true): s = max(amax/448, 1e-12), q = e4m3(clamp(x/s, ±448)).
 // One block per row; two passes over the row (the second from cache).
@@ -349,6 +380,17 @@ hipError_t rotate_quantize(const void* x, bool x_half, int8_t* q, float* scales,
                       : launch_rotated<false, 256, true>(x, q, scales, M, K, *pro, s);
     }
     const Prologue none{};
+    if (K <= kRowMaxK && (rotation == 0 || rotation == 128 || rotation == 256)) {
+        // 12 waves a CU: three 4-wave blocks on each of the 256 CUs, grid-strided over the rows.
+        const int blocks = min((M + kRowWaves - 1) / kRowWaves, 3 * 256);
+        auto xp = static_cast<const uint16_t*>(x);
+#define COZYQ_ROWS(H, R) row_quantize_kernel<H, R><<<blocks, 64 * kRowWaves, 0, s>>>(xp, q, scales, M, K)
+        if (rotation == 0) { if (x_half) COZYQ_ROWS(true, 0); else COZYQ_ROWS(false, 0); }
+        else if (rotation == 128) { if (x_half) COZYQ_ROWS(true, 128); else COZYQ_ROWS(false, 128); }
+        else { if (x_half) COZYQ_ROWS(true, 256); else COZYQ_ROWS(false, 256); }
+#undef COZYQ_ROWS
+        return hipGetLastError();
+    }
     if (rotation == 0) {
         auto qp = reinterpret_cast<uint8_t*>(q);
         return x_half ? launch_rowwise<true, false>(x, qp, scales, M, K, nullptr, s)

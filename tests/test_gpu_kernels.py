@@ -332,6 +332,26 @@ def test_int8_quantize_bit_exact(ops, rotation, dtype, shape):
     assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
 
 
+@pytest.mark.parametrize("rotation", [256, 128, 0])
+@pytest.mark.parametrize("shape", [(4100, 2304), (3073, 4096), (6500, 768), (2, 1280)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_int8_row_quantize_strides_and_passes(ops, rotation, shape):
+    """The one-wave-per-row quantizer (rows of at most 4096 elements): more rows than the grid
+    has waves (each wave takes several rows, the next one's loads in flight), a second LDS pass
+    that covers part of the row (2304 = 2048 + 256), rows that are not whole passes; codes and
+    scales bit-exact, an all-zero row and a row of subnormal-scale values included."""
+    m, k = shape
+    if rotation == 128 and k % 128:
+        pytest.skip("K is a multiple of the rotation")
+    x = activations(m, k, seed=m + 3 * k)
+    x[m - 1] = 0
+    x[0] *= 1e-30
+    q, s = ops.int8_quantize_rot(x.to(DEV), rotation)
+    wq, ws = laws.quantize_rows_int8(x, rotation)
+    assert torch.equal(q.cpu(), wq)
+    assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
+
+
 GEMM_SHAPES = [(1, 8, 256), (300, 512, 1024), (257, 264, 384), (64, 1032, 3072), (513, 256, 4096)]
 
 
