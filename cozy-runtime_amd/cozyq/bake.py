@@ -1,33 +1,37 @@
-"""The LoRA bake on gfx950: cozyq's counterpart of cozy-runtime's `internal/lora_bake.py`.
+"""The LoRA bake on gfx950, under the names of cozy-runtime's `internal/lora_bake.py`.
 
 A LoRA's `up @ down` is added into a stored weight in place and rounded back onto the weight's
-own form, so that the adapted layer serves at the speed of the unadapted one. The reference
-bakes on the GPU with one Triton kernel per stored form (`fused`, `:775-815`); this module keeps
-its surface — `bakeable`, `rotate_factor`, `fused`, `bake`, `probe`, `recipe` and the form
-constants — with the kernels in `csrc/bake.hip` behind `cozyq_bake`, `cozyq_bake_nvfp4` and
-`cozyq_bake_rotate_factor`:
+own form, so the adapted layer serves at the speed of the unadapted one. The surface —
+`bakeable`, `rotate_factor`, `fused`, `bake`, `probe`, `recipe`, the eager entry points and the
+form constants — runs on the kernels of `csrc/bake.hip`.
 
-* plain bf16 (stochastic: 16 noise bits added under the kept ones), f16 and f32 (nearest);
-* `fp8.rowwise` (E4M3 data, stochastic, row scale kept);
-* `int8-convrot256/1` (int8 of the rotated rows, stochastic floor, row scale kept; `down` is
-  rotated into the weight's basis first);
-* canonical `nvfp4` (E2M1 codes on the kept block grid, a block's E4M3 scale refitted only when
-  its baked maximum outgrows 7/6 of it, the second level kept).
+The fused bake (`fused`, `bake`) covers:
+- plain bf16 (stochastic: 16 noise bits under the kept ones), f16 and f32 (nearest);
+- fp8.rowwise (E4M3 data, stochastic, row scale kept);
+- int8.convrot (stochastic floor, row scale kept, `down` rotated into the weight's basis);
+- canonical nvfp4 (E2M1 on the kept block grid; a block's E4M3 scale refitted only past 7/6 of
+  it; the second level kept).
+Element (row, col) draws Triton's Philox word at counter `row · cols + col` under the 31-bit
+seed. The delta is one float32 FMA chain in rank order. The bytes equal `oracle/bake.py`'s.
+Byte parity with the reference's Triton bake rests on reading its `tl.dot` as that chain.
 
-Element (row, col)'s noise is Triton's Philox draw at counter `row * cols + col` under the
-weight's 31-bit seed, and the delta is one float32 FMA chain in rank order, so a bake writes the
-bytes the reference's fused bake writes for the same factors.
+The eager options run on the same kernels:
+- a DoRA gain;
+- LoKr rows (`more`, `Kron`, `dense`);
+- `gain_rows`, `norms` and the `dora` helpers;
+- `bake_rowwise`'s `keep` / `refit` / `regrid` grids and its error-feedback rounding;
+- nvfp4's `refit` grid;
+- `Stats` (any rank).
+`alpha` scales `up` before the product. The reference scales the product after it, which gives
+the same bytes when alpha is a power of two and can differ in the last bit otherwise.
+A stochastic eager bake takes its noise from `seed` or draws `seed` from `generator`; without
+either it refuses, rather than reuse one stream.
 
-What the reference bakes eagerly runs on the same kernels: a DoRA gain on plain or nvfp4 rows
-(plain rows times the gain, nvfp4 decoded values times it, then the delta — the eager law's
-roundings), a LoKr's dense rows (`more`, added to the delta; rotated for int8.convrot), `gain_rows`
-(nearest rounding, no delta) and DoRA's row `norms`. Their stochastic bytes are drawn from the
-Philox stream above, where the reference's eager bake draws from torch's generator: the same law
-in distribution, not the same bytes. `bake_rowwise`'s `refit` / `regrid` grids run on a row-amax
-kernel and the bake kernel's new-scale mode, and `Stats` on an accounting kernel that reads a
-copy of the weight taken before the bake. Not built: nvfp4's `refit` grid and error-feedback
-rounding (options `bake` never selects); asking for them raises NotImplementedError. Tensors off
-the GPU raise.
+Not built, raising NotImplementedError:
+- nvfp4's `refit` grid together with a gain, LoKr rows or `Stats`;
+- nvfp4's `regrid`, which the reference does not define;
+- `bake_rowwise`'s `refit` / `regrid` / feedback together with LoKr rows.
+Tensors off the GPU raise ValueError.
 """
 
 from __future__ import annotations
@@ -68,19 +72,27 @@ class Verdict(NamedTuple):
     detail: str
 
 
+#: `Stats`' running sums, in the order of the accounting kernel's partials where they come
+#: from it.
+_SUMS = ("layers", "elements", "weight_energy", "delta_energy", "error_energy", "kept",
+         "effect_energy", "effect_error", "saturated", "seconds")  # fmt: skip
+
+
 @dataclass(slots=True)
 class Stats:
-    """Sums over every baked element, in the weights' own units (`internal/lora_bake.py:78-123`),
-    taken on the GPU by `cozyq_bake_stats` from the weight before and after each bake."""
+    """Accumulated accounting of one or more bakes (rule B2; the reference's `Stats`,
+    `internal/lora_bake.py:78-123`). Energies are sums of squares in the weight's own units:
+    of the baked target W + delta (`weight_energy`), of the delta, and of the rounding error
+    stored − target. `kept` is the inner product of what changed in storage with the delta.
+    `effect_*` project the delta and the error onto the LoRA's own input directions
+    (`· downᵀ`). `saturated` counts elements clipped at the grid's edge."""
 
     layers: int = 0
     elements: int = 0
-    #: |W + delta|^2, |delta|^2, |stored - (W + delta)|^2 and <stored - W, delta>
     weight_energy: float = 0.0
     delta_energy: float = 0.0
     error_energy: float = 0.0
     kept: float = 0.0
-    #: the delta's action on its own inputs, |delta @ down.T|^2, and the rounding error's there
     effect_energy: float = 0.0
     effect_error: float = 0.0
     saturated: int = 0
@@ -88,40 +100,41 @@ class Stats:
 
     @property
     def retention(self) -> float:
-        """The delta's own direction in what was stored: 1.0 keeps all of it, 0.0 none."""
-        return self.kept / self.delta_energy if self.delta_energy else 1.0
+        """Fraction of the delta's own direction that reached storage (1.0 when there was no
+        delta)."""
+        if not self.delta_energy:
+            return 1.0
+        return self.kept / self.delta_energy
 
     @property
     def sqnr_db(self) -> float:
-        """Baked weight against the rounding error the bake added."""
-        return _db(self.weight_energy, self.error_energy)
+        """Target energy over rounding-error energy, in dB."""
+        return _ratio_db(self.weight_energy, self.error_energy)
 
     @property
     def effect_snr_db(self) -> float:
-        """What the LoRA does to the inputs it reads, against what rounding did to them."""
-        return _db(self.effect_energy, self.effect_error)
+        """The delta's effect on its own inputs over the error's, in dB."""
+        return _ratio_db(self.effect_energy, self.effect_error)
 
     def add(self, other: Stats) -> None:
-        for name in self.__slots__:
+        for name in _SUMS:
             setattr(self, name, getattr(self, name) + getattr(other, name))
 
     def document(self) -> dict[str, float | int]:
-        return {
-            "layers": self.layers,
-            "elements": self.elements,
-            "retention": self.retention,
-            "sqnr_db": self.sqnr_db,
-            "effect_snr_db": self.effect_snr_db,
-            "delta_to_weight_db": _db(self.delta_energy, self.weight_energy),
-            "saturated": self.saturated,
-            "seconds": self.seconds,
-        }
+        figures: dict[str, float | int] = {"layers": self.layers, "elements": self.elements}
+        figures.update(retention=self.retention, sqnr_db=self.sqnr_db, effect_snr_db=self.effect_snr_db,
+                       delta_to_weight_db=_ratio_db(self.delta_energy, self.weight_energy))  # fmt: skip
+        figures.update(saturated=self.saturated, seconds=self.seconds)
+        return figures
 
 
-def _db(signal: float, noise: float) -> float:
+def _ratio_db(signal: float, noise: float) -> float:
+    """10·log10(signal / noise): +inf without noise, -inf without signal."""
     if noise <= 0:
         return math.inf
-    return 10 * math.log10(signal / noise) if signal > 0 else -math.inf
+    if signal <= 0:
+        return -math.inf
+    return 10 * math.log10(signal / noise)
 
 
 def _account(torch: Any, stats: Stats, form: int, before: dict[str, Tensor], after: dict[str, Tensor],
@@ -145,26 +158,33 @@ def _account(torch: Any, stats: Stats, form: int, before: dict[str, Tensor], aft
     stats.seconds += time.perf_counter() - began
 
 
+#: Role signatures (role -> stored dtype) a bake takes, per scheme (rule B1).
+_BAKEABLE_ROLES: dict[str, tuple[dict[str, str], ...]] = {
+    "plain": ({"value": "bf16"}, {"value": "f16"}, {"value": "f32"}),
+    "fp8.rowwise": ({"weight": "f8_e4m3fn", "scale": "f32"},),
+    "int8.convrot": ({"weight": "i8", "scale": "f32"},),
+    "nvfp4": ({"weight": "u8", "scale": "f8_e4m3fn", "scale_2": "f32"},),
+}
+#: Roles a scheme may carry that are not the weight's and stay out of the signature.
+_IGNORED_ROLES = {"nvfp4": frozenset({"input_scale"})}
+
+
 def bakeable(scheme: str, params: Mapping[str, object], roles: Mapping[str, str]) -> bool:
-    """Whether a stored weight (scheme, params, role → dtype) takes `bake`
-    (`internal/lora_bake.py:537-551`): plain bf16 / f16 / f32, `fp8.rowwise` E4M3 with a float32
-    row scale, canonical `nvfp4` (its activation `input_scale` aside) or `int8.convrot`. An
-    int8.convrot weight must carry the 256 rotation the bake rotates `down` by; the reference
-    does not ask and would bake a smaller rotation's weight in the wrong basis."""
-    if scheme == "plain":
-        return dict(roles) in ({"value": "bf16"}, {"value": "f16"}, {"value": "f32"})
-    if scheme == "fp8.rowwise":
-        return dict(roles) == {"weight": "f8_e4m3fn", "scale": "f32"}
+    """Whether a stored weight, given as scheme, params and role -> dtype, takes `bake` (rule
+    B1; the reference's `bakeable`, `internal/lora_bake.py:537-551`). The scheme decides, not
+    the roles: int8.rowwise stores what int8.convrot stores and is not rotated. Here an
+    int8.convrot weight must also carry the 256 rotation that `down` is rotated by."""
+    signatures = _BAKEABLE_ROLES.get(scheme)
+    if signatures is None:
+        return False
+    ignored = _IGNORED_ROLES.get(scheme, frozenset())
+    if {r: d for r, d in roles.items() if r not in ignored} not in signatures:
+        return False
     if scheme == "nvfp4":
-        kept = {role: dtype for role, dtype in roles.items() if role != "input_scale"}
-        return kept == {"weight": "u8", "scale": "f8_e4m3fn", "scale_2": "f32"} and all(
-            params.get(name, value) == value for name, value in NVFP4_PARAMS.items()
-        )
-    return (
-        scheme == "int8.convrot"
-        and dict(roles) == {"weight": "i8", "scale": "f32"}
-        and int(dict(params).get("rotation_size", CONVROT_GROUP)) == CONVROT_GROUP  # type: ignore[call-overload]
-    )
+        return all(params.get(name, wanted) == wanted for name, wanted in NVFP4_PARAMS.items())
+    if scheme == "int8.convrot":
+        return int(params.get("rotation_size", CONVROT_GROUP)) == CONVROT_GROUP  # type: ignore[call-overload]
+    return True
 
 
 def _ops(tensor: Tensor):
@@ -184,9 +204,9 @@ def rotate_factor(torch: Any, down: Tensor) -> Tensor:
 
 @dataclass(frozen=True, slots=True)
 class Kron:
-    """A LoKr term (`internal/lora_bake.py:210-224`): `scale * kron(w1, w2)` (`w1` `[a, b]`,
-    `w2` `[c, d]`), the product's rows `index` (int64 `[out]`, in order). Its rows are expanded
-    with torch on the GPU and added to a bake's delta."""
+    """A LoKr term (rule B3; `internal/lora_bake.py:210-224`): `scale · kron(w1, w2)` for
+    `w1` `[a, b]` and `w2` `[c, d]`, restricted to the product rows `index` (int64, in order).
+    Called with `(start, stop)` it gives rows `index[start:stop]`, float32 `[n, b·d]`."""
 
     w1: Tensor
     w2: Tensor
@@ -194,26 +214,33 @@ class Kron:
     index: Tensor
 
     def __call__(self, start: int, stop: int) -> Tensor:
-        # Row p * c + q of kron(w1, w2) is w1[p] (x) w2[q].
-        at = self.index[start:stop]
+        rows = self.index[start:stop]
         c = self.w2.shape[0]
-        w1, w2 = self.w1[at // c].float(), self.w2[at % c].float()
-        return (w1[:, :, None] * w2[:, None, :]).flatten(1).mul_(self.scale)
+        outer, inner = rows.div(c, rounding_mode="floor"), rows.remainder(c)  # row = outer · c + inner
+        left = self.w1.index_select(0, outer).float()
+        right = self.w2.index_select(0, inner).float()
+        block = left.unsqueeze(2) * right.unsqueeze(1)  # [n, b, d]: w1[p, i] · w2[q, j]
+        return block.reshape(block.shape[0], -1).mul_(self.scale)
+
+
+class _DenseSum:
+    """Rows of the sum of several LoKr terms, the first term's rows accumulated in place."""
+
+    __slots__ = ("terms",)
+
+    def __init__(self, terms: Sequence[Kron]) -> None:
+        self.terms = tuple(terms)
+
+    def __call__(self, start: int, stop: int) -> Tensor:
+        total = self.terms[0](start, stop)
+        for term in self.terms[1:]:
+            total.add_(term(start, stop))
+        return total
 
 
 def dense(terms: Sequence[Kron]) -> Dense | None:
-    """The sum of `terms`' rows, None for none (`internal/lora_bake.py:227-239`)."""
-    if not terms:
-        return None
-    first, *rest = terms
-
-    def rows(start: int, stop: int) -> Tensor:
-        out = first(start, stop)
-        for term in rest:
-            out.add_(term(start, stop))
-        return out
-
-    return rows
+    """The dense rows of `terms` summed, or None for no terms (`internal/lora_bake.py:227-239`)."""
+    return _DenseSum(terms) if terms else None
 
 
 def _more_rows(torch: Any, more: Dense | None, rows: int, rotated: bool) -> Tensor | None:
@@ -317,6 +344,19 @@ def _rounding_flags(rounding: str, allowed: tuple[str, ...] = ("nearest", "stoch
     return NEAREST if rounding == "nearest" else 0
 
 
+def _noise_seed(torch: Any, seed: int | None, generator: Any, stochastic: bool) -> int:
+    """The 31-bit seed of an eager bake's noise: `seed` when given, else one drawn from
+    `generator` (so successive bakes from one generator get fresh streams, as the reference's
+    torch draws do). A stochastic bake with neither raises; a nearest one needs no noise."""
+    if seed is not None:
+        return int(seed) & SEED_MASK
+    if generator is not None:
+        return int(torch.randint(0, SEED_MASK + 1, (1,), generator=generator, device=generator.device).item())
+    if stochastic:
+        raise ValueError("a stochastic bake draws its noise from `seed` or `generator`; give one")
+    return 0
+
+
 def _scaled_up(torch: Any, up: Tensor, alpha: float) -> Tensor:
     """`up` times `alpha` before the product: the reference scales the product instead
     (`_delta`, `internal/lora_bake.py:242-246`), the same for a power of two and within a float32
@@ -327,14 +367,15 @@ def _scaled_up(torch: Any, up: Tensor, alpha: float) -> Tensor:
 
 def bake_plain(torch: Any, weight: Tensor, down: Tensor, up: Tensor, alpha: float, *,
                rounding: str = "nearest", generator: Any = None, stats: Any = None,
-               more: Dense | None = None, gain: Tensor | None = None, seed: int = 0) -> None:  # fmt: skip
+               more: Dense | None = None, gain: Tensor | None = None, seed: int | None = None) -> None:  # fmt: skip
     """`weight = gain * weight + alpha * up @ down`, float32, rounded once to its dtype
     (`internal/lora_bake.py:271-305`); bf16 rounds stochastically on request, other dtypes to
-    nearest. The noise is the Philox stream under `seed` (the reference's eager draws come from
-    `generator`, which is not used here)."""
+    nearest. The noise is the Philox stream under `seed`, or under a seed drawn from
+    `generator`."""
     flags = _rounding_flags(rounding)
     if weight.dtype != torch.bfloat16:
         flags = NEAREST
+    seed = _noise_seed(torch, seed, generator, flags == 0)
     fused(torch, {"value": weight}, down, _scaled_up(torch, up, alpha), seed, gain=gain, more=more,
           flags=flags, stats=stats)  # fmt: skip
 
@@ -346,7 +387,7 @@ ROW_SCALE_FLOOR, E4M3_MAX = 1e-12, 448.0
 
 def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tensor, alpha: float, *,
                  rounding: str = "nearest", grid: str = "refit", generator: Any = None,
-                 stats: Any = None, more: Dense | None = None, seed: int = 0) -> None:  # fmt: skip
+                 stats: Any = None, more: Dense | None = None, seed: int | None = None) -> None:  # fmt: skip
     """Bake into `fp8.rowwise` (`internal/lora_bake.py:319-363`): `data` `[out, in]` E4M3,
     `scale` one float32 per output row. `keep` rounds on the stored grid; `refit` sets each row's scale from its baked maximum,
     `max(amax / 448, 1e-12)`, and `regrid` raises that by 1/32 to 3/32 by the row's golden-ratio
@@ -359,6 +400,7 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
         raise ValueError(f"no grid {grid!r}")
     feedback = rounding == "feedback"
     flags = 0 if feedback else _rounding_flags(rounding)
+    seed = _noise_seed(torch, seed, generator, rounding == "stochastic")
     up_a = _scaled_up(torch, up, alpha)
     raw, scales = data.view(torch.uint8), scale.view(-1)
     if scales.dtype != torch.float32 or not scales.is_contiguous():
@@ -396,11 +438,12 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
 
 def bake_int8_convrot(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tensor, alpha: float, *,
                       rounding: str = "nearest", generator: Any = None, stats: Any = None,
-                      more: Dense | None = None, seed: int = 0) -> None:  # fmt: skip
+                      more: Dense | None = None, seed: int | None = None) -> None:  # fmt: skip
     """Bake into `int8-convrot256/1` (`internal/lora_bake.py:372-423`): `down` and the dense
     rows rotated into the weight's basis, the row scale kept, nearest or stochastic floor,
     clamped to ±127."""
     flags = _rounding_flags(rounding)
+    seed = _noise_seed(torch, seed, generator, flags == 0)
     fused(torch, {"weight": data, "scale": scale}, down, _scaled_up(torch, up, alpha), seed, more=more,
           flags=flags, stats=stats)  # fmt: skip
 
@@ -408,7 +451,7 @@ def bake_int8_convrot(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up:
 def bake_nvfp4(torch: Any, weight: Tensor, scale: Tensor, scale_2: Tensor, down: Tensor, up: Tensor,
                alpha: float, *, rounding: str = "stochastic", grid: str = "keep", generator: Any = None,
                stats: Any = None, more: Dense | None = None, gain: Tensor | None = None,
-               seed: int = 0) -> None:  # fmt: skip
+               seed: int | None = None) -> None:  # fmt: skip
     """Bake into canonical `nvfp4` (`internal/lora_bake.py:458-525`). `keep`: the second level
     kept and a block's scale refitted only past 7/6 of it. `refit`: the second level set from
     the baked tensor's amax and every block's scale from its own, saturation-free."""
@@ -417,6 +460,7 @@ def bake_nvfp4(torch: Any, weight: Tensor, scale: Tensor, scale_2: Tensor, down:
     if grid == "regrid":
         raise NotImplementedError("cozyq bakes nvfp4 on grid 'keep' or 'refit'")
     flags = _rounding_flags(rounding)
+    seed = _noise_seed(torch, seed, generator, flags == 0)
     if grid == "refit":
         _bake_nvfp4_refit(torch, weight, scale, scale_2, down, up, alpha, flags=flags, seed=seed, stats=stats,
                           more=more, gain=gain)  # fmt: skip

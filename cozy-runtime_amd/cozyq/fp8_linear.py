@@ -1,7 +1,7 @@
 """The fp8.rowwise linear's ops on gfx950 — cozyq's counterpart of cozy-runtime's
 `internal/fp8_linear.py` (`quantize`, `gemm`, `linear`, `serving`).
 
-As in `int8_linear`, the HIP kernels are the only implementation: where the reference falls
+As for every op here, the HIP kernels are the only implementation: where the reference falls
 back to torch ops and `_scaled_mm`, a tensor the kernels cannot take raises.
 """
 
@@ -9,7 +9,7 @@ from __future__ import annotations
 
 from typing import Any
 
-from cozyq import int8_linear
+from cozyq import _dispatch
 from cozyq.operands import ROWWISE_FP8, PreQuantized
 
 Tensor = Any
@@ -26,8 +26,8 @@ E4M3_MAX = 448.0
 def quantize(torch: Any, x: Tensor) -> PreQuantized:
     """`x` as the fp8 leaves' shared operand (`internal/fp8_linear.py:66-75`): E4M3 `[M, K]`
     and per-row float32 scales amax/448."""
-    index = int8_linear._served(torch, x)
-    payload, scale = int8_linear.library(index).fp8_quantize(x)
+    index = _dispatch.activation_card(OP, torch, x)
+    payload, scale = _dispatch.library(index).fp8_quantize(x)
     return PreQuantized(payload, scale, tuple(x.shape), ROWWISE_FP8)
 
 
@@ -37,24 +37,24 @@ def gemm(torch: Any, operand: PreQuantized, data: Tensor, scale: Tensor, bias: T
     epilogue, into `out` where given (`internal/fp8_linear.py:78-111`)."""
     if operand.payload.dtype != torch.float8_e4m3fn:
         raise ValueError(f"{OP}: the operand payload must be E4M3, not {operand.payload.dtype}")
-    index = int8_linear._card(operand.payload)
-    int8_linear._half(torch, out_dtype)
-    result = int8_linear.library(index).fp8_gemm(
+    index = _dispatch.card(OP, operand.payload)
+    _dispatch.sixteen_bit(OP, torch, out_dtype)
+    result = _dispatch.library(index).fp8_gemm(
         operand.payload, operand.scale, data, scale, bias, out_dtype,
-        out=int8_linear.into(out, data.shape[0]),
+        out=_dispatch.out_rows(out, data.shape[0]),
     )  # fmt: skip
-    return int8_linear.landed(result.view(*operand.shape[:-1], -1), out)
+    return _dispatch.deliver(result.view(*operand.shape[:-1], -1), out)
 
 
 def linear(torch: Any, x: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None,
            out_dtype: Dtype) -> Tensor:  # fmt: skip
     """`x @ W.T + bias` for one fp8.rowwise weight: `data` E4M3 `[N, K]`, `scale` float32
     (`internal/fp8_linear.py:114-129`); up to 16 rows in one fused launch."""
-    index = int8_linear._served(torch, x, out_dtype)
-    return int8_linear.library(index).fp8_linear(x, data, scale, bias, out_dtype)
+    index = _dispatch.activation_card(OP, torch, x, out_dtype)
+    return _dispatch.library(index).fp8_linear(x, data, scale, bias, out_dtype)
 
 
 def serving(index: int) -> str:
     """The GEMM this card's fp8 leaves serve (`internal/fp8_linear.py:132-141`)."""
-    int8_linear.library(index)
+    _dispatch.library(index)
     return OP

@@ -12,13 +12,12 @@ W4A4 provider serves this build's int4-g64 SVDQuant scheme in place of the refer
 
 from __future__ import annotations
 
-import functools
-from collections.abc import Mapping, Sequence
+from collections.abc import Callable, Mapping, Sequence
 from dataclasses import dataclass
 from typing import Any, ClassVar
 
+from cozyq import _dispatch, fp8_linear, int8_linear, layout, nvfp4_linear, prebuilt, w4a8_linear
 from cozyq import decode as dec
-from cozyq import fp8_linear, int8_linear, layout, nvfp4_linear, prebuilt, w4a8_linear
 from cozyq.operands import INT8_CONVROT, ROWWISE_FP8, PreQuantized, read, shared_operand
 
 Tensor = Any
@@ -31,8 +30,6 @@ SVDQ_INT4 = "cozyq.svdq-int4g64.native-leaf/1"
 NVFP4 = "cozy.nvfp4.native-leaf/1"
 #: The operand geometry each 8-bit leaf's GEMM reads (`internal/encoding/leaves.py:207`).
 OPERANDS = {INT8_CONVROT: INT8_CONVROT, ROWWISE_FP8: ROWWISE_FP8, W4A8: INT8_CONVROT}
-#: The 8-bit leaves' ops by provider (`internal/encoding/leaves.py:355`).
-_NATIVE_OPS: dict[str, Any] = {INT8_CONVROT: int8_linear, ROWWISE_FP8: fp8_linear}
 #: Rows a leaf sends to its op's one-launch linear instead of a shared operand: the int8 GEMV
 #: rows (the reference's `few`), and for fp8 the fused quantize + GEMV kernel's.
 _FEW_ROWS = {INT8_CONVROT: int8_linear.GEMV_ROWS, ROWWISE_FP8: 4}
@@ -51,205 +48,226 @@ def _rank2(shape: Sequence[int]) -> str:
 
 
 def _leaf_geometry(replaced: object, data: Tensor) -> tuple[int, int, Tensor | None]:
-    """`(in_features, out_features, bias)` of the module stood in for
-    (`internal/encoding/leaves.py:437-448`)."""
-    out_features, in_features = int(data.shape[0]), int(data.shape[1])
-    return in_features, out_features, getattr(replaced, "bias", None)
+    """`(in_features, out_features, bias)`: the features from the stored `[N, K]` weight, the
+    bias from the module stood in for (`internal/encoding/leaves.py:437-448`)."""
+    return int(data.shape[1]), int(data.shape[0]), getattr(replaced, "bias", None)
 
 
-def _leaf_class(torch: Any) -> Any:
-    """`EncodedLinear`, built once, lazily (`internal/encoding/leaves.py:234-355`): the roles
-    are buffers (never Parameters), registered under `BUFFERS`' names."""
-    cached = getattr(_leaf_class, "_cached", None)
+def _autocast_dtype(torch: Any, device: Any) -> Dtype | None:
+    kind = device.type
+    return torch.get_autocast_dtype(kind) if torch.is_autocast_enabled(kind) else None
+
+
+# ----------------------------------------------------------------------------- lanes
+#
+# A lane is how one family of leaves computes: the buffer names of its roles, whether its GEMM
+# writes the caller's `out`, the operand geometry it reads, and `run`. The module class below is
+# the same for every family and holds its lane.
+
+
+class _Lane:
+    buffers: Mapping[str, str] = {}
+    writes_into = False
+    operand: str | None = None
+
+    def run(self, torch: Any, leaf: Any, x: Any, prequantized: PreQuantized | None,
+            out: Tensor | None) -> Tensor:  # fmt: skip
+        raise NotImplementedError
+
+
+class _FloatLane(_Lane):
+    """Leaves that compute from the 16-bit activation and add the bias afterwards, in the
+    result's dtype (rules L3, L5): the MX and nvfp4 leaves. `compute(torch, leaf, x, out_dtype)`
+    is the product."""
+
+    def __init__(self, compute: Callable[..., Tensor], buffers: Mapping[str, str] | None = None) -> None:
+        self.compute = compute
+        self.buffers = dict(buffers or {})
+
+    def run(self, torch, leaf, x, prequantized, out):
+        if prequantized is not None or isinstance(x, PreQuantized):
+            raise ValueError(f"{leaf.provider} computes from the activation; it takes no quantized operand")
+        dtype = _autocast_dtype(torch, x.device)
+        product = self.compute(torch, leaf, x if dtype is None else x.to(dtype),
+                               leaf.out_dtype if dtype is None else dtype)  # fmt: skip
+        return product if leaf.bias is None else product + leaf.bias.to(product.dtype)
+
+
+class _QuantizedLane(_Lane):
+    """The 8-bit leaves (rule L4): a producer's operand goes straight to the GEMM; up to
+    `few` rows with no operand take the op's one-launch linear; otherwise the operand handed
+    in (if it has this lane's geometry) or one shared with the sibling leaves, else the
+    one-call linear. The bias is in the GEMM's epilogue; the GEMM writes `out`."""
+
+    buffers = {"weight": "data"}
+    writes_into = True
+
+    def __init__(self, operand: str, few: int) -> None:
+        self.operand = operand
+        self.few = few
+
+    # The op calls, per family.
+    def quantize(self, torch: Any, x: Tensor) -> PreQuantized | None:
+        return int8_linear.quantize(torch, x)
+
+    def gemm(self, torch, leaf, operand, out_dtype, out):
+        return int8_linear.gemm(torch, operand, read(leaf.data), read(leaf.scale), read(leaf.bias),
+                                out_dtype, out)  # fmt: skip
+
+    def linear(self, torch, leaf, x, out_dtype):
+        return int8_linear.linear(torch, x, read(leaf.data), read(leaf.scale), read(leaf.bias), out_dtype)
+
+    def run(self, torch, leaf, x, prequantized, out):
+        if isinstance(x, PreQuantized):
+            dtype = _autocast_dtype(torch, x.payload.device)
+            return self.gemm(torch, leaf, x, leaf.out_dtype if dtype is None else dtype, out)
+        dtype = _autocast_dtype(torch, x.device)
+        x16, out_dtype = (x, leaf.out_dtype) if dtype is None else (x.to(dtype), dtype)
+        operand = prequantized if prequantized is not None and prequantized.provider == self.operand else None
+        if operand is None:
+            if prequantized is None and x.numel() <= self.few * x.shape[-1]:
+                return _dispatch.deliver(self.linear(torch, leaf, x16, out_dtype), out)
+            capturing = x.is_cuda and torch.cuda.is_current_stream_capturing()
+            operand = shared_operand(x, self.operand, lambda: self.quantize(torch, x16),
+                                     None if capturing else leaf)  # fmt: skip
+        if operand is None:
+            return _dispatch.deliver(self.linear(torch, leaf, x16, out_dtype), out)
+        return self.gemm(torch, leaf, operand, out_dtype, out)
+
+
+class _Fp8Lane(_QuantizedLane):
+    def quantize(self, torch, x):
+        return fp8_linear.quantize(torch, x)
+
+    def gemm(self, torch, leaf, operand, out_dtype, out):
+        return fp8_linear.gemm(torch, operand, read(leaf.data), read(leaf.scale), read(leaf.bias),
+                               out_dtype, out)  # fmt: skip
+
+    def linear(self, torch, leaf, x, out_dtype):
+        return fp8_linear.linear(torch, x, read(leaf.data), read(leaf.scale), read(leaf.bias), out_dtype)
+
+
+class _W4a8Lane(_QuantizedLane):
+    """w4a8 codes on int8.convrot's operand: the int8 lane's quantize, its own GEMM."""
+
+    @staticmethod
+    def _weights(leaf: Any) -> prebuilt.W4a8:
+        return prebuilt.W4a8(read(leaf.data), read(leaf.group_scale), read(leaf.scale),
+                             read(leaf._buffers.get("codebook")))  # fmt: skip
+
+    def gemm(self, torch, leaf, operand, out_dtype, out):
+        return w4a8_linear.gemm(torch, operand, self._weights(leaf), read(leaf.bias), out_dtype, out)
+
+    def linear(self, torch, leaf, x, out_dtype):
+        return w4a8_linear.linear(torch, x, self._weights(leaf), read(leaf.bias), out_dtype)
+
+
+class _SvdqLane(_Lane):
+    """The W4A4 leaf: smoothing, int4 activation codes and the low-rank input in one launch,
+    then the GEMM with the low-rank term and the bias before its one rounding."""
+
+    def run(self, torch, leaf, x, prequantized, out):
+        if prequantized is not None or isinstance(x, PreQuantized):
+            raise ValueError("the svdq leaf quantizes its own input; it takes no shared operand")
+        dtype = _autocast_dtype(torch, x.device)
+        out_dtype = leaf.out_dtype if dtype is None else dtype
+        x = x if dtype is None else x.to(dtype)
+        index = _dispatch.activation_card("svdq", torch, x, out_dtype)
+        result = _dispatch.library(index).svdq_linear(
+            x, read(leaf.pre_quant_scale), read(leaf.lowrank_down), read(leaf.weight),
+            read(leaf.scale), read(leaf.lowrank_up), read(leaf.bias), out_dtype)  # fmt: skip
+        return result
+
+
+def _mx_product(torch: Any, leaf: Any, x: Tensor, out_dtype: Dtype) -> Tensor:
+    """The MX leaf's product (`internal/encoding/leaves.py:1505-1516`): x quantized per 32-block
+    at dispatch, then the scaled-MFMA GEMM; the lane adds the bias after the cast."""
+    index = _dispatch.activation_card("mxfp8", torch, x, out_dtype)
+    return _dispatch.library(index).mx_linear(x, leaf.weight, leaf.scale, None, out_dtype).reshape(
+        *x.shape[:-1], -1)  # fmt: skip
+
+
+def _nvfp4_product(torch: Any, leaf: Any, x: Tensor, out_dtype: Dtype) -> Tensor:
+    """The nvfp4 leaf's product (`internal/encoding/leaves.py:1158-1170`)."""
+    return nvfp4_linear.matmul(torch, x, leaf.weight, leaf.weight_scale, None, leaf.weight_scale_2,
+                               out_dtype)  # fmt: skip
+
+
+_NVFP4_BUFFERS = {"scale": "weight_scale", "scale_2": "weight_scale_2"}
+
+
+def _module_class(torch: Any) -> Any:
+    """The `nn.Module` every encoded leaf is (built once, on first use): rules L1–L2, the rest
+    delegated to the leaf's lane."""
+    cached = getattr(_module_class, "_cached", None)
     if cached is not None:
         return cached
-    from torch import nn
 
-    class EncodedLinear(nn.Module):
-        """One linear whose weight is its encoded role set, computed by an encoded GEMM."""
+    class EncodedLinear(torch.nn.Module):
+        """A linear whose weight is its encoded role buffers; `forward` runs its lane."""
 
-        BUFFERS: ClassVar[dict[str, str]] = {}
-        WRITES_INTO: ClassVar[bool] = False
         PURE_WINDOWS: ClassVar[bool] = True
 
-        def __init__(self, forward_fn, roles: Mapping[str, Tensor], bias: Tensor | None,
+        def __init__(self, lane: _Lane, roles: Mapping[str, Tensor], bias: Tensor | None,
                      out_dtype: Dtype, provider: str, encoding: str, in_features: int,
                      out_features: int) -> None:  # fmt: skip
             super().__init__()
-            # The replaced projection's compute dtype, for code that reads the first floating
-            # buffer before casting activations; no bytes, not persisted.
-            self.register_buffer("_logical_dtype",
-                                 next(iter(roles.values())).new_empty(0, dtype=out_dtype),
-                                 persistent=False)  # fmt: skip
-            self._cozy_forward = forward_fn
+            self._cozy_lane = lane
             self._cozy_roles = tuple(sorted(roles))
-            for role, tensor in sorted(roles.items()):
-                self.register_buffer(self.BUFFERS.get(role, role), tensor)
+            device = next(iter(roles.values())).device
+            self.register_buffer("_logical_dtype", torch.empty(0, dtype=out_dtype, device=device),
+                                 persistent=False)  # fmt: skip
+            for role in self._cozy_roles:
+                self.register_buffer(lane.buffers.get(role, role), roles[role])
             self.register_buffer("bias", bias)
             self.out_dtype = out_dtype
-            self.provider = provider
-            self.encoding = encoding
-            self.in_features = in_features
-            self.out_features = out_features
-
-        def roles(self) -> dict[str, Tensor]:
-            return {role: getattr(self, self.BUFFERS.get(role, role)) for role in self._cozy_roles}
-
-        def forward(self, x: Tensor, *, prequantized: PreQuantized | None = None,
-                    out: Tensor | None = None) -> Tensor:  # fmt: skip
-            """The linear; with `out` (e.g. this linear's column range of a sibling group's
-            packed output) the result lands there, which it also returns."""
-            if out is None:
-                return self.linear(x, prequantized)
-            if self.WRITES_INTO:
-                return self.linear(x, prequantized, out)
-            out.copy_(self.linear(x, prequantized))
-            return out
-
-        def linear(self, x: Tensor, prequantized: PreQuantized | None,
-                   out: Tensor | None = None) -> Tensor:  # fmt: skip
-            forward = self._cozy_forward
-            assert forward is not None  # a leaf built without one overrides `linear`
-            if prequantized is None and torch.is_autocast_enabled(x.device.type):
-                dtype = torch.get_autocast_dtype(x.device.type)
-                result = forward(self, x.to(dtype), dtype)
-            else:
-                result = forward(self, x if prequantized is None else prequantized, self.out_dtype)
-            if self.bias is not None:
-                result = result + self.bias.to(result.dtype)
-            return result
-
-        def extra_repr(self) -> str:
-            return (f"in_features={self.in_features}, out_features={self.out_features}, "
-                    f"provider={self.provider!r}, roles={list(self._cozy_roles)}, "
-                    f"out_dtype={self.out_dtype}")  # fmt: skip
-
-    _leaf_class._cached = EncodedLinear
-    return EncodedLinear
-
-
-def _native_leaf_class(torch: Any) -> Any:
-    """`NativeLinear` (`internal/encoding/leaves.py:358-434`): the forward is one call of its
-    provider's op, the bias in the GEMM's epilogue, and a shared operand where siblings read
-    the same input."""
-    cached = getattr(_native_leaf_class, "_cached", None)
-    if cached is not None:
-        return cached
-
-    class NativeLinear(_leaf_class(torch)):
-        BUFFERS: ClassVar[dict[str, str]] = {"weight": "data"}
-        WRITES_INTO: ClassVar[bool] = True
+            self.provider, self.encoding = provider, encoding
+            self.in_features, self.out_features = in_features, out_features
 
         @property
-        def operand(self) -> str:
-            return OPERANDS[self.provider]
+        def BUFFERS(self) -> dict[str, str]:  # noqa: N802 (the reference's attribute name)
+            return dict(self._cozy_lane.buffers)
 
-        def linear(self, x, prequantized, out=None):
-            ops = _NATIVE_OPS[self.provider]
-            out_dtype = self.out_dtype
-            data, scale, bias = read(self.data), read(self.scale), read(self.bias)
-            if isinstance(x, PreQuantized):
-                # A producer's prologue (`int8_rows`) hands the operand in place of x.
-                if torch.is_autocast_enabled(x.payload.device.type):
-                    out_dtype = torch.get_autocast_dtype(x.payload.device.type)
-                return ops.gemm(torch, x, data, scale, bias, out_dtype, out)
-            cast = x
-            if torch.is_autocast_enabled(x.device.type):
-                out_dtype = torch.get_autocast_dtype(x.device.type)
-                cast = x.to(out_dtype)
-            few = x.numel() <= _FEW_ROWS[self.provider] * x.shape[-1]
-            if prequantized is None and few:
-                # A decode step's few rows: the op's one-launch linear.
-                return int8_linear.landed(ops.linear(torch, cast, data, scale, bias, out_dtype), out)
-            if prequantized is None or prequantized.provider != self.provider:
-                capturing = x.is_cuda and torch.cuda.is_current_stream_capturing()
-                sibling = None if capturing else self
-                prequantized = shared_operand(x, self.provider, lambda: ops.quantize(torch, cast),
-                                              sibling)  # fmt: skip
-            if prequantized is not None:
-                return ops.gemm(torch, prequantized, data, scale, bias, out_dtype, out)
-            return int8_linear.landed(ops.linear(torch, cast, data, scale, bias, out_dtype), out)
+        @property
+        def WRITES_INTO(self) -> bool:  # noqa: N802
+            return self._cozy_lane.writes_into
+
+        @property
+        def operand(self) -> str | None:
+            """The activation geometry this leaf's GEMM reads (8-bit leaves), else None."""
+            return self._cozy_lane.operand
+
+        def roles(self) -> dict[str, Tensor]:
+            names = self._cozy_lane.buffers
+            return {role: getattr(self, names.get(role, role)) for role in self._cozy_roles}
+
+        def forward(self, x: Any, *, prequantized: PreQuantized | None = None,
+                    out: Tensor | None = None) -> Tensor:  # fmt: skip
+            lane = self._cozy_lane
+            result = lane.run(torch, self, x, prequantized, out if lane.writes_into else None)
+            if out is None or result is out:
+                return result
+            out.copy_(result)
+            return out
 
         def int8_prologue(self, x, consumers, norm, eps, scale, shift, activation, up=None):
-            """`int8_rows` for consumers led by this leaf."""
+            """`int8_rows` for consumers led by this leaf (int8.convrot's operand)."""
             return int8_linear.prologue(torch, x, consumers, norm=norm, eps=eps, scale=scale,
                                         shift=shift, activation=activation, up=up)  # fmt: skip
 
-    _native_leaf_class._cached = NativeLinear
-    return NativeLinear
+        def extra_repr(self) -> str:
+            return ", ".join((f"in_features={self.in_features}", f"out_features={self.out_features}",
+                              f"provider={self.provider!r}", f"roles={list(self._cozy_roles)}",
+                              f"out_dtype={self.out_dtype}"))  # fmt: skip
+
+    _module_class._cached = EncodedLinear
+    return EncodedLinear
 
 
-def _w4a8_leaf_class(torch: Any) -> Any:
-    """`NativeLinear` over w4a8's roles (`internal/encoding/leaves.py:900-942`): its GEMM
-    (`w4a8_linear`) on int8.convrot's operand, shared with the int8 leaves."""
-    cached = getattr(_w4a8_leaf_class, "_cached", None)
-    if cached is not None:
-        return cached
-
-    class W4a8Linear(_native_leaf_class(torch)):
-        def weights(self) -> prebuilt.W4a8:
-            return prebuilt.W4a8(read(self.data), read(self.group_scale), read(self.scale),
-                                 read(self._buffers.get("codebook")))  # fmt: skip
-
-        def linear(self, x, prequantized, out=None):
-            out_dtype = self.out_dtype
-            if isinstance(x, PreQuantized):
-                if torch.is_autocast_enabled(x.payload.device.type):
-                    out_dtype = torch.get_autocast_dtype(x.payload.device.type)
-                return w4a8_linear.gemm(torch, x, self.weights(), read(self.bias), out_dtype, out)
-            cast = x
-            if torch.is_autocast_enabled(x.device.type):
-                out_dtype = torch.get_autocast_dtype(x.device.type)
-                cast = x.to(out_dtype)
-            if prequantized is None or prequantized.provider != INT8_CONVROT:
-                capturing = x.is_cuda and torch.cuda.is_current_stream_capturing()
-                sibling = None if capturing else self
-                prequantized = shared_operand(x, INT8_CONVROT,
-                                              lambda: int8_linear.quantize(torch, cast), sibling)  # fmt: skip
-            if prequantized is not None:
-                return w4a8_linear.gemm(torch, prequantized, self.weights(), read(self.bias),
-                                        out_dtype, out)  # fmt: skip
-            return int8_linear.landed(
-                w4a8_linear.linear(torch, cast, self.weights(), read(self.bias), out_dtype), out)
-
-    _w4a8_leaf_class._cached = W4a8Linear
-    return W4a8Linear
-
-
-def _svdq_leaf_class(torch: Any) -> Any:
-    """The W4A4 leaf: smoothing, int4 activations and the low-rank input in one launch, then
-    the GEMM with the low-rank add and the bias in its epilogue (one rounding)."""
-    cached = getattr(_svdq_leaf_class, "_cached", None)
-    if cached is not None:
-        return cached
-
-    class SvdqLinear(_leaf_class(torch)):
-        def linear(self, x, prequantized, out=None):
-            if prequantized is not None:
-                raise ValueError("the svdq leaf quantizes its own input; it takes no shared operand")
-            out_dtype = self.out_dtype
-            if torch.is_autocast_enabled(x.device.type):
-                out_dtype = torch.get_autocast_dtype(x.device.type)
-                x = x.to(out_dtype)
-            int8_linear._served(torch, x, out_dtype)
-            lib = int8_linear.library(x.get_device())
-            result = lib.svdq_linear(x, read(self.pre_quant_scale), read(self.lowrank_down),
-                                     read(self.weight), read(self.scale), read(self.lowrank_up),
-                                     read(self.bias), out_dtype)  # fmt: skip
-            return int8_linear.landed(result, out)
-
-    _svdq_leaf_class._cached = SvdqLinear
-    return SvdqLinear
-
-
-def _mx_forward(torch: Any, leaf: Any, x: Tensor, out_dtype: Dtype) -> Tensor:
-    """`MicroScaledNativeLeaf._forward` (`internal/encoding/leaves.py:1505-1516`): the
-    activation quantized per 32-block at dispatch, the scaled-MFMA GEMM; the bias is added by
-    `EncodedLinear.linear` after the cast, as the reference's is."""
-    int8_linear._served(torch, x, out_dtype)
-    lib = int8_linear.library(x.get_device())
-    out = lib.mx_linear(x, leaf.weight, leaf.scale, None, out_dtype)
-    return out.reshape(*x.shape[:-1], -1)
+def _build(torch: Any, lane: _Lane, roles: Mapping[str, Tensor], bias: Tensor | None,
+           out_dtype: Dtype, provider: Any, in_features: int, out_features: int) -> Any:  # fmt: skip
+    return _module_class(torch)(lane, roles, bias, out_dtype, provider.name, provider.encoding,
+                                in_features, out_features)  # fmt: skip
 
 
 class _Provider:
@@ -314,9 +332,9 @@ class RowwiseNativeLeaf(_Provider):
     def leaf(self, torch: Any, parts: Mapping[str, Tensor], replaced: object, out_dtype: Dtype) -> Any:
         data = parts["weight"]
         in_features, out_features, bias = _leaf_geometry(replaced, data)
-        return _native_leaf_class(torch)(
-            None, {"weight": data, "scale": parts["scale"].to(torch.float32)}, bias, out_dtype,
-            self.name, self.encoding, in_features, out_features)  # fmt: skip
+        return _build(torch, _Fp8Lane(ROWWISE_FP8, _FEW_ROWS[ROWWISE_FP8]),
+                      {"weight": data, "scale": parts["scale"].to(torch.float32)}, bias, out_dtype,
+                      self, in_features, out_features)  # fmt: skip
 
 
 @dataclass(frozen=True, slots=True)
@@ -350,9 +368,9 @@ class Int8ConvRotNativeLeaf(_Provider):
     def leaf(self, torch: Any, parts: Mapping[str, Tensor], replaced: object, out_dtype: Dtype) -> Any:
         data = parts["weight"]
         in_features, out_features, bias = _leaf_geometry(replaced, data)
-        return _native_leaf_class(torch)(
-            None, {"weight": data, "scale": parts["scale"].to(torch.float32)}, bias, out_dtype,
-            self.name, self.encoding, in_features, out_features)  # fmt: skip
+        return _build(torch, _QuantizedLane(INT8_CONVROT, _FEW_ROWS[INT8_CONVROT]),
+                      {"weight": data, "scale": parts["scale"].to(torch.float32)}, bias, out_dtype,
+                      self, in_features, out_features)  # fmt: skip
 
 
 @dataclass(frozen=True, slots=True)
@@ -390,9 +408,9 @@ class W4a8NativeLeaf(_Provider):
                  "scale": parts["scale"].to(torch.float32)}  # fmt: skip
         if "codebook" in parts:
             roles["codebook"] = parts["codebook"].to(torch.float32)
-        return _w4a8_leaf_class(torch)(None, roles, getattr(replaced, "bias", None), out_dtype,
-                                       self.name, self.encoding, 2 * int(codes.shape[1]),
-                                       int(codes.shape[0]))  # fmt: skip
+        return _build(torch, _W4a8Lane(INT8_CONVROT, _FEW_ROWS[INT8_CONVROT]), roles,
+                      getattr(replaced, "bias", None), out_dtype, self, 2 * int(codes.shape[1]),
+                      int(codes.shape[0]))  # fmt: skip
 
 
 @dataclass(frozen=True, slots=True)
@@ -440,9 +458,8 @@ class MicroScaledNativeLeaf(_Provider):
             scale = layout.from_blocked(torch, scale, rows, cols)
         else:
             scale = scale.reshape(rows, cols).contiguous()
-        return _leaf_class(torch)(
-            functools.partial(_mx_forward, torch), {"weight": weight, "scale": scale}, bias,
-            out_dtype, self.name, self.encoding, in_features, out_features)  # fmt: skip
+        return _build(torch, _FloatLane(_mx_product), {"weight": weight, "scale": scale}, bias,
+                      out_dtype, self, in_features, out_features)  # fmt: skip
 
 
 @dataclass(frozen=True, slots=True)
@@ -486,27 +503,8 @@ class SvdqInt4NativeLeaf(_Provider):
             "lowrank_down": parts["lowrank_down"].to(torch.bfloat16),
             "lowrank_up": parts["lowrank_up"].to(torch.bfloat16),
         }
-        return _svdq_leaf_class(torch)(None, roles, getattr(replaced, "bias", None), out_dtype,
-                                       self.name, self.encoding, in_features, out_features)  # fmt: skip
-
-
-def _nvfp4_leaf_class(torch: Any) -> Any:
-    """`EncodedLinear` keyed by nvfp4's stored roles (`internal/encoding/leaves.py:1056-1065`)."""
-    cached = getattr(_nvfp4_leaf_class, "_cached", None)
-    if cached is not None:
-        return cached
-
-    class Nvfp4Linear(_leaf_class(torch)):  # type: ignore[misc]
-        BUFFERS: ClassVar[dict[str, str]] = {"scale": "weight_scale", "scale_2": "weight_scale_2"}
-
-    _nvfp4_leaf_class._cached = Nvfp4Linear
-    return Nvfp4Linear
-
-
-def _nvfp4_forward(torch: Any, leaf: Any, x: Tensor, out_dtype: Dtype) -> Tensor:
-    """`Nvfp4NativeLeaf._forward` (`internal/encoding/leaves.py:1158-1170`)."""
-    return nvfp4_linear.matmul(torch, x, leaf.weight, leaf.weight_scale, None, leaf.weight_scale_2,
-                               out_dtype)  # fmt: skip
+        return _build(torch, _SvdqLane(), roles, getattr(replaced, "bias", None), out_dtype, self,
+                      in_features, out_features)  # fmt: skip
 
 
 @dataclass(frozen=True, slots=True)
@@ -563,11 +561,9 @@ class Nvfp4NativeLeaf(_Provider):
         second = parts["scale_2"].to(torch.float32).reshape(1)
         if params.get("global_scale") == "divide":
             second = 1.0 / second
-        return _nvfp4_leaf_class(torch)(
-            functools.partial(_nvfp4_forward, torch),
-            {"weight": weight, "scale": blocked.view(torch.float8_e4m3fn), "scale_2": second},
-            getattr(replaced, "bias", None), out_dtype, self.name, self.encoding, in_features,
-            out_features)  # fmt: skip
+        return _build(torch, _FloatLane(_nvfp4_product, _NVFP4_BUFFERS),
+                      {"weight": weight, "scale": blocked.view(torch.float8_e4m3fn), "scale_2": second},
+                      getattr(replaced, "bias", None), out_dtype, self, in_features, out_features)  # fmt: skip
 
 
 def launch_providers() -> dict[str, tuple[Any, ...]]:

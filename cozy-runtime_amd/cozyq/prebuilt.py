@@ -724,8 +724,6 @@ class Prebuilt:
         data = after["data"]
         rows = int(data.shape[0])
         rank = self._factors(up, down, rows, cols, tuple(after.values()) + tuple(before.values()), gain, more)
-        if rank > 128:
-            raise ValueError("LoRA bake accounting: rank above 128")
         partial = self.torch.empty((rows + 63) // 64, 7, dtype=self.torch.float64, device=data.device)
         code = self._lib.cozyq_bake_stats(
             self.index, form, before["data"].data_ptr(), data.data_ptr(), _ptr(before.get("scale")),

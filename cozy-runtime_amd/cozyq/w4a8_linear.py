@@ -3,7 +3,7 @@
 unpacked to int8 levels on the way to the int8 MFMA and multiplied with int8.convrot's
 activation operand (quantized by the int8 leaves' op and shared with them).
 
-As in `int8_linear`, the HIP kernels are the only implementation: the reference's torch-ops
+As for every op here, the HIP kernels are the only implementation: the reference's torch-ops
 slow path (unpack, then the int8 lane's GEMM) is the many-row config of `Prebuilt.w4a8_gemm`
 itself, on the GPU.
 """
@@ -12,7 +12,7 @@ from __future__ import annotations
 
 from typing import Any
 
-from cozyq import int8_linear, prebuilt
+from cozyq import _dispatch, prebuilt
 from cozyq.operands import INT8_CONVROT, PreQuantized
 
 Tensor = Any
@@ -26,8 +26,8 @@ OPERAND = INT8_CONVROT
 
 def linear(torch: Any, x: Tensor, w: prebuilt.W4a8, bias: Tensor | None, out_dtype: Dtype) -> Tensor:
     """`x @ W.T + bias` for one w4a8 weight (`internal/w4a8_linear.py:72-84`)."""
-    index = int8_linear._served(torch, x, out_dtype)
-    return int8_linear.library(index).w4a8_linear(x, w, bias, out_dtype)
+    index = _dispatch.activation_card(OP, torch, x, out_dtype)
+    return _dispatch.library(index).w4a8_linear(x, w, bias, out_dtype)
 
 
 def gemm(torch: Any, operand: PreQuantized, w: prebuilt.W4a8, bias: Tensor | None,
@@ -36,13 +36,13 @@ def gemm(torch: Any, operand: PreQuantized, w: prebuilt.W4a8, bias: Tensor | Non
     copied into `out` where given (`internal/w4a8_linear.py:87-107`)."""
     if operand.provider != INT8_CONVROT or operand.payload.dtype != torch.int8:
         raise ValueError(f"{OP}: the operand must be int8.convrot's, not {operand.provider}")
-    index = int8_linear._card(operand.payload)
-    int8_linear._half(torch, out_dtype)
-    result = int8_linear.library(index).w4a8_gemm(operand.payload, operand.scale, w, bias, out_dtype)
-    return int8_linear.landed(result.view(*operand.shape[:-1], -1), out)
+    index = _dispatch.card(OP, operand.payload)
+    _dispatch.sixteen_bit(OP, torch, out_dtype)
+    result = _dispatch.library(index).w4a8_gemm(operand.payload, operand.scale, w, bias, out_dtype)
+    return _dispatch.deliver(result.view(*operand.shape[:-1], -1), out)
 
 
 def serving(index: int) -> str:
     """The kernel this card's w4a8 leaves serve (`internal/w4a8_linear.py:64-69`)."""
-    int8_linear.library(index)
+    _dispatch.library(index)
     return OP

@@ -522,7 +522,7 @@ int cozyq_bake_stats(int device, int form, const void* before, const void* after
                      const float* scale_after, const uint8_t* blocks_before, const uint8_t* blocks_after,
                      const float* second, const float* gain, const float* more, const float* up,
                      const float* down, int64_t rows, int64_t cols, int64_t rank, double* partial, void* stream) {
-    if (form < cozyq::kBakeBf16 || form > cozyq::kBakeNvfp4 || !bake_shape(rows, cols, rank) || rank > 128 ||
+    if (form < cozyq::kBakeBf16 || form > cozyq::kBakeNvfp4 || !bake_shape(rows, cols, rank) ||
         (form == cozyq::kBakeNvfp4 && cols % 16))
         return hipErrorInvalidValue;
     if (rows == 0) return hipSuccess;

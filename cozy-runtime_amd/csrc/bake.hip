@@ -553,81 +553,90 @@ __global__ __launch_bounds__(kBakeThreads) void bake_stats_kernel(StatsArgs a, c
     __shared__ double red[kBakeThreads / 64][kStatTerms];
     const int row0 = blockIdx.x * kTileRows;
     const int tid = threadIdx.x, rg = tid >> 4, cg = tid & 15;
-    for (int e = tid; e < 2 * kTileRows * kStatRanks; e += kBakeThreads) (&proj[0][0][0])[e] = 0.0f;
     const float level = kForm == kBakeNvfp4 ? a.second[0] : 1.0f;
     double sum[5] = {0.0, 0.0, 0.0, 0.0, 0.0};  // target², delta², error², kept, saturated
-    for (int col0 = 0; col0 < cols; col0 += kTileCols) {
-        float acc[4][8];
-        tile_delta(acc, up, down, rows, cols, rank, row0, col0, up_lds, down_lds);  // syncs before reuse
-        float dv[4][8], ev[4][8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = row0 + 4 * rg + i;
-            const float gain = (kForm <= kBakeF32 || kForm == kBakeNvfp4) && a.gain && row < rows ? a.gain[row] : 1.0f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int col = col0 + tile_col(cg, j);
-                dv[i][j] = 0.0f;
-                ev[i][j] = 0.0f;
-                if (row >= rows || col >= cols) continue;
-                const int64_t at = static_cast<int64_t>(row) * cols + col;
-                float base = stat_value<kForm>(a.before, a.scale_before, a.blocks_before, level, at, row, col, cols);
-                if constexpr (kForm <= kBakeF32 || kForm == kBakeNvfp4) base = base * gain;
-                const float d = a.more ? acc[i][j] + a.more[at] : acc[i][j];
-                const float target = base + d;
-                const float stored = stat_value<kForm>(a.after, a.scale_after, a.blocks_after, level, at, row, col, cols);
-                const float err = stored - target;
-                sum[0] += static_cast<double>(target) * target;
-                sum[1] += static_cast<double>(d) * d;
-                sum[2] += static_cast<double>(err) * err;
-                sum[3] += static_cast<double>(stored - base) * static_cast<double>(d);
-                if constexpr (kForm == kBakeRowwise) {
-                    sum[4] += __builtin_fabsf(target / a.scale_after[row]) > 464.0f ? 1.0 : 0.0;
-                } else if constexpr (kForm == kBakeInt8) {
-                    const float code = static_cast<float>(static_cast<const int8_t*>(a.before)[at]);
-                    sum[4] += __builtin_fabsf(code + d / a.scale_before[row]) > 127.5f ? 1.0 : 0.0;
-                } else if constexpr (kForm == kBakeNvfp4) {
-                    const float unit = e4m3_sat(a.blocks_after[static_cast<int64_t>(row) * (cols / 16) + col / 16]) * level;
-                    sum[4] += unit > 0.0f && __builtin_fabsf(target / unit) > 6.0f ? 1.0 : 0.0;
-                }
-                dv[i][j] = d;
-                ev[i][j] = err;
-            }
-        }
-        // The projections onto down's rows: each lane's 8 columns, then the 16 lanes of a row group.
-        for (int r = 0; r < rank; ++r) {
-            float dcol[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int col = col0 + tile_col(cg, j);
-                dcol[j] = col < cols ? down[static_cast<int64_t>(r) * cols + col] : 0.0f;
-            }
+    double effect = 0.0, effect_error = 0.0;
+    // The rank-space projections are taken kStatRanks ranks at a time (LDS holds one slice per
+    // row); each slice walks the columns again with the whole delta, and the element sums are
+    // taken on the first walk only.
+    for (int p0 = 0; p0 == 0 || p0 < rank; p0 += kStatRanks) {
+        const int p1 = min(rank, p0 + kStatRanks);
+        for (int e = tid; e < 2 * kTileRows * kStatRanks; e += kBakeThreads) (&proj[0][0][0])[e] = 0.0f;
+        for (int col0 = 0; col0 < cols; col0 += kTileCols) {
+            float acc[4][8];
+            tile_delta(acc, up, down, rows, cols, rank, row0, col0, up_lds, down_lds);  // syncs before reuse
+            float dv[4][8], ev[4][8];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float pd = 0.0f, pe = 0.0f;
+                const int row = row0 + 4 * rg + i;
+                const float gain = (kForm <= kBakeF32 || kForm == kBakeNvfp4) && a.gain && row < rows ? a.gain[row] : 1.0f;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    pd = __builtin_fmaf(dv[i][j], dcol[j], pd);
-                    pe = __builtin_fmaf(ev[i][j], dcol[j], pe);
+                    const int col = col0 + tile_col(cg, j);
+                    dv[i][j] = 0.0f;
+                    ev[i][j] = 0.0f;
+                    if (row >= rows || col >= cols) continue;
+                    const int64_t at = static_cast<int64_t>(row) * cols + col;
+                    float base = stat_value<kForm>(a.before, a.scale_before, a.blocks_before, level, at, row, col, cols);
+                    if constexpr (kForm <= kBakeF32 || kForm == kBakeNvfp4) base = base * gain;
+                    const float d = a.more ? acc[i][j] + a.more[at] : acc[i][j];
+                    const float target = base + d;
+                    const float stored = stat_value<kForm>(a.after, a.scale_after, a.blocks_after, level, at, row, col, cols);
+                    const float err = stored - target;
+                    dv[i][j] = d;
+                    ev[i][j] = err;
+                    if (p0 != 0) continue;
+                    sum[0] += static_cast<double>(target) * target;
+                    sum[1] += static_cast<double>(d) * d;
+                    sum[2] += static_cast<double>(err) * err;
+                    sum[3] += static_cast<double>(stored - base) * static_cast<double>(d);
+                    if constexpr (kForm == kBakeRowwise) {
+                        sum[4] += __builtin_fabsf(target / a.scale_after[row]) > 464.0f ? 1.0 : 0.0;
+                    } else if constexpr (kForm == kBakeInt8) {
+                        const float code = static_cast<float>(static_cast<const int8_t*>(a.before)[at]);
+                        sum[4] += __builtin_fabsf(code + d / a.scale_before[row]) > 127.5f ? 1.0 : 0.0;
+                    } else if constexpr (kForm == kBakeNvfp4) {
+                        const float unit = e4m3_sat(a.blocks_after[static_cast<int64_t>(row) * (cols / 16) + col / 16]) * level;
+                        sum[4] += unit > 0.0f && __builtin_fabsf(target / unit) > 6.0f ? 1.0 : 0.0;
+                    }
+                }
+            }
+            // The slice's projections onto down's rows: each lane's 8 columns, then the 16 lanes
+            // of a row group.
+            for (int r = p0; r < p1; ++r) {
+                float dcol[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int col = col0 + tile_col(cg, j);
+                    dcol[j] = col < cols ? down[static_cast<int64_t>(r) * cols + col] : 0.0f;
                 }
 #pragma unroll
-                for (int off = 1; off < 16; off <<= 1) {
-                    pd += __shfl_xor(pd, off);
-                    pe += __shfl_xor(pe, off);
-                }
-                if (cg == 0) {
-                    proj[0][4 * rg + i][r] += pd;
-                    proj[1][4 * rg + i][r] += pe;
+                for (int i = 0; i < 4; ++i) {
+                    float pd = 0.0f, pe = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        pd = __builtin_fmaf(dv[i][j], dcol[j], pd);
+                        pe = __builtin_fmaf(ev[i][j], dcol[j], pe);
+                    }
+#pragma unroll
+                    for (int off = 1; off < 16; off <<= 1) {
+                        pd += __shfl_xor(pd, off);
+                        pe += __shfl_xor(pe, off);
+                    }
+                    if (cg == 0) {
+                        proj[0][4 * rg + i][r - p0] += pd;
+                        proj[1][4 * rg + i][r - p0] += pe;
+                    }
                 }
             }
         }
-    }
-    __syncthreads();
-    double effect = 0.0, effect_error = 0.0;
-    for (int e = tid; e < kTileRows * kStatRanks; e += kBakeThreads) {
-        const double pd = (&proj[0][0][0])[e], pe = (&proj[1][0][0])[e];
-        effect += pd * pd;
-        effect_error += pe * pe;
+        __syncthreads();
+        for (int e = tid; e < kTileRows * kStatRanks; e += kBakeThreads) {
+            const double pd = (&proj[0][0][0])[e], pe = (&proj[1][0][0])[e];
+            effect += pd * pd;
+            effect_error += pe * pe;
+        }
+        __syncthreads();  // the next slice clears the projections
     }
     double terms[kStatTerms] = {sum[0], sum[1], sum[2], sum[3], sum[4], effect, effect_error};
     const int wave = tid >> 6, lane = tid & 63;

@@ -328,7 +328,8 @@ int cozyq_bake_feedback(int device, uint8_t* data, const float* scale, const flo
  * took (form 4: `down` and `more` rotated). target = base + delta, decoded as the eager reference
  * decodes; partial receives 7 doubles per 64-row group, ceil(rows / 64) · 7 in all: Σ target²,
  * Σ delta², Σ (stored − target)², Σ (stored − base)·delta, the saturated count, Σ (delta @ downᵀ)²
- * and Σ ((stored − target) @ downᵀ)², each in a fixed order. rank ≤ 128. */
+ * and Σ ((stored − target) @ downᵀ)², each in a fixed order (any rank: the projections are taken
+ * 128 ranks at a time). */
 int cozyq_bake_stats(int device, int form, const void* before, const void* after,
                      const float* scale_before, const float* scale_after,
                      const uint8_t* blocks_before, const uint8_t* blocks_after, const float* second,

@@ -9,6 +9,7 @@ the oracle over ragged shapes, ranks and seeds, through the C ABI and the host m
 
 from __future__ import annotations
 
+import math
 import json
 import random
 from fractions import Fraction
@@ -829,15 +830,50 @@ def test_eager_entry_points_refuse_unbuilt_options():
         cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, rounding="feedback",
                         more=lambda a, b: torch.zeros(b - a, 16))  # fmt: skip
     with pytest.raises(ValueError, match="GPU"):
-        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit")  # built
+        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit", seed=1)  # built
     with pytest.raises(NotImplementedError):
         cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="regrid")
     with pytest.raises(NotImplementedError):
-        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit", gain=torch.ones(4))
+        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit", gain=torch.ones(4), seed=1)
     with pytest.raises(ValueError, match="GPU"):
         cb.bake_plain(torch, t, down, up, 1.0, stats=cb.Stats())  # Stats: built
     with pytest.raises(ValueError):
         cb.bake_int8_convrot(torch, t, t, down, up, 1.0, rounding="up")
+
+
+def test_eager_noise_needs_a_seed_or_a_generator():
+    """A stochastic eager bake takes `seed`, or draws a fresh 31-bit one from `generator` on
+    each call; with neither it refuses instead of reusing one stream. Nearest needs none."""
+    from cozyq import bake as cb
+
+    t = torch.zeros(4, 16)
+    down, up = torch.zeros(1, 16), torch.zeros(4, 1)
+    with pytest.raises(ValueError, match="seed"):
+        cb.bake_int8_convrot(torch, t, t, down, up, 1.0, rounding="stochastic")
+    with pytest.raises(ValueError, match="seed"):
+        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0)
+    gen = torch.Generator().manual_seed(5)
+    drawn = [cb._noise_seed(torch, None, gen, True) for _ in range(4)]
+    assert len(set(drawn)) == 4 and all(0 <= d <= cb.SEED_MASK for d in drawn)
+    assert cb._noise_seed(torch, (1 << 40) + 7, None, True) == 7
+    assert cb._noise_seed(torch, None, None, False) == 0
+
+
+def test_kron_rows_against_torch_kron():
+    """`Kron` rows against `torch.kron` (the library routine), whole and sliced, with an index
+    that reorders and skips rows; `dense` sums terms and is None for none."""
+    from cozyq import bake as cb
+
+    gen = torch.Generator().manual_seed(9)
+    w1, w2 = torch.randn(3, 4, generator=gen), torch.randn(5, 2, generator=gen)
+    index = torch.tensor([14, 0, 7, 3, 9, 12])
+    term = cb.Kron(w1, w2, 0.25, index)
+    full = torch.kron(w1, w2) * 0.25
+    assert torch.equal(term(0, 6), full[index])
+    assert torch.equal(term(2, 5), full[index[2:5]])
+    other = cb.Kron(w1 * 2, w2, 1.0, index)
+    assert torch.allclose(cb.dense([term, other])(0, 6), full[index] + torch.kron(w1 * 2, w2)[index])
+    assert cb.dense([]) is None
 
 
 @pytest.mark.gpu
@@ -995,16 +1031,19 @@ def test_stats_properties():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("rank", [5, 200])
 @pytest.mark.parametrize("form", [ob.BF16, ob.F16, ob.F32, ob.ROWWISE, ob.INT8, ob.NVFP4])
-def test_gpu_bake_stats_against_the_oracle(form):
+def test_gpu_bake_stats_against_the_oracle(form, rank):
     """`bake(..., stats=Stats())`: the accounting kernel's sums against the oracle's `account`
     over the same weight before and after (float64 sums: to 1e-9; the rank-space energies, whose
-    projections the kernel sums in float32, to 1e-4; the saturated count exactly)."""
+    projections the kernel sums in float32, to 1e-4; the saturated count exactly). Rank 200
+    takes the projections in two 128-rank slices."""
     from cozyq import bake as cb
 
-    rng = np.random.default_rng(700 + form)
-    rows, cols, rank, seed = 70, 256, 5, 41
-    up = (rng.standard_normal((rows, rank)) * (0.5 if form in (ob.ROWWISE, ob.INT8, ob.NVFP4) else 0.02)).astype(np.float32)
+    rng = np.random.default_rng(700 + form + rank)
+    rows, cols, seed = 70, 256, 41
+    big = 0.5 * math.sqrt(5 / rank)
+    up = (rng.standard_normal((rows, rank)) * (big if form in (ob.ROWWISE, ob.INT8, ob.NVFP4) else 0.02)).astype(np.float32)
     down = rng.standard_normal((rank, cols)).astype(np.float32)
     stats = cb.Stats()
     if form == ob.NVFP4:

@@ -160,7 +160,7 @@ def test_w4a8_leaf_shares_the_int8_operand(monkeypatch):
         shared = (leaf(x), int8(x))
     assert len(calls) == 1
     assert all(torch.equal(a, s) for a, s in zip(alone, shared))
-    assert isinstance(leaf.weights(), prebuilt.W4a8)
+    assert leaf.roles()["group_scale"].dtype == torch.float8_e4m3fn and leaf.codebook is not None
 
 
 def test_int8_leaf_autocast_dtype():

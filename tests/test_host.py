@@ -188,7 +188,7 @@ def test_siblings_share_then_learn_their_group():
     assert first[0] is first[1] is first[2] and len(made) == 1
     x2 = torch.randn(4, 8)  # a new input retires the held operand; q learns its group of 3
     operands.shared_operand(x2, p, _op(made, x2, p), q)
-    assert q._cozy_siblings == 3 and len(made) == 2
+    assert operands.group_size(q) == 3 and len(made) == 2
     x.add_(1)  # an in-place change is never served stale
     operands.shared_operand(x, p, _op(made, x, p), q)
     assert len(made) == 3
@@ -204,3 +204,44 @@ def test_int8_rows_declines_foreign_consumers():
     assert operands.int8_rows(x, (leaf,)) is None  # a CPU tensor: the caller runs its own ops
     with pytest.raises(ValueError, match="gate"):
         operands.int8_rows(x, (leaf,), activation="situ", norm="rms")
+
+
+def test_sharing_groups_grow_exhaust_and_hold_nothing_alone():
+    """Rules S2–S5 in sequence: a learned group of 3 holds its operand for exactly two more
+    reads; one more reader of the same unchanged input grows the maker's group to 4; a maker
+    learned to read alone holds nothing; a freed input drops its operand and its maker learns;
+    inference tensors and consumer-less asks share nothing."""
+    import gc
+
+    class Leaf:
+        pass
+
+    p = operands.INT8_CONVROT
+    q, k, v, w = Leaf(), Leaf(), Leaf(), Leaf()
+    made: list[int] = []
+    x = torch.randn(4, 8)
+    for leaf in (q, k, v):
+        operands.shared_operand(x, p, _op(made, x, p), leaf)
+    x2 = torch.randn(4, 8)
+    operands.shared_operand(x2, p, _op(made, x2, p), w)  # drops q's operand: q's group is 3
+    assert operands.group_size(q) == 3 and len(made) == 2
+    x3 = torch.randn(4, 8)
+    got = [operands.shared_operand(x3, p, _op(made, x3, p), leaf) for leaf in (q, k, v)]
+    assert got[0] is got[1] is got[2] and len(made) == 3  # w's operand dropped: w read alone
+    assert operands.group_size(w) == 1
+    again = operands.shared_operand(x3, p, _op(made, x3, p), w)  # a fourth reader after the group
+    assert again is not got[0] and len(made) == 4 and operands.group_size(q) == 4
+    x4 = torch.randn(4, 8)
+    operands.shared_operand(x4, p, _op(made, x4, p), w)  # w reads alone: nothing held
+    assert operands.shared_operand(x4, p, _op(made, x4, p), k) is not None and len(made) == 6
+    x5 = torch.randn(4, 8)
+    payload = torch.zeros(4, 8)  # an operand that does not keep x5 alive
+    operands.shared_operand(x5, p, _op(made, payload, p), v)  # v's group unknown: held
+    del x5
+    gc.collect()
+    assert operands.group_size(v) == 1  # dropped with its input; v learned it read alone
+    with torch.inference_mode():
+        xi = torch.randn(4, 8)
+    assert operands.shared_operand(xi, p, _op(made, xi, p), q) is None
+    assert operands.shared_operand(x4, p, _op(made, x4, p), None) is None
+    assert len(made) == 7
