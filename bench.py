@@ -145,7 +145,7 @@ def _check(code: int) -> None:
         raise RuntimeError(f"kernel launch failed: {_lib.error_name(code)}")
 
 
-def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
+def bench_c2(torch, ops, lib, stream, steps: int, warmup: int, preroll_for: float = PREROLL_MS) -> dict:
     m, k, n = 4096, 3072, 12288
     x = _activations(torch, m, k, 20261202)
     data, scale = ops.int8_quantize_rot(_weights(torch, n, k, 20261203), 128)
@@ -161,12 +161,21 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
     def gemm():
         _check(lib.cozyq_gemm_ex(0, 0, qp, sp, dp, wp, bp, op, n, 0, m, n, k, 1, stream))
 
+    work = torch.zeros(int(lib.cozyq_linear_workspace_bytes(m)) // 4, dtype=torch.int32, device="cuda")
+
+    def fused():
+        # Rotation, quantization and the GEMM in one persistent launch (`cozyq_linear`).
+        _check(lib.cozyq_linear(0, xp, 0, 128, qp, sp, dp, wp, bp, op, n, 0, m, n, k, 1,
+                                work.data_ptr(), stream))  # fmt: skip
+
     def step():
+        # The product path (`Prebuilt.int8_linear`): quantize, then the GEMM; faster than the
+        # fused launch on MI355X.
         quantize()
         gemm()
 
     timer = Timer(torch)
-    preroll_ms = preroll(torch, step)
+    preroll_ms = preroll(torch, step, preroll_for)
     # The driver's contract: W untimed steps, then exactly K steps between two synchronizations.
     ms_step = timer.run(step, steps, warmup)
 
@@ -179,7 +188,8 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
         _check(lib.cozyq_quantize_rot(0, xp, 0, qp, sp, m, k, 256, stream))
         _check(lib.cozyq_gemm_ex(0, 0, qp, sp, dp256, wp256, bp, op, n, 0, m, n, k, 1, stream))
 
-    med = timer.interleaved({"step": step, "gemm": gemm, "quantize": quantize, "step256": step256})
+    med = timer.interleaved({"step": step, "gemm": gemm, "quantize": quantize, "fused": fused,
+                             "step256": step256})
     ms_gemm, ms_quant, ms_step256 = med["gemm"]["ms"], med["quantize"]["ms"], med["step256"]["ms"]
     ops_count = 2.0 * m * n * k
     gemm_tops = ops_count / (ms_gemm * 1e-3) / 1e12
@@ -190,6 +200,7 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int) -> dict:
         "tops": ops_count / (ms_step * 1e-3) / 1e12,
         "preroll_ms": preroll_ms,
         "step_median_ms": med["step"]["ms"],
+        "fused_one_launch_ms": med["fused"]["ms"],
         "samples": med,
         "gemm_ms": ms_gemm,
         "quantize_ms": ms_quant,
@@ -784,7 +795,7 @@ def only(torch, ops, lib, stream, args) -> int:
         ms = Timer(torch).run(lambda: dst.copy_(src), args.steps, args.warmup)
         figures = {"copy_bytes": nbytes, "us": ms * 1e3, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
     elif args.only == "c2":
-        figures = bench_c2(torch, ops, lib, stream, args.steps, args.warmup)
+        figures = bench_c2(torch, ops, lib, stream, args.steps, args.warmup, args.preroll_ms)
     elif args.only == "c1":
         figures = bench_c1(torch, ops, lib, stream)
     elif args.only == "decode":
@@ -818,6 +829,8 @@ def main() -> int:
     # 20-launch round of the C2 GEMM runs ~12% slower than later ones), so the default warmup
     # covers that.
     parser.add_argument("--warmup", type=int, default=100)
+    parser.add_argument("--preroll-ms", type=float, default=PREROLL_MS,
+                        help="clock pre-roll before timing (profiling runs may shorten it)")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
     parser.add_argument("--only", choices=("c1", "c2", "decode", "int8_decode", "w4a8", "fp8", "svdq", "mx", "weights",
@@ -840,7 +853,7 @@ def main() -> int:
 
     if args.only:
         return only(torch, ops, lib, stream, args)
-    c2 = bench_c2(torch, ops, lib, stream, args.steps, args.warmup)
+    c2 = bench_c2(torch, ops, lib, stream, args.steps, args.warmup, args.preroll_ms)
     print(f"[bench] c2 {c2['ms_per_step']:.4f} ms/step, gemm {c2['gemm_ms']:.4f} ms", file=sys.stderr, flush=True)
     decode = bench_decode(torch, ops, lib, stream, args.steps, args.warmup)
     print(f"[bench] decode M=1 {decode['us']:.2f} us {decode['gbs']:.0f} GB/s", file=sys.stderr, flush=True)

@@ -42,6 +42,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_int, c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, c_int, c_int,
          _P, _P, _P],
     ),
+    "cozyq_linear_workspace_bytes": (c_int64, [c_int64]),
+    "cozyq_linear": (
+        c_int,
+        [c_int, _P, c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, c_int, c_int, _P, _P],
+    ),
     "cozyq_gemm_ex": (
         c_int,
         [c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, c_int, c_int, _P],

@@ -100,6 +100,9 @@ class Prebuilt:
     family: str = FAMILIES[0]
     _lib: Any = field(init=False)
     _checked: set[tuple[object, ...]] = field(init=False, default_factory=set)
+    #: The fused linear's counters, one zeroed int32 buffer per stream (each call leaves its
+    #: buffer zero; calls on one stream run in order, so they share it).
+    _workspaces: dict[int, Tensor] = field(init=False, default_factory=dict)
 
     def __post_init__(self) -> None:
         self._lib = _lib.load()
@@ -126,8 +129,50 @@ class Prebuilt:
             if code != self._lib.cozyq_not_supported():
                 self._check(code, "the GEMV")
                 return out
+        # Quantize, then GEMM: on MI355X two launches beat the fused one (`int8_linear_rot`),
+        # whose quantize jobs run at one wave a SIMD beside the GEMM's full register file.
         q, scales = self.int8_quantize(flat)
         return self.int8_gemm(q, scales, data, scale, bias, out_dtype).view(shape)
+
+    def _linear_fused(
+        self, flat: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None, out_dtype: Dtype,
+        rotation: int, epilogue: int,
+    ) -> tuple[Tensor, Tensor, Tensor] | None:
+        """`cozyq_linear` on checked rows: (out, q, scales), or None where it declines (rows
+        longer than 4096, or an output dtype other than x's) and quantize + GEMM serve."""
+        torch = self.torch
+        rows, width = flat.shape
+        n = int(data.shape[0])
+        out = torch.empty(rows, n, dtype=out_dtype, device=flat.device)
+        q = torch.empty(rows, width, dtype=torch.int8, device=flat.device)
+        scales = torch.empty(rows, dtype=torch.float32, device=flat.device)
+        stream = self._stream()
+        need = int(self._lib.cozyq_linear_workspace_bytes(rows)) // 4
+        work = self._workspaces.get(stream)
+        if work is None or work.numel() < need:
+            work = self._workspaces[stream] = torch.zeros(max(need, 1024), dtype=torch.int32,
+                                                          device=flat.device)  # fmt: skip
+        code = self._lib.cozyq_linear(
+            self.index, flat.data_ptr(), self._half(flat.dtype), rotation, q.data_ptr(),
+            scales.data_ptr(), data.data_ptr(), scale.data_ptr(), _ptr(bias), out.data_ptr(), n,
+            self._half(out_dtype), rows, n, width, epilogue, work.data_ptr(), stream,
+        )  # fmt: skip
+        if code == self._lib.cozyq_not_supported():
+            return None
+        self._check(code, "the fused linear")
+        return out, q, scales
+
+    def int8_linear_rot(
+        self, x: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None, out_dtype: Dtype,
+        rotation: int, epilogue: int = 0,
+    ) -> tuple[Tensor, Tensor, Tensor] | None:
+        """The fused linear (`cozyq_linear`) for any rotation lane (256, 128, 0) and epilogue
+        (0 none, 1 tanh-GELU): (out, q, scales) with q / scales the operand it quantized, or None
+        where it declines."""
+        multiple = 16 if rotation == 0 else rotation
+        flat = self._rows(_Format("int8", False, multiple), x)
+        bias = self._weight(_Format("int8", False, multiple), data, scale, bias, flat.shape[1], out_dtype)
+        return self._linear_fused(flat, data, _aligned(scale), bias, out_dtype, rotation, epilogue)
 
     def fp8_linear(
         self, x: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None, out_dtype: Dtype

@@ -30,6 +30,15 @@ hipError_t fp8_quantize(const void* x, bool x_half, uint8_t* q, float* scales, i
 hipError_t mx_quantize(const void* x, bool x_half, uint8_t* q, uint8_t* scales, int M, int K,
                        hipStream_t s);
 
+// The fused int8 linear (linear.hip): x's rows rotated (256, 128 or 0) and quantized per token
+// into q / qs, then the 256x256-tile int8 GEMM with its epilogue, in one persistent launch; out
+// in x's dtype. K <= 4096. `work` holds linear_workspace_ints(M) int32 counters, zero before the
+// first launch and zero again after each.
+int linear_workspace_ints(int M);
+hipError_t linear_int8(const void* x, bool half, int rotation, int8_t* q, float* qs, const int8_t* w,
+                       const float* ws, const void* bias, void* out, int64_t ldo, int M, int N, int K,
+                       int epilogue, int* work, int device, hipStream_t s);
+
 hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                      const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
                      int epilogue, hipStream_t s);

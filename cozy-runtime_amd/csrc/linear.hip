@@ -1,0 +1,212 @@
+// The fused int8 linear: block-Hadamard rotation, per-token int8 quantization and the W8A8 GEMM
+// with its dequantizing epilogue, in one persistent launch.
+//
+// The reference runs the producer and the GEMM as two launches chained by programmatic
+// dependent launch (kernels/csrc/gemm/rotate.cu:284-295, gemm_tma.cuh:166-173). Here both are
+// jobs of one kernel. Per-token scaling needs a whole row's maximum before any of the row's
+// codes exist, so the rows are quantized once into `q` / `qs` (which the caller may keep as the
+// shared operand) and every output tile of an M-tile waits for that M-tile's rows. The wait is on
+// a counter the quantize jobs raise.
+//
+// Work is split into `queues` job queues (one per XCD when workgroup b runs on XCD b mod 8, the
+// dispatch order on MI355X). Queue x owns M-tiles m with m mod queues == x:
+// - first the quantize jobs of all of them: 16 rows each, a wave per row, rows.h;
+// - then their output tiles, pair of M-tiles by pair, N fastest with the two M-tiles
+//   alternating, so an XCD's concurrent tiles share two X panels and their W panels in its L2.
+// A workgroup claims the next job of its queue with an atomic counter. Before its first tile it
+// waits for its queue's quantize jobs, all claimed before any tile by running workgroups that
+// never wait themselves, so every wait ends. A spin limit guards the wait anyway: past it the
+// workgroup records the fault in the workspace and goes on.
+//
+// The workspace (kernels.h `linear_workspace_ints`) holds the queue heads, an exit count, the
+// fault flag and one done-counter per M-tile. It must be zero before the first launch. The last
+// workgroup to leave sets every counter back to zero, so the next launch on the stream starts
+// clean; launches that overlap on one workspace race.
+#include "gemm_tile.h"
+#include "rows.h"
+
+namespace cozyq {
+namespace {
+
+constexpr int kQRows = 16;          // rows a quantize job takes: 4 a wave
+constexpr int kMaxQueues = 8;       // XCDs on MI355X
+constexpr int kSpinLimit = 1 << 24;  // s_sleep(2) rounds a tile waits at most (~1 s)
+constexpr int kJobSlot = kLdsBytes;  // LDS word that broadcasts a claimed job
+constexpr int kFusedLds = kLdsBytes + 16;
+
+// Workspace layout (int32): [0, 8) queue heads, [8] exit count, [9] fault flag, [16, 16 +
+// tiles_m) quantize jobs finished per M-tile.
+constexpr int kExit = 8, kFault = 9, kDone = 16;
+
+__device__ __forceinline__ int qjobs(int m, int M) {
+    const int rows = min(kTile, M - m * kTile);
+    return (rows + kQRows - 1) / kQRows;
+}
+
+// Job `j` of queue `x`: kind (0 quantize, 1 tile), M-tile and the index within the kind.
+struct Job {
+    int kind, m, index, n;
+};
+
+__device__ __forceinline__ int queue_jobs(int x, int queues, int tiles_m, int tiles_n, int M) {
+    int total = 0;
+    for (int m = x; m < tiles_m; m += queues) total += qjobs(m, M) + tiles_n;
+    return total;
+}
+
+__device__ __forceinline__ Job decode(int j, int x, int queues, int tiles_m, int tiles_n, int M) {
+    // The queue's quantize jobs first, M-tile by M-tile; then its tiles, pair of M-tiles by pair,
+    // N fastest with the two M-tiles alternating.
+    for (int m = x; m < tiles_m; m += queues) {
+        const int n = qjobs(m, M);
+        if (j < n) return {0, m, j, 0};
+        j -= n;
+    }
+    for (int m = x; m < tiles_m; m += 2 * queues) {
+        const int m2 = m + queues;
+        const bool pair = m2 < tiles_m;
+        const int tiles = (pair ? 2 : 1) * tiles_n;
+        if (j < tiles) return {1, pair && (j & 1) ? m2 : m, 0, pair ? j >> 1 : j};
+        j -= tiles;
+    }
+    return {-1, 0, 0, 0};
+}
+
+// A wave's four rows r0 .. r0 + 3 of a quantize job (rows past M skipped), all four rows'
+// loads issued up front: at one wave a SIMD, one load latency for the job instead of one a row.
+template <bool kHalf, int kRot>
+__device__ __forceinline__ void quantize_job(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
+                                                       float* __restrict__ qs, int M, int K, int r0, int lane,
+                                                       float* slice) {
+    constexpr int kWaveRows = kQRows / 4;
+    const int rows = min(kWaveRows, M - r0);
+    uint4 raw[kWaveRows][kRowLoads];
+#pragma unroll
+    for (int i = 0; i < kWaveRows; ++i)
+        row_loads(row_view(x + static_cast<int64_t>(min(r0 + i, M - 1)) * K, K), lane, raw[i]);
+#pragma unroll
+    for (int i = 0; i < kWaveRows; ++i)
+        if (i < rows)
+            quantize_row_wave<kHalf, kRot>(raw[i], K, lane, slice, q + static_cast<int64_t>(r0 + i) * K, qs + r0 + i);
+}
+
+template <bool kHalf, int kRot, bool kOutHalf, bool kBias, int kEpi>
+__global__ __launch_bounds__(kThreads, 1) void linear_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ qs,
+    const int8_t* __restrict__ W, const float* __restrict__ ws, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ out, int64_t ldo, int M, int N, int K, int tiles_m, int tiles_n,
+    int queues, int* __restrict__ work) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kFusedLds];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int qx = blockIdx.x % queues;
+    const int total = queue_jobs(qx, queues, tiles_m, tiles_n, M);
+    int* done = work + kDone;
+    bool acquired = false;  // the queue's rows, once all are quantized
+    for (;;) {
+        if (tid == 0)
+            *reinterpret_cast<int*>(lds + kJobSlot) =
+                __hip_atomic_fetch_add(work + qx, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();  // also: every wave is done with the LDS of the job before
+        const int j = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int*>(lds + kJobSlot));
+        if (j >= total) break;
+        const Job job = decode(j, qx, queues, tiles_m, tiles_n, M);
+        if (job.kind == 0) {
+            quantize_job<kHalf, kRot>(x, q, qs, M, K, job.m * kTile + job.index * kQRows + wave * (kQRows / 4),
+                                      lane, reinterpret_cast<float*>(lds) + wave * kRowLdsFloats<kRot>);
+            // Every wave's codes and scales have reached L2 before the barrier; then one
+            // agent-scope release (a write-back of the XCD's L2) publishes the job.
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+            __syncthreads();
+            if (tid == 0) __hip_atomic_fetch_add(done + job.m, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            continue;
+        }
+        // Before its first tile a workgroup waits for every quantize job of its queue (all
+        // claimed before any tile, by running workgroups that never wait) and acquires their
+        // rows once: an agent-scope acquire invalidates the XCD's L2, so it is taken before the
+        // tiles start filling it, not per tile.
+        if (!acquired) {
+            if (tid == 0) {
+                int spins = 0;
+                for (int m = qx; m < tiles_m; m += queues) {
+                    const int need = qjobs(m, M);
+                    while (__hip_atomic_load(done + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+                        __builtin_amdgcn_s_sleep(2);
+                        if (++spins >= kSpinLimit) {
+                            __hip_atomic_store(work + kFault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            break;
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            acquired = true;
+        }
+        gemm_tile<kInt8, kOutHalf, kBias, kEpi>(
+            lds, reinterpret_cast<const uint8_t*>(q), reinterpret_cast<const uint8_t*>(W), qs, ws,
+            nullptr, nullptr, bias, out, nullptr, ldo, M, N, K, job.m, job.n);
+    }
+    // The last workgroup out resets the counters for the next launch.
+    if (tid == 0) {
+        const int before = __hip_atomic_fetch_add(work + kExit, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (before == static_cast<int>(gridDim.x) - 1) {
+            for (int i = 0; i < kMaxQueues; ++i) __hip_atomic_store(work + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int m = 0; m < tiles_m; ++m) __hip_atomic_store(done + m, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(work + kExit, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+int cu_count(int device) {
+    static int counts[64] = {0};
+    if (device < 0 || device >= 64) return 256;
+    if (counts[device] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0) n = 256;
+        counts[device] = n;
+    }
+    return counts[device];
+}
+
+template <bool kHalf, int kRot, bool kOutHalf, bool kBias, int kEpi>
+hipError_t launch_linear(const void* x, int8_t* q, float* qs, const int8_t* w, const float* ws,
+                         const void* bias, void* out, int64_t ldo, int M, int N, int K, int* work,
+                         int device, hipStream_t s) {
+    const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTile - 1) / kTile;
+    const int queues = min(kMaxQueues, tiles_m);
+    int jobs = 0;
+    for (int m = 0; m < tiles_m; ++m) jobs += (min(kTile, M - m * kTile) + kQRows - 1) / kQRows + tiles_n;
+    const int grid = max(queues, min(cu_count(device), jobs));
+    linear_kernel<kHalf, kRot, kOutHalf, kBias, kEpi><<<grid, kThreads, 0, s>>>(
+        static_cast<const uint16_t*>(x), q, qs, w, ws, static_cast<const uint16_t*>(bias),
+        static_cast<uint16_t*>(out), ldo, M, N, K, tiles_m, tiles_n, queues, work);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int linear_workspace_ints(int M) { return kDone + (M + kTile - 1) / kTile; }
+
+hipError_t linear_int8(const void* x, bool half, int rotation, int8_t* q, float* qs, const int8_t* w,
+                       const float* ws, const void* bias, void* out, int64_t ldo, int M, int N, int K,
+                       int epilogue, int* work, int device, hipStream_t s) {
+    if (M == 0 || N == 0) return hipSuccess;
+    const bool b = bias != nullptr;
+#define COZYQ_LIN(H, R, B, E)                                                                     \
+    if (half == H && rotation == R && b == B && epilogue == E)                                     \
+        return launch_linear<H, R, H, B, E>(x, q, qs, w, ws, bias, out, ldo, M, N, K, work, device, s);
+#define COZYQ_LIN_R(H, B, E) COZYQ_LIN(H, 256, B, E) COZYQ_LIN(H, 128, B, E) COZYQ_LIN(H, 0, B, E)
+    COZYQ_LIN_R(false, false, 0)
+    COZYQ_LIN_R(false, true, 0)
+    COZYQ_LIN_R(false, false, 1)
+    COZYQ_LIN_R(false, true, 1)
+    COZYQ_LIN_R(true, false, 0)
+    COZYQ_LIN_R(true, true, 0)
+    COZYQ_LIN_R(true, false, 1)
+    COZYQ_LIN_R(true, true, 1)
+#undef COZYQ_LIN_R
+#undef COZYQ_LIN
+    return hipErrorInvalidValue;
+}
+
+}  // namespace cozyq

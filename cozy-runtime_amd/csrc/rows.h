@@ -141,8 +141,13 @@ __device__ __forceinline__ void quantize_row_wave(const uint4 (&raw)[kRowLoads],
                 }
             }
             wave_lds_sync();
-            // Phase 2: the outer stages, a lane holding column t of a group's runs.
-            for (int task = lane; task < groups * 16; task += 64) {
+            // Phase 2: the outer stages, a lane holding column t of a group's runs; the lane's
+            // tasks unrolled so their LDS reads are in flight together.
+            constexpr int kTasks = kRowPass / kRot * 16 / 64;
+#pragma unroll
+            for (int u = 0; u < kTasks; ++u) {
+                const int task = lane + 64 * u;
+                if (task >= groups * 16) break;
                 const int g = task / 16, t = task % 16;
                 float v[L::kRuns];
 #pragma unroll

@@ -97,6 +97,22 @@ int cozyq_gemm_ex(int device, int fp8, const void* q, const float* scales, const
                   const float* w_scale, const void* bias, void* out, int64_t ldo, int out_half,
                   int M, int N, int K, int epilogue, void* stream);
 
+/* The whole int8 linear in one launch: the reference's `quantize` then `gemm` (kernels/csrc/
+ * gemm.cpp:83-117 and 119-168, chained by programmatic dependent launch, rotate.cu:284-295 and
+ * gemm_tma.cuh:166-173) fused into one persistent kernel whose quantize jobs feed its GEMM tiles.
+ * x [M, K] 16-bit (x_half: fp16, else bf16) is rotated (`rotation` 256: the reference's H256/16;
+ * 128 and 0: the build's lanes of cozyq_quantize_rot) and quantized per row into q [M, K] int8 and
+ * qs [M] f32 (the operand, which the caller may keep), then out = the int8 law of cozyq_gemm_ex
+ * (epilogue 0 or 1) in x's dtype. K % max(rotation, 16) == 0, K <= 4096 (longer rows, or
+ * out_half != x_half, return hipErrorNotSupported: run cozyq_quantize_rot + cozyq_gemm_ex).
+ * N % 8 == 0, ldo >= N, ldo % 8 == 0; x, q, w and out 16-byte aligned. `workspace` holds
+ * cozyq_linear_workspace_bytes(M) bytes, zero before the first call; each call leaves it zero, so
+ * one workspace serves calls in stream order (calls that overlap on one workspace race). */
+int64_t cozyq_linear_workspace_bytes(int64_t M);
+int cozyq_linear(int device, const void* x, int x_half, int rotation, int8_t* q, float* qs,
+                 const int8_t* w, const float* w_scale, const void* bias, void* out, int64_t ldo,
+                 int out_half, int M, int N, int K, int epilogue, int* workspace, void* stream);
+
 /* Test entry (no reference counterpart): the raw int32 accumulators acc = q·wᵀ of the int8
  * GEMM, [M, N] row-major, for bit-exact checks of the MFMA mainloop. */
 int cozyq_gemm_i32(int device, const int8_t* q, const int8_t* w, int32_t* acc, int M, int N,
