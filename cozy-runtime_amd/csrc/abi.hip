@@ -118,18 +118,22 @@ static int gemm_checked(int device, int fp8, const void* q, const float* scales,
 static int linear_checked(int device, const void* x, int x_half, int rotation, int8_t* q,
                           float* qs, const int8_t* w, const float* w_scale, const void* bias,
                           void* out, int64_t ldo, int out_half, int M, int N, int K, int epilogue,
-                          int* workspace, void* stream) {
+                          int* workspace, bool own_scratch, void* stream) {
     if (M < 0 || N < 1 || N % 8 || epilogue < 0 || epilogue > 1) return hipErrorInvalidValue;
     if (rotation != 0 && rotation != 128 && rotation != 256) return hipErrorInvalidValue;
     if (!fits(K, rotation == 0 ? 16 : rotation)) return hipErrorInvalidValue;
     if (ldo < N || ldo % 8 || !aligned16(out) || !aligned16(x) || !aligned16(q) || !aligned16(w))
         return hipErrorInvalidValue;
-    if (M > 0 && (!qs || !w_scale || !workspace)) return hipErrorInvalidValue;
+    if (M > 0 && (!qs || !w_scale || (!own_scratch && !workspace))) return hipErrorInvalidValue;
+    if (own_scratch && M > cozyq::linear_noalloc_max_rows()) return hipErrorInvalidValue;
     // One wave quantizes a row, so rows longer than 4096 take the two-launch path; the output
     // is in x's dtype.
     if (K > 4096 || out_half != x_half) return hipErrorNotSupported;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
+    if (own_scratch)
+        return cozyq::linear_int8_noalloc(x, x_half != 0, rotation, q, qs, w, w_scale, bias, out, ldo,
+                                          M, N, K, epilogue, device, on(stream));
     return cozyq::linear_int8(x, x_half != 0, rotation, q, qs, w, w_scale, bias, out, ldo, M, N, K,
                               epilogue, workspace, device, on(stream));
 }
@@ -143,7 +147,16 @@ int cozyq_linear(int device, const void* x, int x_half, int rotation, int8_t* q,
                  const int8_t* w, const float* w_scale, const void* bias, void* out, int64_t ldo,
                  int out_half, int M, int N, int K, int epilogue, int* workspace, void* stream) {
     return linear_checked(device, x, x_half, rotation, q, qs, w, w_scale, bias, out, ldo, out_half,
-                          M, N, K, epilogue, workspace, stream);
+                          M, N, K, epilogue, workspace, false, stream);
+}
+
+int cozyq_linear_noalloc_max_rows(void) { return cozyq::linear_noalloc_max_rows(); }
+
+int cozyq_linear_noalloc(int device, const void* x, int x_half, int rotation, int8_t* q, float* qs,
+                         const int8_t* w, const float* w_scale, const void* bias, void* out,
+                         int64_t ldo, int out_half, int M, int N, int K, int epilogue, void* stream) {
+    return linear_checked(device, x, x_half, rotation, q, qs, w, w_scale, bias, out, ldo, out_half,
+                          M, N, K, epilogue, nullptr, true, stream);
 }
 
 int cozyq_gemm(int device, int family, int fp8, const void* q, const float* scales,

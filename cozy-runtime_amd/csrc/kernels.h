@@ -38,6 +38,14 @@ int linear_workspace_ints(int M);
 hipError_t linear_int8(const void* x, bool half, int rotation, int8_t* q, float* qs, const int8_t* w,
                        const float* ws, const void* bias, void* out, int64_t ldo, int M, int N, int K,
                        int epilogue, int* work, int device, hipStream_t s);
+// linear_int8 with its counters in the library's own device array (no workspace, no
+// allocation): M <= linear_noalloc_max_rows(), else hipErrorInvalidValue. Calls that overlap on
+// one GPU race on the array.
+int linear_noalloc_max_rows();
+hipError_t linear_int8_noalloc(const void* x, bool half, int rotation, int8_t* q, float* qs,
+                               const int8_t* w, const float* ws, const void* bias, void* out,
+                               int64_t ldo, int M, int N, int K, int epilogue, int device,
+                               hipStream_t s);
 
 hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                      const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,

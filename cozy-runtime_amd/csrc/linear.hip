@@ -183,6 +183,33 @@ hipError_t launch_linear(const void* x, int8_t* q, float* qs, const int8_t* w, c
     return hipGetLastError();
 }
 
+// The allocation-free variant's counters: a file-scope device array, one per GPU the library
+// runs on, held until the process ends. Host code never passes the array's name to a kernel (it
+// is a host-side stand-in there); it passes the device address hipGetSymbolAddress gives, taken
+// once per device with that device current.
+constexpr int kScratchInts = kDone + 1024;  // up to 1024 M-tiles: M <= 262144
+__device__ __align__(256) int scratch[kScratchInts];
+
+int* scratch_address[64] = {nullptr};
+
+hipError_t scratch_of(int device, int** out) {
+    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+    if (scratch_address[device] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        scratch_address[device] = static_cast<int*>(p);
+    }
+    *out = scratch_address[device];
+    return hipSuccess;
+}
+
+// The counters a launch uses, set to zero on the launch's stream ahead of it (a kernel, not a
+// memset node, so a captured graph replays it correctly).
+__global__ __launch_bounds__(256) void clear_ints(int* __restrict__ p, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+}
+
 }  // namespace
 
 int linear_workspace_ints(int M) { return kDone + (M + kTile - 1) / kTile; }
@@ -207,6 +234,23 @@ hipError_t linear_int8(const void* x, bool half, int rotation, int8_t* q, float*
 #undef COZYQ_LIN_R
 #undef COZYQ_LIN
     return hipErrorInvalidValue;
+}
+
+int linear_noalloc_max_rows() { return (kScratchInts - kDone) * kTile; }
+
+hipError_t linear_int8_noalloc(const void* x, bool half, int rotation, int8_t* q, float* qs,
+                               const int8_t* w, const float* ws, const void* bias, void* out,
+                               int64_t ldo, int M, int N, int K, int epilogue, int device,
+                               hipStream_t s) {
+    if (M > linear_noalloc_max_rows()) return hipErrorInvalidValue;
+    if (M == 0 || N == 0) return hipSuccess;
+    int* counters = nullptr;
+    const hipError_t e = scratch_of(device, &counters);
+    if (e != hipSuccess) return e;
+    clear_ints<<<1, 256, 0, s>>>(counters, linear_workspace_ints(M));
+    const hipError_t launched = hipGetLastError();
+    if (launched != hipSuccess) return launched;
+    return linear_int8(x, half, rotation, q, qs, w, ws, bias, out, ldo, M, N, K, epilogue, counters, device, s);
 }
 
 }  // namespace cozyq

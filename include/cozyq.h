@@ -113,6 +113,17 @@ int cozyq_linear(int device, const void* x, int x_half, int rotation, int8_t* q,
                  const int8_t* w, const float* w_scale, const void* bias, void* out, int64_t ldo,
                  int out_half, int M, int N, int K, int epilogue, int* workspace, void* stream);
 
+/* cozyq_linear that allocates nothing (no reference counterpart; for callers that cannot
+ * allocate: code under graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments without `workspace`: the counters live in the library's own 4 KiB device array
+ * (one per GPU, held until the process ends), cleared by a small kernel on `stream` ahead of each
+ * launch. M <= cozyq_linear_noalloc_max_rows() (262144), else hipErrorInvalidValue before
+ * anything runs. Every call on one GPU shares the array: calls that overlap on a GPU race. */
+int cozyq_linear_noalloc_max_rows(void);
+int cozyq_linear_noalloc(int device, const void* x, int x_half, int rotation, int8_t* q, float* qs,
+                         const int8_t* w, const float* w_scale, const void* bias, void* out,
+                         int64_t ldo, int out_half, int M, int N, int K, int epilogue, void* stream);
+
 /* Test entry (no reference counterpart): the raw int32 accumulators acc = q·wᵀ of the int8
  * GEMM, [M, N] row-major, for bit-exact checks of the MFMA mainloop. */
 int cozyq_gemm_i32(int device, const int8_t* q, const int8_t* w, int32_t* acc, int M, int N,
