@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_int, c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, c_int, c_int,
          _P, _P, _P],
     ),
+    "cozyq_gemm_config": (c_int, [c_int, c_int, c_int, c_int]),
     "cozyq_linear_workspace_bytes": (c_int64, [c_int64]),
     "cozyq_linear_noalloc_max_rows": (c_int, []),
     "cozyq_linear_noalloc": (

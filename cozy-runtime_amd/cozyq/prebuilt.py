@@ -49,9 +49,13 @@ SITU, SWIGLU = 3, 4
 
 #: `w4a8_gemm`'s config that unpacks the codes once and multiplies on the int8 GEMM, and the
 #: rows from which it is chosen (`internal/prebuilt.py:48-49`): past 256 rows the 256x256 int8
-#: GEMM outruns the fused narrow-tile one, and the unpack is one pass over the weight.
-UNPACK = 3
+#: GEMM outruns the fused narrow-tile one, and the unpack is one pass over the weight. It is the
+#: number of the 256x256 tile in the int8 GEMM's table, which the fused 4-bit GEMM lacks; the
+#: fused GEMM's configs 1..4 are that table's narrow tiles.
+UNPACK = 0
 UNPACK_ROWS = 257
+#: The GEMM tile configs (`cozyq_gemm`): 0 256x256, 1 128x128, 2 128x64, 3 64x64, 4 32x64.
+GEMM_CONFIGS = 5
 
 INT8, FP8 = _Format("int8", False, 256), _Format("fp8", True, 16)
 MX = _Format("mxfp8", True, 128)
@@ -236,7 +240,7 @@ class Prebuilt:
                 levels.data_ptr(), n, width, self._stream(),
             )  # fmt: skip
             self._check(code, "the w4a8 unpack")
-            return self.int8_gemm(q, scales, levels, w.scale, bias, out_dtype)
+            return self.int8_gemm(q, scales, levels, w.scale, bias, out_dtype, config)
         out = torch.empty(rows, n, dtype=out_dtype, device=q.device)
         if rows == 0:
             return out

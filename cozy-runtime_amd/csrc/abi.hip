@@ -101,18 +101,20 @@ int cozyq_gemv(int device, const void* x, int x_half, const int8_t* w, const flo
 static int gemm_checked(int device, int fp8, const void* q, const float* scales, const void* w,
                         const float* w_scale, const void* bias, void* out, int64_t ldo,
                         int out_half, int M, int N, int K, int epilogue, int multiple,
-                        void* stream) {
+                        int config, void* stream) {
     if (M < 1 || N < 1 || N % 8 || !fits(K, multiple) || epilogue < 0 || epilogue > 1)
         return hipErrorInvalidValue;
     if (ldo < N || ldo % 8 || !aligned16(out)) return hipErrorInvalidValue;
+    if (config >= cozyq::kGemmConfigs) return hipErrorNotSupported;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
+    if (config < 0) config = -1;
     if (fp8)
         return cozyq::gemm_fp8(static_cast<const uint8_t*>(q), scales,
                                static_cast<const uint8_t*>(w), w_scale, bias, out, ldo, out_half,
-                               M, N, K, epilogue, on(stream));
+                               M, N, K, epilogue, config, on(stream));
     return cozyq::gemm_int8(static_cast<const int8_t*>(q), scales, static_cast<const int8_t*>(w),
-                            w_scale, bias, out, ldo, out_half, M, N, K, epilogue, on(stream));
+                            w_scale, bias, out, ldo, out_half, M, N, K, epilogue, config, on(stream));
 }
 
 static int linear_checked(int device, const void* x, int x_half, int rotation, int8_t* q,
@@ -165,16 +167,20 @@ int cozyq_gemm(int device, int family, int fp8, const void* q, const float* scal
                void* allocate_context, void* stream) {
     (void)allocate; (void)allocate_context;
     if (family != 0) return hipErrorInvalidValue;
-    if (config > 0) return hipErrorNotSupported;
     return gemm_checked(device, fp8, q, scales, w, w_scale, bias, out, ldo, out_half, M, N, K, 0,
-                        fp8 ? 16 : 256, stream);
+                        fp8 ? 16 : 256, config, stream);
+}
+
+int cozyq_gemm_config(int fp8, int M, int N, int K) {
+    if (M < 1 || N < 1 || K < 1) return -1;
+    return cozyq::gemm_config(fp8 != 0, M, N, K);
 }
 
 int cozyq_gemm_ex(int device, int fp8, const void* q, const float* scales, const void* w,
                   const float* w_scale, const void* bias, void* out, int64_t ldo, int out_half,
                   int M, int N, int K, int epilogue, void* stream) {
     return gemm_checked(device, fp8, q, scales, w, w_scale, bias, out, ldo, out_half, M, N, K,
-                        epilogue, 16, stream);
+                        epilogue, 16, -1, stream);
 }
 
 int cozyq_gemm_i32(int device, const int8_t* q, const int8_t* w, int32_t* acc, int M, int N,
@@ -189,13 +195,14 @@ int cozyq_w4a8_gemm(int device, const int8_t* q, const float* scales, const uint
                     const uint8_t* s, const float* codebook, const float* w_scale, const void* bias,
                     void* out, int out_half, int M, int N, int K, int config, void* stream) {
     if (M < 1 || N < 8 || N % 8 || !fits(K, 256)) return hipErrorInvalidValue;
-    if (config > 0) return hipErrorNotSupported;  // config 0: the one (narrow-tile) GEMM
+    // Configs 1..4 are the narrow tiles; 0 (the 256x256 tile) has no fused 4-bit form.
+    if (config == 0 || config >= cozyq::kGemmConfigs) return hipErrorNotSupported;
     if (!aligned16(q) || !aligned16(w) || (reinterpret_cast<uintptr_t>(out) & 7))
         return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
     return cozyq::gemm_w4a8_narrow(q, scales, w, s, codebook, w_scale, bias, out, out_half, M, N,
-                                   K, on(stream));
+                                   K, config < 0 ? -1 : config, on(stream));
 }
 
 int cozyq_w4a8_unpack(int device, const uint8_t* w, const uint8_t* s, const float* codebook,

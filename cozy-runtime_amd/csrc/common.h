@@ -124,6 +124,14 @@ __device__ __forceinline__ float e8m0_value(uint32_t b) {
     return b == 0 ? float_of(1u << 22) : float_of(b << 23);
 }
 
+// tanh-GELU, 0.5·y·(1 + tanh(u)) with u = 0.79788456·(y + 0.044715·y³), as y / (1 + e^(-2u)):
+// e^(-2u) = 2^(y·(c1 + c2·y²)) with c1 = -2·log2(e)·0.79788456 and c2 = 0.044715·c1. Every GEMM
+// tile shares this one sequence, so their GELU outputs agree bit for bit.
+__device__ __forceinline__ float gelu_tanh(float y) {
+    const float t = __builtin_fmaf(-0.10294324f, y * y, -2.3022082f);
+    return y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y * t));
+}
+
 // ---------------------------------------------------------------------------------- MFMA
 // D(16x16) += A(16xK)·B(Kx16). Lane l supplies row l%16 of A and column l%16 of B, its K
 // slice chosen by l/16; both operands loaded with the same pattern pair every k correctly.

@@ -41,11 +41,25 @@ hipError_t dispatch(const void* q, const float* xs, const void* w, const float* 
 
 }  // namespace
 
+// The shape rule, fitted on MI355X over 19 shapes x 5 configs for each of int8 and fp8 (M 128 to
+// 16384, N 640 to 14336, K 1280 to 12288). A 256x256 tile takes ~13 ns per K byte whatever the
+// grid, so a grid of fewer tiles than CUs costs a whole tile's time (40 us at K = 3072 for 12
+// tiles or 192). From 160 tiles (5/8 of the 256 CUs) it still leads: 4096x3072x3072 at 192 tiles
+// 49.9 us against 61.3 us for 128x128, 1024x14336x4096 at 224 tiles 65.6 against 100.4. Below,
+// narrow tiles win by up to 2x (1024x3072x3072: 45.9 us against 21.3 us for 64x64).
+int gemm_config(bool fp8, int M, int N, int K) {
+    (void)fp8; (void)K;
+    const int64_t big = static_cast<int64_t>((M + 255) / 256) * ((N + 255) / 256);
+    if (big >= 160) return 0;
+    return narrow_config(M, N);
+}
+
 hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                      const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
-                     int epilogue, hipStream_t s) {
-    if (M <= 256)  // few rows: narrow tiles keep ~224 workgroups on the weight stream
-        return gemm_int8_narrow(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
+                     int epilogue, int config, hipStream_t s) {
+    if (config < 0) config = gemm_config(false, M, N, K);
+    if (config > 0)
+        return gemm_int8_narrow(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, config, s);
     return dispatch<kInt8>(q, xs, w, ws, nullptr, nullptr, bias, out, ldo, out_half, M, N, K,
                            epilogue, s);
 }
@@ -58,9 +72,10 @@ hipError_t gemm_int8_acc(const int8_t* q, const int8_t* w, int32_t* acc, int M, 
 
 hipError_t gemm_fp8(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                     const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
-                    int epilogue, hipStream_t s) {
-    if (M <= 256)  // few rows: narrow tiles keep ~224 workgroups on the weight stream
-        return gemm_fp8_narrow(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
+                    int epilogue, int config, hipStream_t s) {
+    if (config < 0) config = gemm_config(true, M, N, K);
+    if (config > 0)
+        return gemm_fp8_narrow(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, config, s);
     return dispatch<kFp8>(q, xs, w, ws, nullptr, nullptr, bias, out, ldo, out_half, M, N, K,
                           epilogue, s);
 }

@@ -1,9 +1,10 @@
-// The int8 and fp8 rowwise GEMMs for few rows (M <= 256) on gfx950, with the epilogues of the
-// big kernels: int8 on v_mfma_i32_16x16x64_i8 (exact int32; the CPU law's (acc·xs)·ws, cast,
+// The int8 and fp8 rowwise GEMMs on narrow tiles (configs 1..4), with the epilogues of the
+// 256x256 kernel: int8 on v_mfma_i32_16x16x64_i8 (exact int32; the CPU law's (acc·xs)·ws, cast,
 // then + bias in the output dtype, internal/int8_linear.py:445-448 and :276), fp8 on
-// v_mfma_f32_16x16x128_f8f6f4 ((acc·xs)·ws + bias in float32, one cast). Tiles of kTM x kTN
-// keep a few rows spread over ~224 workgroups: the weight stream, not the matrix core, bounds
-// these shapes (at M = 256 the 58.7 MB fp8 weight is 7.3 us of HBM against 6 us of MFMA).
+// v_mfma_f32_16x16x128_f8f6f4 ((acc·xs)·ws + bias in float32, one cast). They serve grids the
+// 256x256 tile would leave under-filled: few rows, where tiles of kTM x kTN spread the weight
+// stream over hundreds of workgroups (at M = 256 the 58.7 MB fp8 weight is 7.3 us of HBM against
+// 6 us of MFMA), and any shape with fewer than 160 256x256 tiles.
 //
 // A workgroup of 4 waves (2 x 2) owns a kTM x kTN tile; K advances 128 bytes a step through a
 // double-buffered LDS stage filled from registers. Every global read is a buffer load bounded by
@@ -25,10 +26,6 @@ constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer offset past num_recor
 // Physical 16-byte chunk of logical chunk c (0..7) in a 128-byte LDS row r: the 16 rows one
 // fragment read touches at a chunk fall on 16 distinct 4-bank groups.
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
-
-__device__ __forceinline__ float gelu_tanh(float y) {
-    return 0.5f * y * (1.0f + tanhf(0.79788456f * (y + 0.044715f * y * y * y)));
-}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_from(const uint8_t* base, int row0, int rows,
                                                           int K) {
@@ -288,15 +285,20 @@ hipError_t shaped(const uint8_t* q, const float* xs, const uint8_t* w, const flo
     return hipErrorInvalidValue;
 }
 
-template <bool kInt8>
+// Tile configs 1..4 (config 0 is the 256x256 kernel of gemm.hip): 128x128, 128x64, 64x64,
+// 32x64 (rows x columns). Every config computes each output with the same MFMA sequence over K
+// and the same epilogue.
+template <bool kInt8, bool kW4 = false>
 hipError_t narrow(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                   const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
-                  int epilogue, hipStream_t s) {
-    if (M <= 32) return shaped<kInt8, 32, 64>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
-    if (M <= 64) return shaped<kInt8, 64, 64>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
-    if (M <= 128) return shaped<kInt8, 128, 64>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
-    if (M <= 256) return shaped<kInt8, 128, 128>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
-    return hipErrorNotSupported;
+                  int epilogue, int config, hipStream_t s, W4 w4 = W4{nullptr, nullptr}) {
+    switch (config) {
+        case 1: return shaped<kInt8, 128, 128, kW4>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s, w4);
+        case 2: return shaped<kInt8, 128, 64, kW4>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s, w4);
+        case 3: return shaped<kInt8, 64, 64, kW4>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s, w4);
+        case 4: return shaped<kInt8, 32, 64, kW4>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s, w4);
+        default: return hipErrorNotSupported;
+    }
 }
 
 // The unpack law over a whole weight (internal/prebuilt.py:471-492): one thread a group of 16.
@@ -322,13 +324,10 @@ __global__ __launch_bounds__(kThreads) void w4a8_unpack_kernel(const uint8_t* __
 hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* codes,
                             const uint8_t* group_scale, const float* codebook, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
-                            hipStream_t s) {
-    const W4 w4{group_scale, codebook};
-    auto qp = reinterpret_cast<const uint8_t*>(q);
-    if (M <= 32) return shaped<true, 32, 64, true>(qp, xs, codes, ws, bias, out, N, out_half, M, N, K, 0, s, w4);
-    if (M <= 64) return shaped<true, 64, 64, true>(qp, xs, codes, ws, bias, out, N, out_half, M, N, K, 0, s, w4);
-    if (M <= 128) return shaped<true, 128, 64, true>(qp, xs, codes, ws, bias, out, N, out_half, M, N, K, 0, s, w4);
-    return shaped<true, 128, 128, true>(qp, xs, codes, ws, bias, out, N, out_half, M, N, K, 0, s, w4);
+                            int config, hipStream_t s) {
+    return narrow<true, true>(reinterpret_cast<const uint8_t*>(q), xs, codes, ws, bias, out, N,
+                              out_half, M, N, K, 0, config < 0 ? narrow_config(M, N) : config, s,
+                              W4{group_scale, codebook});
 }
 
 hipError_t w4a8_unpack(const uint8_t* codes, const uint8_t* group_scale, const float* codebook,
@@ -340,17 +339,28 @@ hipError_t w4a8_unpack(const uint8_t* codes, const uint8_t* group_scale, const f
     return hipGetLastError();
 }
 
+// The largest narrow tile whose grid reaches 440 workgroups (~1.7 a CU: the sweep's best tile
+// at every shape below 160 256x256 tiles had 448-768), else the smallest.
+int narrow_config(int M, int N) {
+    static constexpr int kRows[] = {0, 128, 128, 64, 32}, kCols[] = {0, 128, 64, 64, 64};
+    for (int c = 1; c < kGemmConfigs; ++c) {
+        const int64_t groups = static_cast<int64_t>((M + kRows[c] - 1) / kRows[c]) * ((N + kCols[c] - 1) / kCols[c]);
+        if (groups >= 440) return c;
+    }
+    return kGemmConfigs - 1;
+}
+
 hipError_t gemm_fp8_narrow(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                            const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
-                           int K, int epilogue, hipStream_t s) {
-    return narrow<false>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
+                           int K, int epilogue, int config, hipStream_t s) {
+    return narrow<false>(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, config, s);
 }
 
 hipError_t gemm_int8_narrow(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                             const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
-                            int K, int epilogue, hipStream_t s) {
+                            int K, int epilogue, int config, hipStream_t s) {
     return narrow<true>(reinterpret_cast<const uint8_t*>(q), xs, reinterpret_cast<const uint8_t*>(w),
-                        ws, bias, out, ldo, out_half, M, N, K, epilogue, s);
+                        ws, bias, out, ldo, out_half, M, N, K, epilogue, config, s);
 }
 
 }  // namespace cozyq

@@ -76,13 +76,6 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 // groups of 256 bytes.
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
 
-// tanh-GELU, 0.5·y·(1 + tanh(u)) with u = 0.79788456·(y + 0.044715·y³), as y / (1 + e^(-2u)):
-// e^(-2u) = 2^(y·(c1 + c2·y²)) with c1 = -2·log2(e)·0.79788456 and c2 = 0.044715·c1.
-__device__ __forceinline__ float gelu_tanh(float y) {
-    const float t = __builtin_fmaf(-0.10294324f, y * y, -2.3022082f);
-    return y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y * t));
-}
-
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 

@@ -47,12 +47,18 @@ hipError_t linear_int8_noalloc(const void* x, bool half, int rotation, int8_t* q
                                int64_t ldo, int M, int N, int K, int epilogue, int device,
                                hipStream_t s);
 
+// The rowwise GEMMs' tile configs: 0 the 256x256 kernel, 1..4 the narrow kernel's 128x128,
+// 128x64, 64x64 and 32x64 (kGemmConfigs in all); -1 lets gemm_config choose by shape. Every
+// config gives the same int8 output bit for bit; an unknown config is hipErrorNotSupported.
+constexpr int kGemmConfigs = 5;
+int gemm_config(bool fp8, int M, int N, int K);
+int narrow_config(int M, int N);
 hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                      const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
-                     int epilogue, hipStream_t s);
+                     int epilogue, int config, hipStream_t s);
 hipError_t gemm_fp8(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                     const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
-                    int epilogue, hipStream_t s);
+                    int epilogue, int config, hipStream_t s);
 hipError_t gemm_mx(const uint8_t* q, const uint8_t* qe, const uint8_t* w, const uint8_t* we,
                    const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
                    hipStream_t s);
@@ -61,20 +67,20 @@ hipError_t gemm_int8_acc(const int8_t* q, const int8_t* w, int32_t* acc, int M, 
 
 hipError_t gemm_fp8_narrow(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                            const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
-                           int K, int epilogue, hipStream_t s);
+                           int K, int epilogue, int config, hipStream_t s);
 
 // w4a8.convrot: codes [N, K/2], E4M3 group scales [N, K/16], codebook (16 float32 levels or
 // null for q − 8); the fused narrow-tile GEMM (int8 q [M, K], the int8 epilogue, out [M, N]) and
-// the unpack to int8 levels [N, K].
+// the unpack to int8 levels [N, K]. The fused GEMM takes configs 1..4 (-1: narrow_config).
 hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* codes,
                             const uint8_t* group_scale, const float* codebook, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
-                            hipStream_t s);
+                            int config, hipStream_t s);
 hipError_t w4a8_unpack(const uint8_t* codes, const uint8_t* group_scale, const float* codebook,
                        int8_t* out, int N, int K, hipStream_t s);
 hipError_t gemm_int8_narrow(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                             const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
-                            int K, int epilogue, hipStream_t s);
+                            int K, int epilogue, int config, hipStream_t s);
 
 // The fused int8 linear for 1..4 rows (rotate H256 + quantize + GEMV in one launch);
 // hipErrorNotSupported past M·K = 16384.

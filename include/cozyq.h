@@ -83,12 +83,20 @@ typedef void* (*cozyq_allocate_fn)(size_t bytes, void* context);
  * then the bias added in the output dtype), bit-for-bit. fp8: float32 accumulation, one cast.
  * out rows are `ldo` elements apart (ldo >= N, ldo % 8 == 0, out 16-byte aligned); w_scale and
  * bias are 16-byte aligned. family must
- * be 0 (the one CDNA4 MFMA family); config -1 chooses by shape, 0 names the 256x256 tile,
- * other values return hipErrorNotSupported. N % 8 == 0; K % 256 (int8) or K % 16 (fp8). */
+ * be 0 (the one CDNA4 MFMA family). config names a tile as the reference's table does
+ * (gemm_sm80.cu:233-289, gemm_fp8.cu:15-58), gfx950's own: 0 the 256x256 tile, 1 128x128,
+ * 2 128x64, 3 64x64, 4 32x64 (rows x columns); -1 chooses by shape (cozyq_gemm_config); 5 and
+ * above return hipErrorNotSupported. Every config gives the same int8 output bit for bit.
+ * N % 8 == 0; K % 256 (int8) or K % 16 (fp8). */
 int cozyq_gemm(int device, int family, int fp8, const void* q, const float* scales,
                const void* w, const float* w_scale, const void* bias, void* out, int64_t ldo,
                int out_half, int M, int N, int K, int config, cozyq_allocate_fn allocate,
                void* allocate_context, void* stream);
+
+/* The config cozyq_gemm (and cozyq_gemm_ex, which always chooses) runs for config -1 at this
+ * shape (reference: the `choose` of gemm_sm80.cu:283-288 and gemm_fp8.cu:23-29, which the
+ * reference does not export); -1 for a non-positive dimension. */
+int cozyq_gemm_config(int fp8, int M, int N, int K);
 
 /* cozyq_gemm with an epilogue activation (no reference counterpart: the reference's epilogue
  * is scales + bias only). epilogue 0: none; 1: tanh-GELU applied in float32 to the result of
@@ -135,8 +143,9 @@ int cozyq_gemm_i32(int device, const int8_t* q, const int8_t* w, int32_t* acc, i
  * uniform grid q - 8): level = clamp(rne(codebook[code] · e4m3(s)), ±127), a NaN product 0
  * (internal/prebuilt.py:471-492). The codes are unpacked in registers on the way to the int8
  * MFMA; the epilogue is cozyq_gemm's int8 law with w_scale [N], bit for bit. out [M, N].
- * N % 8 == 0, K % 256 == 0; q and w 16-byte aligned, out 8-byte aligned. config -1 or 0;
- * others return hipErrorNotSupported. */
+ * N % 8 == 0, K % 256 == 0; q and w 16-byte aligned, out 8-byte aligned. config names
+ * cozyq_gemm's narrow tiles 1..4 (-1: by rows); 0 (the 256x256 tile, which multiplies the
+ * codes unpacked by cozyq_w4a8_unpack) and 5 and above return hipErrorNotSupported. */
 int cozyq_w4a8_gemm(int device, const int8_t* q, const float* scales, const uint8_t* w,
                     const uint8_t* s, const float* codebook, const float* w_scale, const void* bias,
                     void* out, int out_half, int M, int N, int K, int config, void* stream);

@@ -524,6 +524,46 @@ def test_fp8_gemm_within_tolerance(ops, shape, bias):
     assert_close(got, laws.fp8_exact(x, data, scale, b))
 
 
+# (M, N, K): one row; ragged rows and columns on every tile; the 256x256 tile's ragged edges;
+# more rows than the narrow tiles' 128; a K with a partial 128-byte step for fp8.
+CONFIG_SHAPES = [(1, 264, 1024), (100, 520, 768), (300, 1032, 2048), (513, 264, 256),
+                 (1100, 776, 1024), (77, 136, 4096)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("shape", CONFIG_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_every_gemm_config_bit_equal(ops, shape, dtype):
+    """Every tile config of `cozyq_gemm` (0..4 and the shape rule's -1) gives the int8 law bit
+    for bit, with and without bias (as the reference checks each explicit tile,
+    `internal/bench/gemm.py:418-435`); the fp8 configs agree with one another bit for bit (each
+    output's K sum runs in the same MFMA order) and sit within tolerance of the exact law; a
+    config past the table is refused."""
+    from cozyq import prebuilt
+
+    m, n, k = shape
+    x = activations(m, k, seed=m * 7 + k)
+    data, scale = laws.int8_weight_rowwise(weights(n, k, seed=n))
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 0.1).to(dtype)
+    q, s = ops.int8_quantize(x.to(DEV))
+    for bias in (None, b):
+        want = laws.int8_product(q.cpu(), s.cpu(), data, scale, dtype)
+        want = want if bias is None else want + bias
+        for config in range(-1, prebuilt.GEMM_CONFIGS):
+            got = ops.int8_gemm(q, s, data.to(DEV), scale.to(DEV),
+                                None if bias is None else bias.to(DEV), dtype, config)  # fmt: skip
+            assert torch.equal(got.cpu(), want), (config, bias is None)
+    with pytest.raises(ValueError, match="config 5"):
+        ops.int8_gemm(q, s, data.to(DEV), scale.to(DEV), None, dtype, prebuilt.GEMM_CONFIGS)
+    if k % 16 == 0:
+        f8, f8s = laws.fp8_weight(weights(n, k, seed=n + 1))
+        q8, s8 = ops.fp8_quantize(x.to(DEV))
+        outs = [ops.fp8_gemm(q8, s8, f8.to(DEV), f8s.to(DEV), b.to(DEV), dtype, c)
+                for c in range(-1, prebuilt.GEMM_CONFIGS)]  # fmt: skip
+        for config, out in zip(range(-1, prebuilt.GEMM_CONFIGS), outs):
+            assert torch.equal(out, outs[1]), config
+        assert_close(outs[0], laws.fp8_exact(x, f8, f8s, b))
+
+
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(300, 512, 1024), (520, 264, 2064), (40, 136, 4096)],
                          ids=lambda s: "x".join(map(str, s)))  # fmt: skip
@@ -667,9 +707,9 @@ def test_w4a8_linear_bit_exact(ops, shape, codebook):
         got = ops.w4a8_linear(x.to(DEV), w, None if bias is None else bias.to(DEV), torch.bfloat16)
         assert torch.equal(got.cpu(), laws.int8_linear(x, levels, scale, bias, torch.bfloat16))
     q, s = ops.int8_quantize(x.to(DEV))
-    fused = ops.w4a8_gemm(q, s, w, b.to(DEV), torch.bfloat16, 0)
     unpacked = ops.w4a8_gemm(q, s, w, b.to(DEV), torch.bfloat16, prebuilt.UNPACK)
-    assert torch.equal(fused, unpacked)
+    for config in range(1, prebuilt.GEMM_CONFIGS):  # every fused tile
+        assert torch.equal(ops.w4a8_gemm(q, s, w, b.to(DEV), torch.bfloat16, config), unpacked), config
 
 
 # ------------------------------------------------------------------------ MXFP8 lane
