@@ -43,6 +43,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _P, _P, _P],
     ),
     "cozyq_gemm_config": (c_int, [c_int, c_int, c_int, c_int]),
+    "cozyq_svdq_rows": (c_int, [c_int]),
+    "cozyq_svdq_input_scale": (c_int, [c_int, _P, c_int, _P, c_int, c_int, _P, _P]),
+    "cozyq_svdq_quantize": (
+        c_int, [c_int, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P]
+    ),
+    "cozyq_svdq_gemm": (
+        c_int,
+        [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P],
+    ),
     "cozyq_linear_workspace_bytes": (c_int64, [c_int64]),
     "cozyq_linear_noalloc_max_rows": (c_int, []),
     "cozyq_linear_noalloc": (

@@ -173,7 +173,7 @@ class _SvdqLane(_Lane):
         out_dtype = leaf.out_dtype if dtype is None else dtype
         x = x if dtype is None else x.to(dtype)
         index = _dispatch.activation_card("svdq", torch, x, out_dtype)
-        result = _dispatch.library(index).svdq_linear(
+        result = _dispatch.library(index).svdq_int4_linear(
             x, read(leaf.pre_quant_scale), read(leaf.lowrank_down), read(leaf.weight),
             read(leaf.scale), read(leaf.lowrank_up), read(leaf.bias), out_dtype)  # fmt: skip
         return result

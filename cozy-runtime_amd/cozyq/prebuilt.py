@@ -60,6 +60,10 @@ GEMM_CONFIGS = 5
 INT8, FP8 = _Format("int8", False, 256), _Format("fp8", True, 16)
 MX = _Format("mxfp8", True, 128)
 SVDQ = _Format("svdq-int4", False, INT4_GROUP)
+#: svdq.nvfp4: K in whole 64-element GEMM steps (the reference's `kDepth`, svdq.h:15), and the
+#: ranks its kernels take (`internal/svdq_linear.py:49`).
+SVDQ_NVFP4 = _Format("svdq.nvfp4", False, 64)
+NVFP4_RANKS = (32, 64, 128)
 
 
 def _torch():
@@ -401,7 +405,7 @@ class Prebuilt:
         out = self.mx_gemm(q, qs, data, wscales, bias, out_dtype)
         return out.view(*x.shape[:-1], data.shape[0])
 
-    def svdq_quantize(
+    def svdq_int4_quantize(
         self, x: Tensor, p: Tensor, down: Tensor
     ) -> tuple[Tensor, Tensor, Tensor]:
         """The int4-g64 activation side (`cozyq_svdq_int4_quantize`): packed codes `[M, K/2]`,
@@ -427,10 +431,11 @@ class Prebuilt:
         self._check(code, "the svdq quantization")
         return act, ascales, la
 
-    def svdq_gemm(
+    def svdq_int4_gemm(
         self, act: Tensor, ascales: Tensor, la: Tensor, w: Tensor, wscales: Tensor, up: Tensor,
         bias: Tensor | None, out_dtype: Dtype,
     ) -> Tensor:
+        """The int4-g64 GEMM (`cozyq_svdq_int4_gemm`) with the low-rank term and the bias."""
         torch = self.torch
         rows, width = int(act.shape[0]), 2 * int(act.shape[1])
         n, r = int(w.shape[0]), int(up.shape[1])
@@ -461,13 +466,116 @@ class Prebuilt:
         self._check(code, "the svdq GEMM")
         return out
 
-    def svdq_linear(
+    def svdq_int4_linear(
         self, x: Tensor, p: Tensor, down: Tensor, w: Tensor, wscales: Tensor, up: Tensor,
         bias: Tensor | None, out_dtype: Dtype,
     ) -> Tensor:
-        act, ascales, la = self.svdq_quantize(x, p, down)
-        out = self.svdq_gemm(act, ascales, la, w, wscales, up, bias, out_dtype)
+        act, ascales, la = self.svdq_int4_quantize(x, p, down)
+        out = self.svdq_int4_gemm(act, ascales, la, w, wscales, up, bias, out_dtype)
         return out.view(*x.shape[:-1], w.shape[0])
+
+    # ----------------------------------------------------------- svdq.nvfp4 W4A4
+
+    def svdq_input_scale(self, x: Tensor, p: Tensor) -> Tensor:
+        """g_x on the card (`cozyq_svdq_input_scale`; the reference's `activation_scale`,
+        `internal/svdq_linear.py:582-590`, without a stored `input_scale`): float32 [1]."""
+        torch = self.torch
+        flat = self._rows(SVDQ_NVFP4, x)
+        rows, width = flat.shape
+        if p.dtype != torch.float32 or p.numel() != width:
+            raise ValueError(f"svdq: p must be float32 with {width} values")
+        g = torch.empty(1, dtype=torch.float32, device=x.device)
+        code = self._lib.cozyq_svdq_input_scale(
+            self.index, flat.data_ptr(), self._half(flat.dtype), _aligned(p).data_ptr(), rows,
+            width, g.data_ptr(), self._stream())  # fmt: skip
+        self._check(code, "the svdq input scale")
+        return g
+
+    def svdq_quantize(
+        self, x: Tensor, p: Tensor, g: Tensor, down: Tensor
+    ) -> tuple[Tensor, Tensor, Tensor]:
+        """`svdq_quantize` (`internal/svdq_linear.py:510-534`, `kernels/csrc/gemm.cpp:169-178`):
+        x's nvfp4 operand at second level g — codes `[Rows(M), K/2]` (u8, element 2k low) and
+        E4M3 scales `[Rows(M), K/16]` — and the low-rank input `bf16(x·downᵀ)` `[Rows(M), R]`,
+        rows past M zero (Rows(M) = M rounded up to 256)."""
+        torch = self.torch
+        flat = self._rows(SVDQ_NVFP4, x)
+        rows, width = flat.shape
+        r = int(down.shape[0])
+        if r not in NVFP4_RANKS or tuple(down.shape) != (r, width) or down.dtype != torch.bfloat16:
+            raise ValueError(f"svdq: down must be bf16 [R, {width}], R in {NVFP4_RANKS}")
+        if p.dtype != torch.float32 or p.numel() != width:
+            raise ValueError(f"svdq: p must be float32 with {width} values")
+        if g.dtype != torch.float32 or g.numel() != 1 or g.device != x.device:
+            raise ValueError("svdq: g must be one float32 on x's device")
+        padded = self._lib.cozyq_svdq_rows(rows)
+        act = torch.empty(padded, width // 2, dtype=torch.uint8, device=x.device)
+        ascales = torch.empty(padded, width // 16, dtype=torch.float8_e4m3fn, device=x.device)
+        la = torch.empty(padded, r, dtype=torch.bfloat16, device=x.device)
+        code = self._lib.cozyq_svdq_quantize(
+            self.index, flat.data_ptr(), self._half(flat.dtype), _aligned(p).data_ptr(),
+            g.data_ptr(), _aligned(down).data_ptr(), act.data_ptr(), ascales.data_ptr(),
+            la.data_ptr(), rows, width, r, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the svdq quantization")
+        return act, ascales, la
+
+    def svdq_gemm(
+        self, act: Tensor, ascales: Tensor, la: Tensor, rows: int, gx: Tensor, weight: Tensor,
+        scale: Tensor, scale_2: Tensor, up: Tensor, c: Tensor | None, bias: Tensor | None,
+        out_dtype: Dtype,
+    ) -> Tensor:
+        """`svdq_gemm` (`internal/svdq_linear.py:537-567`, `kernels/csrc/gemm.cpp:180-190`):
+        `[rows, N]` = `(A·Wᵀ)·gx·gw·c + la·upᵀ + bias`, rounded once. `weight` u8 `[N, K/2]`
+        and `scale` E4M3 `[N, K/16]` as stored; `scale_2` (gw) and `gx` float32 [1]; `up` bf16
+        `[N, R]`; `c` float32 `[N]` or None."""
+        torch = self.torch
+        width = 2 * int(act.shape[1])
+        n, r = int(weight.shape[0]), int(up.shape[1])
+        if tuple(weight.shape) != (n, width // 2) or tuple(scale.shape) != (n, width // 16):
+            raise ValueError(f"svdq: weight [N, {width // 2}] and scale [N, {width // 16}]")
+        if weight.dtype != torch.uint8 or scale.dtype != torch.float8_e4m3fn:
+            raise ValueError("svdq: the weight is uint8 codes with float8_e4m3fn scales")
+        if r not in NVFP4_RANKS or tuple(up.shape) != (n, r) or up.dtype != torch.bfloat16:
+            raise ValueError(f"svdq: up must be bf16 [N, R], R in {NVFP4_RANKS}")
+        if tuple(la.shape) != (int(act.shape[0]), r) or la.dtype != torch.bfloat16:
+            raise ValueError("svdq: la must be bf16 [Rows(M), R]")
+        if n % 8:
+            raise ValueError("svdq: N must be a multiple of 8")
+        if c is not None and (c.dtype != torch.float32 or c.numel() != n):
+            raise ValueError(f"svdq: channel_scale must be float32 with {n} values")
+        half = self._half(out_dtype)
+        out = torch.empty(rows, n, dtype=out_dtype, device=act.device)
+        if rows == 0:
+            return out
+        bias = None if bias is None else _aligned(bias.to(out_dtype).reshape(-1))
+        tensors = (act, ascales, weight, scale, la, up)
+        act, ascales, weight, scale, la, up = (_aligned(t) for t in tensors)
+        gw = scale_2.to(torch.float32).reshape(1)
+        code = self._lib.cozyq_svdq_gemm(
+            self.index, act.data_ptr(), ascales.data_ptr(), weight.data_ptr(), scale.data_ptr(),
+            gx.data_ptr(), gw.data_ptr(), _ptr(None if c is None else _aligned(c)), la.data_ptr(),
+            up.data_ptr(), _ptr(bias), out.data_ptr(), half, rows, n, width, r, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the svdq GEMM")
+        return out
+
+    def svdq_linear(self, x: Tensor, roles: dict, bias: Tensor | None, out_dtype: Dtype) -> Tensor:
+        """The svdq.nvfp4 linear (`internal/svdq_linear.py:662-697` on the prebuilt kernels):
+        g_x (the stored `input_scale`, else `svdq_input_scale`), `svdq_quantize`, `svdq_gemm`.
+        `roles` as the reference's leaf holds them: `weight`, `scale`, `scale_2`,
+        `pre_quant_scale`, `lowrank_down`, `lowrank_up`, optional `channel_scale` and
+        `input_scale`."""
+        torch = self.torch
+        p = roles["pre_quant_scale"]
+        flat = self._rows(SVDQ_NVFP4, x)
+        stored = roles.get("input_scale")
+        g = self.svdq_input_scale(flat, p) if stored is None else stored.to(torch.float32).reshape(1)
+        act, ascales, la = self.svdq_quantize(flat, p, g, roles["lowrank_down"])
+        out = self.svdq_gemm(act, ascales, la, int(flat.shape[0]), g, roles["weight"],
+                             roles["scale"], roles["scale_2"], roles["lowrank_up"],
+                             roles.get("channel_scale"), bias, out_dtype)  # fmt: skip
+        return out.view(*x.shape[:-1], -1)
 
     # ------------------------------------------------------------------- nvfp4 W4A16
 

@@ -273,6 +273,47 @@ int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales
                                  R, on(stream));
 }
 
+int cozyq_svdq_rows(int M) { return M < 0 ? -1 : cozyq::svdq_nvfp4_padded_rows(M); }
+
+int cozyq_svdq_input_scale(int device, const void* x, int x_half, const float* p, int M, int K,
+                           float* g, void* stream) {
+    if (M < 0 || !fits(K, 64) || !g || !aligned16(x) || !aligned16(p)) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::svdq_nvfp4_input_scale(x, x_half != 0, p, M, K, g, on(stream));
+}
+
+static bool svdq_rank(int R) { return R == 32 || R == 64 || R == 128; }
+
+int cozyq_svdq_quantize(int device, const void* x, int x_half, const float* p, const float* g,
+                        const void* down, void* act, void* ascales, void* la, int M, int K, int R,
+                        void* stream) {
+    if (M < 0 || !fits(K, 64) || !svdq_rank(R)) return hipErrorInvalidValue;
+    if (M > 0 && (!g || !aligned16(x) || !aligned16(p) || !aligned16(down) || !aligned16(act) ||
+                  !aligned16(ascales) || !aligned16(la)))
+        return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::svdq_nvfp4_quantize(x, x_half != 0, p, g, down, static_cast<uint8_t*>(act),
+                                      static_cast<uint8_t*>(ascales), la, M, K, R, on(stream));
+}
+
+int cozyq_svdq_gemm(int device, const void* act, const void* ascales, const void* w,
+                    const void* wscales, const float* gx, const float* gw, const float* c,
+                    const void* la, const void* up, const void* bias, void* out, int out_half,
+                    int M, int N, int K, int R, void* stream) {
+    if (M < 1 || N < 8 || N % 8 || !fits(K, 64) || !svdq_rank(R) || !gx || !gw)
+        return hipErrorInvalidValue;
+    if (!aligned16(act) || !aligned16(ascales) || !aligned16(w) || !aligned16(wscales) ||
+        !aligned16(la) || !aligned16(up) || !aligned16(out) || !aligned16(c) || !aligned16(bias))
+        return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::svdq_nvfp4_gemm(static_cast<const uint8_t*>(act), static_cast<const uint8_t*>(ascales),
+                                  static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(wscales),
+                                  gx, gw, c, la, up, bias, out, out_half != 0, M, N, K, R, on(stream));
+}
+
 int cozyq_decode(int device, int code, const void* w, const void* scale, int scale_type, int grid,
                  int block, int tiled, const float* scale_2, int scale_2_step, int second,
                  const void* post, int post_type, int post_mode, int high_first, void* out,

@@ -125,6 +125,21 @@ struct TableDecode {
     int64_t rows, cols;
 };
 
+// svdq.nvfp4's W4A4 linear (svdq_nvfp4.hip): the activation's second level g_x from x and p;
+// x -> the nvfp4 operand (act [Rows(M), K/2], ascales [Rows(M), K/16], la [Rows(M), R], Rows(M)
+// = svdq_nvfp4_padded_rows(M), rows past M zero); the GEMM out [M, N] = (A·Wᵀ)·gx·gw·c + la·upᵀ
+// + bias, one rounding (c and bias may be null). K % 64 == 0, R in {32, 64, 128}, N % 8 == 0.
+int svdq_nvfp4_padded_rows(int M);
+hipError_t svdq_nvfp4_input_scale(const void* x, bool x_half, const float* p, int M, int K,
+                                  float* g, hipStream_t s);
+hipError_t svdq_nvfp4_quantize(const void* x, bool x_half, const float* p, const float* g,
+                               const void* down, uint8_t* act, uint8_t* ascales, void* la, int M,
+                               int K, int R, hipStream_t s);
+hipError_t svdq_nvfp4_gemm(const uint8_t* act, const uint8_t* ascales, const uint8_t* w,
+                           const uint8_t* wscales, const float* gx, const float* gw,
+                           const float* c, const void* la, const void* up, const void* bias,
+                           void* out, bool out_half, int M, int N, int K, int R, hipStream_t s);
+
 // svdq.nvfp4: codes [rows, cols/2], E4M3 scales per 16 (row-major or 128x4 tiles), scale_2,
 // optional channel scale [rows], smoothing [cols], lowrank_down [rank, cols], lowrank_up
 // [rows, rank].

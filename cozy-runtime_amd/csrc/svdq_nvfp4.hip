@@ -1,0 +1,560 @@
+// SVDQuant W4A4 with nvfp4 operands (svdq.nvfp4) on gfx950: the reference's `svdq_quantize` and
+// `svdq_gemm` (kernels/csrc/gemm.cpp:169-190; law internal/svdq_linear.py:582-659), plus the
+// activation's second level g_x (`activation_scale`, :582-590), which the reference takes with
+// torch ops.
+//
+// Activation side (one kernel): xs = bf16(x·p); per 16-block of a row the E4M3 scale
+// e4m3(clamp(amax|xs| / (6·g), 2^-9, 448)) and each element's E2M1 code by the law's threshold
+// count on |xs / (scale·g)| (ties to the even code), sign in bit 3, packed two a byte with element
+// 2k in the low nibble: act [Rows(M), K/2] and ascales [Rows(M), K/16] row-major, Rows(M) = M
+// rounded up to 256, rows past M zero. The low-rank input la = bf16(x · downᵀ) [Rows(M), R] comes
+// from the same registers on the 16x16x32 half-precision MFMA (x in its own dtype, down cast to
+// it: :598-602).
+//
+// GEMM: out = (A·Wᵀ)·g_x·g_w·c[n] + la·upᵀ + bias[n], rounded once. gfx950's FP4 MFMA scales
+// blocks of 32 by E8M0 exponents (and v_cvt_scalef32_*_fp4 reads only its scale's exponent), so
+// nvfp4's E4M3 scales per 16 cannot ride on it. Instead each operand element is decoded exactly
+// into fp16: E2M1 (v_cvt_scalef32_pk_f16_fp4 at scale 1) times its E4M3 scale (v_pk_mul_f16; the
+// product has at most 6 significant bits and lies in [2^-10, 2688], so fp16 holds it exactly),
+// and the products are summed in float32 on v_mfma_f32_32x32x16_f16. The 256x256 tile, LDS layout
+// and fragment schedule are gemm_tile.h's int8 ones: a 128-byte LDS row holds 64 fp16 elements of
+// K, which the f16 MFMA consumes 32 bytes a step exactly as the int8 MFMA does. Staging goes
+// through registers: each thread loads one A row's and one W row's 32 code bytes and 4 scale
+// bytes for a buffer, decodes them one buffer ahead of the MFMAs that read them, and writes the
+// fp16 rows into the swizzled buffer. The epilogue scales the accumulators by g_x·g_w·c[n], adds
+// la·upᵀ into the same accumulators on v_mfma_f32_32x32x16_bf16, adds the bias and rounds once.
+#include "gemm_tile.h"
+
+namespace cozyq {
+namespace {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kLevelsMax = 448.0f * 6.0f;  // internal/svdq_linear.py:44
+constexpr float kBlockFloor = 0x1p-9f;       // internal/svdq_linear.py:46: E4M3's least subnormal
+constexpr float kInputFloor = 1e-30f;        // internal/svdq_linear.py:590
+constexpr int kPadRows = 256;                // the operand's row padding (the GEMM's row tile)
+
+__host__ __device__ __forceinline__ int padded_rows(int M) { return (M + kPadRows - 1) / kPadRows * kPadRows; }
+
+// Eight 16-bit values (one uint4) as float32.
+template <bool kHalf>
+__device__ __forceinline__ void widen8(const uint4 v, float* f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = widen<kHalf>(static_cast<uint16_t>(w[i] & 0xffffu));
+        f[2 * i + 1] = widen<kHalf>(static_cast<uint16_t>(w[i] >> 16));
+    }
+}
+
+// ------------------------------------------------------------ the activation's second level
+
+__global__ void input_scale_init(uint32_t* g) { *g = bits_of(kInputFloor); }
+
+// g = max(max over x of fl(|x|·p[col]) / 2688, 1e-30). The law takes amax over rows first, then
+// · p, then the max: the same value, since fl(a·p) is monotonic in a for p > 0; the division and
+// the clamp are monotonic too, so each block's candidate enters by an unsigned max of its
+// (non-negative) float bits into *g, which input_scale_init set to the floor.
+template <bool kHalf>
+__global__ __launch_bounds__(256) void input_scale_kernel(const uint16_t* __restrict__ x,
+                                                          const float* __restrict__ p,
+                                                          int64_t chunks, int per_row,
+                                                          uint32_t* __restrict__ g) {
+    __shared__ float red[4];
+    float m = 0.0f;
+    for (int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; c < chunks;
+         c += static_cast<int64_t>(gridDim.x) * 256) {
+        const uint4 v = *reinterpret_cast<const uint4*>(x + c * 8);
+        const int col = static_cast<int>(c % per_row) * 8;
+        const float4 p0 = *reinterpret_cast<const float4*>(p + col);
+        const float4 p1 = *reinterpret_cast<const float4*>(p + col + 4);
+        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        float f[8];
+        widen8<kHalf>(v, f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, __fmul_rn(fabsf(f[i]), pv[i]));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        atomicMax(g, bits_of(fmaxf(__fdiv_rn(m, kLevelsMax), kInputFloor)));
+    }
+}
+
+// ------------------------------------------------------------------- activation quantize
+
+constexpr int kQRows = 16;  // rows a block (the MFMA's M)
+constexpr int kQGroup = 64;  // columns a wave takes at a time: four 16-blocks, one a lane group
+
+// bf16 bits (one uint4) -> fp16 by way of float32, round to nearest even (torch's cast).
+__device__ __forceinline__ f16x8 bf16_to_half8(const uint4 v) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    f16x8 h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h[2 * i] = static_cast<_Float16>(float_of(w[i] << 16));
+        h[2 * i + 1] = static_cast<_Float16>(float_of(w[i] & 0xffff0000u));
+    }
+    return h;
+}
+
+// The E2M1 code of a (already |xs / (scale·g)|): the law's threshold count, nearest value with
+// ties to the even code (internal/svdq_linear.py:613-616).
+__device__ __forceinline__ uint32_t e2m1_count(float a) {
+    return static_cast<uint32_t>(a > 0.25f) + static_cast<uint32_t>(a >= 0.75f) +
+           static_cast<uint32_t>(a > 1.25f) + static_cast<uint32_t>(a >= 1.75f) +
+           static_cast<uint32_t>(a > 2.5f) + static_cast<uint32_t>(a >= 3.5f) +
+           static_cast<uint32_t>(a > 5.0f);
+}
+
+template <int kR>
+constexpr int quantize_waves() { return kR == 128 ? 8 : 16; }  // the partial sums fit the LDS
+
+// Block: kQRows rows (of Rows(M)). Lane l of a wave holds row l%16 and, in each of its 64-column
+// groups, the 16 columns [16·(l/16), +16): exactly one nvfp4 block, so its amax stays in the
+// lane, and the same 16 values feed two 16x16x32 MFMAs against down (read with the same
+// pattern, so every k meets its own down element).
+template <bool kHalf, int kR>
+__global__ __launch_bounds__(quantize_waves<kR>() * 64) void nvfp4_quantize_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ p, const float* __restrict__ g,
+    const uint16_t* __restrict__ down, uint8_t* __restrict__ act, uint8_t* __restrict__ ascales,
+    uint16_t* __restrict__ la, int M, int K) {
+    constexpr int kWaves = quantize_waves<kR>();
+    constexpr int kJ = kR / 16;
+    __shared__ float red[kWaves][kQRows][kR];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, part = lane >> 4;
+    const int m0 = blockIdx.x * kQRows;
+    const int m = m0 + r16;
+    const bool live = m < M;  // rows in [M, Rows(M)) are written as zeros
+    const int row = live ? m : M - 1;
+    const int groups = K / kQGroup;
+    const uint16_t* xrow = x + static_cast<int64_t>(row) * K;
+    const float gv = g[0];
+    const float six_g = __fmul_rn(6.0f, gv);
+
+    f32x4 acc[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int gi = wave; gi < groups; gi += kWaves) {
+        const int col = kQGroup * gi + 16 * part;
+        const uint4 xa = *reinterpret_cast<const uint4*>(xrow + col);
+        const uint4 xb = *reinterpret_cast<const uint4*>(xrow + col + 8);
+        uint4 da[kJ], db[kJ];
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+            const uint16_t* drow = down + static_cast<int64_t>(16 * j + r16) * K + col;
+            da[j] = *reinterpret_cast<const uint4*>(drow);
+            db[j] = *reinterpret_cast<const uint4*>(drow + 8);
+        }
+        float pv[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 q4 = *reinterpret_cast<const float4*>(p + col + 4 * i);
+            pv[4 * i] = q4.x; pv[4 * i + 1] = q4.y; pv[4 * i + 2] = q4.z; pv[4 * i + 3] = q4.w;
+        }
+
+        // internal/svdq_linear.py:592-595: bf16(x·p) in float32; :609-611 the block scale.
+        float v[16];
+        widen8<kHalf>(xa, v);
+        widen8<kHalf>(xb, v + 8);
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            v[i] = float_of(static_cast<uint32_t>(bf16_rn(__fmul_rn(v[i], pv[i]))) << 16);
+            amax = fmaxf(amax, fabsf(v[i]));
+        }
+        const float ratio = fminf(fmaxf(__fdiv_rn(amax, six_g), kBlockFloor), kE4m3Max);
+        const uint32_t sb = e4m3_rn(ratio);
+        const float sg = __fmul_rn(e4m3_value(sb), gv);
+        uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t code = e2m1_count(fabsf(__fdiv_rn(v[i], sg))) + (v[i] < 0.0f ? 8u : 0u);
+            packed[i >> 3] |= code << (4 * (i & 7));
+        }
+        if (!live) packed[0] = packed[1] = 0u;
+        const int64_t base = static_cast<int64_t>(m) * (K / 2) + 32 * gi + 8 * part;
+        *reinterpret_cast<uint2*>(act + base) = make_uint2(packed[0], packed[1]);
+        ascales[static_cast<int64_t>(m) * (K / 16) + 4 * gi + part] = live ? static_cast<uint8_t>(sb) : 0;
+
+        // The low-rank input: x (not xs) against down, in x's dtype.
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+            if constexpr (kHalf) {
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8, xa), bf16_to_half8(da[j]), acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8, xb), bf16_to_half8(db[j]), acc[j], 0, 0, 0);
+            } else {
+                acc[j] = mfma_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, da[j]), acc[j]);
+                acc[j] = mfma_bf16(__builtin_bit_cast(bf16x8, xb), __builtin_bit_cast(bf16x8, db[j]), acc[j]);
+            }
+        }
+    }
+
+    // acc[j]: lane holds rank 16j + l%16 of rows 4·(l/16) + r. Sum the waves' partials.
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][4 * part + r][16 * j + r16] = acc[j][r];
+    __syncthreads();
+    for (int t = tid; t < kQRows * kR; t += kWaves * 64) {
+        const int rl = t / kR, rank = t % kR;
+        float sum = red[0][rl][rank];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) sum += red[w][rl][rank];
+        la[static_cast<int64_t>(m0 + rl) * kR + rank] = m0 + rl < M ? bf16_rn(sum) : 0;
+    }
+}
+
+template <bool kHalf, int kR>
+hipError_t launch_quantize(const void* x, const float* p, const float* g, const void* down,
+                           uint8_t* act, uint8_t* ascales, void* la, int M, int K, hipStream_t s) {
+    const int blocks = padded_rows(M) / kQRows;
+    nvfp4_quantize_kernel<kHalf, kR><<<blocks, quantize_waves<kR>() * 64, 0, s>>>(
+        static_cast<const uint16_t*>(x), p, g, static_cast<const uint16_t*>(down), act, ascales,
+        static_cast<uint16_t*>(la), M, K);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------ GEMM
+
+// One operand row's 64 elements of a buffer (32 code bytes, 4 E4M3 scale bytes) decoded to fp16
+// and written as the 8 swizzled 16-byte chunks of LDS row r. Chunk c holds elements 8c..8c+7:
+// code dword c, 16-block c/2.
+__device__ __forceinline__ void put_row(uint8_t* row, int r, uint4 c0, uint4 c1, uint32_t sb) {
+    const uint32_t dw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    // The four E4M3 scales as fp16 (exact: E4M3's range and precision sit inside fp16's),
+    // converted at unit scale two a call.
+    const f16x2 s01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb, 1.0f, false);
+    const f16x2 s23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb, 1.0f, true);
+    const _Float16 scales[4] = {s01[0], s01[1], s23[0], s23[1]};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const f16x2 s2 = {scales[b], scales[b]};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int c = 2 * b + h;
+            const f16x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw[c], 1.0f, 0) * s2;
+            const f16x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw[c], 1.0f, 1) * s2;
+            const f16x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw[c], 1.0f, 2) * s2;
+            const f16x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw[c], 1.0f, 3) * s2;
+            *reinterpret_cast<uint4*>(row + 16 * swz(r, c)) =
+                make_uint4(__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                           __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3));
+        }
+    }
+}
+
+__device__ __forceinline__ f16x8 as_half8(const i32x8& v, int h) {
+    return __builtin_bit_cast(f16x8, half_of(v, h));
+}
+
+// One 256x256 output tile per workgroup. c (f32 [N]) and bias may be null.
+template <bool kOutHalf>
+__global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ As, const uint8_t* __restrict__ W,
+    const uint8_t* __restrict__ Ws, const float* __restrict__ gx, const float* __restrict__ gw,
+    const float* __restrict__ cs, const uint16_t* __restrict__ la, const uint16_t* __restrict__ up,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K, int R,
+    int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
+    const int2 t = launch_tile(blockIdx.x, tiles_m, tiles_n);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = __builtin_amdgcn_readfirstlane(t.x * kTile);
+    const int n0 = __builtin_amdgcn_readfirstlane(t.y * kTile);
+
+    auto rows_view = [&](const void* base, int rows_left, int row_bytes) {
+        const int64_t span = static_cast<int64_t>(rows_left) * row_bytes;
+        const uint32_t bytes = span > 0x7fffffff ? 0x7fffffffu : static_cast<uint32_t>(span);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+    };
+    const int half_k = K / 2, blocks_k = K / 16;
+    const auto ar = rows_view(A + static_cast<int64_t>(m0) * half_k, M - m0, half_k);
+    const auto asr = rows_view(As + static_cast<int64_t>(m0) * blocks_k, M - m0, blocks_k);
+    const auto wr = rows_view(W + static_cast<int64_t>(n0) * half_k, N - n0, half_k);
+    const auto wsr = rows_view(Ws + static_cast<int64_t>(n0) * blocks_k, N - n0, blocks_k);
+    const int np = K / 64;  // buffers: 64 elements of K each
+
+    // The epilogue's column operands into LDS ahead of the K loop: c (f32) and the bias (two a
+    // lane), for the tile's 256 columns; past N they read as zeros.
+    {
+        const int cc = 64 * wave + lane;
+        if (cs != nullptr) {
+            const auto cr = rows_view(cs + n0, N - n0, 4);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(cr, (LdsPtr*)(lds + kWsOff + 256 * wave), 4, 4 * cc, 0, 0, 0);
+        }
+        if (bias != nullptr && wave < 2) {
+            const auto br = rows_view(bias + n0, N - n0, 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (LdsPtr*)(lds + kBiasOff + 256 * wave), 4, 4 * cc, 0, 0, 0);
+        }
+    }
+
+    // Staging: thread t carries tile row t of A and of W for one buffer.
+    const uint32_t crow = static_cast<uint32_t>(tid * half_k), srow = static_cast<uint32_t>(tid * blocks_k);
+    uint4 xa0, xa1, wa0, wa1;
+    uint32_t xsb, wsb;
+    auto load = [&](int pair) {
+        const uint32_t co = crow + 32 * pair, so = srow + 4 * pair;
+        xa0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, co, 0, 0));
+        xa1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, co + 16, 0, 0));
+        wa0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, co, 0, 0));
+        wa1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, co + 16, 0, 0));
+        xsb = __builtin_amdgcn_raw_buffer_load_b32(asr, so, 0, 0);
+        wsb = __builtin_amdgcn_raw_buffer_load_b32(wsr, so, 0, 0);
+    };
+    auto store = [&](int pair) {
+        uint8_t* buf = lds + (pair & 1) * kPairBytes;
+        put_row(buf + tid * kPairK, tid, xa0, xa1, xsb);
+        put_row(buf + kOpBytes + tid * kPairK, tid, wa0, wa1, wsb);
+    };
+
+    // Fragment reads as gemm_tile.h's int8 kind: lane l supplies row l%32; lane group l/32 its
+    // K chunks; step e of a buffer reads logical chunks 4e + 2h + l/32 (h = 0, 1), each 8 fp16
+    // elements, one f16 MFMA's K half.
+    const int fr = lane & 31, fq = lane >> 5;
+    int aoff[2][2][4], boff[2][2][4];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rw = wn * 128 + i * 32 + fr, rx = wm * 128 + i * 32 + fr;
+                aoff[e][h][i] = kOpBytes + rw * kPairK + 16 * swz(rw, 4 * e + 2 * h + fq);
+                boff[e][h][i] = rx * kPairK + 16 * swz(rx, 4 * e + 2 * h + fq);
+            }
+    auto fetch = [&](int step, Frags& f) {
+        const uint8_t* buf = lds + ((step >> 1) & 1) * kPairBytes;
+        const int e = step & 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const i32x4 alo = *reinterpret_cast<const i32x4*>(buf + aoff[e][0][i]);
+            const i32x4 ahi = *reinterpret_cast<const i32x4*>(buf + aoff[e][1][i]);
+            const i32x4 blo = *reinterpret_cast<const i32x4*>(buf + boff[e][0][i]);
+            const i32x4 bhi = *reinterpret_cast<const i32x4*>(buf + boff[e][1][i]);
+            f.a[i] = __builtin_shufflevector(alo, ahi, 0, 1, 2, 3, 4, 5, 6, 7);
+            f.b[i] = __builtin_shufflevector(blo, bhi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    auto mfmas = [&](const Frags& c) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_half8(c.a[i], h), as_half8(c.b[j], h), acc[i][j], 0, 0, 0);
+    };
+    auto schedule = [&]() {
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
+        }
+    };
+
+    // Buffers 0 and 1 take pairs 0 and 1 before the loop. Pair p + 2's loads are issued at the
+    // top of step 2p + 1 (after the barrier past which no wave reads pair p's buffer), decoded
+    // and written in step 2p + 2, and seen complete at the barrier of step 2p + 3.
+    load(0);
+    fence();
+    wait_vmcnt<0>();
+    fence();
+    store(0);
+    if (np > 1) {
+        load(1);
+        fence();
+        wait_vmcnt<0>();
+        fence();
+        store(1);
+    }
+    fence();
+    wait_vmcnt<0>();
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    fence();
+
+    Frags f0, f1;
+    fetch(0, f0);
+    for (int s = 0; s < 2 * np; s += 2) {
+        const int p = s >> 1;
+        fetch(s + 1, f1);
+        mfmas(f0);
+        schedule();
+        if (p >= 1 && p + 1 < np) {
+            fence();
+            wait_vmcnt<0>();
+            fence();
+            store(p + 1);
+        }
+        fence();
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier();
+        fence();
+        if (p + 2 < np) load(p + 2);
+        fetch(s + 2, f0);  // past the last step: unused registers
+        mfmas(f1);
+        schedule();
+    }
+
+    // Epilogue. Block (i, j): lane holds out[m][n] for m = j-block row l%32 and, per register
+    // r, n = i-block column 8·(r/4) + 4·(l/32) + r%4.
+    fence();
+    wait_vmcnt<0>();
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    fence();
+    const float gxw = __fmul_rn(gx[0], gw[0]);
+    const int nl = wn * 128 + 4 * fq;  // the lane's first column within the tile
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int c = nl + i * 32 + 8 * g;
+            float4 f = make_float4(gxw, gxw, gxw, gxw);
+            if (cs != nullptr) {
+                const float4 cv = *reinterpret_cast<const float4*>(lds + kWsOff + 4 * c);
+                f = make_float4(__fmul_rn(gxw, cv.x), __fmul_rn(gxw, cv.y), __fmul_rn(gxw, cv.z), __fmul_rn(gxw, cv.w));
+            }
+            const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[i][j][4 * g + r] = __fmul_rn(acc[i][j][4 * g + r], fv[r]);
+        }
+
+    // The low-rank term into the same accumulators: A = up rows (the tile's columns), B = la
+    // rows, 16 ranks a call.
+    {
+        const auto upr = rows_view(up + static_cast<int64_t>(n0) * R, N - n0, 2 * R);
+        const auto lar = rows_view(la + static_cast<int64_t>(m0) * R, padded_rows(M) - m0, 2 * R);
+        for (int kk = 0; kk < R; kk += 16) {
+            bf16x8 ua[4], lb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ou = static_cast<uint32_t>(2 * ((wn * 128 + i * 32 + fr) * R + kk + 8 * fq));
+                const uint32_t ol = static_cast<uint32_t>(2 * ((wm * 128 + i * 32 + fr) * R + kk + 8 * fq));
+                ua[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(upr, ou, 0, 0));
+                lb[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(lar, ol, 0, 0));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ua[i], lb[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    uint2 bv[4][4];
+    const bool has_bias = bias != nullptr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            bv[i][g] = has_bias ? *reinterpret_cast<const uint2*>(lds + kBiasOff + 2 * (nl + i * 32 + 8 * g))
+                                : make_uint2(0, 0);
+    // Block row j at a time: computed and staged, then stored as whole rows.
+    uint8_t* stage = lds + wave * kStageBytes;
+    const int cl = (lane & 15) * 8;  // first of the lane's 8 columns in a stored row
+    const int n = n0 + wn * 128 + cl;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ml = j * 32 + fr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * g + r];
+                if (has_bias) {
+                    v[0] = __fadd_rn(v[0], low_of<kOutHalf>(bv[i][g].x));
+                    v[1] = __fadd_rn(v[1], high_of<kOutHalf>(bv[i][g].x));
+                    v[2] = __fadd_rn(v[2], low_of<kOutHalf>(bv[i][g].y));
+                    v[3] = __fadd_rn(v[3], high_of<kOutHalf>(bv[i][g].y));
+                }
+                const int col = i * 32 + 8 * g + 4 * fq;
+                *reinterpret_cast<uint2*>(stage + ml * kStageRow + 2 * col) =
+                    make_uint2(round2<kOutHalf>(v[0], v[1]), round2<kOutHalf>(v[2], v[3]));
+            }
+        wait_lgkmcnt0();  // a wave reads back only its own rows
+#pragma unroll
+        for (int r0 = 0; r0 < 32; r0 += 4) {
+            const int rl = j * 32 + r0 + (lane >> 4);
+            const int m = m0 + wm * 128 + rl;
+            const uint4 v = *reinterpret_cast<const uint4*>(stage + rl * kStageRow + 2 * cl);
+            if (m < M && n < N) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * N + n) = v;
+        }
+    }
+}
+
+}  // namespace
+
+int svdq_nvfp4_padded_rows(int M) { return padded_rows(M); }
+
+hipError_t svdq_nvfp4_input_scale(const void* x, bool x_half, const float* p, int M, int K,
+                                  float* g, hipStream_t s) {
+    uint32_t* word = reinterpret_cast<uint32_t*>(g);
+    input_scale_init<<<1, 1, 0, s>>>(word);
+    const int64_t chunks = static_cast<int64_t>(M) * (K / 8);
+    if (chunks == 0) return hipGetLastError();
+    const int64_t want = (chunks + 255) / 256;
+    const int blocks = static_cast<int>(want < 2048 ? want : 2048);
+    if (x_half)
+        input_scale_kernel<true><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), p, chunks, K / 8, word);
+    else
+        input_scale_kernel<false><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), p, chunks, K / 8, word);
+    return hipGetLastError();
+}
+
+hipError_t svdq_nvfp4_quantize(const void* x, bool x_half, const float* p, const float* g,
+                               const void* down, uint8_t* act, uint8_t* ascales, void* la, int M,
+                               int K, int R, hipStream_t s) {
+    if (M == 0) return hipSuccess;
+#define COZYQ_RANK(RR)                                                                          \
+    if (R == RR)                                                                                \
+        return x_half ? launch_quantize<true, RR>(x, p, g, down, act, ascales, la, M, K, s)     \
+                      : launch_quantize<false, RR>(x, p, g, down, act, ascales, la, M, K, s);
+    COZYQ_RANK(32)
+    COZYQ_RANK(64)
+    COZYQ_RANK(128)
+#undef COZYQ_RANK
+    return hipErrorInvalidValue;
+}
+
+hipError_t svdq_nvfp4_gemm(const uint8_t* act, const uint8_t* ascales, const uint8_t* w,
+                           const uint8_t* wscales, const float* gx, const float* gw,
+                           const float* c, const void* la, const void* up, const void* bias,
+                           void* out, bool out_half, int M, int N, int K, int R, hipStream_t s) {
+    const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTile - 1) / kTile;
+    auto go = [&](auto kernel) {
+        kernel<<<tiles_m * tiles_n, kThreads, 0, s>>>(
+            act, ascales, w, wscales, gx, gw, c, static_cast<const uint16_t*>(la),
+            static_cast<const uint16_t*>(up), static_cast<const uint16_t*>(bias),
+            static_cast<uint16_t*>(out), M, N, K, R, tiles_m, tiles_n);
+        return hipGetLastError();
+    };
+    return out_half ? go(nvfp4_gemm_kernel<true>) : go(nvfp4_gemm_kernel<false>);
+}
+
+}  // namespace cozyq

@@ -199,6 +199,42 @@ int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales
                          const void* up, const void* bias, void* out, int out_half, int M, int N,
                          int K, int R, void* stream);
 
+/* The rows svdq.nvfp4's activation operand is padded to, Rows(M) = M rounded up to 256
+ * (reference: svdq.h:12-13 `kRows`, svdq_linear.py:48 NATIVE_ROWS); -1 for M < 0. */
+int cozyq_svdq_rows(int M);
+
+/* svdq.nvfp4's activation second level (reference: internal/svdq_linear.py:582-590
+ * `activation_scale`, which takes it with torch ops): g[0] = max(max_{m,k} |x[m,k]|·p[k] / 2688,
+ * 1e-30), float32, each product rounded, as the law's max over rows then columns. x [M, K]
+ * 16-bit (x_half: fp16, else bf16), p [K] f32; both 16-byte aligned, K % 64 == 0. */
+int cozyq_svdq_input_scale(int device, const void* x, int x_half, const float* p, int M, int K,
+                           float* g, void* stream);
+
+/* svdq.nvfp4 activation side (reference: gemm.cpp:169-178 `svdq_quantize`, svdq.h:27-33; law
+ * internal/svdq_linear.py:592-618): xs = bf16(x·p); per 16-block of each row the E4M3 scale
+ * e4m3(clamp(amax|xs| / (6·g[0]), 2^-9, 448)) and each element's E2M1 code (nearest, ties to the
+ * even code, of |xs / (scale·g[0])|; sign in bit 3), two a byte with element 2k low. Layouts are
+ * this build's (the reference's are its GEMM's fragment tiles; the sizes are the same):
+ * act [Rows(M), K/2] and ascales [Rows(M), K/16] row-major, la = bf16(x·downᵀ) [Rows(M), R],
+ * down [R, K] bf16 (cast to x's dtype for fp16 x); rows past M are zeros. K % 64 == 0,
+ * R in {32, 64, 128}; every pointer 16-byte aligned. */
+int cozyq_svdq_quantize(int device, const void* x, int x_half, const float* p, const float* g,
+                        const void* down, void* act, void* ascales, void* la, int M, int K, int R,
+                        void* stream);
+
+/* svdq.nvfp4 GEMM (reference: gemm.cpp:180-190 `svdq_gemm`, svdq.h:35-42, svdq.cu:257-485):
+ *   out[m, n] = (A·Wᵀ)[m, n]·gx[0]·gw[0]·c[n] + (la·upᵀ)[m, n] + bias[n], rounded once,
+ * A from cozyq_svdq_quantize's act/ascales, W the stored nvfp4 weight: codes w [N, K/2] (element
+ * 2k low) and E4M3 scales wscales [N, K/16], both row-major as stored (no retiling). Each element
+ * is decoded exactly to fp16 and the products are summed in float32; the low-rank term enters the
+ * same accumulators. up [N, R] bf16; c (f32 [N]) and bias (out's dtype) may be NULL. out [M, N]
+ * bf16, or fp16 with out_half. M >= 1, N % 8 == 0, K % 64 == 0, R in {32, 64, 128}; every
+ * pointer 16-byte aligned. */
+int cozyq_svdq_gemm(int device, const void* act, const void* ascales, const void* w,
+                    const void* wscales, const float* gx, const float* gw, const float* c,
+                    const void* la, const void* up, const void* bias, void* out, int out_half,
+                    int M, int N, int K, int R, void* stream);
+
 /* Stored-format decode into a float destination (reference: the `decoded_float` providers of
  * internal/encoding/formats.py — TensorwiseDequant :438-488, RowwiseDequant :507-569,
  * MicroScaledDequant :588-650, Nvfp4Dequant :762-868 — and the nvfp4 decode core with its

@@ -33,6 +33,14 @@ Pins, exercised in `tests/test_oracle.py`:
   power-of-two smoothing, one-hot and integer-valued down projections (against numpy int64),
   the fp16 cast of `down` for fp16 x, and activations/weights placed on the int4 grid so that
   the product equals numpy's matmul of the dequantized operands, group by group.
+- `svdq_nvfp4_quantize` (svdq.nvfp4's activation law): its E2M1 threshold count against
+  brute-force nearest-E2M1 with ties to the even code over a dense sweep and every midpoint with
+  its float32 neighbours, both signs (-0 keeps code 0); the block scale against the independent
+  bit encoder, the 2^-9 floor of an all-zero block and the 448 saturation; the decode round trip
+  within half an E2M1 step. `svdq_nvfp4_input_scale`: element-by-element numpy float32 brute
+  force, the zero floor and a stored scale. `svdq_nvfp4_exact`: on-grid activations (lossless
+  quantization) against the golden-pinned `decode_nvfp4` weight, c, a one-hot low-rank branch
+  and the bias.
 """
 
 from __future__ import annotations
@@ -497,6 +505,101 @@ def svdq_linear(
     if bias is not None:
         out = out + bias.float()
     return out.to(out_dtype)
+
+
+# ------------------------------------------------------------ W4A4 svdq.nvfp4 SVDQuant
+
+#: svdq.nvfp4's second-level bound (E4M3 max · E2M1 max), the block-scale floor (E4M3's least
+#: subnormal) and the activation scale's floor (`internal/svdq_linear.py:44-47`, `:590`).
+SVDQ_LEVELS_MAX = 448.0 * 6.0
+SVDQ_BLOCK_FLOOR = 2.0**-9
+SVDQ_INPUT_FLOOR = 1e-30
+#: The E2M1 thresholds of `quantize` (`internal/svdq_linear.py:613-616`): (bound, inclusive).
+SVDQ_THRESHOLDS = ((0.25, False), (0.75, True), (1.25, False), (1.75, True), (2.5, False),
+                   (3.5, True), (5.0, False))  # fmt: skip
+
+
+def svdq_nvfp4_input_scale(x: torch.Tensor, p: torch.Tensor,
+                           stored: torch.Tensor | None = None) -> torch.Tensor:
+    """`activation_scale` (`internal/svdq_linear.py:582-590`): the stored `input_scale`, else
+    `max_j(max_i |x_ij| · p_j) / 2688` in float32, floored at 1e-30. Returns float32 [1]."""
+    if stored is not None:
+        return stored.float().reshape(1)
+    flat = x.reshape(-1, int(p.numel()))
+    amax = (flat.abs().amax(0).float() * p.float()).amax()
+    return (amax / SVDQ_LEVELS_MAX).clamp(min=SVDQ_INPUT_FLOOR).reshape(1)
+
+
+def svdq_nvfp4_quantize(xs: torch.Tensor, g: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """`quantize` (`internal/svdq_linear.py:605-618`): `xs` float32 [M, K] (already bf16(x·p))
+    at second level g → E2M1 codes [M, K] (u8, sign in bit 3) and E4M3 scales [M, K/16]:
+    scale = e4m3(clamp(amax / (6g), 2^-9, 448)), code = the threshold count of |xs/(scale·g)|
+    (+8 where xs < 0)."""
+    rows, cols = int(xs.shape[0]), int(xs.shape[1])
+    blocks = xs.float().view(rows, cols // NVFP4_BLOCK, NVFP4_BLOCK)
+    gv = g.float().reshape(())
+    amax = blocks.abs().amax(-1)
+    scale = (amax / (6.0 * gv)).clamp(SVDQ_BLOCK_FLOOR, E4M3_MAX).to(torch.float8_e4m3fn)
+    a = (blocks / (scale.float() * gv).unsqueeze(-1)).abs()
+    code = torch.zeros_like(blocks, dtype=torch.uint8)
+    for bound, inclusive in SVDQ_THRESHOLDS:
+        code = code + ((a >= bound) if inclusive else (a > bound)).to(torch.uint8)
+    code = code + (blocks < 0).to(torch.uint8) * 8
+    return code.view(rows, cols), scale
+
+
+def svdq_nvfp4_pack(codes: torch.Tensor) -> torch.Tensor:
+    """E2M1 codes [M, K] → bytes [M, K/2], element 2k in the low nibble (the stored order the
+    kernels read, `internal/svdq_linear.py:520`)."""
+    return (codes[:, 0::2] | (codes[:, 1::2] << 4)).contiguous()
+
+
+def svdq_nvfp4_values(codes: torch.Tensor, scales: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """`_values` (`internal/svdq_linear.py:627-632`): codes [R, C] (u8) with E4M3 scales [R, C/16]
+    → float32 `(E2M1 · scale) · g`."""
+    lut = torch.tensor(E2M1_VALUES, dtype=torch.float32)
+    blocks = lut[codes.long()].view(codes.shape[0], -1, NVFP4_BLOCK)
+    return (blocks * scales.float().unsqueeze(-1) * g.float().reshape(())).view(codes.shape)
+
+
+def _svdq_weight_values(roles: dict) -> torch.Tensor:
+    packed = roles["weight"].view(torch.uint8)
+    codes = torch.stack((packed & 0x0F, packed >> 4), dim=-1).view(packed.shape[0], -1)
+    return svdq_nvfp4_values(codes, roles["scale"], roles["scale_2"])
+
+
+def svdq_nvfp4_exact(x: torch.Tensor, roles: dict, bias: torch.Tensor | None) -> torch.Tensor:
+    """The svdq.nvfp4 linear in float64 from the law's codes (`internal/svdq_linear.py:427-438`,
+    the reference's own probe target): `(values(q(x·p)) · values(W)ᵀ) · c + bf16(x·downᵀ) · upᵀ
+    + bias`, every product and sum exact."""
+    p = roles["pre_quant_scale"]
+    g = svdq_nvfp4_input_scale(x, p, roles.get("input_scale"))
+    codes, scales = svdq_nvfp4_quantize(svdq_smooth(x, p), g)
+    out = svdq_nvfp4_values(codes, scales, g).double() @ _svdq_weight_values(roles).double().t()
+    if roles.get("channel_scale") is not None:
+        out = out * roles["channel_scale"].double().reshape(1, -1)
+    out = out + svdq_down(x, roles["lowrank_down"]).double() @ roles["lowrank_up"].double().t()
+    return out if bias is None else out + bias.double()
+
+
+def svdq_nvfp4_eager(x: torch.Tensor, roles: dict, bias: torch.Tensor | None,
+                     out_dtype: torch.dtype) -> torch.Tensor:
+    """`eager` (`internal/svdq_linear.py:639-659`), the CPU path timed as the svdq.nvfp4
+    baseline: the activation fake-quantized, float32 matmul against the decoded weight, `· c`,
+    `+` the low-rank branch and the bias in float32, one cast."""
+    p = roles["pre_quant_scale"]
+    flat = x.reshape(-1, int(p.numel()))
+    g = svdq_nvfp4_input_scale(flat, p, roles.get("input_scale"))
+    codes, scales = svdq_nvfp4_quantize(svdq_smooth(flat, p), g)
+    y = svdq_nvfp4_values(codes, scales, g) @ _svdq_weight_values(roles).t()
+    if roles.get("channel_scale") is not None:
+        y = y * roles["channel_scale"].float()
+    half = flat.dtype if flat.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
+    down = (flat.to(half) @ roles["lowrank_down"].to(half).t()).to(torch.bfloat16)
+    y = y + down.float() @ roles["lowrank_up"].float().t()
+    if bias is not None:
+        y = y + bias.float()
+    return y.to(out_dtype)
 
 
 # ------------------------------------------------------------------------ decode laws

@@ -80,7 +80,7 @@ def test_svdq_quantize_bit_exact(ops, shape, dtype, rank):
     m, k = shape
     x = activations(m, k, 31 + m, dtype)
     p, down, _, _, _ = operands(8, k, rank, 32 + k)
-    act, ascales, la = ops.svdq_quantize(x.to(DEV), p.to(DEV), down.to(DEV))
+    act, ascales, la = ops.svdq_int4_quantize(x.to(DEV), p.to(DEV), down.to(DEV))
     torch.cuda.synchronize()
     q, s = laws.int4_quantize(laws.svdq_smooth(x, p))
     assert torch.equal(act.cpu(), laws.pack_int4(q))
@@ -97,7 +97,7 @@ def test_svdq_quantize_edge_groups(ops):
     x[1, 0:64] = 1.0e6
     x[2, 128:192] = (torch.randn(64) * 1e-6).to(torch.bfloat16)
     p, down, _, _, _ = operands(8, k, 16, 42)
-    act, ascales, la = ops.svdq_quantize(x.to(DEV), p.to(DEV), down.to(DEV))
+    act, ascales, la = ops.svdq_int4_quantize(x.to(DEV), p.to(DEV), down.to(DEV))
     torch.cuda.synchronize()
     q, s = laws.int4_quantize(laws.svdq_smooth(x, p))
     assert s[0, 1] == 0 and torch.isinf(s[1, 0]) and 0 < float(s[2, 2]) < 6.1e-5
@@ -116,7 +116,7 @@ def test_svdq_linear_within_tolerance(ops, shape, bias, out_dtype):
     x = activations(m, k, 51 + m)
     p, down, up, codes, scales = operands(n, k, r, 52 + n)
     b = (torch.randn(n, generator=_gen(53)) * 0.5).to(out_dtype) if bias else None
-    out = ops.svdq_linear(x.to(DEV), p.to(DEV), down.to(DEV), codes.to(DEV), scales.to(DEV),
+    out = ops.svdq_int4_linear(x.to(DEV), p.to(DEV), down.to(DEV), codes.to(DEV), scales.to(DEV),
                           up.to(DEV), None if b is None else b.to(DEV), out_dtype)  # fmt: skip
     torch.cuda.synchronize()
     assert out.dtype == out_dtype and out.shape == (m, n)
@@ -131,7 +131,7 @@ def test_svdq_gemm_on_oracle_operands(ops):
     p, down, up, codes, scales = operands(n, k, r, 62)
     q, s = laws.int4_quantize(laws.svdq_smooth(x, p))
     la = laws.svdq_down(x, down)
-    out = ops.svdq_gemm(laws.pack_int4(q).to(DEV), s.to(DEV), la.to(DEV), codes.to(DEV),
+    out = ops.svdq_int4_gemm(laws.pack_int4(q).to(DEV), s.to(DEV), la.to(DEV), codes.to(DEV),
                         scales.to(DEV), up.to(DEV), None, torch.bfloat16)  # fmt: skip
     torch.cuda.synchronize()
     assert_close(out, laws.svdq_exact(x, p, codes, scales, down, up, None))
@@ -145,8 +145,8 @@ def test_svdq_c4_full_size_sampled_rows(ops):
     p, down, up, codes, scales = operands(n, k, r, 20261206)
     bias = (torch.randn(n, generator=_gen(7)) * 0.5).to(torch.bfloat16)
     xd = x.to(DEV)
-    act, ascales, la = ops.svdq_quantize(xd, p.to(DEV), down.to(DEV))
-    out = ops.svdq_gemm(act, ascales, la, codes.to(DEV), scales.to(DEV), up.to(DEV), bias.to(DEV),
+    act, ascales, la = ops.svdq_int4_quantize(xd, p.to(DEV), down.to(DEV))
+    out = ops.svdq_int4_gemm(act, ascales, la, codes.to(DEV), scales.to(DEV), up.to(DEV), bias.to(DEV),
                         torch.bfloat16)  # fmt: skip
     torch.cuda.synchronize()
     q, s = laws.int4_quantize(laws.svdq_smooth(x, p))

@@ -1,0 +1,177 @@
+"""GPU parity of the svdq.nvfp4 W4A4 lane (`cozyq_svdq_input_scale`, `cozyq_svdq_quantize`,
+`cozyq_svdq_gemm`) against the CPU law (`oracle/laws.py`, restating
+`internal/svdq_linear.py:582-659`).
+
+Bar (the reference's own probe, `internal/svdq_linear.py:406-440`): g_x, the E2M1 codes and the
+E4M3 scales bit-exact; la = bf16(x·downᵀ) within one bf16 rounding of its float64 product; the
+output within |got − exact| ≤ ATOL·rms(exact) + RTOL·|exact| of the float64 law
+(`laws.svdq_nvfp4_exact`), and bit-exact where every product and partial sum is exact in float32.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import laws
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+ATOL, RTOL = 1e-2, 2e-2
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from cozyq import prebuilt
+
+    return prebuilt.library(0)
+
+
+def assert_close(got: torch.Tensor, exact: torch.Tensor) -> None:
+    got, exact = got.double().cpu(), exact.double().cpu()
+    rms = exact.pow(2).mean().sqrt().item()
+    err = (got - exact).abs()
+    worst = (err - (ATOL * rms + RTOL * exact.abs())).max().item()
+    assert worst <= 0, f"max excess {worst:.3g} (rms {rms:.3g}, max err {err.max().item():.3g})"
+
+
+def activations(m: int, k: int, seed: int, dtype=torch.bfloat16) -> torch.Tensor:
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=gen)
+    x[:, torch.randperm(k, generator=gen)[: max(1, k // 100)]] *= 20
+    return x.to(dtype)
+
+
+def roles(n: int, k: int, r: int, seed: int, channel: bool = True, stored: bool = False) -> dict:
+    """A random svdq.nvfp4 leaf as the reference's probe draws one
+    (`internal/svdq_linear.py:406-418`)."""
+    gen = torch.Generator().manual_seed(seed)
+    out = {
+        "weight": torch.randint(0, 256, (n, k // 2), generator=gen).to(torch.uint8),
+        "scale": (torch.randn(n, k // 16, generator=gen).abs() + 0.5).to(torch.float8_e4m3fn),
+        "scale_2": torch.full((1,), 0.01),
+        "pre_quant_scale": torch.randn(k, generator=gen).abs() + 0.5,
+        "lowrank_down": (torch.randn(r, k, generator=gen) * 0.05).to(torch.bfloat16),
+        "lowrank_up": (torch.randn(n, r, generator=gen) * 0.05).to(torch.bfloat16),
+    }
+    if channel:
+        out["channel_scale"] = torch.randn(n, generator=gen).abs() + 0.5
+    if stored:
+        out["input_scale"] = torch.tensor([0.05])
+    return out
+
+
+def on(d: dict) -> dict:
+    return {key: t.to(DEV) for key, t in d.items()}
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("shape", [(1, 64), (300, 3072), (2, 4160), (4096, 3072)],
+                         ids=lambda s: "x".join(map(str, s)))  # fmt: skip
+def test_svdq_input_scale_bit_exact(ops, shape, dtype):
+    m, k = shape
+    x = activations(m, k, seed=m + k, dtype=dtype)
+    p = torch.randn(k, generator=torch.Generator().manual_seed(k)).abs() + 0.5
+    got = ops.svdq_input_scale(x.to(DEV), p.to(DEV))
+    want = laws.svdq_nvfp4_input_scale(x, p)
+    assert torch.equal(got.cpu().view(torch.int32), want.view(torch.int32))
+    zero = ops.svdq_input_scale(torch.zeros(m, k, dtype=dtype, device=DEV), p.to(DEV))
+    assert zero.item() == torch.tensor(1e-30).item()  # the law's floor
+
+
+@pytest.mark.parametrize("rank", [32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("shape", [(1, 64), (17, 128), (300, 1024), (257, 3072)],
+                         ids=lambda s: "x".join(map(str, s)))  # fmt: skip
+def test_svdq_quantize_bit_exact(ops, shape, dtype, rank):
+    """Codes and scales bit for bit (every row's blocks, the scale floor of an all-zero row, the
+    sign of -0), rows past M zero, la within one bf16 rounding of its float64 product."""
+    m, k = shape
+    x = activations(m, k, seed=3 * m + k, dtype=dtype)
+    x[m // 2] = 0
+    if m > 2:
+        x[1, :16] = -0.0
+    d = roles(264, k, rank, seed=k)
+    g = laws.svdq_nvfp4_input_scale(x, d["pre_quant_scale"])
+    act, ascales, la = ops.svdq_quantize(x.to(DEV), d["pre_quant_scale"].to(DEV), g.to(DEV),
+                                         d["lowrank_down"].to(DEV))  # fmt: skip
+    padded = -(-m // 256) * 256
+    assert act.shape == (padded, k // 2) and ascales.shape == (padded, k // 16) and la.shape == (padded, rank)
+    codes, scales = laws.svdq_nvfp4_quantize(laws.svdq_smooth(x, d["pre_quant_scale"]), g)
+    assert torch.equal(act[:m].cpu(), laws.svdq_nvfp4_pack(codes))
+    assert torch.equal(ascales[:m].cpu().view(torch.uint8), scales.view(torch.uint8))
+    assert not act[m:].any() and not ascales[m:].view(torch.uint8).any() and not la[m:].view(torch.int16).any()
+    # One bf16 rounding of the float64 product, plus float32 accumulation over K (2^-18 of the
+    # sum of |terms|: where the terms cancel, float32 itself is off by more than a bf16 step).
+    down = d["lowrank_down"].to(dtype).double()
+    exact = x.double() @ down.t()
+    spread = x.double().abs() @ down.abs().t()
+    err = (la[:m].cpu().double() - exact).abs()
+    assert (err <= exact.abs() * 2.0**-8 + spread * 2.0**-18).all(), err.max()
+
+
+@pytest.mark.parametrize("shape", [(300, 264, 256), (1, 520, 64), (513, 256, 192)],
+                         ids=lambda s: "x".join(map(str, s)))  # fmt: skip
+def test_svdq_gemm_bit_exact_where_exact(ops, shape):
+    """Random codes on both sides with E4M3 scales in [1, 2), unit second levels, no c, a zero
+    low-rank branch: every product and partial sum is exact in float32 (at most 23 significant
+    bits), so the output is the float64 law's, cast once, bit for bit — the fp16 decode of each
+    E2M1 code and scale and the MFMA layout, checked exactly."""
+    m, n, k = shape
+    gen = torch.Generator().manual_seed(m + n + k)
+    acodes = torch.randint(0, 16, (m, k), generator=gen).to(torch.uint8)
+    wcodes = torch.randint(0, 16, (n, k), generator=gen).to(torch.uint8)
+    ascl = torch.randint(0x38, 0x40, (m, k // 16), generator=gen).to(torch.uint8).view(torch.float8_e4m3fn)
+    wscl = torch.randint(0x38, 0x40, (n, k // 16), generator=gen).to(torch.uint8).view(torch.float8_e4m3fn)
+    padded = -(-m // 256) * 256
+    act = torch.zeros(padded, k // 2, dtype=torch.uint8)
+    act[:m] = laws.svdq_nvfp4_pack(acodes)
+    asc = torch.zeros(padded, k // 16, dtype=torch.uint8)
+    asc[:m] = ascl.view(torch.uint8)
+    one = torch.ones(1)
+    la = torch.zeros(padded, 32, dtype=torch.bfloat16)
+    up = torch.zeros(n, 32, dtype=torch.bfloat16)
+    exact = laws.svdq_nvfp4_values(acodes, ascl, one).double() @ \
+        laws.svdq_nvfp4_values(wcodes, wscl, one).double().t()  # fmt: skip
+    for dtype in (torch.bfloat16, torch.float16):
+        got = ops.svdq_gemm(act.to(DEV), asc.view(torch.float8_e4m3fn).to(DEV), la.to(DEV), m,
+                            one.to(DEV), laws.svdq_nvfp4_pack(wcodes).to(DEV), wscl.to(DEV),
+                            one.to(DEV), up.to(DEV), None, None, dtype)  # fmt: skip
+        assert torch.equal(got.cpu(), exact.float().to(dtype))
+
+
+CASES = [(1, 256, 64, 32), (100, 520, 1024, 64), (300, 1032, 2048, 128), (513, 264, 3072, 32),
+         (64, 3072, 3072, 32)]
+
+
+@pytest.mark.parametrize("variant", ["plain", "channel+bias", "stored"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c)))
+def test_svdq_linear_within_tolerance(ops, case, dtype, variant):
+    m, n, k, r = case
+    d = roles(n, k, r, seed=n + k, channel=variant == "channel+bias", stored=variant == "stored")
+    x = activations(m, k, seed=m + r, dtype=dtype)
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(9)) * 0.1).to(dtype) \
+        if variant == "channel+bias" else None  # fmt: skip
+    got = ops.svdq_linear(x.to(DEV), on(d), None if b is None else b.to(DEV), dtype)
+    assert got.shape == (m, n) and got.dtype == dtype
+    assert_close(got, laws.svdq_nvfp4_exact(x, d, b))
+
+
+def test_c4_shape_svdq_nvfp4(ops):
+    """BASELINE config 4's shape (M=4096, K=N=3072, rank 32) on the nvfp4 law: operand bit-exact,
+    output within tolerance of the float64 law."""
+    m, n, k, r = 4096, 3072, 3072, 32
+    d = roles(n, k, r, seed=20261202)
+    x = activations(m, k, seed=20261203)
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(4)) * 0.1).to(torch.bfloat16)
+    dd = on(d)
+    g = ops.svdq_input_scale(x.to(DEV), dd["pre_quant_scale"])
+    act, ascales, _ = ops.svdq_quantize(x.to(DEV), dd["pre_quant_scale"], g, dd["lowrank_down"])
+    want_g = laws.svdq_nvfp4_input_scale(x, d["pre_quant_scale"])
+    assert torch.equal(g.cpu().view(torch.int32), want_g.view(torch.int32))
+    codes, scales = laws.svdq_nvfp4_quantize(laws.svdq_smooth(x, d["pre_quant_scale"]), want_g)
+    assert torch.equal(act.cpu(), laws.svdq_nvfp4_pack(codes))
+    assert torch.equal(ascales.cpu().view(torch.uint8), scales.view(torch.uint8))
+    got = ops.svdq_linear(x.to(DEV), dd, b.to(DEV), torch.bfloat16)
+    assert_close(got, laws.svdq_nvfp4_exact(x, d, b))

@@ -590,6 +590,134 @@ def test_svdq_weight_reconstructs_effective_weight():
     assert np.allclose((deq * p.double() + up.double() @ down.double()).numpy(), w.numpy(), rtol=0, atol=1e-12)
 
 
+# ------------------------------------------------------------------ svdq.nvfp4 (W4A4)
+
+_E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def _nearest_even_e2m1(a: np.ndarray) -> np.ndarray:
+    """Brute force: the index of the nearest E2M1 magnitude to each |a|, ties to the even index
+    (the even mantissa), past 6 the top."""
+    dist = np.abs(a[:, None] - _E2M1[None, :])
+    best = dist.min(axis=1, keepdims=True)
+    tied = dist == best
+    idx = np.where(tied.sum(axis=1) > 1, np.argmax(tied & (np.arange(8) % 2 == 0), axis=1), np.argmin(dist, axis=1))
+    return idx
+
+
+def _unit_blocks(values: np.ndarray) -> torch.Tensor:
+    """Blocks of 16 whose first element is 6 (amax 6 at g = 1: scale exactly 1), the other 15
+    the values under test: |xs / (scale·g)| is then each value itself."""
+    v = np.asarray(values, dtype=np.float32)
+    pad = (-len(v)) % 15
+    v = np.concatenate([v, np.zeros(pad, np.float32)]).reshape(-1, 15)
+    blocks = np.concatenate([np.full((v.shape[0], 1), 6.0, np.float32), v], axis=1)
+    return torch.from_numpy(blocks.reshape(1, -1))
+
+
+def test_svdq_nvfp4_code_is_nearest_even_e2m1():
+    """The threshold count of `svdq_nvfp4_quantize` against brute-force nearest-E2M1 with ties to
+    the even code, on a dense sweep plus every midpoint and its float32 neighbours, both signs; a
+    threshold with the wrong strictness fails at its midpoint."""
+    mids = (_E2M1[:-1] + _E2M1[1:]) / 2
+    near = np.concatenate([np.nextafter(mids.astype(np.float32), np.float32(0)), mids.astype(np.float32),
+                           np.nextafter(mids.astype(np.float32), np.float32(7))])  # fmt: skip
+    sweep = np.linspace(0, 6, 2401, dtype=np.float32)
+    vals = np.concatenate([sweep, near]).astype(np.float32)
+    xs = _unit_blocks(np.concatenate([vals, -vals]))
+    codes, scales = laws.svdq_nvfp4_quantize(xs, torch.ones(1))
+    assert (scales.float() == 1.0).all()
+    got = codes.reshape(-1, 16)[:, 1:].reshape(-1).numpy()[: 2 * len(vals)]
+    want = _nearest_even_e2m1(vals.astype(np.float64))
+    assert np.array_equal(got[: len(vals)], want)
+    neg = np.where(vals > 0, want + 8, want)  # -0 keeps code 0: the law's sign is xs < 0
+    assert np.array_equal(got[len(vals):], neg)
+
+
+def test_svdq_nvfp4_block_scale_and_saturation():
+    """The block scale is the E4M3 encoding (independent bit encoder) of amax / (6g) clamped to
+    [2^-9, 448]: all-zero blocks take the floor and code 0, a block past 448·6·g saturates its
+    scale at 448 and its top elements at code 7."""
+    gen = torch.Generator().manual_seed(21)
+    xs = torch.randn(37, 256, generator=gen) * torch.exp2(torch.randint(-12, 12, (37, 1), generator=gen).float())
+    xs[3] = 0
+    xs[5, :16] = 448 * 6 * 40.0
+    g = torch.tensor([0.0123])
+    codes, scales = laws.svdq_nvfp4_quantize(xs, g)
+    amax = xs.view(37, 16, 16).abs().amax(-1)
+    ratio = (amax / (6.0 * g)).clamp(2.0**-9, 448.0)
+    assert np.array_equal(scales.view(torch.uint8).numpy(), laws.e4m3_bits_numpy(ratio.numpy()))
+    assert (scales[3].float() == 2.0**-9).all() and (codes[3] == 0).all()
+    assert scales[5, 0].float() == 448.0 and (codes[5, :16] == 7).all()
+
+
+def test_svdq_nvfp4_round_trip_bound():
+    """Every element decodes to within half an E2M1 step (times scale·g) of xs, except past the
+    top of a saturated block; the decoded block max is within the last step of amax."""
+    gen = torch.Generator().manual_seed(22)
+    x = torch.randn(64, 512, generator=gen).to(torch.bfloat16)
+    p = torch.rand(512, generator=gen) + 0.5
+    xs = laws.svdq_smooth(x, p)
+    g = laws.svdq_nvfp4_input_scale(x, p)
+    codes, scales = laws.svdq_nvfp4_quantize(xs, g)
+    value = laws.svdq_nvfp4_values(codes, scales, g).double()
+    unit = (scales.double() * g.double()).repeat_interleave(16, dim=1)
+    a = (xs.double() / unit).abs()
+    step = torch.where(a < 2, 0.5, torch.where(a < 4, 1.0, 2.0))
+    assert ((value - xs.double()).abs() <= step / 2 * unit * (1 + 1e-6) + 1e-30).all()
+
+
+def test_svdq_nvfp4_input_scale_brute_force():
+    """g = fl(max over elements of fl(|x|·p)) / 2688, floored at 1e-30, element by element in
+    numpy float32; a zero input gives the floor; a stored input_scale is returned as given."""
+    gen = torch.Generator().manual_seed(23)
+    for dtype in (torch.bfloat16, torch.float16):
+        x = (torch.randn(9, 64, generator=gen) * 3).to(dtype)
+        p = torch.rand(64, generator=gen) + 0.25
+        xv, pv = x.float().numpy(), p.numpy()
+        best = np.float32(0)
+        for i in range(9):
+            for j in range(64):
+                best = max(best, np.float32(abs(xv[i, j])) * pv[j])
+        want = max(np.float32(best) / np.float32(2688.0), np.float32(1e-30))
+        got = laws.svdq_nvfp4_input_scale(x, p)
+        assert got.numpy().view(np.uint32)[0] == np.float32(want).view(np.uint32)
+    zero = laws.svdq_nvfp4_input_scale(torch.zeros(3, 64, dtype=torch.bfloat16), torch.ones(64))
+    assert zero.item() == np.float32(1e-30)
+    stored = torch.tensor(0.125)
+    assert laws.svdq_nvfp4_input_scale(x, p, stored).item() == 0.125
+
+
+def test_svdq_nvfp4_exact_on_the_grid_against_decode_law():
+    """Activations already on the nvfp4 grid (amax 6 per block, stored g = 1, unit smoothing):
+    quantization is lossless, and the W4A4 law equals x times the weight as the golden-pinned
+    decode law (`decode_nvfp4`) decodes it, times c, plus the low-rank branch and the bias."""
+    gen = torch.Generator().manual_seed(24)
+    m, n, k, r = 5, 24, 128, 32
+    codes = torch.randint(0, 16, (m, k), generator=gen).to(torch.uint8)
+    codes[:, ::16] = 7
+    codes[codes == 8] = 0  # -0 quantizes to code 0 (the law's sign is xs < 0)
+    x = torch.tensor(laws.E2M1_VALUES)[codes.long()].to(torch.bfloat16)
+    roles = {
+        "weight": torch.randint(0, 256, (n, k // 2), generator=gen).to(torch.uint8),
+        "scale": (torch.rand(n, k // 16, generator=gen) + 0.5).to(torch.float8_e4m3fn),
+        "scale_2": torch.tensor([0.25]),
+        "pre_quant_scale": torch.ones(k),
+        "input_scale": torch.tensor(1.0),
+        "channel_scale": torch.rand(n, generator=gen) + 0.5,
+        "lowrank_down": torch.eye(k)[torch.randperm(k, generator=gen)[:r]].to(torch.bfloat16),
+        "lowrank_up": (torch.randn(n, r, generator=gen) * 0.1).to(torch.bfloat16),
+    }
+    bias = torch.randn(n, generator=gen).to(torch.bfloat16)
+    got_codes, got_scales = laws.svdq_nvfp4_quantize(laws.svdq_smooth(x, roles["pre_quant_scale"]), torch.ones(1))
+    assert torch.equal(got_codes, codes) and (got_scales.float() == 1.0).all()
+    w = laws.decode_nvfp4(roles["weight"], roles["scale"], roles["scale_2"], "row_major", False, False, None,
+                          torch.float32).double()  # fmt: skip
+    la = x.double() @ roles["lowrank_down"].double().t()  # one-hot rows: columns of x, exact in bf16
+    want = (x.double() @ w.t()) * roles["channel_scale"].double() + la @ roles["lowrank_up"].double().t() + bias.double()
+    assert torch.equal(laws.svdq_nvfp4_exact(x, roles, bias), want)
+
+
 # ------------------------------------------------------------------- producer prologue
 
 
