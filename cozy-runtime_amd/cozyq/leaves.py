@@ -6,8 +6,8 @@ A provider (`LeafProvider`, `internal/encoding/formats.py:326-361`) turns one st
 parts into a leaf: an `nn.Module` standing where the replaced linear stood, whose weight is
 its role buffers and whose forward is one of the gfx950 ops. Names, schemes, role names,
 `BUFFERS`, `WRITES_INTO`, `operand`, `forward(x, *, prequantized=None, out=None)` and the
-autocast behaviour are the reference's; the device predicate names the gfx950 row, and the
-W4A4 provider serves this build's int4-g64 SVDQuant scheme in place of the reference's nvfp4.
+autocast behaviour are the reference's; the device predicate names the gfx950 row. The W4A4
+providers serve the reference's svdq.nvfp4 scheme and this build's int4-g64 SVDQuant variant.
 """
 
 from __future__ import annotations
@@ -16,7 +16,7 @@ from collections.abc import Callable, Mapping, Sequence
 from dataclasses import dataclass
 from typing import Any, ClassVar
 
-from cozyq import _dispatch, fp8_linear, int8_linear, layout, nvfp4_linear, prebuilt, w4a8_linear
+from cozyq import _dispatch, fp8_linear, int8_linear, layout, nvfp4_linear, prebuilt, svdq_linear, w4a8_linear
 from cozyq import decode as dec
 from cozyq.operands import INT8_CONVROT, ROWWISE_FP8, PreQuantized, read, shared_operand
 
@@ -27,6 +27,7 @@ Params = tuple[tuple[str, object], ...]
 MXFP8 = "cozy.mxfp8.native-leaf/2"
 W4A8 = "cozy.w4a8-convrot256.native-leaf/1"
 SVDQ_INT4 = "cozyq.svdq-int4g64.native-leaf/1"
+SVDQ = "cozy.svdq-nvfp4.native-leaf/1"
 NVFP4 = "cozy.nvfp4.native-leaf/1"
 #: The operand geometry each 8-bit leaf's GEMM reads (`internal/encoding/leaves.py:207`).
 OPERANDS = {INT8_CONVROT: INT8_CONVROT, ROWWISE_FP8: ROWWISE_FP8, W4A8: INT8_CONVROT}
@@ -179,6 +180,44 @@ class _SvdqLane(_Lane):
         return result
 
 
+class _SvdqNvfp4Lane(_Lane):
+    """The svdq.nvfp4 leaf (`internal/encoding/leaves.py:1205-1263`): the activation smoothed,
+    quantized and down-projected in one launch, then the GEMM with the up-projection, c and the
+    bias before its one rounding. A baked request's LoRAs (`adopt`) enter the branch as more ranks
+    while the ranks together fit the kernels' largest, else as their own term afterwards."""
+
+    adopts = True
+
+    def run(self, torch, leaf, x, prequantized, out):
+        if prequantized is not None or isinstance(x, PreQuantized):
+            raise ValueError("the svdq leaf quantizes its own input; it takes no shared operand")
+        dtype = _autocast_dtype(torch, x.device)
+        out_dtype = leaf.out_dtype if dtype is None else dtype
+        x = x if dtype is None else x.to(dtype)
+        roles = {role: read(t) for role, t in leaf.roles().items()}
+        deltas = leaf.lora() if leaf.lora is not None else []
+        apart = None
+        if deltas:
+            bound = [read(t) for d in deltas for t in d[1:3]]
+            key = (roles["lowrank_down"].data_ptr(), roles["lowrank_up"].data_ptr(),
+                   *((d[0], d[3]) for d in deltas), *(t.data_ptr() for t in bound))  # fmt: skip
+            cached = leaf._cozy_merged
+            if cached is None or cached[0] != key:
+                down = torch.cat(bound[0::2])
+                up = torch.cat([u * d[3] for u, d in zip(bound[1::2], deltas, strict=True)], dim=1)
+                cached = (key, svdq_linear.merged(torch, roles, down, up), (down, up))
+                leaf._cozy_merged = cached
+            if cached[1] is not None:
+                roles.update(cached[1])
+            else:
+                apart = cached[2]
+        y = svdq_linear.linear(torch, x, roles, read(leaf.bias), out_dtype)
+        if apart is not None:  # more ranks than the kernels take: the LoRAs' own term
+            down, up = apart
+            y = y + ((x.to(down.dtype) @ down.t()) @ up.t()).to(y.dtype)
+        return y
+
+
 def _mx_product(torch: Any, leaf: Any, x: Tensor, out_dtype: Dtype) -> Tensor:
     """The MX leaf's product (`internal/encoding/leaves.py:1505-1516`): x quantized per 32-block
     at dispatch, then the scaled-MFMA GEMM; the lane adds the bias after the cast."""
@@ -236,6 +275,19 @@ def _module_class(torch: Any) -> Any:
         def operand(self) -> str | None:
             """The activation geometry this leaf's GEMM reads (8-bit leaves), else None."""
             return self._cozy_lane.operand
+
+        #: A baked request's LoRAs (the reference's `SvdqLinear.lora`): what returns each one's
+        #: `(identity, down [r, K], up [N, r], scale)` as the forward runs; None for none. Only a
+        #: lane that `adopts` reads it.
+        lora: Callable[[], list[tuple[object, Tensor, Tensor, float]]] | None = None
+        #: The branch with the LoRAs merged in, for the factors bound at these addresses.
+        _cozy_merged: tuple[tuple[object, ...], dict[str, Tensor] | None, tuple[Tensor, Tensor]] | None = None
+
+        def adopt(self, lora: Callable[[], list[tuple[object, Tensor, Tensor, float]]] | None) -> None:
+            """Binds a baked request's LoRAs (`internal/encoding/leaves.py:1223-1226`)."""
+            if not getattr(self._cozy_lane, "adopts", False):
+                raise TypeError(f"{self.provider} leaves take no LoRA branch")
+            self.lora = lora
 
         def roles(self) -> dict[str, Tensor]:
             names = self._cozy_lane.buffers
@@ -508,6 +560,71 @@ class SvdqInt4NativeLeaf(_Provider):
 
 
 @dataclass(frozen=True, slots=True)
+class SvdqNvfp4NativeLeaf(_Provider):
+    """`svdq.nvfp4` encoded GEMM (`internal/encoding/leaves.py:1267-1407`): SVDQuant's nvfp4
+    residual, its smoothing and its 16-bit low-rank branch stay resident and are multiplied as
+    they are (`svdq_linear`): the activation is smoothed, quantized to nvfp4 and down-projected in
+    one pass, and the GEMM decodes both operands exactly onto the matrix core and adds the
+    up-projection in its epilogue. The weight is held as stored (row-major scales, element 2k
+    low); a high-first nibble order, cuBLAS scale tiles, a divided second level, an unbuilt rank
+    and 16-bit factors other than bf16 are converted once, at the bind."""
+
+    encoding: str = "svdq.nvfp4"
+    params: Params = ()
+
+    name = property(lambda self: SVDQ)
+    schemes = property(lambda self: frozenset({"svdq.nvfp4"}))
+    code_revision = property(lambda self: "1")
+    suite = property(lambda self: "svdq-nvfp4-native")
+    # The reference's kernels multiply on FP4 tensor cores; these on gfx950's fp16/bf16 MFMA.
+    formats = property(lambda self: frozenset({"bf16"}))
+    required = property(lambda self: frozenset(
+        {"weight", "scale", "scale_2", "pre_quant_scale", "lowrank_down", "lowrank_up"}))
+    optional = property(lambda self: frozenset({"input_scale", "channel_scale"}))
+
+    def supports(self, shape: Sequence[int], params: Mapping[str, object]) -> str:
+        """One matrix, nvfp4's block law, K whole GEMM steps and N % 8
+        (`internal/encoding/leaves.py:1322-1330`, with this GEMM's own multiples)."""
+        why = _rank2(shape) or dec.Nvfp4Dequant().supports(shape, params)
+        if not why and (int(shape[1]) % svdq_linear.K_ALIGN or int(shape[0]) % 8):
+            why = (f"the svdq GEMM needs K % {svdq_linear.K_ALIGN} == 0 and N % 8 == 0; this tensor "
+                   f"is {list(shape)}")  # fmt: skip
+        return why
+
+    def leaf(self, torch: Any, parts: Mapping[str, Tensor], replaced: object, out_dtype: Dtype) -> Any:
+        """`internal/encoding/leaves.py:1347-1407`: the roles where the kernels read them."""
+        params = dict(self.params)
+        down, up = parts["lowrank_down"], parts["lowrank_up"]
+        if int(down.shape[0]) > svdq_linear.RANKS[-1]:
+            raise ValueError(f"a rank-{int(down.shape[0])} branch: the svdq kernels take up to "
+                             f"{svdq_linear.RANKS[-1]}; it decodes instead")  # fmt: skip
+        weight = parts["weight"].view(torch.uint8)
+        if params.get("nibble_order") == "high_first":
+            weight = (weight << 4) | (weight >> 4)  # the kernels read element 2k low
+        out_features, in_features = int(weight.shape[0]), 2 * int(weight.shape[1])
+        scale = parts["scale"].view(torch.uint8)
+        if params.get("scale_layout") == "cublas_128x4":
+            scale = layout.from_blocked(torch, scale, out_features, in_features // 16)
+        scale = scale.reshape(out_features, in_features // 16).contiguous().view(torch.float8_e4m3fn)
+        second = parts["scale_2"].to(torch.float32).reshape(1)
+        if params.get("global_scale") == "divide":
+            second = 1.0 / second
+        rank = int(down.shape[0])
+        if svdq_linear.rank(rank) != rank or torch.bfloat16 not in (down.dtype, up.dtype):
+            down, up = svdq_linear.padded(torch, down, up)
+        elif down.dtype != up.dtype:
+            down, up = down.to(torch.bfloat16), up.to(torch.bfloat16)
+        roles = {"weight": weight.contiguous(), "scale": scale, "scale_2": second,
+                 "pre_quant_scale": parts["pre_quant_scale"].to(torch.float32).reshape(-1),
+                 "lowrank_down": down.contiguous(), "lowrank_up": up.contiguous()}  # fmt: skip
+        for role in ("channel_scale", "input_scale"):
+            if role in parts:
+                roles[role] = parts[role].to(torch.float32).reshape(-1)
+        return _build(torch, _SvdqNvfp4Lane(), roles, getattr(replaced, "bias", None), out_dtype,
+                      self, in_features, out_features)  # fmt: skip
+
+
+@dataclass(frozen=True, slots=True)
 class Nvfp4NativeLeaf(_Provider):
     """`nvfp4` encoded GEMM (`internal/encoding/leaves.py:1069-1203`): the E2M1 payload and E4M3
     block scales stay resident (0.56 bytes a weight). Up to 16 rows take the W4A16 GEMV on the
@@ -570,8 +687,8 @@ def launch_providers() -> dict[str, tuple[Any, ...]]:
     """Scheme -> its encoded-GEMM providers on gfx950, in the reference's preference order
     (`internal/encoding/selection.py:248-274`, the encoded_gemm entries)."""
     out: dict[str, list[Any]] = {}
-    for build in (RowwiseNativeLeaf, Int8ConvRotNativeLeaf, W4a8NativeLeaf, SvdqInt4NativeLeaf,
-                  MicroScaledNativeLeaf, Nvfp4NativeLeaf):
+    for build in (RowwiseNativeLeaf, Int8ConvRotNativeLeaf, W4a8NativeLeaf, SvdqNvfp4NativeLeaf,
+                  SvdqInt4NativeLeaf, MicroScaledNativeLeaf, Nvfp4NativeLeaf):
         for scheme in sorted(build().schemes):
             out.setdefault(scheme, []).append(build(scheme))
     return {scheme: tuple(candidates) for scheme, candidates in out.items()}

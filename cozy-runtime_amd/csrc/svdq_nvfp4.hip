@@ -56,25 +56,30 @@ __global__ void input_scale_init(uint32_t* g) { *g = bits_of(kInputFloor); }
 // g = max(max over x of fl(|x|·p[col]) / 2688, 1e-30). The law takes amax over rows first, then
 // · p, then the max: the same value, since fl(a·p) is monotonic in a for p > 0; the division and
 // the clamp are monotonic too, so each block's candidate enters by an unsigned max of its
-// (non-negative) float bits into *g, which input_scale_init set to the floor.
+// (non-negative) float bits into *g, which input_scale_init set to the floor. A thread keeps its
+// 8-column chunks (and their p) fixed and walks the block's rows; a wave reads 1 KB runs of a row.
 template <bool kHalf>
 __global__ __launch_bounds__(256) void input_scale_kernel(const uint16_t* __restrict__ x,
-                                                          const float* __restrict__ p,
-                                                          int64_t chunks, int per_row,
-                                                          uint32_t* __restrict__ g) {
+                                                          const float* __restrict__ p, int M,
+                                                          int K, uint32_t* __restrict__ g) {
     __shared__ float red[4];
     float m = 0.0f;
-    for (int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; c < chunks;
-         c += static_cast<int64_t>(gridDim.x) * 256) {
-        const uint4 v = *reinterpret_cast<const uint4*>(x + c * 8);
-        const int col = static_cast<int>(c % per_row) * 8;
-        const float4 p0 = *reinterpret_cast<const float4*>(p + col);
-        const float4 p1 = *reinterpret_cast<const float4*>(p + col + 4);
+    const int chunks = K / 8;
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        const float4 p0 = *reinterpret_cast<const float4*>(p + 8 * c);
+        const float4 p1 = *reinterpret_cast<const float4*>(p + 8 * c + 4);
         const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-        float f[8];
-        widen8<kHalf>(v, f);
+        float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // max |x| per column over the rows
+#pragma unroll 4
+        for (int row = blockIdx.x; row < M; row += gridDim.x) {
+            const uint4 v = *reinterpret_cast<const uint4*>(x + static_cast<int64_t>(row) * K + 8 * c);
+            float f[8];
+            widen8<kHalf>(v, f);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) m = fmaxf(m, __fmul_rn(fabsf(f[i]), pv[i]));
+            for (int i = 0; i < 8; ++i) a[i] = fmaxf(a[i], fabsf(f[i]));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, __fmul_rn(a[i], pv[i]));
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
@@ -516,14 +521,12 @@ hipError_t svdq_nvfp4_input_scale(const void* x, bool x_half, const float* p, in
                                   float* g, hipStream_t s) {
     uint32_t* word = reinterpret_cast<uint32_t*>(g);
     input_scale_init<<<1, 1, 0, s>>>(word);
-    const int64_t chunks = static_cast<int64_t>(M) * (K / 8);
-    if (chunks == 0) return hipGetLastError();
-    const int64_t want = (chunks + 255) / 256;
-    const int blocks = static_cast<int>(want < 2048 ? want : 2048);
+    if (M == 0) return hipGetLastError();
+    const int blocks = M < 256 ? M : 256;  // one atomic max a block: few blocks, long rows
     if (x_half)
-        input_scale_kernel<true><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), p, chunks, K / 8, word);
+        input_scale_kernel<true><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), p, M, K, word);
     else
-        input_scale_kernel<false><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), p, chunks, K / 8, word);
+        input_scale_kernel<false><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), p, M, K, word);
     return hipGetLastError();
 }
 

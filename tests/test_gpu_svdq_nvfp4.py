@@ -175,3 +175,110 @@ def test_c4_shape_svdq_nvfp4(ops):
     assert torch.equal(ascales.cpu().view(torch.uint8), scales.view(torch.uint8))
     got = ops.svdq_linear(x.to(DEV), dd, b.to(DEV), torch.bfloat16)
     assert_close(got, laws.svdq_nvfp4_exact(x, d, b))
+
+
+# ------------------------------------------------------------------------------ the leaf
+
+
+class _Linear(torch.nn.Module):
+    def __init__(self, bias: torch.Tensor | None) -> None:
+        super().__init__()
+        self.bias = bias
+
+
+def _as_stored(d: dict, params: dict) -> dict:
+    """The law's roles (`weight` element 2k low, row-major scales, multiply) for stored parts of
+    any convention: the nibbles swapped back, the cuBLAS tiles undone (`laws.from_blocked`, held
+    by the reference's decode vectors), a divided second level inverted."""
+    out = dict(d)
+    n, k = int(d["weight"].shape[0]), 2 * int(d["weight"].shape[1])
+    if params.get("nibble_order") == "high_first":
+        w = d["weight"].view(torch.uint8)
+        out["weight"] = (w << 4) | (w >> 4)
+    if params.get("scale_layout") == "cublas_128x4":
+        grid = laws.from_blocked(d["scale"].view(torch.uint8).reshape(-1), n, k // 16)
+        out["scale"] = grid.reshape(n, k // 16).view(torch.float8_e4m3fn)
+    second = d["scale_2"].float().reshape(1)
+    out["scale_2"] = 1.0 / second if params.get("global_scale") == "divide" else second
+    for role in ("channel_scale", "input_scale", "pre_quant_scale"):
+        if role in out:
+            out[role] = out[role].float()
+    return out
+
+
+def _vector_cases():
+    import vectors
+
+    return [c for c in vectors.cases("svdq", "svdq") if "refuse" not in c]
+
+
+@pytest.mark.parametrize("case", _vector_cases(), ids=lambda c: c["key"])
+def test_svdq_leaf_on_reference_vectors(case):
+    """The provider's leaf from the reference's own svdq.nvfp4 parts (every stored convention
+    the vectors hold: nibble order, cuBLAS tiles, divided second level, E4M3 channel scale, stored
+    input scale, fp16 and f32 factors, rank 4 padded to 32) against the float64 law; a case whose
+    K is not whole GEMM steps is refused by `supports`."""
+    import vectors
+    from cozyq import leaves
+
+    parts, params = vectors.parts(case), dict(case["encoding"]["params"])
+    provider = leaves.SvdqNvfp4NativeLeaf("svdq.nvfp4", tuple(sorted(params.items())))
+    shape = case["shape"]
+    why = provider.supports(shape, params)
+    if shape[1] % 64:
+        assert "K % 64" in why
+        return
+    assert why == ""
+    n, k = shape
+    dtype = torch.float16 if case["dtype"] == "F16" else torch.bfloat16
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 0.1).to(dtype)
+    leaf = provider.leaf(torch, {role: t.to(DEV) for role, t in parts.items()}, _Linear(bias.to(DEV)), dtype)
+    x = activations(37, k, seed=k + n, dtype=dtype)
+    got = leaf(x.to(DEV))
+    assert got.shape == (37, n) and got.dtype == dtype
+    law = _as_stored(parts, params)
+    law["lowrank_down"], law["lowrank_up"] = law["lowrank_down"].to(torch.bfloat16), law["lowrank_up"].to(torch.bfloat16)
+    assert_close(got, laws.svdq_nvfp4_exact(x, law, bias))
+
+
+def test_svdq_leaf_conventions_and_unbuilt_rank():
+    """A larger leaf stored high-first, in cuBLAS tiles, with a divided second level and rank 20
+    (padded to 32), in fp16: the leaf against the law on the stored roles."""
+    from cozyq import leaves
+
+    n, k, r = 264, 1024, 20
+    d = roles(n, k, r, seed=31)
+    d["scale_2"] = torch.tensor(50.0)
+    stored = dict(d)
+    w = d["weight"]
+    stored["weight"] = (w << 4) | (w >> 4)
+    stored["scale"] = laws.to_blocked(d["scale"].view(torch.uint8)).view(torch.float8_e4m3fn)
+    params = (("block_size", 16), ("global_scale", "divide"), ("nibble_order", "high_first"),
+              ("scale_layout", "cublas_128x4"))  # fmt: skip
+    leaf = leaves.SvdqNvfp4NativeLeaf("svdq.nvfp4", params).leaf(
+        torch, {role: t.to(DEV) for role, t in stored.items()}, _Linear(None), torch.float16)  # fmt: skip
+    assert int(leaf.lowrank_down.shape[0]) == 32
+    x = activations(300, k, seed=32, dtype=torch.float16)
+    law = dict(d)
+    law["scale_2"] = 1.0 / torch.tensor([50.0])
+    assert_close(leaf(x.to(DEV)), laws.svdq_nvfp4_exact(x, law, None))
+
+
+@pytest.mark.parametrize("extra", [16, 120], ids=["merged", "apart"])
+def test_svdq_leaf_lora_branches(extra):
+    """A baked request's LoRA (`adopt`): within the kernels' 128 ranks it joins the branch (one
+    GEMM); past them it is its own term. Either way the law plus x·Aᵀ·(s·B)ᵀ."""
+    from cozyq import leaves
+
+    n, k, r = 264, 512, 32
+    d = roles(n, k, r, seed=41)
+    leaf = leaves.SvdqNvfp4NativeLeaf().leaf(torch, on(d), _Linear(None), torch.bfloat16)
+    gen = torch.Generator().manual_seed(42)
+    a = (torch.randn(extra, k, generator=gen) * 0.05).to(torch.bfloat16)
+    b = (torch.randn(n, extra, generator=gen) * 0.05).to(torch.bfloat16)
+    leaf.adopt(lambda: [("lora", a.to(DEV), b.to(DEV), 0.5)])
+    x = activations(64, k, seed=43)
+    got = leaf(x.to(DEV))
+    want = laws.svdq_nvfp4_exact(x, d, None) + (x.double() @ a.double().t()) @ (0.5 * b.double()).t()
+    assert_close(got, want)
+    assert (leaf._cozy_merged[1] is None) == (r + extra > 128)

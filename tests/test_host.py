@@ -21,11 +21,12 @@ class _Linear(torch.nn.Module):
 
 def test_providers_surface_and_launch_table():
     table = leaves.launch_providers()
-    assert set(table) == {"fp8.rowwise", "int8.convrot", "w4a8.convrot", "svdq.int4g64", "mxfp8",
-                          "nvfp4"}  # fmt: skip
+    assert set(table) == {"fp8.rowwise", "int8.convrot", "w4a8.convrot", "svdq.nvfp4",
+                          "svdq.int4g64", "mxfp8", "nvfp4"}  # fmt: skip
     names = {p.name for ps in table.values() for p in ps}
     assert names == {operands.ROWWISE_FP8, operands.INT8_CONVROT, leaves.W4A8, leaves.MXFP8,
-                     leaves.SVDQ_INT4, leaves.NVFP4}  # fmt: skip
+                     leaves.SVDQ, leaves.SVDQ_INT4, leaves.NVFP4}  # fmt: skip
+    assert leaves.SVDQ == "cozy.svdq-nvfp4.native-leaf/1"  # internal/encoding/leaves.py:72
     assert leaves.OPERANDS[leaves.W4A8] == operands.INT8_CONVROT
     for scheme, (provider,) in table.items():
         assert provider.encoding == scheme
@@ -36,6 +37,36 @@ def test_providers_surface_and_launch_table():
         assert leaves.serves(provider, "gfx950") and not leaves.serves(provider, "gfx942")
         with pytest.raises(AssertionError):
             provider.decode(torch, {}, torch.empty(0))
+
+
+def test_svdq_nvfp4_leaf_surface_and_supports():
+    """`internal/encoding/leaves.py:1267-1330`: roles, out dtypes, nvfp4's block law, and this
+    GEMM's K % 64 and N % 8; the rank helpers of `internal/svdq_linear.py:266-299`."""
+    from cozyq import svdq_linear
+
+    sv = leaves.SvdqNvfp4NativeLeaf()
+    assert sv.encoding == "svdq.nvfp4" and sv.suite == "svdq-nvfp4-native"
+    assert sv.required == {"weight", "scale", "scale_2", "pre_quant_scale", "lowrank_down", "lowrank_up"}
+    assert sv.optional == {"input_scale", "channel_scale"}
+    assert sv.out_dtypes == {"bfloat16", "float16"}
+    ok = {"block_size": 16, "global_scale": "multiply", "nibble_order": "low_first",
+          "scale_layout": "row_major"}  # fmt: skip
+    assert sv.supports([3072, 3072], ok) == ""
+    assert "K % 64" in sv.supports([3072, 3040], ok)
+    assert "N % 8" in sv.supports([3074, 3072], ok)
+    assert sv.supports([2, 3072, 3072], ok)
+    assert sv.supports([3072, 3072], {**ok, "block_size": 32})
+    assert [svdq_linear.rank(r) for r in (1, 32, 33, 64, 65, 128)] == [32, 32, 64, 64, 128, 128]
+    with pytest.raises(ValueError):
+        svdq_linear.rank(129)
+    down, up = torch.ones(4, 64), torch.ones(8, 4)
+    d, u = svdq_linear.padded(torch, down, up)
+    assert d.shape == (32, 64) and u.shape == (8, 32) and d.dtype == u.dtype == torch.bfloat16
+    assert not d[4:].any() and not u[:, 4:].any()
+    roles = {"lowrank_down": d, "lowrank_up": u}
+    m = svdq_linear.merged(torch, roles, torch.full((16, 64), 2.0), torch.full((8, 16), 3.0))
+    assert m is not None and m["lowrank_down"].shape == (64, 64) and m["lowrank_up"].shape == (8, 64)
+    assert svdq_linear.merged(torch, roles, torch.ones(100, 64), torch.ones(8, 100)) is None
 
 
 def test_nvfp4_leaf_surface_and_supports():
