@@ -232,31 +232,36 @@ hipError_t launch_quantize(const void* x, const float* p, const float* g, const 
 
 // ------------------------------------------------------------------------------ GEMM
 
-// One operand row's 64 elements of a buffer (32 code bytes, 4 E4M3 scale bytes) decoded to fp16
-// and written as the 8 swizzled 16-byte chunks of LDS row r. Chunk c holds elements 8c..8c+7:
-// code dword c, 16-block c/2.
-__device__ __forceinline__ void put_row(uint8_t* row, int r, uint4 c0, uint4 c1, uint32_t sb) {
-    const uint32_t dw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    // The four E4M3 scales as fp16 (exact: E4M3's range and precision sit inside fp16's),
-    // converted at unit scale two a call.
-    const f16x2 s01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb, 1.0f, false);
-    const f16x2 s23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb, 1.0f, true);
-    const _Float16 scales[4] = {s01[0], s01[1], s23[0], s23[1]};
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        const f16x2 s2 = {scales[b], scales[b]};
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int c = 2 * b + h;
-            const f16x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw[c], 1.0f, 0) * s2;
-            const f16x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw[c], 1.0f, 1) * s2;
-            const f16x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw[c], 1.0f, 2) * s2;
-            const f16x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw[c], 1.0f, 3) * s2;
-            *reinterpret_cast<uint4*>(row + 16 * swz(r, c)) =
-                make_uint4(__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
-                           __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3));
-        }
-    }
+// A buffer row's four E4M3 block scales (one byte each, block b = elements 16b..16b+15) as fp16
+// pairs (exact: E4M3's range and precision sit inside fp16's), converted at unit scale.
+struct RowScales {
+    f16x2 lo, hi;  // blocks 0, 1 and 2, 3
+};
+
+__device__ __forceinline__ RowScales row_scales(uint32_t sb) {
+    return RowScales{__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb, 1.0f, false),
+                     __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb, 1.0f, true)};
+}
+
+// Chunk c (0..7) of a buffer row — elements 8c..8c+7, code dword c, 16-block c/2 — decoded to
+// fp16 (E2M1 at unit scale, times the block's scale) and written at its swizzled place in LDS
+// row r.
+__device__ __forceinline__ void put_chunk(uint8_t* row, int r, int c, uint32_t dw, const RowScales& s) {
+    const _Float16 sc = (c >> 1) == 0 ? s.lo[0] : (c >> 1) == 1 ? s.lo[1] : (c >> 1) == 2 ? s.hi[0] : s.hi[1];
+    const f16x2 s2 = {sc, sc};
+    const f16x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 1.0f, 0) * s2;
+    const f16x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 1.0f, 1) * s2;
+    const f16x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 1.0f, 2) * s2;
+    const f16x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 1.0f, 3) * s2;
+    *reinterpret_cast<uint4*>(row + 16 * swz(r, c)) =
+        make_uint4(__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                   __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3));
+}
+
+__device__ __forceinline__ uint32_t dword_of(const uint4& a, const uint4& b, int c) {
+    const uint4 v = c < 4 ? a : b;
+    const int k = c & 3;
+    return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
 }
 
 __device__ __forceinline__ f16x8 as_half8(const i32x8& v, int h) {
@@ -318,10 +323,18 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         xsb = __builtin_amdgcn_raw_buffer_load_b32(asr, so, 0, 0);
         wsb = __builtin_amdgcn_raw_buffer_load_b32(wsr, so, 0, 0);
     };
+    // Chunk q (0..15) of the thread's two rows of a buffer: the A row's chunks, then W's.
+    auto put = [&](uint8_t* buf, int q, const RowScales& xsc, const RowScales& wsc) {
+        if (q < 8)
+            put_chunk(buf + tid * kPairK, tid, q, dword_of(xa0, xa1, q), xsc);
+        else
+            put_chunk(buf + kOpBytes + tid * kPairK, tid, q - 8, dword_of(wa0, wa1, q - 8), wsc);
+    };
     auto store = [&](int pair) {
         uint8_t* buf = lds + (pair & 1) * kPairBytes;
-        put_row(buf + tid * kPairK, tid, xa0, xa1, xsb);
-        put_row(buf + kOpBytes + tid * kPairK, tid, wa0, wa1, wsb);
+        const RowScales xsc = row_scales(xsb), wsc = row_scales(wsb);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) put(buf, q, xsc, wsc);
     };
 
     // Fragment reads as gemm_tile.h's int8 kind: lane l supplies row l%32; lane group l/32 its
@@ -378,40 +391,57 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         }
     };
 
-    // Buffers 0 and 1 take pairs 0 and 1 before the loop. Pair p + 2's loads are issued at the
-    // top of step 2p + 1 (after the barrier past which no wave reads pair p's buffer), decoded
-    // and written in step 2p + 2, and seen complete at the barrier of step 2p + 3.
+    // Pair p + 1's loads are issued at the top of step 2p - 1 (pair 1's before the loop), and
+    // its rows are decoded and written in step 2p, interleaved with that step's MFMAs, into the
+    // buffer no wave has read since the barrier of step 2p - 1; the barrier of step 2p + 1 makes
+    // them visible. Past the last pair the writes land in a buffer nothing reads again.
     load(0);
     fence();
     wait_vmcnt<0>();
     fence();
     store(0);
-    if (np > 1) {
-        load(1);
-        fence();
-        wait_vmcnt<0>();
-        fence();
-        store(1);
-    }
+    if (np > 1) load(1);
     fence();
-    wait_vmcnt<0>();
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
     fence();
+
+    // Step 2p: 16 slices, each one fragment read for step 2p + 1, two of this step's MFMAs (K
+    // half h = q / 8, so that no MFMA waits on the one before it) and one chunk of pair p + 1
+    // decoded and written.
+    auto even_step = [&](int s, const Frags& cur, Frags& next) {
+        const uint8_t* rbuf = lds + ((s + 1) >> 1 & 1) * kPairBytes;
+        const int e = (s + 1) & 1;
+        uint8_t* wbuf = lds + (((s >> 1) + 1) & 1) * kPairBytes;
+        const RowScales xsc = row_scales(xsb), wsc = row_scales(wsb);
+        i32x4 piece[4][4];  // [i][alo, ahi, blo, bhi]
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int fi = q >> 2, fk = q & 3;
+            const int off = fk < 2 ? aoff[e][fk][fi] : boff[e][fk - 2][fi];
+            piece[fi][fk] = *reinterpret_cast<const i32x4*>(rbuf + off);
+            const int h = q >> 3, i = (q >> 1) & 3, j = 2 * (q & 1);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_half8(cur.a[i], h), as_half8(cur.b[j], h), acc[i][j], 0, 0, 0);
+            acc[i][j + 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_half8(cur.a[i], h), as_half8(cur.b[j + 1], h), acc[i][j + 1], 0, 0, 0);
+            put(wbuf, q, xsc, wsc);
+            __builtin_amdgcn_sched_barrier(0);  // slices stay in order: decode rides under MFMAs
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            next.a[i] = __builtin_shufflevector(piece[i][0], piece[i][1], 0, 1, 2, 3, 4, 5, 6, 7);
+            next.b[i] = __builtin_shufflevector(piece[i][2], piece[i][3], 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    };
 
     Frags f0, f1;
     fetch(0, f0);
     for (int s = 0; s < 2 * np; s += 2) {
         const int p = s >> 1;
-        fetch(s + 1, f1);
-        mfmas(f0);
-        schedule();
-        if (p >= 1 && p + 1 < np) {
-            fence();
-            wait_vmcnt<0>();
-            fence();
-            store(p + 1);
-        }
+        fence();
+        wait_vmcnt<0>();
+        fence();
+        even_step(s, f0, f1);
+        __builtin_amdgcn_sched_barrier(0);  // the step's MFMAs stay ahead of the barrier
         fence();
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
@@ -420,6 +450,7 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         fetch(s + 2, f0);  // past the last step: unused registers
         mfmas(f1);
         schedule();
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // Epilogue. Block (i, j): lane holds out[m][n] for m = j-block row l%32 and, per register
