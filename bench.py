@@ -37,6 +37,7 @@ METRIC = "quantized-linear TOPS & % MFMA peak (M=4096,K=3072,N=12288); M=1 HBM G
 #: MI355X datasheet peaks (dense): int8 5.0 POPS, fp8 5.0 PFLOPS, bf16 2.5 PFLOPS, HBM 8 TB/s.
 PEAK_INT8_TOPS = 5000.0
 PEAK_FP8_TFLOPS = 5000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 / fp16 MFMA
 PEAK_HBM_GBS = 8000.0
 #: HBM bytes per launch come from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs (one counter a
 #: pass, each scaled by the same counter's reading for a 256 MiB device copy), whose summary
@@ -470,17 +471,19 @@ def bench_mx(torch, ops, lib, stream, steps: int) -> dict:
 
 def bench_svdq(torch, ops, lib, stream, steps: int) -> dict:
     """Config 4: SVDQuant W4A4 int4-g64, M=4096, K=N=3072, rank 32: the activation kernel
-    (smoothing, int4 codes, la = bf16(x·downᵀ)) then the GEMM with the low-rank add and bias."""
-    from oracle import laws
+    (smoothing, int4 codes, la = bf16(x·downᵀ)) then the GEMM with the low-rank add and bias.
+    The weight is the package encoder's (`cozyq.encode.encode_svdq_int4`) of W ~ N(0, 0.02)."""
+    from cozyq import encode
 
     m, k, n, r = 4096, 3072, 3072, 32
     gen = torch.Generator().manual_seed(20261204)
     x = _activations(torch, m, k, 81)
     p = (torch.rand(k, generator=gen) * 1.5 + 0.5).cuda()
-    down = (torch.randn(r, k, generator=gen) * 0.02).to(torch.bfloat16)
-    up = (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16)
-    codes, scales = laws.svdq_weight(torch.randn(n, k, generator=gen) * 0.02, p.cpu(), down, up)
-    down, up, codes, scales = down.cuda(), up.cuda(), codes.cuda(), scales.cuda()
+    down = (torch.randn(r, k, generator=gen) * 0.02).to(torch.bfloat16).cuda()
+    up = (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16).cuda()
+    encoded = encode.encode_svdq_int4(torch, "c4", (torch.randn(n, k, generator=gen) * 0.02).cuda(), p,
+                                      down, up)  # fmt: skip
+    codes, scales = encoded.payload, encoded.companions[0].raw
     bias = (torch.randn(n, generator=gen) * 0.5).to(torch.bfloat16).cuda()
     act = torch.empty(m, k // 2, dtype=torch.uint8, device="cuda")
     ascales = torch.empty(m, k // 64, dtype=torch.float16, device="cuda")
@@ -511,6 +514,92 @@ def bench_svdq(torch, ops, lib, stream, steps: int) -> dict:
             "gemm_tops": int4_ops / (g_ms * 1e-3) / 1e12,
             "frac_int8_mfma": int4_ops / (g_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
             "kernel": "svdq_gemm_kernel (int4 unpacked to int8, 32x32x32 MFMA, per-group rescale)"}
+
+
+def bench_svdq_nvfp4(torch, ops, lib, stream, steps: int) -> dict:
+    """Config 4's shape (M=4096, K=N=3072, rank 32) on the reference's own W4A4 law, svdq.nvfp4:
+    g_x (`cozyq_svdq_input_scale`), the activation side (`cozyq_svdq_quantize`: nvfp4 codes and
+    E4M3 scales of bf16(x·p), la = bf16(x·downᵀ)) and the GEMM (`cozyq_svdq_gemm`: both operands
+    decoded exactly to fp16 on the MFMA, low-rank term and c in the epilogue, bias). The weight is
+    random codes and scales in [0.5, ~3], as the reference's own probe draws it
+    (`internal/svdq_linear.py:406-418`)."""
+    m, k, n, r = 4096, 3072, 3072, 32
+    gen = torch.Generator().manual_seed(20261205)
+    x = _activations(torch, m, k, 82)
+    roles = {
+        "weight": torch.randint(0, 256, (n, k // 2), generator=gen).to(torch.uint8).cuda(),
+        "scale": (torch.randn(n, k // 16, generator=gen).abs() + 0.5).to(torch.float8_e4m3fn).cuda(),
+        "scale_2": torch.full((1,), 0.01).cuda(),
+        "pre_quant_scale": (torch.rand(k, generator=gen) * 1.5 + 0.5).cuda(),
+        "lowrank_down": (torch.randn(r, k, generator=gen) * 0.02).to(torch.bfloat16).cuda(),
+        "lowrank_up": (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16).cuda(),
+        "channel_scale": (torch.rand(n, generator=gen) + 0.5).cuda(),
+    }
+    bias = (torch.randn(n, generator=gen) * 0.5).to(torch.bfloat16).cuda()
+    p = roles["pre_quant_scale"]
+    g = ops.svdq_input_scale(x, p)
+    act, ascales, la = ops.svdq_quantize(x, p, g, roles["lowrank_down"])
+
+    def scale():
+        ops.svdq_input_scale(x, p)
+
+    def quantize():
+        ops.svdq_quantize(x, p, g, roles["lowrank_down"])
+
+    def gemm():
+        ops.svdq_gemm(act, ascales, la, m, g, roles["weight"], roles["scale"], roles["scale_2"],
+                      roles["lowrank_up"], roles["channel_scale"], bias, torch.bfloat16)  # fmt: skip
+
+    def step():
+        ops.svdq_linear(x, roles, bias, torch.bfloat16)
+
+    preroll(torch, gemm)
+    med = Timer(torch).interleaved({"scale": scale, "quantize": quantize, "gemm": gemm, "step": step},
+                                   batch=max(2, min(8, steps // 4)))  # fmt: skip
+    g_ms, ms = med["gemm"]["ms"], med["step"]["ms"]
+    flops = 2.0 * m * n * k
+    lowrank_flops = 2.0 * m * r * (k + n)
+    return {"M": m, "K": k, "N": n, "R": r, "us": ms * 1e3, "input_scale_us": med["scale"]["ms"] * 1e3,
+            "quantize_us": med["quantize"]["ms"] * 1e3, "gemm_us": g_ms * 1e3,
+            "tflops": (flops + lowrank_flops) / (ms * 1e-3) / 1e12,
+            "gemm_tflops": flops / (g_ms * 1e-3) / 1e12,
+            "frac_f16_mfma": flops / (g_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+            "kernel": "nvfp4_gemm_kernel (E2M1 x E4M3 decoded to fp16, 32x32x16 f16 MFMA, 256x256)"}
+
+
+def bench_tiles(torch, ops, lib, stream, steps: int) -> dict:
+    """The GEMM tile configs (`cozyq_gemm` config 0..4) at the shapes the shape rule
+    (`cozyq_gemm_config`) was fitted on, int8 and fp8, as interleaved medians: each shape's per-
+    config microseconds, the fastest config and the one config -1 runs."""
+    shapes = [(128, 3072, 3072), (256, 14336, 4096), (512, 14336, 4096), (1024, 14336, 4096),
+              (4096, 14336, 4096), (4096, 12288, 3072), (4096, 9216, 3072), (4096, 3072, 3072),
+              (4096, 3072, 12288), (8192, 640, 2560), (2048, 1280, 1280), (1024, 3072, 3072),
+              (512, 3072, 3072), (2048, 3072, 3072), (16384, 3072, 3072), (384, 3072, 3072),
+              (768, 3072, 3072), (4096, 1280, 5120), (1536, 3072, 3072)]  # fmt: skip
+    timer, rows = Timer(torch), []
+    for kind in ("int8", "fp8"):
+        for m, n, k in shapes:
+            gen = torch.Generator(device="cuda").manual_seed(m + n + k)
+            if kind == "int8":
+                q = torch.randint(-127, 128, (m, k), dtype=torch.int8, device="cuda", generator=gen)
+                w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=gen)
+                f = ops.int8_gemm
+            else:
+                q = torch.randn(m, k, device="cuda", generator=gen).to(torch.float8_e4m3fn)
+                w = (torch.randn(n, k, device="cuda", generator=gen) * 4).to(torch.float8_e4m3fn)
+                f = ops.fp8_gemm
+            xs = torch.rand(m, device="cuda", generator=gen) * 0.01 + 0.001
+            ws = torch.rand(n, device="cuda", generator=gen) * 0.01 + 0.001
+            bias = torch.randn(n, device="cuda", generator=gen).to(torch.bfloat16)
+            fns = {c: (lambda c=c: f(q, xs, w, ws, bias, torch.bfloat16, c)) for c in range(5)}
+            preroll(torch, fns[0], 30)
+            est = timer.run(fns[0], 3, 1)
+            med = timer.interleaved(fns, samples=9, batch=max(2, min(50, int(2.0 / max(est, 1e-3)))))
+            us = {c: round(med[c]["ms"] * 1e3, 2) for c in range(5)}
+            rows.append({"kind": kind, "M": m, "N": n, "K": k, "us": us, "best": min(us, key=us.get),
+                         "chosen": lib.cozyq_gemm_config(int(kind == "fp8"), m, n, k)})  # fmt: skip
+            del q, w
+    return {"tiles": rows}
 
 
 def bench_weights(torch, ops, lib, stream, steps: int) -> dict:
@@ -713,7 +802,8 @@ def cpu_baselines(torch) -> dict:
     (rowwise int8, the literal int32 matmul), C2 on 1024 of its rows (rotation 128 + int8, int32
     matmul, scales, bias, GELU), C3 at M=1024 (e4m3 quantize, dequantize, float32 matmul: CPU
     torch's `_scaled_mm` rejects row-wise scales), C4 at M=1024 (int4-g64 quantize, dequantized
-    float32 matmul + the bf16 low-rank branch), C5 on 512 rows of each DiT shape (MX quantize,
+    float32 matmul + the bf16 low-rank branch; and the reference's svdq.nvfp4 `eager` law on the
+    same shape), C5 on 512 rows of each DiT shape (MX quantize,
     E8M0 dequant, float32 matmul). `value` is the sample's ops per second."""
     from oracle import laws
 
@@ -767,6 +857,15 @@ def cpu_baselines(torch) -> dict:
            2.0 * m4 * n4 * k4 + 2.0 * m4 * r4 * (k4 + n4), "TOPS",
            f"config 4 at M={m4}: smoothing, int4-g64 quantize, dequantized float32 matmul with "
            f"W[{n4},{k4}] int4-g64, rank-32 bf16 low-rank branch")  # fmt: skip
+    roles4 = {"weight": torch.randint(0, 256, (n4, k4 // 2), generator=gen).to(torch.uint8),
+              "scale": (torch.randn(n4, k4 // 16, generator=gen).abs() + 0.5).to(torch.float8_e4m3fn),
+              "scale_2": torch.full((1,), 0.01), "pre_quant_scale": p4, "lowrank_down": down4,
+              "lowrank_up": up4}  # fmt: skip
+    record("c4_nvfp4", lambda: laws.svdq_nvfp4_eager(x4, roles4, None, bf16),
+           2.0 * m4 * n4 * k4 + 2.0 * m4 * r4 * (k4 + n4), "TFLOPS",
+           f"config 4's shape at M={m4} on svdq.nvfp4 (internal/svdq_linear.py:639-659 `eager`): "
+           f"g_x, nvfp4 fake-quantize, float32 matmul with the decoded W[{n4},{k4}], low-rank "
+           "branch")  # fmt: skip
     m5 = 512
     mx_total_ops, mx_seconds = 0.0, 0.0
     for name, (k5, n5) in {"qkv": (3072, 9216), "attn_out": (3072, 3072), "ffn_up": (3072, 12288),
@@ -815,6 +914,10 @@ def only(torch, ops, lib, stream, args) -> int:
         figures = bench_nvfp4(torch, ops, lib, stream, args.steps)
     elif args.only == "bake":
         figures = bench_bake(torch, ops, lib, stream, args.steps)
+    elif args.only == "svdq_nvfp4":
+        figures = bench_svdq_nvfp4(torch, ops, lib, stream, args.steps)
+    elif args.only == "tiles":
+        figures = bench_tiles(torch, ops, lib, stream, args.steps)
     else:
         figures = bench_svdq(torch, ops, lib, stream, args.steps)
     print(json.dumps({"only": args.only, **figures}))
@@ -833,8 +936,9 @@ def main() -> int:
                         help="clock pre-roll before timing (profiling runs may shorten it)")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extra", action="store_true", help="skip configs 3-5")
-    parser.add_argument("--only", choices=("c1", "c2", "decode", "int8_decode", "w4a8", "fp8", "svdq", "mx", "weights",
-                                                    "nvfp4", "bake", "copy"),
+    parser.add_argument("--only", choices=("c1", "c2", "decode", "int8_decode", "w4a8", "fp8", "svdq",
+                                           "svdq_nvfp4", "mx", "weights", "nvfp4", "bake", "tiles",
+                                           "copy"),
                         help="profiling aid: run one leg (or a plain 256 MiB device copy, the "
                              "counter calibration) --steps times and print its figures only")  # fmt: skip
     args = parser.parse_args()
@@ -866,6 +970,7 @@ def main() -> int:
         configs["int8_decode"] = bench_int8_decode(torch, ops, lib, stream, args.steps)
         configs["w4a8"] = bench_w4a8(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["c4_svdq_w4a4"] = bench_svdq(torch, ops, lib, stream, max(10, args.steps // 2))
+        configs["c4_svdq_nvfp4"] = bench_svdq_nvfp4(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["c5_mxfp8"] = bench_mx(torch, ops, lib, stream, max(10, args.steps // 2))
         configs["weight_decode"] = bench_weights(torch, ops, lib, stream, args.steps)["decode_formats"]
         configs["nvfp4_w4a16"] = bench_nvfp4(torch, ops, lib, stream, args.steps)["nvfp4_w4a16_gemv"]

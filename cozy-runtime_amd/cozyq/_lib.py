@@ -44,6 +44,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "cozyq_gemm_config": (c_int, [c_int, c_int, c_int, c_int]),
     "cozyq_svdq_rows": (c_int, [c_int]),
+    "cozyq_encode_svdq_int4": (
+        c_int, [c_int, _P, c_int, _P, _P, _P, c_int, _P, _P, c_int64, c_int, _P]
+    ),
     "cozyq_svdq_input_scale": (c_int, [c_int, _P, c_int, _P, c_int, c_int, _P, _P]),
     "cozyq_svdq_quantize": (
         c_int, [c_int, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P]

@@ -28,6 +28,8 @@ W4A8_CODEBOOK = (
     0.052541, 0.156985, 0.265284, 0.379533, 0.502636, 0.638953, 0.794876, 0.980671,
 )  # fmt: skip
 NVFP4_BLOCK = 16
+#: svdq.int4g64's K-group (this build's W4A4 variant).
+SVDQ_INT4_GROUP = 64
 MX_BLOCK = 32
 E4M3_MAX = 448.0
 #: float64 partials the measure folds through.
@@ -230,3 +232,51 @@ def encode_nvfp4(torch: Any, key: str, values: Tensor) -> Encoded:
         Companion(".weight_scale", "F8_E4M3", [rows, cols // NVFP4_BLOCK], scale.view(torch.float8_e4m3fn)),
         Companion(".weight_scale_2", "F32", [], second),
     ], saturated, sse, energy, worst)  # fmt: skip
+
+
+def _svdq_int4_dense(torch: Any, codes: Tensor, scales: Tensor, p: Tensor, down: Tensor,
+                     up: Tensor) -> Tensor:
+    """The float32 weight an svdq.int4g64 encoding stands for: codes · group scale, back out of
+    the smoothed basis (· p), plus up·down — what `_measured` holds against the source."""
+    rows, cols = int(codes.shape[0]), 2 * int(codes.shape[1])
+    lo = (codes & 0xF).to(torch.int16)
+    hi = (codes >> 4).to(torch.int16)
+    q = torch.stack((lo, hi), dim=-1).reshape(rows, cols)
+    q = torch.where(q >= 8, q - 16, q).float()
+    v = (q.view(rows, -1, SVDQ_INT4_GROUP) * scales.float().unsqueeze(-1)).view(rows, cols)
+    return v * p.float() + up.float() @ down.float()
+
+
+def encode_svdq_int4(torch: Any, key: str, values: Tensor, p: Tensor, down: Tensor,
+                     up: Tensor) -> Encoded:
+    """svdq.int4g64 (this build's W4A4 variant; the reference's svdq writer is tensorfs's): the
+    residual `values − up·down` moved into the smoothed basis (÷ p per input channel), int4 codes
+    per 64-group with fp16 scales (`cozyq_encode_svdq_int4`). Payload U8 [R, C/2] (element 2k
+    low), `.weight_scale` F16 [R, C/64], and the branch and smoothing it was encoded against:
+    `.pre_quant_scale` F32 [C], `.lowrank_down` BF16 [r, C], `.lowrank_up` BF16 [R, r]."""
+    ops, values, rows, cols = _prepare(torch, key, values, SVDQ_INT4_GROUP)
+    device = values.device
+    rank = int(down.shape[0])
+    if tuple(down.shape) != (rank, cols) or tuple(up.shape) != (rows, rank):
+        raise UnsupportedInput(f"{key!r}: the low-rank branch must be down [r, {cols}] and up [{rows}, r]")
+    p = p.to(device=device, dtype=torch.float32).contiguous()
+    down = down.to(device=device, dtype=torch.bfloat16).contiguous()
+    up = up.to(device=device, dtype=torch.bfloat16).contiguous()
+    if p.numel() != cols:
+        raise UnsupportedInput(f"{key!r}: pre_quant_scale must hold {cols} values")
+    codes = torch.empty(rows, cols // 2, dtype=torch.uint8, device=device)
+    scales = torch.empty(rows, cols // SVDQ_INT4_GROUP, dtype=torch.float16, device=device)
+    if rows:
+        code = ops._lib.cozyq_encode_svdq_int4(ops.index, values.data_ptr(), _in_type(torch, values),
+                                               p.data_ptr(), down.data_ptr(), up.data_ptr(), rank,
+                                               codes.data_ptr(), scales.data_ptr(), rows, cols,
+                                               ops._stream())  # fmt: skip
+        ops._check(code, "the svdq int4 encoder")
+    sse, energy, worst = (0.0, 0.0, 0.0) if not rows else _measured(
+        torch, ops, values, _svdq_int4_dense(torch, codes, scales, p, down, up).contiguous())  # fmt: skip
+    return Encoded("U8", [rows, cols // 2], codes, [
+        Companion(".weight_scale", "F16", [rows, cols // SVDQ_INT4_GROUP], scales),
+        Companion(".pre_quant_scale", "F32", [cols], p),
+        Companion(".lowrank_down", "BF16", [rank, cols], down),
+        Companion(".lowrank_up", "BF16", [rows, rank], up),
+    ], 0, sse, energy, worst)  # fmt: skip

@@ -491,6 +491,19 @@ int cozyq_encode_nvfp4(int device, const void* w, int w_type, uint8_t* codes, ui
     return cozyq::encode_nvfp4(w, w_type, rows, K, amax, codes, scale, scale_2, saturated, on(stream));
 }
 
+int cozyq_encode_svdq_int4(int device, const void* w, int w_type, const float* p, const void* down,
+                           const void* up, int rank, uint8_t* codes, uint16_t* scales, int64_t rows,
+                           int K, void* stream) {
+    if (rows < 0 || rank < 0 || rank > 1024 || w_type < 0 || w_type > 2 || !fits(K, 64))
+        return hipErrorInvalidValue;
+    if (rows > 0 && (!w || !p || !codes || !scales || (rank > 0 && (!down || !up)) ||
+                     !aligned16(w) || !aligned16(down) || !aligned16(codes) || !aligned16(scales)))
+        return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::encode_svdq_int4(w, w_type, p, down, up, rank, rows, K, codes, scales, on(stream));
+}
+
 int cozyq_measure(int device, const void* w, int w_type, const float* decoded, int64_t total,
                   double* partial, int parts, double* out, void* stream) {
     if (w_type < 0 || w_type > 2 || total < 0 || parts < 1 || !w || !decoded || !partial || !out)

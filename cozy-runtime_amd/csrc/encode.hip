@@ -15,6 +15,9 @@
 // - nvfp4: g = amax(|w|)/(448·6) (1 for an all-zero tensor); per 16-block the E4M3 scale among
 //   e4m3(amax_b/(6g)) and its two neighbours with the least squared error of (e2m1·s)·g, codes
 //   e2m1 of w/(s·g) rounded to nearest even and saturated at ±6.
+// - svdq.int4g64 (this build's W4A4 variant): the residual w − up·down in float64 moved into the
+//   smoothed basis, v = float32((w − up·down) / p); per 64-group s = fp16(amax|v| / 7), codes
+//   clamp(rne(v / s), −8, 7) (0 where s == 0), two a byte with element 2k low.
 #include "common.h"
 #include "kernels.h"
 #include "rotate.h"
@@ -322,6 +325,61 @@ __global__ __launch_bounds__(kEncThreads) void encode_nvfp4_kernel(const void* _
     if (sat) atomicAdd(saturated, sat);
 }
 
+// ------------------------------------------------------------------------ svdq.int4g64
+
+// One thread an 8-element chunk (K % 64 == 0, so eight threads a group, in one wave): the
+// residual in float64 (bf16 products are exact there; the sums are exact for all but extreme
+// exponent spreads), divided by p in float64 and rounded once to float32, then the group's
+// scale and the codes by the activation law of the int4 GEMM (`svdq_int4_quantize`'s).
+template <int kIn>
+__global__ __launch_bounds__(kEncThreads) void encode_svdq_int4_kernel(
+    const void* __restrict__ w, const float* __restrict__ p, const uint16_t* __restrict__ down,
+    const uint16_t* __restrict__ up, int rank, uint8_t* __restrict__ codes,
+    uint16_t* __restrict__ scales, int64_t chunks, int K) {
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * kEncThreads + threadIdx.x;
+    const bool live = e < chunks;
+    const int per_row = K / 8;
+    const int64_t row = live ? e / per_row : 0;
+    const int c = live ? static_cast<int>(e % per_row) : 0;
+    float wv[8];
+    load8in<kIn>(w, row * K + 8 * c, wv);
+    double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int r = 0; r < rank; ++r) {
+        const double u = static_cast<double>(float_of(static_cast<uint32_t>(up[row * rank + r]) << 16));
+        const uint4 d = *reinterpret_cast<const uint4*>(down + static_cast<int64_t>(r) * K + 8 * c);
+        const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[2 * i] = __fma_rn(u, static_cast<double>(float_of(dw[i] << 16)), acc[2 * i]);
+            acc[2 * i + 1] = __fma_rn(u, static_cast<double>(float_of(dw[i] & 0xffff0000u)), acc[2 * i + 1]);
+        }
+    }
+    float v[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const double res = static_cast<double>(wv[i]) - acc[i];
+        v[i] = static_cast<float>(res / static_cast<double>(p[8 * c + i]));
+        amax = fmaxf(amax, fabsf(v[i]));
+    }
+    // The group's eight chunks are eight consecutive lanes (8 | 64 and groups start at 8-lane
+    // boundaries since K/8 is a multiple of 8).
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const _Float16 s16 = static_cast<_Float16>(__fdiv_rn(amax, 7.0f));
+    const float s = static_cast<float>(s16);
+    uint32_t packed = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float q = 0.0f;
+        if (s != 0.0f) q = fminf(fmaxf(__builtin_rintf(__fdiv_rn(v[i], s)), -8.0f), 7.0f);
+        packed |= (static_cast<uint32_t>(static_cast<int>(q)) & 0xfu) << (4 * i);
+    }
+    if (!live) return;
+    *reinterpret_cast<uint32_t*>(codes + row * (K / 2) + 4 * c) = packed;
+    if ((c & 7) == 0) scales[row * (K / 64) + c / 8] = __builtin_bit_cast(uint16_t, s16);
+}
+
 // ------------------------------------------------------------------------------ measure
 
 // Σ (w − d)², Σ w² (float64) and max |w − d| of a matrix `w` against its decoded float32 `d`,
@@ -458,6 +516,23 @@ hipError_t encode_mx(const void* w, int in_type, int64_t rows, int K, uint8_t* q
 hipError_t encode_nvfp4(const void* w, int in_type, int64_t rows, int K, uint32_t* amax, uint8_t* codes,
                         uint8_t* scale, float* scale_2, unsigned long long* saturated, hipStream_t s) {
     return by_input<Nvfp4Run>(in_type, w, rows, K, amax, codes, scale, scale_2, saturated, s);
+}
+
+hipError_t encode_svdq_int4(const void* w, int in_type, const float* p, const void* down,
+                            const void* up, int rank, int64_t rows, int K, uint8_t* codes,
+                            uint16_t* scales, hipStream_t s) {
+    const int64_t chunks = rows * (K / 8);
+    if (chunks == 0) return hipSuccess;
+    const unsigned blocks = static_cast<unsigned>((chunks + kEncThreads - 1) / kEncThreads);
+    const auto* d = static_cast<const uint16_t*>(down);
+    const auto* u = static_cast<const uint16_t*>(up);
+    if (in_type == kNumF32)
+        encode_svdq_int4_kernel<kNumF32><<<blocks, kEncThreads, 0, s>>>(w, p, d, u, rank, codes, scales, chunks, K);
+    else if (in_type == kNumBf16)
+        encode_svdq_int4_kernel<kNumBf16><<<blocks, kEncThreads, 0, s>>>(w, p, d, u, rank, codes, scales, chunks, K);
+    else
+        encode_svdq_int4_kernel<kNumF16><<<blocks, kEncThreads, 0, s>>>(w, p, d, u, rank, codes, scales, chunks, K);
+    return hipGetLastError();
 }
 
 hipError_t measure(const void* w, int in_type, const float* d, int64_t total, double* partial, int parts,

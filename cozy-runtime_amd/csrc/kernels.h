@@ -184,6 +184,11 @@ hipError_t encode_mx(const void* w, int in_type, int64_t rows, int K, uint8_t* q
                      hipStream_t s);
 hipError_t encode_nvfp4(const void* w, int in_type, int64_t rows, int K, uint32_t* amax, uint8_t* codes,
                         uint8_t* scale, float* scale_2, unsigned long long* saturated, hipStream_t s);
+// svdq.int4g64: codes [rows, K/2] and fp16 group scales [rows, K/64] of (w − up·down) / p, up
+// [rows, rank] and down [rank, K] bf16, p [K] f32; K % 64 == 0.
+hipError_t encode_svdq_int4(const void* w, int in_type, const float* p, const void* down,
+                            const void* up, int rank, int64_t rows, int K, uint8_t* codes,
+                            uint16_t* scales, hipStream_t s);
 // [Σ(w − d)², Σ w², max |w − d|] in float64 into `out`, through `parts` float64 triples.
 hipError_t measure(const void* w, int in_type, const float* d, int64_t total, double* partial, int parts,
                    double* out, hipStream_t s);

@@ -312,6 +312,16 @@ int cozyq_encode_nvfp4(int device, const void* w, int w_type, uint8_t* codes, ui
                        float* scale_2, uint32_t* amax, unsigned long long* saturated, int64_t rows,
                        int K, void* stream);
 
+/* svdq.int4g64 weight producer (this build's W4A4 variant; the reference's svdq writer is
+ * tensorfs's, not in the reference): v = float32((w − up·down) / p) with the residual and the
+ * division in float64, then per 64-group s = fp16(amax|v| / 7) and codes clamp(rne(v / s), −8, 7)
+ * (0 where s == 0), two a byte with element 2k low: codes [rows, K/2], scales [rows, K/64] fp16.
+ * w [rows, K] f32 / bf16 / fp16 by w_type 0 / 1 / 2, p [K] f32, down [rank, K] and up [rows, rank]
+ * bf16. K % 64 == 0; w, down, codes and scales 16-byte aligned. */
+int cozyq_encode_svdq_int4(int device, const void* w, int w_type, const float* p, const void* down,
+                           const void* up, int rank, uint8_t* codes, uint16_t* scales, int64_t rows,
+                           int K, void* stream);
+
 /* What an encoding lost (reference: the measured acceptance facts of derive/microscale.py:64-110,
  * `sse`, `energy`, `max_abs_err`): out = [Σ(w − d)², Σ w², max |w − d|] in float64 over `total`
  * elements of w (w_type as above) against its float32 decode d, folded through `parts`

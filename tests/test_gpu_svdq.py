@@ -154,3 +154,29 @@ def test_svdq_c4_full_size_sampled_rows(ops):
     assert torch.equal(ascales.cpu().view(torch.int16), s.view(torch.int16))
     rows = torch.randperm(m, generator=_gen(8))[:64]
     assert_close(out.cpu()[rows], laws.svdq_exact(x[rows], p, codes, scales, down, up, bias))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "fp16"])
+@pytest.mark.parametrize("shape", [(3072, 3072, 32), (264, 1024, 16), (2, 64, 64), (40, 320, 0)],
+                         ids=lambda s: "x".join(map(str, s)))  # fmt: skip
+def test_svdq_int4_weight_encoder_bit_exact(shape, dtype):
+    """`encode.encode_svdq_int4` (the HIP producer the C4 bench builds its weight with) gives the
+    oracle producer's codes and fp16 scales bit for bit, from f32, bf16 and fp16 sources, with an
+    all-zero group (scale 0, codes 0) and rank 0; its measured loss is the dense decode's."""
+    from cozyq import encode
+
+    n, k, r = shape
+    gen = _gen(n + k + r)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(dtype)
+    w[0, :64] = 0
+    p = torch.rand(k, generator=gen) * 1.5 + 0.5
+    down = (torch.randn(r, k, generator=gen) * 0.02).to(torch.bfloat16)
+    up = (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16)
+    if r:
+        up[0] = 0  # row 0's first group stays all zero
+    enc = encode.encode_svdq_int4(torch, "w", w.to(DEV), p, down, up)
+    codes, scales = laws.svdq_weight(w.float(), p, down, up)
+    assert torch.equal(enc.payload.cpu(), codes)
+    assert torch.equal(enc.companions[0].raw.cpu().view(torch.int16), scales.view(torch.int16))
+    assert (enc.companions[0].raw[0, 0] == 0).item()
+    assert enc.energy > 0 and 0 < enc.relative_frobenius() < 0.2
