@@ -9,9 +9,10 @@
   library GEMM multiplies it (`torch.nn.functional.linear`, hipBLASLt), as the reference's
   cuBLAS call does.
 
-There is no W4A4 lane: gfx950's FP4 MFMA scales blocks of 32 by E8M0 exponents, which cannot hold
-nvfp4's E4M3 scales per 16, so a W4A4 product here would change the law. There is no eager lane
-either: operands off the GPU raise.
+Activations stay 16-bit here, as in the reference's nvfp4 leaf. The W4A4 form, where the
+activation is quantized to nvfp4 too, is svdq.nvfp4's (`cozyq.svdq_linear`): it decodes both
+operands exactly to fp16 on the way to the MFMA. There is no eager lane: operands off the GPU
+raise.
 """
 
 from __future__ import annotations
