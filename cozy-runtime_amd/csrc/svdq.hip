@@ -175,7 +175,7 @@ constexpr int kThreads = 256;                       // 4 waves, each a 64x64 qua
 constexpr int kStageGroups = 4;                     // 64-groups a stage brings in
 constexpr int kRowBytes = kStageGroups * 32;        // packed bytes of one tile row a stage: 128
 constexpr int kOpBytes = kTile * kRowBytes;         // one operand's stage: 16 KB
-constexpr int kScaleBytes = kStageGroups * kTile * 4;  // float32 scales [group][row]: 2 KB
+constexpr int kScaleBytes = kStageGroups * kTile * 2;  // fp16 scales [group][row]: 1 KB
 constexpr int kStageBytes = 2 * kOpBytes + 2 * kScaleBytes;
 constexpr int kStages = 2;
 constexpr uint32_t kOutOfRange = 0x80000000u;       // a buffer offset past num_records reads zeros
@@ -268,8 +268,6 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
     const int sglobal = (wside ? n0 : m0) + srow;
     const bool srow_ok = sglobal < (wside ? N : M);
     const uint16_t* sbase = (wside ? wscales : ascales) + static_cast<int64_t>(srow_ok ? sglobal : 0) * groups;
-    // (1/256 folds the two 16x code factors into the activation scale.)
-    const float sfactor = wside ? 1.0f : 0.00390625f;
 
 #define COZYQ_SVDQ_ISSUE(stage)                                                                     \
     do {                                                                                            \
@@ -291,11 +289,10 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
         }
     };
     auto store_scales = [&](int stage, const uint16_t* sv) {
-        float* dst = reinterpret_cast<float*>(lds + (stage & 1) * kStageBytes + 2 * kOpBytes +
-                                              (wside ? kScaleBytes : 0));
+        uint16_t* dst = reinterpret_cast<uint16_t*>(lds + (stage & 1) * kStageBytes + 2 * kOpBytes +
+                                                    (wside ? kScaleBytes : 0));
 #pragma unroll
-        for (int g = 0; g < kStageGroups; ++g)
-            dst[g * kTile + srow] = static_cast<float>(__builtin_bit_cast(_Float16, sv[g])) * sfactor;
+        for (int g = 0; g < kStageGroups; ++g) dst[g * kTile + srow] = sv[g];
     };
 
     // Accumulators start as the low-rank product la·upᵀ. Block (i, j) of the quadrant: lane l
@@ -322,6 +319,11 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
 #pragma unroll
                 for (int kk = 0; kk < kR / 16; ++kk)
                     facc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lv[i][kk], uv[j][kk], facc[i][j], 0, 0, 0);
+                // The K loop accumulates 256·(Σ q·q)·sa·sw (the codes enter as 16·q bytes), so
+                // the accumulators run in units of 1/256 until the epilogue; both scalings are
+                // exact.
+#pragma unroll
+                for (int r = 0; r < 16; ++r) facc[i][j][r] *= 256.0f;
             }
     }
 
@@ -337,30 +339,35 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
             aoff[i][g] = ra * kRowBytes + 16 * swz(ra, 2 * g + fq);
             boff[i][g] = kOpBytes + rb * kRowBytes + 16 * swz(rb, 2 * g + fq);
         }
-    // Scale addresses: the 16 activation rows of block i come in 4 runs of 4 consecutive rows.
-    const int sa_row = wm * 64 + 4 * fq;
+    // Scale addresses: a lane's row of block i (activation side) and column of block j (weight
+    // side) within the stage's fp16 scale rows.
+    const int sa_row = wm * 64 + fr;
     const int sw_col = wn * 64 + fr;
 
 // One group's int32 partial of a 32x32 block: two MFMAs over its two 32-code K halves.
 #define COZYQ_MMA(A, B)                                                                             \
     __builtin_amdgcn_mfma_i32_32x32x32_i8((A)[1], (B)[1],                                          \
         __builtin_amdgcn_mfma_i32_32x32x32_i8((A)[0], (B)[0], i32x16{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0), 0, 0, 0)
-// Row block I's 16 activation scales of group G (4 runs of 4 consecutive rows).
-#define COZYQ_SA(G, I, DST)                                                                         \
-    _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) {                                              \
-        const float4 f_ = *reinterpret_cast<const float4*>(sa_l + (G) * kTile + sa_row + 32 * (I) + 8 * q_); \
-        (DST)[4 * q_] = f_.x; (DST)[4 * q_ + 1] = f_.y; (DST)[4 * q_ + 2] = f_.z; (DST)[4 * q_ + 3] = f_.w; \
-    }
-#define COZYQ_SW(G, DST)                                                                            \
-    _Pragma("unroll") for (int j_ = 0; j_ < 2; ++j_) (DST)[j_] = sw_l[(G) * kTile + sw_col + 32 * j_];
+// The block's scale products sa[m]·sw[n] as one f16 MFMA with K = 1 (every other k is zero):
+// each product of two fp16 values is exact in float32, and lands where the block's partial does.
+#define COZYQ_T(SA, SB)                                                                             \
+    __builtin_amdgcn_mfma_f32_32x32x16_f16((SA), (SB), f32x16{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0)
 // (The empty asm holds the block's accumulators at this point of the program: without it the
 // arithmetic, which touches no memory, drifts past the scheduling fences below.)
-#define COZYQ_RESCALE(P, I, J, SA, SW)                                                              \
+#define COZYQ_RESCALE(P, T, I, J)                                                                   \
     do {                                                                                            \
         _Pragma("unroll") for (int r_ = 0; r_ < 16; ++r_)                                           \
-            facc[I][J][r_] = __builtin_fmaf(static_cast<float>((P)[r_]) * (SW), (SA)[r_], facc[I][J][r_]); \
+            facc[I][J][r_] = __builtin_fmaf(static_cast<float>((P)[r_]), (T)[r_], facc[I][J][r_]); \
         asm volatile("" : "+v"(facc[I][J]));                                                        \
     } while (0)
+
+    // One group's scale operands: element 0 of lane group 0 holds the row's (column's) scale;
+    // lane group 1's bits are masked to zero (no branch).
+    const uint32_t keep = fq == 0 ? 0xffffu : 0u;
+    auto scale_frag = [&](const uint16_t* base, int idx) {
+        const uint32_t bits = static_cast<uint32_t>(base[idx]) & keep;
+        return __builtin_bit_cast(f16x8, i32x4{static_cast<int32_t>(bits), 0, 0, 0});
+    };
 
     const int nstages = (groups + kStageGroups - 1) / kStageGroups;
     uint16_t sv[kStageGroups];
@@ -378,35 +385,34 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
             load_scales(s + 1, sv);
         }
         const uint8_t* buf = lds + (s & 1) * kStageBytes;
-        const float* sa_l = reinterpret_cast<const float*>(buf + 2 * kOpBytes);
-        const float* sw_l = reinterpret_cast<const float*>(buf + 2 * kOpBytes + kScaleBytes);
+        const uint16_t* sa_l = reinterpret_cast<const uint16_t*>(buf + 2 * kOpBytes);
+        const uint16_t* sw_l = reinterpret_cast<const uint16_t*>(buf + 2 * kOpBytes + kScaleBytes);
         // A stage past the last group holds zero codes and zero scales: it adds nothing.
         //
         // Each group runs as four segments that the scheduler may not reorder across: a
-        // segment issues the next block's two MFMAs and then rescales the block before it, so
-        // the matrix core works while the vector unit converts, and at most two int32 partials
-        // are live. The next group's fragments and scales are read from LDS two or three
-        // segments before their use.
+        // segment issues the next block's partial and scale-product MFMAs and then rescales the
+        // block before it (one conversion and one FMA an output), so the matrix core works
+        // while the vector unit rescales. The next group's fragments are read from LDS two or
+        // three segments before their use.
         i32x4 a[2][2], b[2][2];  // [block][K half], unpacked 16·code bytes
-        float sa0[16], sa1[16], sw[2];
         {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 unpack16(*reinterpret_cast<const i32x4*>(buf + aoff[i][0]), a[i][0], a[i][1]);
                 unpack16(*reinterpret_cast<const i32x4*>(buf + boff[i][0]), b[i][0], b[i][1]);
             }
-            COZYQ_SA(0, 0, sa0);
-            COZYQ_SW(0, sw);
         }
 #pragma unroll
         for (int g = 0; g < kStageGroups; ++g) {
             constexpr int kLast = kStageGroups - 1;
             i32x4 na[2], nb[2];
-            float swn[2];
-            // Segment A: blocks (0,0) and (0,1) issued; next fragments and row block 1's
-            // scales requested; (0,0) rescaled.
+            const f16x8 fa0 = scale_frag(sa_l, g * kTile + sa_row), fa1 = scale_frag(sa_l, g * kTile + sa_row + 32);
+            const f16x8 fb0 = scale_frag(sw_l, g * kTile + sw_col), fb1 = scale_frag(sw_l, g * kTile + sw_col + 32);
+            // Segment A: blocks (0,0) and (0,1) issued; next fragments requested; (0,0) rescaled.
             const i32x16 p00 = COZYQ_MMA(a[0], b[0]);
+            const f32x16 t00 = COZYQ_T(fa0, fb0);
             const i32x16 p01 = COZYQ_MMA(a[0], b[1]);
+            const f32x16 t01 = COZYQ_T(fa0, fb1);
             if (g < kLast) {
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
@@ -414,21 +420,17 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
                     nb[i] = *reinterpret_cast<const i32x4*>(buf + boff[i][g < kLast ? g + 1 : g]);
                 }
             }
-            COZYQ_SA(g, 1, sa1);
-            COZYQ_RESCALE(p00, 0, 0, sa0, sw[0]);
+            COZYQ_RESCALE(p00, t00, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             // Segment B: block (1,0) issued; (0,1) rescaled.
             const i32x16 p10 = COZYQ_MMA(a[1], b[0]);
-            COZYQ_RESCALE(p01, 0, 1, sa0, sw[1]);
+            const f32x16 t10 = COZYQ_T(fa1, fb0);
+            COZYQ_RESCALE(p01, t01, 0, 1);
             __builtin_amdgcn_sched_barrier(0);
-            // Segment C: block (1,1) issued; the next group's row block 0 and column scales
-            // requested; (1,0) rescaled.
+            // Segment C: block (1,1) issued; (1,0) rescaled.
             const i32x16 p11 = COZYQ_MMA(a[1], b[1]);
-            if (g < kLast) {
-                COZYQ_SA(g + 1, 0, sa0);
-                COZYQ_SW(g + 1, swn);
-            }
-            COZYQ_RESCALE(p10, 1, 0, sa1, sw[0]);
+            const f32x16 t11 = COZYQ_T(fa1, fb1);
+            COZYQ_RESCALE(p10, t10, 1, 0);
             __builtin_amdgcn_sched_barrier(0);
             // Segment D: the next group's fragments unpacked; (1,1) rescaled.
             if (g < kLast) {
@@ -438,11 +440,7 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
                     unpack16(nb[i], b[i][0], b[i][1]);
                 }
             }
-            COZYQ_RESCALE(p11, 1, 1, sa1, sw[1]);
-            if (g < kLast) {
-                sw[0] = swn[0];
-                sw[1] = swn[1];
-            }
+            COZYQ_RESCALE(p11, t11, 1, 1);
             __builtin_amdgcn_sched_barrier(0);
         }
         if (more) store_scales(s + 1, sv);
@@ -452,8 +450,7 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
     }
 #undef COZYQ_SVDQ_ISSUE
 #undef COZYQ_MMA
-#undef COZYQ_SA
-#undef COZYQ_SW
+#undef COZYQ_T
 #undef COZYQ_RESCALE
 
     // Epilogue: + bias, one cast, 2-byte stores (32 consecutive columns a row per instruction).
@@ -468,7 +465,7 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * fq + (r & 3);
                 if (m < M && n < N) {
-                    float v = facc[i][j][r];
+                    float v = facc[i][j][r] * 0.00390625f;  // out of the 1/256 units (exact)
                     if constexpr (kBias) v += bv;
                     out[static_cast<int64_t>(m) * N + n] = round_out<kOutHalf>(v);
                 }
