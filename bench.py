@@ -685,7 +685,8 @@ def bench_weights(torch, ops, lib, stream, steps: int) -> dict:
 def bench_nvfp4(torch, ops, lib, stream, steps: int) -> dict:
     """The nvfp4 W4A16 GEMV (`cozyq_nvfp4_gemv`) on config 3's weight shape (K=4096, N=14336:
     29.4 MB of E2M1 codes + 3.7 MB of tiled E4M3 scales, 0.56 bytes a weight) at M = 1 and 16,
-    over 8 rotating weight copies (265 MB, beyond the MALL), graph-replayed; bf16 in and out."""
+    over 8 rotating weight copies (265 MB, beyond the MALL), graph-replayed; bf16 in and out. Then
+    the routes past 16 rows against the reference's (`nvfp4_routes`)."""
     k, n, copies = 4096, 14336, 8
     gen = torch.Generator(device="cuda").manual_seed(97)
     tiled = (-(-n // 128) * 128) * (-(-(k // 16) // 4) * 4)
@@ -709,7 +710,41 @@ def bench_nvfp4(torch, ops, lib, stream, steps: int) -> dict:
         nbytes = n * k // 2 + tiled + m * k * 2 + m * n * 2
         out.append({"M": m, "K": k, "N": n, "us": us, "gbs": nbytes / (us * 1e-6) / 1e9,
                     "frac_hbm": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, "bytes": nbytes})
-    return {"nvfp4_w4a16_gemv": out}
+    return {"nvfp4_w4a16_gemv": out, "nvfp4_w4a16_routes": nvfp4_routes(torch, ops, weights[0], second, k, n)}
+
+
+def nvfp4_routes(torch, ops, weight, second, k: int, n: int) -> list:
+    """The nvfp4 leaf's routes past 16 rows against the reference's (decode the weight into x's
+    dtype with scale_2 folded in, `cozyq_decode`, then the library GEMM,
+    `internal/nvfp4_linear.py:376-385`): the GEMV at M = 32 and 48 on config 3's weight, and the
+    one-launch W4A16 GEMM (`cozyq_nvfp4_gemm`) at 4096 x 12288 x 3072. Medians of 15
+    interleaved samples."""
+    from cozyq import decode as dec
+
+    def rows(m, w, s, kk, nn):
+        x = _activations(torch, m, kk, 99)
+        decoded = torch.empty(nn, kk, dtype=torch.bfloat16, device="cuda")
+
+        def reference():
+            ops.decode_table(dec._CODE["u8"], w, s, dec._NUM["f8_e4m3fn"], decoded, nn, kk,
+                             grid=dec.GRID_BLOCKS, block=16, tiled=True, scale_2=second)  # fmt: skip
+            torch.nn.functional.linear(x, decoded)
+
+        mine = (lambda: ops.nvfp4_gemv(x, w, s, second, torch.bfloat16)) if m <= 64 else \
+            (lambda: ops.nvfp4_gemm(x, w, s, second, None, torch.bfloat16))
+        preroll(torch, reference, 30)
+        med = Timer(torch).interleaved({"cozyq": mine, "decode_blas": reference}, batch=8)
+        return {"M": m, "K": kk, "N": nn, "kernel": "nvfp4_gemv_kernel" if m <= 64 else "nvfp4_gemm_kernel<W4A16>",
+                "us": med["cozyq"]["ms"] * 1e3, "decode_blas_us": med["decode_blas"]["ms"] * 1e3,
+                "tflops": 2.0 * m * nn * kk / (med["cozyq"]["ms"] * 1e-3) / 1e12}
+
+    out = [rows(m, weight[0], weight[1], k, n) for m in (32, 48)]
+    gk, gn = 3072, 12288
+    gen = torch.Generator(device="cuda").manual_seed(96)
+    gw = torch.randint(0, 256, (gn, gk // 2), generator=gen, device="cuda", dtype=torch.int32).to(torch.uint8)
+    gs = torch.randint(0x30, 0x48, (gn * gk // 16,), generator=gen, device="cuda", dtype=torch.int32).to(torch.uint8)
+    out.append(rows(4096, gw, gs, gk, gn))
+    return out
 
 
 def bench_bake(torch, ops, lib, stream, steps: int) -> dict:

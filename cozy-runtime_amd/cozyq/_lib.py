@@ -98,6 +98,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_int, _P, c_int, c_int64, c_int64, _P],
     ),
     "cozyq_nvfp4_gemv": (c_int, [c_int, _P, c_int, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P]),
+    "cozyq_nvfp4_gemm": (c_int, [c_int, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P]),
     "cozyq_encode_int8_convrot": (c_int, [c_int, _P, c_int, _P, _P, c_int64, c_int, _P]),
     "cozyq_encode_w4a8": (c_int, [c_int, _P, c_int, _P, _P, _P, _P, c_int64, c_int, _P]),
     "cozyq_encode_fp8_rowwise": (c_int, [c_int, _P, c_int, _P, _P, c_int64, c_int, _P]),

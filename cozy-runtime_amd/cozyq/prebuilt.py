@@ -581,15 +581,16 @@ class Prebuilt:
 
     def nvfp4_gemv(self, x: Tensor, weight: Tensor, blocked_scale: Tensor, scale_2: Tensor,
                    out_dtype: Dtype) -> Tensor:
-        """`cozyq_nvfp4_gemv` (the `_gemv` path of `internal/nvfp4_linear.py:126-201`): up to 16
-        bf16/fp16 rows against packed E2M1 codes [N, K/2] (low nibble first), E4M3 scales in
-        cuBLAS's 128x4 tiles and a float32 second level; out [M, N] in `out_dtype` (bf16/fp16)."""
+        """`cozyq_nvfp4_gemv` (the `_gemv` path of `internal/nvfp4_linear.py:126-201`, and the
+        decode + GEMM path of `:376-385` up to 64 rows): up to 64 bf16/fp16 rows against packed
+        E2M1 codes [N, K/2] (low nibble first), E4M3 scales in cuBLAS's 128x4 tiles and a float32
+        second level; out [M, N] in `out_dtype` (bf16/fp16)."""
         torch = self.torch
         flat = x.reshape(-1, x.shape[-1])
         rows, cols = int(flat.shape[0]), int(flat.shape[1])
         n = int(weight.shape[0])
-        if rows > 16 or cols % 32 or 2 * int(weight.shape[1]) != cols:
-            raise ValueError(f"nvfp4 GEMV: up to 16 rows and K % 32 == 0 matching the weight's "
+        if rows > 64 or cols % 32 or 2 * int(weight.shape[1]) != cols:
+            raise ValueError(f"nvfp4 GEMV: up to 64 rows and K % 32 == 0 matching the weight's "
                              f"{2 * int(weight.shape[1])} columns; got [{rows}, {cols}]")  # fmt: skip
         flat = flat if flat.is_contiguous() and flat.data_ptr() % 16 == 0 else flat.contiguous().clone()
         out = torch.empty(rows, n, dtype=out_dtype, device=x.device)
@@ -599,6 +600,33 @@ class Prebuilt:
             rows, n, cols, self._stream(),
         )  # fmt: skip
         self._check(code, "the nvfp4 GEMV")
+        return out
+
+    def nvfp4_gemm(self, x: Tensor, weight: Tensor, blocked_scale: Tensor, scale_2: Tensor,
+                   bias: Tensor | None, out_dtype: Dtype) -> Tensor:
+        """`cozyq_nvfp4_gemm` (the decode-then-GEMM path of `internal/nvfp4_linear.py:376-385` as
+        one kernel): bf16/fp16 rows against `nvfp4_gemv`'s operands, W decoded exactly into x's
+        dtype on the matrix core, × scale_2 (+ bias) in the epilogue; K % 64 == 0, N % 8 == 0."""
+        torch = self.torch
+        flat = x.reshape(-1, x.shape[-1])
+        rows, cols = int(flat.shape[0]), int(flat.shape[1])
+        n = int(weight.shape[0])
+        if cols % 64 or n % 8 or 2 * int(weight.shape[1]) != cols:
+            raise ValueError(f"nvfp4 GEMM: K % 64 == 0 and N % 8 == 0 matching the weight's "
+                             f"[{n}, {2 * int(weight.shape[1])}]; got [{rows}, {cols}]")  # fmt: skip
+        if int(blocked_scale.numel()) < -(-n // 128) * 128 * (cols // 16):
+            raise ValueError("nvfp4 GEMM: block scales must cover whole 128-row tiles")
+        flat = flat if flat.is_contiguous() and flat.data_ptr() % 16 == 0 else flat.contiguous().clone()
+        weight, blocked_scale = _aligned(weight), _aligned(blocked_scale)
+        if bias is not None:
+            bias = _aligned(bias.to(out_dtype))
+        out = torch.empty(rows, n, dtype=out_dtype, device=x.device)
+        code = self._lib.cozyq_nvfp4_gemm(
+            self.index, flat.data_ptr(), self._half(flat.dtype), weight.data_ptr(),
+            blocked_scale.data_ptr(), scale_2.data_ptr(), None if bias is None else bias.data_ptr(),
+            out.data_ptr(), self._half(out_dtype), rows, n, cols, self._stream(),
+        )  # fmt: skip
+        self._check(code, "the nvfp4 GEMM")
         return out
 
     # -------------------------------------------------------------- stored-format decode

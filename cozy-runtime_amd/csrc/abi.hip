@@ -423,18 +423,32 @@ int cozyq_decode_svdq(int device, const uint8_t* w, const uint8_t* scale, int ti
 
 int cozyq_nvfp4_gemv(int device, const void* x, int x_half, const uint8_t* w, const uint8_t* scale,
                      const float* scale_2, void* out, int out_half, int M, int N, int K, void* stream) {
-    if (M < 0 || M > 16 || N < 1 || K < 32 || K % 32 || K > cozyq::kMaxK || !x || !w || !scale ||
-        !scale_2 || !out)
+    if (M < 0 || M > 64 || N < 1 || K < 32 || K % 32 || K > cozyq::kMaxK || !w || !scale || !scale_2)
         return hipErrorInvalidValue;
     if (static_cast<int64_t>(N) * (K / 2) >= 0x7fffffff ||
         static_cast<int64_t>((N + 127) / 128 * 128) * ((K / 16 + 3) / 4 * 4) >= 0x7fffffff)
         return hipErrorNotSupported;
-    if (M == 0) return hipSuccess;
-    if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & 3) || (reinterpret_cast<uintptr_t>(out) & 1))
+    if (M == 0) return hipSuccess;  // an empty x may have no address
+    if (!x || !out || !aligned16(x) || (reinterpret_cast<uintptr_t>(w) & 3) || (reinterpret_cast<uintptr_t>(out) & 1))
         return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
     return cozyq::nvfp4_gemv(x, x_half != 0, w, scale, scale_2, out, out_half != 0, M, N, K, on(stream));
+}
+
+int cozyq_nvfp4_gemm(int device, const void* x, int x_half, const uint8_t* w, const uint8_t* scale,
+                     const float* scale_2, const void* bias, void* out, int out_half, int M, int N, int K,
+                     void* stream) {
+    if (M < 0 || N < 8 || N % 8 || !fits(K, 64) || !w || !scale || !scale_2) return hipErrorInvalidValue;
+    if (static_cast<int64_t>(N) * (K / 2) >= 0x7fffffff ||
+        static_cast<int64_t>((N + 127) / 128 * 128) * (K / 16) >= 0x7fffffff)
+        return hipErrorNotSupported;
+    if (M == 0) return hipSuccess;  // an empty x may have no address
+    if (!x || !out || !aligned16(x) || !aligned16(w) || !aligned16(scale) || !aligned16(out) || !aligned16(bias))
+        return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::nvfp4_gemm(x, x_half != 0, w, scale, scale_2, bias, out, out_half != 0, M, N, K, on(stream));
 }
 
 int cozyq_encode_int8_convrot(int device, const void* w, int w_type, int8_t* q, float* scale,

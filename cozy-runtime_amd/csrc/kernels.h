@@ -167,10 +167,16 @@ hipError_t decode_convrot(const int8_t* w, const void* scale, int scale_type, vo
                           int64_t rows, int64_t cols, int digits, hipStream_t s);
 hipError_t decode_svdq(const SvdqDecode& a, int out_type, hipStream_t s);
 
-// nvfp4 W4A16 GEMV (nvfp4.hip): out [M, N] = round((x [M, K] · decode(w)ᵀ) · scale_2), M ≤ 16,
+// nvfp4 W4A16 GEMV (nvfp4.hip): out [M, N] = round((x [M, K] · decode(w)ᵀ) · scale_2), M ≤ 64,
 // codes [N, K/2] low nibble first, E4M3 scales in cuBLAS's 128x4 tiles, K % 32 == 0.
 hipError_t nvfp4_gemv(const void* x, bool x_half, const uint8_t* w, const uint8_t* scale, const float* scale_2,
                       void* out, bool out_half, int M, int N, int K, hipStream_t s);
+
+// nvfp4 W4A16 GEMM (svdq_nvfp4.hip), 256x256 tiles: out [M, N] = round((x · decode(w)ᵀ) · scale_2
+// + bias), W decoded exactly into x's dtype on the way to the MFMA; the same operands as
+// nvfp4_gemv, K % 64 == 0, N % 8 == 0; bias [N] in out's dtype or null.
+hipError_t nvfp4_gemm(const void* x, bool x_half, const uint8_t* w, const uint8_t* scale, const float* scale_2,
+                      const void* bias, void* out, bool out_half, int M, int N, int K, hipStream_t s);
 
 // Weight encoders (encode.hip), input float32 / bf16 / fp16 by `in_type` (kNumF32 .. kNumF16),
 // row-major [rows, K]. encode_rotated: int8.convrot (q, scale) or, with w4, w4a8.convrot (codes

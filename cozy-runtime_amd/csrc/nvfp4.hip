@@ -12,6 +12,8 @@
 // The eight waves' partial sums meet in LDS and are added in wave order, so a row's result does
 // not depend on M or on the rows beside it. Every global read is a bounded buffer load: rows past
 // N or M read zeros.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -64,18 +66,21 @@ __device__ __forceinline__ f32x4 mfma16(i32x4 a, i32x4 b, f32x4 c) {
 }
 
 // kXHalf: activations (and the weights fed beside them) fp16, else bf16; kOutHalf likewise.
+// kMB: 16-row activation blocks (M ≤ 16·kMB), each its own MFMA against the same decoded weights.
 // A macro step is 128 columns: a lane loads 16 bytes of its row's codes (32 weights, columns
 // 128t + 32·sub ..), the two E4M3 scales that cover them (adjacent bytes of a 128x4 tile, as
-// the first block is even) and its activation row's 32 matching columns, and feeds 4 MFMAs,
-// MFMA j taking columns 128t + 32·sub + 8j .. + 8 on both sides: every lane group pairs the
-// same columns of A and B, so the four products add up to the 128-column dot product.
-template <bool kXHalf, bool kOutHalf>
+// the first block is even) and, from each block, its activation row's 32 matching columns, and
+// feeds 4 MFMAs a block, MFMA j taking columns 128t + 32·sub + 8j .. + 8 on both sides: every
+// lane group pairs the same columns of A and B, so the four products add up to the 128-column
+// dot product. A block's MFMAs and sums are the same whatever kMB is, so a row's result does
+// not depend on M.
+template <bool kXHalf, bool kOutHalf, int kMB>
 __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint16_t* __restrict__ x,
                                                                      const uint8_t* __restrict__ w,
                                                                      const uint8_t* __restrict__ scale,
                                                                      const float* __restrict__ scale_2,
                                                                      uint16_t* __restrict__ out, int M, int N, int K) {
-    __shared__ f32x4 partial[kGemvWaves][64];
+    __shared__ f32x4 partial[kGemvWaves][kMB][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // A workgroup's 16 rows are 32q + 4j + p (q, p = 0..3) of a 128-row tile block: the four
     // 16-byte scale chunks of rows 4j .. 4j + 3 hold those 16 rows' scales, so a tile's bytes are
@@ -90,14 +95,18 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
     const __amdgpu_buffer_rsrc_t xr = bounded_rsrc(x, static_cast<int64_t>(M) * K * 2);
     // Rows past N read past the codes' end (zeros); rows past M read past x's end (zeros).
     const int code_row = row < N ? row : N;
-    const int x_row = (lane & 15) < M ? (lane & 15) : M;
+    int x_row[kMB];
+#pragma unroll
+    for (int b = 0; b < kMB; ++b) x_row[b] = 16 * b + (lane & 15) < M ? 16 * b + (lane & 15) : M;
     const int64_t code_base = static_cast<int64_t>(code_row) * (K / 2);
     const int tile_row = (row >> 7) * col_tiles, in_tile = (row & 31) * 16 + ((row & 127) >> 5) * 4;
 
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[kMB];
+#pragma unroll
+    for (int b = 0; b < kMB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int macro = K / 128;  // whole macro steps; a 32..96-column tail is handled below
     for (int t0 = wave; t0 < macro; t0 += kGemvWaves * kStepsAhead) {
-        i32x4 code[kStepsAhead], xv[kStepsAhead][4];
+        i32x4 code[kStepsAhead], xv[kStepsAhead][kMB][4];
         uint32_t sbyte[kStepsAhead];
 #pragma unroll
         for (int j = 0; j < kStepsAhead; ++j) {
@@ -109,18 +118,24 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
                 wr, live ? static_cast<int>(code_base + k / 2) : 0x7ffffff0, 0, 0));
             const int sidx = row < N && live ? ((tile_row + (b >> 2)) * 512 + in_tile + (b & 3)) : 0x7ffffff0;
             sbyte[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, sidx, 0, 0);
-            const int xo = live ? static_cast<int>((static_cast<int64_t>(x_row) * K + k) * 2) : 0x7fffff00;
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                xv[j][q] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                    xr, xo + 16 * q, 0, 0));
+            for (int mb = 0; mb < kMB; ++mb) {
+                const int xo = live ? static_cast<int>((static_cast<int64_t>(x_row[mb]) * K + k) * 2) : 0x7fffff00;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    xv[j][mb][q] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                        xr, xo + 16 * q, 0, 0));
+            }
         }
 #pragma unroll
         for (int j = 0; j < kStepsAhead; ++j) {
             const float s0 = e4m3_value(sbyte[j] & 0xffu), s1 = e4m3_value((sbyte[j] >> 8) & 0xffu);
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                acc = mfma16<kXHalf>(weights8<kXHalf>(static_cast<uint32_t>(code[j][q]), q < 2 ? s0 : s1), xv[j][q], acc);
+            for (int q = 0; q < 4; ++q) {
+                const i32x4 wq = weights8<kXHalf>(static_cast<uint32_t>(code[j][q]), q < 2 ? s0 : s1);
+#pragma unroll
+                for (int mb = 0; mb < kMB; ++mb) acc[mb] = mfma16<kXHalf>(wq, xv[j][mb][q], acc[mb]);
+            }
         }
     }
     // A tail of 1..3 32-column steps past the last whole macro step, one per wave.
@@ -131,22 +146,29 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
         const uint32_t c = __builtin_amdgcn_raw_buffer_load_b32(wr, static_cast<int>(code_base + k / 2), 0, 0);
         const int sidx = row < N ? ((tile_row + (b >> 2)) * 512 + in_tile + (b & 3)) : 0x7fffffff;
         const uint32_t sb = __builtin_amdgcn_raw_buffer_load_b8(sr, sidx, 0, 0);
-        const i32x4 xt = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
-            xr, static_cast<int>((static_cast<int64_t>(x_row) * K + k) * 2), 0, 0));
-        acc = mfma16<kXHalf>(weights8<kXHalf>(c, e4m3_value(sb)), xt, acc);
+        const i32x4 wq = weights8<kXHalf>(c, e4m3_value(sb));
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb) {
+            const i32x4 xt = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                xr, static_cast<int>((static_cast<int64_t>(x_row[mb]) * K + k) * 2), 0, 0));
+            acc[mb] = mfma16<kXHalf>(wq, xt, acc[mb]);
+        }
     }
-    partial[wave][lane] = acc;
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb) partial[wave][mb][lane] = acc[mb];
     __syncthreads();
-    if (wave != 0) return;
-    f32x4 sum = partial[0][lane];
+    // Wave mb < kMB adds block mb's eight partial sums, in wave order.
+    if (wave >= kMB) return;
+    const int mb = wave;
+    f32x4 sum = partial[0][mb][lane];
 #pragma unroll
     for (int v = 1; v < kGemvWaves; ++v) {
-        const f32x4 p = partial[v][lane];
+        const f32x4 p = partial[v][mb][lane];
         sum = f32x4{sum[0] + p[0], sum[1] + p[1], sum[2] + p[2], sum[3] + p[3]};
     }
     // D[i][m]: lane holds MFMA rows 4·(lane/16) + r of column m = lane % 16.
     const float g = scale_2[0];
-    const int m = lane & 15;
+    const int m = 16 * mb + (lane & 15);
     if (m >= M) return;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -162,14 +184,24 @@ hipError_t nvfp4_gemv(const void* x, bool x_half, const uint8_t* w, const uint8_
     const dim3 grid((N + 127) / 128 * 8), block(64 * kGemvWaves);
     const auto* xp = static_cast<const uint16_t*>(x);
     auto* op = static_cast<uint16_t*>(out);
-    if (x_half) {
-        if (out_half) hipLaunchKernelGGL((nvfp4_gemv_kernel<true, true>), grid, block, 0, s, xp, w, scale, scale_2, op, M, N, K);
-        else hipLaunchKernelGGL((nvfp4_gemv_kernel<true, false>), grid, block, 0, s, xp, w, scale, scale_2, op, M, N, K);
-    } else {
-        if (out_half) hipLaunchKernelGGL((nvfp4_gemv_kernel<false, true>), grid, block, 0, s, xp, w, scale, scale_2, op, M, N, K);
-        else hipLaunchKernelGGL((nvfp4_gemv_kernel<false, false>), grid, block, 0, s, xp, w, scale, scale_2, op, M, N, K);
-    }
-    return hipGetLastError();
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, block, 0, s, xp, w, scale, scale_2, op, M, N, K);
+        return hipGetLastError();
+    };
+    auto blocks = [&](auto xh, auto oh) {
+        constexpr bool kX = decltype(xh)::value, kO = decltype(oh)::value;
+        switch ((M + 15) / 16) {
+            case 1: return go(nvfp4_gemv_kernel<kX, kO, 1>);
+            case 2: return go(nvfp4_gemv_kernel<kX, kO, 2>);
+            case 3: return go(nvfp4_gemv_kernel<kX, kO, 3>);
+            case 4: return go(nvfp4_gemv_kernel<kX, kO, 4>);
+            default: return hipErrorInvalidValue;
+        }
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    if (x_half) return out_half ? blocks(T{}, T{}) : blocks(T{}, F{});
+    return out_half ? blocks(F{}, T{}) : blocks(F{}, F{});
 }
 
 }  // namespace cozyq

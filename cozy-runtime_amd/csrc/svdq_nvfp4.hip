@@ -243,9 +243,23 @@ __device__ __forceinline__ RowScales row_scales(uint32_t sb) {
                      __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb, 1.0f, true)};
 }
 
+// The LDS byte address of a pointer into this workgroup's LDS.
+__device__ __forceinline__ uint32_t lds_address(const uint8_t* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t*)p));
+}
+
+// 16 bytes into LDS by a write the compiler does not count. It waits for every LDS-DMA in flight
+// (vmcnt 0) before an LDS write it cannot tell apart from their targets; the W4A16 GEMM writes
+// its decoded W while x's lines of the next pair are still landing elsewhere. Younger LDS
+// operations the compiler does not know of only make its own lgkmcnt waits stricter.
+__device__ __forceinline__ void lds_write16(uint8_t* p, uint4 v) {
+    asm volatile("ds_write_b128 %0, %1" ::"v"(lds_address(p)), "v"(__builtin_bit_cast(i32x4, v)) : "memory");
+}
+
 // Chunk c (0..7) of a buffer row — elements 8c..8c+7, code dword c, 16-block c/2 — decoded to
 // fp16 (E2M1 at unit scale, times the block's scale) and written at its swizzled place in LDS
 // row r.
+template <bool kUncounted = false>
 __device__ __forceinline__ void put_chunk(uint8_t* row, int r, int c, uint32_t dw, const RowScales& s) {
     const _Float16 sc = (c >> 1) == 0 ? s.lo[0] : (c >> 1) == 1 ? s.lo[1] : (c >> 1) == 2 ? s.hi[0] : s.hi[1];
     const f16x2 s2 = {sc, sc};
@@ -253,9 +267,12 @@ __device__ __forceinline__ void put_chunk(uint8_t* row, int r, int c, uint32_t d
     const f16x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 1.0f, 1) * s2;
     const f16x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 1.0f, 2) * s2;
     const f16x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 1.0f, 3) * s2;
-    *reinterpret_cast<uint4*>(row + 16 * swz(r, c)) =
-        make_uint4(__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
-                   __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3));
+    const uint4 v = make_uint4(__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                               __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3));
+    if constexpr (kUncounted)
+        lds_write16(row + 16 * swz(r, c), v);
+    else
+        *reinterpret_cast<uint4*>(row + 16 * swz(r, c)) = v;
 }
 
 __device__ __forceinline__ uint32_t dword_of(const uint4& a, const uint4& b, int c) {
@@ -264,19 +281,86 @@ __device__ __forceinline__ uint32_t dword_of(const uint4& a, const uint4& b, int
     return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
 }
 
-__device__ __forceinline__ f16x8 as_half8(const i32x8& v, int h) {
-    return __builtin_bit_cast(f16x8, half_of(v, h));
+// A wave's fill of its W4A16 stage slots by LDS-DMA: each lane's 32 code bytes from `codes` at
+// `co` and its scale dword from `scales` at `so`.
+__device__ __forceinline__ void fill_stage(uint8_t* st, __amdgpu_buffer_rsrc_t codes, uint32_t co,
+                                           __amdgpu_buffer_rsrc_t scales, uint32_t so) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(codes, (LdsPtr*)st, 16, co, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(codes, (LdsPtr*)(st + 1024), 16, co + 16, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(scales, (LdsPtr*)(st + 2048), 4, so, 0, 0, 0);
 }
 
-// One 256x256 output tile per workgroup. c (f32 [N]) and bias may be null.
-template <bool kOutHalf>
+// A lane's slots of a W4A16 stage (its 32 code bytes at 16·lane and 1024 + 16·lane, its scale
+// dword at 2048 + 4·lane), read by uncounted LDS reads that complete before it returns.
+__device__ __forceinline__ void read_stage(const uint8_t* st, int lane, uint4& lo, uint4& hi, uint32_t& sc) {
+    const uint32_t a = lds_address(st);
+    i32x4 l, h;
+    asm volatile("ds_read_b128 %0, %3\n\t"
+                 "ds_read_b128 %1, %3 offset:1024\n\t"
+                 "ds_read_b32 %2, %4 offset:2048\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(l), "=&v"(h), "=&v"(sc)
+                 : "v"(a + 16 * lane), "v"(a + 4 * lane)
+                 : "memory");
+    lo = __builtin_bit_cast(uint4, l);
+    hi = __builtin_bit_cast(uint4, h);
+}
+
+// The W4A16 form's decode into bf16 (x in bf16): E2M1 at unit scale in float32, times the
+// block's scale (float32, exact), packed to bf16 (exact: at most 6 significant bits); an
+// uncounted write, as the W4A16 GEMM's decode needs.
+__device__ __forceinline__ void put_chunk_bf16(uint8_t* row, int r, int c, uint32_t dw, float sc) {
+    const int w = static_cast<int>(dw);
+    const f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+    const f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+    const f32x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+    const f32x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+    lds_write16(row + 16 * swz(r, c),
+                make_uint4(round2<false>(v0[0] * sc, v0[1] * sc), round2<false>(v1[0] * sc, v1[1] * sc),
+                           round2<false>(v2[0] * sc, v2[1] * sc), round2<false>(v3[0] * sc, v3[1] * sc)));
+}
+
+template <bool kBf16>
+__device__ __forceinline__ f32x16 mfma16x(const i32x8& a, const i32x8& b, int h, f32x16 c) {
+    if constexpr (kBf16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, half_of(a, h)),
+                                                       __builtin_bit_cast(bf16x8, half_of(b, h)), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, half_of(a, h)),
+                                                      __builtin_bit_cast(f16x8, half_of(b, h)), c, 0, 0, 0);
+}
+
+// A wave's 8 LDS-DMA loads of one buffer's 16-bit A rows (gemm_tile.h's COZYQ_ISSUE for one
+// operand): load j fills the 1 KiB at (4j + wave)·1024 from row offsets rowoff[j] + k0.
+__device__ __forceinline__ void issue_lines(__amdgpu_buffer_rsrc_t rsrc, uint8_t* buf, const int (&rowoff)[8],
+                                            const int (&chunk)[8], int k0, int row_bytes, int wave) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t off = (k0 + chunk[j] < row_bytes) ? static_cast<uint32_t>(rowoff[j] + k0) : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LdsPtr*)(buf + (4 * j + wave) * 1024), 16, off, 0, 0, 0);
+    }
+}
+
+enum NvMode { kW4A4 = 0, kW4A16 = 1 };
+// kW4A16 stages W's codes and scales by LDS-DMA past the tile's buffers, each thread its own
+// row: a wave's two 1 KiB code loads and its 256-byte scale load, two stages.
+constexpr int kCodeWave = 2 * 1024 + 256, kCodeStage = 4 * kCodeWave;
+
+// One 256x256 output tile per workgroup.
+// kW4A4 (svdq.nvfp4): A is the activation's nvfp4 operand (codes + row-major E4M3 scales), both
+// operands decoded to fp16; out = (A·Wᵀ)·gx·gw·c + la·upᵀ + bias. c and bias may be null.
+// kW4A16 (nvfp4, x 16-bit): A is x itself ([M, K] bf16, or fp16 with kXHalf), brought by LDS-DMA;
+// W's E4M3 scales sit in cuBLAS's 128x4 tiles; W is decoded into x's dtype; out = (x·Wᵀ)·gw
+// (+ bias). gx, cs, la, up unused.
+template <int kMode, bool kXHalf, bool kOutHalf>
 __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ As, const uint8_t* __restrict__ W,
     const uint8_t* __restrict__ Ws, const float* __restrict__ gx, const float* __restrict__ gw,
     const float* __restrict__ cs, const uint16_t* __restrict__ la, const uint16_t* __restrict__ up,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K, int R,
     int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
+    constexpr bool kBf16 = kMode == kW4A16 && !kXHalf;  // the MFMA and W's decoded type
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes + (kMode == kW4A16 ? 2 * kCodeStage : 0)];
     const int2 t = launch_tile(blockIdx.x, tiles_m, tiles_n);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -290,17 +374,28 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
     };
     const int half_k = K / 2, blocks_k = K / 16;
-    const auto ar = rows_view(A + static_cast<int64_t>(m0) * half_k, M - m0, half_k);
+    const int np = K / 64;  // buffers: 64 elements of K each
+    // A: nvfp4 codes and scales (kW4A4) or x's 2K-byte rows (kW4A16).
+    const int arow_bytes = kMode == kW4A4 ? half_k : 2 * K;
+    const auto ar = rows_view(A + static_cast<int64_t>(m0) * arow_bytes, M - m0, arow_bytes);
     const auto asr = rows_view(As + static_cast<int64_t>(m0) * blocks_k, M - m0, blocks_k);
     const auto wr = rows_view(W + static_cast<int64_t>(n0) * half_k, N - n0, half_k);
-    const auto wsr = rows_view(Ws + static_cast<int64_t>(n0) * blocks_k, N - n0, blocks_k);
-    const int np = K / 64;  // buffers: 64 elements of K each
+    // W's scales: row-major [N, K/16] (kW4A4) or in 128x4 tiles of 512 bytes, K/64 tiles a row of
+    // tiles; a row's four block scales of a buffer are one aligned dword of its tile.
+    const int col_tiles = K / 64;
+    const int64_t tiled_rows = (static_cast<int64_t>(N) + 127) / 128 * 128;
+    const auto wsr = kMode == kW4A4
+        ? rows_view(Ws + static_cast<int64_t>(n0) * blocks_k, N - n0, blocks_k)
+        : rows_view(Ws + static_cast<int64_t>(n0 / 128) * col_tiles * 512,
+                    static_cast<int>(tiled_rows - n0), 4 * col_tiles);
+    const int n_in = tid;  // the thread's W row within the tile
+    const uint32_t tiled_row = static_cast<uint32_t>((n_in >> 7) * col_tiles * 512 + (n_in & 31) * 16 + ((n_in & 127) >> 5) * 4);
 
     // The epilogue's column operands into LDS ahead of the K loop: c (f32) and the bias (two a
     // lane), for the tile's 256 columns; past N they read as zeros.
     {
         const int cc = 64 * wave + lane;
-        if (cs != nullptr) {
+        if (kMode == kW4A4 && cs != nullptr) {
             const auto cr = rows_view(cs + n0, N - n0, 4);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(cr, (LdsPtr*)(lds + kWsOff + 256 * wave), 4, 4 * cc, 0, 0, 0);
         }
@@ -310,36 +405,100 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         }
     }
 
-    // Staging: thread t carries tile row t of A and of W for one buffer.
-    const uint32_t crow = static_cast<uint32_t>(tid * half_k), srow = static_cast<uint32_t>(tid * blocks_k);
-    uint4 xa0, xa1, wa0, wa1;
-    uint32_t xsb, wsb;
-    auto load = [&](int pair) {
-        const uint32_t co = crow + 32 * pair, so = srow + 4 * pair;
-        xa0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, co, 0, 0));
-        xa1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, co + 16, 0, 0));
-        wa0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, co, 0, 0));
-        wa1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, co + 16, 0, 0));
-        xsb = __builtin_amdgcn_raw_buffer_load_b32(asr, so, 0, 0);
-        wsb = __builtin_amdgcn_raw_buffer_load_b32(wsr, so, 0, 0);
-    };
-    // Chunk q (0..15) of the thread's two rows of a buffer: the A row's chunks, then W's.
-    auto put = [&](uint8_t* buf, int q, const RowScales& xsc, const RowScales& wsc) {
-        if (q < 8)
-            put_chunk(buf + tid * kPairK, tid, q, dword_of(xa0, xa1, q), xsc);
-        else
-            put_chunk(buf + kOpBytes + tid * kPairK, tid, q - 8, dword_of(wa0, wa1, q - 8), wsc);
-    };
-    auto store = [&](int pair) {
-        uint8_t* buf = lds + (pair & 1) * kPairBytes;
-        const RowScales xsc = row_scales(xsb), wsc = row_scales(wsb);
+    // kW4A16: x's rows by LDS-DMA in whole 128-byte lines, as gemm_tile.h's operands: load j (0..7)
+    // of a wave fills rows (4j + wave)·8 + l/8 of the buffer's A half, physical chunk l%8.
+    int xrowoff[8], xchunk[8];
 #pragma unroll
-        for (int q = 0; q < 16; ++q) put(buf, q, xsc, wsc);
+    for (int j = 0; j < 8; ++j) {
+        const int r = (4 * j + wave) * 8 + (lane >> 3);
+        xchunk[j] = 16 * swz(r, lane & 7);
+        xrowoff[j] = r * arow_bytes + xchunk[j];
+    }
+    auto issue_x = [&](int pair) {
+        if constexpr (kMode == kW4A16) issue_lines(ar, lds + (pair & 1) * kPairBytes, xrowoff, xchunk, pair * kPairK, arow_bytes, wave);
+    };
+
+    // Staging: thread t carries tile row t of W (and of A's codes, kW4A4) for a buffer. kW4A4
+    // loads it into registers; kW4A16 into its own slots of stage `pair % 2` past the buffers,
+    // two pairs ahead of the decode, and reads it back itself (no barrier: its own loads).
+    constexpr bool kDeep = kMode == kW4A16;
+    struct Regs {
+        uint4 xa0, xa1, wa0, wa1;
+        uint32_t xsb, wsb;
+    };
+    const uint32_t crow = static_cast<uint32_t>(tid * half_k), srow = static_cast<uint32_t>(tid * blocks_k);
+    Regs regs{make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), 0u, 0u};
+    auto stage_of = [&](int pair) { return lds + kLdsBytes + (pair & 1) * kCodeStage + wave * kCodeWave; };
+    // Past the last pair the offsets run past the buffers (zeros) or into later rows: what they
+    // bring is decoded into a buffer nothing reads.
+    auto load = [&](int pair) {
+        const uint32_t co = crow + 32 * pair;
+        if constexpr (kDeep) {
+            fill_stage(stage_of(pair), wr, co, wsr, tiled_row + 512 * pair);
+        } else {
+            const uint32_t so = srow + 4 * pair;
+            regs.wa0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, co, 0, 0));
+            regs.wa1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, co + 16, 0, 0));
+            regs.xa0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, co, 0, 0));
+            regs.xa1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, co + 16, 0, 0));
+            regs.xsb = __builtin_amdgcn_raw_buffer_load_b32(asr, so, 0, 0);
+            regs.wsb = __builtin_amdgcn_raw_buffer_load_b32(wsr, so, 0, 0);
+        }
+    };
+    // The staged rows of `pair` (kW4A16: read back from the thread's slots once its vmcnt wait
+    // has seen them land). The reads are written out so that the compiler, which cannot tell the
+    // stages apart, does not wait for every LDS-DMA in flight (vmcnt 0) before them; they
+    // complete (lgkmcnt 0) before any LDS access the compiler counts.
+    auto staged = [&](int pair) {
+        if constexpr (kDeep) {
+            Regs r = regs;
+            read_stage(stage_of(pair), lane, r.wa0, r.wa1, r.wsb);
+            return r;
+        } else {
+            return regs;
+        }
+    };
+    // Slice q (0..15) of the thread's decode of a buffer: kW4A4 the A row's 8 chunks, then W's;
+    // kW4A16 one W chunk every other slice.
+    struct Scales {
+        RowScales x, w;
+        float wf[4];
+    };
+    auto scales_of = [&](const Regs& r) {
+        Scales sc;
+        sc.x = row_scales(r.xsb);
+        sc.w = row_scales(r.wsb);
+        if constexpr (kBf16) {
+            const f32x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(r.wsb, 1.0f, false);
+            const f32x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(r.wsb, 1.0f, true);
+            sc.wf[0] = lo[0]; sc.wf[1] = lo[1]; sc.wf[2] = hi[0]; sc.wf[3] = hi[1];
+        }
+        return sc;
+    };
+    auto put = [&](uint8_t* buf, int q, const Scales& sc, const Regs& r) {
+        if constexpr (kMode == kW4A4) {
+            if (q < 8)
+                put_chunk(buf + tid * kPairK, tid, q, dword_of(r.xa0, r.xa1, q), sc.x);
+            else
+                put_chunk(buf + kOpBytes + tid * kPairK, tid, q - 8, dword_of(r.wa0, r.wa1, q - 8), sc.w);
+        } else if (q & 1) {
+            const int c = q >> 1;
+            if constexpr (kBf16)
+                put_chunk_bf16(buf + kOpBytes + tid * kPairK, tid, c, dword_of(r.wa0, r.wa1, c), sc.wf[c >> 1]);
+            else
+                put_chunk<true>(buf + kOpBytes + tid * kPairK, tid, c, dword_of(r.wa0, r.wa1, c), sc.w);
+        }
+    };
+    auto store = [&](int pair, const Regs& r) {
+        uint8_t* buf = lds + (pair & 1) * kPairBytes;
+        const Scales sc = scales_of(r);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) put(buf, q, sc, r);
     };
 
     // Fragment reads as gemm_tile.h's int8 kind: lane l supplies row l%32; lane group l/32 its
-    // K chunks; step e of a buffer reads logical chunks 4e + 2h + l/32 (h = 0, 1), each 8 fp16
-    // elements, one f16 MFMA's K half.
+    // K chunks; step e of a buffer reads logical chunks 4e + 2h + l/32 (h = 0, 1), each 8 16-bit
+    // elements, one MFMA's K half.
     const int fr = lane & 31, fq = lane >> 5;
     int aoff[2][2][4], boff[2][2][4];
 #pragma unroll
@@ -380,8 +539,7 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_half8(c.a[i], h), as_half8(c.b[j], h), acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x<kBf16>(c.a[i], c.b[j], h, acc[i][j]);
     };
     auto schedule = [&]() {
 #pragma unroll
@@ -391,29 +549,54 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         }
     };
 
-    // Pair p + 1's loads are issued at the top of step 2p - 1 (pair 1's before the loop), and
-    // its rows are decoded and written in step 2p, interleaved with that step's MFMAs, into the
-    // buffer no wave has read since the barrier of step 2p - 1; the barrier of step 2p + 1 makes
-    // them visible. Past the last pair the writes land in a buffer nothing reads again.
+    // kW4A4: pair p + 1's register loads are issued after the barrier of step 2p - 1 (pair 1's
+    // before the loop) and waited at the top of step 2p, whose slices decode and write them,
+    // between that step's MFMAs, into the buffer no wave has read since that barrier; the barrier
+    // of step 2p + 1 makes them visible.
+    // kW4A16: x's lines of pair p + 2 go by LDS-DMA after the barrier that ends step 2p and must
+    // land by the one that ends step 2p + 2; W's rows of pair p + 3 go with them, into the stage
+    // that step 2p's decode (of pair p + 1) has just read, and are waited at the top of step
+    // 2p + 4. At the top of step 2p a thread's loads in flight are then, in issue order, W(p + 1),
+    // x(p + 1), W(p + 2): vmcnt ≤ 11 means W(p + 1) is in, and vmcnt ≤ 3 that x(p + 1) is. Every
+    // load is issued, past the last pair too, so those counts hold to the end.
+    constexpr int kXIssue = 8, kWIssue = 3;
+    // The issue order the counts rely on is pinned by `order()`.
+    auto order = [&]() {
+        fence();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    issue_x(0);
+    order();
     load(0);
+    order();
+    if constexpr (kDeep) load(1);
     fence();
-    wait_vmcnt<0>();
+    if constexpr (kDeep)
+        wait_vmcnt<kWIssue>();
+    else
+        wait_vmcnt<0>();
     fence();
-    store(0);
-    if (np > 1) load(1);
+    store(0, staged(0));
+    order();
+    issue_x(1);
+    order();
+    if constexpr (kDeep)
+        load(2);
+    else if (np > 1)
+        load(1);
     fence();
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
     fence();
 
     // Step 2p: 16 slices, each one fragment read for step 2p + 1, two of this step's MFMAs (K
-    // half h = q / 8, so that no MFMA waits on the one before it) and one chunk of pair p + 1
-    // decoded and written.
-    auto even_step = [&](int s, const Frags& cur, Frags& next) {
+    // half h = q / 8, so that no MFMA waits on the one before it) and one slice of pair p + 1's
+    // decode.
+    auto even_step = [&](int s, const Frags& cur, Frags& next, const Regs& r) {
         const uint8_t* rbuf = lds + ((s + 1) >> 1 & 1) * kPairBytes;
         const int e = (s + 1) & 1;
         uint8_t* wbuf = lds + (((s >> 1) + 1) & 1) * kPairBytes;
-        const RowScales xsc = row_scales(xsb), wsc = row_scales(wsb);
+        const Scales sc = scales_of(r);
         i32x4 piece[4][4];  // [i][alo, ahi, blo, bhi]
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
@@ -421,9 +604,9 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
             const int off = fk < 2 ? aoff[e][fk][fi] : boff[e][fk - 2][fi];
             piece[fi][fk] = *reinterpret_cast<const i32x4*>(rbuf + off);
             const int h = q >> 3, i = (q >> 1) & 3, j = 2 * (q & 1);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_half8(cur.a[i], h), as_half8(cur.b[j], h), acc[i][j], 0, 0, 0);
-            acc[i][j + 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_half8(cur.a[i], h), as_half8(cur.b[j + 1], h), acc[i][j + 1], 0, 0, 0);
-            put(wbuf, q, xsc, wsc);
+            acc[i][j] = mfma16x<kBf16>(cur.a[i], cur.b[j], h, acc[i][j]);
+            acc[i][j + 1] = mfma16x<kBf16>(cur.a[i], cur.b[j + 1], h, acc[i][j + 1]);
+            put(wbuf, q, sc, r);
             __builtin_amdgcn_sched_barrier(0);  // slices stay in order: decode rides under MFMAs
         }
 #pragma unroll
@@ -435,18 +618,30 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
 
     Frags f0, f1;
     fetch(0, f0);
-    for (int s = 0; s < 2 * np; s += 2) {
-        const int p = s >> 1;
+    // Steps 2p and 2p + 1.
+    for (int p = 0; p < np; ++p) {
+        const int s = 2 * p;
         fence();
-        wait_vmcnt<0>();
+        if constexpr (kDeep)
+            wait_vmcnt<kXIssue + kWIssue>();
+        else
+            wait_vmcnt<0>();
         fence();
-        even_step(s, f0, f1);
+        even_step(s, f0, f1, staged(p + 1));
         __builtin_amdgcn_sched_barrier(0);  // the step's MFMAs stay ahead of the barrier
         fence();
+        if constexpr (kDeep) wait_vmcnt<kWIssue>();
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
         fence();
-        if (p + 2 < np) load(p + 2);
+        if constexpr (kDeep) {
+            issue_x(p + 2);
+            order();
+            load(p + 3);
+            order();
+        } else if (p + 2 < np) {
+            load(p + 2);
+        }
         fetch(s + 2, f0);  // past the last step: unused registers
         mfmas(f1);
         schedule();
@@ -460,7 +655,7 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
     fence();
-    const float gxw = __fmul_rn(gx[0], gw[0]);
+    const float gxw = kMode == kW4A4 ? __fmul_rn(gx[0], gw[0]) : gw[0];
     const int nl = wn * 128 + 4 * fq;  // the lane's first column within the tile
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -468,7 +663,7 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         for (int g = 0; g < 4; ++g) {
             const int c = nl + i * 32 + 8 * g;
             float4 f = make_float4(gxw, gxw, gxw, gxw);
-            if (cs != nullptr) {
+            if (kMode == kW4A4 && cs != nullptr) {
                 const float4 cv = *reinterpret_cast<const float4*>(lds + kWsOff + 4 * c);
                 f = make_float4(__fmul_rn(gxw, cv.x), __fmul_rn(gxw, cv.y), __fmul_rn(gxw, cv.z), __fmul_rn(gxw, cv.w));
             }
@@ -479,9 +674,9 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
                 for (int r = 0; r < 4; ++r) acc[i][j][4 * g + r] = __fmul_rn(acc[i][j][4 * g + r], fv[r]);
         }
 
-    // The low-rank term into the same accumulators: A = up rows (the tile's columns), B = la
-    // rows, 16 ranks a call.
-    {
+    // kW4A4: the low-rank term into the same accumulators: A = up rows (the tile's columns), B =
+    // la rows, 16 ranks a call.
+    if constexpr (kMode == kW4A4) {
         const auto upr = rows_view(up + static_cast<int64_t>(n0) * R, N - n0, 2 * R);
         const auto lar = rows_view(la + static_cast<int64_t>(m0) * R, padded_rows(M) - m0, 2 * R);
         for (int kk = 0; kk < R; kk += 16) {
@@ -588,7 +783,23 @@ hipError_t svdq_nvfp4_gemm(const uint8_t* act, const uint8_t* ascales, const uin
             static_cast<uint16_t*>(out), M, N, K, R, tiles_m, tiles_n);
         return hipGetLastError();
     };
-    return out_half ? go(nvfp4_gemm_kernel<true>) : go(nvfp4_gemm_kernel<false>);
+    return out_half ? go(nvfp4_gemm_kernel<kW4A4, true, true>) : go(nvfp4_gemm_kernel<kW4A4, true, false>);
+}
+
+hipError_t nvfp4_gemm(const void* x, bool x_half, const uint8_t* w, const uint8_t* scale,
+                      const float* scale_2, const void* bias, void* out, bool out_half, int M, int N,
+                      int K, hipStream_t s) {
+    const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTile - 1) / kTile;
+    auto go = [&](auto kernel) {
+        kernel<<<tiles_m * tiles_n, kThreads, 0, s>>>(
+            static_cast<const uint8_t*>(x), nullptr, w, scale, nullptr, scale_2, nullptr, nullptr,
+            nullptr, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), M, N, K, 0,
+            tiles_m, tiles_n);
+        return hipGetLastError();
+    };
+    if (x_half)
+        return out_half ? go(nvfp4_gemm_kernel<kW4A16, true, true>) : go(nvfp4_gemm_kernel<kW4A16, true, false>);
+    return out_half ? go(nvfp4_gemm_kernel<kW4A16, false, true>) : go(nvfp4_gemm_kernel<kW4A16, false, false>);
 }
 
 }  // namespace cozyq

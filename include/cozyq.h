@@ -274,15 +274,28 @@ int cozyq_decode_svdq(int device, const uint8_t* w, const uint8_t* scale, int ti
                       int down_type, const void* up, int up_type, int rank, void* out,
                       int out_type, int64_t rows, int64_t cols, void* stream);
 
-/* nvfp4 W4A16 GEMV for up to 16 rows (reference: the `_gemv` kernel of
- * internal/nvfp4_linear.py:126-201, which serves at most DECODE_ROWS = 16 rows, :338-377):
+/* nvfp4 W4A16 GEMV for up to 64 rows (reference: the `_gemv` kernel of
+ * internal/nvfp4_linear.py:126-201, which serves at most DECODE_ROWS = 16 rows, :338-377; past 16
+ * rows the reference decodes and calls cuBLAS, :376-385, which this kernel replaces up to 64):
  *   out[m, n] = round((Σ_k x[m, k] · (e2m1[n, k] · scale[n, k/16])) · scale_2), float32 sums.
  * w [N, K/2] E2M1 codes, element 2k in the low nibble; scale E4M3 in cuBLAS's 128x4 tiles over
  * [N, K/16] (the leaf's resident layout); scale_2 one float32. x [M, K] bf16 or fp16 (x_half),
- * 16-byte aligned; out [M, N] bf16 or fp16. 0 ≤ M ≤ 16, K % 32 == 0. A row's result does not
+ * 16-byte aligned; out [M, N] bf16 or fp16. 0 ≤ M ≤ 64, K % 32 == 0. A row's result does not
  * depend on M. */
 int cozyq_nvfp4_gemv(int device, const void* x, int x_half, const uint8_t* w, const uint8_t* scale,
                      const float* scale_2, void* out, int out_half, int M, int N, int K, void* stream);
+
+/* nvfp4 W4A16 GEMM for more rows (reference: the decode-then-cuBLAS path of
+ * internal/nvfp4_linear.py:376-385 — `_dequant` into the activation dtype with scale_2 folded in,
+ * then one library GEMM):
+ *   out[m, n] = round((Σ_k x[m, k] · (e2m1[n, k] · scale[n, k/16])) · scale_2 + bias[n]),
+ * float32 sums; the product e2m1 · E4M3 is exact in bf16 and fp16, so W is never rounded (the
+ * reference rounds e2m1 · scale · scale_2 into x's dtype). The operands are nvfp4_gemv's, plus
+ * bias [N] in out's dtype or null; x, w, scale, out and bias 16-byte aligned; M ≥ 0,
+ * K % 64 == 0, N % 8 == 0. 256x256 output tiles. */
+int cozyq_nvfp4_gemm(int device, const void* x, int x_half, const uint8_t* w, const uint8_t* scale,
+                     const float* scale_2, const void* bias, void* out, int out_half, int M, int N, int K,
+                     void* stream);
 
 /* Weight encoders (reference: the tensorfs producers behind derive/microscale.py —
  * encode_int8_convrot256 :295-334, encode_fp8_rowwise :223-262, encode_w4a8 :349-408,

@@ -59,6 +59,23 @@ def test_gemm_config_rule():
     assert lib.cozyq_gemm_config(0, 0, 8, 256) == -1
 
 
+def test_nvfp4_entry_points_refuse_bad_shapes_before_the_device():
+    """`cozyq_nvfp4_gemv` takes 0..64 rows and K % 32 == 0; `cozyq_nvfp4_gemm` K % 64 == 0 and
+    N % 8 == 0. Refusals (hipErrorInvalidValue = 1) and the empty product come back before any
+    device call."""
+    lib = _lib.load()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16
+    g = ctypes.c_void_p(p)
+    assert lib.cozyq_nvfp4_gemv(0, p, 0, p, p, g, p, 0, 65, 64, 64, None) == 1
+    assert lib.cozyq_nvfp4_gemv(0, p, 0, p, p, g, p, 0, 4, 64, 48, None) == 1
+    assert lib.cozyq_nvfp4_gemv(0, None, 0, p, p, g, None, 0, 0, 64, 64, None) == 0
+    assert lib.cozyq_nvfp4_gemm(0, p, 0, p, p, g, None, p, 0, 300, 64, 96, None) == 1
+    assert lib.cozyq_nvfp4_gemm(0, p, 0, p, p, g, None, p, 0, 300, 60, 64, None) == 1
+    assert lib.cozyq_nvfp4_gemm(0, p, 0, p, p, g, None, p + 8, 0, 300, 64, 64, None) == 1
+    assert lib.cozyq_nvfp4_gemm(0, None, 0, p, p, g, None, None, 0, 0, 64, 64, None) == 0
+
+
 def _host(fn: str, values: np.ndarray) -> np.ndarray:
     values = np.ascontiguousarray(values, dtype=np.float32)
     out = np.zeros(values.shape, dtype=np.uint8)

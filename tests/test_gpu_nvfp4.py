@@ -1,9 +1,10 @@
 """The nvfp4 encoded linear on the GPU (`cozyq.nvfp4_linear`, `csrc/nvfp4.hip`).
 
-The W4A16 GEMV (up to 16 rows) and the decode + library GEMM path are held to the float64
-product of the activations and the exact decoded weight (the oracle's `decode_nvfp4`, pinned by
-the reference's nvfp4 vectors), within rtol 2e-2 / atol 1e-2·rms like every floating output
-here. The GEMV's rows are bit-identical whatever M is, and repeat bit for bit.
+The W4A16 GEMV (up to 64 rows; 48 by default), the W4A16 GEMM and the decode + library GEMM path
+are held to the float64 product of the activations and the exact decoded weight (the oracle's
+`decode_nvfp4`, pinned by the reference's nvfp4 vectors), within rtol 2e-2 / atol 1e-2·rms like
+every floating output here. The GEMV's and the GEMM's rows are bit-identical whatever M is, and
+repeat bit for bit.
 """
 
 from __future__ import annotations
@@ -37,7 +38,8 @@ def _close(got: torch.Tensor, want: torch.Tensor) -> None:
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (3, 200, 1024), (16, 264, 96), (16, 4096, 3072)])
+@pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (3, 200, 1024), (16, 264, 96), (16, 4096, 3072),
+                                   (17, 200, 160), (40, 4096, 3072), (64, 1032, 2048)])
 def test_nvfp4_gemv_against_the_exact_product(dtype, m, n, k):
     from cozyq import prebuilt
 
@@ -54,21 +56,78 @@ def test_nvfp4_gemv_rows_do_not_depend_on_m():
     from cozyq import prebuilt
 
     codes, _, blocked, second, _ = _weight(4096, 2048, 9)
-    x = torch.randn(16, 2048, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    x = torch.randn(64, 2048, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
     ops = prebuilt.library(0)
     w, s, g = codes.to(CUDA), blocked.to(CUDA), second.to(CUDA)
     full = ops.nvfp4_gemv(x.to(CUDA), w, s, g, torch.bfloat16).cpu()
     again = ops.nvfp4_gemv(x.to(CUDA), w, s, g, torch.bfloat16).cpu()
     assert torch.equal(full.view(torch.int16), again.view(torch.int16))
-    for m in (1, 5):
+    for m in (1, 5, 16, 17, 33, 50):
         part = ops.nvfp4_gemv(x[:m].to(CUDA), w, s, g, torch.bfloat16).cpu()
         assert torch.equal(part.view(torch.int16), full[:m].view(torch.int16))
 
 
-@pytest.mark.parametrize("rows", [17, 64])
+@pytest.mark.parametrize("dtype,out_dtype", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                             (torch.bfloat16, torch.float16)])
+@pytest.mark.parametrize("m,n,k", [(17, 256, 64), (300, 520, 1024), (256, 1536, 128), (600, 3072, 2048)])
+def test_nvfp4_gemm_against_the_exact_product(dtype, out_dtype, m, n, k):
+    """The W4A16 GEMM: ragged rows and columns (partial 256x256 tiles), one and two K buffers,
+    a bf16 x into an fp16 output."""
+    from cozyq import prebuilt
+
+    codes, _, blocked, second, exact = _weight(n, k, m + n)
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(k)) * 0.5).to(dtype)
+    ops = prebuilt.library(0)
+    got = ops.nvfp4_gemm(x.to(CUDA), codes.to(CUDA), blocked.to(CUDA), second.to(CUDA), None, out_dtype)
+    torch.cuda.synchronize()
+    assert got.shape == (m, n) and got.dtype == out_dtype
+    _close(got, x.double() @ exact.double().t())
+
+
+def test_nvfp4_gemm_bias_rows_and_repeats():
+    """With a bias; a row's result is bit-identical whatever M is, and repeats bit for bit."""
+    from cozyq import prebuilt
+
+    n, k = 776, 512
+    codes, _, blocked, second, exact = _weight(n, k, 11)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(520, k, generator=g).to(torch.bfloat16)
+    bias = (torch.randn(n, generator=g) * 0.3).to(torch.bfloat16)
+    ops = prebuilt.library(0)
+    w, s, sc, b = codes.to(CUDA), blocked.to(CUDA), second.to(CUDA), bias.to(CUDA)
+    full = ops.nvfp4_gemm(x.to(CUDA), w, s, sc, b, torch.bfloat16).cpu()
+    again = ops.nvfp4_gemm(x.to(CUDA), w, s, sc, b, torch.bfloat16).cpu()
+    assert torch.equal(full.view(torch.int16), again.view(torch.int16))
+    _close(full, x.double() @ exact.double().t() + bias.double())
+    for m in (1, 33, 257):
+        part = ops.nvfp4_gemm(x[-m:].to(CUDA), w, s, sc, b, torch.bfloat16).cpu()
+        assert torch.equal(part.view(torch.int16), full[-m:].view(torch.int16))
+    empty = ops.nvfp4_gemm(x[:0].to(CUDA), w, s, sc, b, torch.bfloat16)
+    assert empty.shape == (0, n)
+
+
+@pytest.mark.parametrize("rows", [17, 48, 49, 300])
+def test_nvfp4_matmul_gemv_and_gemm_decode_nothing(rows, monkeypatch):
+    """Up to 48 rows the GEMV, past them (asked for, K % 64 == 0, N % 8 == 0) the W4A16 GEMM: no
+    decoded transient either way."""
+    from cozyq import nvfp4_linear, prebuilt
+
+    n, k = 264, 192
+    codes, _, blocked, second, exact = _weight(n, k, 6)
+    ops = prebuilt.library(0)
+    monkeypatch.setattr(type(ops), "decode_table", lambda *a, **kw: pytest.fail("decoded the weight"))
+    x = torch.randn(rows, k, generator=torch.Generator().manual_seed(8)).to(torch.float16)
+    got = nvfp4_linear.matmul(torch, x.to(CUDA), codes.to(CUDA), blocked.to(CUDA), None,
+                              second.to(CUDA), torch.float32, gemm=True)  # fmt: skip
+    torch.cuda.synchronize()
+    assert got.shape == (rows, n) and got.dtype == torch.float32
+    _close(got, x.double() @ exact.double().t())
+
+
+@pytest.mark.parametrize("rows", [65, 100])
 def test_nvfp4_matmul_more_rows_decodes_per_chunk(rows, monkeypatch):
-    """Past 16 rows: the weight decoded per 128-row chunk (here forced small, so the last chunk
-    is partial) and the library GEMM."""
+    """Past 48 rows by default: the weight decoded per 128-row chunk (here forced small, so the
+    last chunk is partial) and the library GEMM."""
     from cozyq import nvfp4_linear
 
     n, k = 300, 1024
