@@ -568,14 +568,19 @@ def bench_svdq_nvfp4(torch, ops, lib, stream, steps: int) -> dict:
 
 
 def bench_tiles(torch, ops, lib, stream, steps: int) -> dict:
-    """The GEMM tile configs (`cozyq_gemm` config 0..4) at the shapes the shape rule
+    """The GEMM tile configs (`cozyq_gemm` config 0..5) at the shapes the shape rule
     (`cozyq_gemm_config`) was fitted on, int8 and fp8, as interleaved medians: each shape's per-
     config microseconds, the fastest config and the one config -1 runs."""
-    shapes = [(128, 3072, 3072), (256, 14336, 4096), (512, 14336, 4096), (1024, 14336, 4096),
+    from cozyq.prebuilt import GEMM_CONFIGS
+
+    shapes = [(16, 14336, 4096), (64, 14336, 4096), (128, 14336, 4096), (128, 3072, 3072),
+              (256, 14336, 4096), (256, 12288, 3072), (512, 14336, 4096), (1024, 14336, 4096),
               (4096, 14336, 4096), (4096, 12288, 3072), (4096, 9216, 3072), (4096, 3072, 3072),
               (4096, 3072, 12288), (8192, 640, 2560), (2048, 1280, 1280), (1024, 3072, 3072),
               (512, 3072, 3072), (2048, 3072, 3072), (16384, 3072, 3072), (384, 3072, 3072),
-              (768, 3072, 3072), (4096, 1280, 5120), (1536, 3072, 3072)]  # fmt: skip
+              (768, 3072, 3072), (4096, 1280, 5120), (1536, 3072, 3072), (64, 3072, 3072),
+              (32, 12288, 3072)]  # fmt: skip
+    configs = range(GEMM_CONFIGS)
     timer, rows = Timer(torch), []
     for kind in ("int8", "fp8"):
         for m, n, k in shapes:
@@ -591,11 +596,11 @@ def bench_tiles(torch, ops, lib, stream, steps: int) -> dict:
             xs = torch.rand(m, device="cuda", generator=gen) * 0.01 + 0.001
             ws = torch.rand(n, device="cuda", generator=gen) * 0.01 + 0.001
             bias = torch.randn(n, device="cuda", generator=gen).to(torch.bfloat16)
-            fns = {c: (lambda c=c: f(q, xs, w, ws, bias, torch.bfloat16, c)) for c in range(5)}
+            fns = {c: (lambda c=c: f(q, xs, w, ws, bias, torch.bfloat16, c)) for c in configs}
             preroll(torch, fns[0], 30)
             est = timer.run(fns[0], 3, 1)
             med = timer.interleaved(fns, samples=9, batch=max(2, min(50, int(2.0 / max(est, 1e-3)))))
-            us = {c: round(med[c]["ms"] * 1e3, 2) for c in range(5)}
+            us = {c: round(med[c]["ms"] * 1e3, 2) for c in configs}
             rows.append({"kind": kind, "M": m, "N": n, "K": k, "us": us, "best": min(us, key=us.get),
                          "chosen": lib.cozyq_gemm_config(int(kind == "fp8"), m, n, k)})  # fmt: skip
             del q, w

@@ -6,11 +6,12 @@
 // stream over hundreds of workgroups (at M = 256 the 58.7 MB fp8 weight is 7.3 us of HBM against
 // 6 us of MFMA), and any shape with fewer than 160 256x256 tiles.
 //
-// A workgroup of 4 waves (2 x 2) owns a kTM x kTN tile; K advances 128 bytes a step through a
-// double-buffered LDS stage filled from registers. Every global read is a buffer load bounded by
-// the matrix (rows past M or N and bytes past K read as zeros), so no launch shape can read
-// outside the operands. MFMA A is the W tile, B the X tile: each lane's four results are four
-// consecutive output columns of one row.
+// A workgroup of 4 waves (2 x 2) owns a kTM x kTN tile; K advances 128 bytes a step. The int8
+// and fp8 forms (deep_kernel) bring both operands by LDS-DMA into a ring of K steps; the w4a8
+// form (narrow_kernel) unpacks its codes in registers into a double-buffered stage. Every global
+// read is a buffer load bounded by the matrix (rows past M or N and bytes past K read as zeros),
+// so no launch shape can read outside the operands. MFMA A is the W tile, B the X tile: each
+// lane's four results are four consecutive output columns of one row.
 #include <type_traits>
 
 #include "common.h"
@@ -255,14 +256,196 @@ __global__ __launch_bounds__(kThreads) void narrow_kernel(
     }
 }
 
+// The deep form of configs 1..4 (int8 and fp8 rowwise, not w4a8): the same tile, MFMA order and
+// epilogue as narrow_kernel, with the operands brought by LDS-DMA into a ring of kStages K steps
+// in LDS instead of through registers, so kStages - 1 steps of loads are in flight (one in
+// narrow_kernel): at few rows each workgroup streams its weight rows at the latency of a step,
+// and that depth is what fills HBM. Per step a wave issues kTM/32 + kTN/32 loads of 1 KiB (8 rows
+// of 128 bytes, lane l at row l/8, physical chunk l%8 holding logical chunk swz(row, l%8)).
+typedef __attribute__((address_space(3))) void NarrowLds;
+
+template <int N>
+__device__ __forceinline__ void narrow_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+__device__ __forceinline__ void narrow_fence() { asm volatile("" ::: "memory"); }
+
+// One operand's loads of a K step: load j fills rows (4j + wave)·8 .. + 8 of the operand's half.
+template <int kLoads>
+__device__ __forceinline__ void deep_issue(__amdgpu_buffer_rsrc_t rsrc, uint8_t* half, const int (&rowoff)[kLoads],
+                                           const int (&chunk)[kLoads], int k0, int K, int wave) {
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+        const uint32_t off = (k0 + chunk[j] < K) ? static_cast<uint32_t>(rowoff[j] + k0) : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (NarrowLds*)(half + (4 * j + wave) * 1024), 16, off, 0, 0, 0);
+    }
+}
+
+template <bool kInt8, int kTM, int kTN, int kStages, bool kOutHalf, bool kBias, int kEpi>
+__global__ __launch_bounds__(kThreads) void deep_kernel(
+    const uint8_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ xs,
+    const float* __restrict__ ws, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
+    int64_t ldo, int M, int N, int K, int tiles_m) {
+    static_assert(kTM % 32 == 0 && kTN % 32 == 0 && kTM <= 128 && kTN <= 128 && kStages >= 2, "tile");
+    constexpr int kLX = kTM / 32, kLW = kTN / 32;  // a wave's loads a step
+    constexpr int kStageBytes = (kTM + kTN) * kStep;
+    constexpr int kBI = kTN / 32, kBJ = kTM / 32;  // 16x16 blocks of a wave: n by m
+    static_assert((kStages - 2) * (kLX + kLW) < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tm = blockIdx.x % tiles_m, tn = blockIdx.x / tiles_m;
+    const int m0 = __builtin_amdgcn_readfirstlane(tm * kTM);
+    const int n0 = __builtin_amdgcn_readfirstlane(tn * kTN);
+    const __amdgpu_buffer_rsrc_t xr = rows_from(X, m0, M, K);
+    const __amdgpu_buffer_rsrc_t wr = rows_from(W, n0, N, K);
+    const int nk = (K + kStep - 1) / kStep;
+
+    int xoff[kLX], xchunk[kLX], woff[kLW], wchunk[kLW];
+#pragma unroll
+    for (int j = 0; j < kLX; ++j) {
+        const int r = (4 * j + wave) * 8 + (lane >> 3);
+        xchunk[j] = 16 * swz(r, lane & 7);
+        xoff[j] = r * K + xchunk[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kLW; ++j) {
+        const int r = (4 * j + wave) * 8 + (lane >> 3);
+        wchunk[j] = 16 * swz(r, lane & 7);
+        woff[j] = r * K + wchunk[j];
+    }
+    // Every step's loads are issued, past the last too (zeros into a slot nothing reads), so a
+    // wave's count of loads in flight is the same at every wait.
+    auto issue = [&](int ks) {
+        uint8_t* base = lds + (ks % kStages) * kStageBytes;
+        deep_issue<kLX>(xr, base, xoff, xchunk, ks * kStep, K, wave);
+        deep_issue<kLW>(wr, base + kTM * kStep, woff, wchunk, ks * kStep, K, wave);
+    };
+
+    typedef std::conditional_t<kInt8, i32x4, f32x4> Acc;
+    Acc acc[kBI][kBJ];
+#pragma unroll
+    for (int i = 0; i < kBI; ++i)
+#pragma unroll
+        for (int j = 0; j < kBJ; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+
+#pragma unroll
+    for (int ks = 0; ks < kStages - 1; ++ks) issue(ks);
+
+    const int fr = lane & 15, fq = lane >> 4;
+    for (int ks = 0; ks < nk; ++ks) {
+        // Step ks landed (this wave's share; the barrier makes every wave's visible) and every
+        // wave is done with step ks - 1, whose slot takes step ks + kStages - 1.
+        narrow_fence();
+        narrow_vmcnt<(kStages - 2) * (kLX + kLW)>();
+        __builtin_amdgcn_s_barrier();
+        narrow_fence();
+        issue(ks + kStages - 1);
+        const uint8_t* lx = lds + (ks % kStages) * kStageBytes;
+        const uint8_t* lw = lx + kTM * kStep;
+        if constexpr (kInt8) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                i32x4 a[kBI], b[kBJ];
+#pragma unroll
+                for (int i = 0; i < kBI; ++i) {
+                    const int r = wn * (kTN / 2) + i * 16 + fr;
+                    a[i] = *reinterpret_cast<const i32x4*>(&lw[r * kStep + swz(r, 4 * h + fq) * 16]);
+                }
+#pragma unroll
+                for (int j = 0; j < kBJ; ++j) {
+                    const int r = wm * (kTM / 2) + j * 16 + fr;
+                    b[j] = *reinterpret_cast<const i32x4*>(&lx[r * kStep + swz(r, 4 * h + fq) * 16]);
+                }
+#pragma unroll
+                for (int i = 0; i < kBI; ++i)
+#pragma unroll
+                    for (int j = 0; j < kBJ; ++j) acc[i][j] = mfma_i8(a[i], b[j], acc[i][j]);
+            }
+        } else {
+            i32x8 a[kBI], b[kBJ];
+#pragma unroll
+            for (int i = 0; i < kBI; ++i) {
+                const int r = wn * (kTN / 2) + i * 16 + fr;
+                const uint8_t* row = &lw[r * kStep];
+                const i32x4 lo = *reinterpret_cast<const i32x4*>(row + swz(r, fq) * 16);
+                const i32x4 hi = *reinterpret_cast<const i32x4*>(row + swz(r, fq + 4) * 16);
+                a[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+#pragma unroll
+            for (int j = 0; j < kBJ; ++j) {
+                const int r = wm * (kTM / 2) + j * 16 + fr;
+                const uint8_t* row = &lx[r * kStep];
+                const i32x4 lo = *reinterpret_cast<const i32x4*>(row + swz(r, fq) * 16);
+                const i32x4 hi = *reinterpret_cast<const i32x4*>(row + swz(r, fq + 4) * 16);
+                b[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+#pragma unroll
+            for (int i = 0; i < kBI; ++i)
+#pragma unroll
+                for (int j = 0; j < kBJ; ++j) acc[i][j] = mfma_f8(a[i], b[j], acc[i][j]);
+        }
+    }
+    narrow_vmcnt<0>();  // the zero-filling loads past the last step land before the wave ends
+
+    // Epilogue: narrow_kernel's.
+#pragma unroll
+    for (int j = 0; j < kBJ; ++j) {
+        const int m = m0 + wm * (kTM / 2) + j * 16 + fr;
+        if (m >= M) continue;
+        const float xsm = xs[m];
+#pragma unroll
+        for (int i = 0; i < kBI; ++i) {
+            const int n = n0 + wn * (kTN / 2) + i * 16 + 4 * fq;
+            if (n >= N) continue;  // N % 8 == 0: n..n+3 are all in
+            uint16_t o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (kInt8) {
+                    const float v = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][r]), xsm), ws[n + r]);
+                    o[r] = narrow<kOutHalf>(v);
+                    if constexpr (kBias) o[r] = narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(o[r]), widen<kOutHalf>(bias[n + r])));
+                } else {
+                    float v = __fmul_rn(__fmul_rn(acc[i][j][r], xsm), ws[n + r]);
+                    if constexpr (kBias) v = __fadd_rn(v, widen<kOutHalf>(bias[n + r]));
+                    o[r] = narrow<kOutHalf>(v);
+                }
+                if constexpr (kEpi == 1) o[r] = narrow<kOutHalf>(gelu_tanh(widen<kOutHalf>(o[r])));
+            }
+            *reinterpret_cast<uint2*>(out + static_cast<int64_t>(m) * ldo + n) =
+                make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16), o[2] | (static_cast<uint32_t>(o[3]) << 16));
+        }
+    }
+}
+
+// The ring depth of each deep tile: as many K steps as 64 KiB of LDS hold (two workgroups a
+// CU), 2 to 8: 32x64 5, 64x64 4, 128x64 and 128x128 2. Measured at few rows with the weight
+// streamed from HBM, 96 and 128 KiB rings (8 and 12 steps for 32x64) were no faster.
+constexpr int kDeepLds = 65536;
+template <int kTM, int kTN>
+constexpr int deep_stages() {
+    constexpr int fit = kDeepLds / ((kTM + kTN) * kStep);
+    return fit < 2 ? 2 : fit > 8 ? 8 : fit;
+}
+
 template <bool kInt8, int kTM, int kTN, bool kOutHalf, bool kBias, int kEpi, bool kW4>
 hipError_t launch(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,
                   const void* bias, void* out, int64_t ldo, int M, int N, int K, W4 w4,
                   hipStream_t s) {
     const int tiles_m = (M + kTM - 1) / kTM, tiles_n = (N + kTN - 1) / kTN;
-    narrow_kernel<kInt8, kTM, kTN, kOutHalf, kBias, kEpi, kW4><<<tiles_m * tiles_n, kThreads, 0, s>>>(
-        q, w, xs, ws, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, M, N,
-        K, tiles_m, w4);
+    if constexpr (kW4) {
+        narrow_kernel<kInt8, kTM, kTN, kOutHalf, kBias, kEpi, kW4><<<tiles_m * tiles_n, kThreads, 0, s>>>(
+            q, w, xs, ws, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, M, N,
+            K, tiles_m, w4);
+    } else {
+        deep_kernel<kInt8, kTM, kTN, deep_stages<kTM, kTN>(), kOutHalf, kBias, kEpi><<<tiles_m * tiles_n, kThreads, 0, s>>>(
+            q, w, xs, ws, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, M, N,
+            K, tiles_m);
+    }
     return hipGetLastError();
 }
 
@@ -339,15 +522,24 @@ hipError_t w4a8_unpack(const uint8_t* codes, const uint8_t* group_scale, const f
     return hipGetLastError();
 }
 
-// The largest narrow tile whose grid reaches 440 workgroups (~1.7 a CU: the sweep's best tile
-// at every shape below 160 256x256 tiles had 448-768), else the smallest.
+// The narrow tile for M x N (fitted on `bench.py --only tiles`, int8 and fp8). Few rows are
+// bound by the weight stream, which every M-tile reads again: when N alone gives a 64-column tile
+// 192 workgroups (~3/4 of the CUs), the tile that takes all M rows in one M-tile (up to 128)
+// streams it once. Otherwise the largest tile whose grid reaches 288 workgroups (~1.1 a CU: two
+// deep workgroups share a CU), else the smallest.
 int narrow_config(int M, int N) {
-    static constexpr int kRows[] = {0, 128, 128, 64, 32}, kCols[] = {0, 128, 64, 64, 64};
-    for (int c = 1; c < kGemmConfigs; ++c) {
-        const int64_t groups = static_cast<int64_t>((M + kRows[c] - 1) / kRows[c]) * ((N + kCols[c] - 1) / kCols[c]);
-        if (groups >= 440) return c;
+    static constexpr int kTiles = 5;  // configs 1..4 have narrow tiles
+    static constexpr int kRows[kTiles] = {0, 128, 128, 64, 32}, kCols[kTiles] = {0, 128, 64, 64, 64};
+    if ((N + 63) / 64 >= 192) {
+        if (M <= 32) return 4;
+        if (M <= 64) return 3;
+        if (M <= 128) return 2;
     }
-    return kGemmConfigs - 1;
+    for (int c = 1; c < kTiles; ++c) {
+        const int64_t groups = static_cast<int64_t>((M + kRows[c] - 1) / kRows[c]) * ((N + kCols[c] - 1) / kCols[c]);
+        if (groups >= 288) return c;
+    }
+    return kTiles - 1;
 }
 
 hipError_t gemm_fp8_narrow(const uint8_t* q, const float* xs, const uint8_t* w, const float* ws,

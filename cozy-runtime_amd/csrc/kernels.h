@@ -47,7 +47,7 @@ hipError_t linear_int8_noalloc(const void* x, bool half, int rotation, int8_t* q
                                int64_t ldo, int M, int N, int K, int epilogue, int device,
                                hipStream_t s);
 
-// The rowwise GEMMs' tile configs: 0 the 256x256 kernel, 1..4 the narrow kernel's 128x128,
+// The rowwise GEMMs' tile configs: 0 the 256x256 kernel, 1..4 the narrow kernels' 128x128,
 // 128x64, 64x64 and 32x64 (kGemmConfigs in all); -1 lets gemm_config choose by shape. Every
 // config gives the same int8 output bit for bit; an unknown config is hipErrorNotSupported.
 constexpr int kGemmConfigs = 5;

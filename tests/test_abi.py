@@ -42,17 +42,21 @@ def test_constants():
 
 
 def test_gemm_config_rule():
-    """`cozyq_gemm_config` (what config -1 runs): the 256x256 tile (0) from 160 of its tiles, else
-    the largest narrow tile (1: 128x128, 2: 128x64, 3: 64x64, 4: 32x64) whose grid reaches 440
-    workgroups, else 32x64. Each case below is the fastest config the MI355X sweep measured
-    (within 5%) at that shape, for int8 and fp8 alike."""
+    """`cozyq_gemm_config` (what config -1 runs): the 256x256 tile (0) from 160 of its tiles;
+    else, when N gives a 64-column tile 192 workgroups, the one (4: 32x64, 3: 64x64, 2: 128x64)
+    that takes every row (up to 128) in one M-tile; else the largest of 1: 128x128, 2: 128x64,
+    3: 64x64, 4: 32x64 whose grid reaches 288 workgroups, else 32x64. Each case below is the
+    fastest config the MI355X sweep (`bench.py --only tiles`) measured within 3% at that shape,
+    for int8 and fp8 alike, except (8192, 640, 2560), where 128x64 is 8% faster."""
     lib = _lib.load()
     cases = {(4096, 12288, 3072): 0, (4096, 3072, 3072): 0, (1024, 14336, 4096): 0,
-             (16384, 3072, 3072): 0, (4096, 3072, 12288): 0, (2048, 3072, 3072): 2,
-             (1024, 3072, 3072): 3, (768, 3072, 3072): 3, (512, 3072, 3072): 4,
-             (512, 14336, 4096): 1, (256, 14336, 4096): 2, (2048, 1280, 1280): 3,
-             (4096, 1280, 5120): 2, (8192, 640, 2560): 2, (16, 14336, 4096): 4,
-             (1, 14336, 4096): 4}  # fmt: skip
+             (16384, 3072, 3072): 0, (4096, 3072, 12288): 0, (2048, 3072, 3072): 1,
+             (1024, 3072, 3072): 2, (768, 3072, 3072): 2, (512, 3072, 3072): 3,
+             (384, 3072, 3072): 3, (1536, 3072, 3072): 1, (512, 14336, 4096): 1,
+             (256, 14336, 4096): 2, (256, 12288, 3072): 2, (2048, 1280, 1280): 2,
+             (4096, 1280, 5120): 1, (8192, 640, 2560): 1, (16, 14336, 4096): 4,
+             (1, 14336, 4096): 4, (64, 14336, 4096): 3, (128, 14336, 4096): 2,
+             (128, 3072, 3072): 4, (64, 3072, 3072): 4, (32, 12288, 3072): 4}  # fmt: skip
     for (m, n, k), want in cases.items():
         for fp8 in (0, 1):
             assert lib.cozyq_gemm_config(fp8, m, n, k) == want, (m, n, k, fp8)

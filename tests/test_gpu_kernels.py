@@ -527,7 +527,7 @@ def test_fp8_gemm_within_tolerance(ops, shape, bias):
 # (M, N, K): one row; ragged rows and columns on every tile; the 256x256 tile's ragged edges;
 # more rows than the narrow tiles' 128; a K with a partial 128-byte step for fp8.
 CONFIG_SHAPES = [(1, 264, 1024), (100, 520, 768), (300, 1032, 2048), (513, 264, 256),
-                 (1100, 776, 1024), (77, 136, 4096)]
+                 (1100, 776, 1024), (77, 136, 4096), (16, 1032, 4096), (29, 264, 2048)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
@@ -541,6 +541,7 @@ def test_every_gemm_config_bit_equal(ops, shape, dtype):
     from cozyq import prebuilt
 
     m, n, k = shape
+    configs = list(range(-1, prebuilt.GEMM_CONFIGS))
     x = activations(m, k, seed=m * 7 + k)
     data, scale = laws.int8_weight_rowwise(weights(n, k, seed=n))
     b = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 0.1).to(dtype)
@@ -548,7 +549,7 @@ def test_every_gemm_config_bit_equal(ops, shape, dtype):
     for bias in (None, b):
         want = laws.int8_product(q.cpu(), s.cpu(), data, scale, dtype)
         want = want if bias is None else want + bias
-        for config in range(-1, prebuilt.GEMM_CONFIGS):
+        for config in configs:
             got = ops.int8_gemm(q, s, data.to(DEV), scale.to(DEV),
                                 None if bias is None else bias.to(DEV), dtype, config)  # fmt: skip
             assert torch.equal(got.cpu(), want), (config, bias is None)
@@ -557,11 +558,29 @@ def test_every_gemm_config_bit_equal(ops, shape, dtype):
     if k % 16 == 0:
         f8, f8s = laws.fp8_weight(weights(n, k, seed=n + 1))
         q8, s8 = ops.fp8_quantize(x.to(DEV))
-        outs = [ops.fp8_gemm(q8, s8, f8.to(DEV), f8s.to(DEV), b.to(DEV), dtype, c)
-                for c in range(-1, prebuilt.GEMM_CONFIGS)]  # fmt: skip
-        for config, out in zip(range(-1, prebuilt.GEMM_CONFIGS), outs):
+        outs = [ops.fp8_gemm(q8, s8, f8.to(DEV), f8s.to(DEV), b.to(DEV), dtype, c) for c in configs]
+        for config, out in zip(configs, outs):
             assert torch.equal(out, outs[1]), config
         assert_close(outs[0], laws.fp8_exact(x, f8, f8s, b))
+
+
+@pytest.mark.parametrize("shape", [(16, 520, 4112), (3, 264, 80), (32, 136, 1040)],
+                         ids=lambda s: "x".join(map(str, s)))  # fmt: skip
+def test_fp8_configs_partial_k_steps(ops, shape):
+    """Where K ends inside a 128-byte step: every config gives the same bits (zeros past K, the
+    same MFMA order), with bias, within tolerance of the exact law."""
+    from cozyq import prebuilt
+
+    m, n, k = shape
+    x = activations(m, k, seed=m + k)
+    f8, f8s = laws.fp8_weight(weights(n, k, seed=n + 3))
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 0.1).to(torch.bfloat16)
+    q8, s8 = ops.fp8_quantize(x.to(DEV))
+    outs = [ops.fp8_gemm(q8, s8, f8.to(DEV), f8s.to(DEV), b.to(DEV), torch.bfloat16, c)
+            for c in range(prebuilt.GEMM_CONFIGS)]  # fmt: skip
+    for config, out in enumerate(outs):
+        assert torch.equal(out, outs[1]), config
+    assert_close(outs[4], laws.fp8_exact(x, f8, f8s, b))
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
