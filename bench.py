@@ -739,7 +739,9 @@ def nvfp4_routes(torch, ops, weight, second, k: int, n: int) -> list:
             (lambda: ops.nvfp4_gemm(x, w, s, second, None, torch.bfloat16))
         preroll(torch, reference, 30)
         med = Timer(torch).interleaved({"cozyq": mine, "decode_blas": reference}, batch=8)
-        return {"M": m, "K": kk, "N": nn, "kernel": "nvfp4_gemv_kernel" if m <= 64 else "nvfp4_gemm_kernel<W4A16>",
+        kernel = "nvfp4_gemm_kernel<W4A16>" if m > 64 else (
+            "nvfp4_rows_kernel" if m > 8 and kk % 128 == 0 and -(-nn // 64) >= 192 else "nvfp4_gemv_kernel")
+        return {"M": m, "K": kk, "N": nn, "kernel": kernel,
                 "us": med["cozyq"]["ms"] * 1e3, "decode_blas_us": med["decode_blas"]["ms"] * 1e3,
                 "tflops": 2.0 * m * nn * kk / (med["cozyq"]["ms"] * 1e-3) / 1e12}
 

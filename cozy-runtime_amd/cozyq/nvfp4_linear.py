@@ -30,10 +30,10 @@ Dtype = Any
 
 #: The reference's GEMV limit (`internal/nvfp4_linear.py:60`).
 DECODE_ROWS = 16
-#: Up to this many rows the GEMV serves (its kernel takes up to 64): the weight is read once,
-#: 0.56 bytes a weight. Measured against decode + hipBLASLt on three weights (3072², 12288x3072,
-#: 14336x4096): 1.3-5.7x faster up to 48 rows; at 64 it loses on the largest.
-GEMV_ROWS = 48
+#: Up to this many rows the GEMV serves: the weight is read once, 0.56 bytes a weight. Measured
+#: against decode + hipBLASLt on three weights (3072², 12288x3072, 14336x4096): 1.9-5.7x faster
+#: at every M up to 64.
+GEMV_ROWS = 64
 #: The K multiple of the nvfp4 GEMM (one 64-element step); other shapes decode and call the
 #: library GEMM.
 GEMM_K = 64

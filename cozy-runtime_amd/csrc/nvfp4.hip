@@ -177,24 +177,152 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
     }
 }
 
+// The row-block form for 5..64 rows (K % 128 == 0): a workgroup of 4 waves takes 64 weight rows,
+// each wave 16 of them over all of K, so no partial sums meet; the activation's 16·kMB rows come
+// through LDS in 512-column chunks (LDS-DMA, a ring of 2), read once per workgroup instead of once
+// per wave, and a wave keeps kAhead macro steps of its codes and scales in flight in registers.
+// Per macro step a lane decodes its row's 32 weights (two E4M3 blocks) and feeds one MFMA per
+// activation block, as the GEMV above does; a block's sums run in the same order for any kMB.
+typedef __attribute__((address_space(3))) void GemvLds;
+constexpr int kRowBlockFrom = 8;                  // rows above which the row-block form runs
+constexpr int kChunkCols = 512;                   // activation columns a chunk
+constexpr int kXRowBytes = 2 * kChunkCols + 16;   // one activation row of a chunk, padded
+constexpr int kRowsAhead = 8;                     // macro steps of codes in flight a wave
+
+template <int N>
+__device__ __forceinline__ void gemv_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// One wave's share of a chunk's activation rows: row r (r % 4 == wave) is one 1 KiB load.
+template <int kMB>
+__device__ __forceinline__ void gemv_chunk(__amdgpu_buffer_rsrc_t xr, uint8_t* slot, int chunk, int M, int K,
+                                           int wave, int lane) {
+    const int col = chunk * (2 * kChunkCols) + 16 * lane;  // byte within a row
+#pragma unroll
+    for (int j = 0; j < 4 * kMB; ++j) {
+        const int r = 4 * j + wave;
+        const uint32_t off = (r < M && col < 2 * K) ? static_cast<uint32_t>(r * 2 * K + col) : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (GemvLds*)(slot + r * kXRowBytes), 16, off, 0, 0, 0);
+    }
+}
+
+template <bool kXHalf, bool kOutHalf, int kMB>
+__global__ __launch_bounds__(256) void nvfp4_rows_kernel(const uint16_t* __restrict__ x,
+                                                         const uint8_t* __restrict__ w,
+                                                         const uint8_t* __restrict__ scale,
+                                                         const float* __restrict__ scale_2,
+                                                         uint16_t* __restrict__ out, int M, int N, int K) {
+    constexpr int kSlot = 16 * kMB * kXRowBytes;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[2 * kSlot];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int n0 = blockIdx.x * 64 + 16 * wave;  // the wave's first weight row
+    const int row = n0 + (lane & 15);
+    const int sub = lane >> 4;
+    const int col_tiles = K / 64;
+    const __amdgpu_buffer_rsrc_t wr = bounded_rsrc(w, static_cast<int64_t>(N) * (K / 2));
+    const __amdgpu_buffer_rsrc_t sr = bounded_rsrc(scale, static_cast<int64_t>((N + 127) / 128 * 128) * col_tiles * 4);
+    const __amdgpu_buffer_rsrc_t xr = bounded_rsrc(x, static_cast<int64_t>(M) * K * 2);
+    // Rows past N read past the codes' end (zeros).
+    const int64_t code_base = static_cast<int64_t>(row < N ? row : N) * (K / 2) + 16 * sub;
+    const int tile_row = (row >> 7) * col_tiles, in_tile = (row & 31) * 16 + ((row & 127) >> 5) * 4;
+    const int macro = K / 128, chunks = (macro + 3) / 4;
+
+    i32x4 code[kRowsAhead];
+    uint32_t sbyte[kRowsAhead];
+    auto load = [&](int t, int slot) {  // past the last step: zeros, never used
+        const bool live = t < macro;
+        code[slot] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+            wr, live ? static_cast<int>(code_base + 64 * t) : 0x7ffffff0, 0, 0));
+        const int b = 8 * t + 2 * sub;  // the first of its two blocks (even)
+        const int sidx = row < N && live ? ((tile_row + (b >> 2)) * 512 + in_tile + (b & 3)) : 0x7ffffff0;
+        sbyte[slot] = __builtin_amdgcn_raw_buffer_load_b16(sr, sidx, 0, 0);
+    };
+
+    f32x4 acc[kMB];
+#pragma unroll
+    for (int b = 0; b < kMB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    gemv_chunk<kMB>(xr, xs, 0, M, K, wave, lane);
+#pragma unroll
+    for (int t = 0; t < kRowsAhead; ++t) load(t, t);
+
+    // kRowsAhead / 4 chunks (the register window) an iteration, so that slots are static.
+    constexpr int kWindowChunks = kRowsAhead / 4;
+    for (int c0 = 0; c0 < chunks; c0 += kWindowChunks) {
+#pragma unroll
+        for (int h = 0; h < kWindowChunks; ++h) {
+            const int c = c0 + h;
+            // Chunk c landed (the loads issued after its DMA: at most the 8 window refills of
+            // the chunk before), and every wave is done with chunk c - 1's slot.
+            gemv_vmcnt<2 * 4>();
+            __syncthreads();
+            if (c >= chunks) break;
+            gemv_chunk<kMB>(xr, xs + ((c + 1) & 1) * kSlot, c + 1, M, K, wave, lane);
+            const uint8_t* xc = xs + (c & 1) * kSlot;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 4 * c + i, slot = 4 * h + i;
+                if (t < macro) {
+                    const float s0 = e4m3_value(sbyte[slot] & 0xffu), s1 = e4m3_value((sbyte[slot] >> 8) & 0xffu);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const i32x4 wq = weights8<kXHalf>(static_cast<uint32_t>(code[slot][q]), q < 2 ? s0 : s1);
+#pragma unroll
+                        for (int b = 0; b < kMB; ++b) {
+                            const i32x4 xv = *reinterpret_cast<const i32x4*>(
+                                xc + (16 * b + (lane & 15)) * kXRowBytes + 256 * i + 2 * (32 * sub + 8 * q));
+                            acc[b] = mfma16<kXHalf>(wq, xv, acc[b]);
+                        }
+                    }
+                }
+                load(t + kRowsAhead, slot);
+            }
+        }
+    }
+    gemv_vmcnt<0>();  // the zero loads past the end land before the wave ends
+
+    // D[i][m]: lane holds MFMA rows 4·(lane/16) + r of column m = lane % 16.
+    const float g = scale_2[0];
+    const int n = n0 + 4 * sub;
+#pragma unroll
+    for (int b = 0; b < kMB; ++b) {
+        const int m = 16 * b + (lane & 15);
+        if (m >= M) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (n + r < N) out[static_cast<int64_t>(m) * N + n + r] = narrow<kOutHalf>(acc[b][r] * g);
+    }
+}
+
 }  // namespace
 
 hipError_t nvfp4_gemv(const void* x, bool x_half, const uint8_t* w, const uint8_t* scale, const float* scale_2,
                       void* out, bool out_half, int M, int N, int K, hipStream_t s) {
-    const dim3 grid((N + 127) / 128 * 8), block(64 * kGemvWaves);
     const auto* xp = static_cast<const uint16_t*>(x);
     auto* op = static_cast<uint16_t*>(out);
+    // More than 8 rows on a weight whose 64-row groups alone give 192 workgroups: the row-block
+    // kernel (the activation read once per workgroup); otherwise the K-split GEMV.
+    const bool rows = M > kRowBlockFrom && K % 128 == 0 && (N + 63) / 64 >= 192;
     auto go = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, block, 0, s, xp, w, scale, scale_2, op, M, N, K);
+        if (rows)
+            hipLaunchKernelGGL(kernel, dim3((N + 63) / 64), dim3(256), 0, s, xp, w, scale, scale_2, op, M, N, K);
+        else
+            hipLaunchKernelGGL(kernel, dim3((N + 127) / 128 * 8), dim3(64 * kGemvWaves), 0, s, xp, w, scale, scale_2, op, M, N, K);
         return hipGetLastError();
     };
     auto blocks = [&](auto xh, auto oh) {
         constexpr bool kX = decltype(xh)::value, kO = decltype(oh)::value;
-        switch ((M + 15) / 16) {
+        switch ((M + 15) / 16 + (rows ? 4 : 0)) {
             case 1: return go(nvfp4_gemv_kernel<kX, kO, 1>);
             case 2: return go(nvfp4_gemv_kernel<kX, kO, 2>);
             case 3: return go(nvfp4_gemv_kernel<kX, kO, 3>);
             case 4: return go(nvfp4_gemv_kernel<kX, kO, 4>);
+            case 5: return go(nvfp4_rows_kernel<kX, kO, 1>);
+            case 6: return go(nvfp4_rows_kernel<kX, kO, 2>);
+            case 7: return go(nvfp4_rows_kernel<kX, kO, 3>);
+            case 8: return go(nvfp4_rows_kernel<kX, kO, 4>);
             default: return hipErrorInvalidValue;
         }
     };
