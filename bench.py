@@ -740,7 +740,7 @@ def nvfp4_routes(torch, ops, weight, second, k: int, n: int) -> list:
         preroll(torch, reference, 30)
         med = Timer(torch).interleaved({"cozyq": mine, "decode_blas": reference}, batch=8)
         kernel = "nvfp4_gemm_kernel<W4A16>" if m > 64 else (
-            "nvfp4_rows_kernel" if m > 8 and kk % 128 == 0 and -(-nn // 64) >= 192 else "nvfp4_gemv_kernel")
+            "nvfp4_rows_kernel" if m > 4 and kk % 128 == 0 and -(-nn // 64) >= 192 else "nvfp4_gemv_kernel")
         return {"M": m, "K": kk, "N": nn, "kernel": kernel,
                 "us": med["cozyq"]["ms"] * 1e3, "decode_blas_us": med["decode_blas"]["ms"] * 1e3,
                 "tflops": 2.0 * m * nn * kk / (med["cozyq"]["ms"] * 1e-3) / 1e12}

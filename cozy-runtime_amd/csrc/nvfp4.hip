@@ -57,6 +57,12 @@ __device__ __forceinline__ i32x4 weights8(uint32_t word, float s) {
     }
 }
 
+// The two E4M3 block scales in the low 16 bits of `b`, as float32: the hardware conversion at
+// scale 1 (exact, NaN for S.1111.111), with no branch.
+__device__ __forceinline__ f32x2n scales2(uint32_t b) {
+    return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(static_cast<int>(b), 1.0f, false);
+}
+
 template <bool kHalf>
 __device__ __forceinline__ f32x4 mfma16(i32x4 a, i32x4 b, f32x4 c) {
     if constexpr (kHalf)
@@ -129,7 +135,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
         }
 #pragma unroll
         for (int j = 0; j < kStepsAhead; ++j) {
-            const float s0 = e4m3_value(sbyte[j] & 0xffu), s1 = e4m3_value((sbyte[j] >> 8) & 0xffu);
+            const f32x2n sc = scales2(sbyte[j]);
+            const float s0 = sc[0], s1 = sc[1];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const i32x4 wq = weights8<kXHalf>(static_cast<uint32_t>(code[j][q]), q < 2 ? s0 : s1);
@@ -179,12 +186,13 @@ __global__ __launch_bounds__(64 * kGemvWaves) void nvfp4_gemv_kernel(const uint1
 
 // The row-block form for 5..64 rows (K % 128 == 0): a workgroup of 4 waves takes 64 weight rows,
 // each wave 16 of them over all of K, so no partial sums meet; the activation's 16·kMB rows come
-// through LDS in 512-column chunks (LDS-DMA, a ring of 2), read once per workgroup instead of once
-// per wave, and a wave keeps kAhead macro steps of its codes and scales in flight in registers.
+// through LDS in 512-column chunks (LDS-DMA, a ring of 3 up to 32 rows, else 2), read once per
+// workgroup instead of once per wave, and a wave keeps kRowsAhead macro steps of its codes and
+// scales in flight in registers.
 // Per macro step a lane decodes its row's 32 weights (two E4M3 blocks) and feeds one MFMA per
 // activation block, as the GEMV above does; a block's sums run in the same order for any kMB.
 typedef __attribute__((address_space(3))) void GemvLds;
-constexpr int kRowBlockFrom = 8;                  // rows above which the row-block form runs
+constexpr int kRowBlockFrom = 4;                  // rows above which the row-block form runs
 constexpr int kChunkCols = 512;                   // activation columns a chunk
 constexpr int kXRowBytes = 2 * kChunkCols + 16;   // one activation row of a chunk, padded
 constexpr int kRowsAhead = 8;                     // macro steps of codes in flight a wave
@@ -215,7 +223,8 @@ __global__ __launch_bounds__(256) void nvfp4_rows_kernel(const uint16_t* __restr
                                                          const float* __restrict__ scale_2,
                                                          uint16_t* __restrict__ out, int M, int N, int K) {
     constexpr int kSlot = 16 * kMB * kXRowBytes;
-    __shared__ __attribute__((aligned(16))) uint8_t xs[2 * kSlot];
+    constexpr int kRing = kMB <= 2 ? 3 : 2;  // activation chunks in LDS (2 in flight when 3)
+    __shared__ __attribute__((aligned(16))) uint8_t xs[kRing * kSlot];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int n0 = blockIdx.x * 64 + 16 * wave;  // the wave's first weight row
@@ -244,9 +253,14 @@ __global__ __launch_bounds__(256) void nvfp4_rows_kernel(const uint16_t* __restr
     f32x4 acc[kMB];
 #pragma unroll
     for (int b = 0; b < kMB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Issue order, per chunk: its activation DMA, then 8 code and scale loads; so at chunk c's
+    // wait the loads issued after chunk c's DMA number 8 + (kRing - 2)·(4·kMB + 8).
     gemv_chunk<kMB>(xr, xs, 0, M, K, wave, lane);
 #pragma unroll
-    for (int t = 0; t < kRowsAhead; ++t) load(t, t);
+    for (int t = 0; t < 4; ++t) load(t, t);
+    if constexpr (kRing == 3) gemv_chunk<kMB>(xr, xs + kSlot, 1, M, K, wave, lane);
+#pragma unroll
+    for (int t = 4; t < kRowsAhead; ++t) load(t, t);
 
     // kRowsAhead / 4 chunks (the register window) an iteration, so that slots are static.
     constexpr int kWindowChunks = kRowsAhead / 4;
@@ -254,18 +268,19 @@ __global__ __launch_bounds__(256) void nvfp4_rows_kernel(const uint16_t* __restr
 #pragma unroll
         for (int h = 0; h < kWindowChunks; ++h) {
             const int c = c0 + h;
-            // Chunk c landed (the loads issued after its DMA: at most the 8 window refills of
-            // the chunk before), and every wave is done with chunk c - 1's slot.
-            gemv_vmcnt<2 * 4>();
+            // Chunk c landed (this wave's rows; the barrier makes every wave's visible), and
+            // every wave is done with chunk c - 1's slot, which takes chunk c + kRing - 1.
+            gemv_vmcnt<8 + (kRing - 2) * (4 * kMB + 8)>();
             __syncthreads();
             if (c >= chunks) break;
-            gemv_chunk<kMB>(xr, xs + ((c + 1) & 1) * kSlot, c + 1, M, K, wave, lane);
-            const uint8_t* xc = xs + (c & 1) * kSlot;
+            gemv_chunk<kMB>(xr, xs + ((c + kRing - 1) % kRing) * kSlot, c + kRing - 1, M, K, wave, lane);
+            const uint8_t* xc = xs + (c % kRing) * kSlot;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = 4 * c + i, slot = 4 * h + i;
                 if (t < macro) {
-                    const float s0 = e4m3_value(sbyte[slot] & 0xffu), s1 = e4m3_value((sbyte[slot] >> 8) & 0xffu);
+                    const f32x2n sc = scales2(sbyte[slot]);
+                    const float s0 = sc[0], s1 = sc[1];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const i32x4 wq = weights8<kXHalf>(static_cast<uint32_t>(code[slot][q]), q < 2 ? s0 : s1);
@@ -302,7 +317,7 @@ hipError_t nvfp4_gemv(const void* x, bool x_half, const uint8_t* w, const uint8_
                       void* out, bool out_half, int M, int N, int K, hipStream_t s) {
     const auto* xp = static_cast<const uint16_t*>(x);
     auto* op = static_cast<uint16_t*>(out);
-    // More than 8 rows on a weight whose 64-row groups alone give 192 workgroups: the row-block
+    // More than 4 rows on a weight whose 64-row groups alone give 192 workgroups: the row-block
     // kernel (the activation read once per workgroup); otherwise the K-split GEMV.
     const bool rows = M > kRowBlockFrom && K % 128 == 0 && (N + 63) / 64 >= 192;
     auto go = [&](auto kernel) {

@@ -280,7 +280,7 @@ int cozyq_decode_svdq(int device, const uint8_t* w, const uint8_t* scale, int ti
  *   out[m, n] = round((Σ_k x[m, k] · (e2m1[n, k] · scale[n, k/16])) · scale_2), float32 sums.
  * w [N, K/2] E2M1 codes, element 2k in the low nibble; scale E4M3 in cuBLAS's 128x4 tiles over
  * [N, K/16] (the leaf's resident layout); scale_2 one float32. x [M, K] bf16 or fp16 (x_half),
- * 16-byte aligned; out [M, N] bf16 or fp16. 0 ≤ M ≤ 64, K % 32 == 0. Past 8 rows, with K % 128 == 0
+ * 16-byte aligned; out [M, N] bf16 or fp16. 0 ≤ M ≤ 64, K % 32 == 0. Past 4 rows, with K % 128 == 0
  * and at least 192 64-row groups in N, a row-block kernel runs (the activation read once per 64
  * weight rows); within each kernel a row's result does not
  * depend on M. */

@@ -38,7 +38,7 @@ def _close(got: torch.Tensor, want: torch.Tensor) -> None:
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (3, 200, 1024), (16, 264, 96), (16, 4096, 3072),
-                                   (17, 200, 160), (40, 4096, 3072), (64, 1032, 2048), (9, 12288, 640),
+                                   (17, 200, 160), (40, 4096, 3072), (64, 1032, 2048), (5, 12288, 640),
                                    (40, 12296, 3072), (64, 14336, 512)])
 def test_nvfp4_gemv_against_the_exact_product(dtype, m, n, k):
     from cozyq import prebuilt
@@ -52,9 +52,9 @@ def test_nvfp4_gemv_against_the_exact_product(dtype, m, n, k):
     _close(got, x.double() @ exact.double().t())
 
 
-@pytest.mark.parametrize("n,sizes", [(4096, (1, 5, 16, 17, 33, 50)), (12288, (9, 16, 17, 33, 50))])
+@pytest.mark.parametrize("n,sizes", [(4096, (1, 5, 16, 17, 33, 50)), (12288, (5, 9, 16, 17, 33, 50))])
 def test_nvfp4_gemv_rows_do_not_depend_on_m(n, sizes):
-    """Within a kernel (the K-split GEMV; the row-block form past 8 rows when N gives 192
+    """Within a kernel (the K-split GEMV; the row-block form past 4 rows when N gives 192
     64-row groups) a row's bits do not depend on M, and repeat."""
     from cozyq import prebuilt
 
