@@ -116,13 +116,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cozyq_bake_norms": (
         c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]
     ),
-    "cozyq_bake_nvfp4_refit": (c_int, [c_int, _P, _P, _P, c_double, _P, _P, c_int64, c_int64, c_int64, c_uint32, c_int, _P]),
-    "cozyq_bake_feedback": (c_int, [c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P]),
+    "cozyq_bake_nvfp4_refit": (
+        c_int, [c_int, _P, _P, _P, c_double, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_uint32, c_int, _P]
+    ),
+    "cozyq_bake_feedback": (c_int, [c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P]),
     "cozyq_bake_stats": (
-        c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]
+        c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]
     ),
     "cozyq_bake_row_amax": (
-        c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]
+        c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P]
     ),
     "cozyq_bake_rotate_factor": (c_int, [c_int, _P, _P, c_int64, c_int64, _P]),
     "cozyq_host_e4m3": (None, [_P, _P, c_int64]),

@@ -27,11 +27,8 @@ the same bytes when alpha is a power of two and can differ in the last bit other
 A stochastic eager bake takes its noise from `seed` or draws `seed` from `generator`; without
 either it refuses, rather than reuse one stream.
 
-Not built, raising NotImplementedError:
-- nvfp4's `refit` grid together with a gain, LoKr rows or `Stats`;
-- nvfp4's `regrid`, which the reference does not define;
-- `bake_rowwise`'s `refit` / `regrid` / feedback together with LoKr rows.
-Tensors off the GPU raise ValueError.
+Every grid takes a gain (plain and nvfp4 forms), LoKr rows and `Stats`; nvfp4's `regrid` is
+its `refit`, as in the reference (`grid != "keep"`). Tensors off the GPU raise ValueError.
 """
 
 from __future__ import annotations
@@ -407,15 +404,13 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
         raise ValueError("a row-scaled bake keeps a contiguous float32 row scale")
     up32, down32 = up_a.to(torch.float32).contiguous(), down.to(torch.float32).contiguous()
     more_rows = _more_rows(torch, more, raw.shape[0], False)
-    if more_rows is not None and (grid != "keep" or feedback):
-        raise NotImplementedError("cozyq refits or feeds back rowwise scales from up @ down alone (no LoKr rows)")
     ops = _ops(raw)
     began = time.perf_counter()
     before = None if stats is None else {"data": raw.clone(), "scale": scales.clone()}
     if grid == "keep":
         new = scales.clone()
     else:
-        amax = ops.bake_norms(ROWWISE, raw, scales, up32, down32, cols=raw.shape[1], amax=True)
+        amax = ops.bake_norms(ROWWISE, raw, scales, up32, down32, cols=raw.shape[1], amax=True, more=more_rows)
         # amax / 448 as torch runs it on a GPU (the reference's eager bake included): times the
         # float32 reciprocal, written out so that it does not depend on that detail.
         new = (amax * (1.0 / E4M3_MAX)).clamp(min=ROW_SCALE_FLOOR)
@@ -426,7 +421,7 @@ def bake_rowwise(torch: Any, data: Tensor, scale: Tensor, down: Tensor, up: Tens
     if feedback:
         # Each element's nearest-rounding error carried into the next of its 32-column run, the
         # eager law's order `(decode · scale + delta) / new` on every grid, `keep`'s included.
-        ops.bake_feedback(raw, scales, up32, down32, new)
+        ops.bake_feedback(raw, scales, up32, down32, new, more=more_rows)
     else:
         # `keep` too bakes onto a row scale (the kept one), for the eager order above.
         ops.bake(ROWWISE, raw, scales, up32, down32, seed & SEED_MASK, more=more_rows, flags=flags, rescale=new)
@@ -454,14 +449,13 @@ def bake_nvfp4(torch: Any, weight: Tensor, scale: Tensor, scale_2: Tensor, down:
                seed: int | None = None) -> None:  # fmt: skip
     """Bake into canonical `nvfp4` (`internal/lora_bake.py:458-525`). `keep`: the second level
     kept and a block's scale refitted only past 7/6 of it. `refit`: the second level set from
-    the baked tensor's amax and every block's scale from its own, saturation-free."""
+    the baked tensor's amax and every block's scale from its own, saturation-free; `regrid` is
+    `refit` (the reference branches on `grid != "keep"`, `:498`)."""
     if grid not in GRIDS:
         raise ValueError(f"no grid {grid!r}")
-    if grid == "regrid":
-        raise NotImplementedError("cozyq bakes nvfp4 on grid 'keep' or 'refit'")
     flags = _rounding_flags(rounding)
     seed = _noise_seed(torch, seed, generator, flags == 0)
-    if grid == "refit":
+    if grid != "keep":
         _bake_nvfp4_refit(torch, weight, scale, scale_2, down, up, alpha, flags=flags, seed=seed, stats=stats,
                           more=more, gain=gain)  # fmt: skip
         return
@@ -480,25 +474,35 @@ def _bake_nvfp4_refit(torch: Any, weight: Tensor, scale: Tensor, scale_2: Tensor
                       alpha: float, *, flags: int, seed: int, stats: Any, more: Dense | None,
                       gain: Tensor | None) -> None:  # fmt: skip
     """`bake_nvfp4(grid="refit")` (`internal/lora_bake.py:495-525`): the baked tensor's amax (the
-    row maxima of `cozyq_bake_row_amax`, then their maximum) sets the new second level
-    `amax / 2688` in float64 (1 for all zeros), and one launch refits every block on it."""
-    if gain is not None or more is not None or stats is not None:
-        raise NotImplementedError("cozyq refits nvfp4 from up @ down alone (no gain, LoKr rows or Stats)")
+    row maxima of `cozyq_bake_row_amax` over `gain · decode + up @ down + more`, then their
+    maximum) sets the new second level `amax / 2688` in float64 (1 for all zeros), and one launch
+    refits every block on it. `Stats` decode the weight before at the stored level and after at
+    the new one."""
+    began = time.perf_counter()
     raw, blocks = weight.view(torch.uint8), scale.view(torch.uint8)
     rows, cols = int(raw.shape[0]), 2 * int(raw.shape[1])
     up32 = _scaled_up(torch, up, alpha).to(torch.float32).contiguous()
     down32 = down.to(torch.float32).contiguous()
-    second = scale_2.to(torch.float32).reshape(-1)[:1].contiguous()
+    gain32 = None if gain is None else gain.to(torch.float32).reshape(-1).contiguous()
+    more_rows = _more_rows(torch, more, rows, False)
+    # A copy: `second` must keep the stored level while `scale_2` takes the new one.
+    second = scale_2.to(torch.float32).reshape(-1)[:1].clone()
     ops = _ops(raw)
     stored_second = float(second[0])
+    before = None if stats is None else {"data": raw.clone(), "blocks": blocks.clone(), "second": second}
     amax = 0.0
     if rows and cols:
         amax = float(ops.bake_norms(NVFP4, raw, None, up32, down32, cols=cols, blocks=blocks, second=second,
-                                    amax=True).max())  # fmt: skip
+                                    amax=True, gain=gain32, more=more_rows).max())  # fmt: skip
     level = amax / (E4M3_MAX * 6.0) if amax > 0 else 1.0
-    ops.bake_nvfp4_refit(raw, blocks, second, up32, down32, seed & SEED_MASK, level, flags=flags)
+    ops.bake_nvfp4_refit(raw, blocks, second, up32, down32, seed & SEED_MASK, level, flags=flags, gain=gain32,
+                         more=more_rows)  # fmt: skip
     if level != stored_second:
         scale_2.copy_(torch.full_like(scale_2, level))
+    if stats is not None:
+        after = {"data": raw, "blocks": blocks,
+                 "second": torch.full((1,), level, dtype=torch.float32, device=raw.device)}  # fmt: skip
+        _account(torch, stats, NVFP4, before, after, up32, down32, cols, gain32, more_rows, began)
 
 
 def warm(torch: Any, device: int) -> None:

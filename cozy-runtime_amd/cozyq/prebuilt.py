@@ -836,32 +836,36 @@ class Prebuilt:
         self._check(code, "the LoRA bake")
 
     def bake_nvfp4_refit(self, data: Tensor, blocks: Tensor, second: Tensor, up: Tensor, down: Tensor,
-                         seed: int, level: float, *, flags: int = 0) -> None:  # fmt: skip
+                         seed: int, level: float, *, flags: int = 0, gain: Tensor | None = None,
+                         more: Tensor | None = None) -> None:  # fmt: skip
         """`cozyq_bake_nvfp4_refit` in place (`bake_nvfp4` with `grid="refit"`,
-        `internal/lora_bake.py:458-525`): decodes at `second`, refits every block on the new
-        second level `level` (a float64 the caller then stores), `flags` 1 for nearest."""
+        `internal/lora_bake.py:458-525`): decodes at `second` (times `gain` per row), adds
+        `up @ down` (and `more`), refits every block on the new second level `level` (a float64
+        the caller then stores), `flags` 1 for nearest."""
         rows, cols = int(data.shape[0]), 2 * int(data.shape[1])
         if tuple(blocks.shape) != (rows, cols // 16) or not blocks.is_contiguous():
             raise ValueError(f"nvfp4 bake: block scales must be contiguous [{rows}, {cols // 16}]")
-        rank = self._factors(up, down, rows, cols, (data, blocks, second))
+        rank = self._factors(up, down, rows, cols, (data, blocks, second), gain, more)
         code = self._lib.cozyq_bake_nvfp4_refit(
             self.index, data.data_ptr(), blocks.data_ptr(), second.data_ptr(), float(level), up.data_ptr(),
-            down.data_ptr(), rows, cols, rank, seed & 0xFFFFFFFF, flags, self._stream(),
+            down.data_ptr(), _ptr(gain), _ptr(more), rows, cols, rank, seed & 0xFFFFFFFF, flags, self._stream(),
         )  # fmt: skip
         self._check(code, "the nvfp4 refit LoRA bake")
 
-    def bake_feedback(self, data: Tensor, scale: Tensor, up: Tensor, down: Tensor, fresh: Tensor) -> None:
+    def bake_feedback(self, data: Tensor, scale: Tensor, up: Tensor, down: Tensor, fresh: Tensor,
+                      more: Tensor | None = None) -> None:  # fmt: skip
         """`cozyq_bake_feedback` in place (`encode_e4m3` with `feedback` under `bake_rowwise`,
         `internal/lora_bake.py:163-197`, `:319-363`): `data` contiguous E4M3 [rows, cols],
         `scale` its float32 row scales, `fresh` float32 [rows] the scales after the bake (the
-        same values for `keep`); every 32-column run carries its nearest-rounding error."""
+        same values for `keep`), `more` LoKr's dense rows added to the delta; every 32-column run
+        carries its nearest-rounding error."""
         rows, cols = (int(v) for v in data.shape)
-        rank = self._factors(up, down, rows, cols, (data, scale))
+        rank = self._factors(up, down, rows, cols, (data, scale), None, more)
         if fresh.dtype != self.torch.float32 or fresh.numel() != rows or not fresh.is_contiguous():
             raise ValueError(f"LoRA bake: new row scales must be contiguous float32 with {rows} values")
         code = self._lib.cozyq_bake_feedback(
             self.index, data.data_ptr(), scale.data_ptr(), fresh.data_ptr(), up.data_ptr(),
-            down.data_ptr(), rows, cols, rank, self._stream(),
+            down.data_ptr(), _ptr(more), rows, cols, rank, self._stream(),
         )  # fmt: skip
         self._check(code, "the error-feedback LoRA bake")
 
@@ -884,19 +888,29 @@ class Prebuilt:
 
     def bake_norms(self, form: int, data: Tensor, scale: Tensor | None, up: Tensor, down: Tensor,
                    *, cols: int, blocks: Tensor | None = None, second: Tensor | None = None,
-                   amax: bool = False) -> Tensor:  # fmt: skip
+                   amax: bool = False, gain: Tensor | None = None,
+                   more: Tensor | None = None) -> Tensor:  # fmt: skip
         """`cozyq_bake_norms` (`norms`, `internal/lora_bake.py:653-689`): each row's L2 norm of
         the decoded weight plus `up @ down`, float32 [rows]; with `amax`, `cozyq_bake_row_amax`
-        (each row's max |·|). form 5 is nvfp4 (codes `data`, `blocks`, `second`)."""
+        (each row's max |·|, the decoded rows times `gain` and LoKr's `more` added if given).
+        form 5 is nvfp4 (codes `data`, `blocks`, `second`)."""
         rows = int(data.shape[0])
+        if not amax and (gain is not None or more is not None):
+            raise ValueError("bake_norms: a gain or dense rows enter the row maxima only")
         stored = tuple(t for t in (data, scale, blocks, second) if t is not None)
-        rank = self._factors(up, down, rows, cols, stored)
+        rank = self._factors(up, down, rows, cols, stored, gain, more)
         out = self.torch.empty(rows, dtype=self.torch.float32, device=data.device)
-        entry = self._lib.cozyq_bake_row_amax if amax else self._lib.cozyq_bake_norms
-        code = entry(
-            self.index, form, data.data_ptr(), _ptr(scale), _ptr(blocks), _ptr(second),
-            up.data_ptr(), down.data_ptr(), rows, cols, rank, out.data_ptr(), self._stream(),
-        )  # fmt: skip
+        if amax:
+            code = self._lib.cozyq_bake_row_amax(
+                self.index, form, data.data_ptr(), _ptr(scale), _ptr(blocks), _ptr(second),
+                up.data_ptr(), down.data_ptr(), _ptr(gain), _ptr(more), rows, cols, rank,
+                out.data_ptr(), self._stream(),
+            )  # fmt: skip
+        else:
+            code = self._lib.cozyq_bake_norms(
+                self.index, form, data.data_ptr(), _ptr(scale), _ptr(blocks), _ptr(second),
+                up.data_ptr(), down.data_ptr(), rows, cols, rank, out.data_ptr(), self._stream(),
+            )  # fmt: skip
         self._check(code, "the row reduction")
         return out
 
@@ -904,8 +918,9 @@ class Prebuilt:
                    down: Tensor, *, cols: int, gain: Tensor | None = None,
                    more: Tensor | None = None) -> Tensor:  # fmt: skip
         """`cozyq_bake_stats` (`_account`, `internal/lora_bake.py:249-268`): the accounting of one
-        bake from its parts before and after (`data`, and `scale` or `blocks` + `second`), float64
-        [groups, 7] partial sums."""
+        bake from its parts before and after (`data`, and `scale` or `blocks` + `second`; nvfp4's
+        `before["second"]`, if given, is the level the stored weight decoded at before a refit),
+        float64 [groups, 7] partial sums."""
         data = after["data"]
         rows = int(data.shape[0])
         rank = self._factors(up, down, rows, cols, tuple(after.values()) + tuple(before.values()), gain, more)
@@ -913,8 +928,8 @@ class Prebuilt:
         code = self._lib.cozyq_bake_stats(
             self.index, form, before["data"].data_ptr(), data.data_ptr(), _ptr(before.get("scale")),
             _ptr(after.get("scale")), _ptr(before.get("blocks")), _ptr(after.get("blocks")),
-            _ptr(after.get("second")), _ptr(gain), _ptr(more), up.data_ptr(), down.data_ptr(), rows,
-            cols, rank, partial.data_ptr(), self._stream(),
+            _ptr(before.get("second", after.get("second"))), _ptr(after.get("second")), _ptr(gain), _ptr(more),
+            up.data_ptr(), down.data_ptr(), rows, cols, rank, partial.data_ptr(), self._stream(),
         )  # fmt: skip
         self._check(code, "the bake accounting")
         return partial

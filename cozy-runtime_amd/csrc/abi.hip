@@ -581,8 +581,8 @@ int cozyq_bake_nvfp4(int device, uint8_t* data, uint8_t* blocks, const float* se
 }
 
 int cozyq_bake_nvfp4_refit(int device, uint8_t* data, uint8_t* blocks, const float* second, double level,
-                           const float* up, const float* down, int64_t rows, int64_t cols, int64_t rank,
-                           uint32_t seed, int flags, void* stream) {
+                           const float* up, const float* down, const float* gain, const float* more, int64_t rows,
+                           int64_t cols, int64_t rank, uint32_t seed, int flags, void* stream) {
     if (!bake_shape(rows, cols, rank) || cols % 16 || (flags & ~cozyq::kBakeNearest) || !(level > 0.0) ||
         !(level < 3.4e38))
         return hipErrorInvalidValue;
@@ -590,7 +590,7 @@ int cozyq_bake_nvfp4_refit(int device, uint8_t* data, uint8_t* blocks, const flo
     if (!data || !blocks || !second || (rank > 0 && (!up || !down))) return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
-    cozyq::BakeOptions o{nullptr, nullptr, flags, nullptr};
+    cozyq::BakeOptions o{gain, more, flags, nullptr};
     o.refit = true;
     o.level = level;
     return cozyq::bake_nvfp4(data, blocks, second, up, down, o, static_cast<int>(rows), static_cast<int>(cols),
@@ -598,11 +598,14 @@ int cozyq_bake_nvfp4_refit(int device, uint8_t* data, uint8_t* blocks, const flo
 }
 
 static int bake_rows(int device, int form, const void* data, const float* scale, const uint8_t* blocks,
-                     const float* second, const float* up, const float* down, int64_t rows, int64_t cols,
-                     int64_t rank, float* out, bool amax, void* stream) {
+                     const float* second, const float* up, const float* down, const float* gain,
+                     const float* more, int64_t rows, int64_t cols, int64_t rank, float* out, bool amax,
+                     void* stream) {
     if (form < cozyq::kBakeBf16 || form > cozyq::kBakeNvfp4 || !bake_shape(rows, cols, rank) ||
         (form == cozyq::kBakeNvfp4 && cols % 16))
         return hipErrorInvalidValue;
+    // A gain multiplies plain and nvfp4 rows only (the row-scaled forms take none).
+    if (gain && (form == cozyq::kBakeRowwise || form == cozyq::kBakeInt8)) return hipErrorInvalidValue;
     if (rows == 0) return hipSuccess;
     const bool scaled = form == cozyq::kBakeRowwise || form == cozyq::kBakeInt8;
     if (!out || (cols > 0 && !data) || (scaled && !scale) || (form == cozyq::kBakeNvfp4 && (!blocks || !second)) ||
@@ -610,37 +613,41 @@ static int bake_rows(int device, int form, const void* data, const float* scale,
         return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
-    return cozyq::bake_norms(form, data, scale, blocks, second, up, down, static_cast<int>(rows),
+    return cozyq::bake_norms(form, data, scale, blocks, second, up, down, gain, more, static_cast<int>(rows),
                              static_cast<int>(cols), static_cast<int>(rank), out, amax, on(stream));
 }
 
 int cozyq_bake_norms(int device, int form, const void* data, const float* scale, const uint8_t* blocks,
                      const float* second, const float* up, const float* down, int64_t rows, int64_t cols,
                      int64_t rank, float* out, void* stream) {
-    return bake_rows(device, form, data, scale, blocks, second, up, down, rows, cols, rank, out, false, stream);
+    return bake_rows(device, form, data, scale, blocks, second, up, down, nullptr, nullptr, rows, cols, rank, out,
+                     false, stream);
 }
 
 int cozyq_bake_row_amax(int device, int form, const void* data, const float* scale, const uint8_t* blocks,
-                        const float* second, const float* up, const float* down, int64_t rows, int64_t cols,
-                        int64_t rank, float* out, void* stream) {
-    return bake_rows(device, form, data, scale, blocks, second, up, down, rows, cols, rank, out, true, stream);
+                        const float* second, const float* up, const float* down, const float* gain,
+                        const float* more, int64_t rows, int64_t cols, int64_t rank, float* out, void* stream) {
+    return bake_rows(device, form, data, scale, blocks, second, up, down, gain, more, rows, cols, rank, out, true,
+                     stream);
 }
 
 int cozyq_bake_feedback(int device, uint8_t* data, const float* scale, const float* fresh, const float* up,
-                        const float* down, int64_t rows, int64_t cols, int64_t rank, void* stream) {
+                        const float* down, const float* more, int64_t rows, int64_t cols, int64_t rank,
+                        void* stream) {
     if (!bake_shape(rows, cols, rank)) return hipErrorInvalidValue;
     if (rows == 0 || cols == 0) return hipSuccess;
     if (!data || !scale || !fresh || (rank > 0 && (!up || !down))) return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
-    return cozyq::bake_feedback(data, scale, fresh, up, down, static_cast<int>(rows), static_cast<int>(cols),
+    return cozyq::bake_feedback(data, scale, fresh, up, down, more, static_cast<int>(rows), static_cast<int>(cols),
                                 static_cast<int>(rank), on(stream));
 }
 
 int cozyq_bake_stats(int device, int form, const void* before, const void* after, const float* scale_before,
                      const float* scale_after, const uint8_t* blocks_before, const uint8_t* blocks_after,
-                     const float* second, const float* gain, const float* more, const float* up,
-                     const float* down, int64_t rows, int64_t cols, int64_t rank, double* partial, void* stream) {
+                     const float* second, const float* second_after, const float* gain, const float* more,
+                     const float* up, const float* down, int64_t rows, int64_t cols, int64_t rank, double* partial,
+                     void* stream) {
     if (form < cozyq::kBakeBf16 || form > cozyq::kBakeNvfp4 || !bake_shape(rows, cols, rank) ||
         (form == cozyq::kBakeNvfp4 && cols % 16))
         return hipErrorInvalidValue;
@@ -652,7 +659,8 @@ int cozyq_bake_stats(int device, int form, const void* before, const void* after
         return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
-    const cozyq::BakeStats st{before, after, scale_before, scale_after, blocks_before, blocks_after, second, gain, more};
+    const cozyq::BakeStats st{before, after, scale_before, scale_after, blocks_before, blocks_after, second, gain, more,
+                              second_after};
     return cozyq::bake_stats(form, st, up, down, static_cast<int>(rows), static_cast<int>(cols),
                              static_cast<int>(rank), partial, on(stream));
 }

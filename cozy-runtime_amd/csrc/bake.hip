@@ -310,7 +310,8 @@ __global__ __launch_bounds__(kBakeThreads) void bake_feedback_kernel(uint8_t* __
                                                                      const float* __restrict__ scale,
                                                                      const float* __restrict__ fresh,
                                                                      const float* __restrict__ up,
-                                                                     const float* __restrict__ down, int rows,
+                                                                     const float* __restrict__ down,
+                                                                     const float* __restrict__ more, int rows,
                                                                      int cols, int rank) {
     __shared__ float up_lds[kRankChunk][kTileRows];
     __shared__ float down_lds[kRankChunk][kTileCols];
@@ -327,8 +328,11 @@ __global__ __launch_bounds__(kBakeThreads) void bake_feedback_kernel(uint8_t* __
         for (int j = 0; j < 8; ++j) {
             const int cl = tile_col(cg, j), col = col0 + cl;
             float payload = 0.0f;  // columns past the end pad the run with zeros
-            if (row < rows && col < cols)
-                payload = (e4m3_sat(data[static_cast<int64_t>(row) * cols + col]) * unit + acc[i][j]) / now;
+            if (row < rows && col < cols) {
+                const int64_t at = static_cast<int64_t>(row) * cols + col;
+                const float d = more != nullptr ? acc[i][j] + more[at] : acc[i][j];
+                payload = (e4m3_sat(data[at]) * unit + d) / now;
+            }
             stage[rl][cl] = payload;
         }
     }
@@ -456,7 +460,9 @@ __global__ __launch_bounds__(kBakeThreads) void bake_norms_kernel(const void* __
                                                                   const uint8_t* __restrict__ blocks,
                                                                   const float* __restrict__ second,
                                                                   const float* __restrict__ up,
-                                                                  const float* __restrict__ down, int rows, int cols,
+                                                                  const float* __restrict__ down,
+                                                                  const float* __restrict__ gain,
+                                                                  const float* __restrict__ more, int rows, int cols,
                                                                   int rank, float* __restrict__ out) {
     __shared__ float up_lds[kRankChunk][kTileRows];
     __shared__ float down_lds[kRankChunk][kTileCols];
@@ -472,6 +478,7 @@ __global__ __launch_bounds__(kBakeThreads) void bake_norms_kernel(const void* __
             if (row >= rows) continue;
             float unit = 1.0f;
             if constexpr (kForm == kBakeRowwise || kForm == kBakeInt8) unit = scale[row];
+            const float g = gain != nullptr ? gain[row] : 1.0f;
             const int64_t line0 = static_cast<int64_t>(row) * cols;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -489,7 +496,11 @@ __global__ __launch_bounds__(kBakeThreads) void bake_norms_kernel(const void* __
                     const uint32_t code = (col & 1) ? (byte >> 4) : (byte & 15u);
                     value = e2m1_of(code) * (e4m3_sat(blocks[static_cast<int64_t>(row) * (cols / 16) + col / 16]) * second[0]);
                 }
-                const double t = static_cast<double>(value + acc[i][j]);
+                // The eager target: the decoded row times its gain, plus the delta and the dense
+                // rows, each step rounded on its own.
+                if (gain != nullptr) value = value * g;
+                const float d = more != nullptr ? acc[i][j] + more[at] : acc[i][j];
+                const double t = static_cast<double>(value + d);
                 if constexpr (kMax) sums[i] = __builtin_fmax(sums[i], __builtin_fabs(t));
                 else sums[i] += t * t;
             }
@@ -524,6 +535,7 @@ struct StatsArgs {
     const uint8_t* blocks_before;
     const uint8_t* blocks_after;
     const float* second;
+    const float* second_after;  // kBakeNvfp4: the level `after` decodes at (`refit` sets a new one)
     const float* gain;
     const float* more;
 };
@@ -554,6 +566,7 @@ __global__ __launch_bounds__(kBakeThreads) void bake_stats_kernel(StatsArgs a, c
     const int row0 = blockIdx.x * kTileRows;
     const int tid = threadIdx.x, rg = tid >> 4, cg = tid & 15;
     const float level = kForm == kBakeNvfp4 ? a.second[0] : 1.0f;
+    const float level_after = kForm == kBakeNvfp4 ? a.second_after[0] : 1.0f;
     double sum[5] = {0.0, 0.0, 0.0, 0.0, 0.0};  // target², delta², error², kept, saturated
     double effect = 0.0, effect_error = 0.0;
     // The rank-space projections are taken kStatRanks ranks at a time (LDS holds one slice per
@@ -581,7 +594,7 @@ __global__ __launch_bounds__(kBakeThreads) void bake_stats_kernel(StatsArgs a, c
                     if constexpr (kForm <= kBakeF32 || kForm == kBakeNvfp4) base = base * gain;
                     const float d = a.more ? acc[i][j] + a.more[at] : acc[i][j];
                     const float target = base + d;
-                    const float stored = stat_value<kForm>(a.after, a.scale_after, a.blocks_after, level, at, row, col, cols);
+                    const float stored = stat_value<kForm>(a.after, a.scale_after, a.blocks_after, level_after, at, row, col, cols);
                     const float err = stored - target;
                     dv[i][j] = d;
                     ev[i][j] = err;
@@ -596,7 +609,7 @@ __global__ __launch_bounds__(kBakeThreads) void bake_stats_kernel(StatsArgs a, c
                         const float code = static_cast<float>(static_cast<const int8_t*>(a.before)[at]);
                         sum[4] += __builtin_fabsf(code + d / a.scale_before[row]) > 127.5f ? 1.0 : 0.0;
                     } else if constexpr (kForm == kBakeNvfp4) {
-                        const float unit = e4m3_sat(a.blocks_after[static_cast<int64_t>(row) * (cols / 16) + col / 16]) * level;
+                        const float unit = e4m3_sat(a.blocks_after[static_cast<int64_t>(row) * (cols / 16) + col / 16]) * level_after;
                         sum[4] += unit > 0.0f && __builtin_fabsf(target / unit) > 6.0f ? 1.0 : 0.0;
                     }
                 }
@@ -703,15 +716,15 @@ hipError_t launch_bake(void* data, const float* scale, const float* up, const fl
 
 template <int kForm>
 hipError_t launch_norms(const void* data, const float* scale, const uint8_t* blocks, const float* second,
-                        const float* up, const float* down, int rows, int cols, int rank, float* out, bool amax,
-                        hipStream_t s) {
+                        const float* up, const float* down, const float* gain, const float* more, int rows, int cols,
+                        int rank, float* out, bool amax, hipStream_t s) {
     const dim3 grid((rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
     if (amax)
         hipLaunchKernelGGL((bake_norms_kernel<kForm, true>), grid, block, 0, s, data, scale, blocks, second, up, down,
-                           rows, cols, rank, out);
+                           gain, more, rows, cols, rank, out);
     else
         hipLaunchKernelGGL((bake_norms_kernel<kForm, false>), grid, block, 0, s, data, scale, blocks, second, up, down,
-                           rows, cols, rank, out);
+                           gain, more, rows, cols, rank, out);
     return hipGetLastError();
 }
 
@@ -748,30 +761,33 @@ hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const
 }
 
 hipError_t bake_norms(int form, const void* data, const float* scale, const uint8_t* blocks, const float* second,
-                      const float* up, const float* down, int rows, int cols, int rank, float* out, bool amax,
-                      hipStream_t s) {
+                      const float* up, const float* down, const float* gain, const float* more, int rows, int cols,
+                      int rank, float* out, bool amax, hipStream_t s) {
+#define COZYQ_NORMS(F) \
+    case F: return launch_norms<F>(data, scale, blocks, second, up, down, gain, more, rows, cols, rank, out, amax, s);
     switch (form) {
-        case kBakeBf16: return launch_norms<kBakeBf16>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
-        case kBakeF16: return launch_norms<kBakeF16>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
-        case kBakeF32: return launch_norms<kBakeF32>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
-        case kBakeRowwise: return launch_norms<kBakeRowwise>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
-        case kBakeInt8: return launch_norms<kBakeInt8>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
-        case kBakeNvfp4: return launch_norms<kBakeNvfp4>(data, scale, blocks, second, up, down, rows, cols, rank, out, amax, s);
+        COZYQ_NORMS(kBakeBf16)
+        COZYQ_NORMS(kBakeF16)
+        COZYQ_NORMS(kBakeF32)
+        COZYQ_NORMS(kBakeRowwise)
+        COZYQ_NORMS(kBakeInt8)
+        COZYQ_NORMS(kBakeNvfp4)
         default: return hipErrorInvalidValue;
     }
+#undef COZYQ_NORMS
 }
 
 hipError_t bake_feedback(uint8_t* data, const float* scale, const float* fresh, const float* up, const float* down,
-                         int rows, int cols, int rank, hipStream_t s) {
+                         const float* more, int rows, int cols, int rank, hipStream_t s) {
     const dim3 grid((cols + kTileCols - 1) / kTileCols, (rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
-    hipLaunchKernelGGL(bake_feedback_kernel, grid, block, 0, s, data, scale, fresh, up, down, rows, cols, rank);
+    hipLaunchKernelGGL(bake_feedback_kernel, grid, block, 0, s, data, scale, fresh, up, down, more, rows, cols, rank);
     return hipGetLastError();
 }
 
 hipError_t bake_stats(int form, const BakeStats& st, const float* up, const float* down, int rows, int cols, int rank,
                       double* partial, hipStream_t s) {
     const StatsArgs a{st.before, st.after, st.scale_before, st.scale_after, st.blocks_before, st.blocks_after,
-                      st.second, st.gain, st.more};
+                      st.second, st.second_after != nullptr ? st.second_after : st.second, st.gain, st.more};
     const dim3 grid((rows + kTileRows - 1) / kTileRows), block(kBakeThreads);
 #define COZYQ_STATS(F) \
     case F: hipLaunchKernelGGL((bake_stats_kernel<F>), grid, block, 0, s, a, up, down, rows, cols, rank, partial); break;

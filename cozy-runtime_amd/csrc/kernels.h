@@ -222,15 +222,17 @@ hipError_t bake(int form, void* data, const float* scale, const float* up, const
 // codes [rows, cols/2], E4M3 block bytes [rows, cols/16], second level at `second`; cols % 16 == 0.
 hipError_t bake_nvfp4(uint8_t* data, uint8_t* blocks, const float* second, const float* up, const float* down,
                       const BakeOptions& o, int rows, int cols, int rank, uint32_t seed, hipStream_t s);
-// Row L2 norms (or, with `amax`, row maxima of |·|) of the decoded weight plus up @ down into out
-// [rows] (float32); form as above, kBakeNvfp4 with `blocks` and `second`.
+// Row L2 norms (or, with `amax`, row maxima of |·|) of the decoded weight (times `gain`, float32
+// [rows], if given) plus up @ down (plus `more` [rows, cols], if given) into out [rows] (float32);
+// form as above, kBakeNvfp4 with `blocks` and `second`.
 hipError_t bake_norms(int form, const void* data, const float* scale, const uint8_t* blocks, const float* second,
-                      const float* up, const float* down, int rows, int cols, int rank, float* out, bool amax,
-                      hipStream_t s);
+                      const float* up, const float* down, const float* gain, const float* more, int rows, int cols,
+                      int rank, float* out, bool amax, hipStream_t s);
 // fp8.rowwise with error feedback: codes from (e4m3·scale + delta) / fresh rounded to nearest
-// with each run of 32 columns carrying its rounding error; fresh = the rows' scales after.
+// with each run of 32 columns carrying its rounding error; fresh = the rows' scales after; `more`
+// (dense rows [rows, cols], or null) adds to the delta.
 hipError_t bake_feedback(uint8_t* data, const float* scale, const float* fresh, const float* up, const float* down,
-                         int rows, int cols, int rank, hipStream_t s);
+                         const float* more, int rows, int cols, int rank, hipStream_t s);
 // A bake's accounting: the weight before and after (each form's parts), the same gain and dense
 // rows the bake took; partial receives 7 doubles per 64-row workgroup ([target², delta², error²,
 // kept, saturated, effect, effect error]). rank ≤ 128.
@@ -244,6 +246,7 @@ struct BakeStats {
     const float* second;
     const float* gain;
     const float* more;
+    const float* second_after = nullptr;  // nvfp4: the level `after` decodes at; null: `second`
 };
 hipError_t bake_stats(int form, const BakeStats& st, const float* up, const float* down, int rows, int cols, int rank,
                       double* partial, hipStream_t s);

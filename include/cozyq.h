@@ -390,13 +390,15 @@ int cozyq_bake_norms(int device, int form, const void* data, const float* scale,
                      const float* down, int64_t rows, int64_t cols, int64_t rank, float* out,
                      void* stream);
 
-/* Each row's max |decoded stored weight + up @ down| (reference: the row amax `bake_rowwise`'s
- * `refit` takes, internal/lora_bake.py:344-346), out float32 [rows]; arguments as
- * `cozyq_bake_norms`'s. A maximum, so the same on every call. */
+/* Each row's max |decoded stored weight · gain + up @ down + more| (reference: the amax
+ * `bake_rowwise`'s `refit` takes, internal/lora_bake.py:344-346, and `bake_nvfp4`'s, :495-500),
+ * out float32 [rows]; `gain` float32 [rows] (plain and nvfp4 forms only) and `more` float32
+ * [rows, cols] (LoKr's dense rows) or null; the other arguments as `cozyq_bake_norms`'s. A
+ * maximum, so the same on every call. */
 int cozyq_bake_row_amax(int device, int form, const void* data, const float* scale,
                         const uint8_t* blocks, const float* second, const float* up,
-                        const float* down, int64_t rows, int64_t cols, int64_t rank, float* out,
-                        void* stream);
+                        const float* down, const float* gain, const float* more, int64_t rows,
+                        int64_t cols, int64_t rank, float* out, void* stream);
 
 /* An nvfp4 bake with `grid="refit"` (reference: `bake_nvfp4`, internal/lora_bake.py:458-525):
  * the target decodes at the stored `second` level (e2m1·(e4m3(block)·second), plus delta); every
@@ -404,24 +406,28 @@ int cozyq_bake_row_amax(int device, int form, const void* data, const float* sca
  * round on e4m3(block)·float(level). `level` is the new second level the caller takes from the
  * baked tensor's amax (amax / 2688 in double, 1 for all zeros) and then stores; flags 0
  * (stochastic, Philox counter row·cols + col) or 1 (nearest). data [rows, cols/2], blocks
- * [rows, cols/16] in place. */
+ * [rows, cols/16] in place. `gain` float32 [rows] multiplies each decoded row and `more` float32
+ * [rows, cols] adds to the delta (each may be null), as in `cozyq_bake_nvfp4`. */
 int cozyq_bake_nvfp4_refit(int device, uint8_t* data, uint8_t* blocks, const float* second,
-                           double level, const float* up, const float* down, int64_t rows,
-                           int64_t cols, int64_t rank, uint32_t seed, int flags, void* stream);
+                           double level, const float* up, const float* down, const float* gain,
+                           const float* more, int64_t rows, int64_t cols, int64_t rank, uint32_t seed,
+                           int flags, void* stream);
 
 /* An fp8.rowwise bake with error feedback (reference: `encode_e4m3(..., "feedback")`,
  * internal/lora_bake.py:163-197, under `bake_rowwise`): payload (e4m3·scale + delta) / fresh
  * (fresh = each row's scale after the bake: the kept one or a refitted one), each element
  * rounded to nearest E4M3 (saturating at 448) with the rounding error of the element before it
  * in its run of 32 columns added first; runs start at column multiples of 32. No noise. data
- * [rows, cols] E4M3 bytes in place; the caller stores `fresh` as the new scale. */
+ * [rows, cols] E4M3 bytes in place; the caller stores `fresh` as the new scale. `more` float32
+ * [rows, cols] (LoKr's dense rows) adds to the delta, or null. */
 int cozyq_bake_feedback(int device, uint8_t* data, const float* scale, const float* fresh,
-                        const float* up, const float* down, int64_t rows, int64_t cols,
-                        int64_t rank, void* stream);
+                        const float* up, const float* down, const float* more, int64_t rows,
+                        int64_t cols, int64_t rank, void* stream);
 
 /* A bake's accounting (reference: `Stats` and `_account`, internal/lora_bake.py:78-123,249-268):
  * the weight's parts before and after a bake (`before` / `after`, and for form 3-4 the row
- * scales, for form 5 the block bytes and `second`), with the gain, dense rows and factors the bake
+ * scales, for form 5 the block bytes and `second`, the level `before` decodes at, and
+ * `second_after`, the level `after` decodes at: null for `second`), with the gain, dense rows and factors the bake
  * took (form 4: `down` and `more` rotated). target = base + delta, decoded as the eager reference
  * decodes; partial receives 7 doubles per 64-row group, ceil(rows / 64) · 7 in all: Σ target²,
  * Σ delta², Σ (stored − target)², Σ (stored − base)·delta, the saturated count, Σ (delta @ downᵀ)²
@@ -430,8 +436,9 @@ int cozyq_bake_feedback(int device, uint8_t* data, const float* scale, const flo
 int cozyq_bake_stats(int device, int form, const void* before, const void* after,
                      const float* scale_before, const float* scale_after,
                      const uint8_t* blocks_before, const uint8_t* blocks_after, const float* second,
-                     const float* gain, const float* more, const float* up, const float* down,
-                     int64_t rows, int64_t cols, int64_t rank, double* partial, void* stream);
+                     const float* second_after, const float* gain, const float* more, const float* up,
+                     const float* down, int64_t rows, int64_t cols, int64_t rank, double* partial,
+                     void* stream);
 
 /* `down` [rank, cols] in an int8-convrot256/1 weight's basis (reference: `rotate_factor`,
  * internal/lora_bake.py:366-369): each 256 columns times the regular Hadamard H4⊗H4⊗H4⊗H4 in

@@ -32,6 +32,11 @@ Pins, exercised in `tests/test_bake.py`:
   (but the reserved E4M3 codes and signed zeros, as the law says); the mean over seeds of a
   stochastic bake is the exact target (statistical bound); nearest rounding for f16 against
   numpy's own cast.
+- `bake_nvfp4_refit`: the saturation-free and half-step bounds of the refit grid, a uniform
+  gain of 2 equal to decoding at twice the level, LoKr rows `u ⊗ v` (exact float32 products)
+  equal to `u`, `v` appended as the chain's last rank (also for `row_amax`, `bake_feedback`);
+  `e4m3_feedback` by a hand-worked run and run-sum conservation; `account`'s `second_after`
+  against the layout-law decoder of `oracle/laws.py`.
 - `rotate_factor`: the reference's Hadamard expression order (`internal/encoding/formats.py:
   664-671`, evaluated left to right, as `laws.hadamard`) and the closed form H·H = 256·I.
 """
@@ -346,19 +351,27 @@ def bake_nvfp4(data: np.ndarray, blocks: np.ndarray, second: float, up: np.ndarr
 
 def bake_nvfp4_refit(data: np.ndarray, blocks: np.ndarray, second: float, up: np.ndarray,
                      down: np.ndarray, seed: int, *, nearest: bool = False,
+                     gain: np.ndarray | None = None, more: np.ndarray | None = None,
                      ) -> tuple[np.ndarray, np.ndarray, np.float32]:  # fmt: skip
     """`bake_nvfp4` with `grid="refit"` (`internal/lora_bake.py:495-525`): the eager target
-    `round(e2m1·(scale·level)) + delta`; the new second level `amax / (6·448)` in float64 (a
-    Python float there), 1 for an all-zero tensor; every block's scale the least E4M3 code at or
-    above `peak / (6·second)` as torch divides by a Python scalar on its GPU (times the float32
-    reciprocal of the float32 divisor); the unit `e4m3(block) · float32(second)`, a payload of 0
-    where it is 0. Returns the new (codes, blocks, float32 second level)."""
+    `round(round(e2m1·(scale·level))·gain) + round(delta + more)` (`decoded` then `_delta`,
+    `:488-505`; no gain or `more`: those factors drop out); the new second level
+    `amax / (6·448)` in float64 (a Python float there), 1 for an all-zero tensor; every block's
+    scale the least E4M3 code at or above `peak / (6·second)` as torch divides by a Python
+    scalar on its GPU (times the float32 reciprocal of the float32 divisor); the unit
+    `e4m3(block) · float32(second)`, a payload of 0 where it is 0. Returns the new (codes,
+    blocks, float32 second level)."""
     rows, cols = data.shape[0], 2 * data.shape[1]
     level = _F32(second)
     codes = np.stack((data & 15, data >> 4), axis=-1).reshape(rows, cols).astype(np.int64)
     scale_level = (e4m3_value(np.repeat(blocks.astype(np.int64), 16, axis=1)) * level).astype(np.float32)
     d = delta(up.astype(np.float32), down.astype(np.float32))
-    target = ((e2m1_value(codes) * scale_level).astype(np.float32) + d).astype(np.float32)
+    if more is not None:
+        d = (d + more.astype(np.float32)).astype(np.float32)
+    base = (e2m1_value(codes) * scale_level).astype(np.float32)
+    if gain is not None:
+        base = (base * gain.astype(np.float32).reshape(-1, 1)).astype(np.float32)
+    target = (base + d).astype(np.float32)
     amax = float(np.abs(target).max()) if target.size else 0.0
     new = amax / (448.0 * 6.0) if amax > 0 else 1.0
     new32 = _F32(new)
@@ -401,21 +414,27 @@ def e4m3_feedback(payload: np.ndarray) -> np.ndarray:
 
 
 def bake_feedback(data: np.ndarray, scale: np.ndarray, up: np.ndarray, down: np.ndarray,
-                  fresh: np.ndarray) -> np.ndarray:
+                  fresh: np.ndarray, more: np.ndarray | None = None) -> np.ndarray:
     """`bake_rowwise` with `feedback` rounding (`internal/lora_bake.py:319-363`): payloads
     `(decode · scale + delta) / fresh` (`fresh` the row scales after the bake, `scale` itself for
-    `keep`) through `e4m3_feedback`."""
+    `keep`; delta `round(up @ down + more)` with LoKr rows) through `e4m3_feedback`."""
     d = delta(up.astype(np.float32), down.astype(np.float32))
+    if more is not None:
+        d = (d + more.astype(np.float32)).astype(np.float32)
     unit = scale.astype(np.float32).reshape(-1, 1)
     target = ((e4m3_value(data) * unit).astype(np.float32) + d).astype(np.float32)
     return e4m3_feedback((target / fresh.astype(np.float32).reshape(-1, 1)).astype(np.float32))
 
 
-def row_amax(data: np.ndarray, scale: np.ndarray, up: np.ndarray, down: np.ndarray) -> np.ndarray:
-    """An fp8.rowwise weight's row maxima of |decode · scale + up @ down|, float32 — the amax
-    `bake_rowwise`'s `refit` takes (`internal/lora_bake.py:344-346`)."""
+def row_amax(data: np.ndarray, scale: np.ndarray, up: np.ndarray, down: np.ndarray,
+             more: np.ndarray | None = None) -> np.ndarray:
+    """An fp8.rowwise weight's row maxima of |decode · scale + round(up @ down + more)|, float32
+    — the amax `bake_rowwise`'s `refit` takes (`internal/lora_bake.py:344-346`)."""
     base = (e4m3_value(data) * scale.astype(np.float32).reshape(-1, 1)).astype(np.float32)
-    target = (base + delta(up.astype(np.float32), down.astype(np.float32))).astype(np.float32)
+    d = delta(up.astype(np.float32), down.astype(np.float32))
+    if more is not None:
+        d = (d + more.astype(np.float32)).astype(np.float32)
+    target = (base + d).astype(np.float32)
     return np.abs(target).max(axis=1).astype(np.float32)
 
 
@@ -465,17 +484,21 @@ def norms(form: int, data: np.ndarray, scale: np.ndarray | None, up: np.ndarray,
 def account(form: int, before: np.ndarray, after: np.ndarray, up: np.ndarray, down: np.ndarray, *,
             scale_before: np.ndarray | None = None, scale_after: np.ndarray | None = None,
             blocks_before: np.ndarray | None = None, blocks_after: np.ndarray | None = None,
-            second: float = 1.0, gain: np.ndarray | None = None,
+            second: float = 1.0, second_after: float | None = None, gain: np.ndarray | None = None,
             more: np.ndarray | None = None) -> dict[str, float]:  # fmt: skip
     """`_account` (`internal/lora_bake.py:249-268`) of one bake from the weight before and after:
     base and stored decoded as the eager reference decodes, delta the FMA chain (plus `more`),
     target = base + delta in float32, the sums in float64; saturation by each form's payload
-    (`|target / scale| > 464`, `|code + delta / scale| > 127.5`, `|target / unit| > 6`)."""
-    def decoded(data, scale, blocks):
+    (`|target / scale| > 464`, `|code + delta / scale| > 127.5`, `|target / unit| > 6`). nvfp4's
+    `before` decodes at `second`, its `after` at `second_after` (a `refit`'s new level; `second`
+    when None)."""
+    level_after = second if second_after is None else second_after
+
+    def decoded(data, scale, blocks, level=second):
         if form == NVFP4:
             rows, cols = data.shape[0], 2 * data.shape[1]
             codes = np.stack((data & 15, data >> 4), axis=-1).reshape(rows, cols)
-            s = (e4m3_value(np.repeat(blocks.astype(np.int64), 16, axis=1)) * _F32(second)).astype(np.float32)
+            s = (e4m3_value(np.repeat(blocks.astype(np.int64), 16, axis=1)) * _F32(level)).astype(np.float32)
             return (e2m1_value(codes) * s).astype(np.float32)
         if form == BF16:
             return (data.astype(np.uint32) << 16).view(np.float32)
@@ -494,7 +517,7 @@ def account(form: int, before: np.ndarray, after: np.ndarray, up: np.ndarray, do
     if more is not None:
         d = (d + more.astype(np.float32)).astype(np.float32)
     target = (base + d).astype(np.float32)
-    stored = decoded(after, scale_after, blocks_after)
+    stored = decoded(after, scale_after, blocks_after, level_after)
     err = (stored - target).astype(np.float32)
     if form == ROWWISE:
         saturated = int((np.abs((target / scale_after.astype(np.float32).reshape(-1, 1)).astype(np.float32)) > 464).sum())
@@ -502,7 +525,7 @@ def account(form: int, before: np.ndarray, after: np.ndarray, up: np.ndarray, do
         payload = (before.astype(np.float32) + (d / scale_before.astype(np.float32).reshape(-1, 1)).astype(np.float32))
         saturated = int((np.abs(payload.astype(np.float32)) > 127.5).sum())
     elif form == NVFP4:
-        unit = np.repeat((e4m3_value(blocks_after.astype(np.int64)) * _F32(second)).astype(np.float32), 16, axis=1)
+        unit = np.repeat((e4m3_value(blocks_after.astype(np.int64)) * _F32(level_after)).astype(np.float32), 16, axis=1)
         ratio = (target / np.where(unit > 0, unit, _F32(1))).astype(np.float32)
         saturated = int(((unit > 0) & (np.abs(ratio) > 6)).sum())
     else:

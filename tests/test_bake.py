@@ -20,6 +20,7 @@ import pytest
 import torch
 
 from oracle import bake as ob
+from oracle import laws
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 CUDA = "cuda:0"
@@ -376,15 +377,17 @@ def test_abi_refuses_bad_bake_options():
     # A new row scale is for fp8.rowwise only, and not with "no delta".
     assert lib.cozyq_bake(0, 4, 16, 16, 16, 16, None, None, 16, 4, 256, 2, 1, 0, None) != 0
     assert lib.cozyq_bake(0, 3, 16, 16, 16, 16, None, None, 16, 4, 8, 2, 1, 2, None) != 0
-    assert lib.cozyq_bake_row_amax(0, 7, 16, None, None, None, 16, 16, 4, 8, 2, 16, None) != 0
+    assert lib.cozyq_bake_row_amax(0, 7, 16, None, None, None, 16, 16, None, None, 4, 8, 2, 16, None) != 0
     assert lib.cozyq_bake_nvfp4(0, 16, 16, 16, 16, 16, None, None, 4, 24, 2, 1, 0, None) != 0
     assert lib.cozyq_bake_norms(0, 6, 16, None, None, None, 16, 16, 4, 8, 2, 16, None) != 0
     assert lib.cozyq_bake_rotate_factor(0, 16, 16, 2, 100, None) != 0
     # nvfp4 refit: a positive finite level, nearest or stochastic only, 16-column blocks.
-    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, 0.0, 16, 16, 4, 32, 2, 1, 0, None) != 0
-    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, float("inf"), 16, 16, 4, 32, 2, 1, 0, None) != 0
-    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, 1.0, 16, 16, 4, 32, 2, 1, 2, None) != 0
-    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, 1.0, 16, 16, 4, 24, 2, 1, 0, None) != 0
+    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, 0.0, 16, 16, None, None, 4, 32, 2, 1, 0, None) != 0
+    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, float("inf"), 16, 16, None, None, 4, 32, 2, 1, 0, None) != 0
+    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, 1.0, 16, 16, None, None, 4, 32, 2, 1, 2, None) != 0
+    assert lib.cozyq_bake_nvfp4_refit(0, 16, 16, 16, 1.0, 16, 16, None, None, 4, 24, 2, 1, 0, None) != 0
+    # A gain belongs to the plain and nvfp4 forms' row maxima only.
+    assert lib.cozyq_bake_row_amax(0, 3, 16, 16, None, None, 16, 16, 16, None, 4, 8, 2, 16, None) != 0
     # Empty shapes succeed without touching a device.
     assert lib.cozyq_bake(0, 0, None, None, None, None, None, None, None, 0, 8, 2, 1, 0, None) == 0
 
@@ -815,26 +818,25 @@ def test_gpu_lokr_rows_bake_bit_exact(form):
     assert np.array_equal(_bytes(stored[key]), want.view(np.uint8).reshape(rows, -1))
 
 
-def test_eager_entry_points_refuse_unbuilt_options():
+def test_eager_entry_points_take_every_grid_option():
+    """Every grid takes LoKr rows, a gain (nvfp4) and `Stats`: off the GPU each combination gets
+    as far as the device check; an unknown grid or rounding is refused."""
     from cozyq import bake as cb
 
     t = torch.zeros(4, 16)
     down, up = torch.zeros(1, 16), torch.zeros(4, 1)
+    dense = lambda a, b: torch.zeros(b - a, 16)  # noqa: E731
     with pytest.raises(ValueError, match="GPU"):
-        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0)  # default grid "refit": built
+        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0)  # default grid "refit"
     with pytest.raises(ValueError, match="no grid"):
         cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, grid="wide")
-    with pytest.raises(ValueError, match="GPU"):
-        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, grid="keep", rounding="feedback")  # built
-    with pytest.raises(NotImplementedError):
-        cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, rounding="feedback",
-                        more=lambda a, b: torch.zeros(b - a, 16))  # fmt: skip
-    with pytest.raises(ValueError, match="GPU"):
-        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit", seed=1)  # built
-    with pytest.raises(NotImplementedError):
-        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="regrid")
-    with pytest.raises(NotImplementedError):
-        cb.bake_nvfp4(torch, t, t, t, down, up, 1.0, grid="refit", gain=torch.ones(4), seed=1)
+    for grid in cb.GRIDS:
+        with pytest.raises(ValueError, match="GPU"):
+            cb.bake_rowwise(torch, t, torch.ones(4), down, up, 1.0, grid=grid, rounding="feedback", more=dense,
+                            stats=cb.Stats())  # fmt: skip
+        with pytest.raises(ValueError, match="GPU"):
+            cb.bake_nvfp4(torch, t, t, torch.ones(1), down, up, 1.0, grid=grid, gain=torch.ones(4), more=dense,
+                          seed=1, stats=cb.Stats())  # fmt: skip
     with pytest.raises(ValueError, match="GPU"):
         cb.bake_plain(torch, t, down, up, 1.0, stats=cb.Stats())  # Stats: built
     with pytest.raises(ValueError):
@@ -1182,3 +1184,192 @@ def test_gpu_bake_rowwise_keep_eager_order(rounding):
     assert np.array_equal(s.cpu().numpy().view(np.uint32), scale.view(np.uint32))
     assert np.array_equal(w.view(torch.uint8).cpu().numpy(), want)
     assert stats.elements == rows * cols
+
+
+def _exact_rank_one(rng, rows: int, cols: int):
+    """A rank-one `u ⊗ v` whose float32 products are exact (few-bit integers times powers of
+    two), so `fma(u, v, acc)` rounds exactly as `acc + (u · v)` does."""
+    u = (rng.integers(-15, 16, rows) * 2.0 ** -6).astype(np.float32)
+    v = (rng.integers(-15, 16, cols) * 2.0 ** -3).astype(np.float32)
+    return u, v, np.outer(u, v).astype(np.float32)
+
+
+def test_oracle_more_is_one_more_rank():
+    """LoKr rows enter the delta after the chain: with `more = u ⊗ v` exact in float32, adding
+    them equals the factors with `u`, `v` appended as the last rank (the chain's last FMA),
+    for the rowwise row maxima, the feedback bake and the nvfp4 refit."""
+    rng = np.random.default_rng(17)
+    rows, cols, rank = 33, 96, 4
+    data, scale, _ = _stored_for(ob.ROWWISE, rows, cols, 18)
+    up = (rng.standard_normal((rows, rank)) * 0.05).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    u, v, more = _exact_rank_one(rng, rows, cols)
+    up2, down2 = np.concatenate([up, u[:, None]], 1), np.concatenate([down, v[None, :]], 0)
+    amax = ob.row_amax(data, scale, up, down, more)
+    assert np.array_equal(amax, ob.row_amax(data, scale, up2, down2))
+    assert not np.array_equal(amax, ob.row_amax(data, scale, up, down))
+    new = ob.refit_scales(amax, False)
+    assert np.array_equal(ob.bake_feedback(data, scale, up, down, new, more), ob.bake_feedback(data, scale, up2, down2, new))
+    codes, blocks = _nvfp4_stored(rows, cols, rng)
+    got = ob.bake_nvfp4_refit(codes, blocks, 0.05, up, down, 9, more=more)
+    want = ob.bake_nvfp4_refit(codes, blocks, 0.05, up2, down2, 9)
+    assert all(np.array_equal(a, b) for a, b in zip(got, want))
+
+
+def test_oracle_refit_uniform_power_of_two_gain_is_a_level():
+    """A gain of 2 on every row doubles each decoded value exactly, as decoding at twice the
+    stored level does: the refit's codes, blocks and new level are the same either way; a
+    per-row gain moves the level to the new peak."""
+    rng = np.random.default_rng(19)
+    rows, cols, rank = 20, 64, 3
+    codes, blocks = _nvfp4_stored(rows, cols, rng)
+    up = (rng.standard_normal((rows, rank)) * 0.1).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    two = np.full(rows, 2.0, np.float32)
+    got = ob.bake_nvfp4_refit(codes, blocks, 0.03, up, down, 4, gain=two)
+    want = ob.bake_nvfp4_refit(codes, blocks, 0.06, up, down, 4)
+    assert all(np.array_equal(a, b) for a, b in zip(got, want))
+    assert np.array_equal(ob.bake_nvfp4_refit(codes, blocks, 0.03, up, down, 4, gain=np.ones(rows, np.float32))[0],
+                          ob.bake_nvfp4_refit(codes, blocks, 0.03, up, down, 4)[0])  # fmt: skip
+    gain = np.linspace(0.5, 3.0, rows).astype(np.float32)
+    _, _, level = ob.bake_nvfp4_refit(codes, blocks, 0.03, np.zeros((rows, 0), np.float32),
+                                      np.zeros((0, cols), np.float32), 4, gain=gain)  # fmt: skip
+    nib = np.stack((codes & 15, codes >> 4), axis=-1).reshape(rows, cols)
+    scaled = (ob.e4m3_value(np.repeat(blocks.astype(np.int64), 16, axis=1)) * np.float32(0.03)).astype(np.float32)
+    decoded = (ob.e2m1_value(nib) * scaled).astype(np.float32)
+    peak = float(np.abs((decoded * gain[:, None]).astype(np.float32)).max())
+    assert float(level) == np.float32(peak / 2688.0)
+
+
+def test_oracle_account_decodes_after_at_the_new_level():
+    """`account` with `second_after`: the error and kept energies against the weight decoded by
+    the layout-law decoder (pinned by the reference's nvfp4 vectors) at each level. That decoder
+    rounds `(e2m1 · scale) · level` once where the eager decode rounds `e2m1 · (scale · level)`
+    twice, hence the 1e-4 tolerance; decoding after at the stale level misses by far more."""
+    rng = np.random.default_rng(23)
+    rows, cols, rank = 16, 64, 3
+    codes, blocks = _nvfp4_stored(rows, cols, rng)
+    up = (rng.standard_normal((rows, rank)) * 0.1).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    new_codes, new_blocks, level = ob.bake_nvfp4_refit(codes, blocks, 0.03, up, down, 4, nearest=True)
+    got = ob.account(ob.NVFP4, codes, new_codes, up, down, blocks_before=blocks, blocks_after=new_blocks,
+                     second=0.03, second_after=float(level))  # fmt: skip
+
+    def decode(c, b, second):
+        return laws.decode_nvfp4(torch.from_numpy(c), torch.from_numpy(b).view(torch.float8_e4m3fn),
+                                 torch.tensor([second]), "row_major", False, False, None,
+                                 torch.float32).double().numpy()  # fmt: skip
+
+    base = decode(codes, blocks, 0.03)
+    target = (base.astype(np.float32) + ob.delta(up, down)).astype(np.float32).astype(np.float64)
+    stored = decode(new_codes, new_blocks, float(level))
+    assert math.isclose(got["error_energy"], float(((stored - target) ** 2).sum()), rel_tol=1e-4)
+    assert math.isclose(got["kept"], float(((stored - base) * ob.delta(up, down)).sum()), rel_tol=1e-4)
+    assert got["saturated"] == 0  # refit is saturation-free
+    stale = ob.account(ob.NVFP4, codes, new_codes, up, down, blocks_before=blocks, blocks_after=new_blocks,
+                       second=0.03)  # fmt: skip
+    assert not math.isclose(stale["error_energy"], got["error_energy"], rel_tol=1e-2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("grid", ["refit", "regrid"])
+@pytest.mark.parametrize("gain,more,nearest", [(True, False, True), (False, True, False), (True, True, False),
+                                               (True, True, True)])
+def test_gpu_bake_nvfp4_refit_options(grid, gain, more, nearest):
+    """`bake_nvfp4(grid=refit|regrid)` with a DoRA gain, LoKr rows and `Stats`: the new level,
+    every block byte and every code bit-exact against the oracle, the accounting against its
+    `account` with the weight before at the stored level and after at the new one."""
+    from cozyq import bake as cb
+
+    rows, cols, rank, seed = 129, 272, 33, 555
+    rng = np.random.default_rng(rows + int(gain) + 2 * int(more))
+    codes, blocks = _nvfp4_stored(rows, cols, rng)
+    up = (rng.standard_normal((rows, rank)) * 0.1).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    g = rng.uniform(0.5, 2.0, rows).astype(np.float32) if gain else None
+    extra = (rng.standard_normal((rows, cols)) * 0.3).astype(np.float32) if more else None
+    want_codes, want_blocks, level = ob.bake_nvfp4_refit(codes, blocks, 0.04, up, down, seed, nearest=nearest,
+                                                         gain=g, more=extra)  # fmt: skip
+    c, b = torch.from_numpy(codes).to(CUDA), torch.from_numpy(blocks).view(torch.float8_e4m3fn).to(CUDA)
+    second = torch.tensor([0.04], device=CUDA)
+    dense = _cuda(extra)
+    stats = cb.Stats()
+    cb.bake_nvfp4(torch, c, b, second, _cuda(down), _cuda(up), 1.0, grid=grid, seed=seed, stats=stats,
+                  rounding="nearest" if nearest else "stochastic", gain=_cuda(g),
+                  more=None if extra is None else (lambda a, z: dense[a:z]))  # fmt: skip
+    torch.cuda.synchronize()
+    assert second.cpu().numpy().view(np.uint32)[0] == np.float32(level).view(np.uint32)
+    assert np.array_equal(b.view(torch.uint8).cpu().numpy(), want_blocks)
+    assert np.array_equal(c.cpu().numpy(), want_codes)
+    want = ob.account(ob.NVFP4, codes, want_codes, up, down, blocks_before=blocks, blocks_after=want_blocks,
+                      second=0.04, second_after=float(level), gain=g, more=extra)  # fmt: skip
+    assert stats.layers == 1 and stats.elements == rows * cols and stats.saturated == want["saturated"]
+    for name in ("weight_energy", "delta_energy", "error_energy", "kept"):
+        assert abs(getattr(stats, name) - want[name]) <= 1e-9 * max(abs(want[name]), 1e-30) + 1e-30, name
+    for name in ("effect_energy", "effect_error"):
+        assert abs(getattr(stats, name) - want[name]) <= 1e-4 * abs(want[name]) + 1e-12, name
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("grid", ["keep", "refit", "regrid"])
+@pytest.mark.parametrize("rounding", ["feedback", "nearest", "stochastic"])
+def test_gpu_bake_rowwise_lokr_rows_on_every_grid(grid, rounding):
+    """`bake_rowwise` with LoKr rows and `Stats` on every grid and rounding: the row maxima (with
+    the rows), the new scales, every code and the accounting against the oracle."""
+    from cozyq import bake as cb
+    from cozyq import prebuilt
+
+    rows, cols, rank, seed = 70, 300, 6, 99
+    data, scale, rng = _stored_for(ob.ROWWISE, rows, cols, 64)
+    up = (rng.standard_normal((rows, rank)) * 0.05).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    extra = (rng.standard_normal((rows, cols)) * 0.2).astype(np.float32)
+    amax = ob.row_amax(data, scale, up, down, extra)
+    new = scale if grid == "keep" else ob.refit_scales(amax, grid == "regrid")
+    if rounding == "feedback":
+        want = ob.bake_feedback(data, scale, up, down, new, extra)
+    else:
+        want = ob.bake(ob.ROWWISE, data, scale, up, down, seed, more=extra, nearest=rounding == "nearest",
+                       rescale=new)  # fmt: skip
+    w = torch.from_numpy(data).view(torch.float8_e4m3fn).to(CUDA)
+    s, dense = _cuda(scale), _cuda(extra)
+    got_amax = prebuilt.library(0).bake_norms(ob.ROWWISE, w.view(torch.uint8), s, _cuda(up), _cuda(down),
+                                             cols=cols, amax=True, more=dense)  # fmt: skip
+    assert np.array_equal(got_amax.cpu().numpy(), amax)
+    stats = cb.Stats()
+    cb.bake_rowwise(torch, w, s, _cuda(down), _cuda(up), 1.0, rounding=rounding, grid=grid, seed=seed,
+                    more=lambda a, z: dense[a:z], stats=stats)  # fmt: skip
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), new.view(np.uint32))
+    got = w.view(torch.uint8).cpu().numpy()
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} codes differ, first at {bad[0].tolist()}"
+    acc = ob.account(ob.ROWWISE, data, want, up, down, scale_before=scale, scale_after=new, more=extra)
+    assert stats.saturated == acc["saturated"] and stats.elements == rows * cols
+    for name in ("weight_energy", "delta_energy", "error_energy", "kept"):
+        assert abs(getattr(stats, name) - acc[name]) <= 1e-9 * max(abs(acc[name]), 1e-30) + 1e-30, name
+
+
+@pytest.mark.gpu
+def test_gpu_nvfp4_row_amax_with_gain_and_rows():
+    """`cozyq_bake_row_amax` on nvfp4 with a gain and LoKr rows: each row's max of
+    |gain · decode + up @ down + more| bit-exact against the oracle's target."""
+    from cozyq import prebuilt
+
+    rows, cols, rank = 65, 144, 7
+    rng = np.random.default_rng(31)
+    codes, blocks = _nvfp4_stored(rows, cols, rng)
+    up = (rng.standard_normal((rows, rank)) * 0.1).astype(np.float32)
+    down = rng.standard_normal((rank, cols)).astype(np.float32)
+    g = rng.uniform(0.5, 2.0, rows).astype(np.float32)
+    extra = (rng.standard_normal((rows, cols)) * 0.3).astype(np.float32)
+    nib = np.stack((codes & 15, codes >> 4), axis=-1).reshape(rows, cols)
+    scaled = (ob.e4m3_value(np.repeat(blocks.astype(np.int64), 16, axis=1)) * np.float32(0.04)).astype(np.float32)
+    base = ((ob.e2m1_value(nib) * scaled).astype(np.float32) * g[:, None]).astype(np.float32)
+    d = (ob.delta(up, down) + extra).astype(np.float32)
+    want = np.abs((base + d).astype(np.float32)).max(axis=1)
+    got = prebuilt.library(0).bake_norms(ob.NVFP4, torch.from_numpy(codes).to(CUDA), None, _cuda(up), _cuda(down),
+                                        cols=cols, blocks=torch.from_numpy(blocks).to(CUDA),
+                                        second=torch.tensor([0.04], device=CUDA), amax=True, gain=_cuda(g),
+                                        more=_cuda(extra))  # fmt: skip
+    assert np.array_equal(got.cpu().numpy(), want)
