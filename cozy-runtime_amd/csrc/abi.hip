@@ -265,7 +265,8 @@ int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales
                          int K, int R, void* stream) {
     if (M < 1 || N < 1 || N % 8 || !fits(K, 64) || (R != 16 && R != 32 && R != 64))
         return hipErrorInvalidValue;
-    if (!aligned16(act) || !aligned16(w) || !aligned16(la) || !aligned16(up))
+    if (!aligned16(act) || !aligned16(w) || !aligned16(la) || !aligned16(up) || !aligned16(out) ||
+        (reinterpret_cast<uintptr_t>(bias) & 3))
         return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();

@@ -175,7 +175,7 @@ constexpr int kThreads = 256;                       // 4 waves, each a 64x64 qua
 constexpr int kStageGroups = 4;                     // 64-groups a stage brings in
 constexpr int kRowBytes = kStageGroups * 32;        // packed bytes of one tile row a stage: 128
 constexpr int kOpBytes = kTile * kRowBytes;         // one operand's stage: 16 KB
-constexpr int kScaleBytes = kStageGroups * kTile * 2;  // fp16 scales [group][row]: 1 KB
+constexpr int kScaleBytes = kStageGroups * kTile * 4;  // fp16 scales [group][row], 4-byte slots: 2 KB
 constexpr int kStageBytes = 2 * kOpBytes + 2 * kScaleBytes;
 constexpr int kStages = 2;
 constexpr uint32_t kOutOfRange = 0x80000000u;       // a buffer offset past num_records reads zeros
@@ -224,7 +224,10 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
     const uint16_t* __restrict__ la, const uint16_t* __restrict__ up,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K,
     int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
+    // The stages, then the tile's 128 biases (read by the epilogue, which stages each wave's
+    // quadrant in the stage area once the loop is done).
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes + 2 * kTile];
+    uint8_t* const bias_l = lds + kStages * kStageBytes;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -261,13 +264,17 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
         chunk[j] = 16 * swz(r, i & 7);
         rowoff[j] = r * half + chunk[j];
     }
-    // The stage's scales: threads 0..127 the activation rows, 128..255 the weight rows; one
-    // row's kStageGroups fp16 scales each, zero past the matrix.
-    const bool wside = tid >= kTile;
-    const int srow = tid & (kTile - 1);
-    const int sglobal = (wside ? n0 : m0) + srow;
-    const bool srow_ok = sglobal < (wside ? N : M);
-    const uint16_t* sbase = (wside ? wscales : ascales) + static_cast<int64_t>(srow_ok ? sglobal : 0) * groups;
+    // The stage's fp16 scales come by 2-byte LDS-DMA, which writes each lane's value into a
+    // 4-byte slot: scale (group g, row r) of an operand sits in slot g·kTile + r. Load q (0..3)
+    // of a wave covers operand c/8, group (c/2)%4 and rows 64·(c%2) + lane, c = 4q + wave; past
+    // the matrix's rows or its last group they read as zeros.
+    const int64_t asspan = static_cast<int64_t>(M - m0) * groups * 2, wsspan = static_cast<int64_t>(N - n0) * groups * 2;
+    const __amdgpu_buffer_rsrc_t asr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(ascales + static_cast<int64_t>(m0) * groups), 0,
+        asspan > 0x7fffffff ? 0x7fffffffu : static_cast<uint32_t>(asspan), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(wscales + static_cast<int64_t>(n0) * groups), 0,
+        wsspan > 0x7fffffff ? 0x7fffffffu : static_cast<uint32_t>(wsspan), 0x00020000);
 
 #define COZYQ_SVDQ_ISSUE(stage)                                                                     \
     do {                                                                                            \
@@ -279,24 +286,28 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (LdsPtr*)(buf_ + base_), 16, off_, 0, 0, 0); \
             __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LdsPtr*)(buf_ + kOpBytes + base_), 16, off_, 0, 0, 0); \
         }                                                                                           \
+        _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                             \
+            const int c_ = 4 * q + wave, g_ = (c_ >> 1) & 3, r_ = 64 * (c_ & 1) + lane;               \
+            const int gg_ = (stage) * kStageGroups + g_;                                            \
+            const uint32_t so_ = gg_ < groups ? static_cast<uint32_t>(2 * (r_ * groups + gg_)) : kOutOfRange; \
+            uint8_t* dst_ = buf_ + 2 * kOpBytes + (c_ >> 3) * kScaleBytes + 4 * (g_ * kTile + 64 * (c_ & 1)); \
+            __builtin_amdgcn_raw_ptr_buffer_load_lds((c_ >> 3) ? wsr : asr, (LdsPtr*)dst_, 2, so_, 0, 0, 0); \
+        }                                                                                           \
     } while (0)
 
-    auto load_scales = [&](int stage, uint16_t* sv) {
-#pragma unroll
-        for (int g = 0; g < kStageGroups; ++g) {
-            const int gg = stage * kStageGroups + g;
-            sv[g] = (srow_ok && gg < groups) ? sbase[gg] : static_cast<uint16_t>(0);
-        }
-    };
-    auto store_scales = [&](int stage, const uint16_t* sv) {
-        uint16_t* dst = reinterpret_cast<uint16_t*>(lds + (stage & 1) * kStageBytes + 2 * kOpBytes +
-                                                    (wside ? kScaleBytes : 0));
-#pragma unroll
-        for (int g = 0; g < kStageGroups; ++g) dst[g * kTile + srow] = sv[g];
-    };
+    // The first stage and the biases are requested before the low-rank product, so their latency
+    // runs under it. Biases: two a lane by 4-byte LDS-DMA (N % 8 == 0: no partial dword).
+    COZYQ_SVDQ_ISSUE(0);
+    if (kBias && wave == 0) {
+        const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(bias + n0), 0, static_cast<uint32_t>(2 * (N - n0)), 0x00020000);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (LdsPtr*)bias_l, 4, 4 * lane, 0, 0, 0);
+    }
 
-    // Accumulators start as the low-rank product la·upᵀ. Block (i, j) of the quadrant: lane l
-    // holds column n = j-block + l%32 and rows m = i-block + 8·(r/4) + 4·(l/32) + r%4.
+    // Every MFMA takes the weight side as its A operand and the activation side as B, so block
+    // (i, j) — activation rows 32i.., weight columns 32j.. of the quadrant — leaves lane l with
+    // row m = 32i + l%32 and columns n = 32j + 8·(r/4) + 4·(l/32) + r%4: runs of four
+    // consecutive outputs of one row. The accumulators start as the low-rank product la·upᵀ.
     f32x16 facc[2][2];
     {
         bf16x8 lv[2][kR / 16], uv[2][kR / 16];
@@ -318,7 +329,7 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
                 for (int r = 0; r < 16; ++r) facc[i][j][r] = 0.0f;
 #pragma unroll
                 for (int kk = 0; kk < kR / 16; ++kk)
-                    facc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lv[i][kk], uv[j][kk], facc[i][j], 0, 0, 0);
+                    facc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(uv[j][kk], lv[i][kk], facc[i][j], 0, 0, 0);
                 // The K loop accumulates 256·(Σ q·q)·sa·sw (the codes enter as 16·q bytes), so
                 // the accumulators run in units of 1/256 until the epilogue; both scalings are
                 // exact.
@@ -344,14 +355,12 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
     const int sa_row = wm * 64 + fr;
     const int sw_col = wn * 64 + fr;
 
-// One group's int32 partial of a 32x32 block: two MFMAs over its two 32-code K halves.
-#define COZYQ_MMA(A, B)                                                                             \
-    __builtin_amdgcn_mfma_i32_32x32x32_i8((A)[1], (B)[1],                                          \
-        __builtin_amdgcn_mfma_i32_32x32x32_i8((A)[0], (B)[0], i32x16{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0), 0, 0, 0)
-// The block's scale products sa[m]·sw[n] as one f16 MFMA with K = 1 (every other k is zero):
+// One 32-code K half of a block's int32 partial (weight fragment A, activation fragment B).
+#define COZYQ_MMA(W, X, C) __builtin_amdgcn_mfma_i32_32x32x32_i8((W), (X), (C), 0, 0, 0)
+// The block's scale products sw[n]·sa[m] as one f16 MFMA with K = 1 (every other k is zero):
 // each product of two fp16 values is exact in float32, and lands where the block's partial does.
-#define COZYQ_T(SA, SB)                                                                             \
-    __builtin_amdgcn_mfma_f32_32x32x16_f16((SA), (SB), f32x16{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0)
+#define COZYQ_T(SW, SA)                                                                             \
+    __builtin_amdgcn_mfma_f32_32x32x16_f16((SW), (SA), f32x16{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0)
 // (The empty asm holds the block's accumulators at this point of the program: without it the
 // arithmetic, which touches no memory, drifts past the scheduling fences below.)
 #define COZYQ_RESCALE(P, T, I, J)                                                                   \
@@ -364,36 +373,30 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
     // One group's scale operands: element 0 of lane group 0 holds the row's (column's) scale;
     // lane group 1's bits are masked to zero (no branch).
     const uint32_t keep = fq == 0 ? 0xffffu : 0u;
-    auto scale_frag = [&](const uint16_t* base, int idx) {
-        const uint32_t bits = static_cast<uint32_t>(base[idx]) & keep;
+    auto scale_frag = [&](const uint32_t* base, int idx) {
+        const uint32_t bits = base[idx] & keep;
         return __builtin_bit_cast(f16x8, i32x4{static_cast<int32_t>(bits), 0, 0, 0});
     };
 
     const int nstages = (groups + kStageGroups - 1) / kStageGroups;
-    uint16_t sv[kStageGroups];
-    COZYQ_SVDQ_ISSUE(0);
-    load_scales(0, sv);
-    store_scales(0, sv);
+    const i32x16 zero = i32x16{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     fence();
     wait_all();
     __syncthreads();
 
     for (int s = 0; s < nstages; ++s) {
         const bool more = s + 1 < nstages;
-        if (more) {
-            COZYQ_SVDQ_ISSUE(s + 1);
-            load_scales(s + 1, sv);
-        }
+        if (more) COZYQ_SVDQ_ISSUE(s + 1);
         const uint8_t* buf = lds + (s & 1) * kStageBytes;
-        const uint16_t* sa_l = reinterpret_cast<const uint16_t*>(buf + 2 * kOpBytes);
-        const uint16_t* sw_l = reinterpret_cast<const uint16_t*>(buf + 2 * kOpBytes + kScaleBytes);
+        const uint32_t* sa_l = reinterpret_cast<const uint32_t*>(buf + 2 * kOpBytes);
+        const uint32_t* sw_l = reinterpret_cast<const uint32_t*>(buf + 2 * kOpBytes + kScaleBytes);
         // A stage past the last group holds zero codes and zero scales: it adds nothing.
         //
-        // Each group runs as four segments that the scheduler may not reorder across: a
-        // segment issues the next block's partial and scale-product MFMAs and then rescales the
-        // block before it (one conversion and one FMA an output), so the matrix core works
-        // while the vector unit rescales. The next group's fragments are read from LDS two or
-        // three segments before their use.
+        // A group is two halves. Each issues the K halves of two blocks interleaved (no MFMA
+        // waits on the one before it) and their scale products at raised wave priority, so a
+        // SIMD's other wave keeps the matrix core fed, then rescales a finished block (one
+        // conversion and one FMA an output) while the matrix core works. The next group's
+        // fragments are read from LDS in the first half and unpacked in the second.
         i32x4 a[2][2], b[2][2];  // [block][K half], unpacked 16·code bytes
         {
 #pragma unroll
@@ -408,11 +411,14 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
             i32x4 na[2], nb[2];
             const f16x8 fa0 = scale_frag(sa_l, g * kTile + sa_row), fa1 = scale_frag(sa_l, g * kTile + sa_row + 32);
             const f16x8 fb0 = scale_frag(sw_l, g * kTile + sw_col), fb1 = scale_frag(sw_l, g * kTile + sw_col + 32);
-            // Segment A: blocks (0,0) and (0,1) issued; next fragments requested; (0,0) rescaled.
-            const i32x16 p00 = COZYQ_MMA(a[0], b[0]);
-            const f32x16 t00 = COZYQ_T(fa0, fb0);
-            const i32x16 p01 = COZYQ_MMA(a[0], b[1]);
-            const f32x16 t01 = COZYQ_T(fa0, fb1);
+            __builtin_amdgcn_s_setprio(1);
+            const i32x16 q00 = COZYQ_MMA(b[0][0], a[0][0], zero);
+            const i32x16 q01 = COZYQ_MMA(b[1][0], a[0][0], zero);
+            const i32x16 p00 = COZYQ_MMA(b[0][1], a[0][1], q00);
+            const i32x16 p01 = COZYQ_MMA(b[1][1], a[0][1], q01);
+            const f32x16 t00 = COZYQ_T(fb0, fa0);
+            const f32x16 t01 = COZYQ_T(fb1, fa0);
+            __builtin_amdgcn_s_setprio(0);
             if (g < kLast) {
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
@@ -422,17 +428,18 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
             }
             COZYQ_RESCALE(p00, t00, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            // Segment B: block (1,0) issued; (0,1) rescaled.
-            const i32x16 p10 = COZYQ_MMA(a[1], b[0]);
-            const f32x16 t10 = COZYQ_T(fa1, fb0);
+            __builtin_amdgcn_s_setprio(1);
+            const i32x16 q10 = COZYQ_MMA(b[0][0], a[1][0], zero);
+            const i32x16 q11 = COZYQ_MMA(b[1][0], a[1][0], zero);
+            const i32x16 p10 = COZYQ_MMA(b[0][1], a[1][1], q10);
+            const i32x16 p11 = COZYQ_MMA(b[1][1], a[1][1], q11);
+            const f32x16 t10 = COZYQ_T(fb0, fa1);
+            const f32x16 t11 = COZYQ_T(fb1, fa1);
+            __builtin_amdgcn_s_setprio(0);
             COZYQ_RESCALE(p01, t01, 0, 1);
             __builtin_amdgcn_sched_barrier(0);
-            // Segment C: block (1,1) issued; (1,0) rescaled.
-            const i32x16 p11 = COZYQ_MMA(a[1], b[1]);
-            const f32x16 t11 = COZYQ_T(fa1, fb1);
             COZYQ_RESCALE(p10, t10, 1, 0);
             __builtin_amdgcn_sched_barrier(0);
-            // Segment D: the next group's fragments unpacked; (1,1) rescaled.
             if (g < kLast) {
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
@@ -443,7 +450,6 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
             COZYQ_RESCALE(p11, t11, 1, 1);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (more) store_scales(s + 1, sv);
         fence();
         wait_all();
         __syncthreads();
@@ -453,23 +459,46 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
 #undef COZYQ_T
 #undef COZYQ_RESCALE
 
-    // Epilogue: + bias, one cast, 2-byte stores (32 consecutive columns a row per instruction).
+    // Epilogue: + bias, one cast; each run of four outputs goes to the wave's 64x64 quadrant in
+    // LDS as one 8-byte write (the stages are free: every wave has passed the loop's last
+    // barrier), and whole 128-byte quadrant rows come back as 16-byte reads and stores.
+    constexpr int kStageRow = 64 * 2 + 16;  // one staged row: 64 outputs + pad
+    uint8_t* const stage = lds + wave * 64 * kStageRow;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn * 64 + 32 * j + fr;
-        float bv = 0.0f;
-        if constexpr (kBias) bv = widen<kOutHalf>(bias[min(n, N - 1)]);
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * fq + (r & 3);
-                if (m < M && n < N) {
-                    float v = facc[i][j][r] * 0.00390625f;  // out of the 1/256 units (exact)
-                    if constexpr (kBias) v += bv;
-                    out[static_cast<int64_t>(m) * N + n] = round_out<kOutHalf>(v);
-                }
+        for (int g = 0; g < 4; ++g) {
+            const int nl = 32 * j + 8 * g + 4 * fq;  // column within the quadrant
+            float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (kBias) {
+                const uint2 bb = *reinterpret_cast<const uint2*>(bias_l + 2 * (wn * 64 + nl));
+                b4[0] = widen<kOutHalf>(static_cast<uint16_t>(bb.x & 0xffff));
+                b4[1] = widen<kOutHalf>(static_cast<uint16_t>(bb.x >> 16));
+                b4[2] = widen<kOutHalf>(static_cast<uint16_t>(bb.y & 0xffff));
+                b4[3] = widen<kOutHalf>(static_cast<uint16_t>(bb.y >> 16));
             }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                uint16_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v = facc[i][j][4 * g + e] * 0.00390625f;  // out of the 1/256 units (exact)
+                    if constexpr (kBias) v += b4[e];
+                    h[e] = round_out<kOutHalf>(v);
+                }
+                *reinterpret_cast<uint2*>(stage + (32 * i + fr) * kStageRow + 2 * nl) =
+                    make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+            }
+        }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): a wave reads back only its own rows
+    const int c = lane & 7;
+    const int n = n0 + wn * 64 + 8 * c;  // N % 8 == 0: a chunk is wholly in or out
+#pragma unroll
+    for (int t8 = 0; t8 < 8; ++t8) {
+        const int rl = (lane >> 3) + 8 * t8;
+        const int m = m0 + wm * 64 + rl;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + rl * kStageRow + 16 * c);
+        if (m < M && n < N) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * N + n) = v;
     }
 }
 

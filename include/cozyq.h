@@ -193,7 +193,7 @@ int cozyq_svdq_int4_quantize(int device, const void* x, int x_half, const float*
 /* SVDQuant W4A4 GEMM, int4-g64 variant (reference: gemm.cpp:180-190 `svdq_gemm`, svdq.cu:
  * 446-485): out = Σ_g (Σ_{k∈g} act·w)·ascales[m,g]·wscales[n,g] + la·upᵀ + bias, float32
  * accumulation, one cast. w [N, K/2] packed like act; wscales [N, K/64] fp16; up [N, R] bf16.
- * K % 64 == 0, N % 8 == 0. */
+ * K % 64 == 0, N % 8 == 0; act, w, la, up and out 16-byte aligned, bias (if any) 4-byte. */
 int cozyq_svdq_int4_gemm(int device, const uint8_t* act, const uint16_t* ascales,
                          const uint8_t* w, const uint16_t* wscales, const void* la,
                          const void* up, const void* bias, void* out, int out_half, int M, int N,
