@@ -240,6 +240,7 @@ def bench_c1(torch, ops, lib, stream) -> dict:
         quantize()
         gemm()
 
+    preroll(torch, step)
     med = Timer(torch).interleaved({"step": step, "gemm": gemm, "quantize": quantize}, batch=16)
     ops_count = 2.0 * m * n * k
     return {"M": m, "K": k, "N": n, "us": med["step"]["ms"] * 1e3,
@@ -296,6 +297,7 @@ def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -
                 launch(raw)
     torch.cuda.synchronize()
     graph.replay()
+    preroll(torch, graph.replay, 30)
     ms = Timer(torch).interleaved({"graph": graph.replay}, batch=2)["graph"]["ms"] / per_graph
     graph.replay()
     torch.cuda.synchronize()
@@ -331,6 +333,7 @@ def _graph_us(torch, launch, per_graph: int, replays: int) -> float:
                 launch(raw)
     torch.cuda.synchronize()
     graph.replay()
+    preroll(torch, graph.replay, 30)
     batch = max(1, min(4, replays // 4))
     return Timer(torch).interleaved({"graph": graph.replay}, batch=batch)["graph"]["ms"] / per_graph * 1e3
 
@@ -429,6 +432,7 @@ def bench_fp8(torch, ops, lib, stream, m: int, steps: int) -> dict:
                                   None, 0, 0, 1, 0, 0.0, 0, None, stream))  # fmt: skip
         gemm()
 
+    preroll(torch, step)
     med = Timer(torch).interleaved({"gemm": gemm, "step": step}, batch=max(2, min(8, steps // 4)))
     ms = med["gemm"]["ms"]
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
@@ -456,6 +460,7 @@ def bench_mx(torch, ops, lib, stream, steps: int) -> dict:
                                      stream))  # fmt: skip
 
         fns[name], sizes[name] = step, (k, n)
+    preroll(torch, lambda: [fn() for fn in fns.values()])
     med = Timer(torch).interleaved(fns, batch=max(2, min(8, steps // 4)))
     result, total_ops, total_ms = {}, 0.0, 0.0
     for name, (k, n) in sizes.items():
@@ -504,6 +509,7 @@ def bench_svdq(torch, ops, lib, stream, steps: int) -> dict:
         quantize()
         gemm()
 
+    preroll(torch, step)
     med = Timer(torch).interleaved({"quantize": quantize, "gemm": gemm, "step": step},
                                    batch=max(2, min(8, steps // 4)))  # fmt: skip
     q_ms, g_ms, ms = med["quantize"]["ms"], med["gemm"]["ms"], med["step"]["ms"]

@@ -54,8 +54,11 @@ SITU, SWIGLU = 3, 4
 #: fused GEMM's configs 1..4 are that table's narrow tiles.
 UNPACK = 0
 UNPACK_ROWS = 257
-#: The GEMM tile configs (`cozyq_gemm`): 0 256x256, 1 128x128, 2 128x64, 3 64x64, 4 32x64.
-GEMM_CONFIGS = 5
+#: The GEMM tile configs (`cozyq_gemm`): 0 256x256, 1 128x128, 2 128x64, 3 64x64, 4 32x64,
+#: 5 256x192.
+GEMM_CONFIGS = 6
+#: The configs with 256-row tiles, which `w4a8_gemm` runs by unpacking the codes first.
+WIDE_TILES = (UNPACK, 5)
 
 INT8, FP8 = _Format("int8", False, 256), _Format("fp8", True, 16)
 MX = _Format("mxfp8", True, 128)
@@ -227,8 +230,8 @@ class Prebuilt:
     ) -> Tensor:
         """`internal/prebuilt.py:180-222`: `q @ unpack(w).T`, both scales and the bias. From
         `UNPACK_ROWS` rows the codes unpack once to int8 and the int8 GEMM multiplies them
-        (config `UNPACK`); fewer rows take the fused GEMM. Every config is the same law, bit for
-        bit."""
+        (config `UNPACK`, or 5 for the 256x192 tile, else the int8 GEMM's shape rule); fewer rows
+        take the fused GEMM. Every config is the same law, bit for bit."""
         torch = self.torch
         if q.dtype != torch.int8 or q.dim() != 2 or not q.is_contiguous() or q.data_ptr() % 16:
             raise ValueError("w4a8_gemm: q must be a contiguous, aligned int8 [M, K]")
@@ -237,7 +240,7 @@ class Prebuilt:
             raise ValueError(f"w4a8_gemm: scales must be contiguous float32 with {rows} values")
         bias = self._w4a8_weight(w, bias, width, out_dtype)
         n = w.codes.shape[0]
-        if config == UNPACK or (config < 0 and rows >= UNPACK_ROWS):
+        if config in WIDE_TILES or (config < 0 and rows >= UNPACK_ROWS):
             levels = torch.empty(n, width, dtype=torch.int8, device=q.device)
             code = self._lib.cozyq_w4a8_unpack(
                 self.index, w.codes.data_ptr(), w.group_scale.data_ptr(), _ptr(w.codebook),

@@ -195,8 +195,8 @@ int cozyq_w4a8_gemm(int device, const int8_t* q, const float* scales, const uint
                     const uint8_t* s, const float* codebook, const float* w_scale, const void* bias,
                     void* out, int out_half, int M, int N, int K, int config, void* stream) {
     if (M < 1 || N < 8 || N % 8 || !fits(K, 256)) return hipErrorInvalidValue;
-    // Configs 1..4 are the narrow tiles; 0 (the 256x256 tile) has no fused 4-bit form.
-    if (config == 0 || config >= cozyq::kGemmConfigs) return hipErrorNotSupported;
+    // Configs 1..4 are the narrow tiles; 0 and 5 (the 256-row tiles) have no fused 4-bit form.
+    if (config == 0 || config >= 5) return hipErrorNotSupported;
     if (!aligned16(q) || !aligned16(w) || (reinterpret_cast<uintptr_t>(out) & 7))
         return hipErrorInvalidValue;
     const OnDevice guard(device);

@@ -1,10 +1,10 @@
-// The 256x256-tile GEMMs on gfx950: int8 W8A8 (exact int32 accumulation on
+// The 256-row-tile GEMMs on gfx950 (256x256, or 256x192 columns): int8 W8A8 (exact int32 accumulation on
 // v_mfma_i32_32x32x32_i8), fp8 e4m3 row-wise (v_mfma_scale_f32_32x32x64_f8f6f4, float32
 // accumulation) and MXFP8 (the same MFMA with each operand's E8M0 block scales fed to the
 // matrix core), with the dequantizing epilogue fused: out = epilogue(q · wᵀ), q [M, K] and
 // w [N, K] with K contiguous, one byte an element. (Few-row GEMMs are gemm_narrow.hip.)
 //
-// A workgroup of 4 waves owns a 256x256 output tile; each wave a 128x128 quadrant as 4x4 MFMA
+// A workgroup of 4 waves owns a 256x256 output tile (256x192: see gemm_tile); each wave a 128x128 quadrant as 4x4 MFMA
 // blocks of 32x32 (256 accumulator registers a lane, held in AGPRs). A step's MFMAs consume 64
 // bytes of K; the LDS holds two buffers of 128 bytes of K (the X and W tiles' 256 rows x 128
 // bytes, and for MX their rows' four E8M0 bytes), so every load moves whole 128-byte cache lines
@@ -49,10 +49,10 @@ constexpr int kEpiBase = 4 * kStageBytes > 2 * kPairBytes ? 4 * kStageBytes : 2 
 constexpr int kWsOff = kEpiBase, kBiasOff = kEpiBase + 1024, kXsOff = kEpiBase + 1536;
 constexpr int kLdsBytes = kEpiBase + 2560;
 
-// Buffer loads a lane issues per buffer: 8 of 16 bytes for each operand, and for MX one of 4
-// bytes for each operand's scales.
-template <int kKind>
-constexpr int kLoads = kKind == kMx ? 18 : 16;
+// Buffer loads a lane issues per buffer: 8 of 16 bytes for X, kTN / 32 for W, and for MX one
+// of 4 bytes for each operand's scales.
+template <int kKind, int kTN = 256>
+constexpr int kLoads = 8 + kTN / 32 + (kKind == kMx ? 2 : 0);
 
 typedef __attribute__((address_space(3))) void LdsPtr;
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
@@ -138,18 +138,24 @@ __device__ __forceinline__ i32x4 half_of(const i32x8& v, int h) {
     return h == 0 ? __builtin_shufflevector(v, v, 0, 1, 2, 3) : __builtin_shufflevector(v, v, 4, 5, 6, 7);
 }
 
-// One 256x256 output tile (tm, tn) by the workgroup's 4 waves, `lds` holding kLdsBytes. The
+// One 256 x kTN output tile (tm, tn) by the workgroup's 4 waves, `lds` holding kLdsBytes. The
 // caller has made sure every wave is done with `lds` from any earlier use. kEpi: 0 the law's
 // dequantization (+ bias), 1 that then tanh-GELU, 2 the raw int32 accumulators (int8 test
-// entry).
-template <int kKind, bool kOutHalf, bool kBias, int kEpi>
+// entry). kTN is 256, or 192: each wave then owns 128 x 96 (3 x 4 blocks), for grids that 256
+// columns would leave a partial round of tiles (N = 3072: 256 tiles of 256 x 192 at M = 4096
+// against 192 of 256 x 256). Each output's K sum runs in the same MFMA order either way.
+template <int kKind, bool kOutHalf, bool kBias, int kEpi, int kTN = 256>
 __device__ __forceinline__ void gemm_tile(
     uint8_t* __restrict__ lds, const uint8_t* __restrict__ X, const uint8_t* __restrict__ W,
     const float* __restrict__ xs, const float* __restrict__ ws, const uint8_t* __restrict__ xe,
     const uint8_t* __restrict__ we, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
     int32_t* __restrict__ acc_out, int64_t ldo, int M, int N, int K, int tm, int tn) {
     static_assert(kEpi != 2 || kKind == kInt8, "raw accumulators are the int8 GEMM's");
+    static_assert(kTN == 256 || kTN == 192, "tile widths: 256 or 192 columns");
     typedef std::conditional_t<kKind == kInt8, i32x16, f32x16> Acc;
+    constexpr int kNI = kTN / 64;      // W blocks of 32 columns a wave
+    constexpr int kHalfN = kTN / 2;    // a wave's columns
+    constexpr int kWLoads = kTN / 32;  // W buffer loads a wave
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA bases go in M0
@@ -158,7 +164,7 @@ __device__ __forceinline__ void gemm_tile(
     // The tile arithmetic divides on the vector unit; the origin is uniform, and buffer
     // descriptors must sit in scalar registers.
     const int m0 = __builtin_amdgcn_readfirstlane(tm * kTile);
-    const int n0 = __builtin_amdgcn_readfirstlane(tn * kTile);
+    const int n0 = __builtin_amdgcn_readfirstlane(tn * kTN);
 
     // Buffer views of this tile's rows: reads past the last row return zeros.
     auto rows_view = [&](const uint8_t* base, int rows_left, int row_bytes) {
@@ -195,7 +201,8 @@ __device__ __forceinline__ void gemm_tile(
             const uint32_t off_ = (k0_ + chunk[j] < K) ? static_cast<uint32_t>(rowoff[j] + k0_) : kOutOfRange; \
             const int base_ = (4 * j + wave) * 1024;                                                 \
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (LdsPtr*)(buf_ + base_), 16, off_, 0, 0, 0); \
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LdsPtr*)(buf_ + kOpBytes + base_), 16, off_, 0, 0, 0); \
+            if (j < kWLoads)                                                                         \
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LdsPtr*)(buf_ + kOpBytes + base_), 16, off_, 0, 0, 0); \
         }                                                                                            \
         if constexpr (kKind == kMx) {                                                                \
             const uint32_t so_ = (4 * (pair) < kb) ? static_cast<uint32_t>(soff + 4 * (pair)) : kOutOfRange; \
@@ -215,7 +222,7 @@ __device__ __forceinline__ void gemm_tile(
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int rw = wn * 128 + i * 32 + fr, rx = wm * 128 + i * 32 + fr;
+                const int rw = wn * kHalfN + min(i, kNI - 1) * 32 + fr, rx = wm * 128 + i * 32 + fr;
                 aoff[e][h][i] = kOpBytes + rw * kPairK + 16 * swz(rw, 4 * e + 2 * h + fq);
                 boff[e][h][i] = rx * kPairK + 16 * swz(rx, 4 * e + 2 * h + fq);
             }
@@ -225,29 +232,34 @@ __device__ __forceinline__ void gemm_tile(
         const int e = step & 1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const i32x4 alo = *reinterpret_cast<const i32x4*>(buf + aoff[e][0][i]);
-            const i32x4 ahi = *reinterpret_cast<const i32x4*>(buf + aoff[e][1][i]);
+            if (i < kNI) {
+                const i32x4 alo = *reinterpret_cast<const i32x4*>(buf + aoff[e][0][i]);
+                const i32x4 ahi = *reinterpret_cast<const i32x4*>(buf + aoff[e][1][i]);
+                f.a[i] = __builtin_shufflevector(alo, ahi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
             const i32x4 blo = *reinterpret_cast<const i32x4*>(buf + boff[e][0][i]);
             const i32x4 bhi = *reinterpret_cast<const i32x4*>(buf + boff[e][1][i]);
-            f.a[i] = __builtin_shufflevector(alo, ahi, 0, 1, 2, 3, 4, 5, 6, 7);
             f.b[i] = __builtin_shufflevector(blo, bhi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
         if constexpr (kKind == kMx) {
             const int shift = 8 * (2 * e + fq);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int rw = wn * 128 + i * 32 + fr, rx = wm * 128 + i * 32 + fr;
-                const uint32_t sw = *reinterpret_cast<const uint32_t*>(buf + 2 * kOpBytes + kScaleBytes + 4 * rw);
+                if (i < kNI) {
+                    const int rw = wn * kHalfN + i * 32 + fr;
+                    const uint32_t sw = *reinterpret_cast<const uint32_t*>(buf + 2 * kOpBytes + kScaleBytes + 4 * rw);
+                    f.sa[i] = static_cast<int>((sw >> shift) & 0xff);
+                }
+                const int rx = wm * 128 + i * 32 + fr;
                 const uint32_t sx = *reinterpret_cast<const uint32_t*>(buf + 2 * kOpBytes + 4 * rx);
-                f.sa[i] = static_cast<int>((sw >> shift) & 0xff);
                 f.sb[i] = static_cast<int>((sx >> shift) & 0xff);
             }
         }
     };
 
-    Acc acc[4][4];
+    Acc acc[kNI][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kNI; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -279,7 +291,7 @@ __device__ __forceinline__ void gemm_tile(
     COZYQ_ISSUE(0);
     COZYQ_ISSUE(1);
     fence();
-    wait_vmcnt<kLoads<kKind>>();  // pair 0 complete
+    wait_vmcnt<kLoads<kKind, kTN>>();  // pair 0 complete
     __builtin_amdgcn_s_barrier();
     fence();
 
@@ -291,13 +303,13 @@ __device__ __forceinline__ void gemm_tile(
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < kNI; ++i)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(half_of(c.a[i], h), half_of(c.b[j], h), acc[i][j], 0, 0, 0);
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < kNI; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     if constexpr (kKind == kMx)
@@ -307,29 +319,32 @@ __device__ __forceinline__ void gemm_tile(
                 }
         }
     };
-    // Issue order within a step: LDS reads spread one (MX: one to two) per MFMA group.
+    // Issue order within a step: LDS reads spread one (MX: one to two) per MFMA group. A step
+    // has 4·kNI MFMA groups and 2·(kNI + 4) fragment reads (MX: and kNI + 4 scale reads); the
+    // reads past the groups (192 columns: 2, MX 3) follow them.
     auto schedule = [&]() {
         if constexpr (kKind == kInt8) {
 #pragma unroll
-            for (int g = 0; g < 16; ++g) {
+            for (int g = 0; g < 4 * kNI; ++g) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
                 __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
             }
         } else if constexpr (kKind == kFp8) {
 #pragma unroll
-            for (int g = 0; g < 16; ++g) {
+            for (int g = 0; g < 4 * kNI; ++g) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
         } else {
 #pragma unroll
-            for (int g = 0; g < 8; ++g) {
+            for (int g = 0; g < 2 * kNI; ++g) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
         }
+        if constexpr (kTN != 256) __builtin_amdgcn_sched_group_barrier(0x100, kKind == kMx ? 3 : 2, 0);
     };
     // Step 2p: the next step's fragments come from the same buffer, which has landed.
     auto even_step = [&](int s, const Frags& cur, Frags& next) {
@@ -348,7 +363,7 @@ __device__ __forceinline__ void gemm_tile(
         COZYQ_ISSUE((s >> 1) + 2);
         fetch(s + 1, next);  // past the last step: unused registers
         mfmas(cur);
-        __builtin_amdgcn_sched_group_barrier(0x020, kLoads<kKind>, 0);  // the buffer loads first
+        __builtin_amdgcn_sched_group_barrier(0x020, kLoads<kKind, kTN>, 0);  // the buffer loads first
         schedule();
     };
     for (int s = 0; s < 2 * np; s += 2) {
@@ -360,7 +375,7 @@ __device__ __forceinline__ void gemm_tile(
     // r, n = i-block column 8·(r/4) + 4·(l/32) + r%4 (MFMA rows are W rows): four runs of four
     // consecutive columns, each an 8-byte store. The lane's 64 weight scales and biases and 4
     // row scales are read from LDS once, ahead of the arithmetic.
-    const int nl = n0 + wn * 128 + 4 * fq;  // the lane's first column
+    const int nl = n0 + wn * kHalfN + 4 * fq;  // the lane's first column
     if constexpr (kEpi == 2) {
         wait_vmcnt<0>();  // the zero-filling loads past the last step land before the LDS is released
 #pragma unroll
@@ -368,7 +383,7 @@ __device__ __forceinline__ void gemm_tile(
             const int m = m0 + wm * 128 + j * 32 + fr;
             if (m >= M) continue;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < kNI; ++i)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int n = nl + i * 32 + 8 * g;
@@ -386,10 +401,10 @@ __device__ __forceinline__ void gemm_tile(
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
     fence();
-    float4 wsv[4][4];
-    uint2 bv[4][4];
+    float4 wsv[kNI][4];
+    uint2 bv[kNI][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kNI; ++i)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int c = nl - n0 + i * 32 + 8 * g;  // column within the tile
@@ -405,12 +420,12 @@ __device__ __forceinline__ void gemm_tile(
     // the next block row's arithmetic runs (the stores are not waited on).
     uint8_t* stage = lds + wave * kStageBytes;
     const int cl = (lane & 15) * 8;  // first of the lane's 8 columns in a stored row
-    const int n = n0 + wn * 128 + cl;
+    const int n = n0 + wn * kHalfN + cl;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int ml = j * 32 + fr;  // row within the quadrant
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < kNI; ++i)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const float w4[4] = {wsv[i][g].x, wsv[i][g].y, wsv[i][g].z, wsv[i][g].w};
@@ -446,13 +461,14 @@ __device__ __forceinline__ void gemm_tile(
                 *reinterpret_cast<uint2*>(stage + ml * kStageRow + 2 * col) = packed;
             }
         wait_lgkmcnt0();  // a wave reads back only its own rows
-        // Whole rows: 16 lanes cover one quadrant row's 256 bytes; 4 rows an instruction.
+        // Whole rows: 16 lanes cover one quadrant row's 256 bytes (kHalfN = 96: the first 12 of
+        // them, 192 bytes); 4 rows an instruction.
 #pragma unroll
         for (int r0 = 0; r0 < 32; r0 += 4) {
             const int rl = j * 32 + r0 + (lane >> 4);
             const int m = m0 + wm * 128 + rl;
             const uint4 v = *reinterpret_cast<const uint4*>(stage + rl * kStageRow + 2 * cl);
-            if (m < M && n < N) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * ldo + n) = v;
+            if (m < M && n < N && cl < kHalfN) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * ldo + n) = v;
         }
     }
 }
@@ -470,7 +486,7 @@ __device__ __forceinline__ int2 launch_tile(int b, int tiles_m, int tiles_n) {
     return make_int2(group * kGroupM + within % gm, within / gm);
 }
 
-template <int kKind, bool kOutHalf, bool kBias, int kEpi>
+template <int kKind, bool kOutHalf, bool kBias, int kEpi, int kTN = 256>
 __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     const uint8_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ xs,
     const float* __restrict__ ws, const uint8_t* __restrict__ xe, const uint8_t* __restrict__ we,
@@ -480,7 +496,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     // for whole-row stores (rows padded to kStageRow bytes).
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
     const int2 t = launch_tile(blockIdx.x, tiles_m, tiles_n);
-    gemm_tile<kKind, kOutHalf, kBias, kEpi>(lds, X, W, xs, ws, xe, we, bias, out, acc_out, ldo, M, N, K, t.x, t.y);
+    gemm_tile<kKind, kOutHalf, kBias, kEpi, kTN>(lds, X, W, xs, ws, xe, we, bias, out, acc_out, ldo, M, N, K, t.x, t.y);
 }
 
 #undef COZYQ_ISSUE

@@ -48,9 +48,10 @@ hipError_t linear_int8_noalloc(const void* x, bool half, int rotation, int8_t* q
                                hipStream_t s);
 
 // The rowwise GEMMs' tile configs: 0 the 256x256 kernel, 1..4 the narrow kernels' 128x128,
-// 128x64, 64x64 and 32x64 (kGemmConfigs in all); -1 lets gemm_config choose by shape. Every
-// config gives the same int8 output bit for bit; an unknown config is hipErrorNotSupported.
-constexpr int kGemmConfigs = 5;
+// 128x64, 64x64 and 32x64, 5 the 256x192 kernel (kGemmConfigs in all); -1 lets gemm_config
+// choose by shape. Every config gives the same int8 output bit for bit; an unknown config is
+// hipErrorNotSupported.
+constexpr int kGemmConfigs = 6;
 int gemm_config(bool fp8, int M, int N, int K);
 int narrow_config(int M, int N);
 hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,

@@ -85,8 +85,9 @@ typedef void* (*cozyq_allocate_fn)(size_t bytes, void* context);
  * bias are 16-byte aligned. family must
  * be 0 (the one CDNA4 MFMA family). config names a tile as the reference's table does
  * (gemm_sm80.cu:233-289, gemm_fp8.cu:15-58), gfx950's own: 0 the 256x256 tile, 1 128x128,
- * 2 128x64, 3 64x64, 4 32x64 (rows x columns); -1 chooses by shape (cozyq_gemm_config); 5 and
- * above return hipErrorNotSupported. Every config gives the same int8 output bit for bit.
+ * 2 128x64, 3 64x64, 4 32x64, 5 256x192 (rows x columns); -1 chooses by shape
+ * (cozyq_gemm_config); 6 and above return hipErrorNotSupported. Every config gives the same int8
+ * output bit for bit.
  * N % 8 == 0; K % 256 (int8) or K % 16 (fp8). */
 int cozyq_gemm(int device, int family, int fp8, const void* q, const float* scales,
                const void* w, const float* w_scale, const void* bias, void* out, int64_t ldo,
@@ -144,8 +145,8 @@ int cozyq_gemm_i32(int device, const int8_t* q, const int8_t* w, int32_t* acc, i
  * (internal/prebuilt.py:471-492). The codes are unpacked in registers on the way to the int8
  * MFMA; the epilogue is cozyq_gemm's int8 law with w_scale [N], bit for bit. out [M, N].
  * N % 8 == 0, K % 256 == 0; q and w 16-byte aligned, out 8-byte aligned. config names
- * cozyq_gemm's narrow tiles 1..4 (-1: by rows); 0 (the 256x256 tile, which multiplies the
- * codes unpacked by cozyq_w4a8_unpack) and 5 and above return hipErrorNotSupported. */
+ * cozyq_gemm's narrow tiles 1..4 (-1: by rows); 0 and 5 (the 256-row tiles, which multiply
+ * the codes unpacked by cozyq_w4a8_unpack) and 6 and above return hipErrorNotSupported. */
 int cozyq_w4a8_gemm(int device, const int8_t* q, const float* scales, const uint8_t* w,
                     const uint8_t* s, const float* codebook, const float* w_scale, const void* bias,
                     void* out, int out_half, int M, int N, int K, int config, void* stream);

@@ -42,15 +42,18 @@ def test_constants():
 
 
 def test_gemm_config_rule():
-    """`cozyq_gemm_config` (what config -1 runs): the 256x256 tile (0) from 160 of its tiles;
+    """`cozyq_gemm_config` (what config -1 runs): from 160 256x256 tiles a 256-row tile, the
+    256x192 one (5) where its grid needs fewer than 6/5 the rounds of 256x256 tiles over the 256
+    CUs (a round of 3/4-size tiles at ~90% of the rate), else 256x256 (0);
     else, when N gives a 64-column tile 192 workgroups, the one (4: 32x64, 3: 64x64, 2: 128x64)
     that takes every row (up to 128) in one M-tile; else the largest of 1: 128x128, 2: 128x64,
     3: 64x64, 4: 32x64 whose grid reaches 288 workgroups, else 32x64. Each case below is the
     fastest config the MI355X sweep (`bench.py --only tiles`) measured within 3% at that shape,
     for int8 and fp8 alike, except (8192, 640, 2560), where 128x64 is 8% faster."""
     lib = _lib.load()
-    cases = {(4096, 12288, 3072): 0, (4096, 3072, 3072): 0, (1024, 14336, 4096): 0,
-             (16384, 3072, 3072): 0, (4096, 3072, 12288): 0, (2048, 3072, 3072): 1,
+    cases = {(4096, 12288, 3072): 0, (4096, 3072, 3072): 5, (1024, 14336, 4096): 0,
+             (16384, 3072, 3072): 0, (4096, 3072, 12288): 5, (2048, 3072, 3072): 1,
+             (4096, 9216, 3072): 5, (4096, 14336, 4096): 0,
              (1024, 3072, 3072): 2, (768, 3072, 3072): 2, (512, 3072, 3072): 3,
              (384, 3072, 3072): 3, (1536, 3072, 3072): 1, (512, 14336, 4096): 1,
              (256, 14336, 4096): 2, (256, 12288, 3072): 2, (2048, 1280, 1280): 2,

@@ -533,7 +533,7 @@ CONFIG_SHAPES = [(1, 264, 1024), (100, 520, 768), (300, 1032, 2048), (513, 264, 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("shape", CONFIG_SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_every_gemm_config_bit_equal(ops, shape, dtype):
-    """Every tile config of `cozyq_gemm` (0..4 and the shape rule's -1) gives the int8 law bit
+    """Every tile config of `cozyq_gemm` (0..5 and the shape rule's -1) gives the int8 law bit
     for bit, with and without bias (as the reference checks each explicit tile,
     `internal/bench/gemm.py:418-435`); the fp8 configs agree with one another bit for bit (each
     output's K sum runs in the same MFMA order) and sit within tolerance of the exact law; a
@@ -553,7 +553,7 @@ def test_every_gemm_config_bit_equal(ops, shape, dtype):
             got = ops.int8_gemm(q, s, data.to(DEV), scale.to(DEV),
                                 None if bias is None else bias.to(DEV), dtype, config)  # fmt: skip
             assert torch.equal(got.cpu(), want), (config, bias is None)
-    with pytest.raises(ValueError, match="config 5"):
+    with pytest.raises(ValueError, match=f"config {prebuilt.GEMM_CONFIGS}"):
         ops.int8_gemm(q, s, data.to(DEV), scale.to(DEV), None, dtype, prebuilt.GEMM_CONFIGS)
     if k % 16 == 0:
         f8, f8s = laws.fp8_weight(weights(n, k, seed=n + 1))
