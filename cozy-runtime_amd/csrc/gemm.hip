@@ -41,6 +41,8 @@ hipError_t dispatch(const void* q, const float* xs, const void* w, const float* 
     return hipErrorInvalidValue;
 }
 
+}  // namespace
+
 // The large tiles run one workgroup a CU, so a grid costs its number of rounds over the 256 CUs,
 // each round a tile's time. 256x192 tiles do 3/4 of a 256x256 tile's work at ~90% of its rate
 // (more operand bytes per MFMA): they win where their rounds cost under 6/5 of the 256x256
@@ -54,7 +56,6 @@ bool wide_tile(int M, int N) {
     return 5 * r192 < 6 * r256;
 }
 
-}  // namespace
 
 // The shape rule, fitted on MI355X over 19 shapes x 5 configs for each of int8 and fp8 (M 128 to
 // 16384, N 640 to 14336, K 1280 to 12288). A 256x256 tile takes ~13 ns per K byte whatever the

@@ -53,6 +53,9 @@ hipError_t linear_int8_noalloc(const void* x, bool half, int rotation, int8_t* q
 // hipErrorNotSupported.
 constexpr int kGemmConfigs = 6;
 int gemm_config(bool fp8, int M, int N, int K);
+// Whether 256x192 tiles fill the 256 CUs in fewer rounds than 256x256 ones at this shape (the
+// large-tile choice of gemm_config, the MX GEMM and the svdq.nvfp4 GEMM).
+bool wide_tile(int M, int N);
 int narrow_config(int M, int N);
 hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                      const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,

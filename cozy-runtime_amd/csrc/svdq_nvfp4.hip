@@ -352,7 +352,9 @@ constexpr int kCodeWave = 2 * 1024 + 256, kCodeStage = 4 * kCodeWave;
 // kW4A16 (nvfp4, x 16-bit): A is x itself ([M, K] bf16, or fp16 with kXHalf), brought by LDS-DMA;
 // W's E4M3 scales sit in cuBLAS's 128x4 tiles; W is decoded into x's dtype; out = (x·Wᵀ)·gw
 // (+ bias). gx, cs, la, up unused.
-template <int kMode, bool kXHalf, bool kOutHalf>
+// kTN (kW4A4): 256 or 192 columns a tile (wide_tile's choice); at 192 each wave owns 128 x 96,
+// wave 3 neither loads nor decodes W rows, and every output's sum runs in the same order.
+template <int kMode, bool kXHalf, bool kOutHalf, int kTN = 256>
 __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ As, const uint8_t* __restrict__ W,
     const uint8_t* __restrict__ Ws, const float* __restrict__ gx, const float* __restrict__ gw,
@@ -360,13 +362,16 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K, int R,
     int tiles_m, int tiles_n) {
     constexpr bool kBf16 = kMode == kW4A16 && !kXHalf;  // the MFMA and W's decoded type
+    static_assert(kTN == 256 || (kTN == 192 && kMode == kW4A4), "tile widths: 256, or 192 for W4A4");
+    constexpr int kNI = kTN / 64, kHalfN = kTN / 2;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes + (kMode == kW4A16 ? 2 * kCodeStage : 0)];
     const int2 t = launch_tile(blockIdx.x, tiles_m, tiles_n);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = __builtin_amdgcn_readfirstlane(t.x * kTile);
-    const int n0 = __builtin_amdgcn_readfirstlane(t.y * kTile);
+    const int n0 = __builtin_amdgcn_readfirstlane(t.y * kTN);
+    const bool wrow = kTN == 256 || wave < 3;  // the wave's threads carry W rows of the tile
 
     auto rows_view = [&](const void* base, int rows_left, int row_bytes) {
         const int64_t span = static_cast<int64_t>(rows_left) * row_bytes;
@@ -437,12 +442,14 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
             fill_stage(stage_of(pair), wr, co, wsr, tiled_row + 512 * pair);
         } else {
             const uint32_t so = srow + 4 * pair;
-            regs.wa0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, co, 0, 0));
-            regs.wa1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, co + 16, 0, 0));
+            if (wrow) {
+                regs.wa0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, co, 0, 0));
+                regs.wa1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, co + 16, 0, 0));
+                regs.wsb = __builtin_amdgcn_raw_buffer_load_b32(wsr, so, 0, 0);
+            }
             regs.xa0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, co, 0, 0));
             regs.xa1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, co + 16, 0, 0));
             regs.xsb = __builtin_amdgcn_raw_buffer_load_b32(asr, so, 0, 0);
-            regs.wsb = __builtin_amdgcn_raw_buffer_load_b32(wsr, so, 0, 0);
         }
     };
     // The staged rows of `pair` (kW4A16: read back from the thread's slots once its vmcnt wait
@@ -479,7 +486,7 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         if constexpr (kMode == kW4A4) {
             if (q < 8)
                 put_chunk(buf + tid * kPairK, tid, q, dword_of(r.xa0, r.xa1, q), sc.x);
-            else
+            else if (wrow)
                 put_chunk(buf + kOpBytes + tid * kPairK, tid, q - 8, dword_of(r.wa0, r.wa1, q - 8), sc.w);
         } else if (q & 1) {
             const int c = q >> 1;
@@ -507,7 +514,7 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int rw = wn * 128 + i * 32 + fr, rx = wm * 128 + i * 32 + fr;
+                const int rw = wn * kHalfN + min(i, kNI - 1) * 32 + fr, rx = wm * 128 + i * 32 + fr;
                 aoff[e][h][i] = kOpBytes + rw * kPairK + 16 * swz(rw, 4 * e + 2 * h + fq);
                 boff[e][h][i] = rx * kPairK + 16 * swz(rx, 4 * e + 2 * h + fq);
             }
@@ -516,18 +523,20 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         const int e = step & 1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const i32x4 alo = *reinterpret_cast<const i32x4*>(buf + aoff[e][0][i]);
-            const i32x4 ahi = *reinterpret_cast<const i32x4*>(buf + aoff[e][1][i]);
+            if (i < kNI) {
+                const i32x4 alo = *reinterpret_cast<const i32x4*>(buf + aoff[e][0][i]);
+                const i32x4 ahi = *reinterpret_cast<const i32x4*>(buf + aoff[e][1][i]);
+                f.a[i] = __builtin_shufflevector(alo, ahi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
             const i32x4 blo = *reinterpret_cast<const i32x4*>(buf + boff[e][0][i]);
             const i32x4 bhi = *reinterpret_cast<const i32x4*>(buf + boff[e][1][i]);
-            f.a[i] = __builtin_shufflevector(alo, ahi, 0, 1, 2, 3, 4, 5, 6, 7);
             f.b[i] = __builtin_shufflevector(blo, bhi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
     };
 
-    f32x16 acc[4][4];
+    f32x16 acc[kNI][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kNI; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -537,16 +546,17 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < kNI; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x<kBf16>(c.a[i], c.b[j], h, acc[i][j]);
     };
     auto schedule = [&]() {
 #pragma unroll
-        for (int g = 0; g < 16; ++g) {
+        for (int g = 0; g < 4 * kNI; ++g) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
             __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
         }
+        if constexpr (kTN != 256) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     };
 
     // kW4A4: pair p + 1's register loads are issued after the barrier of step 2p - 1 (pair 1's
@@ -602,16 +612,18 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
         for (int q = 0; q < 16; ++q) {
             const int fi = q >> 2, fk = q & 3;
             const int off = fk < 2 ? aoff[e][fk][fi] : boff[e][fk - 2][fi];
-            piece[fi][fk] = *reinterpret_cast<const i32x4*>(rbuf + off);
+            if (fk >= 2 || fi < kNI) piece[fi][fk] = *reinterpret_cast<const i32x4*>(rbuf + off);
             const int h = q >> 3, i = (q >> 1) & 3, j = 2 * (q & 1);
-            acc[i][j] = mfma16x<kBf16>(cur.a[i], cur.b[j], h, acc[i][j]);
-            acc[i][j + 1] = mfma16x<kBf16>(cur.a[i], cur.b[j + 1], h, acc[i][j + 1]);
+            if (i < kNI) {
+                acc[i][j] = mfma16x<kBf16>(cur.a[i], cur.b[j], h, acc[i][j]);
+                acc[i][j + 1] = mfma16x<kBf16>(cur.a[i], cur.b[j + 1], h, acc[i][j + 1]);
+            }
             put(wbuf, q, sc, r);
             __builtin_amdgcn_sched_barrier(0);  // slices stay in order: decode rides under MFMAs
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            next.a[i] = __builtin_shufflevector(piece[i][0], piece[i][1], 0, 1, 2, 3, 4, 5, 6, 7);
+            if (i < kNI) next.a[i] = __builtin_shufflevector(piece[i][0], piece[i][1], 0, 1, 2, 3, 4, 5, 6, 7);
             next.b[i] = __builtin_shufflevector(piece[i][2], piece[i][3], 0, 1, 2, 3, 4, 5, 6, 7);
         }
     };
@@ -656,9 +668,9 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
     __builtin_amdgcn_s_barrier();
     fence();
     const float gxw = kMode == kW4A4 ? __fmul_rn(gx[0], gw[0]) : gw[0];
-    const int nl = wn * 128 + 4 * fq;  // the lane's first column within the tile
+    const int nl = wn * kHalfN + 4 * fq;  // the lane's first column within the tile
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kNI; ++i)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int c = nl + i * 32 + 8 * g;
@@ -683,36 +695,37 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
             bf16x8 ua[4], lb[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t ou = static_cast<uint32_t>(2 * ((wn * 128 + i * 32 + fr) * R + kk + 8 * fq));
+                const uint32_t ou = static_cast<uint32_t>(2 * ((wn * kHalfN + min(i, kNI - 1) * 32 + fr) * R + kk + 8 * fq));
                 const uint32_t ol = static_cast<uint32_t>(2 * ((wm * 128 + i * 32 + fr) * R + kk + 8 * fq));
-                ua[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(upr, ou, 0, 0));
+                if (i < kNI) ua[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(upr, ou, 0, 0));
                 lb[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(lar, ol, 0, 0));
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < kNI; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ua[i], lb[j], acc[i][j], 0, 0, 0);
         }
     }
 
-    uint2 bv[4][4];
+    uint2 bv[kNI][4];
     const bool has_bias = bias != nullptr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kNI; ++i)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
             bv[i][g] = has_bias ? *reinterpret_cast<const uint2*>(lds + kBiasOff + 2 * (nl + i * 32 + 8 * g))
                                 : make_uint2(0, 0);
-    // Block row j at a time: computed and staged, then stored as whole rows.
+    // Block row j at a time: computed and staged, then stored as whole rows (kHalfN = 96: 12 of
+    // each row's 16 lanes).
     uint8_t* stage = lds + wave * kStageBytes;
     const int cl = (lane & 15) * 8;  // first of the lane's 8 columns in a stored row
-    const int n = n0 + wn * 128 + cl;
+    const int n = n0 + wn * kHalfN + cl;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int ml = j * 32 + fr;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < kNI; ++i)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 float v[4];
@@ -734,7 +747,7 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
             const int rl = j * 32 + r0 + (lane >> 4);
             const int m = m0 + wm * 128 + rl;
             const uint4 v = *reinterpret_cast<const uint4*>(stage + rl * kStageRow + 2 * cl);
-            if (m < M && n < N) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * N + n) = v;
+            if (m < M && n < N && cl < kHalfN) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * N + n) = v;
         }
     }
 }
@@ -775,7 +788,8 @@ hipError_t svdq_nvfp4_gemm(const uint8_t* act, const uint8_t* ascales, const uin
                            const uint8_t* wscales, const float* gx, const float* gw,
                            const float* c, const void* la, const void* up, const void* bias,
                            void* out, bool out_half, int M, int N, int K, int R, hipStream_t s) {
-    const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTile - 1) / kTile;
+    const bool wide = wide_tile(M, N);  // 256x192 tiles where they fill the CUs in fewer rounds
+    const int tiles_m = (M + kTile - 1) / kTile, tiles_n = wide ? (N + 191) / 192 : (N + kTile - 1) / kTile;
     auto go = [&](auto kernel) {
         kernel<<<tiles_m * tiles_n, kThreads, 0, s>>>(
             act, ascales, w, wscales, gx, gw, c, static_cast<const uint16_t*>(la),
@@ -783,6 +797,8 @@ hipError_t svdq_nvfp4_gemm(const uint8_t* act, const uint8_t* ascales, const uin
             static_cast<uint16_t*>(out), M, N, K, R, tiles_m, tiles_n);
         return hipGetLastError();
     };
+    if (wide)
+        return out_half ? go(nvfp4_gemm_kernel<kW4A4, true, true, 192>) : go(nvfp4_gemm_kernel<kW4A4, true, false, 192>);
     return out_half ? go(nvfp4_gemm_kernel<kW4A4, true, true>) : go(nvfp4_gemm_kernel<kW4A4, true, false>);
 }
 

@@ -110,13 +110,15 @@ def test_svdq_quantize_bit_exact(ops, shape, dtype, rank):
     assert (err <= exact.abs() * 2.0**-8 + spread * 2.0**-18).all(), err.max()
 
 
-@pytest.mark.parametrize("shape", [(300, 264, 256), (1, 520, 64), (513, 256, 192)],
+@pytest.mark.parametrize("shape", [(300, 264, 256), (1, 520, 64), (513, 256, 192), (4096, 12288, 64)],
                          ids=lambda s: "x".join(map(str, s)))  # fmt: skip
 def test_svdq_gemm_bit_exact_where_exact(ops, shape):
     """Random codes on both sides with E4M3 scales in [1, 2), unit second levels, no c, a zero
     low-rank branch: every product and partial sum is exact in float32 (at most 23 significant
     bits), so the output is the float64 law's, cast once, bit for bit — the fp16 decode of each
-    E2M1 code and scale and the MFMA layout, checked exactly."""
+    E2M1 code and scale and the MFMA layout, checked exactly. The small grids run 256x192 tiles
+    (partial ones past N = 192 or 384), 4096 x 12288 the 256x256 tile (768 tiles: three rounds,
+    where 256x192 would need four)."""
     m, n, k = shape
     gen = torch.Generator().manual_seed(m + n + k)
     acodes = torch.randint(0, 16, (m, k), generator=gen).to(torch.uint8)
