@@ -311,6 +311,156 @@ __global__ __launch_bounds__(256) void nvfp4_rows_kernel(const uint16_t* __restr
     }
 }
 
+// The streaming form for 1 or 2 activation rows and K ≤ 4096 (measured at config 3's weight: M = 1
+// 11.7 → 8.9 µs, M = 2 12.0 → 11.5; from 3 rows the per-row MFMA chains make it slower than the
+// K-split form): each wave streams kStreamRows whole
+// weight rows as contiguous 1 KiB loads (lane l at byte 16·l of a 2 KiB span: its 32 codes,
+// columns 2048·j + 32·l ..), with the non-temporal policy, the way the fp8 decode GEMV streams
+// its rows, instead of 16 rows × 64 bytes an instruction. The activation rows sit in LDS (16-bit,
+// zeros past K). MFMA q of a span takes each lane's 8 weights 8q .. 8q + 7 (decoded as the GEMV
+// above does) as A row l%16, k-block l/16, and the activation's same 8 columns as B column l%16,
+// so D[i][i] sums the 8-column products of the four lanes i, i + 16, i + 32, i + 48: the trace of
+// D, accumulated over the four groups and the spans, is the row's dot product. One MFMA chain per
+// activation row, so a row's result does not depend on M. The block scales of the workgroup's 8
+// rows come into LDS first, by 16-byte loads of the 128-byte lines that hold them (a 128x4 tile
+// keeps rows r .. r + 7 of a 32-row group in one line): a 2-byte load a lane and row touches 32
+// lines an instruction and measured ~3 µs of config 3's M = 1 decode.
+constexpr int kStreamWaves = 4;
+constexpr int kStreamRows = 2;     // weight rows a wave streams
+constexpr int kStreamBatch = 2;    // 2 KiB spans of each row in flight
+constexpr int kStreamMaxK = 4096;  // activation rows a thread stages in registers: K ≤ this
+constexpr int kStreamPolicy = 3;   // sc0 nt: each weight byte is read once per call
+constexpr int kStreamRowsMax = 2;  // activation rows the streaming form serves
+
+template <bool kXHalf, bool kOutHalf, int kM>
+__global__ __launch_bounds__(64 * kStreamWaves) void nvfp4_stream_kernel(const uint16_t* __restrict__ x,
+                                                                         const uint8_t* __restrict__ w,
+                                                                         const uint8_t* __restrict__ scale,
+                                                                         const float* __restrict__ scale_2,
+                                                                         uint16_t* __restrict__ out, int N, int K) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t xl[];  // kM rows of `xbytes`, then the scales
+    constexpr int kThreads = 64 * kStreamWaves;
+    constexpr int kPieces = kStreamMaxK * 2 / 16 / kThreads;  // 16-byte activation pieces a thread, per row
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int spans = (K + 2047) / 2048, xbytes = spans * 4096;
+    const int row0 = blockIdx.x * (kStreamWaves * kStreamRows);  // the workgroup's 8 rows
+    const int n0 = row0 + wave * kStreamRows;
+    const int width = K / 16, col_tiles = (width + 3) / 4;
+    uint32_t* const sl = reinterpret_cast<uint32_t*>(xl + kM * xbytes);  // [span][8 rows][32 tiles]
+    const __amdgpu_buffer_rsrc_t wr = bounded_rsrc(w, static_cast<int64_t>(N) * (K / 2));
+    const __amdgpu_buffer_rsrc_t sr = bounded_rsrc(scale, static_cast<int64_t>((N + 127) / 128 * 128) * col_tiles * 4);
+    const __amdgpu_buffer_rsrc_t xr = bounded_rsrc(x, static_cast<int64_t>(kM) * K * 2);
+
+    // 1. The activation rows' pieces into registers first (a wave's loads complete in issue
+    //    order: issued after the weights, they would wait for the whole stream).
+    uint4 xv[kM][kPieces];
+#pragma unroll
+    for (int m = 0; m < kM; ++m)
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p) {
+            const int b = 16 * (tid + kThreads * p);  // byte within the row
+            xv[m][p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                xr, b < 2 * K ? m * 2 * K + b : 0x7ffffff0, 0, 0));
+        }
+    // The 8 rows' scale lines: thread t brings, for each span, the 16 bytes of column tile t/8
+    // that hold row row0 + t%8 (and the three rows 32, 64 and 96 apart in its 128-row block).
+    static_assert(kStreamWaves * kStreamRows == 8 && 64 * kStreamWaves == 256, "8 rows, 256 threads");
+    uint4 svv[kStreamMaxK / 2048];
+#pragma unroll
+    for (int j = 0; j < kStreamMaxK / 2048; ++j) {
+        const int tile = 32 * j + (tid >> 3), r = row0 + (tid & 7);
+        const int off = ((r >> 7) * col_tiles + tile) * 512 + (r & 31) * 16;
+        svv[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+            sr, j < spans && tile < col_tiles ? off : 0x7ffffff0, 0, 0));
+    }
+    asm volatile("" ::: "memory");
+
+    // 2. The weight stream: kStreamBatch spans of each row.
+    uint4 wv[kStreamRows][kStreamBatch];
+    auto issue = [&](int first) {
+#pragma unroll
+        for (int i = 0; i < kStreamRows; ++i)
+#pragma unroll
+            for (int b = 0; b < kStreamBatch; ++b) {
+                const int row = n0 + i, col = 2048 * (first + b) + 32 * lane;
+                const bool live = row < N && col < K;
+                wv[i][b] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                    wr, live ? row * (K / 2) + col / 2 : 0x7ffffff0, 0, kStreamPolicy));
+            }
+    };
+    issue(0);
+
+    // 3. The activation into LDS, zeros past K (the pieces past xbytes are never read).
+#pragma unroll
+    for (int m = 0; m < kM; ++m)
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p) {
+            const int b = 16 * (tid + kThreads * p);
+            if (b < xbytes) *reinterpret_cast<uint4*>(xl + m * xbytes + b) = xv[m][p];
+        }
+    {
+        // The row's dword of the 16 bytes: its 32-row group's slot (all 8 rows share it).
+        const int slot = (row0 & 127) >> 5;
+#pragma unroll
+        for (int j = 0; j < kStreamMaxK / 2048; ++j) {
+            const uint32_t d[4] = {svv[j].x, svv[j].y, svv[j].z, svv[j].w};
+            if (j < spans) sl[(j * 8 + (tid & 7)) * 32 + (tid >> 3)] = d[slot];
+        }
+    }
+    __syncthreads();
+
+    // 4. Products: the trace accumulates over the groups and the spans.
+    f32x4 acc[kStreamRows][kM];
+#pragma unroll
+    for (int i = 0; i < kStreamRows; ++i)
+#pragma unroll
+        for (int m = 0; m < kM; ++m) acc[i][m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int first = 0; first < spans; first += kStreamBatch) {
+        if (first != 0) issue(first);
+#pragma unroll
+        for (int b = 0; b < kStreamBatch; ++b) {
+            if (first + b >= spans) break;
+            i32x4 xb[kM][4];
+#pragma unroll
+            for (int m = 0; m < kM; ++m)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    xb[m][q] = *reinterpret_cast<const i32x4*>(xl + m * xbytes + 4096 * (first + b) + 64 * lane + 16 * q);
+#pragma unroll
+            for (int i = 0; i < kStreamRows; ++i) {
+                // The lane's blocks 2l and 2l + 1 of the span: bytes 2(l&1) and 2(l&1) + 1 of tile l/2.
+                const uint32_t sd = sl[((first + b) * 8 + wave * kStreamRows + i) * 32 + (lane >> 1)];
+                const f32x2n sc = scales2(sd >> (16 * (lane & 1)));
+                const uint32_t d[4] = {wv[i][b].x, wv[i][b].y, wv[i][b].z, wv[i][b].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const i32x4 wq = weights8<kXHalf>(d[q], q < 2 ? sc[0] : sc[1]);
+#pragma unroll
+                    for (int m = 0; m < kM; ++m) acc[i][m] = mfma16<kXHalf>(wq, xb[m][q], acc[i][m]);
+                }
+            }
+        }
+    }
+
+    // 5. The trace: D[a][a] sits in lane a + 16·(a/4), register a % 4; the 64 lanes' sum.
+    const int a = lane & 15;
+    const bool diagonal = (lane >> 4) == (a >> 2);
+    const float g = scale_2[0];
+#pragma unroll
+    for (int i = 0; i < kStreamRows; ++i)
+#pragma unroll
+        for (int m = 0; m < kM; ++m) {
+            const f32x4 d = acc[i][m];
+            const int r = a & 3;
+            float v = r == 0 ? d[0] : (r == 1 ? d[1] : (r == 2 ? d[2] : d[3]));
+            v = diagonal ? v : 0.0f;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0 && n0 + i < N) out[static_cast<int64_t>(m) * N + n0 + i] = narrow<kOutHalf>(v * g);
+        }
+}
+
 }  // namespace
 
 hipError_t nvfp4_gemv(const void* x, bool x_half, const uint8_t* w, const uint8_t* scale, const float* scale_2,
@@ -320,6 +470,23 @@ hipError_t nvfp4_gemv(const void* x, bool x_half, const uint8_t* w, const uint8_
     // More than 4 rows on a weight whose 64-row groups alone give 192 workgroups: the row-block
     // kernel (the activation read once per workgroup); otherwise the K-split GEMV.
     const bool rows = M > kRowBlockFrom && K % 128 == 0 && (N + 63) / 64 >= 192;
+    // One or two rows of a short activation: the streaming form.
+    if (M >= 1 && M <= kStreamRowsMax && K <= kStreamMaxK) {
+        const int64_t lds = (static_cast<int64_t>(M) * 4096 + 1024) * ((K + 2047) / 2048);
+        auto stream = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3((N + kStreamWaves * kStreamRows - 1) / (kStreamWaves * kStreamRows)),
+                               dim3(64 * kStreamWaves), lds, s, xp, w, scale, scale_2, op, N, K);
+            return hipGetLastError();
+        };
+        auto by_rows = [&](auto xh, auto oh) {
+            constexpr bool kX = decltype(xh)::value, kO = decltype(oh)::value;
+            return M == 1 ? stream(nvfp4_stream_kernel<kX, kO, 1>) : stream(nvfp4_stream_kernel<kX, kO, 2>);
+        };
+        using T = std::true_type;
+        using F = std::false_type;
+        if (x_half) return out_half ? by_rows(T{}, T{}) : by_rows(T{}, F{});
+        return out_half ? by_rows(F{}, T{}) : by_rows(F{}, F{});
+    }
     auto go = [&](auto kernel) {
         if (rows)
             hipLaunchKernelGGL(kernel, dim3((N + 63) / 64), dim3(256), 0, s, xp, w, scale, scale_2, op, M, N, K);

@@ -37,7 +37,8 @@ def _close(got: torch.Tensor, want: torch.Tensor) -> None:
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (3, 200, 1024), (16, 264, 96), (16, 4096, 3072),
+@pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (2, 14336, 4096), (1, 200, 96), (2, 264, 2080), (1, 12296, 3072),
+                                   (3, 200, 1024), (16, 264, 96), (16, 4096, 3072),
                                    (17, 200, 160), (40, 4096, 3072), (64, 1032, 2048), (5, 12288, 640),
                                    (40, 12296, 3072), (64, 14336, 512)])
 def test_nvfp4_gemv_against_the_exact_product(dtype, m, n, k):
@@ -52,10 +53,10 @@ def test_nvfp4_gemv_against_the_exact_product(dtype, m, n, k):
     _close(got, x.double() @ exact.double().t())
 
 
-@pytest.mark.parametrize("n,sizes", [(4096, (1, 5, 16, 17, 33, 50)), (12288, (5, 9, 16, 17, 33, 50))])
+@pytest.mark.parametrize("n,sizes", [(4096, (3, 5, 16, 17, 33, 50)), (12288, (5, 9, 16, 17, 33, 50))])
 def test_nvfp4_gemv_rows_do_not_depend_on_m(n, sizes):
-    """Within a kernel (the K-split GEMV; the row-block form past 4 rows when N gives 192
-    64-row groups) a row's bits do not depend on M, and repeat."""
+    """Within a kernel (the streaming form at 1 or 2 rows; the K-split GEMV; the row-block form
+    past 4 rows when N gives 192 64-row groups) a row's bits do not depend on M, and repeat."""
     from cozyq import prebuilt
 
     codes, _, blocked, second, _ = _weight(n, 2048, 9)
@@ -68,6 +69,10 @@ def test_nvfp4_gemv_rows_do_not_depend_on_m(n, sizes):
     for m in sizes:
         part = ops.nvfp4_gemv(x[:m].to(CUDA), w, s, g, torch.bfloat16).cpu()
         assert torch.equal(part.view(torch.int16), full[:m].view(torch.int16))
+    two = ops.nvfp4_gemv(x[:2].to(CUDA), w, s, g, torch.bfloat16).cpu()
+    one = ops.nvfp4_gemv(x[:1].to(CUDA), w, s, g, torch.bfloat16).cpu()
+    assert torch.equal(one.view(torch.int16), two[:1].view(torch.int16))
+    assert torch.equal(two.view(torch.int16), ops.nvfp4_gemv(x[:2].to(CUDA), w, s, g, torch.bfloat16).cpu().view(torch.int16))
 
 
 @pytest.mark.parametrize("dtype,out_dtype", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
