@@ -376,9 +376,9 @@ def bench_int8_decode(torch, ops, lib, stream, steps: int) -> dict:
 
 def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
     """The w4a8.convrot GEMM on config 2's weight shape (K=3072, N=12288; 4-bit codes + E4M3
-    group scales, 21.2 MB against int8's 37.7 MB) at M = 1, 16, 256 (the fused GEMM, codes
-    unpacked in registers) and 4096 (unpack once + the 256x256 int8 GEMM), int8.convrot's
-    operand precomputed; bias + bf16 out."""
+    group scales, 21.2 MB against int8's 37.7 MB) at M = 1 (the GEMV form), 16, 256 (the fused
+    GEMM, codes unpacked in registers) and 4096 (unpack once + the 256x256 int8 GEMM),
+    int8.convrot's operand precomputed; bias + bf16 out; one weight, reused across calls."""
     from cozyq import prebuilt
 
     k, n = 3072, 12288
@@ -411,7 +411,8 @@ def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
         weight_bytes = n * k // 2 + n * k // 16 + n * 4
         rows.append({"M": m, "us": ms * 1e3, "tops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
                      "weight_gbs": weight_bytes / (ms * 1e-3) / 1e9,
-                     "path": "fused narrow GEMM" if m < prebuilt.UNPACK_ROWS else "unpack + int8 GEMM"})
+                     "path": ("GEMV (w4a8_decode_kernel)" if m <= 4 else "fused narrow GEMM")
+                     if m < prebuilt.UNPACK_ROWS else "unpack + int8 GEMM"})
     return {"K": k, "N": n, "rows": rows}
 
 

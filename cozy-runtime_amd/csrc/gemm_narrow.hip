@@ -502,12 +502,176 @@ __global__ __launch_bounds__(kThreads) void w4a8_unpack_kernel(const uint8_t* __
     *reinterpret_cast<uint4*>(out + row * K + grp * 16) = v;
 }
 
+// The w4a8.convrot GEMV for 1..4 quantized rows: the int8 decode GEMV's structure on 4-bit codes.
+// Each wave streams kW4Rows whole weight rows as contiguous 1 KiB code loads (lane l at byte
+// 16·l of a span: 32 codes, columns 2048·j + 32·l .., two groups, whose scale bytes are the row's
+// bytes 128·j + 2·l and + 1), non-temporal; the codes unpack to int8 levels through the
+// workgroup's 256 x 16 level table (w4_unpack16); the quantized activation rows sit in LDS. The
+// dot products are the trace of v_mfma_i32_16x16x64_i8 (lane l supplies A row l%16 and B column
+// l%16, k-block l/16: the same 16 columns of the weight row and of the activation), exact int32,
+// and the epilogue is the int8 law's, so every output equals the tiled GEMM's bit for bit.
+constexpr int kW4Waves = 4;
+constexpr int kW4Rows = 4;       // weight rows a wave
+constexpr int kW4Batch = 2;      // 1 KiB code spans of each row in flight
+constexpr int kW4MaxK = 8192;    // activation rows a thread stages: K ≤ this
+constexpr int kW4Policy = 3;     // sc0 nt: each code byte is read once per call
+
+template <bool kOutHalf, bool kBias, int kM>
+__global__ __launch_bounds__(64 * kW4Waves) void w4a8_decode_kernel(
+    const int8_t* __restrict__ q, const float* __restrict__ xs, const uint8_t* __restrict__ codes, W4 w4,
+    const float* __restrict__ ws, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int N, int K) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // the level table, then kM code rows
+    constexpr int kThreadsW4 = 64 * kW4Waves;
+    constexpr int kPieces = kW4MaxK / 16 / kThreadsW4;
+    static_assert(kThreadsW4 == 256, "one level-table row a thread");
+    uint32_t* const table = reinterpret_cast<uint32_t*>(smem);
+    int8_t* const xq = reinterpret_cast<int8_t*>(smem + 256 * 16);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int spans = (K + 2047) / 2048, stride = spans * 2048;
+    const int nw = blockIdx.x * (kW4Waves * kW4Rows) + wave * kW4Rows;  // the wave's first row
+
+    // 1. The activation rows' 16-byte pieces first (loads complete in issue order).
+    const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(q), 0, kM * K, 0x00020000);
+    uint4 xv[kM][kPieces];
+#pragma unroll
+    for (int m = 0; m < kM; ++m)
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p) {
+            const int b = 16 * (tid + kThreadsW4 * p);
+            xv[m][p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                qr, b < K ? m * K + b : 0x7ffffff0, 0, 0));
+        }
+    asm volatile("" ::: "memory");
+
+    // 2. The code stream and each lane's two group-scale bytes.
+    const int64_t rows_bytes = static_cast<int64_t>(N) * (K / 2);
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(codes), 0, rows_bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(rows_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(w4.group_scale), 0, static_cast<int>(static_cast<int64_t>(N) * (K / 16)), 0x00020000);
+    uint4 wv[kW4Rows][kW4Batch];
+    uint32_t gv[kW4Rows][kW4Batch];
+    auto issue = [&](int first) {
+#pragma unroll
+        for (int i = 0; i < kW4Rows; ++i)
+#pragma unroll
+            for (int b = 0; b < kW4Batch; ++b) {
+                const int row = nw + i, col = 2048 * (first + b) + 32 * lane;
+                const bool live = row < N && col < K;
+                wv[i][b] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                    cr, live ? row * (K / 2) + col / 2 : 0x7ffffff0, 0, kW4Policy));
+                gv[i][b] = __builtin_amdgcn_raw_buffer_load_b16(gr, live ? row * (K / 16) + col / 16 : 0x7ffffff0, 0, 0);
+            }
+    };
+    issue(0);
+
+    // 3. The level table (row tid) and the activation codes into LDS, zeros past K.
+    w4_table_row(w4.codebook, table, tid);
+#pragma unroll
+    for (int m = 0; m < kM; ++m)
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p) {
+            const int b = 16 * (tid + kThreadsW4 * p);
+            if (b < stride) *reinterpret_cast<uint4*>(xq + m * stride + b) = xv[m][p];
+        }
+    __syncthreads();
+
+    // 4. Products: the trace accumulates over the spans.
+    i32x4 acc[kW4Rows][kM];
+#pragma unroll
+    for (int i = 0; i < kW4Rows; ++i)
+#pragma unroll
+        for (int m = 0; m < kM; ++m) acc[i][m] = i32x4{0, 0, 0, 0};
+    for (int first = 0; first < spans; first += kW4Batch) {
+        if (first != 0) issue(first);
+#pragma unroll
+        for (int b = 0; b < kW4Batch; ++b) {
+            if (first + b >= spans) break;
+            i32x4 xb[kM][2];
+#pragma unroll
+            for (int m = 0; m < kM; ++m)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    xb[m][h] = *reinterpret_cast<const i32x4*>(xq + m * stride + 2048 * (first + b) + 32 * lane + 16 * h);
+#pragma unroll
+            for (int i = 0; i < kW4Rows; ++i) {
+                const uint4 c = wv[i][b];
+                const i32x4 l0 = __builtin_bit_cast(i32x4, w4_unpack16(c.x, c.y, table, gv[i][b] & 0xffu));
+                const i32x4 l1 = __builtin_bit_cast(i32x4, w4_unpack16(c.z, c.w, table, (gv[i][b] >> 8) & 0xffu));
+#pragma unroll
+                for (int m = 0; m < kM; ++m) {
+                    acc[i][m] = mfma_i8(l0, xb[m][0], acc[i][m]);
+                    acc[i][m] = mfma_i8(l1, xb[m][1], acc[i][m]);
+                }
+            }
+        }
+    }
+
+    // 5. The trace: D[a][a] sits in lane a + 16·(a/4), register a % 4; the 64 lanes' sum.
+    const int a = lane & 15;
+    const bool diagonal = (lane >> 4) == (a >> 2);
+    int dot[kW4Rows][kM];
+#pragma unroll
+    for (int i = 0; i < kW4Rows; ++i)
+#pragma unroll
+        for (int m = 0; m < kM; ++m) {
+            const i32x4 d = acc[i][m];
+            const int r = a & 3;
+            int v = r == 0 ? d[0] : (r == 1 ? d[1] : (r == 2 ? d[2] : d[3]));
+            v = diagonal ? v : 0;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            dot[i][m] = v;
+        }
+    if (lane != 0 || nw >= N) return;  // N % 8 == 0: a wave's four rows are all in or all out
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        uint32_t o[2];
+#pragma unroll
+        for (int i = 0; i < kW4Rows; ++i) {
+            // internal/int8_linear.py:445-448 then :276: (acc·xs)·ws, cast, + bias in the output dtype.
+            const float v = __fmul_rn(__fmul_rn(static_cast<float>(dot[i][m]), xs[m]), ws[nw + i]);
+            uint32_t h = ::cozyq::narrow<kOutHalf>(v);  // (this file's `narrow` launcher hides it)
+            if constexpr (kBias)
+                h = ::cozyq::narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(bias[nw + i])));
+            o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
+        }
+        *reinterpret_cast<uint2*>(out + static_cast<int64_t>(m) * N + nw) = make_uint2(o[0], o[1]);
+    }
+}
+
+template <bool kOutHalf, bool kBias>
+hipError_t launch_w4a8_decode(const int8_t* q, const float* xs, const uint8_t* codes, W4 w4, const float* ws,
+                              const void* bias, void* out, int M, int N, int K, hipStream_t s) {
+    const int blocks = (N + kW4Waves * kW4Rows - 1) / (kW4Waves * kW4Rows);
+    const int64_t lds = 256 * 16 + static_cast<int64_t>(M) * ((K + 2047) / 2048) * 2048;
+    const auto* b = static_cast<const uint16_t*>(bias);
+    auto* o = static_cast<uint16_t*>(out);
+    switch (M) {
+        case 1: w4a8_decode_kernel<kOutHalf, kBias, 1><<<blocks, 64 * kW4Waves, lds, s>>>(q, xs, codes, w4, ws, b, o, N, K); break;
+        case 2: w4a8_decode_kernel<kOutHalf, kBias, 2><<<blocks, 64 * kW4Waves, lds, s>>>(q, xs, codes, w4, ws, b, o, N, K); break;
+        case 3: w4a8_decode_kernel<kOutHalf, kBias, 3><<<blocks, 64 * kW4Waves, lds, s>>>(q, xs, codes, w4, ws, b, o, N, K); break;
+        default: w4a8_decode_kernel<kOutHalf, kBias, 4><<<blocks, 64 * kW4Waves, lds, s>>>(q, xs, codes, w4, ws, b, o, N, K); break;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* codes,
                             const uint8_t* group_scale, const float* codebook, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
                             int config, hipStream_t s) {
+    // 1..4 rows by shape: the GEMV form (the same bits as every tile config).
+    if (config < 0 && M <= 4 && K <= kW4MaxK) {
+        const W4 w4{group_scale, codebook};
+        if (out_half)
+            return bias ? launch_w4a8_decode<true, true>(q, xs, codes, w4, ws, bias, out, M, N, K, s)
+                        : launch_w4a8_decode<true, false>(q, xs, codes, w4, ws, bias, out, M, N, K, s);
+        return bias ? launch_w4a8_decode<false, true>(q, xs, codes, w4, ws, bias, out, M, N, K, s)
+                    : launch_w4a8_decode<false, false>(q, xs, codes, w4, ws, bias, out, M, N, K, s);
+    }
     return narrow<true, true>(reinterpret_cast<const uint8_t*>(q), xs, codes, ws, bias, out, N,
                               out_half, M, N, K, 0, config < 0 ? narrow_config(M, N) : config, s,
                               W4{group_scale, codebook});
