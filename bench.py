@@ -395,10 +395,10 @@ def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
         out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         args = (q.data_ptr(), s.data_ptr())
 
-        def fused():
+        def fused(st=stream):
             _check(lib.cozyq_w4a8_gemm(0, *args, codes.data_ptr(), w.group_scale.data_ptr(), None,
                                        w.scale.data_ptr(), bias.data_ptr(), out.data_ptr(), 0, m, n,
-                                       k, -1, stream))  # fmt: skip
+                                       k, -1, st))  # fmt: skip
 
         def unpacked():
             _check(lib.cozyq_w4a8_unpack(0, codes.data_ptr(), w.group_scale.data_ptr(), None,
@@ -407,7 +407,12 @@ def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
                                   bias.data_ptr(), out.data_ptr(), n, 0, m, n, k, -1, None, None,
                                   stream))  # fmt: skip
 
-        ms = Timer(torch).run(fused if m < prebuilt.UNPACK_ROWS else unpacked, steps, 5)
+        # Few rows: a HIP graph of launches, replayed (back-to-back launches from Python would
+        # time the host's launch rate, not the kernel).
+        if m < prebuilt.UNPACK_ROWS:
+            ms = _graph_us(torch, fused, 32, steps) * 1e-3
+        else:
+            ms = Timer(torch).run(unpacked, steps, 5)
         weight_bytes = n * k // 2 + n * k // 16 + n * 4
         rows.append({"M": m, "us": ms * 1e3, "tops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
                      "weight_gbs": weight_bytes / (ms * 1e-3) / 1e9,
