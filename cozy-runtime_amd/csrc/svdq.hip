@@ -187,9 +187,12 @@ __device__ __forceinline__ void wait_all() {
     __builtin_amdgcn_s_waitcnt(0);  // vmcnt, expcnt and lgkmcnt all zero
 }
 
-// 16-byte chunk c (0..7) of a 128-byte LDS row r sits at chunk c ^ (r % 8): 8 consecutive rows
-// read at one chunk hit 8 distinct 16-byte bank groups.
-__device__ __forceinline__ int swz(int r, int c) { return c ^ (r & 7); }
+// 16-byte chunk c (0..7) of a 128-byte LDS row r sits at chunk c ^ ((r / 2) % 8). A fragment's
+// ds_read_b128 is served 16 lanes (16 consecutive rows at one chunk) at a time over 256 bytes of
+// banks (measured on MI355X), so those rows need distinct (r % 2, chunk) pairs; c ^ (r % 8) gave
+// rows r and r + 8 the same banks (2-way conflicts on every read). The rows arrive by whole-row
+// LDS-DMA, 8 lanes a row, which any such permutation keeps conflict-free.
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
 
 // 32 packed codes (16 bytes, element 2k in the low nibble of byte k) -> bytes holding 16·code,
 // as the two 16-byte operands of one group's two MFMAs: each dword's low nibbles shifted up,
