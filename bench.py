@@ -576,7 +576,7 @@ def bench_svdq_nvfp4(torch, ops, lib, stream, steps: int) -> dict:
             "tflops": (flops + lowrank_flops) / (ms * 1e-3) / 1e12,
             "gemm_tflops": flops / (g_ms * 1e-3) / 1e12,
             "frac_f16_mfma": flops / (g_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-            "kernel": "nvfp4_gemm_kernel (E2M1 x E4M3 decoded to fp16, 32x32x16 f16 MFMA, 256x256)"}
+            "kernel": "nvfp4_gemm_kernel (E2M1 x E4M3 decoded to fp16, 32x32x16 f16 MFMA, 256x192 tiles by the round rule)"}
 
 
 def bench_tiles(torch, ops, lib, stream, steps: int) -> dict:

@@ -55,29 +55,45 @@ __global__ void input_scale_init(uint32_t* g) { *g = bits_of(kInputFloor); }
 
 // g = max(max over x of fl(|x|·p[col]) / 2688, 1e-30). The law takes amax over rows first, then
 // · p, then the max: the same value, since fl(a·p) is monotonic in a for p > 0; the division and
-// the clamp are monotonic too, so each block's candidate enters by an unsigned max of its
-// (non-negative) float bits into *g, which input_scale_init set to the floor. A thread keeps its
-// 8-column chunks (and their p) fixed and walks the block's rows; a wave reads 1 KB runs of a row.
+// the clamp are monotonic too, so each workgroup's candidate enters by an unsigned max of its
+// (non-negative) float bits into *g, which input_scale_init set to the floor.
+// Atomics on the one word serialize (~10 ns each measured on MI355X, against ~6 us for the whole
+// read at C4's size), so there are few workgroups, each of many waves: ~256 of kScaleGroups x
+// kScaleThreads threads, and a workgroup whose candidate does not exceed what *g already holds
+// skips its atomic. Thread (t, q) of workgroup (bx, by) takes the 8-column chunk
+// kScaleThreads·bx + t of the runs of kScaleRows rows kScaleRows·(kScaleGroups·by + q), then
+// every kScaleGroups·gridDim.y-th run; a run's loads are in flight together (a wave reads a
+// 1 KiB piece of each row), rows past M repeat the last.
+constexpr int kScaleThreads = 128;
+constexpr int kScaleGroups = 4;
+constexpr int kScaleRows = 8;
+
 template <bool kHalf>
-__global__ __launch_bounds__(256) void input_scale_kernel(const uint16_t* __restrict__ x,
-                                                          const float* __restrict__ p, int M,
-                                                          int K, uint32_t* __restrict__ g) {
-    __shared__ float red[4];
+__global__ __launch_bounds__(kScaleThreads * kScaleGroups) void input_scale_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ p, int M, int K, uint32_t* __restrict__ g) {
+    __shared__ float red[kScaleThreads * kScaleGroups / 64];
+    const int t = threadIdx.x % kScaleThreads, q = threadIdx.x / kScaleThreads;
+    const int c = blockIdx.x * kScaleThreads + t;
     float m = 0.0f;
-    const int chunks = K / 8;
-    for (int c = threadIdx.x; c < chunks; c += 256) {
+    if (c < K / 8) {
+        float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // max |x| per column over the rows
+        for (int r0 = (blockIdx.y * kScaleGroups + q) * kScaleRows; r0 < M;
+             r0 += gridDim.y * kScaleGroups * kScaleRows) {
+            uint4 v[kScaleRows];
+#pragma unroll
+            for (int r = 0; r < kScaleRows; ++r)
+                v[r] = *reinterpret_cast<const uint4*>(x + static_cast<int64_t>(min(r0 + r, M - 1)) * K + 8 * c);
+#pragma unroll
+            for (int r = 0; r < kScaleRows; ++r) {
+                float f[8];
+                widen8<kHalf>(v[r], f);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a[i] = fmaxf(a[i], fabsf(f[i]));
+            }
+        }
         const float4 p0 = *reinterpret_cast<const float4*>(p + 8 * c);
         const float4 p1 = *reinterpret_cast<const float4*>(p + 8 * c + 4);
         const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-        float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // max |x| per column over the rows
-#pragma unroll 4
-        for (int row = blockIdx.x; row < M; row += gridDim.x) {
-            const uint4 v = *reinterpret_cast<const uint4*>(x + static_cast<int64_t>(row) * K + 8 * c);
-            float f[8];
-            widen8<kHalf>(v, f);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) a[i] = fmaxf(a[i], fabsf(f[i]));
-        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) m = fmaxf(m, __fmul_rn(a[i], pv[i]));
     }
@@ -86,8 +102,10 @@ __global__ __launch_bounds__(256) void input_scale_kernel(const uint16_t* __rest
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     if (threadIdx.x == 0) {
-        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        atomicMax(g, bits_of(fmaxf(__fdiv_rn(m, kLevelsMax), kInputFloor)));
+#pragma unroll
+        for (int w = 1; w < kScaleThreads * kScaleGroups / 64; ++w) m = fmaxf(m, red[w]);
+        const uint32_t bits = bits_of(fmaxf(__fdiv_rn(m, kLevelsMax), kInputFloor));
+        if (bits > __hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(g, bits);
     }
 }
 
@@ -115,6 +133,24 @@ __device__ __forceinline__ uint32_t e2m1_count(float a) {
            static_cast<uint32_t>(a > 1.25f) + static_cast<uint32_t>(a >= 1.75f) +
            static_cast<uint32_t>(a > 2.5f) + static_cast<uint32_t>(a >= 3.5f) +
            static_cast<uint32_t>(a > 5.0f);
+}
+
+// xs / (scale·g) for v_cvt_scalef32_pk_fp4_f32 at unit scale. That conversion (nearest, ties to
+// the even code, saturating at 6) gives the law's threshold count, sign included, on every finite
+// nonzero quotient and on ±inf (held against e2m1_count over all 2^32 float32 bit patterns on
+// MI355X); it writes the sign of −0 and converts NaN to 6, where the law writes code 0 for
+// xs = −0 and NaN. So −0 becomes +0 first and NaN gives +0. Otherwise the quotient is RN(xs / sg)
+// (div_rn, for finite xs and finite sg > 0).
+__device__ __forceinline__ float e2m1_quotient(float xs, float sg, float rs) {
+    const float z = __fadd_rn(xs, 0.0f);  // −0 → +0, everything else unchanged
+    const float q = div_rn(z, sg, rs);
+    return z == z ? q : 0.0f;
+}
+
+// Codes of quotients a and b into byte kByte of `word` (a in the low nibble).
+template <int kByte>
+__device__ __forceinline__ uint32_t put_e2m1_pair(uint32_t word, float a, float b) {
+    return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, a, b, 1.0f, kByte);
 }
 
 template <int kR>
@@ -148,42 +184,75 @@ __global__ __launch_bounds__(quantize_waves<kR>() * 64) void nvfp4_quantize_kern
 #pragma unroll
     for (int j = 0; j < kJ; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int gi = wave; gi < groups; gi += kWaves) {
+    // A group's operands: the lane's 16 elements of its row, their p, and down's rows at the same
+    // columns. The next group's are loaded before the current one is worked on, with no branch
+    // around the loads (past the wave's last group they load that group again).
+    struct Group {
+        uint4 xa, xb, da[kJ], db[kJ];
+        float4 p4[4];
+    };
+    auto fetch = [&](int gi, Group& in) {
         const int col = kQGroup * gi + 16 * part;
-        const uint4 xa = *reinterpret_cast<const uint4*>(xrow + col);
-        const uint4 xb = *reinterpret_cast<const uint4*>(xrow + col + 8);
-        uint4 da[kJ], db[kJ];
+        in.xa = *reinterpret_cast<const uint4*>(xrow + col);
+        in.xb = *reinterpret_cast<const uint4*>(xrow + col + 8);
 #pragma unroll
         for (int j = 0; j < kJ; ++j) {
             const uint16_t* drow = down + static_cast<int64_t>(16 * j + r16) * K + col;
-            da[j] = *reinterpret_cast<const uint4*>(drow);
-            db[j] = *reinterpret_cast<const uint4*>(drow + 8);
+            in.da[j] = *reinterpret_cast<const uint4*>(drow);
+            in.db[j] = *reinterpret_cast<const uint4*>(drow + 8);
         }
-        float pv[16];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 q4 = *reinterpret_cast<const float4*>(p + col + 4 * i);
-            pv[4 * i] = q4.x; pv[4 * i + 1] = q4.y; pv[4 * i + 2] = q4.z; pv[4 * i + 3] = q4.w;
-        }
+        for (int i = 0; i < 4; ++i) in.p4[i] = *reinterpret_cast<const float4*>(p + col + 4 * i);
+    };
+    Group cur, nxt;
+    fetch(min(wave, groups - 1), cur);
+    for (int gi = wave; gi < groups; gi += kWaves) {
+        fetch(min(gi + kWaves, groups - 1), nxt);
+        const uint4 xa = cur.xa, xb = cur.xb;
+        const float pv[16] = {cur.p4[0].x, cur.p4[0].y, cur.p4[0].z, cur.p4[0].w, cur.p4[1].x, cur.p4[1].y,
+                              cur.p4[1].z, cur.p4[1].w, cur.p4[2].x, cur.p4[2].y, cur.p4[2].z, cur.p4[2].w,
+                              cur.p4[3].x, cur.p4[3].y, cur.p4[3].z, cur.p4[3].w};
 
-        // internal/svdq_linear.py:592-595: bf16(x·p) in float32; :609-611 the block scale.
+        // internal/svdq_linear.py:592-595: xs = bf16(x·p), a pair rounded in one
+        // v_cvt_pk_bf16_f32 (round to nearest even, as bf16_rn); :609-611 the block scale.
         float v[16];
         widen8<kHalf>(xa, v);
         widen8<kHalf>(xb, v + 8);
         float amax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            v[i] = float_of(static_cast<uint32_t>(bf16_rn(__fmul_rn(v[i], pv[i]))) << 16);
-            amax = fmaxf(amax, fabsf(v[i]));
+        for (int i = 0; i < 16; i += 2) {
+            const uint32_t pr = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                f32x2{__fmul_rn(v[i], pv[i]), __fmul_rn(v[i + 1], pv[i + 1])}, bf16x2));
+            v[i] = float_of(pr << 16);
+            v[i + 1] = float_of(pr & 0xffff0000u);
+            amax = fmaxf(amax, fmaxf(fabsf(v[i]), fabsf(v[i + 1])));
         }
         const float ratio = fminf(fmaxf(__fdiv_rn(amax, six_g), kBlockFloor), kE4m3Max);
         const uint32_t sb = e4m3_rn(ratio);
         const float sg = __fmul_rn(e4m3_value(sb), gv);
         uint32_t packed[2] = {0u, 0u};
+        if (amax < __builtin_huge_valf() && sg < __builtin_huge_valf()) {
+            // :612-616: the codes, two a conversion (element 2k in the low nibble).
+            const float rs = __fdiv_rn(1.0f, sg);
+            float q[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t code = e2m1_count(fabsf(__fdiv_rn(v[i], sg))) + (v[i] < 0.0f ? 8u : 0u);
-            packed[i >> 3] |= code << (4 * (i & 7));
+            for (int i = 0; i < 16; ++i) q[i] = e2m1_quotient(v[i], sg, rs);
+            packed[0] = put_e2m1_pair<0>(packed[0], q[0], q[1]);
+            packed[0] = put_e2m1_pair<1>(packed[0], q[2], q[3]);
+            packed[0] = put_e2m1_pair<2>(packed[0], q[4], q[5]);
+            packed[0] = put_e2m1_pair<3>(packed[0], q[6], q[7]);
+            packed[1] = put_e2m1_pair<0>(packed[1], q[8], q[9]);
+            packed[1] = put_e2m1_pair<1>(packed[1], q[10], q[11]);
+            packed[1] = put_e2m1_pair<2>(packed[1], q[12], q[13]);
+            packed[1] = put_e2m1_pair<3>(packed[1], q[14], q[15]);
+        } else {
+            // An infinite block maximum or scale: the law's divisions and threshold count as
+            // written.
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t code = e2m1_count(fabsf(__fdiv_rn(v[i], sg))) + (v[i] < 0.0f ? 8u : 0u);
+                packed[i >> 3] |= code << (4 * (i & 7));
+            }
         }
         if (!live) packed[0] = packed[1] = 0u;
         const int64_t base = static_cast<int64_t>(m) * (K / 2) + 32 * gi + 8 * part;
@@ -195,14 +264,15 @@ __global__ __launch_bounds__(quantize_waves<kR>() * 64) void nvfp4_quantize_kern
         for (int j = 0; j < kJ; ++j) {
             if constexpr (kHalf) {
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(f16x8, xa), bf16_to_half8(da[j]), acc[j], 0, 0, 0);
+                    __builtin_bit_cast(f16x8, xa), bf16_to_half8(cur.da[j]), acc[j], 0, 0, 0);
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(f16x8, xb), bf16_to_half8(db[j]), acc[j], 0, 0, 0);
+                    __builtin_bit_cast(f16x8, xb), bf16_to_half8(cur.db[j]), acc[j], 0, 0, 0);
             } else {
-                acc[j] = mfma_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, da[j]), acc[j]);
-                acc[j] = mfma_bf16(__builtin_bit_cast(bf16x8, xb), __builtin_bit_cast(bf16x8, db[j]), acc[j]);
+                acc[j] = mfma_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, cur.da[j]), acc[j]);
+                acc[j] = mfma_bf16(__builtin_bit_cast(bf16x8, xb), __builtin_bit_cast(bf16x8, cur.db[j]), acc[j]);
             }
         }
+        cur = nxt;
     }
 
     // acc[j]: lane holds rank 16j + l%16 of rows 4·(l/16) + r. Sum the waves' partials.
@@ -761,11 +831,15 @@ hipError_t svdq_nvfp4_input_scale(const void* x, bool x_half, const float* p, in
     uint32_t* word = reinterpret_cast<uint32_t*>(g);
     input_scale_init<<<1, 1, 0, s>>>(word);
     if (M == 0) return hipGetLastError();
-    const int blocks = M < 256 ? M : 256;  // one atomic max a block: few blocks, long rows
+    // ~256 workgroups (one a CU): the column chunks' workgroups times enough row slots.
+    const int gx = (K / 8 + kScaleThreads - 1) / kScaleThreads;
+    const int runs = (M + kScaleGroups * kScaleRows - 1) / (kScaleGroups * kScaleRows);
+    const dim3 grid(gx, min(runs, max(1, 256 / gx)));
+    constexpr int threads = kScaleThreads * kScaleGroups;
     if (x_half)
-        input_scale_kernel<true><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), p, M, K, word);
+        input_scale_kernel<true><<<grid, threads, 0, s>>>(static_cast<const uint16_t*>(x), p, M, K, word);
     else
-        input_scale_kernel<false><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), p, M, K, word);
+        input_scale_kernel<false><<<grid, threads, 0, s>>>(static_cast<const uint16_t*>(x), p, M, K, word);
     return hipGetLastError();
 }
 

@@ -110,6 +110,42 @@ def test_svdq_quantize_bit_exact(ops, shape, dtype, rank):
     assert (err <= exact.abs() * 2.0**-8 + spread * 2.0**-18).all(), err.max()
 
 
+def test_svdq_quantize_rounding_ties_bit_exact(ops):
+    """Codes exactly at every rounding threshold of the law and one bf16 step either side
+    (xs / (scale·g) = 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5; both signs), past the largest level
+    (6.5, 7), at ±0, at subnormal and tiny xs: ties go to the even code, −0 codes as +0, a tiny
+    negative as −0. g = 1 (the tensor's largest |x·p| is 2688) and, where a block holds 6, its
+    scale is 1, so the quotients are the values themselves."""
+    k, m = 256, 8
+    thresholds = [0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0]
+
+    def bf(v: float) -> torch.Tensor:
+        return torch.tensor(v, dtype=torch.bfloat16)
+
+    def nudge(v: float, d: int) -> torch.Tensor:  # d bf16 steps away from v
+        return (bf(v).view(torch.int16) + d).view(torch.bfloat16)
+
+    blocks = [torch.stack([bf(6.0), bf(t), nudge(t, 1), nudge(t, -1), -bf(t), -nudge(t, 1), -nudge(t, -1)]
+                          + [bf(0.0)] * 9) for t in thresholds]  # fmt: skip
+    x = torch.zeros(m, k, dtype=torch.bfloat16)
+    for r in range(m):
+        for b, blk in enumerate(blocks):
+            at = 16 * ((b + r) % 16)
+            x[r, at:at + 16] = blk
+    x[0, 255] = 2688.0
+    x[1, 200:204] = torch.tensor([-0.0, 0.0, 1e-40, -1e-40]).to(torch.bfloat16)
+    x[2, 200:216] = torch.tensor([7.0, 6.5, -7.0, 1e-3, -1e-3, 0.0, -0.0, 3.0] * 2).to(torch.bfloat16)
+    x[4, 232:248] = torch.tensor([1e-30, -1e-30, 1e-38, 5.0, 0.25, -0.25, 0.75, -0.75] * 2).to(torch.bfloat16)
+    p = torch.ones(k)
+    g = laws.svdq_nvfp4_input_scale(x, p)
+    assert g.item() == 1.0
+    down = torch.zeros(32, k, dtype=torch.bfloat16)
+    act, ascales, _ = ops.svdq_quantize(x.to(DEV), p.to(DEV), g.to(DEV), down.to(DEV))
+    codes, scales = laws.svdq_nvfp4_quantize(laws.svdq_smooth(x, p), g)
+    assert torch.equal(act[:m].cpu(), laws.svdq_nvfp4_pack(codes))
+    assert torch.equal(ascales[:m].cpu().view(torch.uint8), scales.view(torch.uint8))
+
+
 @pytest.mark.parametrize("shape", [(300, 264, 256), (1, 520, 64), (513, 256, 192), (4096, 12288, 64)],
                          ids=lambda s: "x".join(map(str, s)))  # fmt: skip
 def test_svdq_gemm_bit_exact_where_exact(ops, shape):
