@@ -131,6 +131,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cozyq_host_mx_byte": (None, [_P, _P, c_int64]),
     "cozyq_probe_div": (c_int, [c_int, _P, _P, _P, c_int64, _P]),
     "cozyq_probe_e4m3": (c_int, [c_int, _P, _P, c_int64, _P]),
+    "cozyq_probe_e2m1": (c_int, [c_int, _P, _P, c_int64, _P]),
     "cozyq_probe_mfma": (c_int, [c_int, c_int, _P, _P, _P, _P, _P, _P]),
 }
 

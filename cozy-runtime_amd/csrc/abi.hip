@@ -677,6 +677,13 @@ int cozyq_probe_e4m3(int device, const float* in, uint8_t* out, int64_t n, void*
     return cozyq::e4m3_probe(in, out, n, on(stream));
 }
 
+int cozyq_probe_e2m1(int device, const float* in, uint8_t* out, int64_t n, void* stream) {
+    if (n < 0 || n % 2) return hipErrorInvalidValue;
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    return cozyq::e2m1_probe(in, out, n, on(stream));
+}
+
 int cozyq_probe_div(int device, const float* x, const float* s, float* out, int64_t n,
                     void* stream) {
     if (n < 0) return hipErrorInvalidValue;

@@ -262,6 +262,7 @@ hipError_t rotate_factor(const float* down, float* out, int64_t groups, hipStrea
 namespace cozyq {
 hipError_t div_probe(const float* x, const float* s, float* out, int64_t n, hipStream_t st);
 hipError_t e4m3_probe(const float* in, uint8_t* out, int64_t n, hipStream_t s);
+hipError_t e2m1_probe(const float* in, uint8_t* out, int64_t n, hipStream_t s);
 hipError_t mfma_probe(int kind, const void* a, const void* b, const void* sa, const void* sb,
                       void* d, hipStream_t s);
 }  // namespace cozyq

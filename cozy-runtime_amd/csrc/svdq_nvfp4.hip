@@ -822,9 +822,25 @@ __global__ __launch_bounds__(kThreads, 1) void nvfp4_gemm_kernel(
     }
 }
 
+// Test entry: the quantizer's code conversion of values taken as quotients (scale·g = 1), two
+// codes a byte (the first in the low nibble).
+__global__ void e2m1_probe_kernel(const float* in, uint8_t* out, int64_t pairs) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= pairs) return;
+    out[i] = static_cast<uint8_t>(
+        put_e2m1_pair<0>(0u, e2m1_quotient(in[2 * i], 1.0f, 1.0f), e2m1_quotient(in[2 * i + 1], 1.0f, 1.0f)));
+}
+
 }  // namespace
 
 int svdq_nvfp4_padded_rows(int M) { return padded_rows(M); }
+
+hipError_t e2m1_probe(const float* in, uint8_t* out, int64_t n, hipStream_t s) {
+    const int64_t pairs = n / 2;
+    if (pairs == 0) return hipSuccess;
+    e2m1_probe_kernel<<<static_cast<unsigned>((pairs + 255) / 256), 256, 0, s>>>(in, out, pairs);
+    return hipGetLastError();
+}
 
 hipError_t svdq_nvfp4_input_scale(const void* x, bool x_half, const float* p, int M, int K,
                                   float* g, hipStream_t s) {

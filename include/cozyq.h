@@ -458,6 +458,12 @@ void cozyq_host_mx_byte(const float* amax, uint8_t* out, int64_t n);
  * conversion (v_cvt_pk_fp8_f32), n even, to hold it against the software encoder. */
 int cozyq_probe_e4m3(int device, const float* in, uint8_t* out, int64_t n, void* stream);
 
+/* Test entry (no reference counterpart): float32 values, taken as quotients xs / (scale·g), ->
+ * the svdq.nvfp4 quantizer's E2M1 codes (v_cvt_scalef32_pk_fp4_f32 after its −0 and NaN
+ * fix-ups), two a byte, the first in the low nibble; n even. Holds the conversion against the
+ * law's threshold count (internal/svdq_linear.py:612-616). */
+int cozyq_probe_e2m1(int device, const float* in, uint8_t* out, int64_t n, void* stream);
+
 /* Test entry (no reference counterpart): x / s through the quantizers' reciprocal-and-correction
  * division, to hold it against IEEE division. */
 int cozyq_probe_div(int device, const float* x, const float* s, float* out, int64_t n,

@@ -110,6 +110,47 @@ def test_svdq_quantize_bit_exact(ops, shape, dtype, rank):
     assert (err <= exact.abs() * 2.0**-8 + spread * 2.0**-18).all(), err.max()
 
 
+def test_e2m1_conversion_matches_the_threshold_law():
+    """The quantizer's code conversion (`cozyq_probe_e2m1`: v_cvt_scalef32_pk_fp4_f32 at unit
+    scale after its −0 and NaN fix-ups) against the law's threshold count
+    (`laws.SVDQ_THRESHOLDS`, internal/svdq_linear.py:612-616; sign from xs < 0) on every float32
+    of both signs in [2^-4, 2^4) (every threshold and the saturation past 6), and on zeros,
+    subnormals, tiny and huge values, ±inf and NaN."""
+    import numpy as np
+
+    from cozyq import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def law(v: np.ndarray) -> np.ndarray:
+        a = np.abs(v)
+        code = np.zeros(v.shape, dtype=np.uint8)
+        for bound, inclusive in laws.SVDQ_THRESHOLDS:
+            code += (a >= bound) if inclusive else (a > bound)
+        return code + (v < 0).astype(np.uint8) * 8
+
+    def check(v: np.ndarray) -> None:
+        tin = torch.from_numpy(v).to(DEV)
+        tout = torch.empty(v.size // 2, dtype=torch.uint8, device=DEV)
+        assert lib.cozyq_probe_e2m1(0, tin.data_ptr(), tout.data_ptr(), v.size, stream) == 0
+        packed = tout.cpu().numpy()
+        got = np.stack([packed & 0x0F, packed >> 4], axis=-1).reshape(-1)
+        want = law(v)
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, f"{bad.size} differ, e.g. {v[bad[:4]]} -> {got[bad[:4]]} vs {want[bad[:4]]}"
+
+    for e in range(-4, 4):  # one binade [2^e, 2^(e+1)) of both signs at a time
+        bits = (np.arange(1 << 23, dtype=np.uint32) | np.uint32((127 + e) << 23))
+        v = bits.view(np.float32)
+        check(np.concatenate([v, -v]))
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, -np.nan, 1e-45, -1e-45, 1e-40, -1e-40,
+                        1.1754944e-38, -1.1754944e-38, 1e-30, -1e-30, 0.1, -0.1, 16.0, -16.0, 1e30,
+                        -1e30, 3.4028235e38, -3.4028235e38], dtype=np.float32)
+    with np.errstate(invalid="ignore"):
+        check(special)
+
+
 def test_svdq_quantize_rounding_ties_bit_exact(ops):
     """Codes exactly at every rounding threshold of the law and one bf16 step either side
     (xs / (scale·g) = 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5; both signs), past the largest level
