@@ -138,7 +138,7 @@ __device__ __forceinline__ uint32_t e2m1_count(float a) {
 // xs / (scale·g) for v_cvt_scalef32_pk_fp4_f32 at unit scale. That conversion (nearest, ties to
 // the even code, saturating at 6) gives the law's threshold count, sign included, on every finite
 // nonzero quotient and on ±inf (held against e2m1_count over all 2^32 float32 bit patterns on
-// MI355X); it writes the sign of −0 and converts NaN to 6, where the law writes code 0 for
+// MI355X; cozyq_probe_e2m1's test repeats it on every float32 of [2^-4, 2^4)); it writes the sign of −0 and converts NaN to 6, where the law writes code 0 for
 // xs = −0 and NaN. So −0 becomes +0 first and NaN gives +0. Otherwise the quotient is RN(xs / sg)
 // (div_rn, for finite xs and finite sg > 0).
 __device__ __forceinline__ float e2m1_quotient(float xs, float sg, float rs) {
