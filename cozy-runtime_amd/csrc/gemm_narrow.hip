@@ -102,7 +102,12 @@ __global__ __launch_bounds__(kThreads) void narrow_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     // M-tiles fastest: the workgroups in flight together share their weight tiles in L2.
-    const int tm = blockIdx.x % tiles_m, tn = blockIdx.x / tiles_m;
+    // Workgroup b runs on XCD b % 8: the M-tiles of one N-tile go to the same XCD (b, b + 8, ...),
+    // so the ones after the first find that weight panel in its L2.
+    const int tiles_n = gridDim.x / tiles_m;
+    const bool xcd = tiles_m > 1 && tiles_n % 8 == 0;
+    const int tm = xcd ? (blockIdx.x >> 3) % tiles_m : blockIdx.x % tiles_m;
+    const int tn = xcd ? ((blockIdx.x >> 3) / tiles_m) * 8 + (blockIdx.x & 7) : blockIdx.x / tiles_m;
     const int m0 = __builtin_amdgcn_readfirstlane(tm * kTM);
     const int n0 = __builtin_amdgcn_readfirstlane(tn * kTN);
     const __amdgpu_buffer_rsrc_t xr = rows_from(X, m0, M, K);
@@ -298,7 +303,12 @@ __global__ __launch_bounds__(kThreads) void deep_kernel(
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const int tm = blockIdx.x % tiles_m, tn = blockIdx.x / tiles_m;
+    // Workgroup b runs on XCD b % 8: the M-tiles of one N-tile go to the same XCD (b, b + 8, ...),
+    // so the ones after the first find that weight panel in its L2.
+    const int tiles_n = gridDim.x / tiles_m;
+    const bool xcd = tiles_m > 1 && tiles_n % 8 == 0;
+    const int tm = xcd ? (blockIdx.x >> 3) % tiles_m : blockIdx.x % tiles_m;
+    const int tn = xcd ? ((blockIdx.x >> 3) / tiles_m) * 8 + (blockIdx.x & 7) : blockIdx.x / tiles_m;
     const int m0 = __builtin_amdgcn_readfirstlane(tm * kTM);
     const int n0 = __builtin_amdgcn_readfirstlane(tn * kTN);
     const __amdgpu_buffer_rsrc_t xr = rows_from(X, m0, M, K);
