@@ -630,8 +630,7 @@ __global__ __launch_bounds__(64 * kW4Waves) void w4a8_decode_kernel(
             const int r = a & 3;
             int v = r == 0 ? d[0] : (r == 1 ? d[1] : (r == 2 ? d[2] : d[3]));
             v = diagonal ? v : 0;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            v = diagonal_sum(v);
             dot[i][m] = v;
         }
     if (lane != 0 || nw >= N) return;  // N % 8 == 0: a wave's four rows are all in or all out

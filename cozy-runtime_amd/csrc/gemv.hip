@@ -181,7 +181,7 @@ __global__ __launch_bounds__(kDThreads) void fp8_decode_kernel(
             const int r = a & 3;
             float v = r == 0 ? d[0] : (r == 1 ? d[1] : (r == 2 ? d[2] : d[3]));
             v = diagonal ? v : 0.0f;
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            v = diagonal_sum(v);
             dot[i][m] = v;
         }
     static_assert(8 % kRowsPerWave == 0, "N % 8 == 0 keeps a wave's rows whole");
@@ -379,7 +379,7 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
             const int r = a & 3;
             int v = r == 0 ? d[0] : (r == 1 ? d[1] : (r == 2 ? d[2] : d[3]));
             v = diagonal ? v : 0;
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            v = diagonal_sum(v);
             dot[i][m] = v;
         }
     if (lane != 0 || nw >= N) return;  // N % 4 == 0: a wave's rows are all in or all out

@@ -455,8 +455,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void nvfp4_stream_kernel(const u
             const int r = a & 3;
             float v = r == 0 ? d[0] : (r == 1 ? d[1] : (r == 2 ? d[2] : d[3]));
             v = diagonal ? v : 0.0f;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            v = diagonal_sum(v);
             if (lane == 0 && n0 + i < N) out[static_cast<int64_t>(m) * N + n0 + i] = narrow<kOutHalf>(v * g);
         }
 }
