@@ -18,7 +18,7 @@ namespace {
 
 constexpr int kThreads = 256;
 __device__ __forceinline__ float block_max(float v, float* red) {
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    v = wave_max(v);  // rows.h: DPP, every lane of the workgroup active
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (lane == 0) red[wave] = v;
     __syncthreads();
