@@ -5,6 +5,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "rotate.h"
+#include "rows.h"
 
 namespace cozyq {
 namespace {
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(kDThreads) void fp8_decode_kernel(
                 amax[m] = fmaxf(amax[m], fabsf(widen<kXHalf>(w4[i] >> 16)));
             }
         }
-        for (int off = 32; off > 0; off >>= 1) amax[m] = fmaxf(amax[m], __shfl_xor(amax[m], off));
+        amax[m] = wave_max(amax[m]);
         if (lane == 0) red[wave][m] = amax[m];
     }
     __syncthreads();
@@ -307,7 +308,7 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
             rotate_lds_chunk<256, kDThreads>(work, width, tid, rot[m][c4], amax[m]);
             __syncthreads();
         }
-        for (int off = 32; off > 0; off >>= 1) amax[m] = fmaxf(amax[m], __shfl_xor(amax[m], off));
+        amax[m] = wave_max(amax[m]);
         if (lane == 0) red[wave][m] = amax[m];
     }
     __syncthreads();
