@@ -327,8 +327,8 @@ __global__ __launch_bounds__(kThreads) void mx_quantize_kernel(
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, dpp_move<0xB1>(amax));  // the block's 4 lanes: quad_perm 1,0,3,2
+    amax = fmaxf(amax, dpp_move<0x4E>(amax));  // quad_perm 2,3,0,1
     const uint32_t byte = mx_byte(amax);
     // x / 2^(byte-127) as x · 2^(127-byte): the same real number, rounded once either way.
     const float inv = byte >= 254 ? float_of(1u << 22) : float_of((254u - byte) << 23);
