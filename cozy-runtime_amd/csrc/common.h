@@ -75,6 +75,28 @@ __host__ __device__ __forceinline__ uint8_t e4m3_rn(float v) {
 // RN(x / s) (Markstein's theorem; quotients that underflow excepted, which every caller here maps
 // to code 0 anyway). The sign is x's, as a true division's is (the correction turns −0 into +0).
 // Held against IEEE division by the GPU tests.
+// x from the lane that DPP control kCtrl names (every lane active).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, false));
+}
+
+// The maximum over a wave, uniform: each 16-lane row's by DPP (quad swaps, then rotations of the
+// row by 4 and 8 lanes), then the four rows' read from lanes 0, 16, 32 and 48. No LDS round trip
+// (the ds_bpermute shuffles it replaces wait on the LDS crossbar); a maximum is exact in any order.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm 1,0,3,2
+    v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm 2,3,0,1
+    v = fmaxf(v, dpp_move<0x124>(v));  // row_ror:4
+    v = fmaxf(v, dpp_move<0x128>(v));  // row_ror:8
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // The sum over a wave of a value that is zero outside lanes 0-3, 20-23, 40-43 and 60-63: the
 // diagonal of a 16x16 MFMA result (lane l holds rows 4·(l/16) + r of column l%16), one quad of
 // each 16-lane row. Each quad is summed by two DPP quad swaps, then the four quad sums are read

@@ -97,8 +97,7 @@ __global__ __launch_bounds__(kScaleThreads * kScaleGroups) void input_scale_kern
 #pragma unroll
         for (int i = 0; i < 8; ++i) m = fmaxf(m, __fmul_rn(a[i], pv[i]));
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = wave_max(m);  // every lane of the workgroup active
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     if (threadIdx.x == 0) {
