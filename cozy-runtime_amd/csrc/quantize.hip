@@ -314,6 +314,46 @@ __global__ __launch_bounds__(kThreads) void rowwise_quantize_kernel(
     if (scale < __builtin_huge_valf()) emit(std::true_type{}); else emit(std::false_type{});
 }
 
+// fp8 rows of at most kRowMaxK elements with no prologue: one wave per row (rows.h's loads and
+// wave maximum), the same law as rowwise_quantize_kernel<fp8> element for element (s = max(amax /
+// 448, floor), codes e4m3(clamp(x / s, ±448))), with no workgroup barrier and no second pass.
+template <bool kHalf>
+__global__ __launch_bounds__(256) void fp8_row_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
+                                                      float* __restrict__ scales, int M, int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;  // a whole wave
+    uint4 raw[kRowLoads];
+    row_loads(row_view(x + static_cast<int64_t>(row) * K, K), lane, raw);
+    float v[kRowLoads][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRowLoads; ++i) {
+        unpack8<kHalf>(raw[i], v[i]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
+    }
+    amax = wave_max(amax);
+    const float scale = fmaxf(amax / kE4m3Max, kScaleFloor);
+    if (lane == 0) scales[row] = scale;
+    uint8_t* qr = q + static_cast<int64_t>(row) * K;
+    const float rs = 1.0f / scale;
+    auto emit = [&](auto fast) {
+        constexpr bool kFast = decltype(fast)::value;
+#pragma unroll
+        for (int i = 0; i < kRowLoads; ++i) {
+            const int e = 8 * (lane + 64 * i);
+            if (e >= K) continue;
+            float r[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                r[j] = fminf(fmaxf(kFast ? div_rn(v[i][j], scale, rs) : v[i][j] / scale, -kE4m3Max), kE4m3Max);
+            *reinterpret_cast<uint2*>(qr + e) = make_uint2(e4m3x4(r[0], r[1], r[2], r[3]), e4m3x4(r[4], r[5], r[6], r[7]));
+        }
+    };
+    if (scale < __builtin_huge_valf()) emit(std::true_type{}); else emit(std::false_type{});
+}
+
 // MX quantization: 4 threads per 32-element block, 8 elements each.
 template <bool kHalf>
 __global__ __launch_bounds__(kThreads) void mx_quantize_kernel(
@@ -362,6 +402,12 @@ template <bool kHalf, bool kFp8>
 hipError_t launch_rowwise(const void* x, uint8_t* q, float* scales, int M, int K,
                           const Prologue* pro, hipStream_t s) {
     auto xp = static_cast<const uint16_t*>(x);
+    if constexpr (kFp8) {
+        if (pro == nullptr && K <= kRowMaxK && K % 8 == 0) {
+            fp8_row_kernel<kHalf><<<(M + 3) / 4, 256, 0, s>>>(xp, q, scales, M, K);
+            return hipGetLastError();
+        }
+    }
     if (pro != nullptr)
         rowwise_quantize_kernel<kHalf, kFp8, true><<<M, kThreads, 0, s>>>(xp, q, scales, K, *pro);
     else
