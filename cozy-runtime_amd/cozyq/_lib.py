@@ -57,6 +57,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "cozyq_linear_workspace_bytes": (c_int64, [c_int64]),
     "cozyq_linear_noalloc_max_rows": (c_int, []),
+    "cozyq_linear_status": (c_int, [c_int, _P, _P]),
+    "cozyq_linear_noalloc_status": (c_int, [c_int, _P]),
+    "cozyq_linear_test_spin_limit": (None, [c_int]),
     "cozyq_linear_noalloc": (
         c_int,
         [c_int, _P, c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, c_int, c_int, _P],

@@ -175,15 +175,30 @@ class Prebuilt:
 
     def int8_linear_rot(
         self, x: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None, out_dtype: Dtype,
-        rotation: int, epilogue: int = 0,
+        rotation: int, epilogue: int = 0, verify: bool = False,
     ) -> tuple[Tensor, Tensor, Tensor] | None:
         """The fused linear (`cozyq_linear`) for any rotation lane (256, 128, 0) and epilogue
         (0 none, 1 tanh-GELU): (out, q, scales) with q / scales the operand it quantized, or None
-        where it declines."""
+        where it declines. A tile whose wait for its rows gave up is written as NaN; `verify`
+        synchronizes the stream after the call and raises RuntimeError if that happened."""
         multiple = 16 if rotation == 0 else rotation
         flat = self._rows(_Format("int8", False, multiple), x)
         bias = self._weight(_Format("int8", False, multiple), data, scale, bias, flat.shape[1], out_dtype)
-        return self._linear_fused(flat, data, _aligned(scale), bias, out_dtype, rotation, epilogue)
+        done = self._linear_fused(flat, data, _aligned(scale), bias, out_dtype, rotation, epilogue)
+        if verify and done is not None:
+            self.linear_status()
+        return done
+
+    def linear_status(self) -> None:
+        """Raises RuntimeError if a fused linear on this stream's workspace gave up waiting for
+        its rows since the last check (its tiles were written as NaN); synchronizes the stream
+        and clears the record (`cozyq_linear_status`)."""
+        stream = self._stream()
+        work = self._workspaces.get(stream)
+        if work is None:
+            return
+        self._check(self._lib.cozyq_linear_status(self.index, work.data_ptr(), stream),
+                    "the fused linear (a tile's wait for its rows gave up)")  # fmt: skip
 
     def fp8_linear(
         self, x: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None, out_dtype: Dtype

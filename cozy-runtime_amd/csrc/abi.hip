@@ -154,6 +154,26 @@ int cozyq_linear(int device, const void* x, int x_half, int rotation, int8_t* q,
 
 int cozyq_linear_noalloc_max_rows(void) { return cozyq::linear_noalloc_max_rows(); }
 
+static int linear_status_checked(int device, int* workspace, void* stream) {
+    const OnDevice guard(device);
+    if (guard.error() != hipSuccess) return guard.error();
+    int status = 0;
+    const hipError_t e = cozyq::linear_status(workspace, device, on(stream), &status);
+    if (e != hipSuccess) return e;
+    return status ? hipErrorLaunchTimeOut : hipSuccess;
+}
+
+int cozyq_linear_status(int device, int* workspace, void* stream) {
+    if (workspace == nullptr) return hipErrorInvalidValue;
+    return linear_status_checked(device, workspace, stream);
+}
+
+int cozyq_linear_noalloc_status(int device, void* stream) {
+    return linear_status_checked(device, nullptr, stream);
+}
+
+void cozyq_linear_test_spin_limit(int limit) { cozyq::linear_set_spin_limit(limit); }
+
 int cozyq_linear_noalloc(int device, const void* x, int x_half, int rotation, int8_t* q, float* qs,
                          const int8_t* w, const float* w_scale, const void* bias, void* out,
                          int64_t ldo, int out_half, int M, int N, int K, int epilogue, void* stream) {

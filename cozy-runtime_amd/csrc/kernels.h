@@ -42,6 +42,13 @@ hipError_t linear_int8(const void* x, bool half, int rotation, int8_t* q, float*
 // allocation): M <= linear_noalloc_max_rows(), else hipErrorInvalidValue. Calls that overlap on
 // one GPU race on the array.
 int linear_noalloc_max_rows();
+// The status word of a fused linear's counters (`work`, or the allocation-free array when null):
+// 1 if a launch since the last read gave up waiting for its rows (its tiles were written as NaN),
+// else 0; reading it synchronizes `s` and clears the word.
+hipError_t linear_status(int* work, int device, hipStream_t s, int* status);
+// Test hook: the spin limit of later fused launches (0 the default; negative: every wait gives
+// up at once).
+void linear_set_spin_limit(int limit);
 hipError_t linear_int8_noalloc(const void* x, bool half, int rotation, int8_t* q, float* qs,
                                const int8_t* w, const float* ws, const void* bias, void* out,
                                int64_t ldo, int M, int N, int K, int epilogue, int device,

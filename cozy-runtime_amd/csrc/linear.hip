@@ -16,12 +16,14 @@
 // A workgroup claims the next job of its queue with an atomic counter. Before its first tile it
 // waits for its queue's quantize jobs, all claimed before any tile by running workgroups that
 // never wait themselves, so every wait ends. A spin limit guards the wait anyway: past it the
-// workgroup records the fault in the workspace and goes on.
+// workgroup records the fault and writes NaN into every output tile it claims instead of
+// computing it from codes that may not exist yet, so no tile is ever silently wrong.
 //
 // The workspace (kernels.h `linear_workspace_ints`) holds the queue heads, an exit count, the
-// fault flag and one done-counter per M-tile. It must be zero before the first launch. The last
-// workgroup to leave sets every counter back to zero, so the next launch on the stream starts
-// clean; launches that overlap on one workspace race.
+// fault flag, a status word and one done-counter per M-tile. It must be zero before the first
+// launch. The last workgroup to leave moves the fault flag into the status word and sets every
+// counter back to zero, so the next launch on the stream starts clean; the status word stays set
+// until the host reads it (linear_status). Launches that overlap on one workspace race.
 #include "gemm_tile.h"
 #include "rows.h"
 
@@ -34,9 +36,14 @@ constexpr int kSpinLimit = 1 << 24;  // s_sleep(2) rounds a tile waits at most (
 constexpr int kJobSlot = kLdsBytes;  // LDS word that broadcasts a claimed job
 constexpr int kFusedLds = kLdsBytes + 16;
 
-// Workspace layout (int32): [0, 8) queue heads, [8] exit count, [9] fault flag, [16, 16 +
-// tiles_m) quantize jobs finished per M-tile.
-constexpr int kExit = 8, kFault = 9, kDone = 16;
+// Workspace layout (int32): [0, 8) queue heads, [8] exit count, [9] fault flag (this launch),
+// [10] status (a launch since the last read gave up a wait), [16, 16 + tiles_m) quantize jobs
+// finished per M-tile.
+constexpr int kExit = 8, kFault = 9, kStatus = 10, kDone = 16;
+
+// The spin limit launches use: kSpinLimit, or what the test hook set (a negative value makes
+// every wait give up at once, which exercises the fault path without any wave waiting).
+int spin_limit_setting = kSpinLimit;
 
 __device__ __forceinline__ int qjobs(int m, int M) {
     const int rows = min(kTile, M - m * kTile);
@@ -90,18 +97,30 @@ __device__ __forceinline__ void quantize_job(const uint16_t* __restrict__ x, int
             quantize_row_wave<kHalf, kRot>(raw[i], K, lane, slice, q + static_cast<int64_t>(r0 + i) * K, qs + r0 + i);
 }
 
+// Output tile (tm, tn) filled with the output dtype's NaN: what a workgroup whose wait gave up
+// writes in place of the tile.
+template <bool kOutHalf>
+__device__ __forceinline__ void nan_tile(uint16_t* __restrict__ out, int64_t ldo, int M, int N, int tm, int tn) {
+    const uint16_t nan = kOutHalf ? 0x7e00 : 0x7fc0;
+    const int m0 = tm * kTile, n0 = tn * kTile;
+    const int rows = min(kTile, M - m0), cols = min(kTile, N - n0);
+    for (int i = threadIdx.x; i < rows * cols; i += blockDim.x)
+        out[static_cast<int64_t>(m0 + i / cols) * ldo + n0 + i % cols] = nan;
+}
+
 template <bool kHalf, int kRot, bool kOutHalf, bool kBias, int kEpi>
 __global__ __launch_bounds__(kThreads, 1) void linear_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ qs,
     const int8_t* __restrict__ W, const float* __restrict__ ws, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ out, int64_t ldo, int M, int N, int K, int tiles_m, int tiles_n,
-    int queues, int* __restrict__ work) {
+    int queues, int* __restrict__ work, int spin_limit) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kFusedLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int qx = blockIdx.x % queues;
     const int total = queue_jobs(qx, queues, tiles_m, tiles_n, M);
     int* done = work + kDone;
     bool acquired = false;  // the queue's rows, once all are quantized
+    bool faulted = false;   // the wait for them gave up: tiles are written as NaN
     for (;;) {
         if (tid == 0)
             *reinterpret_cast<int*>(lds + kJobSlot) =
@@ -127,29 +146,43 @@ __global__ __launch_bounds__(kThreads, 1) void linear_kernel(
         if (!acquired) {
             if (tid == 0) {
                 int spins = 0;
-                for (int m = qx; m < tiles_m; m += queues) {
+                bool gave_up = spin_limit < 0;
+                for (int m = qx; m < tiles_m && !gave_up; m += queues) {
                     const int need = qjobs(m, M);
                     while (__hip_atomic_load(done + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
                         __builtin_amdgcn_s_sleep(2);
-                        if (++spins >= kSpinLimit) {
-                            __hip_atomic_store(work + kFault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (++spins >= spin_limit) {
+                            gave_up = true;
                             break;
                         }
                     }
                 }
+                if (gave_up) __hip_atomic_store(work + kFault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *reinterpret_cast<int*>(lds + kJobSlot + 4) = gave_up;
             }
             __syncthreads();
+            faulted = *reinterpret_cast<const int*>(lds + kJobSlot + 4) != 0;
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             acquired = true;
+        }
+        if (faulted) {
+            nan_tile<kOutHalf>(out, ldo, M, N, job.m, job.n);
+            continue;
         }
         gemm_tile<kInt8, kOutHalf, kBias, kEpi>(
             lds, reinterpret_cast<const uint8_t*>(q), reinterpret_cast<const uint8_t*>(W), qs, ws,
             nullptr, nullptr, bias, out, nullptr, ldo, M, N, K, job.m, job.n);
     }
-    // The last workgroup out resets the counters for the next launch.
+    // The last workgroup out moves the fault flag into the status word and resets the counters
+    // for the next launch. Every workgroup's fault store precedes its exit increment, which the
+    // last one's acquire sees.
     if (tid == 0) {
         const int before = __hip_atomic_fetch_add(work + kExit, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         if (before == static_cast<int>(gridDim.x) - 1) {
+            if (__hip_atomic_load(work + kFault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                __hip_atomic_store(work + kStatus, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(work + kFault, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             for (int i = 0; i < kMaxQueues; ++i) __hip_atomic_store(work + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             for (int m = 0; m < tiles_m; ++m) __hip_atomic_store(done + m, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(work + kExit, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -179,7 +212,7 @@ hipError_t launch_linear(const void* x, int8_t* q, float* qs, const int8_t* w, c
     const int grid = max(queues, min(cu_count(device), jobs));
     linear_kernel<kHalf, kRot, kOutHalf, kBias, kEpi><<<grid, kThreads, 0, s>>>(
         static_cast<const uint16_t*>(x), q, qs, w, ws, static_cast<const uint16_t*>(bias),
-        static_cast<uint16_t*>(out), ldo, M, N, K, tiles_m, tiles_n, queues, work);
+        static_cast<uint16_t*>(out), ldo, M, N, K, tiles_m, tiles_n, queues, work, spin_limit_setting);
     return hipGetLastError();
 }
 
@@ -205,7 +238,8 @@ hipError_t scratch_of(int device, int** out) {
 }
 
 // The counters a launch uses, set to zero on the launch's stream ahead of it (a kernel, not a
-// memset node, so a captured graph replays it correctly).
+// memset node, so a captured graph replays it correctly). The status word is cleared with them:
+// the allocation-free entry point's status describes its last call.
 __global__ __launch_bounds__(256) void clear_ints(int* __restrict__ p, int n) {
     for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
 }
@@ -237,6 +271,27 @@ hipError_t linear_int8(const void* x, bool half, int rotation, int8_t* q, float*
 }
 
 int linear_noalloc_max_rows() { return (kScratchInts - kDone) * kTile; }
+
+hipError_t linear_status(int* work, int device, hipStream_t s, int* status) {
+    if (work == nullptr) {
+        const hipError_t e = scratch_of(device, &work);
+        if (e != hipSuccess) return e;
+    }
+    int word = 0;
+    hipError_t e = hipMemcpyAsync(&word, work + kStatus, sizeof(int), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return e;
+    if (word != 0) {
+        clear_ints<<<1, 64, 0, s>>>(work + kStatus, 1);
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) return e;
+    }
+    *status = word;
+    return hipSuccess;
+}
+
+void linear_set_spin_limit(int limit) { spin_limit_setting = limit == 0 ? kSpinLimit : limit; }
 
 hipError_t linear_int8_noalloc(const void* x, bool half, int rotation, int8_t* q, float* qs,
                                const int8_t* w, const float* ws, const void* bias, void* out,

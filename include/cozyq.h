@@ -124,11 +124,24 @@ int cozyq_linear(int device, const void* x, int x_half, int rotation, int8_t* q,
 
 /* cozyq_linear that allocates nothing (no reference counterpart; for callers that cannot
  * allocate: code under graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * Same arguments without `workspace`: the counters live in the library's own 4 KiB device array
+ * Same arguments without `workspace`: the counters live in the library's own 4160-byte device array
  * (one per GPU, held until the process ends), cleared by a small kernel on `stream` ahead of each
  * launch. M <= cozyq_linear_noalloc_max_rows() (262144), else hipErrorInvalidValue before
  * anything runs. Every call on one GPU shares the array: calls that overlap on a GPU race. */
 int cozyq_linear_noalloc_max_rows(void);
+
+/* The fused linear's fault report (no reference counterpart: the reference's programmatic
+ * dependent launch has no wait to give up). A tile waits for its rows' quantize jobs with a
+ * bounded spin; a workgroup whose spin gives up writes NaN into every output tile it claims (never
+ * a tile computed from codes that may not exist yet) and the launch records it in the counters'
+ * status word. cozyq_linear_status synchronizes `stream`, returns hipErrorLaunchTimeOut if a call
+ * on `workspace` gave up since the last read (and clears the record), else 0.
+ * cozyq_linear_noalloc_status does the same for the allocation-free entry point's last call. */
+int cozyq_linear_status(int device, int* workspace, void* stream);
+int cozyq_linear_noalloc_status(int device, void* stream);
+/* Test entry: the spin limit of later fused launches in this process (0 restores the default;
+ * negative makes every wait give up at once, so the fault path runs with no wave waiting). */
+void cozyq_linear_test_spin_limit(int limit);
 int cozyq_linear_noalloc(int device, const void* x, int x_half, int rotation, int8_t* q, float* qs,
                          const int8_t* w, const float* w_scale, const void* bias, void* out,
                          int64_t ldo, int out_half, int M, int N, int K, int epilogue, void* stream);

@@ -120,3 +120,34 @@ def test_c2_full_size_fused_equals_two_launch(ops):
     q2, s2 = ops.int8_quantize_rot(x, 128)
     assert torch.equal(q, q2) and torch.equal(s, s2)
     assert torch.equal(out, ops.int8_gemm_ex(q2, s2, data, scale, bias, torch.bfloat16, 1))
+
+
+def test_fused_linear_reports_a_wait_that_gives_up(ops):
+    """The bounded wait's failure path, forced from the host (`cozyq_linear_test_spin_limit(-1)`
+    makes every workgroup give up before it waits, so every kernel exits normally): every output
+    is the output dtype's NaN, never a tile computed from codes that may not exist yet; the status
+    read reports it once and clears it; the quantize jobs still write the law's operand; the
+    counters are left zero, and the next call, at the default limit, is the law again."""
+    lib = ops._lib
+    m, n, k = 600, 520, 1024
+    x = activations(m, k, seed=31)
+    data, scale = weight(n, k, 256, seed=32)
+    dx, dd, ds = x.to(DEV), data.to(DEV), scale.to(DEV)
+    lib.cozyq_linear_test_spin_limit(-1)
+    try:
+        for dtype in (torch.bfloat16, torch.float16):
+            out, q, s = ops.int8_linear_rot(dx.to(dtype), dd, ds, None, dtype, 256)
+            torch.cuda.synchronize()
+            assert torch.isnan(out.cpu().float()).all()
+            wq, ws = laws.quantize_rows_int8(x.to(dtype), 256)
+            assert torch.equal(q.cpu(), wq)
+            assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
+    finally:
+        lib.cozyq_linear_test_spin_limit(0)
+    with pytest.raises(RuntimeError, match="gave up"):
+        ops.linear_status()
+    ops.linear_status()  # the record was cleared by the read
+    for work in ops._workspaces.values():
+        assert not work.any()
+    out, _, _ = ops.int8_linear_rot(dx, dd, ds, None, torch.bfloat16, 256, verify=True)
+    assert torch.equal(out.cpu(), laws.int8_linear(x, data, scale, None, torch.bfloat16))

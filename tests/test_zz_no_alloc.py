@@ -57,3 +57,31 @@ def test_linear_noalloc_matches_the_workspace_entry_point():
             bias.data_ptr(), x.data_ptr(), 264, 0, rows + 1, 264, 256, 0, torch.cuda.current_stream().cuda_stream]
     refused = lib.cozyq_linear_noalloc(*args)  # refused before anything runs
     assert _lib.error_name(refused) == "hipErrorInvalidValue"
+
+
+def test_linear_noalloc_reports_a_wait_that_gives_up():
+    """The failure path of the fused kernel's bounded wait through the allocation-free entry
+    point, forced from the host (every workgroup gives up before it waits, so every kernel exits
+    normally): NaN outputs, the status read reports it (hipErrorLaunchTimeOut) once; the next
+    call, at the default limit, equals the workspace entry point and reads back clean."""
+    from cozyq import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    x, data, scale, bias = _operands(700, 520, 1024, 4)
+    lib.cozyq_linear_test_spin_limit(-1)
+    try:
+        out, _, _ = _call(lib, lib.cozyq_linear_noalloc, x, data, scale, bias, None)
+        torch.cuda.synchronize()
+    finally:
+        lib.cozyq_linear_test_spin_limit(0)
+    assert torch.isnan(out.float()).all()
+    assert _lib.error_name(lib.cozyq_linear_noalloc_status(0, stream)) == "hipErrorLaunchTimeOut"
+    assert lib.cozyq_linear_noalloc_status(0, stream) == 0
+    got = _call(lib, lib.cozyq_linear_noalloc, x, data, scale, bias, None)
+    work = torch.zeros(int(lib.cozyq_linear_workspace_bytes(700)) // 4, dtype=torch.int32, device=DEV)
+    want = _call(lib, lib.cozyq_linear, x, data, scale, bias, work)
+    torch.cuda.synchronize()
+    assert lib.cozyq_linear_noalloc_status(0, stream) == 0
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
