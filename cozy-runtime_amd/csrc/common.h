@@ -70,11 +70,6 @@ __host__ __device__ __forceinline__ uint8_t e4m3_rn(float v) {
     return static_cast<uint8_t>(sign | (kept - (120u << 3)));
 }
 
-// x / s for s > 0, rounded to nearest even, given r = RN(1/s): q = RN(x·r) is within an ulp of
-// x / s, the remainder x − q·s is exact on the FMA, and one correction q + rem·r rounds to
-// RN(x / s) (Markstein's theorem; quotients that underflow excepted, which every caller here maps
-// to code 0 anyway). The sign is x's, as a true division's is (the correction turns −0 into +0).
-// Held against IEEE division by the GPU tests.
 // x from the lane that DPP control kCtrl names (every lane active).
 template <int kCtrl>
 __device__ __forceinline__ float dpp_move(float x) {
@@ -97,6 +92,25 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// IEEE 754-2019 maximum (v_maximum3_f32 on gfx950): a NaN operand gives NaN, as torch's amax
+// does, where fmaxf would drop it.
+__device__ __forceinline__ float nan_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float nan_min(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+
+// wave_max with NaN propagated: the wave's maximum, or NaN if any lane holds one.
+__device__ __forceinline__ float wave_max_nan(float v) {
+    v = nan_max(v, dpp_move<0xB1>(v));
+    v = nan_max(v, dpp_move<0x4E>(v));
+    v = nan_max(v, dpp_move<0x124>(v));
+    v = nan_max(v, dpp_move<0x128>(v));
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return nan_max(nan_max(r0, r1), nan_max(r2, r3));
+}
+
 // The sum over a wave of a value that is zero outside lanes 0-3, 20-23, 40-43 and 60-63: the
 // diagonal of a 16x16 MFMA result (lane l holds rows 4·(l/16) + r of column l%16), one quad of
 // each 16-lane row. Each quad is summed by two DPP quad swaps, then the four quad sums are read
@@ -115,6 +129,11 @@ __device__ __forceinline__ T diagonal_sum(T v) {
     return ((q0 + q1) + q2) + q3;
 }
 
+// x / s for s > 0, rounded to nearest even, given r = RN(1/s): q = RN(x·r) is within an ulp of
+// x / s, the remainder x − q·s is exact on the FMA, and one correction q + rem·r rounds to
+// RN(x / s) (Markstein's theorem; quotients that underflow excepted, which every caller here maps
+// to code 0 anyway). The sign is x's, as a true division's is (the correction turns −0 into +0).
+// Held against IEEE division by the GPU tests.
 __device__ __forceinline__ float div_rn(float x, float s, float r) {
     const float q = x * r;
     const float rem = __builtin_fmaf(-q, s, x);

@@ -56,7 +56,8 @@ __global__ void input_scale_init(uint32_t* g) { *g = bits_of(kInputFloor); }
 // g = max(max over x of fl(|x|·p[col]) / 2688, 1e-30). The law takes amax over rows first, then
 // · p, then the max: the same value, since fl(a·p) is monotonic in a for p > 0; the division and
 // the clamp are monotonic too, so each workgroup's candidate enters by an unsigned max of its
-// (non-negative) float bits into *g, which input_scale_init set to the floor.
+// (non-negative) float bits into *g, which input_scale_init set to the floor. Maxima propagate
+// NaN, as torch's amax does, so an x holding a NaN gives g = NaN, as the law does.
 // Atomics on the one word serialize (~10 ns each measured on MI355X, against ~6 us for the whole
 // read at C4's size), so there are few workgroups, each of many waves: ~256 of kScaleGroups x
 // kScaleThreads threads, and a workgroup whose candidate does not exceed what *g already holds
@@ -88,22 +89,24 @@ __global__ __launch_bounds__(kScaleThreads * kScaleGroups) void input_scale_kern
                 float f[8];
                 widen8<kHalf>(v[r], f);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) a[i] = fmaxf(a[i], fabsf(f[i]));
+                for (int i = 0; i < 8; ++i) a[i] = nan_max(a[i], fabsf(f[i]));
             }
         }
         const float4 p0 = *reinterpret_cast<const float4*>(p + 8 * c);
         const float4 p1 = *reinterpret_cast<const float4*>(p + 8 * c + 4);
         const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) m = fmaxf(m, __fmul_rn(a[i], pv[i]));
+        for (int i = 0; i < 8; ++i) m = nan_max(m, __fmul_rn(a[i], pv[i]));
     }
-    m = wave_max(m);  // every lane of the workgroup active
+    m = wave_max_nan(m);  // every lane of the workgroup active
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     if (threadIdx.x == 0) {
 #pragma unroll
-        for (int w = 1; w < kScaleThreads * kScaleGroups / 64; ++w) m = fmaxf(m, red[w]);
-        const uint32_t bits = bits_of(fmaxf(__fdiv_rn(m, kLevelsMax), kInputFloor));
+        for (int w = 1; w < kScaleThreads * kScaleGroups / 64; ++w) m = nan_max(m, red[w]);
+        // A NaN anywhere in x makes g NaN, as the law's amax and clamp do; its bits (a positive
+        // NaN, |x| cleared the sign) exceed every non-negative float's, so it wins the max.
+        const uint32_t bits = bits_of(nan_max(__fdiv_rn(m, kLevelsMax), kInputFloor));
         if (bits > __hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(g, bits);
     }
 }
@@ -224,9 +227,11 @@ __global__ __launch_bounds__(quantize_waves<kR>() * 64) void nvfp4_quantize_kern
                 f32x2{__fmul_rn(v[i], pv[i]), __fmul_rn(v[i + 1], pv[i + 1])}, bf16x2));
             v[i] = float_of(pr << 16);
             v[i + 1] = float_of(pr & 0xffff0000u);
-            amax = fmaxf(amax, fmaxf(fabsf(v[i]), fabsf(v[i + 1])));
+            amax = nan_max(amax, nan_max(fabsf(v[i]), fabsf(v[i + 1])));
         }
-        const float ratio = fminf(fmaxf(__fdiv_rn(amax, six_g), kBlockFloor), kE4m3Max);
+        // NaN-propagating, as the law's amax and clamp: a block holding a NaN gets the E4M3 NaN
+        // scale, and then every code is the threshold count of NaN (0), + 8 where x < 0.
+        const float ratio = nan_min(nan_max(__fdiv_rn(amax, six_g), kBlockFloor), kE4m3Max);
         const uint32_t sb = e4m3_rn(ratio);
         const float sg = __fmul_rn(e4m3_value(sb), gv);
         uint32_t packed[2] = {0u, 0u};

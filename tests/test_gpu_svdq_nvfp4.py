@@ -361,3 +361,27 @@ def test_svdq_leaf_lora_branches(extra):
     want = laws.svdq_nvfp4_exact(x, d, None) + (x.double() @ a.double().t()) @ (0.5 * b.double()).t()
     assert_close(got, want)
     assert (leaf._cozy_merged[1] is None) == (r + extra > 128)
+
+
+def test_svdq_quantize_and_input_scale_propagate_nan(ops):
+    """A NaN in x, as the law treats it (torch's amax and clamp propagate NaN): the block holding
+    it gets the E4M3 NaN scale 0x7F and codes 0, + 8 where x < 0 (every threshold comparison with
+    a NaN quotient is false); the other blocks are untouched; and the input scale of an x holding
+    a NaN is NaN. Held to the oracle bit for bit, at a stored (finite) second level."""
+    m, k = 40, 256
+    x = activations(m, k, seed=41)
+    x[3, 17] = float("nan")
+    x[10, 200] = float("nan")
+    x[10, 201] = -1.0
+    x[10, 202] = 1.0
+    d = roles(264, k, 32, seed=42)
+    p = d["pre_quant_scale"]
+    g = torch.tensor([0.05])
+    act, ascales, _ = ops.svdq_quantize(x.to(DEV), p.to(DEV), g.to(DEV), d["lowrank_down"].to(DEV))
+    codes, scales = laws.svdq_nvfp4_quantize(laws.svdq_smooth(x, p), g)
+    assert scales.view(torch.uint8)[3, 1] == 0x7F and scales.view(torch.uint8)[10, 12] == 0x7F
+    assert codes[10, 201] == 8 and codes[10, 202] == 0 and codes[10, 200] == 0
+    assert torch.equal(act[:m].cpu(), laws.svdq_nvfp4_pack(codes))
+    assert torch.equal(ascales[:m].cpu().view(torch.uint8), scales.view(torch.uint8))
+    got = ops.svdq_input_scale(x.to(DEV), p.to(DEV))
+    assert torch.isnan(got).all() and torch.isnan(laws.svdq_nvfp4_input_scale(x, p)).all()

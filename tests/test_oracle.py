@@ -811,3 +811,25 @@ def test_w4a8_unpack_every_scale_and_code_against_numpy():
             want = np.rint(scale_f * levels[None, :])
         want = np.clip(np.nan_to_num(want, nan=0.0), -127, 127).astype(np.int8)
         assert np.array_equal(laws.w4a8_unpack(codes, scales, book).numpy(), want)
+
+
+def test_svdq_nvfp4_nan_block_is_pinned():
+    """A block holding a NaN under `svdq_nvfp4_quantize`, against what IEEE arithmetic fixes: its
+    amax is NaN, so its scale is the E4M3 NaN byte 0x7F; every quotient by a NaN scale is NaN and
+    fails every threshold comparison, so each code is 0, + 8 where the element is negative (the
+    NaN itself is not); a neighbouring block is as without the NaN. The input scale of a tensor
+    holding a NaN is NaN (amax and clamp propagate it)."""
+    xs = torch.zeros(1, 32)
+    xs[0, :16] = torch.linspace(-3, 3, 16)
+    xs[0, 16:] = torch.linspace(-3, 3, 16)
+    xs[0, 5] = float("nan")
+    g = torch.tensor([0.5])
+    codes, scales = laws.svdq_nvfp4_quantize(xs, g)
+    assert scales.view(torch.uint8)[0, 0] == 0x7F
+    want = (xs[0, :16] < 0).to(torch.uint8) * 8
+    assert torch.equal(codes[0, :16], want)
+    clean = xs.clone()
+    clean[0, :16] = 0
+    c2, s2 = laws.svdq_nvfp4_quantize(clean, g)
+    assert torch.equal(codes[0, 16:], c2[0, 16:]) and scales[0, 1].view(torch.uint8) == s2[0, 1].view(torch.uint8)
+    assert torch.isnan(laws.svdq_nvfp4_input_scale(xs, torch.ones(32))).all()
