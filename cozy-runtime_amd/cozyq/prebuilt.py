@@ -15,6 +15,7 @@ from dataclasses import dataclass, field
 from typing import Any
 
 from cozyq import _lib
+from cozyq._admit import ALIGN, EXTENT, KIND, LAYOUT, ROWS, Operand, Placement, admit, every, off_card
 
 Tensor = Any
 Dtype = Any
@@ -22,8 +23,6 @@ Dtype = Any
 #: The one tensor-core family this library carries (the reference's `FAMILIES`,
 #: `_kernels/__init__.py`): CDNA4's MFMA on gfx950.
 FAMILIES = ("mfma.cdna4",)
-#: How many checked weights `Prebuilt` remembers (`internal/prebuilt.py:75`).
-CHECKED = 4096
 #: Rows the fused fp8 linear takes in one launch (`cozyq_fp8_linear`); more rows quantize once
 #: and run the GEMM.
 FP8_SMALL_ROWS = 4
@@ -110,40 +109,54 @@ class Prebuilt:
     index: int
     family: str = FAMILIES[0]
     _lib: Any = field(init=False)
-    _checked: set[tuple[object, ...]] = field(init=False, default_factory=set)
+    #: 16-bit dtype -> whether it is fp16 (the kernels' `half` flag).
+    _halves: dict[Any, bool] = field(init=False, default_factory=dict)
     #: The fused linear's counters, one zeroed int32 buffer per stream (each call leaves its
     #: buffer zero; calls on one stream run in order, so they share it).
     _workspaces: dict[int, Tensor] = field(init=False, default_factory=dict)
 
     def __post_init__(self) -> None:
         self._lib = _lib.load()
+        self._halves = {self.torch.bfloat16: False, self.torch.float16: True}
 
     # ------------------------------------------------------------------ reference surface
 
     def int8_linear(
         self, x: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None, out_dtype: Dtype
     ) -> Tensor:
-        """`x @ W.T + bias` for an int8.convrot weight (`internal/prebuilt.py:99-117`): the GEMV
-        for up to `GEMV_ROWS` rows where it serves, else quantize + GEMM."""
+        """`x @ W.T + bias` for an int8.convrot weight (`internal/prebuilt.py:99-117`): the
+        one-launch GEMV where it takes the rows (`_gemv`), else quantize + GEMM. (Two launches
+        also beat the fused one, `int8_linear_rot`, on MI355X: its quantize jobs run at one wave a
+        SIMD beside the GEMM's full register file.)"""
         flat = self._rows(INT8, x)
-        rows, width = flat.shape
-        bias = self._weight(INT8, data, scale, bias, width, out_dtype)
+        bias = self._weight(INT8, data, scale, bias, flat.shape[1], out_dtype)
         scale = _aligned(scale)
         shape = (*x.shape[:-1], data.shape[0])
-        if rows <= self._lib.cozyq_gemv_rows():
-            out = self.torch.empty(shape, dtype=out_dtype, device=x.device)
-            code = 0 if rows == 0 else self._lib.cozyq_gemv(
-                self.index, flat.data_ptr(), self._half(flat.dtype), data.data_ptr(),
-                scale.data_ptr(), _ptr(bias), out.data_ptr(), self._half(out_dtype), rows,
-                data.shape[0], width, self._stream(),
-            )  # fmt: skip
-            if code != self._lib.cozyq_not_supported():
-                self._check(code, "the GEMV")
-                return out
-        # Quantize, then GEMM: on MI355X two launches beat the fused one (`int8_linear_rot`),
-        # whose quantize jobs run at one wave a SIMD beside the GEMM's full register file.
+        served = self._gemv(flat, data, scale, bias, out_dtype, shape)
+        if served is not None:
+            return served
         q, scales = self.int8_quantize(flat)
         return self.int8_gemm(q, scales, data, scale, bias, out_dtype).view(shape)
+
+    def _gemv(self, flat: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None,
+              out_dtype: Dtype, shape: tuple[int, ...]) -> Tensor | None:  # fmt: skip
+        """The whole int8 linear of up to `GEMV_ROWS` checked rows in one launch
+        (`cozyq_gemv`), or None where it declines (more rows, or rows too wide for it)."""
+        rows, width = flat.shape
+        if rows > self._lib.cozyq_gemv_rows():
+            return None
+        out = self.torch.empty(shape, dtype=out_dtype, device=flat.device)
+        if rows == 0:
+            return out
+        code = self._lib.cozyq_gemv(
+            self.index, flat.data_ptr(), self._half(flat.dtype), data.data_ptr(), scale.data_ptr(),
+            _ptr(bias), out.data_ptr(), self._half(out_dtype), rows, data.shape[0], width,
+            self._stream(),
+        )  # fmt: skip
+        if code == self._lib.cozyq_not_supported():
+            return None
+        self._check(code, "the GEMV")
+        return out
 
     def _linear_fused(
         self, flat: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None, out_dtype: Dtype,
@@ -248,11 +261,7 @@ class Prebuilt:
         (config `UNPACK`, or 5 for the 256x192 tile, else the int8 GEMM's shape rule); fewer rows
         take the fused GEMM. Every config is the same law, bit for bit."""
         torch = self.torch
-        if q.dtype != torch.int8 or q.dim() != 2 or not q.is_contiguous() or q.data_ptr() % 16:
-            raise ValueError("w4a8_gemm: q must be a contiguous, aligned int8 [M, K]")
-        rows, width = q.shape
-        if scales.dtype != torch.float32 or scales.numel() != rows or not scales.is_contiguous():
-            raise ValueError(f"w4a8_gemm: scales must be contiguous float32 with {rows} values")
+        rows, width = self._operand("w4a8_gemm", torch.int8, q, scales)
         bias = self._w4a8_weight(w, bias, width, out_dtype)
         n = w.codes.shape[0]
         if config in WIDE_TILES or (config < 0 and rows >= UNPACK_ROWS):
@@ -289,30 +298,31 @@ class Prebuilt:
         return levels
 
     def _w4a8_weight(self, w: W4a8, bias: Tensor | None, width: int, out_dtype: Dtype) -> Tensor | None:
-        """`internal/prebuilt.py:224-251`."""
+        """Contract V5 (`internal/prebuilt.py:224-251`): the w4a8 weight's tensors, and `bias`
+        in the output dtype."""
         torch = self.torch
-        n = w.codes.shape[0]
-        shapes = ((w.codes, (n, width // 2)), (w.group_scale, (n, width // 16)), (w.scale, (n,)))
-        if any(tuple(t.shape) != shape or not t.is_contiguous() for t, shape in shapes):
-            raise ValueError(f"w4a8: codes, group scales and scale must be [{n}, {width // 2}], "
-                             f"[{n}, {width // 16}] and [{n}], contiguous")  # fmt: skip
-        if w.codes.element_size() != 1 or w.group_scale.dtype != torch.float8_e4m3fn:
-            raise ValueError("w4a8: codes are bytes and group scales E4M3")
-        if w.scale.dtype != torch.float32 or n % 8 or w.codes.data_ptr() % 16:
-            raise ValueError("w4a8: scale is float32, N a multiple of 8, codes 16-byte aligned")
-        if w.group_scale.data_ptr() % 4:
-            raise ValueError("w4a8: group scales must be 4-byte aligned")
-        if w.codebook is not None and (w.codebook.dtype != torch.float32 or w.codebook.numel() != 16):
-            raise ValueError("w4a8: the codebook is 16 float32 levels")
-        on = [t for t in (w.codes, w.group_scale, w.scale, w.codebook, bias) if t is not None]
-        if any(not t.is_cuda or t.get_device() != self.index for t in on):
+        n = int(w.codes.shape[0])
+        shapes = (f"w4a8: codes, group scales and scale must be [{n}, {width // 2}], "
+                  f"[{n}, {width // 16}] and [{n}], contiguous")  # fmt: skip
+        kinds = "w4a8: codes are bytes and group scales E4M3"
+        packing = "w4a8: scale is float32, N a multiple of 8, codes 16-byte aligned"
+        admit(
+            (w.codes, Operand(itemsize=1, extents=(n, width // 2), dense=True, align=16, rows=8),
+             {**every(shapes, EXTENT, LAYOUT), KIND: kinds, **every(packing, ALIGN, ROWS)}),
+            (w.group_scale, Operand(kinds=(torch.float8_e4m3fn,), extents=(n, width // 16), dense=True, align=4),
+             {**every(shapes, EXTENT, LAYOUT), KIND: kinds, ALIGN: "w4a8: group scales must be 4-byte aligned"}),
+            (w.scale, Operand(kinds=(torch.float32,), extents=(n,), dense=True),
+             {**every(shapes, EXTENT, LAYOUT), KIND: packing}),
+        )  # fmt: skip
+        if w.codebook is not None:
+            admit((w.codebook, Operand(kinds=(torch.float32,), count=16),
+                   every("w4a8: the codebook is 16 float32 levels", KIND, EXTENT)))  # fmt: skip
+        if off_card(self.index, w.codes, w.group_scale, w.scale, w.codebook, bias):
             raise ValueError(f"w4a8: the weight's tensors must be on cuda:{self.index}")
         self._half(out_dtype)
-        if bias is None:
-            return None
-        if bias.numel() != n:
+        if bias is not None and bias.numel() != n:
             raise ValueError(f"w4a8: bias must have {n} values")
-        return bias.to(out_dtype).contiguous()
+        return None if bias is None else bias.to(out_dtype).contiguous()
 
     def int8_gemm(
         self, q: Tensor, scales: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None,
@@ -404,7 +414,7 @@ class Prebuilt:
             raise ValueError("mx_gemm: N must be a multiple of 8")
         self._half(out_dtype)
         bias = None if bias is None else bias.to(out_dtype).contiguous()
-        direct = out is not None and _writable(out, rows, n, out_dtype, q.device)
+        direct = out is not None and Placement(rows, n, out_dtype, q.device).takes(out)
         result = out if direct else torch.empty(rows, n, dtype=out_dtype, device=q.device)
         if rows == 0:
             return _landed(result, out)
@@ -705,16 +715,21 @@ class Prebuilt:
         `activation(norm(x)·(1 + scale) + shift)` folded in. A gated row (SiTU, or SwiGLU
         without `up`) quantizes to half its width."""
         torch = self.torch
+        # Contract V6: which prologues a call may combine.
         gated = activation == SITU or (activation == SWIGLU and up is None)
-        flat = self._rows(f, x, x.shape[-1] // 2 if gated else x.shape[-1])
-        rows, width = flat.shape[0], flat.shape[1] // 2 if gated else flat.shape[1]
-        if gated and (x.shape[-1] % 2 or norm or scale is not None or shift is not None):
-            raise ValueError(f"{f.name}_quantize: a gated activation takes [hidden | gate] rows alone")
-        if up is not None and (
-            activation != SWIGLU or up.shape != x.shape or up.dtype != x.dtype or norm
-            or scale is not None or shift is not None
-        ):
-            raise ValueError(f"{f.name}_quantize: SwiGLU takes gate and up rows of one shape alone")
+        width = x.shape[-1] // 2 if gated else x.shape[-1]
+        flat = self._rows(f, x, width)
+        rows = flat.shape[0]
+        plain = not norm and scale is None and shift is None
+        refusals = (
+            (gated and (x.shape[-1] % 2 or not plain),
+             f"{f.name}_quantize: a gated activation takes [hidden | gate] rows alone"),
+            (up is not None and (activation != SWIGLU or up.shape != x.shape or up.dtype != x.dtype or not plain),
+             f"{f.name}_quantize: SwiGLU takes gate and up rows of one shape alone"),
+        )  # fmt: skip
+        for refused, text in refusals:
+            if refused:
+                raise ValueError(text)
         other = None if up is None else self._rows(f, up)
         q = torch.empty(rows, width, dtype=torch.float8_e4m3fn if f.fp8 else torch.int8,
                         device=x.device)  # fmt: skip
@@ -752,18 +767,13 @@ class Prebuilt:
         """`internal/prebuilt.py:293-358`: `[M, N]` into `out` where given, written in place when
         its rows sit 16-byte multiples apart, else copied into it."""
         torch = self.torch
-        want = torch.float8_e4m3fn if f.fp8 else torch.int8
-        if q.dtype != want or q.dim() != 2 or not q.is_contiguous() or q.data_ptr() % 16:
-            raise ValueError(f"{f.name}_gemm: q must be a contiguous, aligned {want} [M, K]")
-        rows, width = q.shape
-        if scales.dtype != torch.float32 or scales.numel() != rows or not scales.is_contiguous():
-            raise ValueError(f"{f.name}_gemm: scales must be contiguous float32 with {rows} values")
+        rows, width = self._operand(f"{f.name}_gemm", torch.float8_e4m3fn if f.fp8 else torch.int8, q, scales)
         if width % f.multiple:
             raise ValueError(f"{f.name}_gemm: K must be a multiple of {f.multiple}, not {width}")
         bias = self._weight(f, data, scale, bias, width, out_dtype)
         scale = _aligned(scale)
         n = data.shape[0]
-        direct = out is not None and _writable(out, rows, n, out_dtype, q.device)
+        direct = out is not None and Placement(rows, n, out_dtype, q.device).takes(out)
         result = out if direct and out is not None else torch.empty(
             rows, n, dtype=out_dtype, device=q.device)
         if rows == 0:
@@ -786,48 +796,48 @@ class Prebuilt:
         self._check(code, "the GEMM")
         return _landed(result, out)
 
+    def _operand(self, op: str, code: Dtype, q: Tensor, scales: Tensor) -> tuple[int, int]:
+        """Contract V3: a quantized operand, codes `q` [M, K] and float32 row scales; (M, K)."""
+        admit((q, Operand(kinds=(code,), extents=(None, None), dense=True, align=16),
+               every(f"{op}: q must be a contiguous, aligned {code} [M, K]")))  # fmt: skip
+        rows, width = (int(d) for d in q.shape)
+        admit((scales, Operand(kinds=(self.torch.float32,), count=rows, dense=True),
+               every(f"{op}: scales must be contiguous float32 with {rows} values")))  # fmt: skip
+        return rows, width
+
     def _rows(self, f: _Format, x: Tensor, width: int | None = None) -> Tensor:
-        """`internal/prebuilt.py:360-370`: contiguous, 16-byte aligned rows on this card."""
-        width = x.shape[-1] if width is None else width
-        if not x.is_cuda or x.get_device() != self.index:
+        """Contract V1 (`internal/prebuilt.py:360-370`): x on this card, each row quantizing to
+        `width` elements (x's last extent unless given) that the kernels take; the rows as one
+        contiguous matrix at a 16-byte address."""
+        width = int(x.shape[-1] if width is None else width)
+        limit = int(self._lib.cozyq_max_k())
+        if off_card(self.index, x):
             raise ValueError(f"{f.name}: x must be on cuda:{self.index}")
-        if width % f.multiple or width > self._lib.cozyq_max_k():
-            raise ValueError(f"{f.name}: K must be a multiple of {f.multiple} up to "
-                             f"{self._lib.cozyq_max_k()}, not {width}")  # fmt: skip
-        flat = x.reshape(-1, x.shape[-1]).contiguous()
-        return flat if flat.data_ptr() % 16 == 0 else flat.clone()
+        if width > limit or width % f.multiple:
+            raise ValueError(f"{f.name}: K must be a multiple of {f.multiple} up to {limit}, not {width}")
+        return _aligned(x.reshape(-1, x.shape[-1]))
 
     def _weight(
         self, f: _Format, data: Tensor, scale: Tensor, bias: Tensor | None, width: int,
         out_dtype: Dtype,
     ) -> Tensor | None:
-        """`internal/prebuilt.py:372-406`."""
-        key = (data.dtype, scale.dtype, data.data_ptr(), scale.data_ptr(), *data.shape, width,
-               out_dtype)  # fmt: skip
-        if bias is None and key in self._checked and data.is_contiguous():
-            return None
+        """Contract V2 (`internal/prebuilt.py:372-406`): an 8-bit weight (codes [N, width] and
+        float32 row scales) on this card, a 16-bit output dtype, and `bias` in it."""
         torch = self.torch
-        want = torch.float8_e4m3fn if f.fp8 else torch.int8
-        if data.dtype != want or data.dim() != 2 or data.shape[1] != width:
-            raise ValueError(f"{f.name}: data must be {want} [N, {width}]")
-        if not data.is_contiguous() or data.data_ptr() % 16 or data.shape[0] % 8:
-            raise ValueError(f"{f.name}: data must be contiguous, aligned, N a multiple of 8")
-        if scale.dtype != torch.float32 or scale.numel() != data.shape[0]:
-            raise ValueError(f"{f.name}: scale must be float32 with {data.shape[0]} values")
-        if not scale.is_contiguous():
-            raise ValueError(f"{f.name}: scale must be contiguous")
-        on = (data, scale) if bias is None else (data, scale, bias)
-        if any(t.get_device() != self.index for t in on):
+        code = torch.float8_e4m3fn if f.fp8 else torch.int8
+        admit((data, Operand(kinds=(code,), extents=(None, width), dense=True, align=16, rows=8),
+               {**every(f"{f.name}: data must be {code} [N, {width}]", KIND, EXTENT),
+                **every(f"{f.name}: data must be contiguous, aligned, N a multiple of 8", LAYOUT, ALIGN, ROWS)}))
+        n = int(data.shape[0])
+        admit((scale, Operand(kinds=(torch.float32,), count=n, dense=True),
+               {**every(f"{f.name}: scale must be float32 with {n} values", KIND, EXTENT),
+                LAYOUT: f"{f.name}: scale must be contiguous"}))  # fmt: skip
+        if off_card(self.index, data, scale, bias):
             raise ValueError(f"{f.name}: the weight's tensors must be on cuda:{self.index}")
         self._half(out_dtype)
-        if bias is None:
-            if len(self._checked) >= CHECKED:
-                self._checked.clear()
-            self._checked.add(key)
-            return None
-        if bias.numel() != data.shape[0]:
-            raise ValueError(f"{f.name}: bias must have {data.shape[0]} values")
-        return _aligned(bias.to(out_dtype))
+        if bias is not None and bias.numel() != n:
+            raise ValueError(f"{f.name}: bias must have {n} values")
+        return None if bias is None else _aligned(bias.to(out_dtype))
 
     # -------------------------------------------------------------- LoRA bake
 
@@ -992,12 +1002,16 @@ class Prebuilt:
         return rank
 
     def _half(self, dtype: Dtype) -> bool:
-        if dtype not in (self.torch.bfloat16, self.torch.float16):
+        """Contract V4: the kernels' flag for a 16-bit activation or output dtype (fp16 True,
+        bf16 False); any other dtype raises."""
+        half = self._halves.get(dtype)
+        if half is None:
             raise ValueError(f"8-bit linear: activations and outputs are bf16 or fp16, not {dtype}")
-        return bool(dtype == self.torch.float16)
+        return half
 
     def _stream(self) -> int:
-        return int(self.torch._C._cuda_getCurrentRawStream(self.index))
+        """The raw handle of torch's current stream on this card, which every launch uses."""
+        return int(self.torch.cuda.current_stream(self.index).cuda_stream)
 
     def _check(self, code: int, what: str) -> None:
         """`internal/prebuilt.py:428-434`."""
@@ -1012,19 +1026,6 @@ class Prebuilt:
 def _out_type(torch: Any, dtype: Dtype) -> int:
     """The decode kernels' destination code: 0 f32, 1 bf16, 2 f16."""
     return {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[dtype]
-
-
-def _writable(out: Tensor, rows: int, n: int, dtype: Dtype, device: Any) -> bool:
-    """`internal/prebuilt.py:449-460`."""
-    return (
-        out.dtype == dtype
-        and out.device == device
-        and tuple(out.shape) == (rows, n)
-        and out.stride(1) == 1
-        and out.stride(0) >= n
-        and out.stride(0) * out.element_size() % 16 == 0
-        and out.data_ptr() % 16 == 0
-    )
 
 
 def _landed(result: Tensor, out: Tensor | None) -> Tensor:

@@ -39,31 +39,47 @@ NATIVE = "cozyq-svdq-nvfp4-mfma"
 
 
 def rank(r: int) -> int:
-    """The built rank a branch of rank `r` is padded to (`internal/svdq_linear.py:266-271`)."""
-    for built in RANKS:
-        if r <= built:
-            return built
-    raise ValueError(f"a low-rank branch of rank {r} exceeds the kernels' {RANKS[-1]}")
+    """Contract R1: the least built rank that holds `r` ranks (`internal/svdq_linear.py:266-271`);
+    a branch past the largest raises ValueError."""
+    fits = [built for built in RANKS if built >= r]
+    if not fits:
+        raise ValueError(f"a low-rank branch of rank {r} exceeds the kernels' {RANKS[-1]}")
+    return fits[0]
+
+
+def _branch(torch: Any, parts: list[tuple[Tensor, Tensor]]) -> tuple[Tensor, Tensor]:
+    """The factors (down [r_i, K], up [N, r_i]) laid end to end in one bf16 branch of the least
+    built rank that holds them all, the ranks past their sum zero (they add nothing to
+    `la·upᵀ`): each factor is copied into its slice of a zeroed buffer, rounded to bf16 on the way."""
+    total = sum(int(d.shape[0]) for d, _ in parts)
+    width = rank(total)
+    first_down, first_up = parts[0]
+    down = torch.zeros(width, first_down.shape[1], dtype=torch.bfloat16, device=first_down.device)
+    up = torch.zeros(first_up.shape[0], width, dtype=torch.bfloat16, device=first_up.device)
+    at = 0
+    for d, u in parts:
+        r = int(d.shape[0])
+        down[at:at + r].copy_(d)
+        up[:, at:at + r].copy_(u)
+        at += r
+    return down, up
 
 
 def padded(torch: Any, down: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
-    """A branch `(down [r, K], up [N, r])` in bf16 with zero rows (columns) up to its built rank
-    (`internal/svdq_linear.py:274-283`): the zeros add nothing to `la·upᵀ`."""
-    r, wide = int(down.shape[0]), rank(int(down.shape[0]))
-    down = torch.cat([down.to(torch.bfloat16), down.new_zeros(wide - r, down.shape[1], dtype=torch.bfloat16)])
-    up = torch.cat([up.to(torch.bfloat16), up.new_zeros(up.shape[0], wide - r, dtype=torch.bfloat16)], 1)
-    return down.contiguous(), up.contiguous()
+    """Contract R2 (`internal/svdq_linear.py:274-283`): a branch `(down [r, K], up [N, r])` as
+    contiguous bf16 of rank `rank(r)`, zero past r."""
+    return _branch(torch, [(down, up)])
 
 
 def merged(torch: Any, roles: Mapping[str, Tensor], down: Tensor, up: Tensor) -> dict[str, Tensor] | None:
-    """The low-rank roles with a LoRA's factors as more ranks (`internal/svdq_linear.py:286-299`):
-    `x·downᵀ·upᵀ` gains `x·Aᵀ·(s·B)ᵀ` with no rounding of the weight. None when the ranks
-    together exceed the kernels' largest; the caller then adds the LoRA's term itself."""
-    if int(roles["lowrank_down"].shape[0]) + int(down.shape[0]) > RANKS[-1]:
+    """Contract R3 (`internal/svdq_linear.py:286-299`): the low-rank roles with a LoRA's
+    factors appended as more ranks, so `x·downᵀ·upᵀ` gains `x·Aᵀ·(s·B)ᵀ` with no rounding of
+    the weight; None when the ranks together pass the kernels' largest (the caller then adds the
+    LoRA's term itself)."""
+    own_down, own_up = roles["lowrank_down"], roles["lowrank_up"]
+    if int(own_down.shape[0]) + int(down.shape[0]) > RANKS[-1]:
         return None
-    both = torch.cat([roles["lowrank_down"], down.to(torch.bfloat16)])
-    wide = torch.cat([roles["lowrank_up"], up.to(torch.bfloat16)], dim=1)
-    both, wide = padded(torch, both, wide)
+    both, wide = _branch(torch, [(own_down, own_up), (down, up)])
     return {"lowrank_down": both, "lowrank_up": wide}
 
 
