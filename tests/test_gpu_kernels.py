@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+from fullsize import checksums_exact, tile_rows
 from oracle import laws
 
 pytestmark = pytest.mark.gpu
@@ -820,8 +821,8 @@ def test_c3_decode_shapes_within_tolerance(ops, c3_weight, m):
 
 def test_c3_full_size_fp8_codes_and_sampled_rows(ops):
     """BASELINE config 3 at M=4096 (K=4096, N=14336): every e4m3 code and scale of the
-    activation bit-exact, and 48 sampled output rows within tolerance of the float64 product;
-    the whole output finite."""
+    activation bit-exact, and 2 rows of every M-tile (32, each against every column) within
+    tolerance of the float64 product; the whole output finite."""
     m, k, n = 4096, 4096, 14336
     x = activations(m, k, seed=20261203)
     data, scale = laws.fp8_weight(weights(n, k, seed=20261204))
@@ -831,7 +832,7 @@ def test_c3_full_size_fp8_codes_and_sampled_rows(ops):
     assert torch.equal(q.cpu().view(torch.uint8), wq.view(torch.uint8))
     assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
     out = ops.fp8_gemm(q, s, data.to(DEV), scale.to(DEV), bias.to(DEV), torch.bfloat16)
-    rows = torch.randperm(m, generator=torch.Generator().manual_seed(8))[:48]
+    rows = tile_rows(m, 2)
     exact = (wq[rows].double() @ data.double().t()) * ws[rows].double() * scale.double().reshape(1, -1)
     assert_close(out.cpu()[rows], exact + bias.double())
     assert math.isfinite(out.float().abs().max().item())
@@ -841,8 +842,8 @@ def test_c3_full_size_fp8_codes_and_sampled_rows(ops):
                          ids=["qkv", "attn_out", "ffn_up", "ffn_down"])
 def test_c5_full_size_mx_codes_and_sampled_rows(ops, shape):
     """BASELINE config 5 at M=4096 over the DiT block's four shapes: every e4m3 code and E8M0
-    byte of the activation bit-exact, and 32 sampled output rows within tolerance of the float64
-    product of the dequantized operands."""
+    byte of the activation bit-exact, and 2 rows of every M-tile (32, each against every column)
+    within tolerance of the float64 product of the dequantized operands."""
     k, n = shape
     m = 4096
     x = activations(m, k, seed=20261205 + k)
@@ -852,16 +853,17 @@ def test_c5_full_size_mx_codes_and_sampled_rows(ops, shape):
     assert torch.equal(q.cpu().view(torch.uint8), wq.view(torch.uint8))
     assert torch.equal(qs.cpu(), wqs)
     out = ops.mx_gemm(q, qs, data.to(DEV), wbyte.to(DEV), None, torch.bfloat16)
-    rows = torch.randperm(m, generator=torch.Generator().manual_seed(9))[:32]
+    rows = tile_rows(m, 2)
     exact = laws.mx_dequantize(wq[rows], wqs[rows]).double() @ laws.mx_dequantize(data, wbyte).double().t()
     assert_close(out.cpu()[rows], exact)
     assert math.isfinite(out.float().abs().max().item())
 
 
 def test_c2_full_size_codes_and_sampled_rows(ops):
-    """BASELINE config 2 at its real shape: every code and scale bit-exact, the int32
-    accumulators of 48 sampled rows exact, and the bias + GELU outputs of those rows within
-    tolerance."""
+    """BASELINE config 2 at its real shape: every code and scale bit-exact; the whole int32
+    accumulator matrix exact by its row and column checksums (weighted and plain, int64), and 4
+    rows of every M-tile exactly; the bias + GELU outputs of those 64 rows, against every column,
+    within tolerance of the float64 law; the whole output finite."""
     m, k, n = 4096, 3072, 12288
     x = activations(m, k, seed=20261202)
     w = weights(n, k, seed=20261203)
@@ -872,9 +874,11 @@ def test_c2_full_size_codes_and_sampled_rows(ops):
     assert torch.equal(q.cpu(), wq)
     assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
     out = ops.int8_gemm_ex(q, s, data.to(DEV), scale.to(DEV), bias.to(DEV), torch.bfloat16, 1)
-    acc = ops.int8_acc(q, data.to(DEV))
-    rows = torch.randperm(m, generator=torch.Generator().manual_seed(6))[:48]
-    assert torch.equal(acc.cpu()[rows], laws.int32_gemm(wq[rows], data))
+    acc = ops.int8_acc(q, data.to(DEV)).cpu()
+    checksums_exact(acc, wq, data, seed=6)
+    rows = tile_rows(m)
+    assert len(rows) == 64
+    assert torch.equal(acc[rows], laws.int32_gemm(wq[rows], data))
     exact = laws.int32_gemm(wq[rows], data).double() * ws[rows].double() * scale.double()
     exact = laws.gelu_tanh((exact + bias.double()).float()).double()
     assert_close(out.cpu()[rows], exact)

@@ -11,6 +11,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from fullsize import tile_rows
 from oracle import laws
 
 pytestmark = pytest.mark.gpu
@@ -109,17 +110,27 @@ def test_fused_linear_declines(ops):
 
 
 def test_c2_full_size_fused_equals_two_launch(ops):
-    """BASELINE config 2 at its real shape through the fused launch: operand and bias + GELU
-    output bit-exact to the two-launch path (whose operand the full-size test holds to the law)."""
+    """BASELINE config 2 at its real shape through the fused launch: every code and scale of the
+    operand bit-exact to the CPU law; the bias + GELU outputs of 4 rows of every M-tile (each
+    against every column) within tolerance of the float64 law; and the whole output bit-exact to
+    the two-launch path's."""
     m, k, n = 4096, 3072, 12288
-    x = activations(m, k, seed=20261202).to(DEV)
+    x = activations(m, k, seed=20261202)
     data, scale = weight(n, k, 128, seed=20261203)
-    data, scale = data.to(DEV), scale.to(DEV)
-    bias = (torch.randn(n, generator=torch.Generator().manual_seed(5)) * 0.1).to(torch.bfloat16).to(DEV)
-    out, q, s = ops.int8_linear_rot(x, data, scale, bias, torch.bfloat16, 128, 1)
-    q2, s2 = ops.int8_quantize_rot(x, 128)
-    assert torch.equal(q, q2) and torch.equal(s, s2)
-    assert torch.equal(out, ops.int8_gemm_ex(q2, s2, data, scale, bias, torch.bfloat16, 1))
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(5)) * 0.1).to(torch.bfloat16)
+    dd, ds, db = data.to(DEV), scale.to(DEV), bias.to(DEV)
+    out, q, s = ops.int8_linear_rot(x.to(DEV), dd, ds, db, torch.bfloat16, 128, 1)
+    wq, ws = laws.quantize_rows_int8(x, 128)
+    assert torch.equal(q.cpu(), wq)
+    assert torch.equal(s.cpu().view(torch.int32), ws.reshape(-1).view(torch.int32))
+    rows = tile_rows(m)
+    exact = laws.int32_gemm(wq[rows], data).double() * ws[rows].double() * scale.double()
+    exact = laws.gelu_tanh((exact + bias.double()).float()).double()
+    got = out.cpu()[rows].double()
+    rms = exact.pow(2).mean().sqrt()
+    assert ((got - exact).abs() <= 1e-2 * rms + 2e-2 * exact.abs()).all()
+    q2, s2 = ops.int8_quantize_rot(x.to(DEV), 128)
+    assert torch.equal(out, ops.int8_gemm_ex(q2, s2, dd, ds, db, torch.bfloat16, 1))
 
 
 def test_fused_linear_reports_a_wait_that_gives_up(ops):
