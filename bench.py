@@ -338,12 +338,11 @@ def _graph_us(torch, launch, per_graph: int, replays: int) -> float:
     return Timer(torch).interleaved({"graph": graph.replay}, batch=batch)["graph"]["ms"] / per_graph * 1e3
 
 
-def bench_int8_decode(torch, ops, lib, stream, steps: int) -> dict:
-    """The int8.convrot linear at decode size on config 2's weight (M=1, K=3072, N=12288): the
-    fused GEMV (`cozyq_gemv`: rotation, quantization and GEMV in one launch) against the
-    two-launch path (quantize, then the narrow-tile GEMM), each over 8 rotating weight copies
-    (302 MB, beyond the MALL), graph-replayed."""
-    m, k, n, copies = 1, 3072, 12288, 8
+def _int8_decode_shape(torch, ops, lib, m: int, k: int, n: int, replays: int) -> dict:
+    """The fused int8 GEMV (`cozyq_gemv`: rotation, quantization and GEMV in one launch) against
+    the two-launch path (quantize, then the GEMM's shape rule) at one shape, each over enough
+    rotating weight copies (> 600 MB) that the 256 MB MALL cannot hold them, graph-replayed."""
+    copies = max(8, int(600e6 // (n * k)) + 1)
     x = _activations(torch, m, k, 61)
     weights = [ops.int8_quantize_rot(_weights(torch, n, k, 62 + c), 256) for c in range(copies)]
     out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
@@ -365,13 +364,24 @@ def bench_int8_decode(torch, ops, lib, stream, steps: int) -> dict:
         _check(lib.cozyq_gemm(0, 0, 0, q.data_ptr(), qs.data_ptr(), w.data_ptr(), ws.data_ptr(),
                               None, out.data_ptr(), n, 0, m, n, k, -1, None, None, raw))  # fmt: skip
 
-    replays = max(4, steps // 8)
-    us = _graph_us(torch, fused, 8 * copies, replays)
-    us_two = _graph_us(torch, two_launch, 8 * copies, replays)
+    us = _graph_us(torch, fused, 8 * copies if copies <= 8 else copies, replays)
+    us_two = _graph_us(torch, two_launch, 8 * copies if copies <= 8 else copies, replays)
     nbytes = n * k + n * 4 + m * k * 2 + m * n * 2
     return {"M": m, "K": k, "N": n, "us": us, "gbs": nbytes / (us * 1e-6) / 1e9,
             "frac_hbm": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, "us_quantize_then_gemm": us_two,
-            "kernel": "int8_decode_kernel (rotation + quantize fused with the GEMV)"}
+            "weight_copies": copies}
+
+
+def bench_int8_decode(torch, ops, lib, stream, steps: int) -> dict:
+    """The int8.convrot linear at decode size on config 2's weight (M=1, K=3072, N=12288), and
+    the GEMV's wide rows (the reference's `gemv` range, `rotate.cu:453-468`: M=1 to K=32768, M=2
+    to 16384, M=4 at an FFN-down's K=12288), each against quantize + GEMM."""
+    replays = max(4, steps // 8)
+    row = _int8_decode_shape(torch, ops, lib, 1, 3072, 12288, replays)
+    row["kernel"] = "int8_decode_kernel (rotation + quantize fused with the GEMV)"
+    row["wide_rows"] = [_int8_decode_shape(torch, ops, lib, m, k, n, replays)
+                        for m, k, n in ((1, 32768, 4096), (2, 12288, 3072), (4, 12288, 3072))]
+    return row
 
 
 def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:

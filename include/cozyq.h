@@ -65,9 +65,10 @@ int cozyq_quantize_rot(int device, const void* x, int x_half, int8_t* q, float* 
 /* The fused few-row int8 linear (reference: gemm.cpp:117-125 `gemv`, rotate.cu:351-407): each
  * row of x rotated and quantized by cozyq_quantize's int8 law inside the kernel, then
  * out = ((acc·s_x)·w_scale, cast) + bias in the output dtype, bit for bit the CPU law. Served for
- * 1 <= M <= 4 with M·K <= 16384, N % 8 == 0, x and w 16-byte aligned and out 8-byte aligned;
- * other shapes return hipErrorNotSupported and the caller quantizes + GEMMs (the reference's
- * order). K % 256 == 0. */
+ * 1 <= M <= 4 with K up to 32768 (M = 1), 16384 (M = 2) or 12288 (M = 3, 4) — the reference's
+ * range, M·K + M·(warps + 1)·4 <= 48 KiB, and more at M = 2 — N % 8 == 0, x and w 16-byte aligned
+ * and out 8-byte aligned; other shapes return hipErrorNotSupported and the caller quantizes +
+ * GEMMs (the reference's order). K % 256 == 0. */
 int cozyq_gemv(int device, const void* x, int x_half, const int8_t* w, const float* w_scale,
                const void* bias, void* out, int out_half, int M, int N, int K, void* stream);
 

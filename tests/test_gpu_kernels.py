@@ -388,14 +388,16 @@ def test_int8_linear_bit_exact(ops, shape, dtype, bias):
 
 
 GEMV_SHAPES = [(1, 256), (1, 768), (1, 3072), (1, 4096), (1, 8192), (1, 12288), (1, 16384),
-               (2, 3072), (2, 8192), (3, 1024), (3, 4096), (4, 2304), (4, 4096)]
+               (1, 24576), (1, 32768), (2, 3072), (2, 8192), (2, 12288), (2, 16384), (3, 1024),
+               (3, 4096), (3, 12288), (4, 2304), (4, 4096), (4, 8192), (4, 12288)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("shape", GEMV_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
 def test_int8_gemv_bit_exact(ops, shape, dtype):
     """The fused few-row int8 linear (`cozyq_gemv`: rotation, per-row int8 and the GEMV in one
-    launch) is served for M <= 4, M·K <= 16384, and equals the CPU law bit for bit: codes from
+    launch) is served for M <= 4 up to K = 32768 (M = 1), 16384 (M = 2) and 12288 (M = 3, 4), the
+    reference's range (`rotate.cu:453-468`) and more, and equals the CPU law bit for bit: codes from
     the rotation, exact int32 products, the epilogue's roundings. Rows include an all-zero row
     (the scale floor) and an outlier channel; N = 1032 leaves a ragged last workgroup."""
     from cozyq import _lib
@@ -422,14 +424,17 @@ def test_int8_gemv_bit_exact(ops, shape, dtype):
         assert torch.equal(out.cpu(), laws.int8_linear(x, data, scale, b, dtype))
 
 
-def test_int8_gemv_declines_wide_rows(ops):
-    """Past M·K = 16384 the GEMV answers NOT_SUPPORTED and `int8_linear` quantizes + GEMMs, as
-    the reference's caller does (`internal/prebuilt.py:99-118`): still bit-exact."""
+@pytest.mark.parametrize("shape", [(2, 16640), (3, 12544), (4, 12544)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_int8_gemv_declines_wide_rows(ops, shape):
+    """Past its widest rows (K > 16384 at M = 2, > 12288 at M = 3 and 4) the GEMV answers
+    NOT_SUPPORTED and `int8_linear` quantizes + GEMMs, as the reference's caller does
+    (`internal/prebuilt.py:99-118`): still bit-exact."""
     from cozyq import _lib
 
     lib = _lib.load()
-    m, n, k = 2, 264, 12288
-    gen = torch.Generator().manual_seed(5)
+    m, k = shape
+    n = 264
+    gen = torch.Generator().manual_seed(5 + k)
     data = torch.randint(-127, 128, (n, k), generator=gen, dtype=torch.int8)
     scale = (torch.randn(n, generator=gen).abs() + 0.5) * 1e-3
     x = torch.randn(m, k, generator=gen).to(torch.bfloat16)
