@@ -250,8 +250,9 @@ def bench_c1(torch, ops, lib, stream) -> dict:
 
 
 def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -> dict:
-    """Config 3 at decode size: the fused fp8 linear (quantize + GEMV, one launch), 8 rotating
-    weight copies (470 MB, beyond the 256 MB MALL). A decode step is a few microseconds of GPU
+    """Config 3 at decode size: the fused fp8 linear (quantize + product in one launch: the GEMV
+    to 4 rows, the row-tile kernel to 16), 8 rotating weight copies (470 MB, beyond the 256 MB
+    MALL). A decode step is a few microseconds of GPU
     work, less than a Python-issued launch costs on the host, so the launches are captured
     once into a HIP graph (64 of them, 8 per copy) and the graph is replayed: `us` is GPU time
     per linear. `us_eager` is the same launches issued one by one from Python. The graph's
@@ -264,15 +265,16 @@ def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -
     xp, op = x.data_ptr(), out.data_ptr()
     turn = [0]
 
-    # Up to 4 rows: one fused launch. More: quantize once, then the (narrow-tile) GEMM, the path
-    # `Prebuilt.fp8_linear` takes.
+    # Up to 16 rows: one fused launch (the GEMV to 4 rows, the row-tile kernel to 16). More
+    # (or `two_launch`): quantize once, then the (narrow-tile) GEMM, the path
+    # `Prebuilt.fp8_linear` takes past the fused kernels.
     q = torch.empty(m, k, dtype=torch.uint8, device="cuda")
     qs = torch.empty(m, dtype=torch.float32, device="cuda")
 
-    def launch(raw_stream):
+    def launch(raw_stream, fused=m <= 16):
         wp, sp = ptrs[turn[0] % copies]
         turn[0] += 1
-        if m <= 4:
+        if fused:
             _check(lib.cozyq_fp8_linear(0, xp, 0, wp, sp, None, op, 0, m, n, k, raw_stream))
             return
         _check(lib.cozyq_quantize(0, 1, xp, 0, q.data_ptr(), qs.data_ptr(), m, k, None, None, 0,
@@ -309,13 +311,19 @@ def bench_decode(torch, ops, lib, stream, steps: int, warmup: int, m: int = 1) -
         raise RuntimeError("decode: the graph replay differs from the eager launch")
     nbytes = n * k + n * 4 + m * k * 2 + m * n * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"M": m, "K": k, "N": n, "us": ms * 1e3, "us_eager": eager_ms * 1e3, "bytes": nbytes,
-            "gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
-            "traffic": (pmc_traffic("decode", "void fp8_decode_kernel") or {}).get("total"),
-            "weight_copies": copies,
-            "timing": "HIP graph of 64 launches, replayed; median of 15 samples of 2 replays",
-            "kernel": "fp8_decode_kernel (quantize fused with the GEMV)" if m <= 4 else
-                      "rowwise_quantize_kernel<fp8> + fp8_narrow_kernel"}
+    row = {"M": m, "K": k, "N": n, "us": ms * 1e3, "us_eager": eager_ms * 1e3, "bytes": nbytes,
+           "gbs": gbs, "frac": gbs / PEAK_HBM_GBS, "weight_copies": copies,
+           "timing": "HIP graph of 64 launches, replayed; median of 15 samples of 2 replays"}
+    if m <= 4:
+        row["traffic"] = (pmc_traffic("decode", "void fp8_decode_kernel") or {}).get("total")
+        row["kernel"] = "fp8_decode_kernel (quantize fused with the GEMV)"
+    else:
+        row["traffic"] = (pmc_traffic("fp8", "void fp8_rows_kernel") or {}).get("total")
+        row["kernel"] = "fp8_rows_kernel (quantize fused with the row-tile product)"
+        # The same graph-replayed timing of the two-launch path (quantize + narrow GEMM).
+        row["us_quantize_then_gemm"] = _graph_us(
+            torch, lambda raw: launch(raw, fused=False), 8 * copies, max(4, steps // 8))
+    return row
 
 
 def _graph_us(torch, launch, per_graph: int, replays: int) -> float:
@@ -388,17 +396,28 @@ def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
     """The w4a8.convrot GEMM on config 2's weight shape (K=3072, N=12288; 4-bit codes + E4M3
     group scales, 21.2 MB against int8's 37.7 MB) at M = 1 (the GEMV form), 16, 256 (the fused
     GEMM, codes unpacked in registers) and 4096 (unpack once + the 256x256 int8 GEMM),
-    int8.convrot's operand precomputed; bias + bf16 out; one weight, reused across calls."""
+    int8.convrot's operand precomputed; bias + bf16 out; 14 rotating weight copies (297 MB,
+    beyond the 256 MB MALL), one per call."""
     from cozyq import prebuilt
 
-    k, n = 3072, 12288
+    k, n, copies = 3072, 12288, 14
     gen = torch.Generator(device="cuda").manual_seed(91)
-    codes = torch.randint(0, 256, (n, k // 2), generator=gen, device="cuda", dtype=torch.uint8)
-    gs = (torch.randn(n, k // 16, generator=gen, device="cuda").abs() * 40 + 16).clamp(max=440)
-    w = prebuilt.W4a8(codes, gs.to(torch.float8_e4m3fn),
-                      (torch.rand(n, generator=gen, device="cuda") + 0.5) * 1e-3, None)  # fmt: skip
+    weights = []
+    for _ in range(copies):
+        codes = torch.randint(0, 256, (n, k // 2), generator=gen, device="cuda", dtype=torch.uint8)
+        gs = (torch.randn(n, k // 16, generator=gen, device="cuda").abs() * 40 + 16).clamp(max=440)
+        weights.append(prebuilt.W4a8(codes, gs.to(torch.float8_e4m3fn),
+                                     (torch.rand(n, generator=gen, device="cuda") + 0.5) * 1e-3,
+                                     None))  # fmt: skip
     bias = torch.randn(n, generator=gen, device="cuda").to(torch.bfloat16)
     levels = torch.empty(n, k, dtype=torch.int8, device="cuda")
+    turn = [0]
+
+    def next_weight():
+        w = weights[turn[0] % copies]
+        turn[0] += 1
+        return w
+
     rows = []
     for m in (1, 16, 256, 4096):
         q, s = ops.int8_quantize(_activations(torch, m, k, 92))
@@ -406,12 +425,14 @@ def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
         args = (q.data_ptr(), s.data_ptr())
 
         def fused(st=stream):
-            _check(lib.cozyq_w4a8_gemm(0, *args, codes.data_ptr(), w.group_scale.data_ptr(), None,
-                                       w.scale.data_ptr(), bias.data_ptr(), out.data_ptr(), 0, m, n,
-                                       k, -1, st))  # fmt: skip
+            w = next_weight()
+            _check(lib.cozyq_w4a8_gemm(0, *args, w.codes.data_ptr(), w.group_scale.data_ptr(),
+                                       None, w.scale.data_ptr(), bias.data_ptr(), out.data_ptr(),
+                                       0, m, n, k, -1, st))  # fmt: skip
 
         def unpacked():
-            _check(lib.cozyq_w4a8_unpack(0, codes.data_ptr(), w.group_scale.data_ptr(), None,
+            w = next_weight()
+            _check(lib.cozyq_w4a8_unpack(0, w.codes.data_ptr(), w.group_scale.data_ptr(), None,
                                          levels.data_ptr(), n, k, stream))  # fmt: skip
             _check(lib.cozyq_gemm(0, 0, 0, *args, levels.data_ptr(), w.scale.data_ptr(),
                                   bias.data_ptr(), out.data_ptr(), n, 0, m, n, k, -1, None, None,
@@ -420,7 +441,7 @@ def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
         # Few rows: a HIP graph of launches, replayed (back-to-back launches from Python would
         # time the host's launch rate, not the kernel).
         if m < prebuilt.UNPACK_ROWS:
-            ms = _graph_us(torch, fused, 32, steps) * 1e-3
+            ms = _graph_us(torch, fused, 2 * copies, steps) * 1e-3
         else:
             ms = Timer(torch).run(unpacked, steps, 5)
         weight_bytes = n * k // 2 + n * k // 16 + n * 4
@@ -428,20 +449,26 @@ def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
                      "weight_gbs": weight_bytes / (ms * 1e-3) / 1e9,
                      "path": ("GEMV (w4a8_decode_kernel)" if m <= 4 else "fused narrow GEMM")
                      if m < prebuilt.UNPACK_ROWS else "unpack + int8 GEMM"})
-    return {"K": k, "N": n, "rows": rows}
+    return {"K": k, "N": n, "rows": rows, "weight_copies": copies}
 
 
 def bench_fp8(torch, ops, lib, stream, m: int, steps: int) -> dict:
-    k, n = 4096, 14336
+    """Config 3's fp8 linear at M rows (K=4096, N=14336; per-token E4M3 activations, per-channel
+    E4M3 weight) over 6 rotating weight copies (352 MB, beyond the 256 MB MALL), one per call:
+    `us` the GEMM alone, `step_us` quantize + GEMM."""
+    k, n, copies = 4096, 14336, 6
     x = _activations(torch, m, k, 33)
-    data, scale = ops.fp8_quantize(_weights(torch, n, k, 34))
+    weights = [ops.fp8_quantize(_weights(torch, n, k, 34 + c)) for c in range(copies)]
     q, s = ops.fp8_quantize(x)
     out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-    args = (q.data_ptr(), s.data_ptr(), data.data_ptr(), scale.data_ptr())
+    turn = [0]
 
     def gemm():
-        _check(lib.cozyq_gemm(0, 0, 1, *args, None, out.data_ptr(), n, 0, m, n, k, -1, None, None,
-                              stream))  # fmt: skip
+        data, scale = weights[turn[0] % copies]
+        turn[0] += 1
+        _check(lib.cozyq_gemm(0, 0, 1, q.data_ptr(), s.data_ptr(), data.data_ptr(),
+                              scale.data_ptr(), None, out.data_ptr(), n, 0, m, n, k, -1, None,
+                              None, stream))  # fmt: skip
 
     def step():
         _check(lib.cozyq_quantize(0, 1, x.data_ptr(), 0, q.data_ptr(), s.data_ptr(), m, k, None,
@@ -453,7 +480,7 @@ def bench_fp8(torch, ops, lib, stream, m: int, steps: int) -> dict:
     ms = med["gemm"]["ms"]
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     return {"M": m, "us": ms * 1e3, "step_us": med["step"]["ms"] * 1e3, "tflops": tflops,
-            "frac_mfma": tflops / PEAK_FP8_TFLOPS}
+            "frac_mfma": tflops / PEAK_FP8_TFLOPS, "weight_copies": copies}
 
 
 def bench_mx(torch, ops, lib, stream, steps: int) -> dict:

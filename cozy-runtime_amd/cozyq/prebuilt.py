@@ -23,9 +23,10 @@ Dtype = Any
 #: The one tensor-core family this library carries (the reference's `FAMILIES`,
 #: `_kernels/__init__.py`): CDNA4's MFMA on gfx950.
 FAMILIES = ("mfma.cdna4",)
-#: Rows the fused fp8 linear takes in one launch (`cozyq_fp8_linear`); more rows quantize once
-#: and run the GEMM.
-FP8_SMALL_ROWS = 4
+#: Rows the fused fp8 linear may take in one launch (`cozyq_fp8_linear`: up to 4 rows the GEMV,
+#: 5 to 16 with K <= 4096 the row-tile kernel; it answers NOT_SUPPORTED past that); more rows
+#: quantize once and run the GEMM.
+FP8_SMALL_ROWS = 16
 #: The svdq low-rank ranks the kernels take.
 RANKS = (16, 32, 64)
 #: int4 SVDQuant K-group.
@@ -217,7 +218,8 @@ class Prebuilt:
         self, x: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None, out_dtype: Dtype
     ) -> Tensor:
         """`x @ W.T + bias` for an fp8.rowwise weight (`internal/prebuilt.py:119-124`). Up to
-        `FP8_SMALL_ROWS` rows run as one fused launch (quantize + GEMV), more as two."""
+        `FP8_SMALL_ROWS` rows run as one fused launch (quantize + product) where the library takes
+        the shape, the rest as two."""
         flat = self._rows(FP8, x)
         rows, width = flat.shape
         shape = (*x.shape[:-1], data.shape[0])

@@ -231,4 +231,24 @@ __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// ------------------------------------------------------------------ waits and LDS-DMA
+// LDS pointers for buffer_load ... lds (the LDS-DMA loads: 64 lanes x 16 bytes land contiguous
+// at the uniform base the pointer gives, lane l at +16l).
+typedef __attribute__((address_space(3))) void LdsPtr;
+
+// s_waitcnt with only vmcnt <= N (expcnt and lgkmcnt left unconstrained): gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// s_waitcnt lgkmcnt(0) alone.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));
+}
+
+// Keeps the compiler from moving memory operations across the waits and barriers around it.
+__device__ __forceinline__ void fence() { asm volatile("" ::: "memory"); }
+
 }  // namespace cozyq

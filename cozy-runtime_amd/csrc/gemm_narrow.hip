@@ -267,15 +267,6 @@ __global__ __launch_bounds__(kThreads) void narrow_kernel(
 // narrow_kernel): at few rows each workgroup streams its weight rows at the latency of a step,
 // and that depth is what fills HBM. Per step a wave issues kTM/32 + kTN/32 loads of 1 KiB (8 rows
 // of 128 bytes, lane l at row l/8, physical chunk l%8 holding logical chunk swz(row, l%8)).
-typedef __attribute__((address_space(3))) void NarrowLds;
-
-template <int N>
-__device__ __forceinline__ void narrow_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-__device__ __forceinline__ void narrow_fence() { asm volatile("" ::: "memory"); }
 
 // One operand's loads of a K step: load j fills rows (4j + wave)·8 .. + 8 of the operand's half.
 template <int kLoads>
@@ -284,7 +275,7 @@ __device__ __forceinline__ void deep_issue(__amdgpu_buffer_rsrc_t rsrc, uint8_t*
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
         const uint32_t off = (k0 + chunk[j] < K) ? static_cast<uint32_t>(rowoff[j] + k0) : kOutOfRange;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (NarrowLds*)(half + (4 * j + wave) * 1024), 16, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LdsPtr*)(half + (4 * j + wave) * 1024), 16, off, 0, 0, 0);
     }
 }
 
@@ -350,10 +341,10 @@ __global__ __launch_bounds__(kThreads) void deep_kernel(
     for (int ks = 0; ks < nk; ++ks) {
         // Step ks landed (this wave's share; the barrier makes every wave's visible) and every
         // wave is done with step ks - 1, whose slot takes step ks + kStages - 1.
-        narrow_fence();
-        narrow_vmcnt<(kStages - 2) * (kLX + kLW)>();
+        fence();
+        wait_vmcnt<(kStages - 2) * (kLX + kLW)>();
         __builtin_amdgcn_s_barrier();
-        narrow_fence();
+        fence();
         issue(ks + kStages - 1);
         const uint8_t* lx = lds + (ks % kStages) * kStageBytes;
         const uint8_t* lw = lx + kTM * kStep;
@@ -400,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void deep_kernel(
                 for (int j = 0; j < kBJ; ++j) acc[i][j] = mfma_f8(a[i], b[j], acc[i][j]);
         }
     }
-    narrow_vmcnt<0>();  // the zero-filling loads past the last step land before the wave ends
+    wait_vmcnt<0>();  // the zero-filling loads past the last step land before the wave ends
 
     // Epilogue: narrow_kernel's.
 #pragma unroll

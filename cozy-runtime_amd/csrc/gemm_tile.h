@@ -54,22 +54,7 @@ constexpr int kLdsBytes = kEpiBase + 2560;
 template <int kKind, int kTN = 256>
 constexpr int kLoads = 8 + kTN / 32 + (kKind == kMx ? 2 : 0);
 
-typedef __attribute__((address_space(3))) void LdsPtr;
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
-
-// s_waitcnt with only vmcnt <= N (expcnt and lgkmcnt left unconstrained): gfx9 encoding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// Keeps the compiler from moving memory operations across the waits and barriers below.
-__device__ __forceinline__ void fence() { asm volatile("" ::: "memory"); }
-
-__device__ __forceinline__ void wait_lgkmcnt0() {
-    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));
-}
 
 // 16-byte chunk `c` (0..7) of a 128-byte LDS row `r` sits at chunk c ^ ((r/2) % 8): the 16 rows
 // a ds_read_b128 serves together, read at one logical chunk, land on 16 distinct 16-byte bank

@@ -211,6 +211,241 @@ __global__ __launch_bounds__(kDThreads) void fp8_decode_kernel(
     }
 }
 
+// The fp8 rowwise linear for 5..16 rows in one launch. Quantizing all rows in every workgroup
+// costs VALU time per CU (about 4.5 operations an element), so the grid is one workgroup per CU:
+// the CUs share N in 8-row units (at most 64 rows, four 16-row tiles, a workgroup) and a
+// workgroup's 8 waves split K (at most 4 steps of 128 bytes each, K <= 4096). A wave loads its K
+// slice of every activation row straight into the MFMA's B layout (lane l: row l%16), the
+// workgroup meets once in LDS for the rows' whole amax, and each wave quantizes its slice into
+// B registers (the law bit for bit, as above). The product is the plain 16x16x128 MFMA, A = 16
+// weight rows, B = the activation rows (zero past M).
+//
+// The weight reaches the MFMA through LDS. A register load in the A layout reads 64-byte pieces
+// of 16 rows, which streams at ~4.5 TB/s on MI355X; here each load is an LDS-DMA of 2 rows x
+// 512 contiguous bytes (the wave's K slice of two rows) into a per-wave slot of one 16-row tile
+// (two slots a wave, 128 KB a workgroup), where a row's 16-byte chunk c sits at chunk
+// c ^ (row % 16), so the A-layout reads (16 rows at one chunk) hit 16 distinct bank groups.
+// Tiles 0 and 1 are loaded first. Once the workgroup has met for the amax, tile 0's A operands
+// are read into registers and its slot refilled with tile 2 before the quantization, and tile 1
+// likewise with tile 3 after it. Measured at M=16, K=4096, N=14336 (back-to-back launches over
+// 8 weight copies): 14.0 us, against 14.6 refilling each slot after its products, 16.4 refilling
+// before the amax meeting (which then waits for every wave's tile 0), and 18-19 loading all
+// four tiles into registers and staging them through LDS afterwards. The waves' partial sums
+// meet in LDS and are added in wave order.
+constexpr int kRTiles = 4;                   // 16-row weight tiles a workgroup owns at most
+constexpr int kRWaves = 8;                   // waves a workgroup: K split 8 ways
+constexpr int kRSteps = 4;                   // 128-byte K steps a wave owns at most
+constexpr int kRStage = 16 * 128 * kRSteps;  // one tile's slice: 16 rows x 512 bytes
+constexpr uint32_t kFar = 0x7fff0000u;       // a buffer offset past every resource here (reads 0)
+
+template <bool kXHalf, bool kOutHalf, bool kBias>
+__global__ __launch_bounds__(64 * kRWaves) void fp8_rows_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ W, const float* __restrict__ ws,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K,
+    int units, int groups) {
+    static_assert(kRWaves >= kRTiles && kRWaves * kRTiles * 64 * 16 <= kRWaves * kRStage, "partials fit a slot array");
+    // The two slots are separate arrays: the compiler's wait before an LDS read then covers only
+    // the LDS-DMA loads into the slot read, not the ones in flight to the other.
+    __shared__ __attribute__((aligned(1024))) uint8_t slot0[kRWaves * kRStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot1[kRWaves * kRStage];
+    __shared__ uint32_t red[kRWaves][16];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA bases go in M0
+    const int r = lane & 15, g = lane >> 4;
+    // The workgroup's rows: 8-row units [u0, u1) of N's.
+    const int u0 = static_cast<int>(static_cast<int64_t>(blockIdx.x) * units / groups);
+    const int u1 = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * units / groups);
+    const int row0 = 8 * u0, rows = 8 * (u1 - u0);
+    // The wave's 128-byte K steps [s0, s1); bytes from kend on read as zeros.
+    const int steps_all = (K + 127) / 128;
+    const int s0 = wave * steps_all / kRWaves, s1 = (wave + 1) * steps_all / kRWaves;
+    const int kend = min(K, 128 * s1);
+    const int kl = 128 * s0 + 16 * g;
+
+    // 0. The epilogue's row scales and bias (wave t finishes tile t; lane l holds weight rows
+    //    16t + 4g + (0..3) of activation row l%16), fetched first so the end waits on nothing.
+    const int n_out = 16 * wave + 4 * g;
+    const bool emits = wave < kRTiles && n_out < rows && r < M;  // rows % 8 == 0: whole 4-row groups
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ws), 0, 4 * N, 0x00020000);
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(bias), 0, kBias ? 2 * N : 0, 0x00020000);
+    float wscale[4];
+    uint16_t bterm[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = row0 + n_out + i;
+        wscale[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, emits ? 4 * n : kFar, 0, 0));
+        if constexpr (kBias) bterm[i] = __builtin_amdgcn_raw_buffer_load_b16(br, emits ? 2 * n : kFar, 0, 0);
+    }
+
+    // 1. The activation slice, B layout: step j, part p = the 8 elements at kl + 128j + 64(p/2)
+    //    + 8(p%2) of row r (rows past M lie past the resource).
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, 2 * M * K, 0x00020000);
+    uint4 xv[kRSteps][4];
+#pragma unroll
+    for (int j = 0; j < kRSteps; ++j)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int e = kl + 128 * j + 64 * (p >> 1) + 8 * (p & 1);
+            const uint32_t off = e < kend ? 2u * static_cast<uint32_t>(r * K + e) : kFar;
+            xv[j][p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+        }
+    fence();  // the weight loads stay behind the activation's
+
+    // 2. Weight tiles 0 and 1 by LDS-DMA: load i of tile t fills rows 2i, 2i+1 of slot t (lane
+    //    l: row 16t + 2i + l/32, physical chunk l % 32 holding the row's logical chunk
+    //    (l % 32) ^ (row % 16) of the wave's slice).
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(W + static_cast<int64_t>(row0) * K), 0, rows * K, 0x00020000);
+    uint8_t* const slot[2] = {slot0 + wave * kRStage, slot1 + wave * kRStage};
+    uint32_t src[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = 2 * i + (lane >> 5);
+        const int k = 128 * s0 + 16 * ((lane & 31) ^ row);
+        src[i] = k < kend ? static_cast<uint32_t>(row * K + k) : kFar;
+    }
+    auto stage = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t off = 16 * t + 2 * i + (lane >> 5) < rows ? src[i] + static_cast<uint32_t>(16 * t * K) : kFar;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LdsPtr*)(slot[t & 1] + 1024 * i), 16, off, 0, 0, kStreamPolicy);
+        }
+    };
+    stage(0);
+    stage(1);
+
+    // 4. Row amax: bf16 and fp16 magnitudes order as their bit patterns, so the maximum is
+    //    taken on the integers (two a packed op); a NaN's pattern exceeds every number's, so a
+    //    row holding one gets a NaN scale and NaN outputs, as the law's row does.
+    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 m2 = {0, 0};
+#pragma unroll
+    for (int j = 0; j < kRSteps; ++j)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t d4[4] = {xv[j][p].x, xv[j][p].y, xv[j][p].z, xv[j][p].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, d4[i] & 0x7fff7fffu));
+        }
+    uint32_t top = max(static_cast<uint32_t>(m2.x), static_cast<uint32_t>(m2.y));
+    top = max(top, static_cast<uint32_t>(__shfl_xor(static_cast<int>(top), 16)));
+    top = max(top, static_cast<uint32_t>(__shfl_xor(static_cast<int>(top), 32)));
+    if (g == 0) red[wave][r] = top;
+    // A bare barrier: __syncthreads() would also wait for the weight loads in flight.
+    fence();
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    fence();
+#pragma unroll
+    for (int w = 0; w < kRWaves; ++w) top = max(top, red[w][r]);
+    // Row r's scale (internal/fp8_linear.py:60-61), lane l's row l%16.
+    const float s = fmaxf(widen<kXHalf>(static_cast<uint16_t>(top)) / kE4m3Max, kScaleFloor);
+    const float rs = 1.0f / s;
+
+    // Tile 0 lands (tile 1 may still be in flight behind it): its A operands go to registers
+    // (row r, logical chunks 8j + g and 8j + 4 + g) and its slot takes tile 2 before the
+    // quantization, so the stream does not wait on it.
+    auto read_tile = [&](int t, uint4 (&a)[kRSteps][2]) {
+        const uint8_t* base = slot[t & 1] + r * 512;
+#pragma unroll
+        for (int j = 0; j < kRSteps; ++j) {
+            a[j][0] = *reinterpret_cast<const uint4*>(base + 16 * ((8 * j + g) ^ r));
+            a[j][1] = *reinterpret_cast<const uint4*>(base + 16 * ((8 * j + 4 + g) ^ r));
+        }
+    };
+    auto land = [&](int t, uint4 (&a)[kRSteps][2]) {
+        __builtin_amdgcn_sched_barrier(0);
+        fence();
+        wait_vmcnt<8>();
+        fence();
+        read_tile(t, a);
+        fence();
+        wait_lgkmcnt0();
+        fence();
+        stage(t + 2);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    uint4 early[2][kRSteps][2];
+    land(0, early[0]);
+
+    // 5. Codes: B operand of step j, bytes 0-15 = elements kl + 128j + [0, 16), bytes 16-31 =
+    //    + 64 + [0, 16). x / s as div_rn without the sign fix (a zero's sign adds nothing to a
+    //    sum); the cast rounds |x / s| <= 448·(1 + 2^-23) to 448 as the law's clamp would.
+    i32x8 codes[kRSteps];
+#pragma unroll
+    for (int j = 0; j < kRSteps; ++j) {
+        uint32_t c[8];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t d4[4] = {xv[j][p].x, xv[j][p].y, xv[j][p].z, xv[j][p].w};
+            float q[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint16_t h = static_cast<uint16_t>((i & 1) ? (d4[i / 2] >> 16) : (d4[i / 2] & 0xffffu));
+                const float v = widen<kXHalf>(h);
+                const float q0 = v * rs;
+                q[i] = __builtin_fmaf(__builtin_fmaf(-q0, s, v), rs, q0);
+            }
+            c[2 * p] = e4m3x4(q[0], q[1], q[2], q[3]);
+            c[2 * p + 1] = e4m3x4(q[4], q[5], q[6], q[7]);
+        }
+        codes[j] = i32x8{static_cast<int>(c[0]), static_cast<int>(c[1]), static_cast<int>(c[2]),
+                         static_cast<int>(c[3]), static_cast<int>(c[4]), static_cast<int>(c[5]),
+                         static_cast<int>(c[6]), static_cast<int>(c[7])};
+    }
+
+    land(1, early[1]);
+
+    // 6. Products: tiles 0 and 1 from registers, 2 and 3 from their slots as they land.
+    auto product = [&](const uint4 (&a)[kRSteps][2]) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < kRSteps; ++j) {
+            const i32x8 op = {static_cast<int>(a[j][0].x), static_cast<int>(a[j][0].y), static_cast<int>(a[j][0].z),
+                              static_cast<int>(a[j][0].w), static_cast<int>(a[j][1].x), static_cast<int>(a[j][1].y),
+                              static_cast<int>(a[j][1].z), static_cast<int>(a[j][1].w)};
+            acc = mfma_f8(op, codes[j], acc);
+        }
+        return acc;
+    };
+    f32x4 acc[kRTiles];
+    acc[0] = product(early[0]);
+    acc[1] = product(early[1]);
+#pragma unroll
+    for (int t = 2; t < kRTiles; ++t) {
+        __builtin_amdgcn_sched_barrier(0);  // the wait for tile t stays after the work above
+        fence();
+        if (t == 2) wait_vmcnt<8>(); else wait_vmcnt<0>();
+        fence();
+        uint4 a[kRSteps][2];
+        read_tile(t, a);
+        acc[t] = product(a);
+    }
+
+    // 7. The waves' partial sums (over the slots, once every wave is done with its own), added
+    //    in wave order; wave t finishes tile t.
+    f32x4* part = reinterpret_cast<f32x4*>(slot0);  // [kRWaves][kRTiles][64]
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < kRTiles; ++t) part[(wave * kRTiles + t) * 64 + lane] = acc[t];
+    __syncthreads();
+    if (!emits) return;
+    f32x4 sum = part[wave * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < kRWaves; ++w) sum += part[(w * kRTiles + wave) * 64 + lane];
+    uint32_t o[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float v = __fmul_rn(__fmul_rn(sum[i], s), wscale[i]);
+        if constexpr (kBias) v = __fadd_rn(v, widen<kOutHalf>(bterm[i]));
+        const uint32_t h = narrow<kOutHalf>(v);
+        o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
+    }
+    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(r) * N + row0 + n_out) = make_uint2(o[0], o[1]);
+}
+
 // The int8 linear for 1..4 rows in one launch (reference: rotate.cu:351-407 `gemv_kernel`):
 // each workgroup rotates (H256/16) and quantizes the activation rows into LDS bit for bit as the
 // CPU law does (internal/int8_linear.py:422-428; the rotation's phases are rotate.h's) while its
@@ -470,19 +705,36 @@ hipError_t launch_decode(const uint16_t* x, const uint8_t* w, const float* ws,
     return hipErrorNotSupported;
 }
 
+constexpr int kRowsMaxK = 128 * kRWaves * kRSteps;  // 4096
+
+template <bool kXHalf, bool kOutHalf, bool kBias>
+hipError_t launch_rows(const uint16_t* x, const uint8_t* w, const float* ws, const uint16_t* bias,
+                       uint16_t* out, int M, int N, int K, hipStream_t s) {
+    int device = 0;
+    const hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    const int units = N / 8;
+    const int groups = max(min(cu_count(device), units), (units + 2 * kRTiles - 1) / (2 * kRTiles));
+    fp8_rows_kernel<kXHalf, kOutHalf, kBias><<<groups, 64 * kRWaves, 0, s>>>(x, w, ws, bias, out, M, N, K, units, groups);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t fp8_linear_small(const void* x, bool x_half, const uint8_t* w, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
                             hipStream_t s) {
-    // 1..4 rows whose activation fits the registers; the rest is quantize + narrow GEMM.
-    if (M < 1 || M > 4 || static_cast<int64_t>(M) * K > kXLoads * kDThreads * 8) return hipErrorNotSupported;
+    // 1..4 rows whose activation fits the registers (the GEMV), 5..16 rows with K <= 4096 (the
+    // row-tile kernel); the rest is quantize + narrow GEMM.
+    const bool gemv = M >= 1 && M <= 4 && static_cast<int64_t>(M) * K <= kXLoads * kDThreads * 8;
+    if (!gemv && (M < 5 || M > 16 || K > kRowsMaxK)) return hipErrorNotSupported;
     auto xp = static_cast<const uint16_t*>(x);
     auto bp = static_cast<const uint16_t*>(bias);
     auto op = static_cast<uint16_t*>(out);
 #define COZYQ_CASE(XH, OH, B)                                                                      \
     if (x_half == XH && out_half == OH && (bias != nullptr) == B)                                  \
-        return launch_decode<XH, OH, B>(xp, w, ws, bp, op, M, N, K, s);
+        return gemv ? launch_decode<XH, OH, B>(xp, w, ws, bp, op, M, N, K, s)                      \
+                    : launch_rows<XH, OH, B>(xp, w, ws, bp, op, M, N, K, s);
     COZYQ_CASE(false, false, false)
     COZYQ_CASE(false, false, true)
     COZYQ_CASE(false, true, false)

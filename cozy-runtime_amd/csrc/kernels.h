@@ -93,14 +93,19 @@ hipError_t gemm_int8_narrow(const int8_t* q, const float* xs, const int8_t* w, c
                             const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
                             int K, int epilogue, int config, hipStream_t s);
 
+// The compute units of `device` (256 on MI355X), read once per device.
+int cu_count(int device);
+
 // The fused int8 linear for 1..4 rows (rotate H256 + quantize + GEMV in one launch);
-// hipErrorNotSupported past M·K = 16384.
+// hipErrorNotSupported past int8_gemv_max_k(M).
 // The widest rows the fused few-row int8 linear takes at M rows (0 past 4): 32768 at M = 1,
 // 16384 at 2, 12288 at 3 and 4.
 int int8_gemv_max_k(int M);
 hipError_t int8_linear_small(const void* x, bool x_half, const int8_t* w, const float* ws,
                              const void* bias, void* out, bool out_half, int M, int N, int K,
                              hipStream_t s);
+// The fused fp8 linear for 1..4 rows (the GEMV, M·K <= 16384) and 5..16 rows (K <= 4096);
+// hipErrorNotSupported elsewhere.
 hipError_t fp8_linear_small(const void* x, bool x_half, const uint8_t* w, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
                             hipStream_t s);

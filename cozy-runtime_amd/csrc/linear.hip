@@ -190,17 +190,6 @@ __global__ __launch_bounds__(kThreads, 1) void linear_kernel(
     }
 }
 
-int cu_count(int device) {
-    static int counts[64] = {0};
-    if (device < 0 || device >= 64) return 256;
-    if (counts[device] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0) n = 256;
-        counts[device] = n;
-    }
-    return counts[device];
-}
-
 template <bool kHalf, int kRot, bool kOutHalf, bool kBias, int kEpi>
 hipError_t launch_linear(const void* x, int8_t* q, float* qs, const int8_t* w, const float* ws,
                          const void* bias, void* out, int64_t ldo, int M, int N, int K, int* work,
@@ -245,6 +234,17 @@ __global__ __launch_bounds__(256) void clear_ints(int* __restrict__ p, int n) {
 }
 
 }  // namespace
+
+int cu_count(int device) {
+    static int counts[64] = {0};
+    if (device < 0 || device >= 64) return 256;
+    if (counts[device] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0) n = 256;
+        counts[device] = n;
+    }
+    return counts[device];
+}
 
 int linear_workspace_ints(int M) { return kDone + (M + kTile - 1) / kTile; }
 

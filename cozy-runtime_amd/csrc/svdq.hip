@@ -18,7 +18,6 @@
 namespace cozyq {
 namespace {
 
-typedef __attribute__((address_space(3))) void LdsPtr;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));

@@ -614,7 +614,7 @@ def test_fp8_gemm_gelu_and_fp16_within_tolerance(ops, shape, out_dtype):
     assert_close(out, laws.gelu_tanh(rounded.float()).double())
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 13, 16])
 @pytest.mark.parametrize("k", [4096, 1040, 16384, 8208])
 def test_fp8_small_linear_within_tolerance(ops, m, k):
     n = 1032
@@ -624,6 +624,66 @@ def test_fp8_small_linear_within_tolerance(ops, m, k):
     got = ops.fp8_linear(x.to(DEV), data.to(DEV), scale.to(DEV), b.to(DEV), torch.bfloat16)
     assert got.shape == (m, n)
     assert_close(got, laws.fp8_exact(x, data, scale, b))
+
+
+#: (M, N, K) through the fused fp8 kernels: the GEMV (M <= 4) and the row-tile kernel (5..16
+#: rows, K <= 4096), whose workgroups own 8..64 weight rows (N = 14336: 56 rows, three whole
+#: 16-row tiles and a half; N = 2056: one workgroup of 16 rows among 8-row ones; N = 16392:
+#: more 8-row units than 8 a CU, so more workgroups than CUs) and whose waves split K (K = 16
+#: and 400: waves with no K step or a partial one).
+FUSED_FP8_SHAPES = [(1, 14336, 4096), (3, 2056, 1040), (5, 14336, 4096), (9, 2056, 1040),
+                    (16, 14336, 4096), (16, 16392, 1024), (12, 264, 16), (7, 520, 400),
+                    (16, 8, 4096)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("shape", FUSED_FP8_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_fp8_fused_codes_bit_exact(ops, shape, dtype):
+    """A selector weight (row n holds e4m3 1.0 at column n % K, scale 1) makes output n of row m
+    the activation's code q[m][n % K] times the row's scale: one float32 product rounded to the
+    output dtype, with no sum. So every code and scale the fused kernel made inside itself is
+    held bit for bit against the law's (a zero's sign aside), at every K position each wave and
+    lane group owns, and every output lands at its row and column."""
+    from cozyq import prebuilt
+
+    m, n, k = shape
+    x = activations(m, k, seed=900 + m + k, dtype=dtype)
+    x[0, :3] = torch.tensor([1e-7, -3e-5, 0.0]).to(dtype)  # subnormal codes and a zero
+    if m > 2:
+        x[m - 1] = 0  # a zero row: the scale floor
+    data = torch.zeros(n, k, dtype=torch.uint8)
+    data[torch.arange(n), torch.arange(n) % k] = 0x38  # e4m3 1.0
+    data = data.view(torch.float8_e4m3fn)
+    ones = torch.ones(n)
+    got = ops.fp8_linear(x.to(DEV), data.to(DEV), ones.to(DEV), None, dtype)
+    assert m <= prebuilt.FP8_SMALL_ROWS
+    wq, ws = laws.fp8_quantize(x)
+    picked = wq.float()[:, torch.arange(n) % k]
+    assert torch.equal(got.cpu(), (picked * ws.reshape(-1, 1)).to(dtype))
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("dtypes", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.bfloat16),
+                                    (torch.bfloat16, torch.float16)],
+                         ids=["bf16", "fp16-in", "fp16-out"])  # fmt: skip
+@pytest.mark.parametrize("shape", FUSED_FP8_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_fp8_fused_within_tolerance(ops, shape, dtypes, bias):
+    """The fused fp8 kernels' sums (the row-tile kernel adds its waves' K slices in wave order)
+    within tolerance of the float64 product of the law's codes, each input and output dtype,
+    with and without bias; the same shape through quantize + GEMM agrees as closely."""
+    m, n, k = shape
+    x_dtype, out_dtype = dtypes
+    x = activations(m, k, seed=950 + m + k, dtype=x_dtype)
+    data, scale = laws.fp8_weight(weights(n, k, seed=951 + n))
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(952)) * 0.1).to(out_dtype) \
+        if bias else None
+    xd, wd, sd = x.to(DEV), data.to(DEV), scale.to(DEV)
+    bd = None if b is None else b.to(DEV)
+    got = ops.fp8_linear(xd, wd, sd, bd, out_dtype)
+    exact = laws.fp8_exact(x, data, scale, b)
+    assert_close(got, exact)
+    q, s = ops.fp8_quantize(xd)
+    assert_close(ops.fp8_gemm(q, s, wd, sd, bd, out_dtype), exact)
 
 
 # ------------------------------------------------------------------ producer prologue
