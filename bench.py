@@ -1096,6 +1096,7 @@ def main() -> int:
         "configs": {"c2_rotation256": [c2["rotation256"]], **configs},
         "cpu_baseline": None if baselines is None else baselines["c2"],
         "cpu_baselines": baselines,
+        "self_check": {name: v.detail for name, v in ops.verdicts.items()},
     }
     print(json.dumps(line))
     return 0

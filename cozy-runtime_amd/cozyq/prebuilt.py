@@ -12,9 +12,10 @@ module imports without it.
 from __future__ import annotations
 
 from dataclasses import dataclass, field
+from functools import partial
 from typing import Any
 
-from cozyq import _lib
+from cozyq import _lib, verify
 from cozyq._admit import ALIGN, EXTENT, KIND, LAYOUT, ROWS, Operand, Placement, admit, every, off_card
 
 Tensor = Any
@@ -115,6 +116,8 @@ class Prebuilt:
     #: The fused linear's counters, one zeroed int32 buffer per stream (each call leaves its
     #: buffer zero; calls on one stream run in order, so they share it).
     _workspaces: dict[int, Tensor] = field(init=False, default_factory=dict)
+    #: format -> its self-check on this card (`cozyq.verify`), set by `library`.
+    verdicts: dict[str, Any] = field(init=False, default_factory=dict)
 
     def __post_init__(self) -> None:
         self._lib = _lib.load()
@@ -1041,9 +1044,10 @@ _LIBRARIES: dict[int, Prebuilt] = {}
 
 
 def library(index: int = 0) -> Prebuilt:
-    """The op library on cuda:`index`, opened once (`internal/prebuilt.py:568-598`). Raises
+    """The op library on cuda:`index`, opened once and only once each format's kernels pass their
+    self-check on the card (`internal/prebuilt.py:568-598`; `cozyq.verify`). Raises
     `_lib.KernelsAbsent` where the HIP library is not built or loadable, and RuntimeError where
-    the device is not the gfx950 the library carries."""
+    the device is not the gfx950 the library carries or a format fails its check."""
     found = _LIBRARIES.get(index)
     if found is not None:
         return found
@@ -1054,5 +1058,17 @@ def library(index: int = 0) -> Prebuilt:
     carried = _lib.load().cozyq_arch().decode()
     if arch != carried:
         raise RuntimeError(f"cozyq carries {carried} device code; cuda:{index} is {arch}")
-    ops = _LIBRARIES[index] = Prebuilt(torch, index)
+    ops = Prebuilt(torch, index)
+    digest = verify.library_digest(_lib.PATH)
+    with torch.cuda.device(index):
+        ops.verdicts = {
+            name: verify.verified(f"{name}-{arch}-{digest}", partial(probe, torch, ops),
+                                  verify.cuda_fault(torch))
+            for name, probe in verify.PROBES.items()
+        }  # fmt: skip
+    failed = [f"{name}: {v.detail}" for name, v in ops.verdicts.items() if not v.ok]
+    if failed:
+        raise RuntimeError(f"cozyq: the kernels failed their self-check on cuda:{index} ({arch}): "
+                           + "; ".join(failed))
+    _LIBRARIES[index] = ops
     return ops
