@@ -257,9 +257,13 @@ __global__ __launch_bounds__(64 * kRWaves) void fp8_rows_kernel(
     const int u0 = static_cast<int>(static_cast<int64_t>(blockIdx.x) * units / groups);
     const int u1 = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * units / groups);
     const int row0 = 8 * u0, rows = 8 * (u1 - u0);
-    // The wave's 128-byte K steps [s0, s1); bytes from kend on read as zeros.
+    // The wave's 128-byte K steps [s0, s1); bytes from kend on read as zeros. Every workgroup
+    // reads the whole activation, and the 32 workgroups of an XCD (b, b + 8, ...) run together:
+    // rotating which wave takes which K slice by b / 8 spreads their simultaneous activation loads
+    // over 8 slices instead of one (measured 14.9 -> 13.5 us at M=16, K=4096, N=14336).
     const int steps_all = (K + 127) / 128;
-    const int s0 = wave * steps_all / kRWaves, s1 = (wave + 1) * steps_all / kRWaves;
+    const int slice = (wave + static_cast<int>(blockIdx.x >> 3)) & (kRWaves - 1);
+    const int s0 = slice * steps_all / kRWaves, s1 = (slice + 1) * steps_all / kRWaves;
     const int kend = min(K, 128 * s1);
     const int kl = 128 * s0 + 16 * g;
 
