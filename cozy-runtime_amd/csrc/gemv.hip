@@ -233,16 +233,19 @@ __global__ __launch_bounds__(kDThreads) void fp8_decode_kernel(
 // four tiles into registers and staging them through LDS afterwards. The waves' partial sums
 // meet in LDS and are added in wave order.
 constexpr int kRTiles = 4;                   // 16-row weight tiles a workgroup owns at most
-constexpr int kRWaves = 8;                   // waves a workgroup: K split 8 ways
-constexpr int kRSteps = 4;                   // 128-byte K steps a wave owns at most
-constexpr int kRStage = 16 * 128 * kRSteps;  // one tile's slice: 16 rows x 512 bytes
+constexpr int kRSpan = 32;                   // 128-byte K steps a workgroup spans (K <= 4096)
 constexpr uint32_t kFar = 0x7fff0000u;       // a buffer offset past every resource here (reads 0)
 
-template <bool kXHalf, bool kOutHalf, bool kBias>
+template <bool kXHalf, bool kOutHalf, bool kBias, int kRWaves>
 __global__ __launch_bounds__(64 * kRWaves) void fp8_rows_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ W, const float* __restrict__ ws,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K,
     int units, int groups) {
+    constexpr int kRSteps = kRSpan / kRWaves;     // 128-byte K steps a wave owns at most
+    constexpr int kRStage = 16 * 128 * kRSteps;   // one tile's slice: 16 rows x 128·kRSteps bytes
+    constexpr int kChunks = 8 * kRSteps;          // 16-byte chunks of a row's slice
+    constexpr int kRowsPerLoad = 64 / kChunks;    // rows one 1 KiB LDS-DMA load fills
+    constexpr int kTileLoads = 16 / kRowsPerLoad;  // loads a tile takes
     static_assert(kRWaves >= kRTiles && kRWaves * kRTiles * 64 * 16 <= kRWaves * kRStage, "partials fit a slot array");
     // The two slots are separate arrays: the compiler's wait before an LDS read then covers only
     // the LDS-DMA loads into the slot read, not the ones in flight to the other.
@@ -296,23 +299,23 @@ __global__ __launch_bounds__(64 * kRWaves) void fp8_rows_kernel(
         }
     fence();  // the weight loads stay behind the activation's
 
-    // 2. Weight tiles 0 and 1 by LDS-DMA: load i of tile t fills rows 2i, 2i+1 of slot t (lane
-    //    l: row 16t + 2i + l/32, physical chunk l % 32 holding the row's logical chunk
-    //    (l % 32) ^ (row % 16) of the wave's slice).
+    // 2. Weight tiles 0 and 1 by LDS-DMA: load i of tile t fills kRowsPerLoad rows of slot t
+    //    (2 at 8 waves: lane l takes row 16t + 2i + l/32 and physical chunk l % 32, which holds
+    //    the row's logical chunk (l % 32) ^ (row % 16) of the wave's slice).
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(W + static_cast<int64_t>(row0) * K), 0, rows * K, 0x00020000);
     uint8_t* const slot[2] = {slot0 + wave * kRStage, slot1 + wave * kRStage};
-    uint32_t src[8];
+    uint32_t src[kTileLoads];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int row = 2 * i + (lane >> 5);
-        const int k = 128 * s0 + 16 * ((lane & 31) ^ row);
+    for (int i = 0; i < kTileLoads; ++i) {
+        const int row = kRowsPerLoad * i + lane / kChunks;
+        const int k = 128 * s0 + 16 * ((lane % kChunks) ^ (row & 15));
         src[i] = k < kend ? static_cast<uint32_t>(row * K + k) : kFar;
     }
     auto stage = [&](int t) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t off = 16 * t + 2 * i + (lane >> 5) < rows ? src[i] + static_cast<uint32_t>(16 * t * K) : kFar;
+        for (int i = 0; i < kTileLoads; ++i) {
+            const uint32_t off = 16 * t + kRowsPerLoad * i + lane / kChunks < rows ? src[i] + static_cast<uint32_t>(16 * t * K) : kFar;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LdsPtr*)(slot[t & 1] + 1024 * i), 16, off, 0, 0, kStreamPolicy);
         }
     };
@@ -352,7 +355,7 @@ __global__ __launch_bounds__(64 * kRWaves) void fp8_rows_kernel(
     // (row r, logical chunks 8j + g and 8j + 4 + g) and its slot takes tile 2 before the
     // quantization, so the stream does not wait on it.
     auto read_tile = [&](int t, uint4 (&a)[kRSteps][2]) {
-        const uint8_t* base = slot[t & 1] + r * 512;
+        const uint8_t* base = slot[t & 1] + r * (16 * kChunks);
 #pragma unroll
         for (int j = 0; j < kRSteps; ++j) {
             a[j][0] = *reinterpret_cast<const uint4*>(base + 16 * ((8 * j + g) ^ r));
@@ -362,7 +365,7 @@ __global__ __launch_bounds__(64 * kRWaves) void fp8_rows_kernel(
     auto land = [&](int t, uint4 (&a)[kRSteps][2]) {
         __builtin_amdgcn_sched_barrier(0);
         fence();
-        wait_vmcnt<8>();
+        wait_vmcnt<kTileLoads>();
         fence();
         read_tile(t, a);
         fence();
@@ -421,7 +424,7 @@ __global__ __launch_bounds__(64 * kRWaves) void fp8_rows_kernel(
     for (int t = 2; t < kRTiles; ++t) {
         __builtin_amdgcn_sched_barrier(0);  // the wait for tile t stays after the work above
         fence();
-        if (t == 2) wait_vmcnt<8>(); else wait_vmcnt<0>();
+        if (t == 2) wait_vmcnt<kTileLoads>(); else wait_vmcnt<0>();
         fence();
         uint4 a[kRSteps][2];
         read_tile(t, a);
@@ -709,7 +712,8 @@ hipError_t launch_decode(const uint16_t* x, const uint8_t* w, const float* ws,
     return hipErrorNotSupported;
 }
 
-constexpr int kRowsMaxK = 128 * kRWaves * kRSteps;  // 4096
+constexpr int kRowsMaxK = 128 * kRSpan;  // 4096
+constexpr int kRowsWaves = 8;  // fp8_rows_kernel's waves a workgroup
 
 template <bool kXHalf, bool kOutHalf, bool kBias>
 hipError_t launch_rows(const uint16_t* x, const uint8_t* w, const float* ws, const uint16_t* bias,
@@ -719,7 +723,7 @@ hipError_t launch_rows(const uint16_t* x, const uint8_t* w, const float* ws, con
     if (e != hipSuccess) return e;
     const int units = N / 8;
     const int groups = max(min(cu_count(device), units), (units + 2 * kRTiles - 1) / (2 * kRTiles));
-    fp8_rows_kernel<kXHalf, kOutHalf, kBias><<<groups, 64 * kRWaves, 0, s>>>(x, w, ws, bias, out, M, N, K, units, groups);
+    fp8_rows_kernel<kXHalf, kOutHalf, kBias, kRowsWaves><<<groups, 64 * kRowsWaves, 0, s>>>(x, w, ws, bias, out, M, N, K, units, groups);
     return hipGetLastError();
 }
 
