@@ -17,16 +17,46 @@ hipError_t launch(const void* q, const float* xs, const void* w, const float* ws
     return hipGetLastError();
 }
 
+// Where a grid of 256x256 tiles ends in a partial round of at most half the CUs, the tiles of
+// its full rounds are a block of whole columns (tiles_m x `head` tiles, a multiple of the CU
+// count) and the rest of the columns go to a second launch of 256x128 tiles: one round of
+// half-sized tiles in place of a round at most half full. 0 where the grid does not split so.
+int tail_columns(int M, int N) {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return 0;
+    const int64_t cus = cu_count(device);
+    const int64_t tm = (M + kTile - 1) / kTile, tn = (N + kTile - 1) / kTile;
+    const int64_t tiles = tm * tn, rounds = (tiles + cus - 1) / cus;
+    const int64_t last = tiles - (rounds - 1) * cus;
+    if (rounds < 2 || 2 * last > cus || ((rounds - 1) * cus) % tm != 0) return 0;
+    const int64_t head = (rounds - 1) * cus / tm;  // 256-column tiles in the head launch
+    if (head >= tn || tm * ((N - head * kTile + 127) / 128) > cus) return 0;
+    return static_cast<int>(head * kTile);
+}
+
 template <int kKind>
 hipError_t dispatch(const void* q, const float* xs, const void* w, const float* ws,
                     const uint8_t* xe, const uint8_t* we, const void* bias, void* out,
                     int64_t ldo, bool out_half, int M, int N, int K, int epilogue, bool wide,
                     hipStream_t s) {
     const bool b = bias != nullptr;
+    const int head = wide ? 0 : tail_columns(M, N);
+    // The tail's operands: W rows, their scales (MX: E8M0 rows of K/32 bytes), biases and output
+    // columns from `head` on.
+    const auto w8 = static_cast<const uint8_t*>(w);
+    const void* tw = w8 + static_cast<int64_t>(head) * K;
+    const float* tws = ws == nullptr ? nullptr : ws + head;
+    const uint8_t* twe = we == nullptr ? nullptr : we + static_cast<int64_t>(head) * (K / 32);
+    const void* tb = bias == nullptr ? nullptr : static_cast<const uint16_t*>(bias) + head;
+    void* to = static_cast<uint16_t*>(out) + head;
 #define COZYQ_CASE(H, B, E)                                                                     \
-    if (out_half == H && b == B && epilogue == E)                                               \
-        return wide ? launch<kKind, H, B, E, 192>(q, xs, w, ws, xe, we, bias, out, nullptr, ldo, M, N, K, s) \
-                    : launch<kKind, H, B, E>(q, xs, w, ws, xe, we, bias, out, nullptr, ldo, M, N, K, s);
+    if (out_half == H && b == B && epilogue == E) {                                             \
+        if (wide) return launch<kKind, H, B, E, 192>(q, xs, w, ws, xe, we, bias, out, nullptr, ldo, M, N, K, s); \
+        if (head == 0) return launch<kKind, H, B, E>(q, xs, w, ws, xe, we, bias, out, nullptr, ldo, M, N, K, s); \
+        const hipError_t e_ = launch<kKind, H, B, E>(q, xs, w, ws, xe, we, bias, out, nullptr, ldo, M, head, K, s); \
+        if (e_ != hipSuccess) return e_;                                                        \
+        return launch<kKind, H, B, E, 128>(q, xs, tw, tws, xe, twe, tb, to, nullptr, ldo, M, N - head, K, s); \
+    }
     COZYQ_CASE(false, false, 0)
     COZYQ_CASE(false, true, 0)
     COZYQ_CASE(true, false, 0)

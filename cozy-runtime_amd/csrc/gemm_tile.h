@@ -128,7 +128,8 @@ __device__ __forceinline__ i32x4 half_of(const i32x8& v, int h) {
 // dequantization (+ bias), 1 that then tanh-GELU, 2 the raw int32 accumulators (int8 test
 // entry). kTN is 256, or 192: each wave then owns 128 x 96 (3 x 4 blocks), for grids that 256
 // columns would leave a partial round of tiles (N = 3072: 256 tiles of 256 x 192 at M = 4096
-// against 192 of 256 x 256). Each output's K sum runs in the same MFMA order either way.
+// against 192 of 256 x 256); or 128 (2 x 4 blocks), the half-width tiles a grid's partial last
+// round runs as. Each output's K sum runs in the same MFMA order every way.
 template <int kKind, bool kOutHalf, bool kBias, int kEpi, int kTN = 256>
 __device__ __forceinline__ void gemm_tile(
     uint8_t* __restrict__ lds, const uint8_t* __restrict__ X, const uint8_t* __restrict__ W,
@@ -136,7 +137,7 @@ __device__ __forceinline__ void gemm_tile(
     const uint8_t* __restrict__ we, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
     int32_t* __restrict__ acc_out, int64_t ldo, int M, int N, int K, int tm, int tn) {
     static_assert(kEpi != 2 || kKind == kInt8, "raw accumulators are the int8 GEMM's");
-    static_assert(kTN == 256 || kTN == 192, "tile widths: 256 or 192 columns");
+    static_assert(kTN == 256 || kTN == 192 || kTN == 128, "tile widths: 256, 192 or 128 columns");
     typedef std::conditional_t<kKind == kInt8, i32x16, f32x16> Acc;
     constexpr int kNI = kTN / 64;      // W blocks of 32 columns a wave
     constexpr int kHalfN = kTN / 2;    // a wave's columns
@@ -329,7 +330,9 @@ __device__ __forceinline__ void gemm_tile(
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
         }
-        if constexpr (kTN != 256) __builtin_amdgcn_sched_group_barrier(0x100, kKind == kMx ? 3 : 2, 0);
+        // The reads past the groups: 2·(kNI + 4) fragment reads (MX: and kNI + 4 scale reads)
+        // against one a group (MX: three a pair of groups).
+        if constexpr (kTN != 256) __builtin_amdgcn_sched_group_barrier(0x100, kKind == kMx ? 12 - 3 * kNI : 8 - 2 * kNI, 0);
     };
     // Step 2p: the next step's fragments come from the same buffer, which has landed.
     auto even_step = [&](int s, const Frags& cur, Frags& next) {

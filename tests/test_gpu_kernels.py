@@ -570,6 +570,31 @@ def test_every_gemm_config_bit_equal(ops, shape, dtype):
         assert_close(outs[0], laws.fp8_exact(x, f8, f8s, b))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_partial_last_round_runs_half_width_tiles_bit_equal(ops, dtype):
+    """Config 0 on a grid whose last round is at most half full (M=4096, N=4352: 272 tiles of
+    256x256 on 256 CUs) runs its full round on 256x256 tiles and the last 256 columns as a second
+    launch of 256x128 tiles. int8's outputs equal the law bit for bit, with and without bias;
+    fp8's equal the 128x128 config's bits (each output's K sum in the same MFMA order) and sit
+    within tolerance of the exact law."""
+    m, n, k = 4096, 4352, 512
+    x = activations(m, k, seed=4352)
+    data, scale = laws.int8_weight_rowwise(weights(n, k, seed=4353))
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(4354)) * 0.1).to(dtype)
+    q, s = ops.int8_quantize(x.to(DEV))
+    wd, sd, bd = data.to(DEV), scale.to(DEV), b.to(DEV)
+    want = laws.int8_product(q.cpu(), s.cpu(), data, scale, dtype)
+    assert torch.equal(ops.int8_gemm(q, s, wd, sd, None, dtype, 0).cpu(), want)
+    got = ops.int8_gemm(q, s, wd, sd, bd, dtype, 0)
+    assert torch.equal(got.cpu(), want + b)
+    assert torch.equal(got, ops.int8_gemm(q, s, wd, sd, bd, dtype, 1))
+    f8, f8s = laws.fp8_weight(weights(n, k, seed=4355))
+    q8, s8 = ops.fp8_quantize(x.to(DEV))
+    outs = [ops.fp8_gemm(q8, s8, f8.to(DEV), f8s.to(DEV), bd, dtype, c) for c in (0, 1)]
+    assert torch.equal(outs[0], outs[1])
+    assert_close(outs[0], laws.fp8_exact(x, f8, f8s, b))
+
+
 @pytest.mark.parametrize("shape", [(16, 520, 4112), (3, 264, 80), (32, 136, 1040)],
                          ids=lambda s: "x".join(map(str, s)))  # fmt: skip
 def test_fp8_configs_partial_k_steps(ops, shape):
