@@ -718,7 +718,7 @@ void cozyq_host_mx_byte(const float* amax, uint8_t* out, int64_t n) {
 
 int cozyq_probe_mfma(int device, int kind, const void* a, const void* b, const void* sa,
                      const void* sb, void* d, void* stream) {
-    if (kind < 0 || kind > 6) return hipErrorInvalidValue;
+    if (kind < 0 || kind > 8) return hipErrorInvalidValue;
     const OnDevice guard(device);
     if (guard.error() != hipSuccess) return guard.error();
     return cozyq::mfma_probe(kind, a, b, sa, sb, d, on(stream));

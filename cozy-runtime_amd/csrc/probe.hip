@@ -28,6 +28,20 @@ __global__ void mfma_probe_kernel(int kind, const uint8_t* a, const uint8_t* b, 
         for (int i = 0; i < 16; ++i) z[i] = 0.0f;
         const f32x16 c = kind == 5 ? mfma_f8_32(a8, b8, z) : mfma_f8_32_scaled(a8, b8, z, sa[l], sb[l]);
         for (int i = 0; i < 16; ++i) r[i] = bits_of(c[i]);
+    } else if (kind == 7) {
+        f32x16 z;
+        for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+        const int32_t a0 = a8[0], b0 = b8[0];
+        const f32x16 c = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, a0),
+                                                              __builtin_bit_cast(float, b0), z, 0, 0, 0);
+        for (int i = 0; i < 16; ++i) r[i] = bits_of(c[i]);
+    } else if (kind == 8) {
+        typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+        f32x16 z;
+        for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+        const f32x16 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a4),
+                                                                __builtin_bit_cast(f16x8_t, b4), z, 0, 0, 0);
+        for (int i = 0; i < 16; ++i) r[i] = bits_of(c[i]);
     } else if (kind == 0) {
         const i32x4 c = mfma_i8(a4, b4, i32x4{0, 0, 0, 0});
         for (int i = 0; i < 4; ++i) r[i] = static_cast<uint32_t>(c[i]);

@@ -8,10 +8,12 @@
 //
 // GEMM: out = Σ_g (Σ_{k∈g} a·w)·sa[m,g]·sw[n,g] + la·upᵀ + bias, one cast. The packed codes are
 // unpacked in registers to bytes holding 16·code (a nibble shifted into a byte's top half keeps
-// its sign), multiplied on v_mfma_i32_32x32x32_i8 into a fresh int32 partial per 64-group (two
-// MFMAs), and each partial is rescaled into float32 accumulators that start from the low-rank
-// product (v_mfma_f32_32x32x16_bf16). The 1/256 of the two 16x factors rides on the activation
-// scale, an exact power of two.
+// its sign), multiplied on v_mfma_i32_32x32x32_i8 into a fresh int32 partial P per 64-group (two
+// MFMAs) that starts from the bits of 1.5·2^23, so it reads as the float 1.5·2^23 + P; one FMA an
+// output adds it times sa·sw (an f16 MFMA) into float32 accumulators that start from the
+// low-rank product (v_mfma_f32_32x32x16_bf16), and an f32 MFMA takes the 1.5·2^23·sa·sw part out
+// again for two groups at a time. The accumulators run in units of 1/256 (the two 16x factors)
+// until the epilogue, an exact power of two.
 #include "common.h"
 #include "kernels.h"
 
@@ -174,7 +176,7 @@ constexpr int kThreads = 256;                       // 4 waves, each a 64x64 qua
 constexpr int kStageGroups = 4;                     // 64-groups a stage brings in
 constexpr int kRowBytes = kStageGroups * 32;        // packed bytes of one tile row a stage: 128
 constexpr int kOpBytes = kTile * kRowBytes;         // one operand's stage: 16 KB
-constexpr int kScaleBytes = kStageGroups * kTile * 4;  // fp16 scales [group][row], 4-byte slots: 2 KB
+constexpr int kScaleBytes = kStageGroups * kTile * 4;  // one operand's scales of a stage: 2 KB
 constexpr int kStageBytes = 2 * kOpBytes + 2 * kScaleBytes;
 constexpr int kStages = 2;
 constexpr uint32_t kOutOfRange = 0x80000000u;       // a buffer offset past num_records reads zeros
@@ -219,7 +221,11 @@ __device__ __forceinline__ uint16_t round_out(float v) {
     }
 }
 
-template <bool kOutHalf, bool kBias, int kR>
+// kWide (the group count a multiple of 8, the scale arrays 16-byte aligned): a lane brings one
+// row's scales of 8 groups (two stages) as one 16-byte load. Otherwise every (group, row) scale
+// is its own 2-byte load, whose 64 lanes touch as many cache lines as rows (a row's scales sit
+// groups·2 bytes apart): those loads cost as much time as the code loads.
+template <bool kOutHalf, bool kBias, int kR, bool kWide>
 __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
     const uint8_t* __restrict__ act, const uint16_t* __restrict__ ascales,
     const uint8_t* __restrict__ w, const uint16_t* __restrict__ wscales,
@@ -266,10 +272,14 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
         chunk[j] = 16 * swz(r, i & 7);
         rowoff[j] = r * half + chunk[j];
     }
-    // The stage's fp16 scales come by 2-byte LDS-DMA, which writes each lane's value into a
-    // 4-byte slot: scale (group g, row r) of an operand sits in slot g·kTile + r. Load q (0..3)
-    // of a wave covers operand c/8, group (c/2)%4 and rows 64·(c%2) + lane, c = 4q + wave; past
-    // the matrix's rows or its last group they read as zeros.
+    // Scales, in a stage buffer's scale area (2·kScaleBytes after its codes):
+    // - kWide: the area of buffer b%2 holds stages 2b and 2b+1 (groups 8b..8b+7) as [operand]
+    //   [row][8 fp16], 16 bytes a row; wave w brings operand w/2, rows 64·(w%2) + lane;
+    // - otherwise each stage's own area holds its 4 groups by 2-byte LDS-DMA, which writes each
+    //   lane's value into a 4-byte slot: scale (group g, row r) of an operand sits in slot
+    //   operand·kTile·4 + g·kTile + r. Load q (0..3) of a wave covers operand c/8, group (c/2)%4
+    //   and rows 64·(c%2) + lane, c = 4q + wave.
+    // Past the matrix's rows or its last group they read as zeros.
     const int64_t asspan = static_cast<int64_t>(M - m0) * groups * 2, wsspan = static_cast<int64_t>(N - n0) * groups * 2;
     const __amdgpu_buffer_rsrc_t asr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(ascales + static_cast<int64_t>(m0) * groups), 0,
@@ -288,12 +298,21 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (LdsPtr*)(buf_ + base_), 16, off_, 0, 0, 0); \
             __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LdsPtr*)(buf_ + kOpBytes + base_), 16, off_, 0, 0, 0); \
         }                                                                                           \
-        _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                             \
-            const int c_ = 4 * q + wave, g_ = (c_ >> 1) & 3, r_ = 64 * (c_ & 1) + lane;               \
-            const int gg_ = (stage) * kStageGroups + g_;                                            \
-            const uint32_t so_ = gg_ < groups ? static_cast<uint32_t>(2 * (r_ * groups + gg_)) : kOutOfRange; \
-            uint8_t* dst_ = buf_ + 2 * kOpBytes + (c_ >> 3) * kScaleBytes + 4 * (g_ * kTile + 64 * (c_ & 1)); \
-            __builtin_amdgcn_raw_ptr_buffer_load_lds((c_ >> 3) ? wsr : asr, (LdsPtr*)dst_, 2, so_, 0, 0, 0); \
+        if constexpr (kWide) {                                                                      \
+            if (((stage) & 1) == 0) {                                                               \
+                const int b_ = (stage) >> 1, r_ = 64 * (wave & 1) + lane;                             \
+                const uint32_t so_ = 8 * b_ < groups ? static_cast<uint32_t>(2 * (r_ * groups + 8 * b_)) : kOutOfRange; \
+                uint8_t* dst_ = lds + (b_ & 1) * kStageBytes + 2 * kOpBytes + (wave >> 1) * 2048 + 1024 * (wave & 1); \
+                __builtin_amdgcn_raw_ptr_buffer_load_lds((wave >> 1) ? wsr : asr, (LdsPtr*)dst_, 16, so_, 0, 0, 0); \
+            }                                                                                       \
+        } else {                                                                                    \
+            _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                         \
+                const int c_ = 4 * q + wave, g_ = (c_ >> 1) & 3, r_ = 64 * (c_ & 1) + lane;           \
+                const int gg_ = (stage) * kStageGroups + g_;                                        \
+                const uint32_t so_ = gg_ < groups ? static_cast<uint32_t>(2 * (r_ * groups + gg_)) : kOutOfRange; \
+                uint8_t* dst_ = buf_ + 2 * kOpBytes + (c_ >> 3) * kScaleBytes + 4 * (g_ * kTile + 64 * (c_ & 1)); \
+                __builtin_amdgcn_raw_ptr_buffer_load_lds((c_ >> 3) ? wsr : asr, (LdsPtr*)dst_, 2, so_, 0, 0, 0); \
+            }                                                                                       \
         }                                                                                           \
     } while (0)
 
@@ -359,105 +378,182 @@ __global__ __launch_bounds__(kThreads, 2) void svdq_gemm_kernel(
 
 // One 32-code K half of a block's int32 partial (weight fragment A, activation fragment B).
 #define COZYQ_MMA(W, X, C) __builtin_amdgcn_mfma_i32_32x32x32_i8((W), (X), (C), 0, 0, 0)
+// The first K half starts from the bits of kOffset = 1.5·2^23 instead of zero: |P| <= 2^20 (64
+// products of 16·code bytes, each at most 2^14 in magnitude), so the int32 result P + 0x4B400000
+// is the float kOffset + P exactly and needs no conversion.
+// The kOffset part of two groups' products leaves the accumulators as one f32 MFMA with K = 2.
+#define COZYQ_OFF_MMA(SW, SA, C) __builtin_amdgcn_mfma_f32_32x32x2f32((SW), (SA), (C), 0, 0, 0)
 // The block's scale products sw[n]·sa[m] as one f16 MFMA with K = 1 (every other k is zero):
 // each product of two fp16 values is exact in float32, and lands where the block's partial does.
 #define COZYQ_T(SW, SA)                                                                             \
     __builtin_amdgcn_mfma_f32_32x32x16_f16((SW), (SA), f32x16{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0)
 // (The empty asm holds the block's accumulators at this point of the program: without it the
 // arithmetic, which touches no memory, drifts past the scheduling fences below.)
+// (The partial is reinterpreted as a whole vector: clang's bit cast of one element of a vector
+// reads element 0 whatever the index.)
 #define COZYQ_RESCALE(P, T, I, J)                                                                   \
     do {                                                                                            \
+        const f32x16 f_ = __builtin_bit_cast(f32x16, (P));                                          \
         _Pragma("unroll") for (int r_ = 0; r_ < 16; ++r_)                                           \
-            facc[I][J][r_] = __builtin_fmaf(static_cast<float>((P)[r_]), (T)[r_], facc[I][J][r_]); \
+            facc[I][J][r_] = __builtin_fmaf(f_[r_], (T)[r_], facc[I][J][r_]);                       \
         asm volatile("" : "+v"(facc[I][J]));                                                        \
     } while (0)
 
     // One group's scale operands: element 0 of lane group 0 holds the row's (column's) scale;
     // lane group 1's bits are masked to zero (no branch).
     const uint32_t keep = fq == 0 ? 0xffffu : 0u;
-    auto scale_frag = [&](const uint32_t* base, int idx) {
-        const uint32_t bits = base[idx] & keep;
-        return __builtin_bit_cast(f16x8, i32x4{static_cast<int32_t>(bits), 0, 0, 0});
+    // Stage s's scale of group g (0..3) and row r of operand op (0: activation, 1: weight), its
+    // fp16 bits in the low half.
+    auto scale_bits = [&](int s, int op, int g, int r) -> uint32_t {
+        if constexpr (kWide) {
+            return *reinterpret_cast<const uint16_t*>(lds + ((s >> 1) & 1) * kStageBytes + 2 * kOpBytes + op * 2048 +
+                                                      16 * r + 2 * (4 * (s & 1) + g));
+        } else {
+            return *reinterpret_cast<const uint32_t*>(lds + (s & 1) * kStageBytes + 2 * kOpBytes + op * kScaleBytes +
+                                                      4 * (g * kTile + r)) & 0xffffu;
+        }
+    };
+    auto frag_of = [](uint32_t bits) { return __builtin_bit_cast(f16x8, i32x4{static_cast<int32_t>(bits), 0, 0, 0}); };
+    auto scale_frag = [&](int s, int op, int g, int r) { return frag_of(scale_bits(s, op, g, r) & keep); };
+
+    // A group adds (kOffset + P)·sa·sw per output (one FMA); the kOffset part of a stage's groups
+    // 2p and 2p + 1 is taken out by one f32 MFMA with K = 2 a block: lane group l/32 supplies
+    // group 2p + l/32's -kOffset·sw[n] (A) and sa[m] (B). Each product is exact in float32
+    // (kOffset·sw has 13 significant bits, sa 11), so only the accumulator's rounding enters,
+    // at the magnitude of kOffset·sa·sw (2^-24 of it a step).
+    constexpr float kOffset = 12582912.0f;  // 1.5·2^23; its bits are 0x4B400000
+    auto half_at = [&](int s, int op, int g, int r) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(scale_bits(s, op, g, r))));
     };
 
     const int nstages = (groups + kStageGroups - 1) / kStageGroups;
-    const i32x16 zero = i32x16{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    constexpr int32_t kBits = 0x4B400000;
+    const i32x16 seed = i32x16{kBits, kBits, kBits, kBits, kBits, kBits, kBits, kBits,  // kOffset's bits
+                               kBits, kBits, kBits, kBits, kBits, kBits, kBits, kBits};
     fence();
     wait_all();
     __syncthreads();
+
+    // The loop is a pipeline over block steps (4 a group: blocks (0,0), (0,1), (1,0), (1,1) of
+    // activation block i and weight block j). Step t issues block t's MFMAs (at even groups first
+    // its share of the offset) and rescales block t - 1, whose results arrived meanwhile; each
+    // MFMA is followed by a few of the rescale's FMAs in the issue order, so one wave keeps the
+    // matrix core and the VALU busy together. The next group's fragments are read from LDS at
+    // its first step and unpacked into the registers its blocks free: a[0] after step 1, b[0]
+    // after step 2, a[1] and b[1] after step 3.
+    i32x16 pp = seed;  // the block in flight: kOffset + P as int32 bits
+    f32x16 tp = {};    // its scale products
+    i32x4 a[2][2], b[2][2];  // [block][K half], unpacked 16·code bytes of the current group
+    f16x8 fa[2], fb[2];      // its scale operands
+    // One block step: MFMAs of block (I, J) of group G interleaved with the rescale of the
+    // block before it (PI, PJ), when there is one.
+#define COZYQ_STEP(G, I, J, PI, PJ, RESCALE_PREV)                                                   \
+    do {                                                                                            \
+        if constexpr (((G) & 1) == 0)                                                               \
+            facc[I][J] = COZYQ_OFF_MMA(ow[J], oa[I], facc[I][J]);                                   \
+        const i32x16 q_ = COZYQ_MMA(b[J][0], a[I][0], seed);                                        \
+        const i32x16 p_ = COZYQ_MMA(b[J][1], a[I][1], q_);                                          \
+        const f32x16 t_ = COZYQ_T(fb[J], fa[I]);                                                    \
+        if (RESCALE_PREV) COZYQ_RESCALE(pp, tp, PI, PJ);                                            \
+        pp = p_;                                                                                    \
+        tp = t_;                                                                                    \
+        if constexpr (((G) & 1) == 0) {                                                             \
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                      \
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);                                      \
+        }                                                                                           \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  /* MFMA */                              \
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  /* VALU */                              \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                          \
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);                                          \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                          \
+        __builtin_amdgcn_sched_group_barrier(0x002, 30, 0);                                         \
+        __builtin_amdgcn_sched_barrier(0);                                                          \
+    } while (0)
 
     for (int s = 0; s < nstages; ++s) {
         const bool more = s + 1 < nstages;
         if (more) COZYQ_SVDQ_ISSUE(s + 1);
         const uint8_t* buf = lds + (s & 1) * kStageBytes;
-        const uint32_t* sa_l = reinterpret_cast<const uint32_t*>(buf + 2 * kOpBytes);
-        const uint32_t* sw_l = reinterpret_cast<const uint32_t*>(buf + 2 * kOpBytes + kScaleBytes);
         // A stage past the last group holds zero codes and zero scales: it adds nothing.
-        //
-        // A group is two halves. Each issues the K halves of two blocks interleaved (no MFMA
-        // waits on the one before it) and their scale products at raised wave priority, so a
-        // SIMD's other wave keeps the matrix core fed, then rescales a finished block (one
-        // conversion and one FMA an output) while the matrix core works. The next group's
-        // fragments are read from LDS in the first half and unpacked in the second.
-        i32x4 a[2][2], b[2][2];  // [block][K half], unpacked 16·code bytes
-        {
+        // The offset operands of pair p (groups 2p, 2p + 1): -kOffset·sw of column block j and
+        // sa of row block i, lane group l/32 holding group 2p + l/32.
+        float ow[2], oa[2];
+        auto offsets = [&](int p) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                unpack16(*reinterpret_cast<const i32x4*>(buf + aoff[i][0]), a[i][0], a[i][1]);
-                unpack16(*reinterpret_cast<const i32x4*>(buf + boff[i][0]), b[i][0], b[i][1]);
+                ow[i] = -kOffset * half_at(s, 1, 2 * p + fq, sw_col + 32 * i);
+                oa[i] = half_at(s, 0, 2 * p + fq, sa_row + 32 * i);
             }
+        };
+        offsets(0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            unpack16(*reinterpret_cast<const i32x4*>(buf + aoff[i][0]), a[i][0], a[i][1]);
+            unpack16(*reinterpret_cast<const i32x4*>(buf + boff[i][0]), b[i][0], b[i][1]);
+            fa[i] = scale_frag(s, 0, 0, sa_row + 32 * i);
+            fb[i] = scale_frag(s, 1, 0, sw_col + 32 * i);
         }
 #pragma unroll
         for (int g = 0; g < kStageGroups; ++g) {
             constexpr int kLast = kStageGroups - 1;
+            const int gn = g < kLast ? g + 1 : g;
             i32x4 na[2], nb[2];
-            const f16x8 fa0 = scale_frag(sa_l, g * kTile + sa_row), fa1 = scale_frag(sa_l, g * kTile + sa_row + 32);
-            const f16x8 fb0 = scale_frag(sw_l, g * kTile + sw_col), fb1 = scale_frag(sw_l, g * kTile + sw_col + 32);
-            __builtin_amdgcn_s_setprio(1);
-            const i32x16 q00 = COZYQ_MMA(b[0][0], a[0][0], zero);
-            const i32x16 q01 = COZYQ_MMA(b[1][0], a[0][0], zero);
-            const i32x16 p00 = COZYQ_MMA(b[0][1], a[0][1], q00);
-            const i32x16 p01 = COZYQ_MMA(b[1][1], a[0][1], q01);
-            const f32x16 t00 = COZYQ_T(fb0, fa0);
-            const f32x16 t01 = COZYQ_T(fb1, fa0);
-            __builtin_amdgcn_s_setprio(0);
+            uint32_t nfa[2], nfb[2];  // the next group's scale bits
             if (g < kLast) {
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
-                    na[i] = *reinterpret_cast<const i32x4*>(buf + aoff[i][g < kLast ? g + 1 : g]);
-                    nb[i] = *reinterpret_cast<const i32x4*>(buf + boff[i][g < kLast ? g + 1 : g]);
+                    na[i] = *reinterpret_cast<const i32x4*>(buf + aoff[i][gn]);
+                    nb[i] = *reinterpret_cast<const i32x4*>(buf + boff[i][gn]);
+                    nfa[i] = scale_bits(s, 0, gn, sa_row + 32 * i) & keep;
+                    nfb[i] = scale_bits(s, 1, gn, sw_col + 32 * i) & keep;
                 }
             }
-            COZYQ_RESCALE(p00, t00, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_setprio(1);
-            const i32x16 q10 = COZYQ_MMA(b[0][0], a[1][0], zero);
-            const i32x16 q11 = COZYQ_MMA(b[1][0], a[1][0], zero);
-            const i32x16 p10 = COZYQ_MMA(b[0][1], a[1][1], q10);
-            const i32x16 p11 = COZYQ_MMA(b[1][1], a[1][1], q11);
-            const f32x16 t10 = COZYQ_T(fb0, fa1);
-            const f32x16 t11 = COZYQ_T(fb1, fa1);
-            __builtin_amdgcn_s_setprio(0);
-            COZYQ_RESCALE(p01, t01, 0, 1);
-            __builtin_amdgcn_sched_barrier(0);
-            COZYQ_RESCALE(p10, t10, 1, 0);
-            __builtin_amdgcn_sched_barrier(0);
+            if (g == 2) offsets(1);
+            switch (g) {  // (g is unrolled: each case is its own code)
+                case 0: COZYQ_STEP(0, 0, 0, 1, 1, s > 0); break;
+                case 1: COZYQ_STEP(1, 0, 0, 1, 1, true); break;
+                case 2: COZYQ_STEP(2, 0, 0, 1, 1, true); break;
+                default: COZYQ_STEP(3, 0, 0, 1, 1, true); break;
+            }
+            switch (g) {
+                case 0: COZYQ_STEP(0, 0, 1, 0, 0, true); break;
+                case 1: COZYQ_STEP(1, 0, 1, 0, 0, true); break;
+                case 2: COZYQ_STEP(2, 0, 1, 0, 0, true); break;
+                default: COZYQ_STEP(3, 0, 1, 0, 0, true); break;
+            }
+            switch (g) {
+                case 0: COZYQ_STEP(0, 1, 0, 0, 1, true); break;
+                case 1: COZYQ_STEP(1, 1, 0, 0, 1, true); break;
+                case 2: COZYQ_STEP(2, 1, 0, 0, 1, true); break;
+                default: COZYQ_STEP(3, 1, 0, 0, 1, true); break;
+            }
+            if (g < kLast) unpack16(na[0], a[0][0], a[0][1]);
+            switch (g) {
+                case 0: COZYQ_STEP(0, 1, 1, 1, 0, true); break;
+                case 1: COZYQ_STEP(1, 1, 1, 1, 0, true); break;
+                case 2: COZYQ_STEP(2, 1, 1, 1, 0, true); break;
+                default: COZYQ_STEP(3, 1, 1, 1, 0, true); break;
+            }
             if (g < kLast) {
+                unpack16(nb[0], b[0][0], b[0][1]);
+                unpack16(na[1], a[1][0], a[1][1]);
+                unpack16(nb[1], b[1][0], b[1][1]);
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
-                    unpack16(na[i], a[i][0], a[i][1]);
-                    unpack16(nb[i], b[i][0], b[i][1]);
+                    fa[i] = frag_of(nfa[i]);
+                    fb[i] = frag_of(nfb[i]);
                 }
             }
-            COZYQ_RESCALE(p11, t11, 1, 1);
-            __builtin_amdgcn_sched_barrier(0);
         }
         fence();
         wait_all();
         __syncthreads();
     }
+    COZYQ_RESCALE(pp, tp, 1, 1);  // the last block
+#undef COZYQ_STEP
 #undef COZYQ_SVDQ_ISSUE
 #undef COZYQ_MMA
+#undef COZYQ_OFF_MMA
 #undef COZYQ_T
 #undef COZYQ_RESCALE
 
@@ -509,7 +605,10 @@ hipError_t launch_gemm(const uint8_t* act, const uint16_t* ascales, const uint8_
                        const uint16_t* wscales, const void* la, const void* up, const void* bias,
                        void* out, int M, int N, int K, hipStream_t s) {
     const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTile - 1) / kTile;
-    svdq_gemm_kernel<kOutHalf, kBias, kR><<<tiles_m * tiles_n, kThreads, 0, s>>>(
+    const bool wide = (K / kGroup) % 8 == 0 && reinterpret_cast<uintptr_t>(ascales) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(wscales) % 16 == 0;
+    auto kernel = wide ? svdq_gemm_kernel<kOutHalf, kBias, kR, true> : svdq_gemm_kernel<kOutHalf, kBias, kR, false>;
+    kernel<<<tiles_m * tiles_n, kThreads, 0, s>>>(
         act, ascales, w, wscales, static_cast<const uint16_t*>(la),
         static_cast<const uint16_t*>(up), static_cast<const uint16_t*>(bias),
         static_cast<uint16_t*>(out), M, N, K, tiles_m, tiles_n);

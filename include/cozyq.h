@@ -489,8 +489,9 @@ int cozyq_probe_div(int device, const float* x, const float* s, float* out, int6
  * 1: f32_16x16x128_f8f6f4 e4m3 (64 lanes x 32 bytes); 2: the same with E8M0 scales sa, sb
  * (one byte a lane); 3: f32_16x16x32_bf16 (64 lanes x 16 bytes); 4: i32_32x32x32_i8 (64 lanes
  * x 16 bytes); 5: f32_32x32x64_f8f6f4 e4m3 (64 lanes x 32 bytes); 6: the same with E8M0
- * scales. a and b are read as 64 lanes x 32 bytes; d receives 64 lanes x 16 int32/float32
- * words (the 16x16 kinds fill the first 4). */
+ * scales; 7: f32_32x32x2_f32 (one float a lane, the first 4 bytes); 8: f32_32x32x16_f16 (64
+ * lanes x 16 bytes). a and b are read as 64 lanes x 32 bytes; d receives 64 lanes x 16
+ * int32/float32 words (the 16x16 kinds fill the first 4). */
 int cozyq_probe_mfma(int device, int kind, const void* a, const void* b, const void* sa,
                      const void* sb, void* d, void* stream);
 

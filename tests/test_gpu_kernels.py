@@ -134,7 +134,7 @@ def _probe(kind: int, a: np.ndarray, b: np.ndarray, sa=None, sb=None) -> np.ndar
     assert code == 0
     torch.cuda.synchronize()
     out = d.cpu().numpy()
-    return out if kind in (4, 5, 6) else out[:, :4].copy()
+    return out if kind in (4, 5, 6, 7, 8) else out[:, :4].copy()
 
 
 def _expand(lanes: np.ndarray, per_lane: int) -> np.ndarray:
@@ -308,6 +308,64 @@ def test_mfma_bf16_layout():
     want = _expand(a[:, :8].double().numpy(), 8) @ _expand(b[:, :8].double().numpy(), 8).T
     _check_layout(d.astype(np.float64), want, exact=False)
     del rng
+
+
+def _out32(d: np.ndarray, want: np.ndarray) -> list[tuple[int, int, float, float]]:
+    """(lane, register, got, want) wherever a 32x32 result misses `want` (register r of lane l
+    holds row 8·(r/4) + 4·(l/32) + r%4 of column l%32)."""
+    return [(lane, r, float(d[lane, r]), float(want[8 * (r // 4) + 4 * (lane // 32) + r % 4, lane % 32]))
+            for lane in range(64) for r in range(16)
+            if d[lane, r] != np.float32(want[8 * (r // 4) + 4 * (lane // 32) + r % 4, lane % 32])]  # fmt: skip
+
+
+def test_mfma_f32_32x32x2_layout_and_exact_products():
+    """32x32x2 f32: lane l supplies row (column) l%32 at K index l/32. Fed the svdq GEMM's offset
+    operands (-1.5·2^23·sw with 12 significant bits, sa with 11), each product is exact in float32
+    and the two-term sum is rounded once: every output equals float32 of the float64 sum."""
+    rng = np.random.default_rng(7)
+    sw = rng.uniform(0.004, 0.02, 64).astype(np.float16).astype(np.float64)
+    sa = rng.uniform(0.3, 8.0, 64).astype(np.float16).astype(np.float64)
+    a = np.zeros((64, 8), np.float32)
+    b = np.zeros((64, 8), np.float32)
+    a[:, 0] = -12582912.0 * sw
+    b[:, 0] = sa
+    assert np.array_equal(a[:, 0].astype(np.float64), -12582912.0 * sw)
+    d = _probe(7, a, b).view(np.float32)
+    mat_a = np.zeros((32, 2))
+    mat_b = np.zeros((2, 32))
+    for lane in range(64):
+        mat_a[lane % 32, lane // 32] = a[lane, 0]
+        mat_b[lane // 32, lane % 32] = b[lane, 0]
+    misses = _out32(d, mat_a @ mat_b)
+    assert not misses, (len(misses), misses[:4])
+
+
+def test_mfma_f16_32x32x16_layout():
+    """32x32x16 f16: lane l supplies row (column) l%32 and K slice 8·(l/32).. +8; every product
+    of two fp16 values is exact in float32, so with one nonzero k the output is exact."""
+    rng = np.random.default_rng(8)
+    a = rng.uniform(-4, 4, (64, 16)).astype(np.float16)
+    b = rng.uniform(-4, 4, (64, 16)).astype(np.float16)
+    a[:, 8:] = 0
+    b[:, 8:] = 0
+    d = _probe(8, a, b).view(np.float32).astype(np.float64)
+    mat_a = np.zeros((32, 16))
+    mat_b = np.zeros((16, 32))
+    for lane in range(64):
+        mat_a[lane % 32, 8 * (lane // 32):8 * (lane // 32) + 8] = a[lane, :8]
+        mat_b[8 * (lane // 32):8 * (lane // 32) + 8, lane % 32] = b[lane, :8]
+    want = mat_a @ mat_b
+    for lane in range(64):
+        for r in range(16):
+            ref = want[8 * (r // 4) + 4 * (lane // 32) + r % 4, lane % 32]
+            assert abs(d[lane, r] - ref) <= 1e-6 * (1 + abs(ref)), (lane, r)
+    one = np.zeros((64, 16), np.float16)
+    other = np.zeros((64, 16), np.float16)
+    one[:32, 0] = a[:32, 0]  # K = 1: lane group 0's element 0
+    other[:32, 0] = b[:32, 0]
+    d1 = _probe(8, one, other).view(np.float32)
+    want1 = np.outer(one[:32, 0].astype(np.float64), other[:32, 0].astype(np.float64))
+    assert not _out32(d1, want1)
 
 
 # ------------------------------------------------------------------------ int8 lane
