@@ -470,8 +470,11 @@ constexpr int kIRows = 4;
 constexpr int kIXLoads = 24;
 
 template <bool kXHalf, bool kOutHalf, bool kBias, int kM, int kChunks>
+// (x is deliberately not __restrict__: loads through a read-only restrict argument count as
+// invariant, and the compiler sank them below the weight stream into the blocks that use them,
+// so the rotation's first wait, in-order, waited for every weight load of the batch.)
 __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
-    const uint16_t* __restrict__ x, const int8_t* __restrict__ W, const float* __restrict__ ws,
+    const uint16_t* x, const int8_t* __restrict__ W, const float* __restrict__ ws,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int N, int K) {
     static_assert(kM * kChunks <= kIXLoads, "activation registers");
     using L = Layout<256>;
