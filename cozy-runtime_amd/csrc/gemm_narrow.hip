@@ -45,18 +45,30 @@ struct W4 {
     const float* codebook;  // null: the uniform grid
 };
 
+// The 16 levels of a codebook (null: the uniform grid q − 8).
+__device__ __forceinline__ void w4_levels(const float* codebook, float (&book)[16]) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) book[c] = codebook != nullptr ? codebook[c] : static_cast<float>(c - 8);
+}
+
 // T[b][c] for b = the calling thread's index (256 threads), as 16 bytes at table + 16·b.
-__device__ __forceinline__ void w4_table_row(const float* codebook, uint32_t* table, int b) {
+__device__ __forceinline__ void w4_table_row(const float (&book)[16], uint32_t* table, int b) {
     const float e = e4m3_value(static_cast<uint32_t>(b));
     uint32_t words[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-        const float level = codebook != nullptr ? codebook[c] : static_cast<float>(c - 8);
+        const float level = book[c];
         float r = __builtin_rintf(level * e);  // torch.round: half to even
         r = __builtin_isnan(r) ? 0.0f : fminf(fmaxf(r, -127.0f), 127.0f);
         words[c / 4] |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int>(r))) << (8 * (c % 4));
     }
     *reinterpret_cast<uint4*>(table + 4 * b) = make_uint4(words[0], words[1], words[2], words[3]);
+}
+
+__device__ __forceinline__ void w4_table_row(const float* codebook, uint32_t* table, int b) {
+    float book[16];
+    w4_levels(codebook, book);
+    w4_table_row(book, table, b);
 }
 
 // 16 codes (8 bytes, k order) of one group with scale byte b -> their 16 int8 levels (k order),
@@ -516,6 +528,8 @@ constexpr int kW4Rows = 4;       // weight rows a wave
 constexpr int kW4Batch = 2;      // 1 KiB code spans of each row in flight
 constexpr int kW4MaxK = 8192;    // activation rows a thread stages: K ≤ this
 constexpr int kW4Policy = 3;     // sc0 nt: each code byte is read once per call
+constexpr int kW4RowsMax = 16;   // rows the row-tile form takes (one MFMA's B columns)
+constexpr uint32_t kFarW4 = 0x7fff0000u;  // a buffer offset past every resource here (reads 0)
 
 template <bool kOutHalf, bool kBias, int kM>
 __global__ __launch_bounds__(64 * kW4Waves) void w4a8_decode_kernel(
@@ -641,6 +655,127 @@ __global__ __launch_bounds__(64 * kW4Waves) void w4a8_decode_kernel(
     }
 }
 
+// The w4a8.convrot linear for 5..16 quantized rows: one 16-row weight tile a workgroup, its K
+// split over kW4RWaves waves, on the plain v_mfma_i32_16x16x64_i8 (A = 16 weight rows, B = the
+// activation rows, zero past M). Lane l (row r = l%16, part g = l/16) of a wave loads 16
+// contiguous code bytes of weight row r per 128-code step t (codes 128t + 32g .. + 32: two
+// groups, whose two scale bytes are adjacent) and the same 32 activation elements of row r in
+// two 16-byte pieces, so each of the step's two MFMAs meets A and B on the same 16 k's; the 4
+// lanes of a row read 64 contiguous bytes. Every load is issued before the level table is
+// built; steps past a wave's share read zeros (activation zeros make them add nothing). The
+// waves' int32 partials meet in LDS (exact, in any order), and the epilogue is the int8 law's,
+// so the outputs equal every tile config's bit for bit.
+constexpr int kW4RWaves = 4;
+
+template <bool kOutHalf, bool kBias, int kSteps>
+__global__ __launch_bounds__(64 * kW4RWaves) void w4a8_rows_kernel(
+    const int8_t* q, const float* xs, const uint8_t* codes, W4 w4, const float* ws,
+    const uint16_t* bias, uint16_t* out, int M, int N, int K) {
+    // (No pointer here is __restrict__: loads through restrict read-only arguments count as
+    // invariant and may be sunk below later loads; these must stay in issue order.)
+    __shared__ __attribute__((aligned(16))) uint32_t table[256 * 4];
+    __shared__ i32x4 part[kW4RWaves][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int steps = K / 128;  // K % 256 == 0
+    const int t0 = wave * steps / kW4RWaves, t1 = (wave + 1) * steps / kW4RWaves;
+
+    // 0. The codebook's levels ahead of the streams: the table is built once they are issued,
+    //    and a wait for a load issued after them would wait for every one of them (in order).
+    float book[16];
+    w4_levels(w4.codebook, book);
+    asm volatile("" ::: "memory");
+
+    // 1. The activation pieces: row r, elements 128t + 32g + 16h .. + 16 (zeros past M or the
+    //    wave's steps).
+    const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(q), 0, M * K, 0x00020000);
+    i32x4 xb[kSteps][2];
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int t = t0 + j;
+            const uint32_t off = t < t1 && r < M ? static_cast<uint32_t>(r * K + 128 * t + 32 * g + 16 * h) : kFarW4;
+            xb[j][h] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
+        }
+    asm volatile("" ::: "memory");
+
+    // 2. The codes (16 bytes a lane a step, non-temporal) and the two group-scale bytes.
+    const int64_t rows_bytes = static_cast<int64_t>(N - n0) * (K / 2);
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(codes + static_cast<int64_t>(n0) * (K / 2)), 0,
+        rows_bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(rows_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(w4.group_scale + static_cast<int64_t>(n0) * (K / 16)), 0,
+        static_cast<int>(static_cast<int64_t>(N - n0) * (K / 16)), 0x00020000);
+    uint4 cv[kSteps];
+    uint16_t gv[kSteps];  // (16-bit: widened at its use, not ahead of the barrier)
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+        const int t = t0 + j;
+        const bool live = t < t1 && n0 + r < N;
+        cv[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+            cr, live ? static_cast<uint32_t>(r * (K / 2) + 64 * t + 16 * g) : kFarW4, 0, kW4Policy));
+        gv[j] = __builtin_amdgcn_raw_buffer_load_b16(gr, live ? static_cast<uint32_t>(r * (K / 16) + 8 * t + 2 * g) : kFarW4, 0, 0);
+    }
+
+    // 3. The level table (row tid); a bare barrier (a full one would also wait for the loads).
+    w4_table_row(book, table, tid);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    // 4. Products over the wave's steps.
+    i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+        const uint32_t sb = gv[j];
+        const i32x4 l0 = __builtin_bit_cast(i32x4, w4_unpack16(cv[j].x, cv[j].y, table, sb & 0xffu));
+        const i32x4 l1 = __builtin_bit_cast(i32x4, w4_unpack16(cv[j].z, cv[j].w, table, sb >> 8));
+        acc = mfma_i8(l0, xb[j][0], acc);
+        acc = mfma_i8(l1, xb[j][1], acc);
+    }
+
+    // 5. The waves' partials (lane l: activation row l%16, weight rows 4·(l/16) + 0..3), then
+    //    (acc·xs)·ws, cast, + bias in the output dtype (internal/int8_linear.py:445-448, :276).
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 1; w < kW4RWaves; ++w) acc += part[w][lane];
+    const int n = n0 + 4 * g;
+    if (r >= M || n >= N) return;  // N % 8 == 0: a lane's four rows are all in or all out
+    uint32_t o[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float v = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), xs[r]), ws[n + i]);
+        uint32_t h = ::cozyq::narrow<kOutHalf>(v);
+        if constexpr (kBias)
+            h = ::cozyq::narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(bias[n + i])));
+        o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
+    }
+    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(r) * N + n) = make_uint2(o[0], o[1]);
+}
+
+template <bool kOutHalf, bool kBias>
+hipError_t launch_w4a8_rows(const int8_t* q, const float* xs, const uint8_t* codes, W4 w4, const float* ws,
+                            const void* bias, void* out, int M, int N, int K, hipStream_t s) {
+    const int blocks = (N + 15) / 16;
+    const int per_wave = (K / 128 + kW4RWaves - 1) / kW4RWaves;
+    const auto* b = static_cast<const uint16_t*>(bias);
+    auto* o = static_cast<uint16_t*>(out);
+    if (per_wave <= 4)
+        w4a8_rows_kernel<kOutHalf, kBias, 4><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
+    else if (per_wave <= 8)
+        w4a8_rows_kernel<kOutHalf, kBias, 8><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
+    else
+        w4a8_rows_kernel<kOutHalf, kBias, 16><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
+    return hipGetLastError();
+}
+
 template <bool kOutHalf, bool kBias>
 hipError_t launch_w4a8_decode(const int8_t* q, const float* xs, const uint8_t* codes, W4 w4, const float* ws,
                               const void* bias, void* out, int M, int N, int K, hipStream_t s) {
@@ -663,7 +798,8 @@ hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* cod
                             const uint8_t* group_scale, const float* codebook, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
                             int config, hipStream_t s) {
-    // 1..4 rows by shape: the GEMV form (the same bits as every tile config).
+    // 1..4 rows by shape: the GEMV form; 5..16 the row-tile kernel (the same bits as every tile
+    // config).
     if (config < 0 && M <= 4 && K <= kW4MaxK) {
         const W4 w4{group_scale, codebook};
         if (out_half)
@@ -671,6 +807,14 @@ hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* cod
                         : launch_w4a8_decode<true, false>(q, xs, codes, w4, ws, bias, out, M, N, K, s);
         return bias ? launch_w4a8_decode<false, true>(q, xs, codes, w4, ws, bias, out, M, N, K, s)
                     : launch_w4a8_decode<false, false>(q, xs, codes, w4, ws, bias, out, M, N, K, s);
+    }
+    if (config < 0 && M <= kW4RowsMax && K <= kW4MaxK) {
+        const W4 w4{group_scale, codebook};
+        if (out_half)
+            return bias ? launch_w4a8_rows<true, true>(q, xs, codes, w4, ws, bias, out, M, N, K, s)
+                        : launch_w4a8_rows<true, false>(q, xs, codes, w4, ws, bias, out, M, N, K, s);
+        return bias ? launch_w4a8_rows<false, true>(q, xs, codes, w4, ws, bias, out, M, N, K, s)
+                    : launch_w4a8_rows<false, false>(q, xs, codes, w4, ws, bias, out, M, N, K, s);
     }
     return narrow<true, true>(reinterpret_cast<const uint8_t*>(q), xs, codes, ws, bias, out, N,
                               out_half, M, N, K, 0, config < 0 ? narrow_config(M, N) : config, s,
