@@ -489,5 +489,210 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
 
 #undef COZYQ_ISSUE
 
+// ---------------------------------------------------------------- int8 256x256 with 8 waves
+//
+// The int8 256x256 tile with the law's epilogue runs as 8 waves, two a SIMD: wave w owns X rows
+// 128·(w/4).. (4 blocks of 32) and W rows 64·(w%4).. (2 blocks), 128 accumulators, so two waves
+// fit a SIMD's registers. A SIMD's second wave issues while the first waits (on LDS reads, the
+// pair barrier) and the epilogue's VALU work comes from both: C2 (4096 x 12288 x 3072, bias +
+// GELU) 168-170 -> 155-156 us on one box, outputs bit-identical to the 4-wave tile (int32 sums
+// are exact in any order). Each wave reads 1.5x the fragment bytes a 4-wave quadrant does per
+// MFMA, within the LDS's rate. Fragments are fetched a K half (32 bytes) at a time, one half
+// ahead, so the two halves' registers and the accumulators stay within 256.
+constexpr int kThreads8 = 512;
+constexpr int kStageRow8 = 64 * 2 + 16;                 // staged output row: 64 outputs + pad
+constexpr int kStageBytes8 = 128 * kStageRow8;          // one wave's staged 128 x 64
+constexpr int kEpiBase8 = 8 * kStageBytes8 > 2 * kPairBytes ? 8 * kStageBytes8 : 2 * kPairBytes;
+constexpr int kWsOff8 = kEpiBase8, kBiasOff8 = kEpiBase8 + 1024, kXsOff8 = kEpiBase8 + 1536;
+constexpr int kLdsBytes8 = kEpiBase8 + 2560;
+constexpr int kLoads8 = 8;                              // LDS-DMA loads a wave a pair (4 X, 4 W)
+static_assert(kLdsBytes8 <= 160 * 1024, "one workgroup's LDS");
+
+template <bool kOutHalf, bool kBias, int kEpi>
+__device__ __forceinline__ void gemm_tile8(
+    uint8_t* __restrict__ lds, const uint8_t* __restrict__ X, const uint8_t* __restrict__ W,
+    const float* __restrict__ xs, const float* __restrict__ ws, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ out, int64_t ldo, int M, int N, int K, int tm, int tn) {
+    static_assert(kEpi == 0 || kEpi == 1, "the law's epilogue, optionally tanh-GELU");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int m0 = __builtin_amdgcn_readfirstlane(tm * kTile);
+    const int n0 = __builtin_amdgcn_readfirstlane(tn * kTile);
+    auto rows_view = [&](const uint8_t* base, int rows_left, int row_bytes) {
+        const int64_t span = static_cast<int64_t>(rows_left) * row_bytes;
+        const uint32_t bytes = span > 0x7fffffff ? 0x7fffffffu : static_cast<uint32_t>(span);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, bytes, 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t xr = rows_view(X + static_cast<int64_t>(m0) * K, M - m0, K);
+    const __amdgpu_buffer_rsrc_t wr = rows_view(W + static_cast<int64_t>(n0) * K, N - n0, K);
+
+    // Load j (0..3) of a wave fills rows [(8j + wave)·8, +8) of each operand's buffer, whole
+    // 128-byte lines as the 4-wave tile's loads do.
+    int rowoff[4], chunk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = (8 * j + wave) * 8 + (lane >> 3);
+        chunk[j] = 16 * swz(r, lane & 7);
+        rowoff[j] = r * K + chunk[j];
+    }
+    auto issue = [&](int pair) {
+        uint8_t* buf = lds + (pair & 1) * kPairBytes;
+        const int k0 = pair * kPairK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t off = (k0 + chunk[j] < K) ? static_cast<uint32_t>(rowoff[j] + k0) : kOutOfRange;
+            const int base = (8 * j + wave) * 1024;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (LdsPtr*)(buf + base), 16, off, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LdsPtr*)(buf + kOpBytes + base), 16, off, 0, 0, 0);
+        }
+    };
+
+    // Half q = 2·step + h: step parity e picks the buffer's chunks 4e + 2h + l/32; step s reads
+    // buffer (s/2) % 2.
+    const int fr = lane & 31, fq = lane >> 5;
+    struct Half { i32x4 a[2], b[4]; };
+    auto fetch = [&](int q, Half& f) {
+        const int step = q >> 1, h = q & 1, e = step & 1;
+        const uint8_t* buf = lds + ((step >> 1) & 1) * kPairBytes;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int rw = wn * 64 + i * 32 + fr;
+            f.a[i] = *reinterpret_cast<const i32x4*>(buf + kOpBytes + rw * kPairK + 16 * swz(rw, 4 * e + 2 * h + fq));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int rx = wm * 128 + j * 32 + fr;
+            f.b[j] = *reinterpret_cast<const i32x4*>(buf + rx * kPairK + 16 * swz(rx, 4 * e + 2 * h + fq));
+        }
+    };
+
+    i32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    // The epilogue's operands first (waves 0-3 cover the tile's 256 columns and rows).
+    if (wave < 4) {
+        const int c = 64 * wave + lane;
+        const auto wsr = rows_view(reinterpret_cast<const uint8_t*>(ws + n0), N - n0, 4);
+        const auto xsr = rows_view(reinterpret_cast<const uint8_t*>(xs + m0), M - m0, 4);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, (LdsPtr*)(lds + kWsOff8 + 256 * wave), 4, 4 * c, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xsr, (LdsPtr*)(lds + kXsOff8 + 256 * wave), 4, 4 * c, 0, 0, 0);
+        if constexpr (kBias) {
+            if (wave < 2) {
+                const auto br = rows_view(reinterpret_cast<const uint8_t*>(bias + n0), N - n0, 2);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (LdsPtr*)(lds + kBiasOff8 + 256 * wave), 4, 4 * c, 0, 0, 0);
+            }
+        }
+    }
+    const int np = (K + kPairK - 1) / kPairK;
+    issue(0);
+    issue(1);
+    fence();
+    wait_vmcnt<kLoads8>();  // pair 0 (and the epilogue operands ahead of it) complete
+    __builtin_amdgcn_s_barrier();
+    fence();
+
+    auto mfmas = [&](const Half& c) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(c.a[i], c.b[j], acc[i][j], 0, 0, 0);
+    };
+    Half f0, f1;
+    fetch(0, f0);
+    // Pair p: halves 4p .. 4p + 3, each fetching the next while its MFMAs run. Before the last,
+    // pair p + 1 must have landed and every wave's reads of pair p be done: the workgroup meets,
+    // pair p + 2 refills buffer p % 2, and the next half comes from buffer (p + 1) % 2. Past the
+    // last pair the loads read zeros into a buffer nothing reads.
+    __builtin_amdgcn_s_setprio(1);
+    for (int p = 0; p < np; ++p) {
+        const int q = 4 * p;
+        fetch(q + 1, f1);
+        mfmas(f0);
+        fetch(q + 2, f0);
+        mfmas(f1);
+        fetch(q + 3, f1);
+        mfmas(f0);
+        fence();
+        wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier();
+        fence();
+        issue(p + 2);
+        fetch(q + 4, f0);
+        mfmas(f1);
+    }
+    __builtin_amdgcn_s_setprio(0);
+
+    // Epilogue: the 4-wave tile's, on the wave's 128 x 64 (block (i, j): lane holds out[m][n]
+    // for m = j-block row l%32, n = i-block column 8·(r/4) + 4·(l/32) + r%4).
+    fence();
+    wait_vmcnt<0>();
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    fence();
+    const int nl = n0 + wn * 64 + 4 * fq;
+    float4 wsv[2][4];
+    uint2 bv[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int c = nl - n0 + i * 32 + 8 * g;
+            wsv[i][g] = *reinterpret_cast<const float4*>(lds + kWsOff8 + 4 * c);
+            if constexpr (kBias) bv[i][g] = *reinterpret_cast<const uint2*>(lds + kBiasOff8 + 2 * c);
+        }
+    float xsv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xsv[j] = *reinterpret_cast<const float*>(lds + kXsOff8 + 4 * (wm * 128 + j * 32 + fr));
+    uint8_t* stage = lds + wave * kStageBytes8;
+    const int cl = (lane & 7) * 8;  // first of the lane's 8 columns in a stored row
+    const int n = n0 + wn * 64 + cl;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ml = j * 32 + fr;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float w4[4] = {wsv[i][g].x, wsv[i][g].y, wsv[i][g].z, wsv[i][g].w};
+                const uint2 b2 = kBias ? bv[i][g] : make_uint2(0, 0);
+                // internal/int8_linear.py:445-448: (acc·xs)·ws, each product rounded to float32.
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    v[r] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][4 * g + r]), xsv[j]), w4[r]);
+                const uint2 packed = make_uint2(finish2<kOutHalf, kBias, kEpi>(v[0], v[1], b2.x),
+                                                finish2<kOutHalf, kBias, kEpi>(v[2], v[3], b2.y));
+                *reinterpret_cast<uint2*>(stage + ml * kStageRow8 + 2 * (i * 32 + 8 * g + 4 * fq)) = packed;
+            }
+        wait_lgkmcnt0();  // a wave reads back only its own rows
+        // Whole rows: 8 lanes cover one row's 128 bytes, 8 rows an instruction.
+#pragma unroll
+        for (int r0 = 0; r0 < 32; r0 += 8) {
+            const int rl = j * 32 + r0 + (lane >> 3);
+            const int m = m0 + wm * 128 + rl;
+            const uint4 v = *reinterpret_cast<const uint4*>(stage + rl * kStageRow8 + 2 * cl);
+            if (m < M && n < N) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * ldo + n) = v;
+        }
+    }
+}
+
+template <bool kOutHalf, bool kBias, int kEpi>
+__global__ __launch_bounds__(kThreads8, 1) void gemm8_kernel(
+    const uint8_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ xs,
+    const float* __restrict__ ws, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
+    int64_t ldo, int M, int N, int K, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes8];
+    const int2 t = launch_tile(blockIdx.x, tiles_m, tiles_n);
+    gemm_tile8<kOutHalf, kBias, kEpi>(lds, X, W, xs, ws, bias, out, ldo, M, N, K, t.x, t.y);
+}
+
 }  // namespace
 }  // namespace cozyq
