@@ -10,8 +10,8 @@ hipError_t launch(const void* q, const float* xs, const void* w, const float* ws
                   const uint8_t* xe, const uint8_t* we, const void* bias, void* out,
                   int32_t* acc, int64_t ldo, int M, int N, int K, hipStream_t s) {
     const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTN - 1) / kTN;
-    if constexpr (kKind == kInt8 && kTN == 256 && kEpi != 2) {  // the 8-wave tile
-        gemm8_kernel<kOutHalf, kBias, kEpi><<<tiles_m * tiles_n, kThreads8, 0, s>>>(
+    if constexpr (kKind != kMx && kTN == 256 && kEpi != 2) {  // the 8-wave tile
+        gemm8_kernel<kKind, kOutHalf, kBias, kEpi><<<tiles_m * tiles_n, kThreads8, 0, s>>>(
             static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(w), xs, ws,
             static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, M, N, K, tiles_m, tiles_n);
         return hipGetLastError();

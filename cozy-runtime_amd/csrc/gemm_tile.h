@@ -491,7 +491,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
 
 // ---------------------------------------------------------------- int8 256x256 with 8 waves
 //
-// The int8 256x256 tile with the law's epilogue runs as 8 waves, two a SIMD: wave w owns X rows
+// The int8 and fp8 256x256 tiles with the law's epilogue run as 8 waves, two a SIMD: wave w owns X rows
 // 128·(w/4).. (4 blocks of 32) and W rows 64·(w%4).. (2 blocks), 128 accumulators, so two waves
 // fit a SIMD's registers. A SIMD's second wave issues while the first waits (on LDS reads, the
 // pair barrier) and the epilogue's VALU work comes from both: C2 (4096 x 12288 x 3072, bias +
@@ -508,12 +508,14 @@ constexpr int kLdsBytes8 = kEpiBase8 + 2560;
 constexpr int kLoads8 = 8;                              // LDS-DMA loads a wave a pair (4 X, 4 W)
 static_assert(kLdsBytes8 <= 160 * 1024, "one workgroup's LDS");
 
-template <bool kOutHalf, bool kBias, int kEpi>
+template <int kKind, bool kOutHalf, bool kBias, int kEpi>
 __device__ __forceinline__ void gemm_tile8(
     uint8_t* __restrict__ lds, const uint8_t* __restrict__ X, const uint8_t* __restrict__ W,
     const float* __restrict__ xs, const float* __restrict__ ws, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ out, int64_t ldo, int M, int N, int K, int tm, int tn) {
     static_assert(kEpi == 0 || kEpi == 1, "the law's epilogue, optionally tanh-GELU");
+    static_assert(kKind == kInt8 || kKind == kFp8, "int8 and fp8 (MX keeps the 4-wave tile)");
+    typedef std::conditional_t<kKind == kInt8, i32x16, f32x16> Acc;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3;
@@ -548,26 +550,22 @@ __device__ __forceinline__ void gemm_tile8(
         }
     };
 
-    // Half q = 2·step + h: step parity e picks the buffer's chunks 4e + 2h + l/32; step s reads
-    // buffer (s/2) % 2.
+    // int8: half q = 2·step + h reads the buffer's chunks 4e + 2h + l/32 (e the step's parity;
+    // step s reads buffer (s/2) % 2), one 32-byte K half of the i8 MFMA. fp8: a step's 64 bytes
+    // (chunks 4e + l/32 and 4e + 2 + l/32: the f8 MFMA's K = 64 operand) in two pieces, W blocks
+    // with X blocks 0-1, then X blocks 2-3 on the same W fragments.
     const int fr = lane & 31, fq = lane >> 5;
-    struct Half { i32x4 a[2], b[4]; };
-    auto fetch = [&](int q, Half& f) {
-        const int step = q >> 1, h = q & 1, e = step & 1;
-        const uint8_t* buf = lds + ((step >> 1) & 1) * kPairBytes;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int rw = wn * 64 + i * 32 + fr;
-            f.a[i] = *reinterpret_cast<const i32x4*>(buf + kOpBytes + rw * kPairK + 16 * swz(rw, 4 * e + 2 * h + fq));
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int rx = wm * 128 + j * 32 + fr;
-            f.b[j] = *reinterpret_cast<const i32x4*>(buf + rx * kPairK + 16 * swz(rx, 4 * e + 2 * h + fq));
-        }
+    auto frag_at = [&](int step, int h, bool w_side, int block) {
+        const uint8_t* buf = lds + ((step >> 1) & 1) * kPairBytes + (w_side ? kOpBytes : 0);
+        const int row = w_side ? wn * 64 + block * 32 + fr : wm * 128 + block * 32 + fr;
+        return *reinterpret_cast<const i32x4*>(buf + row * kPairK + 16 * swz(row, 4 * (step & 1) + 2 * h + fq));
+    };
+    auto frag8_at = [&](int step, bool w_side, int block) {
+        const i32x4 lo = frag_at(step, 0, w_side, block), hi = frag_at(step, 1, w_side, block);
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     };
 
-    i32x16 acc[2][4];
+    Acc acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -596,37 +594,81 @@ __device__ __forceinline__ void gemm_tile8(
     wait_vmcnt<kLoads8>();  // pair 0 (and the epilogue operands ahead of it) complete
     __builtin_amdgcn_s_barrier();
     fence();
-
-    auto mfmas = [&](const Half& c) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(c.a[i], c.b[j], acc[i][j], 0, 0, 0);
-    };
-    Half f0, f1;
-    fetch(0, f0);
-    // Pair p: halves 4p .. 4p + 3, each fetching the next while its MFMAs run. Before the last,
-    // pair p + 1 must have landed and every wave's reads of pair p be done: the workgroup meets,
-    // pair p + 2 refills buffer p % 2, and the next half comes from buffer (p + 1) % 2. Past the
-    // last pair the loads read zeros into a buffer nothing reads.
-    __builtin_amdgcn_s_setprio(1);
-    for (int p = 0; p < np; ++p) {
-        const int q = 4 * p;
-        fetch(q + 1, f1);
-        mfmas(f0);
-        fetch(q + 2, f0);
-        mfmas(f1);
-        fetch(q + 3, f1);
-        mfmas(f0);
+    // Pair p: before its last piece, pair p + 1 must have landed and every wave's reads of pair
+    // p be done: the workgroup meets, pair p + 2 refills buffer p % 2, and the next piece comes
+    // from buffer (p + 1) % 2. Past the last pair the loads read zeros into a buffer nothing reads.
+    auto meet = [&](int p) {
         fence();
         wait_vmcnt<0>();
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
         fence();
         issue(p + 2);
-        fetch(q + 4, f0);
-        mfmas(f1);
+    };
+    __builtin_amdgcn_s_setprio(1);
+    if constexpr (kKind == kInt8) {
+        struct Half { i32x4 a[2], b[4]; };
+        auto fetch = [&](int q, Half& f) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) f.a[i] = frag_at(q >> 1, q & 1, true, i);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f.b[j] = frag_at(q >> 1, q & 1, false, j);
+        };
+        auto mfmas = [&](const Half& c) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(c.a[i], c.b[j], acc[i][j], 0, 0, 0);
+        };
+        Half f0, f1;
+        fetch(0, f0);
+        for (int p = 0; p < np; ++p) {
+            const int q = 4 * p;
+            fetch(q + 1, f1);
+            mfmas(f0);
+            fetch(q + 2, f0);
+            mfmas(f1);
+            fetch(q + 3, f1);
+            mfmas(f0);
+            meet(p);
+            fetch(q + 4, f0);
+            mfmas(f1);
+        }
+    } else {
+        // W fragments of two steps alternate (wa0 for even steps, wa1 for odd); xb holds the X
+        // blocks of the piece running, xn those fetched for the next.
+        i32x8 wa0[2], wa1[2], xb[2], xn[2];
+        auto mfmas = [&](const i32x8 (&a)[2], const i32x8 (&b)[2], int j0) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j0 + j] = mfma_f8_32(a[i], b[j], acc[i][j0 + j]);
+        };
+#pragma unroll
+        for (int i = 0; i < 2; ++i) wa0[i] = frag8_at(0, true, i);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) xb[j] = frag8_at(0, false, j);
+        for (int p = 0; p < np; ++p) {
+            const int s0 = 2 * p, s1 = 2 * p + 1;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) xn[j] = frag8_at(s0, false, 2 + j);
+            mfmas(wa0, xb, 0);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) wa1[i] = frag8_at(s1, true, i);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) xb[j] = frag8_at(s1, false, j);
+            mfmas(wa0, xn, 2);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) xn[j] = frag8_at(s1, false, 2 + j);
+            mfmas(wa1, xb, 0);
+            meet(p);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) wa0[i] = frag8_at(s1 + 1, true, i);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) xb[j] = frag8_at(s1 + 1, false, j);
+            mfmas(wa1, xn, 2);
+        }
     }
     __builtin_amdgcn_s_setprio(0);
 
@@ -663,13 +705,27 @@ __device__ __forceinline__ void gemm_tile8(
             for (int g = 0; g < 4; ++g) {
                 const float w4[4] = {wsv[i][g].x, wsv[i][g].y, wsv[i][g].z, wsv[i][g].w};
                 const uint2 b2 = kBias ? bv[i][g] : make_uint2(0, 0);
-                // internal/int8_linear.py:445-448: (acc·xs)·ws, each product rounded to float32.
                 float v[4];
+                uint2 packed;
+                if constexpr (kKind == kInt8) {
+                    // internal/int8_linear.py:445-448: (acc·xs)·ws, each product rounded to float32.
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    v[r] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][4 * g + r]), xsv[j]), w4[r]);
-                const uint2 packed = make_uint2(finish2<kOutHalf, kBias, kEpi>(v[0], v[1], b2.x),
-                                                finish2<kOutHalf, kBias, kEpi>(v[2], v[3], b2.y));
+                    for (int r = 0; r < 4; ++r)
+                        v[r] = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][4 * g + r]), xsv[j]), w4[r]);
+                    packed = make_uint2(finish2<kOutHalf, kBias, kEpi>(v[0], v[1], b2.x),
+                                        finish2<kOutHalf, kBias, kEpi>(v[2], v[3], b2.y));
+                } else {
+                    // internal/fp8_linear.py:92-111: (acc·xs)·ws + bias in float32, one rounding.
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v[r] = __fmul_rn(__fmul_rn(acc[i][j][4 * g + r], xsv[j]), w4[r]);
+                    if constexpr (kBias) {
+                        v[0] = __fadd_rn(v[0], low_of<kOutHalf>(b2.x));
+                        v[1] = __fadd_rn(v[1], high_of<kOutHalf>(b2.x));
+                        v[2] = __fadd_rn(v[2], low_of<kOutHalf>(b2.y));
+                        v[3] = __fadd_rn(v[3], high_of<kOutHalf>(b2.y));
+                    }
+                    packed = make_uint2(finish2_float<kOutHalf, kEpi>(v[0], v[1]), finish2_float<kOutHalf, kEpi>(v[2], v[3]));
+                }
                 *reinterpret_cast<uint2*>(stage + ml * kStageRow8 + 2 * (i * 32 + 8 * g + 4 * fq)) = packed;
             }
         wait_lgkmcnt0();  // a wave reads back only its own rows
@@ -684,14 +740,14 @@ __device__ __forceinline__ void gemm_tile8(
     }
 }
 
-template <bool kOutHalf, bool kBias, int kEpi>
+template <int kKind, bool kOutHalf, bool kBias, int kEpi>
 __global__ __launch_bounds__(kThreads8, 1) void gemm8_kernel(
     const uint8_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ xs,
     const float* __restrict__ ws, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
     int64_t ldo, int M, int N, int K, int tiles_m, int tiles_n) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes8];
     const int2 t = launch_tile(blockIdx.x, tiles_m, tiles_n);
-    gemm_tile8<kOutHalf, kBias, kEpi>(lds, X, W, xs, ws, bias, out, ldo, M, N, K, t.x, t.y);
+    gemm_tile8<kKind, kOutHalf, kBias, kEpi>(lds, X, W, xs, ws, bias, out, ldo, M, N, K, t.x, t.y);
 }
 
 }  // namespace
