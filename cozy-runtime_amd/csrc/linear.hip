@@ -10,7 +10,7 @@
 //
 // Work is split into `queues` job queues (one per XCD when workgroup b runs on XCD b mod 8, the
 // dispatch order on MI355X). Queue x owns M-tiles m with m mod queues == x:
-// - first the quantize jobs of all of them: 16 rows each, a wave per row, rows.h;
+// - first the quantize jobs of all of them: 16 rows each, two a wave (rows.h);
 // - then their output tiles, pair of M-tiles by pair, N fastest with the two M-tiles
 //   alternating, so an XCD's concurrent tiles share two X panels and their W panels in its L2.
 // A workgroup claims the next job of its queue with an atomic counter. Before its first tile it
@@ -30,11 +30,15 @@
 namespace cozyq {
 namespace {
 
-constexpr int kQRows = 16;          // rows a quantize job takes: 4 a wave
+constexpr int kQRows = 16;          // rows a quantize job takes: 2 a wave
 constexpr int kMaxQueues = 8;       // XCDs on MI355X
 constexpr int kSpinLimit = 1 << 24;  // s_sleep(2) rounds a tile waits at most (~1 s)
-constexpr int kJobSlot = kLdsBytes;  // LDS word that broadcasts a claimed job
-constexpr int kFusedLds = kLdsBytes + 16;
+constexpr int kJobSlot = kLdsBytes8;  // LDS word that broadcasts a claimed job
+constexpr int kFusedLds = kLdsBytes8 + 16;
+constexpr int kQWaveRows = kQRows / (kThreads8 / 64);  // a wave's rows of a quantize job
+static_assert(kThreads8 / 64 * kRowLdsFloats<128> * 4 <= kLdsBytes8 &&
+                  kThreads8 / 64 * kRowLdsFloats<256> * 4 <= kLdsBytes8,
+              "every wave's rotation slice fits the tile's LDS");
 
 // Workspace layout (int32): [0, 8) queue heads, [8] exit count, [9] fault flag (this launch),
 // [10] status (a launch since the last read gave up a wait), [16, 16 + tiles_m) quantize jobs
@@ -79,13 +83,13 @@ __device__ __forceinline__ Job decode(int j, int x, int queues, int tiles_m, int
     return {-1, 0, 0, 0};
 }
 
-// A wave's four rows r0 .. r0 + 3 of a quantize job (rows past M skipped), all four rows'
-// loads issued up front: at one wave a SIMD, one load latency for the job instead of one a row.
+// A wave's rows r0 .. r0 + kQWaveRows - 1 of a quantize job (rows past M skipped), their loads
+// issued up front: one load latency for the job instead of one a row.
 template <bool kHalf, int kRot>
 __device__ __forceinline__ void quantize_job(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
                                                        float* __restrict__ qs, int M, int K, int r0, int lane,
                                                        float* slice) {
-    constexpr int kWaveRows = kQRows / 4;
+    constexpr int kWaveRows = kQWaveRows;
     const int rows = min(kWaveRows, M - r0);
     uint4 raw[kWaveRows][kRowLoads];
 #pragma unroll
@@ -109,7 +113,7 @@ __device__ __forceinline__ void nan_tile(uint16_t* __restrict__ out, int64_t ldo
 }
 
 template <bool kHalf, int kRot, bool kOutHalf, bool kBias, int kEpi>
-__global__ __launch_bounds__(kThreads, 1) void linear_kernel(
+__global__ __launch_bounds__(kThreads8, 1) void linear_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ qs,
     const int8_t* __restrict__ W, const float* __restrict__ ws, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ out, int64_t ldo, int M, int N, int K, int tiles_m, int tiles_n,
@@ -130,7 +134,7 @@ __global__ __launch_bounds__(kThreads, 1) void linear_kernel(
         if (j >= total) break;
         const Job job = decode(j, qx, queues, tiles_m, tiles_n, M);
         if (job.kind == 0) {
-            quantize_job<kHalf, kRot>(x, q, qs, M, K, job.m * kTile + job.index * kQRows + wave * (kQRows / 4),
+            quantize_job<kHalf, kRot>(x, q, qs, M, K, job.m * kTile + job.index * kQRows + wave * kQWaveRows,
                                       lane, reinterpret_cast<float*>(lds) + wave * kRowLdsFloats<kRot>);
             // Every wave's codes and scales have reached L2 before the barrier; then one
             // agent-scope release (a write-back of the XCD's L2) publishes the job.
@@ -169,9 +173,9 @@ __global__ __launch_bounds__(kThreads, 1) void linear_kernel(
             nan_tile<kOutHalf>(out, ldo, M, N, job.m, job.n);
             continue;
         }
-        gemm_tile<kInt8, kOutHalf, kBias, kEpi>(
+        gemm_tile8<kInt8, kOutHalf, kBias, kEpi>(
             lds, reinterpret_cast<const uint8_t*>(q), reinterpret_cast<const uint8_t*>(W), qs, ws,
-            nullptr, nullptr, bias, out, nullptr, ldo, M, N, K, job.m, job.n);
+            bias, out, ldo, M, N, K, job.m, job.n);
     }
     // The last workgroup out moves the fault flag into the status word and resets the counters
     // for the next launch. Every workgroup's fault store precedes its exit increment, which the
@@ -199,7 +203,7 @@ hipError_t launch_linear(const void* x, int8_t* q, float* qs, const int8_t* w, c
     int jobs = 0;
     for (int m = 0; m < tiles_m; ++m) jobs += (min(kTile, M - m * kTile) + kQRows - 1) / kQRows + tiles_n;
     const int grid = max(queues, min(cu_count(device), jobs));
-    linear_kernel<kHalf, kRot, kOutHalf, kBias, kEpi><<<grid, kThreads, 0, s>>>(
+    linear_kernel<kHalf, kRot, kOutHalf, kBias, kEpi><<<grid, kThreads8, 0, s>>>(
         static_cast<const uint16_t*>(x), q, qs, w, ws, static_cast<const uint16_t*>(bias),
         static_cast<uint16_t*>(out), ldo, M, N, K, tiles_m, tiles_n, queues, work, spin_limit_setting);
     return hipGetLastError();
