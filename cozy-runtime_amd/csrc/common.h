@@ -251,4 +251,29 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 // Keeps the compiler from moving memory operations across the waits and barriers around it.
 __device__ __forceinline__ void fence() { asm volatile("" ::: "memory"); }
 
+// A GEMV epilogue's operands for a wave's rows nw .. nw + kRows - 1: the weight's row scales and
+// the bias, for loading with the activation, before the weight stream. Loaded after it (where
+// they are used), every wave's end waits out one more memory round trip. Rows past N read zeros.
+template <int kRows, bool kBias>
+struct RowEpilogue {
+    float ws[kRows];
+    uint16_t bias[kRows];
+};
+
+template <int kRows, bool kBias>
+__device__ __forceinline__ RowEpilogue<kRows, kBias> row_epilogue(const float* ws, const uint16_t* bias, int nw, int N) {
+    RowEpilogue<kRows, kBias> e;
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ws), 0, 4 * N, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < kRows; ++i)
+        e.ws[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, 4 * (nw + i), 0, 0));
+    if constexpr (kBias) {
+        const __amdgpu_buffer_rsrc_t br =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(bias), 0, 2 * N, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < kRows; ++i) e.bias[i] = __builtin_amdgcn_raw_buffer_load_b16(br, 2 * (nw + i), 0, 0);
+    }
+    return e;
+}
+
 }  // namespace cozyq

@@ -557,6 +557,15 @@ __global__ __launch_bounds__(64 * kW4Waves) void w4a8_decode_kernel(
             xv[m][p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                 qr, b < K ? m * K + b : 0x7ffffff0, 0, 0));
         }
+    // The epilogue's operands (the rows' scales, the weight rows' scales, the bias) come with the
+    // activation, ahead of the code stream (common.h `row_epilogue`).
+    const RowEpilogue<kW4Rows, kBias> epi = row_epilogue<kW4Rows, kBias>(ws, bias, nw, N);
+    float xsv[kM];
+    {
+        const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(xs), 0, 4 * kM, 0x00020000);
+#pragma unroll
+        for (int m = 0; m < kM; ++m) xsv[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, 4 * m, 0, 0));
+    }
     asm volatile("" ::: "memory");
 
     // 2. The code stream and each lane's two group-scale bytes.
@@ -645,10 +654,10 @@ __global__ __launch_bounds__(64 * kW4Waves) void w4a8_decode_kernel(
 #pragma unroll
         for (int i = 0; i < kW4Rows; ++i) {
             // internal/int8_linear.py:445-448 then :276: (acc·xs)·ws, cast, + bias in the output dtype.
-            const float v = __fmul_rn(__fmul_rn(static_cast<float>(dot[i][m]), xs[m]), ws[nw + i]);
+            const float v = __fmul_rn(__fmul_rn(static_cast<float>(dot[i][m]), xsv[m]), epi.ws[i]);
             uint32_t h = ::cozyq::narrow<kOutHalf>(v);  // (this file's `narrow` launcher hides it)
             if constexpr (kBias)
-                h = ::cozyq::narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(bias[nw + i])));
+                h = ::cozyq::narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(epi.bias[i])));
             o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
         }
         *reinterpret_cast<uint2*>(out + static_cast<int64_t>(m) * N + nw) = make_uint2(o[0], o[1]);

@@ -64,6 +64,7 @@ __global__ __launch_bounds__(kDThreads) void fp8_decode_kernel(
             xv[m][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, 2 * e, 0, 0));
         }
     }
+    const RowEpilogue<kRowsPerWave, kBias> epi = row_epilogue<kRowsPerWave, kBias>(ws, bias, nw, N);
     asm volatile("" ::: "memory");  // the weight loads stay behind the activation's
 
     // 2. The weight stream: kSpanBatch 2 KB spans of each of the wave's rows, two 1 KB loads each.
@@ -193,8 +194,8 @@ __global__ __launch_bounds__(kDThreads) void fp8_decode_kernel(
         uint32_t o[(kRowsPerWave + 1) / 2];
 #pragma unroll
         for (int i = 0; i < kRowsPerWave; ++i) {
-            float v = __fmul_rn(__fmul_rn(dot[i][m], s), ws[nw + i]);
-            if constexpr (kBias) v = __fadd_rn(v, widen<kOutHalf>(bias[nw + i]));
+            float v = __fmul_rn(__fmul_rn(dot[i][m], s), epi.ws[i]);
+            if constexpr (kBias) v = __fadd_rn(v, widen<kOutHalf>(epi.bias[i]));
             const uint32_t h = narrow<kOutHalf>(v);
             o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
         }
@@ -505,6 +506,7 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
             xv[m][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, 2 * e, 0, 0));
         }
     }
+    const RowEpilogue<kIRows, kBias> epi = row_epilogue<kIRows, kBias>(ws, bias, nw, N);
     asm volatile("" ::: "memory");  // the weight loads stay behind the activation's
 
     // 2. The weight stream: kISpanBatch 1 KB spans of each of the wave's rows.
@@ -654,10 +656,10 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
 #pragma unroll
         for (int i = 0; i < kIRows; ++i) {
             // internal/int8_linear.py:445-448 then :276: (acc·xs)·ws, cast, + bias in the output dtype.
-            const float v = __fmul_rn(__fmul_rn(static_cast<float>(dot[i][m]), scale[m]), ws[nw + i]);
+            const float v = __fmul_rn(__fmul_rn(static_cast<float>(dot[i][m]), scale[m]), epi.ws[i]);
             uint32_t h = narrow<kOutHalf>(v);
             if constexpr (kBias)
-                h = narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(bias[nw + i])));
+                h = narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(epi.bias[i])));
             o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
         }
         uint16_t* dst = out + static_cast<int64_t>(m) * N + nw;
