@@ -28,6 +28,24 @@ FAMILIES = ("mfma.cdna4",)
 #: 5 to 16 with K <= 4096 the row-tile kernel; it answers NOT_SUPPORTED past that); more rows
 #: quantize once and run the GEMM.
 FP8_SMALL_ROWS = 16
+#: From 3 rows, and `GEMV_TWO_LAUNCH_AREA` rows x output features up, the int8 linear quantizes
+#: once and runs the GEMM instead of the one-launch GEMV (same bits). Each GEMV workgroup rotates
+#: every row of x itself, so that work grows with rows x N; measured on MI355X (graph replays over
+#: weights past the MALL, µs GEMV / two launches): K=3072 N=12288 M=3 17.9 / 15.0, M=4 22.4 / 15.1;
+#: K=4096 N=14336 M=3 21.9 / 20.3, M=4 27.1 / 21.2; N=3072 (K 3072 or 12288) and two rows keep
+#: the GEMV (M=4 K=3072 N=3072 11.7 / 13.5, M=2 N=12288 11.9 / 15.0).
+GEMV_TWO_LAUNCH_ROWS = 3
+GEMV_TWO_LAUNCH_AREA = 24576
+
+
+def gemv_serves(rows: int, features: int) -> bool:
+    """Whether the int8 linear of `rows` rows and `features` outputs takes the one-launch GEMV
+    (within its row range; it may still decline a width), rather than quantize + GEMM."""
+    if rows >= GEMV_TWO_LAUNCH_ROWS and rows * features >= GEMV_TWO_LAUNCH_AREA:
+        return False
+    return True
+
+
 #: The svdq low-rank ranks the kernels take.
 RANKS = (16, 32, 64)
 #: int4 SVDQuant K-group.
@@ -145,9 +163,10 @@ class Prebuilt:
     def _gemv(self, flat: Tensor, data: Tensor, scale: Tensor, bias: Tensor | None,
               out_dtype: Dtype, shape: tuple[int, ...]) -> Tensor | None:  # fmt: skip
         """The whole int8 linear of up to `GEMV_ROWS` checked rows in one launch
-        (`cozyq_gemv`), or None where it declines (more rows, or rows too wide for it)."""
+        (`cozyq_gemv`), or None where it declines (more rows, rows too wide for it, or a shape
+        where quantize + GEMM is faster, `gemv_serves`)."""
         rows, width = flat.shape
-        if rows > self._lib.cozyq_gemv_rows():
+        if rows > self._lib.cozyq_gemv_rows() or not gemv_serves(rows, int(data.shape[0])):
             return None
         out = self.torch.empty(shape, dtype=out_dtype, device=flat.device)
         if rows == 0:

@@ -126,3 +126,13 @@ def test_svdq_rank_padding_and_merge():
     got = x @ m["lowrank_down"].double().t() @ m["lowrank_up"].double().t()
     assert torch.allclose(got, want, rtol=0, atol=1e-9)
     assert svdq_linear.merged(torch, roles, torch.zeros(97, 64), torch.zeros(48, 97)) is None
+
+
+def test_int8_gemv_route_rule():
+    """The int8 linear keeps the one-launch GEMV for 1-2 rows and for narrow weights, and sends
+    3-4 rows of wide weights to quantize + GEMM (the faster route there, same bits)."""
+    assert prebuilt.gemv_serves(1, 14336) and prebuilt.gemv_serves(2, 12288)
+    assert prebuilt.gemv_serves(4, 3072) and prebuilt.gemv_serves(3, 3072)
+    assert not prebuilt.gemv_serves(3, 12288) and not prebuilt.gemv_serves(4, 12288)
+    assert not prebuilt.gemv_serves(3, 14336) and not prebuilt.gemv_serves(4, 6144)
+    assert prebuilt.gemv_serves(3, 8191) and not prebuilt.gemv_serves(3, 8192)
