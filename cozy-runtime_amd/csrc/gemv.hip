@@ -718,6 +718,7 @@ hipError_t launch_decode(const uint16_t* x, const uint8_t* w, const float* ws,
 }
 
 constexpr int kRowsMaxK = 128 * kRSpan;  // 4096
+constexpr int64_t kRowsFromArea = 36864;  // rows x N from which 3 and 4 rows take the row tile
 constexpr int kRowsWaves = 8;  // fp8_rows_kernel's waves a workgroup
 
 template <bool kXHalf, bool kOutHalf, bool kBias>
@@ -738,9 +739,15 @@ hipError_t fp8_linear_small(const void* x, bool x_half, const uint8_t* w, const 
                             const void* bias, void* out, bool out_half, int M, int N, int K,
                             hipStream_t s) {
     // 1..4 rows whose activation fits the registers (the GEMV), 5..16 rows with K <= 4096 (the
-    // row-tile kernel); the rest is quantize + narrow GEMM.
-    const bool gemv = M >= 1 && M <= 4 && static_cast<int64_t>(M) * K <= kXLoads * kDThreads * 8;
-    if (!gemv && (M < 5 || M > 16 || K > kRowsMaxK)) return hipErrorNotSupported;
+    // row-tile kernel); the rest is quantize + narrow GEMM. 3 and 4 rows of a wide weight also
+    // take the row-tile kernel: each GEMV wave's MFMA chain grows with the rows, the row tile's
+    // does not (graph replays over weights past the MALL, us GEMV / row tile: N=14336 K=4096
+    // M=3 13.1 / 12.5, M=4 15.5 / 12.5; N=12288 K=3072 M=3 10.8 / 10.8, M=4 12.9 / 10.6;
+    // N=4096 K=4096 M=4 6.8 / 9.5).
+    const bool wide = M >= 3 && M <= 4 && static_cast<int64_t>(M) * N >= kRowsFromArea && K <= kRowsMaxK;
+    const bool gemv = !wide && M >= 1 && M <= 4 && static_cast<int64_t>(M) * K <= kXLoads * kDThreads * 8;
+    const bool tiles = wide || (M >= 5 && M <= 16 && K <= kRowsMaxK);
+    if (!gemv && !tiles) return hipErrorNotSupported;
     auto xp = static_cast<const uint16_t*>(x);
     auto bp = static_cast<const uint16_t*>(bias);
     auto op = static_cast<uint16_t*>(out);

@@ -176,8 +176,9 @@ int cozyq_w4a8_unpack(int device, const uint8_t* w, const uint8_t* s, const floa
  * fp8 GEMV, internal/fp8_linear.py:114-129 quantizes then multiplies): each row of x quantized
  * by cozyq_quantize's fp8 law inside the kernel, then out = acc·s_x·w_scale (+ bias).
  * M <= 4 with M·K <= 16384 (the GEMV), or 5 <= M <= 16 with K <= 4096 (the row-tile
- * kernel: one workgroup a CU, each owning 8-row units of N); K % 16 == 0; other shapes answer
- * NOT_SUPPORTED (the caller quantizes once and calls cozyq_gemm). */
+ * kernel: one workgroup a CU, each owning 8-row units of N; 3 and 4 rows with M·N >= 36864 and
+ * K <= 4096 take it too, faster there); K % 16 == 0; other shapes answer NOT_SUPPORTED (the
+ * caller quantizes once and calls cozyq_gemm). */
 int cozyq_fp8_linear(int device, const void* x, int x_half, const uint8_t* w,
                      const float* w_scale, const void* bias, void* out, int out_half, int M,
                      int N, int K, void* stream);

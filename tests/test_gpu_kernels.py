@@ -710,13 +710,14 @@ def test_fp8_small_linear_within_tolerance(ops, m, k):
 
 
 #: (M, N, K) through the fused fp8 kernels: the GEMV (M <= 4) and the row-tile kernel (5..16
-#: rows, K <= 4096), whose workgroups own 8..64 weight rows (N = 14336: 56 rows, three whole
-#: 16-row tiles and a half; N = 2056: one workgroup of 16 rows among 8-row ones; N = 16392:
-#: more 8-row units than 8 a CU, so more workgroups than CUs) and whose waves split K (K = 16
-#: and 400: waves with no K step or a partial one).
+#: rows, K <= 4096, and 3..4 rows of a wide weight: 4 x 14336, 3 x 12288), whose workgroups own
+#: 8..64 weight rows (N = 14336: 56 rows, three whole 16-row tiles and a half; N = 2056: one
+#: workgroup of 16 rows among 8-row ones; N = 16392: more 8-row units than 8 a CU, so more
+#: workgroups than CUs) and whose waves split K (K = 16 and 400: waves with no K step or a
+#: partial one).
 FUSED_FP8_SHAPES = [(1, 14336, 4096), (3, 2056, 1040), (5, 14336, 4096), (9, 2056, 1040),
                     (16, 14336, 4096), (16, 16392, 1024), (12, 264, 16), (7, 520, 400),
-                    (16, 8, 4096)]
+                    (16, 8, 4096), (4, 14336, 4096), (3, 12288, 3072)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
