@@ -447,7 +447,7 @@ def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
         weight_bytes = n * k // 2 + n * k // 16 + n * 4
         rows.append({"M": m, "us": ms * 1e3, "tops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
                      "weight_gbs": weight_bytes / (ms * 1e-3) / 1e9,
-                     "path": ("GEMV (w4a8_decode_kernel)" if m <= 4 else "row-tile kernel (w4a8_rows_kernel)"
+                     "path": ("GEMV (w4a8_decode_kernel)" if m <= 2 else "row-tile kernel (w4a8_rows_kernel)"
                               if m <= 16 else "fused narrow GEMM")
                      if m < prebuilt.UNPACK_ROWS else "unpack + int8 GEMM"})
     return {"K": k, "N": n, "rows": rows, "weight_copies": copies}

@@ -529,6 +529,7 @@ constexpr int kW4Batch = 2;      // 1 KiB code spans of each row in flight
 constexpr int kW4MaxK = 8192;    // activation rows a thread stages: K ≤ this
 constexpr int kW4Policy = 3;     // sc0 nt: each code byte is read once per call
 constexpr int kW4RowsMax = 16;   // rows the row-tile form takes (one MFMA's B columns)
+constexpr int kW4GemvRows = 2;   // rows the GEMV form takes
 constexpr uint32_t kFarW4 = 0x7fff0000u;  // a buffer offset past every resource here (reads 0)
 
 template <bool kOutHalf, bool kBias, int kM>
@@ -794,9 +795,7 @@ hipError_t launch_w4a8_decode(const int8_t* q, const float* xs, const uint8_t* c
     auto* o = static_cast<uint16_t*>(out);
     switch (M) {
         case 1: w4a8_decode_kernel<kOutHalf, kBias, 1><<<blocks, 64 * kW4Waves, lds, s>>>(q, xs, codes, w4, ws, b, o, N, K); break;
-        case 2: w4a8_decode_kernel<kOutHalf, kBias, 2><<<blocks, 64 * kW4Waves, lds, s>>>(q, xs, codes, w4, ws, b, o, N, K); break;
-        case 3: w4a8_decode_kernel<kOutHalf, kBias, 3><<<blocks, 64 * kW4Waves, lds, s>>>(q, xs, codes, w4, ws, b, o, N, K); break;
-        default: w4a8_decode_kernel<kOutHalf, kBias, 4><<<blocks, 64 * kW4Waves, lds, s>>>(q, xs, codes, w4, ws, b, o, N, K); break;
+        default: w4a8_decode_kernel<kOutHalf, kBias, 2><<<blocks, 64 * kW4Waves, lds, s>>>(q, xs, codes, w4, ws, b, o, N, K); break;
     }
     return hipGetLastError();
 }
@@ -807,9 +806,12 @@ hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* cod
                             const uint8_t* group_scale, const float* codebook, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
                             int config, hipStream_t s) {
-    // 1..4 rows by shape: the GEMV form; 5..16 the row-tile kernel (the same bits as every tile
-    // config).
-    if (config < 0 && M <= 4 && K <= kW4MaxK) {
+    // 1..2 rows by shape: the GEMV form; 3..16 the row-tile kernel (the same bits as every tile
+    // config). The GEMV form's MFMA chains grow with the rows, the row tile's do not (graph
+    // replays over weights past the MALL, us GEMV / row tile: K=3072 N=12288 M=2 10.2 / 10.0,
+    // M=3 13.7 / 10.1, M=4 15.7 / 10.3; K=4096 N=14336 M=1 11.2 / 13.3, M=2 12.7 / 13.2, M=3
+    // 16.6 / 13.6; K=3072 N=3072 M=3 7.4 / 5.9).
+    if (config < 0 && M <= kW4GemvRows && K <= kW4MaxK) {
         const W4 w4{group_scale, codebook};
         if (out_half)
             return bias ? launch_w4a8_decode<true, true>(q, xs, codes, w4, ws, bias, out, M, N, K, s)

@@ -864,8 +864,8 @@ def test_w4a8_unpack_every_scale_byte_bit_exact(ops, codebook):
                                    (300, 520, 1024)],
                          ids=lambda s: "x".join(map(str, s)))  # fmt: skip
 def test_w4a8_linear_bit_exact(ops, shape, codebook):
-    """The w4a8 linear (int8.convrot's operand; the GEMV form at 1..4 rows, the row-tile kernel
-    at 5..16, the fused unpack-in-registers GEMM up to 256 rows, unpack + the int8 GEMM beyond)
+    """The w4a8 linear (int8.convrot's operand; the GEMV form at 1..2 rows, the row-tile kernel
+    at 3..16, the fused unpack-in-registers GEMM up to 256 rows, unpack + the int8 GEMM beyond)
     equals the int8 CPU law on the unpacked levels, bit for bit, with and without bias; the
     fused and unpack configs agree bit for bit."""
     from cozyq import prebuilt
