@@ -195,7 +195,7 @@ def bench_c2(torch, ops, lib, stream, steps: int, warmup: int, preroll_for: floa
     ops_count = 2.0 * m * n * k
     gemm_tops = ops_count / (ms_gemm * 1e-3) / 1e12
     traffic_alg = m * k + n * k + m * n * 2 + n * 2 + (m + n) * 4
-    c2_traffic = pmc_traffic("c2", "void gemm8_kernel<false, true, 1>")
+    c2_traffic = pmc_traffic("c2", "void gemm8_kernel<0, false, true, 1>")
     return {
         "ms_per_step": ms_step,
         "tops": ops_count / (ms_step * 1e-3) / 1e12,
