@@ -25,8 +25,8 @@ Dtype = Any
 #: `_kernels/__init__.py`): CDNA4's MFMA on gfx950.
 FAMILIES = ("mfma.cdna4",)
 #: Rows the fused fp8 linear may take in one launch (`cozyq_fp8_linear`: up to 4 rows the GEMV,
-#: 5 to 16 with K <= 4096 the row-tile kernel; it answers NOT_SUPPORTED past that); more rows
-#: quantize once and run the GEMM.
+#: 5 to 16 with K <= 4096 the row-tile kernel, which also takes 3-4 rows of a wide weight; it
+#: answers NOT_SUPPORTED past that); more rows quantize once and run the GEMM.
 FP8_SMALL_ROWS = 16
 #: From 3 rows, and `GEMV_TWO_LAUNCH_AREA` rows x output features up, the int8 linear quantizes
 #: once and runs the GEMM instead of the one-launch GEMV (same bits). Each GEMV workgroup rotates

@@ -463,7 +463,8 @@ __global__ __launch_bounds__(64 * kRWaves) void fp8_rows_kernel(
 // dot product as the trace of a 16x16x64 MFMA over 16 64-byte pieces of one 1 KB span.
 constexpr int kISpanBatch = 4;  // 1 KB spans of each row a wave has in flight
 // Weight rows a wave owns: 4 measured 5% faster than 2 at M=1, K=3072, N=12288 on MI355X (the
-// workgroup's rotation is shared by twice the rows), 8 slower.
+// workgroup's rotation is shared by twice the rows); 6 (two workgroups a CU there) 9.0 -> 9.5 us
+// and 8 slower.
 constexpr int kIRows = 4;
 // Activation registers a thread may hold (8 bf16 a uint4, 2048 elements a row a uint4 across the
 // workgroup): 24, so that with the rotated values (M·K/256 floats) the widest admitted rows still
