@@ -515,7 +515,8 @@ __global__ __launch_bounds__(kThreads) void w4a8_unpack_kernel(const uint8_t* __
     *reinterpret_cast<uint4*>(out + row * K + grp * 16) = v;
 }
 
-// The w4a8.convrot GEMV for 1..4 quantized rows: the int8 decode GEMV's structure on 4-bit codes.
+// The w4a8.convrot GEMV for 1..2 quantized rows (more take the row-tile kernel below, faster from
+// 3 rows): the int8 decode GEMV's structure on 4-bit codes.
 // Each wave streams kW4Rows whole weight rows as contiguous 1 KiB code loads (lane l at byte
 // 16·l of a span: 32 codes, columns 2048·j + 32·l .., two groups, whose scale bytes are the row's
 // bytes 128·j + 2·l and + 1), non-temporal; the codes unpack to int8 levels through the
@@ -665,7 +666,7 @@ __global__ __launch_bounds__(64 * kW4Waves) void w4a8_decode_kernel(
     }
 }
 
-// The w4a8.convrot linear for 5..16 quantized rows: one 16-row weight tile a workgroup, its K
+// The w4a8.convrot linear for 3..16 quantized rows: one 16-row weight tile a workgroup, its K
 // split over kW4RWaves waves, on the plain v_mfma_i32_16x16x64_i8 (A = 16 weight rows, B = the
 // activation rows, zero past M). Lane l (row r = l%16, part g = l/16) of a wave loads 16
 // contiguous code bytes of weight row r per 128-code step t (codes 128t + 32g .. + 32: two
