@@ -1,7 +1,9 @@
-// The fp8 rowwise linear for 1..4 rows in one launch (decode): the activation rows are quantized
-// (internal/fp8_linear.py:56-63's law, bit for bit) inside the GEMV, so a decode step is one
-// launch bound by streaming the e4m3 weight from HBM once. More rows answer NOT_SUPPORTED and the
-// caller quantizes once and runs the narrow GEMM (gemm_narrow.hip).
+// The few-row linears in one launch. fp8 rowwise: the GEMV for 1..4 rows (decode) and the
+// row-tile kernel for 5..16 rows (and 3..4 rows of a wide weight); the activation rows are
+// quantized (internal/fp8_linear.py:56-63's law, bit for bit) inside the kernel, so a decode step
+// is one launch bound by streaming the e4m3 weight from HBM once. More rows answer NOT_SUPPORTED
+// and the caller quantizes once and runs the narrow GEMM (gemm_narrow.hip). int8.convrot: the
+// GEMV for 1..4 rows, rotation and quantization inside it.
 #include "common.h"
 #include "kernels.h"
 #include "rotate.h"
@@ -212,7 +214,8 @@ __global__ __launch_bounds__(kDThreads) void fp8_decode_kernel(
     }
 }
 
-// The fp8 rowwise linear for 5..16 rows in one launch. Quantizing all rows in every workgroup
+// The fp8 rowwise linear for 5..16 rows (and 3..4 rows of a wide weight, where it outruns the
+// GEMV) in one launch. Quantizing all rows in every workgroup
 // costs VALU time per CU (about 4.5 operations an element), so the grid is one workgroup per CU:
 // the CUs share N in 8-row units (at most 64 rows, four 16-row tiles, a workgroup) and a
 // workgroup's 8 waves split K (at most 4 steps of 128 bytes each, K <= 4096). A wave loads its K
