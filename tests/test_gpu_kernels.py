@@ -428,11 +428,14 @@ def test_int8_accumulators_bit_exact(ops, shape):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(3, 512, 1024), (300, 512, 1024), (257, 264, 768),
                                    (1, 1032, 4096), (16, 136, 256), (64, 520, 1024),
-                                   (129, 264, 768), (256, 2048, 512)],
+                                   (129, 264, 768), (256, 2048, 512), (4, 6144, 768),
+                                   (3, 8192, 512), (4, 6136, 256)],
                          ids=lambda s: "x".join(map(str, s)))  # fmt: skip
 def test_int8_linear_bit_exact(ops, shape, dtype, bias):
     """The whole int8.convrot linear (quantize + GEMM + epilogue) equals the CPU law bit for bit,
-    with the probe's recipe (`internal/prebuilt.py:616-623`): random int8 data, scales ~1e-3."""
+    with the probe's recipe (`internal/prebuilt.py:616-623`): random int8 data, scales ~1e-3.
+    4 x 6144 and 3 x 8192 take quantize + GEMM by the few-row route rule, 4 x 6136 (just below
+    it) the one-launch GEMV."""
     m, n, k = shape
     gen = torch.Generator().manual_seed(20261017 + m)
     data = torch.randint(-127, 128, (n, k), generator=gen, dtype=torch.int8)
