@@ -59,13 +59,14 @@ __device__ __forceinline__ f16x8 bf16_to_half8(const uint4 v) {
 // columns [16·(l/16), +16): the group's amax is two shuffles away, and the same 16 values feed
 // two 16x16x32 MFMAs (columns +0..7 and +8..15; down is read with the same pattern, so every
 // k is paired with its own down element).
-template <bool kHalf, int kR>
+template <bool kHalf, int kR, bool kPl>
 __global__ __launch_bounds__(kQWaves * 64) void svdq_quantize_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ p, const uint16_t* __restrict__ down,
     uint8_t* __restrict__ act, uint16_t* __restrict__ ascales, uint16_t* __restrict__ la, int M,
     int K) {
     constexpr int kJ = kR / 16;
     __shared__ float red[kQWaves][kQRows][kR];
+    extern __shared__ __attribute__((aligned(16))) float pl[];  // the smoothing factors p[K]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r16 = lane & 15, part = lane >> 4;
@@ -78,6 +79,15 @@ __global__ __launch_bounds__(kQWaves * 64) void svdq_quantize_kernel(
     f32x4 acc[kJ];
 #pragma unroll
     for (int j = 0; j < kJ; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // kPl: p once per block into LDS (the block's 16 rows share it; read from memory, every lane
+    // fetches its 16 columns' factors itself, 16 times the bytes: C4's shape 14.7 -> 13.7 us).
+    if constexpr (kPl) {
+        for (int i = 4 * tid; i < K; i += 4 * kQWaves * 64)
+            *reinterpret_cast<float4*>(pl + i) = *reinterpret_cast<const float4*>(p + i);
+        __syncthreads();
+    }
+    const float* const pv_src = kPl ? pl : p;
 
     for (int g = wave; g < groups; g += kQWaves) {
         const int col = kGroup * g + 16 * part;
@@ -93,7 +103,7 @@ __global__ __launch_bounds__(kQWaves * 64) void svdq_quantize_kernel(
         float pv[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float4 q4 = *reinterpret_cast<const float4*>(p + col + 4 * i);
+            const float4 q4 = *reinterpret_cast<const float4*>(pv_src + col + 4 * i);
             pv[4 * i] = q4.x; pv[4 * i + 1] = q4.y; pv[4 * i + 2] = q4.z; pv[4 * i + 3] = q4.w;
         }
 
@@ -159,13 +169,20 @@ __global__ __launch_bounds__(kQWaves * 64) void svdq_quantize_kernel(
     }
 }
 
+constexpr int kPlMaxK = 12288;  // widest rows whose p the quantize kernel stages in LDS (48 KB)
+
 template <bool kHalf, int kR>
 hipError_t launch_quantize(const void* x, const float* p, const void* down, uint8_t* act,
                            uint16_t* ascales, void* la, int M, int K, hipStream_t s) {
     const int blocks = (M + kQRows - 1) / kQRows;
-    svdq_quantize_kernel<kHalf, kR><<<blocks, kQWaves * 64, 0, s>>>(
-        static_cast<const uint16_t*>(x), p, static_cast<const uint16_t*>(down), act, ascales,
-        static_cast<uint16_t*>(la), M, K);
+    auto xp = static_cast<const uint16_t*>(x);
+    auto dp = static_cast<const uint16_t*>(down);
+    auto lp = static_cast<uint16_t*>(la);
+    if (K <= kPlMaxK)
+        svdq_quantize_kernel<kHalf, kR, true><<<blocks, kQWaves * 64, static_cast<size_t>(K) * 4, s>>>(
+            xp, p, dp, act, ascales, lp, M, K);
+    else
+        svdq_quantize_kernel<kHalf, kR, false><<<blocks, kQWaves * 64, 0, s>>>(xp, p, dp, act, ascales, lp, M, K);
     return hipGetLastError();
 }
 

@@ -75,7 +75,7 @@ def assert_la(got: torch.Tensor, x: torch.Tensor, down: torch.Tensor) -> None:
 
 @pytest.mark.parametrize("rank", [16, 32, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shape", [(1, 64), (5, 192), (77, 3072), (300, 1024)],
+@pytest.mark.parametrize("shape", [(1, 64), (5, 192), (77, 3072), (300, 1024), (3, 12352)],
                          ids=lambda s: f"{s[0]}x{s[1]}")  # fmt: skip
 def test_svdq_quantize_bit_exact(ops, shape, dtype, rank):
     m, k = shape
