@@ -162,7 +162,7 @@ constexpr int quantize_waves() { return kR == 128 ? 8 : 16; }  // the partial su
 // groups, the 16 columns [16·(l/16), +16): exactly one nvfp4 block, so its amax stays in the
 // lane, and the same 16 values feed two 16x16x32 MFMAs against down (read with the same
 // pattern, so every k meets its own down element).
-template <bool kHalf, int kR>
+template <bool kHalf, int kR, bool kPl>
 __global__ __launch_bounds__(quantize_waves<kR>() * 64) void nvfp4_quantize_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ p, const float* __restrict__ g,
     const uint16_t* __restrict__ down, uint8_t* __restrict__ act, uint8_t* __restrict__ ascales,
@@ -170,6 +170,7 @@ __global__ __launch_bounds__(quantize_waves<kR>() * 64) void nvfp4_quantize_kern
     constexpr int kWaves = quantize_waves<kR>();
     constexpr int kJ = kR / 16;
     __shared__ float red[kWaves][kQRows][kR];
+    extern __shared__ __attribute__((aligned(16))) float pl[];  // kPl: the smoothing factors p[K]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r16 = lane & 15, part = lane >> 4;
@@ -185,6 +186,14 @@ __global__ __launch_bounds__(quantize_waves<kR>() * 64) void nvfp4_quantize_kern
     f32x4 acc[kJ];
 #pragma unroll
     for (int j = 0; j < kJ; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // kPl: p once per block into LDS (the block's rows share it; read from memory, every lane
+    // fetches its 16 columns' factors itself, 16 times the bytes).
+    if constexpr (kPl) {
+        for (int i = 4 * tid; i < K; i += 4 * kWaves * 64)
+            *reinterpret_cast<float4*>(pl + i) = *reinterpret_cast<const float4*>(p + i);
+        __syncthreads();
+    }
 
     // A group's operands: the lane's 16 elements of its row, their p, and down's rows at the same
     // columns. The next group's are loaded before the current one is worked on, with no branch
@@ -203,14 +212,21 @@ __global__ __launch_bounds__(quantize_waves<kR>() * 64) void nvfp4_quantize_kern
             in.da[j] = *reinterpret_cast<const uint4*>(drow);
             in.db[j] = *reinterpret_cast<const uint4*>(drow + 8);
         }
+        if constexpr (!kPl) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) in.p4[i] = *reinterpret_cast<const float4*>(p + col + 4 * i);
+            for (int i = 0; i < 4; ++i) in.p4[i] = *reinterpret_cast<const float4*>(p + col + 4 * i);
+        }
     };
     Group cur, nxt;
     fetch(min(wave, groups - 1), cur);
     for (int gi = wave; gi < groups; gi += kWaves) {
         fetch(min(gi + kWaves, groups - 1), nxt);
         const uint4 xa = cur.xa, xb = cur.xb;
+        if constexpr (kPl) {
+            const int col = kQGroup * gi + 16 * part;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur.p4[i] = *reinterpret_cast<const float4*>(pl + col + 4 * i);
+        }
         const float pv[16] = {cur.p4[0].x, cur.p4[0].y, cur.p4[0].z, cur.p4[0].w, cur.p4[1].x, cur.p4[1].y,
                               cur.p4[1].z, cur.p4[1].w, cur.p4[2].x, cur.p4[2].y, cur.p4[2].z, cur.p4[2].w,
                               cur.p4[3].x, cur.p4[3].y, cur.p4[3].z, cur.p4[3].w};
@@ -298,9 +314,16 @@ template <bool kHalf, int kR>
 hipError_t launch_quantize(const void* x, const float* p, const float* g, const void* down,
                            uint8_t* act, uint8_t* ascales, void* la, int M, int K, hipStream_t s) {
     const int blocks = padded_rows(M) / kQRows;
-    nvfp4_quantize_kernel<kHalf, kR><<<blocks, quantize_waves<kR>() * 64, 0, s>>>(
-        static_cast<const uint16_t*>(x), p, g, static_cast<const uint16_t*>(down), act, ascales,
-        static_cast<uint16_t*>(la), M, K);
+    auto xp = static_cast<const uint16_t*>(x);
+    auto dp = static_cast<const uint16_t*>(down);
+    auto lp = static_cast<uint16_t*>(la);
+    // p staged in LDS up to 12288 columns (48 KB beside the partial sums).
+    if (K <= 12288)
+        nvfp4_quantize_kernel<kHalf, kR, true><<<blocks, quantize_waves<kR>() * 64, static_cast<size_t>(K) * 4, s>>>(
+            xp, p, g, dp, act, ascales, lp, M, K);
+    else
+        nvfp4_quantize_kernel<kHalf, kR, false><<<blocks, quantize_waves<kR>() * 64, 0, s>>>(
+            xp, p, g, dp, act, ascales, lp, M, K);
     return hipGetLastError();
 }
 

@@ -81,7 +81,7 @@ def test_svdq_input_scale_bit_exact(ops, shape, dtype):
 
 @pytest.mark.parametrize("rank", [32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
-@pytest.mark.parametrize("shape", [(1, 64), (17, 128), (300, 1024), (257, 3072)],
+@pytest.mark.parametrize("shape", [(1, 64), (17, 128), (300, 1024), (257, 3072), (2, 12352)],
                          ids=lambda s: "x".join(map(str, s)))  # fmt: skip
 def test_svdq_quantize_bit_exact(ops, shape, dtype, rank):
     """Codes and scales bit for bit (every row's blocks, the scale floor of an all-zero row, the
