@@ -861,7 +861,7 @@ def test_w4a8_unpack_every_scale_byte_bit_exact(ops, codebook):
 
 
 @pytest.mark.parametrize("codebook", [True, False], ids=["codebook", "uniform"])
-@pytest.mark.parametrize("shape", [(1, 264, 1024), (3, 520, 1024), (2, 12288, 3072), (4, 1032, 8192),
+@pytest.mark.parametrize("shape", [(1, 264, 1024), (3, 520, 1024), (2, 12288, 3072), (4, 12288, 3072), (4, 1032, 8192),
                                    (1, 136, 256), (16, 136, 256), (5, 520, 1024), (9, 1032, 8192),
                                    (13, 264, 768), (16, 12288, 3072), (100, 256, 3072), (256, 512, 768),
                                    (300, 520, 1024)],
