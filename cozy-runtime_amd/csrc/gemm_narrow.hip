@@ -530,6 +530,14 @@ constexpr int kW4Batch = 2;      // 1 KiB code spans of each row in flight
 constexpr int kW4MaxK = 8192;    // activation rows a thread stages: K ≤ this
 constexpr int kW4Policy = 3;     // sc0 nt: each code byte is read once per call
 constexpr int kW4RowsMax = 16;   // rows the row-tile form takes (one MFMA's B columns)
+// 17..32 rows: the row-tile form with two 16-row activation blocks, for K ≤ 4096 (its
+// activation registers) and M·K ≤ 98304. Graph replays over weights past the MALL, µs narrow
+// tile / row tile, bit-equal: K=3072 N=12288 M=17 19.6 / 15.3, M=24 19.7 / 16.2, M=32 19.7 /
+// 17.7; K=4096 N=14336 M=20 25.1 / 22.5, M=32 25.1 / 26.2 (past the area rule); K=3072 N=3072
+// M=32 19.0 / 8.5.
+constexpr int kW4Rows2Max = 32;
+constexpr int kW4Rows2MaxK = 4096;
+constexpr int64_t kW4Rows2Area = 98304;
 constexpr int kW4GemvRows = 2;   // rows the GEMV form takes
 constexpr uint32_t kFarW4 = 0x7fff0000u;  // a buffer offset past every resource here (reads 0)
 
@@ -666,26 +674,27 @@ __global__ __launch_bounds__(64 * kW4Waves) void w4a8_decode_kernel(
     }
 }
 
-// The w4a8.convrot linear for 3..16 quantized rows: one 16-row weight tile a workgroup, its K
+// The w4a8.convrot linear for 3..32 quantized rows: one 16-row weight tile a workgroup, its K
 // split over kW4RWaves waves, on the plain v_mfma_i32_16x16x64_i8 (A = 16 weight rows, B = the
-// activation rows, zero past M). Lane l (row r = l%16, part g = l/16) of a wave loads 16
-// contiguous code bytes of weight row r per 128-code step t (codes 128t + 32g .. + 32: two
-// groups, whose two scale bytes are adjacent) and the same 32 activation elements of row r in
-// two 16-byte pieces, so each of the step's two MFMAs meets A and B on the same 16 k's; the 4
-// lanes of a row read 64 contiguous bytes. Every load is issued before the level table is
-// built; steps past a wave's share read zeros (activation zeros make them add nothing). The
-// waves' int32 partials meet in LDS (exact, in any order), and the epilogue is the int8 law's,
-// so the outputs equal every tile config's bit for bit.
+// activation rows, zero past M; kCols blocks of 16 of them, each A unpacked once for all).
+// Lane l (row r = l%16, part g = l/16) of a wave loads 16 contiguous code bytes of weight row r
+// per 128-code step t (codes 128t + 32g .. + 32: two groups, whose two scale bytes are adjacent)
+// and the same 32 activation elements of row r in two 16-byte pieces, so each of the step's two
+// MFMAs meets A and B on the same 16 k's; the 4 lanes of a row read 64 contiguous bytes. Every
+// load is issued before the level table is built; steps past a wave's share read zeros
+// (activation zeros make them add nothing). The waves' int32 partials meet in LDS (exact, in any
+// order), and the epilogue is the int8 law's, so the outputs equal every tile config's bit for
+// bit.
 constexpr int kW4RWaves = 4;
 
-template <bool kOutHalf, bool kBias, int kSteps>
+template <bool kOutHalf, bool kBias, int kSteps, int kCols>
 __global__ __launch_bounds__(64 * kW4RWaves) void w4a8_rows_kernel(
     const int8_t* q, const float* xs, const uint8_t* codes, W4 w4, const float* ws,
     const uint16_t* bias, uint16_t* out, int M, int N, int K) {
     // (No pointer here is __restrict__: loads through restrict read-only arguments count as
     // invariant and may be sunk below later loads; these must stay in issue order.)
     __shared__ __attribute__((aligned(16))) uint32_t table[256 * 4];
-    __shared__ i32x4 part[kW4RWaves][64];
+    __shared__ i32x4 part[kW4RWaves][kCols][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, g = lane >> 4;
@@ -699,18 +708,20 @@ __global__ __launch_bounds__(64 * kW4RWaves) void w4a8_rows_kernel(
     w4_levels(w4.codebook, book);
     asm volatile("" ::: "memory");
 
-    // 1. The activation pieces: row r, elements 128t + 32g + 16h .. + 16 (zeros past M or the
-    //    wave's steps).
+    // 1. The activation pieces: row 16c + r of each 16-row block c, elements 128t + 32g + 16h
+    //    .. + 16 (zeros past M or the wave's steps).
     const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(q), 0, M * K, 0x00020000);
-    i32x4 xb[kSteps][2];
+    i32x4 xb[kCols][kSteps][2];
 #pragma unroll
-    for (int j = 0; j < kSteps; ++j)
+    for (int c = 0; c < kCols; ++c)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int t = t0 + j;
-            const uint32_t off = t < t1 && r < M ? static_cast<uint32_t>(r * K + 128 * t + 32 * g + 16 * h) : kFarW4;
-            xb[j][h] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
-        }
+        for (int j = 0; j < kSteps; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int t = t0 + j, row = 16 * c + r;
+                const uint32_t off = t < t1 && row < M ? static_cast<uint32_t>(row * K + 128 * t + 32 * g + 16 * h) : kFarW4;
+                xb[c][j][h] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
+            }
     asm volatile("" ::: "memory");
 
     // 2. The codes (16 bytes a lane a step, non-temporal) and the group scales.
@@ -752,7 +763,9 @@ __global__ __launch_bounds__(64 * kW4RWaves) void w4a8_rows_kernel(
     asm volatile("" ::: "memory");
 
     // 4. Products over the wave's steps.
-    i32x4 acc = {0, 0, 0, 0};
+    i32x4 acc[kCols];
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) acc[c] = i32x4{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < kSteps; ++j) {
         const uint4 s4 = sv[j / 2];
@@ -760,29 +773,38 @@ __global__ __launch_bounds__(64 * kW4RWaves) void w4a8_rows_kernel(
         const uint32_t sb = (d >> (16 * (g & 1))) & 0xffffu;
         const i32x4 l0 = __builtin_bit_cast(i32x4, w4_unpack16(cv[j].x, cv[j].y, table, sb & 0xffu));
         const i32x4 l1 = __builtin_bit_cast(i32x4, w4_unpack16(cv[j].z, cv[j].w, table, sb >> 8));
-        acc = mfma_i8(l0, xb[j][0], acc);
-        acc = mfma_i8(l1, xb[j][1], acc);
+#pragma unroll
+        for (int c = 0; c < kCols; ++c) {
+            acc[c] = mfma_i8(l0, xb[c][j][0], acc[c]);
+            acc[c] = mfma_i8(l1, xb[c][j][1], acc[c]);
+        }
     }
 
     // 5. The waves' partials (lane l: activation row l%16, weight rows 4·(l/16) + 0..3), then
     //    (acc·xs)·ws, cast, + bias in the output dtype (internal/int8_linear.py:445-448, :276).
-    part[wave][lane] = acc;
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) part[wave][c][lane] = acc[c];
     __syncthreads();
     if (wave != 0) return;
-#pragma unroll
-    for (int w = 1; w < kW4RWaves; ++w) acc += part[w][lane];
     const int n = n0 + 4 * g;
-    if (r >= M || n >= N) return;  // N % 8 == 0: a lane's four rows are all in or all out
-    uint32_t o[2];
+    if (n >= N) return;  // N % 8 == 0: a lane's four rows are all in or all out
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float v = __fmul_rn(__fmul_rn(static_cast<float>(acc[i]), xs[r]), ws[n + i]);
-        uint32_t h = ::cozyq::narrow<kOutHalf>(v);
-        if constexpr (kBias)
-            h = ::cozyq::narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(bias[n + i])));
-        o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
+    for (int c = 0; c < kCols; ++c) {
+#pragma unroll
+        for (int w = 1; w < kW4RWaves; ++w) acc[c] += part[w][c][lane];
+        const int row = 16 * c + r;
+        if (row >= M) continue;
+        uint32_t o[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float v = __fmul_rn(__fmul_rn(static_cast<float>(acc[c][i]), xs[row]), ws[n + i]);
+            uint32_t h = ::cozyq::narrow<kOutHalf>(v);
+            if constexpr (kBias)
+                h = ::cozyq::narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(bias[n + i])));
+            o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
+        }
+        *reinterpret_cast<uint2*>(out + static_cast<int64_t>(row) * N + n) = make_uint2(o[0], o[1]);
     }
-    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(r) * N + n) = make_uint2(o[0], o[1]);
 }
 
 template <bool kOutHalf, bool kBias>
@@ -792,12 +814,17 @@ hipError_t launch_w4a8_rows(const int8_t* q, const float* xs, const uint8_t* cod
     const int per_wave = (K / 128 + kW4RWaves - 1) / kW4RWaves;
     const auto* b = static_cast<const uint16_t*>(bias);
     auto* o = static_cast<uint16_t*>(out);
-    if (per_wave <= 4)
-        w4a8_rows_kernel<kOutHalf, kBias, 4><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
+    if (M > 16) {  // two 16-row activation blocks (the caller keeps K <= kW4Rows2MaxK)
+        if (per_wave <= 4)
+            w4a8_rows_kernel<kOutHalf, kBias, 4, 2><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
+        else
+            w4a8_rows_kernel<kOutHalf, kBias, 8, 2><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
+    } else if (per_wave <= 4)
+        w4a8_rows_kernel<kOutHalf, kBias, 4, 1><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
     else if (per_wave <= 8)
-        w4a8_rows_kernel<kOutHalf, kBias, 8><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
+        w4a8_rows_kernel<kOutHalf, kBias, 8, 1><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
     else
-        w4a8_rows_kernel<kOutHalf, kBias, 16><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
+        w4a8_rows_kernel<kOutHalf, kBias, 16, 1><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, codes, w4, ws, b, o, M, N, K);
     return hipGetLastError();
 }
 
@@ -821,8 +848,8 @@ hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* cod
                             const uint8_t* group_scale, const float* codebook, const float* ws,
                             const void* bias, void* out, bool out_half, int M, int N, int K,
                             int config, hipStream_t s) {
-    // 1..2 rows by shape: the GEMV form; 3..16 the row-tile kernel (the same bits as every tile
-    // config). The GEMV form's MFMA chains grow with the rows, the row tile's do not (graph
+    // 1..2 rows by shape: the GEMV form; 3..16 (and 17..32 by the rule above) the row-tile
+    // kernel (the same bits as every tile config). The GEMV form's MFMA chains grow with the rows, the row tile's do not (graph
     // replays over weights past the MALL, us GEMV / row tile: K=3072 N=12288 M=2 10.2 / 10.0,
     // M=3 13.7 / 10.1, M=4 15.7 / 10.3; K=4096 N=14336 M=1 11.2 / 13.3, M=2 12.7 / 13.2, M=3
     // 16.6 / 13.6; K=3072 N=3072 M=3 7.4 / 5.9).
@@ -834,7 +861,8 @@ hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* cod
         return bias ? launch_w4a8_decode<false, true>(q, xs, codes, w4, ws, bias, out, M, N, K, s)
                     : launch_w4a8_decode<false, false>(q, xs, codes, w4, ws, bias, out, M, N, K, s);
     }
-    if (config < 0 && M <= kW4RowsMax && K <= kW4MaxK) {
+    const bool two = M <= kW4Rows2Max && K <= kW4Rows2MaxK && static_cast<int64_t>(M) * K <= kW4Rows2Area;
+    if (config < 0 && ((M <= kW4RowsMax && K <= kW4MaxK) || two)) {
         const W4 w4{group_scale, codebook};
         if (out_half)
             return bias ? launch_w4a8_rows<true, true>(q, xs, codes, w4, ws, bias, out, M, N, K, s)

@@ -160,7 +160,8 @@ int cozyq_gemm_i32(int device, const int8_t* q, const int8_t* w, int32_t* acc, i
  * MFMA; the epilogue is cozyq_gemm's int8 law with w_scale [N], bit for bit. out [M, N].
  * N % 8 == 0, K % 256 == 0; q and w 16-byte aligned, out 8-byte aligned. config names
  * cozyq_gemm's narrow tiles 1..4 (-1: by rows, a GEMV form for 1..2 rows and a row-tile
- * kernel for 3..16 rows with K <= 8192, the same bits); 0 and 5 (the 256-row tiles, which multiply
+ * kernel for 3..16 rows with K <= 8192 and 17..32 with K <= 4096 and M·K <= 98304, the same
+ * bits); 0 and 5 (the 256-row tiles, which multiply
  * the codes unpacked by cozyq_w4a8_unpack) and 6 and above return hipErrorNotSupported. */
 int cozyq_w4a8_gemm(int device, const int8_t* q, const float* scales, const uint8_t* w,
                     const uint8_t* s, const float* codebook, const float* w_scale, const void* bias,

@@ -864,11 +864,13 @@ def test_w4a8_unpack_every_scale_byte_bit_exact(ops, codebook):
 @pytest.mark.parametrize("shape", [(1, 264, 1024), (3, 520, 1024), (2, 12288, 3072), (4, 12288, 3072), (4, 1032, 8192),
                                    (1, 136, 256), (16, 136, 256), (5, 520, 1024), (9, 1032, 8192),
                                    (13, 264, 768), (16, 12288, 3072), (100, 256, 3072), (256, 512, 768),
-                                   (300, 520, 1024)],
+                                   (300, 520, 1024), (17, 136, 4096), (24, 520, 1024), (32, 1032, 3072),
+                                   (32, 264, 4096)],
                          ids=lambda s: "x".join(map(str, s)))  # fmt: skip
 def test_w4a8_linear_bit_exact(ops, shape, codebook):
     """The w4a8 linear (int8.convrot's operand; the GEMV form at 1..2 rows, the row-tile kernel
-    at 3..16, the fused unpack-in-registers GEMM up to 256 rows, unpack + the int8 GEMM beyond)
+    at 3..16 and, in two activation blocks, at 17..32 rows with M·K ≤ 98304 and K ≤ 4096, the
+    fused unpack-in-registers GEMM up to 256 rows, unpack + the int8 GEMM beyond)
     equals the int8 CPU law on the unpacked levels, bit for bit, with and without bias; the
     fused and unpack configs agree bit for bit."""
     from cozyq import prebuilt
