@@ -394,8 +394,9 @@ def bench_int8_decode(torch, ops, lib, stream, steps: int) -> dict:
 
 def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
     """The w4a8.convrot GEMM on config 2's weight shape (K=3072, N=12288; 4-bit codes + E4M3
-    group scales, 21.2 MB against int8's 37.7 MB) at M = 1 (the GEMV form), 16, 256 (the fused
-    GEMM, codes unpacked in registers) and 4096 (unpack once + the 256x256 int8 GEMM),
+    group scales, 21.2 MB against int8's 37.7 MB) at M = 1 (the GEMV form), 16 and 32 (the row
+    tile), 256 (the fused GEMM, codes unpacked in registers) and 4096 (unpack once + the 256x256
+    int8 GEMM),
     int8.convrot's operand precomputed; bias + bf16 out; 14 rotating weight copies (297 MB,
     beyond the 256 MB MALL), one per call."""
     from cozyq import prebuilt
@@ -419,7 +420,7 @@ def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
         return w
 
     rows = []
-    for m in (1, 16, 256, 4096):
+    for m in (1, 16, 32, 256, 4096):
         q, s = ops.int8_quantize(_activations(torch, m, k, 92))
         out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         args = (q.data_ptr(), s.data_ptr())
@@ -448,7 +449,7 @@ def bench_w4a8(torch, ops, lib, stream, steps: int) -> dict:
         rows.append({"M": m, "us": ms * 1e3, "tops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
                      "weight_gbs": weight_bytes / (ms * 1e-3) / 1e9,
                      "path": ("GEMV (w4a8_decode_kernel)" if m <= 2 else "row-tile kernel (w4a8_rows_kernel)"
-                              if m <= 16 else "fused narrow GEMM")
+                              if m <= 32 else "fused narrow GEMM")
                      if m < prebuilt.UNPACK_ROWS else "unpack + int8 GEMM"})
     return {"K": k, "N": n, "rows": rows, "weight_copies": copies}
 
