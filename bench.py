@@ -348,8 +348,9 @@ def _graph_us(torch, launch, per_graph: int, replays: int) -> float:
 
 def _int8_decode_shape(torch, ops, lib, m: int, k: int, n: int, replays: int) -> dict:
     """The fused int8 GEMV (`cozyq_gemv`: rotation, quantization and GEMV in one launch) against
-    the two-launch path (quantize, then the GEMM's shape rule) at one shape, each over enough
-    rotating weight copies (> 600 MB) that the 256 MB MALL cannot hold them, graph-replayed."""
+    the two-launch path (quantize, then the GEMM's shape rule: at 1..4 rows a GEMV on the codes)
+    at one shape, each over enough rotating weight copies (> 600 MB) that the 256 MB MALL cannot
+    hold them, graph-replayed; `int8_linear_takes` names the route `Prebuilt.int8_linear` takes."""
     copies = max(8, int(600e6 // (n * k)) + 1)
     x = _activations(torch, m, k, 61)
     weights = [ops.int8_quantize_rot(_weights(torch, n, k, 62 + c), 256) for c in range(copies)]
@@ -375,9 +376,12 @@ def _int8_decode_shape(torch, ops, lib, m: int, k: int, n: int, replays: int) ->
     us = _graph_us(torch, fused, 8 * copies if copies <= 8 else copies, replays)
     us_two = _graph_us(torch, two_launch, 8 * copies if copies <= 8 else copies, replays)
     nbytes = n * k + n * 4 + m * k * 2 + m * n * 2
+    from cozyq import prebuilt
+
     return {"M": m, "K": k, "N": n, "us": us, "gbs": nbytes / (us * 1e-6) / 1e9,
             "frac_hbm": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, "us_quantize_then_gemm": us_two,
-            "weight_copies": copies}
+            "weight_copies": copies,
+            "int8_linear_takes": "one launch" if prebuilt.gemv_serves(m, k) else "quantize + GEMM"}
 
 
 def bench_int8_decode(torch, ops, lib, stream, steps: int) -> dict:

@@ -28,20 +28,21 @@ FAMILIES = ("mfma.cdna4",)
 #: 5 to 16 with K <= 4096 the row-tile kernel, which also takes 3-4 rows of a wide weight; it
 #: answers NOT_SUPPORTED past that); more rows quantize once and run the GEMM.
 FP8_SMALL_ROWS = 16
-#: From 3 rows, and `GEMV_TWO_LAUNCH_AREA` rows x output features up, the int8 linear quantizes
-#: once and runs the GEMM instead of the one-launch GEMV (same bits). Each GEMV workgroup rotates
-#: every row of x itself, so that work grows with rows x N; measured on MI355X (graph replays over
-#: weights past the MALL, µs GEMV / two launches): K=3072 N=12288 M=3 17.9 / 15.0, M=4 22.4 / 15.1;
-#: K=4096 N=14336 M=3 21.9 / 20.3, M=4 27.1 / 21.2; N=3072 (K 3072 or 12288) and two rows keep
-#: the GEMV (M=4 K=3072 N=3072 11.7 / 13.5, M=2 N=12288 11.9 / 15.0).
-GEMV_TWO_LAUNCH_ROWS = 3
-GEMV_TWO_LAUNCH_AREA = 24576
+#: From 2 rows, and `GEMV_TWO_LAUNCH_AREA` rows x K up, the int8 linear quantizes once and runs
+#: the GEMM (at 1..4 rows a GEMV on the quantized rows) instead of the one-launch GEMV (same
+#: bits). Each one-launch workgroup rotates every row of x itself, so that work grows with rows x
+#: K; measured on MI355X (graph replays over weights past the MALL, µs one launch / two):
+#: K=3072 N=12288 M=1 9.2 / 12.5, M=2 11.8 / 13.3, M=3 18.0 / 14.0, M=4 22.4 / 15.3; K=4096
+#: N=14336 M=2 16.0 / 17.9, M=4 27.3 / 20.7; K=12288 N=3072 M=2 18.0 / 14.9, M=4 28.4 / 16.7;
+#: K=3072 N=3072 M=4 11.8 / 10.8; K=16384 N=4096 M=2 27.5 / 24.0; K=32768 N=4096 M=1 41.7 / 47.3.
+GEMV_TWO_LAUNCH_ROWS = 2
+GEMV_TWO_LAUNCH_AREA = 9216
 
 
-def gemv_serves(rows: int, features: int) -> bool:
-    """Whether the int8 linear of `rows` rows and `features` outputs takes the one-launch GEMV
+def gemv_serves(rows: int, width: int) -> bool:
+    """Whether the int8 linear of `rows` rows of `width` elements takes the one-launch GEMV
     (within its row range; it may still decline a width), rather than quantize + GEMM."""
-    if rows >= GEMV_TWO_LAUNCH_ROWS and rows * features >= GEMV_TWO_LAUNCH_AREA:
+    if rows >= GEMV_TWO_LAUNCH_ROWS and rows * width >= GEMV_TWO_LAUNCH_AREA:
         return False
     return True
 
@@ -166,7 +167,7 @@ class Prebuilt:
         (`cozyq_gemv`), or None where it declines (more rows, rows too wide for it, or a shape
         where quantize + GEMM is faster, `gemv_serves`)."""
         rows, width = flat.shape
-        if rows > self._lib.cozyq_gemv_rows() or not gemv_serves(rows, int(data.shape[0])):
+        if rows > self._lib.cozyq_gemv_rows() or not gemv_serves(rows, width):
             return None
         out = self.torch.empty(shape, dtype=out_dtype, device=flat.device)
         if rows == 0:

@@ -5,8 +5,9 @@ is no other lane to fall back to, so it raises). cozyq's counterpart of cozy-run
 probe of `internal/prebuilt.py:601-675`.
 
 - `probe_int8` / `probe_fp8` run the serving entry points on small problems: the linear at a
-  GEMV-sized and a GEMM-sized M, bf16 and fp16, and every GEMM tile config on the same operand
-  (int8's integer sums must give every config the same bits).
+  GEMV-sized and a GEMM-sized M, the GEMM's shape rule at the GEMV-sized M, bf16 and fp16, and
+  every GEMM tile config on the same operand (int8's integer sums must give every config the
+  same bits).
 - Their law is restated here in float64 on the device (the format definitions: per-token int8
   of the 256-point rotated rows, `internal/int8_linear.py:422-428`, and per-token e4m3,
   `internal/fp8_linear.py:56-63`). A kernel that rounds the same law its own way loses ~2^-9 to
@@ -218,6 +219,9 @@ def _probe(torch: Any, ops: Any, fp8: bool) -> Verdict:
             x = randn(m, WIDTH).to(dtype)
             want = law(torch, x, data, scale, bias)
             errors[f"{name} linear M={m}"] = error(torch, linear(x, data, scale, bias, dtype), want)
+            if m < ROWS:  # the shape rule's GEMM on few quantized rows
+                qm, sm = quantize(x)
+                errors[f"{name} GEMM M={m}"] = error(torch, gemm(qm, sm, data, scale, bias, dtype, -1), want)
         q, s = quantize(x)
         first = None
         for config in range(configs):
@@ -232,7 +236,8 @@ def _probe(torch: Any, ops: Any, fp8: bool) -> Verdict:
 
 def probe_int8(torch: Any, ops: Any) -> Verdict:
     """int8.convrot's kernels on the card: the linear at M = 3 (the fused GEMV) and 300
-    (quantize + the shape rule's GEMM), bf16 and fp16, and every tile config bit-equal."""
+    (quantize + the shape rule's GEMM), the GEMM at M = 3 (the GEMV on the quantized rows), bf16
+    and fp16, and every tile config bit-equal."""
     return _probe(torch, ops, fp8=False)
 
 

@@ -110,6 +110,11 @@ int gemm_config(bool fp8, int M, int N, int K) {
 hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                      const void* bias, void* out, int64_t ldo, bool out_half, int M, int N, int K,
                      int epilogue, int config, hipStream_t s) {
+    // 1..4 rows by the shape rule: the GEMV on the quantized rows, where it applies.
+    if (config < 0 && M <= 4 && epilogue == 0) {
+        const hipError_t e = int8_codes_gemv(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (config < 0) config = gemm_config(false, M, N, K);
     if (config > 0 && config < 5)
         return gemm_int8_narrow(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, config, s);

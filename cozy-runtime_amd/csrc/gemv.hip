@@ -672,6 +672,159 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
     }
 }
 
+// The int8 GEMV on codes already quantized (cozyq_gemm's int8 product at 1..4 rows, by the
+// shape rule): int8_decode_kernel's weight stream, products and epilogue, with the rows' codes and
+// scales read from memory instead of made in the workgroup. A thread loads 16-byte runs of every
+// row (zeros past K) ahead of the weight stream and stores them to LDS, where the products read
+// them as in the fused kernel; (acc·xs)·ws, one cast, + bias in the output dtype, as every tile.
+template <bool kOutHalf, bool kBias, int kM, int kRuns>
+__global__ __launch_bounds__(kDThreads) void int8_codes_gemv_kernel(
+    const int8_t* q, const float* xs, const int8_t* __restrict__ W, const float* __restrict__ ws,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int64_t ldo, int N, int K) {
+    static_assert(kM * kRuns <= kIXLoads, "activation registers");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    int8_t* xq = reinterpret_cast<int8_t*>(smem);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int spans = (K + 1023) / 1024;
+    const int stride = spans * 1024;
+    const int nw = blockIdx.x * (kDWaves * kIRows) + wave * kIRows;  // the wave's first row
+
+    // 1. The codes: the thread's 16-byte runs of every row, then the row scales and the
+    // epilogue's operands, all ahead of the weight stream.
+    uint4 cv[kM][kRuns];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t*>(q + static_cast<int64_t>(m) * K), 0, K, 0x00020000);
+#pragma unroll
+        for (int c = 0; c < kRuns; ++c)
+            cv[m][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(qr, c * (kDThreads * 16) + tid * 16, 0, 0));
+    }
+    float scale[kM];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) scale[m] = xs[m];
+    const RowEpilogue<kIRows, kBias> epi = row_epilogue<kIRows, kBias>(ws, bias, nw, N);
+    asm volatile("" ::: "memory");  // the weight loads stay behind the codes'
+
+    // 2. The weight stream, as int8_decode_kernel's.
+    __amdgpu_buffer_rsrc_t wr[kIRows];
+#pragma unroll
+    for (int i = 0; i < kIRows; ++i)
+        wr[i] = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t*>(W + static_cast<int64_t>(min(nw + i, N - 1)) * K), 0, K, 0x00020000);
+    constexpr bool kTwo = kRuns > 1;  // rows longer than one batch of spans
+    uint4 wa[kIRows][kISpanBatch], wb[kTwo ? kIRows : 1][kISpanBatch];
+    auto issue = [&](auto& wv, int first) {
+#pragma unroll
+        for (int i = 0; i < kIRows; ++i)
+#pragma unroll
+            for (int b = 0; b < kISpanBatch; ++b) {
+                const int k = (first + b) * 1024 + 16 * lane;  // >= K reads zeros
+                wv[i][b] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr[i], k, 0, kStreamPolicy));
+            }
+    };
+    issue(wa, 0);
+
+    // 3. The codes into LDS (`stride` bytes a row, zeros past K).
+#pragma unroll
+    for (int m = 0; m < kM; ++m)
+#pragma unroll
+        for (int c = 0; c < kRuns; ++c) {
+            const int e = c * (kDThreads * 16) + tid * 16;
+            if (e < stride) *reinterpret_cast<uint4*>(xq + m * stride + e) = cv[m][c];
+        }
+    __syncthreads();
+
+    // 4. Products, the trace and the epilogue: int8_decode_kernel's.
+    i32x4 acc[kIRows][kM];
+#pragma unroll
+    for (int i = 0; i < kIRows; ++i)
+#pragma unroll
+        for (int m = 0; m < kM; ++m) acc[i][m] = i32x4{0, 0, 0, 0};
+    auto consume = [&](const auto& wv, int first) {
+#pragma unroll
+        for (int b = 0; b < kISpanBatch; ++b) {
+            if (first + b >= spans) break;
+            i32x4 xb[kM];
+#pragma unroll
+            for (int m = 0; m < kM; ++m)
+                xb[m] = *reinterpret_cast<const i32x4*>(xq + m * stride + (first + b) * 1024 + 16 * lane);
+#pragma unroll
+            for (int i = 0; i < kIRows; ++i) {
+                const i32x4 a = __builtin_bit_cast(i32x4, wv[i][b]);
+#pragma unroll
+                for (int m = 0; m < kM; ++m) acc[i][m] = mfma_i8(a, xb[m], acc[i][m]);
+            }
+        }
+    };
+    if constexpr (kTwo) {
+        for (int first = 0; first < spans; first += 2 * kISpanBatch) {
+            if (first + kISpanBatch < spans) issue(wb, first + kISpanBatch);
+            consume(wa, first);
+            if (first + kISpanBatch >= spans) break;
+            if (first + 2 * kISpanBatch < spans) issue(wa, first + 2 * kISpanBatch);
+            consume(wb, first + kISpanBatch);
+        }
+    } else {
+        consume(wa, 0);
+    }
+    const int a = lane & 15;
+    const bool diagonal = (lane >> 4) == (a >> 2);
+    int dot[kIRows][kM];
+#pragma unroll
+    for (int i = 0; i < kIRows; ++i)
+#pragma unroll
+        for (int m = 0; m < kM; ++m) {
+            const i32x4 d = acc[i][m];
+            const int r = a & 3;
+            int v = r == 0 ? d[0] : (r == 1 ? d[1] : (r == 2 ? d[2] : d[3]));
+            v = diagonal ? v : 0;
+            dot[i][m] = diagonal_sum(v);
+        }
+    if (lane != 0 || nw >= N) return;  // N % 4 == 0: a wave's rows are all in or all out
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        uint32_t o[(kIRows + 1) / 2];
+#pragma unroll
+        for (int i = 0; i < kIRows; ++i) {
+            const float v = __fmul_rn(__fmul_rn(static_cast<float>(dot[i][m]), scale[m]), epi.ws[i]);
+            uint32_t h = narrow<kOutHalf>(v);
+            if constexpr (kBias)
+                h = narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(epi.bias[i])));
+            o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
+        }
+        static_assert(kIRows == 4, "the store below writes four outputs");
+        *reinterpret_cast<uint2*>(out + static_cast<int64_t>(m) * ldo + nw) = make_uint2(o[0], o[1]);
+    }
+}
+
+template <bool kOutHalf, bool kBias>
+hipError_t launch_int8_codes_gemv(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
+                                  const uint16_t* bias, uint16_t* out, int64_t ldo, int M, int N,
+                                  int K, hipStream_t s) {
+    const int blocks = (N + kDWaves * kIRows - 1) / (kDWaves * kIRows);
+    const int64_t lds = static_cast<int64_t>(M) * ((K + 1023) / 1024) * 1024;
+    const int runs = (K + kDThreads * 16 - 1) / (kDThreads * 16);
+#define COZYQ_ROWS(R, C)                                                                           \
+    if (M == R && runs <= C) {                                                                     \
+        int8_codes_gemv_kernel<kOutHalf, kBias, R, C><<<blocks, kDThreads, lds, s>>>(q, xs, w, ws, bias, out, ldo, N, K); \
+        return hipGetLastError();                                                                  \
+    }
+    COZYQ_ROWS(1, 1)
+    COZYQ_ROWS(1, 3)
+    COZYQ_ROWS(1, 8)
+    COZYQ_ROWS(2, 1)
+    COZYQ_ROWS(2, 4)
+    COZYQ_ROWS(3, 1)
+    COZYQ_ROWS(3, 3)
+    COZYQ_ROWS(4, 1)
+    COZYQ_ROWS(4, 3)
+#undef COZYQ_ROWS
+    return hipErrorNotSupported;
+}
+
 template <bool kXHalf, bool kOutHalf, bool kBias>
 hipError_t launch_int8_decode(const uint16_t* x, const int8_t* w, const float* ws,
                               const uint16_t* bias, uint16_t* out, int M, int N, int K,
@@ -798,6 +951,21 @@ hipError_t int8_linear_small(const void* x, bool x_half, const int8_t* w, const 
     COZYQ_CASE(true, true, true)
 #undef COZYQ_CASE
     return hipErrorInvalidValue;
+}
+
+hipError_t int8_codes_gemv(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
+                           const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
+                           int K, hipStream_t s) {
+    // 1..4 rows whose codes fit the registers and 48 KiB of LDS: K <= 32768 at 1 row, 16384 at
+    // 2, 12288 at 3..4. N % 4 == 0 (a wave's four rows all in or all out).
+    if (M < 1 || M > 4 || N % 4 || K > (M == 1 ? 32768 : M == 2 ? 16384 : 12288)) return hipErrorNotSupported;
+    auto bp = static_cast<const uint16_t*>(bias);
+    auto op = static_cast<uint16_t*>(out);
+    if (out_half)
+        return bias ? launch_int8_codes_gemv<true, true>(q, xs, w, ws, bp, op, ldo, M, N, K, s)
+                    : launch_int8_codes_gemv<true, false>(q, xs, w, ws, bp, op, ldo, M, N, K, s);
+    return bias ? launch_int8_codes_gemv<false, true>(q, xs, w, ws, bp, op, ldo, M, N, K, s)
+                : launch_int8_codes_gemv<false, false>(q, xs, w, ws, bp, op, ldo, M, N, K, s);
 }
 
 }  // namespace cozyq

@@ -104,6 +104,12 @@ int int8_gemv_max_k(int M);
 hipError_t int8_linear_small(const void* x, bool x_half, const int8_t* w, const float* ws,
                              const void* bias, void* out, bool out_half, int M, int N, int K,
                              hipStream_t s);
+// The int8 GEMV on quantized rows (cozyq_gemm's int8 product, 1..4 rows): K <= 32768 at 1 row,
+// 16384 at 2, 12288 at 3..4, N % 4 == 0; hipErrorNotSupported elsewhere. The same bits as every
+// tile.
+hipError_t int8_codes_gemv(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
+                           const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
+                           int K, hipStream_t s);
 // The fused fp8 linear for 1..4 rows (the GEMV, M·K <= 16384) and 5..16 rows (K <= 4096);
 // hipErrorNotSupported elsewhere.
 hipError_t fp8_linear_small(const void* x, bool x_half, const uint8_t* w, const float* ws,

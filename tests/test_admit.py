@@ -129,10 +129,11 @@ def test_svdq_rank_padding_and_merge():
 
 
 def test_int8_gemv_route_rule():
-    """The int8 linear keeps the one-launch GEMV for 1-2 rows and for narrow weights, and sends
-    3-4 rows of wide weights to quantize + GEMM (the faster route there, same bits)."""
-    assert prebuilt.gemv_serves(1, 14336) and prebuilt.gemv_serves(2, 12288)
-    assert prebuilt.gemv_serves(4, 3072) and prebuilt.gemv_serves(3, 3072)
-    assert not prebuilt.gemv_serves(3, 12288) and not prebuilt.gemv_serves(4, 12288)
-    assert not prebuilt.gemv_serves(3, 14336) and not prebuilt.gemv_serves(4, 6144)
-    assert prebuilt.gemv_serves(3, 8191) and not prebuilt.gemv_serves(3, 8192)
+    """The int8 linear keeps the one-launch GEMV for one row and for short rows, and sends 2-4
+    rows with rows x K >= 9216 to quantize + GEMM (the faster route there, same bits)."""
+    assert prebuilt.gemv_serves(1, 3072) and prebuilt.gemv_serves(1, 32768)
+    assert prebuilt.gemv_serves(2, 3072) and prebuilt.gemv_serves(2, 4096) and prebuilt.gemv_serves(3, 1024)
+    assert not prebuilt.gemv_serves(3, 3072) and not prebuilt.gemv_serves(4, 3072)
+    assert not prebuilt.gemv_serves(2, 12288) and not prebuilt.gemv_serves(2, 16384)
+    assert prebuilt.gemv_serves(2, 4352) and not prebuilt.gemv_serves(2, 4608)
+    assert prebuilt.gemv_serves(3, 2816) and not prebuilt.gemv_serves(4, 2304)

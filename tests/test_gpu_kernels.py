@@ -555,6 +555,37 @@ def test_int8_output_into_wider_rows(ops):
     assert (packed[:, :n] == 0).all() and (packed[:, 2 * n:] == 0).all()
 
 
+# (M, N, K): each row count on one batch of 1 KiB spans and on two (a partial last span), and
+# at its widest K (32768 at M = 1, 16384 at 2, 12288 at 3..4); N ragged against the workgroup's
+# 16 rows.
+CODES_GEMV_SHAPES = [(1, 264, 256), (2, 1032, 1280), (3, 136, 4352), (4, 264, 3072),
+                     (4, 520, 12288), (3, 264, 12288), (2, 136, 16384), (1, 264, 32768)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("shape", CODES_GEMV_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_int8_codes_gemv_bit_exact(ops, shape, dtype):
+    """`cozyq_gemm`'s int8 product at 1..4 rows (config -1: the GEMV on the quantized rows)
+    equals the int8 law and the 128x64 tile bit for bit, with and without bias, and writes in
+    place into rows `ldo` apart."""
+    m, n, k = shape
+    x = activations(m, k, seed=m * 11 + k)
+    data, scale = laws.int8_weight_rowwise(weights(n, k, seed=n + k))
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(k)) * 0.1).to(dtype)
+    q, s = ops.int8_quantize(x.to(DEV))
+    for bias in (None, b):
+        want = laws.int8_product(q.cpu(), s.cpu(), data, scale, dtype)
+        want = want if bias is None else want + bias
+        dev_bias = None if bias is None else bias.to(DEV)
+        got = ops.int8_gemm(q, s, data.to(DEV), scale.to(DEV), dev_bias, dtype, -1)
+        assert torch.equal(got.cpu(), want), bias is None
+        assert torch.equal(got, ops.int8_gemm(q, s, data.to(DEV), scale.to(DEV), dev_bias, dtype, 2))
+    packed = torch.zeros(m, 3 * n, dtype=dtype, device=DEV)
+    ops.int8_gemm(q, s, data.to(DEV), scale.to(DEV), b.to(DEV), dtype, -1, out=packed[:, n:2 * n])
+    assert torch.equal(packed[:, n:2 * n].cpu(), want)
+    assert (packed[:, :n] == 0).all() and (packed[:, 2 * n:] == 0).all()
+
+
 # ------------------------------------------------------------------------- fp8 lane
 
 
