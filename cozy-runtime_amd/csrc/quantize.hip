@@ -179,6 +179,22 @@ __global__ __launch_bounds__(kThreads) void rotate_quantize_kernel(
     const int chunks = (K + kChunk - 1) / kChunk;
     float out[kMaxChunks][16];
     float amax = 0.0f;
+    // Without a prologue the whole row is loaded first (branch-free buffer loads, zeros past K):
+    // loaded chunk by chunk, each chunk waited out its own load latency behind the previous
+    // chunk's rotation (quantize + few-row GEMV, graph replays: M=1 K=32768 46.9 -> 45.1 us,
+    // M=4 K=12288 16.6 -> 16.5; one chunk, K <= 4096, unchanged).
+    constexpr int kRuns = kChunk / (kThreads * 8);  // a thread's 8-element runs of a chunk
+    uint4 xv[kPro ? 1 : kMaxChunks][kRuns];
+    if constexpr (!kPro) {
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(xr), 0, 2 * K, 0x00020000);
+#pragma unroll
+        for (int c = 0; c < kMaxChunks; ++c)
+#pragma unroll
+            for (int h = 0; h < kRuns; ++h)
+                xv[c][h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                    xrs, 2 * (c * kChunk + h * kThreads * 8 + tid * 8), 0, 0));
+    }
 
 #pragma unroll
     for (int c = 0; c < kMaxChunks; ++c) {
@@ -186,12 +202,21 @@ __global__ __launch_bounds__(kThreads) void rotate_quantize_kernel(
         const int base = c * kChunk;
         const int width = min(kChunk, K - base);
         // Phase 1: the chunk into LDS, 16 bytes a load.
-        for (int e = tid * 8; e < width; e += kThreads * 8) {
+#pragma unroll
+        for (int h = 0; h < kRuns; ++h) {
+            const int e = h * kThreads * 8 + tid * 8;
+            if (e >= width) break;
             float v[8];
-            if constexpr (kPro)
+            if constexpr (kPro) {
                 load8_prologue<kHalf>(pro, x, row, K, base + e, stats.x, stats.y, v);
-            else
-                load8<kHalf>(xr + base + e, v);
+            } else {
+                const uint32_t w[4] = {xv[c][h].x, xv[c][h].y, xv[c][h].z, xv[c][h].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[2 * i] = widen<kHalf>(static_cast<uint16_t>(w[i] & 0xffffu));
+                    v[2 * i + 1] = widen<kHalf>(static_cast<uint16_t>(w[i] >> 16));
+                }
+            }
             const int g = e / kRot, within = e % kRot;
             float* dst = lds + L::at(g, within / 16, within % 16);
             *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
