@@ -678,6 +678,8 @@ __global__ __launch_bounds__(kDThreads) void int8_decode_kernel(
 // row (zeros past K) ahead of the weight stream and stores them to LDS, where the products read
 // them as in the fused kernel; (acc·xs)·ws, one cast, + bias in the output dtype, as every tile.
 template <bool kOutHalf, bool kBias, int kM, int kRuns>
+// (q is not __restrict__, for int8_decode_kernel's reason: its loads must stay ahead of the
+// weight stream.)
 __global__ __launch_bounds__(kDThreads) void int8_codes_gemv_kernel(
     const int8_t* q, const float* xs, const int8_t* __restrict__ W, const float* __restrict__ ws,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int64_t ldo, int N, int K) {
