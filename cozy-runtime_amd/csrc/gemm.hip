@@ -115,6 +115,15 @@ hipError_t gemm_int8(const int8_t* q, const float* xs, const int8_t* w, const fl
         const hipError_t e = int8_codes_gemv(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, s);
         if (e != hipErrorNotSupported) return e;
     }
+    // 5..32 rows of a weight of at most 4096 outputs: the 16-row weight tile, whose N/16
+    // workgroups fill the chip where the narrow tiles' N/64 do not (graph replays over weights past
+    // the MALL, µs narrow / row tile, bit-equal: K=3072 N=3072 M=16 8.4 / 6.6, M=32 9.0 / 8.6;
+    // K=1024 N=1032 M=16 4.9 / 3.1; K=2048 N=4096 M=32 7.1 / 6.1). Wider weights keep the narrow
+    // tile (K=3072 N=12288 M=5 10.1 / 12.8, M=16 10.4 / 14.4).
+    if (config < 0 && M >= 5 && M <= 32 && N <= 4096 && epilogue == 0) {
+        const hipError_t e = int8_rows_gemm(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (config < 0) config = gemm_config(false, M, N, K);
     if (config > 0 && config < 5)
         return gemm_int8_narrow(q, xs, w, ws, bias, out, ldo, out_half, M, N, K, epilogue, config, s);

@@ -828,6 +828,114 @@ hipError_t launch_w4a8_rows(const int8_t* q, const float* xs, const uint8_t* cod
     return hipGetLastError();
 }
 
+// The int8 product for 5..32 quantized rows with K <= 4096 (cozyq_gemm's shape rule, no
+// epilogue activation): w4a8_rows_kernel's tile on int8 weights. One 16-row weight tile a
+// workgroup, K split over its waves; lane l (row r = l%16, part g = l/16) loads 32 contiguous
+// weight bytes of row r per 128-byte step t (k = 128t + 32g .. + 32, two 16-byte pieces) and the
+// same k's of each activation row, zeros past K, M or N. The waves' int32 partials meet in LDS
+// and the epilogue is the int8 law's, so the outputs equal every tile config's bit for bit.
+constexpr int kI8RowsMaxK = 4096;
+
+template <bool kOutHalf, bool kBias, int kSteps, int kCols>
+__global__ __launch_bounds__(64 * kW4RWaves) void int8_rows_kernel(
+    const int8_t* q, const float* xs, const int8_t* w, const float* ws, const uint16_t* bias,
+    uint16_t* out, int64_t ldo, int M, int N, int K) {
+    // (Not __restrict__, as in w4a8_rows_kernel: the loads must stay in issue order.)
+    __shared__ i32x4 part[kW4RWaves][kCols][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int steps = (K + 127) / 128;  // K % 16 == 0: a 16-byte piece is wholly in or past K
+    const int t0 = wave * steps / kW4RWaves, t1 = (wave + 1) * steps / kW4RWaves;
+
+    // 1. The activation pieces of each 16-row block c, then 2. the weight pieces (non-temporal).
+    const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(q), 0, M * K, 0x00020000);
+    i32x4 xb[kCols][kSteps][2];
+#pragma unroll
+    for (int c = 0; c < kCols; ++c)
+#pragma unroll
+        for (int j = 0; j < kSteps; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int t = t0 + j, row = 16 * c + r, k = 128 * t + 32 * g + 16 * h;
+                const uint32_t off = t < t1 && row < M && k < K ? static_cast<uint32_t>(row * K + k) : kFarW4;
+                xb[c][j][h] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
+            }
+    asm volatile("" ::: "memory");
+    const int64_t rows_bytes = static_cast<int64_t>(N - n0) * K;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(w + static_cast<int64_t>(n0) * K), 0,
+        rows_bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(rows_bytes), 0x00020000);
+    i32x4 wv[kSteps][2];
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int t = t0 + j, k = 128 * t + 32 * g + 16 * h;
+            const bool live = t < t1 && n0 + r < N && k < K;
+            wv[j][h] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                wr, live ? static_cast<uint32_t>(r * K + k) : kFarW4, 0, kW4Policy));
+        }
+
+    // 3. Products over the wave's steps.
+    i32x4 acc[kCols];
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) acc[c] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j)
+#pragma unroll
+        for (int c = 0; c < kCols; ++c) {
+            acc[c] = mfma_i8(wv[j][0], xb[c][j][0], acc[c]);
+            acc[c] = mfma_i8(wv[j][1], xb[c][j][1], acc[c]);
+        }
+
+    // 4. The waves' partials, then (acc·xs)·ws, cast, + bias in the output dtype
+    //    (internal/int8_linear.py:445-448, :276).
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) part[wave][c][lane] = acc[c];
+    __syncthreads();
+    if (wave != 0) return;
+    const int n = n0 + 4 * g;
+    if (n >= N) return;  // N % 8 == 0: a lane's four rows are all in or all out
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) {
+#pragma unroll
+        for (int v = 1; v < kW4RWaves; ++v) acc[c] += part[v][c][lane];
+        const int row = 16 * c + r;
+        if (row >= M) continue;
+        uint32_t o[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float v = __fmul_rn(__fmul_rn(static_cast<float>(acc[c][i]), xs[row]), ws[n + i]);
+            uint32_t h = ::cozyq::narrow<kOutHalf>(v);
+            if constexpr (kBias)
+                h = ::cozyq::narrow<kOutHalf>(__fadd_rn(widen<kOutHalf>(static_cast<uint16_t>(h)), widen<kOutHalf>(bias[n + i])));
+            o[i / 2] = (i & 1) ? (o[i / 2] | (h << 16)) : h;
+        }
+        *reinterpret_cast<uint2*>(out + static_cast<int64_t>(row) * ldo + n) = make_uint2(o[0], o[1]);
+    }
+}
+
+template <bool kOutHalf, bool kBias>
+hipError_t launch_int8_rows(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
+                            const void* bias, void* out, int64_t ldo, int M, int N, int K, hipStream_t s) {
+    const int blocks = (N + 15) / 16;
+    const int per_wave = ((K + 127) / 128 + kW4RWaves - 1) / kW4RWaves;
+    const auto* b = static_cast<const uint16_t*>(bias);
+    auto* o = static_cast<uint16_t*>(out);
+    if (M > 16) {
+        if (per_wave <= 4)
+            int8_rows_kernel<kOutHalf, kBias, 4, 2><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, w, ws, b, o, ldo, M, N, K);
+        else
+            int8_rows_kernel<kOutHalf, kBias, 8, 2><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, w, ws, b, o, ldo, M, N, K);
+    } else if (per_wave <= 4)
+        int8_rows_kernel<kOutHalf, kBias, 4, 1><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, w, ws, b, o, ldo, M, N, K);
+    else
+        int8_rows_kernel<kOutHalf, kBias, 8, 1><<<blocks, 64 * kW4RWaves, 0, s>>>(q, xs, w, ws, b, o, ldo, M, N, K);
+    return hipGetLastError();
+}
+
 template <bool kOutHalf, bool kBias>
 hipError_t launch_w4a8_decode(const int8_t* q, const float* xs, const uint8_t* codes, W4 w4, const float* ws,
                               const void* bias, void* out, int M, int N, int K, hipStream_t s) {
@@ -873,6 +981,17 @@ hipError_t gemm_w4a8_narrow(const int8_t* q, const float* xs, const uint8_t* cod
     return narrow<true, true>(reinterpret_cast<const uint8_t*>(q), xs, codes, ws, bias, out, N,
                               out_half, M, N, K, 0, config < 0 ? narrow_config(M, N) : config, s,
                               W4{group_scale, codebook});
+}
+
+hipError_t int8_rows_gemm(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
+                          const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
+                          int K, hipStream_t s) {
+    if (M < 1 || M > 32 || K > kI8RowsMaxK || N % 8) return hipErrorNotSupported;
+    if (out_half)
+        return bias ? launch_int8_rows<true, true>(q, xs, w, ws, bias, out, ldo, M, N, K, s)
+                    : launch_int8_rows<true, false>(q, xs, w, ws, bias, out, ldo, M, N, K, s);
+    return bias ? launch_int8_rows<false, true>(q, xs, w, ws, bias, out, ldo, M, N, K, s)
+                : launch_int8_rows<false, false>(q, xs, w, ws, bias, out, ldo, M, N, K, s);
 }
 
 hipError_t w4a8_unpack(const uint8_t* codes, const uint8_t* group_scale, const float* codebook,

@@ -92,6 +92,11 @@ hipError_t w4a8_unpack(const uint8_t* codes, const uint8_t* group_scale, const f
 hipError_t gemm_int8_narrow(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
                             const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
                             int K, int epilogue, int config, hipStream_t s);
+// The int8 product on a 16-row weight tile a workgroup for 1..32 quantized rows, K <= 4096,
+// N % 8 == 0 (hipErrorNotSupported elsewhere); the same bits as every tile config.
+hipError_t int8_rows_gemm(const int8_t* q, const float* xs, const int8_t* w, const float* ws,
+                          const void* bias, void* out, int64_t ldo, bool out_half, int M, int N,
+                          int K, hipStream_t s);
 
 // The compute units of `device` (256 on MI355X), read once per device.
 int cu_count(int device);

@@ -88,7 +88,8 @@ typedef void* (*cozyq_allocate_fn)(size_t bytes, void* context);
  * (gemm_sm80.cu:233-289, gemm_fp8.cu:15-58), gfx950's own: 0 the 256x256 tile, 1 128x128,
  * 2 128x64, 3 64x64, 4 32x64, 5 256x192 (rows x columns); -1 chooses by shape
  * (cozyq_gemm_config; int8 at 1..4 rows with no epilogue activation takes a GEMV on the
- * quantized rows where K <= 32768 / 16384 / 12288 at 1 / 2 / 3..4 rows); 6 and above return
+ * quantized rows where K <= 32768 / 16384 / 12288 at 1 / 2 / 3..4 rows, and at 5..32 rows with
+ * K <= 4096 and N <= 4096 a 16-row weight tile); 6 and above return
  * hipErrorNotSupported. Every config gives the same int8 output bit for bit.
  * N % 8 == 0; K % 256 (int8) or K % 16 (fp8). */
 int cozyq_gemm(int device, int family, int fp8, const void* q, const float* scales,

@@ -555,19 +555,23 @@ def test_int8_output_into_wider_rows(ops):
     assert (packed[:, :n] == 0).all() and (packed[:, 2 * n:] == 0).all()
 
 
-# (M, N, K): each row count on one batch of 1 KiB spans and on two (a partial last span), and
-# at its widest K (32768 at M = 1, 16384 at 2, 12288 at 3..4); N ragged against the workgroup's
-# 16 rows.
+# (M, N, K): the GEMV's row counts on one batch of 1 KiB spans and on two (a partial last span),
+# and at their widest K (32768 at M = 1, 16384 at 2, 12288 at 3..4); the row tile's 5..32 rows
+# in one and two activation blocks, past its K (4352) and past its rows (33); N ragged against
+# the workgroup's 16 rows.
 CODES_GEMV_SHAPES = [(1, 264, 256), (2, 1032, 1280), (3, 136, 4352), (4, 264, 3072),
-                     (4, 520, 12288), (3, 264, 12288), (2, 136, 16384), (1, 264, 32768)]
+                     (4, 520, 12288), (3, 264, 12288), (2, 136, 16384), (1, 264, 32768),
+                     (5, 136, 256), (8, 1032, 1280), (16, 264, 3072), (16, 136, 4352),
+                     (17, 520, 4096), (24, 136, 1280), (32, 1032, 2048), (33, 264, 1024)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("shape", CODES_GEMV_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_int8_codes_gemv_bit_exact(ops, shape, dtype):
-    """`cozyq_gemm`'s int8 product at 1..4 rows (config -1: the GEMV on the quantized rows)
-    equals the int8 law and the 128x64 tile bit for bit, with and without bias, and writes in
-    place into rows `ldo` apart."""
+def test_int8_few_rows_gemm_bit_exact(ops, shape, dtype):
+    """`cozyq_gemm`'s int8 product at few rows (config -1: the GEMV on the quantized rows at
+    1..4, the 16-row weight tile at 5..32 with K <= 4096 and N <= 4096) equals the int8 law and
+    the 128x64 tile bit for bit, with and without bias, and writes in place into rows `ldo`
+    apart."""
     m, n, k = shape
     x = activations(m, k, seed=m * 11 + k)
     data, scale = laws.int8_weight_rowwise(weights(n, k, seed=n + k))
