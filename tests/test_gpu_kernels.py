@@ -526,10 +526,11 @@ def test_int8_gemm_rotation_lanes_and_gelu(ops, rotation):
     assert rel < 0.05
 
 
-@pytest.mark.parametrize("m", [5, 40, 100])
+@pytest.mark.parametrize("m", [3, 5, 20, 40, 100])
 def test_int8_narrow_ragged_k_bit_exact(ops, m):
-    """Few rows (the narrow tiles) with K = 1040, a last 128-byte step only partly inside the
-    rows: the rotation-free lane, bit-exact to the CPU law."""
+    """Few rows (the GEMV on the quantized rows at 3, the 16-row weight tile at 5 and 20, the
+    narrow tiles beyond) with K = 1040, a last 128-byte step only partly inside the rows: the
+    rotation-free lane, bit-exact to the CPU law."""
     n, k = 264, 1040
     x = activations(m, k, seed=71 + m)
     data, scale = laws.int8_weight_rowwise(weights(n, k, seed=72))
